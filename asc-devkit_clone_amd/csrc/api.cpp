@@ -1,0 +1,602 @@
+// api.cpp -- the C ABI of libascq (include/ascq.h): argument validation, the Matmul handle and dispatch to
+// the gfx950 kernels.  Every entry point checks its arguments on the host and returns a negative status
+// before launching anything; there is no CPU fallback -- every compute path is a HIP kernel.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "../../include/ascq.h"
+#include "launch.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+ascq_status fail(ascq_status code, const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+ascq_status hip_status(hipError_t e, const char* what)
+{
+    if (e == hipSuccess) return ASCQ_OK;
+    return fail(ASCQ_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+inline bool valid_round(int32_t r) { return r >= ASCQ_ROUND_NONE && r <= ASCQ_ROUND_TRUNC; }
+
+}  // namespace
+
+struct ascq_matmul_s {
+    ascq_matmul_types ty{};
+    int64_t M = 0, N = 0, K = 0;        // org shape
+    int64_t sm = -1, sn = -1, sk = -1;  // single shape (-1: the org shape)
+    const void* a = nullptr;
+    int32_t trans_a = 0;
+    const void* b = nullptr;
+    int32_t trans_b = 0;
+    const void* bias = nullptr;
+    bool quant_set = false;
+    const uint64_t* qvec = nullptr;
+    uint64_t qscalar = 0;
+    bool aq_set = false;
+    bool aq_vec = false;
+    uint16_t aq_off = 0, aq_scale = 0;
+    const void* aq_off_vec = nullptr;
+    const void* aq_scale_vec = nullptr;
+    int64_t aq_group = 0;
+    const uint8_t* scale_a = nullptr;
+    int32_t trans_sa = 0;
+    const uint8_t* scale_b = nullptr;
+    int32_t trans_sb = 1;  // SetTensorScaleB defaults isTransposeScaleB = true (mx_matmul_impl.h:148)
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    bool ws_owned = false;
+};
+
+namespace {
+
+enum Kind { K_NONE, K_INT8, K_ANTIQUANT, K_MX };
+
+Kind kind_of(const ascq_matmul_types& t)
+{
+    if (t.a_type == ASCQ_DT_INT8 && t.b_type == ASCQ_DT_INT8) return K_INT8;
+    if (t.a_type == ASCQ_DT_F16 && (t.b_type == ASCQ_DT_INT8 || t.b_type == ASCQ_DT_INT4)) return K_ANTIQUANT;
+    if (t.a_type == ASCQ_DT_FP4_E2M1 && t.b_type == ASCQ_DT_FP4_E2M1 && t.scale_type == ASCQ_DT_E8M0) return K_MX;
+    return K_NONE;
+}
+
+size_t workspace_need(const ascq_matmul_s* h)
+{
+    switch (kind_of(h->ty)) {
+    case K_ANTIQUANT: {
+        size_t need = 0;
+        if (h->ty.b_format == ASCQ_FORMAT_ND) need += ascq::weight_pack_bytes(h->ty.b_type, h->K, h->N);
+        if (h->aq_set && !h->aq_vec) need += 2 * ((size_t)h->N * 2 + 256);
+        return need;
+    }
+    case K_MX: return h->trans_b ? 0 : (size_t)h->N * (size_t)(h->K / 2);
+    default: return 0;
+    }
+}
+
+ascq_status ensure_workspace(ascq_matmul_s* h)
+{
+    const size_t need = workspace_need(h);
+    if (need == 0 || h->ws_bytes >= need) return ASCQ_OK;
+    if (h->ws && !h->ws_owned) return fail(ASCQ_E_INVALID_ARG, "workspace of %zu bytes is smaller than %zu", h->ws_bytes, need);
+    if (h->ws_owned && h->ws) (void)hipFree(h->ws);
+    h->ws = nullptr;
+    h->ws_bytes = 0;
+    hipError_t e = hipMalloc(&h->ws, need);
+    if (e != hipSuccess) return hip_status(e, "hipMalloc(workspace)");
+    h->ws_bytes = need;
+    h->ws_owned = true;
+    return ASCQ_OK;
+}
+
+__global__ void fill_u16_kernel(uint16_t* p, int64_t n, uint16_t v)
+{
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = v;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ascq_last_error(void) { return g_err.c_str(); }
+
+const char* ascq_version(void) { return "ascq 0.1 (gfx950)"; }
+
+int32_t ascq_device_count(void)
+{
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+uint64_t ascq_pack_quant_pre(float m1, int32_t offset9, int32_t sign_flag)
+{
+    uint32_t u;
+    std::memcpy(&u, &m1, 4);
+    return (uint64_t)u | ((uint64_t)((uint32_t)offset9 & 0x1ffu) << 37) | ((uint64_t)(sign_flag & 1) << 46);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Matmul
+// ------------------------------------------------------------------------------------------------
+ascq_status ascq_matmul_create(const ascq_matmul_types* types, ascq_matmul_t* out)
+{
+    if (!types || !out) return fail(ASCQ_E_INVALID_ARG, "matmul_create: null argument");
+    *out = nullptr;
+    const Kind k = kind_of(*types);
+    if (k == K_NONE)
+        return fail(ASCQ_E_UNSUPPORTED, "matmul_create: unsupported A/B types (%d, %d)", types->a_type, types->b_type);
+    if (k == K_INT8) {
+        if (types->c_type != ASCQ_DT_F16 && types->c_type != ASCQ_DT_BF16 && types->c_type != ASCQ_DT_INT32)
+            return fail(ASCQ_E_UNSUPPORTED, "matmul_create: int8 matmul supports C = f16, bf16 or int32");
+        if (types->bias_type != 0 && types->bias_type != ASCQ_DT_INT32)
+            return fail(ASCQ_E_UNSUPPORTED, "matmul_create: int8 matmul bias must be int32");
+        if (types->b_format != ASCQ_FORMAT_ND) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: int8 B must be ND");
+    } else if (k == K_ANTIQUANT) {
+        if (types->c_type != ASCQ_DT_F16) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: weight-only matmul supports C = f16");
+        if (types->bias_type != 0) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: weight-only matmul has no bias path");
+    } else {
+        if (types->c_type != ASCQ_DT_BF16 && types->c_type != ASCQ_DT_F32)
+            return fail(ASCQ_E_UNSUPPORTED, "matmul_create: MX matmul supports C = bf16 or f32");
+        if (types->bias_type != 0) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: MX matmul bias is not supported");
+        if (types->b_format != ASCQ_FORMAT_ND) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: MX B must be ND");
+    }
+    auto* h = new (std::nothrow) ascq_matmul_s();
+    if (!h) return fail(ASCQ_E_INVALID_ARG, "matmul_create: out of host memory");
+    h->ty = *types;
+    *out = h;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_set_org_shape(ascq_matmul_t h, int64_t m, int64_t n, int64_t k)
+{
+    if (!h) return fail(ASCQ_E_INVALID_ARG, "null handle");
+    if (m <= 0 || n <= 0 || k <= 0) return fail(ASCQ_E_INVALID_ARG, "set_org_shape: shape must be positive");
+    h->M = m;
+    h->N = n;
+    h->K = k;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_set_single_shape(ascq_matmul_t h, int64_t m, int64_t n, int64_t k)
+{
+    if (!h) return fail(ASCQ_E_INVALID_ARG, "null handle");
+    if (m <= 0 || n <= 0 || k <= 0) return fail(ASCQ_E_INVALID_ARG, "set_single_shape: shape must be positive");
+    h->sm = m;
+    h->sn = n;
+    h->sk = k;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_set_tail(ascq_matmul_t h, int64_t tail_m, int64_t tail_n, int64_t tail_k)
+{
+    if (!h) return fail(ASCQ_E_INVALID_ARG, "null handle");
+    // SetTail(-1) keeps a dimension (matmul.h:117 default arguments)
+    if (tail_m > 0) h->sm = tail_m;
+    if (tail_n > 0) h->sn = tail_n;
+    if (tail_k > 0) h->sk = tail_k;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_set_tensor_a(ascq_matmul_t h, const void* a, int32_t is_transpose_a)
+{
+    if (!h || !a) return fail(ASCQ_E_INVALID_ARG, "set_tensor_a: null argument");
+    h->a = a;
+    h->trans_a = is_transpose_a ? 1 : 0;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_set_tensor_b(ascq_matmul_t h, const void* b, int32_t is_transpose_b)
+{
+    if (!h || !b) return fail(ASCQ_E_INVALID_ARG, "set_tensor_b: null argument");
+    h->b = b;
+    h->trans_b = is_transpose_b ? 1 : 0;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_set_bias(ascq_matmul_t h, const void* bias)
+{
+    if (!h || !bias) return fail(ASCQ_E_INVALID_ARG, "set_bias: null argument");
+    if (h->ty.bias_type != ASCQ_DT_INT32) return fail(ASCQ_E_UNSUPPORTED, "set_bias: the handle has no int32 bias type");
+    h->bias = bias;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_disable_bias(ascq_matmul_t h)
+{
+    if (!h) return fail(ASCQ_E_INVALID_ARG, "null handle");
+    h->bias = nullptr;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_set_quant_scalar(ascq_matmul_t h, uint64_t quant_scalar)
+{
+    if (!h) return fail(ASCQ_E_INVALID_ARG, "null handle");
+    if (kind_of(h->ty) != K_INT8 || h->ty.c_type == ASCQ_DT_INT32)
+        return fail(ASCQ_E_UNSUPPORTED, "set_quant_scalar: no quant epilogue for this type combination");
+    h->quant_set = true;
+    h->qvec = nullptr;
+    h->qscalar = quant_scalar;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_set_quant_vector(ascq_matmul_t h, const uint64_t* quant_vector)
+{
+    if (!h || !quant_vector) return fail(ASCQ_E_INVALID_ARG, "set_quant_vector: null argument");
+    if (kind_of(h->ty) != K_INT8 || h->ty.c_type == ASCQ_DT_INT32)
+        return fail(ASCQ_E_UNSUPPORTED, "set_quant_vector: no quant epilogue for this type combination");
+    if (!aligned(quant_vector, 8)) return fail(ASCQ_E_INVALID_ARG, "set_quant_vector: pointer must be 8-byte aligned");
+    h->quant_set = true;
+    h->qvec = quant_vector;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_set_antiquant_scalar(ascq_matmul_t h, uint16_t offset_f16, uint16_t scale_f16)
+{
+    if (!h) return fail(ASCQ_E_INVALID_ARG, "null handle");
+    if (kind_of(h->ty) != K_ANTIQUANT) return fail(ASCQ_E_UNSUPPORTED, "set_antiquant_scalar: not a weight-only handle");
+    h->aq_set = true;
+    h->aq_vec = false;
+    h->aq_off = offset_f16;
+    h->aq_scale = scale_f16;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_set_antiquant_vector(ascq_matmul_t h, const void* offset, const void* scale, int64_t group_size)
+{
+    if (!h || !scale) return fail(ASCQ_E_INVALID_ARG, "set_antiquant_vector: null argument");
+    if (kind_of(h->ty) != K_ANTIQUANT) return fail(ASCQ_E_UNSUPPORTED, "set_antiquant_vector: not a weight-only handle");
+    if (group_size < 0 || (group_size > 0 && group_size % 32 != 0))
+        return fail(ASCQ_E_INVALID_ARG, "set_antiquant_vector: group_size must be 0 or a multiple of 32");
+    h->aq_set = true;
+    h->aq_vec = true;
+    h->aq_off_vec = offset;
+    h->aq_scale_vec = scale;
+    h->aq_group = group_size;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_set_tensor_scale_a(ascq_matmul_t h, const uint8_t* scale_a, int32_t is_transpose_scale_a)
+{
+    if (!h || !scale_a) return fail(ASCQ_E_INVALID_ARG, "set_tensor_scale_a: null argument");
+    if (kind_of(h->ty) != K_MX) return fail(ASCQ_E_UNSUPPORTED, "set_tensor_scale_a: not an MX handle");
+    h->scale_a = scale_a;
+    h->trans_sa = is_transpose_scale_a ? 1 : 0;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_set_tensor_scale_b(ascq_matmul_t h, const uint8_t* scale_b, int32_t is_transpose_scale_b)
+{
+    if (!h || !scale_b) return fail(ASCQ_E_INVALID_ARG, "set_tensor_scale_b: null argument");
+    if (kind_of(h->ty) != K_MX) return fail(ASCQ_E_UNSUPPORTED, "set_tensor_scale_b: not an MX handle");
+    h->scale_b = scale_b;
+    h->trans_sb = is_transpose_scale_b ? 1 : 0;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_workspace_size(ascq_matmul_t h, size_t* bytes)
+{
+    if (!h || !bytes) return fail(ASCQ_E_INVALID_ARG, "workspace_size: null argument");
+    *bytes = workspace_need(h);
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_set_workspace(ascq_matmul_t h, void* workspace, size_t bytes)
+{
+    if (!h) return fail(ASCQ_E_INVALID_ARG, "null handle");
+    if (h->ws_owned && h->ws) (void)hipFree(h->ws);
+    h->ws = workspace;
+    h->ws_bytes = workspace ? bytes : 0;
+    h->ws_owned = false;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic, void* stream)
+{
+    if (!h || !c) return fail(ASCQ_E_INVALID_ARG, "iterate_all: null argument");
+    if (en_atomic != 0) return fail(ASCQ_E_UNSUPPORTED, "iterate_all: enAtomic != 0 is not supported");
+    if (!h->a || !h->b) return fail(ASCQ_E_STATE, "iterate_all: SetTensorA and SetTensorB must precede IterateAll");
+    if (h->M <= 0) return fail(ASCQ_E_STATE, "iterate_all: SetOrgShape must precede IterateAll");
+    const int64_t m = h->sm > 0 ? h->sm : h->M, n = h->sn > 0 ? h->sn : h->N, k = h->sk > 0 ? h->sk : h->K;
+    if (m > h->M || n > h->N || k > h->K) return fail(ASCQ_E_INVALID_ARG, "iterate_all: single shape exceeds org shape");
+    hipStream_t st = S(stream);
+    switch (kind_of(h->ty)) {
+    case K_INT8: {
+        if (h->ty.c_type != ASCQ_DT_INT32 && !h->quant_set)
+            return fail(ASCQ_E_STATE, "iterate_all: f16/bf16 output needs SetQuantScalar or SetQuantVector");
+        ascq::GemmI8Args g{};
+        g.A = (const int8_t*)h->a;
+        g.B = (const int8_t*)h->b;
+        g.bias = (const int32_t*)h->bias;
+        g.C = c;
+        g.M = m;
+        g.N = n;
+        g.K = k;
+        g.lda = h->trans_a ? h->M : h->K;
+        g.ldb = h->trans_b ? h->K : h->N;
+        g.ldc = h->N;
+        g.qvec = h->qvec;
+        g.qscalar = h->qscalar;
+        g.epi = h->ty.c_type == ASCQ_DT_INT32 ? ascq::EPI_I32
+                                               : (h->ty.c_type == ASCQ_DT_F16 ? ascq::EPI_DEQ_F16 : ascq::EPI_DEQ_BF16);
+        g.trans_a = h->trans_a;
+        g.trans_b = h->trans_b;
+        return hip_status(ascq::launch_gemm_i8(g, st), "gemm_i8");
+    }
+    case K_ANTIQUANT: {
+        if (!h->aq_set) return fail(ASCQ_E_STATE, "iterate_all: SetAntiQuantScalar/Vector must precede IterateAll");
+        if (m != h->M || n != h->N || k != h->K)
+            return fail(ASCQ_E_UNSUPPORTED, "iterate_all: weight-only matmul computes the full org shape only");
+        if (h->trans_a) return fail(ASCQ_E_UNSUPPORTED, "iterate_all: weight-only matmul needs A = [M, K]");
+        if (h->K % 128 != 0 || h->N % 16 != 0)
+            return fail(ASCQ_E_UNSUPPORTED, "iterate_all: weight-only matmul needs K %% 128 == 0 and N %% 16 == 0");
+        if (h->aq_vec && h->aq_group > 0 && h->K % h->aq_group != 0)
+            return fail(ASCQ_E_INVALID_ARG, "iterate_all: group_size must divide K");
+        if (!aligned(h->a, 16)) return fail(ASCQ_E_INVALID_ARG, "iterate_all: A must be 16-byte aligned");
+        ascq_status s = ensure_workspace(h);
+        if (s != ASCQ_OK) return s;
+        uint8_t* ws = (uint8_t*)h->ws;
+        const void* wp = h->b;
+        if (h->ty.b_format == ASCQ_FORMAT_ND) {
+            hipError_t e = ascq::launch_weight_pack(ws, h->b, h->ty.b_type, h->K, h->N, h->trans_b, st);
+            if (e != hipSuccess) return hip_status(e, "weight_pack");
+            wp = ws;
+            ws += (ascq::weight_pack_bytes(h->ty.b_type, h->K, h->N) + 255) / 256 * 256;
+        } else if (!aligned(h->b, 16)) {
+            return fail(ASCQ_E_INVALID_ARG, "iterate_all: packed B must be 16-byte aligned");
+        }
+        const uint16_t* sc = (const uint16_t*)h->aq_scale_vec;
+        const uint16_t* of = (const uint16_t*)h->aq_off_vec;
+        int64_t grp = h->aq_group;
+        if (!h->aq_vec) {
+            uint16_t* s16 = (uint16_t*)ws;
+            uint16_t* o16 = s16 + (h->N + 127) / 128 * 128;
+            hipLaunchKernelGGL(fill_u16_kernel, dim3(64), dim3(256), 0, st, s16, h->N, h->aq_scale);
+            hipLaunchKernelGGL(fill_u16_kernel, dim3(64), dim3(256), 0, st, o16, h->N, h->aq_off);
+            sc = s16;
+            of = o16;
+            grp = 0;
+        }
+        return hip_status(ascq::launch_antiquant_matmul((uint16_t*)c, (const uint16_t*)h->a, wp, h->ty.b_type, sc, of,
+                                                        grp, h->M, h->N, h->K, st),
+                          "antiquant_matmul");
+    }
+    case K_MX: {
+        if (!h->scale_a || !h->scale_b) return fail(ASCQ_E_STATE, "iterate_all: SetTensorScaleA/B must precede IterateAll");
+        if (m != h->M || n != h->N || k != h->K)
+            return fail(ASCQ_E_UNSUPPORTED, "iterate_all: MX matmul computes the full org shape only");
+        if (h->trans_a) return fail(ASCQ_E_UNSUPPORTED, "iterate_all: MX matmul needs A = [M, K]");
+        if (h->K % 128 != 0) return fail(ASCQ_E_UNSUPPORTED, "iterate_all: MX matmul needs K %% 128 == 0");
+        if (!h->trans_b && h->N % 2 != 0) return fail(ASCQ_E_INVALID_ARG, "iterate_all: [K, N] fp4 B needs even N");
+        if (!aligned(h->a, 16) || !aligned(h->b, 16) || !aligned(h->scale_a, 4) || !aligned(h->scale_b, 4))
+            return fail(ASCQ_E_INVALID_ARG, "iterate_all: MX operands must be 16-byte (scales 4-byte) aligned");
+        ascq_status s = ensure_workspace(h);
+        if (s != ASCQ_OK) return s;
+        const uint8_t* bt = (const uint8_t*)h->b;
+        if (!h->trans_b) {
+            hipError_t e = ascq::launch_fp4_transpose((uint8_t*)h->ws, (const uint8_t*)h->b, h->K, h->N, st);
+            if (e != hipSuccess) return hip_status(e, "fp4_transpose");
+            bt = (const uint8_t*)h->ws;
+        }
+        ascq::MxGemmArgs g{};
+        g.A = (const uint8_t*)h->a;
+        g.B = bt;
+        g.sA = h->scale_a;
+        g.sB = h->scale_b;
+        g.M = h->M;
+        g.N = h->N;
+        g.K = h->K;
+        g.sa_layout = h->trans_sa;
+        g.sb_layout = h->trans_sb;
+        g.C = c;
+        g.c_type = h->ty.c_type;  // ascq_dtype codes equal the device DT_* codes
+        return hip_status(ascq::launch_mx_gemm(g, st), "mx_gemm");
+    }
+    default: return fail(ASCQ_E_UNSUPPORTED, "iterate_all: unsupported handle");
+    }
+}
+
+ascq_status ascq_matmul_end(ascq_matmul_t h)
+{
+    if (!h) return fail(ASCQ_E_INVALID_ARG, "null handle");
+    h->a = h->b = h->bias = nullptr;
+    h->quant_set = h->aq_set = false;
+    h->qvec = nullptr;
+    h->scale_a = h->scale_b = nullptr;
+    h->sm = h->sn = h->sk = -1;
+    return ASCQ_OK;
+}
+
+ascq_status ascq_matmul_destroy(ascq_matmul_t h)
+{
+    if (!h) return ASCQ_OK;
+    if (h->ws_owned && h->ws) (void)hipFree(h->ws);
+    delete h;
+    return ASCQ_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// AscendQuant / AscendDequant / AscendAntiQuant
+// ------------------------------------------------------------------------------------------------
+ascq_status ascq_ascend_quant_per_token(int8_t* dst, const void* src, int32_t src_type, const float* scale,
+                                        const float* offset, const ascq_quant_param* para, void* stream)
+{
+    if (!dst || !src || !scale || !para) return fail(ASCQ_E_INVALID_ARG, "quant_per_token: null argument");
+    if (src_type != ASCQ_DT_F16 && src_type != ASCQ_DT_BF16 && src_type != ASCQ_DT_F32)
+        return fail(ASCQ_E_UNSUPPORTED, "quant_per_token: src must be f16, bf16 or f32");
+    if (para->n == 0) return fail(ASCQ_E_INVALID_ARG, "quant_per_token: n must be positive");
+    if (para->cal_count % para->n != 0)
+        return fail(ASCQ_E_INVALID_ARG, "quant_per_token: calCount must be an integer multiple of n");
+    if (!valid_round(para->round_mode)) return fail(ASCQ_E_INVALID_ARG, "quant_per_token: bad round mode");
+    if (para->has_offset && !offset) return fail(ASCQ_E_INVALID_ARG, "quant_per_token: has_offset needs an offset tensor");
+    const uint32_t m = para->cal_count / para->n;
+    if (m == 0) return ASCQ_OK;
+    return hip_status(ascq::launch_quant_per_token(dst, src, src_type, scale, para->has_offset ? offset : nullptr, m,
+                                                   para->n, para->round_mode, S(stream)),
+                      "quant_per_token");
+}
+
+ascq_status ascq_ascend_quant_dynamic_per_token(int8_t* dst, float* scale_out, const void* src, int32_t src_type,
+                                                uint32_t m, uint32_t n, int32_t round_mode, void* stream)
+{
+    if (!dst || !scale_out || !src) return fail(ASCQ_E_INVALID_ARG, "quant_dynamic_per_token: null argument");
+    if (src_type != ASCQ_DT_F16 && src_type != ASCQ_DT_BF16 && src_type != ASCQ_DT_F32)
+        return fail(ASCQ_E_UNSUPPORTED, "quant_dynamic_per_token: src must be f16, bf16 or f32");
+    if (!valid_round(round_mode)) return fail(ASCQ_E_INVALID_ARG, "quant_dynamic_per_token: bad round mode");
+    if (m == 0 || n == 0) return ASCQ_OK;
+    return hip_status(ascq::launch_quant_dynamic_per_token(dst, scale_out, src, src_type, m, n, round_mode, S(stream)),
+                      "quant_dynamic_per_token");
+}
+
+ascq_status ascq_ascend_quant(int8_t* dst, const void* src, int32_t src_type, const uint16_t* scale,
+                              const uint16_t* offset, uint16_t scale_scalar, uint16_t offset_scalar, uint32_t cal_count,
+                              uint32_t scale_count, void* stream)
+{
+    if (!dst || !src) return fail(ASCQ_E_INVALID_ARG, "ascend_quant: null argument");
+    if (src_type != ASCQ_DT_F16 && src_type != ASCQ_DT_F32)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_quant: src must be f16 or f32");
+    if ((scale || offset) && scale_count == 0) return fail(ASCQ_E_INVALID_ARG, "ascend_quant: scale_count must be positive");
+    if (scale_count && cal_count % scale_count != 0)
+        return fail(ASCQ_E_INVALID_ARG, "ascend_quant: calCount must be an integer multiple of scaleCount");
+    if (cal_count == 0) return ASCQ_OK;
+    return hip_status(ascq::launch_quant_legacy(dst, src, src_type, scale, offset, scale_scalar, offset_scalar, cal_count,
+                                                (scale || offset) ? scale_count : 0u, S(stream)),
+                      "ascend_quant");
+}
+
+ascq_status ascq_ascend_dequant(void* dst, int32_t dst_type, const void* src, int32_t src_type, const void* scale,
+                                int32_t scale_type, float scale_scalar, int32_t policy,
+                                const ascq_dequant_param* params, void* stream)
+{
+    if (!dst || !src || !params) return fail(ASCQ_E_INVALID_ARG, "ascend_dequant: null argument");
+    if (dst_type != ASCQ_DT_F16 && dst_type != ASCQ_DT_BF16 && dst_type != ASCQ_DT_F32)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant: dst must be f16, bf16 or f32");
+    if (src_type != ASCQ_DT_INT32 && src_type != ASCQ_DT_INT8)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant: src must be int32 or int8");
+    if (policy != ASCQ_POLICY_PER_TENSOR && policy != ASCQ_POLICY_PER_CHANNEL && policy != ASCQ_POLICY_PER_TOKEN)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant: policy must be per-tensor, per-channel or per-token");
+    if (policy != ASCQ_POLICY_PER_TENSOR) {
+        if (!scale) return fail(ASCQ_E_INVALID_ARG, "ascend_dequant: null scale");
+        if (scale_type != ASCQ_DT_F32 && scale_type != ASCQ_DT_F16 && scale_type != ASCQ_DT_BF16 &&
+            scale_type != ASCQ_DT_U64)
+            return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant: scale must be f32, f16, bf16 or u64");
+    }
+    if (policy == ASCQ_POLICY_PER_CHANNEL && params->cal_count > params->n)
+        return fail(ASCQ_E_INVALID_ARG, "ascend_dequant: calCount must not exceed n");
+    if (params->m == 0 || params->n == 0) return ASCQ_OK;
+    return hip_status(ascq::launch_dequant(dst, dst_type, src, src_type, scale, scale_type, scale_scalar, policy,
+                                           params->m, params->n, params->cal_count, S(stream)),
+                      "ascend_dequant");
+}
+
+ascq_status ascq_ascend_antiquant(void* dst, int32_t dst_type, const void* src, int32_t src_type, const void* offset,
+                                  const void* scale, uint32_t k, uint32_t n, uint32_t group_size, int32_t is_transpose,
+                                  int32_t arith, void* stream)
+{
+    if (!dst || !src || !scale) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant: null argument");
+    if (dst_type != ASCQ_DT_F16 && dst_type != ASCQ_DT_BF16)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant: dst must be f16 or bf16");
+    if (src_type != ASCQ_DT_INT8 && src_type != ASCQ_DT_INT4)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant: src must be int8 or int4");
+    if (arith != ASCQ_ARITH_F16 && arith != ASCQ_ARITH_F32) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant: bad arith");
+    if (group_size && k % group_size != 0) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant: group_size must divide K");
+    if (src_type == ASCQ_DT_INT4 && ((uint64_t)k * n) % 2 != 0)
+        return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant: int4 needs an even element count");
+    if (k == 0 || n == 0) return ASCQ_OK;
+    const uint32_t g = group_size ? group_size : k;
+    return hip_status(ascq::launch_antiquant(dst, dst_type, src, src_type, offset, scale, k, n, g, is_transpose ? 1 : 0,
+                                             dst_type == ASCQ_DT_BF16 ? 1 : arith, S(stream)),
+                      "ascend_antiquant");
+}
+
+// ------------------------------------------------------------------------------------------------
+// weight-only antiquant matmul
+// ------------------------------------------------------------------------------------------------
+ascq_status ascq_weight_pack_size(int32_t w_type, int64_t k, int64_t n, size_t* bytes)
+{
+    if (!bytes) return fail(ASCQ_E_INVALID_ARG, "weight_pack_size: null argument");
+    if (w_type != ASCQ_DT_INT8 && w_type != ASCQ_DT_INT4) return fail(ASCQ_E_UNSUPPORTED, "weight_pack_size: int8 or int4");
+    if (k <= 0 || n <= 0 || k % 128 != 0 || n % 16 != 0)
+        return fail(ASCQ_E_INVALID_ARG, "weight_pack_size: K %% 128 == 0 and N %% 16 == 0 required");
+    *bytes = ascq::weight_pack_bytes(w_type, k, n);
+    return ASCQ_OK;
+}
+
+ascq_status ascq_weight_pack(void* packed, const void* w, int32_t w_type, int64_t k, int64_t n, int32_t is_transpose,
+                             void* stream)
+{
+    size_t bytes = 0;
+    ascq_status s = ascq_weight_pack_size(w_type, k, n, &bytes);
+    if (s != ASCQ_OK) return s;
+    if (!packed || !w) return fail(ASCQ_E_INVALID_ARG, "weight_pack: null argument");
+    if (!aligned(packed, 16)) return fail(ASCQ_E_INVALID_ARG, "weight_pack: output must be 16-byte aligned");
+    return hip_status(ascq::launch_weight_pack(packed, w, w_type, k, n, is_transpose ? 1 : 0, S(stream)), "weight_pack");
+}
+
+ascq_status ascq_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w_packed, int32_t w_type,
+                                  const uint16_t* scale, const uint16_t* offset, int64_t group_size, int64_t m,
+                                  int64_t n, int64_t k, void* stream)
+{
+    if (!y || !x || !w_packed || !scale) return fail(ASCQ_E_INVALID_ARG, "antiquant_matmul: null argument");
+    if (w_type != ASCQ_DT_INT8 && w_type != ASCQ_DT_INT4) return fail(ASCQ_E_UNSUPPORTED, "antiquant_matmul: int8 or int4");
+    if (m <= 0 || n <= 0 || k <= 0) return fail(ASCQ_E_INVALID_ARG, "antiquant_matmul: shape must be positive");
+    if (k % 128 != 0 || n % 16 != 0)
+        return fail(ASCQ_E_INVALID_ARG, "antiquant_matmul: K %% 128 == 0 and N %% 16 == 0 required");
+    if (group_size < 0 || (group_size > 0 && (group_size % 32 != 0 || k % group_size != 0)))
+        return fail(ASCQ_E_INVALID_ARG, "antiquant_matmul: group_size must be 0 or a multiple of 32 dividing K");
+    if (!aligned(x, 16) || !aligned(w_packed, 16))
+        return fail(ASCQ_E_INVALID_ARG, "antiquant_matmul: x and the packed weight must be 16-byte aligned");
+    return hip_status(ascq::launch_antiquant_matmul(y, x, w_packed, w_type, scale, offset, group_size, m, n, k, S(stream)),
+                      "antiquant_matmul");
+}
+
+// ------------------------------------------------------------------------------------------------
+// quantized group matmul
+// ------------------------------------------------------------------------------------------------
+ascq_status ascq_quant_group_matmul(void* y, int32_t out_type, const int8_t* x, const float* per_token_scale,
+                                    const int8_t* w, int32_t w_trans, const float* scale, const int64_t* group_list,
+                                    int32_t list_type, int64_t num_groups, int64_t m, int64_t k, int64_t n, void* stream)
+{
+    if (!y || !x || !per_token_scale || !w || !scale || !group_list)
+        return fail(ASCQ_E_INVALID_ARG, "quant_group_matmul: null argument");
+    if (out_type != ASCQ_DT_BF16 && out_type != ASCQ_DT_F16)
+        return fail(ASCQ_E_UNSUPPORTED, "quant_group_matmul: output must be bf16 or f16");
+    if (list_type != 0 && list_type != 1) return fail(ASCQ_E_INVALID_ARG, "quant_group_matmul: list_type must be 0 or 1");
+    if (num_groups <= 0 || num_groups > 1024) return fail(ASCQ_E_INVALID_ARG, "quant_group_matmul: 1 <= groups <= 1024");
+    if (m <= 0 || k <= 0 || n <= 0) return fail(ASCQ_E_INVALID_ARG, "quant_group_matmul: shape must be positive");
+    ascq::GroupGemmArgs g{};
+    g.Y = y;
+    g.out_type = out_type;
+    g.X = x;
+    g.pts = per_token_scale;
+    g.W = w;
+    g.w_trans = w_trans ? 1 : 0;
+    g.scale = scale;
+    g.group_list = group_list;
+    g.list_type = list_type;
+    g.G = num_groups;
+    g.M = m;
+    g.K = k;
+    g.N = n;
+    return hip_status(ascq::launch_group_gemm(g, S(stream)), "quant_group_matmul");
+}
+
+}  // extern "C"

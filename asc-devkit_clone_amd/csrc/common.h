@@ -1,0 +1,129 @@
+// common.h -- shared device helpers for the gfx950 kernels of libascq.
+//
+// Numeric conventions (the same as the reference arithmetic restated for this library):
+//  * f16 / bf16 travel as uint16_t bit patterns;
+//  * conversions to f16 / bf16 round to nearest even and saturate to the finite range
+//    (docs/zh/api/SIMD-API/basic_api/data_structures/precision_conversion.md:30), NaN stays NaN;
+//  * every fp32 operation is one IEEE operation: the library is built with -ffp-contract=off
+//    so a multiply followed by an add never becomes an fma unless written as one.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ascq {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef short s8v __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+// dtype / round-mode codes shared with include/ascq.h
+enum : int32_t {
+    DT_INT8 = 1, DT_UINT8 = 2, DT_INT4 = 3, DT_INT32 = 4, DT_F16 = 5, DT_BF16 = 6, DT_F32 = 7, DT_U64 = 8,
+    DT_FP8_E4M3 = 9, DT_FP8_E5M2 = 10, DT_FP4_E2M1 = 11, DT_E8M0 = 12, DT_INT64 = 13
+};
+enum : int32_t { RM_NONE = 0, RM_RINT = 1, RM_FLOOR = 2, RM_CEIL = 3, RM_ROUND = 4, RM_TRUNC = 5 };
+
+__device__ __forceinline__ uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
+__device__ __forceinline__ _Float16 bits_h(uint16_t u) { return __builtin_bit_cast(_Float16, u); }
+
+// fp32 -> f16, rne, saturating (|x| > 65504 -> +-65504; NaN kept)
+__device__ __forceinline__ uint16_t f32_to_f16_sat(float x)
+{
+    float c = __builtin_fabsf(x) > 65504.0f ? __builtin_copysignf(65504.0f, x) : x;
+    return h_bits((_Float16)c);
+}
+// fp32 -> f16, rne, IEEE overflow to inf
+__device__ __forceinline__ uint16_t f32_to_f16(float x) { return h_bits((_Float16)x); }
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)bits_h(h); }
+
+// fp32 -> bf16, rne, saturating (overflow and inf -> +-max finite, NaN quieted)
+__device__ __forceinline__ uint16_t f32_to_bf16_sat(float x)
+{
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    uint32_t r = u + 0x7fffu + ((u >> 16) & 1u);
+    uint16_t b = (uint16_t)(r >> 16);
+    if ((b & 0x7fffu) == 0x7f80u) b = (uint16_t)((b & 0x8000u) | 0x7f7fu);
+    return b;
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// QUANT_PRE word -> M1 multiplier: bits [31:13] as fp32, low 13 bits cleared
+__device__ __forceinline__ float quant_pre_m1(uint64_t w) { return __uint_as_float((uint32_t)w & 0xFFFFE000u); }
+
+// RoundMode to integral float
+__device__ __forceinline__ float round_mode_f(float v, int mode)
+{
+    switch (mode) {
+    case RM_FLOOR: return __builtin_floorf(v);
+    case RM_CEIL: return __builtin_ceilf(v);
+    case RM_ROUND: return __builtin_roundf(v);
+    case RM_TRUNC: return __builtin_truncf(v);
+    default: return __builtin_rintf(v);
+    }
+}
+
+// integral float -> int8 with saturation; NaN -> 0
+__device__ __forceinline__ int32_t sat_s8_from_integral(float r)
+{
+    if (r != r) return 0;
+    r = __builtin_fminf(__builtin_fmaxf(r, -128.0f), 127.0f);
+    return (int32_t)r;
+}
+
+template <int MODE>
+__device__ __forceinline__ int32_t quant_s8(float v)
+{
+    float r;
+    if constexpr (MODE == RM_FLOOR) r = __builtin_floorf(v);
+    else if constexpr (MODE == RM_CEIL) r = __builtin_ceilf(v);
+    else if constexpr (MODE == RM_ROUND) r = __builtin_roundf(v);
+    else if constexpr (MODE == RM_TRUNC) r = __builtin_truncf(v);
+    else r = __builtin_rintf(v);
+    return sat_s8_from_integral(r);
+}
+
+__device__ __forceinline__ uint32_t pack4_s8(int32_t a, int32_t b, int32_t c, int32_t d)
+{
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+}
+
+// store an fp32 value as dtype (F16 / BF16 / F32), rne + sat
+__device__ __forceinline__ void store_cast(void* p, int64_t i, float v, int dtype)
+{
+    if (dtype == DT_F16) ((uint16_t*)p)[i] = f32_to_f16_sat(v);
+    else if (dtype == DT_BF16) ((uint16_t*)p)[i] = f32_to_bf16_sat(v);
+    else ((float*)p)[i] = v;
+}
+
+__device__ __forceinline__ float load_f32_of(const void* p, int64_t i, int dtype)
+{
+    switch (dtype) {
+    case DT_F16: return f16_to_f32(((const uint16_t*)p)[i]);
+    case DT_BF16: return bf16_to_f32(((const uint16_t*)p)[i]);
+    case DT_F32: return ((const float*)p)[i];
+    case DT_INT32: return (float)((const int32_t*)p)[i];
+    case DT_INT8: return (float)((const int8_t*)p)[i];
+    case DT_U64: return __uint_as_float((uint32_t)((const uint64_t*)p)[i]);
+    default: return 0.0f;
+    }
+}
+
+// wave64 reductions
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+}  // namespace ascq

@@ -1,0 +1,79 @@
+// launch.h -- host-side launchers of the gfx950 kernels (called by api.cpp after argument validation).
+// Every launcher enqueues on `st` and returns the launch status; none allocates device memory
+// unless its comment says so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ascq {
+
+// quant.hip
+hipError_t launch_quant_dynamic_per_token(int8_t* q, float* scale_out, const void* x, int src_type, uint32_t m,
+                                          uint32_t n, int round_mode, hipStream_t st);
+hipError_t launch_quant_per_token(int8_t* q, const void* x, int src_type, const float* scale, const float* offset,
+                                  uint32_t m, uint32_t n, int round_mode, hipStream_t st);
+hipError_t launch_quant_legacy(int8_t* q, const void* x, int src_type, const uint16_t* scale, const uint16_t* offset,
+                               uint16_t scale_scalar, uint16_t offset_scalar, uint32_t cal_count,
+                               uint32_t scale_count, hipStream_t st);
+hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                          float scale_scalar, int policy, uint32_t m, uint32_t n, uint32_t cal_count, hipStream_t st);
+hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset,
+                            const void* scale, uint32_t K, uint32_t N, uint32_t g, int is_transpose, int arith,
+                            hipStream_t st);
+
+// gemm_i8.hip
+enum : int { EPI_I32 = 0, EPI_DEQ_F16 = 1, EPI_DEQ_BF16 = 2 };
+struct GemmI8Args {
+    const int8_t* A;      // [M, K] row-major (lda), or [K, M] when trans_a
+    const int8_t* B;      // [K, N] row-major (ldb), or [N, K] when trans_b
+    const int32_t* bias;  // [N] or null
+    void* C;              // [M, N] row-major (ldc)
+    int64_t M, N, K, lda, ldb, ldc;
+    const uint64_t* qvec; // per-channel QUANT_PRE words [N] or null
+    uint64_t qscalar;
+    int epi;              // EPI_*
+    int trans_a, trans_b;
+};
+hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st);
+
+// group_gemm.hip
+struct GroupGemmArgs {
+    void* Y;
+    int out_type;             // DT_BF16 / DT_F16
+    const int8_t* X;          // [M, K]
+    const float* pts;         // [M]
+    const int8_t* W;          // [G, K, N] or [G, N, K]
+    int w_trans;
+    const float* scale;       // [G, N]
+    const int64_t* group_list;
+    int list_type;            // 0 prefix offsets [G+1], 1 counts [G]
+    int64_t G, M, K, N;
+};
+hipError_t launch_group_gemm(const GroupGemmArgs& a, hipStream_t st);
+
+// gemv_antiquant.hip
+size_t weight_pack_bytes(int w_type, int64_t K, int64_t N);
+hipError_t launch_weight_pack(void* packed, const void* w, int w_type, int64_t K, int64_t N, int is_transpose,
+                              hipStream_t st);
+hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* wp, int w_type, const uint16_t* scale,
+                                   const uint16_t* offset, int64_t group, int64_t M, int64_t N, int64_t K,
+                                   hipStream_t st);
+
+// mx_gemm.hip
+struct MxGemmArgs {
+    const uint8_t* A;       // [M, K/2] packed E2M1
+    const uint8_t* B;       // [N, K/2] packed (after any transpose)
+    const uint8_t* sA;      // scales
+    const uint8_t* sB;
+    int64_t M, N, K;
+    int sa_layout;          // 0: [M, sK]; 1: [sK/2, M, 2]
+    int sb_layout;          // 0: [sK/2, N, 2]; 1: [N, sK]
+    void* C;                // [M, N]
+    int c_type;             // DT_BF16 / DT_F32
+};
+hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st);
+// transpose a [K, N] packed fp4 matrix (two per byte along N) into [N, K] (two per byte along K)
+hipError_t launch_fp4_transpose(uint8_t* dst, const uint8_t* src, int64_t K, int64_t N, hipStream_t st);
+
+}  // namespace ascq

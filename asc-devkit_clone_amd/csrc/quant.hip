@@ -1,0 +1,355 @@
+// quant.hip -- AscendQuant / AscendDequant / AscendAntiQuant for gfx950.
+//
+// These ops are HBM-bound streams.  Layout in HBM is the reference's: row-major [m, n] tensors, one
+// scale per row (per-token) or per column (per-channel).  Each kernel moves 16-byte vectors per lane so a
+// wave issues 1 KiB contiguous requests; the per-token dynamic quant keeps a whole row in registers so
+// the input is read from HBM exactly once (absmax pass and quantise pass share the registers).
+//
+// Reference arithmetic (see include/ascq.h for the entry points):
+//  per-token quant   impl/adv_api/detail/quantization/quant/ascend_quant_per_group_3510_impl.h:142-178
+//                    + TransRegForS8 ascend_quant_3510_impl.h:958-968 -> sat_s8(round(f32(x)*s (+o)))
+//  legacy quant      ascend_quant_pre_impl.h:101-164 (half Mul, half Add, Cast<int8_t,half> rint/sat)
+//  dequant           ascend_dequant_3510_impl.h:37-75, 254-287; ascend_dequant_common_impl.h:196-364
+//  antiquant         ascend_antiquant_impl.h:63-96 (half ops), ascend_antiquant_c220_impl.h:46-75 (fp32 ops)
+#include "common.h"
+#include "launch.h"
+
+namespace ascq {
+
+// ---------------------------------------------------------------------------------------------
+// Dynamic per-token quant, f16 / bf16 input, row resident in registers.
+// One 256-thread workgroup per row; thread t holds 16-byte chunks t, t+256, ... (VEC of them).
+// ---------------------------------------------------------------------------------------------
+template <bool BF16>
+__device__ __forceinline__ float half_bits_to_f32(uint32_t w, int hi)
+{
+    uint16_t b = (uint16_t)(hi ? (w >> 16) : (w & 0xffffu));
+    return BF16 ? bf16_to_f32(b) : f16_to_f32(b);
+}
+
+template <int VEC, int MODE, bool BF16>
+__global__ __launch_bounds__(256) void quant_dyn_row_kernel(const u32x4* __restrict__ x, u32x2* __restrict__ q,
+                                                            float* __restrict__ scale_out, uint32_t chunks)
+{
+    __shared__ float red[4];
+    const uint32_t row = blockIdx.x;
+    const uint32_t t = threadIdx.x;
+    const u32x4* xr = x + (size_t)row * chunks;
+    u32x4 v[VEC];
+    float amax = 0.0f;
+    h2 hmax = {(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+        uint32_t c = t + j * 256u;
+        if (c < chunks) v[j] = __builtin_nontemporal_load(xr + c);
+        else v[j] = (u32x4){0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+        uint32_t w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if constexpr (BF16) {
+                amax = __builtin_fmaxf(amax, __builtin_fabsf(half_bits_to_f32<true>(w4[e], 0)));
+                amax = __builtin_fmaxf(amax, __builtin_fabsf(half_bits_to_f32<true>(w4[e], 1)));
+            } else {
+                // |h| via the sign mask, packed f16 maxNum (NaN ignored, like the oracle)
+                h2 a = __builtin_bit_cast(h2, w4[e] & 0x7fff7fffu);
+                hmax = __builtin_elementwise_max(hmax, a);
+            }
+        }
+    }
+    if constexpr (!BF16) amax = __builtin_fmaxf((float)hmax.x, (float)hmax.y);
+    amax = wave_max(amax);
+    if ((t & 63u) == 0) red[t >> 6] = amax;
+    __syncthreads();
+    amax = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+    const float mult = amax > 0.0f ? 127.0f / amax : 0.0f;
+    if (t == 0) scale_out[row] = amax / 127.0f;
+    u32x2* qr = q + (size_t)row * chunks;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+        uint32_t c = t + j * 256u;
+        if (c >= chunks) break;
+        uint32_t w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        int32_t r[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            r[2 * e] = quant_s8<MODE>(half_bits_to_f32<BF16>(w4[e], 0) * mult);
+            r[2 * e + 1] = quant_s8<MODE>(half_bits_to_f32<BF16>(w4[e], 1) * mult);
+        }
+        u32x2 o = {pack4_s8(r[0], r[1], r[2], r[3]), pack4_s8(r[4], r[5], r[6], r[7])};
+        __builtin_nontemporal_store(o, qr + c);
+    }
+}
+
+// Generic dynamic per-token quant (any n, f16 / bf16 / f32 input): one workgroup per row, two passes
+// over the row (the second pass hits L2).
+template <int MODE>
+__global__ __launch_bounds__(256) void quant_dyn_generic_kernel(const void* __restrict__ x, int8_t* __restrict__ q,
+                                                                float* __restrict__ scale_out, uint32_t n,
+                                                                int src_type)
+{
+    __shared__ float red[4];
+    const uint32_t row = blockIdx.x;
+    const uint32_t t = threadIdx.x;
+    const int64_t base = (int64_t)row * n;
+    float amax = 0.0f;
+    for (uint32_t j = t; j < n; j += 256u) amax = __builtin_fmaxf(amax, __builtin_fabsf(load_f32_of(x, base + j, src_type)));
+    amax = wave_max(amax);
+    if ((t & 63u) == 0) red[t >> 6] = amax;
+    __syncthreads();
+    amax = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+    const float mult = amax > 0.0f ? 127.0f / amax : 0.0f;
+    if (t == 0) scale_out[row] = amax / 127.0f;
+    for (uint32_t j = t; j < n; j += 256u) q[base + j] = (int8_t)quant_s8<MODE>(load_f32_of(x, base + j, src_type) * mult);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Per-token quant with given fp32 scale / offset (policy API PER_TOKEN).
+// ---------------------------------------------------------------------------------------------
+template <int MODE, bool HAS_OFFSET>
+__global__ __launch_bounds__(256) void quant_per_token_kernel(const void* __restrict__ x, int8_t* __restrict__ q,
+                                                              const float* __restrict__ scale,
+                                                              const float* __restrict__ offset, int64_t total,
+                                                              uint32_t n, int src_type)
+{
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        int64_t row = i / n;
+        float v = load_f32_of(x, i, src_type) * scale[row];
+        if constexpr (HAS_OFFSET) v = v + offset[row];
+        q[i] = (int8_t)quant_s8<MODE>(v);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Legacy AscendQuant: half arithmetic.  t = half(x); t = t*s; t = t+o; q = sat_s8(rint(t)).
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quant_legacy_f16_kernel(const void* __restrict__ x, int8_t* __restrict__ q,
+                                                               const uint16_t* __restrict__ scale,
+                                                               const uint16_t* __restrict__ offset,
+                                                               uint16_t scale_scalar, uint16_t offset_scalar,
+                                                               int64_t total, uint32_t scale_count, int src_type)
+{
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        _Float16 xh = src_type == DT_F16 ? bits_h(((const uint16_t*)x)[i]) : (_Float16)(((const float*)x)[i]);
+        uint32_t c = scale_count ? (uint32_t)(i % scale_count) : 0u;
+        _Float16 s = bits_h(scale ? scale[c] : scale_scalar);
+        _Float16 o = bits_h(offset ? offset[c] : offset_scalar);
+        _Float16 t = xh * s;
+        t = t + o;
+        q[i] = (int8_t)quant_s8<RM_RINT>((float)t);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Dequant
+// ---------------------------------------------------------------------------------------------
+// Fast path: int8 [m, n] x fp32 scale[row] -> f16, n % 16 == 0.  16 elements per lane per step.
+__global__ __launch_bounds__(256) void dequant_i8_token_f16_kernel(const u32x4* __restrict__ q,
+                                                                   const float* __restrict__ scale,
+                                                                   u32x4* __restrict__ y, int64_t chunks,
+                                                                   uint32_t chunks_per_row)
+{
+    for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < chunks; c += (int64_t)gridDim.x * 256) {
+        const float s = scale[c / chunks_per_row];
+        u32x4 v = __builtin_nontemporal_load(q + c);
+        uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+        uint32_t o[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            int32_t w = (int32_t)w4[e];
+            float f0 = (float)((w << 24) >> 24) * s;
+            float f1 = (float)((w << 16) >> 24) * s;
+            float f2 = (float)((w << 8) >> 24) * s;
+            float f3 = (float)(w >> 24) * s;
+            o[2 * e] = (uint32_t)f32_to_f16_sat(f0) | ((uint32_t)f32_to_f16_sat(f1) << 16);
+            o[2 * e + 1] = (uint32_t)f32_to_f16_sat(f2) | ((uint32_t)f32_to_f16_sat(f3) << 16);
+        }
+        __builtin_nontemporal_store((u32x4){o[0], o[1], o[2], o[3]}, y + 2 * c);
+        __builtin_nontemporal_store((u32x4){o[4], o[5], o[6], o[7]}, y + 2 * c + 1);
+    }
+}
+
+// Generic: policy PER_CHANNEL (j < cal_count uses scale[j]), PER_TOKEN (scale[i]), PER_TENSOR (scalar).
+__global__ __launch_bounds__(256) void dequant_generic_kernel(void* __restrict__ y, int dst_type,
+                                                              const void* __restrict__ src, int src_type,
+                                                              const void* __restrict__ scale, int scale_type,
+                                                              float scale_scalar, int policy, uint32_t m, uint32_t n,
+                                                              uint32_t cols)
+{
+    const int64_t total = (int64_t)m * cols;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
+        int64_t i = t / cols, j = t % cols;
+        float s = policy == 1 ? load_f32_of(scale, j, scale_type)
+                              : (policy == 2 ? load_f32_of(scale, i, scale_type) : scale_scalar);
+        int64_t idx = i * n + j;
+        float v = load_f32_of(src, idx, src_type) * s;
+        store_cast(y, idx, v, dst_type);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// AscendAntiQuant (elementwise): dst = (q + offset) * scale
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ int32_t load_q(const void* src, int src_type, int64_t idx)
+{
+    if (src_type == DT_INT8) return ((const int8_t*)src)[idx];
+    uint8_t b = ((const uint8_t*)src)[idx >> 1];
+    int32_t nib = (idx & 1) ? (b >> 4) : (b & 0xf);
+    return nib >= 8 ? nib - 16 : nib;
+}
+
+__global__ __launch_bounds__(256) void antiquant_kernel(void* __restrict__ dst, int dst_type,
+                                                        const void* __restrict__ src, int src_type,
+                                                        const uint16_t* __restrict__ offset,
+                                                        const uint16_t* __restrict__ scale, uint32_t K, uint32_t N,
+                                                        uint32_t g, int is_transpose, int arith)
+{
+    const int64_t total = (int64_t)K * N;
+    const uint32_t G = K / g;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
+        // t enumerates dst in memory order
+        int64_t k, n;
+        if (is_transpose) { n = t / K; k = t % K; }
+        else { k = t / N; n = t % N; }
+        int64_t sidx = is_transpose ? n * G + k / g : (k / g) * N + n;
+        int32_t qv = load_q(src, src_type, t);
+        if (dst_type == DT_F16 && arith == 0) {
+            _Float16 w = (_Float16)(float)qv;
+            if (offset) w = w + bits_h(offset[sidx]);
+            w = w * bits_h(scale[sidx]);
+            ((uint16_t*)dst)[t] = h_bits(w);
+        } else {
+            float sc = load_f32_of(scale, sidx, dst_type);
+            float v = (float)qv;
+            if (offset) v = v + load_f32_of(offset, sidx, dst_type);
+            v = v * sc;
+            store_cast(dst, t, v, dst_type);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------------------------
+static int grid_for(int64_t items, int per_block = 256)
+{
+    int64_t b = (items + per_block - 1) / per_block;
+    int64_t cap = 256 * 8 * 4; // 8192 blocks: enough to fill 256 CUs several times over
+    if (b > cap) b = cap;
+    return (int)(b < 1 ? 1 : b);
+}
+
+template <int MODE>
+static hipError_t launch_dyn_row(const void* x, int8_t* q, float* s, uint32_t m, uint32_t chunks, bool bf16,
+                                 hipStream_t st)
+{
+    dim3 grid(m), block(256);
+#define ASCQ_DYN(V)                                                                                                   \
+    if (chunks <= 256u * V) {                                                                                         \
+        if (bf16) hipLaunchKernelGGL((quant_dyn_row_kernel<V, MODE, true>), grid, block, 0, st, (const u32x4*)x,     \
+                                     (u32x2*)q, s, chunks);                                                           \
+        else hipLaunchKernelGGL((quant_dyn_row_kernel<V, MODE, false>), grid, block, 0, st, (const u32x4*)x,         \
+                                (u32x2*)q, s, chunks);                                                                \
+        return hipGetLastError();                                                                                     \
+    }
+    ASCQ_DYN(1)
+    ASCQ_DYN(2)
+    ASCQ_DYN(4)
+    ASCQ_DYN(8)
+#undef ASCQ_DYN
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_quant_dynamic_per_token(int8_t* q, float* scale_out, const void* x, int src_type, uint32_t m,
+                                          uint32_t n, int round_mode, hipStream_t st)
+{
+    const bool half_src = (src_type == DT_F16 || src_type == DT_BF16);
+    const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0);
+    if (half_src && aligned && n % 8 == 0 && n <= 256u * 8u * 8u) {
+        uint32_t chunks = n / 8;
+        bool bf = src_type == DT_BF16;
+        switch (round_mode) {
+        case RM_FLOOR: return launch_dyn_row<RM_FLOOR>(x, q, scale_out, m, chunks, bf, st);
+        case RM_CEIL: return launch_dyn_row<RM_CEIL>(x, q, scale_out, m, chunks, bf, st);
+        case RM_ROUND: return launch_dyn_row<RM_ROUND>(x, q, scale_out, m, chunks, bf, st);
+        case RM_TRUNC: return launch_dyn_row<RM_TRUNC>(x, q, scale_out, m, chunks, bf, st);
+        default: return launch_dyn_row<RM_RINT>(x, q, scale_out, m, chunks, bf, st);
+        }
+    }
+    dim3 grid(m), block(256);
+    switch (round_mode) {
+#define ASCQ_G(MD) hipLaunchKernelGGL((quant_dyn_generic_kernel<MD>), grid, block, 0, st, x, q, scale_out, n, src_type); break;
+    case RM_FLOOR: ASCQ_G(RM_FLOOR)
+    case RM_CEIL: ASCQ_G(RM_CEIL)
+    case RM_ROUND: ASCQ_G(RM_ROUND)
+    case RM_TRUNC: ASCQ_G(RM_TRUNC)
+    default: ASCQ_G(RM_RINT)
+#undef ASCQ_G
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_quant_per_token(int8_t* q, const void* x, int src_type, const float* scale, const float* offset,
+                                  uint32_t m, uint32_t n, int round_mode, hipStream_t st)
+{
+    int64_t total = (int64_t)m * n;
+    dim3 grid(grid_for(total)), block(256);
+#define ASCQ_PT(MD)                                                                                                 \
+    if (offset) hipLaunchKernelGGL((quant_per_token_kernel<MD, true>), grid, block, 0, st, x, q, scale, offset,     \
+                                   total, n, src_type);                                                             \
+    else hipLaunchKernelGGL((quant_per_token_kernel<MD, false>), grid, block, 0, st, x, q, scale, offset, total, n, \
+                            src_type);                                                                              \
+    break;
+    switch (round_mode) {
+    case RM_FLOOR: ASCQ_PT(RM_FLOOR)
+    case RM_CEIL: ASCQ_PT(RM_CEIL)
+    case RM_ROUND: ASCQ_PT(RM_ROUND)
+    case RM_TRUNC: ASCQ_PT(RM_TRUNC)
+    default: ASCQ_PT(RM_RINT)
+    }
+#undef ASCQ_PT
+    return hipGetLastError();
+}
+
+hipError_t launch_quant_legacy(int8_t* q, const void* x, int src_type, const uint16_t* scale, const uint16_t* offset,
+                               uint16_t scale_scalar, uint16_t offset_scalar, uint32_t cal_count,
+                               uint32_t scale_count, hipStream_t st)
+{
+    dim3 grid(grid_for(cal_count)), block(256);
+    hipLaunchKernelGGL(quant_legacy_f16_kernel, grid, block, 0, st, x, q, scale, offset, scale_scalar, offset_scalar,
+                       (int64_t)cal_count, scale_count, src_type);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                          float scale_scalar, int policy, uint32_t m, uint32_t n, uint32_t cal_count, hipStream_t st)
+{
+    const bool fast = policy == 2 && src_type == DT_INT8 && dst_type == DT_F16 && scale_type == DT_F32 &&
+                      n % 16 == 0 && ((uintptr_t)src % 16 == 0) && ((uintptr_t)y % 16 == 0);
+    if (fast) {
+        int64_t chunks = (int64_t)m * n / 16;
+        dim3 grid(grid_for(chunks)), block(256);
+        hipLaunchKernelGGL(dequant_i8_token_f16_kernel, grid, block, 0, st, (const u32x4*)src, (const float*)scale,
+                           (u32x4*)y, chunks, n / 16);
+        return hipGetLastError();
+    }
+    uint32_t cols = policy == 1 ? cal_count : n;
+    dim3 grid(grid_for((int64_t)m * cols)), block(256);
+    hipLaunchKernelGGL(dequant_generic_kernel, grid, block, 0, st, y, dst_type, src, src_type, scale, scale_type,
+                       scale_scalar, policy, m, n, cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset,
+                            const void* scale, uint32_t K, uint32_t N, uint32_t g, int is_transpose, int arith,
+                            hipStream_t st)
+{
+    dim3 grid(grid_for((int64_t)K * N)), block(256);
+    hipLaunchKernelGGL(antiquant_kernel, grid, block, 0, st, dst, dst_type, src, src_type, (const uint16_t*)offset,
+                       (const uint16_t*)scale, K, N, g, is_transpose, arith);
+    return hipGetLastError();
+}
+
+}  // namespace ascq

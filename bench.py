@@ -1,0 +1,348 @@
+"""Benchmark of the MI355X quantized-inference hot path (one GPU).
+
+Headline (the JSON line's value): AscendQuant per-token dynamic quant f16 [8192, 8192] -> int8 + fp32 scale,
+then AscendDequant back to f16 -- one step = both ops over one batch, inputs resident in HBM.  value = whole-job
+algorithmic GB/s (6*M*N + 8*M bytes per step).  Buffers are rotated over more than the 256 MB Infinity Cache so
+the figure is HBM, not MALL, bandwidth.
+
+Also measured and reported under "other_configs": the W8A8 int8 Matmul + per-channel DEQF16 (128x512x256 and the
+8192^3 throughput shape), the W4A16 / W8A16 decode GEMV (M in {1, 16, 64}), the MoE group matmul and the MX-FP4
+8192^3 GEMM.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only headline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "asc-devkit_clone_amd"))
+
+METRIC = "int8/MXFP4 GEMM TOPS (%MFMA peak); antiquant GEMV + quant op HBM GB/s (%peak)"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0      # dense int8 MFMA, MI355X
+MXFP4_PEAK_TFLOPS = 10100.0  # dense fp4 MFMA, MI355X
+F16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 * 2 ** 20
+
+
+def rotation(bytes_per_set: int, minimum: int = 2) -> int:
+    return max(minimum, int(np.ceil(2.5 * MALL_BYTES / bytes_per_set)))
+
+
+def parse_traffic() -> dict:
+    """Per-launch HBM bytes measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (profiles/pmc_traffic.txt:
+    '<kernel-key> <bytes>' lines, copy-kernel calibrated)."""
+    p = ROOT / "profiles" / "pmc_traffic.txt"
+    out = {}
+    if p.exists():
+        for ln in p.read_text().splitlines():
+            ln = ln.strip()
+            if not ln or ln.startswith("#"):
+                continue
+            parts = ln.split()
+            if len(parts) >= 2:
+                try:
+                    out[parts[0]] = float(parts[1])
+                except ValueError:
+                    pass
+    return out
+
+
+class Timer:
+    """Per-kernel HIP event pairs on the stream the kernels are launched on (torch's current stream)."""
+
+    def __init__(self, torch, n):
+        self.torch = torch
+        self.ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(n)]
+
+    def ms(self, i):
+        return self.ev[i][0].elapsed_time(self.ev[i][1])
+
+
+def bench_headline(torch, ascq, steps, warmup):
+    M = N = 8192
+    bytes_quant = 2 * M * N + M * N + 4 * M
+    bytes_dequant = M * N + 4 * M + 2 * M * N
+    per_set = 2 * M * N + M * N + 4 * M + 2 * M * N
+    R = rotation(per_set)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(20261201)
+    xs, qs, ss, ys = [], [], [], []
+    for _ in range(R):
+        x = torch.randn((M, N), generator=g, device="cuda", dtype=torch.float32)
+        mask = torch.rand((M, N), generator=g, device="cuda") < 0.001
+        x = torch.where(mask, x * 50.0, x).to(torch.float16)
+        xs.append(x)
+        qs.append(torch.empty((M, N), dtype=torch.int8, device="cuda"))
+        ss.append(torch.empty((M,), dtype=torch.float32, device="cuda"))
+        ys.append(torch.empty((M, N), dtype=torch.float16, device="cuda"))
+    stream = torch.cuda.current_stream()
+
+    def step(i, ev=None):
+        r = i % R
+        if ev is not None:
+            ev[0][0].record(stream)
+        ascq.quant_dynamic_per_token(xs[r], out=qs[r], scale_out=ss[r])
+        if ev is not None:
+            ev[0][1].record(stream)
+            ev[1][0].record(stream)
+        ascq.ascend_dequant(qs[r], ss[r], ascq.PER_TOKEN, torch.float16, out=ys[r])
+        if ev is not None:
+            ev[1][1].record(stream)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    timers = [Timer(torch, 2) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        step(warmup + i, timers[i].ev)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = start.elapsed_time(end)
+    q_ms = float(np.mean([t.ms(0) for t in timers]))
+    d_ms = float(np.mean([t.ms(1) for t in timers]))
+    return dict(M=M, N=N, R=R, total_ms=total_ms, wall_s=wall, q_ms=q_ms, d_ms=d_ms, bytes_quant=bytes_quant,
+                bytes_dequant=bytes_dequant)
+
+
+def cpu_baseline_headline(budget_s=10.0):
+    """The oracle (C restatement, OpenMP) timed on the host: dynamic per-token quant + dequant over the
+    full 8192 x 8192 workload, repeated until ~budget_s seconds have been spent (min 2 reps)."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O
+
+    M = N = 8192
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((M, N), dtype=np.float32).astype(np.float16).view(np.uint16)
+    O.quant_dynamic_per_token(x[:64], O.F16)  # load + warm
+    reps, spent = 0, 0.0
+    while reps < 2 or spent < budget_s:
+        t0 = time.perf_counter()
+        q, s = O.quant_dynamic_per_token(x, O.F16)
+        O.dequant(q, O.INT8, s, O.F32, O.PER_TOKEN, O.F16)
+        spent += time.perf_counter() - t0
+        reps += 1
+    per = spent / reps
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return dict(value=(6 * M * N + 8 * M) / per / 1e9, unit="GB/s", cores=threads, kind="port",
+                sample=f"full 8192x8192 f16 workload, {reps} reps of quant+dequant ({spent:.1f} s), "
+                       f"oracle/ascq_oracle.c at -O3 -march=x86-64-v3 with {threads} OpenMP threads")
+
+
+# ----------------------------------------------------------------------------------------------
+# other configs (GPU only)
+# ----------------------------------------------------------------------------------------------
+def _time_loop(torch, fn, iters, warmup=3):
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(iters):
+        fn(i)
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters
+
+
+def bench_w8a8(torch, ascq, M, N, K, iters):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1)
+    per = M * K + K * N + 2 * M * N
+    R = rotation(per, 1) if M * N * K > 1e9 else 1
+    A = [torch.randint(-127, 128, (M, K), generator=g, device="cuda", dtype=torch.int8) for _ in range(R)]
+    B = [torch.randint(-127, 128, (K, N), generator=g, device="cuda", dtype=torch.int8) for _ in range(R)]
+    bias = torch.randint(-(1 << 15), 1 << 15, (N,), generator=g, device="cuda", dtype=torch.int32)
+    sc = torch.exp(torch.empty(N, device="cuda").uniform_(np.log(2.0 ** -12), np.log(2.0 ** -6), generator=g))
+    words = sc.view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    C = [torch.empty((M, N), dtype=torch.float16, device="cuda") for _ in range(R)]
+    mm = ascq.Matmul(ascq.INT8, ascq.INT8, ascq.F16, ascq.INT32)
+    mm.SetOrgShape(M, N, K)
+    mm.SetQuantVector(words)
+    mm.SetBias(bias)
+
+    def fn(i):
+        r = i % R
+        mm.SetTensorA(A[r])
+        mm.SetTensorB(B[r])
+        mm.IterateAll(C[r])
+
+    ms = _time_loop(torch, fn, iters)
+    tops = 2 * M * N * K / (ms * 1e-3) / 1e12
+    return dict(workload=f"W8A8 int8 Matmul + bias + per-channel DEQF16 -> f16, M={M} N={N} K={K}",
+                ms=ms, value=tops, unit="TOPS", frac_of_peak=tops / INT8_PEAK_TOPS)
+
+
+def bench_gemv(torch, ascq, w_type, M, iters):
+    K, N, grp = 4096, 11008, 128
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    wb = K * N // (2 if w_type == ascq.INT4 else 1)
+    R = rotation(wb)
+    wps = []
+    for _ in range(R):
+        wps.append(torch.randint(0, 256, (wb,), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8))
+    scale = torch.exp(torch.empty((K // grp, N), device="cuda").uniform_(np.log(1e-3), np.log(1e-1), generator=g)).half()
+    offset = torch.empty((K // grp, N), device="cuda").uniform_(-8, 8, generator=g).half()
+    x = torch.randn((M, K), generator=g, device="cuda").half()
+    y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+
+    def fn(i):
+        ascq.antiquant_matmul(x, wps[i % R], w_type, scale, offset, grp, N, out=y)
+
+    ms = _time_loop(torch, fn, iters)
+    bits = 4 if w_type == ascq.INT4 else 8
+    nbytes = K * N * bits // 8 + 2 * (K // grp) * N * 2 + 2 * M * K + 2 * M * N
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(workload=f"W{bits}A16 antiquant GEMV, M={M} K={K} N={N} g={grp}", ms=ms, value=gbs, unit="GB/s",
+                frac_of_peak=gbs / HBM_PEAK_GBS, tflops=2 * M * N * K / (ms * 1e-3) / 1e12)
+
+
+def bench_group(torch, ascq, iters):
+    G, T, K, N = 16, 4096, 4096, 1408
+    rng = np.random.default_rng(4)
+    p = 1.0 / (np.arange(1, G + 1) ** 1.1)
+    counts = rng.multinomial(T, p / p.sum())
+    offsets = torch.from_numpy(np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)).cuda()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    per = T * K + G * K * N + 2 * T * N
+    R = rotation(per)
+    xs = [torch.randint(-127, 128, (T, K), generator=g, device="cuda", dtype=torch.int8) for _ in range(R)]
+    ws = [torch.randint(-127, 128, (G, K, N), generator=g, device="cuda", dtype=torch.int8) for _ in range(R)]
+    pts = torch.rand(T, generator=g, device="cuda") * 0.01
+    scale = torch.rand((G, N), generator=g, device="cuda") * 0.01
+    y = torch.empty((T, N), dtype=torch.bfloat16, device="cuda")
+
+    def fn(i):
+        r = i % R
+        ascq.quant_group_matmul(xs[r], pts, ws[r], scale, offsets, 0, out=y)
+
+    ms = _time_loop(torch, fn, iters)
+    ops = 2 * T * K * N
+    nbytes = T * K + 4 * T + G * K * N + 4 * G * N + 2 * T * N + 8 * (G + 1)
+    tops = ops / (ms * 1e-3) / 1e12
+    attainable = min(INT8_PEAK_TOPS, ops / nbytes * HBM_PEAK_GBS / 1e3)
+    return dict(workload=f"MoE quant group matmul, {G} experts Zipf(1.1), T={T} K={K} N={N}, bf16 out",
+                ms=ms, value=tops, unit="TOPS", frac_of_peak=tops / INT8_PEAK_TOPS,
+                frac_of_attainable=tops / attainable, gbs=nbytes / (ms * 1e-3) / 1e9,
+                group_counts=[int(c) for c in counts])
+
+
+def bench_mx(torch, ascq, iters, trans_b=True):
+    M = N = K = 8192
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    A = torch.randint(0, 256, (M, K // 2), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8)
+    B = torch.randint(0, 256, (N, K // 2), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8)
+    sA = torch.randint(124, 129, (M, K // 32), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8)
+    sB = torch.randint(124, 129, (N, K // 32), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8)
+    C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    mm = ascq.Matmul(ascq.FP4_E2M1, ascq.FP4_E2M1, ascq.BF16, 0, ascq.E8M0)
+    mm.SetOrgShape(M, N, K)
+    mm.SetTensorA(A)
+    mm.SetTensorB(B, trans_b)
+    mm.SetTensorScaleA(sA, False)
+    mm.SetTensorScaleB(sB, True)
+
+    def fn(i):
+        mm.IterateAll(C)
+
+    ms = _time_loop(torch, fn, iters, warmup=2)
+    tf = 2 * M * N * K / (ms * 1e-3) / 1e12
+    return dict(workload=f"MX-FP4 E2M1/E8M0 GEMM {M}x{N}x{K}, fp32 acc, bf16 out, B given "
+                         + ("[N,K] (isTransposeB)" if trans_b else "[K,N] (transposed on the fly)"),
+                ms=ms, value=tf, unit="TFLOPS", frac_of_peak=tf / MXFP4_PEAK_TFLOPS)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="all", choices=["all", "headline"])
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build targets one MI355X; run with --gpus 1 (no multi-GPU path exists)"}))
+        return 2
+
+    import torch
+
+    import ascq
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.init()
+    h = bench_headline(torch, ascq, args.steps, args.warmup)
+    step_ms = h["total_ms"] / args.steps
+    step_bytes = h["bytes_quant"] + h["bytes_dequant"]
+    value = step_bytes / (step_ms * 1e-3) / 1e9
+    traffic = parse_traffic().get("quant_dyn_row_f16_8192x8192")
+    q_gbs = h["bytes_quant"] / (h["q_ms"] * 1e-3) / 1e9
+    rec = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16->int8 (fp32 scale arithmetic)",
+        "data": "synthetic: N(0,1) f16 with 0.1% outliers x50, seeded; "
+                f"{h['R']} rotating input/output sets (> 256 MB Infinity Cache)",
+        "config": {"workload": "AscendQuant per-token dynamic quant f16 [8192,8192] -> int8 + fp32 scale[8192], "
+                               "then AscendDequant -> f16", "rows": h["M"], "cols": h["N"],
+                   "round_mode": "rint", "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(q_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(q_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "quant_dyn_row_kernel (AscendQuant per-token dynamic)",
+                     "algorithmic_bytes_per_launch": h["bytes_quant"], "avg_launch_ms": round(h["q_ms"], 5)},
+        "dequant_kernel": {"achieved": round(h["bytes_dequant"] / (h["d_ms"] * 1e-3) / 1e9, 2), "unit": "GB/s",
+                           "avg_launch_ms": round(h["d_ms"], 5)},
+    }
+    if args.only == "all":
+        others = []
+        for fn in (lambda: bench_w8a8(torch, ascq, 128, 256, 512, 200),
+                   lambda: bench_w8a8(torch, ascq, 8192, 8192, 8192, 10),
+                   lambda: bench_gemv(torch, ascq, ascq.INT4, 1, 200),
+                   lambda: bench_gemv(torch, ascq, ascq.INT4, 16, 200),
+                   lambda: bench_gemv(torch, ascq, ascq.INT4, 64, 200),
+                   lambda: bench_gemv(torch, ascq, ascq.INT8, 1, 200),
+                   lambda: bench_gemv(torch, ascq, ascq.INT8, 16, 200),
+                   lambda: bench_gemv(torch, ascq, ascq.INT8, 64, 200),
+                   lambda: bench_group(torch, ascq, 20),
+                   lambda: bench_mx(torch, ascq, 10, True),
+                   lambda: bench_mx(torch, ascq, 5, False)):
+            try:
+                r = fn()
+                others.append({k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()})
+            except Exception as e:  # report, do not hide
+                others.append({"error": repr(e)})
+            torch.cuda.empty_cache()
+        rec["other_configs"] = others
+    if not args.no_cpu:
+        rec["cpu_baseline"] = cpu_baseline_headline()
+    print(json.dumps(rec))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,277 @@
+/*
+ * ascq.h -- C ABI of the MI355X (gfx950) quantized-inference library (libascq.so).
+ *
+ * The library re-implements, for one AMD Instinct MI355X, the quantized hot path of the
+ * Ascend C devkit (asc-devkit 9.3.0): the adv_api Matmul on int8 / fp8 / MX-FP4 operands
+ * with the fused dequant epilogue, AscendQuant / AscendDequant / AscendAntiQuant, the
+ * weight-only antiquant matmul and the quantized group matmul used for MoE.
+ *
+ * In the reference these are C++ templates instantiated inside a device kernel; here each
+ * becomes one host call that validates its arguments and enqueues hand-written HIP kernels
+ * on the caller's stream.  Each declaration names the reference interface it replaces
+ * (paths relative to the asc-devkit source tree).
+ *
+ * Conventions
+ *  - All tensor pointers are device pointers owned by the caller (the reference's
+ *    GlobalTensor is likewise a non-owning view, matmul_quant.asc:79-83).
+ *  - `stream` is a hipStream_t passed as void*; NULL is the default stream.  Calls are
+ *    stream-ordered and asynchronous.
+ *  - f16 / bf16 scalars are passed as their uint16_t bit patterns.
+ *  - Return codes: ASCQ_OK (0) or a negative ascq_status; invalid arguments are rejected on
+ *    the host before anything is launched (the reference's host tiling returns -1 on bad
+ *    input, impl/adv_api/tiling/matmul/matmul_tiling.cpp:26-33; its device-side checks,
+ *    impl/adv_api/detail/api_check/kernel_api_check.h:25-33, exist only in CPU debug).
+ *  - ascq_last_error() returns a text description of the last failure on this thread.
+ *  - Handles are not thread-safe; use one handle per host thread / stream.
+ */
+#ifndef ASCQ_H
+#define ASCQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t ascq_status;
+#define ASCQ_OK 0
+#define ASCQ_E_INVALID_ARG (-1) /* mirrors GetTiling's -1 (matmul_tiling.cpp:26-33) */
+#define ASCQ_E_UNSUPPORTED (-2) /* a dtype / layout / mode combination this build does not implement */
+#define ASCQ_E_HIP (-3)         /* a HIP runtime call failed (see ascq_last_error) */
+#define ASCQ_E_STATE (-4)       /* calls out of order, e.g. IterateAll before SetTensorA */
+
+/* Element types.  Mirrors the reference's device types (int8_t, int4b_t, half, bfloat16_t,
+ * fp8_e4m3fn_t, fp8_e5m2_t, fp4x2_e2m1_t, fp8_e8m0_t; include/basic_api/kernel_type.h and
+ * impl/adv_api/detail/matmul/utils/matmul_type_def.h:114-131). */
+typedef enum {
+    ASCQ_DT_INT8 = 1,
+    ASCQ_DT_UINT8 = 2,
+    ASCQ_DT_INT4 = 3,      /* int4b_t, two per byte, even element in the low nibble */
+    ASCQ_DT_INT32 = 4,
+    ASCQ_DT_F16 = 5,
+    ASCQ_DT_BF16 = 6,
+    ASCQ_DT_F32 = 7,
+    ASCQ_DT_U64 = 8,       /* uint64 deq-scale words (low 32 bits = fp32 scale) */
+    ASCQ_DT_FP8_E4M3 = 9,  /* fp8_e4m3fn_t */
+    ASCQ_DT_FP8_E5M2 = 10, /* fp8_e5m2_t */
+    ASCQ_DT_FP4_E2M1 = 11, /* fp4x2_e2m1_t, two per byte, even element in the low nibble */
+    ASCQ_DT_E8M0 = 12,     /* fp8_e8m0_t shared exponent */
+    ASCQ_DT_INT64 = 13
+} ascq_dtype;
+
+/* RoundMode (impl/basic_api/utils/kernel_utils_mode.h:103-118). NONE acts as RINT on lossy casts. */
+typedef enum {
+    ASCQ_ROUND_NONE = 0,
+    ASCQ_ROUND_RINT = 1,  /* half to even */
+    ASCQ_ROUND_FLOOR = 2,
+    ASCQ_ROUND_CEIL = 3,
+    ASCQ_ROUND_ROUND = 4, /* half away from zero */
+    ASCQ_ROUND_TRUNC = 5
+} ascq_round_mode;
+
+/* AscendQuantPolicy / AscendDeQuantPolicy (include/adv_api/quantization/ascend_quant_utils.h:74-81,
+ * ascend_dequant_utils.h:37) plus the legacy per-tensor / per-channel forms. */
+typedef enum {
+    ASCQ_POLICY_PER_TENSOR = 0,
+    ASCQ_POLICY_PER_CHANNEL = 1,
+    ASCQ_POLICY_PER_TOKEN = 2,
+    ASCQ_POLICY_PER_GROUP = 3
+} ascq_policy;
+
+/* Arithmetic of AscendAntiQuant: half ops (arch 2201, ascend_antiquant_impl.h:63-96) or fp32 ops
+ * with one final rint cast (bf16 output, ascend_antiquant_c220_impl.h:46-75; arch 3510 fp16 path). */
+typedef enum { ASCQ_ARITH_F16 = 0, ASCQ_ARITH_F32 = 1 } ascq_arith;
+
+/* ------------------------------------------------------------------------------------------
+ * Library
+ * ------------------------------------------------------------------------------------------ */
+const char* ascq_last_error(void);
+const char* ascq_version(void);
+/* Number of HIP devices visible (0 without a GPU); makes no other HIP call. */
+int32_t ascq_device_count(void);
+
+/* Pack an fp32 multiplier, a 9-bit offset and the sign flag into a QUANT_PRE word
+ * (docs/zh/api/SIMD-API/c_api/cube_datamove/cube_store_key_features/accompanying_quantization.md:79-103;
+ * the reference sample packs (uint64)(*(uint32*)&f), matmul_quant.asc:111-113).  Host only. */
+uint64_t ascq_pack_quant_pre(float m1, int32_t offset9, int32_t sign_flag);
+
+/* ------------------------------------------------------------------------------------------
+ * Matmul high-level API
+ * Replaces AscendC::Matmul<MatmulType<GM,ND,A>, <B>, <C>, <Bias>, CFG> and
+ * MatmulTypeWithScale (include/adv_api/matmul/matmul.h:54-400; matmul_intf.h:42-111;
+ * impl/adv_api/detail/matmul/utils/matmul_type_def.h:114-131) together with
+ * REGIST_MATMUL_OBJ / Init(TCubeTiling*) (matmul_intf.h:40).  One handle computes the whole
+ * singleShape block; the gfx950 tile decomposition replaces TCubeTiling.
+ *
+ * Supported type combinations (A, B, C, Bias) and epilogues:
+ *  int8, int8, f16,   int32   + SetQuantScalar/Vector -> DEQF16 / VDEQF16
+ *  int8, int8, bf16,  int32   + SetQuantScalar/Vector -> QS322BF16_PRE / VQS322BF16_PRE
+ *  int8, int8, int32, int32   (no quant)              -> raw int32 accumulators
+ *  f16,  int8|int4, f16, f32  + SetAntiQuantScalar/Vector (weight-only, optional groups)
+ *  fp4_e2m1, fp4_e2m1, bf16|f32 with E8M0 scales (SetTensorScaleA/B) -> MX block-scaled
+ * ------------------------------------------------------------------------------------------ */
+typedef struct ascq_matmul_s* ascq_matmul_t;
+
+/* CubeFormat of B (MatmulType<TPosition, CubeFormat, T>, impl/adv_api/detail/matmul/utils/matmul_type_def.h:40;
+ * CubeFormat include/adv_api/matmul/matmul_config.h:23-35):
+ * ND is the reference's row-major layout; PACKED is the output of ascq_weight_pack (weight-only only). */
+typedef enum { ASCQ_FORMAT_ND = 0, ASCQ_FORMAT_PACKED = 1 } ascq_format;
+
+typedef struct {
+    int32_t a_type;     /* ascq_dtype of A */
+    int32_t b_type;     /* ascq_dtype of B */
+    int32_t c_type;     /* ascq_dtype of C */
+    int32_t bias_type;  /* ascq_dtype of the bias (0 = no bias type) */
+    int32_t scale_type; /* ASCQ_DT_E8M0 for MX operands (MatmulTypeWithScale), else 0 */
+    int32_t b_format;   /* ascq_format of B */
+} ascq_matmul_types;
+
+/* REGIST_MATMUL_OBJ + Init (matmul_intf.h:40; matmul.h:79-95) */
+ascq_status ascq_matmul_create(const ascq_matmul_types* types, ascq_matmul_t* out);
+/* SetOrgShape(orgM, orgN, orgK) (matmul.h:94): full matrix shape; sets the leading dimensions */
+ascq_status ascq_matmul_set_org_shape(ascq_matmul_t h, int64_t m, int64_t n, int64_t k);
+/* SetSingleShape / SetTail (matmul.h:110, :117): the block this call computes (defaults to org shape) */
+ascq_status ascq_matmul_set_single_shape(ascq_matmul_t h, int64_t m, int64_t n, int64_t k);
+ascq_status ascq_matmul_set_tail(ascq_matmul_t h, int64_t tail_m, int64_t tail_n, int64_t tail_k);
+/* SetTensorA / SetTensorB (matmul.h:123-129; impl matmul_impl_base.h:560-638) */
+ascq_status ascq_matmul_set_tensor_a(ascq_matmul_t h, const void* a, int32_t is_transpose_a);
+ascq_status ascq_matmul_set_tensor_b(ascq_matmul_t h, const void* b, int32_t is_transpose_b);
+/* SetBias / DisableBias (matmul.h:134, :224) */
+ascq_status ascq_matmul_set_bias(ascq_matmul_t h, const void* bias);
+ascq_status ascq_matmul_disable_bias(ascq_matmul_t h);
+/* SetQuantScalar / SetQuantVector (matmul.h:175-185; quant_processor_fixpipe.h:74-117,209-234) */
+ascq_status ascq_matmul_set_quant_scalar(ascq_matmul_t h, uint64_t quant_scalar);
+ascq_status ascq_matmul_set_quant_vector(ascq_matmul_t h, const uint64_t* quant_vector /* [N] */);
+/* SetAntiQuantScalar / SetAntiQuantVector (matmul.h:161-170; antiquant_processor_using_ub.h:32-136).
+ * group_size 0 = per-channel vectors [N] (the reference's only form); group_size g > 0 = [K/g, N]
+ * vectors (per-group, an extension).  offset may be NULL (scale only). */
+ascq_status ascq_matmul_set_antiquant_scalar(ascq_matmul_t h, uint16_t offset_f16, uint16_t scale_f16);
+ascq_status ascq_matmul_set_antiquant_vector(ascq_matmul_t h, const void* offset, const void* scale,
+                                             int64_t group_size);
+/* SetTensorScaleA / SetTensorScaleB (mx_matmul_impl.h:136-188; examples/.../matmul_mx/matmul_mx.asc:194-203).
+ * scaleA: [M, sK] (transpose: [sK/2, M, 2]); scaleB: [sK/2, N, 2] (transpose: [N, sK]); sK = ceil(K/64)*2. */
+ascq_status ascq_matmul_set_tensor_scale_a(ascq_matmul_t h, const uint8_t* scale_a, int32_t is_transpose_scale_a);
+ascq_status ascq_matmul_set_tensor_scale_b(ascq_matmul_t h, const uint8_t* scale_b, int32_t is_transpose_scale_b);
+/* Optional device workspace for handles that need one (MX with a [K,N] B; W4/W8 with ND B):
+ * ascq_matmul_workspace_size() bytes.  Without it IterateAll allocates on first use. */
+ascq_status ascq_matmul_workspace_size(ascq_matmul_t h, size_t* bytes);
+ascq_status ascq_matmul_set_workspace(ascq_matmul_t h, void* workspace, size_t bytes);
+/* IterateAll(GlobalTensor<C>, enAtomic) (matmul.h:262; matmul_impl.h:119-137).  en_atomic must be 0. */
+ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic, void* stream);
+/* End (matmul.h:358): releases per-call bindings; the handle may be re-bound and reused */
+ascq_status ascq_matmul_end(ascq_matmul_t h);
+ascq_status ascq_matmul_destroy(ascq_matmul_t h);
+
+/* ------------------------------------------------------------------------------------------
+ * AscendQuant
+ * ------------------------------------------------------------------------------------------ */
+/* AscendQuantParam{m, n, calCount, groupSize} + AscendQuantConfig{hasOffset, kDim, roundMode}
+ * (include/adv_api/quantization/ascend_quant_utils.h:31-89) */
+typedef struct {
+    uint32_t m;
+    uint32_t n;
+    uint32_t cal_count;
+    uint32_t group_size;
+    int32_t has_offset;
+    int32_t kdim;
+    int32_t round_mode; /* ascq_round_mode */
+} ascq_quant_param;
+
+/* AscendQuant<int8_t, srcT, float, false, config, PER_TOKEN>(dst, src, scale[m], offset[m], para)
+ * (ascend_quant.h:714-777; impl ascend_quant_per_group_3510_impl.h:142-178, 1341-1367, 1455-1501).
+ * src_type: F16, BF16 or F32.  q = sat_s8(round(f32(x)*scale[row] (+offset[row]))).
+ * cal_count must be a multiple of n (ascend_quant_per_group_3510_impl.h:1476-1477); m = cal_count/n rows. */
+ascq_status ascq_ascend_quant_per_token(int8_t* dst, const void* src, int32_t src_type, const float* scale,
+                                        const float* offset, const ascq_quant_param* para, void* stream);
+/* Dynamic per-token quant: per-row absmax, multiplier 127/absmax, the PER_TOKEN quant above with that
+ * multiplier, and scale_out[row] = absmax/127 for the dequant.  (The reference leaves the absmax
+ * reduction to the caller; this entry point is that caller plus AscendQuant PER_TOKEN.) */
+ascq_status ascq_ascend_quant_dynamic_per_token(int8_t* dst, float* scale_out, const void* src,
+                                                int32_t src_type, uint32_t m, uint32_t n, int32_t round_mode,
+                                                void* stream);
+/* Legacy AscendQuant per-tensor / per-channel, half arithmetic (ascend_quant.h:64-293;
+ * impl ascend_quant_pre_impl.h:101-164, 320-483).  src_type F16 or F32.
+ * scale / offset: device half vectors of scale_count elements, or NULL to use the scalars
+ * (half bit patterns).  Element i uses scale[i % scale_count]; scale_count must divide cal_count. */
+ascq_status ascq_ascend_quant(int8_t* dst, const void* src, int32_t src_type, const uint16_t* scale,
+                              const uint16_t* offset, uint16_t scale_scalar, uint16_t offset_scalar,
+                              uint32_t cal_count, uint32_t scale_count, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * AscendDequant
+ * ------------------------------------------------------------------------------------------ */
+/* DequantParams{m, n, calCount} (ascend_dequant_utils.h:26-30) */
+typedef struct {
+    uint32_t m;
+    uint32_t n;
+    uint32_t cal_count;
+} ascq_dequant_param;
+
+/* AscendDequant<dstT, scaleT>(dst, src, deqScale, params) (ascend_dequant.h:59-122; impl
+ * ascend_dequant_common_impl.h:196-364, ascend_dequant_3510_impl.h:37-75) and the PER_TOKEN policy form
+ * (ascend_dequant.h:293-315; ascend_dequant_3510_impl.h:254-287).
+ *   policy PER_CHANNEL: dst[i][j] = cast(f32(src[i][j]) * scale[j]) for j < cal_count (other columns untouched)
+ *   policy PER_TOKEN:   dst[i][j] = cast(f32(src[i][j]) * scale[i])
+ *   policy PER_TENSOR:  dst[i][j] = cast(f32(src[i][j]) * scale_scalar)
+ * src_type INT32 (the reference's type) or INT8 (widened on load); dst_type F16, BF16 or F32;
+ * scale_type F32, F16, BF16 or U64 (low 32 bits).  cast = round to nearest even, saturating. */
+ascq_status ascq_ascend_dequant(void* dst, int32_t dst_type, const void* src, int32_t src_type, const void* scale,
+                                int32_t scale_type, float scale_scalar, int32_t policy,
+                                const ascq_dequant_param* params, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * AscendAntiQuant
+ * ------------------------------------------------------------------------------------------ */
+/* AscendAntiQuant<InputDataType, OutputDataType, isTranspose>(dst, src, offset, scale, tmp, K, shapeInfo)
+ * (include/adv_api/quantization/ascend_antiquant.h:47-225; AntiQuantShapeInfo ascend_antiquant_utils.h:26-31;
+ * impl ascend_antiquant_impl.h:48-96, 285-411, ascend_antiquant_c220_impl.h:46-100).
+ *   dst = (src + offset) * scale.  src_type INT8 or INT4; dst_type F16 or BF16 (offset/scale are dst_type).
+ *   is_transpose 0: src [K, N], offset/scale [K/group, N];  1: src [N, K], offset/scale [N, K/group].
+ *   group_size 0 = per-channel ([1, N] / [N, 1]).  offset NULL = scale only.  arith: ascq_arith
+ *   (BF16 output always uses fp32 arithmetic). */
+ascq_status ascq_ascend_antiquant(void* dst, int32_t dst_type, const void* src, int32_t src_type,
+                                  const void* offset, const void* scale, uint32_t k, uint32_t n,
+                                  uint32_t group_size, int32_t is_transpose, int32_t arith, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Weight-only antiquant matmul (W8A16 / W4A16)
+ * The reference composes AscendAntiQuant (per group) with a half Matmul (fp32 L0C, half out);
+ * here one fused kernel dequantises B in registers and feeds fp16 MFMA.
+ * ------------------------------------------------------------------------------------------ */
+/* Bytes of the packed B for a [K, N] weight of w_type INT8 or INT4 (K % 128 == 0, N % 16 == 0). */
+ascq_status ascq_weight_pack_size(int32_t w_type, int64_t k, int64_t n, size_t* bytes);
+/* Repack a row-major weight (is_transpose 0: [K, N]; 1: [N, K]) into the MFMA-native tile layout used by
+ * ascq_antiquant_matmul -- the counterpart of the reference's ND -> NZ weight conversion
+ * (examples/01_simd_cpp_api/05_best_practices/03_fusion_compute/quant_group_matmul_high_performance/
+ * scripts/gen_data.py:62; layout described in asc-devkit_clone_amd/csrc/gemv_antiquant.hip).
+ * Device to device, on `stream`. */
+ascq_status ascq_weight_pack(void* packed, const void* w, int32_t w_type, int64_t k, int64_t n,
+                             int32_t is_transpose, void* stream);
+/* y[M,N] (f16) = x[M,K] (f16) @ antiquant(w_packed) with fp32 accumulation: AscendAntiQuant per group
+ * (ascend_antiquant_impl.h:63-96, 366-411) fused with a half Matmul whose L0C is fp32
+ * (impl/adv_api/detail/matmul/utils/matmul_utils.h:171-174).
+ * scale/offset: f16 [K/group_size, N]; offset may be NULL; group_size a multiple of 32 dividing K,
+ * or 0 for per-channel [1, N].  M >= 1 (any value; decode shapes M in {1..64} are the fast path). */
+ascq_status ascq_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w_packed, int32_t w_type,
+                                  const uint16_t* scale, const uint16_t* offset, int64_t group_size, int64_t m,
+                                  int64_t n, int64_t k, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Quantized group matmul (MoE)
+ * Replaces quant_group_matmul_custom (examples/01_simd_cpp_api/05_best_practices/03_fusion_compute/
+ * quant_group_matmul_high_performance/quant_group_matmul_custom.asc:89-452, formula README_en.md:36-60):
+ *   for group g, rows [s_g, s_g + cnt_g):  y = cast( (f32(x_g @ W_g) * scale[g, n]) * per_token_scale[m] )
+ * x int8 [M, K]; per_token_scale f32 [M]; w int8 [G, K, N] (w_trans: [G, N, K]); scale f32 [G, N];
+ * group_list int64 on the device: list_type 0 = G+1 prefix offsets, 1 = G counts (the reference form,
+ * :263).  Rows outside every group are not written.  out_type BF16 or F16.  No activation is applied.
+ * ------------------------------------------------------------------------------------------ */
+ascq_status ascq_quant_group_matmul(void* y, int32_t out_type, const int8_t* x, const float* per_token_scale,
+                                    const int8_t* w, int32_t w_trans, const float* scale,
+                                    const int64_t* group_list, int32_t list_type, int64_t num_groups, int64_t m,
+                                    int64_t k, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ASCQ_H */

@@ -1,0 +1,587 @@
+/*
+ * ascq_oracle.c -- CPU restatement of the asc-devkit quantized-inference arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker, and bench.py's CPU baseline).  The
+ * product library never links or calls this file.  See ascq_oracle.h for the
+ * numeric conventions; each function below cites the reference lines it follows.
+ *
+ * Build: oracle/Makefile (gcc -O3 -march=x86-64-v3 -fopenmp -ffp-contract=off).
+ */
+#include "ascq_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ------------------------------------------------------------------------ */
+/* scalar codecs                                                             */
+/* ------------------------------------------------------------------------ */
+
+/* IEEE binary32 -> binary16, round to nearest even.  sat != 0 clamps overflow (and +-inf) to +-65504,
+ * the saturating conversion of docs/zh/api/SIMD-API/basic_api/data_structures/precision_conversion.md:30
+ * ("overflow is handled in saturation mode by default") and the DEQF16 boundary rule of
+ * docs/zh/api/appendix/matrix_compute_move_out_interface_boundary_value_summary.md:104. */
+uint16_t oq_f32_to_f16(float x, int sat)
+{
+    uint32_t u = f2u(x);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu)); /* NaN, quieted */
+    if (a >= 0x477ff000u) return (uint16_t)(sign | (sat ? 0x7bffu : 0x7c00u));    /* >= 65520 or inf */
+    if (a >= 0x38800000u) {                                                       /* normal result */
+        uint32_t r = a + 0xfffu + ((a >> 13) & 1u);
+        return (uint16_t)(sign | ((r - 0x38000000u) >> 13));
+    }
+    /* subnormal / zero result: |x| * 2^24 is exact; rint under the default (nearest-even) mode */
+    float m = rintf(u2f(a) * 16777216.0f);
+    return (uint16_t)(sign | (uint16_t)m); /* m == 1024 becomes the smallest normal, as it should */
+}
+
+float oq_f16_to_f32(uint16_t h)
+{
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    if (e == 0) {
+        float v = (float)m * (1.0f / 16777216.0f); /* exact */
+        return sign ? -v : v;
+    }
+    if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+/* binary32 -> bfloat16, round to nearest even (CAST_RINT, ascend_dequant_common_impl.h:196-206) */
+uint16_t oq_f32_to_bf16(float x, int sat)
+{
+    uint32_t u = f2u(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    if ((u & 0x7fffffffu) == 0x7f800000u) return (uint16_t)(sat ? ((u >> 16) & 0x8000u) | 0x7f7fu : (u >> 16));
+    uint32_t r = u + 0x7fffu + ((u >> 16) & 1u);
+    uint16_t b = (uint16_t)(r >> 16);
+    if (sat && (b & 0x7fffu) == 0x7f80u) b = (uint16_t)((b & 0x8000u) | 0x7f7fu);
+    return b;
+}
+
+float oq_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* binary64 -> binary16 / bfloat16 with one round-to-nearest-even (used where the exact value of a half op
+ * or of an exact dot product is held in a double, so that no double rounding through fp32 occurs) */
+uint16_t oq_f64_to_f16(double d, int sat)
+{
+    if (d != d) return 0x7e00u;
+    uint16_t sign = signbit(d) ? 0x8000u : 0u;
+    double a = fabs(d);
+    if (a >= 65520.0) return (uint16_t)(sign | (sat ? 0x7bffu : 0x7c00u));
+    int e;
+    frexp(a, &e);              /* a in [2^(e-1), 2^e) */
+    int q = e - 11;            /* ulp of an 11-bit significand in that binade */
+    if (q < -24) q = -24;      /* subnormal spacing */
+    double v = ldexp(nearbyint(ldexp(a, -q)), q);
+    return (uint16_t)(sign | oq_f32_to_f16((float)v, 0)); /* v is a binary16 value: exact */
+}
+
+uint16_t oq_f64_to_bf16(double d, int sat)
+{
+    if (d != d) return 0x7fc0u;
+    uint16_t sign = signbit(d) ? 0x8000u : 0u;
+    double a = fabs(d);
+    if (a >= ldexp(511.0, 119)) return (uint16_t)(sign | (sat ? 0x7f7fu : 0x7f80u)); /* (2-2^-8)*2^127 */
+    int e;
+    frexp(a, &e);
+    int q = e - 8;
+    if (q < -133) q = -133;
+    double v = ldexp(nearbyint(ldexp(a, -q)), q);
+    return (uint16_t)(sign | oq_f32_to_bf16((float)v, 0));
+}
+
+/* QUANT_PRE M1: bits 13..31 hold a (1,8,10) float; the low 13 bits do not take part
+ * (accompanying_quantization.md:79-103, table "M1"; gen_data_s322f16.py:38-52 decodes the same field) */
+float oq_quant_pre_m1(uint64_t word) { return u2f((uint32_t)(word & 0xFFFFE000u)); }
+
+/* host packing used by the reference sample: (uint64)(*(uint32*)&f) (matmul_quant.asc:111-113), plus the
+ * 9-bit offset at bits 37..45 and the sign flag at bit 46 (accompanying_quantization.md table 1/2) */
+uint64_t oq_pack_quant_pre(float m1, int32_t offset9, int32_t sign)
+{
+    return (uint64_t)f2u(m1) | ((uint64_t)((uint32_t)offset9 & 0x1ffu) << 37) | ((uint64_t)(sign & 1) << 46);
+}
+
+/* RoundMode semantics of Cast.md "RoundMode" table; NaN converts to 0, results clamp to int32 */
+int32_t oq_round_to_int(float v, int mode)
+{
+    if (v != v) return 0;
+    float r;
+    switch (mode) {
+    case OQ_ROUND_FLOOR: r = floorf(v); break;
+    case OQ_ROUND_CEIL: r = ceilf(v); break;
+    case OQ_ROUND_ROUND: r = roundf(v); break; /* half away from zero */
+    case OQ_ROUND_TRUNC: r = truncf(v); break;
+    default: r = rintf(v); break;              /* NONE / RINT: half to even */
+    }
+    if (r >= 2147483647.0f) return 2147483647;
+    if (r <= -2147483648.0f) return (int32_t)0x80000000u;
+    return (int32_t)r;
+}
+
+int8_t oq_sat_s8(int32_t v) { return (int8_t)(v > 127 ? 127 : (v < -128 ? -128 : v)); }
+
+/* OCP MX v1.0 E2M1: sign | 2-bit exponent (bias 1) | 1-bit mantissa; exact values
+ * {0, .5, 1, 1.5, 2, 3, 4, 6} (precision_conversion.md "fp4x2_e2m1_t -> bfloat16_t": lossless) */
+float oq_e2m1_decode(uint8_t nib)
+{
+    static const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+    float v = mag[nib & 7u];
+    return (nib & 8u) ? -v : v;
+}
+
+/* nearest E2M1 code, ties to the even code, saturating at 6 (OCP MX v1.0 section 5.3 conversion) */
+uint8_t oq_e2m1_encode_rne(float x)
+{
+    uint8_t s = (f2u(x) >> 31) ? 8u : 0u;
+    float a = fabsf(x);
+    if (a != a) return 0;
+    /* midpoints between consecutive magnitudes; at a tie pick the code with an even mantissa bit */
+    static const float mid[7] = {0.25f, 0.75f, 1.25f, 1.75f, 2.5f, 3.5f, 5.0f};
+    uint8_t c = 0;
+    while (c < 7 && a > mid[c]) ++c;
+    if (c < 7 && a == mid[c] && (c & 1u)) ++c; /* tie: code c is odd -> go to c+1 (even) */
+    return (uint8_t)(s | c);
+}
+
+/* E8M0: 2^(e-127); 0xFF is NaN (OCP MX v1.0 section 5.4) */
+float oq_e8m0_decode(uint8_t e)
+{
+    if (e == 0xFFu) return u2f(0x7fc00000u);
+    if (e == 0) return u2f(0x00400000u); /* 2^-127, a float subnormal */
+    return u2f((uint32_t)e << 23);
+}
+
+/* shared exponent = floor(log2(amax)) - emax(E2M1)=2, clamped to [0,254]; amax == 0 gives 127 */
+uint8_t oq_mx_shared_exp(float amax)
+{
+    if (!(amax > 0.0f)) return 127u;
+    int e = (int)((f2u(amax) >> 23) & 0xffu);
+    if (e == 0) return 0u; /* subnormal amax: floor(log2) - 2 is below the e8m0 range */
+    int se = e - 2;
+    if (se < 0) se = 0;
+    if (se > 254) se = 254;
+    return (uint8_t)se;
+}
+
+/* fp8: fmt OQ_FP8_E4M3 (e4m3fn: bias 7, no inf, 0x7f/0xff NaN) or OQ_FP8_E5M2 (bias 15, IEEE inf/NaN) */
+float oq_fp8_decode(uint8_t v, int fmt)
+{
+    int s = v >> 7;
+    float r;
+    if (fmt == OQ_FP8_E4M3) {
+        int e = (v >> 3) & 0xf, m = v & 7;
+        if (e == 15 && m == 7) return u2f(0x7fc00000u);
+        r = e ? ldexpf(1.0f + m / 8.0f, e - 7) : ldexpf(m / 8.0f, -6);
+    } else {
+        int e = (v >> 2) & 0x1f, m = v & 3;
+        if (e == 31) return m ? u2f(0x7fc00000u) : (s ? -INFINITY : INFINITY);
+        r = e ? ldexpf(1.0f + m / 4.0f, e - 15) : ldexpf(m / 4.0f, -14);
+    }
+    return s ? -r : r;
+}
+
+static inline float load_as_f32(const void* p, int type, int64_t i)
+{
+    switch (type) {
+    case OQ_F16: return oq_f16_to_f32(((const uint16_t*)p)[i]);
+    case OQ_BF16: return oq_bf16_to_f32(((const uint16_t*)p)[i]);
+    case OQ_F32: return ((const float*)p)[i];
+    case OQ_INT32: return (float)((const int32_t*)p)[i]; /* rne, exact below 2^24 */
+    case OQ_INT8: return (float)((const int8_t*)p)[i];
+    case OQ_U64: return u2f((uint32_t)(((const uint64_t*)p)[i] & 0xffffffffu)); /* low half of the word */
+    default: return 0.0f;
+    }
+}
+
+static inline void store_from_f32(void* p, int type, int64_t i, float v)
+{
+    switch (type) {
+    case OQ_F16: ((uint16_t*)p)[i] = oq_f32_to_f16(v, 1); break;
+    case OQ_BF16: ((uint16_t*)p)[i] = oq_f32_to_bf16(v, 1); break;
+    case OQ_F32: ((float*)p)[i] = v; break;
+    default: break;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Matmul int8 x int8 -> int32 (+bias)                                       */
+/* ------------------------------------------------------------------------ */
+
+/* acc[m,n] = sum_k A[m,k]*B[k,n] + bias[n] in int32 (MmadCompute with isBias,
+ * impl/adv_api/detail/matmul/stage/compute/mmad_compute.h:40-90; L0C type int32 for int8 inputs,
+ * impl/adv_api/detail/matmul/utils/matmul_utils.h:134-175).  The sum is formed in int64 and wrapped. */
+void oq_matmul_i8(const int8_t* A, const int8_t* B, const int32_t* bias, int32_t* C,
+                  int64_t M, int64_t N, int64_t K, int transA, int transB)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m) {
+        int64_t* row = (int64_t*)calloc((size_t)N, sizeof(int64_t));
+        for (int64_t k = 0; k < K; ++k) {
+            int64_t a = transA ? A[k * M + m] : A[m * K + k];
+            if (!a) continue;
+            if (!transB) {
+                const int8_t* b = B + k * N;
+                for (int64_t n = 0; n < N; ++n) row[n] += a * b[n];
+            } else {
+                for (int64_t n = 0; n < N; ++n) row[n] += a * B[n * K + k];
+            }
+        }
+        for (int64_t n = 0; n < N; ++n) {
+            int64_t v = row[n] + (bias ? bias[n] : 0);
+            C[m * N + n] = (int32_t)(uint32_t)(uint64_t)v;
+        }
+        free(row);
+    }
+}
+
+/* DEQF16 / VDEQF16 (int32 -> half) and QS322BF16_PRE / VQS322BF16_PRE (int32 -> bf16):
+ * out = sat(rne(f32(acc) * M1)), M1 from the QUANT_PRE word; modes chosen in
+ * impl/adv_api/detail/matmul/stage/copy_cube_out/quant/quant_processor_fixpipe.h:89-117,209-234.
+ * The product is one fp32 multiply (documented choice; the fixpipe's internal width is not public). */
+void oq_mm_dequant(const int32_t* acc, void* out, int out_type, int64_t M, int64_t N,
+                   const uint64_t* qvec, uint64_t qscalar)
+{
+    float ms = oq_quant_pre_m1(qscalar);
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; ++n) {
+            float m1 = qvec ? oq_quant_pre_m1(qvec[n]) : ms;
+            float v = (float)acc[m * N + n] * m1;
+            store_from_f32(out, out_type, m * N + n, v);
+        }
+}
+
+/* fp8 operands: L0C is fp32 (matmul_utils.h:134-175), epilogue (V)QF322{F16,BF16,F32}_PRE
+ * (quant_processor_fixpipe.h:101-115): out = cast(acc_f32 * M1).  The product sum is exact in double and
+ * rounded once to fp32 here; the device accumulates in fp32, so this path is compared within a tolerance. */
+void oq_matmul_fp8(const uint8_t* A, const uint8_t* B, int a_fmt, int b_fmt, void* out, int out_type,
+                   int64_t M, int64_t N, int64_t K, int transA, int transB,
+                   const uint64_t* qvec, uint64_t qscalar, double* exact_out)
+{
+    float ms = oq_quant_pre_m1(qscalar);
+    int use_q = (qvec != NULL) || (qscalar != 0);
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; ++n) {
+            double s = 0.0;
+            for (int64_t k = 0; k < K; ++k) {
+                double a = oq_fp8_decode(transA ? A[k * M + m] : A[m * K + k], a_fmt);
+                double b = oq_fp8_decode(transB ? B[n * K + k] : B[k * N + n], b_fmt);
+                s += a * b;
+            }
+            if (exact_out) exact_out[m * N + n] = s;
+            float v = (float)s;
+            if (use_q) v = v * (qvec ? oq_quant_pre_m1(qvec[n]) : ms);
+            store_from_f32(out, out_type, m * N + n, v);
+        }
+}
+
+/* ------------------------------------------------------------------------ */
+/* AscendQuant                                                               */
+/* ------------------------------------------------------------------------ */
+
+/* PER_TOKEN, int8 output, fp32 scale (policy API include/adv_api/quantization/ascend_quant.h:714-777):
+ * QuantPerTokenForS8VF (impl/adv_api/detail/quantization/quant/ascend_quant_per_group_3510_impl.h:142-178)
+ * casts x to fp32, Mul by the row scale, Add the row offset (fp32), then TransRegForS8
+ * (ascend_quant_3510_impl.h:958-968): fp32 -> s16 (round mode, SAT) -> f16 -> s8 (SAT).  The s16 and f16
+ * steps are exact for every value that does not saturate to int8, so the result is sat_s8(round(v)). */
+void oq_quant_per_token(int8_t* dst, const void* src, int src_type, const float* scale, const float* offset,
+                        int64_t m, int64_t n, int round_mode)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < m; ++i) {
+        float s = scale[i];
+        float o = offset ? offset[i] : 0.0f;
+        for (int64_t j = 0; j < n; ++j) {
+            float v = load_as_f32(src, src_type, i * n + j) * s;
+            if (offset) v = v + o;
+            int32_t r = oq_round_to_int(v, round_mode);
+            if (r > 32767) r = 32767;
+            if (r < -32768) r = -32768;
+            dst[i * n + j] = oq_sat_s8(r);
+        }
+    }
+}
+
+/* Dynamic per-token quant (config "AscendQuant per-token dynamic"): the absmax reduction is the caller's
+ * job in the reference (no ReduceMax in impl/adv_api/detail/quantization); this restatement defines it as
+ * absmax = max |f32(x)| over the row (NaN ignored), multiplier = 127/absmax (one fp32 division, 0 when
+ * absmax == 0), scale_out = absmax/127, then the PER_TOKEN quant above with the multiplier as its scale. */
+void oq_quant_dynamic_per_token(int8_t* dst, float* scale_out, const void* src, int src_type,
+                                int64_t m, int64_t n, int round_mode)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < m; ++i) {
+        float amax = 0.0f;
+        for (int64_t j = 0; j < n; ++j) {
+            float a = fabsf(load_as_f32(src, src_type, i * n + j));
+            if (a > amax) amax = a;
+        }
+        float mult = amax > 0.0f ? 127.0f / amax : 0.0f;
+        scale_out[i] = amax / 127.0f;
+        for (int64_t j = 0; j < n; ++j) {
+            float v = load_as_f32(src, src_type, i * n + j) * mult;
+            dst[i * n + j] = oq_sat_s8(oq_round_to_int(v, round_mode));
+        }
+    }
+}
+
+/* Legacy AscendQuant (per-tensor / per-channel) in fp16 arithmetic, arch 2201:
+ * AscendQuantPerChannelIntrinsicsImpl (impl/adv_api/detail/quantization/quant/ascend_quant_pre_impl.h:101-164):
+ * fp32 input is first Cast to half (CAST_NONE = rint), then Mul (half), Add/Adds offset (half), then
+ * Cast<int8_t, half>(CAST_NONE) which rounds half-to-even and saturates (Cast.md:92, precision_conversion.md:30).
+ * Element i uses scale[i % scale_count] (scaleCount divides calCount, ascend_quant_common_impl.h:132-188).
+ * The half ops are IEEE binary16 with one rounding each; the product of two halves is exact in fp32 and the
+ * sum of two halves is exact in fp64, so one rounding to binary16 reproduces each op. */
+void oq_quant_legacy_f16(int8_t* dst, const void* src, int src_type, const uint16_t* scale_vec,
+                         uint16_t scale_scalar, const uint16_t* offset_vec, uint16_t offset_scalar,
+                         int64_t cal_count, int64_t scale_count)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < cal_count; ++i) {
+        uint16_t xh = src_type == OQ_F16 ? ((const uint16_t*)src)[i] : oq_f32_to_f16(((const float*)src)[i], 0);
+        int64_t c = scale_count > 0 ? i % scale_count : 0;
+        uint16_t sh = scale_vec ? scale_vec[c] : scale_scalar;
+        uint16_t oh = offset_vec ? offset_vec[c] : offset_scalar;
+        uint16_t t = oq_f64_to_f16((double)oq_f16_to_f32(xh) * (double)oq_f16_to_f32(sh), 0);
+        uint16_t u = oq_f64_to_f16((double)oq_f16_to_f32(t) + (double)oq_f16_to_f32(oh), 0);
+        float tv = oq_f16_to_f32(u);
+        dst[i] = oq_sat_s8(oq_round_to_int(tv, OQ_ROUND_RINT));
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* AscendDequant                                                             */
+/* ------------------------------------------------------------------------ */
+
+/* dst = cast(f32(src) * f32(scale)), cast = rne + sat:
+ *  - PER_CHANNEL (legacy DequantParams{m, n, calCount}): dst[i][j] for j < calCount uses scale[j]
+ *    (include/adv_api/quantization/ascend_dequant.h:38-72, v220 impl ascend_dequant_common_impl.h:196-364,
+ *    3510 DequantPerchannelVFImpl ascend_dequant_3510_impl.h:37-75); columns >= calCount are not written.
+ *    A uint64 deqScale uses the low 32 bits as the fp32 scale ("only half of uint64_t is used", :62-64).
+ *  - PER_TENSOR: scalar deqScale (AscendDequantScalarImpl, ascend_dequant.h:278-291).
+ *  - PER_TOKEN (policy API, ascend_dequant.h:293-315): scale[i] broadcast along the row,
+ *    DeQuantPerTokenForS32VF (ascend_dequant_3510_impl.h:254-287): int32 -> fp32, Mul, cast RINT/SAT.
+ * int8 sources are widened to int32 first (exact).  int32 -> fp32 rounds to nearest: v220 uses RINT, 3510
+ * uses round-half-away (MrgZRndA); both are exact below 2^24 and the restatement uses RINT. */
+void oq_dequant(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                float scale_scalar, int policy, int64_t m, int64_t n, int64_t cal_count)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < m; ++i) {
+        int64_t cols = policy == OQ_PER_CHANNEL ? cal_count : n;
+        for (int64_t j = 0; j < cols; ++j) {
+            float s;
+            if (policy == OQ_PER_CHANNEL) s = load_as_f32(scale, scale_type, j);
+            else if (policy == OQ_PER_TOKEN) s = load_as_f32(scale, scale_type, i);
+            else s = scale_scalar;
+            float v = load_as_f32(src, src_type, i * n + j) * s;
+            store_from_f32(dst, dst_type, i * n + j, v);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* AscendAntiQuant                                                           */
+/* ------------------------------------------------------------------------ */
+
+static inline int32_t load_q(const void* src, int src_type, int64_t idx)
+{
+    if (src_type == OQ_INT8) return ((const int8_t*)src)[idx];
+    /* int4b_t packed two per byte, the even element in the low nibble
+     * (examples/01_simd_cpp_api/04_advanced_api/00_matmul/matmul_int4/scripts/gen_data.py packing) */
+    uint8_t byte = ((const uint8_t*)src)[idx >> 1];
+    int32_t nib = (idx & 1) ? (byte >> 4) : (byte & 0xf);
+    return nib >= 8 ? nib - 16 : nib;
+}
+
+/* dst = scale * (src + offset) (include/adv_api/quantization/ascend_antiquant.h:36-46):
+ *  - ARITH_F16 (fp16 output, arch 2201): AntiQuantInnerLoop (impl/adv_api/detail/quantization/antiquant/
+ *    ascend_antiquant_impl.h:63-96): Cast int->half (exact), Add offset (half), Mul scale (half);
+ *  - ARITH_F32: cast to fp32, Add, Mul in fp32, Cast RINT to the output type
+ *    (bf16: ascend_antiquant_c220_impl.h:46-75; 3510 scalar path ascend_antiquant_3510_impl.h:320-330).
+ * Layout (ascend_antiquant_impl.h:366-411 and the no-transpose path :285-330):
+ *  is_transpose == 0: src [K, N], offset/scale [K/group, N] (group == K: per-channel [1, N]);
+ *  is_transpose == 1: src [N, K], offset/scale [N, K/group] (AntiQuantShapeInfo, ascend_antiquant_utils.h:26-31).
+ * offset == NULL means no offset (the scale-only overloads). */
+void oq_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset, const void* scale,
+                  int64_t K, int64_t N, int64_t group_size, int is_transpose, int arith)
+{
+    int64_t G = group_size > 0 ? K / group_size : 1;
+    int64_t g = group_size > 0 ? group_size : K;
+#pragma omp parallel for schedule(static)
+    for (int64_t k = 0; k < K; ++k)
+        for (int64_t n = 0; n < N; ++n) {
+            int64_t idx = is_transpose ? n * K + k : k * N + n;
+            int64_t sidx = is_transpose ? n * G + k / g : (k / g) * N + n;
+            int32_t q = load_q(src, src_type, idx);
+            float sc = load_as_f32(scale, dst_type, sidx);
+            float of = offset ? load_as_f32(offset, dst_type, sidx) : 0.0f;
+            if (arith == OQ_ARITH_F16 && dst_type == OQ_F16) {
+                /* half(q) is exact; q + offset and the product are exact in double, rounded once each */
+                uint16_t w = oq_f32_to_f16((float)q, 0);
+                if (offset) w = oq_f64_to_f16((double)q + (double)of, 0);
+                w = oq_f64_to_f16((double)oq_f16_to_f32(w) * (double)sc, 0);
+                ((uint16_t*)dst)[idx] = w;
+            } else {
+                float v = (float)q;
+                if (offset) v = v + of;
+                v = v * sc;
+                store_from_f32(dst, dst_type, idx, v);
+            }
+        }
+}
+
+/* Weight-only antiquant matmul (W8A16 / W4A16): the reference composes AscendAntiQuant (fp16 ops, above) with
+ * a half x half Matmul whose L0C type is fp32 (GetMmDstType<half> = float, matmul_utils.h:171-174) and whose
+ * fixpipe casts fp32 -> half with rint.  Products of two halves are exact; the restatement sums them in
+ * double (exact up to one rounding per add at ~2^-53), keeps that sum, and rounds it to half once.
+ * x [M,K] half; w [K,N] (w_transpose: [N,K]); scale/offset [K/group, N] (w_transpose: [N, K/group]). */
+void oq_antiquant_matmul(uint16_t* y, double* y_exact, double* y_absdot, const uint16_t* x, const void* w,
+                         int w_type, const uint16_t* scale, const uint16_t* offset, int64_t group_size,
+                         int64_t M, int64_t N, int64_t K, int w_transpose)
+{
+    uint16_t* wf = (uint16_t*)malloc((size_t)(K * N) * sizeof(uint16_t));
+    oq_antiquant(wf, OQ_F16, w, w_type, offset, scale, K, N, group_size, w_transpose, OQ_ARITH_F16);
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m) {
+        double* acc = (double*)calloc((size_t)N, sizeof(double));
+        double* aab = (double*)calloc((size_t)N, sizeof(double));
+        for (int64_t k = 0; k < K; ++k) {
+            double xv = oq_f16_to_f32(x[m * K + k]);
+            if (xv == 0.0) continue;
+            for (int64_t n = 0; n < N; ++n) {
+                double p = xv * (double)oq_f16_to_f32(wf[w_transpose ? n * K + k : k * N + n]);
+                acc[n] += p;
+                aab[n] += fabs(p);
+            }
+        }
+        for (int64_t n = 0; n < N; ++n) {
+            if (y_exact) y_exact[m * N + n] = acc[n];
+            if (y_absdot) y_absdot[m * N + n] = aab[n];
+            if (y) y[m * N + n] = oq_f64_to_f16(acc[n], 1);
+        }
+        free(acc);
+        free(aab);
+    }
+    free(wf);
+}
+
+/* ------------------------------------------------------------------------ */
+/* QuantGroupMatmul (MoE)                                                    */
+/* ------------------------------------------------------------------------ */
+
+/* examples/01_simd_cpp_api/05_best_practices/03_fusion_compute/quant_group_matmul_high_performance/
+ * quant_group_matmul_custom.asc: group rows [s_g, s_g+cnt_g) (Process :255-288), int32 accumulate on the
+ * cube (MMCompute :296-334), then AscendDequant(acc x scale[g,n]) to fp32 (:433), Mul by perTokenScale[m]
+ * (:439), and the final Cast (:450; CAST_NONE = rint).  The Gelu of the sample (:445) is not applied.
+ * list_type 0: group_list holds G+1 int64 prefix offsets (offsets[0] = first row); 1: G int64 counts
+ * (the reference's GetValue(groupIdx) counts, :263).  w [G,K,N] ND, or [G,N,K] when w_trans. */
+void oq_group_matmul(void* y, int out_type, const int8_t* x, const float* pts, const int8_t* w, int w_trans,
+                     const float* scale, const int64_t* group_list, int list_type, int64_t G, int64_t M,
+                     int64_t K, int64_t N)
+{
+    int64_t start = list_type == 0 ? group_list[0] : 0;
+    for (int64_t g = 0; g < G; ++g) {
+        int64_t cnt = list_type == 0 ? group_list[g + 1] - group_list[g] : group_list[g];
+        int64_t s = start;
+        start += cnt > 0 ? cnt : 0;
+        if (cnt <= 0) continue;
+        const int8_t* wg = w + g * K * N;
+#pragma omp parallel for schedule(static)
+        for (int64_t m = s; m < s + cnt; ++m) {
+            if (m < 0 || m >= M) continue;
+            for (int64_t n = 0; n < N; ++n) {
+                int64_t acc = 0;
+                for (int64_t k = 0; k < K; ++k)
+                    acc += (int64_t)x[m * K + k] * (int64_t)(w_trans ? wg[n * K + k] : wg[k * N + n]);
+                float v = (float)(int32_t)(uint32_t)(uint64_t)acc * scale[g * N + n];
+                v = v * pts[m];
+                store_from_f32(y, out_type, m * N + n, v);
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* MX block-scaled matmul                                                    */
+/* ------------------------------------------------------------------------ */
+
+static inline float mx_elem(const uint8_t* p, int64_t idx, int fmt)
+{
+    if (fmt == OQ_FP4_E2M1) {
+        uint8_t b = p[idx >> 1];
+        return oq_e2m1_decode((idx & 1) ? (uint8_t)(b >> 4) : (uint8_t)(b & 0xf));
+    }
+    return oq_fp8_decode(p[idx], fmt);
+}
+
+/* C[m,n] = sum_k a[m,k] 2^(SA[m,k/32]-127) * b[k,n] 2^(SB[k/32,n]-127), golden computed in fp64 and cast to
+ * bf16 (examples/01_simd_cpp_api/05_best_practices/01_matrix_compute/matmul_mxfp4_high_performance/scripts/
+ * gen_data.py:47-61; MmadMx include/basic_api/kernel_operator_mm_intf.h:348-352; type
+ * impl/adv_api/detail/matmul/utils/matmul_type_def.h:114-131).  Packing: two fp4 per byte along the
+ * contiguous axis, the even element in the low nibble (gen_data.py:25-34).
+ * A [M,K]; B [K,N] (transB: [N,K]).  sK = ceil(K/64)*2 (gen_data.py:40).
+ * scale_a_layout 0: scaleA [M, sK]; 1: [sK/2, M, 2].  scale_b_layout 0: scaleB [sK/2, N, 2] (the sample's
+ * layout, gen_data.py:63 and README_en.md:64-66); 1: [N, sK].
+ * rows != NULL restricts the computation to the listed rows (C rows not listed are untouched). */
+void oq_mx_matmul(uint16_t* C, double* C_exact, double* C_absdot, const uint8_t* A, const uint8_t* B,
+                  const uint8_t* scaleA, const uint8_t* scaleB, int64_t M, int64_t N, int64_t K, int transB,
+                  int scale_a_layout, int scale_b_layout, int elem_fmt, const int64_t* rows, int64_t n_rows)
+{
+    int64_t sK = (K + 63) / 64 * 2;
+    int64_t nr = rows ? n_rows : M;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t r = 0; r < nr; ++r) {
+        int64_t m = rows ? rows[r] : r;
+        double* arow = (double*)malloc((size_t)K * sizeof(double));
+        for (int64_t k = 0; k < K; ++k) {
+            int64_t kb = k / 32;
+            uint8_t sa = scale_a_layout == 0 ? scaleA[m * sK + kb] : scaleA[(kb / 2) * M * 2 + m * 2 + (kb & 1)];
+            arow[k] = (double)mx_elem(A, m * K + k, elem_fmt) * (double)oq_e8m0_decode(sa);
+        }
+        for (int64_t n = 0; n < N; ++n) {
+            double s = 0.0, sa_ = 0.0;
+            for (int64_t k = 0; k < K; ++k) {
+                int64_t kb = k / 32;
+                uint8_t sb = scale_b_layout == 0 ? scaleB[(kb / 2) * N * 2 + n * 2 + (kb & 1)] : scaleB[n * sK + kb];
+                double b = (double)mx_elem(B, transB ? n * K + k : k * N + n, elem_fmt) * (double)oq_e8m0_decode(sb);
+                double p = arow[k] * b;
+                s += p;
+                sa_ += fabs(p);
+            }
+            if (C_exact) C_exact[m * N + n] = s;
+            if (C_absdot) C_absdot[m * N + n] = sa_;
+            if (C) C[m * N + n] = oq_f64_to_bf16(s, 1);
+        }
+        free(arow);
+    }
+}
+
+/* MX quantisation along the contiguous axis (rows of length K): shared exponent per 32 elements from the
+ * block absmax (oq_mx_shared_exp), elements = E2M1 rne of x / 2^(e-127).  Output: packed [R, K/2] and
+ * scales [R, K/32] row-major.  Used to build MX inputs the way the MX-FP4 workload specifies them. */
+void oq_mx_quantize_fp4(uint8_t* packed, uint8_t* scales, const float* x, int64_t R, int64_t K)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < R; ++r)
+        for (int64_t kb = 0; kb < K / 32; ++kb) {
+            const float* blk = x + r * K + kb * 32;
+            float amax = 0.0f;
+            for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(blk[i]));
+            uint8_t e = oq_mx_shared_exp(amax);
+            scales[r * (K / 32) + kb] = e;
+            float inv = 1.0f / oq_e8m0_decode(e); /* power of two: exact */
+            for (int i = 0; i < 32; i += 2) {
+                uint8_t lo = oq_e2m1_encode_rne(blk[i] * inv);
+                uint8_t hi = oq_e2m1_encode_rne(blk[i + 1] * inv);
+                packed[r * (K / 2) + kb * 16 + i / 2] = (uint8_t)(lo | (hi << 4));
+            }
+        }
+}

@@ -1,0 +1,210 @@
+"""numpy front-end of the CPU oracle (oracle/liboracle.so).
+
+Test infrastructure only: used by tests/, the smoke check and bench.py's cpu_baseline leg as the
+checker; the product path never calls it.  Arrays are numpy; f16 / bf16 travel as uint16 bit patterns.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+ORACLE_DIR = ROOT / "oracle"
+ORACLE_SO = ORACLE_DIR / "liboracle.so"
+
+INT8, UINT8, INT4, INT32, F16, BF16, F32, U64, FP8_E4M3, FP8_E5M2, FP4_E2M1, E8M0, INT64 = range(1, 14)
+ROUND_NONE, ROUND_RINT, ROUND_FLOOR, ROUND_CEIL, ROUND_ROUND, ROUND_TRUNC = range(6)
+PER_TENSOR, PER_CHANNEL, PER_TOKEN, PER_GROUP = range(4)
+ARITH_F16, ARITH_F32 = 0, 1
+
+_lib = None
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+
+
+def build_if_missing() -> None:
+    if not ORACLE_SO.exists():
+        subprocess.run(["make", "-C", str(ORACLE_DIR)], check=True, capture_output=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        build_if_missing()
+        L = ctypes.CDLL(str(ORACLE_SO))
+        sig = {
+            "oq_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float, ctypes.c_int]),
+            "oq_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+            "oq_f32_to_bf16": (ctypes.c_uint16, [ctypes.c_float, ctypes.c_int]),
+            "oq_bf16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+            "oq_f64_to_f16": (ctypes.c_uint16, [ctypes.c_double, ctypes.c_int]),
+            "oq_f64_to_bf16": (ctypes.c_uint16, [ctypes.c_double, ctypes.c_int]),
+            "oq_quant_pre_m1": (ctypes.c_float, [ctypes.c_uint64]),
+            "oq_pack_quant_pre": (ctypes.c_uint64, [ctypes.c_float, ctypes.c_int32, ctypes.c_int32]),
+            "oq_round_to_int": (ctypes.c_int32, [ctypes.c_float, ctypes.c_int]),
+            "oq_e2m1_decode": (ctypes.c_float, [ctypes.c_uint8]),
+            "oq_e2m1_encode_rne": (ctypes.c_uint8, [ctypes.c_float]),
+            "oq_e8m0_decode": (ctypes.c_float, [ctypes.c_uint8]),
+            "oq_mx_shared_exp": (ctypes.c_uint8, [ctypes.c_float]),
+            "oq_fp8_decode": (ctypes.c_float, [ctypes.c_uint8, ctypes.c_int]),
+            "oq_matmul_i8": (None, [_P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int]),
+            "oq_mm_dequant": (None, [_P, _P, ctypes.c_int, _I64, _I64, _P, ctypes.c_uint64]),
+            "oq_quant_per_token": (None, [_P, _P, ctypes.c_int, _P, _P, _I64, _I64, ctypes.c_int]),
+            "oq_quant_dynamic_per_token": (None, [_P, _P, _P, ctypes.c_int, _I64, _I64, ctypes.c_int]),
+            "oq_quant_legacy_f16": (None, [_P, _P, ctypes.c_int, _P, ctypes.c_uint16, _P, ctypes.c_uint16, _I64, _I64]),
+            "oq_dequant": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int, ctypes.c_float, ctypes.c_int,
+                                  _I64, _I64, _I64]),
+            "oq_antiquant": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, _P, _I64, _I64, _I64, ctypes.c_int,
+                                    ctypes.c_int]),
+            "oq_antiquant_matmul": (None, [_P, _P, _P, _P, _P, ctypes.c_int, _P, _P, _I64, _I64, _I64, _I64,
+                                           ctypes.c_int]),
+            "oq_group_matmul": (None, [_P, ctypes.c_int, _P, _P, _P, ctypes.c_int, _P, _P, ctypes.c_int, _I64, _I64,
+                                       _I64, _I64]),
+            "oq_mx_matmul": (None, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_int, _P, _I64]),
+            "oq_mx_quantize_fp4": (None, [_P, _P, _P, _I64, _I64]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be contiguous"
+    return a.ctypes.data
+
+
+# ---------------- scalar helpers (vectorised over numpy inputs) ----------------
+def f32_to_f16(x, sat=True) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    f = lib().oq_f32_to_f16
+    return np.array([f(float(v), int(sat)) for v in x], dtype=np.uint16)
+
+
+def matmul_i8(A, B, bias=None, trans_a=False, trans_b=False):
+    A = np.ascontiguousarray(A, np.int8)
+    B = np.ascontiguousarray(B, np.int8)
+    M = A.shape[1] if trans_a else A.shape[0]
+    K = A.shape[0] if trans_a else A.shape[1]
+    N = B.shape[0] if trans_b else B.shape[1]
+    C = np.empty((M, N), np.int32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.int32)
+    lib().oq_matmul_i8(_p(A), _p(B), _p(b), _p(C), M, N, K, int(trans_a), int(trans_b))
+    return C
+
+
+def mm_dequant(acc, out_type=F16, qvec=None, qscalar=0):
+    acc = np.ascontiguousarray(acc, np.int32)
+    M, N = acc.shape
+    out = np.empty((M, N), np.uint16)
+    qv = None if qvec is None else np.ascontiguousarray(qvec, np.uint64)
+    lib().oq_mm_dequant(_p(acc), _p(out), out_type, M, N, _p(qv), int(qscalar))
+    return out
+
+
+def quant_per_token(x, src_type, scale, offset=None, round_mode=ROUND_RINT):
+    x = np.ascontiguousarray(x)
+    m, n = x.shape
+    q = np.empty((m, n), np.int8)
+    s = np.ascontiguousarray(scale, np.float32)
+    o = None if offset is None else np.ascontiguousarray(offset, np.float32)
+    lib().oq_quant_per_token(_p(q), _p(x), src_type, _p(s), _p(o), m, n, round_mode)
+    return q
+
+
+def quant_dynamic_per_token(x, src_type, round_mode=ROUND_RINT):
+    x = np.ascontiguousarray(x)
+    m, n = x.shape
+    q = np.empty((m, n), np.int8)
+    s = np.empty((m,), np.float32)
+    lib().oq_quant_dynamic_per_token(_p(q), _p(s), _p(x), src_type, m, n, round_mode)
+    return q, s
+
+
+def quant_legacy_f16(x, src_type, scale_vec=None, scale_scalar=0x3C00, offset_vec=None, offset_scalar=0,
+                     scale_count=0):
+    x = np.ascontiguousarray(x)
+    q = np.empty(x.shape, np.int8)
+    sv = None if scale_vec is None else np.ascontiguousarray(scale_vec, np.uint16)
+    ov = None if offset_vec is None else np.ascontiguousarray(offset_vec, np.uint16)
+    lib().oq_quant_legacy_f16(_p(q), _p(x), src_type, _p(sv), scale_scalar, _p(ov), offset_scalar, x.size,
+                              scale_count)
+    return q
+
+
+def dequant(src, src_type, scale, scale_type, policy, dst_type=F16, cal_count=None, scale_scalar=1.0, dst=None):
+    src = np.ascontiguousarray(src)
+    m, n = src.shape
+    if dst is None:
+        dst = np.zeros((m, n), np.float32 if dst_type == F32 else np.uint16)
+    sc = None if scale is None else np.ascontiguousarray(scale)
+    lib().oq_dequant(_p(dst), dst_type, _p(src), src_type, _p(sc), scale_type, float(scale_scalar), policy, m, n,
+                     n if cal_count is None else cal_count)
+    return dst
+
+
+def antiquant(src, src_type, scale, offset, K, N, group_size=0, is_transpose=False, dst_type=F16, arith=ARITH_F16):
+    src = np.ascontiguousarray(src)
+    dst = np.empty((N, K) if is_transpose else (K, N), np.uint16)
+    sc = np.ascontiguousarray(scale, np.uint16)
+    of = None if offset is None else np.ascontiguousarray(offset, np.uint16)
+    lib().oq_antiquant(_p(dst), dst_type, _p(src), src_type, _p(of), _p(sc), K, N, group_size, int(is_transpose),
+                       arith)
+    return dst
+
+
+def antiquant_matmul(x_f16bits, w, w_type, scale, offset, group_size, M, N, K, w_transpose=False):
+    x = np.ascontiguousarray(x_f16bits, np.uint16)
+    w = np.ascontiguousarray(w)
+    y = np.empty((M, N), np.uint16)
+    ye = np.empty((M, N), np.float64)
+    ya = np.empty((M, N), np.float64)
+    sc = np.ascontiguousarray(scale, np.uint16)
+    of = None if offset is None else np.ascontiguousarray(offset, np.uint16)
+    lib().oq_antiquant_matmul(_p(y), _p(ye), _p(ya), _p(x), _p(w), w_type, _p(sc), _p(of), group_size, M, N, K,
+                              int(w_transpose))
+    return y, ye, ya
+
+
+def group_matmul(x, pts, w, scale, group_list, list_type, G, M, K, N, out_type=BF16, w_trans=False, y=None):
+    x = np.ascontiguousarray(x, np.int8)
+    pts = np.ascontiguousarray(pts, np.float32)
+    w = np.ascontiguousarray(w, np.int8)
+    scale = np.ascontiguousarray(scale, np.float32)
+    gl = np.ascontiguousarray(group_list, np.int64)
+    if y is None:
+        y = np.zeros((M, N), np.uint16)
+    lib().oq_group_matmul(_p(y), out_type, _p(x), _p(pts), _p(w), int(w_trans), _p(scale), _p(gl), list_type, G, M, K,
+                          N)
+    return y
+
+
+def mx_matmul(A, B, sA, sB, M, N, K, trans_b=False, sa_layout=0, sb_layout=0, elem_fmt=FP4_E2M1, rows=None):
+    A = np.ascontiguousarray(A, np.uint8)
+    B = np.ascontiguousarray(B, np.uint8)
+    sA = np.ascontiguousarray(sA, np.uint8)
+    sB = np.ascontiguousarray(sB, np.uint8)
+    C = np.zeros((M, N), np.uint16)
+    Ce = np.zeros((M, N), np.float64)
+    Ca = np.zeros((M, N), np.float64)
+    r = None if rows is None else np.ascontiguousarray(rows, np.int64)
+    lib().oq_mx_matmul(_p(C), _p(Ce), _p(Ca), _p(A), _p(B), _p(sA), _p(sB), M, N, K, int(trans_b), sa_layout,
+                       sb_layout, elem_fmt, _p(r), 0 if r is None else r.size)
+    return C, Ce, Ca
+
+
+def mx_quantize_fp4(x):
+    x = np.ascontiguousarray(x, np.float32)
+    R, K = x.shape
+    packed = np.empty((R, K // 2), np.uint8)
+    scales = np.empty((R, K // 32), np.uint8)
+    lib().oq_mx_quantize_fp4(_p(packed), _p(scales), _p(x), R, K)
+    return packed, scales

@@ -1,0 +1,155 @@
+"""CPU tests of the C ABI: libascq.so loads, exports every function include/ascq.h declares, and rejects
+invalid arguments on the host (negative status, nothing launched) -- no GPU needed for any of these."""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import ascq
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "ascq.h"
+
+
+def declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(ascq_[a-z0-9_]+)\s*\(", text))
+
+
+def test_library_loads():
+    L = ascq.lib()
+    assert L.ascq_version().decode().startswith("ascq")
+
+
+def test_exports_every_declared_symbol():
+    declared = declared_functions()
+    assert len(declared) >= 30
+    out = subprocess.run(["nm", "-D", "--defined-only", str(ascq.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    missing = declared - exported
+    assert not missing, f"declared but not exported: {sorted(missing)}"
+    # and the binding's signature table covers exactly the declared set
+    assert set(ascq.SIGNATURES) == declared
+
+
+def test_pack_quant_pre_matches_reference_packing():
+    # (uint64)(*(uint32*)&f) for f = 0.1 (matmul_quant.asc:111-113)
+    f = ctypes.c_float(0.1)
+    bits = ctypes.cast(ctypes.pointer(f), ctypes.POINTER(ctypes.c_uint32)).contents.value
+    assert ascq.pack_quant_pre(0.1) == bits
+    w = ascq.pack_quant_pre(1.0, offset9=-3, sign=1)
+    assert w & 0xFFFFFFFF == 0x3F800000
+    assert (w >> 37) & 0x1FF == (-3) & 0x1FF
+    assert (w >> 46) & 1 == 1
+
+
+def _err(status, expect):
+    assert status == expect, f"status {status}: {ascq.last_error()}"
+
+
+def test_quant_argument_checks():
+    L = ascq.lib()
+    P = ascq._QuantParam(0, 7, 15, 0, 0, 1, ascq.ROUND_RINT)  # calCount not a multiple of n
+    dummy = ctypes.c_void_p(0x1000)
+    _err(L.ascq_ascend_quant_per_token(dummy, dummy, ascq.F16, dummy, None, ctypes.byref(P), None),
+         ascq.E_INVALID_ARG)
+    assert "multiple of n" in ascq.last_error()
+    P = ascq._QuantParam(0, 8, 16, 0, 0, 1, 17)  # bad round mode
+    _err(L.ascq_ascend_quant_per_token(dummy, dummy, ascq.F16, dummy, None, ctypes.byref(P), None),
+         ascq.E_INVALID_ARG)
+    P = ascq._QuantParam(0, 8, 16, 0, 1, 1, 1)  # has_offset without an offset tensor
+    _err(L.ascq_ascend_quant_per_token(dummy, dummy, ascq.F16, dummy, None, ctypes.byref(P), None),
+         ascq.E_INVALID_ARG)
+    _err(L.ascq_ascend_quant_per_token(None, dummy, ascq.F16, dummy, None, ctypes.byref(P), None),
+         ascq.E_INVALID_ARG)
+    _err(L.ascq_ascend_quant_dynamic_per_token(dummy, dummy, dummy, ascq.INT32, 4, 4, 1, None), ascq.E_UNSUPPORTED)
+    _err(L.ascq_ascend_quant(dummy, dummy, ascq.F16, dummy, None, 0, 0, 100, 3, None), ascq.E_INVALID_ARG)
+    # zero-sized work is a no-op that succeeds without touching the device
+    _err(L.ascq_ascend_quant_dynamic_per_token(dummy, dummy, dummy, ascq.F16, 0, 16, 1, None), ascq.OK)
+
+
+def test_dequant_antiquant_argument_checks():
+    L = ascq.lib()
+    d = ctypes.c_void_p(0x1000)
+    p = ascq._DequantParam(4, 8, 9)  # calCount > n
+    _err(L.ascq_ascend_dequant(d, ascq.F16, d, ascq.INT32, d, ascq.F32, 1.0, ascq.PER_CHANNEL, ctypes.byref(p), None),
+         ascq.E_INVALID_ARG)
+    p = ascq._DequantParam(4, 8, 8)
+    _err(L.ascq_ascend_dequant(d, ascq.INT8, d, ascq.INT32, d, ascq.F32, 1.0, ascq.PER_CHANNEL, ctypes.byref(p), None),
+         ascq.E_UNSUPPORTED)
+    _err(L.ascq_ascend_dequant(d, ascq.F16, d, ascq.INT32, None, ascq.F32, 1.0, ascq.PER_TOKEN, ctypes.byref(p), None),
+         ascq.E_INVALID_ARG)
+    _err(L.ascq_ascend_antiquant(d, ascq.F16, d, ascq.INT8, d, d, 100, 8, 32, 0, 0, None), ascq.E_INVALID_ARG)
+    _err(L.ascq_ascend_antiquant(d, ascq.F32, d, ascq.INT8, d, d, 128, 8, 32, 0, 0, None), ascq.E_UNSUPPORTED)
+
+
+def test_gemv_group_argument_checks():
+    L = ascq.lib()
+    d = ctypes.c_void_p(0x1000)
+    sz = ctypes.c_size_t(0)
+    _err(L.ascq_weight_pack_size(ascq.INT4, 4096, 11008, ctypes.byref(sz)), ascq.OK)
+    assert sz.value == 4096 * 11008 // 2
+    _err(L.ascq_weight_pack_size(ascq.INT8, 100, 16, ctypes.byref(sz)), ascq.E_INVALID_ARG)
+    _err(L.ascq_antiquant_matmul(d, d, d, ascq.INT4, d, d, 48, 1, 64, 256, None), ascq.E_INVALID_ARG)  # g % 32
+    _err(L.ascq_antiquant_matmul(d, d, d, ascq.INT4, d, d, 96, 1, 64, 256, None), ascq.E_INVALID_ARG)  # g !| K
+    _err(L.ascq_antiquant_matmul(d, ctypes.c_void_p(0x1001), d, ascq.INT4, d, d, 128, 1, 64, 256, None),
+         ascq.E_INVALID_ARG)  # misaligned x
+    _err(L.ascq_quant_group_matmul(d, ascq.F32, d, d, d, 0, d, d, 0, 4, 8, 16, 16, None), ascq.E_UNSUPPORTED)
+    _err(L.ascq_quant_group_matmul(d, ascq.BF16, d, d, d, 0, d, d, 2, 4, 8, 16, 16, None), ascq.E_INVALID_ARG)
+
+
+def test_matmul_handle_state_machine():
+    L = ascq.lib()
+    h = ctypes.c_void_p()
+    bad = ascq._MatmulTypes(ascq.F16, ascq.F16, ascq.F16, 0, 0, 0)
+    _err(L.ascq_matmul_create(ctypes.byref(bad), ctypes.byref(h)), ascq.E_UNSUPPORTED)
+    t = ascq._MatmulTypes(ascq.INT8, ascq.INT8, ascq.F16, ascq.INT32, 0, 0)
+    _err(L.ascq_matmul_create(ctypes.byref(t), ctypes.byref(h)), ascq.OK)
+    d = ctypes.c_void_p(0x1000)
+    _err(L.ascq_matmul_iterate_all(h, d, 0, None), ascq.E_STATE)          # no tensors yet
+    _err(L.ascq_matmul_set_tensor_a(h, d, 0), ascq.OK)
+    _err(L.ascq_matmul_set_tensor_b(h, d, 0), ascq.OK)
+    _err(L.ascq_matmul_iterate_all(h, d, 0, None), ascq.E_STATE)          # no org shape
+    _err(L.ascq_matmul_set_org_shape(h, 128, 256, 512), ascq.OK)
+    _err(L.ascq_matmul_iterate_all(h, d, 0, None), ascq.E_STATE)          # f16 out without quant params
+    _err(L.ascq_matmul_iterate_all(h, d, 1, None), ascq.E_UNSUPPORTED)    # enAtomic
+    _err(L.ascq_matmul_set_antiquant_scalar(h, 0, 0), ascq.E_UNSUPPORTED)
+    _err(L.ascq_matmul_set_tensor_scale_a(h, d, 0), ascq.E_UNSUPPORTED)
+    _err(L.ascq_matmul_set_single_shape(h, 256, 256, 512), ascq.OK)
+    _err(L.ascq_matmul_set_quant_scalar(h, 0x3F800000), ascq.OK)
+    _err(L.ascq_matmul_iterate_all(h, d, 0, None), ascq.E_INVALID_ARG)   # single shape exceeds org shape
+    _err(L.ascq_matmul_end(h), ascq.OK)
+    _err(L.ascq_matmul_destroy(h), ascq.OK)
+    mx = ascq._MatmulTypes(ascq.FP4_E2M1, ascq.FP4_E2M1, ascq.BF16, 0, ascq.E8M0, 0)
+    _err(L.ascq_matmul_create(ctypes.byref(mx), ctypes.byref(h)), ascq.OK)
+    _err(L.ascq_matmul_set_org_shape(h, 128, 128, 96), ascq.OK)
+    _err(L.ascq_matmul_set_tensor_a(h, d, 0), ascq.OK)
+    _err(L.ascq_matmul_set_tensor_b(h, d, 1), ascq.OK)
+    _err(L.ascq_matmul_iterate_all(h, d, 0, None), ascq.E_STATE)          # no scales
+    _err(L.ascq_matmul_set_tensor_scale_a(h, d, 0), ascq.OK)
+    _err(L.ascq_matmul_set_tensor_scale_b(h, d, 1), ascq.OK)
+    _err(L.ascq_matmul_iterate_all(h, d, 0, None), ascq.E_UNSUPPORTED)    # K % 128
+    _err(L.ascq_matmul_destroy(h), ascq.OK)
+
+
+def test_no_device_reports_zero_or_more():
+    assert ascq.lib().ascq_device_count() >= 0
+
+
+@pytest.mark.parametrize("name", sorted(declared_functions()))
+def test_header_comment_cites_reference_or_is_library_utility(name):
+    """Every Matmul / quant entry point's declaration block carries a reference citation (file:line)."""
+    text = HEADER.read_text()
+    idx = text.index(name + "(")
+    block = text[max(0, idx - 900):idx]
+    utility = {"ascq_last_error", "ascq_version", "ascq_device_count", "ascq_weight_pack_size",
+               "ascq_matmul_workspace_size", "ascq_matmul_set_workspace", "ascq_matmul_destroy"}
+    if name in utility:
+        return
+    assert re.search(r"\.(h|asc|md|cpp|py):\d+", block), f"{name}: no reference file:line nearby"

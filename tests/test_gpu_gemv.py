@@ -1,0 +1,127 @@
+"""GPU parity: weight-only antiquant matmul (W4A16 / W8A16) vs the oracle.
+
+The dequantised weights follow AscendAntiQuant bit-exactly; the dot products accumulate in fp32, whose
+order differs from any reference, so the output is checked against the exact (fp64) sum with the rigorous
+bound  |y - s| <= ulp16(|s| + d)/2 + d,  d = K * 2^-24 * sum|x*w|  (fp32 summation error bound), and most
+outputs must equal the correctly rounded exact sum."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from conftest import seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _ulp16(v):
+    a = np.maximum(np.abs(v), 2.0 ** -14)
+    return 2.0 ** (np.floor(np.log2(a)) - 10)
+
+
+def make_weights(rng, K, N, w_type, group, with_offset=True):
+    G = K // group if group else 1
+    if w_type == O.INT8:
+        w = rng.integers(-128, 128, (K, N), dtype=np.int8)
+    else:
+        nib = rng.integers(0, 16, K * N, dtype=np.uint8)
+        w = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8).reshape(K, N // 2)
+    scale = np.exp(rng.uniform(np.log(1e-3), np.log(1e-1), (G, N))).astype(np.float16)
+    offset = rng.uniform(-8, 8, (G, N)).astype(np.float16) if with_offset else None
+    return w, scale, offset
+
+
+def check_close(y_gpu, y_exact, y_abs, K, frac_exact=0.98):
+    y = y_gpu.astype(np.float64)
+    d = K * 2.0 ** -24 * y_abs
+    tol = 0.5 * _ulp16(np.abs(y_exact) + d) + d
+    err = np.abs(y - y_exact)
+    bad = err > tol
+    assert not bad.any(), f"{bad.sum()} outputs outside the fp32-accumulation bound; max err {err.max()}"
+    exact = (y_gpu == np.float16(y_exact)).mean()
+    assert exact >= frac_exact, f"only {exact:.4f} of outputs equal the correctly rounded sum"
+
+
+@pytest.mark.parametrize("w_type", ["int4", "int8"])
+@pytest.mark.parametrize("M", [1, 16, 64, 3, 40, 100])
+def test_config3_decode_shape(ascq_gpu, oracle, w_type, M):
+    """x f16 [M, 4096] ~ N(0,1); W [4096, 11008]; g=128 f16 scale log-uniform [1e-3,1e-1], offset U[-8,8]."""
+    rng = seeded(300 + M)
+    K, N, g = 4096, 11008, 128
+    code = O.INT8 if w_type == "int8" else O.INT4
+    w, scale, offset = make_weights(rng, K, N, code, g)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    wp = ascq_gpu.weight_pack(_dev(w), ascq_gpu.INT8 if w_type == "int8" else ascq_gpu.INT4, K, N)
+    y = ascq_gpu.antiquant_matmul(_dev(x), wp, ascq_gpu.INT8 if w_type == "int8" else ascq_gpu.INT4, _dev(scale),
+                                  _dev(offset), g, N)
+    y_ref, y_exact, y_abs = O.antiquant_matmul(x.view(np.uint16), w, code, scale.view(np.uint16),
+                                               offset.view(np.uint16), g, M, N, K)
+    check_close(y.cpu().numpy(), y_exact, y_abs, K)
+
+
+@pytest.mark.parametrize("w_type", ["int4", "int8"])
+@pytest.mark.parametrize("group", [0, 32, 64, 256])
+@pytest.mark.parametrize("with_offset", [True, False])
+@pytest.mark.parametrize("transpose", [False, True])
+def test_groups_and_layouts(ascq_gpu, oracle, w_type, group, with_offset, transpose):
+    rng = seeded(17 + group)
+    K, N, M = 512, 96, 5
+    code = O.INT8 if w_type == "int8" else O.INT4
+    w, scale, offset = make_weights(rng, K, N, code, group, with_offset)
+    if transpose:  # weight given [N, K]
+        if code == O.INT8:
+            w = np.ascontiguousarray(w.T)
+        else:
+            nib = np.stack([w & 0xF, w >> 4], -1).reshape(K, N)
+            t = np.ascontiguousarray(nib.T).reshape(-1)
+            w = (t[0::2] | (t[1::2] << 4)).astype(np.uint8)
+    x = (rng.standard_normal((M, K)) * 2).astype(np.float16)
+    at = ascq_gpu.INT8 if w_type == "int8" else ascq_gpu.INT4
+    wp = ascq_gpu.weight_pack(_dev(w), at, K, N, is_transpose=transpose)
+    y = ascq_gpu.antiquant_matmul(_dev(x), wp, at, _dev(scale), None if offset is None else _dev(offset), group, N)
+    # oracle scale layout is [K/g, N] for the [K, N] weight; for the transposed weight it is [N, K/g]
+    sc = scale if not transpose else np.ascontiguousarray(scale.T)
+    of = None if offset is None else (offset if not transpose else np.ascontiguousarray(offset.T))
+    _, y_exact, y_abs = O.antiquant_matmul(x.view(np.uint16), w, code, sc.view(np.uint16),
+                                           None if of is None else of.view(np.uint16), group, M, N, K,
+                                           w_transpose=transpose)
+    check_close(y.cpu().numpy(), y_exact, y_abs, K)
+
+
+@pytest.mark.parametrize("w_type", ["int4", "int8"])
+@pytest.mark.parametrize("b_format", ["nd", "packed"])
+def test_matmul_handle_antiquant(ascq_gpu, oracle, w_type, b_format):
+    """Matmul<half, int8|int4, half> with SetAntiQuantVector (per group) and SetAntiQuantScalar."""
+    rng = seeded(23)
+    K, N, M, g = 256, 64, 7, 128
+    code = O.INT8 if w_type == "int8" else O.INT4
+    at = ascq_gpu.INT8 if w_type == "int8" else ascq_gpu.INT4
+    w, scale, offset = make_weights(rng, K, N, code, g)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    fmt = ascq_gpu.FORMAT_ND if b_format == "nd" else ascq_gpu.FORMAT_PACKED
+    wd = _dev(w) if b_format == "nd" else ascq_gpu.weight_pack(_dev(w), at, K, N)
+    for mode in ("vector", "scalar"):
+        mm = ascq_gpu.Matmul(ascq_gpu.F16, at, ascq_gpu.F16, b_format=fmt)
+        mm.SetOrgShape(M, N, K)
+        mm.SetTensorA(_dev(x))
+        mm.SetTensorB(wd)
+        if mode == "vector":
+            mm.SetAntiQuantVector(_dev(offset), _dev(scale), g)
+            sc, of, gg = scale, offset, g
+        else:
+            mm.SetAntiQuantScalar(1.5, 0.0123)
+            sc = np.full((1, N), 0.0123, np.float16)
+            of = np.full((1, N), 1.5, np.float16)
+            gg = 0
+        y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        mm.IterateAll(y)
+        mm.End()
+        _, y_exact, y_abs = O.antiquant_matmul(x.view(np.uint16), w, code, sc.view(np.uint16), of.view(np.uint16),
+                                               gg, M, N, K)
+        check_close(y.cpu().numpy(), y_exact, y_abs, K)

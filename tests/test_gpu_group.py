@@ -1,0 +1,70 @@
+"""GPU parity: quantized group matmul (MoE) vs the oracle, bit-exact (int32 accumulate + fp32 epilogue)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from conftest import seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def zipf_counts(rng, tokens, experts, s=1.1):
+    p = 1.0 / (np.arange(1, experts + 1) ** s)
+    p /= p.sum()
+    return rng.multinomial(tokens, p).astype(np.int64)
+
+
+def bf16_bits_of_f32(v: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(v, np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("list_type", [0, 1])
+@pytest.mark.parametrize("w_trans", [False, True])
+@pytest.mark.parametrize("out", ["bf16", "f16"])
+def test_group_matmul_small(ascq_gpu, oracle, list_type, w_trans, out):
+    rng = seeded(40 + list_type + 2 * w_trans)
+    G, K, N = 5, 320, 160
+    counts = np.array([70, 0, 133, 1, 96], np.int64)  # includes an empty and a single-row group
+    M = int(counts.sum()) + 9  # trailing rows belong to no group and must stay untouched
+    x = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-127, 128, (G, N, K) if w_trans else (G, K, N), dtype=np.int8)
+    pts = rng.normal(0, 0.01, M).astype(np.float32)
+    scale = rng.normal(0, 0.01, (G, N)).astype(np.float32)
+    gl = np.concatenate([[0], np.cumsum(counts)]) if list_type == 0 else counts
+    ycode, tdt = (O.BF16, torch.bfloat16) if out == "bf16" else (O.F16, torch.float16)
+    y = torch.full((M, N), 3.0, dtype=tdt, device="cuda")
+    ascq_gpu.quant_group_matmul(_dev(x), _dev(pts), _dev(w), _dev(scale), _dev(gl), list_type, w_trans, tdt, out=y)
+    y0 = torch.full((M, N), 3.0, dtype=tdt).view(torch.int16).numpy().view(np.uint16).copy()
+    ref = O.group_matmul(x, pts, w, scale, gl, list_type, G, M, K, N, ycode, w_trans, y=y0)
+    np.testing.assert_array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), ref)
+
+
+def test_config4_moe_full_size(ascq_gpu, oracle):
+    """16 experts, 4096 tokens routed by a seeded multinomial (Zipf s=1.1), K=4096, N=1408, int64 prefix-sum
+    offsets, bf16 out.  Reference: exact int accumulators from fp64 BLAS (|acc| < 2^53), then the epilogue
+    f32(f32(acc)*scale[g,n])*pts[m] in numpy float32 and torch's rne bfloat16 cast."""
+    rng = seeded(4)
+    G, T, K, N = 16, 4096, 4096, 1408
+    counts = zipf_counts(rng, T, G)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    x = rng.integers(-127, 128, (T, K), dtype=np.int8)
+    pts = np.exp(rng.uniform(np.log(1e-3), np.log(1e-1), T)).astype(np.float32)
+    w = rng.integers(-127, 128, (G, K, N), dtype=np.int8)
+    scale = np.exp(rng.uniform(np.log(1e-4), np.log(1e-2), (G, N))).astype(np.float32)
+    y = ascq_gpu.quant_group_matmul(_dev(x), _dev(pts), _dev(w), _dev(scale), _dev(offsets), 0)
+    got = y.cpu().view(torch.int16).numpy().view(np.uint16)
+    xf = x.astype(np.float64)
+    for g in range(G):
+        s, e = offsets[g], offsets[g + 1]
+        if e == s:
+            continue
+        acc = (xf[s:e] @ w[g].astype(np.float64)).astype(np.float32)  # exact int -> f32 rne
+        v = (acc * scale[g][None, :]).astype(np.float32) * pts[s:e, None]
+        np.testing.assert_array_equal(got[s:e], bf16_bits_of_f32(v.astype(np.float32)), err_msg=f"group {g}")

@@ -1,0 +1,144 @@
+"""GPU parity: int8 Matmul with fused dequant (DEQF16 / QS322BF16 / raw int32) through the Matmul handle.
+
+int32 accumulators and the dequantised outputs are bit-exact vs the oracle."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from conftest import seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _quant_words(rng, n, lo=2.0 ** -12, hi=2.0 ** -6):
+    s = np.exp(rng.uniform(np.log(lo), np.log(hi), n)).astype(np.float32)
+    return s.view(np.uint32).astype(np.uint64)  # (uint64)(*(uint32*)&f): matmul_quant.asc:111-113
+
+
+def _run(ascq, A, B, bias, c_type, words=None, scalar=None, trans_b=False, M=None, N=None, K=None):
+    M = M or A.shape[0]
+    K = K or A.shape[1]
+    N = N or (B.shape[0] if trans_b else B.shape[1])
+    torch_c = {ascq.F16: torch.float16, ascq.BF16: torch.bfloat16, ascq.INT32: torch.int32}[c_type]
+    mm = ascq.Matmul(ascq.INT8, ascq.INT8, c_type, ascq.INT32 if bias is not None else 0)
+    mm.SetOrgShape(M, N, K)
+    if words is not None:
+        mm.SetQuantVector(_dev(words.view(np.int64)))
+    elif scalar is not None:
+        mm.SetQuantScalar(scalar)
+    mm.SetTensorA(_dev(A))
+    mm.SetTensorB(_dev(B), trans_b)
+    if bias is not None:
+        mm.SetBias(_dev(bias))
+    c = torch.empty((M, N), dtype=torch_c, device="cuda")
+    mm.IterateAll(c)
+    mm.End()
+    torch.cuda.synchronize()
+    return c.cpu()
+
+
+def _bits(t):
+    return t.view(torch.int16).numpy().view(np.uint16) if t.dtype in (torch.float16, torch.bfloat16) else t.numpy()
+
+
+def test_config1_w8a8_per_channel_deqf16(ascq_gpu, oracle):
+    """W8A8: A [128,512], B [512,256] uniform [-127,127], int32 bias [-2^15,2^15], per-channel scale
+    log-uniform [2^-12, 2^-6] -> fp16 [128,256].  int32 bit-exact, fp16 bit-exact vs the oracle."""
+    rng = seeded(1)
+    M, K, N = 128, 512, 256
+    A = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-127, 128, (K, N), dtype=np.int8)
+    bias = rng.integers(-(1 << 15), (1 << 15) + 1, N, dtype=np.int32)
+    words = _quant_words(rng, N)
+    acc_ref = O.matmul_i8(A, B, bias)
+    c32 = _run(ascq_gpu, A, B, bias, ascq_gpu.INT32)
+    np.testing.assert_array_equal(c32.numpy(), acc_ref)
+    c16 = _run(ascq_gpu, A, B, bias, ascq_gpu.F16, words=words)
+    np.testing.assert_array_equal(_bits(c16), O.mm_dequant(acc_ref, O.F16, qvec=words))
+
+
+@pytest.mark.parametrize("c_type", ["f16", "bf16"])
+@pytest.mark.parametrize("vector", [False, True])
+@pytest.mark.parametrize("trans_b", [False, True])
+@pytest.mark.parametrize("shape", [(128, 256, 512), (77, 200, 96), (300, 132, 1040), (1, 16, 16), (1024, 1024, 1024)])
+def test_int8_matmul_variants(ascq_gpu, oracle, c_type, vector, trans_b, shape):
+    rng = seeded(sum(shape) + 3 * vector + trans_b)
+    M, N, K = shape
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, (N, K) if trans_b else (K, N), dtype=np.int8)
+    bias = rng.integers(-(1 << 20), 1 << 20, N, dtype=np.int32)
+    acc_ref = O.matmul_i8(A, B, bias, trans_b=trans_b)
+    code = ascq_gpu.F16 if c_type == "f16" else ascq_gpu.BF16
+    ocode = O.F16 if c_type == "f16" else O.BF16
+    if vector:
+        words = _quant_words(rng, N, 2.0 ** -20, 2.0 ** -4)
+        c = _run(ascq_gpu, A, B, bias, code, words=words, trans_b=trans_b)
+        ref = O.mm_dequant(acc_ref, ocode, qvec=words)
+    else:
+        word = int(np.float32(0.00123).view(np.uint32))
+        c = _run(ascq_gpu, A, B, bias, code, scalar=word, trans_b=trans_b)
+        ref = O.mm_dequant(acc_ref, ocode, qscalar=word)
+    np.testing.assert_array_equal(_bits(c), ref)
+
+
+def test_int8_matmul_int32_big(ascq_gpu, oracle):
+    rng = seeded(9)
+    M, N, K = 2048, 1536, 2048
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, (K, N), dtype=np.int8)
+    c = _run(ascq_gpu, A, B, None, ascq_gpu.INT32)
+    # exact in float64 BLAS: |sum| < 2^53
+    ref = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.int64).astype(np.int32)
+    np.testing.assert_array_equal(c.numpy(), ref)
+
+
+def test_deqf16_saturation_and_sign(ascq_gpu, oracle):
+    """DEQF16 saturates to +-65504; negative and power-of-two scales; acc = 0."""
+    M, K, N = 32, 64, 64
+    A = np.full((M, K), 127, np.int8)
+    A[1] = -127
+    A[2] = 0
+    B = np.full((K, N), 127, np.int8)
+    s = np.full(N, 1.0, np.float32)
+    s[1::4] = -0.5
+    s[2::4] = 2.0 ** -10
+    s[3::4] = 123.456  # acc*s far beyond 65504 -> saturates
+    words = s.view(np.uint32).astype(np.uint64)
+    c = _run(ascq_gpu, A, B, None, ascq_gpu.F16, words=words)
+    ref = O.mm_dequant(O.matmul_i8(A, B), O.F16, qvec=words)
+    got = _bits(c)
+    np.testing.assert_array_equal(got, ref)
+    assert (got[0, 3::4] == 0x7BFF).all() and (got[1, 3::4] == 0xFBFF).all() and (got[2] == 0).all()
+
+
+def test_single_shape_block(ascq_gpu, oracle):
+    """SetSingleShape / SetTail: compute one block of a larger matrix with org-shape leading dimensions,
+    the way the reference kernel offsets its GlobalTensors per core (matmul_quant.asc:135-154)."""
+    rng = seeded(5)
+    M, N, K = 256, 512, 256
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, (K, N), dtype=np.int8)
+    ref = O.matmul_i8(A, B)
+    a_d, b_d = _dev(A), _dev(B)
+    c = torch.zeros((M, N), dtype=torch.int32, device="cuda")
+    m0, n0, bm, bn = 64, 128, 100, 200
+    mm = ascq_gpu.Matmul(ascq_gpu.INT8, ascq_gpu.INT8, ascq_gpu.INT32)
+    mm.SetOrgShape(M, N, K)
+    mm.SetSingleShape(128, 256, K)
+    mm.SetTail(bm, bn)
+    mm.SetTensorA(a_d.data_ptr() + m0 * K)
+    mm.SetTensorB(b_d.data_ptr() + n0)
+    mm.IterateAll(c.data_ptr() + (m0 * N + n0) * 4)
+    mm.End()
+    got = c.cpu().numpy()
+    np.testing.assert_array_equal(got[m0:m0 + bm, n0:n0 + bn], ref[m0:m0 + bm, n0:n0 + bn])
+    mask = np.ones_like(got, bool)
+    mask[m0:m0 + bm, n0:n0 + bn] = False
+    assert (got[mask] == 0).all()

@@ -1,0 +1,119 @@
+"""GPU parity: MX-FP4 block-scaled Matmul (E2M1 elements, E8M0 per 32 K) vs the fp64 dequant-then-matmul
+golden of the reference (matmul_mxfp4_high_performance/scripts/gen_data.py).
+
+Tolerance: the workload's rel-err <= 1e-3 (normwise), and per element the bf16 output lies within
+ulp_bf16(|s| + d)/2 + d of the exact sum s, d = K * 2^-24 * sum|a*b| (fp32 accumulation bound)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from conftest import seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _ulp_bf16(v):
+    a = np.maximum(np.abs(v), 2.0 ** -126)
+    return 2.0 ** (np.floor(np.log2(a)) - 7)
+
+
+def bf16_to_f64(bits):
+    return (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def mx_inputs(rng, M, N, K):
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    bt = rng.standard_normal((N, K)).astype(np.float32)
+    A, sA = O.mx_quantize_fp4(a)      # A [M, K/2], sA [M, K/32]
+    Bt, sBt = O.mx_quantize_fp4(bt)   # B^T [N, K/2], sB^T [N, K/32]
+    return A, sA, Bt, sBt
+
+
+def to_kn(Bt, N, K):
+    """[N, K] packed along K -> [K, N] packed along N (the reference's non-transposed B)."""
+    nib = np.stack([Bt & 0xF, Bt >> 4], -1).reshape(N, K)
+    t = np.ascontiguousarray(nib.T).reshape(-1)
+    return (t[0::2] | (t[1::2] << 4)).astype(np.uint8).reshape(K, N // 2)
+
+
+def scale_pairs(s_rows):
+    """[R, sK] -> [sK/2, R, 2] (gen_data.py:63 layout)."""
+    R, sK = s_rows.shape
+    return np.ascontiguousarray(s_rows.T.reshape(sK // 2, 2, R).transpose(0, 2, 1))
+
+
+def run_mx(ascq, A, sA, B, sB, M, N, K, trans_b, sa_t, sb_t, c_type):
+    mm = ascq.Matmul(ascq.FP4_E2M1, ascq.FP4_E2M1, c_type, 0, ascq.E8M0)
+    mm.SetOrgShape(M, N, K)
+    mm.SetTensorA(_dev(A))
+    mm.SetTensorB(_dev(B), trans_b)
+    mm.SetTensorScaleA(_dev(sA), sa_t)
+    mm.SetTensorScaleB(_dev(sB), sb_t)
+    c = torch.empty((M, N), dtype=torch.bfloat16 if c_type == ascq.BF16 else torch.float32, device="cuda")
+    mm.IterateAll(c)
+    mm.End()
+    torch.cuda.synchronize()
+    return c.cpu()
+
+
+def check(got_f64, exact, absd, K, rel=1e-3):
+    d = K * 2.0 ** -24 * absd
+    tol = 0.5 * _ulp_bf16(np.abs(exact) + d) + d
+    err = np.abs(got_f64 - exact)
+    assert (err <= tol).all(), f"{(err > tol).sum()} elements outside the bound; max {err.max()}"
+    r = np.linalg.norm(got_f64 - exact) / max(np.linalg.norm(exact), 1e-30)
+    assert r <= rel, f"normwise rel err {r}"
+
+
+@pytest.mark.parametrize("trans_b", [True, False])
+@pytest.mark.parametrize("sa_t", [0, 1])
+@pytest.mark.parametrize("sb_t", [0, 1])
+@pytest.mark.parametrize("shape", [(256, 256, 512), (64, 96, 128), (130, 70, 384)])
+def test_mx_small(ascq_gpu, oracle, trans_b, sa_t, sb_t, shape):
+    M, N, K = shape
+    rng = seeded(M + N + K)
+    A, sA, Bt, sBt = mx_inputs(rng, M, N, K)
+    # scale exponents spread over a wide range to exercise the per-block scaling
+    sA = (sA.astype(np.int32) + rng.integers(-20, 21, sA.shape)).clip(1, 254).astype(np.uint8)
+    sBt = (sBt.astype(np.int32) + rng.integers(-20, 21, sBt.shape)).clip(1, 254).astype(np.uint8)
+    sA_dev = scale_pairs(sA) if sa_t else sA                 # isTransposeScaleA: [sK/2, M, 2]
+    sB_dev = sBt if sb_t else scale_pairs(sBt)               # isTransposeScaleB: [N, sK]; else [sK/2, N, 2]
+    B_dev = Bt if trans_b else to_kn(Bt, N, K)
+    c = run_mx(ascq_gpu, A, sA_dev, B_dev, sB_dev, M, N, K, trans_b, sa_t, sb_t, ascq_gpu.BF16)
+    C, Ce, Ca = O.mx_matmul(A, Bt, sA, sBt, M, N, K, trans_b=True, sa_layout=0, sb_layout=1)
+    got = bf16_to_f64(c.view(torch.int16).numpy().view(np.uint16))
+    check(got, Ce, Ca, K)
+
+
+def test_mx_f32_out(ascq_gpu, oracle):
+    M, N, K = 128, 128, 256
+    rng = seeded(77)
+    A, sA, Bt, sBt = mx_inputs(rng, M, N, K)
+    c = run_mx(ascq_gpu, A, sA, Bt, sBt, M, N, K, True, 0, 1, ascq_gpu.F32)
+    _, Ce, Ca = O.mx_matmul(A, Bt, sA, sBt, M, N, K, trans_b=True, sa_layout=0, sb_layout=1)
+    got = c.numpy().astype(np.float64)
+    d = K * 2.0 ** -24 * Ca
+    assert (np.abs(got - Ce) <= d + 1e-30).all()
+
+
+@pytest.mark.parametrize("trans_b", [True, False])
+def test_config5_full_size_sampled(ascq_gpu, oracle, trans_b):
+    """A, B E2M1 [8192, 8192] from N(0,1), MX-quantised per 32-element K block, fp32 accumulate, bf16 out;
+    rows sampled across the whole output (the fp64 golden of every row would take minutes on the CPU)."""
+    M = N = K = 8192
+    rng = seeded(5)
+    A, sA, Bt, sBt = mx_inputs(rng, M, N, K)
+    B_dev = Bt if trans_b else to_kn(Bt, N, K)
+    sB_dev = sBt if trans_b else scale_pairs(sBt)
+    c = run_mx(ascq_gpu, A, sA, B_dev, sB_dev, M, N, K, trans_b, 0, 1 if trans_b else 0, ascq_gpu.BF16)
+    rows = np.unique(np.concatenate([[0, 1, 255, 256, 4095, 8191], rng.integers(0, M, 10)])).astype(np.int64)
+    _, Ce, Ca = O.mx_matmul(A, Bt, sA, sBt, M, N, K, trans_b=True, sa_layout=0, sb_layout=1, rows=rows)
+    got = bf16_to_f64(c.view(torch.int16).numpy().view(np.uint16)[rows])
+    check(got, Ce[rows], Ca[rows], K)

@@ -1,0 +1,213 @@
+"""GPU parity: AscendQuant / AscendDequant / AscendAntiQuant through the C ABI vs the oracle (bit-exact)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from conftest import seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def _f16_input(rng, m, n, outlier_frac=0.001, outlier_mult=50.0):
+    x = rng.standard_normal((m, n)).astype(np.float32)
+    k = max(1, int(m * n * outlier_frac))
+    idx = rng.choice(m * n, size=k, replace=False)
+    x.ravel()[idx] *= outlier_mult
+    return x.astype(np.float16)
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("m,n", [(64, 8192), (33, 4096), (7, 16384), (5, 1000), (3, 8), (2, 24), (1, 65536)])
+def test_dynamic_per_token_f16(ascq_gpu, oracle, m, n):
+    rng = seeded(100 + m + n)
+    x = _f16_input(rng, m, n)
+    q, s = ascq_gpu.quant_dynamic_per_token(_dev(x))
+    torch.cuda.synchronize()
+    q_ref, s_ref = O.quant_dynamic_per_token(x.view(np.uint16), O.F16)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("mode", [O.ROUND_RINT, O.ROUND_FLOOR, O.ROUND_CEIL, O.ROUND_ROUND, O.ROUND_TRUNC])
+def test_dynamic_per_token_round_modes(ascq_gpu, oracle, mode):
+    rng = seeded(7 + mode)
+    x = _f16_input(rng, 16, 2048)
+    # plant exact ties: values whose scaled magnitude lands on k + 0.5 (row absmax fixed at 127)
+    x[:, 0] = np.float16(127.0)
+    x[:, 1:9] = np.array([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5], np.float16)
+    q, s = ascq_gpu.quant_dynamic_per_token(_dev(x), round_mode=mode)
+    q_ref, s_ref = O.quant_dynamic_per_token(x.view(np.uint16), O.F16, mode)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+
+
+@pytest.mark.parametrize("dtype,code", [(torch.bfloat16, O.BF16), (torch.float32, O.F32)])
+def test_dynamic_per_token_other_src(ascq_gpu, oracle, dtype, code):
+    rng = seeded(11)
+    x = torch.from_numpy(rng.standard_normal((9, 3000)).astype(np.float32)).to(dtype)
+    q, s = ascq_gpu.quant_dynamic_per_token(x.cuda())
+    xn = x.view(torch.int16).numpy().view(np.uint16) if dtype == torch.bfloat16 else x.numpy()
+    q_ref, s_ref = O.quant_dynamic_per_token(xn, code)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+
+
+def test_dynamic_per_token_zero_rows(ascq_gpu, oracle):
+    x = np.zeros((4, 512), np.float16)
+    x[2, 5] = np.float16(-3.0)
+    q, s = ascq_gpu.quant_dynamic_per_token(_dev(x))
+    q_ref, s_ref = O.quant_dynamic_per_token(x.view(np.uint16), O.F16)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    assert s_ref[0] == 0 and q_ref[2, 5] == -127
+
+
+@pytest.mark.parametrize("src", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("has_offset", [False, True])
+def test_per_token_given_scale(ascq_gpu, oracle, src, has_offset):
+    rng = seeded(21)
+    m, n = 13, 777
+    x32 = rng.standard_normal((m, n)).astype(np.float32) * 4
+    scale = rng.uniform(0.5, 20.0, m).astype(np.float32)
+    offset = rng.uniform(-5, 5, m).astype(np.float32) if has_offset else None
+    if src == "f16":
+        xt = torch.from_numpy(x32.astype(np.float16))
+        xn, code = x32.astype(np.float16).view(np.uint16), O.F16
+    elif src == "bf16":
+        xt = torch.from_numpy(x32).to(torch.bfloat16)
+        xn, code = xt.view(torch.int16).numpy().view(np.uint16), O.BF16
+    else:
+        xt = torch.from_numpy(x32)
+        xn, code = x32, O.F32
+    q = ascq_gpu.quant_per_token(xt.cuda(), _dev(scale), None if offset is None else _dev(offset))
+    q_ref = O.quant_per_token(xn, code, scale, offset)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+@pytest.mark.parametrize("src", ["f16", "f32"])
+def test_legacy_quant_f16_arith(ascq_gpu, oracle, per_channel, src):
+    rng = seeded(31)
+    n_total, sc = 4096, 64
+    x32 = rng.uniform(-8, 8, n_total).astype(np.float32)
+    if per_channel:
+        scale = rng.uniform(0.5, 8, sc).astype(np.float16)
+        offset = rng.uniform(-2, 2, sc).astype(np.float16)
+        q = ascq_gpu.ascend_quant(torch.from_numpy(x32.astype(np.float16) if src == "f16" else x32).cuda(),
+                                  scale=_dev(scale), offset=_dev(offset))
+        q_ref = O.quant_legacy_f16(x32.astype(np.float16).view(np.uint16) if src == "f16" else x32,
+                                   O.F16 if src == "f16" else O.F32, scale_vec=scale.view(np.uint16),
+                                   offset_vec=offset.view(np.uint16), scale_count=sc)
+    else:
+        q = ascq_gpu.ascend_quant(torch.from_numpy(x32.astype(np.float16) if src == "f16" else x32).cuda(),
+                                  scale_scalar=2.0, offset_scalar=0.9)
+        q_ref = O.quant_legacy_f16(x32.astype(np.float16).view(np.uint16) if src == "f16" else x32,
+                                   O.F16 if src == "f16" else O.F32, scale_scalar=0x4000,
+                                   offset_scalar=int(np.float16(0.9).view(np.uint16)))
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("m,n", [(64, 8192), (5, 48), (3, 20)])
+def test_dequant_per_token_int8(ascq_gpu, oracle, m, n):
+    rng = seeded(41 + n)
+    q = rng.integers(-128, 128, (m, n), dtype=np.int8)
+    scale = (rng.uniform(0.0, 1.0, m) * 0.05).astype(np.float32)
+    y = ascq_gpu.ascend_dequant(_dev(q), _dev(scale), ascq_gpu.PER_TOKEN, torch.float16)
+    y_ref = O.dequant(q, O.INT8, scale, O.F32, O.PER_TOKEN, O.F16)
+    np.testing.assert_array_equal(y.cpu().numpy().view(np.uint16), y_ref)
+
+
+@pytest.mark.parametrize("dst", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("scale_kind", ["f32", "f16", "u64"])
+def test_dequant_per_channel_int32(ascq_gpu, oracle, dst, scale_kind):
+    """Legacy DequantParams{m, n, calCount}: columns >= calCount must be left untouched."""
+    rng = seeded(51)
+    m, n, cal = 128, 32, 24
+    src = rng.integers(-(1 << 20), 1 << 20, (m, n), dtype=np.int32)
+    s32 = rng.uniform(-100, 100, n).astype(np.float32)
+    if scale_kind == "f32":
+        st, sn, code = torch.from_numpy(s32), s32, O.F32
+    elif scale_kind == "f16":
+        st, sn, code = torch.from_numpy(s32.astype(np.float16)), s32.astype(np.float16), O.F16
+    else:
+        words = s32.view(np.uint32).astype(np.uint64) | (np.uint64(0xABC) << np.uint64(40))
+        st, sn, code = torch.from_numpy(words.view(np.int64)), words, O.U64
+    init = torch.full((m, n), 7.0, dtype=dst)
+    out = init.cuda()
+    ascq_gpu.ascend_dequant(_dev(src), st.cuda(), ascq_gpu.PER_CHANNEL, dst, cal_count=cal, out=out)
+    dst_code = {torch.float16: O.F16, torch.bfloat16: O.BF16, torch.float32: O.F32}[dst]
+    if dst == torch.float32:
+        ref0, got = init.numpy().copy(), out.cpu().numpy()
+    else:
+        ref0, got = init.view(torch.int16).numpy().view(np.uint16).copy(), out.cpu().view(torch.int16).numpy().view(np.uint16)
+    y_ref = O.dequant(src, O.INT32, sn, code, O.PER_CHANNEL, dst_code, cal_count=cal, dst=ref0)
+    np.testing.assert_array_equal(got.view(np.uint32) if dst == torch.float32 else got,
+                                  y_ref.view(np.uint32) if dst == torch.float32 else y_ref)
+    assert (got[:, cal:] == ref0[:, cal:]).all()
+
+
+def test_dequant_per_tensor(ascq_gpu, oracle):
+    rng = seeded(61)
+    src = rng.integers(-(1 << 24), 1 << 24, (17, 40), dtype=np.int32)
+    y = ascq_gpu.ascend_dequant(_dev(src), None, ascq_gpu.PER_TENSOR, torch.bfloat16, scale_scalar=0.0123)
+    y_ref = O.dequant(src, O.INT32, None, 0, O.PER_TENSOR, O.BF16, scale_scalar=np.float32(0.0123))
+    np.testing.assert_array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), y_ref)
+
+
+@pytest.mark.parametrize("src_type", ["int8", "int4"])
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("group", [0, 32, 128])
+@pytest.mark.parametrize("dst,arith", [("f16", 0), ("f16", 1), ("bf16", 1)])
+@pytest.mark.parametrize("with_offset", [True, False])
+def test_antiquant(ascq_gpu, oracle, src_type, transpose, group, dst, arith, with_offset):
+    rng = seeded(71)
+    K, N = 256, 96
+    G = K // group if group else 1
+    if src_type == "int8":
+        w = rng.integers(-128, 128, (N, K) if transpose else (K, N), dtype=np.int8)
+        code = O.INT8
+    else:
+        nib = rng.integers(0, 16, K * N, dtype=np.uint8)
+        w = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8)
+        code = O.INT4
+    sshape = (N, G) if transpose else (G, N)
+    scale32 = np.exp(rng.uniform(np.log(1e-3), np.log(1e-1), sshape)).astype(np.float32)
+    off32 = rng.uniform(-8, 8, sshape).astype(np.float32)
+    if dst == "f16":
+        scale_t, off_t = torch.from_numpy(scale32.astype(np.float16)), torch.from_numpy(off32.astype(np.float16))
+        dtt, dcode = torch.float16, O.F16
+    else:
+        scale_t, off_t = torch.from_numpy(scale32).to(torch.bfloat16), torch.from_numpy(off32).to(torch.bfloat16)
+        dtt, dcode = torch.bfloat16, O.BF16
+    off_dev = off_t.cuda() if with_offset else None
+    y = ascq_gpu.ascend_antiquant(_dev(w), ascq_gpu.INT8 if src_type == "int8" else ascq_gpu.INT4, scale_t.cuda(),
+                                  off_dev, K, N, group, transpose, dtt, arith)
+    y_ref = O.antiquant(w, code, scale_t.view(torch.int16).numpy().view(np.uint16),
+                        off_t.view(torch.int16).numpy().view(np.uint16) if with_offset else None,
+                        K, N, group, transpose, dcode, arith)
+    np.testing.assert_array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), y_ref)
+
+
+def test_config2_full_size_quant_dequant(ascq_gpu, oracle):
+    """AscendQuant per-token dynamic quant f16 [8192, 8192] (0.1% outliers x50) -> int8 + fp32 scale, then
+    AscendDequant back to f16: both outputs bit-exact vs the oracle at the full workload size."""
+    rng = seeded(2)
+    m = n = 8192
+    x = _f16_input(rng, m, n)
+    xd = _dev(x)
+    q, s = ascq_gpu.quant_dynamic_per_token(xd)
+    y = ascq_gpu.ascend_dequant(q, s, ascq_gpu.PER_TOKEN, torch.float16)
+    torch.cuda.synchronize()
+    q_ref, s_ref = O.quant_dynamic_per_token(x.view(np.uint16), O.F16)
+    qn = q.cpu().numpy()
+    np.testing.assert_array_equal(qn, q_ref)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    assert np.abs(qn.astype(np.int32)).max() <= 127
+    y_ref = O.dequant(q_ref, O.INT8, s_ref, O.F32, O.PER_TOKEN, O.F16)
+    np.testing.assert_array_equal(y.cpu().numpy().view(np.uint16), y_ref)
