@@ -1,0 +1,380 @@
+"""Pins of the oracle (CPU, no GPU).
+
+Every oracle function is checked against something other than its own formula:
+  * the reference examples' golden procedures (tests/golden/*.npz, see make_golden.py) with the reference's
+    verification tolerances where its golden is itself approximate;
+  * trusted IEEE implementations: numpy float16 casts, torch bfloat16 / float8 casts, numpy float32 arithmetic;
+  * closed forms and brute force on small inputs (exact rationals, nearest-neighbour search over a codebook).
+"""
+from __future__ import annotations
+
+import math
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+
+GOLD = Path(__file__).resolve().parent / "golden"
+rng0 = np.random.default_rng(12345)
+
+
+def ref_verify(out, golden, rtol=1e-3, atol=1e-3, err_tol=1e-3):
+    """verify_result.py of the reference examples: np.isclose with rtol/atol, error ratio <= err_tol."""
+    bad = ~np.isclose(out.astype(np.float64), golden.astype(np.float64), rtol=rtol, atol=atol, equal_nan=True)
+    return bad.mean() <= err_tol
+
+
+# --------------------------------------------------------------------------- scalar codecs
+def _random_f32(n):
+    bits = rng0.integers(0, 2 ** 32, n, dtype=np.uint64).astype(np.uint32)
+    specials = np.array([0, 0x80000000, 0x33000000, 0x33000001, 0x387FE000, 0x387FF000, 0x38800000, 0x477FE000,
+                         0x477FEFFF, 0x477FF000, 0x477FF001, 0x7F800000, 0xFF800000, 0x7FC00000, 0x3F801000,
+                         0x3F803000, 0x3F800FFF, 0x00000001], np.uint32)
+    # values in the f16 range with exact ties at the 13 discarded bits
+    ties = (rng0.integers(0x33000000, 0x47800000, n // 4, dtype=np.uint64).astype(np.uint32) & ~np.uint32(0x1FFF)) | 0x1000
+    return np.concatenate([bits, specials, ties]).view(np.float32)
+
+
+def test_f32_to_f16_matches_numpy():
+    x = _random_f32(40000)
+    got = O.f32_to_f16(x, sat=False)
+    exp = x.astype(np.float16).view(np.uint16)
+    nan = np.isnan(x)
+    assert (got[~nan] == exp[~nan]).all()
+    assert np.isnan(got[nan].view(np.float16)).all()
+
+
+def test_f32_to_f16_saturating():
+    x = _random_f32(20000)
+    got = O.f32_to_f16(x, sat=True).view(np.float16).astype(np.float32)
+    fin = ~np.isnan(x)
+    exp = np.clip(x[fin], -65504, 65504).astype(np.float16).astype(np.float32)
+    assert (got[fin] == exp).all()
+
+
+def test_f16_to_f32_all_codes():
+    L = O.lib()
+    codes = np.arange(65536, dtype=np.uint16)
+    got = np.array([L.oq_f16_to_f32(int(c)) for c in codes], np.float32)
+    exp = codes.view(np.float16).astype(np.float32)
+    nan = np.isnan(exp)
+    assert (got[~nan].view(np.uint32) == exp[~nan].view(np.uint32)).all() and np.isnan(got[nan]).all()
+
+
+def test_f32_to_bf16_matches_torch():
+    L = O.lib()
+    x = _random_f32(30000)
+    x = x[np.isfinite(x) & (np.abs(x) < 3.38e38)]
+    got = np.array([L.oq_f32_to_bf16(float(v), 0) for v in x], np.uint16)
+    exp = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert (got == exp).all()
+    assert L.oq_f32_to_bf16(3.4e38, 1) == 0x7F7F and L.oq_f32_to_bf16(float("inf"), 1) == 0x7F7F
+    assert L.oq_f32_to_bf16(-float("inf"), 1) == 0xFF7F
+
+
+def test_f64_to_f16_matches_numpy():
+    L = O.lib()
+    d = np.concatenate([rng0.standard_normal(20000) * 10.0 ** rng0.integers(-8, 5, 20000),
+                        np.array([1 + 2.0 ** -11, 1 + 2.0 ** -11 + 2.0 ** -40, 2.0 ** -25, 3 * 2.0 ** -26, 65519.99,
+                                  65520.0, 2049.0, 2051.0])])
+    got = np.array([L.oq_f64_to_f16(float(v), 0) for v in d], np.uint16)
+    exp = d.astype(np.float16).view(np.uint16)
+    assert (got == exp).all()
+
+
+def _nearest_even(d, grid):
+    """brute-force round-to-nearest-even of d onto a sorted grid of (value, code) pairs"""
+    vals = grid[0]
+    i = np.searchsorted(vals, d)
+    cands = [j for j in (i - 1, i) if 0 <= j < len(vals)]
+    best = min(cands, key=lambda j: (abs(vals[j] - d), grid[1][j] & 1))
+    return grid[1][best]
+
+
+def test_f64_to_bf16_brute_force():
+    L = O.lib()
+    codes = np.arange(0, 0x7F80, dtype=np.uint16)
+    vals = (codes.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    grid = (vals, codes)
+    for d in np.concatenate([np.abs(rng0.standard_normal(3000)) * 10.0 ** rng0.integers(-30, 30, 3000),
+                             vals[1000:1010] + (vals[1001:1011] - vals[1000:1010]) / 2]):
+        assert L.oq_f64_to_bf16(float(d), 0) == _nearest_even(d, grid)
+        assert L.oq_f64_to_bf16(float(-d), 0) == (_nearest_even(d, grid) | 0x8000)
+
+
+def test_quant_pre_m1_matches_gen_data_decode():
+    """accompanying_quantization.md table 1 / gen_data_s322f16.py extract_quant_params: M1 = (-1)^s (1+m/1024)
+    2^(e-127) from bits [31:13]; offset bits [45:37]; sign flag bit 46."""
+    L = O.lib()
+    for f in [0.1, 1.0, -0.5, 3.14159, 2.0 ** -12, 1e-30, 65504.0, -7.7e10]:
+        w = L.oq_pack_quant_pre(f, 0, 0)
+        bits = (w >> 13) & 0xFFFFF
+        s, e, m = (bits >> 18) & 1, (bits >> 10) & 0xFF, bits & 0x3FF
+        ref = (-1) ** s * (1 + m / 1024) * 2.0 ** (e - 127)
+        assert L.oq_quant_pre_m1(w) == np.float32(ref)
+    w = L.oq_pack_quant_pre(1.0, -5, 1)
+    assert (w >> 37) & 0x1FF == (-5) & 0x1FF and (w >> 46) & 1 == 1
+    assert L.oq_quant_pre_m1(np.float32(0.1).view(np.uint32)) == np.float32(0.0999755859375)
+
+
+@pytest.mark.parametrize("mode,fn", [(O.ROUND_RINT, np.rint), (O.ROUND_FLOOR, np.floor), (O.ROUND_CEIL, np.ceil),
+                                     (O.ROUND_TRUNC, np.trunc),
+                                     (O.ROUND_ROUND, lambda v: np.sign(v) * np.floor(np.abs(v) + 0.5))])
+def test_round_modes(mode, fn):
+    L = O.lib()
+    v = np.concatenate([np.arange(-40, 41) / 4.0, rng0.uniform(-300, 300, 500)]).astype(np.float32)
+    got = np.array([L.oq_round_to_int(float(x), mode) for x in v])
+    assert (got == fn(v.astype(np.float64)).astype(np.int64)).all()
+    assert L.oq_round_to_int(float("nan"), mode) == 0
+
+
+# --------------------------------------------------------------------------- MX / fp8 codecs
+E2M1 = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]  # OCP MX v1.0 table of E2M1 magnitudes
+
+
+def test_e2m1_decode_table():
+    L = O.lib()
+    for c in range(16):
+        v = E2M1[c & 7] * (-1 if c & 8 else 1)
+        assert L.oq_e2m1_decode(c) == v
+
+
+def test_e2m1_encode_nearest_even():
+    L = O.lib()
+    pos = [(E2M1[c], c) for c in range(8)]
+    xs = np.concatenate([rng0.uniform(-8, 8, 4000), [0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, 7.0, -0.25, -5.0]])
+    for x in xs:
+        a = abs(float(x))
+        best = min(pos, key=lambda p: (abs(p[0] - a), p[1] & 1))[1]
+        exp = best | (8 if x < 0 else 0)
+        got = L.oq_e2m1_encode_rne(float(x))
+        assert got == exp or (best == 0 and got & 7 == 0), (x, got, exp)
+
+
+def test_e8m0_and_shared_exp():
+    L = O.lib()
+    for e in range(255):
+        assert L.oq_e8m0_decode(e) == np.float32(2.0 ** (e - 127))
+    assert math.isnan(L.oq_e8m0_decode(255))
+    for a in list(rng0.uniform(1e-6, 1e6, 500)) + [1.0, 4.0, 0.75, 6.0, 6.01]:
+        assert L.oq_mx_shared_exp(float(np.float32(a))) == math.floor(math.log2(float(np.float32(a)))) - 2 + 127
+
+
+@pytest.mark.parametrize("fmt,tdt", [(O.FP8_E4M3, torch.float8_e4m3fn), (O.FP8_E5M2, torch.float8_e5m2)])
+def test_fp8_decode_matches_torch(fmt, tdt):
+    L = O.lib()
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    exp = codes.view(tdt).to(torch.float32).numpy()
+    got = np.array([L.oq_fp8_decode(int(c), fmt) for c in range(256)], np.float32)
+    nan = np.isnan(exp)
+    assert np.isnan(got[nan]).all() and (got[~nan] == exp[~nan]).all()
+
+
+# --------------------------------------------------------------------------- ops vs golden fixtures
+def test_deqf16_seed9_golden_exact():
+    f = np.load(GOLD / "deqf16_seed9.npz")
+    acc = O.matmul_i8(f["x1"], f["x2"])
+    out = O.mm_dequant(acc, O.F16, qscalar=int(f["quant_word"][0]))
+    assert (out == f["golden"].view(np.uint16)).all()
+
+
+def test_matmul_quant_vector_golden_within_reference_tolerance():
+    f = np.load(GOLD / "matmul_quant_vector.npz")
+    acc = O.matmul_i8(f["x1"], f["x2"], f["bias"])
+    out = O.mm_dequant(acc, O.F16, qvec=f["quant_words"]).view(np.float16)
+    g = f["golden"]
+    assert ref_verify(out, g)
+    # the golden rounds acc to f16 before the multiply; the fixpipe multiplies the exact acc: identical
+    # whenever acc is exactly representable in f16
+    small = np.abs(acc) <= 2048
+    assert (out[small] == g[small]).all()
+
+
+def test_quant_example_golden_exact():
+    f = np.load(GOLD / "quant_example.npz")
+    q = O.quant_legacy_f16(f["src"].view(np.uint16), O.F16, scale_scalar=0x4000,
+                           offset_scalar=int(np.float16(0.9).view(np.uint16)))
+    assert (q == f["golden"]).all()
+
+
+def test_dequant_example_golden_exact():
+    f = np.load(GOLD / "dequant_example.npz")
+    y = O.dequant(f["inp"], O.INT32, f["scale"], O.F32, O.PER_CHANNEL, O.F32, cal_count=32)
+    assert (y.view(np.uint32) == f["golden"].view(np.uint32)).all()
+
+
+@pytest.mark.parametrize("arch,arith", [("2201", O.ARITH_F16), ("3510", O.ARITH_F32)])
+def test_antiquant_seed10_golden_exact(arch, arith):
+    f = np.load(GOLD / "antiquant_seed10.npz")
+    y = O.antiquant(f["src"], O.INT8, f["scale"].view(np.uint16), f["offset"].view(np.uint16), 8, 128, 8, False,
+                    O.F16, arith)
+    assert (y == f[f"golden_{arch}"].view(np.uint16)).all()
+
+
+def test_group_matmul_golden_within_reference_tolerance():
+    f = np.load(GOLD / "group_matmul_example.npz")
+    G, (m, k), n = 4, f["x"].shape, f["weight"].shape[2]
+    y = O.group_matmul(f["x"], f["pts"], f["weight"], f["scale"], f["group_list"], 1, G, m, k, n, O.F16)
+    # verify_result.py of that example: rtol = atol = 1e-3, error ratio <= 1e-4
+    assert ref_verify(y.view(np.float16), f["golden"], err_tol=1e-4)
+
+
+def test_mx_example_golden_exact():
+    f = np.load(GOLD / "mx_example.npz")
+    M = N = K = 256
+    Bt = np.ascontiguousarray(f["b_packed"])
+    C, Ce, _ = O.mx_matmul(f["a_packed"], Bt, f["scale_a"], f["scale_b_pairs"], M, N, K, trans_b=False,
+                           sa_layout=0, sb_layout=0)
+    assert (C == f["golden_bf16"]).all()
+
+
+# --------------------------------------------------------------------------- ops vs independent numpy / exact
+def test_matmul_i8_vs_numpy():
+    A = rng0.integers(-128, 128, (37, 300), dtype=np.int8)
+    B = rng0.integers(-128, 128, (300, 45), dtype=np.int8)
+    bias = rng0.integers(-(2 ** 31), 2 ** 31 - 1, 45, dtype=np.int64).astype(np.int32)
+    exp = (A.astype(np.int64) @ B.astype(np.int64) + bias).astype(np.int64)
+    exp = ((exp + 2 ** 31) % 2 ** 32 - 2 ** 31).astype(np.int32)  # two's-complement wrap
+    assert (O.matmul_i8(A, B, bias) == exp).all()
+    assert (O.matmul_i8(A, np.ascontiguousarray(B.T), bias, trans_b=True) == exp).all()
+    assert (O.matmul_i8(np.ascontiguousarray(A.T), B, bias, trans_a=True) == exp).all()
+
+
+def test_mm_dequant_vs_numpy_f32():
+    acc = rng0.integers(-(2 ** 26), 2 ** 26, (64, 48)).astype(np.int32)
+    s = (np.exp(rng0.uniform(-20, 5, 48)) * np.where(rng0.random(48) < 0.2, -1, 1)).astype(np.float32)
+    words = s.view(np.uint32).astype(np.uint64)
+    m1 = (s.view(np.uint32) & np.uint32(0xFFFFE000)).view(np.float32)
+    exp16 = np.clip(acc.astype(np.float32) * m1, -65504, 65504).astype(np.float16).view(np.uint16)
+    assert (O.mm_dequant(acc, O.F16, qvec=words) == exp16).all()
+    expb = torch.from_numpy(acc.astype(np.float32) * m1).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert (O.mm_dequant(acc, O.BF16, qvec=words) == expb).all()
+
+
+def test_quant_per_token_vs_numpy():
+    x = (rng0.standard_normal((20, 300)) * 30).astype(np.float32)
+    s = rng0.uniform(0.1, 3, 20).astype(np.float32)
+    o = rng0.uniform(-4, 4, 20).astype(np.float32)
+    v = x * s[:, None] + o[:, None]
+    exp = np.clip(np.rint(v), -128, 127).astype(np.int8)
+    assert (O.quant_per_token(x, O.F32, s, o) == exp).all()
+    exp_floor = np.clip(np.floor(x * s[:, None]), -128, 127).astype(np.int8)
+    assert (O.quant_per_token(x, O.F32, s, None, O.ROUND_FLOOR) == exp_floor).all()
+
+
+def test_dynamic_quant_invariants_and_numpy():
+    x = rng0.standard_normal((50, 1024)).astype(np.float32)
+    x[rng0.random(x.shape) < 0.001] *= 50
+    x16 = x.astype(np.float16)
+    q, s = O.quant_dynamic_per_token(x16.view(np.uint16), O.F16)
+    xf = x16.astype(np.float32)
+    amax = np.abs(xf).max(1)
+    mult = np.float32(127.0) / amax
+    assert (q == np.clip(np.rint(xf * mult[:, None]), -128, 127).astype(np.int8)).all()
+    assert (s == (amax / np.float32(127.0)).astype(np.float32)).all()
+    assert np.abs(q.astype(np.int32)).max() <= 127
+    # the row maximum maps to +-127 exactly
+    rows = np.arange(50)
+    assert (np.abs(q[rows, np.abs(xf).argmax(1)]) == 127).all()
+
+
+def _half_round_exact(fr: Fraction) -> np.float16:
+    """round an exact rational to binary16 (nearest, ties to even) by brute force over neighbouring codes"""
+    f = float(fr)
+    h = np.float16(f)
+    cands = [h, np.nextafter(h, np.float16(np.inf)), np.nextafter(h, np.float16(-np.inf))]
+    return min(cands, key=lambda c: (abs(Fraction(float(c)) - fr), int(c.view(np.uint16)) & 1))
+
+
+def test_legacy_quant_half_ops_exact_rationals():
+    x = rng0.uniform(-8, 8, 600).astype(np.float16)
+    sc = rng0.uniform(0.01, 30, 8).astype(np.float16)
+    of = (rng0.uniform(-3, 3, 8) * 10.0 ** rng0.integers(-6, 1, 8)).astype(np.float16)
+    q = O.quant_legacy_f16(x.view(np.uint16), O.F16, scale_vec=sc.view(np.uint16), offset_vec=of.view(np.uint16),
+                           scale_count=8)
+    for i in range(600):
+        t = _half_round_exact(Fraction(float(x[i])) * Fraction(float(sc[i % 8])))
+        t = _half_round_exact(Fraction(float(t)) + Fraction(float(of[i % 8])))
+        exp = int(np.clip(np.rint(np.float64(t)), -128, 127))
+        assert q[i] == exp
+
+
+def test_antiquant_f16_ops_exact_rationals_int4_groups():
+    K, N, g = 64, 6, 32
+    nib = rng0.integers(0, 16, K * N, dtype=np.uint8)
+    packed = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8)
+    qv = np.where(nib >= 8, nib.astype(np.int32) - 16, nib.astype(np.int32)).reshape(K, N)
+    sc = np.exp(rng0.uniform(-7, -2, (K // g, N))).astype(np.float16)
+    of = (rng0.uniform(-8, 8, (K // g, N)) * 10.0 ** rng0.integers(-5, 1, (K // g, N))).astype(np.float16)
+    y = O.antiquant(packed, O.INT4, sc.view(np.uint16), of.view(np.uint16), K, N, g).view(np.float16)
+    for k in range(K):
+        for n in range(N):
+            t = _half_round_exact(Fraction(int(qv[k, n])) + Fraction(float(of[k // g, n])))
+            t = _half_round_exact(Fraction(float(t)) * Fraction(float(sc[k // g, n])))
+            assert y[k, n] == t
+
+
+def test_antiquant_matmul_vs_numpy():
+    M, K, N, g = 3, 256, 32, 128
+    w = rng0.integers(-128, 128, (K, N), dtype=np.int8)
+    sc = np.exp(rng0.uniform(np.log(1e-3), np.log(1e-1), (K // g, N))).astype(np.float16)
+    of = rng0.uniform(-8, 8, (K // g, N)).astype(np.float16)
+    x = rng0.standard_normal((M, K)).astype(np.float16)
+    y, ye, ya = O.antiquant_matmul(x.view(np.uint16), w, O.INT8, sc.view(np.uint16), of.view(np.uint16), g, M, N, K)
+    wf = O.antiquant(w, O.INT8, sc.view(np.uint16), of.view(np.uint16), K, N, g).view(np.float16)
+    exact = x.astype(np.float64) @ wf.astype(np.float64)
+    assert np.allclose(ye, exact, rtol=1e-12, atol=1e-12)
+    assert (y.view(np.float16) == ye.astype(np.float16)).all()
+    assert np.allclose(ya, np.abs(x.astype(np.float64)) @ np.abs(wf.astype(np.float64)), rtol=1e-12)
+
+
+def test_group_matmul_vs_numpy_exact():
+    G, K, N = 3, 200, 40
+    counts = np.array([5, 0, 11], np.int64)
+    M = 20
+    x = rng0.integers(-127, 128, (M, K), dtype=np.int8)
+    w = rng0.integers(-127, 128, (G, K, N), dtype=np.int8)
+    pts = rng0.uniform(1e-3, 1e-1, M).astype(np.float32)
+    sc = rng0.uniform(1e-4, 1e-2, (G, N)).astype(np.float32)
+    y = O.group_matmul(x, pts, w, sc, counts, 1, G, M, K, N, O.BF16)
+    off = np.concatenate([[0], np.cumsum(counts)])
+    for g in range(G):
+        s, e = off[g], off[g + 1]
+        acc = (x[s:e].astype(np.int64) @ w[g].astype(np.int64)).astype(np.float32)
+        v = (acc * sc[g]) * pts[s:e, None]
+        exp = torch.from_numpy(v.astype(np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        assert (y[s:e] == exp).all()
+    assert (y[16:] == 0).all()
+
+
+def test_mx_matmul_vs_numpy_decode():
+    M, N, K = 8, 12, 128
+    A = rng0.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    Bt = rng0.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sA = rng0.integers(110, 140, (M, K // 32), dtype=np.uint8)
+    sB = rng0.integers(110, 140, (N, K // 32), dtype=np.uint8)
+    table = np.array([E2M1[c & 7] * (-1 if c & 8 else 1) for c in range(16)])
+
+    def dec(p, s):
+        v = table[np.stack([p & 0xF, p >> 4], -1).reshape(p.shape[0], -1)]
+        return v * 2.0 ** (np.repeat(s.astype(np.float64), 32, axis=1) - 127)
+
+    exact = dec(A, sA) @ dec(Bt, sB).T
+    _, Ce, _ = O.mx_matmul(A, Bt, sA, sB, M, N, K, trans_b=True, sa_layout=0, sb_layout=1)
+    assert np.allclose(Ce, exact, rtol=1e-13, atol=1e-13)
+
+
+def test_mx_quantize_fp4_roundtrip():
+    x = rng0.standard_normal((16, 256)).astype(np.float32)
+    p, s = O.mx_quantize_fp4(x)
+    table = np.array([E2M1[c & 7] * (-1 if c & 8 else 1) for c in range(16)])
+    v = table[np.stack([p & 0xF, p >> 4], -1).reshape(16, 256)] * 2.0 ** (np.repeat(s, 32, 1).astype(np.float64) - 127)
+    # every block max lands within the E2M1 range after scaling and the relative error is bounded by the
+    # coarsest E2M1 spacing (half of 2 at magnitude 4..6 -> 1/4 of the block scale * 4)
+    blk = np.abs(x.reshape(16, 8, 32)).max(-1)
+    assert (blk / 2.0 ** (s.astype(np.float64) - 127) < 8).all()
+    assert np.abs(v - x).max() <= (2.0 ** (s.astype(np.float64) - 127)).max()
