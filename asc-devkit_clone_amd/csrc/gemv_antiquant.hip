@@ -119,7 +119,9 @@ __device__ __forceinline__ h8 dequant8(uint32_t w0, uint32_t w1, h2 off, h2 sc)
 
 // One workgroup = KSPLIT waves over the same NBW 16-column strips, each wave a K/KSPLIT range; partial
 // 16x16 tiles are summed through LDS in a fixed order.  MT = number of 16-row m tiles (ceil(M/16)).
-template <int MT, int NBW, int KSPLIT, bool INT4, bool HAS_OFF>
+// Latency: a wave issues all weight loads (and, when the quant group is a multiple of 128, all scale /
+// offset loads) of a KPW-tile chunk before its first MFMA, and prefetches the activations one k tile ahead.
+template <int MT, int NBW, int KSPLIT, int KPW, bool INT4, bool HAS_OFF, bool G128>
 __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* __restrict__ y,
                                                                      const uint16_t* __restrict__ x,
                                                                      const uint8_t* __restrict__ wp,
@@ -129,12 +131,14 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
 {
     constexpr int TILE_BYTES = INT4 ? 1024 : 2048;
     constexpr int LANE_BYTES = INT4 ? 16 : 32;
+    constexpr int WV = INT4 ? 1 : 2;
     __shared__ v4f red[KSPLIT > 1 ? KSPLIT - 1 : 1][MT][NBW][64];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t KB = K / KT;
-    const int64_t kb_per = KB / KSPLIT;
-    const int64_t kb0 = wave * kb_per, kb1 = (wave == KSPLIT - 1) ? KB : kb0 + kb_per;
+    const int64_t kb_per = (KB + KSPLIT - 1) / KSPLIT;
+    const int64_t kb0 = wave * kb_per;
+    const int64_t kb1 = kb0 + kb_per < KB ? kb0 + kb_per : KB;
     const int64_t nb0 = (int64_t)blockIdx.x * NBW;
     const int64_t NBT = N / 16;
     const int col_in = lane & 15, kq = lane >> 4;
@@ -145,50 +149,78 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
 #pragma unroll
         for (int b = 0; b < NBW; ++b) acc[a][b] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-    for (int64_t kb = kb0; kb < kb1; ++kb) {
-        // weights of this k tile for the NBW strips
-        u32x4 wv[NBW][INT4 ? 1 : 2];
+    auto load_x = [&](int64_t kb, h8 (&xf)[MT][4]) {
 #pragma unroll
-        for (int b = 0; b < NBW; ++b) {
-            const int64_t nb = nb0 + b;
-            if (nb < NBT) {
-                const u32x4* p = (const u32x4*)(wp + (nb * KB + kb) * TILE_BYTES + lane * LANE_BYTES);
-                wv[b][0] = __builtin_nontemporal_load(p);
-                if constexpr (!INT4) wv[b][1] = __builtin_nontemporal_load(p + 1);
-            } else {
-                wv[b][0] = (u32x4){0u, 0u, 0u, 0u};
-                if constexpr (!INT4) wv[b][1] = (u32x4){0u, 0u, 0u, 0u};
-            }
+        for (int a = 0; a < MT; ++a) {
+            const int64_t m = 16 * a + col_in;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                xf[a][j] = (m < M && kb < kb1) ? *(const h8*)(x + m * K + kb * KT + 32 * j + 8 * kq) : (h8){};
         }
+    };
+
+    for (int64_t kc = kb0; kc < kb1; kc += KPW) {
+        u32x4 wv[KPW][NBW][WV];
+        h2 sc[G128 ? KPW : 1][NBW], of[G128 ? KPW : 1][NBW];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t k = kb * KT + 32 * j + 8 * kq;
-            // activations: A fragment rows m = 16 a + col_in, k .. k+7
-            h8 af[MT];
-#pragma unroll
-            for (int a = 0; a < MT; ++a) {
-                const int64_t m = 16 * a + col_in;
-                af[a] = m < M ? *(const h8*)(x + m * K + k) : (h8){};
-            }
-            const int64_t grp = k / g;
+        for (int i = 0; i < KPW; ++i)
 #pragma unroll
             for (int b = 0; b < NBW; ++b) {
-                const int64_t n = (nb0 + b) * 16 + col_in;
-                const bool ok = (nb0 + b) < NBT;
-                const _Float16 s = ok ? bits_h(scale[grp * N + n]) : (_Float16)0.0f;
-                const _Float16 o = (HAS_OFF && ok) ? bits_h(offset[grp * N + n]) : (_Float16)0.0f;
-                uint32_t w0, w1 = 0;
-                if constexpr (INT4) {
-                    w0 = wv[b][0][j];
-                } else {
-                    w0 = wv[b][j >> 1][(j & 1) * 2];
-                    w1 = wv[b][j >> 1][(j & 1) * 2 + 1];
-                }
-                const h8 bf = dequant8<INT4, HAS_OFF>(w0, w1, (h2){o, o}, (h2){s, s});
+                const int64_t kb = kc + i, nb = nb0 + b;
+                const bool ok = kb < kb1 && nb < NBT;
+                const u32x4* p = (const u32x4*)(wp + (nb * KB + kb) * TILE_BYTES + lane * LANE_BYTES);
 #pragma unroll
-                for (int a = 0; a < MT; ++a)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bf, acc[a][b], 0, 0, 0);
+                for (int v = 0; v < WV; ++v) wv[i][b][v] = ok ? __builtin_nontemporal_load(p + v) : (u32x4){0u, 0u, 0u, 0u};
+                if constexpr (G128) {
+                    const int64_t idx = ((kb * KT) / g) * N + nb * 16 + col_in;
+                    const _Float16 s = ok ? bits_h(scale[idx]) : (_Float16)0.0f;
+                    const _Float16 o = (HAS_OFF && ok) ? bits_h(offset[idx]) : (_Float16)0.0f;
+                    sc[i][b] = (h2){s, s};
+                    of[i][b] = (h2){o, o};
+                }
             }
+        h8 xa[MT][4];
+        load_x(kc, xa);
+#pragma unroll
+        for (int i = 0; i < KPW; ++i) {
+            const int64_t kb = kc + i;
+            if (kb >= kb1) break;
+            h8 xn[MT][4];
+            load_x(kb + 1, xn);  // next k tile (zeros past this wave's range)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int b = 0; b < NBW; ++b) {
+                    h2 s2, o2;
+                    if constexpr (G128) {
+                        s2 = sc[i][b];
+                        o2 = of[i][b];
+                    } else {
+                        const int64_t n = (nb0 + b) * 16 + col_in;
+                        const bool ok = (nb0 + b) < NBT;
+                        const int64_t idx = ((kb * KT + 32 * j + 8 * kq) / g) * N + n;
+                        const _Float16 s = ok ? bits_h(scale[idx]) : (_Float16)0.0f;
+                        const _Float16 o = (HAS_OFF && ok) ? bits_h(offset[idx]) : (_Float16)0.0f;
+                        s2 = (h2){s, s};
+                        o2 = (h2){o, o};
+                    }
+                    uint32_t w0, w1 = 0;
+                    if constexpr (INT4) {
+                        w0 = wv[i][b][0][j];
+                    } else {
+                        w0 = wv[i][b][j >> 1][(j & 1) * 2];
+                        w1 = wv[i][b][j >> 1][(j & 1) * 2 + 1];
+                    }
+                    const h8 bf = dequant8<INT4, HAS_OFF>(w0, w1, o2, s2);
+#pragma unroll
+                    for (int a = 0; a < MT; ++a)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[a][j], bf, acc[a][b], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int a = 0; a < MT; ++a)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xa[a][j] = xn[a][j];
         }
     }
 
@@ -223,18 +255,30 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
         }
 }
 
-template <int MT, int NBW, int KSPLIT, bool INT4>
-static void launch_aq(uint16_t* y, const uint16_t* x, const void* wp, const uint16_t* scale, const uint16_t* offset,
-                      int64_t g, int64_t M, int64_t N, int64_t K, hipStream_t st)
+template <int MT, int NBW, int KSPLIT, int KPW, bool INT4, bool HAS_OFF>
+static void launch_aq2(uint16_t* y, const uint16_t* x, const void* wp, const uint16_t* scale, const uint16_t* offset,
+                       int64_t g, int64_t M, int64_t N, int64_t K, hipStream_t st)
 {
-    const int64_t NBT = N / 16;
-    const unsigned blocks = (unsigned)((NBT + NBW - 1) / NBW);
-    if (offset)
-        hipLaunchKernelGGL((antiquant_gemm_kernel<MT, NBW, KSPLIT, INT4, true>), dim3(blocks), dim3(KSPLIT * 64), 0,
-                           st, y, x, (const uint8_t*)wp, scale, offset, M, N, K, g);
+    const unsigned blocks = (unsigned)((N / 16 + NBW - 1) / NBW);
+    if (g % KT == 0)
+        hipLaunchKernelGGL((antiquant_gemm_kernel<MT, NBW, KSPLIT, KPW, INT4, HAS_OFF, true>), dim3(blocks),
+                           dim3(KSPLIT * 64), 0, st, y, x, (const uint8_t*)wp, scale, offset, M, N, K, g);
     else
-        hipLaunchKernelGGL((antiquant_gemm_kernel<MT, NBW, KSPLIT, INT4, false>), dim3(blocks), dim3(KSPLIT * 64),
-                           0, st, y, x, (const uint8_t*)wp, scale, offset, M, N, K, g);
+        hipLaunchKernelGGL((antiquant_gemm_kernel<MT, NBW, KSPLIT, KPW, INT4, HAS_OFF, false>), dim3(blocks),
+                           dim3(KSPLIT * 64), 0, st, y, x, (const uint8_t*)wp, scale, offset, M, N, K, g);
+}
+
+template <int MT, int NBW, int KSPLIT, int KPW>
+static void launch_aq(uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
+                      const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, hipStream_t st)
+{
+    if (int4) {
+        if (offset) launch_aq2<MT, NBW, KSPLIT, KPW, true, true>(y, x, wp, scale, offset, g, M, N, K, st);
+        else launch_aq2<MT, NBW, KSPLIT, KPW, true, false>(y, x, wp, scale, offset, g, M, N, K, st);
+    } else {
+        if (offset) launch_aq2<MT, NBW, KSPLIT, KPW, false, true>(y, x, wp, scale, offset, g, M, N, K, st);
+        else launch_aq2<MT, NBW, KSPLIT, KPW, false, false>(y, x, wp, scale, offset, g, M, N, K, st);
+    }
 }
 
 // M is processed in chunks of 64 rows (4 m tiles); decode shapes are a single launch.
@@ -248,16 +292,9 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
         const int64_t mc = (M - m0) < 64 ? (M - m0) : 64;
         const uint16_t* xc = x + m0 * K;
         uint16_t* yc = y + m0 * N;
-        if (mc <= 16) {
-            if (int4) launch_aq<1, 1, 4, true>(yc, xc, wp, scale, offset, g, mc, N, K, st);
-            else launch_aq<1, 1, 4, false>(yc, xc, wp, scale, offset, g, mc, N, K, st);
-        } else if (mc <= 32) {
-            if (int4) launch_aq<2, 2, 4, true>(yc, xc, wp, scale, offset, g, mc, N, K, st);
-            else launch_aq<2, 2, 4, false>(yc, xc, wp, scale, offset, g, mc, N, K, st);
-        } else {
-            if (int4) launch_aq<4, 2, 4, true>(yc, xc, wp, scale, offset, g, mc, N, K, st);
-            else launch_aq<4, 2, 4, false>(yc, xc, wp, scale, offset, g, mc, N, K, st);
-        }
+        if (mc <= 16) launch_aq<1, 1, 4, 8>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+        else if (mc <= 32) launch_aq<2, 2, 4, 4>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+        else launch_aq<4, 2, 4, 4>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

@@ -145,29 +145,42 @@ __global__ __launch_bounds__(256) void quant_legacy_f16_kernel(const void* __res
 // ---------------------------------------------------------------------------------------------
 // Dequant
 // ---------------------------------------------------------------------------------------------
-// Fast path: int8 [m, n] x fp32 scale[row] -> f16, n % 16 == 0.  16 elements per lane per step.
+// Fast path: int8 [m, n] x fp32 scale[row] -> f16, n % 16 == 0.  Each lane converts U 16-byte chunks per
+// step, all U loads issued before the first conversion.
+template <int U>
 __global__ __launch_bounds__(256) void dequant_i8_token_f16_kernel(const u32x4* __restrict__ q,
                                                                    const float* __restrict__ scale,
                                                                    u32x4* __restrict__ y, int64_t chunks,
                                                                    uint32_t chunks_per_row)
 {
-    for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < chunks; c += (int64_t)gridDim.x * 256) {
-        const float s = scale[c / chunks_per_row];
-        u32x4 v = __builtin_nontemporal_load(q + c);
-        uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-        uint32_t o[8];
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t c0 = (int64_t)blockIdx.x * 256 + threadIdx.x; c0 < chunks; c0 += stride * U) {
+        u32x4 v[U];
+        float s[U];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            int32_t w = (int32_t)w4[e];
-            float f0 = (float)((w << 24) >> 24) * s;
-            float f1 = (float)((w << 16) >> 24) * s;
-            float f2 = (float)((w << 8) >> 24) * s;
-            float f3 = (float)(w >> 24) * s;
-            o[2 * e] = (uint32_t)f32_to_f16_sat(f0) | ((uint32_t)f32_to_f16_sat(f1) << 16);
-            o[2 * e + 1] = (uint32_t)f32_to_f16_sat(f2) | ((uint32_t)f32_to_f16_sat(f3) << 16);
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = c0 + u * stride;
+            v[u] = c < chunks ? __builtin_nontemporal_load(q + c) : (u32x4){0u, 0u, 0u, 0u};
+            s[u] = c < chunks ? scale[c / chunks_per_row] : 0.0f;
         }
-        __builtin_nontemporal_store((u32x4){o[0], o[1], o[2], o[3]}, y + 2 * c);
-        __builtin_nontemporal_store((u32x4){o[4], o[5], o[6], o[7]}, y + 2 * c + 1);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = c0 + u * stride;
+            if (c >= chunks) break;
+            uint32_t o[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int32_t w = (int32_t)v[u][e];
+                const float f0 = (float)((w << 24) >> 24) * s[u];
+                const float f1 = (float)((w << 16) >> 24) * s[u];
+                const float f2 = (float)((w << 8) >> 24) * s[u];
+                const float f3 = (float)(w >> 24) * s[u];
+                o[2 * e] = (uint32_t)f32_to_f16_sat(f0) | ((uint32_t)f32_to_f16_sat(f1) << 16);
+                o[2 * e + 1] = (uint32_t)f32_to_f16_sat(f2) | ((uint32_t)f32_to_f16_sat(f3) << 16);
+            }
+            __builtin_nontemporal_store((u32x4){o[0], o[1], o[2], o[3]}, y + 2 * c);
+            __builtin_nontemporal_store((u32x4){o[4], o[5], o[6], o[7]}, y + 2 * c + 1);
+        }
     }
 }
 
@@ -329,10 +342,11 @@ hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, 
     const bool fast = policy == 2 && src_type == DT_INT8 && dst_type == DT_F16 && scale_type == DT_F32 &&
                       n % 16 == 0 && ((uintptr_t)src % 16 == 0) && ((uintptr_t)y % 16 == 0);
     if (fast) {
-        int64_t chunks = (int64_t)m * n / 16;
-        dim3 grid(grid_for(chunks)), block(256);
-        hipLaunchKernelGGL(dequant_i8_token_f16_kernel, grid, block, 0, st, (const u32x4*)src, (const float*)scale,
-                           (u32x4*)y, chunks, n / 16);
+        const int64_t chunks = (int64_t)m * n / 16;
+        int64_t blocks = (chunks + 512 - 1) / 512;  // 2 chunks per lane: one pass over the tensor
+        if (blocks > (1 << 20)) blocks = 1 << 20;
+        hipLaunchKernelGGL(dequant_i8_token_f16_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, st,
+                           (const u32x4*)src, (const float*)scale, (u32x4*)y, chunks, n / 16);
         return hipGetLastError();
     }
     uint32_t cols = policy == 1 ? cal_count : n;

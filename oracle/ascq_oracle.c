@@ -10,6 +10,12 @@
 #include "ascq_oracle.h"
 
 #include <math.h>
+
+/* Planted-mistake switches for tests/test_oracle_mutants.py, which compiles this file with -DOQ_MUTANT=n and
+ * checks that the pinning tests reject every mutant.  0 (the default) is the oracle itself. */
+#ifndef OQ_MUTANT
+#define OQ_MUTANT 0
+#endif
 #include <stdlib.h>
 #include <string.h>
 
@@ -32,7 +38,7 @@ uint16_t oq_f32_to_f16(float x, int sat)
     if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu)); /* NaN, quieted */
     if (a >= 0x477ff000u) return (uint16_t)(sign | (sat ? 0x7bffu : 0x7c00u));    /* >= 65520 or inf */
     if (a >= 0x38800000u) {                                                       /* normal result */
-        uint32_t r = a + 0xfffu + ((a >> 13) & 1u);
+        uint32_t r = a + 0xfffu + (OQ_MUTANT == 10 ? 1u : ((a >> 13) & 1u));
         return (uint16_t)(sign | ((r - 0x38000000u) >> 13));
     }
     /* subnormal / zero result: |x| * 2^24 is exact; rint under the default (nearest-even) mode */
@@ -98,7 +104,7 @@ uint16_t oq_f64_to_bf16(double d, int sat)
 
 /* QUANT_PRE M1: bits 13..31 hold a (1,8,10) float; the low 13 bits do not take part
  * (accompanying_quantization.md:79-103, table "M1"; gen_data_s322f16.py:38-52 decodes the same field) */
-float oq_quant_pre_m1(uint64_t word) { return u2f((uint32_t)(word & 0xFFFFE000u)); }
+float oq_quant_pre_m1(uint64_t word) { return u2f((uint32_t)(word & (OQ_MUTANT == 1 ? 0xFFFFFFFFu : 0xFFFFE000u))); }
 
 /* host packing used by the reference sample: (uint64)(*(uint32*)&f) (matmul_quant.asc:111-113), plus the
  * 9-bit offset at bits 37..45 and the sign flag at bit 46 (accompanying_quantization.md table 1/2) */
@@ -117,7 +123,7 @@ int32_t oq_round_to_int(float v, int mode)
     case OQ_ROUND_CEIL: r = ceilf(v); break;
     case OQ_ROUND_ROUND: r = roundf(v); break; /* half away from zero */
     case OQ_ROUND_TRUNC: r = truncf(v); break;
-    default: r = rintf(v); break;              /* NONE / RINT: half to even */
+    default: r = OQ_MUTANT == 2 ? roundf(v) : rintf(v); break; /* NONE / RINT: half to even */
     }
     if (r >= 2147483647.0f) return 2147483647;
     if (r <= -2147483648.0f) return (int32_t)0x80000000u;
@@ -130,7 +136,7 @@ int8_t oq_sat_s8(int32_t v) { return (int8_t)(v > 127 ? 127 : (v < -128 ? -128 :
  * {0, .5, 1, 1.5, 2, 3, 4, 6} (precision_conversion.md "fp4x2_e2m1_t -> bfloat16_t": lossless) */
 float oq_e2m1_decode(uint8_t nib)
 {
-    static const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+    static const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, OQ_MUTANT == 9 ? 2.5f : 3.0f, 4.0f, 6.0f};
     float v = mag[nib & 7u];
     return (nib & 8u) ? -v : v;
 }
@@ -233,7 +239,7 @@ void oq_matmul_i8(const int8_t* A, const int8_t* B, const int32_t* bias, int32_t
             }
         }
         for (int64_t n = 0; n < N; ++n) {
-            int64_t v = row[n] + (bias ? bias[n] : 0);
+            int64_t v = row[n] + ((bias && OQ_MUTANT != 4) ? bias[n] : 0);
             C[m * N + n] = (int32_t)(uint32_t)(uint64_t)v;
         }
         free(row);
@@ -323,7 +329,7 @@ void oq_quant_dynamic_per_token(int8_t* dst, float* scale_out, const void* src, 
             float a = fabsf(load_as_f32(src, src_type, i * n + j));
             if (a > amax) amax = a;
         }
-        float mult = amax > 0.0f ? 127.0f / amax : 0.0f;
+        float mult = amax > 0.0f ? (OQ_MUTANT == 8 ? 1.0f / (amax / 127.0f) : 127.0f / amax) : 0.0f;
         scale_out[i] = amax / 127.0f;
         for (int64_t j = 0; j < n; ++j) {
             float v = load_as_f32(src, src_type, i * n + j) * mult;
@@ -350,7 +356,8 @@ void oq_quant_legacy_f16(int8_t* dst, const void* src, int src_type, const uint1
         uint16_t sh = scale_vec ? scale_vec[c] : scale_scalar;
         uint16_t oh = offset_vec ? offset_vec[c] : offset_scalar;
         uint16_t t = oq_f64_to_f16((double)oq_f16_to_f32(xh) * (double)oq_f16_to_f32(sh), 0);
-        uint16_t u = oq_f64_to_f16((double)oq_f16_to_f32(t) + (double)oq_f16_to_f32(oh), 0);
+        uint16_t u = OQ_MUTANT == 11 ? oq_f64_to_f16((double)oq_f16_to_f32(xh) * oq_f16_to_f32(sh) + oq_f16_to_f32(oh), 0)
+                                     : oq_f64_to_f16((double)oq_f16_to_f32(t) + (double)oq_f16_to_f32(oh), 0);
         float tv = oq_f16_to_f32(u);
         dst[i] = oq_sat_s8(oq_round_to_int(tv, OQ_ROUND_RINT));
     }
@@ -378,7 +385,7 @@ void oq_dequant(void* dst, int dst_type, const void* src, int src_type, const vo
         int64_t cols = policy == OQ_PER_CHANNEL ? cal_count : n;
         for (int64_t j = 0; j < cols; ++j) {
             float s;
-            if (policy == OQ_PER_CHANNEL) s = load_as_f32(scale, scale_type, j);
+            if (policy == OQ_PER_CHANNEL) s = load_as_f32(scale, scale_type, OQ_MUTANT == 12 ? i % cal_count : j);
             else if (policy == OQ_PER_TOKEN) s = load_as_f32(scale, scale_type, i);
             else s = scale_scalar;
             float v = load_as_f32(src, src_type, i * n + j) * s;
@@ -397,7 +404,7 @@ static inline int32_t load_q(const void* src, int src_type, int64_t idx)
     /* int4b_t packed two per byte, the even element in the low nibble
      * (examples/01_simd_cpp_api/04_advanced_api/00_matmul/matmul_int4/scripts/gen_data.py packing) */
     uint8_t byte = ((const uint8_t*)src)[idx >> 1];
-    int32_t nib = (idx & 1) ? (byte >> 4) : (byte & 0xf);
+    int32_t nib = ((idx & 1) ^ (OQ_MUTANT == 3)) ? (byte >> 4) : (byte & 0xf);
     return nib >= 8 ? nib - 16 : nib;
 }
 
@@ -426,8 +433,13 @@ void oq_antiquant(void* dst, int dst_type, const void* src, int src_type, const 
             if (arith == OQ_ARITH_F16 && dst_type == OQ_F16) {
                 /* half(q) is exact; q + offset and the product are exact in double, rounded once each */
                 uint16_t w = oq_f32_to_f16((float)q, 0);
-                if (offset) w = oq_f64_to_f16((double)q + (double)of, 0);
-                w = oq_f64_to_f16((double)oq_f16_to_f32(w) * (double)sc, 0);
+                if (OQ_MUTANT == 7) {
+                    w = oq_f64_to_f16((double)q * (double)sc, 0);
+                    if (offset) w = oq_f64_to_f16((double)oq_f16_to_f32(w) + (double)of, 0);
+                } else {
+                    if (offset) w = oq_f64_to_f16((double)q + (double)of, 0);
+                    w = oq_f64_to_f16((double)oq_f16_to_f32(w) * (double)sc, 0);
+                }
                 ((uint16_t*)dst)[idx] = w;
             } else {
                 float v = (float)q;
@@ -501,8 +513,8 @@ void oq_group_matmul(void* y, int out_type, const int8_t* x, const float* pts, c
                 int64_t acc = 0;
                 for (int64_t k = 0; k < K; ++k)
                     acc += (int64_t)x[m * K + k] * (int64_t)(w_trans ? wg[n * K + k] : wg[k * N + n]);
-                float v = (float)(int32_t)(uint32_t)(uint64_t)acc * scale[g * N + n];
-                v = v * pts[m];
+                float v = (float)(int32_t)(uint32_t)(uint64_t)acc * (OQ_MUTANT == 5 ? pts[m] : scale[g * N + n]);
+                v = v * (OQ_MUTANT == 5 ? scale[g * N + n] : pts[m]);
                 store_from_f32(y, out_type, m * N + n, v);
             }
         }
@@ -550,7 +562,8 @@ void oq_mx_matmul(uint16_t* C, double* C_exact, double* C_absdot, const uint8_t*
             double s = 0.0, sa_ = 0.0;
             for (int64_t k = 0; k < K; ++k) {
                 int64_t kb = k / 32;
-                uint8_t sb = scale_b_layout == 0 ? scaleB[(kb / 2) * N * 2 + n * 2 + (kb & 1)] : scaleB[n * sK + kb];
+                uint8_t sb = (scale_b_layout == 0 && OQ_MUTANT != 6) ? scaleB[(kb / 2) * N * 2 + n * 2 + (kb & 1)]
+                                                                     : scaleB[n * sK + kb];
                 double b = (double)mx_elem(B, transB ? n * K + k : k * N + n, elem_fmt) * (double)oq_e8m0_decode(sb);
                 double p = arow[k] * b;
                 s += p;

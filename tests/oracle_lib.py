@@ -6,6 +6,7 @@ checker; the product path never calls it.  Arrays are numpy; f16 / bf16 travel a
 from __future__ import annotations
 
 import ctypes
+import os
 import subprocess
 from pathlib import Path
 
@@ -13,7 +14,7 @@ import numpy as np
 
 ROOT = Path(__file__).resolve().parent.parent
 ORACLE_DIR = ROOT / "oracle"
-ORACLE_SO = ORACLE_DIR / "liboracle.so"
+ORACLE_SO = Path(os.environ.get("ASCQ_ORACLE_SO", ORACLE_DIR / "liboracle.so"))
 
 INT8, UINT8, INT4, INT32, F16, BF16, F32, U64, FP8_E4M3, FP8_E5M2, FP4_E2M1, E8M0, INT64 = range(1, 14)
 ROUND_NONE, ROUND_RINT, ROUND_FLOOR, ROUND_CEIL, ROUND_ROUND, ROUND_TRUNC = range(6)

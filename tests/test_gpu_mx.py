@@ -73,7 +73,7 @@ def check(got_f64, exact, absd, K, golden_bits=None, rel=1e-3):
         g = bf16_to_f64(golden_bits)
         r = np.linalg.norm(got_f64 - g) / max(np.linalg.norm(g), 1e-30)
         assert r <= rel, f"normwise rel err vs bf16(fp64) golden {r}"
-        assert (got_f64 == g).mean() > 0.99
+        assert (got_f64 == g).mean() > 0.95
 
 
 @pytest.mark.parametrize("trans_b", [True, False])

@@ -282,6 +282,24 @@ def test_dynamic_quant_invariants_and_numpy():
     assert (np.abs(q[rows, np.abs(xf).argmax(1)]) == 127).all()
 
 
+def test_dynamic_quant_exhaustive_half_rows():
+    """Each row holds every non-negative binary16 value up to its absmax, so all rounding boundaries of
+    x * (127 / absmax) are visited; the multiplier is one fp32 division (not 1 / (absmax / 127))."""
+    codes = np.arange(0, 0x7C00, dtype=np.uint16)
+    allh = codes.view(np.float16).astype(np.float32)
+    amaxes = [0.50048828125, 0.83203125, 1.1376953125, 1.5166015625, 1.990234375, 2.169921875, 13.140625]
+    n = int((allh <= max(amaxes)).sum())
+    x = np.zeros((len(amaxes), n), np.float16)
+    for i, a in enumerate(amaxes):
+        v = allh[allh <= a].astype(np.float16)
+        x[i, :v.size] = v
+        x[i, v.size:] = -v[: n - v.size] if v.size else 0
+    q, s = O.quant_dynamic_per_token(x.view(np.uint16), O.F16)
+    xf = x.astype(np.float32)
+    mult = (np.float32(127.0) / np.abs(xf).max(1)).astype(np.float32)
+    assert (q == np.clip(np.rint(xf * mult[:, None]), -128, 127).astype(np.int8)).all()
+
+
 def _half_round_exact(fr: Fraction) -> np.float16:
     """round an exact rational to binary16 (nearest, ties to even) by brute force over neighbouring codes"""
     f = float(fr)
@@ -349,6 +367,27 @@ def test_group_matmul_vs_numpy_exact():
         exp = torch.from_numpy(v.astype(np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
         assert (y[s:e] == exp).all()
     assert (y[16:] == 0).all()
+
+
+def test_group_matmul_f32_epilogue_order():
+    """fp32 output exposes the epilogue's rounding order: (acc * scale[g, n]) first, then * pts[m]
+    (quant_group_matmul_custom.asc's dequant of the int32 tile, then the per-token multiply)."""
+    G, K, N, M = 2, 64, 48, 24
+    counts = np.array([10, 14], np.int64)
+    x = rng0.integers(-127, 128, (M, K), dtype=np.int8)
+    w = rng0.integers(-127, 128, (G, K, N), dtype=np.int8)
+    pts = rng0.uniform(1e-3, 1e-1, M).astype(np.float32)
+    sc = rng0.uniform(1e-4, 1e-2, (G, N)).astype(np.float32)
+    y = O.group_matmul(x, pts, w, sc, counts, 1, G, M, K, N, O.F32, y=np.zeros((M, N), np.float32))
+    off = np.concatenate([[0], np.cumsum(counts)])
+    for g in range(G):
+        s, e = off[g], off[g + 1]
+        acc = (x[s:e].astype(np.int64) @ w[g].astype(np.int64)).astype(np.float32)
+        first = (acc * sc[g][None, :]).astype(np.float32)
+        exp = (first * pts[s:e, None]).astype(np.float32)
+        assert np.array_equal(y[s:e], exp)
+        other = ((acc * pts[s:e, None]).astype(np.float32) * sc[g][None, :]).astype(np.float32)
+        assert not np.array_equal(other, exp)  # the two orders differ on these inputs
 
 
 def test_mx_matmul_vs_numpy_decode():

@@ -1,0 +1,67 @@
+"""The oracle's pins must catch plausible mistakes.
+
+oracle/ascq_oracle.c carries planted-mistake switches (OQ_MUTANT = n): a dropped 13-bit truncation of the
+QUANT_PRE multiplier, half-away instead of half-even rounding, a swapped int4 nibble order, a dropped bias, a
+reordered group-matmul epilogue, a transposed MX scale index, offset/scale applied in the wrong order, a
+double-rounded multiplier, a wrong E2M1 code, a ties-away f16 cast, an unrounded half add, and a per-channel
+dequant indexed by row.  Each mutant is compiled on the CPU into a temporary library and the pinning tests of
+tests/test_oracle.py are run against it; every mutant must fail at least one of them.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+SRC = ROOT / "oracle" / "ascq_oracle.c"
+
+MUTANTS = {
+    1: "QUANT_PRE M1 not truncated to (1,8,10) bits",
+    2: "rint replaced by round-half-away",
+    3: "int4 nibble order swapped",
+    4: "int32 bias dropped",
+    5: "group epilogue multiplies the per-token scale first",
+    6: "MX [sK/2, N, 2] scale layout read as [N, sK]",
+    7: "antiquant multiplies before adding the offset",
+    8: "dynamic quant multiplier 1/(absmax/127) (double rounding)",
+    9: "E2M1 code 5 decoded as 2.5",
+    10: "f32->f16 ties rounded away from zero",
+    11: "legacy quant: product not rounded to half before the offset add",
+    12: "per-channel dequant indexed by row",
+}
+
+
+@pytest.fixture(scope="module")
+def mutant_dir(tmp_path_factory):
+    return tmp_path_factory.mktemp("oracle_mutants")
+
+
+def _build(n: int, d: Path) -> Path:
+    so = d / f"liboracle_m{n}.so"
+    cmd = ["gcc", "-O2", "-march=x86-64-v3", "-fopenmp", "-fPIC", "-ffp-contract=off", "-std=c11", "-shared",
+           f"-DOQ_MUTANT={n}", "-o", str(so), str(SRC), "-lm"]
+    subprocess.run(cmd, check=True, capture_output=True)
+    return so
+
+
+@pytest.mark.parametrize("n", sorted(MUTANTS))
+def test_pins_reject_mutant(n, mutant_dir):
+    so = _build(n, mutant_dir)
+    env = dict(os.environ, ASCQ_ORACLE_SO=str(so), OMP_NUM_THREADS="4")
+    r = subprocess.run([sys.executable, "-m", "pytest", "-q", "-x", "-p", "no:cacheprovider", "-W", "ignore",
+                        str(ROOT / "tests" / "test_oracle.py")], cwd=ROOT, env=env, capture_output=True, text=True,
+                       timeout=600)
+    assert r.returncode != 0, f"mutant {n} ({MUTANTS[n]}) passed every pin:\n{r.stdout[-2000:]}"
+
+
+def test_unmutated_oracle_passes(mutant_dir):
+    so = _build(0, mutant_dir)
+    env = dict(os.environ, ASCQ_ORACLE_SO=str(so), OMP_NUM_THREADS="4")
+    r = subprocess.run([sys.executable, "-m", "pytest", "-q", "-p", "no:cacheprovider", "-W", "ignore",
+                        str(ROOT / "tests" / "test_oracle.py")], cwd=ROOT, env=env, capture_output=True, text=True,
+                       timeout=600)
+    assert r.returncode == 0, r.stdout[-3000:]
