@@ -78,6 +78,8 @@ Kind kind_of(const ascq_matmul_types& t)
     return K_NONE;
 }
 
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
 size_t workspace_need(const ascq_matmul_s* h)
 {
     switch (kind_of(h->ty)) {
@@ -87,7 +89,13 @@ size_t workspace_need(const ascq_matmul_s* h)
         if (h->aq_set && !h->aq_vec) need += 2 * ((size_t)h->N * 2 + 256);
         return need;
     }
-    case K_MX: return h->trans_b ? 0 : (size_t)h->N * (size_t)(h->K / 2);
+    case K_MX: {
+        // [K, N] B transposed to [N, K]; both scale tensors rearranged stage-major; 256-byte aligned parts
+        const size_t sk = (size_t)((h->K + 63) / 64 * 2);
+        size_t need = h->trans_b ? 0 : align256((size_t)h->N * (size_t)(h->K / 2));
+        need += align256((size_t)h->M * sk + 16) + align256((size_t)h->N * sk + 16);  // + copy slack
+        return need;
+    }
     default: return 0;
     }
 }
@@ -391,21 +399,35 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         ascq_status s = ensure_workspace(h);
         if (s != ASCQ_OK) return s;
         const uint8_t* bt = (const uint8_t*)h->b;
+        const uint8_t* sa = h->scale_a;
+        const uint8_t* sb = h->scale_b;
+        const int64_t sk = (h->K + 63) / 64 * 2;
+        uint8_t* ws = (uint8_t*)h->ws;
         if (!h->trans_b) {
-            hipError_t e = ascq::launch_fp4_transpose((uint8_t*)h->ws, (const uint8_t*)h->b, h->K, h->N, st);
+            hipError_t e = ascq::launch_fp4_transpose(ws, (const uint8_t*)h->b, h->K, h->N, st);
             if (e != hipSuccess) return hip_status(e, "fp4_transpose");
-            bt = (const uint8_t*)h->ws;
+            bt = ws;
+            ws += align256((size_t)h->N * (size_t)(h->K / 2));
+        }
+        {  // scaleA [M, sK] (or [sK/2, M, 2] with isTransposeScaleA) -> stage-major
+            hipError_t e = ascq::launch_mx_scale_stage_major(ws, h->scale_a, h->M, sk, h->trans_sa ? 1 : 0, st);
+            if (e != hipSuccess) return hip_status(e, "mx_scale_stage_major(A)");
+            sa = ws;
+            ws += align256((size_t)h->M * (size_t)sk + 16);
+        }
+        {  // scaleB [sK/2, N, 2] (or [N, sK] with isTransposeScaleB) -> stage-major
+            hipError_t e = ascq::launch_mx_scale_stage_major(ws, h->scale_b, h->N, sk, h->trans_sb ? 0 : 1, st);
+            if (e != hipSuccess) return hip_status(e, "mx_scale_stage_major(B)");
+            sb = ws;
         }
         ascq::MxGemmArgs g{};
         g.A = (const uint8_t*)h->a;
         g.B = bt;
-        g.sA = h->scale_a;
-        g.sB = h->scale_b;
+        g.sA = sa;
+        g.sB = sb;
         g.M = h->M;
         g.N = h->N;
         g.K = h->K;
-        g.sa_layout = h->trans_sa;
-        g.sb_layout = h->trans_sb;
         g.C = c;
         g.c_type = h->ty.c_type;  // ascq_dtype codes equal the device DT_* codes
         return hip_status(ascq::launch_mx_gemm(g, st), "mx_gemm");

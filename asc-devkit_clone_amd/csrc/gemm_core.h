@@ -4,21 +4,33 @@
 // MFMA: the 32x32 forms, v_mfma_i32_32x32x32_i8 and v_mfma_scale_f32_32x32x64_f8f6f4 -- on gfx950 they issue at
 // the full int8 / fp4 rate, the 16x16 forms at about half of it (measured: 4.80 vs 2.71 int8 POPS, 9.34 vs
 // 4.80 fp4 POPS on one MI355X).  Both consume 32 K bytes per row per instruction, 16 bytes per lane: lane l
-// holds row l % 32 at K bytes 16 (l / 32) .. +15 of the step.  One stage holds ROWB = 64*KSTEPS bytes of K for
-// every tile row of A and B (int8: 64*KSTEPS elements, fp4: 128*KSTEPS), i.e. 2*KSTEPS MFMA k-steps.
-// Layout and schedule:
-//  * LDS rows are unpadded, ROWB bytes, and 16-byte chunks are XOR-swizzled: logical chunk c of row r lives at
-//    chunk c ^ ((r / (256/ROWB)) % CH).  The 16 lanes an MFMA operand read serves together then hit 16
-//    distinct 4-bank groups, and a wave's staging write is 1 KiB contiguous.
+// holds row l % 32 at K bytes 16 (l / 32) .. +15 of the step.  One stage holds ROWB = 64 bytes of K for every
+// tile row of A and B (int8: 64 elements, fp4: 128), i.e. two MFMA k-steps.
+//
+// Pipeline: a ring of STAGES LDS stages.  K-contiguous operands are copied global -> LDS by buffer loads with
+// the LDS destination (buffer_load_dwordx4 ... lds): no registers are involved, so STAGES - 1 stages are in
+// flight while one is multiplied.  Per iteration each wave waits (s_waitcnt vmcnt) for its own copies of the
+// current stage, one barrier publishes them to all waves and frees the stage multiplied last iteration, and
+// the copies of the stage STAGES - 1 ahead are issued into that freed slot before the MFMAs start.  Every wave
+// issues the same number of copies every iteration (out-of-range copies read zeros), so the vmcnt threshold is
+// a compile-time constant.
+//
+// Layout:
+//  * LDS rows are unpadded, 64 bytes, and 16-byte chunks are XOR-swizzled: logical chunk c of row r lives at
+//    chunk c ^ ((r / 4) % 4).  The 16 lanes an MFMA operand read serves together then hit 16 distinct 4-bank
+//    groups.  A copy instruction writes 1 KiB contiguous (lane l -> row l / 4, chunk l % 4); the swizzle is
+//    applied on the global side (lane l fetches logical chunk (l % 4) ^ ((row / 4) % 4)).
 //  * Global reads are raw buffer loads: an out-of-range offset returns zeros, so tile edges and the K tail
-//    need no branches and the whole loop body stays in one basic block for the scheduler.
-//  * Two LDS stages; the loads of stage k+1 are issued before the MFMAs of stage k, a scheduling barrier keeps
-//    those MFMAs ahead of the LDS store (whose wait on the loads would otherwise stall them), one barrier per
-//    stage.
-//  * B given row-major [K, N] (int8 only) is transposed on its way into LDS: each lane loads an 8(k) x 4(n)
-//    byte block as 8 dwords and v_perm_b32 turns it into 4 K-contiguous 8-byte pieces.
-//  * MX: the E8M0 scales of each tile row for the stage's 4*KSTEPS K blocks ride in the same stage
-//    (4*KSTEPS bytes per row); a lane reads the byte of its (row, block) -- k-step s, block 2s + l / 32.
+//    need no branches.
+//  * B given row-major [K, N] (int8 only) goes through registers instead: each lane loads an 8(k) x 4(n) byte
+//    block as 8 dwords, v_perm_b32 turns it into 4 K-contiguous 8-byte pieces, and they are written one
+//    iteration after they were loaded (two iterations of latency cover; the registers are double-buffered).
+//    The row written by store j of a lane is rotated by (n-block / 4) so the 64 lanes of a store spread over
+//    the LDS banks.
+//  * MX: the E8M0 scales arrive stage-major ([sK/4][rows][4]: for each stage, the 4-byte words of all rows),
+//    so a stage's scales for 256 tile rows are one contiguous 1 KiB copy into the stage.  (Row-major scales
+//    would cost one cache line per row per stage.)  A lane reads the scale word of its fragment row once per
+//    stage, shifts it by 8 * (l / 32), and the MFMA's op_sel takes byte 2s for k-step s: block 2s + l / 32.
 //  * Accumulator layout of one 32x32 tile: lane l, register r holds row 8(r/4) + 4(l/32) + r%4, column l%32.
 #pragma once
 
@@ -39,6 +51,34 @@ __device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) { return __buil
 __device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
 __device__ __forceinline__ u32x2 bload8(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0); }
 __device__ __forceinline__ uint32_t bload2(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16 bytes per lane, global (buffer) -> LDS at lds_wave_base + 16 * lane; lds_wave_base must be wave-uniform.
+__device__ __forceinline__ void copy16_to_lds(rsrc_t r, uint8_t* lds_wave_base, uint32_t off)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_wave_base, 16, off, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding: vmcnt[3:0] | expcnt << 4 |
+// lgkmcnt << 8 | vmcnt[5:4] << 14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// workgroup barrier that the compiler may not move memory accesses across (no hardware fence: the waits are
+// explicit)
+__device__ __forceinline__ void stage_barrier()
+{
+    __builtin_amdgcn_sched_barrier(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_sched_barrier(0);
+}
 
 __device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
 
@@ -78,75 +118,72 @@ struct CoreArgs {
     uint32_t lda, ldb;    // leading dimensions in bytes
     int32_t rows, cols;   // valid rows of A / columns of B in this tile (from the tile origin)
     uint32_t a0, b0;      // byte offsets of the tile origin in the A / B buffers
-    int64_t kbytes;       // K extent in bytes (int8: K; fp4: K/2)
-    // MX scales
+    int64_t kbytes;       // K extent in bytes (int8: K; fp4: K/2); a multiple of 16
+    // MX scales, stage-major: word (stage s, row r) = blocks 4s .. 4s + 3 of row r, at byte (s * rows + r) * 4
     rsrc_t sa, sb;
     uint32_t sa0_row, sb0_row;  // first row / column index of the tile
-    uint32_t sa_rows, sb_rows;  // M / N (for the pair layouts)
-    uint32_t sk;                // scale blocks per row (sK)
-    int sa_pairs, sb_pairs;     // 1: [sK/2][R][2] layout; 0: [R][sK]
+    uint32_t sa_rows, sb_rows;  // M / N: the stage stride in words
+    uint32_t sk;                // scale blocks per row (sK, a multiple of 4)
 };
 
-template <int BM, int BN, int WM, int WN, int KSTEPS, bool B_KCONTIG, int OP>
+template <int BM, int BN, int WM, int WN, int STAGES, bool B_KCONTIG, int OP>
 struct GemmCore {
-    static constexpr int NT = WM * WN * 64;
+    static constexpr int NW = WM * WN;
+    static constexpr int NT = NW * 64;
     static constexpr int WTM = BM / WM, WTN = BN / WN;
     static constexpr int FM = WTM / 32, FN = WTN / 32;
-    static constexpr int ROWB = 64 * KSTEPS;
-    static constexpr int CH = ROWB / 16;
-    static constexpr int RPW = 256 / ROWB;  // rows per 64-bank wrap
-    static constexpr int A_LD = BM * CH / NT;
-    static constexpr int B_LD = B_KCONTIG ? BN * CH / NT : 1;
-    static constexpr int B_BLK = B_KCONTIG ? 1 : (ROWB / 8) * (BN / 4) / NT;
-    static constexpr int SCB = OP == OP_MXFP4 ? 4 * KSTEPS : 0;  // scale bytes per row per stage
-    static constexpr int SC_LD = OP == OP_MXFP4 ? (BM + BN + NT - 1) / NT : 1;
-    static constexpr int STAGE = (BM + BN) * ROWB + (BM + BN) * SCB;
-    static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE;
+    static constexpr int ROWB = 64;                   // K bytes per row per stage
+    static constexpr int CH = ROWB / 16;              // 16-byte chunks per row
+    static constexpr int ROWS_PER_COPY = 64 / CH;     // rows one wave-wide 1 KiB copy covers
+    static constexpr int A_COPIES = BM / ROWS_PER_COPY / NW;              // per wave per stage
+    static constexpr int B_COPIES = B_KCONTIG ? BN / ROWS_PER_COPY / NW : 0;
+    static constexpr int SCB = 4;                     // MX scale bytes per row per stage (4 blocks of 32)
+    // MX scales, stage-major in memory ([sK/4][rows][4]): the words of 256 consecutive rows for one stage are
+    // 1 KiB contiguous, one wave-wide 16-byte copy.  SA_REG / SB_REG: the A / B word regions of a stage.
+    // Every wave issues SC_COPIES copies; those past the real ones read out of range into a dummy area, so
+    // the per-wave copy count (and with it the vmcnt threshold) is the same for all waves.
+    static constexpr int SA_INSTR = OP == OP_MXFP4 ? (BM + 255) / 256 : 0;
+    static constexpr int SB_INSTR = OP == OP_MXFP4 ? (BN + 255) / 256 : 0;
+    static constexpr int SA_REG = SA_INSTR * 1024, SB_REG = SB_INSTR * 1024;
+    static constexpr int SC_COPIES = (SA_INSTR + SB_INSTR + NW - 1) / NW;
+    static constexpr int SC_BYTES = SA_REG + SB_REG;
+    static constexpr int DUMMY_BYTES = OP == OP_MXFP4 && SC_COPIES * NW > SA_INSTR + SB_INSTR ? 1024 : 0;
+    static constexpr int COPIES = A_COPIES + B_COPIES + SC_COPIES;
+    static constexpr int B_BLK = B_KCONTIG ? 0 : (ROWB / 8) * (BN / 4) / NT;  // 8x4-byte blocks per lane
+    static constexpr int B_LOADS = 8 * B_BLK;         // dword loads per lane per stage for a [K, N] B
+    static constexpr int STAGE = (BM + BN) * ROWB + SC_BYTES;
+    static constexpr size_t LDS_BYTES = (size_t)STAGES * STAGE + DUMMY_BYTES;
+    // vmem operations of this wave issued after stage kt's copies, at the top of iteration kt
+    static constexpr int IN_FLIGHT = (STAGES - 2) * (COPIES + B_LOADS);
     typedef typename std::conditional<OP == OP_I8, v16i, v16f>::type acc_t;
     static_assert(FM >= 1 && FN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
+    static_assert(BM % (ROWS_PER_COPY * NW) == 0 && A_COPIES >= 1, "A copies must split evenly over the waves");
+    static_assert(!B_KCONTIG || (BN % (ROWS_PER_COPY * NW) == 0 && B_COPIES >= 1), "B copies");
+    static_assert(B_KCONTIG || (((ROWB / 8) * (BN / 4)) % NT == 0 && B_BLK >= 1), "B blocks");
+    static_assert(OP == OP_I8 || B_KCONTIG, "fp4 B must be K-contiguous");
+    static_assert(OP == OP_I8 || (BM % 64 == 0 && BN % 64 == 0), "scale row groups");
+    static_assert(STAGES >= 3 && IN_FLIGHT < 64, "stages");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 
-    // position of accumulator register r of tile (i, j) inside the block tile
     __device__ __forceinline__ static int frag_row(int wm, int i, int r, int lane)
     {
         return wm * WTM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
     }
     __device__ __forceinline__ static int frag_col(int wn, int j, int lane) { return wn * WTN + j * 32 + (lane & 31); }
-    static_assert((BM * CH) % NT == 0 && A_LD >= 1, "A staging");
-    static_assert(B_KCONTIG ? ((BN * CH) % NT == 0 && B_LD >= 1) : (((ROWB / 8) * (BN / 4)) % NT == 0 && B_BLK >= 1),
-                  "B staging");
-    static_assert(OP == OP_I8 || B_KCONTIG, "fp4 B must be K-contiguous");
-
-    __device__ __forceinline__ static int swz(int row, int c) { return c ^ ((row / RPW) % CH); }
+    __device__ __forceinline__ static int swz(int row, int c) { return c ^ ((row >> 2) & 3); }
 
     __device__ __forceinline__ static void run(const CoreArgs& p, uint8_t* smem, acc_t (&acc)[FM][FN])
     {
-        const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+        const int t = threadIdx.x, lane = t & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: copy bases stay scalar
         const int wm = wave / WN, wn = wave % WN;
+        typedef uint32_t breg_t[B_BLK > 0 ? B_BLK : 1][8];
+        breg_t rb0, rb1;  // two register sets, alternated by the 2x-unrolled main loop (no copies between them)
 
-        u32x4 ra[A_LD];
-        u32x4 rb[B_LD];
-        uint32_t rbt[B_BLK][8];
-        u32x2 rs[SC_LD];
-
-        auto load_global = [&](int64_t kt) {
-            const int64_t kb0 = kt * ROWB;
-#pragma unroll
-            for (int i = 0; i < A_LD; ++i) {
-                const int id = t + i * NT, row = id / CH, c = id % CH;
-                const int64_t k = kb0 + c * 16;
-                const uint32_t off = (row < p.rows && k < p.kbytes) ? p.a0 + (uint32_t)row * p.lda + (uint32_t)k : OOB;
-                ra[i] = bload16(p.a, off);
-            }
-            if constexpr (B_KCONTIG) {
-#pragma unroll
-                for (int i = 0; i < B_LD; ++i) {
-                    const int id = t + i * NT, row = id / CH, c = id % CH;
-                    const int64_t k = kb0 + c * 16;
-                    const uint32_t off =
-                        (row < p.cols && k < p.kbytes) ? p.b0 + (uint32_t)row * p.ldb + (uint32_t)k : OOB;
-                    rb[i] = bload16(p.b, off);
-                }
-            } else {
+        // [K, N] B: the 8x4-byte blocks of stage kt into rbt
+        auto load_b_regs = [&](breg_t& rbt, int64_t kt) {
+            if constexpr (!B_KCONTIG) {
+                const int64_t kb0 = kt * ROWB;
 #pragma unroll
                 for (int i = 0; i < B_BLK; ++i) {
                     const int id = t + i * NT, nb = id % (BN / 4), kb = id / (BN / 4);
@@ -159,71 +196,66 @@ struct GemmCore {
                     }
                 }
             }
-            if constexpr (OP == OP_MXFP4) {
-                const uint32_t blk0 = (uint32_t)(kt * 4 * KSTEPS);
-#pragma unroll
-                for (int i = 0; i < SC_LD; ++i) {
-                    const int r = t + i * NT;
-                    u32x2 v = (u32x2){0x7f7f7f7fu, 0x7f7f7f7fu};
-                    const bool is_a = r < BM;
-                    const bool valid = is_a ? (r < p.rows) : (r < BM + BN && (r - BM) < p.cols);
-                    const rsrc_t sr = is_a ? p.sa : p.sb;
-                    const int pairs = is_a ? p.sa_pairs : p.sb_pairs;
-                    const uint32_t idx = is_a ? p.sa0_row + r : p.sb0_row + (r - BM);
-                    const uint32_t R = is_a ? p.sa_rows : p.sb_rows;
-                    if (valid && blk0 < p.sk) {
-                        if (!pairs) {
-                            if constexpr (KSTEPS == 2) v = bload8(sr, idx * p.sk + blk0);
-                            else v.x = bload4(sr, idx * p.sk + blk0);
-                        } else {
-                            uint32_t w[2 * KSTEPS];
-#pragma unroll
-                            for (int q = 0; q < 2 * KSTEPS; ++q) w[q] = bload2(sr, ((blk0 >> 1) + q) * R * 2 + idx * 2);
-                            v.x = (w[0] & 0xffffu) | (w[1] << 16);
-                            if constexpr (KSTEPS == 2) v.y = (w[2] & 0xffffu) | (w[3] << 16);
-                        }
-                    }
-                    rs[i] = v;
-                }
-            }
         };
-
-        auto store_lds = [&](int buf) {
-            uint8_t* sA = smem + buf * STAGE;
-            uint8_t* sB = sA + BM * ROWB;
-#pragma unroll
-            for (int i = 0; i < A_LD; ++i) {
-                const int id = t + i * NT, row = id / CH, c = id % CH;
-                *(u32x4*)(sA + row * ROWB + swz(row, c) * 16) = ra[i];
-            }
-            if constexpr (B_KCONTIG) {
-#pragma unroll
-                for (int i = 0; i < B_LD; ++i) {
-                    const int id = t + i * NT, row = id / CH, c = id % CH;
-                    *(u32x4*)(sB + row * ROWB + swz(row, c) * 16) = rb[i];
-                }
-            } else {
+        // transpose the blocks held in rb and write them K-contiguous into the B part of a slot
+        auto store_b_regs = [&](breg_t& rb, int slot) {
+            if constexpr (!B_KCONTIG) {
+                uint8_t* sB = smem + slot * STAGE + BM * ROWB;
 #pragma unroll
                 for (int i = 0; i < B_BLK; ++i) {
                     const int id = t + i * NT, nb = id % (BN / 4), kb = id / (BN / 4);
                     uint32_t lo[4], hi[4];
-                    transpose4x4(rbt[i][0], rbt[i][1], rbt[i][2], rbt[i][3], lo[0], lo[1], lo[2], lo[3]);
-                    transpose4x4(rbt[i][4], rbt[i][5], rbt[i][6], rbt[i][7], hi[0], hi[1], hi[2], hi[3]);
+                    transpose4x4(rb[i][0], rb[i][1], rb[i][2], rb[i][3], lo[0], lo[1], lo[2], lo[3]);
+                    transpose4x4(rb[i][4], rb[i][5], rb[i][6], rb[i][7], hi[0], hi[1], hi[2], hi[3]);
+                    const int rot = (nb >> 2) & 3;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const int n = nb * 4 + j;
-                        *(u32x2*)(sB + n * ROWB + swz(n, kb >> 1) * 16 + (kb & 1) * 8) = (u32x2){lo[j], hi[j]};
+                        const int jj = (j + rot) & 3;
+                        const uint32_t l = jj == 0 ? lo[0] : jj == 1 ? lo[1] : jj == 2 ? lo[2] : lo[3];
+                        const uint32_t h = jj == 0 ? hi[0] : jj == 1 ? hi[1] : jj == 2 ? hi[2] : hi[3];
+                        const int n = nb * 4 + jj;
+                        *(u32x2*)(sB + n * ROWB + swz(n, kb >> 1) * 16 + (kb & 1) * 8) = (u32x2){l, h};
                     }
                 }
             }
+        };
+
+        auto issue_copies = [&](int64_t kt, int slot) {
+            uint8_t* sA = smem + slot * STAGE;
+            uint8_t* sB = sA + BM * ROWB;
+            const int64_t kb0 = kt * ROWB;
+            const int rin = lane / CH, phys = lane % CH;
+#pragma unroll
+            for (int j = 0; j < A_COPIES; ++j) {
+                const int row0 = (wave * A_COPIES + j) * ROWS_PER_COPY;
+                const int row = row0 + rin;
+                const int64_t k = kb0 + swz(row, phys) * 16;
+                const uint32_t off = (row < p.rows && k < p.kbytes) ? p.a0 + (uint32_t)row * p.lda + (uint32_t)k : OOB;
+                copy16_to_lds(p.a, sA + row0 * ROWB, off);
+            }
+#pragma unroll
+            for (int j = 0; j < B_COPIES; ++j) {
+                const int row0 = (wave * B_COPIES + j) * ROWS_PER_COPY;
+                const int row = row0 + rin;
+                const int64_t k = kb0 + swz(row, phys) * 16;
+                const uint32_t off = (row < p.cols && k < p.kbytes) ? p.b0 + (uint32_t)row * p.ldb + (uint32_t)k : OOB;
+                copy16_to_lds(p.b, sB + row0 * ROWB, off);
+            }
             if constexpr (OP == OP_MXFP4) {
                 uint8_t* sS = sA + (BM + BN) * ROWB;
+                const bool kval = (uint32_t)(kt * 4) < p.sk;
 #pragma unroll
-                for (int i = 0; i < SC_LD; ++i) {
-                    const int r = t + i * NT;
-                    if (r < BM + BN) {
-                        if constexpr (KSTEPS == 2) *(u32x2*)(sS + r * SCB) = rs[i];
-                        else *(uint32_t*)(sS + r * SCB) = rs[i].x;
+                for (int j = 0; j < SC_COPIES; ++j) {
+                    const int g = wave * SC_COPIES + j;  // wave-uniform
+                    if (g < SA_INSTR) {
+                        const uint32_t off = kval ? ((uint32_t)kt * p.sa_rows + p.sa0_row + g * 256) * 4 + lane * 16 : OOB;
+                        copy16_to_lds(p.sa, sS + g * 1024, off);
+                    } else if (g < SA_INSTR + SB_INSTR) {
+                        const uint32_t off =
+                            kval ? ((uint32_t)kt * p.sb_rows + p.sb0_row + (g - SA_INSTR) * 256) * 4 + lane * 16 : OOB;
+                        copy16_to_lds(p.sb, sS + SA_REG + (g - SA_INSTR) * 1024, off);
+                    } else {
+                        copy16_to_lds(p.sa, smem + STAGES * STAGE, OOB);
                     }
                 }
             }
@@ -236,25 +268,47 @@ struct GemmCore {
 
         const int r32 = lane & 31, kh = lane >> 5;
         const int64_t nk = (p.kbytes + ROWB - 1) / ROWB;
-        load_global(0);
-        store_lds(0);
-        __syncthreads();
-        for (int64_t kt = 0; kt < nk; ++kt) {
-            const int buf = (int)(kt & 1);
-            load_global(kt + 1);  // past the end every offset is out of range: zeros, no memory traffic
-            const uint8_t* sA = smem + buf * STAGE;
+
+        // prologue: stages 0 .. STAGES - 2 in flight; a [K, N] B is written for stages 0 .. STAGES - 3 and
+        // held in rb1 for stage STAGES - 2 (written at the end of iteration 0)
+#pragma unroll
+        for (int s = 0; s < STAGES - 1; ++s) {
+            if (s < STAGES - 2) load_b_regs(rb0, s);
+            else load_b_regs(rb1, s);
+            __builtin_amdgcn_sched_barrier(0);
+            issue_copies(s, s);
+            __builtin_amdgcn_sched_barrier(0);
+            if (s < STAGES - 2) store_b_regs(rb0, s);
+        }
+
+        // one iteration: stage kt is multiplied; the registers of stage kt + STAGES - 1 are loaded into rb_new and
+        // those of stage kt + STAGES - 2 (loaded one iteration ago into rb_old) are written to their slot
+        auto iteration = [&](int64_t kt, breg_t& rb_new, breg_t& rb_old) {
+            const int slot = (int)(kt % STAGES);
+            const int nslot = (int)((kt + STAGES - 1) % STAGES);
+            const int pslot = (int)((kt + STAGES - 2) % STAGES);
+            wait_vmcnt<IN_FLIGHT>();  // this wave's copies of stage kt have landed
+            stage_barrier();          // ... and every wave's; the slot multiplied last iteration is free
+            load_b_regs(rb_new, kt + STAGES - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            issue_copies(kt + STAGES - 1, nslot);
+            __builtin_amdgcn_sched_barrier(0);
+            const uint8_t* sA = smem + slot * STAGE;
             const uint8_t* sB = sA + BM * ROWB;
+            // MX: one scale word per fragment row per stage (blocks 0..3); shifted by 8 * (lane / 32) so that
+            // byte 2s is this lane's block 2s + lane / 32 and the MFMA's op_sel picks it
+            uint32_t swa[OP == OP_MXFP4 ? FM : 1], swb[OP == OP_MXFP4 ? FN : 1];
+            if constexpr (OP == OP_MXFP4) {
+                const uint8_t* sS = sA + (BM + BN) * ROWB;
 #pragma unroll
-            for (int s = 0; s < 2 * KSTEPS; ++s) {
+                for (int i = 0; i < FM; ++i) swa[i] = *(const uint32_t*)(sS + (wm * WTM + i * 32 + r32) * SCB) >> (8 * kh);
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    swb[j] = *(const uint32_t*)(sS + SA_REG + (wn * WTN + j * 32 + r32) * SCB) >> (8 * kh);
+            }
+#pragma unroll
+            for (int s = 0; s < ROWB / 32; ++s) {
                 const int c = s * 2 + kh;  // 16-byte chunk of this lane for k-step s (= MX block index)
-                int sa[FM], sb[FN];
-                if constexpr (OP == OP_MXFP4) {
-                    const uint8_t* sS = sA + (BM + BN) * ROWB;
-#pragma unroll
-                    for (int i = 0; i < FM; ++i) sa[i] = sS[(wm * WTM + i * 32 + r32) * SCB + c];
-#pragma unroll
-                    for (int j = 0; j < FN; ++j) sb[j] = sS[(BM + wn * WTN + j * 32 + r32) * SCB + c];
-                }
                 v4i fa[FM];
 #pragma unroll
                 for (int i = 0; i < FM; ++i) {
@@ -272,17 +326,30 @@ struct GemmCore {
                         } else {
                             const v8i a8 = (v8i){fa[i][0], fa[i][1], fa[i][2], fa[i][3], 0, 0, 0, 0};
                             const v8i b8 = (v8i){fb[0], fb[1], fb[2], fb[3], 0, 0, 0, 0};
-                            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[i][j], 4, 4, 0,
-                                                                                         sa[i], 0, sb[j]);
+                            if (s == 0)
+                                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[i][j], 4, 4, 0,
+                                                                                             swa[i], 0, swb[j]);
+                            else
+                                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[i][j], 4, 4, 2,
+                                                                                             swa[i], 2, swb[j]);
                         }
                     }
                 }
             }
-            // keep this stage's MFMAs ahead of the LDS store, whose wait on the loads would otherwise stall them
-            __builtin_amdgcn_sched_barrier(0);
-            store_lds(buf ^ 1);
-            __syncthreads();
+            if constexpr (!B_KCONTIG) {
+                // rb_old's slot was freed two iterations ago and is next read after at least one more barrier
+                __builtin_amdgcn_sched_barrier(0);
+                store_b_regs(rb_old, pslot);
+            }
+        };
+        int64_t kt = 0;
+        for (; kt + 1 < nk; kt += 2) {
+            iteration(kt, rb0, rb1);
+            iteration(kt + 1, rb1, rb0);
         }
+        if (kt < nk) iteration(kt, rb0, rb1);
+        // drain: no copy may still target LDS when the caller reuses it or the wave ends
+        wait_vmcnt<0>();
     }
 };
 

@@ -4,9 +4,9 @@
 // stage/compute/mmad_compute.h:40-90 Mmad int8 -> int32 L0C; stage/copy_cube_out/copy_cube_out_fixpipe.h:339-357
 // and quant/quant_processor_fixpipe.h:74-234 for the DEQF16 / QS322BF16_PRE epilogue).
 //
-// gfx950 design: the LDS-staged v_mfma_i32_32x32x32_i8 main loop of gemm_core.h (branch-free buffer loads,
-// XOR-swizzled LDS, MFMAs overlapped with the next stage's loads, in-flight byte transpose of a row-major
-// [K, N] B), XCD-aware tile order, and the fixpipe epilogue in registers:
+// gfx950 design: the v_mfma_i32_32x32x32_i8 main loop of gemm_core.h (a ring of LDS stages filled by
+// global->LDS buffer copies, XOR-swizzled LDS, in-flight byte transpose of a row-major [K, N] B), XCD-aware
+// tile order, and the fixpipe epilogue in registers:
 //   acc (+ int32 bias) -> f32 (rne) x M1[n] -> f16 / bf16 (rne, saturating); M1 = QUANT_PRE bits [31:13]
 //   (accompanying_quantization.md:79-103).
 #include "common.h"
@@ -15,10 +15,10 @@
 
 namespace ascq {
 
-template <int BM, int BN, int WM, int WN, int KS, bool TB>
+template <int BM, int BN, int WM, int WN, int ST, bool TB>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
 {
-    using T = GemmCore<BM, BN, WM, WN, KS, TB, OP_I8>;
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tiles_m = (int)((p.M + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
     int tm, tn;
@@ -66,10 +66,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
 // QuantGroupMatmul: the m axis is split into G ragged groups (group_list), group g multiplies its rows by
 // W[g].  Workgroup slot -> (m-tile of the concatenated groups, n-tile); m-tiles never straddle a group.
 // Slots beyond the real tile count exit at once (the grid is sized for ceil(M/BM) + G m-tiles).
-template <int BM, int BN, int WM, int WN, int KS, bool TB>
+template <int BM, int BN, int WM, int WN, int ST, bool TB>
 __global__ __launch_bounds__(WM * WN * 64) void group_gemm_i8_kernel(GroupGemmArgs p)
 {
-    using T = GemmCore<BM, BN, WM, WN, KS, TB, OP_I8>;
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int64_t g_start[65], g_tile[65];
     const int G = (int)p.G;
@@ -158,19 +158,19 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(GemmI8Args p)
     }
 }
 
-template <int BM, int BN, int WM, int WN, int KS, bool TB>
+template <int BM, int BN, int WM, int WN, int ST, bool TB>
 static hipError_t launch_tiled(const GemmI8Args& a, hipStream_t st)
 {
-    using T = GemmCore<BM, BN, WM, WN, KS, TB, OP_I8>;
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8>;
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)gemm_i8_kernel<BM, BN, WM, WN, KS, TB>,
+        hipError_t e = hipFuncSetAttribute((const void*)gemm_i8_kernel<BM, BN, WM, WN, ST, TB>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::LDS_BYTES);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WM, WN, KS, TB>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
+    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WM, WN, ST, TB>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
     return hipGetLastError();
 }
 
@@ -181,8 +181,8 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
                                 : (a.ldb % 4 == 0 && a.N % 4 == 0 && ((uintptr_t)a.B % 4 == 0) && a.ldb * a.K < (1ll << 31));
     if (a_ok && b_ok && a.K % 16 == 0) {
         const bool big = a.M >= 1024 && a.N >= 1024;
-        if (a.trans_b) return big ? launch_tiled<256, 256, 4, 2, 2, true>(a, st) : launch_tiled<64, 64, 2, 2, 2, true>(a, st);
-        return big ? launch_tiled<256, 256, 4, 2, 2, false>(a, st) : launch_tiled<64, 128, 2, 2, 2, false>(a, st);
+        if (a.trans_b) return big ? launch_tiled<256, 256, 4, 2, 4, true>(a, st) : launch_tiled<64, 64, 2, 2, 4, true>(a, st);
+        return big ? launch_tiled<256, 256, 4, 2, 4, false>(a, st) : launch_tiled<64, 128, 2, 2, 4, false>(a, st);
     }
     int64_t blocks = (a.M * a.N + 255) / 256;
     if (blocks > 65536) blocks = 65536;
@@ -217,19 +217,19 @@ __global__ __launch_bounds__(256) void group_gemm_generic_kernel(GroupGemmArgs p
     }
 }
 
-template <int BM, int BN, int WM, int WN, int KS, bool TB>
+template <int BM, int BN, int WM, int WN, int ST, bool TB>
 static hipError_t launch_group_tiled(const GroupGemmArgs& a, hipStream_t st)
 {
-    using T = GemmCore<BM, BN, WM, WN, KS, TB, OP_I8>;
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8>;
     const int64_t slots = ((a.M + BM - 1) / BM + a.G) * ((a.N + BN - 1) / BN);
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)group_gemm_i8_kernel<BM, BN, WM, WN, KS, TB>,
+        hipError_t e = hipFuncSetAttribute((const void*)group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::LDS_BYTES);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((group_gemm_i8_kernel<BM, BN, WM, WN, KS, TB>), dim3((unsigned)slots), dim3(T::NT), T::LDS_BYTES,
+    hipLaunchKernelGGL((group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB>), dim3((unsigned)slots), dim3(T::NT), T::LDS_BYTES,
                        st, a);
     return hipGetLastError();
 }
@@ -240,8 +240,8 @@ hipError_t launch_group_gemm(const GroupGemmArgs& a, hipStream_t st)
                     (a.w_trans ? ((uintptr_t)a.W % 16 == 0) : (a.N % 4 == 0 && (uintptr_t)a.W % 4 == 0)) && a.G <= 64 &&
                     a.M * a.K < (1ll << 31) && a.K * a.N < (1ll << 31);
     if (ok) {
-        if (a.w_trans) return launch_group_tiled<128, 128, 2, 2, 2, true>(a, st);
-        return launch_group_tiled<128, 128, 2, 2, 2, false>(a, st);
+        if (a.w_trans) return launch_group_tiled<128, 128, 2, 2, 4, true>(a, st);
+        return launch_group_tiled<128, 128, 2, 2, 4, false>(a, st);
     }
     int64_t blocks = (a.M * a.N + 255) / 256;
     if (blocks > 65536) blocks = 65536;

@@ -145,42 +145,42 @@ __global__ __launch_bounds__(256) void quant_legacy_f16_kernel(const void* __res
 // ---------------------------------------------------------------------------------------------
 // Dequant
 // ---------------------------------------------------------------------------------------------
-// Fast path: int8 [m, n] x fp32 scale[row] -> f16, n % 16 == 0.  Each lane converts U 16-byte chunks per
-// step, all U loads issued before the first conversion.
+// Fast path: int8 [m, n] x fp32 scale[row] -> f16, n % 8 == 0.  A block owns one row segment of 256 * U
+// units of 8 elements; lane t converts units t, t + 256, ... (8-byte loads, 16-byte stores, both contiguous
+// across the wave), so every store instruction writes whole cache lines.  The row and its scale are per-block
+// scalars: no per-element index division.
 template <int U>
-__global__ __launch_bounds__(256) void dequant_i8_token_f16_kernel(const u32x4* __restrict__ q,
+__global__ __launch_bounds__(256) void dequant_i8_token_f16_kernel(const u32x2* __restrict__ q,
                                                                    const float* __restrict__ scale,
-                                                                   u32x4* __restrict__ y, int64_t chunks,
-                                                                   uint32_t chunks_per_row)
+                                                                   u32x4* __restrict__ y, uint32_t units_per_row,
+                                                                   uint32_t segs)
 {
-    const int64_t stride = (int64_t)gridDim.x * 256;
-    for (int64_t c0 = (int64_t)blockIdx.x * 256 + threadIdx.x; c0 < chunks; c0 += stride * U) {
-        u32x4 v[U];
-        float s[U];
+    const uint32_t row = blockIdx.x / segs;
+    const uint32_t u0 = (blockIdx.x - row * segs) * (256u * U) + threadIdx.x;
+    const size_t base = (size_t)row * units_per_row;
+    const float s = scale[row];
+    u32x2 v[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t c = c0 + u * stride;
-            v[u] = c < chunks ? __builtin_nontemporal_load(q + c) : (u32x4){0u, 0u, 0u, 0u};
-            s[u] = c < chunks ? scale[c / chunks_per_row] : 0.0f;
+    for (int k = 0; k < U; ++k) {
+        const uint32_t u = u0 + k * 256u;
+        v[k] = u < units_per_row ? __builtin_nontemporal_load(q + base + u) : (u32x2){0u, 0u};
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const uint32_t u = u0 + k * 256u;
+        if (u >= units_per_row) break;
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int32_t w = (int32_t)v[k][e];
+            const float f0 = (float)((w << 24) >> 24) * s;
+            const float f1 = (float)((w << 16) >> 24) * s;
+            const float f2 = (float)((w << 8) >> 24) * s;
+            const float f3 = (float)(w >> 24) * s;
+            o[2 * e] = (uint32_t)f32_to_f16_sat(f0) | ((uint32_t)f32_to_f16_sat(f1) << 16);
+            o[2 * e + 1] = (uint32_t)f32_to_f16_sat(f2) | ((uint32_t)f32_to_f16_sat(f3) << 16);
         }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t c = c0 + u * stride;
-            if (c >= chunks) break;
-            uint32_t o[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int32_t w = (int32_t)v[u][e];
-                const float f0 = (float)((w << 24) >> 24) * s[u];
-                const float f1 = (float)((w << 16) >> 24) * s[u];
-                const float f2 = (float)((w << 8) >> 24) * s[u];
-                const float f3 = (float)(w >> 24) * s[u];
-                o[2 * e] = (uint32_t)f32_to_f16_sat(f0) | ((uint32_t)f32_to_f16_sat(f1) << 16);
-                o[2 * e + 1] = (uint32_t)f32_to_f16_sat(f2) | ((uint32_t)f32_to_f16_sat(f3) << 16);
-            }
-            __builtin_nontemporal_store((u32x4){o[0], o[1], o[2], o[3]}, y + 2 * c);
-            __builtin_nontemporal_store((u32x4){o[4], o[5], o[6], o[7]}, y + 2 * c + 1);
-        }
+        __builtin_nontemporal_store((u32x4){o[0], o[1], o[2], o[3]}, y + base + u);
     }
 }
 
@@ -340,13 +340,15 @@ hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, 
                           float scale_scalar, int policy, uint32_t m, uint32_t n, uint32_t cal_count, hipStream_t st)
 {
     const bool fast = policy == 2 && src_type == DT_INT8 && dst_type == DT_F16 && scale_type == DT_F32 &&
-                      n % 16 == 0 && ((uintptr_t)src % 16 == 0) && ((uintptr_t)y % 16 == 0);
+                      n % 8 == 0 && ((uintptr_t)src % 8 == 0) && ((uintptr_t)y % 16 == 0) && m > 0 && n > 0;
     if (fast) {
-        const int64_t chunks = (int64_t)m * n / 16;
-        int64_t blocks = (chunks + 512 - 1) / 512;  // 2 chunks per lane: one pass over the tensor
-        if (blocks > (1 << 20)) blocks = 1 << 20;
-        hipLaunchKernelGGL(dequant_i8_token_f16_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, st,
-                           (const u32x4*)src, (const float*)scale, (u32x4*)y, chunks, n / 16);
+        constexpr int U = 2;  // measured best at 8192 x 8192 (U = 1: 37.6 us, 2: 33.7 us, 4: 34.6 us)
+        const uint32_t upr = n / 8;
+        const uint32_t segs = (upr + 256 * U - 1) / (256 * U);
+        const uint64_t blocks = (uint64_t)m * segs;
+        if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(dequant_i8_token_f16_kernel<U>, dim3((unsigned)blocks), dim3(256), 0, st,
+                           (const u32x2*)src, (const float*)scale, (u32x4*)y, upr, segs);
         return hipGetLastError();
     }
     uint32_t cols = policy == 1 ? cal_count : n;

@@ -9,7 +9,8 @@ Also measured and reported under "other_configs": the W8A8 int8 Matmul + per-cha
 8192^3 throughput shape), the W4A16 / W8A16 decode GEMV (M in {1, 16, 64}), the MoE group matmul and the MX-FP4
 8192^3 GEMM.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only headline]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                  [--only all|headline|w8a8|gemv|group|mx|traffic]
 """
 from __future__ import annotations
 
@@ -270,13 +271,55 @@ def bench_mx(torch, ascq, iters, trans_b=True):
                 ms=ms, value=tf, unit="TFLOPS", frac_of_peak=tf / MXFP4_PEAK_TFLOPS)
 
 
+def traffic_probe(torch, ascq):
+    """One launch each of a plain 256 MiB copy (the calibration for FETCH_SIZE / WRITE_SIZE), the dynamic
+    quant kernel and the dequant kernel on the 8192 x 8192 f16 workload, with a 1 GiB fill between them so
+    the Infinity Cache holds none of the next kernel's inputs.  Meant to run under rocprofv3 --pmc."""
+    M = N = 8192
+    x = torch.randn((M, N), device="cuda").half()
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    src = torch.randint(0, 255, (256 << 20,), dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    flush.fill_(1)
+    dst.copy_(src)
+    flush.fill_(2)
+    q, s = ascq.quant_dynamic_per_token(x)
+    flush.fill_(3)
+    ascq.ascend_dequant(q, s, ascq.PER_TOKEN, torch.float16)
+    torch.cuda.synchronize()
+    return {"traffic_probe": "copy 268435456 B, quant f16 8192x8192, dequant int8 8192x8192 -> f16"}
+
+
+OTHER = {
+    "w8a8": [lambda t, a: bench_w8a8(t, a, 128, 256, 512, 200), lambda t, a: bench_w8a8(t, a, 8192, 8192, 8192, 10)],
+    "gemv": [lambda t, a, w=w, m=m: bench_gemv(t, a, getattr(a, w), m, 200)
+             for w in ("INT4", "INT8") for m in (1, 16, 64)],
+    "group": [lambda t, a: bench_group(t, a, 20)],
+    "mx": [lambda t, a: bench_mx(t, a, 10, True), lambda t, a: bench_mx(t, a, 5, False)],
+}
+
+
+def run_others(torch, ascq, which):
+    out = []
+    for key in (["w8a8", "gemv", "group", "mx"] if which == "all" else [which]):
+        for fn in OTHER[key]:
+            try:
+                r = fn(torch, ascq)
+                out.append({k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()})
+            except Exception as e:  # report, do not hide
+                out.append({"error": repr(e)})
+            torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="all", choices=["all", "headline"])
+    ap.add_argument("--only", default="all", choices=["all", "headline", "w8a8", "gemv", "group", "mx", "traffic"],
+                    help="run one workload family (the JSON contract line is printed for all / headline)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one MI355X; run with --gpus 1 (no multi-GPU path exists)"}))
@@ -288,6 +331,12 @@ def main() -> int:
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.init()
+    if args.only == "traffic":
+        print(json.dumps(traffic_probe(torch, ascq)))
+        return 0
+    if args.only in ("w8a8", "gemv", "group", "mx"):
+        print(json.dumps({"other_configs": run_others(torch, ascq, args.only)}))
+        return 0
     h = bench_headline(torch, ascq, args.steps, args.warmup)
     step_ms = h["total_ms"] / args.steps
     step_bytes = h["bytes_quant"] + h["bytes_dequant"]
@@ -319,25 +368,7 @@ def main() -> int:
                            "avg_launch_ms": round(h["d_ms"], 5)},
     }
     if args.only == "all":
-        others = []
-        for fn in (lambda: bench_w8a8(torch, ascq, 128, 256, 512, 200),
-                   lambda: bench_w8a8(torch, ascq, 8192, 8192, 8192, 10),
-                   lambda: bench_gemv(torch, ascq, ascq.INT4, 1, 200),
-                   lambda: bench_gemv(torch, ascq, ascq.INT4, 16, 200),
-                   lambda: bench_gemv(torch, ascq, ascq.INT4, 64, 200),
-                   lambda: bench_gemv(torch, ascq, ascq.INT8, 1, 200),
-                   lambda: bench_gemv(torch, ascq, ascq.INT8, 16, 200),
-                   lambda: bench_gemv(torch, ascq, ascq.INT8, 64, 200),
-                   lambda: bench_group(torch, ascq, 20),
-                   lambda: bench_mx(torch, ascq, 10, True),
-                   lambda: bench_mx(torch, ascq, 5, False)):
-            try:
-                r = fn()
-                others.append({k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()})
-            except Exception as e:  # report, do not hide
-                others.append({"error": repr(e)})
-            torch.cuda.empty_cache()
-        rec["other_configs"] = others
+        rec["other_configs"] = run_others(torch, ascq, "all")
     if not args.no_cpu:
         rec["cpu_baseline"] = cpu_baseline_headline()
     print(json.dumps(rec))

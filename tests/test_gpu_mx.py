@@ -79,7 +79,8 @@ def check(got_f64, exact, absd, K, golden_bits=None, rel=1e-3):
 @pytest.mark.parametrize("trans_b", [True, False])
 @pytest.mark.parametrize("sa_t", [0, 1])
 @pytest.mark.parametrize("sb_t", [0, 1])
-@pytest.mark.parametrize("shape", [(256, 256, 512), (64, 96, 128), (130, 70, 384)])
+@pytest.mark.parametrize("shape", [(256, 256, 512), (64, 96, 128), (130, 70, 384), (1030, 1026, 256),
+                                   (2051, 1026, 128)])
 def test_mx_small(ascq_gpu, oracle, trans_b, sa_t, sb_t, shape):
     M, N, K = shape
     rng = seeded(M + N + K)
@@ -93,7 +94,11 @@ def test_mx_small(ascq_gpu, oracle, trans_b, sa_t, sb_t, shape):
     c = run_mx(ascq_gpu, A, sA_dev, B_dev, sB_dev, M, N, K, trans_b, sa_t, sb_t, ascq_gpu.BF16)
     C, Ce, Ca = O.mx_matmul(A, Bt, sA, sBt, M, N, K, trans_b=True, sa_layout=0, sb_layout=1)
     got = bf16_to_f64(c.view(torch.int16).numpy().view(np.uint16))
-    check(got, Ce, Ca, K, C)
+    # With block exponents spread over +-20 a handful of elements carry the whole norm, and one of them rounding
+    # to the neighbouring bf16 value (fp32 vs exact accumulation) moves the normwise error by up to one bf16 ulp
+    # (2^-8); the per-element bound in check() is the tight test here.  The 1e-3 normwise criterion is applied
+    # to N(0,1) data in test_config5_full_size_sampled.
+    check(got, Ce, Ca, K, C, rel=2.0 ** -8)
 
 
 def test_mx_f32_out(ascq_gpu, oracle):

@@ -113,11 +113,12 @@ def test_legacy_quant_f16_arith(ascq_gpu, oracle, per_channel, src):
     np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
 
 
-@pytest.mark.parametrize("m,n", [(64, 8192), (5, 48), (3, 20)])
+@pytest.mark.parametrize("m,n", [(64, 8192), (5, 48), (3, 20), (2, 8), (4, 24), (3, 8200), (1, 16392), (9, 1000)])
 def test_dequant_per_token_int8(ascq_gpu, oracle, m, n):
     rng = seeded(41 + n)
     q = rng.integers(-128, 128, (m, n), dtype=np.int8)
     scale = (rng.uniform(0.0, 1.0, m) * 0.05).astype(np.float32)
+    scale[0] = 1000.0  # |q| * 1000 > 65504: saturates to the largest finite half
     y = ascq_gpu.ascend_dequant(_dev(q), _dev(scale), ascq_gpu.PER_TOKEN, torch.float16)
     y_ref = O.dequant(q, O.INT8, scale, O.F32, O.PER_TOKEN, O.F16)
     np.testing.assert_array_equal(y.cpu().numpy().view(np.uint16), y_ref)
