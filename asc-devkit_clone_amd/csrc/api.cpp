@@ -80,9 +80,18 @@ Kind kind_of(const ascq_matmul_types& t)
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
+// int8 B given [K, N]: for large problems it is transposed to [N, K] in the workspace first, so the GEMM
+// copies both operands straight into LDS (the transpose costs 2 K N bytes of traffic; the in-loop byte
+// transpose of the [K, N] path roughly halves the GEMM's rate).
+bool i8_transposes_b(const ascq_matmul_s* h)
+{
+    return !h->trans_b && h->M >= 512 && h->N % 16 == 0 && h->K % 16 == 0;
+}
+
 size_t workspace_need(const ascq_matmul_s* h)
 {
     switch (kind_of(h->ty)) {
+    case K_INT8: return i8_transposes_b(h) ? align256((size_t)h->N * (size_t)h->K) : 0;
     case K_ANTIQUANT: {
         size_t need = 0;
         if (h->ty.b_format == ASCQ_FORMAT_ND) need += ascq::weight_pack_bytes(h->ty.b_type, h->K, h->N);
@@ -347,6 +356,15 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
                                                : (h->ty.c_type == ASCQ_DT_F16 ? ascq::EPI_DEQ_F16 : ascq::EPI_DEQ_BF16);
         g.trans_a = h->trans_a;
         g.trans_b = h->trans_b;
+        if (i8_transposes_b(h) && n == h->N && k == h->K && aligned(h->b, 16)) {
+            ascq_status s = ensure_workspace(h);
+            if (s != ASCQ_OK) return s;
+            hipError_t e = ascq::launch_transpose_i8((uint8_t*)h->ws, (const uint8_t*)h->b, h->K, h->N, st);
+            if (e != hipSuccess) return hip_status(e, "transpose_i8");
+            g.B = (const int8_t*)h->ws;
+            g.ldb = h->K;
+            g.trans_b = 1;
+        }
         return hip_status(ascq::launch_gemm_i8(g, st), "gemm_i8");
     }
     case K_ANTIQUANT: {

@@ -71,6 +71,10 @@ struct MxGemmArgs {
     int c_type;             // DT_BF16 / DT_F32
 };
 hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st);
+// transpose.hip: int8 [rows, cols] -> [cols, rows]; fp4 [K, N] -> [N, K] tiled fast path (returns false when
+// the shape / alignment does not allow it)
+hipError_t launch_transpose_i8(uint8_t* dst, const uint8_t* src, int64_t rows, int64_t cols, hipStream_t st);
+bool fp4_transpose_tiled(uint8_t* dst, const uint8_t* src, int64_t K, int64_t N, hipStream_t st, hipError_t* err);
 // E8M0 scales [R, sK] (src_layout 0) or [sK/2, R, 2] (1) -> stage-major [sK/4][R][4]
 hipError_t launch_mx_scale_stage_major(uint8_t* dst, const uint8_t* src, int64_t R, int64_t sK, int src_layout,
                                        hipStream_t st);

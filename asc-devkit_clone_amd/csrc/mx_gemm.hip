@@ -86,6 +86,8 @@ __global__ __launch_bounds__(256) void fp4_transpose_kernel(uint8_t* __restrict_
 
 hipError_t launch_fp4_transpose(uint8_t* dst, const uint8_t* src, int64_t K, int64_t N, hipStream_t st)
 {
+    hipError_t err = hipSuccess;
+    if (fp4_transpose_tiled(dst, src, K, N, st, &err)) return err;
     int64_t blocks = (N * K / 2 + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     hipLaunchKernelGGL(fp4_transpose_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, src, K, N);

@@ -1,0 +1,138 @@
+// transpose.hip -- byte and nibble transposes that turn a row-major [K, N] B operand into the K-contiguous
+// [N, K] layout the GEMM main loop copies straight into LDS.
+//
+// One 256-thread workgroup per 128 (k) x 128 (byte column) tile:
+//  * load: 16-byte chunks, eight lanes per 128-byte row segment, into LDS [k][128 bytes]; the dword column
+//    of each chunk is XOR-swizzled by ((k / 16) % 4) * 8 so the transposed reads below spread over the banks;
+//  * each lane then owns 4 byte columns x 16 k: 16 dword reads (rows k0 .. k0 + 15), four 4x4 byte
+//    transposes (v_perm_b32), and per column 16 consecutive k bytes;
+//  * int8: out[n][k0 .. k0 + 15] is one 16-byte store, eight lanes per 128-byte output row segment;
+//  * fp4 (two E2M1 per byte, even index in the low nibble): byte column c holds n = 2c (low nibbles) and
+//    n = 2c + 1 (high nibbles); the 16 k bytes of a column become 8 bytes of row 2c and 8 of row 2c + 1
+//    (k pairs packed low nibble first), two 8-byte stores.
+// Tiles on the edge load zeros past the matrix and store only inside it; the fast path needs the row length
+// in bytes and the row count to be multiples of 16 (the caller falls back to a plain kernel otherwise).
+#include "common.h"
+#include "launch.h"
+
+namespace ascq {
+
+__device__ __forceinline__ uint32_t tperm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
+
+// 4x4 byte transpose: in r[i] byte j = M[i][j]; out t[j] byte i = M[i][j]
+__device__ __forceinline__ void tr4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3, uint32_t& t0, uint32_t& t1,
+                                      uint32_t& t2, uint32_t& t3)
+{
+    const uint32_t lo01 = tperm(r1, r0, 0x05010400u);
+    const uint32_t hi01 = tperm(r1, r0, 0x07030602u);
+    const uint32_t lo23 = tperm(r3, r2, 0x05010400u);
+    const uint32_t hi23 = tperm(r3, r2, 0x07030602u);
+    t0 = tperm(lo23, lo01, 0x05040100u);
+    t1 = tperm(lo23, lo01, 0x07060302u);
+    t2 = tperm(hi23, hi01, 0x05040100u);
+    t3 = tperm(hi23, hi01, 0x07060302u);
+}
+
+// four k bytes (k, k+1, k+2, k+3) of one fp4 byte column -> 16 bits of the even-n row (low nibbles) and 16 bits
+// of the odd-n row (high nibbles), each as (k, k+1) packed low nibble first
+__device__ __forceinline__ void split_nibbles(uint32_t w, uint32_t& even, uint32_t& odd)
+{
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    const uint32_t l2 = lo | (lo >> 4), h2 = hi | (hi >> 4);  // bytes 0 and 2 hold the packed pairs
+    even = (l2 & 0xFFu) | ((l2 >> 8) & 0xFF00u);
+    odd = (h2 & 0xFFu) | ((h2 >> 8) & 0xFF00u);
+}
+
+template <bool FP4>
+__global__ __launch_bounds__(256) void transpose_tile_kernel(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src,
+                                                             int64_t rows, int64_t cols)
+{
+    __shared__ __attribute__((aligned(16))) uint32_t tile[128 * 32];  // [k][32 dwords]
+    const int64_t tiles_c = (cols + 127) / 128;
+    const int64_t k0 = (int64_t)(blockIdx.x / tiles_c) * 128, c0 = (int64_t)(blockIdx.x % tiles_c) * 128;
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int id = t + i * 256, r = id / 8, ch = id % 8;  // row r, 16-byte chunk ch
+        const int64_t k = k0 + r, c = c0 + ch * 16;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (k < rows && c < cols) v = *(const u32x4*)(src + k * cols + c);
+        const int dw = (ch * 4) ^ (((r >> 4) & 3) << 3);
+        *(u32x4*)&tile[r * 32 + dw] = v;
+    }
+    __syncthreads();
+    const int lane = t & 63, wave = t >> 6;
+    const int kq = lane & 7, cq = (lane >> 3) + 8 * wave;  // 16 k rows (kq), 4 byte columns (cq)
+    uint32_t w[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int kr = kq * 16 + r;
+        w[r] = tile[kr * 32 + (cq ^ (((kr >> 4) & 3) << 3))];
+    }
+    uint32_t col[4][4];  // col[j][q]: bytes k 4q .. 4q + 3 of byte column 4cq + j
+#pragma unroll
+    for (int q = 0; q < 4; ++q) tr4x4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3], col[0][q], col[1][q], col[2][q], col[3][q]);
+    const int64_t kk = k0 + kq * 16;
+    if (kk >= rows) return;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t c = c0 + cq * 4 + j;
+        if (c >= cols) break;
+        if constexpr (!FP4) {
+            *(u32x4*)(dst + c * rows + kk) = (u32x4){col[j][0], col[j][1], col[j][2], col[j][3]};
+        } else {
+            uint32_t e[4], o[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) split_nibbles(col[j][q], e[q], o[q]);
+            const int64_t half = rows / 2;  // output rows are K/2 bytes
+            *(u32x2*)(dst + (2 * c) * half + kk / 2) = (u32x2){e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+            *(u32x2*)(dst + (2 * c + 1) * half + kk / 2) = (u32x2){o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+        }
+    }
+}
+
+// plain int8 transpose for any shape: one thread per output byte
+__global__ __launch_bounds__(256) void transpose_i8_plain_kernel(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src,
+                                                                 int64_t rows, int64_t cols)
+{
+    const int64_t total = rows * cols;
+    for (int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x; o < total; o += (int64_t)gridDim.x * 256) {
+        const int64_t c = o / rows, r = o % rows;
+        dst[o] = src[r * cols + c];
+    }
+}
+
+static bool tiled_ok(const void* dst, const void* src, int64_t rows, int64_t cols)
+{
+    return rows % 16 == 0 && cols % 16 == 0 && (uintptr_t)dst % 16 == 0 && (uintptr_t)src % 16 == 0 &&
+           rows * cols < (1ll << 40);
+}
+
+hipError_t launch_transpose_i8(uint8_t* dst, const uint8_t* src, int64_t rows, int64_t cols, hipStream_t st)
+{
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    if (tiled_ok(dst, src, rows, cols)) {
+        const int64_t tiles = ((rows + 127) / 128) * ((cols + 127) / 128);
+        if (tiles > 0x7FFFFFFF) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(transpose_tile_kernel<false>, dim3((unsigned)tiles), dim3(256), 0, st, dst, src, rows, cols);
+        return hipGetLastError();
+    }
+    int64_t blocks = (rows * cols + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(transpose_i8_plain_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, src, rows, cols);
+    return hipGetLastError();
+}
+
+// [K, N] fp4 (two per byte along N) -> [N, K] (two per byte along K); the tiled path needs K % 16 == 0 and
+// N % 32 == 0, else the caller uses launch_fp4_transpose's plain kernel.
+bool fp4_transpose_tiled(uint8_t* dst, const uint8_t* src, int64_t K, int64_t N, hipStream_t st, hipError_t* err)
+{
+    if (!tiled_ok(dst, src, K, N / 2) || N % 32 != 0) return false;
+    const int64_t tiles = ((K + 127) / 128) * ((N / 2 + 127) / 128);
+    if (tiles > 0x7FFFFFFF) return false;
+    hipLaunchKernelGGL(transpose_tile_kernel<true>, dim3((unsigned)tiles), dim3(256), 0, st, dst, src, K, N / 2);
+    *err = hipGetLastError();
+    return true;
+}
+
+}  // namespace ascq

@@ -67,7 +67,8 @@ def test_config1_w8a8_per_channel_deqf16(ascq_gpu, oracle):
 @pytest.mark.parametrize("c_type", ["f16", "bf16"])
 @pytest.mark.parametrize("vector", [False, True])
 @pytest.mark.parametrize("trans_b", [False, True])
-@pytest.mark.parametrize("shape", [(128, 256, 512), (77, 200, 96), (300, 132, 1040), (1, 16, 16), (1024, 1024, 1024)])
+@pytest.mark.parametrize("shape", [(128, 256, 512), (77, 200, 96), (300, 132, 1040), (1, 16, 16), (1024, 1024, 1024),
+                                   (600, 272, 1040), (520, 200, 96)])
 def test_int8_matmul_variants(ascq_gpu, oracle, c_type, vector, trans_b, shape):
     rng = seeded(sum(shape) + 3 * vector + trans_b)
     M, N, K = shape
