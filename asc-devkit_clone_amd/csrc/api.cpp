@@ -100,9 +100,8 @@ size_t workspace_need(const ascq_matmul_s* h)
     }
     case K_MX: {
         // [K, N] B transposed to [N, K]; both scale tensors rearranged stage-major; 256-byte aligned parts
-        const size_t sk = (size_t)((h->K + 63) / 64 * 2);
         size_t need = h->trans_b ? 0 : align256((size_t)h->N * (size_t)(h->K / 2));
-        need += align256((size_t)h->M * sk + 16) + align256((size_t)h->N * sk + 16);  // + copy slack
+        need += ascq::mx_scale_workspace_bytes(h->M, h->N, h->K);
         return need;
     }
     default: return 0;
@@ -381,6 +380,8 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         if (s != ASCQ_OK) return s;
         uint8_t* ws = (uint8_t*)h->ws;
         const void* wp = h->b;
+        if (h->K * h->N >= (1ll << 31))
+            return fail(ASCQ_E_UNSUPPORTED, "iterate_all: the weight must stay below 2^31 elements");
         if (h->ty.b_format == ASCQ_FORMAT_ND) {
             hipError_t e = ascq::launch_weight_pack(ws, h->b, h->ty.b_type, h->K, h->N, h->trans_b, st);
             if (e != hipSuccess) return hip_status(e, "weight_pack");
@@ -419,7 +420,6 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         const uint8_t* bt = (const uint8_t*)h->b;
         const uint8_t* sa = h->scale_a;
         const uint8_t* sb = h->scale_b;
-        const int64_t sk = (h->K + 63) / 64 * 2;
         uint8_t* ws = (uint8_t*)h->ws;
         if (!h->trans_b) {
             hipError_t e = ascq::launch_fp4_transpose(ws, (const uint8_t*)h->b, h->K, h->N, st);
@@ -427,22 +427,14 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
             bt = ws;
             ws += align256((size_t)h->N * (size_t)(h->K / 2));
         }
-        {  // scaleA [M, sK] (or [sK/2, M, 2] with isTransposeScaleA) -> stage-major
-            hipError_t e = ascq::launch_mx_scale_stage_major(ws, h->scale_a, h->M, sk, h->trans_sa ? 1 : 0, st);
-            if (e != hipSuccess) return hip_status(e, "mx_scale_stage_major(A)");
-            sa = ws;
-            ws += align256((size_t)h->M * (size_t)sk + 16);
-        }
-        {  // scaleB [sK/2, N, 2] (or [N, sK] with isTransposeScaleB) -> stage-major
-            hipError_t e = ascq::launch_mx_scale_stage_major(ws, h->scale_b, h->N, sk, h->trans_sb ? 0 : 1, st);
-            if (e != hipSuccess) return hip_status(e, "mx_scale_stage_major(B)");
-            sb = ws;
-        }
         ascq::MxGemmArgs g{};
         g.A = (const uint8_t*)h->a;
         g.B = bt;
         g.sA = sa;
         g.sB = sb;
+        g.sa_layout = h->trans_sa ? 1 : 0;  // scaleA [M, sK], or [sK/2, M, 2] with isTransposeScaleA
+        g.sb_layout = h->trans_sb ? 1 : 0;  // scaleB [sK/2, N, 2], or [N, sK] with isTransposeScaleB
+        g.ws_scales = ws;  // after the B transpose (if any); the GEMM rearranges both scale tensors here
         g.M = h->M;
         g.N = h->N;
         g.K = h->K;
@@ -604,6 +596,8 @@ ascq_status ascq_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w_
         return fail(ASCQ_E_INVALID_ARG, "antiquant_matmul: group_size must be 0 or a multiple of 32 dividing K");
     if (!aligned(x, 16) || !aligned(w_packed, 16))
         return fail(ASCQ_E_INVALID_ARG, "antiquant_matmul: x and the packed weight must be 16-byte aligned");
+    if (k * n >= (1ll << 31) || 64 * k * 2 >= (1ll << 31))
+        return fail(ASCQ_E_UNSUPPORTED, "antiquant_matmul: the weight must stay below 2^31 elements");
     return hip_status(ascq::launch_antiquant_matmul(y, x, w_packed, w_type, scale, offset, group_size, m, n, k, S(stream)),
                       "antiquant_matmul");
 }

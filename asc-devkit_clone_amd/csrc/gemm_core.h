@@ -4,8 +4,9 @@
 // MFMA: the 32x32 forms, v_mfma_i32_32x32x32_i8 and v_mfma_scale_f32_32x32x64_f8f6f4 -- on gfx950 they issue at
 // the full int8 / fp4 rate, the 16x16 forms at about half of it (measured: 4.80 vs 2.71 int8 POPS, 9.34 vs
 // 4.80 fp4 POPS on one MI355X).  Both consume 32 K bytes per row per instruction, 16 bytes per lane: lane l
-// holds row l % 32 at K bytes 16 (l / 32) .. +15 of the step.  One stage holds ROWB = 64 bytes of K for every
-// tile row of A and B (int8: 64 elements, fp4: 128), i.e. two MFMA k-steps.
+// holds row l % 32 at K bytes 16 (l / 32) .. +15 of the step.  One stage holds ROWB (64 or 128) bytes of K for
+// every tile row of A and B (int8: ROWB elements, fp4: 2 ROWB), i.e. ROWB / 32 MFMA k-steps.  With ROWB = 128
+// every copied row is one whole 128-byte cache line, which halves the L2 requests per byte.
 //
 // Pipeline: a ring of STAGES LDS stages.  K-contiguous operands are copied global -> LDS by buffer loads with
 // the LDS destination (buffer_load_dwordx4 ... lds): no registers are involved, so STAGES - 1 stages are in
@@ -16,10 +17,10 @@
 // a compile-time constant.
 //
 // Layout:
-//  * LDS rows are unpadded, 64 bytes, and 16-byte chunks are XOR-swizzled: logical chunk c of row r lives at
-//    chunk c ^ ((r / 4) % 4).  The 16 lanes an MFMA operand read serves together then hit 16 distinct 4-bank
-//    groups.  A copy instruction writes 1 KiB contiguous (lane l -> row l / 4, chunk l % 4); the swizzle is
-//    applied on the global side (lane l fetches logical chunk (l % 4) ^ ((row / 4) % 4)).
+//  * LDS rows are unpadded, ROWB bytes, and 16-byte chunks are XOR-swizzled: logical chunk c of row r lives at
+//    chunk c ^ ((r / (256 / ROWB)) % (ROWB / 16)).  The 16 lanes an MFMA operand read serves together then hit
+//    16 distinct 4-bank groups.  A copy instruction writes 1 KiB contiguous (lane l -> row l / (ROWB / 16),
+//    chunk l % (ROWB / 16)); the swizzle is applied on the global side.
 //  * Global reads are raw buffer loads: an out-of-range offset returns zeros, so tile edges and the K tail
 //    need no branches.
 //  * B given row-major [K, N] (int8 only) goes through registers instead: each lane loads an 8(k) x 4(n) byte
@@ -27,10 +28,11 @@
 //    iteration after they were loaded (two iterations of latency cover; the registers are double-buffered).
 //    The row written by store j of a lane is rotated by (n-block / 4) so the 64 lanes of a store spread over
 //    the LDS banks.
-//  * MX: the E8M0 scales arrive stage-major ([sK/4][rows][4]: for each stage, the 4-byte words of all rows),
-//    so a stage's scales for 256 tile rows are one contiguous 1 KiB copy into the stage.  (Row-major scales
-//    would cost one cache line per row per stage.)  A lane reads the scale word of its fragment row once per
-//    stage, shifts it by 8 * (l / 32), and the MFMA's op_sel takes byte 2s for k-step s: block 2s + l / 32.
+//  * MX: the E8M0 scales arrive stage-major ([sK/SCB][rows][SCB], SCB = ROWB / 16 scale bytes per row per
+//    stage), so a stage's scales for 1024 / SCB tile rows are one contiguous 1 KiB copy into the stage.
+//    (Row-major scales would cost one cache line per row per stage.)  A lane reads the scale words of its
+//    fragment row once per stage, shifts them by 8 * (l / 32), and the MFMA's op_sel picks the byte of
+//    block 2s + l / 32 for k-step s.
 //  * Accumulator layout of one 32x32 tile: lane l, register r holds row 8(r/4) + 4(l/32) + r%4, column l%32.
 #pragma once
 
@@ -119,31 +121,34 @@ struct CoreArgs {
     int32_t rows, cols;   // valid rows of A / columns of B in this tile (from the tile origin)
     uint32_t a0, b0;      // byte offsets of the tile origin in the A / B buffers
     int64_t kbytes;       // K extent in bytes (int8: K; fp4: K/2); a multiple of 16
-    // MX scales, stage-major: word (stage s, row r) = blocks 4s .. 4s + 3 of row r, at byte (s * rows + r) * 4
+    // MX scales, stage-major: the SCB bytes of (stage s, row r) = blocks SCB s .. SCB s + SCB - 1 of row r, at
+    // byte (s * rows + r) * SCB
     rsrc_t sa, sb;
     uint32_t sa0_row, sb0_row;  // first row / column index of the tile
-    uint32_t sa_rows, sb_rows;  // M / N: the stage stride in words
-    uint32_t sk;                // scale blocks per row (sK, a multiple of 4)
+    uint32_t sa_rows, sb_rows;  // M / N: the stage stride in rows
+    uint32_t sk;                // scale blocks per row (sK, a multiple of SCB)
 };
 
-template <int BM, int BN, int WM, int WN, int STAGES, bool B_KCONTIG, int OP>
+template <int BM, int BN, int WM, int WN, int STAGES, bool B_KCONTIG, int OP, int ROWB_ = 64>
 struct GemmCore {
     static constexpr int NW = WM * WN;
     static constexpr int NT = NW * 64;
     static constexpr int WTM = BM / WM, WTN = BN / WN;
     static constexpr int FM = WTM / 32, FN = WTN / 32;
-    static constexpr int ROWB = 64;                   // K bytes per row per stage
+    static constexpr int ROWB = ROWB_;                // K bytes per row per stage (64 or 128)
     static constexpr int CH = ROWB / 16;              // 16-byte chunks per row
+    static constexpr int RPW = 256 / ROWB;            // rows per 256-byte bank window
     static constexpr int ROWS_PER_COPY = 64 / CH;     // rows one wave-wide 1 KiB copy covers
     static constexpr int A_COPIES = BM / ROWS_PER_COPY / NW;              // per wave per stage
     static constexpr int B_COPIES = B_KCONTIG ? BN / ROWS_PER_COPY / NW : 0;
-    static constexpr int SCB = 4;                     // MX scale bytes per row per stage (4 blocks of 32)
-    // MX scales, stage-major in memory ([sK/4][rows][4]): the words of 256 consecutive rows for one stage are
-    // 1 KiB contiguous, one wave-wide 16-byte copy.  SA_REG / SB_REG: the A / B word regions of a stage.
-    // Every wave issues SC_COPIES copies; those past the real ones read out of range into a dummy area, so
-    // the per-wave copy count (and with it the vmcnt threshold) is the same for all waves.
-    static constexpr int SA_INSTR = OP == OP_MXFP4 ? (BM + 255) / 256 : 0;
-    static constexpr int SB_INSTR = OP == OP_MXFP4 ? (BN + 255) / 256 : 0;
+    static constexpr int SCB = ROWB / 16;             // MX scale bytes per row per stage (blocks of 32 fp4)
+    static constexpr int SC_ROWS = 1024 / SCB;        // rows whose stage scales fill one 1 KiB copy
+    // MX scales, stage-major in memory ([sK/SCB][rows][SCB]): the scale bytes of SC_ROWS consecutive rows for
+    // one stage are 1 KiB contiguous, one wave-wide 16-byte copy.  SA_REG / SB_REG: the A / B scale regions
+    // of a stage.  Every wave issues SC_COPIES copies; those past the real ones read out of range into a
+    // dummy area, so the per-wave copy count (and with it the vmcnt threshold) is the same for all waves.
+    static constexpr int SA_INSTR = OP == OP_MXFP4 ? (BM + SC_ROWS - 1) / SC_ROWS : 0;
+    static constexpr int SB_INSTR = OP == OP_MXFP4 ? (BN + SC_ROWS - 1) / SC_ROWS : 0;
     static constexpr int SA_REG = SA_INSTR * 1024, SB_REG = SB_INSTR * 1024;
     static constexpr int SC_COPIES = (SA_INSTR + SB_INSTR + NW - 1) / NW;
     static constexpr int SC_BYTES = SA_REG + SB_REG;
@@ -162,7 +167,8 @@ struct GemmCore {
     static_assert(B_KCONTIG || (((ROWB / 8) * (BN / 4)) % NT == 0 && B_BLK >= 1), "B blocks");
     static_assert(OP == OP_I8 || B_KCONTIG, "fp4 B must be K-contiguous");
     static_assert(OP == OP_I8 || (BM % 64 == 0 && BN % 64 == 0), "scale row groups");
-    static_assert(STAGES >= 3 && IN_FLIGHT < 64, "stages");
+    static_assert((STAGES >= 3 || (B_KCONTIG && STAGES == 2)) && IN_FLIGHT < 64, "stages");
+    static_assert(ROWB == 64 || ROWB == 128, "stage row");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 
     __device__ __forceinline__ static int frag_row(int wm, int i, int r, int lane)
@@ -170,7 +176,7 @@ struct GemmCore {
         return wm * WTM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
     }
     __device__ __forceinline__ static int frag_col(int wn, int j, int lane) { return wn * WTN + j * 32 + (lane & 31); }
-    __device__ __forceinline__ static int swz(int row, int c) { return c ^ ((row >> 2) & 3); }
+    __device__ __forceinline__ static int swz(int row, int c) { return c ^ ((row / RPW) % CH); }
 
     __device__ __forceinline__ static void run(const CoreArgs& p, uint8_t* smem, acc_t (&acc)[FM][FN])
     {
@@ -243,16 +249,18 @@ struct GemmCore {
             }
             if constexpr (OP == OP_MXFP4) {
                 uint8_t* sS = sA + (BM + BN) * ROWB;
-                const bool kval = (uint32_t)(kt * 4) < p.sk;
+                const bool kval = (uint32_t)(kt * SCB) < p.sk;
 #pragma unroll
                 for (int j = 0; j < SC_COPIES; ++j) {
                     const int g = wave * SC_COPIES + j;  // wave-uniform
                     if (g < SA_INSTR) {
-                        const uint32_t off = kval ? ((uint32_t)kt * p.sa_rows + p.sa0_row + g * 256) * 4 + lane * 16 : OOB;
+                        const uint32_t off =
+                            kval ? ((uint32_t)kt * p.sa_rows + p.sa0_row + g * SC_ROWS) * SCB + lane * 16 : OOB;
                         copy16_to_lds(p.sa, sS + g * 1024, off);
                     } else if (g < SA_INSTR + SB_INSTR) {
                         const uint32_t off =
-                            kval ? ((uint32_t)kt * p.sb_rows + p.sb0_row + (g - SA_INSTR) * 256) * 4 + lane * 16 : OOB;
+                            kval ? ((uint32_t)kt * p.sb_rows + p.sb0_row + (g - SA_INSTR) * SC_ROWS) * SCB + lane * 16
+                                 : OOB;
                         copy16_to_lds(p.sb, sS + SA_REG + (g - SA_INSTR) * 1024, off);
                     } else {
                         copy16_to_lds(p.sa, smem + STAGES * STAGE, OOB);
@@ -287,51 +295,60 @@ struct GemmCore {
             const int slot = (int)(kt % STAGES);
             const int nslot = (int)((kt + STAGES - 1) % STAGES);
             const int pslot = (int)((kt + STAGES - 2) % STAGES);
-            wait_vmcnt<IN_FLIGHT>();  // this wave's copies of stage kt have landed
-            stage_barrier();          // ... and every wave's; the slot multiplied last iteration is free
+            __builtin_amdgcn_sched_barrier(0);  // the wait stays below the previous iteration's MFMAs
+            wait_vmcnt<IN_FLIGHT>();            // this wave's copies of stage kt have landed
+            stage_barrier();                    // ... and every wave's; the slot multiplied last iteration is free
             load_b_regs(rb_new, kt + STAGES - 1);
             __builtin_amdgcn_sched_barrier(0);
             issue_copies(kt + STAGES - 1, nslot);
             __builtin_amdgcn_sched_barrier(0);
             const uint8_t* sA = smem + slot * STAGE;
             const uint8_t* sB = sA + BM * ROWB;
-            // MX: one scale word per fragment row per stage (blocks 0..3); shifted by 8 * (lane / 32) so that
-            // byte 2s is this lane's block 2s + lane / 32 and the MFMA's op_sel picks it
-            uint32_t swa[OP == OP_MXFP4 ? FM : 1], swb[OP == OP_MXFP4 ? FN : 1];
-            if constexpr (OP == OP_MXFP4) {
-                const uint8_t* sS = sA + (BM + BN) * ROWB;
+            // k-steps in pairs (one 64-byte half row per pair); a scheduling barrier between pairs keeps the
+            // fragment reads of a 128-byte stage from being hoisted together (they would not fit the register file
+            // at two waves per SIMD).  MX: for pair h the scale word of each fragment row (blocks 4h .. 4h + 3),
+            // shifted by 8 * (lane / 32) so that byte 2(s % 2) is this lane's block 2s + lane / 32 of k-step s and
+            // the MFMA's op_sel picks it.
 #pragma unroll
-                for (int i = 0; i < FM; ++i) swa[i] = *(const uint32_t*)(sS + (wm * WTM + i * 32 + r32) * SCB) >> (8 * kh);
+            for (int h = 0; h < ROWB / 64; ++h) {
+                if (h > 0) __builtin_amdgcn_sched_barrier(0);
+                uint32_t swa[OP == OP_MXFP4 ? FM : 1], swb[OP == OP_MXFP4 ? FN : 1];
+                if constexpr (OP == OP_MXFP4) {
+                    const uint8_t* sS = sA + (BM + BN) * ROWB;
 #pragma unroll
-                for (int j = 0; j < FN; ++j)
-                    swb[j] = *(const uint32_t*)(sS + SA_REG + (wn * WTN + j * 32 + r32) * SCB) >> (8 * kh);
-            }
+                    for (int i = 0; i < FM; ++i)
+                        swa[i] = ((const uint32_t*)(sS + (wm * WTM + i * 32 + r32) * SCB))[h] >> (8 * kh);
 #pragma unroll
-            for (int s = 0; s < ROWB / 32; ++s) {
-                const int c = s * 2 + kh;  // 16-byte chunk of this lane for k-step s (= MX block index)
-                v4i fa[FM];
-#pragma unroll
-                for (int i = 0; i < FM; ++i) {
-                    const int row = wm * WTM + i * 32 + r32;
-                    fa[i] = *(const v4i*)(sA + row * ROWB + swz(row, c) * 16);
+                    for (int j = 0; j < FN; ++j)
+                        swb[j] = ((const uint32_t*)(sS + SA_REG + (wn * WTN + j * 32 + r32) * SCB))[h] >> (8 * kh);
                 }
 #pragma unroll
-                for (int j = 0; j < FN; ++j) {
-                    const int row = wn * WTN + j * 32 + r32;
-                    const v4i fb = *(const v4i*)(sB + row * ROWB + swz(row, c) * 16);
+                for (int s = 2 * h; s < 2 * h + 2; ++s) {
+                    const int c = s * 2 + kh;  // 16-byte chunk of this lane for k-step s (= MX block index)
+                    v4i fa[FM];
 #pragma unroll
                     for (int i = 0; i < FM; ++i) {
-                        if constexpr (OP == OP_I8) {
-                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb, acc[i][j], 0, 0, 0);
-                        } else {
-                            const v8i a8 = (v8i){fa[i][0], fa[i][1], fa[i][2], fa[i][3], 0, 0, 0, 0};
-                            const v8i b8 = (v8i){fb[0], fb[1], fb[2], fb[3], 0, 0, 0, 0};
-                            if (s == 0)
-                                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[i][j], 4, 4, 0,
-                                                                                             swa[i], 0, swb[j]);
-                            else
-                                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[i][j], 4, 4, 2,
-                                                                                             swa[i], 2, swb[j]);
+                        const int row = wm * WTM + i * 32 + r32;
+                        fa[i] = *(const v4i*)(sA + row * ROWB + swz(row, c) * 16);
+                    }
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) {
+                        const int row = wn * WTN + j * 32 + r32;
+                        const v4i fb = *(const v4i*)(sB + row * ROWB + swz(row, c) * 16);
+#pragma unroll
+                        for (int i = 0; i < FM; ++i) {
+                            if constexpr (OP == OP_I8) {
+                                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb, acc[i][j], 0, 0, 0);
+                            } else {
+                                const v8i a8 = (v8i){fa[i][0], fa[i][1], fa[i][2], fa[i][3], 0, 0, 0, 0};
+                                const v8i b8 = (v8i){fb[0], fb[1], fb[2], fb[3], 0, 0, 0, 0};
+                                if ((s & 1) == 0)
+                                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[i][j], 4, 4, 0,
+                                                                                                 swa[i], 0, swb[j]);
+                                else
+                                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[i][j], 4, 4, 2,
+                                                                                                 swa[i], 2, swb[j]);
+                            }
                         }
                     }
                 }

@@ -15,10 +15,10 @@
 
 namespace ascq {
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8>;
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tiles_m = (int)((p.M + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
     int tm, tn;
@@ -64,19 +64,27 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
 }
 
 // QuantGroupMatmul: the m axis is split into G ragged groups (group_list), group g multiplies its rows by
-// W[g].  Workgroup slot -> (m-tile of the concatenated groups, n-tile); m-tiles never straddle a group.
-// Slots beyond the real tile count exit at once (the grid is sized for ceil(M/BM) + G m-tiles).
-template <int BM, int BN, int WM, int WN, int ST, bool TB>
+// W[g].  The real tiles are ordered group-major, then n-tile, then m-tile within the group, and the order is cut
+// into 8 contiguous ranges, one per XCD (workgroup ids go round-robin over the XCDs): an XCD then works on one
+// or two experts' column ranges, so its L2 holds the weight columns it streams instead of every XCD fetching
+// every expert's weights.  Ids past the real tile count exit at once (the grid is sized for ceil(M/BM) + G
+// m-tiles); m-tiles never straddle a group.
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64>
 __global__ __launch_bounds__(WM * WN * 64) void group_gemm_i8_kernel(GroupGemmArgs p)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8>;
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ int64_t g_start[65], g_tile[65];
+    __shared__ int64_t g_start[65], g_tile[65], g_list[65];
     const int G = (int)p.G;
+    // the group list is read by G + 1 lanes at once (a serial walk would put G dependent loads in front of
+    // every workgroup), then prefix-summed from LDS
+    const int nl = p.list_type == 0 ? G + 1 : G;
+    if ((int)threadIdx.x < nl) g_list[threadIdx.x] = p.group_list[threadIdx.x];
+    __syncthreads();
     if (threadIdx.x == 0) {
-        int64_t s = p.list_type == 0 ? p.group_list[0] : 0, tiles = 0;
+        int64_t s = p.list_type == 0 ? g_list[0] : 0, tiles = 0;
         for (int g = 0; g < G; ++g) {
-            int64_t cnt = p.list_type == 0 ? p.group_list[g + 1] - p.group_list[g] : p.group_list[g];
+            int64_t cnt = p.list_type == 0 ? g_list[g + 1] - g_list[g] : g_list[g];
             if (cnt < 0) cnt = 0;
             g_start[g] = s;
             g_tile[g] = tiles;
@@ -87,13 +95,17 @@ __global__ __launch_bounds__(WM * WN * 64) void group_gemm_i8_kernel(GroupGemmAr
         g_tile[G] = tiles;
     }
     __syncthreads();
-    const int tiles_n = (int)((p.N + BN - 1) / BN);
-    const int64_t mt = blockIdx.x / tiles_n;
-    const int tn = blockIdx.x % tiles_n;
-    if (mt >= g_tile[G]) return;
+    const int64_t tiles_n = (p.N + BN - 1) / BN;
+    const int64_t total = g_tile[G] * tiles_n;   // real (m-tile, n-tile) pairs
+    const int64_t per_xcd = (total + 7) / 8;
+    const int64_t lin = (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if ((int64_t)(blockIdx.x / 8) >= per_xcd || lin >= total) return;
     int g = 0;
-    while (g + 1 < G && g_tile[g + 1] <= mt) ++g;
-    const int64_t m0 = g_start[g] + (mt - g_tile[g]) * BM;
+    while (g + 1 < G && g_tile[g + 1] * tiles_n <= lin) ++g;
+    const int64_t mt_g = g_tile[g + 1] - g_tile[g];  // m-tiles of group g (>= 1 here)
+    const int64_t rem = lin - g_tile[g] * tiles_n;
+    const int tn = (int)(rem / mt_g);
+    const int64_t m0 = g_start[g] + (rem % mt_g) * BM;
     int64_t m_end = g_start[g + 1];
     if (m_end > p.M) m_end = p.M;
     if (m0 < 0 || m0 >= m_end) return;  // offsets come from device memory: never form a row outside [0, M)
@@ -158,19 +170,19 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(GemmI8Args p)
     }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64>
 static hipError_t launch_tiled(const GemmI8Args& a, hipStream_t st)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8>;
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB>;
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)gemm_i8_kernel<BM, BN, WM, WN, ST, TB>,
+        hipError_t e = hipFuncSetAttribute((const void*)gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::LDS_BYTES);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WM, WN, ST, TB>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
+    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
     return hipGetLastError();
 }
 
@@ -181,7 +193,10 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
                                 : (a.ldb % 4 == 0 && a.N % 4 == 0 && ((uintptr_t)a.B % 4 == 0) && a.ldb * a.K < (1ll << 31));
     if (a_ok && b_ok && a.K % 16 == 0) {
         const bool big = a.M >= 1024 && a.N >= 1024;
-        if (a.trans_b) return big ? launch_tiled<256, 256, 4, 2, 4, true>(a, st) : launch_tiled<64, 64, 2, 2, 4, true>(a, st);
+        if (a.trans_b)
+            return big ? (a.K % 128 == 0 ? launch_tiled<256, 256, 4, 2, 2, true, 128>(a, st)
+                                         : launch_tiled<256, 256, 4, 2, 4, true>(a, st))
+                       : launch_tiled<64, 64, 2, 2, 4, true>(a, st);
         return big ? launch_tiled<256, 256, 4, 2, 4, false>(a, st) : launch_tiled<64, 128, 2, 2, 4, false>(a, st);
     }
     int64_t blocks = (a.M * a.N + 255) / 256;
@@ -217,19 +232,19 @@ __global__ __launch_bounds__(256) void group_gemm_generic_kernel(GroupGemmArgs p
     }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64>
 static hipError_t launch_group_tiled(const GroupGemmArgs& a, hipStream_t st)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8>;
-    const int64_t slots = ((a.M + BM - 1) / BM + a.G) * ((a.N + BN - 1) / BN);
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB>;
+    const int64_t slots = (((a.M + BM - 1) / BM + a.G) * ((a.N + BN - 1) / BN) + 7) / 8 * 8;
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB>,
+        hipError_t e = hipFuncSetAttribute((const void*)group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::LDS_BYTES);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB>), dim3((unsigned)slots), dim3(T::NT), T::LDS_BYTES,
+    hipLaunchKernelGGL((group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>), dim3((unsigned)slots), dim3(T::NT), T::LDS_BYTES,
                        st, a);
     return hipGetLastError();
 }
@@ -240,6 +255,10 @@ hipError_t launch_group_gemm(const GroupGemmArgs& a, hipStream_t st)
                     (a.w_trans ? ((uintptr_t)a.W % 16 == 0) : (a.N % 4 == 0 && (uintptr_t)a.W % 4 == 0)) && a.G <= 64 &&
                     a.M * a.K < (1ll << 31) && a.K * a.N < (1ll << 31);
     if (ok) {
+        // 128 x 256 tiles on 8 waves: the MoE shape (4096 tokens, 16 experts, N = 1408) needs ~250 tiles, one
+        // per CU; 128-byte stages give each wave 16 MFMAs per barrier, three stages keep two in flight
+        if (a.w_trans && a.K % 128 == 0) return launch_group_tiled<128, 256, 2, 4, 3, true, 128>(a, st);
+        if (a.w_trans) return launch_group_tiled<128, 256, 2, 4, 6, true>(a, st);
         if (a.w_trans) return launch_group_tiled<128, 128, 2, 2, 4, true>(a, st);
         return launch_group_tiled<128, 128, 2, 2, 4, false>(a, st);
     }

@@ -85,21 +85,30 @@ hipError_t launch_weight_pack(void* packed, const void* w, int w_type, int64_t K
     return hipGetLastError();
 }
 
+// 0x64006400 (two binary16 1024.0) held in a VGPR: with both masks as literals the compiler cannot fuse the
+// and / or of the int4 unpacking into one v_and_or_b32 (a VOP3 instruction takes no literal operand here)
+__device__ __forceinline__ uint32_t half_magic_vgpr()
+{
+    uint32_t m;
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(m));
+    return m;
+}
+
 // dequantise one 8-element B fragment: codes -> half(half(q + off) * scale)
 template <bool INT4, bool HAS_OFF>
-__device__ __forceinline__ h8 dequant8(uint32_t w0, uint32_t w1, h2 off, h2 sc)
+__device__ __forceinline__ h8 dequant8(uint32_t w0, uint32_t w1, h2 off, h2 sc, uint32_t magic)
 {
     uint32_t d[4];
     if constexpr (INT4) {
         // w0 holds all 8 nibbles of the step; pair i = (w0 >> 4i) & 0x000F000F
 #pragma unroll
-        for (int i = 0; i < 4; ++i) d[i] = ((w0 >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+        for (int i = 0; i < 4; ++i) d[i] = ((w0 >> (4 * i)) & 0x000F000Fu) | magic;
     } else {
-        // bytes b0..b3 of w0 and w1 -> halves 0x64bb
-        d[0] = __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u);
-        d[1] = __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u);
-        d[2] = __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u);
-        d[3] = __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u);
+        // bytes b0..b3 of w0 and w1 -> halves 0x64bb (selector 5 = byte 1 of magic = 0x64)
+        d[0] = __builtin_amdgcn_perm(magic, w0, 0x05010500u);
+        d[1] = __builtin_amdgcn_perm(magic, w0, 0x05030502u);
+        d[2] = __builtin_amdgcn_perm(magic, w1, 0x05010500u);
+        d[3] = __builtin_amdgcn_perm(magic, w1, 0x05030502u);
     }
     const h2 bias = INT4 ? (h2){(_Float16)1032.0f, (_Float16)1032.0f} : (h2){(_Float16)1152.0f, (_Float16)1152.0f};
     h2 r[4];
@@ -117,11 +126,25 @@ __device__ __forceinline__ h8 dequant8(uint32_t w0, uint32_t w1, h2 off, h2 sc)
     return out;
 }
 
-// One workgroup = KSPLIT waves over the same NBW 16-column strips, each wave a K/KSPLIT range; partial
-// 16x16 tiles are summed through LDS in a fixed order.  MT = number of 16-row m tiles (ceil(M/16)).
-// Latency: a wave issues all weight loads (and, when the quant group is a multiple of 128, all scale /
-// offset loads) of a KPW-tile chunk before its first MFMA, and prefetches the activations one k tile ahead.
-template <int MT, int NBW, int KSPLIT, int KPW, bool INT4, bool HAS_OFF, bool G128>
+typedef __amdgpu_buffer_rsrc_t aq_rsrc_t;
+constexpr uint32_t AQ_OOB = 0x80000000u;  // out-of-range buffer offset: the load returns zeros
+
+__device__ __forceinline__ aq_rsrc_t aq_rsrc(const void* base, uint64_t bytes)
+{
+    const uint32_t n = bytes >= 0x7FFFFFFFull ? 0x7FFFFFFFu : (uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+
+// One workgroup = KSPLIT waves over the same NBW 16-column strips; wave w takes the k tiles
+// (r * KSPLIT + w) * TPW + i of round r.  In a round a wave first issues every load it needs -- TPW x NBW
+// weight tiles, their scale / offset values, and its activation fragments -- as buffer loads (out-of-range
+// offsets read zeros: tiles past K multiply zero activations), then dequantises and multiplies.  Partial 16x16
+// tiles of the KSPLIT waves are summed through LDS in a fixed order.  MT = number of 16-row m tiles.
+// XLDS (decode batches, M <= 4, MT = 1): the activations x[0:M, 0:K] are staged in LDS once per workgroup
+// (loads issued before the weights, so their latency hides under the weight stream) and the MFMA A fragments
+// are read from there; rows m >= M read a zeroed 16-byte slot.  This keeps the kernel under 64 VGPRs, so every
+// workgroup of a decode launch is resident at once and the weight stream overlaps the dequantisation.
+template <int MT, int NBW, int KSPLIT, int TPW, bool INT4, bool HAS_OFF, bool G128, bool XLDS>
 __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* __restrict__ y,
                                                                      const uint16_t* __restrict__ x,
                                                                      const uint8_t* __restrict__ wp,
@@ -133,76 +156,135 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
     constexpr int LANE_BYTES = INT4 ? 16 : 32;
     constexpr int WV = INT4 ? 1 : 2;
     __shared__ v4f red[KSPLIT > 1 ? KSPLIT - 1 : 1][MT][NBW][64];
+    extern __shared__ __attribute__((aligned(16))) uint8_t xs[];  // XLDS: x[M][K] halves, then 16 zero bytes
+    static_assert(!XLDS || MT == 1, "LDS activations are for one m tile");
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t KB = K / KT;
-    const int64_t kb_per = (KB + KSPLIT - 1) / KSPLIT;
-    const int64_t kb0 = wave * kb_per;
-    const int64_t kb1 = kb0 + kb_per < KB ? kb0 + kb_per : KB;
     const int64_t nb0 = (int64_t)blockIdx.x * NBW;
     const int64_t NBT = N / 16;
     const int col_in = lane & 15, kq = lane >> 4;
+    const aq_rsrc_t rw = aq_rsrc(wp, (uint64_t)K * N / (INT4 ? 2 : 1));
+    const aq_rsrc_t rx = aq_rsrc(x, (uint64_t)M * K * 2);
+    const aq_rsrc_t rs = aq_rsrc(scale, (uint64_t)((K + g - 1) / g) * N * 2);
+    const aq_rsrc_t ro = aq_rsrc(HAS_OFF ? offset : scale, (uint64_t)((K + g - 1) / g) * N * 2);
 
     v4f acc[MT][NBW];
 #pragma unroll
     for (int a = 0; a < MT; ++a)
 #pragma unroll
         for (int b = 0; b < NBW; ++b) acc[a][b] = (v4f){0.f, 0.f, 0.f, 0.f};
+    const uint32_t magic = half_magic_vgpr();
 
-    auto load_x = [&](int64_t kb, h8 (&xf)[MT][4]) {
+    // XLDS: stage x (M * K * 2 bytes, a multiple of 256) -- these loads are the first this wave issues
+    constexpr int XL = 4;  // 16-byte chunks per thread per pass
+    u32x4 xv[XLDS ? XL : 1];
+    const int64_t xchunks = XLDS ? M * K * 2 / 16 : 0;
+    const int64_t xpasses = (xchunks + (int64_t)KSPLIT * 64 * XL - 1) / ((int64_t)KSPLIT * 64 * XL);
+    auto stage_x = [&](int64_t pass) {
 #pragma unroll
-        for (int a = 0; a < MT; ++a) {
-            const int64_t m = 16 * a + col_in;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                xf[a][j] = (m < M && kb < kb1) ? *(const h8*)(x + m * K + kb * KT + 32 * j + 8 * kq) : (h8){};
+        for (int u = 0; u < XL; ++u) {
+            const int64_t c = (pass * XL + u) * KSPLIT * 64 + threadIdx.x;
+            xv[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, c < xchunks ? (uint32_t)(c * 16) : AQ_OOB, 0, 0);
         }
     };
+    auto store_x = [&](int64_t pass) {
+#pragma unroll
+        for (int u = 0; u < XL; ++u) {
+            const int64_t c = (pass * XL + u) * KSPLIT * 64 + threadIdx.x;
+            if (c < xchunks) *(u32x4*)(xs + c * 16) = xv[u];
+        }
+    };
+    if constexpr (XLDS) {
+        if (threadIdx.x == 0) *(u32x4*)(xs + xchunks * 16) = (u32x4){0u, 0u, 0u, 0u};
+        for (int64_t ps = 0; ps + 1 < xpasses; ++ps) {  // shapes beyond one pass (large K) stage serially
+            stage_x(ps);
+            store_x(ps);
+        }
+        stage_x(xpasses - 1);  // the last pass stays in flight under the first round's weight loads
+    }
+    bool x_ready = !XLDS;
 
-    for (int64_t kc = kb0; kc < kb1; kc += KPW) {
-        u32x4 wv[KPW][NBW][WV];
-        h2 sc[G128 ? KPW : 1][NBW], of[G128 ? KPW : 1][NBW];
+    const int64_t rounds = (KB + KSPLIT * TPW - 1) / (KSPLIT * TPW);
+    for (int64_t r = 0; r < rounds; ++r) {
+        const int64_t t0 = (r * KSPLIT + wave) * TPW;  // first k tile of this wave in this round
+        u32x4 wv[TPW][NBW][WV];
+        uint32_t sc[G128 ? TPW : 1][NBW], of[G128 ? TPW : 1][NBW];
+        h8 xa[XLDS ? 1 : TPW][MT][4];
+        // issue order = use order (activations, scales, weights of tile 0, then tile 1, ...): loads retire in
+        // order, so tile i can start as soon as its own data has landed while later tiles are still in flight
 #pragma unroll
-        for (int i = 0; i < KPW; ++i)
+        for (int i = 0; i < TPW; ++i) {
+            const int64_t kb = t0 + i;
+            if constexpr (!XLDS) {
 #pragma unroll
-            for (int b = 0; b < NBW; ++b) {
-                const int64_t kb = kc + i, nb = nb0 + b;
-                const bool ok = kb < kb1 && nb < NBT;
-                const u32x4* p = (const u32x4*)(wp + (nb * KB + kb) * TILE_BYTES + lane * LANE_BYTES);
+                for (int a = 0; a < MT; ++a) {
+                    const int64_t m = 16 * a + col_in;
 #pragma unroll
-                for (int v = 0; v < WV; ++v) wv[i][b][v] = ok ? __builtin_nontemporal_load(p + v) : (u32x4){0u, 0u, 0u, 0u};
-                if constexpr (G128) {
-                    const int64_t idx = ((kb * KT) / g) * N + nb * 16 + col_in;
-                    const _Float16 s = ok ? bits_h(scale[idx]) : (_Float16)0.0f;
-                    const _Float16 o = (HAS_OFF && ok) ? bits_h(offset[idx]) : (_Float16)0.0f;
-                    sc[i][b] = (h2){s, s};
-                    of[i][b] = (h2){o, o};
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t xo =
+                            (m < M && kb < KB) ? (uint32_t)((m * K + kb * KT + 32 * j + 8 * kq) * 2) : AQ_OOB;
+                        xa[i][a][j] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0));
+                    }
                 }
             }
-        h8 xa[MT][4];
-        load_x(kc, xa);
 #pragma unroll
-        for (int i = 0; i < KPW; ++i) {
-            const int64_t kb = kc + i;
-            if (kb >= kb1) break;
-            h8 xn[MT][4];
-            load_x(kb + 1, xn);  // next k tile (zeros past this wave's range)
+            for (int b = 0; b < NBW; ++b) {
+                const int64_t nb = nb0 + b;
+                const bool ok = kb < KB && nb < NBT;
+                if constexpr (G128) {
+                    const uint32_t so = ok ? (uint32_t)((((kb * KT) / g) * N + nb * 16 + col_in) * 2) : AQ_OOB;
+                    sc[i][b] = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0);
+                    of[i][b] = HAS_OFF ? __builtin_amdgcn_raw_buffer_load_b16(ro, so, 0, 0) : 0u;
+                }
+                const uint32_t off = ok ? (uint32_t)((nb * KB + kb) * TILE_BYTES + lane * LANE_BYTES) : AQ_OOB;
+#pragma unroll
+                for (int v = 0; v < WV; ++v) wv[i][b][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, off + 16 * v, 0, 0);
+            }
+        }
+        // every load of the round is in flight before the first dequantisation (the scheduler would otherwise
+        // sink loads next to their MFMAs and pay a memory latency per k tile)
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (XLDS) {
+            if (!x_ready) {  // first round: the staged x lands (it was issued before any weight), then publish it
+                store_x(xpasses - 1);
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                __builtin_amdgcn_s_barrier();
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                x_ready = true;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TPW; ++i) {
+            const int64_t kb = t0 + i;
+            if constexpr (XLDS) {
+                const bool xok = col_in < M && kb < KB;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int64_t xo = xok ? (col_in * K + kb * KT + 32 * j + 8 * kq) * 2 : xchunks * 16;
+                    xa[0][0][j] = *(const h8*)(xs + xo);
+                }
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
 #pragma unroll
                 for (int b = 0; b < NBW; ++b) {
                     h2 s2, o2;
                     if constexpr (G128) {
-                        s2 = sc[i][b];
-                        o2 = of[i][b];
+                        const _Float16 sv = bits_h((uint16_t)sc[i][b]), ov = bits_h((uint16_t)of[i][b]);
+                        s2 = (h2){sv, sv};
+                        o2 = (h2){ov, ov};
                     } else {
-                        const int64_t n = (nb0 + b) * 16 + col_in;
-                        const bool ok = (nb0 + b) < NBT;
-                        const int64_t idx = ((kb * KT + 32 * j + 8 * kq) / g) * N + n;
-                        const _Float16 s = ok ? bits_h(scale[idx]) : (_Float16)0.0f;
-                        const _Float16 o = (HAS_OFF && ok) ? bits_h(offset[idx]) : (_Float16)0.0f;
-                        s2 = (h2){s, s};
-                        o2 = (h2){o, o};
+                        const int64_t nb = nb0 + b;
+                        const bool ok = kb < KB && nb < NBT;
+                        const uint32_t so =
+                            ok ? (uint32_t)((((kb * KT + 32 * j + 8 * kq) / g) * N + nb * 16 + col_in) * 2) : AQ_OOB;
+                        const _Float16 sv = bits_h((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0));
+                        const _Float16 ov =
+                            HAS_OFF ? bits_h((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(ro, so, 0, 0)) : (_Float16)0.0f;
+                        s2 = (h2){sv, sv};
+                        o2 = (h2){ov, ov};
                     }
                     uint32_t w0, w1 = 0;
                     if constexpr (INT4) {
@@ -211,16 +293,12 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
                         w0 = wv[i][b][j >> 1][(j & 1) * 2];
                         w1 = wv[i][b][j >> 1][(j & 1) * 2 + 1];
                     }
-                    const h8 bf = dequant8<INT4, HAS_OFF>(w0, w1, o2, s2);
+                    const h8 bf = dequant8<INT4, HAS_OFF>(w0, w1, o2, s2, magic);
 #pragma unroll
                     for (int a = 0; a < MT; ++a)
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[a][j], bf, acc[a][b], 0, 0, 0);
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[XLDS ? 0 : i][a][j], bf, acc[a][b], 0, 0, 0);
                 }
             }
-#pragma unroll
-            for (int a = 0; a < MT; ++a)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) xa[a][j] = xn[a][j];
         }
     }
 
@@ -255,33 +333,35 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
         }
 }
 
-template <int MT, int NBW, int KSPLIT, int KPW, bool INT4, bool HAS_OFF>
+template <int MT, int NBW, int KSPLIT, int TPW, bool INT4, bool HAS_OFF, bool XLDS>
 static void launch_aq2(uint16_t* y, const uint16_t* x, const void* wp, const uint16_t* scale, const uint16_t* offset,
                        int64_t g, int64_t M, int64_t N, int64_t K, hipStream_t st)
 {
     const unsigned blocks = (unsigned)((N / 16 + NBW - 1) / NBW);
+    const size_t lds = XLDS ? (size_t)(M * K * 2 + 16) : 0;
     if (g % KT == 0)
-        hipLaunchKernelGGL((antiquant_gemm_kernel<MT, NBW, KSPLIT, KPW, INT4, HAS_OFF, true>), dim3(blocks),
-                           dim3(KSPLIT * 64), 0, st, y, x, (const uint8_t*)wp, scale, offset, M, N, K, g);
+        hipLaunchKernelGGL((antiquant_gemm_kernel<MT, NBW, KSPLIT, TPW, INT4, HAS_OFF, true, XLDS>), dim3(blocks),
+                           dim3(KSPLIT * 64), lds, st, y, x, (const uint8_t*)wp, scale, offset, M, N, K, g);
     else
-        hipLaunchKernelGGL((antiquant_gemm_kernel<MT, NBW, KSPLIT, KPW, INT4, HAS_OFF, false>), dim3(blocks),
-                           dim3(KSPLIT * 64), 0, st, y, x, (const uint8_t*)wp, scale, offset, M, N, K, g);
+        hipLaunchKernelGGL((antiquant_gemm_kernel<MT, NBW, KSPLIT, TPW, INT4, HAS_OFF, false, XLDS>), dim3(blocks),
+                           dim3(KSPLIT * 64), lds, st, y, x, (const uint8_t*)wp, scale, offset, M, N, K, g);
 }
 
-template <int MT, int NBW, int KSPLIT, int KPW>
+template <int MT, int NBW, int KSPLIT, int TPW, bool XLDS = false>
 static void launch_aq(uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
                       const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, hipStream_t st)
 {
     if (int4) {
-        if (offset) launch_aq2<MT, NBW, KSPLIT, KPW, true, true>(y, x, wp, scale, offset, g, M, N, K, st);
-        else launch_aq2<MT, NBW, KSPLIT, KPW, true, false>(y, x, wp, scale, offset, g, M, N, K, st);
+        if (offset) launch_aq2<MT, NBW, KSPLIT, TPW, true, true, XLDS>(y, x, wp, scale, offset, g, M, N, K, st);
+        else launch_aq2<MT, NBW, KSPLIT, TPW, true, false, XLDS>(y, x, wp, scale, offset, g, M, N, K, st);
     } else {
-        if (offset) launch_aq2<MT, NBW, KSPLIT, KPW, false, true>(y, x, wp, scale, offset, g, M, N, K, st);
-        else launch_aq2<MT, NBW, KSPLIT, KPW, false, false>(y, x, wp, scale, offset, g, M, N, K, st);
+        if (offset) launch_aq2<MT, NBW, KSPLIT, TPW, false, true, XLDS>(y, x, wp, scale, offset, g, M, N, K, st);
+        else launch_aq2<MT, NBW, KSPLIT, TPW, false, false, XLDS>(y, x, wp, scale, offset, g, M, N, K, st);
     }
 }
 
-// M is processed in chunks of 64 rows (4 m tiles); decode shapes are a single launch.
+// M is processed in chunks of 64 rows (4 m tiles); decode shapes are a single launch.  The packed weight,
+// x and the scales must each stay below 2^31 bytes (buffer offsets; checked by the caller).
 hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* wp, int w_type, const uint16_t* scale,
                                    const uint16_t* offset, int64_t group, int64_t M, int64_t N, int64_t K,
                                    hipStream_t st)
@@ -292,9 +372,13 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
         const int64_t mc = (M - m0) < 64 ? (M - m0) : 64;
         const uint16_t* xc = x + m0 * K;
         uint16_t* yc = y + m0 * N;
-        if (mc <= 16) launch_aq<1, 1, 4, 8>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
-        else if (mc <= 32) launch_aq<2, 2, 4, 4>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
-        else launch_aq<4, 2, 4, 4>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+        // decode batches: int4 stages x in LDS (4 waves x 8 k tiles measured fastest at K = 4096); int8
+        // streams twice the bytes per element and does better with 8 waves x 4 tiles and x in registers
+        if (int4 && mc <= 4 && mc * K * 2 + 16 <= 48 * 1024)
+            launch_aq<1, 1, 4, 8, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+        else if (mc <= 16) launch_aq<1, 1, 8, 4>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+        else if (mc <= 32) launch_aq<2, 2, 8, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+        else launch_aq<4, 2, 8, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

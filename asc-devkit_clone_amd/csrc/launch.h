@@ -64,8 +64,10 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
 struct MxGemmArgs {
     const uint8_t* A;       // [M, K/2] packed E2M1
     const uint8_t* B;       // [N, K/2] packed (after any transpose)
-    const uint8_t* sA;      // scales, stage-major [sK/4][M][4] (launch_mx_scale_stage_major)
-    const uint8_t* sB;      // [sK/4][N][4]
+    const uint8_t* sA;      // scales as given: [M, sK] (sa_layout 0) or [sK/2, M, 2] (1)
+    const uint8_t* sB;      // [sK/2, N, 2] (sb_layout 0) or [N, sK] (1)
+    int sa_layout, sb_layout;
+    uint8_t* ws_scales;     // mx_scale_workspace_bytes(M, N, K) bytes: the stage-major copies of both
     int64_t M, N, K;
     void* C;                // [M, N]
     int c_type;             // DT_BF16 / DT_F32
@@ -75,9 +77,7 @@ hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st);
 // the shape / alignment does not allow it)
 hipError_t launch_transpose_i8(uint8_t* dst, const uint8_t* src, int64_t rows, int64_t cols, hipStream_t st);
 bool fp4_transpose_tiled(uint8_t* dst, const uint8_t* src, int64_t K, int64_t N, hipStream_t st, hipError_t* err);
-// E8M0 scales [R, sK] (src_layout 0) or [sK/2, R, 2] (1) -> stage-major [sK/4][R][4]
-hipError_t launch_mx_scale_stage_major(uint8_t* dst, const uint8_t* src, int64_t R, int64_t sK, int src_layout,
-                                       hipStream_t st);
+size_t mx_scale_workspace_bytes(int64_t M, int64_t N, int64_t K);
 // transpose a [K, N] packed fp4 matrix (two per byte along N) into [N, K] (two per byte along K)
 hipError_t launch_fp4_transpose(uint8_t* dst, const uint8_t* src, int64_t K, int64_t N, hipStream_t st);
 

@@ -9,8 +9,8 @@
 // (lane / 32), and one E8M0 scale byte for that (row, block) -- the hardware applies 2^(e-127) per 32-element
 // block, which is exactly the MX product.  Two fp4 per byte, even k in the low nibble: the reference packing
 // (gen_data.py:25-34) is also the MFMA's nibble order.  Block tile 256 x 256, 128 fp4 of K per stage, four
-// stages, 8 waves (4 x 2), wave tile 64 x 128.  The E8M0 scales, rearranged stage-major by mx_scale_stage_major_kernel, ride in the
-// same LDS stage.  B stored [K, N]
+// stages, 8 waves (4 x 2), wave tile 64 x 128.  The E8M0 scales, rearranged
+// stage-major by mx_scale_stage_major_kernel, ride in the same LDS stage.  B stored [K, N]
 // (the reference's non-transposed layout, two fp4 per byte along N) is first transposed to [N, K] in a
 // workspace by fp4_transpose_kernel.
 #include "common.h"
@@ -19,10 +19,11 @@
 
 namespace ascq {
 
-template <int BM, int BN, int WM, int WN, int ST>
-__global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p)
+template <int BM, int BN, int WM, int WN, int ST, int RB>
+__global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, const uint8_t* __restrict__ sa_sm,
+                                                                const uint8_t* __restrict__ sb_sm)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, true, OP_MXFP4>;
+    using T = GemmCore<BM, BN, WM, WN, ST, true, OP_MXFP4, RB>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_mx[];
     const int64_t M = p.M, N = p.N, K = p.K;
     const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
@@ -40,8 +41,8 @@ __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p)
     c.b0 = (uint32_t)(n0 * (K / 2));
     c.kbytes = K / 2;
     // the stage-major scale buffers carry 16 bytes of slack: a 16-byte copy at the end never straddles the range
-    c.sa = make_rsrc(p.sA, (uint32_t)(M * sK + 16));
-    c.sb = make_rsrc(p.sB, (uint32_t)(N * sK + 16));
+    c.sa = make_rsrc(sa_sm, (uint32_t)(M * sK + 16));
+    c.sb = make_rsrc(sb_sm, (uint32_t)(N * sK + 16));
     c.sa0_row = (uint32_t)m0;
     c.sb0_row = (uint32_t)n0;
     c.sa_rows = (uint32_t)M;
@@ -94,61 +95,85 @@ hipError_t launch_fp4_transpose(uint8_t* dst, const uint8_t* src, int64_t K, int
     return hipGetLastError();
 }
 
-// E8M0 scales -> the stage-major layout the kernel reads: dst word (g, r) = blocks 4g .. 4g + 3 of row r, at
-// byte (g * R + r) * 4.  src_layout 0: [R, sK] row-major; 1: [sK/2, R, 2] (pairs of blocks, rows inner).
-// One thread per (group, row).
-__global__ __launch_bounds__(256) void mx_scale_stage_major_kernel(uint32_t* __restrict__ dst,
+// E8M0 scales -> the stage-major layout the kernel reads: the SCB bytes of (group g, row r) are blocks
+// SCB g .. SCB g + SCB - 1 of row r, at byte (g * R + r) * SCB.  src_layout 0: [R, sK] row-major; 1: [sK/2, R, 2]
+// (pairs of blocks, rows inner).  One thread per (group, row).
+template <int SCB>
+__global__ __launch_bounds__(256) void mx_scale_stage_major_kernel(uint8_t* __restrict__ dst,
                                                                    const uint8_t* __restrict__ src, int64_t R,
                                                                    int64_t sK, int src_layout)
 {
-    const int64_t groups = sK / 4, total = groups * R;
+    const int64_t groups = sK / SCB, total = groups * R;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
         const int64_t g = i / R, r = i % R;
-        uint32_t w;
+        uint32_t w[SCB / 4];
         if (src_layout == 0) {
-            w = *(const uint32_t*)(src + r * sK + 4 * g);
+#pragma unroll
+            for (int q = 0; q < SCB / 4; ++q) w[q] = *(const uint32_t*)(src + r * sK + SCB * g + 4 * q);
         } else {
             const uint16_t* s16 = (const uint16_t*)src;
-            w = (uint32_t)s16[(2 * g) * R + r] | ((uint32_t)s16[(2 * g + 1) * R + r] << 16);
+#pragma unroll
+            for (int q = 0; q < SCB / 4; ++q) {
+                const int64_t p0 = (SCB * g + 4 * q) / 2;  // pair index of block SCB g + 4 q
+                w[q] = (uint32_t)s16[p0 * R + r] | ((uint32_t)s16[(p0 + 1) * R + r] << 16);
+            }
         }
-        dst[i] = w;
+#pragma unroll
+        for (int q = 0; q < SCB / 4; ++q) ((uint32_t*)dst)[i * (SCB / 4) + q] = w[q];
     }
 }
 
-hipError_t launch_mx_scale_stage_major(uint8_t* dst, const uint8_t* src, int64_t R, int64_t sK, int src_layout,
-                                       hipStream_t st)
+template <int SCB>
+static hipError_t launch_scale_stage_major(uint8_t* dst, const uint8_t* src, int64_t R, int64_t sK, int src_layout,
+                                           hipStream_t st)
 {
-    int64_t blocks = (R * (sK / 4) + 255) / 256;
+    int64_t blocks = (R * (sK / SCB) + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(mx_scale_stage_major_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (uint32_t*)dst, src, R,
-                       sK, src_layout);
+    hipLaunchKernelGGL(mx_scale_stage_major_kernel<SCB>, dim3((unsigned)blocks), dim3(256), 0, st, dst, src, R, sK,
+                       src_layout);
     return hipGetLastError();
 }
 
-template <int BM, int BN, int WM, int WN, int ST>
+size_t mx_scale_workspace_bytes(int64_t M, int64_t N, int64_t K)
+{
+    const int64_t sK = (K + 63) / 64 * 2;
+    return (size_t)((M * sK + 16 + 255) / 256 * 256 + (N * sK + 16 + 255) / 256 * 256);
+}
+
+template <int BM, int BN, int WM, int WN, int ST, int RB>
 static hipError_t launch_mx_tiled(const MxGemmArgs& a, hipStream_t st)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, true, OP_MXFP4>;
+    using T = GemmCore<BM, BN, WM, WN, ST, true, OP_MXFP4, RB>;
+    constexpr int SCB = T::SCB;
+    const int64_t sK = (a.K + 63) / 64 * 2;
+    uint8_t* sa_sm = a.ws_scales;
+    uint8_t* sb_sm = a.ws_scales + (a.M * sK + 16 + 255) / 256 * 256;
+    hipError_t e = launch_scale_stage_major<SCB>(sa_sm, a.sA, a.M, sK, a.sa_layout == 1 ? 1 : 0, st);
+    if (e != hipSuccess) return e;
+    e = launch_scale_stage_major<SCB>(sb_sm, a.sB, a.N, sK, a.sb_layout == 0 ? 1 : 0, st);
+    if (e != hipSuccess) return e;
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)mx_gemm_kernel<BM, BN, WM, WN, ST>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::LDS_BYTES);
+        e = hipFuncSetAttribute((const void*)mx_gemm_kernel<BM, BN, WM, WN, ST, RB>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::LDS_BYTES);
         if (e != hipSuccess) return e;
         attr = true;
     }
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
-    hipLaunchKernelGGL((mx_gemm_kernel<BM, BN, WM, WN, ST>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
+    hipLaunchKernelGGL((mx_gemm_kernel<BM, BN, WM, WN, ST, RB>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a, sa_sm,
+                       sb_sm);
     return hipGetLastError();
 }
 
-// K must be a multiple of 128 (one LDS stage is 128 fp4 of K) and both scale tensors stage-major (the caller
-// converts them with launch_mx_scale_stage_major).
+// K must be a multiple of 128 (one 64-byte LDS stage row is 128 fp4 of K); the scales are rearranged
+// stage-major into a.ws_scales (mx_scale_workspace_bytes) before the GEMM.
 hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st)
 {
-    if (a.K % 128 != 0) return hipErrorInvalidValue;
-    if (a.M >= 1024 && a.N >= 1024) return launch_mx_tiled<256, 256, 4, 2, 4>(a, st);
-    return launch_mx_tiled<64, 64, 2, 2, 4>(a, st);
+    if (a.K % 128 != 0 || !a.ws_scales) return hipErrorInvalidValue;
+    const bool big = a.M >= 1024 && a.N >= 1024;
+    if (big) return launch_mx_tiled<256, 256, 4, 2, 4, 64>(a, st);
+    return launch_mx_tiled<64, 64, 2, 2, 4, 64>(a, st);
 }
 
 }  // namespace ascq

@@ -214,7 +214,7 @@ def bench_gemv(torch, ascq, w_type, M, iters):
                 frac_of_peak=gbs / HBM_PEAK_GBS, tflops=2 * M * N * K / (ms * 1e-3) / 1e12)
 
 
-def bench_group(torch, ascq, iters):
+def bench_group(torch, ascq, iters, w_trans=False):
     G, T, K, N = 16, 4096, 4096, 1408
     rng = np.random.default_rng(4)
     p = 1.0 / (np.arange(1, G + 1) ** 1.1)
@@ -225,21 +225,23 @@ def bench_group(torch, ascq, iters):
     per = T * K + G * K * N + 2 * T * N
     R = rotation(per)
     xs = [torch.randint(-127, 128, (T, K), generator=g, device="cuda", dtype=torch.int8) for _ in range(R)]
-    ws = [torch.randint(-127, 128, (G, K, N), generator=g, device="cuda", dtype=torch.int8) for _ in range(R)]
+    wshape = (G, N, K) if w_trans else (G, K, N)
+    ws = [torch.randint(-127, 128, wshape, generator=g, device="cuda", dtype=torch.int8) for _ in range(R)]
     pts = torch.rand(T, generator=g, device="cuda") * 0.01
     scale = torch.rand((G, N), generator=g, device="cuda") * 0.01
     y = torch.empty((T, N), dtype=torch.bfloat16, device="cuda")
 
     def fn(i):
         r = i % R
-        ascq.quant_group_matmul(xs[r], pts, ws[r], scale, offsets, 0, out=y)
+        ascq.quant_group_matmul(xs[r], pts, ws[r], scale, offsets, 0, out=y, w_trans=w_trans)
 
     ms = _time_loop(torch, fn, iters)
     ops = 2 * T * K * N
     nbytes = T * K + 4 * T + G * K * N + 4 * G * N + 2 * T * N + 8 * (G + 1)
     tops = ops / (ms * 1e-3) / 1e12
     attainable = min(INT8_PEAK_TOPS, ops / nbytes * HBM_PEAK_GBS / 1e3)
-    return dict(workload=f"MoE quant group matmul, {G} experts Zipf(1.1), T={T} K={K} N={N}, bf16 out",
+    return dict(workload=f"MoE quant group matmul, {G} experts Zipf(1.1), T={T} K={K} N={N}, bf16 out, W given "
+                         + ("[G,N,K] (K-contiguous, pre-formatted)" if w_trans else "[G,K,N]"),
                 ms=ms, value=tops, unit="TOPS", frac_of_peak=tops / INT8_PEAK_TOPS,
                 frac_of_attainable=tops / attainable, gbs=nbytes / (ms * 1e-3) / 1e9,
                 group_counts=[int(c) for c in counts])
@@ -294,7 +296,7 @@ OTHER = {
     "w8a8": [lambda t, a: bench_w8a8(t, a, 128, 256, 512, 200), lambda t, a: bench_w8a8(t, a, 8192, 8192, 8192, 10)],
     "gemv": [lambda t, a, w=w, m=m: bench_gemv(t, a, getattr(a, w), m, 200)
              for w in ("INT4", "INT8") for m in (1, 16, 64)],
-    "group": [lambda t, a: bench_group(t, a, 20)],
+    "group": [lambda t, a: bench_group(t, a, 20, True), lambda t, a: bench_group(t, a, 20, False)],
     "mx": [lambda t, a: bench_mx(t, a, 10, True), lambda t, a: bench_mx(t, a, 5, False)],
 }
 

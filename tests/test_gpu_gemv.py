@@ -69,9 +69,10 @@ def test_config3_decode_shape(ascq_gpu, oracle, w_type, M):
 @pytest.mark.parametrize("group", [0, 32, 64, 256])
 @pytest.mark.parametrize("with_offset", [True, False])
 @pytest.mark.parametrize("transpose", [False, True])
-def test_groups_and_layouts(ascq_gpu, oracle, w_type, group, with_offset, transpose):
+@pytest.mark.parametrize("M", [5, 1])
+def test_groups_and_layouts(ascq_gpu, oracle, w_type, group, with_offset, transpose, M):
     rng = seeded(17 + group)
-    K, N, M = 512, 96, 5
+    K, N = 512, 96
     code = O.INT8 if w_type == "int8" else O.INT4
     w, scale, offset = make_weights(rng, K, N, code, group, with_offset)
     if transpose:  # weight given [N, K]

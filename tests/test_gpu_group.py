@@ -28,9 +28,10 @@ def bf16_bits_of_f32(v: np.ndarray) -> np.ndarray:
 @pytest.mark.parametrize("list_type", [0, 1])
 @pytest.mark.parametrize("w_trans", [False, True])
 @pytest.mark.parametrize("out", ["bf16", "f16"])
-def test_group_matmul_small(ascq_gpu, oracle, list_type, w_trans, out):
+@pytest.mark.parametrize("K", [320, 384])
+def test_group_matmul_small(ascq_gpu, oracle, list_type, w_trans, out, K):
     rng = seeded(40 + list_type + 2 * w_trans)
-    G, K, N = 5, 320, 160
+    G, N = 5, 160
     counts = np.array([70, 0, 133, 1, 96], np.int64)  # includes an empty and a single-row group
     M = int(counts.sum()) + 9  # trailing rows belong to no group and must stay untouched
     x = rng.integers(-127, 128, (M, K), dtype=np.int8)
@@ -46,10 +47,12 @@ def test_group_matmul_small(ascq_gpu, oracle, list_type, w_trans, out):
     np.testing.assert_array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), ref)
 
 
-def test_config4_moe_full_size(ascq_gpu, oracle):
+@pytest.mark.parametrize("w_trans", [False, True])
+def test_config4_moe_full_size(ascq_gpu, oracle, w_trans):
     """16 experts, 4096 tokens routed by a seeded multinomial (Zipf s=1.1), K=4096, N=1408, int64 prefix-sum
-    offsets, bf16 out.  Reference: exact int accumulators from fp64 BLAS (|acc| < 2^53), then the epilogue
-    f32(f32(acc)*scale[g,n])*pts[m] in numpy float32 and torch's rne bfloat16 cast."""
+    offsets, bf16 out; the expert weights given [G, K, N] or K-contiguous [G, N, K].  Reference: exact int
+    accumulators from fp64 BLAS (|acc| < 2^53), then the epilogue f32(f32(acc)*scale[g,n])*pts[m] in numpy float32
+    and torch's rne bfloat16 cast."""
     rng = seeded(4)
     G, T, K, N = 16, 4096, 4096, 1408
     counts = zipf_counts(rng, T, G)
@@ -58,7 +61,8 @@ def test_config4_moe_full_size(ascq_gpu, oracle):
     pts = np.exp(rng.uniform(np.log(1e-3), np.log(1e-1), T)).astype(np.float32)
     w = rng.integers(-127, 128, (G, K, N), dtype=np.int8)
     scale = np.exp(rng.uniform(np.log(1e-4), np.log(1e-2), (G, N))).astype(np.float32)
-    y = ascq_gpu.quant_group_matmul(_dev(x), _dev(pts), _dev(w), _dev(scale), _dev(offsets), 0)
+    w_dev = _dev(np.ascontiguousarray(w.transpose(0, 2, 1))) if w_trans else _dev(w)
+    y = ascq_gpu.quant_group_matmul(_dev(x), _dev(pts), w_dev, _dev(scale), _dev(offsets), 0, w_trans)
     got = y.cpu().view(torch.int16).numpy().view(np.uint16)
     xf = x.astype(np.float64)
     for g in range(G):
