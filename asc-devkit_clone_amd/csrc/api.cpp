@@ -68,30 +68,58 @@ struct ascq_matmul_s {
 
 namespace {
 
-enum Kind { K_NONE, K_INT8, K_ANTIQUANT, K_MX };
+enum Kind { K_NONE, K_INT8, K_ANTIQUANT, K_MX, K_F8 };
+
+bool is_f8(int32_t t) { return t == ASCQ_DT_FP8_E4M3 || t == ASCQ_DT_FP8_E5M2; }
+// f8f6f4 format code of an fp8 / fp4 element type (the MFMA's cbsz / blgp field)
+int f8f6f4_code(int32_t t) { return t == ASCQ_DT_FP8_E5M2 ? 1 : (t == ASCQ_DT_FP4_E2M1 ? 4 : 0); }
 
 Kind kind_of(const ascq_matmul_types& t)
 {
     if (t.a_type == ASCQ_DT_INT8 && t.b_type == ASCQ_DT_INT8) return K_INT8;
     if (t.a_type == ASCQ_DT_F16 && (t.b_type == ASCQ_DT_INT8 || t.b_type == ASCQ_DT_INT4)) return K_ANTIQUANT;
-    if (t.a_type == ASCQ_DT_FP4_E2M1 && t.b_type == ASCQ_DT_FP4_E2M1 && t.scale_type == ASCQ_DT_E8M0) return K_MX;
+    if (t.scale_type == ASCQ_DT_E8M0 &&
+        ((t.a_type == ASCQ_DT_FP4_E2M1 && t.b_type == ASCQ_DT_FP4_E2M1) || (is_f8(t.a_type) && is_f8(t.b_type))))
+        return K_MX;
+    if (t.scale_type == 0 && is_f8(t.a_type) && is_f8(t.b_type)) return K_F8;
     return K_NONE;
+}
+
+bool mx_is_fp4(const ascq_matmul_s* h) { return h->ty.a_type == ASCQ_DT_FP4_E2M1; }
+
+// DEQF16 / QS322BF16_PRE for int8 with f16 / bf16 C; QF322{F16,BF16,F32}_PRE for fp8 (quant_processor_utils.h:31-55)
+bool has_quant_epilogue(const ascq_matmul_types& t)
+{
+    const Kind k = kind_of(t);
+    return (k == K_INT8 && t.c_type != ASCQ_DT_INT32) || k == K_F8;
 }
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-// int8 B given [K, N]: for large problems it is transposed to [N, K] in the workspace first, so the GEMM
-// copies both operands straight into LDS (the transpose costs 2 K N bytes of traffic; the in-loop byte
-// transpose of the [K, N] path roughly halves the GEMM's rate).
-bool i8_transposes_b(const ascq_matmul_s* h)
+// int8 / fp8 B given [K, N]: for large problems the whole org B is transposed to [N, K] in the workspace
+// first, so the GEMM copies both operands straight into LDS (the transpose costs 2 K N bytes of traffic; the
+// in-loop byte transpose of the [K, N] path roughly halves the GEMM's rate).
+bool bytes_transposes_b(const ascq_matmul_s* h)
 {
     return !h->trans_b && h->M >= 512 && h->N % 16 == 0 && h->K % 16 == 0;
+}
+
+// int8 / fp8 A given [K, M] (isTransA): the whole org A is transposed to [M, K] in the workspace (the tiled
+// GEMM reads K-contiguous A rows only)
+bool bytes_transposes_a(const ascq_matmul_s* h) { return h->trans_a != 0; }
+
+size_t bytes_workspace(const ascq_matmul_s* h)
+{
+    size_t need = bytes_transposes_b(h) ? align256((size_t)h->N * (size_t)h->K) : 0;
+    if (bytes_transposes_a(h)) need += align256((size_t)h->M * (size_t)h->K);
+    return need;
 }
 
 size_t workspace_need(const ascq_matmul_s* h)
 {
     switch (kind_of(h->ty)) {
-    case K_INT8: return i8_transposes_b(h) ? align256((size_t)h->N * (size_t)h->K) : 0;
+    case K_INT8:
+    case K_F8: return bytes_workspace(h);
     case K_ANTIQUANT: {
         size_t need = 0;
         if (h->ty.b_format == ASCQ_FORMAT_ND) need += ascq::weight_pack_bytes(h->ty.b_type, h->K, h->N);
@@ -100,7 +128,8 @@ size_t workspace_need(const ascq_matmul_s* h)
     }
     case K_MX: {
         // [K, N] B transposed to [N, K]; both scale tensors rearranged stage-major; 256-byte aligned parts
-        size_t need = h->trans_b ? 0 : align256((size_t)h->N * (size_t)(h->K / 2));
+        const size_t kb = mx_is_fp4(h) ? (size_t)(h->K / 2) : (size_t)h->K;
+        size_t need = h->trans_b ? 0 : align256((size_t)h->N * kb);
         need += ascq::mx_scale_workspace_bytes(h->M, h->N, h->K);
         return need;
     }
@@ -120,6 +149,46 @@ ascq_status ensure_workspace(ascq_matmul_s* h)
     if (e != hipSuccess) return hip_status(e, "hipMalloc(workspace)");
     h->ws_bytes = need;
     h->ws_owned = true;
+    return ASCQ_OK;
+}
+
+// int8 / fp8 operands after the workspace transposes (bytes_transposes_a / _b): pointers, leading dimensions
+// (org shape) and the layouts the GEMM sees
+struct ByteOperands {
+    const uint8_t* A;
+    const uint8_t* B;
+    int64_t lda, ldb;
+    int trans_a, trans_b;
+};
+
+ascq_status prepare_byte_operands(ascq_matmul_s* h, hipStream_t st, ByteOperands& o)
+{
+    o.A = (const uint8_t*)h->a;
+    o.B = (const uint8_t*)h->b;
+    o.lda = h->trans_a ? h->M : h->K;
+    o.ldb = h->trans_b ? h->K : h->N;
+    o.trans_a = h->trans_a;
+    o.trans_b = h->trans_b;
+    const bool tb = bytes_transposes_b(h), ta = bytes_transposes_a(h);
+    if (!tb && !ta) return ASCQ_OK;
+    ascq_status s = ensure_workspace(h);
+    if (s != ASCQ_OK) return s;
+    uint8_t* ws = (uint8_t*)h->ws;
+    if (tb) {  // B [K, N] -> [N, K]
+        hipError_t e = ascq::launch_transpose_i8(ws, (const uint8_t*)h->b, h->K, h->N, st);
+        if (e != hipSuccess) return hip_status(e, "transpose B");
+        o.B = ws;
+        o.ldb = h->K;
+        o.trans_b = 1;
+        ws += align256((size_t)h->N * (size_t)h->K);
+    }
+    if (ta) {  // A [K, M] -> [M, K]
+        hipError_t e = ascq::launch_transpose_i8(ws, (const uint8_t*)h->a, h->K, h->M, st);
+        if (e != hipSuccess) return hip_status(e, "transpose A");
+        o.A = ws;
+        o.lda = h->K;
+        o.trans_a = 0;
+    }
     return ASCQ_OK;
 }
 
@@ -169,6 +238,12 @@ ascq_status ascq_matmul_create(const ascq_matmul_types* types, ascq_matmul_t* ou
     } else if (k == K_ANTIQUANT) {
         if (types->c_type != ASCQ_DT_F16) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: weight-only matmul supports C = f16");
         if (types->bias_type != 0) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: weight-only matmul has no bias path");
+    } else if (k == K_F8) {
+        if (types->c_type != ASCQ_DT_F16 && types->c_type != ASCQ_DT_BF16 && types->c_type != ASCQ_DT_F32)
+            return fail(ASCQ_E_UNSUPPORTED, "matmul_create: fp8 matmul supports C = f16, bf16 or f32");
+        if (types->bias_type != 0 && types->bias_type != ASCQ_DT_F32)
+            return fail(ASCQ_E_UNSUPPORTED, "matmul_create: fp8 matmul bias must be f32");
+        if (types->b_format != ASCQ_FORMAT_ND) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: fp8 B must be ND");
     } else {
         if (types->c_type != ASCQ_DT_BF16 && types->c_type != ASCQ_DT_F32)
             return fail(ASCQ_E_UNSUPPORTED, "matmul_create: MX matmul supports C = bf16 or f32");
@@ -231,7 +306,9 @@ ascq_status ascq_matmul_set_tensor_b(ascq_matmul_t h, const void* b, int32_t is_
 ascq_status ascq_matmul_set_bias(ascq_matmul_t h, const void* bias)
 {
     if (!h || !bias) return fail(ASCQ_E_INVALID_ARG, "set_bias: null argument");
-    if (h->ty.bias_type != ASCQ_DT_INT32) return fail(ASCQ_E_UNSUPPORTED, "set_bias: the handle has no int32 bias type");
+    if (h->ty.bias_type != ASCQ_DT_INT32 && h->ty.bias_type != ASCQ_DT_F32)
+        return fail(ASCQ_E_UNSUPPORTED, "set_bias: the handle has no bias type");
+    if (!aligned(bias, 4)) return fail(ASCQ_E_INVALID_ARG, "set_bias: pointer must be 4-byte aligned");
     h->bias = bias;
     return ASCQ_OK;
 }
@@ -246,7 +323,7 @@ ascq_status ascq_matmul_disable_bias(ascq_matmul_t h)
 ascq_status ascq_matmul_set_quant_scalar(ascq_matmul_t h, uint64_t quant_scalar)
 {
     if (!h) return fail(ASCQ_E_INVALID_ARG, "null handle");
-    if (kind_of(h->ty) != K_INT8 || h->ty.c_type == ASCQ_DT_INT32)
+    if (!has_quant_epilogue(h->ty))
         return fail(ASCQ_E_UNSUPPORTED, "set_quant_scalar: no quant epilogue for this type combination");
     h->quant_set = true;
     h->qvec = nullptr;
@@ -257,7 +334,7 @@ ascq_status ascq_matmul_set_quant_scalar(ascq_matmul_t h, uint64_t quant_scalar)
 ascq_status ascq_matmul_set_quant_vector(ascq_matmul_t h, const uint64_t* quant_vector)
 {
     if (!h || !quant_vector) return fail(ASCQ_E_INVALID_ARG, "set_quant_vector: null argument");
-    if (kind_of(h->ty) != K_INT8 || h->ty.c_type == ASCQ_DT_INT32)
+    if (!has_quant_epilogue(h->ty))
         return fail(ASCQ_E_UNSUPPORTED, "set_quant_vector: no quant epilogue for this type combination");
     if (!aligned(quant_vector, 8)) return fail(ASCQ_E_INVALID_ARG, "set_quant_vector: pointer must be 8-byte aligned");
     h->quant_set = true;
@@ -353,18 +430,41 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         g.qscalar = h->qscalar;
         g.epi = h->ty.c_type == ASCQ_DT_INT32 ? ascq::EPI_I32
                                                : (h->ty.c_type == ASCQ_DT_F16 ? ascq::EPI_DEQ_F16 : ascq::EPI_DEQ_BF16);
-        g.trans_a = h->trans_a;
-        g.trans_b = h->trans_b;
-        if (i8_transposes_b(h) && n == h->N && k == h->K && aligned(h->b, 16)) {
-            ascq_status s = ensure_workspace(h);
-            if (s != ASCQ_OK) return s;
-            hipError_t e = ascq::launch_transpose_i8((uint8_t*)h->ws, (const uint8_t*)h->b, h->K, h->N, st);
-            if (e != hipSuccess) return hip_status(e, "transpose_i8");
-            g.B = (const int8_t*)h->ws;
-            g.ldb = h->K;
-            g.trans_b = 1;
-        }
+        ByteOperands o;
+        ascq_status s = prepare_byte_operands(h, st, o);
+        if (s != ASCQ_OK) return s;
+        g.A = (const int8_t*)o.A;
+        g.B = (const int8_t*)o.B;
+        g.lda = o.lda;
+        g.ldb = o.ldb;
+        g.trans_a = o.trans_a;
+        g.trans_b = o.trans_b;
         return hip_status(ascq::launch_gemm_i8(g, st), "gemm_i8");
+    }
+    case K_F8: {
+        ascq::GemmF8Args g{};
+        ByteOperands o;
+        ascq_status s = prepare_byte_operands(h, st, o);
+        if (s != ASCQ_OK) return s;
+        g.A = o.A;
+        g.B = o.B;
+        g.lda = o.lda;
+        g.ldb = o.ldb;
+        g.trans_a = o.trans_a;
+        g.trans_b = o.trans_b;
+        g.bias = (const float*)h->bias;
+        g.C = c;
+        g.M = m;
+        g.N = n;
+        g.K = k;
+        g.ldc = h->N;
+        g.qvec = h->qvec;
+        g.qscalar = h->qscalar;
+        g.use_quant = h->quant_set ? 1 : 0;
+        g.c_type = h->ty.c_type;  // ascq_dtype codes equal the device DT_* codes
+        g.fmt_a = f8f6f4_code(h->ty.a_type);
+        g.fmt_b = f8f6f4_code(h->ty.b_type);
+        return hip_status(ascq::launch_gemm_f8(g, st), "gemm_f8");
     }
     case K_ANTIQUANT: {
         if (!h->aq_set) return fail(ASCQ_E_STATE, "iterate_all: SetAntiQuantScalar/Vector must precede IterateAll");
@@ -411,8 +511,13 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         if (m != h->M || n != h->N || k != h->K)
             return fail(ASCQ_E_UNSUPPORTED, "iterate_all: MX matmul computes the full org shape only");
         if (h->trans_a) return fail(ASCQ_E_UNSUPPORTED, "iterate_all: MX matmul needs A = [M, K]");
-        if (h->K % 128 != 0) return fail(ASCQ_E_UNSUPPORTED, "iterate_all: MX matmul needs K %% 128 == 0");
-        if (!h->trans_b && h->N % 2 != 0) return fail(ASCQ_E_INVALID_ARG, "iterate_all: [K, N] fp4 B needs even N");
+        const bool fp4 = mx_is_fp4(h);
+        if (h->K % (fp4 ? 128 : 64) != 0)
+            return fail(ASCQ_E_UNSUPPORTED, "iterate_all: MX matmul needs K %% %d == 0", fp4 ? 128 : 64);
+        const int64_t kb = fp4 ? h->K / 2 : h->K;  // bytes per row
+        if (h->M * kb >= (1ll << 31) || h->N * kb >= (1ll << 31))
+            return fail(ASCQ_E_UNSUPPORTED, "iterate_all: MX operands must stay below 2 GiB");
+        if (fp4 && !h->trans_b && h->N % 2 != 0) return fail(ASCQ_E_INVALID_ARG, "iterate_all: [K, N] fp4 B needs even N");
         if (!aligned(h->a, 16) || !aligned(h->b, 16) || !aligned(h->scale_a, 4) || !aligned(h->scale_b, 4))
             return fail(ASCQ_E_INVALID_ARG, "iterate_all: MX operands must be 16-byte (scales 4-byte) aligned");
         ascq_status s = ensure_workspace(h);
@@ -422,10 +527,11 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         const uint8_t* sb = h->scale_b;
         uint8_t* ws = (uint8_t*)h->ws;
         if (!h->trans_b) {
-            hipError_t e = ascq::launch_fp4_transpose(ws, (const uint8_t*)h->b, h->K, h->N, st);
-            if (e != hipSuccess) return hip_status(e, "fp4_transpose");
+            hipError_t e = fp4 ? ascq::launch_fp4_transpose(ws, (const uint8_t*)h->b, h->K, h->N, st)
+                               : ascq::launch_transpose_i8(ws, (const uint8_t*)h->b, h->K, h->N, st);
+            if (e != hipSuccess) return hip_status(e, "transpose B");
             bt = ws;
-            ws += align256((size_t)h->N * (size_t)(h->K / 2));
+            ws += align256((size_t)h->N * (size_t)(fp4 ? h->K / 2 : h->K));
         }
         ascq::MxGemmArgs g{};
         g.A = (const uint8_t*)h->a;
@@ -440,6 +546,8 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         g.K = h->K;
         g.C = c;
         g.c_type = h->ty.c_type;  // ascq_dtype codes equal the device DT_* codes
+        g.fmt_a = f8f6f4_code(h->ty.a_type);
+        g.fmt_b = f8f6f4_code(h->ty.b_type);
         return hip_status(ascq::launch_mx_gemm(g, st), "mx_gemm");
     }
     default: return fail(ASCQ_E_UNSUPPORTED, "iterate_all: unsupported handle");

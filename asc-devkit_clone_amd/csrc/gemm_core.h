@@ -1,12 +1,18 @@
-// gemm_core.h -- the LDS-staged MFMA main loop shared by the int8 Matmul, the MoE group matmul and the MX-FP4
-// Matmul (gfx950).
+// gemm_core.h -- the LDS-staged MFMA main loop shared by the int8 and fp8 Matmuls, the MoE group matmul and
+// the MX (FP4 / FP8 element) Matmuls (gfx950).
 //
-// MFMA: the 32x32 forms, v_mfma_i32_32x32x32_i8 and v_mfma_scale_f32_32x32x64_f8f6f4 -- on gfx950 they issue at
-// the full int8 / fp4 rate, the 16x16 forms at about half of it (measured: 4.80 vs 2.71 int8 POPS, 9.34 vs
-// 4.80 fp4 POPS on one MI355X).  Both consume 32 K bytes per row per instruction, 16 bytes per lane: lane l
-// holds row l % 32 at K bytes 16 (l / 32) .. +15 of the step.  One stage holds ROWB (64 or 128) bytes of K for
-// every tile row of A and B (int8: ROWB elements, fp4: 2 ROWB), i.e. ROWB / 32 MFMA k-steps.  With ROWB = 128
-// every copied row is one whole 128-byte cache line, which halves the L2 requests per byte.
+// MFMA: the 32x32 forms, v_mfma_i32_32x32x32_i8 and v_mfma_[scale_]f32_32x32x64_f8f6f4 -- on gfx950 they issue
+// at the full int8 / fp8 / fp4 rate, the 16x16 forms at about half of it (measured: 4.80 vs 2.71 int8 POPS,
+// 9.34 vs 4.80 fp4 POPS on one MI355X).  A k-step (one instruction) covers 32 int8, 64 fp4 or 64 fp8 of K per
+// row: 32, 32 or 64 bytes.  Lane l holds row l % 32.  int8 / fp4: 16 bytes, the K half l / 32 of the step (fp4:
+// 32 elements, one MX block).  fp8: 32 bytes in two register quads; the instruction's K order is [quad 0 of
+// lanes 0-31, quad 0 of lanes 32-63, quad 1 of lanes 0-31, quad 1 of lanes 32-63], so lane l takes K bytes
+// 16 (l / 32) .. +15 into quad 0 and 32 + 16 (l / 32) .. +15 into quad 1, and MX block b (K 32 b .. 32 b + 31)
+// is quad b of every lane, its scale supplied by lanes 32 b .. 32 b + 31 (measured with one nonzero K per row
+// and different block scales).
+// One stage holds ROWB (64 or 128) bytes of K for every tile row of A and B, i.e. ROWB / 32 (int8, fp4) or
+// ROWB / 64 (fp8) k-steps.  With ROWB = 128 every copied row is one whole 128-byte cache line, which halves
+// the L2 requests per byte.
 //
 // Pipeline: a ring of STAGES LDS stages.  K-contiguous operands are copied global -> LDS by buffer loads with
 // the LDS destination (buffer_load_dwordx4 ... lds): no registers are involved, so STAGES - 1 stages are in
@@ -28,11 +34,14 @@
 //    iteration after they were loaded (two iterations of latency cover; the registers are double-buffered).
 //    The row written by store j of a lane is rotated by (n-block / 4) so the 64 lanes of a store spread over
 //    the LDS banks.
-//  * MX: the E8M0 scales arrive stage-major ([sK/SCB][rows][SCB], SCB = ROWB / 16 scale bytes per row per
-//    stage), so a stage's scales for 1024 / SCB tile rows are one contiguous 1 KiB copy into the stage.
+//  * MX: the E8M0 scales arrive stage-major ([sK/SCB][rows][SCB], SCB = scale bytes per row per stage: ROWB / 16
+//    for fp4, ROWB / 32 for fp8), so a stage's scales for 1024 / SCB tile rows are one contiguous 1 KiB copy
+//    into the stage.
 //    (Row-major scales would cost one cache line per row per stage.)  A lane reads the scale words of its
-//    fragment row once per stage, shifts them by 8 * (l / 32), and the MFMA's op_sel picks the byte of
-//    block 2s + l / 32 for k-step s.
+//    fragment row per pair of k-steps (a 16-bit pair when a stage holds a single fp8 k-step), shifts them by
+//    8 * (l / 32), and the MFMA's op_sel picks the byte of block 2s + l / 32 for k-step s.
+//  * fp8 without block scales uses the same instruction with zero scale operands, which the compiler emits as
+//    the unscaled v_mfma_f32_32x32x64_f8f6f4.
 //  * Accumulator layout of one 32x32 tile: lane l, register r holds row 8(r/4) + 4(l/32) + r%4, column l%32.
 #pragma once
 
@@ -113,14 +122,19 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
     tn = in_group / gm;
 }
 
-enum { OP_I8 = 0, OP_MXFP4 = 1 };
+// operand kinds: int8; MX block-scaled E2M1; fp8 (per-tensor / per-channel dequant in the epilogue); MX
+// block-scaled fp8
+enum { OP_I8 = 0, OP_MXFP4 = 1, OP_F8 = 2, OP_MXF8 = 3 };
+
+// f8f6f4 format codes (the MFMA's cbsz / blgp fields)
+enum { F8F6F4_E4M3 = 0, F8F6F4_E5M2 = 1, F8F6F4_E2M1 = 4 };
 
 struct CoreArgs {
     rsrc_t a, b;          // A: rows of lda bytes; B: rows of ldb bytes ([n][k] when K-contiguous, else [k][n])
     uint32_t lda, ldb;    // leading dimensions in bytes
     int32_t rows, cols;   // valid rows of A / columns of B in this tile (from the tile origin)
     uint32_t a0, b0;      // byte offsets of the tile origin in the A / B buffers
-    int64_t kbytes;       // K extent in bytes (int8: K; fp4: K/2); a multiple of 16
+    int64_t kbytes;       // K extent in bytes (int8, fp8: K; fp4: K/2); a multiple of 16
     // MX scales, stage-major: the SCB bytes of (stage s, row r) = blocks SCB s .. SCB s + SCB - 1 of row r, at
     // byte (s * rows + r) * SCB
     rsrc_t sa, sb;
@@ -129,8 +143,13 @@ struct CoreArgs {
     uint32_t sk;                // scale blocks per row (sK, a multiple of SCB)
 };
 
-template <int BM, int BN, int WM, int WN, int STAGES, bool B_KCONTIG, int OP, int ROWB_ = 64>
+// FMT (fp8 ops): f8f6f4 format code of A in bits 0-2 and of B in bits 3-5
+template <int BM, int BN, int WM, int WN, int STAGES, bool B_KCONTIG, int OP, int ROWB_ = 64, int FMT = 0>
 struct GemmCore {
+    static constexpr bool IS_MX = OP == OP_MXFP4 || OP == OP_MXF8;
+    static constexpr bool IS_F8 = OP == OP_F8 || OP == OP_MXF8;
+    static constexpr int CBSZ = OP == OP_MXFP4 ? F8F6F4_E2M1 : (FMT & 7);
+    static constexpr int BLGP = OP == OP_MXFP4 ? F8F6F4_E2M1 : ((FMT >> 3) & 7);
     static constexpr int NW = WM * WN;
     static constexpr int NT = NW * 64;
     static constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -141,18 +160,23 @@ struct GemmCore {
     static constexpr int ROWS_PER_COPY = 64 / CH;     // rows one wave-wide 1 KiB copy covers
     static constexpr int A_COPIES = BM / ROWS_PER_COPY / NW;              // per wave per stage
     static constexpr int B_COPIES = B_KCONTIG ? BN / ROWS_PER_COPY / NW : 0;
-    static constexpr int SCB = ROWB / 16;             // MX scale bytes per row per stage (blocks of 32 fp4)
+    static constexpr int KSB = IS_F8 ? 64 : 32;       // K bytes per row per k-step
+    static constexpr int LCH = KSB / 32;              // 16-byte chunks per lane per k-step
+    static constexpr int KPS = ROWB / KSB;            // k-steps per stage
+    static constexpr int NH = KPS >= 2 ? KPS / 2 : 1; // pairs of k-steps per stage (one MX scale word each)
+    static constexpr int SPH = KPS >= 2 ? 2 : 1;      // k-steps per pair
+    static constexpr int SCB = ROWB / (IS_F8 ? 32 : 16);  // MX scale bytes per row per stage (blocks of 32)
     static constexpr int SC_ROWS = 1024 / SCB;        // rows whose stage scales fill one 1 KiB copy
     // MX scales, stage-major in memory ([sK/SCB][rows][SCB]): the scale bytes of SC_ROWS consecutive rows for
     // one stage are 1 KiB contiguous, one wave-wide 16-byte copy.  SA_REG / SB_REG: the A / B scale regions
     // of a stage.  Every wave issues SC_COPIES copies; those past the real ones read out of range into a
     // dummy area, so the per-wave copy count (and with it the vmcnt threshold) is the same for all waves.
-    static constexpr int SA_INSTR = OP == OP_MXFP4 ? (BM + SC_ROWS - 1) / SC_ROWS : 0;
-    static constexpr int SB_INSTR = OP == OP_MXFP4 ? (BN + SC_ROWS - 1) / SC_ROWS : 0;
+    static constexpr int SA_INSTR = IS_MX ? (BM + SC_ROWS - 1) / SC_ROWS : 0;
+    static constexpr int SB_INSTR = IS_MX ? (BN + SC_ROWS - 1) / SC_ROWS : 0;
     static constexpr int SA_REG = SA_INSTR * 1024, SB_REG = SB_INSTR * 1024;
     static constexpr int SC_COPIES = (SA_INSTR + SB_INSTR + NW - 1) / NW;
     static constexpr int SC_BYTES = SA_REG + SB_REG;
-    static constexpr int DUMMY_BYTES = OP == OP_MXFP4 && SC_COPIES * NW > SA_INSTR + SB_INSTR ? 1024 : 0;
+    static constexpr int DUMMY_BYTES = IS_MX && SC_COPIES * NW > SA_INSTR + SB_INSTR ? 1024 : 0;
     static constexpr int COPIES = A_COPIES + B_COPIES + SC_COPIES;
     static constexpr int B_BLK = B_KCONTIG ? 0 : (ROWB / 8) * (BN / 4) / NT;  // 8x4-byte blocks per lane
     static constexpr int B_LOADS = 8 * B_BLK;         // dword loads per lane per stage for a [K, N] B
@@ -165,8 +189,10 @@ struct GemmCore {
     static_assert(BM % (ROWS_PER_COPY * NW) == 0 && A_COPIES >= 1, "A copies must split evenly over the waves");
     static_assert(!B_KCONTIG || (BN % (ROWS_PER_COPY * NW) == 0 && B_COPIES >= 1), "B copies");
     static_assert(B_KCONTIG || (((ROWB / 8) * (BN / 4)) % NT == 0 && B_BLK >= 1), "B blocks");
-    static_assert(OP == OP_I8 || B_KCONTIG, "fp4 B must be K-contiguous");
-    static_assert(OP == OP_I8 || (BM % 64 == 0 && BN % 64 == 0), "scale row groups");
+    static_assert(!IS_MX || B_KCONTIG, "MX B must be K-contiguous");
+    static_assert(!IS_MX || (BM % 64 == 0 && BN % 64 == 0), "scale row groups");
+    static_assert(!IS_MX || SCB % 4 == 0 || SCB == 2, "MX stage scale bytes per row");
+    static_assert(KPS >= 1, "a stage holds at least one k-step");
     static_assert((STAGES >= 3 || (B_KCONTIG && STAGES == 2)) && IN_FLIGHT < 64, "stages");
     static_assert(ROWB == 64 || ROWB == 128, "stage row");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS");
@@ -177,6 +203,28 @@ struct GemmCore {
     }
     __device__ __forceinline__ static int frag_col(int wn, int j, int lane) { return wn * WTN + j * 32 + (lane & 31); }
     __device__ __forceinline__ static int swz(int row, int c) { return c ^ ((row / RPW) % CH); }
+
+    // MX scale bytes of pair h for one tile row: four blocks (a 32-bit word), or two when a stage holds a single
+    // fp8 k-step (SCB = 2)
+    __device__ __forceinline__ static uint32_t scale_word(const uint8_t* region, int row, int h)
+    {
+        if constexpr (SCB == 2) return ((const uint16_t*)(region + row * SCB))[0];
+        else return ((const uint32_t*)(region + row * SCB))[h];
+    }
+
+    // the operand fragment of k-step s for tile row `row` of a stage: 16 bytes (upper half zero) or 32 bytes
+    __device__ __forceinline__ static v8i read_frag(const uint8_t* base, int row, int s, int kh)
+    {
+        if constexpr (LCH == 1) {
+            const v4i x = *(const v4i*)(base + row * ROWB + swz(row, s * 2 + kh) * 16);
+            return (v8i){x[0], x[1], x[2], x[3], 0, 0, 0, 0};
+        } else {
+            const int c = s * 4 + kh;
+            const v4i x = *(const v4i*)(base + row * ROWB + swz(row, c) * 16);
+            const v4i y = *(const v4i*)(base + row * ROWB + swz(row, c + 2) * 16);
+            return (v8i){x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+        }
+    }
 
     __device__ __forceinline__ static void run(const CoreArgs& p, uint8_t* smem, acc_t (&acc)[FM][FN])
     {
@@ -247,7 +295,7 @@ struct GemmCore {
                 const uint32_t off = (row < p.cols && k < p.kbytes) ? p.b0 + (uint32_t)row * p.ldb + (uint32_t)k : OOB;
                 copy16_to_lds(p.b, sB + row0 * ROWB, off);
             }
-            if constexpr (OP == OP_MXFP4) {
+            if constexpr (IS_MX) {
                 uint8_t* sS = sA + (BM + BN) * ROWB;
                 const bool kval = (uint32_t)(kt * SCB) < p.sk;
 #pragma unroll
@@ -304,50 +352,48 @@ struct GemmCore {
             __builtin_amdgcn_sched_barrier(0);
             const uint8_t* sA = smem + slot * STAGE;
             const uint8_t* sB = sA + BM * ROWB;
-            // k-steps in pairs (one 64-byte half row per pair); a scheduling barrier between pairs keeps the
-            // fragment reads of a 128-byte stage from being hoisted together (they would not fit the register file
-            // at two waves per SIMD).  MX: for pair h the scale word of each fragment row (blocks 4h .. 4h + 3),
-            // shifted by 8 * (lane / 32) so that byte 2(s % 2) is this lane's block 2s + lane / 32 of k-step s and
-            // the MFMA's op_sel picks it.
+            // k-steps in pairs; a scheduling barrier between pairs keeps the fragment reads of a stage from
+            // being hoisted together (they would not fit the register file at two waves per SIMD).  MX: for pair
+            // h the scale word of each fragment row (blocks 4h .. 4h + 3), shifted by 8 * (lane / 32) so that
+            // byte 2(s % 2) is block 2s + lane / 32 -- the block whose scale this lane supplies for k-step s --
+            // and the MFMA's op_sel picks it.
 #pragma unroll
-            for (int h = 0; h < ROWB / 64; ++h) {
+            for (int h = 0; h < NH; ++h) {
                 if (h > 0) __builtin_amdgcn_sched_barrier(0);
-                uint32_t swa[OP == OP_MXFP4 ? FM : 1], swb[OP == OP_MXFP4 ? FN : 1];
-                if constexpr (OP == OP_MXFP4) {
+                uint32_t swa[IS_MX ? FM : 1], swb[IS_MX ? FN : 1];
+                if constexpr (IS_MX) {
                     const uint8_t* sS = sA + (BM + BN) * ROWB;
 #pragma unroll
-                    for (int i = 0; i < FM; ++i)
-                        swa[i] = ((const uint32_t*)(sS + (wm * WTM + i * 32 + r32) * SCB))[h] >> (8 * kh);
+                    for (int i = 0; i < FM; ++i) swa[i] = scale_word(sS, wm * WTM + i * 32 + r32, h) >> (8 * kh);
 #pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        swb[j] = ((const uint32_t*)(sS + SA_REG + (wn * WTN + j * 32 + r32) * SCB))[h] >> (8 * kh);
+                    for (int j = 0; j < FN; ++j) swb[j] = scale_word(sS + SA_REG, wn * WTN + j * 32 + r32, h) >> (8 * kh);
                 }
 #pragma unroll
-                for (int s = 2 * h; s < 2 * h + 2; ++s) {
-                    const int c = s * 2 + kh;  // 16-byte chunk of this lane for k-step s (= MX block index)
-                    v4i fa[FM];
+                for (int s = SPH * h; s < SPH * h + SPH; ++s) {
+                    // this lane's 16-byte chunks of k-step s: s * 2 + kh (int8, fp4), s * 4 + kh and s * 4 + 2 + kh
+                    // (fp8)
+                    v8i fa[FM];
 #pragma unroll
-                    for (int i = 0; i < FM; ++i) {
-                        const int row = wm * WTM + i * 32 + r32;
-                        fa[i] = *(const v4i*)(sA + row * ROWB + swz(row, c) * 16);
-                    }
+                    for (int i = 0; i < FM; ++i) fa[i] = read_frag(sA, wm * WTM + i * 32 + r32, s, kh);
 #pragma unroll
                     for (int j = 0; j < FN; ++j) {
-                        const int row = wn * WTN + j * 32 + r32;
-                        const v4i fb = *(const v4i*)(sB + row * ROWB + swz(row, c) * 16);
+                        const v8i fb = read_frag(sB, wn * WTN + j * 32 + r32, s, kh);
 #pragma unroll
                         for (int i = 0; i < FM; ++i) {
                             if constexpr (OP == OP_I8) {
-                                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb, acc[i][j], 0, 0, 0);
+                                const v4i a4 = (v4i){fa[i][0], fa[i][1], fa[i][2], fa[i][3]};
+                                const v4i b4 = (v4i){fb[0], fb[1], fb[2], fb[3]};
+                                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, b4, acc[i][j], 0, 0, 0);
+                            } else if constexpr (OP == OP_F8) {
+                                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb, acc[i][j], CBSZ,
+                                                                                             BLGP, 0, 0, 0, 0);
                             } else {
-                                const v8i a8 = (v8i){fa[i][0], fa[i][1], fa[i][2], fa[i][3], 0, 0, 0, 0};
-                                const v8i b8 = (v8i){fb[0], fb[1], fb[2], fb[3], 0, 0, 0, 0};
                                 if ((s & 1) == 0)
-                                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[i][j], 4, 4, 0,
-                                                                                                 swa[i], 0, swb[j]);
+                                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                                        fa[i], fb, acc[i][j], CBSZ, BLGP, 0, swa[i], 0, swb[j]);
                                 else
-                                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[i][j], 4, 4, 2,
-                                                                                                 swa[i], 2, swb[j]);
+                                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                                        fa[i], fb, acc[i][j], CBSZ, BLGP, 2, swa[i], 2, swb[j]);
                             }
                         }
                     }

@@ -1,0 +1,168 @@
+// gemm_f8.hip -- fp8 (e4m3fn / e5m2, any mix) x fp8 -> fp32 GEMM on CDNA4 MFMA with the fixpipe epilogue fused.
+//
+// Replaces the adv_api Matmul with fp8 A / B (examples/01_simd_cpp_api/04_advanced_api/00_matmul/matmul_fp8/
+// matmul_fp8.asc; L0C type fp32, impl/adv_api/detail/matmul/utils/matmul_utils.h:134-175) and its
+// QF322F16_PRE / QF322BF16_PRE / QF322F32_PRE epilogue (stage/copy_cube_out/quant/quant_processor_fixpipe.h:101-115,
+// mode rules quant_processor_utils.h:39-43):
+//   out = cast((acc + bias[n]) * M1)   with M1 from SetQuantScalar / SetQuantVector (QUANT_PRE bits [31:13]),
+//   out = cast(acc + bias[n])          without a quant word (F322F16 / F322BF16 / F32).
+// The float bias seeds the accumulator in the reference (MmadCompute with isBias, mmad_compute.h:40-90); adding
+// it to the finished fp32 sum differs only by fp32 rounding.
+//
+// gfx950 design: the gemm_core.h main loop with v_mfma_f32_32x32x64_f8f6f4 (the f8f6f4 MFMA with zero scale
+// operands), cbsz / blgp selecting e4m3 (0) or e5m2 (1) per operand: per lane 32 fp8 of one row in two
+// register quads, 64 K per instruction (K order in gemm_core.h).  The instruction sums each group of 16
+// consecutive K products (one register quad) aligned to the group's largest product and drops what falls below
+// 2^(e_max - 13) (measured: 1 + 2^-15 gives 1 within a group and 1 + 2^-15 across groups or k-steps), so
+// results differ from an fp32-accumulated sum by up to ~2^-13 of the group maxima.  gfx950's fp8 formats are
+// the OCP ones: e4m3 with no infinities and S.1111.111 as NaN (fp8_e4m3fn_t) and IEEE-like e5m2 (fp8_e5m2_t).
+// Tiles, stages and the [K, N] B register transpose are those of the int8 GEMM (fp8 operands are bytes like
+// int8).  hifloat8 (the reference's third format) has no gfx950 hardware encoding and is not accepted by the
+// host API.
+#include "common.h"
+#include "gemm_core.h"
+#include "launch.h"
+
+namespace ascq {
+
+// fp8 bits -> fp32, from the format definitions (e4m3fn: bias 7, NaN = S.1111.111, no inf; e5m2: bias 15,
+// exponent 31 = inf / NaN)
+__device__ __forceinline__ float fp8_to_f32(uint8_t v, int fmt)
+{
+    const uint32_t s = (uint32_t)(v & 0x80u) << 24;
+    if (fmt == F8F6F4_E4M3) {
+        const uint32_t e = (v >> 3) & 15u, m = v & 7u;
+        if (e == 15u && m == 7u) return __uint_as_float(0x7fc00000u);
+        if (e == 0u) return __uint_as_float(s | __float_as_uint((float)m * 0x1p-9f));
+        return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+    }
+    const uint32_t e = (v >> 2) & 31u, m = v & 3u;
+    if (e == 31u) return __uint_as_float(m ? 0x7fc00000u : (s | 0x7f800000u));
+    if (e == 0u) return __uint_as_float(s | __float_as_uint((float)m * 0x1p-16f));
+    return __uint_as_float(s | ((e + 112u) << 23) | (m << 21));
+}
+
+__device__ __forceinline__ void store_f8_out(void* C, int c_type, int64_t o, float v)
+{
+    if (c_type == DT_F32) ((float*)C)[o] = v;
+    else if (c_type == DT_F16) ((uint16_t*)C)[o] = f32_to_f16_sat(v);
+    else ((uint16_t*)C)[o] = f32_to_bf16_sat(v);
+}
+
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
+{
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_F8, RB, FMT>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem_f8[];
+    const int tiles_m = (int)((p.M + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    CoreArgs c{};
+    c.a = make_rsrc(p.A, (uint32_t)(p.lda * (p.M - 1) + p.K));
+    c.b = TB ? make_rsrc(p.B, (uint32_t)(p.ldb * (p.N - 1) + p.K)) : make_rsrc(p.B, (uint32_t)(p.ldb * (p.K - 1) + p.N));
+    c.lda = (uint32_t)p.lda;
+    c.ldb = (uint32_t)p.ldb;
+    c.rows = (int32_t)(p.M - m0 < BM ? p.M - m0 : BM);
+    c.cols = (int32_t)(p.N - n0 < BN ? p.N - n0 : BN);
+    c.a0 = (uint32_t)(m0 * p.lda);
+    c.b0 = (uint32_t)(TB ? n0 * p.ldb : n0);
+    c.kbytes = p.K;
+    typename T::acc_t acc[T::FM][T::FN];
+    T::run(c, smem_f8, acc);
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const float mscalar = quant_pre_m1(p.qscalar);
+#pragma unroll
+    for (int j = 0; j < T::FN; ++j) {
+        const int64_t col = n0 + T::frag_col(wn, j, lane);
+        if (col >= p.N) continue;
+        const float bias = p.bias ? p.bias[col] : 0.0f;
+        const float m1 = p.qvec ? quant_pre_m1(p.qvec[col]) : mscalar;
+#pragma unroll
+        for (int i = 0; i < T::FM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = m0 + T::frag_row(wm, i, r, lane);
+                if (row >= p.M) continue;
+                float v = acc[i][j][r];
+                if (p.bias) v = v + bias;
+                if (p.use_quant) v = v * m1;
+                store_f8_out(p.C, p.c_type, row * p.ldc + col, v);
+            }
+        }
+    }
+}
+
+// Any shape / layout / alignment: one thread per output element, fp32 accumulation in k order.
+__global__ __launch_bounds__(256) void gemm_f8_generic_kernel(GemmF8Args p)
+{
+    const int64_t total = p.M * p.N;
+    const float mscalar = quant_pre_m1(p.qscalar);
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+        const int64_t m = e / p.N, n = e % p.N;
+        float acc = 0.0f;
+        for (int64_t k = 0; k < p.K; ++k) {
+            const float a = fp8_to_f32(p.trans_a ? p.A[k * p.lda + m] : p.A[m * p.lda + k], p.fmt_a);
+            const float b = fp8_to_f32(p.trans_b ? p.B[n * p.ldb + k] : p.B[k * p.ldb + n], p.fmt_b);
+            acc = acc + a * b;  // the product of two fp8 values is exact in fp32
+        }
+        if (p.bias) acc = acc + p.bias[n];
+        if (p.use_quant) acc = acc * (p.qvec ? quant_pre_m1(p.qvec[n]) : mscalar);
+        store_f8_out(p.C, p.c_type, m * p.ldc + n, acc);
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT>
+static hipError_t launch_f8_tiled(const GemmF8Args& a, hipStream_t st)
+{
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_F8, RB, FMT>;
+    const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::LDS_BYTES);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
+    return hipGetLastError();
+}
+
+template <int FMT>
+static hipError_t launch_f8_fmt(const GemmF8Args& a, hipStream_t st)
+{
+    const bool big = a.M >= 1024 && a.N >= 1024;
+    if (a.trans_b) {
+        if (big) return a.K % 128 == 0 ? launch_f8_tiled<256, 256, 4, 2, 2, true, 128, FMT>(a, st)
+                                       : launch_f8_tiled<256, 256, 4, 2, 4, true, 64, FMT>(a, st);
+        return launch_f8_tiled<64, 64, 2, 2, 4, true, 64, FMT>(a, st);
+    }
+    // a large [K, N] B is transposed by the host layer first; this in-loop transpose serves the rest
+    return launch_f8_tiled<64, 128, 2, 2, 4, false, 64, FMT>(a, st);
+}
+
+hipError_t launch_gemm_f8(const GemmF8Args& a, hipStream_t st)
+{
+    if ((a.fmt_a != F8F6F4_E4M3 && a.fmt_a != F8F6F4_E5M2) || (a.fmt_b != F8F6F4_E4M3 && a.fmt_b != F8F6F4_E5M2))
+        return hipErrorInvalidValue;
+    const bool a_ok = !a.trans_a && a.lda % 16 == 0 && ((uintptr_t)a.A % 16 == 0) && a.lda * a.M < (1ll << 31);
+    const bool b_ok = a.trans_b ? (a.ldb % 16 == 0 && ((uintptr_t)a.B % 16 == 0) && a.ldb * a.N < (1ll << 31))
+                                : (a.ldb % 4 == 0 && a.N % 4 == 0 && ((uintptr_t)a.B % 4 == 0) && a.ldb * a.K < (1ll << 31));
+    if (a_ok && b_ok && a.K % 16 == 0) {
+        switch (a.fmt_a | (a.fmt_b << 3)) {
+        case F8F6F4_E4M3 | (F8F6F4_E4M3 << 3): return launch_f8_fmt<F8F6F4_E4M3 | (F8F6F4_E4M3 << 3)>(a, st);
+        case F8F6F4_E5M2 | (F8F6F4_E5M2 << 3): return launch_f8_fmt<F8F6F4_E5M2 | (F8F6F4_E5M2 << 3)>(a, st);
+        case F8F6F4_E4M3 | (F8F6F4_E5M2 << 3): return launch_f8_fmt<F8F6F4_E4M3 | (F8F6F4_E5M2 << 3)>(a, st);
+        default: return launch_f8_fmt<F8F6F4_E5M2 | (F8F6F4_E4M3 << 3)>(a, st);
+        }
+    }
+    int64_t blocks = (a.M * a.N + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(gemm_f8_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace ascq

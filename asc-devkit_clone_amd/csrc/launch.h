@@ -37,6 +37,22 @@ struct GemmI8Args {
 };
 hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st);
 
+// gemm_f8.hip
+struct GemmF8Args {
+    const uint8_t* A;     // fp8 [M, K] row-major (lda), or [K, M] when trans_a
+    const uint8_t* B;     // fp8 [K, N] row-major (ldb), or [N, K] when trans_b
+    const float* bias;    // [N] or null
+    void* C;              // [M, N] row-major (ldc)
+    int64_t M, N, K, lda, ldb, ldc;
+    const uint64_t* qvec; // per-channel QUANT_PRE words [N] or null
+    uint64_t qscalar;
+    int use_quant;        // 1: multiply by M1 (SetQuantScalar / SetQuantVector was called)
+    int c_type;           // DT_F16 / DT_BF16 / DT_F32
+    int fmt_a, fmt_b;     // f8f6f4 codes: 0 e4m3fn, 1 e5m2
+    int trans_a, trans_b;
+};
+hipError_t launch_gemm_f8(const GemmF8Args& a, hipStream_t st);
+
 // group_gemm.hip
 struct GroupGemmArgs {
     void* Y;
@@ -62,8 +78,8 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
 
 // mx_gemm.hip
 struct MxGemmArgs {
-    const uint8_t* A;       // [M, K/2] packed E2M1
-    const uint8_t* B;       // [N, K/2] packed (after any transpose)
+    const uint8_t* A;       // [M, K/2] packed E2M1, or [M, K] fp8
+    const uint8_t* B;       // [N, K/2] packed, or [N, K] fp8 (after any transpose)
     const uint8_t* sA;      // scales as given: [M, sK] (sa_layout 0) or [sK/2, M, 2] (1)
     const uint8_t* sB;      // [sK/2, N, 2] (sb_layout 0) or [N, sK] (1)
     int sa_layout, sb_layout;
@@ -71,6 +87,7 @@ struct MxGemmArgs {
     int64_t M, N, K;
     void* C;                // [M, N]
     int c_type;             // DT_BF16 / DT_F32
+    int fmt_a, fmt_b;       // f8f6f4 codes of the elements: 4 E2M1 (both), or fp8 0 e4m3fn / 1 e5m2 (any mix)
 };
 hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st);
 // transpose.hip: int8 [rows, cols] -> [cols, rows]; fp4 [K, N] -> [N, K] tiled fast path (returns false when

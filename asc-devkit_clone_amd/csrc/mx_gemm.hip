@@ -1,8 +1,11 @@
-// mx_gemm.hip -- MX-FP4 (E2M1 elements, E8M0 scale per 32 K) block-scaled GEMM on gfx950.
+// mx_gemm.hip -- MX block-scaled GEMM on gfx950: E2M1 (MX-FP4) or fp8 e4m3fn / e5m2 (MX-FP8) elements with one
+// E8M0 scale per 32 K.
 //
-// Reference: Matmul<MatmulTypeWithScale<..., fp4x2_e2m1_t, ...>> with SetTensorScaleA/B and IterateAll
-// (impl/adv_api/detail/matmul/mx_matmul_impl.h:136-188; MmadMx include/basic_api/kernel_operator_mm_intf.h:348-352),
-// fp32 accumulation, F322BF16 (rint) in the fixpipe.  Golden: matmul_mxfp4_high_performance/scripts/gen_data.py.
+// Reference: Matmul<MatmulTypeWithScale<..., fp4x2_e2m1_t | fp8_e4m3fn_t | fp8_e5m2_t, ...>> with
+// SetTensorScaleA/B and IterateAll (impl/adv_api/detail/matmul/mx_matmul_impl.h:136-188; MmadMx
+// include/basic_api/kernel_operator_mm_intf.h:348-352), fp32 accumulation, F322BF16 (rint) in the fixpipe.
+// Golden: matmul_mxfp4_high_performance/scripts/gen_data.py; the MX-FP8 sample is
+// examples/01_simd_cpp_api/04_advanced_api/00_matmul/matmul_mx/matmul_mx.asc:90-244 (e5m2 elements, fp32 C).
 //
 // gfx950 design: the LDS-ring main loop of gemm_core.h with v_mfma_scale_f32_32x32x64_f8f6f4, both formats
 // FP4 (cbsz = blgp = 4): per lane 32 E2M1 values (16 bytes, one MX block) of row (lane % 32) at k block
@@ -13,33 +16,40 @@
 // stage-major by mx_scale_stage_major_kernel, ride in the same LDS stage.  B stored [K, N]
 // (the reference's non-transposed layout, two fp4 per byte along N) is first transposed to [N, K] in a
 // workspace by fp4_transpose_kernel.
+//
+// MX-FP8 uses the same instruction with fp8 format codes: per lane 32 fp8 of one row (32 bytes, two register
+// quads; MX block b of a k-step is quad b of all 64 lanes, see gemm_core.h);
+// 64 fp8 of K per 64-byte stage row (one k-step, a 16-bit pair of scales per row), four stages of 256 x 256
+// (128-byte stages spill the copy offsets at 256 VGPRs).  A [K, N] fp8 B is transposed to [N, K] by the byte
+// transpose first.
 #include "common.h"
 #include "gemm_core.h"
 #include "launch.h"
 
 namespace ascq {
 
-template <int BM, int BN, int WM, int WN, int ST, int RB>
+template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT>
 __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, const uint8_t* __restrict__ sa_sm,
                                                                 const uint8_t* __restrict__ sb_sm)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, true, OP_MXFP4, RB>;
+    using T = GemmCore<BM, BN, WM, WN, ST, true, OP, RB, FMT>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_mx[];
     const int64_t M = p.M, N = p.N, K = p.K;
+    const int64_t KB = OP == OP_MXFP4 ? K / 2 : K;  // bytes per row
     const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
     int tm, tn;
     tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     const int64_t sK = (K + 63) / 64 * 2;
     CoreArgs c{};
-    c.a = make_rsrc(p.A, (uint32_t)(M * (K / 2)));
-    c.b = make_rsrc(p.B, (uint32_t)(N * (K / 2)));
-    c.lda = c.ldb = (uint32_t)(K / 2);
+    c.a = make_rsrc(p.A, (uint32_t)(M * KB));
+    c.b = make_rsrc(p.B, (uint32_t)(N * KB));
+    c.lda = c.ldb = (uint32_t)KB;
     c.rows = (int32_t)(M - m0 < BM ? M - m0 : BM);
     c.cols = (int32_t)(N - n0 < BN ? N - n0 : BN);
-    c.a0 = (uint32_t)(m0 * (K / 2));
-    c.b0 = (uint32_t)(n0 * (K / 2));
-    c.kbytes = K / 2;
+    c.a0 = (uint32_t)(m0 * KB);
+    c.b0 = (uint32_t)(n0 * KB);
+    c.kbytes = KB;
     // the stage-major scale buffers carry 16 bytes of slack: a 16-byte copy at the end never straddles the range
     c.sa = make_rsrc(sa_sm, (uint32_t)(M * sK + 16));
     c.sb = make_rsrc(sb_sm, (uint32_t)(N * sK + 16));
@@ -106,7 +116,12 @@ __global__ __launch_bounds__(256) void mx_scale_stage_major_kernel(uint8_t* __re
     const int64_t groups = sK / SCB, total = groups * R;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
         const int64_t g = i / R, r = i % R;
-        uint32_t w[SCB / 4];
+        if constexpr (SCB == 2) {  // one 16-bit pair of blocks (2g, 2g + 1); layout 1 stores exactly those pairs
+            ((uint16_t*)dst)[i] = src_layout == 0 ? *(const uint16_t*)(src + r * sK + 2 * g)
+                                                  : ((const uint16_t*)src)[g * R + r];
+            continue;
+        }
+        uint32_t w[SCB / 4 > 0 ? SCB / 4 : 1];
         if (src_layout == 0) {
 #pragma unroll
             for (int q = 0; q < SCB / 4; ++q) w[q] = *(const uint32_t*)(src + r * sK + SCB * g + 4 * q);
@@ -141,10 +156,10 @@ size_t mx_scale_workspace_bytes(int64_t M, int64_t N, int64_t K)
     return (size_t)((M * sK + 16 + 255) / 256 * 256 + (N * sK + 16 + 255) / 256 * 256);
 }
 
-template <int BM, int BN, int WM, int WN, int ST, int RB>
+template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT>
 static hipError_t launch_mx_tiled(const MxGemmArgs& a, hipStream_t st)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, true, OP_MXFP4, RB>;
+    using T = GemmCore<BM, BN, WM, WN, ST, true, OP, RB, FMT>;
     constexpr int SCB = T::SCB;
     const int64_t sK = (a.K + 63) / 64 * 2;
     uint8_t* sa_sm = a.ws_scales;
@@ -155,25 +170,43 @@ static hipError_t launch_mx_tiled(const MxGemmArgs& a, hipStream_t st)
     if (e != hipSuccess) return e;
     static bool attr = false;
     if (!attr) {
-        e = hipFuncSetAttribute((const void*)mx_gemm_kernel<BM, BN, WM, WN, ST, RB>,
+        e = hipFuncSetAttribute((const void*)mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::LDS_BYTES);
         if (e != hipSuccess) return e;
         attr = true;
     }
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
-    hipLaunchKernelGGL((mx_gemm_kernel<BM, BN, WM, WN, ST, RB>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a, sa_sm,
-                       sb_sm);
+    hipLaunchKernelGGL((mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a,
+                       sa_sm, sb_sm);
     return hipGetLastError();
 }
 
-// K must be a multiple of 128 (one 64-byte LDS stage row is 128 fp4 of K); the scales are rearranged
+template <int FMT>
+static hipError_t launch_mx_f8(const MxGemmArgs& a, hipStream_t st)
+{
+    const bool big = a.M >= 1024 && a.N >= 1024;
+    if (big) return launch_mx_tiled<256, 256, 4, 2, 4, 64, OP_MXF8, FMT>(a, st);
+    return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXF8, FMT>(a, st);
+}
+
+// K must be a multiple of one LDS stage row: 128 fp4 (64 bytes) or 64 fp8 (64 bytes); the scales are rearranged
 // stage-major into a.ws_scales (mx_scale_workspace_bytes) before the GEMM.
 hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st)
 {
-    if (a.K % 128 != 0 || !a.ws_scales) return hipErrorInvalidValue;
+    const bool fp4 = a.fmt_a == F8F6F4_E2M1 && a.fmt_b == F8F6F4_E2M1;
+    if (a.K % (fp4 ? 128 : 64) != 0 || !a.ws_scales) return hipErrorInvalidValue;
     const bool big = a.M >= 1024 && a.N >= 1024;
-    if (big) return launch_mx_tiled<256, 256, 4, 2, 4, 64>(a, st);
-    return launch_mx_tiled<64, 64, 2, 2, 4, 64>(a, st);
+    if (fp4) {
+        if (big) return launch_mx_tiled<256, 256, 4, 2, 4, 64, OP_MXFP4, 0>(a, st);
+        return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP4, 0>(a, st);
+    }
+    switch (a.fmt_a | (a.fmt_b << 3)) {
+    case F8F6F4_E4M3 | (F8F6F4_E4M3 << 3): return launch_mx_f8<F8F6F4_E4M3 | (F8F6F4_E4M3 << 3)>(a, st);
+    case F8F6F4_E5M2 | (F8F6F4_E5M2 << 3): return launch_mx_f8<F8F6F4_E5M2 | (F8F6F4_E5M2 << 3)>(a, st);
+    case F8F6F4_E4M3 | (F8F6F4_E5M2 << 3): return launch_mx_f8<F8F6F4_E4M3 | (F8F6F4_E5M2 << 3)>(a, st);
+    case F8F6F4_E5M2 | (F8F6F4_E4M3 << 3): return launch_mx_f8<F8F6F4_E5M2 | (F8F6F4_E4M3 << 3)>(a, st);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace ascq

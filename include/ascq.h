@@ -109,7 +109,12 @@ uint64_t ascq_pack_quant_pre(float m1, int32_t offset9, int32_t sign_flag);
  *  int8, int8, bf16,  int32   + SetQuantScalar/Vector -> QS322BF16_PRE / VQS322BF16_PRE
  *  int8, int8, int32, int32   (no quant)              -> raw int32 accumulators
  *  f16,  int8|int4, f16, f32  + SetAntiQuantScalar/Vector (weight-only, optional groups)
- *  fp4_e2m1, fp4_e2m1, bf16|f32 with E8M0 scales (SetTensorScaleA/B) -> MX block-scaled
+ *  fp8_e4m3|fp8_e5m2 (any mix), f16|bf16|f32, f32 bias
+ *                               (+ SetQuantScalar/Vector -> QF322F16 / QF322BF16 / QF322F32 _PRE; without a
+ *                               quant word a plain cast; quant_processor_fixpipe.h:101-115)
+ *  fp4_e2m1, fp4_e2m1, bf16|f32 with E8M0 scales (SetTensorScaleA/B) -> MX block-scaled (K % 128 == 0)
+ *  fp8_e4m3|fp8_e5m2 (any mix), bf16|f32 with E8M0 scales -> MX-FP8 (matmul_mx.asc:90-244; K % 64 == 0)
+ * int8 / fp8 A given [K, M] (isTransA) and a large [K, N] B are transposed into the workspace first.
  * ------------------------------------------------------------------------------------------ */
 typedef struct ascq_matmul_s* ascq_matmul_t;
 
@@ -153,7 +158,8 @@ ascq_status ascq_matmul_set_antiquant_vector(ascq_matmul_t h, const void* offset
  * scaleA: [M, sK] (transpose: [sK/2, M, 2]); scaleB: [sK/2, N, 2] (transpose: [N, sK]); sK = ceil(K/64)*2. */
 ascq_status ascq_matmul_set_tensor_scale_a(ascq_matmul_t h, const uint8_t* scale_a, int32_t is_transpose_scale_a);
 ascq_status ascq_matmul_set_tensor_scale_b(ascq_matmul_t h, const uint8_t* scale_b, int32_t is_transpose_scale_b);
-/* Optional device workspace for handles that need one (MX with a [K,N] B; W4/W8 with ND B):
+/* Optional device workspace for handles that need one (int8 / fp8 with isTransA or a large [K,N] B; MX;
+ * W4/W8 with ND B):
  * ascq_matmul_workspace_size() bytes.  Without it IterateAll allocates on first use. */
 ascq_status ascq_matmul_workspace_size(ascq_matmul_t h, size_t* bytes);
 ascq_status ascq_matmul_set_workspace(ascq_matmul_t h, void* workspace, size_t bytes);

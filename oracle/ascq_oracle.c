@@ -263,29 +263,56 @@ void oq_mm_dequant(const int32_t* acc, void* out, int out_type, int64_t M, int64
         }
 }
 
-/* fp8 operands: L0C is fp32 (matmul_utils.h:134-175), epilogue (V)QF322{F16,BF16,F32}_PRE
- * (quant_processor_fixpipe.h:101-115): out = cast(acc_f32 * M1).  The product sum is exact in double and
- * rounded once to fp32 here; the device accumulates in fp32, so this path is compared within a tolerance. */
-void oq_matmul_fp8(const uint8_t* A, const uint8_t* B, int a_fmt, int b_fmt, void* out, int out_type,
-                   int64_t M, int64_t N, int64_t K, int transA, int transB,
-                   const uint64_t* qvec, uint64_t qscalar, double* exact_out)
+/* fp8 operands: L0C is fp32 (matmul_utils.h:134-175); a float bias seeds L0C before the k loop (MmadCompute
+ * with isBias, mmad_compute.h:40-90; the fp8 sample adds a float [1, N] bias, matmul_fp8/scripts/gen_data.py
+ * tf_matmul + bias); the epilogue is (V)QF322{F16,BF16,F32}_PRE (quant_processor_fixpipe.h:101-115):
+ * out = cast((acc + bias) * M1), or a plain cast (F322F16 / F322BF16 / F32) when no quant word is set
+ * (quant_processor_utils.h:39-43).  The product sum is exact in double and rounded once to fp32 here; the
+ * device accumulates in fp32 and aligns the products of each 16-element K group to the group's largest one,
+ * so this path is compared within a tolerance built from sum |a b| (absdot_out) and the sum over 16-element
+ * K groups of the group's largest |a b| (blockmax_out; either output may be NULL).
+ * use_q: 1 when SetQuantScalar / SetQuantVector was called. */
+void oq_matmul_fp8(const uint8_t* A, const uint8_t* B, int a_fmt, int b_fmt, const float* bias, void* out,
+                   int out_type, int64_t M, int64_t N, int64_t K, int transA, int transB, int use_q,
+                   const uint64_t* qvec, uint64_t qscalar, double* exact_out, double* absdot_out,
+                   double* blockmax_out)
 {
     float ms = oq_quant_pre_m1(qscalar);
-    int use_q = (qvec != NULL) || (qscalar != 0);
+    /* B decoded once, [n][k] */
+    double* bd = (double*)malloc((size_t)(N * K) * sizeof(double));
+    if (!bd) return;
 #pragma omp parallel for schedule(static)
-    for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t k = 0; k < K; ++k) bd[n * K + k] = oq_fp8_decode(transB ? B[n * K + k] : B[k * N + n], b_fmt);
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m) {
+        double* arow = (double*)malloc((size_t)K * sizeof(double));
+        if (!arow) continue;
+        for (int64_t k = 0; k < K; ++k) arow[k] = oq_fp8_decode(transA ? A[k * M + m] : A[m * K + k], a_fmt);
         for (int64_t n = 0; n < N; ++n) {
-            double s = 0.0;
+            const double* bn = bd + n * K;
+            double s = 0.0, sa = 0.0, sb = 0.0, bmx = 0.0;
             for (int64_t k = 0; k < K; ++k) {
-                double a = oq_fp8_decode(transA ? A[k * M + m] : A[m * K + k], a_fmt);
-                double b = oq_fp8_decode(transB ? B[n * K + k] : B[k * N + n], b_fmt);
-                s += a * b;
+                double p = arow[k] * bn[k];
+                s += p;
+                sa += fabs(p);
+                if (fabs(p) > bmx) bmx = fabs(p);
+                if (k % 16 == 15 || k == K - 1) {
+                    sb += bmx;
+                    bmx = 0.0;
+                }
             }
+            if (bias) s += (double)bias[n];
             if (exact_out) exact_out[m * N + n] = s;
+            if (absdot_out) absdot_out[m * N + n] = sa;
+            if (blockmax_out) blockmax_out[m * N + n] = sb;
             float v = (float)s;
             if (use_q) v = v * (qvec ? oq_quant_pre_m1(qvec[n]) : ms);
             store_from_f32(out, out_type, m * N + n, v);
         }
+        free(arow);
+    }
+    free(bd);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -542,13 +569,19 @@ static inline float mx_elem(const uint8_t* p, int64_t idx, int fmt)
  * A [M,K]; B [K,N] (transB: [N,K]).  sK = ceil(K/64)*2 (gen_data.py:40).
  * scale_a_layout 0: scaleA [M, sK]; 1: [sK/2, M, 2].  scale_b_layout 0: scaleB [sK/2, N, 2] (the sample's
  * layout, gen_data.py:63 and README_en.md:64-66); 1: [N, sK].
- * rows != NULL restricts the computation to the listed rows (C rows not listed are untouched). */
+ * elem_fmt: element type of A (OQ_FP4_E2M1, OQ_FP8_E4M3, OQ_FP8_E5M2; fp8 elements are one per byte, the
+ * MX-FP8 sample matmul_mx/matmul_mx.asc:90-244); B uses elem_fmt >> 8 when that is nonzero, else elem_fmt.
+ * rows != NULL restricts the computation to the listed rows (C rows not listed are untouched).
+ * C_blockmax (may be NULL): per output, the sum over 16-element K groups of the group's largest |a b|. */
 void oq_mx_matmul(uint16_t* C, double* C_exact, double* C_absdot, const uint8_t* A, const uint8_t* B,
                   const uint8_t* scaleA, const uint8_t* scaleB, int64_t M, int64_t N, int64_t K, int transB,
-                  int scale_a_layout, int scale_b_layout, int elem_fmt, const int64_t* rows, int64_t n_rows)
+                  int scale_a_layout, int scale_b_layout, int elem_fmt, const int64_t* rows, int64_t n_rows,
+                  double* C_blockmax)
 {
     int64_t sK = (K + 63) / 64 * 2;
     int64_t nr = rows ? n_rows : M;
+    const int fmt_b = (elem_fmt >> 8) ? (elem_fmt >> 8) : elem_fmt;
+    elem_fmt &= 0xff;
 #pragma omp parallel for schedule(dynamic, 1)
     for (int64_t r = 0; r < nr; ++r) {
         int64_t m = rows ? rows[r] : r;
@@ -559,18 +592,24 @@ void oq_mx_matmul(uint16_t* C, double* C_exact, double* C_absdot, const uint8_t*
             arow[k] = (double)mx_elem(A, m * K + k, elem_fmt) * (double)oq_e8m0_decode(sa);
         }
         for (int64_t n = 0; n < N; ++n) {
-            double s = 0.0, sa_ = 0.0;
+            double s = 0.0, sa_ = 0.0, sbm = 0.0, bmx = 0.0;
             for (int64_t k = 0; k < K; ++k) {
                 int64_t kb = k / 32;
                 uint8_t sb = (scale_b_layout == 0 && OQ_MUTANT != 6) ? scaleB[(kb / 2) * N * 2 + n * 2 + (kb & 1)]
                                                                      : scaleB[n * sK + kb];
-                double b = (double)mx_elem(B, transB ? n * K + k : k * N + n, elem_fmt) * (double)oq_e8m0_decode(sb);
+                double b = (double)mx_elem(B, transB ? n * K + k : k * N + n, fmt_b) * (double)oq_e8m0_decode(sb);
                 double p = arow[k] * b;
                 s += p;
                 sa_ += fabs(p);
+                if (fabs(p) > bmx) bmx = fabs(p);
+                if (k % 16 == 15 || k == K - 1) {
+                    sbm += bmx;
+                    bmx = 0.0;
+                }
             }
             if (C_exact) C_exact[m * N + n] = s;
             if (C_absdot) C_absdot[m * N + n] = sa_;
+            if (C_blockmax) C_blockmax[m * N + n] = sbm;
             if (C) C[m * N + n] = oq_f64_to_bf16(s, 1);
         }
         free(arow);

@@ -71,9 +71,10 @@ void oq_matmul_i8(const int8_t* A, const int8_t* B, const int32_t* bias, int32_t
 void oq_mm_dequant(const int32_t* acc, void* out, int out_type, int64_t M, int64_t N,
                    const uint64_t* qvec, uint64_t qscalar);
 /* fp8 x fp8 -> fp32 accumulate (exact products, double sum) -> (V)QF322{F16,BF16,F32}_PRE */
-void oq_matmul_fp8(const uint8_t* A, const uint8_t* B, int a_fmt, int b_fmt, void* out, int out_type,
-                   int64_t M, int64_t N, int64_t K, int transA, int transB,
-                   const uint64_t* qvec, uint64_t qscalar, double* exact_out);
+void oq_matmul_fp8(const uint8_t* A, const uint8_t* B, int a_fmt, int b_fmt, const float* bias, void* out,
+                   int out_type, int64_t M, int64_t N, int64_t K, int transA, int transB, int use_q,
+                   const uint64_t* qvec, uint64_t qscalar, double* exact_out, double* absdot_out,
+                   double* blockmax_out);
 
 /* AscendQuant PER_TOKEN (policy API): q = sat_s8(round(f32(x)*scale[row] (+offset[row]))) */
 void oq_quant_per_token(int8_t* dst, const void* src, int src_type, const float* scale, const float* offset,
@@ -100,10 +101,12 @@ void oq_antiquant_matmul(uint16_t* y, double* y_exact, double* y_absdot, const u
 void oq_group_matmul(void* y, int out_type, const int8_t* x, const float* pts, const int8_t* w, int w_trans,
                      const float* scale, const int64_t* group_list, int list_type, int64_t G, int64_t M,
                      int64_t K, int64_t N);
-/* MX-FP4 block-scaled matmul, fp64 dequant-then-matmul (reference golden) -> bf16 (rne) */
+/* MX block-scaled matmul (E2M1 or fp8 elements; elem_fmt = A format | B format << 8, B defaulting to A's),
+ * fp64 dequant-then-matmul (reference golden) -> bf16 (rne) */
 void oq_mx_matmul(uint16_t* C, double* C_exact, double* C_absdot, const uint8_t* A, const uint8_t* B,
                   const uint8_t* scaleA, const uint8_t* scaleB, int64_t M, int64_t N, int64_t K, int transB,
-                  int scale_a_layout, int scale_b_layout, int elem_fmt, const int64_t* rows, int64_t n_rows);
+                  int scale_a_layout, int scale_b_layout, int elem_fmt, const int64_t* rows, int64_t n_rows,
+                  double* C_blockmax);
 /* MX quantisation of fp32 data along K: one e8m0 per 32 elements, E2M1 elements (used to make inputs) */
 void oq_mx_quantize_fp4(uint8_t* packed, uint8_t* scales, const float* x, int64_t R, int64_t K);
 

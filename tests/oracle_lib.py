@@ -53,6 +53,8 @@ def lib() -> ctypes.CDLL:
             "oq_fp8_decode": (ctypes.c_float, [ctypes.c_uint8, ctypes.c_int]),
             "oq_matmul_i8": (None, [_P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int]),
             "oq_mm_dequant": (None, [_P, _P, ctypes.c_int, _I64, _I64, _P, ctypes.c_uint64]),
+            "oq_matmul_fp8": (None, [_P, _P, ctypes.c_int, ctypes.c_int, _P, _P, ctypes.c_int, _I64, _I64, _I64,
+                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, ctypes.c_uint64, _P, _P, _P]),
             "oq_quant_per_token": (None, [_P, _P, ctypes.c_int, _P, _P, _I64, _I64, ctypes.c_int]),
             "oq_quant_dynamic_per_token": (None, [_P, _P, _P, ctypes.c_int, _I64, _I64, ctypes.c_int]),
             "oq_quant_legacy_f16": (None, [_P, _P, ctypes.c_int, _P, ctypes.c_uint16, _P, ctypes.c_uint16, _I64, _I64]),
@@ -65,7 +67,7 @@ def lib() -> ctypes.CDLL:
             "oq_group_matmul": (None, [_P, ctypes.c_int, _P, _P, _P, ctypes.c_int, _P, _P, ctypes.c_int, _I64, _I64,
                                        _I64, _I64]),
             "oq_mx_matmul": (None, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int,
-                                    ctypes.c_int, ctypes.c_int, _P, _I64]),
+                                    ctypes.c_int, ctypes.c_int, _P, _I64, _P]),
             "oq_mx_quantize_fp4": (None, [_P, _P, _P, _I64, _I64]),
         }
         for name, (res, args) in sig.items():
@@ -100,6 +102,26 @@ def matmul_i8(A, B, bias=None, trans_a=False, trans_b=False):
     b = None if bias is None else np.ascontiguousarray(bias, np.int32)
     lib().oq_matmul_i8(_p(A), _p(B), _p(b), _p(C), M, N, K, int(trans_a), int(trans_b))
     return C
+
+
+def matmul_fp8(A, B, a_fmt, b_fmt, bias=None, out_type=F32, trans_a=False, trans_b=False, use_q=False, qvec=None,
+               qscalar=0):
+    """fp8 Matmul (bytes in, fp8 codes FP8_E4M3 / FP8_E5M2): returns (out, exact fp64 sum + bias, sum |a b|,
+    sum over 16-element K groups of the group's largest |a b|)."""
+    A = np.ascontiguousarray(A, np.uint8)
+    B = np.ascontiguousarray(B, np.uint8)
+    M = A.shape[1] if trans_a else A.shape[0]
+    K = A.shape[0] if trans_a else A.shape[1]
+    N = B.shape[0] if trans_b else B.shape[1]
+    out = np.empty((M, N), np.float32 if out_type == F32 else np.uint16)
+    exact = np.empty((M, N), np.float64)
+    absd = np.empty((M, N), np.float64)
+    bmax = np.empty((M, N), np.float64)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    qv = None if qvec is None else np.ascontiguousarray(qvec, np.uint64)
+    lib().oq_matmul_fp8(_p(A), _p(B), a_fmt, b_fmt, _p(b), _p(out), out_type, M, N, K, int(trans_a), int(trans_b),
+                        int(use_q), _p(qv), int(qscalar), _p(exact), _p(absd), _p(bmax))
+    return out, exact, absd, bmax
 
 
 def mm_dequant(acc, out_type=F16, qvec=None, qscalar=0):
@@ -188,7 +210,10 @@ def group_matmul(x, pts, w, scale, group_list, list_type, G, M, K, N, out_type=B
     return y
 
 
-def mx_matmul(A, B, sA, sB, M, N, K, trans_b=False, sa_layout=0, sb_layout=0, elem_fmt=FP4_E2M1, rows=None):
+def mx_matmul(A, B, sA, sB, M, N, K, trans_b=False, sa_layout=0, sb_layout=0, elem_fmt=FP4_E2M1, rows=None,
+              fmt_b=None, blockmax=False):
+    """returns (bf16 C, exact fp64 C, sum |a b|) and, with blockmax=True, the sum over 16-element K groups of
+    the group's largest |a b| as a fourth array"""
     A = np.ascontiguousarray(A, np.uint8)
     B = np.ascontiguousarray(B, np.uint8)
     sA = np.ascontiguousarray(sA, np.uint8)
@@ -196,10 +221,11 @@ def mx_matmul(A, B, sA, sB, M, N, K, trans_b=False, sa_layout=0, sb_layout=0, el
     C = np.zeros((M, N), np.uint16)
     Ce = np.zeros((M, N), np.float64)
     Ca = np.zeros((M, N), np.float64)
+    Cb = np.zeros((M, N), np.float64) if blockmax else None
     r = None if rows is None else np.ascontiguousarray(rows, np.int64)
     lib().oq_mx_matmul(_p(C), _p(Ce), _p(Ca), _p(A), _p(B), _p(sA), _p(sB), M, N, K, int(trans_b), sa_layout,
-                       sb_layout, elem_fmt, _p(r), 0 if r is None else r.size)
-    return C, Ce, Ca
+                       sb_layout, elem_fmt | ((fmt_b or 0) << 8), _p(r), 0 if r is None else r.size, _p(Cb))
+    return (C, Ce, Ca, Cb) if blockmax else (C, Ce, Ca)
 
 
 def mx_quantize_fp4(x):

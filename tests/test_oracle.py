@@ -412,8 +412,105 @@ def test_mx_quantize_fp4_roundtrip():
     p, s = O.mx_quantize_fp4(x)
     table = np.array([E2M1[c & 7] * (-1 if c & 8 else 1) for c in range(16)])
     v = table[np.stack([p & 0xF, p >> 4], -1).reshape(16, 256)] * 2.0 ** (np.repeat(s, 32, 1).astype(np.float64) - 127)
-    # every block max lands within the E2M1 range after scaling and the relative error is bounded by the
-    # coarsest E2M1 spacing (half of 2 at magnitude 4..6 -> 1/4 of the block scale * 4)
-    blk = np.abs(x.reshape(16, 8, 32)).max(-1)
-    assert (blk / 2.0 ** (s.astype(np.float64) - 127) < 8).all()
-    assert np.abs(v - x).max() <= (2.0 ** (s.astype(np.float64) - 127)).max()
+    # the shared exponent puts every block max at 4 <= |x| / scale < 8; E2M1 spacing is at most 2 (between 4
+    # and 6), so an element inside the E2M1 range is off by at most one scale unit, and one clamped from
+    # [6, 8) to 6 by less than two
+    scale = 2.0 ** (np.repeat(s, 32, 1).astype(np.float64) - 127)
+    blk = np.abs(x.reshape(16, 8, 32)).max(-1) / 2.0 ** (s.astype(np.float64) - 127)
+    assert ((blk >= 4) & (blk < 8)).all()
+    err = np.abs(v - x)
+    inside = np.abs(x) / scale <= 6
+    assert (err[inside] <= scale[inside]).all()
+    assert (err < 2 * scale).all()
+
+
+# --------------------------------------------------------------------------- fp8 operand Matmul / MX-FP8
+_T8 = {O.FP8_E4M3: torch.float8_e4m3fn, O.FP8_E5M2: torch.float8_e5m2}
+
+
+def fp8_bytes(rng, shape, fmt, lo=0, hi=256):
+    """random fp8 codes without NaN / inf (e4m3fn: S.1111.111 is NaN; e5m2: exponent 31 is inf / NaN)"""
+    c = rng.integers(lo, hi, shape, dtype=np.int64).astype(np.uint8)
+    bad = (c & 0x7F) == 0x7F if fmt == O.FP8_E4M3 else (c & 0x7C) == 0x7C
+    return np.where(bad, c & 0x80, c).astype(np.uint8)
+
+
+def torch_decode(codes, fmt):
+    return torch.from_numpy(np.ascontiguousarray(codes)).view(_T8[fmt]).to(torch.float64).numpy()
+
+
+@pytest.mark.parametrize("fa,fb", [(O.FP8_E4M3, O.FP8_E4M3), (O.FP8_E5M2, O.FP8_E5M2), (O.FP8_E4M3, O.FP8_E5M2),
+                                   (O.FP8_E5M2, O.FP8_E4M3)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, True), (False, True)])
+def test_matmul_fp8_vs_torch_decode(fa, fb, ta, tb):
+    """exact sum vs torch's float8 decode and a float64 matmul; bias enters once, in the fp64 sum"""
+    M, N, K = 9, 13, 70
+    rng = np.random.default_rng(801)
+    A = fp8_bytes(rng, (K, M) if ta else (M, K), fa)
+    B = fp8_bytes(rng, (N, K) if tb else (K, N), fb)
+    bias = rng.standard_normal(N).astype(np.float32)
+    _, exact, absd, bmax = O.matmul_fp8(A, B, fa, fb, bias=bias, trans_a=ta, trans_b=tb)
+    a = torch_decode(A, fa)
+    b = torch_decode(B, fb)
+    a = a.T if ta else a
+    b = b.T if tb else b
+    ref = a @ b
+    assert np.allclose(exact, ref + bias.astype(np.float64), rtol=0, atol=1e-12 * np.abs(a) @ np.abs(b) + 1e-30)
+    assert np.allclose(absd, np.abs(a) @ np.abs(b), rtol=1e-13, atol=0)
+    P = np.abs(a[:, :, None] * b[None, :, :])  # [M, K, N]
+    ref_bmax = sum(P[:, h:h + 16, :].max(1) for h in range(0, K, 16))  # K = 70: groups of 16 x 4, 6
+    assert np.allclose(bmax, ref_bmax, rtol=1e-15, atol=0)
+
+
+@pytest.mark.parametrize("out_type,tdt", [(O.F16, torch.float16), (O.BF16, torch.bfloat16), (O.F32, torch.float32)])
+def test_matmul_fp8_epilogue_vs_torch(out_type, tdt):
+    """QF322{F16,BF16,F32}_PRE: fp32(acc + bias) * M1 (M1 = the word's bits 13..31) then torch's rne cast;
+    without a quant word the plain cast; per-channel words pick column n"""
+    M, N, K = 6, 20, 64
+    rng = np.random.default_rng(802)
+    A = fp8_bytes(rng, (M, K), O.FP8_E4M3, 0, 120)
+    B = fp8_bytes(rng, (K, N), O.FP8_E4M3, 0, 120)
+    bias = rng.standard_normal(N).astype(np.float32)
+    words = np.array([O.lib().oq_pack_quant_pre(float(v), 0, 0) | 0x1FFF for v in rng.uniform(0.01, 2.0, N)],
+                     np.uint64)
+    m1 = (words.astype(np.uint64) & np.uint64(0xFFFFE000)).astype(np.uint32).view(np.float32)
+
+    def as_f64(out):
+        if out_type == O.F32:
+            return out.astype(np.float64)
+        return torch.from_numpy(out.view(np.int16)).view(tdt).to(torch.float64).numpy()
+
+    for use_q, qvec in [(False, None), (True, words)]:
+        out, exact, _, _ = O.matmul_fp8(A, B, O.FP8_E4M3, O.FP8_E4M3, bias=bias, out_type=out_type, use_q=use_q,
+                                     qvec=qvec)
+        v = exact.astype(np.float32)
+        if use_q:
+            v = (v * m1[None, :]).astype(np.float32)
+        exp = torch.from_numpy(v).to(tdt).to(torch.float64).numpy()
+        if out_type == O.F16:
+            exp = np.clip(exp, -65504.0, 65504.0)  # the fixpipe cast saturates
+        assert np.array_equal(as_f64(out), exp)
+    # scalar word: column-independent M1
+    out, exact, _, _ = O.matmul_fp8(A, B, O.FP8_E4M3, O.FP8_E4M3, out_type=O.F32, use_q=True, qscalar=int(words[3]))
+    assert np.array_equal(out, (exact.astype(np.float32) * m1[3]).astype(np.float32))
+
+
+@pytest.mark.parametrize("fa,fb", [(O.FP8_E4M3, O.FP8_E4M3), (O.FP8_E5M2, O.FP8_E4M3)])
+def test_mx_matmul_fp8_vs_torch_decode(fa, fb):
+    """MX-FP8: elements decoded by torch, scales 2^(e-127) per 32 K, both scale layouts of the sample"""
+    M, N, K = 5, 7, 128
+    rng = np.random.default_rng(803)
+    A = fp8_bytes(rng, (M, K), fa)
+    B = fp8_bytes(rng, (K, N), fb)
+    sK = K // 32
+    sA = rng.integers(115, 135, (M, sK), dtype=np.uint8)
+    sB = rng.integers(115, 135, (N, sK), dtype=np.uint8)
+    a = torch_decode(A, fa) * 2.0 ** (np.repeat(sA.astype(np.float64), 32, 1) - 127)
+    b = torch_decode(B, fb) * 2.0 ** (np.repeat(sB.astype(np.float64), 32, 1).T - 127)
+    sB_pairs = np.ascontiguousarray(sB.T.reshape(sK // 2, 2, N).transpose(0, 2, 1))  # [sK/2, N, 2]
+    _, Ce, Ca, Cb = O.mx_matmul(A, B, sA, sB_pairs, M, N, K, trans_b=False, sa_layout=0, sb_layout=0, elem_fmt=fa,
+                                fmt_b=fb, blockmax=True)
+    assert np.allclose(Ce, a @ b, rtol=0, atol=1e-12 * (np.abs(a) @ np.abs(b)))
+    assert np.allclose(Ca, np.abs(a) @ np.abs(b), rtol=1e-13, atol=0)
+    P = np.abs(a[:, :, None] * b[None, :, :])
+    assert np.allclose(Cb, sum(P[:, h:h + 16, :].max(1) for h in range(0, K, 16)), rtol=1e-15, atol=0)
