@@ -6,11 +6,11 @@ algorithmic GB/s (6*M*N + 8*M bytes per step).  Buffers are rotated over more th
 the figure is HBM, not MALL, bandwidth.
 
 Also measured and reported under "other_configs": the W8A8 int8 Matmul + per-channel DEQF16 (128x512x256 and the
-8192^3 throughput shape), the W4A16 / W8A16 decode GEMV (M in {1, 16, 64}), the MoE group matmul and the MX-FP4
-8192^3 GEMM.
+8192^3 throughput shape), the W4A16 / W8A16 decode GEMV (M in {1, 16, 64}), the MoE group matmul (both weight
+layouts), the MX-FP4 8192^3 GEMM and the fp8 / MX-FP8 8192^3 GEMMs.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                  [--only all|headline|w8a8|gemv|group|mx|traffic]
+                  [--only all|headline|w8a8|gemv|group|mx|fp8|traffic]
 """
 from __future__ import annotations
 
@@ -30,6 +30,7 @@ METRIC = "int8/MXFP4 GEMM TOPS (%MFMA peak); antiquant GEMV + quant op HBM GB/s 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0      # dense int8 MFMA, MI355X
 MXFP4_PEAK_TFLOPS = 10100.0  # dense fp4 MFMA, MI355X
+FP8_PEAK_TFLOPS = 5000.0     # dense fp8 MFMA, MI355X
 F16_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 * 2 ** 20
 
@@ -273,6 +274,62 @@ def bench_mx(torch, ascq, iters, trans_b=True):
                 ms=ms, value=tf, unit="TFLOPS", frac_of_peak=tf / MXFP4_PEAK_TFLOPS)
 
 
+def _fp8_bytes(torch, shape, g, dt):
+    """N(0, 1) cast to fp8 (no NaN codes), as raw bytes"""
+    return torch.randn(shape, generator=g, device="cuda").to(dt).view(torch.uint8)
+
+
+def bench_fp8(torch, ascq, iters, trans_b=True):
+    """fp8 e4m3 x e4m3 Matmul 8192^3, fp32 accumulation, per-channel QF322BF16_PRE -> bf16"""
+    M = N = K = 8192
+    g = torch.Generator(device="cuda")
+    g.manual_seed(6)
+    A = _fp8_bytes(torch, (M, K), g, torch.float8_e4m3fn)
+    B = _fp8_bytes(torch, (N, K) if trans_b else (K, N), g, torch.float8_e4m3fn)
+    words = torch.full((N,), 0x3C000000, dtype=torch.int64, device="cuda")  # M1 = 2^-7
+    C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    mm = ascq.Matmul(ascq.FP8_E4M3, ascq.FP8_E4M3, ascq.BF16)
+    mm.SetOrgShape(M, N, K)
+    mm.SetTensorA(A)
+    mm.SetTensorB(B, trans_b)
+    mm.SetQuantVector(words)
+
+    def fn(i):
+        mm.IterateAll(C)
+
+    ms = _time_loop(torch, fn, iters, warmup=2)
+    tf = 2 * M * N * K / (ms * 1e-3) / 1e12
+    return dict(workload=f"fp8 e4m3 Matmul {M}x{N}x{K}, fp32 acc, per-channel QF322BF16_PRE -> bf16, B given "
+                         + ("[N,K] (isTransposeB)" if trans_b else "[K,N] (transposed into the workspace)"),
+                ms=ms, value=tf, unit="TFLOPS", frac_of_peak=tf / FP8_PEAK_TFLOPS)
+
+
+def bench_mxfp8(torch, ascq, iters):
+    """MX-FP8 (e4m3 elements, E8M0 per 32 K) GEMM 8192^3 -> bf16"""
+    M = N = K = 8192
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    A = _fp8_bytes(torch, (M, K), g, torch.float8_e4m3fn)
+    B = _fp8_bytes(torch, (N, K), g, torch.float8_e4m3fn)
+    sA = torch.randint(124, 129, (M, K // 32), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8)
+    sB = torch.randint(124, 129, (N, K // 32), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8)
+    C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    mm = ascq.Matmul(ascq.FP8_E4M3, ascq.FP8_E4M3, ascq.BF16, 0, ascq.E8M0)
+    mm.SetOrgShape(M, N, K)
+    mm.SetTensorA(A)
+    mm.SetTensorB(B, True)
+    mm.SetTensorScaleA(sA, False)
+    mm.SetTensorScaleB(sB, True)
+
+    def fn(i):
+        mm.IterateAll(C)
+
+    ms = _time_loop(torch, fn, iters, warmup=2)
+    tf = 2 * M * N * K / (ms * 1e-3) / 1e12
+    return dict(workload=f"MX-FP8 e4m3/E8M0 GEMM {M}x{N}x{K}, fp32 acc, bf16 out, B given [N,K]",
+                ms=ms, value=tf, unit="TFLOPS", frac_of_peak=tf / FP8_PEAK_TFLOPS)
+
+
 def traffic_probe(torch, ascq):
     """One launch each of a plain 256 MiB copy (the calibration for FETCH_SIZE / WRITE_SIZE), the dynamic
     quant kernel and the dequant kernel on the 8192 x 8192 f16 workload, with a 1 GiB fill between them so
@@ -298,12 +355,14 @@ OTHER = {
              for w in ("INT4", "INT8") for m in (1, 16, 64)],
     "group": [lambda t, a: bench_group(t, a, 20, True), lambda t, a: bench_group(t, a, 20, False)],
     "mx": [lambda t, a: bench_mx(t, a, 10, True), lambda t, a: bench_mx(t, a, 5, False)],
+    "fp8": [lambda t, a: bench_fp8(t, a, 10, True), lambda t, a: bench_fp8(t, a, 5, False),
+            lambda t, a: bench_mxfp8(t, a, 10)],
 }
 
 
 def run_others(torch, ascq, which):
     out = []
-    for key in (["w8a8", "gemv", "group", "mx"] if which == "all" else [which]):
+    for key in (["w8a8", "gemv", "group", "mx", "fp8"] if which == "all" else [which]):
         for fn in OTHER[key]:
             try:
                 r = fn(torch, ascq)
@@ -320,7 +379,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="all", choices=["all", "headline", "w8a8", "gemv", "group", "mx", "traffic"],
+    ap.add_argument("--only", default="all",
+                    choices=["all", "headline", "w8a8", "gemv", "group", "mx", "fp8", "traffic"],
                     help="run one workload family (the JSON contract line is printed for all / headline)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -336,7 +396,7 @@ def main() -> int:
     if args.only == "traffic":
         print(json.dumps(traffic_probe(torch, ascq)))
         return 0
-    if args.only in ("w8a8", "gemv", "group", "mx"):
+    if args.only in ("w8a8", "gemv", "group", "mx", "fp8"):
         print(json.dumps({"other_configs": run_others(torch, ascq, args.only)}))
         return 0
     h = bench_headline(torch, ascq, args.steps, args.warmup)
