@@ -59,6 +59,43 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_floa
 // QUANT_PRE word -> M1 multiplier: bits [31:13] as fp32, low 13 bits cleared
 __device__ __forceinline__ float quant_pre_m1(uint64_t w) { return __uint_as_float((uint32_t)w & 0xFFFFE000u); }
 
+// (V)REQ8 / (V)QF322B8_PRE after the multiply by M1 (examples/02_simd_c_api/03_c_api/03_matrix_compute/
+// asc_copy_l0c2gm/scripts/gen_data_s322s8.py:56-80): NaN -> 0, clamp to [-256, 255], round half to even, add
+// the word's 9-bit offset (bits 37-45, 0..511), saturate to int8 when the sign flag (bit 46) is set, else to
+// uint8.  Bits 32-36 (shift, mode control) are ignored, as on arch 3510.
+__device__ __forceinline__ uint8_t requant8(float v, uint64_t w)
+{
+    if (v != v) v = 0.0f;  // fmaxf would turn NaN into -256
+    const float c = fminf(fmaxf(v, -256.0f), 255.0f);
+    const int t = (int)__builtin_rintf(c) + (int)((w >> 37) & 0x1FFu);
+    if ((w >> 46) & 1u) return (uint8_t)(int8_t)(t < -128 ? -128 : (t > 127 ? 127 : t));
+    return (uint8_t)(t < 0 ? 0 : (t > 255 ? 255 : t));
+}
+
+// f32 -> fp8 with round to nearest even, on the bit pattern.  e4m3fn (fmt 0) saturates as the fixpipe's default
+// mode does: |x| >= 448 and +-inf give +-448, NaN gives 0.  e5m2 (fmt 1): overflow (|x| >= 61440) gives +-inf,
+// NaN gives 0x7F.  Normal results: add the rounding bias below the kept mantissa bits (half minus one, plus the
+// kept LSB for ties to even) and shift; subnormal results: scale to the subnormal step and rint.
+__device__ __forceinline__ uint8_t f32_to_fp8(float x, int fmt)
+{
+    const uint32_t u = __float_as_uint(x);
+    const uint32_t sign = (u >> 24) & 0x80u, a = u & 0x7FFFFFFFu;
+    if (fmt == 0) {
+        if (a > 0x7F800000u) return 0;
+        if (a >= 0x43E00000u) return (uint8_t)(sign | 0x7Eu);  // 448
+        if (a < 0x3C800000u)                                   // below 2^-6: multiples of 2^-9
+            return (uint8_t)(sign | (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f));
+        const uint32_t r = (a + 0x7FFFFu + ((a >> 20) & 1u)) >> 20;
+        return (uint8_t)(sign | (r - (120u << 3)));
+    }
+    if (a > 0x7F800000u) return 0x7Fu;
+    if (a >= 0x47700000u) return (uint8_t)(sign | 0x7Cu);     // 61440 rounds to inf
+    if (a < 0x38800000u)                                       // below 2^-14: multiples of 2^-16
+        return (uint8_t)(sign | (uint32_t)__builtin_rintf(__uint_as_float(a) * 65536.0f));
+    const uint32_t r = (a + 0xFFFFFu + ((a >> 21) & 1u)) >> 21;
+    return (uint8_t)(sign | (r - (112u << 2)));
+}
+
 // RoundMode to integral float
 __device__ __forceinline__ float round_mode_f(float v, int mode)
 {

@@ -5,7 +5,9 @@
 // QF322F16_PRE / QF322BF16_PRE / QF322F32_PRE epilogue (stage/copy_cube_out/quant/quant_processor_fixpipe.h:101-115,
 // mode rules quant_processor_utils.h:39-43):
 //   out = cast((acc + bias[n]) * M1)   with M1 from SetQuantScalar / SetQuantVector (QUANT_PRE bits [31:13]),
-//   out = cast(acc + bias[n])          without a quant word (F322F16 / F322BF16 / F32).
+//   out = cast(acc + bias[n])          without a quant word (F322F16 / F322BF16 / F32);
+// int8 / uint8 C is (V)QF322B8_PRE (requant8: clamp, rint, + the word's offset, saturate by its sign flag) and
+// fp8 C is (V)QF322FP8_PRE (f32_to_fp8: rne, e4m3 saturating at 448), both with a quant word.
 // The float bias seeds the accumulator in the reference (MmadCompute with isBias, mmad_compute.h:40-90); adding
 // it to the finished fp32 sum differs only by fp32 rounding.
 //
@@ -42,11 +44,14 @@ __device__ __forceinline__ float fp8_to_f32(uint8_t v, int fmt)
     return __uint_as_float(s | ((e + 112u) << 23) | (m << 21));
 }
 
-__device__ __forceinline__ void store_f8_out(void* C, int c_type, int64_t o, float v)
+// w: the column's QUANT_PRE word (offset and sign flag of QF322B8)
+__device__ __forceinline__ void store_f8_out(void* C, int c_type, int64_t o, float v, uint64_t w)
 {
     if (c_type == DT_F32) ((float*)C)[o] = v;
     else if (c_type == DT_F16) ((uint16_t*)C)[o] = f32_to_f16_sat(v);
-    else ((uint16_t*)C)[o] = f32_to_bf16_sat(v);
+    else if (c_type == DT_BF16) ((uint16_t*)C)[o] = f32_to_bf16_sat(v);
+    else if (c_type == DT_INT8 || c_type == DT_UINT8) ((uint8_t*)C)[o] = requant8(v, w);
+    else ((uint8_t*)C)[o] = f32_to_fp8(v, c_type == DT_FP8_E5M2 ? 1 : 0);
 }
 
 template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT>
@@ -79,7 +84,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
         const int64_t col = n0 + T::frag_col(wn, j, lane);
         if (col >= p.N) continue;
         const float bias = p.bias ? p.bias[col] : 0.0f;
-        const float m1 = p.qvec ? quant_pre_m1(p.qvec[col]) : mscalar;
+        const uint64_t w = p.qvec ? p.qvec[col] : p.qscalar;
+        const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
 #pragma unroll
         for (int i = 0; i < T::FM; ++i) {
 #pragma unroll
@@ -89,7 +95,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
                 float v = acc[i][j][r];
                 if (p.bias) v = v + bias;
                 if (p.use_quant) v = v * m1;
-                store_f8_out(p.C, p.c_type, row * p.ldc + col, v);
+                store_f8_out(p.C, p.c_type, row * p.ldc + col, v, w);
             }
         }
     }
@@ -109,8 +115,9 @@ __global__ __launch_bounds__(256) void gemm_f8_generic_kernel(GemmF8Args p)
             acc = acc + a * b;  // the product of two fp8 values is exact in fp32
         }
         if (p.bias) acc = acc + p.bias[n];
-        if (p.use_quant) acc = acc * (p.qvec ? quant_pre_m1(p.qvec[n]) : mscalar);
-        store_f8_out(p.C, p.c_type, m * p.ldc + n, acc);
+        const uint64_t w = p.qvec ? p.qvec[n] : p.qscalar;
+        if (p.use_quant) acc = acc * (p.qvec ? quant_pre_m1(w) : mscalar);
+        store_f8_out(p.C, p.c_type, m * p.ldc + n, acc, w);
     }
 }
 

@@ -1,13 +1,14 @@
-// gemm_i8.hip -- int8 x int8 -> int32 GEMM on CDNA4 MFMA with the fixpipe dequant fused in the epilogue.
+// gemm_i8.hip -- int8 x int8 -> int32 GEMM on CDNA4 MFMA with the fixpipe dequant / requant fused in the epilogue.
 //
 // Replaces the adv_api Matmul quant scenario (impl/adv_api/detail/matmul/matmul_impl.h:119-137 IterateAll;
 // stage/compute/mmad_compute.h:40-90 Mmad int8 -> int32 L0C; stage/copy_cube_out/copy_cube_out_fixpipe.h:339-357
-// and quant/quant_processor_fixpipe.h:74-234 for the DEQF16 / QS322BF16_PRE epilogue).
+// and quant/quant_processor_fixpipe.h:74-234 for the DEQF16 / QS322BF16_PRE / REQ8 epilogues).
 //
 // gfx950 design: the v_mfma_i32_32x32x32_i8 main loop of gemm_core.h (a ring of LDS stages filled by
 // global->LDS buffer copies, XOR-swizzled LDS, in-flight byte transpose of a row-major [K, N] B), XCD-aware
 // tile order, and the fixpipe epilogue in registers:
-//   acc (+ int32 bias) -> f32 (rne) x M1[n] -> f16 / bf16 (rne, saturating); M1 = QUANT_PRE bits [31:13]
+//   acc (+ int32 bias) -> f32 (rne) x M1[n] -> f16 / bf16 (rne, saturating), or -> requant8 (int8 / uint8 C:
+//   clamp, rint, + offset, saturate by the word's sign flag); M1 = QUANT_PRE bits [31:13]
 //   (accompanying_quantization.md:79-103).
 #include "common.h"
 #include "gemm_core.h"
@@ -46,7 +47,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
         const int64_t col = n0 + T::frag_col(wn, j, lane);
         if (col >= p.N) continue;
         const int32_t bias = p.bias ? p.bias[col] : 0;
-        const float m1 = p.qvec ? quant_pre_m1(p.qvec[col]) : mscalar;
+        const uint64_t w = p.qvec ? p.qvec[col] : p.qscalar;
+        const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
 #pragma unroll
         for (int i = 0; i < T::FM; ++i) {
 #pragma unroll
@@ -57,7 +59,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
                 const int64_t o = row * p.ldc + col;
                 if (p.epi == EPI_I32) ((int32_t*)p.C)[o] = v;
                 else if (p.epi == EPI_DEQ_F16) ((uint16_t*)p.C)[o] = f32_to_f16_sat((float)v * m1);
-                else ((uint16_t*)p.C)[o] = f32_to_bf16_sat((float)v * m1);
+                else if (p.epi == EPI_DEQ_BF16) ((uint16_t*)p.C)[o] = f32_to_bf16_sat((float)v * m1);
+                else ((uint8_t*)p.C)[o] = requant8((float)v * m1, w);
             }
         }
     }
@@ -162,11 +165,13 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(GemmI8Args p)
             acc += (uint32_t)(a * b);
         }
         const int32_t v = (int32_t)(acc + (uint32_t)(p.bias ? p.bias[n] : 0));
-        const float m1 = p.qvec ? quant_pre_m1(p.qvec[n]) : mscalar;
+        const uint64_t w = p.qvec ? p.qvec[n] : p.qscalar;
+        const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
         const int64_t o = m * p.ldc + n;
         if (p.epi == EPI_I32) ((int32_t*)p.C)[o] = v;
         else if (p.epi == EPI_DEQ_F16) ((uint16_t*)p.C)[o] = f32_to_f16_sat((float)v * m1);
-        else ((uint16_t*)p.C)[o] = f32_to_bf16_sat((float)v * m1);
+        else if (p.epi == EPI_DEQ_BF16) ((uint16_t*)p.C)[o] = f32_to_bf16_sat((float)v * m1);
+        else ((uint8_t*)p.C)[o] = requant8((float)v * m1, w);
     }
 }
 

@@ -23,7 +23,7 @@ hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_ty
                             hipStream_t st);
 
 // gemm_i8.hip
-enum : int { EPI_I32 = 0, EPI_DEQ_F16 = 1, EPI_DEQ_BF16 = 2 };
+enum : int { EPI_I32 = 0, EPI_DEQ_F16 = 1, EPI_DEQ_BF16 = 2, EPI_REQ8 = 3 };
 struct GemmI8Args {
     const int8_t* A;      // [M, K] row-major (lda), or [K, M] when trans_a
     const int8_t* B;      // [K, N] row-major (ldb), or [N, K] when trans_b
@@ -47,7 +47,7 @@ struct GemmF8Args {
     const uint64_t* qvec; // per-channel QUANT_PRE words [N] or null
     uint64_t qscalar;
     int use_quant;        // 1: multiply by M1 (SetQuantScalar / SetQuantVector was called)
-    int c_type;           // DT_F16 / DT_BF16 / DT_F32
+    int c_type;           // DT_F16 / DT_BF16 / DT_F32; DT_INT8 / DT_UINT8 (QF322B8); DT_FP8_E4M3 / _E5M2 (QF322FP8)
     int fmt_a, fmt_b;     // f8f6f4 codes: 0 e4m3fn, 1 e5m2
     int trans_a, trans_b;
 };

@@ -108,10 +108,15 @@ uint64_t ascq_pack_quant_pre(float m1, int32_t offset9, int32_t sign_flag);
  *  int8, int8, f16,   int32   + SetQuantScalar/Vector -> DEQF16 / VDEQF16
  *  int8, int8, bf16,  int32   + SetQuantScalar/Vector -> QS322BF16_PRE / VQS322BF16_PRE
  *  int8, int8, int32, int32   (no quant)              -> raw int32 accumulators
+ *  int8, int8, int8|uint8, int32 + SetQuantScalar/Vector -> REQ8 / VREQ8: sat8(rint(clamp(f32(acc) * M1,
+ *                               -256, 255)) + offset), the word's sign flag picking int8 or uint8 saturation
+ *                               (quant_processor_fixpipe.h:93-94, 211-212)
  *  f16,  int8|int4, f16, f32  + SetAntiQuantScalar/Vector (weight-only, optional groups)
  *  fp8_e4m3|fp8_e5m2 (any mix), f16|bf16|f32, f32 bias
  *                               (+ SetQuantScalar/Vector -> QF322F16 / QF322BF16 / QF322F32 _PRE; without a
  *                               quant word a plain cast; quant_processor_fixpipe.h:101-115)
+ *  fp8, fp8, int8|uint8 + SetQuantScalar/Vector -> QF322B8_PRE (as REQ8 on the fp32 accumulator)
+ *  fp8, fp8, fp8_e4m3|fp8_e5m2 + SetQuantScalar/Vector -> QF322FP8_PRE (rne; e4m3 saturates at +-448, NaN -> 0)
  *  fp4_e2m1, fp4_e2m1, bf16|f32 with E8M0 scales (SetTensorScaleA/B) -> MX block-scaled (K % 128 == 0)
  *  fp8_e4m3|fp8_e5m2 (any mix), bf16|f32 with E8M0 scales -> MX-FP8 (matmul_mx.asc:90-244; K % 64 == 0)
  * int8 / fp8 A given [K, M] (isTransA) and a large [K, N] B are transposed into the workspace first.

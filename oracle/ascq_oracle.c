@@ -192,6 +192,55 @@ float oq_fp8_decode(uint8_t v, int fmt)
     return s ? -r : r;
 }
 
+/* f32 -> fp8, round to nearest even, by nearest search over the format's finite values (ties: the code with the
+ * even mantissa, i.e. the even code).  e4m3fn follows the fixpipe's default saturation mode
+ * (docs/zh/api/appendix/matrix_compute_move_out_interface_boundary_value_summary.md:23, 65-67, 87): |x| >= 448
+ * and +-inf give +-448, NaN gives 0.  e5m2 is not under that control (same file :28): overflow rounds to +-inf
+ * (|x| >= 61440, the midpoint above the largest finite 57344), NaN stays NaN (0x7F). */
+uint8_t oq_f32_to_fp8(float x, int fmt)
+{
+    const int e4 = fmt == OQ_FP8_E4M3;
+    const uint8_t sign = signbit(x) ? 0x80 : 0x00;
+    if (isnan(x)) return e4 ? 0x00 : 0x7F;
+    float a = fabsf(x);
+    const int top = e4 ? 0x7E : 0x7B; /* largest finite magnitude code */
+    if (e4 && a >= 448.0f) return (uint8_t)(sign | 0x7E);
+    if (!e4 && a >= 61440.0f) return (uint8_t)(sign | 0x7C);
+    /* binary search for the largest code whose value is <= a (codes 0..top increase with value) */
+    int lo = 0, hi = top;
+    while (lo < hi) {
+        int mid = (lo + hi + 1) / 2;
+        if (oq_fp8_decode((uint8_t)mid, fmt) <= a) lo = mid;
+        else hi = mid - 1;
+    }
+    int c = lo; /* e5m2 between 57344 and 61440 stays at the top code */
+    if (c < top) {
+        double d0 = (double)a - oq_fp8_decode((uint8_t)c, fmt);
+        double d1 = (double)oq_fp8_decode((uint8_t)(c + 1), fmt) - (double)a;
+        if (d1 < d0 || (d1 == d0 && ((c & 1) || OQ_MUTANT == 14))) c = c + 1;
+    }
+    return (uint8_t)(sign | c);
+}
+
+/* (V)REQ8 / (V)QF322B8_PRE after the multiply (gen_data_s322s8.py:56-80, gen_data_f322s8.py:56-80 with the
+ * ReLU coefficient equal to M1; accompanying_quantization.md:79-103 for the word): NaN -> 0 (boundary-value
+ * table :76-79), clamp to [-256, 255], round half to even, add the 9-bit offset (bits 37-45, 0..511,
+ * asc_set_l0c_copy_prequant.md:106), saturate to int8 when the sign flag (bit 46) is set, else to uint8.
+ * Bits 32-36 (shift N, MCB) are ignored as on arch 3510 (accompanying_quantization.md table 2). */
+uint8_t oq_requant8(float v, uint64_t word)
+{
+    if (isnan(v)) v = 0.0f;
+    if (OQ_MUTANT == 13) v += (float)((word >> 37) & 0x1FFu);
+    float c = v < -256.0f ? -256.0f : (v > 255.0f ? 255.0f : v);
+    int t = (int)rintf(c) + (OQ_MUTANT == 13 ? 0 : (int)((word >> 37) & 0x1FFu));
+    if (((word >> 46) & 1u) || OQ_MUTANT == 15) {
+        t = t < -128 ? -128 : (t > 127 ? 127 : t);
+        return (uint8_t)(int8_t)t;
+    }
+    t = t < 0 ? 0 : (t > 255 ? 255 : t);
+    return (uint8_t)t;
+}
+
 static inline float load_as_f32(const void* p, int type, int64_t i)
 {
     switch (type) {
@@ -263,6 +312,18 @@ void oq_mm_dequant(const int32_t* acc, void* out, int out_type, int64_t M, int64
         }
 }
 
+/* (V)REQ8 epilogue of the int8 Matmul with an int8 / uint8 C (quant_processor_fixpipe.h:89-99, 209-214):
+ * out = requant8(f32(acc) * M1, word), word = qvec[n] or qscalar; f32(acc) rounds to nearest even. */
+void oq_mm_requant(const int32_t* acc, uint8_t* out, int64_t M, int64_t N, const uint64_t* qvec, uint64_t qscalar)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; ++n) {
+            uint64_t w = qvec ? qvec[n] : qscalar;
+            out[m * N + n] = oq_requant8((float)acc[m * N + n] * oq_quant_pre_m1(w), w);
+        }
+}
+
 /* fp8 operands: L0C is fp32 (matmul_utils.h:134-175); a float bias seeds L0C before the k loop (MmadCompute
  * with isBias, mmad_compute.h:40-90; the fp8 sample adds a float [1, N] bias, matmul_fp8/scripts/gen_data.py
  * tf_matmul + bias); the epilogue is (V)QF322{F16,BF16,F32}_PRE (quant_processor_fixpipe.h:101-115):
@@ -271,7 +332,9 @@ void oq_mm_dequant(const int32_t* acc, void* out, int out_type, int64_t M, int64
  * device accumulates in fp32 and aligns the products of each 16-element K group to the group's largest one,
  * so this path is compared within a tolerance built from sum |a b| (absdot_out) and the sum over 16-element
  * K groups of the group's largest |a b| (blockmax_out; either output may be NULL).
- * use_q: 1 when SetQuantScalar / SetQuantVector was called. */
+ * use_q: 1 when SetQuantScalar / SetQuantVector was called.
+ * out_type OQ_INT8 / OQ_UINT8: (V)QF322B8_PRE, oq_requant8((acc + bias) * M1, word); OQ_FP8_E4M3 / _E5M2:
+ * (V)QF322FP8_PRE (quant_processor_fixpipe.h:101-103, 219-221), oq_f32_to_fp8((acc + bias) * M1). */
 void oq_matmul_fp8(const uint8_t* A, const uint8_t* B, int a_fmt, int b_fmt, const float* bias, void* out,
                    int out_type, int64_t M, int64_t N, int64_t K, int transA, int transB, int use_q,
                    const uint64_t* qvec, uint64_t qscalar, double* exact_out, double* absdot_out,
@@ -308,7 +371,12 @@ void oq_matmul_fp8(const uint8_t* A, const uint8_t* B, int a_fmt, int b_fmt, con
             if (blockmax_out) blockmax_out[m * N + n] = sb;
             float v = (float)s;
             if (use_q) v = v * (qvec ? oq_quant_pre_m1(qvec[n]) : ms);
-            store_from_f32(out, out_type, m * N + n, v);
+            if (out_type == OQ_INT8 || out_type == OQ_UINT8)
+                ((uint8_t*)out)[m * N + n] = oq_requant8(v, qvec ? qvec[n] : qscalar);
+            else if (out_type == OQ_FP8_E4M3 || out_type == OQ_FP8_E5M2)
+                ((uint8_t*)out)[m * N + n] = oq_f32_to_fp8(v, out_type);
+            else
+                store_from_f32(out, out_type, m * N + n, v);
         }
         free(arow);
     }

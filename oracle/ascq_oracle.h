@@ -70,6 +70,12 @@ void oq_matmul_i8(const int8_t* A, const int8_t* B, const int32_t* bias, int32_t
  * qvec != NULL selects the per-channel (vector) word qvec[n], else qscalar */
 void oq_mm_dequant(const int32_t* acc, void* out, int out_type, int64_t M, int64_t N,
                    const uint64_t* qvec, uint64_t qscalar);
+/* f32 -> fp8 (rne; e4m3fn saturating to +-448 with NaN -> 0, e5m2 overflowing to inf) */
+uint8_t oq_f32_to_fp8(float x, int fmt);
+/* REQ8 / QF322B8 after the multiply: clamp [-256, 255], rint, + 9-bit offset, saturate by the sign flag */
+uint8_t oq_requant8(float v, uint64_t word);
+/* (V)REQ8: int32 -> int8 / uint8 with the word's M1, offset and sign flag */
+void oq_mm_requant(const int32_t* acc, uint8_t* out, int64_t M, int64_t N, const uint64_t* qvec, uint64_t qscalar);
 /* fp8 x fp8 -> fp32 accumulate (exact products, double sum) -> (V)QF322{F16,BF16,F32}_PRE */
 void oq_matmul_fp8(const uint8_t* A, const uint8_t* B, int a_fmt, int b_fmt, const float* bias, void* out,
                    int out_type, int64_t M, int64_t N, int64_t K, int transA, int transB, int use_q,

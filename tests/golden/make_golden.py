@@ -155,12 +155,59 @@ def mx_example():
          scale_b_pairs=np.ascontiguousarray(s2_pairs), golden_bf16=golden.view(np.uint16))
 
 
-def main():
-    for f in (deqf16_seed9, matmul_quant_vector, quant_example, dequant_example, antiquant_seed10,
-              group_matmul_example, mx_example):
-        f()
-        print("wrote", f.__name__)
+L0C2GM = "examples/02_simd_c_api/03_c_api/03_matrix_compute/asc_copy_l0c2gm/scripts/"
+
+
+def _req8(v, word):
+    """the scripts' req8_pre / qf322b8_pre with the ReLU coefficient equal to M1 (pre_relu_mode 0): clip to
+    [-256, 255], np.round (half to even), + offset, clip to the int8 range (sign flag set)"""
+    m1 = np.float32((np.uint32(word & 0xFFFFFFFF) & np.uint32(0xFFFFE000)).view(np.float32))
+    off = int((int(word) >> 37) & 0x1FF)
+    q = np.round(np.clip(v.astype(np.float32) * m1, -256, 255)).astype(np.int16) + off
+    return np.clip(q, -128, 127).astype(np.int8)
+
+
+def req8_seed9():
+    """asc_copy_l0c2gm/scripts/gen_data_s322s8.py: int8 [128,128] x [128,256] in [-3,3) with seed 9, (V)REQ8 with
+    M1 = 2 in every column and the sign flag set (int8 C), ReLU coefficient = M1; golden int8."""
+    np.random.seed(9)
+    M, K, N = 128, 128, 256
+    x1 = np.random.randint(-3, 3, [M, K]).astype(np.int8)
+    x2 = np.random.randint(-3, 3, [K, N]).astype(np.int8)
+    acc = x1.astype(np.int32) @ x2.astype(np.int32)
+    word = int(np.float32(2.0).view(np.uint32)) | 0x400000000000
+    golden = _req8(acc, word)
+    save("req8_seed9", L0C2GM + "gen_data_s322s8.py:29-80,83-136", x1=x1, x2=x2,
+         quant_word=np.array([word], np.uint64), golden=golden)
+
+
+def qf322b8_seed9():
+    """asc_copy_l0c2gm/scripts/gen_data.py scenario 4 / 5: f16 [128,128] x [128,256] in [-1,3) with seed 9, fp32
+    matmul (numpy float32), (V)QF322B8_PRE with M1 = 2 and the sign flag (int8 C); golden int8.  The fp32
+    accumulators are stored with the golden: the fixture pins the epilogue."""
+    np.random.seed(9)
+    M, K, N = 128, 128, 256
+    x1 = np.random.uniform(-1, 3, [M, K]).astype(np.float16)
+    x2 = np.random.uniform(-1, 3, [K, N]).astype(np.float16)
+    acc = np.matmul(x1.astype(np.float32), x2.astype(np.float32)).astype(np.float32)
+    word = int(np.float32(2.0).view(np.uint32)) | 0x400000000000
+    golden = _req8(acc, word)
+    save("qf322b8_seed9", L0C2GM + "gen_data.py:56-80,83-116,119-148", acc_f32=acc,
+         quant_word=np.array([word], np.uint64), golden=golden)
+
+
+ALL = ("deqf16_seed9", "matmul_quant_vector", "quant_example", "dequant_example", "antiquant_seed10",
+       "group_matmul_example", "mx_example", "req8_seed9", "qf322b8_seed9")
+
+
+def main(names=None):
+    """python tests/golden/make_golden.py [fixture ...] (default: all)"""
+    for name in names or ALL:
+        globals()[name]()
+        print("wrote", name)
 
 
 if __name__ == "__main__":
-    main()
+    import sys
+
+    main(sys.argv[1:])

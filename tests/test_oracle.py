@@ -514,3 +514,115 @@ def test_mx_matmul_fp8_vs_torch_decode(fa, fb):
     assert np.allclose(Ca, np.abs(a) @ np.abs(b), rtol=1e-13, atol=0)
     P = np.abs(a[:, :, None] * b[None, :, :])
     assert np.allclose(Cb, sum(P[:, h:h + 16, :].max(1) for h in range(0, K, 16)), rtol=1e-15, atol=0)
+
+
+# --------------------------------------------------------------------------- requant epilogues (REQ8 / QF322B8 / QF322FP8)
+def _word(m1, offset=0, sign=1):
+    return int(O.lib().oq_pack_quant_pre(float(m1), int(offset), int(sign)))
+
+
+def test_req8_seed9_golden_exact():
+    """(V)REQ8 golden of asc_copy_l0c2gm (gen_data_s322s8.py, seed 9): scalar and per-channel forms"""
+    f = np.load(GOLD / "req8_seed9.npz")
+    acc = O.matmul_i8(f["x1"], f["x2"])
+    w = int(f["quant_word"][0])
+    assert np.array_equal(O.mm_requant(acc, qscalar=w).view(np.int8), f["golden"])
+    qv = np.full(acc.shape[1], w, np.uint64)
+    assert np.array_equal(O.mm_requant(acc, qvec=qv).view(np.int8), f["golden"])
+
+
+def test_qf322b8_seed9_golden_exact():
+    """(V)QF322B8_PRE golden of asc_copy_l0c2gm scenario 4 / 5 (gen_data.py, seed 9), on its fp32 accumulators"""
+    f = np.load(GOLD / "qf322b8_seed9.npz")
+    w = int(f["quant_word"][0])
+    L = O.lib()
+    acc = f["acc_f32"]
+    m1 = float(np.uint32(w & 0xFFFFE000).view(np.float32))
+    got = np.array([L.oq_requant8(float(np.float32(v) * np.float32(m1)), w) for v in acc.ravel()], np.uint8)
+    assert np.array_equal(got.view(np.int8).reshape(acc.shape), f["golden"])
+
+
+def test_prequant_doc_example():
+    """asc_set_l0c_copy_prequant.md example: identity x identity, scale 2, offset 3, signed -> 5 on the
+    diagonal, 3 elsewhere (the offset is added after the multiply, zeros included)"""
+    L = O.lib()
+    w = _word(2.0, 3, 1)
+    acc = np.eye(16, dtype=np.float32)
+    got = np.array([[L.oq_requant8(float(v * 2.0), w) for v in row] for row in acc], np.uint8).view(np.int8)
+    exp = np.full((16, 16), 3, np.int8)
+    np.fill_diagonal(exp, 5)
+    assert np.array_equal(got, exp)
+    # the fp8 Matmul path with the same word: e4m3 identity (0x38 = 1.0)
+    A = np.zeros((16, 16), np.uint8)
+    np.fill_diagonal(A, 0x38)
+    out, _, _, _ = O.matmul_fp8(A, A, O.FP8_E4M3, O.FP8_E4M3, out_type=O.INT8, use_q=True, qscalar=w)
+    assert np.array_equal(out.view(np.int8), exp)
+
+
+def test_requant8_boundaries_and_offsets():
+    """closed form over random values, offsets 0..511 and both sign flags; NaN -> 0, +-inf saturate
+    (matrix_compute_move_out_interface_boundary_value_summary.md:74-79, 106-109)"""
+    L = O.lib()
+    rng = np.random.default_rng(804)
+    v = np.concatenate([rng.uniform(-700, 700, 3000), np.arange(-260, 260) + 0.5, [255.4, 255.5, -256.5]])
+    v = v.astype(np.float32)
+    for _ in range(6):
+        off, sign = int(rng.integers(0, 512)), int(rng.integers(0, 2))
+        w = _word(1.0, off, sign) | (0x1F << 32)  # bits 32-36 (shift, MCB) are ignored
+        got = np.array([L.oq_requant8(float(x), w) for x in v], np.uint8)
+        t = np.round(np.clip(v.astype(np.float64), -256, 255)) + off
+        exp = np.clip(t, -128, 127).astype(np.int8).view(np.uint8) if sign else np.clip(t, 0, 255).astype(np.uint8)
+        assert np.array_equal(got, exp), (off, sign)
+    ws, wu = _word(1.0, 0, 1), _word(1.0, 0, 0)
+    assert L.oq_requant8(float("nan"), ws) == 0 and L.oq_requant8(float("nan"), wu) == 0
+    assert L.oq_requant8(float("inf"), ws) == 127 and L.oq_requant8(float("-inf"), ws) == 0x80
+    assert L.oq_requant8(float("inf"), wu) == 255 and L.oq_requant8(float("-inf"), wu) == 0
+
+
+@pytest.mark.parametrize("fmt", [O.FP8_E4M3, O.FP8_E5M2])
+def test_f32_to_fp8_vs_torch(fmt):
+    """in-range values (including exact ties between neighbouring codes and subnormals) vs torch's rne cast;
+    e4m3 saturates to +-448 with NaN -> 0 (fixpipe default), e5m2 overflows to inf (NaN stays NaN)"""
+    L = O.lib()
+    tdt = _T8[fmt]
+    top = 448.0 if fmt == O.FP8_E4M3 else 57344.0
+    rng = np.random.default_rng(805)
+    vals = np.exp(rng.uniform(np.log(2.0 ** -20), np.log(top), 4000)) * rng.choice([-1, 1], 4000)
+    codes = np.arange(256, dtype=np.uint8)
+    dec = torch_decode(codes, fmt)
+    fin = np.sort(np.unique(np.abs(dec[np.isfinite(dec)])))
+    mids = (fin[1:] + fin[:-1]) / 2  # exact ties
+    vals = np.concatenate([vals, mids, -mids, fin, [0.0, -0.0]]).astype(np.float32)
+    vals = vals[np.abs(vals) <= top]
+    got = np.array([L.oq_f32_to_fp8(float(x), fmt) for x in vals], np.uint8)
+    exp = torch.from_numpy(vals).to(tdt).view(torch.uint8).numpy()
+    assert np.array_equal(got, exp)
+    if fmt == O.FP8_E4M3:
+        for x, c in [(449.0, 0x7E), (1e6, 0x7E), (-1e6, 0xFE), (float("inf"), 0x7E), (float("-inf"), 0xFE),
+                     (float("nan"), 0x00)]:
+            assert L.oq_f32_to_fp8(x, fmt) == c
+    else:
+        for x, c in [(61439.0, 0x7B), (61440.0, 0x7C), (-1e9, 0xFC), (float("inf"), 0x7C)]:
+            assert L.oq_f32_to_fp8(x, fmt) == c
+        assert L.oq_f32_to_fp8(float("nan"), fmt) == 0x7F
+
+
+def test_matmul_fp8_requant_outputs_compose():
+    """QF322B8 / QF322FP8 outputs of oq_matmul_fp8 equal requant8 / f32_to_fp8 of fp32((s + bias)) * M1"""
+    L = O.lib()
+    rng = np.random.default_rng(806)
+    M, N, K = 7, 9, 64
+    A = fp8_bytes(rng, (M, K), O.FP8_E4M3, 0, 100)
+    B = fp8_bytes(rng, (K, N), O.FP8_E5M2, 0, 100)
+    bias = rng.standard_normal(N).astype(np.float32)
+    words = np.array([_word(x, int(o), int(sg)) for x, o, sg in
+                      zip(rng.uniform(0.05, 3.0, N), rng.integers(0, 512, N), rng.integers(0, 2, N))], np.uint64)
+    m1 = (words & np.uint64(0xFFFFE000)).astype(np.uint32).view(np.float32)
+    for ot in (O.INT8, O.FP8_E4M3, O.FP8_E5M2):
+        out, exact, _, _ = O.matmul_fp8(A, B, O.FP8_E4M3, O.FP8_E5M2, bias=bias, out_type=ot, use_q=True, qvec=words)
+        v = (exact.astype(np.float32) * m1[None, :]).astype(np.float32)
+        if ot == O.INT8:
+            exp = np.array([[L.oq_requant8(float(v[i, j]), int(words[j])) for j in range(N)] for i in range(M)])
+        else:
+            exp = np.array([[L.oq_f32_to_fp8(float(v[i, j]), ot) for j in range(N)] for i in range(M)])
+        assert np.array_equal(out.view(np.uint8), exp.astype(np.uint8))
