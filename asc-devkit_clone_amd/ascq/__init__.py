@@ -26,6 +26,7 @@ INT8, UINT8, INT4, INT32, F16, BF16, F32, U64, FP8_E4M3, FP8_E5M2, FP4_E2M1, E8M
 # ascq_round_mode
 ROUND_NONE, ROUND_RINT, ROUND_FLOOR, ROUND_CEIL, ROUND_ROUND, ROUND_TRUNC = range(6)
 # ascq_policy
+ACT_NONE, ACT_FASTER_GELU = 0, 1
 PER_TENSOR, PER_CHANNEL, PER_TOKEN, PER_GROUP = range(4)
 # ascq_arith
 ARITH_F16, ARITH_F32 = 0, 1
@@ -107,7 +108,7 @@ SIGNATURES = {
     "ascq_weight_pack_size": (_I32, [_I32, _I64, _I64, ctypes.POINTER(ctypes.c_size_t)]),
     "ascq_weight_pack": (_I32, [_P, _P, _I32, _I64, _I64, _I32, _P]),
     "ascq_antiquant_matmul": (_I32, [_P, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _I64, _P]),
-    "ascq_quant_group_matmul": (_I32, [_P, _I32, _P, _P, _P, _I32, _P, _P, _I32, _I64, _I64, _I64, _I64, _P]),
+    "ascq_quant_group_matmul": (_I32, [_P, _I32, _P, _P, _P, _I32, _P, _P, _I32, _I64, _I64, _I64, _I64, _I32, _P]),
 }
 
 _lib = None
@@ -254,14 +255,16 @@ def antiquant_matmul(x: torch.Tensor, w_packed: torch.Tensor, w_type: int, scale
 # ------------------------------------------------------------------------------------------
 def quant_group_matmul(x: torch.Tensor, per_token_scale: torch.Tensor, w: torch.Tensor, scale: torch.Tensor,
                        group_list: torch.Tensor, list_type: int = 0, w_trans: bool = False,
-                       out_dtype=torch.bfloat16, out=None, stream=None):
+                       out_dtype=torch.bfloat16, out=None, stream=None, activation: int = 0):
+    """activation: ACT_NONE or ACT_FASTER_GELU (the reference sample's epilogue)"""
     m, k = x.shape
     g = scale.shape[0]
     n = scale.shape[1]
     out_type = {torch.bfloat16: BF16, torch.float16: F16}[out_dtype]
     y = out if out is not None else torch.empty((m, n), dtype=out_dtype, device=x.device)
     check(lib().ascq_quant_group_matmul(_ptr(y), out_type, _ptr(x), _ptr(per_token_scale), _ptr(w), int(w_trans),
-                                        _ptr(scale), _ptr(group_list), list_type, g, m, k, n, _stream(stream)),
+                                        _ptr(scale), _ptr(group_list), list_type, g, m, k, n, int(activation),
+                                        _stream(stream)),
           "quant_group_matmul")
     return y
 

@@ -725,13 +725,16 @@ ascq_status ascq_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w_
 // ------------------------------------------------------------------------------------------------
 ascq_status ascq_quant_group_matmul(void* y, int32_t out_type, const int8_t* x, const float* per_token_scale,
                                     const int8_t* w, int32_t w_trans, const float* scale, const int64_t* group_list,
-                                    int32_t list_type, int64_t num_groups, int64_t m, int64_t k, int64_t n, void* stream)
+                                    int32_t list_type, int64_t num_groups, int64_t m, int64_t k, int64_t n,
+                                    int32_t activation, void* stream)
 {
     if (!y || !x || !per_token_scale || !w || !scale || !group_list)
         return fail(ASCQ_E_INVALID_ARG, "quant_group_matmul: null argument");
     if (out_type != ASCQ_DT_BF16 && out_type != ASCQ_DT_F16)
         return fail(ASCQ_E_UNSUPPORTED, "quant_group_matmul: output must be bf16 or f16");
     if (list_type != 0 && list_type != 1) return fail(ASCQ_E_INVALID_ARG, "quant_group_matmul: list_type must be 0 or 1");
+    if (activation != ASCQ_ACT_NONE && activation != ASCQ_ACT_FASTER_GELU)
+        return fail(ASCQ_E_INVALID_ARG, "quant_group_matmul: unknown activation %d", activation);
     if (num_groups <= 0 || num_groups > 1024) return fail(ASCQ_E_INVALID_ARG, "quant_group_matmul: 1 <= groups <= 1024");
     if (m <= 0 || k <= 0 || n <= 0) return fail(ASCQ_E_INVALID_ARG, "quant_group_matmul: shape must be positive");
     ascq::GroupGemmArgs g{};
@@ -748,6 +751,7 @@ ascq_status ascq_quant_group_matmul(void* y, int32_t out_type, const int8_t* x, 
     g.M = m;
     g.K = k;
     g.N = n;
+    g.act = activation;
     return hip_status(ascq::launch_group_gemm(g, S(stream)), "quant_group_matmul");
 }
 

@@ -59,6 +59,10 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_floa
 // QUANT_PRE word -> M1 multiplier: bits [31:13] as fp32, low 13 bits cleared
 __device__ __forceinline__ float quant_pre_m1(uint64_t w) { return __uint_as_float((uint32_t)w & 0xFFFFE000u); }
 
+// FasterGelu, x / (1 + exp(-1.702 x)) in fp32 (impl/adv_api/detail/activation/gelu/gelu_3510_impl.h:113-122):
+// for x -> -inf the exp overflows to inf and the result is -0, as there
+__device__ __forceinline__ float faster_gelu(float x) { return x / (1.0f + expf(-1.702f * x)); }
+
 // (V)REQ8 / (V)QF322B8_PRE after the multiply by M1 (examples/02_simd_c_api/03_c_api/03_matrix_compute/
 // asc_copy_l0c2gm/scripts/gen_data_s322s8.py:56-80): NaN -> 0, clamp to [-256, 255], round half to even, add
 // the word's 9-bit offset (bits 37-45, 0..511), saturate to int8 when the sign flag (bit 46) is set, else to

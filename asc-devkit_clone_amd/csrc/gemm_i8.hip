@@ -126,8 +126,8 @@ __global__ __launch_bounds__(WM * WN * 64) void group_gemm_i8_kernel(GroupGemmAr
     typename T::acc_t acc[T::FM][T::FN];
     T::run(c, smem, acc);
 
-    // epilogue (quant_group_matmul_custom.asc:424-452 without the Gelu): AscendDequant acc*scale[g,n] in fp32,
-    // Mul by the per-token scale in fp32, one rounding cast to the output type.
+    // epilogue (quant_group_matmul_custom.asc:424-452): AscendDequant acc*scale[g,n] in fp32, Mul by the
+    // per-token scale in fp32, optional FasterGelu in fp32, one rounding cast to the output type.
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
 #pragma unroll
@@ -143,6 +143,7 @@ __global__ __launch_bounds__(WM * WN * 64) void group_gemm_i8_kernel(GroupGemmAr
                 if (row >= m_end) continue;
                 float v = (float)acc[i][j][r] * sc;
                 v = v * p.pts[row];
+                if (p.act) v = faster_gelu(v);
                 const int64_t o = row * p.N + col;
                 if (p.out_type == DT_F16) ((uint16_t*)p.Y)[o] = f32_to_f16_sat(v);
                 else ((uint16_t*)p.Y)[o] = f32_to_bf16_sat(v);
@@ -232,6 +233,7 @@ __global__ __launch_bounds__(256) void group_gemm_generic_kernel(GroupGemmArgs p
             acc += (uint32_t)((int32_t)p.X[m * p.K + k] * (int32_t)(p.w_trans ? Wg[n * p.K + k] : Wg[k * p.N + n]));
         float v = (float)(int32_t)acc * p.scale[(int64_t)g * p.N + n];
         v = v * p.pts[m];
+        if (p.act) v = faster_gelu(v);
         if (p.out_type == DT_F16) ((uint16_t*)p.Y)[m * p.N + n] = f32_to_f16_sat(v);
         else ((uint16_t*)p.Y)[m * p.N + n] = f32_to_bf16_sat(v);
     }

@@ -65,6 +65,7 @@ struct GroupGemmArgs {
     const int64_t* group_list;
     int list_type;            // 0 prefix offsets [G+1], 1 counts [G]
     int64_t G, M, K, N;
+    int act;                  // 0 none, 1 FasterGelu
 };
 hipError_t launch_group_gemm(const GroupGemmArgs& a, hipStream_t st);
 

@@ -270,17 +270,24 @@ ascq_status ascq_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w_
 
 /* ------------------------------------------------------------------------------------------
  * Quantized group matmul (MoE)
+ * ------------------------------------------------------------------------------------------ */
+/* Activation of the group-matmul epilogue: none, or the sample's FasterGelu x / (1 + exp(-1.702 x)) in fp32
+ * (quant_group_matmul_custom.asc:442-445; impl/adv_api/detail/activation/gelu/gelu_3510_impl.h:113-122). */
+typedef enum { ASCQ_ACT_NONE = 0, ASCQ_ACT_FASTER_GELU = 1 } ascq_activation;
+
+/* ------------------------------------------------------------------------------------------
  * Replaces quant_group_matmul_custom (examples/01_simd_cpp_api/05_best_practices/03_fusion_compute/
  * quant_group_matmul_high_performance/quant_group_matmul_custom.asc:89-452, formula README_en.md:36-60):
- *   for group g, rows [s_g, s_g + cnt_g):  y = cast( (f32(x_g @ W_g) * scale[g, n]) * per_token_scale[m] )
+ *   for group g, rows [s_g, s_g + cnt_g):  y = cast( act( (f32(x_g @ W_g) * scale[g, n]) * per_token_scale[m] ) )
  * x int8 [M, K]; per_token_scale f32 [M]; w int8 [G, K, N] (w_trans: [G, N, K]); scale f32 [G, N];
  * group_list int64 on the device: list_type 0 = G+1 prefix offsets, 1 = G counts (the reference form,
- * :263).  Rows outside every group are not written.  out_type BF16 or F16.  No activation is applied.
+ * :263).  Rows outside every group are not written.  out_type BF16 or F16.  activation: ascq_activation (the
+ * sample applies ASCQ_ACT_FASTER_GELU with f16 output).
  * ------------------------------------------------------------------------------------------ */
 ascq_status ascq_quant_group_matmul(void* y, int32_t out_type, const int8_t* x, const float* per_token_scale,
                                     const int8_t* w, int32_t w_trans, const float* scale,
                                     const int64_t* group_list, int32_t list_type, int64_t num_groups, int64_t m,
-                                    int64_t k, int64_t n, void* stream);
+                                    int64_t k, int64_t n, int32_t activation, void* stream);
 
 #ifdef __cplusplus
 }

@@ -584,15 +584,28 @@ void oq_antiquant_matmul(uint16_t* y, double* y_exact, double* y_absdot, const u
 /* QuantGroupMatmul (MoE)                                                    */
 /* ------------------------------------------------------------------------ */
 
+/* FasterGelu of the group-matmul example (quant_group_matmul_custom.asc:442-445), restating the fp32 op
+ * sequence of the arch 3510 float path (impl/adv_api/detail/activation/gelu/gelu_3510_impl.h:113-122): Muls by
+ * -1.702f, Exp, Adds 1, Div -- each an fp32 result (exp taken in double and rounded once to fp32, so it
+ * overflows to inf above ~88.72 and the result is then -0, as on the reference). */
+float oq_faster_gelu(float x)
+{
+    float t = x * (OQ_MUTANT == 16 ? 1.702f : -1.702f);
+    float e = (float)exp((double)t);
+    float d = e + 1.0f;
+    return x / d;
+}
+
 /* examples/01_simd_cpp_api/05_best_practices/03_fusion_compute/quant_group_matmul_high_performance/
  * quant_group_matmul_custom.asc: group rows [s_g, s_g+cnt_g) (Process :255-288), int32 accumulate on the
  * cube (MMCompute :296-334), then AscendDequant(acc x scale[g,n]) to fp32 (:433), Mul by perTokenScale[m]
- * (:439), and the final Cast (:450; CAST_NONE = rint).  The Gelu of the sample (:445) is not applied.
+ * (:439), act != 0: the sample's FasterGelu (:445, oq_faster_gelu in fp32 ops), and the final Cast (:450;
+ * CAST_NONE = rint).
  * list_type 0: group_list holds G+1 int64 prefix offsets (offsets[0] = first row); 1: G int64 counts
  * (the reference's GetValue(groupIdx) counts, :263).  w [G,K,N] ND, or [G,N,K] when w_trans. */
 void oq_group_matmul(void* y, int out_type, const int8_t* x, const float* pts, const int8_t* w, int w_trans,
                      const float* scale, const int64_t* group_list, int list_type, int64_t G, int64_t M,
-                     int64_t K, int64_t N)
+                     int64_t K, int64_t N, int act)
 {
     int64_t start = list_type == 0 ? group_list[0] : 0;
     for (int64_t g = 0; g < G; ++g) {
@@ -610,6 +623,7 @@ void oq_group_matmul(void* y, int out_type, const int8_t* x, const float* pts, c
                     acc += (int64_t)x[m * K + k] * (int64_t)(w_trans ? wg[n * K + k] : wg[k * N + n]);
                 float v = (float)(int32_t)(uint32_t)(uint64_t)acc * (OQ_MUTANT == 5 ? pts[m] : scale[g * N + n]);
                 v = v * (OQ_MUTANT == 5 ? scale[g * N + n] : pts[m]);
+                if (act) v = oq_faster_gelu(v);
                 store_from_f32(y, out_type, m * N + n, v);
             }
         }

@@ -103,10 +103,13 @@ void oq_antiquant(void* dst, int dst_type, const void* src, int src_type, const 
 void oq_antiquant_matmul(uint16_t* y, double* y_exact, double* y_absdot, const uint16_t* x, const void* w,
                          int w_type, const uint16_t* scale, const uint16_t* offset, int64_t group_size,
                          int64_t M, int64_t N, int64_t K, int w_transpose);
-/* QuantGroupMatmul (MoE): per group g rows [s_g, e_g): y = cast(f32(f32(acc)*scale[g,n]) * pts[m]) */
+/* FasterGelu x / (1 + exp(-1.702 x)) as fp32 ops (Muls, Exp, Adds, Div) */
+float oq_faster_gelu(float x);
+/* QuantGroupMatmul (MoE): per group g rows [s_g, e_g): y = cast(f32(f32(acc)*scale[g,n]) * pts[m]), with
+ * act != 0 cast(FasterGelu(...)) */
 void oq_group_matmul(void* y, int out_type, const int8_t* x, const float* pts, const int8_t* w, int w_trans,
                      const float* scale, const int64_t* group_list, int list_type, int64_t G, int64_t M,
-                     int64_t K, int64_t N);
+                     int64_t K, int64_t N, int act);
 /* MX block-scaled matmul (E2M1 or fp8 elements; elem_fmt = A format | B format << 8, B defaulting to A's),
  * fp64 dequant-then-matmul (reference golden) -> bf16 (rne) */
 void oq_mx_matmul(uint16_t* C, double* C_exact, double* C_absdot, const uint8_t* A, const uint8_t* B,

@@ -123,6 +123,30 @@ def group_matmul_example():
          pts=pts.reshape(-1), group_list=group_list, golden=out.astype(np.float16))
 
 
+def group_matmul_gelu_example():
+    """the same generator with its FastGelu (gen_data.py:19-23, applied to the float32 mmOut with numpy
+    float32 ops) and the f16 golden: 4 equal groups, x / weight in [-10,10), scale and perTokenScale N(0, 0.01)
+    (reduced to m=256, k=128, n=128; seed 4321)."""
+    np.random.seed(4321)
+    G, m, k, n = 4, 256, 128, 128
+    group_list = np.array([m // G] * G, dtype=np.int64)
+    x = np.random.randint(-10, 10, [m, k]).astype(np.int8)
+    weight = np.random.randint(-10, 10, [G, k, n]).astype(np.int8)
+    scale = np.random.normal(0, 0.01, (G, n)).astype(np.float32)
+    pts = np.random.normal(0, 0.01, (m, 1)).astype(np.float32)
+    idx = [0] + np.cumsum(group_list).tolist()
+    out = np.empty((m, n), np.float32)
+    for i in range(G):
+        s, e = idx[i], idx[i + 1]
+        out[s:e] = np.dot(x[s:e].astype(np.float32), weight[i].astype(np.float32))
+        out[s:e] *= scale[i] * pts[s:e]
+    ax = np.abs(out)
+    gelu = out * np.exp(np.float32(0.851) * (out - ax)) / (1 + np.exp(np.float32(-1.702) * ax))
+    save("group_matmul_gelu_example", "examples/01_simd_cpp_api/05_best_practices/03_fusion_compute/"
+         "quant_group_matmul_high_performance/scripts/gen_data.py:19-54", x=x, weight=weight, scale=scale,
+         pts=pts.reshape(-1), group_list=group_list, golden=gelu.astype(np.float32).astype(np.float16))
+
+
 def mx_example():
     """01_matrix_compute/matmul_mxfp4_high_performance/scripts/gen_data.py: elements in {-1, 0, 1}, e8m0 scales
     in [127, 129], fp64 dequant-then-matmul golden cast to bf16; packing even element in the low nibble,
@@ -197,7 +221,7 @@ def qf322b8_seed9():
 
 
 ALL = ("deqf16_seed9", "matmul_quant_vector", "quant_example", "dequant_example", "antiquant_seed10",
-       "group_matmul_example", "mx_example", "req8_seed9", "qf322b8_seed9")
+       "group_matmul_example", "mx_example", "req8_seed9", "qf322b8_seed9", "group_matmul_gelu_example")
 
 
 def main(names=None):

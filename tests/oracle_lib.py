@@ -68,7 +68,8 @@ def lib() -> ctypes.CDLL:
             "oq_antiquant_matmul": (None, [_P, _P, _P, _P, _P, ctypes.c_int, _P, _P, _I64, _I64, _I64, _I64,
                                            ctypes.c_int]),
             "oq_group_matmul": (None, [_P, ctypes.c_int, _P, _P, _P, ctypes.c_int, _P, _P, ctypes.c_int, _I64, _I64,
-                                       _I64, _I64]),
+                                       _I64, _I64, ctypes.c_int]),
+            "oq_faster_gelu": (ctypes.c_float, [ctypes.c_float]),
             "oq_mx_matmul": (None, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_int, ctypes.c_int, _P, _I64, _P]),
             "oq_mx_quantize_fp4": (None, [_P, _P, _P, _I64, _I64]),
@@ -212,7 +213,7 @@ def antiquant_matmul(x_f16bits, w, w_type, scale, offset, group_size, M, N, K, w
     return y, ye, ya
 
 
-def group_matmul(x, pts, w, scale, group_list, list_type, G, M, K, N, out_type=BF16, w_trans=False, y=None):
+def group_matmul(x, pts, w, scale, group_list, list_type, G, M, K, N, out_type=BF16, w_trans=False, y=None, act=0):
     x = np.ascontiguousarray(x, np.int8)
     pts = np.ascontiguousarray(pts, np.float32)
     w = np.ascontiguousarray(w, np.int8)
@@ -221,7 +222,7 @@ def group_matmul(x, pts, w, scale, group_list, list_type, G, M, K, N, out_type=B
     if y is None:
         y = np.zeros((M, N), np.uint16)
     lib().oq_group_matmul(_p(y), out_type, _p(x), _p(pts), _p(w), int(w_trans), _p(scale), _p(gl), list_type, G, M, K,
-                          N)
+                          N, int(act))
     return y
 
 

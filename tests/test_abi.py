@@ -100,8 +100,9 @@ def test_gemv_group_argument_checks():
     _err(L.ascq_antiquant_matmul(d, d, d, ascq.INT4, d, d, 96, 1, 64, 256, None), ascq.E_INVALID_ARG)  # g !| K
     _err(L.ascq_antiquant_matmul(d, ctypes.c_void_p(0x1001), d, ascq.INT4, d, d, 128, 1, 64, 256, None),
          ascq.E_INVALID_ARG)  # misaligned x
-    _err(L.ascq_quant_group_matmul(d, ascq.F32, d, d, d, 0, d, d, 0, 4, 8, 16, 16, None), ascq.E_UNSUPPORTED)
-    _err(L.ascq_quant_group_matmul(d, ascq.BF16, d, d, d, 0, d, d, 2, 4, 8, 16, 16, None), ascq.E_INVALID_ARG)
+    _err(L.ascq_quant_group_matmul(d, ascq.F32, d, d, d, 0, d, d, 0, 4, 8, 16, 16, 0, None), ascq.E_UNSUPPORTED)
+    _err(L.ascq_quant_group_matmul(d, ascq.BF16, d, d, d, 0, d, d, 2, 4, 8, 16, 16, 0, None), ascq.E_INVALID_ARG)
+    _err(L.ascq_quant_group_matmul(d, ascq.BF16, d, d, d, 0, d, d, 0, 4, 8, 16, 16, 7, None), ascq.E_INVALID_ARG)
 
 
 def test_matmul_handle_state_machine():

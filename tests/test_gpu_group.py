@@ -72,3 +72,47 @@ def test_config4_moe_full_size(ascq_gpu, oracle, w_trans):
         acc = (xf[s:e] @ w[g].astype(np.float64)).astype(np.float32)  # exact int -> f32 rne
         v = (acc * scale[g][None, :]).astype(np.float32) * pts[s:e, None]
         np.testing.assert_array_equal(got[s:e], bf16_bits_of_f32(v.astype(np.float32)), err_msg=f"group {g}")
+
+
+def _f16_ulp(v):
+    a = np.maximum(np.abs(v), 2.0 ** -14)
+    return 2.0 ** (np.floor(np.log2(a)) - 10)
+
+
+@pytest.mark.parametrize("w_trans", [False, True])
+@pytest.mark.parametrize("out", ["f16", "bf16"])
+def test_group_matmul_faster_gelu(ascq_gpu, oracle, w_trans, out):
+    """the sample's epilogue with FasterGelu (quant_group_matmul_custom.asc:442-450): device and oracle both run
+    the fp32 op sequence x / (1 + exp(-1.702 x)); the device's expf may differ from the correctly rounded exp by
+    an fp32 ulp, so outputs agree within one output ulp, and bit-exactly on >= 99 %"""
+    rng = seeded(77 + w_trans)
+    G, K, N = 6, 512, 272
+    counts = np.array([300, 0, 17, 1, 250, 90], np.int64)
+    M = int(counts.sum())
+    x = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-127, 128, (G, N, K) if w_trans else (G, K, N), dtype=np.int8)
+    pts = rng.normal(0, 0.01, M).astype(np.float32)
+    scale = rng.normal(0, 0.01, (G, N)).astype(np.float32)  # |v| up to ~ a few: the curved part of the Gelu
+    ycode, tdt = (O.BF16, torch.bfloat16) if out == "bf16" else (O.F16, torch.float16)
+    y = ascq_gpu.quant_group_matmul(_dev(x), _dev(pts), _dev(w), _dev(scale), _dev(counts), 1, w_trans, tdt,
+                                    activation=ascq_gpu.ACT_FASTER_GELU)
+    got = y.cpu().to(torch.float64).numpy()
+    ref_bits = O.group_matmul(x, pts, w, scale, counts, 1, G, M, K, N, ycode, w_trans, act=1)
+    ref = torch.from_numpy(ref_bits.view(np.int16)).view(tdt).to(torch.float64).numpy()
+    ulp = _f16_ulp(ref) if out == "f16" else 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -126))) - 7)
+    assert (np.abs(got - ref) <= ulp).all()
+    assert (got == ref).mean() >= 0.99
+
+
+def test_group_matmul_gelu_sample_golden(ascq_gpu, oracle):
+    """the restated sample golden with FastGelu (tests/golden/group_matmul_gelu_example.npz), judged by the
+    sample's verify_result.py criterion (isclose rtol = atol = 1e-3, error ratio <= 1e-4)"""
+    from pathlib import Path
+
+    f = np.load(Path(__file__).resolve().parent / "golden" / "group_matmul_gelu_example.npz")
+    y = ascq_gpu.quant_group_matmul(_dev(f["x"]), _dev(f["pts"]), _dev(f["weight"]), _dev(f["scale"]),
+                                    _dev(f["group_list"]), 1, False, torch.float16,
+                                    activation=ascq_gpu.ACT_FASTER_GELU)
+    out = y.cpu().numpy().astype(np.float64)
+    bad = ~np.isclose(out, f["golden"].astype(np.float64), rtol=1e-3, atol=1e-3)
+    assert bad.mean() <= 1e-4

@@ -626,3 +626,34 @@ def test_matmul_fp8_requant_outputs_compose():
         else:
             exp = np.array([[L.oq_f32_to_fp8(float(v[i, j]), ot) for j in range(N)] for i in range(M)])
         assert np.array_equal(out.view(np.uint8), exp.astype(np.uint8))
+
+
+# --------------------------------------------------------------------------- group matmul FasterGelu
+def test_faster_gelu_vs_sample_formula():
+    """oq_faster_gelu (fp32 ops x / (1 + exp(-1.702 x))) against the sample's algebraically different form
+    x * exp(0.851 (x - |x|)) / (1 + exp(-1.702 |x|)) (gen_data.py:19-23) in float64: within the fp32 rounding
+    errors of the op sequence, and -0 where the fp32 exp overflows (x below ~-52.1; the float64 form gives a value below 1e-36)"""
+    L = O.lib()
+    x = np.concatenate([np.linspace(-60, 60, 2001), np.random.default_rng(807).normal(0, 3, 2000),
+                        [-1e30, -90.0, -1e-30, 0.0, 1e-30, 90.0, 1e30]]).astype(np.float32)
+    c = float(np.float32(1.702))
+    xd = x.astype(np.float64)
+    ref = xd * np.exp(c / 2 * (xd - np.abs(xd))) / (1 + np.exp(-c * np.abs(xd)))
+    got = np.array([L.oq_faster_gelu(float(v)) for v in x], np.float64)
+    # the fp32 product -1.702 x carries a relative error 2^-24, which exp turns into |1.702 x| 2^-24 relative
+    rtol = (4 + c * np.abs(xd)) * 2.0 ** -24
+    assert (np.abs(got - ref) <= rtol * np.abs(ref) + 1e-36).all()
+    tail = x < -52.2
+    assert (got[tail] == 0).all() and np.signbit(got[tail]).all()
+
+
+def test_group_matmul_gelu_golden_within_reference_tolerance():
+    """the sample's verify_result.py criterion (isclose rtol = atol = 1e-3, error ratio <= 1e-4) against the
+    restated golden with FastGelu, and the bare epilogue (act = 0) does not pass it"""
+    f = np.load(GOLD / "group_matmul_gelu_example.npz")
+    m, k = f["x"].shape
+    G, _, n = f["weight"].shape
+    y = O.group_matmul(f["x"], f["pts"], f["weight"], f["scale"], f["group_list"], 1, G, m, k, n, O.F16, act=1)
+    assert ref_verify(y.view(np.float16), f["golden"], err_tol=1e-4)
+    y0 = O.group_matmul(f["x"], f["pts"], f["weight"], f["scale"], f["group_list"], 1, G, m, k, n, O.F16, act=0)
+    assert not ref_verify(y0.view(np.float16), f["golden"], err_tol=1e-4)

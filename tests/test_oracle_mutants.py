@@ -4,8 +4,8 @@ oracle/ascq_oracle.c carries planted-mistake switches (OQ_MUTANT = n): a dropped
 QUANT_PRE multiplier, half-away instead of half-even rounding, a swapped int4 nibble order, a dropped bias, a
 reordered group-matmul epilogue, a transposed MX scale index, offset/scale applied in the wrong order, a
 double-rounded multiplier, a wrong E2M1 code, a ties-away f16 cast, an unrounded half add, a per-channel
-dequant indexed by row, a requant offset added before the clamp, a ties-away fp8 cast and an ignored requant
-sign flag.  Each mutant is compiled on the CPU into a temporary library and the pinning tests of
+dequant indexed by row, a requant offset added before the clamp, a ties-away fp8 cast, an ignored requant
+sign flag and a FasterGelu with the wrong sign.  Each mutant is compiled on the CPU into a temporary library and the pinning tests of
 tests/test_oracle.py are run against it; every mutant must fail at least one of them.
 """
 from __future__ import annotations
@@ -36,6 +36,7 @@ MUTANTS = {
     13: "requant offset added before the [-256, 255] clamp",
     14: "f32->fp8 ties rounded away from zero",
     15: "requant sign flag ignored (always int8 saturation)",
+    16: "FasterGelu coefficient with the wrong sign",
 }
 
 
