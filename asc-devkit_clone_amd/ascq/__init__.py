@@ -71,6 +71,19 @@ class _MatmulTypes(ctypes.Structure):
     ]
 
 
+CUBE_TILING_FIELDS = (
+    "usedCoreNum M N Ka Kb singleCoreM singleCoreN singleCoreK baseM baseN baseK depthA1 depthB1 stepM stepN isBias "
+    "transLength iterateOrder shareMode shareL1Size shareL0CSize shareUbSize batchM batchN singleBatchM singleBatchN "
+    "stepKa stepKb depthAL1CacheUB depthBL1CacheUB dbL0A dbL0B dbL0C ALayoutInfoB ALayoutInfoS ALayoutInfoN "
+    "ALayoutInfoG ALayoutInfoD BLayoutInfoB BLayoutInfoS BLayoutInfoN BLayoutInfoG BLayoutInfoD CLayoutInfoB "
+    "CLayoutInfoS1 CLayoutInfoN CLayoutInfoG CLayoutInfoS2 BatchNum mxTypePara").split()
+
+
+class CubeTiling(ctypes.Structure):
+    """ascq_cube_tiling: the reference's TCubeTiling fields in their order (matmul_tilingdata.h:21-72)"""
+    _fields_ = [(f, ctypes.c_int32) for f in CUBE_TILING_FIELDS]
+
+
 _P = ctypes.c_void_p
 _I32, _U32, _I64, _U64, _U16, _U8, _F32 = (ctypes.c_int32, ctypes.c_uint32, ctypes.c_int64, ctypes.c_uint64,
                                           ctypes.c_uint16, ctypes.c_uint8, ctypes.c_float)
@@ -82,6 +95,7 @@ SIGNATURES = {
     "ascq_device_count": (_I32, []),
     "ascq_pack_quant_pre": (_U64, [_F32, _I32, _I32]),
     "ascq_matmul_create": (_I32, [ctypes.POINTER(_MatmulTypes), ctypes.POINTER(_P)]),
+    "ascq_matmul_init": (_I32, [_P, ctypes.POINTER(CubeTiling)]),
     "ascq_matmul_set_org_shape": (_I32, [_P, _I64, _I64, _I64]),
     "ascq_matmul_set_single_shape": (_I32, [_P, _I64, _I64, _I64]),
     "ascq_matmul_set_tail": (_I32, [_P, _I64, _I64, _I64]),
@@ -109,6 +123,9 @@ SIGNATURES = {
     "ascq_weight_pack": (_I32, [_P, _P, _I32, _I64, _I64, _I32, _P]),
     "ascq_antiquant_matmul": (_I32, [_P, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "ascq_quant_group_matmul": (_I32, [_P, _I32, _P, _P, _P, _I32, _P, _P, _I32, _I64, _I64, _I64, _I64, _I32, _P]),
+    "ascq_nz_size": (ctypes.c_size_t, [_I32, _I64, _I64, _I64]),
+    "ascq_nz_to_nd": (_I32, [_P, _P, _I32, _I64, _I64, _I64, _I32, _P]),
+    "ascq_nd_to_nz": (_I32, [_P, _P, _I32, _I64, _I64, _I64, _P]),
 }
 
 _lib = None
@@ -270,6 +287,31 @@ def quant_group_matmul(x: torch.Tensor, per_token_scale: torch.Tensor, w: torch.
 
 
 # ------------------------------------------------------------------------------------------
+# NZ fractal <-> ND
+# ------------------------------------------------------------------------------------------
+def nz_size(dtype: int, batch: int, rows: int, cols: int) -> int:
+    return int(lib().ascq_nz_size(dtype, batch, rows, cols))
+
+
+def nz_to_nd(src: torch.Tensor, dtype: int, batch: int, rows: int, cols: int, transpose_out: bool = False, out=None,
+             stream=None):
+    """NZ bytes -> ND [batch, rows, cols] (transpose_out: [batch, cols, rows]) as a uint8 tensor of that shape
+    times the element size"""
+    esize = {INT8: 1, UINT8: 1, FP8_E4M3: 1, FP8_E5M2: 1, F16: 2, BF16: 2, INT32: 4, F32: 4}[dtype]
+    shape = (batch, cols, rows * esize) if transpose_out else (batch, rows, cols * esize)
+    y = out if out is not None else torch.empty(shape, dtype=torch.uint8, device=src.device)
+    check(lib().ascq_nz_to_nd(_ptr(y), _ptr(src), dtype, batch, rows, cols, int(transpose_out), _stream(stream)),
+          "nz_to_nd")
+    return y
+
+
+def nd_to_nz(src: torch.Tensor, dtype: int, batch: int, rows: int, cols: int, out=None, stream=None):
+    y = out if out is not None else torch.empty(nz_size(dtype, batch, rows, cols), dtype=torch.uint8, device=src.device)
+    check(lib().ascq_nd_to_nz(_ptr(y), _ptr(src), dtype, batch, rows, cols, _stream(stream)), "nd_to_nz")
+    return y
+
+
+# ------------------------------------------------------------------------------------------
 # Matmul handle (mirrors AscendC::Matmul's call sequence)
 # ------------------------------------------------------------------------------------------
 class Matmul:
@@ -288,6 +330,9 @@ class Matmul:
         if h is not None and h.value and _lib is not None:
             _lib.ascq_matmul_destroy(h)
             self._h = None
+
+    def Init(self, tiling: CubeTiling):
+        check(lib().ascq_matmul_init(self._h, ctypes.byref(tiling)), "Init")
 
     def SetOrgShape(self, m: int, n: int, k: int):
         check(lib().ascq_matmul_set_org_shape(self._h, m, n, k), "SetOrgShape")

@@ -260,6 +260,18 @@ ascq_status ascq_matmul_create(const ascq_matmul_types* types, ascq_matmul_t* ou
     return ASCQ_OK;
 }
 
+ascq_status ascq_matmul_init(ascq_matmul_t h, const ascq_cube_tiling* t)
+{
+    if (!h || !t) return fail(ASCQ_E_INVALID_ARG, "matmul_init: null argument");
+    if (t->M <= 0 || t->N <= 0 || t->Ka <= 0) return fail(ASCQ_E_INVALID_ARG, "matmul_init: tiling shape must be positive");
+    if (t->Kb != t->Ka) return fail(ASCQ_E_INVALID_ARG, "matmul_init: Ka (%d) and Kb (%d) differ", t->Ka, t->Kb);
+    h->M = t->M;
+    h->N = t->N;
+    h->K = t->Ka;
+    h->sm = h->sn = h->sk = -1;
+    return ASCQ_OK;
+}
+
 ascq_status ascq_matmul_set_org_shape(ascq_matmul_t h, int64_t m, int64_t n, int64_t k)
 {
     if (!h) return fail(ASCQ_E_INVALID_ARG, "null handle");
@@ -753,6 +765,64 @@ ascq_status ascq_quant_group_matmul(void* y, int32_t out_type, const int8_t* x, 
     g.N = n;
     g.act = activation;
     return hip_status(ascq::launch_group_gemm(g, S(stream)), "quant_group_matmul");
+}
+
+// ------------------------------------------------------------------------------------------------
+// NZ fractal <-> ND
+// ------------------------------------------------------------------------------------------------
+namespace {
+int elem_bytes(int32_t dtype)
+{
+    switch (dtype) {
+    case ASCQ_DT_INT8:
+    case ASCQ_DT_UINT8:
+    case ASCQ_DT_FP8_E4M3:
+    case ASCQ_DT_FP8_E5M2: return 1;
+    case ASCQ_DT_F16:
+    case ASCQ_DT_BF16: return 2;
+    case ASCQ_DT_INT32:
+    case ASCQ_DT_F32: return 4;
+    default: return 0;
+    }
+}
+
+ascq_status check_nz_args(const char* what, const void* dst, const void* src, int32_t dtype, int64_t batch,
+                          int64_t rows, int64_t cols)
+{
+    if (!dst || !src) return fail(ASCQ_E_INVALID_ARG, "%s: null argument", what);
+    if (elem_bytes(dtype) == 0) return fail(ASCQ_E_UNSUPPORTED, "%s: unsupported element type %d", what, dtype);
+    if (batch <= 0 || rows <= 0 || cols <= 0) return fail(ASCQ_E_INVALID_ARG, "%s: shape must be positive", what);
+    if (ascq::nz_bytes(batch, rows, cols, elem_bytes(dtype)) >= ((size_t)1 << 40))
+        return fail(ASCQ_E_UNSUPPORTED, "%s: matrix too large", what);
+    return ASCQ_OK;
+}
+}  // namespace
+
+size_t ascq_nz_size(int32_t dtype, int64_t batch, int64_t rows, int64_t cols)
+{
+    const int e = elem_bytes(dtype);
+    if (e == 0 || batch <= 0 || rows <= 0 || cols <= 0) return 0;
+    return ascq::nz_bytes(batch, rows, cols, e);
+}
+
+ascq_status ascq_nz_to_nd(void* dst, const void* src, int32_t dtype, int64_t batch, int64_t rows, int64_t cols,
+                          int32_t transpose_out, void* stream)
+{
+    ascq_status s = check_nz_args("nz_to_nd", dst, src, dtype, batch, rows, cols);
+    if (s != ASCQ_OK) return s;
+    if (transpose_out && elem_bytes(dtype) != 1)
+        return fail(ASCQ_E_UNSUPPORTED, "nz_to_nd: transpose_out needs a 1-byte element type");
+    return hip_status(ascq::launch_nz_to_nd(dst, src, elem_bytes(dtype), batch, rows, cols, transpose_out ? 1 : 0,
+                                            S(stream)),
+                      "nz_to_nd");
+}
+
+ascq_status ascq_nd_to_nz(void* dst, const void* src, int32_t dtype, int64_t batch, int64_t rows, int64_t cols,
+                          void* stream)
+{
+    ascq_status s = check_nz_args("nd_to_nz", dst, src, dtype, batch, rows, cols);
+    if (s != ASCQ_OK) return s;
+    return hip_status(ascq::launch_nd_to_nz(dst, src, elem_bytes(dtype), batch, rows, cols, S(stream)), "nd_to_nz");
 }
 
 }  // extern "C"

@@ -96,6 +96,12 @@ hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st);
 hipError_t launch_transpose_i8(uint8_t* dst, const uint8_t* src, int64_t rows, int64_t cols, hipStream_t st);
 bool fp4_transpose_tiled(uint8_t* dst, const uint8_t* src, int64_t K, int64_t N, hipStream_t st, hipError_t* err);
 size_t mx_scale_workspace_bytes(int64_t M, int64_t N, int64_t K);
+// layout.hip: NZ fractal ([ceil(cols*esize/32)][ceil(rows/16)][16][32 bytes]) <-> ND, per matrix of a batch
+size_t nz_bytes(int64_t batch, int64_t rows, int64_t cols, int esize);
+hipError_t launch_nz_to_nd(void* dst, const void* src, int esize, int64_t batch, int64_t rows, int64_t cols,
+                           int transpose_out, hipStream_t st);
+hipError_t launch_nd_to_nz(void* dst, const void* src, int esize, int64_t batch, int64_t rows, int64_t cols,
+                           hipStream_t st);
 // transpose a [K, N] packed fp4 matrix (two per byte along N) into [N, K] (two per byte along K)
 hipError_t launch_fp4_transpose(uint8_t* dst, const uint8_t* src, int64_t K, int64_t N, hipStream_t st);
 

@@ -139,6 +139,23 @@ typedef struct {
 
 /* REGIST_MATMUL_OBJ + Init (matmul_intf.h:40; matmul.h:79-95) */
 ascq_status ascq_matmul_create(const ascq_matmul_types* types, ascq_matmul_t* out);
+
+/* The reference's host tiling result, TCubeTiling (include/adv_api/matmul/matmul_tilingdata.h:21-72): the same
+ * int32 fields in the same order, so host code that fills, copies or serialises one passes it unchanged.  Only
+ * the shape fields are read here; the rest describe the Ascend core split and buffers and are ignored. */
+typedef struct {
+    int32_t usedCoreNum, M, N, Ka, Kb, singleCoreM, singleCoreN, singleCoreK, baseM, baseN, baseK, depthA1, depthB1,
+        stepM, stepN, isBias, transLength, iterateOrder, shareMode, shareL1Size, shareL0CSize, shareUbSize, batchM,
+        batchN, singleBatchM, singleBatchN, stepKa, stepKb, depthAL1CacheUB, depthBL1CacheUB, dbL0A, dbL0B, dbL0C,
+        ALayoutInfoB, ALayoutInfoS, ALayoutInfoN, ALayoutInfoG, ALayoutInfoD, BLayoutInfoB, BLayoutInfoS,
+        BLayoutInfoN, BLayoutInfoG, BLayoutInfoD, CLayoutInfoB, CLayoutInfoS1, CLayoutInfoN, CLayoutInfoG,
+        CLayoutInfoS2, BatchNum, mxTypePara;
+} ascq_cube_tiling;
+
+/* Init(const TCubeTiling*) (matmul.h:79-95): the org shape becomes (M, N, Ka); Ka must equal Kb.  The per-core
+ * split (usedCoreNum, singleCoreM/N/K) is not applied: one IterateAll computes the whole org shape, which is
+ * what the reference's cores compute together (set_single_shape still restricts a call to a block). */
+ascq_status ascq_matmul_init(ascq_matmul_t h, const ascq_cube_tiling* tiling);
 /* SetOrgShape(orgM, orgN, orgK) (matmul.h:94): full matrix shape; sets the leading dimensions */
 ascq_status ascq_matmul_set_org_shape(ascq_matmul_t h, int64_t m, int64_t n, int64_t k);
 /* SetSingleShape / SetTail (matmul.h:110, :117): the block this call computes (defaults to org shape) */
@@ -288,6 +305,24 @@ ascq_status ascq_quant_group_matmul(void* y, int32_t out_type, const int8_t* x, 
                                     const int8_t* w, int32_t w_trans, const float* scale,
                                     const int64_t* group_list, int32_t list_type, int64_t num_groups, int64_t m,
                                     int64_t k, int64_t n, int32_t activation, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * NZ fractal <-> ND layout converters
+ * CubeFormat::NZ (include/adv_api/matmul/matmul_config.h:23-35): each [rows, cols] matrix of a batch is stored
+ * [ceil(cols / C0)][ceil(rows / 16)][16][C0], C0 = 32 bytes of elements (int8 / fp8: 32, f16 / bf16: 16,
+ * f32 / int32: 8) -- e.g. the group-matmul weights, weight.reshape([G, K/16, 16, N/32, 32]).transpose(0, 3, 1, 2, 4)
+ * (examples/01_simd_cpp_api/05_best_practices/03_fusion_compute/quant_group_matmul_high_performance/scripts/
+ * gen_data.py:62).  Device to device on `stream`.
+ * ------------------------------------------------------------------------------------------ */
+/* Bytes of the NZ form of `batch` [rows, cols] matrices of `dtype` (padding included); 0 on bad arguments. */
+size_t ascq_nz_size(int32_t dtype, int64_t batch, int64_t rows, int64_t cols);
+/* NZ -> ND [batch][rows][cols]; transpose_out = 1 (1-byte types) writes [batch][cols][rows] instead: NZ int8
+ * expert weights [G, K, N] become the K-contiguous [G, N, K] that ascq_quant_group_matmul takes with w_trans. */
+ascq_status ascq_nz_to_nd(void* dst, const void* src, int32_t dtype, int64_t batch, int64_t rows, int64_t cols,
+                          int32_t transpose_out, void* stream);
+/* ND [batch][rows][cols] -> NZ (padding written as zero) */
+ascq_status ascq_nd_to_nz(void* dst, const void* src, int32_t dtype, int64_t batch, int64_t rows, int64_t cols,
+                          void* stream);
 
 #ifdef __cplusplus
 }

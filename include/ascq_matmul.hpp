@@ -35,6 +35,8 @@ public:
     Matmul(const Matmul&) = delete;
     Matmul& operator=(const Matmul&) = delete;
 
+    // Init(const TCubeTiling*) / REGIST_MATMUL_OBJ(..., &tiling): the org shape from the tiling
+    void Init(const ascq_cube_tiling* tiling) { check(ascq_matmul_init(h_, tiling), "Init"); }
     void SetOrgShape(int64_t m, int64_t n, int64_t k) { check(ascq_matmul_set_org_shape(h_, m, n, k), "SetOrgShape"); }
     void SetSingleShape(int64_t m, int64_t n, int64_t k)
     {
@@ -78,6 +80,95 @@ public:
 
 private:
     ascq_matmul_t h_ = nullptr;
+};
+
+// Host tiling builder with the reference's call sequence (matmul_tiling::MultiCoreMatmulTiling,
+// include/adv_api/matmul/matmul_tiling_base.h:329-556): SetAType / SetBType / SetCType / SetBiasType / SetShape /
+// SetOrgShape / SetBias / SetDequantType / SetBufferSpace / GetTiling.  GetTiling returns -1, as the reference
+// does (impl/adv_api/tiling/matmul/matmul_tiling.cpp:28-35), when the description is incomplete or the type
+// combination has no kernel here; otherwise 0 and a tiling whose shape fields Matmul::Init reads.  The Ascend
+// buffer / core-split settings have no meaning for one gfx950 launch and are accepted and ignored.
+enum class TPosition { GM, VECIN, VECCALC, VECOUT, A1, A2, B1, B2, CO1, CO2, TSCM };
+enum class CubeFormat { ND, NZ, ZN, ZZ, NN, ND_ALIGN, SCALAR, VECTOR };
+enum class DequantType { SCALAR, TENSOR };
+
+class MultiCoreMatmulTiling {
+public:
+    MultiCoreMatmulTiling() = default;
+    int32_t SetDim(int32_t) { return 0; }
+    int32_t SetAType(TPosition, CubeFormat f, ascq_dtype t, bool isTrans = false) { return set(a_, f, t, isTrans); }
+    int32_t SetBType(TPosition, CubeFormat f, ascq_dtype t, bool isTrans = false) { return set(b_, f, t, isTrans); }
+    int32_t SetCType(TPosition, CubeFormat f, ascq_dtype t) { return set(c_, f, t, false); }
+    int32_t SetBiasType(TPosition, CubeFormat f, ascq_dtype t) { return set(bias_, f, t, false); }
+    int32_t SetDequantType(DequantType) { return 0; }
+    int32_t SetShape(int32_t m, int32_t n, int32_t k)
+    {
+        m_ = m;
+        n_ = n;
+        k_ = k;
+        return 0;
+    }
+    int32_t SetOrgShape(int32_t m, int32_t n, int32_t k) { return SetOrgShape(m, n, k, k); }
+    int32_t SetOrgShape(int32_t m, int32_t n, int32_t ka, int32_t kb)
+    {
+        om_ = m;
+        on_ = n;
+        oka_ = ka;
+        okb_ = kb;
+        return 0;
+    }
+    int32_t SetBias(bool isBias = false)
+    {
+        isBias_ = isBias;
+        return 0;
+    }
+    int32_t SetBufferSpace(int32_t = -1, int32_t = -1, int32_t = -1, int32_t = -1) { return 0; }
+    int32_t SetFixSplit(int32_t = -1, int32_t = -1, int32_t = -1) { return 0; }
+
+    int64_t GetTiling(ascq_cube_tiling& t) const
+    {
+        const int32_t M = om_ > 0 ? om_ : m_, N = on_ > 0 ? on_ : n_, Ka = oka_ > 0 ? oka_ : k_;
+        const int32_t Kb = okb_ > 0 ? okb_ : Ka;
+        if (!a_.set || !b_.set || !c_.set || M <= 0 || N <= 0 || Ka <= 0 || Ka != Kb) return -1;
+        if (m_ > M || n_ > N || k_ > Ka) return -1;
+        if (a_.fmt != CubeFormat::ND || b_.fmt != CubeFormat::ND || c_.fmt != CubeFormat::ND) return -1;
+        // the type combination must have a kernel: the library decides (a transient handle)
+        ascq_matmul_types ty{a_.type, b_.type, c_.type, bias_.set && isBias_ ? bias_.type : 0, 0, ASCQ_FORMAT_ND};
+        ascq_matmul_t h = nullptr;
+        if (ascq_matmul_create(&ty, &h) != ASCQ_OK) return -1;
+        ascq_matmul_destroy(h);
+        t = ascq_cube_tiling{};
+        t.usedCoreNum = 1;  // one launch covers the whole shape
+        t.M = M;
+        t.N = N;
+        t.Ka = Ka;
+        t.Kb = Kb;
+        t.singleCoreM = m_ > 0 ? m_ : M;
+        t.singleCoreN = n_ > 0 ? n_ : N;
+        t.singleCoreK = k_ > 0 ? k_ : Ka;
+        t.isBias = isBias_ ? 1 : 0;
+        t.BatchNum = 1;
+        return 0;
+    }
+
+private:
+    struct Desc {
+        bool set = false;
+        CubeFormat fmt = CubeFormat::ND;
+        int32_t type = 0;
+        bool trans = false;
+    };
+    static int32_t set(Desc& d, CubeFormat f, ascq_dtype t, bool trans)
+    {
+        d.set = true;
+        d.fmt = f;
+        d.type = t;
+        d.trans = trans;
+        return 0;
+    }
+    Desc a_, b_, c_, bias_;
+    int32_t m_ = -1, n_ = -1, k_ = -1, om_ = -1, on_ = -1, oka_ = -1, okb_ = -1;
+    bool isBias_ = false;
 };
 
 }  // namespace ascq

@@ -719,3 +719,42 @@ void oq_mx_quantize_fp4(uint8_t* packed, uint8_t* scales, const float* x, int64_
             }
         }
 }
+
+/* ------------------------------------------------------------------------ */
+/* NZ fractal <-> ND                                                         */
+/* ------------------------------------------------------------------------ */
+
+/* CubeFormat::NZ (include/adv_api/matmul/matmul_config.h:23-35), as the group-matmul generator writes its weights
+ * (quant_group_matmul_high_performance/scripts/gen_data.py:62: reshape [G, k/16, 16, n/32, 32], transpose
+ * (0, 3, 1, 2, 4)): element (r, c) of matrix b at byte
+ *   b * nz_mat + ((cb * r16 + r / 16) * 16 + r % 16) * 32 + (c * esize) % 32,   cb = (c * esize) / 32,
+ * r16 = ceil(rows / 16), nz_mat = ceil(cols * esize / 32) * r16 * 512.  Element by element, byte by byte. */
+static int64_t nz_index(int64_t b, int64_t r, int64_t cbyte, int64_t rows, int64_t cols_b)
+{
+    int64_t r16 = (rows + 15) / 16, c32 = (cols_b + 31) / 32;
+    int64_t cb = cbyte / 32;
+    return b * c32 * r16 * 512 + ((cb * r16 + r / 16) * 16 + r % 16) * 32 + cbyte % 32;
+}
+
+void oq_nz_to_nd(uint8_t* dst, const uint8_t* src, int esize, int64_t batch, int64_t rows, int64_t cols,
+                 int transpose_out)
+{
+    int64_t cols_b = cols * esize;
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t r = 0; r < rows; ++r)
+            for (int64_t c = 0; c < cols; ++c)
+                for (int e = 0; e < esize; ++e) {
+                    uint8_t v = src[nz_index(b, r, c * esize + e, rows, cols_b)];
+                    if (transpose_out) dst[(b * cols + c) * rows * esize + r * esize + e] = v;
+                    else dst[(b * rows + r) * cols_b + c * esize + e] = v;
+                }
+}
+
+void oq_nd_to_nz(uint8_t* dst, const uint8_t* src, int esize, int64_t batch, int64_t rows, int64_t cols)
+{
+    int64_t cols_b = cols * esize, r16 = (rows + 15) / 16, c32 = (cols_b + 31) / 32;
+    memset(dst, 0, (size_t)(batch * c32 * r16 * 512));
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t r = 0; r < rows; ++r)
+            for (int64_t cb = 0; cb < cols_b; ++cb) dst[nz_index(b, r, cb, rows, cols_b)] = src[(b * rows + r) * cols_b + cb];
+}

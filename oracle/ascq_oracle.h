@@ -122,4 +122,9 @@ void oq_mx_quantize_fp4(uint8_t* packed, uint8_t* scales, const float* x, int64_
 #ifdef __cplusplus
 }
 #endif
+/* NZ fractal ([ceil(cols*esize/32)][ceil(rows/16)][16][32 bytes] per matrix) <-> ND, byte by byte */
+void oq_nz_to_nd(uint8_t* dst, const uint8_t* src, int esize, int64_t batch, int64_t rows, int64_t cols,
+                 int transpose_out);
+void oq_nd_to_nz(uint8_t* dst, const uint8_t* src, int esize, int64_t batch, int64_t rows, int64_t cols);
+
 #endif

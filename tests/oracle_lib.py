@@ -70,6 +70,8 @@ def lib() -> ctypes.CDLL:
             "oq_group_matmul": (None, [_P, ctypes.c_int, _P, _P, _P, ctypes.c_int, _P, _P, ctypes.c_int, _I64, _I64,
                                        _I64, _I64, ctypes.c_int]),
             "oq_faster_gelu": (ctypes.c_float, [ctypes.c_float]),
+            "oq_nz_to_nd": (None, [_P, _P, ctypes.c_int, _I64, _I64, _I64, ctypes.c_int]),
+            "oq_nd_to_nz": (None, [_P, _P, ctypes.c_int, _I64, _I64, _I64]),
             "oq_mx_matmul": (None, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_int, ctypes.c_int, _P, _I64, _P]),
             "oq_mx_quantize_fp4": (None, [_P, _P, _P, _I64, _I64]),
@@ -128,6 +130,24 @@ def matmul_fp8(A, B, a_fmt, b_fmt, bias=None, out_type=F32, trans_a=False, trans
     lib().oq_matmul_fp8(_p(A), _p(B), a_fmt, b_fmt, _p(b), _p(out), out_type, M, N, K, int(trans_a), int(trans_b),
                         int(use_q), _p(qv), int(qscalar), _p(exact), _p(absd), _p(bmax))
     return out, exact, absd, bmax
+
+
+def nz_size(esize, batch, rows, cols):
+    return batch * ((cols * esize + 31) // 32) * ((rows + 15) // 16) * 512
+
+
+def nz_to_nd(nz, esize, batch, rows, cols, transpose_out=False):
+    nz = np.ascontiguousarray(nz, np.uint8).reshape(-1)
+    out = np.empty(batch * rows * cols * esize, np.uint8)
+    lib().oq_nz_to_nd(_p(out), _p(nz), esize, batch, rows, cols, int(transpose_out))
+    return out.reshape((batch, cols, rows * esize) if transpose_out else (batch, rows, cols * esize))
+
+
+def nd_to_nz(nd, esize, batch, rows, cols):
+    nd = np.ascontiguousarray(nd).view(np.uint8).reshape(-1)
+    out = np.empty(nz_size(esize, batch, rows, cols), np.uint8)
+    lib().oq_nd_to_nz(_p(out), _p(nd), esize, batch, rows, cols)
+    return out
 
 
 def mm_requant(acc, qvec=None, qscalar=0):

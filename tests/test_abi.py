@@ -154,3 +154,31 @@ def test_header_comment_cites_reference_or_is_library_utility(name):
     if name in utility:
         return
     assert re.search(r"\.(h|asc|md|cpp|py):\d+", block), f"{name}: no reference file:line nearby"
+
+
+def test_tiling_shim_compiles_and_behaves(tmp_path):
+    """include/ascq_matmul.hpp's TCubeTiling mirror, MultiCoreMatmulTiling and Matmul::Init, compiled with g++
+    as reference-style host code and run on the CPU (tests/cpp/tiling_shim.cpp)"""
+    exe = tmp_path / "tiling_shim"
+    libdir = Path(ascq.LIB_PATH).parent
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-I", str(ROOT / "include"), str(ROOT / "tests" / "cpp" / "tiling_shim.cpp"),
+                    "-L", str(libdir), "-lascq", f"-Wl,-rpath,{libdir}", "-o", str(exe)], check=True, capture_output=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+def test_cube_tiling_struct_matches_header():
+    assert ctypes.sizeof(ascq.CubeTiling) == 200
+    assert ascq.CubeTiling.Ka.offset == 12 and ascq.CubeTiling.mxTypePara.offset == 196
+
+
+def test_nz_argument_checks():
+    L = ascq.lib()
+    d = ctypes.c_void_p(0x1000)
+    _err(L.ascq_nz_to_nd(d, d, ascq.U64, 1, 16, 32, 0, None), ascq.E_UNSUPPORTED)
+    _err(L.ascq_nz_to_nd(d, d, ascq.F16, 1, 16, 32, 1, None), ascq.E_UNSUPPORTED)  # transpose needs 1-byte
+    _err(L.ascq_nd_to_nz(d, d, ascq.INT8, 1, 0, 32, None), ascq.E_INVALID_ARG)
+    _err(L.ascq_nz_to_nd(None, d, ascq.INT8, 1, 16, 32, 0, None), ascq.E_INVALID_ARG)
+    assert L.ascq_nz_size(ascq.INT8, 2, 17, 33) == 2 * 2 * 2 * 512
+    assert L.ascq_nz_size(ascq.F16, 1, 16, 16) == 512
+    assert L.ascq_nz_size(ascq.U64, 1, 16, 16) == 0

@@ -657,3 +657,32 @@ def test_group_matmul_gelu_golden_within_reference_tolerance():
     assert ref_verify(y.view(np.float16), f["golden"], err_tol=1e-4)
     y0 = O.group_matmul(f["x"], f["pts"], f["weight"], f["scale"], f["group_list"], 1, G, m, k, n, O.F16, act=0)
     assert not ref_verify(y0.view(np.float16), f["golden"], err_tol=1e-4)
+
+
+# --------------------------------------------------------------------------- NZ fractal layout
+@pytest.mark.parametrize("G,K,N", [(3, 64, 96), (1, 16, 32)])
+def test_nz_to_nd_matches_generator_layout(G, K, N):
+    """the group-matmul generator's NZ weights, weight.reshape([G, K/16, 16, N/32, 32]).transpose(0, 3, 1, 2, 4)
+    (gen_data.py:62), back to ND [G, K, N] and to K-contiguous [G, N, K]; and ND -> NZ reproduces them"""
+    rng = np.random.default_rng(808)
+    w = rng.integers(-128, 128, (G, K, N)).astype(np.int8)
+    nz = np.ascontiguousarray(w.reshape(G, K // 16, 16, N // 32, 32).transpose(0, 3, 1, 2, 4))
+    assert np.array_equal(O.nz_to_nd(nz, 1, G, K, N).view(np.int8), w)
+    assert np.array_equal(O.nz_to_nd(nz, 1, G, K, N, transpose_out=True).view(np.int8), w.transpose(0, 2, 1))
+    assert np.array_equal(O.nd_to_nz(w, 1, G, K, N), nz.reshape(-1).view(np.uint8))
+
+
+@pytest.mark.parametrize("dt,esize", [(np.int8, 1), (np.float16, 2), (np.float32, 4)])
+def test_nz_padding_and_element_sizes(dt, esize):
+    """ragged rows / columns: NZ pads to 16 rows and 32-byte column blocks (zeros), C0 = 32 / element bytes"""
+    rng = np.random.default_rng(809)
+    B, R, C = 2, 37, 45
+    nd = rng.integers(-100, 100, (B, R, C)).astype(dt)
+    c0 = 32 // esize
+    Rp, Cp = -(-R // 16) * 16, -(-C // c0) * c0
+    pad = np.zeros((B, Rp, Cp), dt)
+    pad[:, :R, :C] = nd
+    ref = np.ascontiguousarray(pad.reshape(B, Rp // 16, 16, Cp // c0, c0).transpose(0, 3, 1, 2, 4))
+    nz = O.nd_to_nz(nd, esize, B, R, C)
+    assert np.array_equal(nz, ref.reshape(-1).view(np.uint8))
+    assert np.array_equal(O.nz_to_nd(nz, esize, B, R, C).view(dt).reshape(B, R, C), nd)
