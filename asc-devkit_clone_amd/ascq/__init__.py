@@ -93,6 +93,7 @@ SIGNATURES = {
     "ascq_last_error": (ctypes.c_char_p, []),
     "ascq_version": (ctypes.c_char_p, []),
     "ascq_device_count": (_I32, []),
+    "ascq_set_launch_events": (_I32, [_P, _P]),
     "ascq_pack_quant_pre": (_U64, [_F32, _I32, _I32]),
     "ascq_matmul_create": (_I32, [ctypes.POINTER(_MatmulTypes), ctypes.POINTER(_P)]),
     "ascq_matmul_init": (_I32, [_P, ctypes.POINTER(CubeTiling)]),

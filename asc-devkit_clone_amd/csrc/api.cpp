@@ -15,6 +15,7 @@
 namespace {
 
 thread_local std::string g_err;
+thread_local ascq::LaunchEvents g_launch_events;
 
 ascq_status fail(ascq_status code, const char* fmt, ...)
 {
@@ -199,9 +200,20 @@ __global__ void fill_u16_kernel(uint16_t* p, int64_t n, uint16_t v)
 
 }  // namespace
 
+ascq::LaunchEvents& ascq::launch_events() { return g_launch_events; }
+
 extern "C" {
 
 const char* ascq_last_error(void) { return g_err.c_str(); }
+
+ascq_status ascq_set_launch_events(void* start, void* stop)
+{
+    if ((start == nullptr) != (stop == nullptr))
+        return fail(ASCQ_E_INVALID_ARG, "set_launch_events: give both events or neither");
+    g_launch_events.start = reinterpret_cast<hipEvent_t>(start);
+    g_launch_events.stop = reinterpret_cast<hipEvent_t>(stop);
+    return ASCQ_OK;
+}
 
 const char* ascq_version(void) { return "ascq 0.1 (gfx950)"; }
 

@@ -133,7 +133,7 @@ static hipError_t launch_f8_tiled(const GemmF8Args& a, hipStream_t st)
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
+    launch_k((gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
     return hipGetLastError();
 }
 
@@ -168,7 +168,7 @@ hipError_t launch_gemm_f8(const GemmF8Args& a, hipStream_t st)
     int64_t blocks = (a.M * a.N + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(gemm_f8_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    launch_k(gemm_f8_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

@@ -188,7 +188,7 @@ static hipError_t launch_tiled(const GemmI8Args& a, hipStream_t st)
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
+    launch_k((gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
     return hipGetLastError();
 }
 
@@ -208,7 +208,7 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
     int64_t blocks = (a.M * a.N + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(gemm_i8_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    launch_k(gemm_i8_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
@@ -251,7 +251,7 @@ static hipError_t launch_group_tiled(const GroupGemmArgs& a, hipStream_t st)
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>), dim3((unsigned)slots), dim3(T::NT), T::LDS_BYTES,
+    launch_k((group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>), dim3((unsigned)slots), dim3(T::NT), T::LDS_BYTES,
                        st, a);
     return hipGetLastError();
 }
@@ -272,7 +272,7 @@ hipError_t launch_group_gemm(const GroupGemmArgs& a, hipStream_t st)
     int64_t blocks = (a.M * a.N + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(group_gemm_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    launch_k(group_gemm_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

@@ -340,10 +340,10 @@ static void launch_aq2(uint16_t* y, const uint16_t* x, const void* wp, const uin
     const unsigned blocks = (unsigned)((N / 16 + NBW - 1) / NBW);
     const size_t lds = XLDS ? (size_t)(M * K * 2 + 16) : 0;
     if (g % KT == 0)
-        hipLaunchKernelGGL((antiquant_gemm_kernel<MT, NBW, KSPLIT, TPW, INT4, HAS_OFF, true, XLDS>), dim3(blocks),
+        launch_k((antiquant_gemm_kernel<MT, NBW, KSPLIT, TPW, INT4, HAS_OFF, true, XLDS>), dim3(blocks),
                            dim3(KSPLIT * 64), lds, st, y, x, (const uint8_t*)wp, scale, offset, M, N, K, g);
     else
-        hipLaunchKernelGGL((antiquant_gemm_kernel<MT, NBW, KSPLIT, TPW, INT4, HAS_OFF, false, XLDS>), dim3(blocks),
+        launch_k((antiquant_gemm_kernel<MT, NBW, KSPLIT, TPW, INT4, HAS_OFF, false, XLDS>), dim3(blocks),
                            dim3(KSPLIT * 64), lds, st, y, x, (const uint8_t*)wp, scale, offset, M, N, K, g);
 }
 

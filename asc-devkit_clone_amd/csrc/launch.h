@@ -3,10 +3,31 @@
 // unless its comment says so.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace ascq {
+
+// One-shot kernel timing hook (ascq_set_launch_events): the next launch_k on this thread records the two events
+// at its dispatch's start and end -- hipExtLaunchKernelGGL binds them to the dispatch itself, so no marker packet
+// lands between kernels -- and clears them; without events launch_k is a plain launch.  Compute kernels go through
+// launch_k, helper kernels (layout transposes, scale rearrangement) do not, so an entry point's events time its
+// main kernel.
+struct LaunchEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchEvents& launch_events();  // thread-local; api.cpp
+
+template <typename F, typename... Args>
+inline hipError_t launch_k(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t st, Args... args)
+{
+    LaunchEvents& e = launch_events();
+    const hipEvent_t a = e.start, b = e.stop;
+    e = LaunchEvents{};
+    hipExtLaunchKernelGGL(kernel, grid, block, shm, st, a, b, 0u, args...);
+    return hipGetLastError();
+}
 
 // quant.hip
 hipError_t launch_quant_dynamic_per_token(int8_t* q, float* scale_out, const void* x, int src_type, uint32_t m,

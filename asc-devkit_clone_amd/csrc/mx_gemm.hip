@@ -176,7 +176,7 @@ static hipError_t launch_mx_tiled(const MxGemmArgs& a, hipStream_t st)
         attr = true;
     }
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
-    hipLaunchKernelGGL((mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a,
+    launch_k((mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a,
                        sa_sm, sb_sm);
     return hipGetLastError();
 }

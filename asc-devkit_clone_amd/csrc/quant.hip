@@ -261,9 +261,9 @@ static hipError_t launch_dyn_row(const void* x, int8_t* q, float* s, uint32_t m,
     dim3 grid(m), block(256);
 #define ASCQ_DYN(V)                                                                                                   \
     if (chunks <= 256u * V) {                                                                                         \
-        if (bf16) hipLaunchKernelGGL((quant_dyn_row_kernel<V, MODE, true>), grid, block, 0, st, (const u32x4*)x,     \
+        if (bf16) launch_k((quant_dyn_row_kernel<V, MODE, true>), grid, block, 0, st, (const u32x4*)x,     \
                                      (u32x2*)q, s, chunks);                                                           \
-        else hipLaunchKernelGGL((quant_dyn_row_kernel<V, MODE, false>), grid, block, 0, st, (const u32x4*)x,         \
+        else launch_k((quant_dyn_row_kernel<V, MODE, false>), grid, block, 0, st, (const u32x4*)x,         \
                                 (u32x2*)q, s, chunks);                                                                \
         return hipGetLastError();                                                                                     \
     }
@@ -293,7 +293,7 @@ hipError_t launch_quant_dynamic_per_token(int8_t* q, float* scale_out, const voi
     }
     dim3 grid(m), block(256);
     switch (round_mode) {
-#define ASCQ_G(MD) hipLaunchKernelGGL((quant_dyn_generic_kernel<MD>), grid, block, 0, st, x, q, scale_out, n, src_type); break;
+#define ASCQ_G(MD) launch_k((quant_dyn_generic_kernel<MD>), grid, block, 0, st, x, q, scale_out, n, src_type); break;
     case RM_FLOOR: ASCQ_G(RM_FLOOR)
     case RM_CEIL: ASCQ_G(RM_CEIL)
     case RM_ROUND: ASCQ_G(RM_ROUND)
@@ -310,9 +310,9 @@ hipError_t launch_quant_per_token(int8_t* q, const void* x, int src_type, const 
     int64_t total = (int64_t)m * n;
     dim3 grid(grid_for(total)), block(256);
 #define ASCQ_PT(MD)                                                                                                 \
-    if (offset) hipLaunchKernelGGL((quant_per_token_kernel<MD, true>), grid, block, 0, st, x, q, scale, offset,     \
+    if (offset) launch_k((quant_per_token_kernel<MD, true>), grid, block, 0, st, x, q, scale, offset,     \
                                    total, n, src_type);                                                             \
-    else hipLaunchKernelGGL((quant_per_token_kernel<MD, false>), grid, block, 0, st, x, q, scale, offset, total, n, \
+    else launch_k((quant_per_token_kernel<MD, false>), grid, block, 0, st, x, q, scale, offset, total, n, \
                             src_type);                                                                              \
     break;
     switch (round_mode) {
@@ -331,7 +331,7 @@ hipError_t launch_quant_legacy(int8_t* q, const void* x, int src_type, const uin
                                uint32_t scale_count, hipStream_t st)
 {
     dim3 grid(grid_for(cal_count)), block(256);
-    hipLaunchKernelGGL(quant_legacy_f16_kernel, grid, block, 0, st, x, q, scale, offset, scale_scalar, offset_scalar,
+    launch_k(quant_legacy_f16_kernel, grid, block, 0, st, x, q, scale, offset, scale_scalar, offset_scalar,
                        (int64_t)cal_count, scale_count, src_type);
     return hipGetLastError();
 }
@@ -347,13 +347,13 @@ hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, 
         const uint32_t segs = (upr + 256 * U - 1) / (256 * U);
         const uint64_t blocks = (uint64_t)m * segs;
         if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
-        hipLaunchKernelGGL(dequant_i8_token_f16_kernel<U>, dim3((unsigned)blocks), dim3(256), 0, st,
+        launch_k(dequant_i8_token_f16_kernel<U>, dim3((unsigned)blocks), dim3(256), 0, st,
                            (const u32x2*)src, (const float*)scale, (u32x4*)y, upr, segs);
         return hipGetLastError();
     }
     uint32_t cols = policy == 1 ? cal_count : n;
     dim3 grid(grid_for((int64_t)m * cols)), block(256);
-    hipLaunchKernelGGL(dequant_generic_kernel, grid, block, 0, st, y, dst_type, src, src_type, scale, scale_type,
+    launch_k(dequant_generic_kernel, grid, block, 0, st, y, dst_type, src, src_type, scale, scale_type,
                        scale_scalar, policy, m, n, cols);
     return hipGetLastError();
 }
@@ -363,7 +363,7 @@ hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_ty
                             hipStream_t st)
 {
     dim3 grid(grid_for((int64_t)K * N)), block(256);
-    hipLaunchKernelGGL(antiquant_kernel, grid, block, 0, st, dst, dst_type, src, src_type, (const uint16_t*)offset,
+    launch_k(antiquant_kernel, grid, block, 0, st, dst, dst_type, src, src_type, (const uint16_t*)offset,
                        (const uint16_t*)scale, K, N, g, is_transpose, arith);
     return hipGetLastError();
 }

@@ -90,6 +90,11 @@ const char* ascq_last_error(void);
 const char* ascq_version(void);
 /* Number of HIP devices visible (0 without a GPU); makes no other HIP call. */
 int32_t ascq_device_count(void);
+/* Kernel timing hook, no counterpart in the reference (for benchmarks and profilers that need a kernel's own
+ * duration without marker packets between kernels): start / stop are hipEvent_t handles (both or neither); the
+ * next entry point called on this thread records them at the start and end of its main kernel's dispatch
+ * (hipExtLaunchKernelGGL), then the hook clears itself. */
+ascq_status ascq_set_launch_events(void* start, void* stop);
 
 /* Pack an fp32 multiplier, a 9-bit offset and the sign flag into a QUANT_PRE word
  * (docs/zh/api/SIMD-API/c_api/cube_datamove/cube_store_key_features/accompanying_quantization.md:79-103;

@@ -212,3 +212,31 @@ def test_config2_full_size_quant_dequant(ascq_gpu, oracle):
     assert np.abs(qn.astype(np.int32)).max() <= 127
     y_ref = O.dequant(q_ref, O.INT8, s_ref, O.F32, O.PER_TOKEN, O.F16)
     np.testing.assert_array_equal(y.cpu().numpy().view(np.uint16), y_ref)
+
+
+def test_launch_events_time_the_main_kernel(ascq_gpu):
+    """ascq_set_launch_events: the next entry point's kernel is launched with the two events bound to its
+    dispatch; they then hold a positive elapsed time, and the hook is one-shot (a second call leaves it clear)"""
+    import ctypes
+    from pathlib import Path
+
+    p = Path(torch.__file__).resolve().parent / "lib" / "libamdhip64.so"
+    hip = ctypes.CDLL(str(p) if p.exists() else "libamdhip64.so.7")
+    hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipEventCreate(ctypes.byref(a)) == 0 and hip.hipEventCreate(ctypes.byref(b)) == 0
+    x = torch.randn((2048, 4096), device="cuda").half()
+    L = ascq_gpu.lib()
+    assert L.ascq_set_launch_events(a, None) == ascq_gpu.E_INVALID_ARG  # both or neither
+    assert L.ascq_set_launch_events(a, b) == 0
+    q, s = ascq_gpu.quant_dynamic_per_token(x)
+    q2, s2 = ascq_gpu.quant_dynamic_per_token(x)  # not timed: the hook cleared itself
+    torch.cuda.synchronize()
+    ms = ctypes.c_float()
+    assert hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+    assert 0.0 < ms.value < 50.0
+    assert torch.equal(q, q2) and torch.equal(s, s2)
+    hip.hipEventDestroy(a)
+    hip.hipEventDestroy(b)
