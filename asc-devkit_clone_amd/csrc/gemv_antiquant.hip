@@ -126,6 +126,14 @@ __device__ __forceinline__ h8 dequant8(uint32_t w0, uint32_t w1, h2 off, h2 sc, 
     return out;
 }
 
+// s_waitcnt vmcnt(N) with the other counters left alone (vmcnt[3:0] | expcnt << 4 | lgkmcnt << 8 | vmcnt[5:4] << 14)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_aq()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 typedef __amdgpu_buffer_rsrc_t aq_rsrc_t;
 constexpr uint32_t AQ_OOB = 0x80000000u;  // out-of-range buffer offset: the load returns zeros
 
@@ -333,6 +341,179 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
         }
 }
 
+// Small-batch form (4 < M <= 64, group size a multiple of 128).  The activation tile x[0:16 MT, k0:k0 + 128 KSW]
+// of each round is copied global -> LDS by buffer loads with an LDS destination (no registers) into a ring of ST
+// stages, ST - 1 rounds ahead, and shared by all waves of the workgroup; wave (s, kw) owns 16-column strip s of the
+// workgroup's NS strips and k tile (round * KSW + kw), whose weight tile (with its scale / offset) is loaded into a
+// register ring ST - 1 rounds ahead as well.  Every wave issues the same number of memory operations per round, so
+// one s_waitcnt vmcnt with a constant threshold plus one barrier per round make a stage visible and free the
+// stage read in the previous round.  Each 16-byte chunk c of row r is stored at chunk c ^ (r % 16) of its LDS
+// row (the swizzle is applied to the global address of the copy), so the 16 rows of an MFMA fragment read hit 16
+// distinct bank groups.  The KSW partial 16x16 tiles of a strip are summed through LDS in a fixed order.
+template <int MT, int NS, int KSW, int ST, bool INT4, bool HAS_OFF>
+struct AqDma {
+    static constexpr int NW = NS * KSW, NT = NW * 64;
+    static constexpr int ROWS = 16 * MT;
+    static constexpr int ROWB = KSW * KT * 2;           // LDS bytes per staged row (one round)
+    static constexpr int CH = ROWB / 16;                 // 16-byte chunks per row
+    static constexpr int SLOT = ROWS * ROWB;             // one stage
+    static constexpr int CPW = 4 * MT / NS;              // 1 KiB copies per wave per round
+    static constexpr int WV = INT4 ? 1 : 2;              // 16-byte weight loads per lane per tile
+    static constexpr int WL = WV + (HAS_OFF ? 2 : 1);    // vmem operations per wave per round besides the copies
+    static constexpr int IN_FLIGHT = (ST - 2) * (CPW + WL);
+    static constexpr int RED = (KSW - 1) * NS * MT * 64 * 16;
+    static constexpr int LDS = ST * SLOT > RED ? ST * SLOT : RED;
+    static_assert((4 * MT) % NS == 0 && CPW >= 1, "copies split evenly over the waves");
+    static_assert(CH >= 16 && (CH & (CH - 1)) == 0, "swizzle needs 16+ chunks per row, a power of two");
+    static_assert(ST >= 3 && IN_FLIGHT < 64 && LDS <= 160 * 1024, "stages");
+};
+
+template <int MT, int NS, int KSW, int ST, bool INT4, bool HAS_OFF, bool ROT = false>
+__global__ __launch_bounds__(NS * KSW * 64) void aq_dma_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
+                                                               const uint8_t* __restrict__ wp,
+                                                               const uint16_t* __restrict__ scale,
+                                                               const uint16_t* __restrict__ offset, int64_t M,
+                                                               int64_t N, int64_t K, int64_t g, int64_t ldx)
+{
+    using P = AqDma<MT, NS, KSW, ST, INT4, HAS_OFF>;
+    constexpr int TILE_BYTES = INT4 ? 1024 : 2048;
+    constexpr int LANE_BYTES = INT4 ? 16 : 32;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[P::LDS];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int s = wave / KSW, kw = wave % KSW;
+    const int64_t KB = K / KT, NBT = N / 16;
+    const int64_t nb = (int64_t)blockIdx.x * NS + s;
+    const int col_in = lane & 15, kq = lane >> 4;
+    const aq_rsrc_t rw = aq_rsrc(wp, (uint64_t)K * N / (INT4 ? 2 : 1));
+    const aq_rsrc_t rx = aq_rsrc(x, (uint64_t)((M - 1) * ldx + K) * 2);
+    const aq_rsrc_t rs = aq_rsrc(scale, (uint64_t)((K + g - 1) / g) * N * 2);
+    const aq_rsrc_t ro = aq_rsrc(HAS_OFF ? offset : scale, (uint64_t)((K + g - 1) / g) * N * 2);
+    const uint32_t magic = half_magic_vgpr();
+    const int64_t rounds = (KB + KSW - 1) / KSW;
+    const int64_t rot = ROT ? (int64_t)((blockIdx.x * 5u) % (uint32_t)rounds) : 0;
+    // round r reads k block (r + rot) mod rounds; rounds past the end read zeros
+    auto phys = [&](int64_t r) -> int64_t {
+        if (r >= rounds) return KB;  // past every k block
+        const int64_t q = r + rot;
+        return q >= rounds ? q - rounds : q;
+    };
+
+    v4f acc[MT];
+#pragma unroll
+    for (int a = 0; a < MT; ++a) acc[a] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    // x copies of round r into stage `slot`: copy j of this wave covers chunks 64 (wave CPW + j) .. + 63
+    auto issue_x = [&](int64_t r, int slot) {
+#pragma unroll
+        for (int j = 0; j < P::CPW; ++j) {
+            const int gcopy = wave * P::CPW + j;
+            const int q = gcopy * 64 + lane;
+            const int row = q / P::CH, p = q % P::CH;
+            const int c = p ^ (row & 15);  // logical chunk held at physical chunk p
+            const int64_t k = phys(r) * KSW * KT + c * 8;
+            const uint32_t off = (row < M && k < K) ? (uint32_t)((row * ldx + k) * 2) : AQ_OOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(smem + slot * P::SLOT + gcopy * 1024),
+                                                     16, off, 0, 0, 0);
+        }
+    };
+    struct WTile {
+        u32x4 w[P::WV];
+        uint32_t sc, of;
+    };
+    auto load_w = [&](int64_t r, WTile& t) {
+        const int64_t kb = phys(r) * KSW + kw;
+        const bool ok = kb < KB && nb < NBT;
+        const uint32_t off = ok ? (uint32_t)((nb * KB + kb) * TILE_BYTES + lane * LANE_BYTES) : AQ_OOB;
+#pragma unroll
+        for (int v = 0; v < P::WV; ++v) t.w[v] = __builtin_amdgcn_raw_buffer_load_b128(rw, off + 16 * v, 0, 0);
+        const uint32_t so = ok ? (uint32_t)((((kb * KT) / g) * N + nb * 16 + col_in) * 2) : AQ_OOB;
+        t.sc = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0);
+        if constexpr (HAS_OFF) t.of = __builtin_amdgcn_raw_buffer_load_b16(ro, so, 0, 0);
+        else t.of = 0u;
+    };
+    auto compute = [&](int slot, const WTile& t) {
+        const uint8_t* xb = smem + slot * P::SLOT;
+        const _Float16 sv = bits_h((uint16_t)t.sc), ov = bits_h((uint16_t)t.of);
+        const h2 s2 = (h2){sv, sv}, o2 = (h2){ov, ov};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t w0, w1 = 0;
+            if constexpr (INT4) {
+                w0 = t.w[0][j];
+            } else {
+                w0 = t.w[j >> 1][(j & 1) * 2];
+                w1 = t.w[j >> 1][(j & 1) * 2 + 1];
+            }
+            const h8 bf = dequant8<INT4, HAS_OFF>(w0, w1, o2, s2, magic);
+            const int c = kw * 16 + 4 * j + kq;  // logical chunk of this lane's 8 k values
+#pragma unroll
+            for (int a = 0; a < MT; ++a) {
+                const int row = 16 * a + col_in;
+                const h8 xa = *(const h8*)(xb + row * P::ROWB + (c ^ (row & 15)) * 16);
+                acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, bf, acc[a], 0, 0, 0);
+            }
+        }
+    };
+
+    WTile wt[ST];
+    // prologue: rounds 0 .. ST - 2 in flight
+#pragma unroll
+    for (int r = 0; r < ST - 1; ++r) {
+        issue_x(r, r);
+        load_w(r, wt[r]);
+    }
+    // round r: its stage has landed (this wave's copies: vmcnt; everyone's: the barrier, which also frees the
+    // stage read in round r - 1), then round r + ST - 1 is issued into that freed stage, then round r computes
+    for (int64_t r0 = 0; r0 < rounds; r0 += ST) {
+#pragma unroll
+        for (int u = 0; u < ST; ++u) {
+            const int64_t r = r0 + u;
+            if (r < rounds) {
+                __builtin_amdgcn_sched_barrier(0);
+                wait_vmcnt_aq<P::IN_FLIGHT>();
+                __builtin_amdgcn_sched_barrier(0);
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                __builtin_amdgcn_s_barrier();
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                __builtin_amdgcn_sched_barrier(0);
+                // the next round's operations are always issued (out-of-range ones read zeros), so every wave
+                // keeps the same number in flight and the vmcnt threshold stays exact
+                issue_x(r + ST - 1, (u + ST - 1) % ST);
+                load_w(r + ST - 1, wt[(u + ST - 1) % ST]);
+                __builtin_amdgcn_sched_barrier(0);
+                compute(u, wt[u]);
+            }
+        }
+    }
+    wait_vmcnt_aq<0>();  // no copy may still target LDS when it is reused below or the wave ends
+    __syncthreads();
+
+    if constexpr (KSW > 1) {
+        v4f* red = (v4f*)smem;  // [KSW - 1][NS][MT][64]
+        if (kw > 0) {
+#pragma unroll
+            for (int a = 0; a < MT; ++a) red[(((kw - 1) * NS + s) * MT + a) * 64 + lane] = acc[a];
+        }
+        __syncthreads();
+        if (kw != 0) return;
+#pragma unroll
+        for (int w = 0; w < KSW - 1; ++w)
+#pragma unroll
+            for (int a = 0; a < MT; ++a) acc[a] += red[((w * NS + s) * MT + a) * 64 + lane];
+    }
+    if (nb >= NBT) return;
+    const int64_t n = nb * 16 + col_in;
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t m = 16 * a + 4 * kq + i;
+            if (m < M) y[m * N + n] = f32_to_f16_sat(acc[a][i]);
+        }
+}
+
 template <int MT, int NBW, int KSPLIT, int TPW, bool INT4, bool HAS_OFF, bool XLDS>
 static void launch_aq2(uint16_t* y, const uint16_t* x, const void* wp, const uint16_t* scale, const uint16_t* offset,
                        int64_t g, int64_t M, int64_t N, int64_t K, hipStream_t st)
@@ -360,6 +541,21 @@ static void launch_aq(uint16_t* y, const uint16_t* x, const void* wp, bool int4,
     }
 }
 
+template <int MT, int NS, int KSW, int ST, bool ROT>
+static void launch_dma(uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
+                       const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, hipStream_t st)
+{
+    const dim3 grid((unsigned)((N / 16 + NS - 1) / NS)), block(NS * KSW * 64);
+    const uint8_t* w = (const uint8_t*)wp;
+    if (int4) {
+        if (offset) launch_k((aq_dma_kernel<MT, NS, KSW, ST, true, true, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K);
+        else launch_k((aq_dma_kernel<MT, NS, KSW, ST, true, false, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K);
+    } else {
+        if (offset) launch_k((aq_dma_kernel<MT, NS, KSW, ST, false, true, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K);
+        else launch_k((aq_dma_kernel<MT, NS, KSW, ST, false, false, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K);
+    }
+}
+
 // M is processed in chunks of 64 rows (4 m tiles); decode shapes are a single launch.  The packed weight,
 // x and the scales must each stay below 2^31 bytes (buffer offsets; checked by the caller).
 hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* wp, int w_type, const uint16_t* scale,
@@ -372,11 +568,22 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
         const int64_t mc = (M - m0) < 64 ? (M - m0) : 64;
         const uint16_t* xc = x + m0 * K;
         uint16_t* yc = y + m0 * N;
-        // decode batches: int4 stages x in LDS (4 waves x 8 k tiles measured fastest at K = 4096); int8
-        // streams twice the bytes per element and does better with 8 waves x 4 tiles and x in registers
+        // decode batches (M <= 4): int4 stages x in LDS (4 waves x 8 k tiles measured fastest at K = 4096); int8
+        // streams twice the bytes per element and does better with 8 waves x 4 tiles and x in registers.
+        // Larger batches: x through the LDS ring of aq_dma_kernel (shapes measured fastest at K = 4096,
+        // N = 11008; the 64-row form rotates each workgroup's k order, which measured ~8 % faster there).
         if (int4 && mc <= 4 && mc * K * 2 + 16 <= 48 * 1024)
             launch_aq<1, 1, 4, 8, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
-        else if (mc <= 16) launch_aq<1, 1, 8, 4>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+        else if (mc > 4 && g % KT == 0) {
+            if (mc <= 16) {
+                if (int4) launch_dma<1, 2, 4, 4, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+                else launch_dma<1, 2, 4, 3, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+            } else if (mc <= 32) {
+                launch_dma<2, 4, 4, 4, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+            } else {
+                launch_dma<4, 4, 2, 3, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+            }
+        } else if (mc <= 16) launch_aq<1, 1, 8, 4>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
         else if (mc <= 32) launch_aq<2, 2, 8, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
         else launch_aq<4, 2, 8, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
         hipError_t e = hipGetLastError();

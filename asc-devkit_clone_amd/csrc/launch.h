@@ -20,13 +20,12 @@ struct LaunchEvents {
 LaunchEvents& launch_events();  // thread-local; api.cpp
 
 template <typename F, typename... Args>
-inline hipError_t launch_k(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t st, Args... args)
+inline void launch_k(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t st, Args... args)
 {
     LaunchEvents& e = launch_events();
     const hipEvent_t a = e.start, b = e.stop;
     e = LaunchEvents{};
-    hipExtLaunchKernelGGL(kernel, grid, block, shm, st, a, b, 0u, args...);
-    return hipGetLastError();
+    hipExtLaunchKernelGGL(kernel, grid, block, shm, st, a, b, 0u, args...);  // callers check hipGetLastError()
 }
 
 // quant.hip

@@ -49,7 +49,7 @@ def check_close(y_gpu, y_exact, y_abs, K, frac_exact=0.98):
 
 
 @pytest.mark.parametrize("w_type", ["int4", "int8"])
-@pytest.mark.parametrize("M", [1, 16, 64, 3, 40, 100])
+@pytest.mark.parametrize("M", [1, 16, 64, 3, 29, 40, 100])
 def test_config3_decode_shape(ascq_gpu, oracle, w_type, M):
     """x f16 [M, 4096] ~ N(0,1); W [4096, 11008]; g=128 f16 scale log-uniform [1e-3,1e-1], offset U[-8,8]."""
     rng = seeded(300 + M)
@@ -92,6 +92,25 @@ def test_groups_and_layouts(ascq_gpu, oracle, w_type, group, with_offset, transp
     _, y_exact, y_abs = O.antiquant_matmul(x.view(np.uint16), w, code, sc.view(np.uint16),
                                            None if of is None else of.view(np.uint16), group, M, N, K,
                                            w_transpose=transpose)
+    check_close(y.cpu().numpy(), y_exact, y_abs, K)
+
+
+@pytest.mark.parametrize("w_type", ["int4", "int8"])
+@pytest.mark.parametrize("M", [6, 16, 24, 48, 64])
+@pytest.mark.parametrize("K", [640, 384])
+def test_batch_ring_partial_rounds(ascq_gpu, oracle, w_type, M, K):
+    """Batches 4 < M <= 64 stage x through an LDS ring of k rounds (128 x 2 or 128 x 4 k per round) and give each
+    workgroup 2 or 4 column strips: K = 640 / 384 end in a partial round, N = 48 in a partial workgroup."""
+    rng = seeded(900 + M + K)
+    N, g = 48, 128
+    code = O.INT8 if w_type == "int8" else O.INT4
+    at = ascq_gpu.INT8 if w_type == "int8" else ascq_gpu.INT4
+    w, scale, offset = make_weights(rng, K, N, code, g)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    wp = ascq_gpu.weight_pack(_dev(w), at, K, N)
+    y = ascq_gpu.antiquant_matmul(_dev(x), wp, at, _dev(scale), _dev(offset), g, N)
+    _, y_exact, y_abs = O.antiquant_matmul(x.view(np.uint16), w, code, scale.view(np.uint16), offset.view(np.uint16),
+                                           g, M, N, K)
     check_close(y.cpu().numpy(), y_exact, y_abs, K)
 
 
