@@ -18,7 +18,8 @@
 //  * codes are stored offset-binary (q + 8 for int4, q + 128 for int8) so that OR-ing them under the
 //    binary16 exponent of 1024 gives 1024 + code exactly; subtracting 1032 / 1152 restores q exactly;
 //  * int4: in the 32-bit word of step j, element e sits at bits 4*(e/2) (e even) or 16 + 4*(e/2) (e odd),
-//    so (word >> 4i) & 0x000F000F yields the pair (2i, 2i+1) as two half lanes;
+//    so (word >> 4i) & 0x000F000F yields the pair (2i, 2i+1) as two half lanes (dequant8 masks the odd pairs in
+//    place instead and divides by 16 exactly);
 //    int8: the 8 codes of step j are bytes 0..7 of an 8-byte chunk, in k order.
 //
 // Roofline: at decode shapes the kernel streams the packed weight once (K*N/2 or K*N bytes) plus the
@@ -99,24 +100,38 @@ template <bool INT4, bool HAS_OFF>
 __device__ __forceinline__ h8 dequant8(uint32_t w0, uint32_t w1, h2 off, h2 sc, uint32_t magic)
 {
     uint32_t d[4];
+    h2 qv[4];
     if constexpr (INT4) {
-        // w0 holds all 8 nibbles of the step; pair i = (w0 >> 4i) & 0x000F000F
-#pragma unroll
-        for (int i = 0; i < 4; ++i) d[i] = ((w0 >> (4 * i)) & 0x000F000Fu) | magic;
+        // w0 holds all 8 nibbles of the step.  Pairs 0 / 2 (bits 0-3 / 8-11 of each half) OR under the exponent of
+        // 1024 as 1024 + c; pairs 1 / 3 (bits 4-7 / 12-15) are masked in place, giving 1024 + 16 c, and
+        // 1024 + 16 c -> c - 8 is one exact fma (x / 16 - 72), so no shift by 4 or 12 is needed
+        const uint32_t w8 = w0 >> 8;
+        d[0] = (w0 & 0x000F000Fu) | magic;
+        d[1] = (w0 & 0x00F000F0u) | magic;
+        d[2] = (w8 & 0x000F000Fu) | magic;
+        d[3] = (w8 & 0x00F000F0u) | magic;
+        const h2 bias = (h2){(_Float16)1032.0f, (_Float16)1032.0f};
+        const h2 sixteenth = (h2){(_Float16)0.0625f, (_Float16)0.0625f}, b16 = (h2){(_Float16)-72.0f, (_Float16)-72.0f};
+        qv[0] = __builtin_bit_cast(h2, d[0]) - bias;                                       // exact
+        qv[1] = __builtin_elementwise_fma(__builtin_bit_cast(h2, d[1]), sixteenth, b16);  // exact
+        qv[2] = __builtin_bit_cast(h2, d[2]) - bias;
+        qv[3] = __builtin_elementwise_fma(__builtin_bit_cast(h2, d[3]), sixteenth, b16);
     } else {
         // bytes b0..b3 of w0 and w1 -> halves 0x64bb (selector 5 = byte 1 of magic = 0x64)
         d[0] = __builtin_amdgcn_perm(magic, w0, 0x05010500u);
         d[1] = __builtin_amdgcn_perm(magic, w0, 0x05030502u);
         d[2] = __builtin_amdgcn_perm(magic, w1, 0x05010500u);
         d[3] = __builtin_amdgcn_perm(magic, w1, 0x05030502u);
+        const h2 bias = (h2){(_Float16)1152.0f, (_Float16)1152.0f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[i] = __builtin_bit_cast(h2, d[i]) - bias;  // exact
     }
-    const h2 bias = INT4 ? (h2){(_Float16)1032.0f, (_Float16)1032.0f} : (h2){(_Float16)1152.0f, (_Float16)1152.0f};
     h2 r[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        h2 q = __builtin_bit_cast(h2, d[i]) - bias;  // exact
-        if constexpr (HAS_OFF) q = q + off;          // one rounding
-        r[i] = q * sc;                               // one rounding
+        h2 q = qv[i];
+        if constexpr (HAS_OFF) q = q + off;  // one rounding
+        r[i] = q * sc;                       // one rounding
     }
     h8 out;
     out.s01 = r[0];
@@ -150,8 +165,8 @@ __device__ __forceinline__ aq_rsrc_t aq_rsrc(const void* base, uint64_t bytes)
 // tiles of the KSPLIT waves are summed through LDS in a fixed order.  MT = number of 16-row m tiles.
 // XLDS (decode batches, M <= 4, MT = 1): the activations x[0:M, 0:K] are staged in LDS once per workgroup
 // (loads issued before the weights, so their latency hides under the weight stream) and the MFMA A fragments
-// are read from there; rows m >= M read a zeroed 16-byte slot.  This keeps the kernel under 64 VGPRs, so every
-// workgroup of a decode launch is resident at once and the weight stream overlaps the dequantisation.
+// are read from there; rows m >= M read a zeroed 16-byte slot.  This takes the four 16-byte activation loads per
+// tile off the vector memory path, which then carries little more than the weight stream.
 template <int MT, int NBW, int KSPLIT, int TPW, bool INT4, bool HAS_OFF, bool G128, bool XLDS>
 __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* __restrict__ y,
                                                                      const uint16_t* __restrict__ x,
@@ -166,6 +181,7 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
     __shared__ v4f red[KSPLIT > 1 ? KSPLIT - 1 : 1][MT][NBW][64];
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];  // XLDS: x[M][K] halves, then 16 zero bytes
     static_assert(!XLDS || MT == 1, "LDS activations are for one m tile");
+    constexpr bool GSC = G128 && NBW == 1 && TPW % 4 == 0;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t KB = K / KT;
@@ -219,6 +235,20 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
         u32x4 wv[TPW][NBW][WV];
         uint32_t sc[G128 ? TPW : 1][NBW], of[G128 ? TPW : 1][NBW];
         h8 xa[XLDS ? 1 : TPW][MT][4];
+        // GSC: the scale / offset rows of 4 consecutive tiles come in one 2-byte load each (lane (kq, c) fetches
+        // tile t0 + 4 h + kq, column c) and are handed to the lanes that need them with ds_bpermute, instead of
+        // two loads per tile -- measured ~1.3 us faster at M = 1, K = 4096, N = 11008
+        uint32_t scl[GSC ? TPW / 4 : 1], ofl[GSC ? TPW / 4 : 1];
+        if constexpr (GSC) {
+#pragma unroll
+            for (int h = 0; h < TPW / 4; ++h) {
+                const int64_t kb = t0 + 4 * h + kq;
+                const bool ok = kb < KB && nb0 < NBT;
+                const uint32_t so = ok ? (uint32_t)((((kb * KT) / g) * N + nb0 * 16 + col_in) * 2) : AQ_OOB;
+                scl[h] = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0);
+                ofl[h] = HAS_OFF ? __builtin_amdgcn_raw_buffer_load_b16(ro, so, 0, 0) : 0u;
+            }
+        }
         // issue order = use order (activations, scales, weights of tile 0, then tile 1, ...): loads retire in
         // order, so tile i can start as soon as its own data has landed while later tiles are still in flight
 #pragma unroll
@@ -240,7 +270,7 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
             for (int b = 0; b < NBW; ++b) {
                 const int64_t nb = nb0 + b;
                 const bool ok = kb < KB && nb < NBT;
-                if constexpr (G128) {
+                if constexpr (G128 && !GSC) {
                     const uint32_t so = ok ? (uint32_t)((((kb * KT) / g) * N + nb * 16 + col_in) * 2) : AQ_OOB;
                     sc[i][b] = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0);
                     of[i][b] = HAS_OFF ? __builtin_amdgcn_raw_buffer_load_b16(ro, so, 0, 0) : 0u;
@@ -280,7 +310,18 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
                 for (int b = 0; b < NBW; ++b) {
                     h2 s2, o2;
                     if constexpr (G128) {
-                        const _Float16 sv = bits_h((uint16_t)sc[i][b]), ov = bits_h((uint16_t)of[i][b]);
+                        uint32_t sci, ofi;
+                        if constexpr (GSC) {
+                            const uint32_t pk = scl[i >> 2] | (ofl[i >> 2] << 16);
+                            const uint32_t v =
+                                (uint32_t)__builtin_amdgcn_ds_bpermute(((i & 3) * 16 + col_in) * 4, (int)pk);
+                            sci = v & 0xFFFFu;
+                            ofi = v >> 16;
+                        } else {
+                            sci = sc[i][b];
+                            ofi = of[i][b];
+                        }
+                        const _Float16 sv = bits_h((uint16_t)sci), ov = bits_h((uint16_t)ofi);
                         s2 = (h2){sv, sv};
                         o2 = (h2){ov, ov};
                     } else {
@@ -568,12 +609,14 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
         const int64_t mc = (M - m0) < 64 ? (M - m0) : 64;
         const uint16_t* xc = x + m0 * K;
         uint16_t* yc = y + m0 * N;
-        // decode batches (M <= 4): int4 stages x in LDS (4 waves x 8 k tiles measured fastest at K = 4096); int8
-        // streams twice the bytes per element and does better with 8 waves x 4 tiles and x in registers.
+        // decode batches (M <= 4): x staged in LDS; int4 with 4 waves x 8 k tiles, int8 (twice the bytes per
+        // element) with 8 waves x 4 tiles, both measured fastest at K = 4096.
         // Larger batches: x through the LDS ring of aq_dma_kernel (shapes measured fastest at K = 4096,
         // N = 11008; the 64-row form rotates each workgroup's k order, which measured ~8 % faster there).
-        if (int4 && mc <= 4 && mc * K * 2 + 16 <= 48 * 1024)
-            launch_aq<1, 1, 4, 8, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+        if (mc <= 4 && mc * K * 2 + 16 <= 48 * 1024) {
+            if (int4) launch_aq<1, 1, 4, 8, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+            else launch_aq<1, 1, 8, 4, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+        }
         else if (mc > 4 && g % KT == 0) {
             if (mc <= 16) {
                 if (int4) launch_dma<1, 2, 4, 4, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
