@@ -18,7 +18,8 @@
 // the LDS destination (buffer_load_dwordx4 ... lds): no registers are involved, so STAGES - 1 stages are in
 // flight while one is multiplied.  Per iteration each wave waits (s_waitcnt vmcnt) for its own copies of the
 // current stage, one barrier publishes them to all waves and frees the stage multiplied last iteration, and
-// the copies of the stage STAGES - 1 ahead are issued into that freed slot before the MFMAs start.  Every wave
+// the copies of the stage STAGES - 1 ahead are issued into that freed slot, a few before each k-step of the
+// iteration (so they interleave with the MFMAs instead of stalling the wave in one burst).  Every wave
 // issues the same number of copies every iteration (out-of-range copies read zeros), so the vmcnt threshold is
 // a compile-time constant.
 //
@@ -62,6 +63,22 @@ __device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) { return __buil
 __device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
 __device__ __forceinline__ u32x2 bload8(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0); }
 __device__ __forceinline__ uint32_t bload2(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0); }
+
+// Output tile of an epilogue: a buffer resource whose range ends after the tile's last valid row, so stores of
+// rows past the matrix are dropped by the hardware range check, and 32-bit offsets inside the tile (row pitch
+// ldc elements of esize bytes; the caller keeps rows * ldc * esize below 2^31).  Columns past the matrix are
+// given the out-of-range offset by the caller.
+struct TileOut {
+    rsrc_t r;
+    uint32_t pitch;  // bytes per row
+};
+__device__ __forceinline__ TileOut tile_out(void* C, int64_t m0, int64_t n0, int64_t ldc, int rows, int cols, int esize)
+{
+    TileOut t;
+    t.r = make_rsrc((uint8_t*)C + (m0 * ldc + n0) * esize, (uint32_t)(((int64_t)(rows - 1) * ldc + cols) * esize));
+    t.pitch = (uint32_t)(ldc * esize);
+    return t;
+}
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -184,6 +201,7 @@ struct GemmCore {
     static constexpr size_t LDS_BYTES = (size_t)STAGES * STAGE + DUMMY_BYTES;
     // vmem operations of this wave issued after stage kt's copies, at the top of iteration kt
     static constexpr int IN_FLIGHT = (STAGES - 2) * (COPIES + B_LOADS);
+    static constexpr int CPS = (COPIES + KPS - 1) / KPS;  // copies issued before each k-step of a stage
     typedef typename std::conditional<OP == OP_I8, v16i, v16f>::type acc_t;
     static_assert(FM >= 1 && FN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
     static_assert(BM % (ROWS_PER_COPY * NW) == 0 && A_COPIES >= 1, "A copies must split evenly over the waves");
@@ -274,47 +292,44 @@ struct GemmCore {
             }
         };
 
-        auto issue_copies = [&](int64_t kt, int slot) {
+        // copy u (0 <= u < COPIES) of stage kt into slot: A rows, then B rows, then MX scale blocks
+        auto issue_copy = [&](int64_t kt, int slot, int u) {
             uint8_t* sA = smem + slot * STAGE;
             uint8_t* sB = sA + BM * ROWB;
             const int64_t kb0 = kt * ROWB;
             const int rin = lane / CH, phys = lane % CH;
-#pragma unroll
-            for (int j = 0; j < A_COPIES; ++j) {
-                const int row0 = (wave * A_COPIES + j) * ROWS_PER_COPY;
+            if (u < A_COPIES) {
+                const int row0 = (wave * A_COPIES + u) * ROWS_PER_COPY;
                 const int row = row0 + rin;
                 const int64_t k = kb0 + swz(row, phys) * 16;
                 const uint32_t off = (row < p.rows && k < p.kbytes) ? p.a0 + (uint32_t)row * p.lda + (uint32_t)k : OOB;
                 copy16_to_lds(p.a, sA + row0 * ROWB, off);
-            }
-#pragma unroll
-            for (int j = 0; j < B_COPIES; ++j) {
-                const int row0 = (wave * B_COPIES + j) * ROWS_PER_COPY;
+            } else if (u < A_COPIES + B_COPIES) {
+                const int row0 = (wave * B_COPIES + (u - A_COPIES)) * ROWS_PER_COPY;
                 const int row = row0 + rin;
                 const int64_t k = kb0 + swz(row, phys) * 16;
                 const uint32_t off = (row < p.cols && k < p.kbytes) ? p.b0 + (uint32_t)row * p.ldb + (uint32_t)k : OOB;
                 copy16_to_lds(p.b, sB + row0 * ROWB, off);
-            }
-            if constexpr (IS_MX) {
+            } else if constexpr (IS_MX) {
                 uint8_t* sS = sA + (BM + BN) * ROWB;
                 const bool kval = (uint32_t)(kt * SCB) < p.sk;
-#pragma unroll
-                for (int j = 0; j < SC_COPIES; ++j) {
-                    const int g = wave * SC_COPIES + j;  // wave-uniform
-                    if (g < SA_INSTR) {
-                        const uint32_t off =
-                            kval ? ((uint32_t)kt * p.sa_rows + p.sa0_row + g * SC_ROWS) * SCB + lane * 16 : OOB;
-                        copy16_to_lds(p.sa, sS + g * 1024, off);
-                    } else if (g < SA_INSTR + SB_INSTR) {
-                        const uint32_t off =
-                            kval ? ((uint32_t)kt * p.sb_rows + p.sb0_row + (g - SA_INSTR) * SC_ROWS) * SCB + lane * 16
-                                 : OOB;
-                        copy16_to_lds(p.sb, sS + SA_REG + (g - SA_INSTR) * 1024, off);
-                    } else {
-                        copy16_to_lds(p.sa, smem + STAGES * STAGE, OOB);
-                    }
+                const int g = wave * SC_COPIES + (u - A_COPIES - B_COPIES);  // wave-uniform
+                if (g < SA_INSTR) {
+                    const uint32_t off =
+                        kval ? ((uint32_t)kt * p.sa_rows + p.sa0_row + g * SC_ROWS) * SCB + lane * 16 : OOB;
+                    copy16_to_lds(p.sa, sS + g * 1024, off);
+                } else if (g < SA_INSTR + SB_INSTR) {
+                    const uint32_t off =
+                        kval ? ((uint32_t)kt * p.sb_rows + p.sb0_row + (g - SA_INSTR) * SC_ROWS) * SCB + lane * 16 : OOB;
+                    copy16_to_lds(p.sb, sS + SA_REG + (g - SA_INSTR) * 1024, off);
+                } else {
+                    copy16_to_lds(p.sa, smem + STAGES * STAGE, OOB);
                 }
             }
+        };
+        auto issue_copies = [&](int64_t kt, int slot) {
+#pragma unroll
+            for (int u = 0; u < COPIES; ++u) issue_copy(kt, slot, u);
         };
 
 #pragma unroll
@@ -348,8 +363,6 @@ struct GemmCore {
             stage_barrier();                    // ... and every wave's; the slot multiplied last iteration is free
             load_b_regs(rb_new, kt + STAGES - 1);
             __builtin_amdgcn_sched_barrier(0);
-            issue_copies(kt + STAGES - 1, nslot);
-            __builtin_amdgcn_sched_barrier(0);
             const uint8_t* sA = smem + slot * STAGE;
             const uint8_t* sB = sA + BM * ROWB;
             // k-steps in pairs; a scheduling barrier between pairs keeps the fragment reads of a stage from
@@ -370,6 +383,12 @@ struct GemmCore {
                 }
 #pragma unroll
                 for (int s = SPH * h; s < SPH * h + SPH; ++s) {
+                    // the copies of stage kt + STAGES - 1 are spread over the k-steps of this stage (CPS before
+                    // each), so no wave stalls on a burst of them in front of its MFMAs (measured 13-14 % faster
+                    // than issuing them all after the barrier)
+#pragma unroll
+                    for (int u = s * CPS; u < (s + 1) * CPS && u < COPIES; ++u) issue_copy(kt + STAGES - 1, nslot, u);
+                    __builtin_amdgcn_sched_barrier(0);
                     // this lane's 16-byte chunks of k-step s: s * 2 + kh (int8, fp4), s * 4 + kh and s * 4 + 2 + kh
                     // (fp8)
                     v8i fa[FM];

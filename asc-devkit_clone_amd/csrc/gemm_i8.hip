@@ -38,32 +38,44 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
     typename T::acc_t acc[T::FM][T::FN];
     T::run(c, smem, acc);
 
-    // epilogue: per 32x32 accumulator tile, lane holds column lane%32 and 16 rows (GemmCore::frag_row)
+    // epilogue: per 32x32 accumulator tile, lane holds column lane%32 and 16 rows (GemmCore::frag_row); stores go
+    // through a buffer resource over the output tile (rows past M dropped by its range, 32-bit offsets)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const float mscalar = quant_pre_m1(p.qscalar);
+    const int esize = p.epi == EPI_I32 ? 4 : (p.epi == EPI_REQ8 ? 1 : 2);
+    const TileOut out = tile_out(p.C, m0, n0, p.ldc, c.rows, c.cols, esize);
+    auto store = [&](auto conv, auto put) {
 #pragma unroll
-    for (int j = 0; j < T::FN; ++j) {
-        const int64_t col = n0 + T::frag_col(wn, j, lane);
-        if (col >= p.N) continue;
-        const int32_t bias = p.bias ? p.bias[col] : 0;
-        const uint64_t w = p.qvec ? p.qvec[col] : p.qscalar;
-        const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
+        for (int j = 0; j < T::FN; ++j) {
+            const int cl = T::frag_col(wn, j, lane);
+            const bool cok = cl < c.cols;
+            const int64_t col = n0 + cl;
+            const int32_t bias = (p.bias && cok) ? p.bias[col] : 0;
+            const uint64_t w = (p.qvec && cok) ? p.qvec[col] : p.qscalar;
+            const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
+            const uint32_t cbase = cok ? (uint32_t)(cl * esize) : OOB;
 #pragma unroll
-        for (int i = 0; i < T::FM; ++i) {
+            for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + T::frag_row(wm, i, r, lane);
-                if (row >= p.M) continue;
-                const int32_t v = (int32_t)((uint32_t)acc[i][j][r] + (uint32_t)bias);
-                const int64_t o = row * p.ldc + col;
-                if (p.epi == EPI_I32) ((int32_t*)p.C)[o] = v;
-                else if (p.epi == EPI_DEQ_F16) ((uint16_t*)p.C)[o] = f32_to_f16_sat((float)v * m1);
-                else if (p.epi == EPI_DEQ_BF16) ((uint16_t*)p.C)[o] = f32_to_bf16_sat((float)v * m1);
-                else ((uint8_t*)p.C)[o] = requant8((float)v * m1, w);
-            }
+                for (int r = 0; r < 16; ++r) {
+                    const int32_t v = (int32_t)((uint32_t)acc[i][j][r] + (uint32_t)bias);
+                    put(conv(v, m1, w), cbase + (uint32_t)T::frag_row(wm, i, r, lane) * out.pitch);
+                }
         }
-    }
+    };
+    if (p.epi == EPI_I32)
+        store([](int32_t v, float, uint64_t) { return (uint32_t)v; },
+              [&](uint32_t x, uint32_t o) { __builtin_amdgcn_raw_buffer_store_b32(x, out.r, o, 0, 0); });
+    else if (p.epi == EPI_DEQ_F16)
+        store([](int32_t v, float m1, uint64_t) { return f32_to_f16_sat((float)v * m1); },
+              [&](uint16_t x, uint32_t o) { __builtin_amdgcn_raw_buffer_store_b16(x, out.r, o, 0, 0); });
+    else if (p.epi == EPI_DEQ_BF16)
+        store([](int32_t v, float m1, uint64_t) { return f32_to_bf16_sat((float)v * m1); },
+              [&](uint16_t x, uint32_t o) { __builtin_amdgcn_raw_buffer_store_b16(x, out.r, o, 0, 0); });
+    else
+        store([](int32_t v, float m1, uint64_t w) { return requant8((float)v * m1, w); },
+              [&](uint8_t x, uint32_t o) { __builtin_amdgcn_raw_buffer_store_b8(x, out.r, o, 0, 0); });
 }
 
 // QuantGroupMatmul: the m axis is split into G ragged groups (group_list), group g multiplies its rows by
@@ -130,26 +142,36 @@ __global__ __launch_bounds__(WM * WN * 64) void group_gemm_i8_kernel(GroupGemmAr
     // per-token scale in fp32, optional FasterGelu in fp32, one rounding cast to the output type.
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
+    // stores through a buffer resource over the output tile: rows past the group's end are out of its range
+    const TileOut out = tile_out(p.Y, m0, n0, p.N, c.rows, c.cols, 2);
+    const rsrc_t rp = make_rsrc(p.pts + m0, (uint32_t)(c.rows * 4));
+    float pt[T::FM][16];  // per-token scales of this lane's rows (rows past the group read 0 and are not stored)
 #pragma unroll
-    for (int j = 0; j < T::FN; ++j) {
-        const int64_t col = n0 + T::frag_col(wn, j, lane);
-        if (col >= p.N) continue;
-        const float sc = p.scale[(int64_t)g * p.N + col];
+    for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-        for (int i = 0; i < T::FM; ++i) {
+        for (int r = 0; r < 16; ++r)
+            pt[i][r] = __uint_as_float(bload4(rp, (uint32_t)T::frag_row(wm, i, r, lane) * 4));
+    auto store = [&](auto cvt) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + T::frag_row(wm, i, r, lane);
-                if (row >= m_end) continue;
-                float v = (float)acc[i][j][r] * sc;
-                v = v * p.pts[row];
-                if (p.act) v = faster_gelu(v);
-                const int64_t o = row * p.N + col;
-                if (p.out_type == DT_F16) ((uint16_t*)p.Y)[o] = f32_to_f16_sat(v);
-                else ((uint16_t*)p.Y)[o] = f32_to_bf16_sat(v);
-            }
+        for (int j = 0; j < T::FN; ++j) {
+            const int cl = T::frag_col(wn, j, lane);
+            const bool cok = cl < c.cols;
+            const float sc = cok ? p.scale[(int64_t)g * p.N + n0 + cl] : 0.0f;
+            const uint32_t cbase = cok ? (uint32_t)(cl * 2) : OOB;
+#pragma unroll
+            for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float v = (float)acc[i][j][r] * sc;
+                    v = v * pt[i][r];
+                    if (p.act) v = faster_gelu(v);
+                    __builtin_amdgcn_raw_buffer_store_b16(cvt(v), out.r, cbase + (uint32_t)T::frag_row(wm, i, r, lane) * out.pitch,
+                                                          0, 0);
+                }
         }
-    }
+    };
+    if (p.out_type == DT_F16) store([](float v) { return f32_to_f16_sat(v); });
+    else store([](float v) { return f32_to_bf16_sat(v); });
 }
 
 // Any shape / layout / alignment: one thread per output element, int32 accumulate, same epilogue.
@@ -197,7 +219,8 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
     const bool a_ok = !a.trans_a && a.lda % 16 == 0 && ((uintptr_t)a.A % 16 == 0) && a.lda * a.M < (1ll << 31);
     const bool b_ok = a.trans_b ? (a.ldb % 16 == 0 && ((uintptr_t)a.B % 16 == 0) && a.ldb * a.N < (1ll << 31))
                                 : (a.ldb % 4 == 0 && a.N % 4 == 0 && ((uintptr_t)a.B % 4 == 0) && a.ldb * a.K < (1ll << 31));
-    if (a_ok && b_ok && a.K % 16 == 0) {
+    // the tiled epilogue addresses a 256-row output tile with 32-bit offsets
+    if (a_ok && b_ok && a.K % 16 == 0 && a.ldc < (1ll << 21)) {
         const bool big = a.M >= 1024 && a.N >= 1024;
         if (a.trans_b)
             return big ? (a.K % 128 == 0 ? launch_tiled<256, 256, 4, 2, 2, true, 128>(a, st)

@@ -181,7 +181,7 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
     __shared__ v4f red[KSPLIT > 1 ? KSPLIT - 1 : 1][MT][NBW][64];
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];  // XLDS: x[M][K] halves, then 16 zero bytes
     static_assert(!XLDS || MT == 1, "LDS activations are for one m tile");
-    constexpr bool GSC = G128 && NBW == 1 && TPW % 4 == 0;
+    constexpr bool GSC = G128 && TPW % 4 == 0;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t KB = K / KT;
@@ -238,16 +238,19 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
         // GSC: the scale / offset rows of 4 consecutive tiles come in one 2-byte load each (lane (kq, c) fetches
         // tile t0 + 4 h + kq, column c) and are handed to the lanes that need them with ds_bpermute, instead of
         // two loads per tile -- measured ~1.3 us faster at M = 1, K = 4096, N = 11008
-        uint32_t scl[GSC ? TPW / 4 : 1], ofl[GSC ? TPW / 4 : 1];
+        uint32_t scl[GSC ? TPW / 4 : 1][NBW], ofl[GSC ? TPW / 4 : 1][NBW];
         if constexpr (GSC) {
 #pragma unroll
-            for (int h = 0; h < TPW / 4; ++h) {
-                const int64_t kb = t0 + 4 * h + kq;
-                const bool ok = kb < KB && nb0 < NBT;
-                const uint32_t so = ok ? (uint32_t)((((kb * KT) / g) * N + nb0 * 16 + col_in) * 2) : AQ_OOB;
-                scl[h] = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0);
-                ofl[h] = HAS_OFF ? __builtin_amdgcn_raw_buffer_load_b16(ro, so, 0, 0) : 0u;
-            }
+            for (int h = 0; h < TPW / 4; ++h)
+#pragma unroll
+                for (int b = 0; b < NBW; ++b) {
+                    const int64_t kb = t0 + 4 * h + kq;
+                    const bool ok = kb < KB && nb0 + b < NBT;
+                    const uint32_t so =
+                        ok ? (uint32_t)((((kb * KT) / g) * N + (nb0 + b) * 16 + col_in) * 2) : AQ_OOB;
+                    scl[h][b] = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0);
+                    ofl[h][b] = HAS_OFF ? __builtin_amdgcn_raw_buffer_load_b16(ro, so, 0, 0) : 0u;
+                }
         }
         // issue order = use order (activations, scales, weights of tile 0, then tile 1, ...): loads retire in
         // order, so tile i can start as soon as its own data has landed while later tiles are still in flight
@@ -312,7 +315,7 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
                     if constexpr (G128) {
                         uint32_t sci, ofi;
                         if constexpr (GSC) {
-                            const uint32_t pk = scl[i >> 2] | (ofl[i >> 2] << 16);
+                            const uint32_t pk = scl[i >> 2][b] | (ofl[i >> 2][b] << 16);
                             const uint32_t v =
                                 (uint32_t)__builtin_amdgcn_ds_bpermute(((i & 3) * 16 + col_in) * 4, (int)pk);
                             sci = v & 0xFFFFu;
