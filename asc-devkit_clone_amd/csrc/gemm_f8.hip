@@ -76,29 +76,42 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
     typename T::acc_t acc[T::FM][T::FN];
     T::run(c, smem_f8, acc);
 
+    // epilogue through a buffer resource over the output tile (rows past M dropped by its range)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const float mscalar = quant_pre_m1(p.qscalar);
+    const int esize = p.c_type == DT_F32 ? 4 : ((p.c_type == DT_F16 || p.c_type == DT_BF16) ? 2 : 1);
+    const TileOut out = tile_out(p.C, m0, n0, p.ldc, c.rows, c.cols, esize);
+    auto store = [&](auto conv, auto put) {
 #pragma unroll
-    for (int j = 0; j < T::FN; ++j) {
-        const int64_t col = n0 + T::frag_col(wn, j, lane);
-        if (col >= p.N) continue;
-        const float bias = p.bias ? p.bias[col] : 0.0f;
-        const uint64_t w = p.qvec ? p.qvec[col] : p.qscalar;
-        const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
+        for (int j = 0; j < T::FN; ++j) {
+            const int cl = T::frag_col(wn, j, lane);
+            const bool cok = cl < c.cols;
+            const int64_t col = n0 + cl;
+            const float bias = (p.bias && cok) ? p.bias[col] : 0.0f;
+            const uint64_t w = (p.qvec && cok) ? p.qvec[col] : p.qscalar;
+            const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
+            const uint32_t cbase = cok ? (uint32_t)(cl * esize) : OOB;
 #pragma unroll
-        for (int i = 0; i < T::FM; ++i) {
+            for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + T::frag_row(wm, i, r, lane);
-                if (row >= p.M) continue;
-                float v = acc[i][j][r];
-                if (p.bias) v = v + bias;
-                if (p.use_quant) v = v * m1;
-                store_f8_out(p.C, p.c_type, row * p.ldc + col, v, w);
-            }
+                for (int r = 0; r < 16; ++r) {
+                    float v = acc[i][j][r];
+                    if (p.bias) v = v + bias;
+                    if (p.use_quant) v = v * m1;
+                    put(conv(v, w), cbase + (uint32_t)T::frag_row(wm, i, r, lane) * out.pitch);
+                }
         }
-    }
+    };
+    auto put32 = [&](uint32_t x, uint32_t o) { __builtin_amdgcn_raw_buffer_store_b32(x, out.r, o, 0, 0); };
+    auto put16 = [&](uint16_t x, uint32_t o) { __builtin_amdgcn_raw_buffer_store_b16(x, out.r, o, 0, 0); };
+    auto put8 = [&](uint8_t x, uint32_t o) { __builtin_amdgcn_raw_buffer_store_b8(x, out.r, o, 0, 0); };
+    if (p.c_type == DT_F32) store([](float v, uint64_t) { return __float_as_uint(v); }, put32);
+    else if (p.c_type == DT_F16) store([](float v, uint64_t) { return f32_to_f16_sat(v); }, put16);
+    else if (p.c_type == DT_BF16) store([](float v, uint64_t) { return f32_to_bf16_sat(v); }, put16);
+    else if (p.c_type == DT_INT8 || p.c_type == DT_UINT8) store([](float v, uint64_t w) { return requant8(v, w); }, put8);
+    else if (p.c_type == DT_FP8_E5M2) store([](float v, uint64_t) { return f32_to_fp8(v, 1); }, put8);
+    else store([](float v, uint64_t) { return f32_to_fp8(v, 0); }, put8);
 }
 
 // Any shape / layout / alignment: one thread per output element, fp32 accumulation in k order.
@@ -157,7 +170,8 @@ hipError_t launch_gemm_f8(const GemmF8Args& a, hipStream_t st)
     const bool a_ok = !a.trans_a && a.lda % 16 == 0 && ((uintptr_t)a.A % 16 == 0) && a.lda * a.M < (1ll << 31);
     const bool b_ok = a.trans_b ? (a.ldb % 16 == 0 && ((uintptr_t)a.B % 16 == 0) && a.ldb * a.N < (1ll << 31))
                                 : (a.ldb % 4 == 0 && a.N % 4 == 0 && ((uintptr_t)a.B % 4 == 0) && a.ldb * a.K < (1ll << 31));
-    if (a_ok && b_ok && a.K % 16 == 0) {
+    // the tiled epilogue addresses a 256-row output tile with 32-bit offsets
+    if (a_ok && b_ok && a.K % 16 == 0 && a.ldc < (1ll << 21)) {
         switch (a.fmt_a | (a.fmt_b << 3)) {
         case F8F6F4_E4M3 | (F8F6F4_E4M3 << 3): return launch_f8_fmt<F8F6F4_E4M3 | (F8F6F4_E4M3 << 3)>(a, st);
         case F8F6F4_E5M2 | (F8F6F4_E5M2 << 3): return launch_f8_fmt<F8F6F4_E5M2 | (F8F6F4_E5M2 << 3)>(a, st);

@@ -61,20 +61,22 @@ __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, con
     typename T::acc_t acc[T::FM][T::FN];
     T::run(c, smem_mx, acc);
 
+    // epilogue through a buffer resource over the output tile (rows past M dropped by its range)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
+    const bool f32 = p.c_type == DT_F32;
+    const TileOut out = tile_out(p.C, m0, n0, N, c.rows, c.cols, f32 ? 4 : 2);
 #pragma unroll
     for (int j = 0; j < T::FN; ++j) {
-        const int64_t col = n0 + T::frag_col(wn, j, lane);
-        if (col >= N) continue;
+        const int cl = T::frag_col(wn, j, lane);
+        const uint32_t cbase = cl < c.cols ? (uint32_t)(cl * (f32 ? 4 : 2)) : OOB;
 #pragma unroll
         for (int i = 0; i < T::FM; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + T::frag_row(wm, i, r, lane);
-                if (row >= M) continue;
-                if (p.c_type == DT_F32) ((float*)p.C)[row * N + col] = acc[i][j][r];
-                else ((uint16_t*)p.C)[row * N + col] = f32_to_bf16_sat(acc[i][j][r]);
+                const uint32_t o = cbase + (uint32_t)T::frag_row(wm, i, r, lane) * out.pitch;
+                if (f32) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][r]), out.r, o, 0, 0);
+                else __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_sat(acc[i][j][r]), out.r, o, 0, 0);
             }
     }
 }
@@ -194,7 +196,8 @@ static hipError_t launch_mx_f8(const MxGemmArgs& a, hipStream_t st)
 hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st)
 {
     const bool fp4 = a.fmt_a == F8F6F4_E2M1 && a.fmt_b == F8F6F4_E2M1;
-    if (a.K % (fp4 ? 128 : 64) != 0 || !a.ws_scales) return hipErrorInvalidValue;
+    // (the epilogue addresses a 256-row output tile with 32-bit offsets: N < 2^21)
+    if (a.K % (fp4 ? 128 : 64) != 0 || !a.ws_scales || a.N >= (1ll << 21)) return hipErrorInvalidValue;
     const bool big = a.M >= 1024 && a.N >= 1024;
     if (fp4) {
         if (big) return launch_mx_tiled<256, 256, 4, 2, 4, 64, OP_MXFP4, 0>(a, st);
