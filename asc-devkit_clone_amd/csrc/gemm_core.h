@@ -161,7 +161,7 @@ struct CoreArgs {
 };
 
 // FMT (fp8 ops): f8f6f4 format code of A in bits 0-2 and of B in bits 3-5
-template <int BM, int BN, int WM, int WN, int STAGES, bool B_KCONTIG, int OP, int ROWB_ = 64, int FMT = 0>
+template <int BM, int BN, int WM, int WN, int STAGES, bool B_KCONTIG, int OP, int ROWB_ = 64, int FMT = 0, bool ILV = true>
 struct GemmCore {
     static constexpr bool IS_MX = OP == OP_MXFP4 || OP == OP_MXF8;
     static constexpr bool IS_F8 = OP == OP_F8 || OP == OP_MXF8;
@@ -201,7 +201,8 @@ struct GemmCore {
     static constexpr size_t LDS_BYTES = (size_t)STAGES * STAGE + DUMMY_BYTES;
     // vmem operations of this wave issued after stage kt's copies, at the top of iteration kt
     static constexpr int IN_FLIGHT = (STAGES - 2) * (COPIES + B_LOADS);
-    static constexpr int CPS = (COPIES + KPS - 1) / KPS;  // copies issued before each k-step of a stage
+    // copies issued before each k-step of a stage (ILV false: all before the first)
+    static constexpr int CPS = ILV ? (COPIES + KPS - 1) / KPS : COPIES;
     typedef typename std::conditional<OP == OP_I8, v16i, v16f>::type acc_t;
     static_assert(FM >= 1 && FN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
     static_assert(BM % (ROWS_PER_COPY * NW) == 0 && A_COPIES >= 1, "A copies must split evenly over the waves");

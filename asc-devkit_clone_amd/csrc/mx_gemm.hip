@@ -28,11 +28,11 @@
 
 namespace ascq {
 
-template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT>
+template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true>
 __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, const uint8_t* __restrict__ sa_sm,
                                                                 const uint8_t* __restrict__ sb_sm)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, true, OP, RB, FMT>;
+    using T = GemmCore<BM, BN, WM, WN, ST, true, OP, RB, FMT, ILV>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_mx[];
     const int64_t M = p.M, N = p.N, K = p.K;
     const int64_t KB = OP == OP_MXFP4 ? K / 2 : K;  // bytes per row
@@ -64,21 +64,23 @@ __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, con
     // epilogue through a buffer resource over the output tile (rows past M dropped by its range)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
-    const bool f32 = p.c_type == DT_F32;
-    const TileOut out = tile_out(p.C, m0, n0, N, c.rows, c.cols, f32 ? 4 : 2);
+    const int esize = p.c_type == DT_F32 ? 4 : 2;
+    const TileOut out = tile_out(p.C, m0, n0, N, c.rows, c.cols, esize);
+    auto store = [&](auto put) {
 #pragma unroll
-    for (int j = 0; j < T::FN; ++j) {
-        const int cl = T::frag_col(wn, j, lane);
-        const uint32_t cbase = cl < c.cols ? (uint32_t)(cl * (f32 ? 4 : 2)) : OOB;
+        for (int j = 0; j < T::FN; ++j) {
+            const int cl = T::frag_col(wn, j, lane);
+            const uint32_t cbase = cl < c.cols ? (uint32_t)(cl * esize) : OOB;
 #pragma unroll
-        for (int i = 0; i < T::FM; ++i)
+            for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t o = cbase + (uint32_t)T::frag_row(wm, i, r, lane) * out.pitch;
-                if (f32) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][r]), out.r, o, 0, 0);
-                else __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_sat(acc[i][j][r]), out.r, o, 0, 0);
-            }
-    }
+                for (int r = 0; r < 16; ++r) put(acc[i][j][r], cbase + (uint32_t)T::frag_row(wm, i, r, lane) * out.pitch);
+        }
+    };
+    if (p.c_type == DT_F32)
+        store([&](float v, uint32_t o) { __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), out.r, o, 0, 0); });
+    else
+        store([&](float v, uint32_t o) { __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_sat(v), out.r, o, 0, 0); });
 }
 
 // [K, N] (two fp4 per byte along N) -> [N, K] (two per byte along K).  One thread per output byte.
@@ -158,10 +160,10 @@ size_t mx_scale_workspace_bytes(int64_t M, int64_t N, int64_t K)
     return (size_t)((M * sK + 16 + 255) / 256 * 256 + (N * sK + 16 + 255) / 256 * 256);
 }
 
-template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT>
+template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true>
 static hipError_t launch_mx_tiled(const MxGemmArgs& a, hipStream_t st)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, true, OP, RB, FMT>;
+    using T = GemmCore<BM, BN, WM, WN, ST, true, OP, RB, FMT, ILV>;
     constexpr int SCB = T::SCB;
     const int64_t sK = (a.K + 63) / 64 * 2;
     uint8_t* sa_sm = a.ws_scales;
@@ -172,13 +174,13 @@ static hipError_t launch_mx_tiled(const MxGemmArgs& a, hipStream_t st)
     if (e != hipSuccess) return e;
     static bool attr = false;
     if (!attr) {
-        e = hipFuncSetAttribute((const void*)mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT>,
+        e = hipFuncSetAttribute((const void*)mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT, ILV>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::LDS_BYTES);
         if (e != hipSuccess) return e;
         attr = true;
     }
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
-    launch_k((mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a,
+    launch_k((mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT, ILV>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a,
                        sa_sm, sb_sm);
     return hipGetLastError();
 }
