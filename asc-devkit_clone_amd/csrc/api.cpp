@@ -243,8 +243,9 @@ ascq_status ascq_matmul_create(const ascq_matmul_types* types, ascq_matmul_t* ou
         return fail(ASCQ_E_UNSUPPORTED, "matmul_create: unsupported A/B types (%d, %d)", types->a_type, types->b_type);
     if (k == K_INT8) {
         if (types->c_type != ASCQ_DT_F16 && types->c_type != ASCQ_DT_BF16 && types->c_type != ASCQ_DT_INT32 &&
-            types->c_type != ASCQ_DT_INT8 && types->c_type != ASCQ_DT_UINT8)
-            return fail(ASCQ_E_UNSUPPORTED, "matmul_create: int8 matmul supports C = f16, bf16, int32, int8 or uint8");
+            types->c_type != ASCQ_DT_INT8 && types->c_type != ASCQ_DT_UINT8 && types->c_type != ASCQ_DT_INT4)
+            return fail(ASCQ_E_UNSUPPORTED,
+                        "matmul_create: int8 matmul supports C = f16, bf16, int32, int8, uint8 or int4");
         if (types->bias_type != 0 && types->bias_type != ASCQ_DT_INT32)
             return fail(ASCQ_E_UNSUPPORTED, "matmul_create: int8 matmul bias must be int32");
         if (types->b_format != ASCQ_FORMAT_ND) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: int8 B must be ND");
@@ -253,9 +254,10 @@ ascq_status ascq_matmul_create(const ascq_matmul_types* types, ascq_matmul_t* ou
         if (types->bias_type != 0) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: weight-only matmul has no bias path");
     } else if (k == K_F8) {
         if (types->c_type != ASCQ_DT_F16 && types->c_type != ASCQ_DT_BF16 && types->c_type != ASCQ_DT_F32 &&
-            types->c_type != ASCQ_DT_INT8 && types->c_type != ASCQ_DT_UINT8 && !is_f8(types->c_type))
+            types->c_type != ASCQ_DT_INT8 && types->c_type != ASCQ_DT_UINT8 && types->c_type != ASCQ_DT_INT4 &&
+            !is_f8(types->c_type))
             return fail(ASCQ_E_UNSUPPORTED,
-                        "matmul_create: fp8 matmul supports C = f16, bf16, f32, int8, uint8, fp8_e4m3 or fp8_e5m2");
+                        "matmul_create: fp8 matmul supports C = f16, bf16, f32, int8, uint8, int4, fp8_e4m3 or fp8_e5m2");
         if (types->bias_type != 0 && types->bias_type != ASCQ_DT_F32)
             return fail(ASCQ_E_UNSUPPORTED, "matmul_create: fp8 matmul bias must be f32");
         if (types->b_format != ASCQ_FORMAT_ND) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: fp8 B must be ND");
@@ -441,7 +443,9 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
     switch (kind_of(h->ty)) {
     case K_INT8: {
         if (h->ty.c_type != ASCQ_DT_INT32 && !h->quant_set)
-            return fail(ASCQ_E_STATE, "iterate_all: f16/bf16/int8/uint8 output needs SetQuantScalar or SetQuantVector");
+            return fail(ASCQ_E_STATE, "iterate_all: f16/bf16/int8/uint8/int4 output needs SetQuantScalar or SetQuantVector");
+        if (h->ty.c_type == ASCQ_DT_INT4 && (h->N % 2 != 0 || n % 2 != 0))
+            return fail(ASCQ_E_INVALID_ARG, "iterate_all: int4 C packs two codes per byte: N must be even");
         ascq::GemmI8Args g{};
         g.A = (const int8_t*)h->a;
         g.B = (const int8_t*)h->b;
@@ -459,7 +463,8 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         case ASCQ_DT_INT32: g.epi = ascq::EPI_I32; break;
         case ASCQ_DT_F16: g.epi = ascq::EPI_DEQ_F16; break;
         case ASCQ_DT_BF16: g.epi = ascq::EPI_DEQ_BF16; break;
-        default: g.epi = ascq::EPI_REQ8; break;  // int8 / uint8: (V)REQ8
+        case ASCQ_DT_INT4: g.epi = ascq::EPI_REQ4; break;  // (V)REQ4
+        default: g.epi = ascq::EPI_REQ8; break;            // int8 / uint8: (V)REQ8
         }
         ByteOperands o;
         ascq_status s = prepare_byte_operands(h, st, o);
@@ -474,8 +479,10 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
     }
     case K_F8: {
         const int32_t ct = h->ty.c_type;
-        if ((ct == ASCQ_DT_INT8 || ct == ASCQ_DT_UINT8 || is_f8(ct)) && !h->quant_set)
-            return fail(ASCQ_E_STATE, "iterate_all: int8/uint8/fp8 output needs SetQuantScalar or SetQuantVector");
+        if ((ct == ASCQ_DT_INT8 || ct == ASCQ_DT_UINT8 || ct == ASCQ_DT_INT4 || is_f8(ct)) && !h->quant_set)
+            return fail(ASCQ_E_STATE, "iterate_all: int8/uint8/int4/fp8 output needs SetQuantScalar or SetQuantVector");
+        if (ct == ASCQ_DT_INT4 && (h->N % 2 != 0 || n % 2 != 0))
+            return fail(ASCQ_E_INVALID_ARG, "iterate_all: int4 C packs two codes per byte: N must be even");
         ascq::GemmF8Args g{};
         ByteOperands o;
         ascq_status s = prepare_byte_operands(h, st, o);

@@ -76,6 +76,19 @@ __device__ __forceinline__ uint8_t requant8(float v, uint64_t w)
     return (uint8_t)(t < 0 ? 0 : (t > 255 ? 255 : t));
 }
 
+// (V)REQ4 / (V)QF322S4_PRE after the multiply by M1: the same 9-bit intermediate as REQ8 (NaN -> 0, clamp to
+// [-256, 255], rint, + the word's offset), then saturation to int4 [-8, 7]
+// (docs/zh/api/SIMD-API/c_api/cube_datamove/cube_store_aux_config/asc_set_l0c_copy_prequant.md:37-41, 106;
+// docs/zh/api/appendix/matrix_compute_move_out_interface_boundary_value_summary.md:110-111).  Returns the code in
+// the low 4 bits.
+__device__ __forceinline__ uint32_t requant4(float v, uint64_t w)
+{
+    if (v != v) v = 0.0f;
+    const float c = fminf(fmaxf(v, -256.0f), 255.0f);
+    const int t = (int)__builtin_rintf(c) + (int)((w >> 37) & 0x1FFu);
+    return (uint32_t)(t < -8 ? -8 : (t > 7 ? 7 : t)) & 0xFu;
+}
+
 // f32 -> fp8 with round to nearest even, on the bit pattern.  e4m3fn (fmt 0) saturates as the fixpipe's default
 // mode does: |x| >= 448 and +-inf give +-448, NaN gives 0.  e5m2 (fmt 1): overflow (|x| >= 61440) gives +-inf,
 // NaN gives 0x7F.  Normal results: add the rounding bias below the kept mantissa bits (half minus one, plus the

@@ -80,6 +80,27 @@ __device__ __forceinline__ TileOut tile_out(void* C, int64_t m0, int64_t n0, int
     return t;
 }
 
+// int4 output tile (two codes per byte, even column in the low nibble; ldc even): byte pitch ldc / 2
+__device__ __forceinline__ TileOut tile_out_int4(void* C, int64_t m0, int64_t n0, int64_t ldc, int rows, int cols)
+{
+    TileOut t;
+    t.r = make_rsrc((uint8_t*)C + (m0 * ldc + n0) / 2, (uint32_t)((int64_t)(rows - 1) * (ldc / 2) + (cols + 1) / 2));
+    t.pitch = (uint32_t)(ldc / 2);
+    return t;
+}
+
+// Packs the int4 codes of a 32-column accumulator fragment: lanes 2t and 2t + 1 hold columns 2t and 2t + 1 of the
+// same rows, so the even lane stores (own | neighbour << 4); odd lanes, and columns past the tile, store nothing.
+// Every lane must call it (the neighbour's code comes through a cross-lane move).
+__device__ __forceinline__ void store_int4_pair(const TileOut& o, uint32_t q, int cl, int cols, int lane,
+                                                uint32_t row_off)
+{
+    const uint32_t nb = (uint32_t)__shfl_xor((int)q, 1, 64);
+    const uint32_t hi = cl + 1 < cols ? (nb & 0xFu) : 0u;
+    const uint32_t off = ((lane & 1) == 0 && cl < cols) ? (uint32_t)(cl >> 1) + row_off : OOB;
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)((q & 0xFu) | (hi << 4)), o.r, off, 0, 0);
+}
+
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // 16 bytes per lane, global (buffer) -> LDS at lds_wave_base + 16 * lane; lds_wave_base must be wave-uniform.

@@ -80,6 +80,28 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const float mscalar = quant_pre_m1(p.qscalar);
+    if (p.c_type == DT_INT4) {  // (V)QF322S4_PRE: int4 codes, two per byte
+        const TileOut o4 = tile_out_int4(p.C, m0, n0, p.ldc, c.rows, c.cols);
+#pragma unroll
+        for (int j = 0; j < T::FN; ++j) {
+            const int cl = T::frag_col(wn, j, lane);
+            const bool cok = cl < c.cols;
+            const int64_t col = n0 + cl;
+            const float bias = (p.bias && cok) ? p.bias[col] : 0.0f;
+            const uint64_t w = (p.qvec && cok) ? p.qvec[col] : p.qscalar;
+            const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
+#pragma unroll
+            for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float v = acc[i][j][r];
+                    if (p.bias) v = v + bias;
+                    store_int4_pair(o4, requant4(v * m1, w), cl, c.cols, lane,
+                                    (uint32_t)T::frag_row(wm, i, r, lane) * o4.pitch);
+                }
+        }
+        return;
+    }
     const int esize = p.c_type == DT_F32 ? 4 : ((p.c_type == DT_F16 || p.c_type == DT_BF16) ? 2 : 1);
     const TileOut out = tile_out(p.C, m0, n0, p.ldc, c.rows, c.cols, esize);
     auto store = [&](auto conv, auto put) {
@@ -117,10 +139,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
 // Any shape / layout / alignment: one thread per output element, fp32 accumulation in k order.
 __global__ __launch_bounds__(256) void gemm_f8_generic_kernel(GemmF8Args p)
 {
-    const int64_t total = p.M * p.N;
     const float mscalar = quant_pre_m1(p.qscalar);
-    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
-        const int64_t m = e / p.N, n = e % p.N;
+    // (acc + bias) * M1 of element (m, n), fp32 accumulation in k order
+    auto value = [&](int64_t m, int64_t n, uint64_t w) {
         float acc = 0.0f;
         for (int64_t k = 0; k < p.K; ++k) {
             const float a = fp8_to_f32(p.trans_a ? p.A[k * p.lda + m] : p.A[m * p.lda + k], p.fmt_a);
@@ -128,9 +149,27 @@ __global__ __launch_bounds__(256) void gemm_f8_generic_kernel(GemmF8Args p)
             acc = acc + a * b;  // the product of two fp8 values is exact in fp32
         }
         if (p.bias) acc = acc + p.bias[n];
-        const uint64_t w = p.qvec ? p.qvec[n] : p.qscalar;
         if (p.use_quant) acc = acc * (p.qvec ? quant_pre_m1(w) : mscalar);
-        store_f8_out(p.C, p.c_type, m * p.ldc + n, acc, w);
+        return acc;
+    };
+    if (p.c_type == DT_INT4) {  // one thread per output byte (two int4 codes; N and ldc even)
+        const int64_t half = p.N / 2, total = p.M * half;
+        for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+            const int64_t m = e / half, n = 2 * (e % half);
+            uint32_t q[2];
+            for (int h = 0; h < 2; ++h) {
+                const uint64_t w = p.qvec ? p.qvec[n + h] : p.qscalar;
+                q[h] = requant4(value(m, n + h, w), w);
+            }
+            ((uint8_t*)p.C)[(m * p.ldc + n) / 2] = (uint8_t)(q[0] | (q[1] << 4));
+        }
+        return;
+    }
+    const int64_t total = p.M * p.N;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+        const int64_t m = e / p.N, n = e % p.N;
+        const uint64_t w = p.qvec ? p.qvec[n] : p.qscalar;
+        store_f8_out(p.C, p.c_type, m * p.ldc + n, value(m, n, w), w);
     }
 }
 

@@ -43,6 +43,27 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const float mscalar = quant_pre_m1(p.qscalar);
+    if (p.epi == EPI_REQ4) {  // (V)REQ4: int4 codes, two per byte
+        const TileOut o4 = tile_out_int4(p.C, m0, n0, p.ldc, c.rows, c.cols);
+#pragma unroll
+        for (int j = 0; j < T::FN; ++j) {
+            const int cl = T::frag_col(wn, j, lane);
+            const bool cok = cl < c.cols;
+            const int64_t col = n0 + cl;
+            const int32_t bias = (p.bias && cok) ? p.bias[col] : 0;
+            const uint64_t w = (p.qvec && cok) ? p.qvec[col] : p.qscalar;
+            const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
+#pragma unroll
+            for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int32_t v = (int32_t)((uint32_t)acc[i][j][r] + (uint32_t)bias);
+                    store_int4_pair(o4, requant4((float)v * m1, w), cl, c.cols, lane,
+                                    (uint32_t)T::frag_row(wm, i, r, lane) * o4.pitch);
+                }
+        }
+        return;
+    }
     const int esize = p.epi == EPI_I32 ? 4 : (p.epi == EPI_REQ8 ? 1 : 2);
     const TileOut out = tile_out(p.C, m0, n0, p.ldc, c.rows, c.cols, esize);
     auto store = [&](auto conv, auto put) {
@@ -177,17 +198,34 @@ __global__ __launch_bounds__(WM * WN * 64) void group_gemm_i8_kernel(GroupGemmAr
 // Any shape / layout / alignment: one thread per output element, int32 accumulate, same epilogue.
 __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(GemmI8Args p)
 {
-    const int64_t total = p.M * p.N;
     const float mscalar = quant_pre_m1(p.qscalar);
-    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
-        const int64_t m = e / p.N, n = e % p.N;
+    // acc + bias of element (m, n), int32 wrap-around as the MFMA accumulates
+    auto value = [&](int64_t m, int64_t n) {
         uint32_t acc = 0;
         for (int64_t k = 0; k < p.K; ++k) {
             const int32_t a = p.trans_a ? p.A[k * p.lda + m] : p.A[m * p.lda + k];
             const int32_t b = p.trans_b ? p.B[n * p.ldb + k] : p.B[k * p.ldb + n];
             acc += (uint32_t)(a * b);
         }
-        const int32_t v = (int32_t)(acc + (uint32_t)(p.bias ? p.bias[n] : 0));
+        return (int32_t)(acc + (uint32_t)(p.bias ? p.bias[n] : 0));
+    };
+    if (p.epi == EPI_REQ4) {  // one thread per output byte (two int4 codes; N and ldc even)
+        const int64_t half = p.N / 2, total = p.M * half;
+        for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+            const int64_t m = e / half, n = 2 * (e % half);
+            uint32_t q[2];
+            for (int h = 0; h < 2; ++h) {
+                const uint64_t w = p.qvec ? p.qvec[n + h] : p.qscalar;
+                q[h] = requant4((float)value(m, n + h) * (p.qvec ? quant_pre_m1(w) : mscalar), w);
+            }
+            ((uint8_t*)p.C)[(m * p.ldc + n) / 2] = (uint8_t)(q[0] | (q[1] << 4));
+        }
+        return;
+    }
+    const int64_t total = p.M * p.N;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+        const int64_t m = e / p.N, n = e % p.N;
+        const int32_t v = value(m, n);
         const uint64_t w = p.qvec ? p.qvec[n] : p.qscalar;
         const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
         const int64_t o = m * p.ldc + n;

@@ -43,7 +43,7 @@ hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_ty
                             hipStream_t st);
 
 // gemm_i8.hip
-enum : int { EPI_I32 = 0, EPI_DEQ_F16 = 1, EPI_DEQ_BF16 = 2, EPI_REQ8 = 3 };
+enum : int { EPI_I32 = 0, EPI_DEQ_F16 = 1, EPI_DEQ_BF16 = 2, EPI_REQ8 = 3, EPI_REQ4 = 4 };
 struct GemmI8Args {
     const int8_t* A;      // [M, K] row-major (lda), or [K, M] when trans_a
     const int8_t* B;      // [K, N] row-major (ldb), or [N, K] when trans_b

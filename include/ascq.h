@@ -120,6 +120,12 @@ uint64_t ascq_pack_quant_pre(float m1, int32_t offset9, int32_t sign_flag);
  *  fp8_e4m3|fp8_e5m2 (any mix), f16|bf16|f32, f32 bias
  *                               (+ SetQuantScalar/Vector -> QF322F16 / QF322BF16 / QF322F32 _PRE; without a
  *                               quant word a plain cast; quant_processor_fixpipe.h:101-115)
+ *  int8, int8, int4, int32 + SetQuantScalar/Vector -> REQ4 / VREQ4: sat4(rint(clamp(f32(acc) * M1, -256, 255))
+ *                               + offset), C packed two codes per byte (even column in the low nibble, N even);
+ *                               a fixpipe mode of the reference (asc_set_l0c_copy_prequant.md:37-41, boundary table
+ *                               matrix_compute_move_out_interface_boundary_value_summary.md:110-111) that the
+ *                               Matmul's own mode table does not select
+ *  fp8, fp8, int4 + SetQuantScalar/Vector -> QF322S4_PRE (as REQ4 on the fp32 accumulator)
  *  fp8, fp8, int8|uint8 + SetQuantScalar/Vector -> QF322B8_PRE (as REQ8 on the fp32 accumulator)
  *  fp8, fp8, fp8_e4m3|fp8_e5m2 + SetQuantScalar/Vector -> QF322FP8_PRE (rne; e4m3 saturates at +-448, NaN -> 0)
  *  fp4_e2m1, fp4_e2m1, bf16|f32 with E8M0 scales (SetTensorScaleA/B) -> MX block-scaled (K % 128 == 0)

@@ -241,6 +241,53 @@ uint8_t oq_requant8(float v, uint64_t word)
     return (uint8_t)t;
 }
 
+/* (V)REQ4 / (V)QF322S4_PRE, int4 output of the fixpipe (docs/zh/api/SIMD-API/c_api/cube_datamove/
+ * cube_store_aux_config/asc_set_l0c_copy_prequant.md:37-41 (modes), :106 and :117 (the 9-bit offset applies to
+ * REQ4 / QF322S4_PRE, the sign flag does not), docs/zh/api/appendix/
+ * matrix_compute_move_out_interface_boundary_value_summary.md:110-111 (saturation to 7 / -8)).  The reference
+ * ships no golden for these modes; the 9-bit intermediate (clamp to [-256, 255], rint, + offset) is taken from
+ * REQ8's golden (gen_data_s322s8.py:56-80), so only the documented saturation pins this beyond that assumption.
+ * Returns the int4 code in the low nibble. */
+uint8_t oq_requant4(float v, uint64_t word)
+{
+    if (isnan(v)) v = 0.0f;
+    float c = v < -256.0f ? -256.0f : (v > 255.0f ? 255.0f : v);
+    int t = (int)rintf(c) + (OQ_MUTANT == 17 ? 0 : (int)((word >> 37) & 0x1FFu));
+    t = t < -8 ? -8 : (t > 7 ? 7 : t);
+    return (uint8_t)(t & 0xF);
+}
+
+/* int32 accumulators [M, N] -> (V)REQ4 codes packed two per byte ([M, N/2], even column in the low nibble, the
+ * int4b_t layout of examples/01_simd_cpp_api/04_advanced_api/00_matmul/matmul_int4/scripts/gen_data.py);
+ * N even */
+void oq_mm_requant4(const int32_t* acc, uint8_t* out, int64_t M, int64_t N, const uint64_t* qvec, uint64_t qscalar)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; n += 2) {
+            uint8_t q[2];
+            for (int h = 0; h < 2; ++h) {
+                const uint64_t w = qvec ? qvec[n + h] : qscalar;
+                q[h] = oq_requant4((float)acc[m * N + n + h] * oq_quant_pre_m1(w), w);
+            }
+            out[(m * N + n) / 2] = OQ_MUTANT == 18 ? (uint8_t)(q[1] | (q[0] << 4)) : (uint8_t)(q[0] | (q[1] << 4));
+        }
+}
+
+/* fp32 L0C values (acc + bias) [M, N] -> (V)QF322S4_PRE codes: requant4(v * M1, word), packed as above */
+void oq_requant4_f32(const float* v, uint8_t* out, int64_t M, int64_t N, const uint64_t* qvec, uint64_t qscalar)
+{
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; n += 2) {
+            uint8_t q[2];
+            for (int h = 0; h < 2; ++h) {
+                const uint64_t w = qvec ? qvec[n + h] : qscalar;
+                q[h] = oq_requant4(v[m * N + n + h] * oq_quant_pre_m1(w), w);
+            }
+            out[(m * N + n) / 2] = OQ_MUTANT == 18 ? (uint8_t)(q[1] | (q[0] << 4)) : (uint8_t)(q[0] | (q[1] << 4));
+        }
+}
+
 static inline float load_as_f32(const void* p, int type, int64_t i)
 {
     switch (type) {

@@ -54,6 +54,9 @@ def lib() -> ctypes.CDLL:
             "oq_f32_to_fp8": (ctypes.c_uint8, [ctypes.c_float, ctypes.c_int]),
             "oq_requant8": (ctypes.c_uint8, [ctypes.c_float, ctypes.c_uint64]),
             "oq_mm_requant": (None, [_P, _P, _I64, _I64, _P, ctypes.c_uint64]),
+            "oq_requant4": (ctypes.c_uint8, [ctypes.c_float, ctypes.c_uint64]),
+            "oq_mm_requant4": (None, [_P, _P, _I64, _I64, _P, ctypes.c_uint64]),
+            "oq_requant4_f32": (None, [_P, _P, _I64, _I64, _P, ctypes.c_uint64]),
             "oq_matmul_i8": (None, [_P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int]),
             "oq_mm_dequant": (None, [_P, _P, ctypes.c_int, _I64, _I64, _P, ctypes.c_uint64]),
             "oq_matmul_fp8": (None, [_P, _P, ctypes.c_int, ctypes.c_int, _P, _P, ctypes.c_int, _I64, _I64, _I64,
@@ -157,6 +160,36 @@ def mm_requant(acc, qvec=None, qscalar=0):
     out = np.empty((M, N), np.uint8)
     qv = None if qvec is None else np.ascontiguousarray(qvec, np.uint64)
     lib().oq_mm_requant(_p(acc), _p(out), M, N, _p(qv), int(qscalar))
+    return out
+
+
+def mm_requant4(acc, qvec=None, qscalar=0):
+    """(V)REQ4: int32 accumulators [M, N] (N even) -> int4 codes packed two per byte [M, N/2]"""
+    acc = np.ascontiguousarray(acc, np.int32)
+    M, N = acc.shape
+    out = np.empty((M, N // 2), np.uint8)
+    qv = None if qvec is None else np.ascontiguousarray(qvec, np.uint64)
+    lib().oq_mm_requant4(_p(acc), _p(out), M, N, _p(qv), int(qscalar))
+    return out
+
+
+def requant4_f32(v, qvec=None, qscalar=0):
+    """(V)QF322S4_PRE on fp32 values (acc + bias) [M, N] (N even) -> packed int4 codes [M, N/2]"""
+    v = np.ascontiguousarray(v, np.float32)
+    M, N = v.shape
+    out = np.empty((M, N // 2), np.uint8)
+    qv = None if qvec is None else np.ascontiguousarray(qvec, np.uint64)
+    lib().oq_requant4_f32(_p(v), _p(out), M, N, _p(qv), int(qscalar))
+    return out
+
+
+def unpack_int4(packed, n):
+    """[M, N/2] bytes -> [M, N] int8 values (even column in the low nibble, two's complement nibbles)"""
+    lo = (packed & 0xF).astype(np.int8)
+    hi = (packed >> 4).astype(np.int8)
+    out = np.empty((packed.shape[0], n), np.int8)
+    out[:, 0::2] = np.where(lo >= 8, lo - 16, lo)
+    out[:, 1::2] = np.where(hi >= 8, hi - 16, hi)
     return out
 
 

@@ -178,3 +178,89 @@ def test_requant_needs_quant_word(ascq_gpu):
     mm.SetTensorB(a)
     with pytest.raises(ascq_gpu.AscqError):
         mm.IterateAll(torch.empty((16, 16), dtype=torch.uint8, device="cuda"))
+
+
+# --------------------------------------------------------------------------- REQ4 / QF322S4 (int4 C)
+def words4(rng, n, lo, hi):
+    """QUANT_PRE words for int4 output: M1 log-uniform in [lo, hi], offsets 0..3 (a larger offset saturates every
+    output at 7), random sign flags (ignored by the int4 modes), bits 32-36 set at random"""
+    m1 = np.exp(rng.uniform(np.log(lo), np.log(hi), n)).astype(np.float32)
+    off = rng.integers(0, 4, n)
+    sign = rng.integers(0, 2, n)
+    w = np.array([O.lib().oq_pack_quant_pre(float(a), int(o), int(s)) for a, o, s in zip(m1, off, sign)], np.uint64)
+    return w | (rng.integers(0, 32, n).astype(np.uint64) << np.uint64(32))
+
+
+def run4(ascq, a_t, b_t, A, B, M, N, K, trans_b=False, bias=None, qvec=None, qscalar=None, bias_t=0):
+    mm = ascq.Matmul(a_t, b_t, ascq.INT4, bias_t if bias is not None else 0)
+    mm.SetOrgShape(M, N, K)
+    mm.SetTensorA(_dev(A))
+    mm.SetTensorB(_dev(B), trans_b)
+    if bias is not None:
+        mm.SetBias(_dev(bias))
+    if qvec is not None:
+        mm.SetQuantVector(_dev(qvec.view(np.int64)))
+    else:
+        mm.SetQuantScalar(int(qscalar))
+    c = torch.full((M, N // 2), 0x5A, dtype=torch.uint8, device="cuda")
+    mm.IterateAll(c)
+    mm.End()
+    torch.cuda.synchronize()
+    return c.cpu().numpy()
+
+
+@pytest.mark.parametrize("M,N,K", [(200, 136, 208), (64, 64, 64), (1100, 1040, 1040), (37, 18, 53)])
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_req4_vs_oracle(ascq_gpu, M, N, K, trans_b):
+    """(V)REQ4 bit-exact: int32 sums are exact on both sides; (37, 18, 53) takes the untiled kernel"""
+    rng = seeded(M * 5 + N * 11 + K + trans_b)
+    A = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    B = rng.integers(-128, 128, (N, K) if trans_b else (K, N)).astype(np.int8)
+    bias = rng.integers(-(1 << 14), 1 << 14, N).astype(np.int32)
+    acc = O.matmul_i8(A, B, bias=bias, trans_b=trans_b)
+    qv = words4(rng, N, 2.0 ** -15, 2.0 ** -10)  # |acc| up to ~K * 2^14: spreads over the int4 range
+    got = run4(ascq_gpu, ascq_gpu.INT8, ascq_gpu.INT8, A, B, M, N, K, trans_b, bias, qvec=qv, bias_t=ascq_gpu.INT32)
+    exp = O.mm_requant4(acc, qvec=qv)
+    assert np.array_equal(got, exp), f"{(got != exp).sum()} mismatching bytes"
+    vals = O.unpack_int4(exp, N)
+    assert (vals == 7).mean() < 0.5 and (vals == -8).mean() < 0.5  # not a blanket saturation
+    ws = int(qv[1])
+    got = run4(ascq_gpu, ascq_gpu.INT8, ascq_gpu.INT8, A, B, M, N, K, trans_b, bias, qscalar=ws, bias_t=ascq_gpu.INT32)
+    assert np.array_equal(got, O.mm_requant4(acc, qscalar=ws))
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 16, 16), (200, 136, 208), (1100, 1040, 1040)])
+def test_fp8_qf322s4_vs_oracle(ascq_gpu, M, N, K):
+    """(V)QF322S4_PRE: each output lies between the mode applied to the low and the high end of the oracle's
+    interval [s - d, s + d] (the fp8 MFMA's group-alignment error, test_gpu_fp8.py), equals the oracle where
+    those agree, and overall at least 97 % equal it"""
+    fa, fb = O.FP8_E4M3, O.FP8_E5M2
+    rng = seeded(M + 3 * N + K)
+    trans_b = M > 512
+    A, B = fp8_inputs(rng, M, N, K, fa, fb, trans_b)
+    bias = rng.standard_normal(N).astype(np.float32)
+    qv = words4(rng, N, 2.0 ** -1, 2.0 ** 2)
+    _, exact, absd, bmax = O.matmul_fp8(A, B, fa, fb, bias=bias, out_type=O.F32, trans_b=trans_b)
+    got = O.unpack_int4(run4(ascq_gpu, ascq_gpu.FP8_E4M3, ascq_gpu.FP8_E5M2, A, B, M, N, K, trans_b, bias, qvec=qv,
+                             bias_t=ascq_gpu.F32), N)
+    d = 2.0 ** -8 * bmax + K * 2.0 ** -24 * (absd + np.abs(bias)[None, :].astype(np.float64))
+    lo = O.unpack_int4(O.requant4_f32((exact - d).astype(np.float32), qvec=qv), N)
+    hi = O.unpack_int4(O.requant4_f32((exact + d).astype(np.float32), qvec=qv), N)
+    e = O.unpack_int4(O.requant4_f32(exact.astype(np.float32), qvec=qv), N)
+    assert ((got >= lo) & (got <= hi)).all(), f"{(~((got >= lo) & (got <= hi))).sum()} outputs outside the interval"
+    settled = lo == hi
+    assert np.array_equal(got[settled], e[settled])
+    assert (got == e).mean() > 0.97
+
+
+def test_int4_output_needs_even_n(ascq_gpu):
+    """int4 C packs two codes per byte: an odd N is an argument error, not a half-written byte"""
+    mm = ascq_gpu.Matmul(ascq_gpu.INT8, ascq_gpu.INT8, ascq_gpu.INT4)
+    mm.SetOrgShape(16, 15, 32)
+    a = torch.zeros((16, 32), dtype=torch.int8, device="cuda")
+    b = torch.zeros((32, 15), dtype=torch.int8, device="cuda")
+    mm.SetTensorA(a)
+    mm.SetTensorB(b)
+    mm.SetQuantScalar(int(O.lib().oq_pack_quant_pre(1.0, 0, 1)))
+    with pytest.raises(ascq_gpu.AscqError):
+        mm.IterateAll(torch.empty((16, 8), dtype=torch.uint8, device="cuda"))

@@ -579,6 +579,29 @@ def test_requant8_boundaries_and_offsets():
     assert L.oq_requant8(float("inf"), wu) == 255 and L.oq_requant8(float("-inf"), wu) == 0
 
 
+def test_requant4_saturation_offset_and_packing():
+    """(V)REQ4 / QF322S4_PRE: saturation to 7 / -8 (matrix_compute_move_out_interface_boundary_value_summary.md:
+    110-111), the 9-bit offset applies after rounding and the sign flag does not (asc_set_l0c_copy_prequant.md:106,
+    117); codes packed two per byte with the even column in the low nibble (the int4b_t layout of
+    matmul_int4/scripts/gen_data.py: (x[j+1] << 4) + (x[j] & 0xF))"""
+    L = O.lib()
+    w = _word(1.0, 0, 1)
+    nan, inf = float("nan"), float("inf")
+    for v, e in [(0.0, 0), (7.4, 7), (7.5, 7), (6.5, 6), (2.5, 2), (-2.5, -2), (-7.5, -8), (-8.5, -8), (-9.0, -8),
+                 (1e6, 7), (-1e6, -8), (nan, 0), (inf, 7), (-inf, -8)]:
+        assert L.oq_requant4(v, w) == e & 0xF, v
+    w3 = _word(1.0, 3, 0)
+    assert L.oq_requant4(2.0, w3) == 5 and L.oq_requant4(5.0, w3) == 7 and L.oq_requant4(-12.0, w3) == 0x8
+    assert L.oq_requant4(-20.0, _word(1.0, 15, 1)) == (-5 & 0xF) == L.oq_requant4(-20.0, _word(1.0, 15, 0))
+    assert L.oq_requant4(-1e6, _word(1.0, 300, 1)) == 7  # clamped to -256 before the offset: 44 -> 7
+    assert O.mm_requant4(np.array([[12, -13]], np.int32), qscalar=_word(0.5, 0, 1)).tolist() == [[0xA6]]  # x M1 first
+    acc = np.array([[1, -2, 7, -8, 100, -100, 3, 0]], np.int32)
+    assert O.mm_requant4(acc, qscalar=w).tolist() == [[0xE1, 0x87, 0x87, 0x03]]
+    assert np.array_equal(O.unpack_int4(O.mm_requant4(acc, qscalar=w), 8), [[1, -2, 7, -8, 7, -8, 3, 0]])
+    f = np.array([[0.25, -0.75, 6.5, 7.5]], np.float32)  # fp32 path: rint ties to even
+    assert O.unpack_int4(O.requant4_f32(f, qscalar=w), 4).tolist() == [[0, -1, 6, 7]]
+
+
 @pytest.mark.parametrize("fmt", [O.FP8_E4M3, O.FP8_E5M2])
 def test_f32_to_fp8_vs_torch(fmt):
     """in-range values (including exact ties between neighbouring codes and subnormals) vs torch's rne cast;

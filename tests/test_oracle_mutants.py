@@ -37,6 +37,8 @@ MUTANTS = {
     14: "f32->fp8 ties rounded away from zero",
     15: "requant sign flag ignored (always int8 saturation)",
     16: "FasterGelu coefficient with the wrong sign",
+    17: "int4 requant without the 9-bit offset",
+    18: "int4 requant output nibbles swapped",
 }
 
 
