@@ -69,7 +69,7 @@ struct ascq_matmul_s {
 
 namespace {
 
-enum Kind { K_NONE, K_INT8, K_ANTIQUANT, K_MX, K_F8 };
+enum Kind { K_NONE, K_INT8, K_ANTIQUANT, K_MX, K_F8, K_INT4 };
 
 bool is_f8(int32_t t) { return t == ASCQ_DT_FP8_E4M3 || t == ASCQ_DT_FP8_E5M2; }
 // f8f6f4 format code of an fp8 / fp4 element type (the MFMA's cbsz / blgp field)
@@ -78,6 +78,7 @@ int f8f6f4_code(int32_t t) { return t == ASCQ_DT_FP8_E5M2 ? 1 : (t == ASCQ_DT_FP
 Kind kind_of(const ascq_matmul_types& t)
 {
     if (t.a_type == ASCQ_DT_INT8 && t.b_type == ASCQ_DT_INT8) return K_INT8;
+    if (t.a_type == ASCQ_DT_INT4 && t.b_type == ASCQ_DT_INT4) return K_INT4;
     if (t.a_type == ASCQ_DT_F16 && (t.b_type == ASCQ_DT_INT8 || t.b_type == ASCQ_DT_INT4)) return K_ANTIQUANT;
     if (t.scale_type == ASCQ_DT_E8M0 &&
         ((t.a_type == ASCQ_DT_FP4_E2M1 && t.b_type == ASCQ_DT_FP4_E2M1) || (is_f8(t.a_type) && is_f8(t.b_type))))
@@ -92,7 +93,7 @@ bool mx_is_fp4(const ascq_matmul_s* h) { return h->ty.a_type == ASCQ_DT_FP4_E2M1
 bool has_quant_epilogue(const ascq_matmul_types& t)
 {
     const Kind k = kind_of(t);
-    return (k == K_INT8 && t.c_type != ASCQ_DT_INT32) || k == K_F8;
+    return ((k == K_INT8 || k == K_INT4) && t.c_type != ASCQ_DT_INT32) || k == K_F8;
 }
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -121,6 +122,9 @@ size_t workspace_need(const ascq_matmul_s* h)
     switch (kind_of(h->ty)) {
     case K_INT8:
     case K_F8: return bytes_workspace(h);
+    case K_INT4:  // A and B unpacked to int8 [M, K] / [N, K]; a [K, N] B is nibble-transposed to [N, K/2] first
+        return align256((size_t)h->M * (size_t)h->K) + align256((size_t)h->N * (size_t)h->K) +
+               (h->trans_b ? 0 : align256((size_t)h->N * (size_t)h->K / 2));
     case K_ANTIQUANT: {
         size_t need = 0;
         if (h->ty.b_format == ASCQ_FORMAT_ND) need += ascq::weight_pack_bytes(h->ty.b_type, h->K, h->N);
@@ -241,7 +245,7 @@ ascq_status ascq_matmul_create(const ascq_matmul_types* types, ascq_matmul_t* ou
     const Kind k = kind_of(*types);
     if (k == K_NONE)
         return fail(ASCQ_E_UNSUPPORTED, "matmul_create: unsupported A/B types (%d, %d)", types->a_type, types->b_type);
-    if (k == K_INT8) {
+    if (k == K_INT8 || k == K_INT4) {
         if (types->c_type != ASCQ_DT_F16 && types->c_type != ASCQ_DT_BF16 && types->c_type != ASCQ_DT_INT32 &&
             types->c_type != ASCQ_DT_INT8 && types->c_type != ASCQ_DT_UINT8 && types->c_type != ASCQ_DT_INT4)
             return fail(ASCQ_E_UNSUPPORTED,
@@ -476,6 +480,56 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         g.trans_a = o.trans_a;
         g.trans_b = o.trans_b;
         return hip_status(ascq::launch_gemm_i8(g, st), "gemm_i8");
+    }
+    case K_INT4: {
+        // int4b_t A / B (matmul_int4.asc:151; README constraints: A not transposed, C int32 or half): both are
+        // unpacked to int8 in the workspace, then the int8 GEMM and its epilogues run unchanged (exact: int4 x int4
+        // products sum in int32 as on the cube unit)
+        if (h->trans_a) return fail(ASCQ_E_UNSUPPORTED, "iterate_all: an int4 A cannot be transposed");
+        if (h->K % 2 != 0 || h->N % 2 != 0)
+            return fail(ASCQ_E_INVALID_ARG, "iterate_all: int4 operands pack two per byte: K and N must be even");
+        if (h->ty.c_type != ASCQ_DT_INT32 && !h->quant_set)
+            return fail(ASCQ_E_STATE, "iterate_all: f16/bf16/int8/uint8/int4 output needs SetQuantScalar or SetQuantVector");
+        if (h->ty.c_type == ASCQ_DT_INT4 && n % 2 != 0)
+            return fail(ASCQ_E_INVALID_ARG, "iterate_all: int4 C packs two codes per byte: N must be even");
+        ascq_status s = ensure_workspace(h);
+        if (s != ASCQ_OK) return s;
+        int8_t* a8 = (int8_t*)h->ws;
+        int8_t* b8 = a8 + align256((size_t)h->M * (size_t)h->K);
+        hipError_t e = ascq::launch_unpack_int4(a8, (const uint8_t*)h->a, h->M * h->K / 2, st);
+        if (e != hipSuccess) return hip_status(e, "unpack A");
+        const uint8_t* bsrc = (const uint8_t*)h->b;
+        if (!h->trans_b) {  // [K, N/2] packed along N -> [N, K/2] packed along K
+            uint8_t* bt = (uint8_t*)b8 + align256((size_t)h->N * (size_t)h->K);
+            e = ascq::launch_fp4_transpose(bt, bsrc, h->K, h->N, st);
+            if (e != hipSuccess) return hip_status(e, "transpose B");
+            bsrc = bt;
+        }
+        e = ascq::launch_unpack_int4(b8, bsrc, h->N * h->K / 2, st);
+        if (e != hipSuccess) return hip_status(e, "unpack B");
+        ascq::GemmI8Args g{};
+        g.A = a8;
+        g.B = b8;
+        g.bias = (const int32_t*)h->bias;
+        g.C = c;
+        g.M = m;
+        g.N = n;
+        g.K = k;
+        g.lda = h->K;
+        g.ldb = h->K;
+        g.ldc = h->N;
+        g.qvec = h->qvec;
+        g.qscalar = h->qscalar;
+        g.trans_a = 0;
+        g.trans_b = 1;
+        switch (h->ty.c_type) {
+        case ASCQ_DT_INT32: g.epi = ascq::EPI_I32; break;
+        case ASCQ_DT_F16: g.epi = ascq::EPI_DEQ_F16; break;
+        case ASCQ_DT_BF16: g.epi = ascq::EPI_DEQ_BF16; break;
+        case ASCQ_DT_INT4: g.epi = ascq::EPI_REQ4; break;
+        default: g.epi = ascq::EPI_REQ8; break;
+        }
+        return hip_status(ascq::launch_gemm_i8(g, st), "gemm_i8 (int4 operands)");
     }
     case K_F8: {
         const int32_t ct = h->ty.c_type;

@@ -122,6 +122,8 @@ hipError_t launch_nz_to_nd(void* dst, const void* src, int esize, int64_t batch,
                            int transpose_out, hipStream_t st);
 hipError_t launch_nd_to_nz(void* dst, const void* src, int esize, int64_t batch, int64_t rows, int64_t cols,
                            hipStream_t st);
+// int4 (two per byte, even element in the low nibble) -> int8, elementwise over `bytes` input bytes
+hipError_t launch_unpack_int4(int8_t* dst, const uint8_t* src, int64_t bytes, hipStream_t st);
 // transpose a [K, N] packed fp4 matrix (two per byte along N) into [N, K] (two per byte along K)
 hipError_t launch_fp4_transpose(uint8_t* dst, const uint8_t* src, int64_t K, int64_t N, hipStream_t st);
 

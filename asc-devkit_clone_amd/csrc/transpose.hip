@@ -135,4 +135,50 @@ bool fp4_transpose_tiled(uint8_t* dst, const uint8_t* src, int64_t K, int64_t N,
     return true;
 }
 
+// int4 (two's complement nibbles, two per byte, even element in the low nibble -- the int4b_t layout of
+// examples/01_simd_cpp_api/04_advanced_api/00_matmul/matmul_int4/scripts/gen_data.py) -> int8, elementwise over
+// `bytes` input bytes.  Fast path: 8 input bytes -> 16 output bytes per thread; per byte lane the two's complement
+// nibble n becomes offset-binary s = n ^ 8 (value s - 8), and ((s | 0x80) - 8) ^ 0x80 is s - 8 as a byte (the
+// subtraction never borrows across bytes); low / high nibbles are then interleaved with v_perm_b32.
+__device__ __forceinline__ uint32_t sext_nibbles(uint32_t n)  // four nibbles (one per byte) -> four int8
+{
+    return (((n ^ 0x08080808u) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+}
+
+__global__ __launch_bounds__(256) void unpack_int4_kernel(int8_t* __restrict__ dst, const uint8_t* __restrict__ src,
+                                                          int64_t bytes, bool fast)
+{
+    if (fast) {
+        const int64_t chunks = bytes / 8;
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < chunks; i += (int64_t)gridDim.x * 256) {
+            const u32x2 w = *(const u32x2*)(src + 8 * i);
+            u32x4 o;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t lo = sext_nibbles(w[h] & 0x0F0F0F0Fu), hi = sext_nibbles((w[h] >> 4) & 0x0F0F0F0Fu);
+                o[2 * h] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);      // lo.b0 hi.b0 lo.b1 hi.b1
+                o[2 * h + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // lo.b2 hi.b2 lo.b3 hi.b3
+            }
+            *(u32x4*)(dst + 16 * i) = o;
+        }
+        return;
+    }
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < bytes; i += (int64_t)gridDim.x * 256) {
+        const uint32_t b = src[i];
+        const uint32_t s = sext_nibbles((b & 0xFu) | ((b >> 4) << 8));
+        dst[2 * i] = (int8_t)(s & 0xFFu);
+        dst[2 * i + 1] = (int8_t)((s >> 8) & 0xFFu);
+    }
+}
+
+hipError_t launch_unpack_int4(int8_t* dst, const uint8_t* src, int64_t bytes, hipStream_t st)
+{
+    if (bytes <= 0) return hipSuccess;
+    const bool fast = bytes % 8 == 0 && (uintptr_t)src % 8 == 0 && (uintptr_t)dst % 16 == 0;
+    int64_t blocks = ((fast ? bytes / 8 : bytes) + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(unpack_int4_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, src, bytes, fast);
+    return hipGetLastError();
+}
+
 }  // namespace ascq

@@ -116,6 +116,9 @@ uint64_t ascq_pack_quant_pre(float m1, int32_t offset9, int32_t sign_flag);
  *  int8, int8, int8|uint8, int32 + SetQuantScalar/Vector -> REQ8 / VREQ8: sat8(rint(clamp(f32(acc) * M1,
  *                               -256, 255)) + offset), the word's sign flag picking int8 or uint8 saturation
  *                               (quant_processor_fixpipe.h:93-94, 211-212)
+ *  int4, int4, int32|f16 (or any int8 C above), int32 bias -> the int8 epilogues on exact int32 sums
+ *                               (matmul_int4/matmul_int4.asc:151; A not transposed, K and N even): both operands
+ *                               are unpacked to int8 in the workspace, B given [K, N] nibble-transposed first
  *  f16,  int8|int4, f16, f32  + SetAntiQuantScalar/Vector (weight-only, optional groups)
  *  fp8_e4m3|fp8_e5m2 (any mix), f16|bf16|f32, f32 bias
  *                               (+ SetQuantScalar/Vector -> QF322F16 / QF322BF16 / QF322F32 _PRE; without a

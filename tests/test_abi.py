@@ -139,6 +139,34 @@ def test_matmul_handle_state_machine():
     _err(L.ascq_matmul_destroy(h), ascq.OK)
 
 
+def test_int4_operand_handle():
+    """int4b_t A / B (matmul_int4): accepted with int32 / f16 C; the workspace holds both operands unpacked to
+    int8, plus the nibble-transposed B when B is given [K, N]; a transposed A and odd K / N are rejected before
+    any launch"""
+    L = ascq.lib()
+    h = ctypes.c_void_p()
+    d = ctypes.c_void_p(0x1000)
+    t = ascq._MatmulTypes(ascq.INT4, ascq.INT4, ascq.INT32, ascq.INT32, 0, 0)
+    _err(L.ascq_matmul_create(ctypes.byref(t), ctypes.byref(h)), ascq.OK)
+    _err(L.ascq_matmul_set_org_shape(h, 256, 7680, 128), ascq.OK)
+    _err(L.ascq_matmul_set_tensor_a(h, d, 0), ascq.OK)
+    _err(L.ascq_matmul_set_tensor_b(h, d, 0), ascq.OK)
+    ws = ctypes.c_size_t()
+    _err(L.ascq_matmul_workspace_size(h, ctypes.byref(ws)), ascq.OK)
+    assert ws.value == 256 * 128 + 7680 * 128 + 7680 * 64
+    _err(L.ascq_matmul_set_tensor_b(h, d, 1), ascq.OK)
+    _err(L.ascq_matmul_workspace_size(h, ctypes.byref(ws)), ascq.OK)
+    assert ws.value == 256 * 128 + 7680 * 128
+    _err(L.ascq_matmul_set_tensor_a(h, d, 1), ascq.OK)
+    _err(L.ascq_matmul_iterate_all(h, d, 0, None), ascq.E_UNSUPPORTED)   # transposed int4 A
+    _err(L.ascq_matmul_set_tensor_a(h, d, 0), ascq.OK)
+    _err(L.ascq_matmul_set_org_shape(h, 16, 16, 15), ascq.OK)
+    _err(L.ascq_matmul_iterate_all(h, d, 0, None), ascq.E_INVALID_ARG)   # odd K
+    _err(L.ascq_matmul_destroy(h), ascq.OK)
+    t = ascq._MatmulTypes(ascq.INT4, ascq.INT4, ascq.F32, 0, 0, 0)
+    _err(L.ascq_matmul_create(ctypes.byref(t), ctypes.byref(h)), ascq.E_UNSUPPORTED)
+
+
 def test_no_device_reports_zero_or_more():
     assert ascq.lib().ascq_device_count() >= 0
 

@@ -144,3 +144,66 @@ def test_single_shape_block(ascq_gpu, oracle):
     mask = np.ones_like(got, bool)
     mask[m0:m0 + bm, n0:n0 + bn] = False
     assert (got[mask] == 0).all()
+
+
+# --------------------------------------------------------------------------- int4b_t A / B (W4A4)
+def pack_int4_rows(x):
+    """int values in [-8, 7], [R, C] (C even) -> [R, C/2] bytes, the packing of matmul_int4/scripts/gen_data.py:
+    byte = (x[j + 1] << 4) + (x[j] & 0xF) in int8 arithmetic"""
+    x = np.asarray(x, np.int8)
+    return ((x[:, 1::2].astype(np.int32) << 4) + (x[:, 0::2].astype(np.int32) & 0xF)).astype(np.int8)
+
+
+def _run4(ascq, A4, B4, M, N, K, c_type, bias=None, words=None, trans_b=False, trans_a=False):
+    torch_c = {ascq.F16: torch.float16, ascq.INT32: torch.int32}[c_type]
+    mm = ascq.Matmul(ascq.INT4, ascq.INT4, c_type, ascq.INT32 if bias is not None else 0)
+    mm.SetOrgShape(M, N, K)
+    if words is not None:
+        mm.SetQuantVector(_dev(words.view(np.int64)))
+    mm.SetTensorA(_dev(A4), trans_a)
+    mm.SetTensorB(_dev(B4), trans_b)
+    if bias is not None:
+        mm.SetBias(_dev(bias))
+    c = torch.empty((M, N), dtype=torch_c, device="cuda")
+    mm.IterateAll(c)
+    mm.End()
+    torch.cuda.synchronize()
+    return c.cpu().numpy()
+
+
+def test_int4_matmul_sample_shape(ascq_gpu, oracle):
+    """the matmul_int4 sample: M = 256, N = 7680, K = 128, values from uniform(-5, 5) cast to int8 (so -4..4),
+    int32 bias, int32 C; golden = int32 A @ B + bias (gen_data.py)"""
+    rng = seeded(404)
+    M, N, K = 256, 7680, 128
+    x1 = rng.uniform(-5, 5, (M, K)).astype(np.int8)
+    x2 = rng.uniform(-5, 5, (K, N)).astype(np.int8)
+    bias = rng.uniform(-5, 5, N).astype(np.int32)
+    golden = x1.astype(np.int64) @ x2.astype(np.int64) + bias
+    got = _run4(ascq_gpu, pack_int4_rows(x1), pack_int4_rows(x2), M, N, K, ascq_gpu.INT32, bias=bias)
+    assert np.array_equal(got, golden.astype(np.int32))
+
+
+@pytest.mark.parametrize("trans_b", [False, True])
+@pytest.mark.parametrize("shape", [(200, 136, 208), (1024, 1024, 1024), (6, 18, 34)])
+def test_int4_matmul_deqf16(ascq_gpu, oracle, trans_b, shape):
+    """full int4 range, per-channel DEQF16: bit-exact vs the oracle's int32 sums and epilogue; B given [K, N]
+    (packed along N) or [N, K] (isTransposeB, packed along K)"""
+    M, N, K = shape
+    rng = seeded(M + N + K + 7 * trans_b)
+    a = rng.integers(-8, 8, (M, K)).astype(np.int8)
+    b = rng.integers(-8, 8, (K, N)).astype(np.int8)
+    bias = rng.integers(-(1 << 10), 1 << 10, N).astype(np.int32)
+    words = _quant_words(rng, N, 2.0 ** -6, 2.0 ** -1)
+    B4 = pack_int4_rows(np.ascontiguousarray(b.T)) if trans_b else pack_int4_rows(b)
+    got = _run4(ascq_gpu, pack_int4_rows(a), B4, M, N, K, ascq_gpu.F16, bias=bias, words=words, trans_b=trans_b)
+    acc = O.matmul_i8(a, b, bias=bias)
+    exp = O.mm_dequant(acc, O.F16, qvec=words)
+    assert np.array_equal(got.view(np.uint16), exp)
+
+
+def test_int4_a_transposed_rejected(ascq_gpu, oracle):
+    """matmul_int4 README: an int4 A cannot be transposed"""
+    a = np.zeros((16, 8), np.int8)
+    with pytest.raises(ascq_gpu.AscqError):
+        _run4(ascq_gpu, a, a, 16, 16, 16, ascq_gpu.INT32, trans_a=True)
