@@ -120,6 +120,8 @@ SIGNATURES = {
     "ascq_ascend_quant": (_I32, [_P, _P, _I32, _P, _P, _U16, _U16, _U32, _U32, _P]),
     "ascq_ascend_dequant": (_I32, [_P, _I32, _P, _I32, _P, _I32, _F32, _I32, ctypes.POINTER(_DequantParam), _P]),
     "ascq_ascend_antiquant": (_I32, [_P, _I32, _P, _I32, _P, _P, _U32, _U32, _U32, _I32, _I32, _P]),
+    "ascq_ascend_antiquant_policy": (_I32, [_P, _I32, _P, _I32, _P, _P, _I32, _I32, ctypes.c_int64, ctypes.c_int64,
+                                            ctypes.c_int64, _I32, _I32, _P]),
     "ascq_weight_pack_size": (_I32, [_I32, _I64, _I64, ctypes.POINTER(ctypes.c_size_t)]),
     "ascq_weight_pack": (_I32, [_P, _P, _I32, _I64, _I64, _I32, _P]),
     "ascq_antiquant_matmul": (_I32, [_P, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _I64, _P]),
@@ -240,6 +242,19 @@ def ascend_antiquant(src: torch.Tensor, src_type: int, scale: torch.Tensor, offs
     y = out if out is not None else torch.empty(shape, dtype=dst_dtype, device=src.device)
     check(lib().ascq_ascend_antiquant(_ptr(y), dst_type, _ptr(src), src_type, _ptr(offset), _ptr(scale), k, n,
                                       group_size, int(is_transpose), arith, _stream(stream)), "ascend_antiquant")
+    return y
+
+
+def ascend_antiquant_policy(src: torch.Tensor, src_type: int, scale: torch.Tensor, scale_type: int, policy: int,
+                            m: int, n: int, group_size: int = 0, offset=None, k_dim: int = 0,
+                            is_transpose: bool = False, dst_dtype=torch.float16, out=None, stream=None):
+    """AscendAntiQuant policy form (PER_TOKEN / PER_GROUP) over [m, n]: int8 / fp8 sources with f16 / bf16 / f32
+    scales, fp4 E2M1 sources with E8M0 group scales.  Returns [m, n] of dst_dtype."""
+    dst_type = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}[dst_dtype]
+    y = out if out is not None else torch.empty((m, n), dtype=dst_dtype, device=src.device)
+    check(lib().ascq_ascend_antiquant_policy(_ptr(y), dst_type, _ptr(src), src_type, _ptr(scale), _ptr(offset),
+                                             scale_type, policy, m, n, group_size, k_dim, int(is_transpose),
+                                             _stream(stream)), "ascend_antiquant_policy")
     return y
 
 

@@ -762,6 +762,43 @@ ascq_status ascq_ascend_antiquant(void* dst, int32_t dst_type, const void* src, 
                       "ascend_antiquant");
 }
 
+ascq_status ascq_ascend_antiquant_policy(void* dst, int32_t dst_type, const void* src, int32_t src_type,
+                                         const void* scale, const void* offset, int32_t scale_type, int32_t policy,
+                                         int64_t m, int64_t n, int64_t group_size, int32_t k_dim, int32_t is_transpose,
+                                         void* stream)
+{
+    if (!dst || !src || !scale) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_policy: null argument");
+    if (m < 0 || n < 0) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_policy: negative shape");
+    if (policy != ASCQ_POLICY_PER_TOKEN && policy != ASCQ_POLICY_PER_GROUP)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: policy must be PER_TOKEN or PER_GROUP");
+    if (k_dim != 0 && k_dim != 1) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_policy: k_dim must be 0 or 1");
+    if (policy == ASCQ_POLICY_PER_GROUP && (group_size <= 0 || group_size % 32 != 0))
+        return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_policy: group_size must be a positive multiple of 32");
+    const bool fp8 = src_type == ASCQ_DT_FP8_E4M3 || src_type == ASCQ_DT_FP8_E5M2;
+    const bool out_ok = dst_type == ASCQ_DT_F16 || dst_type == ASCQ_DT_BF16 || dst_type == ASCQ_DT_F32;
+    if (src_type == ASCQ_DT_FP4_E2M1) {
+        if (policy != ASCQ_POLICY_PER_GROUP || scale_type != ASCQ_DT_E8M0 || offset)
+            return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: fp4 takes PER_GROUP E8M0 scales and no offset");
+        if (dst_type != ASCQ_DT_F16 && dst_type != ASCQ_DT_BF16)
+            return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: fp4 output must be f16 or bf16");
+        if (n % 2 != 0) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_policy: fp4 rows pack two per byte (n even)");
+    } else if (src_type == ASCQ_DT_INT8 || fp8) {
+        if (scale_type != ASCQ_DT_F16 && scale_type != ASCQ_DT_BF16 && scale_type != ASCQ_DT_F32)
+            return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: scale must be f16, bf16 or f32");
+        if (!out_ok) return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: dst must be f16, bf16 or f32");
+        if (!fp8 && scale_type != ASCQ_DT_F32 && dst_type != scale_type)
+            return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: int8 with a 16-bit scale writes the scale type");
+    } else {
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: src must be int8, fp8_e4m3, fp8_e5m2 or fp4_e2m1");
+    }
+    if (m == 0 || n == 0) return ASCQ_OK;
+    const int col_groups = (k_dim == 1 && !is_transpose) || (k_dim == 0 && is_transpose);
+    return hip_status(ascq::launch_antiquant_policy(dst, dst_type, src, src_type, scale, offset, scale_type,
+                                                    policy == ASCQ_POLICY_PER_TOKEN ? 1 : 0, m, n, group_size, col_groups,
+                                                    is_transpose ? 1 : 0, S(stream)),
+                      "ascend_antiquant_policy");
+}
+
 // ------------------------------------------------------------------------------------------------
 // weight-only antiquant matmul
 // ------------------------------------------------------------------------------------------------

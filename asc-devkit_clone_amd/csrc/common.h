@@ -113,6 +113,31 @@ __device__ __forceinline__ uint8_t f32_to_fp8(float x, int fmt)
     return (uint8_t)(sign | (r - (112u << 2)));
 }
 
+// fp8 bits -> fp32 from the OCP format definitions: e4m3fn (bias 7, S.1111.111 = NaN, no inf) or e5m2 (bias 15,
+// exponent 31 = inf / NaN); every code is exact in fp32
+__device__ __forceinline__ float fp8_bits_to_f32(uint32_t v, bool e5m2)
+{
+    const uint32_t s = (v & 0x80u) << 24;
+    if (!e5m2) {
+        const uint32_t e = (v >> 3) & 15u, m = v & 7u;
+        if (e == 15u && m == 7u) return __uint_as_float(0x7fc00000u);
+        if (e == 0u) return __uint_as_float(s | __float_as_uint((float)m * 0x1p-9f));
+        return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+    }
+    const uint32_t e = (v >> 2) & 31u, m = v & 3u;
+    if (e == 31u) return __uint_as_float(m ? 0x7fc00000u : (s | 0x7f800000u));
+    if (e == 0u) return __uint_as_float(s | __float_as_uint((float)m * 0x1p-16f));
+    return __uint_as_float(s | ((e + 112u) << 23) | (m << 21));
+}
+
+// E2M1 nibble -> fp32 (OCP MX v1.0: S.EE.M, bias 1; magnitudes 0, 0.5, 1, 1.5, 2, 3, 4, 6)
+__device__ __forceinline__ float e2m1_to_f32(uint32_t nib)
+{
+    const uint32_t e = (nib >> 1) & 3u, m = nib & 1u;
+    const float mag = e == 0u ? 0.5f * (float)m : (1.0f + 0.5f * (float)m) * (float)(1u << (e - 1u));
+    return (nib & 8u) ? -mag : mag;
+}
+
 // RoundMode to integral float
 __device__ __forceinline__ float round_mode_f(float v, int mode)
 {

@@ -27,22 +27,8 @@
 
 namespace ascq {
 
-// fp8 bits -> fp32, from the format definitions (e4m3fn: bias 7, NaN = S.1111.111, no inf; e5m2: bias 15,
-// exponent 31 = inf / NaN)
-__device__ __forceinline__ float fp8_to_f32(uint8_t v, int fmt)
-{
-    const uint32_t s = (uint32_t)(v & 0x80u) << 24;
-    if (fmt == F8F6F4_E4M3) {
-        const uint32_t e = (v >> 3) & 15u, m = v & 7u;
-        if (e == 15u && m == 7u) return __uint_as_float(0x7fc00000u);
-        if (e == 0u) return __uint_as_float(s | __float_as_uint((float)m * 0x1p-9f));
-        return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
-    }
-    const uint32_t e = (v >> 2) & 31u, m = v & 3u;
-    if (e == 31u) return __uint_as_float(m ? 0x7fc00000u : (s | 0x7f800000u));
-    if (e == 0u) return __uint_as_float(s | __float_as_uint((float)m * 0x1p-16f));
-    return __uint_as_float(s | ((e + 112u) << 23) | (m << 21));
-}
+// fp8 bits -> fp32 (common.h), the format picked by its f8f6f4 code
+__device__ __forceinline__ float fp8_to_f32(uint8_t v, int fmt) { return fp8_bits_to_f32(v, fmt != F8F6F4_E4M3); }
 
 // w: the column's QUANT_PRE word (offset and sign flag of QF322B8)
 __device__ __forceinline__ void store_f8_out(void* C, int c_type, int64_t o, float v, uint64_t w)

@@ -38,6 +38,9 @@ hipError_t launch_quant_legacy(int8_t* q, const void* x, int src_type, const uin
                                uint32_t scale_count, hipStream_t st);
 hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
                           float scale_scalar, int policy, uint32_t m, uint32_t n, uint32_t cal_count, hipStream_t st);
+hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale,
+                                   const void* offset, int scale_type, int per_token, int64_t m, int64_t n,
+                                   int64_t g, int col_groups, int is_transpose, hipStream_t st);
 hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset,
                             const void* scale, uint32_t K, uint32_t N, uint32_t g, int is_transpose, int arith,
                             hipStream_t st);

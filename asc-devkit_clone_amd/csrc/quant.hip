@@ -358,6 +358,78 @@ hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, 
     return hipGetLastError();
 }
 
+// AscendAntiQuant policy form (arch 3510, ascend_antiquant_3510_impl.h:1386-1412, 1458-2110, 2175-2221): one thread
+// per element of the [m, n] tensor.  Half and bf16 arithmetic is an fp32 operation rounded once to the 16-bit
+// type, which equals the correctly rounded 16-bit operation (fp32 carries more than 2p + 2 bits of either).
+__device__ __forceinline__ float bf16_round(float x)  // rne to bf16, overflow to inf, NaN kept
+{
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return x;
+    return __uint_as_float(((u + 0x7fffu + ((u >> 16) & 1u)) >> 16) << 16);
+}
+__device__ __forceinline__ float round_scale_t(float x, int t)
+{
+    if (t == DT_F16) return (float)(_Float16)x;
+    if (t == DT_BF16) return bf16_round(x);
+    return x;
+}
+__device__ __forceinline__ float load_scale_t(const void* p, int t, int64_t i)
+{
+    if (t == DT_F16) return f16_to_f32(((const uint16_t*)p)[i]);
+    if (t == DT_BF16) return bf16_to_f32(((const uint16_t*)p)[i]);
+    return ((const float*)p)[i];
+}
+
+__global__ __launch_bounds__(256) void antiquant_policy_kernel(void* __restrict__ dst, int dst_type,
+                                                               const void* __restrict__ src, int src_type,
+                                                               const void* __restrict__ scale,
+                                                               const void* __restrict__ offset, int scale_type,
+                                                               int per_token, int64_t m, int64_t n, int64_t g,
+                                                               int col_groups, int is_transpose)
+{
+    const int64_t total = m * n, sk = g > 0 ? (n + g - 1) / g : 1;
+    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+        const int64_t r = idx / n, c = idx % n;
+        const int64_t sidx = per_token ? (is_transpose ? c : r) : (col_groups ? r * sk + c / g : (r / g) * n + c);
+        if (src_type == DT_FP4_E2M1) {  // E8M0 scale, bf16 product, no offset
+            const uint32_t b = ((const uint8_t*)src)[idx >> 1];
+            const float v = e2m1_to_f32((idx & 1) ? (b >> 4) : (b & 0xFu));
+            const uint32_t e = ((const uint8_t*)scale)[sidx];
+            const float sc = e == 255u ? __uint_as_float(0x7fffffffu) : (e == 0u ? __uint_as_float(0x00400000u)
+                                                                                 : __uint_as_float(e << 23));
+            const float p = bf16_round(v * sc);
+            if (dst_type == DT_F16) ((uint16_t*)dst)[idx] = f32_to_f16_sat(p);
+            else ((uint16_t*)dst)[idx] = (uint16_t)(__float_as_uint(p) >> 16);
+            continue;
+        }
+        const float s = load_scale_t(scale, scale_type, sidx);
+        const float o = offset ? load_scale_t(offset, scale_type, sidx) : 0.0f;
+        if (src_type == DT_FP8_E4M3 || src_type == DT_FP8_E5M2) {  // fp32 arithmetic
+            float v = fp8_bits_to_f32(((const uint8_t*)src)[idx], src_type == DT_FP8_E5M2);
+            if (offset) v = v + o;
+            v = v * s;
+            store_cast(dst, idx, v, dst_type);
+            continue;
+        }
+        float v = (float)((const int8_t*)src)[idx];  // arithmetic in the scale type
+        if (offset) v = round_scale_t(v + o, scale_type);
+        v = round_scale_t(v * s, scale_type);
+        if (scale_type == DT_F16) ((uint16_t*)dst)[idx] = f32_to_f16(v);
+        else if (scale_type == DT_BF16) ((uint16_t*)dst)[idx] = (uint16_t)(__float_as_uint(v) >> 16);
+        else store_cast(dst, idx, v, dst_type);
+    }
+}
+
+hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale,
+                                   const void* offset, int scale_type, int per_token, int64_t m, int64_t n,
+                                   int64_t g, int col_groups, int is_transpose, hipStream_t st)
+{
+    dim3 grid(grid_for(m * n)), block(256);
+    launch_k(antiquant_policy_kernel, grid, block, 0, st, dst, dst_type, src, src_type, scale, offset, scale_type,
+             per_token, m, n, g, col_groups, is_transpose);
+    return hipGetLastError();
+}
+
 hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset,
                             const void* scale, uint32_t K, uint32_t N, uint32_t g, int is_transpose, int arith,
                             hipStream_t st)

@@ -276,6 +276,29 @@ ascq_status ascq_ascend_antiquant(void* dst, int32_t dst_type, const void* src, 
                                   const void* offset, const void* scale, uint32_t k, uint32_t n,
                                   uint32_t group_size, int32_t is_transpose, int32_t arith, void* stream);
 
+/* AscendAntiQuant<dstT, srcT, scaleT, config{hasOffset, isTranspose, kDim}, policy>(dst, src, scale, offset,
+ * {m, n, calCount = m * n, groupSize}), the arch-3510 policy form (include/adv_api/quantization/ascend_antiquant.h:
+ * 235-259; AscendAntiQuantConfig / Policy / Param impl/adv_api/detail/quantization/antiquant/
+ * ascend_antiquant_common.h:46-66; impl ascend_antiquant_3510_impl.h:1386-1412, 1458-2110, dispatch :2175-2221).
+ * src / dst [m, n] row-major.  Scale (and offset, NULL = config.hasOffset false) index of element (r, c):
+ *   PER_TOKEN: scale[r] (is_transpose: scale[c]);
+ *   PER_GROUP: along the columns, scale[r][c / group] ([m][ceil(n/group)]), when (k_dim == 1 && !is_transpose) ||
+ *              (k_dim == 0 && is_transpose); else along the rows, scale[r / group][c] ([ceil(m/group)][n]);
+ *              group_size a positive multiple of 32.
+ * Arithmetic:
+ *   src INT8: (src + offset) * scale, each op rounded in scale_type (F16 / BF16 / F32); a 16-bit scale_type
+ *             writes dst of that type, F32 writes F32 or casts rne + saturating to F16 / BF16;
+ *   src FP8_E4M3 / FP8_E5M2: the same in fp32 whatever scale_type (F16 / BF16 / F32), cast to dst;
+ *   src FP4_E2M1 ([m, n/2] bytes, even element in the low nibble; n even): PER_GROUP only, scale_type E8M0
+ *             (2^(e-127); e = 0 -> 2^-127, e = 255 -> NaN), no offset; bf16(src) * bf16(scale) rounded to bf16,
+ *             dst BF16 or F16 (saturating cast).
+ * fp4 e1m2 and hifloat8 sources are not accepted (no published encoding / no gfx950 encoding).
+ * (ConvertSrc / StoreF32Res: ascend_antiquant_3510_impl.h:1363-1403; fp4 kernels :1724-1828) */
+ascq_status ascq_ascend_antiquant_policy(void* dst, int32_t dst_type, const void* src, int32_t src_type,
+                                         const void* scale, const void* offset, int32_t scale_type, int32_t policy,
+                                         int64_t m, int64_t n, int64_t group_size, int32_t k_dim, int32_t is_transpose,
+                                         void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * Weight-only antiquant matmul (W8A16 / W4A16)
  * The reference composes AscendAntiQuant (per group) with a half Matmul (fp32 L0C, half out);

@@ -592,6 +592,71 @@ void oq_antiquant(void* dst, int dst_type, const void* src, int src_type, const 
         }
 }
 
+/* AscendAntiQuant<dstT, srcT, scaleT, config{hasOffset, isTranspose, kDim}, policy>(dst, src, scale, offset,
+ * {m, n, calCount, groupSize}) of arch 3510 (include/adv_api/quantization/ascend_antiquant.h:235-259; config and
+ * policy impl/adv_api/detail/quantization/antiquant/ascend_antiquant_common.h:46-66; dispatch
+ * ascend_antiquant_3510_impl.h:2175-2221) over an [m, n] tensor, element (r, c) at r * n + c:
+ *  - scale / offset index: PER_TOKEN one per row (isTranspose: one per column, :1510-1550); PER_GROUP along the
+ *    columns ([m][ceil(n/g)], ForCol) when (kDim == 1 && !isTranspose) || (kDim == 0 && isTranspose), else along
+ *    the rows ([ceil(m/g)][n], ForRow) (:2205-2212);
+ *  - int8 source (ForRow / ForCol / PerToken B8 kernels, :1458-1497, :1670-1711, :1965-2011): ConvertSrc to scaleT
+ *    (exact, :1386-1403), + offset and * scale in scaleT, each one rounding (half, bf16 or fp32); a 16-bit scaleT
+ *    is stored as is (dstT = scaleT), an fp32 one as fp32 or cast rne + saturating (StoreF32Res, :1363-1373);
+ *  - fp8 source (Fp8 kernels, :1563-1599, :1874-1917, :2059-2108): fp32 throughout (fp8, scale and offset converted
+ *    exactly), + offset then * scale in fp32, StoreF32Res;
+ *  - fp4 E2M1 source with E8M0 scales, PER_GROUP only, no offset (:1724-1781, :1793-1828): bf16(src) (exact) times
+ *    the scale as bf16 (e << 7; e = 0 gives 0x0040 = 2^-127, e = 255 gives NaN 0x7FFF), one bf16 rounding, then for
+ *    half output a rne + saturating cast.
+ * offset == NULL: no offset (config.hasOffset false). */
+static inline double round_to(double x, int t) /* one IEEE rounding into scaleT (half / bf16 / fp32), rne */
+{
+    if (t == OQ_F16) return oq_f16_to_f32(oq_f64_to_f16(x, 0));
+    if (t == OQ_BF16) return oq_bf16_to_f32(oq_f64_to_bf16(x, 0));
+    return (double)(float)x;
+}
+
+void oq_antiquant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale, const void* offset,
+                         int scale_type, int policy, int64_t m, int64_t n, int64_t group, int k_dim, int is_transpose)
+{
+    const int col_groups = (k_dim == 1 && !is_transpose) || (k_dim == 0 && is_transpose);
+    const int64_t sk = group > 0 ? (n + group - 1) / group : 1;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < m; ++r)
+        for (int64_t c = 0; c < n; ++c) {
+            const int64_t idx = r * n + c;
+            int64_t sidx;
+            if (policy == OQ_PER_TOKEN) sidx = is_transpose ? c : r;
+            else if (col_groups ^ (OQ_MUTANT == 19)) sidx = r * sk + c / group;
+            else sidx = (r / group) * n + c;
+            if (src_type == OQ_FP4_E2M1) {
+                const uint8_t b = ((const uint8_t*)src)[idx >> 1];
+                const double v = oq_e2m1_decode((idx & 1) ? (uint8_t)(b >> 4) : (uint8_t)(b & 0xF));
+                const uint8_t e = ((const uint8_t*)scale)[sidx];
+                const double sc = e == 255 ? NAN : (e == 0 ? ldexp(1.0, -127) : ldexp(1.0, (int)e - 127));
+                const double p = round_to(v * sc, OQ_BF16);  /* exact product, one bf16 rounding */
+                if (dst_type == OQ_F16) ((uint16_t*)dst)[idx] = oq_f64_to_f16(p, 1);
+                else ((uint16_t*)dst)[idx] = oq_f64_to_bf16(p, 0);  /* already a bf16 value */
+                continue;
+            }
+            const double s = load_as_f32(scale, scale_type, sidx);
+            const double o = offset ? load_as_f32(offset, scale_type, sidx) : 0.0;
+            if (src_type == OQ_FP8_E4M3 || src_type == OQ_FP8_E5M2) {
+                const int t = OQ_MUTANT == 20 ? scale_type : OQ_F32;  /* mutant: fp8 in scaleT arithmetic */
+                double v = oq_fp8_decode(((const uint8_t*)src)[idx], src_type);
+                if (offset) v = round_to(v + o, t);
+                v = round_to(v * s, t);
+                store_from_f32(dst, dst_type, idx, (float)v);
+                continue;
+            }
+            double v = (double)((const int8_t*)src)[idx];  /* exact in every scaleT */
+            if (offset) v = round_to(v + o, scale_type);
+            v = round_to(v * s, scale_type);
+            if (scale_type == OQ_F16) ((uint16_t*)dst)[idx] = oq_f64_to_f16(v, 0);
+            else if (scale_type == OQ_BF16) ((uint16_t*)dst)[idx] = oq_f64_to_bf16(v, 0);
+            else store_from_f32(dst, dst_type, idx, (float)v);
+        }
+}
+
 /* Weight-only antiquant matmul (W8A16 / W4A16): the reference composes AscendAntiQuant (fp16 ops, above) with
  * a half x half Matmul whose L0C type is fp32 (GetMmDstType<half> = float, matmul_utils.h:171-174) and whose
  * fixpipe casts fp32 -> half with rint.  Products of two halves are exact; the restatement sums them in

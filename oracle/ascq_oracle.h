@@ -101,6 +101,10 @@ void oq_dequant(void* dst, int dst_type, const void* src, int src_type, const vo
 /* AscendAntiQuant: dst = (src + offset) * scale, per-channel or per-group */
 void oq_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset, const void* scale,
                   int64_t K, int64_t N, int64_t group_size, int is_transpose, int arith);
+/* AscendAntiQuant policy form (arch 3510): PER_TOKEN / PER_GROUP over [m, n]; int8 (scaleT arithmetic), fp8 (fp32
+ * arithmetic) or fp4 E2M1 with E8M0 scales (bf16 product) sources */
+void oq_antiquant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale, const void* offset,
+                         int scale_type, int policy, int64_t m, int64_t n, int64_t group, int k_dim, int is_transpose);
 /* weight-only antiquant matmul = AscendAntiQuant (fp16 ops) + fp16 matmul with fp32 accumulation.
  * Exact sum (double) -> f16; also returns the exact sum and sum |x*w| (for the accumulation bound) */
 void oq_antiquant_matmul(uint16_t* y, double* y_exact, double* y_absdot, const uint16_t* x, const void* w,

@@ -55,6 +55,8 @@ def lib() -> ctypes.CDLL:
             "oq_requant8": (ctypes.c_uint8, [ctypes.c_float, ctypes.c_uint64]),
             "oq_mm_requant": (None, [_P, _P, _I64, _I64, _P, ctypes.c_uint64]),
             "oq_requant4": (ctypes.c_uint8, [ctypes.c_float, ctypes.c_uint64]),
+            "oq_antiquant_policy": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int,
+                                           _I64, _I64, _I64, ctypes.c_int, ctypes.c_int]),
             "oq_mm_requant4": (None, [_P, _P, _I64, _I64, _P, ctypes.c_uint64]),
             "oq_requant4_f32": (None, [_P, _P, _I64, _I64, _P, ctypes.c_uint64]),
             "oq_matmul_i8": (None, [_P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int]),
@@ -160,6 +162,19 @@ def mm_requant(acc, qvec=None, qscalar=0):
     out = np.empty((M, N), np.uint8)
     qv = None if qvec is None else np.ascontiguousarray(qvec, np.uint64)
     lib().oq_mm_requant(_p(acc), _p(out), M, N, _p(qv), int(qscalar))
+    return out
+
+
+def antiquant_policy(src, src_type, scale, scale_type, dst_type, policy, m, n, group=0, offset=None, k_dim=0,
+                     is_transpose=False):
+    """AscendAntiQuant policy form over [m, n]: src int8 [m, n], fp8 bytes [m, n] or fp4 [m, n/2]; scale / offset
+    arrays of scale_type (f16 / bf16 as uint16 bits, f32, E8M0 bytes); returns dst (uint16 bits or float32)"""
+    out = np.empty((m, n), np.float32 if dst_type == F32 else np.uint16)
+    src = np.ascontiguousarray(src)
+    sc = np.ascontiguousarray(scale)
+    of = None if offset is None else np.ascontiguousarray(offset)
+    lib().oq_antiquant_policy(_p(out), dst_type, _p(src), src_type, _p(sc), _p(of), scale_type, policy, m, n, group,
+                              k_dim, int(is_transpose))
     return out
 
 

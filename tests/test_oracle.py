@@ -709,3 +709,95 @@ def test_nz_padding_and_element_sizes(dt, esize):
     nz = O.nd_to_nz(nd, esize, B, R, C)
     assert np.array_equal(nz, ref.reshape(-1).view(np.uint8))
     assert np.array_equal(O.nz_to_nd(nz, esize, B, R, C).view(dt).reshape(B, R, C), nd)
+
+
+# --------------------------------------------------------------------------- AscendAntiQuant policy form (3510)
+def _bf16_bits(x):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def _bf16_vals(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits, np.uint16).view(np.int16)).view(torch.bfloat16).float().numpy()
+
+
+def test_antiquant_policy_int8_half_and_bf16_arithmetic():
+    """int8 source: + offset and * scale each rounded in scaleT -- numpy float16 arithmetic for half, torch bfloat16
+    arithmetic for bf16 (ascend_antiquant_3510_impl.h:1386-1412, 1965-2011)"""
+    rng = np.random.default_rng(901)
+    m, n, g = 64, 48, 32
+    q = rng.integers(-128, 128, (m, n)).astype(np.int8)
+    sc = rng.uniform(0.001, 3.0, ((m + g - 1) // g, n))
+    of = rng.uniform(-20.0, 20.0, ((m + g - 1) // g, n))
+    rows = np.arange(m) // g
+    sh, oh = sc.astype(np.float16), of.astype(np.float16)
+    got = O.antiquant_policy(q, O.INT8, sh.view(np.uint16), O.F16, O.F16, O.PER_GROUP, m, n, g, oh.view(np.uint16))
+    exp = (q.astype(np.float16) + oh[rows]) * sh[rows]
+    assert np.array_equal(got, exp.view(np.uint16))
+    sb, ob = _bf16_bits(sc), _bf16_bits(of)
+    got = O.antiquant_policy(q, O.INT8, sb, O.BF16, O.BF16, O.PER_GROUP, m, n, g, ob)
+    tq = torch.from_numpy(q.astype(np.float32)).to(torch.bfloat16)
+    ts = torch.from_numpy(_bf16_vals(sb)[rows]).to(torch.bfloat16)
+    to = torch.from_numpy(_bf16_vals(ob)[rows]).to(torch.bfloat16)
+    exp = ((tq + to) * ts).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, exp)
+
+
+def test_antiquant_policy_fp32_scale_and_fp8_source():
+    """fp32 scaleT (and every fp8 source) compute in fp32 and cast once (rne, saturating) to the output; an fp8
+    source with half scales still computes in fp32 (the half product would round twice)"""
+    rng = np.random.default_rng(902)
+    m, n = 16, 64
+    q = rng.integers(-128, 128, (m, n)).astype(np.int8)
+    sc = rng.uniform(0.001, 3.0, m).astype(np.float32)
+    of = rng.uniform(-5.0, 5.0, m).astype(np.float32)
+    got = O.antiquant_policy(q, O.INT8, sc, O.F32, O.F32, O.PER_TOKEN, m, n, offset=of)
+    exp = (q.astype(np.float32) + of[:, None]) * sc[:, None]
+    assert np.array_equal(got, exp)
+    got16 = O.antiquant_policy(q, O.INT8, sc, O.F32, O.F16, O.PER_TOKEN, m, n, offset=of)
+    assert np.array_equal(got16, exp.astype(np.float16).view(np.uint16))
+    codes = rng.integers(0, 256, (m, n)).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x3C  # no e4m3 NaN codes
+    sh = rng.uniform(0.5, 1.5, n).astype(np.float16)
+    oh = rng.uniform(-3.0, 3.0, n).astype(np.float16)
+    got = O.antiquant_policy(codes, O.FP8_E4M3, sh.view(np.uint16), O.F16, O.F16, O.PER_TOKEN, m, n,
+                             offset=oh.view(np.uint16), is_transpose=True)  # transposed: one scale per column
+    v = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    exp = ((v + oh.astype(np.float32)[None, :]) * sh.astype(np.float32)[None, :]).astype(np.float16)
+    assert np.array_equal(got, exp.view(np.uint16))
+
+
+@pytest.mark.parametrize("k_dim,transpose", [(0, False), (1, False), (0, True), (1, True)])
+def test_antiquant_policy_group_axis(k_dim, transpose):
+    """PER_GROUP scale layout: along the columns ([m][ceil(n/g)]) when (kDim 1, not transposed) or (kDim 0,
+    transposed), else along the rows ([ceil(m/g)][n]) (ascend_antiquant_3510_impl.h:2205-2212); scales 2^j make
+    every index visible in the output"""
+    m, n, g = 64, 96, 32
+    q = np.ones((m, n), np.int8)
+    col = (k_dim == 1 and not transpose) or (k_dim == 0 and transpose)
+    shape = (m, (n + g - 1) // g) if col else ((m + g - 1) // g, n)
+    sc = np.exp2(np.arange(shape[0] * shape[1]) % 24 - 12).astype(np.float32).reshape(shape)
+    got = O.antiquant_policy(q, O.INT8, sc, O.F32, O.F32, O.PER_GROUP, m, n, g, k_dim=k_dim, is_transpose=transpose)
+    r, c = np.meshgrid(np.arange(m), np.arange(n), indexing="ij")
+    exp = sc[r, c // g] if col else sc[r // g, c]
+    assert np.array_equal(got, exp)
+
+
+def test_antiquant_policy_fp4_e8m0():
+    """fp4 E2M1 with E8M0 group scales: bf16(v) * bf16(2^(e-127)) rounded once to bf16; e = 0 is 2^-127 (bf16
+    0x0040), e = 255 NaN; half output is a saturating cast of that bf16 (ascend_antiquant_3510_impl.h:1724-1828)"""
+    m, n, g = 4, 64, 32
+    nib = np.tile(np.arange(16, dtype=np.uint8), (m, n // 16))
+    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    e = np.array([[127, 130], [0, 1], [254, 120], [255, 127]], np.uint8)
+    got = O.antiquant_policy(packed, O.FP4_E2M1, e, O.E8M0, O.BF16, O.PER_GROUP, m, n, g, k_dim=1)
+    mag = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6], np.float64)
+    vals = np.concatenate([mag, -mag])[nib]
+    scale = np.where(e == 0, 2.0 ** -127, np.exp2(e.astype(np.float64) - 127))[:, np.arange(n) // g]
+    prod = vals * scale
+    exp = _bf16_bits(prod.astype(np.float32))  # products of <= 2 significant bits: exact unless they overflow
+    exp[3, :32] = 0x7FFF                       # e = 255 -> NaN (the NaN pattern of the scale)
+    assert np.array_equal(got[:3], exp[:3]) and np.isnan(_bf16_vals(got[3, :32])).all()
+    assert np.array_equal(got[3, 32:], exp[3, 32:])
+    assert got[1, 2] == 0x0040 and got[2, 15] == 0xFF80  # 1 * 2^-127 (bf16 subnormal); -6 * 2^127 overflows to -inf
+    h = O.antiquant_policy(packed, O.FP4_E2M1, e, O.E8M0, O.F16, O.PER_GROUP, m, n, g, k_dim=1)
+    assert h[0, 15] == np.float16(-6.0).view(np.uint16) and h[2, 7] == 0x7BFF  # 6 * 2^127 saturates to 65504

@@ -39,6 +39,8 @@ MUTANTS = {
     16: "FasterGelu coefficient with the wrong sign",
     17: "int4 requant without the 9-bit offset",
     18: "int4 requant output nibbles swapped",
+    19: "per-group antiquant scales indexed along the wrong axis",
+    20: "fp8 antiquant computed in the scale type instead of fp32",
 }
 
 
