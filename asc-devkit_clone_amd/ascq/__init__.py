@@ -117,6 +117,7 @@ SIGNATURES = {
     "ascq_matmul_destroy": (_I32, [_P]),
     "ascq_ascend_quant_per_token": (_I32, [_P, _P, _I32, _P, _P, ctypes.POINTER(_QuantParam), _P]),
     "ascq_ascend_quant_dynamic_per_token": (_I32, [_P, _P, _P, _I32, _U32, _U32, _I32, _P]),
+    "ascq_ascend_quant_policy": (_I32, [_P, _I32, _P, _I32, _P, _P, _F32, _I32, _I32, ctypes.POINTER(_QuantParam), _P]),
     "ascq_ascend_quant": (_I32, [_P, _P, _I32, _P, _P, _U16, _U16, _U32, _U32, _P]),
     "ascq_ascend_dequant": (_I32, [_P, _I32, _P, _I32, _P, _I32, _F32, _I32, ctypes.POINTER(_DequantParam), _P]),
     "ascq_ascend_antiquant": (_I32, [_P, _I32, _P, _I32, _P, _P, _U32, _U32, _U32, _I32, _I32, _P]),
@@ -203,6 +204,30 @@ def quant_per_token(x: torch.Tensor, scale: torch.Tensor, offset=None, round_mod
     p = _QuantParam(m, n, m * n, 0, 1 if offset is not None else 0, 1, round_mode)
     check(lib().ascq_ascend_quant_per_token(_ptr(q), _ptr(x), src_type, _ptr(scale), _ptr(offset), ctypes.byref(p),
                                             _stream(stream)), "quant_per_token")
+    return q
+
+
+def ascend_quant_policy(x: torch.Tensor, scale: torch.Tensor, policy: int, dst_type: int = INT8,
+                        group_size: int = 0, offset=None, offset_scalar=None, k_dim: int = 1,
+                        round_mode: int = ROUND_RINT, scale_type: int | None = None, out=None, stream=None):
+    """AscendQuant policy form (PER_TOKEN / PER_GROUP) of x [m, n] (f16 / bf16 / f32) to int8, fp8 (e4m3 / e5m2;
+    returned as uint8 codes) or E2M1 (two codes a byte, [m, n/2] uint8).  scale / offset f16 / bf16 / f32; a
+    scalar offset_scalar applies when no offset tensor is given."""
+    m, n = x.shape
+    src_type = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}[x.dtype]
+    if scale_type is None:
+        scale_type = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}[scale.dtype]
+    if out is not None:
+        q = out
+    elif dst_type == FP4_E2M1:
+        q = torch.empty((m, n // 2), dtype=torch.uint8, device=x.device)
+    else:
+        q = torch.empty((m, n), dtype=torch.int8 if dst_type == INT8 else torch.uint8, device=x.device)
+    has_off = offset is not None or offset_scalar is not None
+    p = _QuantParam(m, n, m * n, group_size, int(has_off), k_dim, round_mode)
+    check(lib().ascq_ascend_quant_policy(_ptr(q), dst_type, _ptr(x), src_type, _ptr(scale), _ptr(offset),
+                                         float(offset_scalar or 0.0), scale_type, policy, ctypes.byref(p),
+                                         _stream(stream)), "ascend_quant_policy")
     return q
 
 

@@ -689,6 +689,43 @@ ascq_status ascq_ascend_quant_per_token(int8_t* dst, const void* src, int32_t sr
                       "quant_per_token");
 }
 
+ascq_status ascq_ascend_quant_policy(void* dst, int32_t dst_type, const void* src, int32_t src_type,
+                                     const void* scale, const void* offset, float offset_scalar, int32_t scale_type,
+                                     int32_t policy, const ascq_quant_param* para, void* stream)
+{
+    if (!dst || !src || !scale || !para) return fail(ASCQ_E_INVALID_ARG, "ascend_quant_policy: null argument");
+    const auto fp_type = [](int32_t t) { return t == ASCQ_DT_F16 || t == ASCQ_DT_BF16 || t == ASCQ_DT_F32; };
+    if (!fp_type(src_type)) return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: src must be f16, bf16 or f32");
+    if (!fp_type(scale_type)) return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: scale must be f16, bf16 or f32");
+    const bool fp8 = dst_type == ASCQ_DT_FP8_E4M3 || dst_type == ASCQ_DT_FP8_E5M2;
+    const bool fp4 = dst_type == ASCQ_DT_FP4_E2M1;
+    if (!fp8 && !fp4 && dst_type != ASCQ_DT_INT8)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: dst must be int8, fp8_e4m3, fp8_e5m2 or fp4_e2m1");
+    if (policy != ASCQ_POLICY_PER_TOKEN && policy != ASCQ_POLICY_PER_GROUP)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: policy must be PER_TOKEN or PER_GROUP");
+    if (policy == ASCQ_POLICY_PER_TOKEN && fp4)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: PER_TOKEN writes int8 or fp8");
+    if (policy == ASCQ_POLICY_PER_GROUP) {
+        if (para->kdim != 0 && para->kdim != 1) return fail(ASCQ_E_INVALID_ARG, "ascend_quant_policy: kdim must be 0 or 1");
+        if (para->group_size == 0 || para->group_size % 32 != 0)
+            return fail(ASCQ_E_INVALID_ARG, "ascend_quant_policy: group_size must be a positive multiple of 32");
+    }
+    if (!fp8 && scale_type != ASCQ_DT_F32 && scale_type != src_type)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: a 16-bit scale needs a source of the same type");
+    if (!valid_round(para->round_mode)) return fail(ASCQ_E_INVALID_ARG, "ascend_quant_policy: bad round mode");
+    if (para->n == 0) return fail(ASCQ_E_INVALID_ARG, "ascend_quant_policy: n must be positive");
+    if (para->cal_count % para->n != 0)
+        return fail(ASCQ_E_INVALID_ARG, "ascend_quant_policy: calCount must be an integer multiple of n");
+    if (fp4 && para->n % 2 != 0) return fail(ASCQ_E_INVALID_ARG, "ascend_quant_policy: fp4 rows pack two per byte (n even)");
+    const int64_t rows = para->cal_count / para->n;
+    if (rows == 0) return ASCQ_OK;
+    return hip_status(ascq::launch_quant_policy(dst, dst_type, src, src_type, scale, scale_type, offset,
+                                                para->has_offset ? 1 : 0, offset_scalar,
+                                                policy == ASCQ_POLICY_PER_TOKEN ? 1 : 0, rows, para->n,
+                                                para->group_size, para->kdim, para->round_mode, S(stream)),
+                      "ascend_quant_policy");
+}
+
 ascq_status ascq_ascend_quant_dynamic_per_token(int8_t* dst, float* scale_out, const void* src, int32_t src_type,
                                                 uint32_t m, uint32_t n, int32_t round_mode, void* stream)
 {

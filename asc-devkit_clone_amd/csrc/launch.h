@@ -44,6 +44,9 @@ hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int
 hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset,
                             const void* scale, uint32_t K, uint32_t N, uint32_t g, int is_transpose, int arith,
                             hipStream_t st);
+hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale,
+                               int scale_type, const void* offset, int has_offset, float offset_scalar, int per_token,
+                               int64_t m, int64_t n, int64_t g, int k_dim, int round_mode, hipStream_t st);
 
 // gemm_i8.hip
 enum : int { EPI_I32 = 0, EPI_DEQ_F16 = 1, EPI_DEQ_BF16 = 2, EPI_REQ8 = 3, EPI_REQ4 = 4 };

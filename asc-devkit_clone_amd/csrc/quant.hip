@@ -430,6 +430,216 @@ hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------------------
+// AscendQuant policy form (arch 3510, ascend_quant_per_group_3510_impl.h:33-1340, dispatch :1451-1504):
+// PER_TOKEN / PER_GROUP over [m, n] to int8, fp8 or E2M1.  Each lane takes 8 consecutive elements: one or two
+// 16-byte source loads, one scale (PER_TOKEN, or a group along the row -- group sizes are multiples of 32) or
+// 8 contiguous scales (groups down the columns), and an 8- (int8 / fp8) or 4-byte (E2M1) store.  Rows whose
+// length is not a multiple of 8, or unaligned pointers, take the per-element path of the same kernel.
+// ---------------------------------------------------------------------------------------------
+enum : int { QD_INT8 = 0, QD_E4M3 = 1, QD_E5M2 = 2, QD_E2M1 = 3 };
+enum : int { QL_TOKEN = 0, QL_KCOL = 1, QL_KROW = 2 };
+
+struct QuantPolicyArgs {
+    void* dst;
+    const void* src;
+    const void* scale;
+    const void* offset;  // tensor indexed like scale, or null
+    float off_scalar;    // used when has_off and offset is null (already a scaleT value)
+    int has_off;
+    int src_type, scale_type, round_mode, layout, fast;
+    int64_t m, n, g, sk, units;  // units: ceil(m * n / 8)
+};
+
+// f32 -> fp8 with rint and saturation: NaN -> 0, overflow and inf -> +-max finite (TransRegForFp8,
+// ascend_quant_3510_impl.h:888-896; docs/zh/api/SIMD-API/tensor_api/reg_vector_compute/type_conversion/cast.md:109)
+__device__ __forceinline__ uint32_t f32_to_fp8_sat(float x, bool e5m2)
+{
+    if (x != x) return 0u;
+    const float mx = e5m2 ? 57344.0f : 448.0f;
+    return f32_to_fp8(__builtin_fminf(__builtin_fmaxf(x, -mx), mx), e5m2 ? 1 : 0);
+}
+
+// bf16 value -> E2M1 code in round mode `mode`, saturating at +-6 (Cast<fp4x2_e2m1_t, bfloat16_t>, cast.md:96).
+// The code table is three uniform segments -- [0, 2) in steps of 0.5 (codes 0-4), [2, 4) in steps of 1 (4-6),
+// [4, 6] in steps of 2 (6-7) -- so the code is the segment base plus the rounded, exactly scaled offset into it;
+// every base is even, so ties to even on the offset are ties to an even code.  A directed mode on a negative value
+// rounds the magnitude the other way.  NaN -> 0.
+__device__ __forceinline__ uint32_t bf16_to_e2m1(float v, int mode)
+{
+    if (v != v) return 0u;
+    const uint32_t s = (__float_as_uint(v) >> 28) & 8u;
+    const float a = __builtin_fabsf(v);
+    if (a >= 6.0f) return s | 7u;
+    int mm = mode;
+    if (s) mm = mode == RM_FLOOR ? RM_CEIL : (mode == RM_CEIL ? RM_FLOOR : mode);
+    float q;
+    uint32_t base;
+    if (a < 2.0f) q = a * 2.0f, base = 0u;
+    else if (a < 4.0f) q = a - 2.0f, base = 4u;
+    else q = (a - 4.0f) * 0.5f, base = 6u;
+    return s | (base + (uint32_t)round_mode_f(q, mm));
+}
+
+// one scaleT rounding of an fp32 result (exact for products of two 16-bit values; a single correct rounding for
+// sums, since fp32 holds more than 2p + 2 bits of half and bf16)
+template <int T>
+__device__ __forceinline__ float rnd_t(float x)
+{
+    if constexpr (T == DT_F16) return (float)(_Float16)x;
+    else if constexpr (T == DT_BF16) return bf16_round(x);
+    else return x;
+}
+
+__device__ __forceinline__ void load8_f32(const void* p, int t, int64_t i, float (&o)[8])
+{
+    if (t == DT_F32) {
+        const u32x4 a = __builtin_nontemporal_load((const u32x4*)((const float*)p + i));
+        const u32x4 b = __builtin_nontemporal_load((const u32x4*)((const float*)p + i) + 1);
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = __uint_as_float(w[j]);
+        return;
+    }
+    const u32x4 a = __builtin_nontemporal_load((const u32x4*)((const uint16_t*)p + i));
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint16_t lo = (uint16_t)(w[j] & 0xffffu), hi = (uint16_t)(w[j] >> 16);
+        o[2 * j] = t == DT_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
+        o[2 * j + 1] = t == DT_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+    }
+}
+
+template <int DST, int T>
+__global__ __launch_bounds__(256) void quant_policy_kernel(QuantPolicyArgs a)
+{
+    const int64_t total = a.m * a.n;
+    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < a.units; u += (int64_t)gridDim.x * 256) {
+        const int64_t e0 = u * 8;
+        float x[8], s[8], o[8];
+        if (a.fast) {  // n % 8 == 0: the 8 elements share a row; aligned 16-byte loads
+            const int64_t r = e0 / a.n, c = e0 - r * a.n;
+            load8_f32(a.src, a.src_type, e0, x);
+            if (a.layout == QL_KROW) {
+                const int64_t si = (r / a.g) * a.n + c;
+                load8_f32(a.scale, a.scale_type, si, s);
+                if (a.offset) load8_f32(a.offset, a.scale_type, si, o);
+            } else {
+                const int64_t si = a.layout == QL_TOKEN ? r : r * a.sk + c / a.g;
+                const float sv = load_scale_t(a.scale, a.scale_type, si);
+                const float ov = a.offset ? load_scale_t(a.offset, a.scale_type, si) : 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) s[j] = sv, o[j] = ov;
+            }
+            if (!a.offset) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = a.off_scalar;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int64_t e = e0 + j < total ? e0 + j : total - 1;  // clamped; lanes past the end are not stored
+                const int64_t r = e / a.n, c = e - r * a.n;
+                const int64_t si = a.layout == QL_TOKEN ? r : (a.layout == QL_KCOL ? r * a.sk + c / a.g
+                                                                                    : (r / a.g) * a.n + c);
+                x[j] = load_scale_t(a.src, a.src_type, e);
+                s[j] = load_scale_t(a.scale, a.scale_type, si);
+                o[j] = a.offset ? load_scale_t(a.offset, a.scale_type, si) : a.off_scalar;
+            }
+        }
+        uint32_t code[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float v = rnd_t<T>(x[j] * s[j]);
+            if (DST != QD_E2M1 && a.has_off) v = rnd_t<T>(v + o[j]);
+            if constexpr (DST == QD_INT8) {
+                code[j] = (uint32_t)sat_s8_from_integral(round_mode_f(v, a.round_mode)) & 0xffu;
+            } else if constexpr (DST == QD_E4M3 || DST == QD_E5M2) {
+                code[j] = f32_to_fp8_sat(v, DST == QD_E5M2);
+            } else {
+                if constexpr (T != DT_BF16) v = v != v ? 0.0f : bf16_to_f32(f32_to_bf16_sat(v));
+                code[j] = bf16_to_e2m1(v, a.round_mode);
+            }
+        }
+        if constexpr (DST == QD_E2M1) {
+            const uint32_t w = code[0] | (code[1] << 4) | (code[2] << 8) | (code[3] << 12) | (code[4] << 16) |
+                               (code[5] << 20) | (code[6] << 24) | (code[7] << 28);
+            uint8_t* d = (uint8_t*)a.dst + e0 / 2;
+            if (a.fast) {
+                __builtin_nontemporal_store(w, (uint32_t*)d);
+            } else {
+                for (int j = 0; j < 4; ++j)
+                    if (e0 + 2 * j < total) d[j] = (uint8_t)(w >> (8 * j));
+            }
+        } else {
+            uint8_t* d = (uint8_t*)a.dst + e0;
+            if (a.fast) {
+                const u32x2 w = {code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24),
+                                 code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24)};
+                __builtin_nontemporal_store(w, (u32x2*)d);
+            } else {
+                for (int j = 0; j < 8; ++j)
+                    if (e0 + j < total) d[j] = (uint8_t)code[j];
+            }
+        }
+    }
+}
+
+hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale,
+                               int scale_type, const void* offset, int has_offset, float offset_scalar, int per_token,
+                               int64_t m, int64_t n, int64_t g, int k_dim, int round_mode, hipStream_t st)
+{
+    QuantPolicyArgs a;
+    a.dst = dst;
+    a.src = src;
+    a.scale = scale;
+    a.offset = has_offset ? offset : nullptr;
+    // the scalar offset is a scaleT value: round it (rne) to the scale type once, here
+    float os = offset_scalar;
+    if (scale_type == DT_F16) {
+        os = (float)(_Float16)os;
+    } else if (scale_type == DT_BF16) {
+        uint32_t u = __builtin_bit_cast(uint32_t, os);
+        if ((u & 0x7fffffffu) <= 0x7f800000u) u = ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16) << 16;
+        os = __builtin_bit_cast(float, u);
+    }
+    a.off_scalar = os;
+    a.has_off = has_offset;
+    a.src_type = src_type;
+    a.scale_type = scale_type;
+    a.round_mode = round_mode;
+    a.layout = per_token ? QL_TOKEN : (k_dim == 1 ? QL_KCOL : QL_KROW);
+    a.m = m;
+    a.n = n;
+    a.g = g > 0 ? g : 1;
+    a.sk = (n + a.g - 1) / a.g;
+    a.units = (m * n + 7) / 8;
+    const int dk = dst_type == DT_INT8 ? QD_INT8
+                   : dst_type == DT_FP8_E4M3 ? QD_E4M3
+                   : dst_type == DT_FP8_E5M2 ? QD_E5M2 : QD_E2M1;
+    const uintptr_t dal = dk == QD_E2M1 ? 4 : 8;
+    const bool al = (uintptr_t)src % 16 == 0 && (uintptr_t)dst % dal == 0 &&
+                    (a.layout != QL_KROW || ((uintptr_t)scale % 16 == 0 && (uintptr_t)a.offset % 16 == 0));
+    a.fast = n % 8 == 0 && al;
+    const int t = (dk == QD_E4M3 || dk == QD_E5M2) ? DT_F32 : scale_type;  // arithmetic type
+    dim3 grid(grid_for(a.units)), block(256);
+#define QP_LAUNCH(D, T) launch_k(quant_policy_kernel<D, T>, grid, block, 0, st, a)
+    if (dk == QD_E4M3) QP_LAUNCH(QD_E4M3, DT_F32);
+    else if (dk == QD_E5M2) QP_LAUNCH(QD_E5M2, DT_F32);
+    else if (dk == QD_INT8) {
+        if (t == DT_F16) QP_LAUNCH(QD_INT8, DT_F16);
+        else if (t == DT_BF16) QP_LAUNCH(QD_INT8, DT_BF16);
+        else QP_LAUNCH(QD_INT8, DT_F32);
+    } else {
+        if (t == DT_F16) QP_LAUNCH(QD_E2M1, DT_F16);
+        else if (t == DT_BF16) QP_LAUNCH(QD_E2M1, DT_BF16);
+        else QP_LAUNCH(QD_E2M1, DT_F32);
+    }
+#undef QP_LAUNCH
+    return hipGetLastError();
+}
+
 hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset,
                             const void* scale, uint32_t K, uint32_t N, uint32_t g, int is_transpose, int arith,
                             hipStream_t st)

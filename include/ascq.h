@@ -232,6 +232,30 @@ ascq_status ascq_ascend_quant_per_token(int8_t* dst, const void* src, int32_t sr
 ascq_status ascq_ascend_quant_dynamic_per_token(int8_t* dst, float* scale_out, const void* src,
                                                 int32_t src_type, uint32_t m, uint32_t n, int32_t round_mode,
                                                 void* stream);
+/* AscendQuant<dstT, srcT, scaleT, false, config{hasOffset, kDim, roundMode}, policy>(dst, src, scale, offset, para),
+ * the arch-3510 policy form (include/adv_api/quantization/ascend_quant.h:714-777; impl
+ * impl/adv_api/detail/quantization/quant/ascend_quant_per_group_3510_impl.h:33-1340, dispatch :1451-1504;
+ * TransRegForFp8 / S8 / Fp4 ascend_quant_3510_impl.h:888-1036).  src / dst [rows, n] row-major with
+ * rows = cal_count / n; para->group_size, has_offset, kdim and round_mode as in the config.
+ * Scale (and offset) index of element (r, c):
+ *   PER_TOKEN: scale[r];
+ *   PER_GROUP, kdim 1: scale[r][c / group] ([rows][ceil(n/group)]); kdim 0: scale[r / group][c]
+ *              ([ceil(rows/group)][n]); group_size a positive multiple of 32.
+ * dst_type and arithmetic:
+ *   INT8: y = x * scale (+ offset), each op rounded in scale_type, then clamp(round_mode(y), -128, 127), NaN -> 0;
+ *   FP8_E4M3 / FP8_E5M2: the same ops in fp32 whatever scale_type, then rint with saturation (overflow and
+ *         inf -> +-max finite, NaN -> 0); round_mode is not used (every mode is rint, :888-896);
+ *   FP4_E2M1 (PER_GROUP only; offset ignored, :1385): y = x * scale in scale_type; an f16 / f32 y is rounded to
+ *         bf16 (rne, saturating, NaN -> 0); then E2M1 in round_mode with saturation at +-6; two codes a byte, even
+ *         element in the low nibble (n even).
+ * src_type F16, BF16 or F32; scale_type F16, BF16 or F32.  For INT8 / FP4_E2M1 a 16-bit scale_type needs a source
+ * of the same type (a 16-bit source meets an F32 scale as fp32); FP8 accepts every pair.
+ * Offset (para->has_offset): the tensor `offset` (scale_type, indexed like scale) or, when it is NULL, the scalar
+ * offset_scalar rounded (rne) to scale_type -- the overloads taking `const scaleT offset` (ascend_quant.h:737-777).
+ * hifloat8 and fp4 e1m2 outputs are not accepted (no gfx950 encoding). */
+ascq_status ascq_ascend_quant_policy(void* dst, int32_t dst_type, const void* src, int32_t src_type,
+                                     const void* scale, const void* offset, float offset_scalar, int32_t scale_type,
+                                     int32_t policy, const ascq_quant_param* para, void* stream);
 /* Legacy AscendQuant per-tensor / per-channel, half arithmetic (ascend_quant.h:64-293;
  * impl ascend_quant_pre_impl.h:101-164, 320-483).  src_type F16 or F32.
  * scale / offset: device half vectors of scale_count elements, or NULL to use the scalars

@@ -657,6 +657,104 @@ void oq_antiquant_policy(void* dst, int dst_type, const void* src, int src_type,
         }
 }
 
+/* ------------------------------------------------------------------------ */
+/* AscendQuant policy form (arch 3510): PER_TOKEN / PER_GROUP                */
+/* ------------------------------------------------------------------------ */
+
+/* E2M1 code of x under round mode `mode` with saturation at +-6: Cast<fp4x2_e2m1_t, bfloat16_t> accepts
+ * floor / rint / round / ceil / trunc (docs/zh/api/SIMD-API/tensor_api/reg_vector_compute/type_conversion/
+ * cast.md:96); TransRegForFp4 sends every other mode to rint (ascend_quant_3510_impl.h:995-1036).  The magnitude
+ * is bracketed on the code table; a directed mode picks by the sign of x; a negative value that rounds to zero
+ * keeps its sign.  NaN -> 0 (the saturating casts' rule, cast.md:108-109). */
+uint8_t oq_e2m1_encode(double x, int mode)
+{
+    static const double mag[8] = {0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0};
+    if (x != x) return 0;
+    const int neg = signbit(x) != 0;
+    const uint8_t s = neg ? 8u : 0u;
+    const double a = fabs(x);
+    if (a >= 6.0) return (uint8_t)(s | 7u);
+    int lo = 0;
+    while (mag[lo + 1] <= a) ++lo; /* mag[lo] <= a < mag[lo + 1] */
+    if (mag[lo] == a) return (uint8_t)(s | lo);
+    const int hi = lo + 1;
+    const double dl = a - mag[lo], dh = mag[hi] - a;
+    int c;
+    switch (mode) {
+    case OQ_ROUND_TRUNC: c = lo; break;
+    case OQ_ROUND_FLOOR: c = (neg && OQ_MUTANT != 25) ? hi : lo; break;
+    case OQ_ROUND_CEIL: c = (neg && OQ_MUTANT != 25) ? lo : hi; break;
+    case OQ_ROUND_ROUND: c = dl < dh ? lo : hi; break;           /* ties away from zero */
+    default: c = dl < dh ? lo : (dh < dl ? hi : ((lo & 1) ? hi : lo)); break; /* ties to the even code */
+    }
+    return (uint8_t)(s | c);
+}
+
+/* f32 -> fp8 with rint and saturation (TransRegForFp8, ascend_quant_3510_impl.h:888-896: every round mode but
+ * rint maps to LayoutZMrgZRndRSatS, i.e. rint + SAT): finite overflow and +-inf clamp to the largest finite
+ * magnitude, NaN -> 0 (cast.md:108-109). */
+uint8_t oq_f32_to_fp8_sat(float x, int fmt)
+{
+    if (x != x) return 0;
+    const float mx = fmt == OQ_FP8_E4M3 ? 448.0f : 57344.0f;
+    if (fabsf(x) > mx) x = copysignf(mx, x);
+    return oq_f32_to_fp8(x, fmt);
+}
+
+/* AscendQuant<dstT, srcT, scaleT, false, config{hasOffset, kDim, roundMode}, policy>(dst, src, scale, offset,
+ * {m, n, calCount = m * n, groupSize}) (include/adv_api/quantization/ascend_quant.h:714-777; impl
+ * ascend_quant_per_group_3510_impl.h:33-79 / 142-346 PER_TOKEN, 347-726 PER_GROUP kDim 1, 727-1340 kDim 0,
+ * dispatch 1451-1504).  Scale / offset index of element (r, c): PER_TOKEN scale[r]; PER_GROUP kDim 1
+ * scale[r * ceil(n / group) + c / group]; kDim 0 scale[(r / group) * n + c].
+ *   int8 dst: y = x * s (+ o), each op rounded in scaleT (a 16-bit src meets an f32 scale as f32), then
+ *            clamp(round_mode(y), -128, 127) (TransRegForS8 :934-992; NaN -> 0);
+ *   fp8 dst: the same ops in f32 whatever scaleT (:33-79, 393-431), then rint + SAT;
+ *   E2M1 dst (PER_GROUP only; offset ignored, :1385): y = x * s in scaleT, a float / half y rounded to bf16 rne
+ *            with saturation (NaN -> 0), then the E2M1 cast in round_mode (TransRegForFp4 :995-1036); two codes a
+ *            byte, even element in the low nibble.
+ * offset: a tensor indexed like scale, or (offset == NULL, has_offset) the scalar offset_scalar rounded to scaleT
+ * (the overloads taking `const scaleT offset`, :192-235, 297-333). */
+void oq_quant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                     const void* offset, int has_offset, float offset_scalar, int policy, int64_t m, int64_t n,
+                     int64_t group, int k_dim, int round_mode)
+{
+    const int fp8 = dst_type == OQ_FP8_E4M3 || dst_type == OQ_FP8_E5M2;
+    const int fp4 = dst_type == OQ_FP4_E2M1;
+    const int t = (fp8 && OQ_MUTANT != 21) ? OQ_F32 : scale_type; /* arithmetic type */
+    const int off = has_offset && !fp4;
+    const int64_t sk = group > 0 ? (n + group - 1) / group : 1;
+    const double os = round_to((double)offset_scalar, scale_type);
+    uint8_t* codes = fp4 ? (uint8_t*)malloc((size_t)(m * n) + 1) : NULL;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < m; ++r)
+        for (int64_t c = 0; c < n; ++c) {
+            const int64_t idx = r * n + c;
+            int64_t sidx;
+            if (policy == OQ_PER_TOKEN) sidx = r;
+            else if ((k_dim == 1) ^ (OQ_MUTANT == 23)) sidx = r * sk + c / group;
+            else sidx = (r / group) * n + c;
+            const double x = load_as_f32(src, src_type, idx);
+            const double s = load_as_f32(scale, scale_type, sidx);
+            double v = x * s; /* exact: two 24-bit significands */
+            if (!(off && OQ_MUTANT == 24)) v = round_to(v, t);
+            if (off) v = round_to(v + (offset ? (double)load_as_f32(offset, scale_type, sidx) : os), t);
+            if (fp8) {
+                ((uint8_t*)dst)[idx] = oq_f32_to_fp8_sat((float)v, dst_type);
+            } else if (fp4) {
+                double b = v;
+                if (t != OQ_BF16 && OQ_MUTANT != 22) b = v != v ? 0.0 : oq_bf16_to_f32(oq_f64_to_bf16(v, 1));
+                codes[idx] = oq_e2m1_encode(b, round_mode);
+            } else {
+                ((int8_t*)dst)[idx] = oq_sat_s8(oq_round_to_int((float)v, round_mode));
+            }
+        }
+    if (fp4) {
+        for (int64_t i = 0; i < m * n; i += 2)
+            ((uint8_t*)dst)[i >> 1] = (uint8_t)(codes[i] | ((i + 1 < m * n ? codes[i + 1] : 0u) << 4));
+        free(codes);
+    }
+}
+
 /* Weight-only antiquant matmul (W8A16 / W4A16): the reference composes AscendAntiQuant (fp16 ops, above) with
  * a half x half Matmul whose L0C type is fp32 (GetMmDstType<half> = float, matmul_utils.h:171-174) and whose
  * fixpipe casts fp32 -> half with rint.  Products of two halves are exact; the restatement sums them in

@@ -105,6 +105,15 @@ void oq_antiquant(void* dst, int dst_type, const void* src, int src_type, const 
  * arithmetic) or fp4 E2M1 with E8M0 scales (bf16 product) sources */
 void oq_antiquant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale, const void* offset,
                          int scale_type, int policy, int64_t m, int64_t n, int64_t group, int k_dim, int is_transpose);
+/* E2M1 code of x in round mode `mode`, saturating at +-6, NaN -> 0 */
+uint8_t oq_e2m1_encode(double x, int mode);
+/* f32 -> fp8, rint + saturation (overflow and inf -> +-max finite, NaN -> 0) */
+uint8_t oq_f32_to_fp8_sat(float x, int fmt);
+/* AscendQuant policy form (arch 3510): PER_TOKEN / PER_GROUP over [m, n] to int8 (scaleT arithmetic), fp8 (fp32
+ * arithmetic) or E2M1 (scaleT product -> bf16 -> E2M1, PER_GROUP only); offset tensor, scalar or none */
+void oq_quant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                     const void* offset, int has_offset, float offset_scalar, int policy, int64_t m, int64_t n,
+                     int64_t group, int k_dim, int round_mode);
 /* weight-only antiquant matmul = AscendAntiQuant (fp16 ops) + fp16 matmul with fp32 accumulation.
  * Exact sum (double) -> f16; also returns the exact sum and sum |x*w| (for the accumulation bound) */
 void oq_antiquant_matmul(uint16_t* y, double* y_exact, double* y_absdot, const uint16_t* x, const void* w,

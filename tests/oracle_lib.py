@@ -58,6 +58,10 @@ def lib() -> ctypes.CDLL:
             "oq_antiquant_policy": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int,
                                            _I64, _I64, _I64, ctypes.c_int, ctypes.c_int]),
             "oq_mm_requant4": (None, [_P, _P, _I64, _I64, _P, ctypes.c_uint64]),
+            "oq_e2m1_encode": (ctypes.c_uint8, [ctypes.c_double, ctypes.c_int]),
+            "oq_f32_to_fp8_sat": (ctypes.c_uint8, [ctypes.c_float, ctypes.c_int]),
+            "oq_quant_policy": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int,
+                                       ctypes.c_float, ctypes.c_int, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int]),
             "oq_requant4_f32": (None, [_P, _P, _I64, _I64, _P, ctypes.c_uint64]),
             "oq_matmul_i8": (None, [_P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int]),
             "oq_mm_dequant": (None, [_P, _P, ctypes.c_int, _I64, _I64, _P, ctypes.c_uint64]),
@@ -175,6 +179,24 @@ def antiquant_policy(src, src_type, scale, scale_type, dst_type, policy, m, n, g
     of = None if offset is None else np.ascontiguousarray(offset)
     lib().oq_antiquant_policy(_p(out), dst_type, _p(src), src_type, _p(sc), _p(of), scale_type, policy, m, n, group,
                               k_dim, int(is_transpose))
+    return out
+
+
+def quant_policy(src, src_type, scale, scale_type, dst_type, policy, m, n, group=0, offset=None,
+                 offset_scalar=None, k_dim=1, round_mode=ROUND_RINT):
+    """AscendQuant policy form over [m, n]: src (uint16 bits or float32) [m, n]; scale / offset arrays of
+    scale_type; offset_scalar a float (rounded to scale_type); returns int8 [m, n], fp8 bytes [m, n] or E2M1
+    codes packed [m, n/2]"""
+    if dst_type == FP4_E2M1:
+        out = np.empty((m, n // 2), np.uint8)
+    else:
+        out = np.empty((m, n), np.int8 if dst_type == INT8 else np.uint8)
+    src = np.ascontiguousarray(src)
+    sc = np.ascontiguousarray(scale)
+    of = None if offset is None else np.ascontiguousarray(offset)
+    has_off = offset is not None or offset_scalar is not None
+    lib().oq_quant_policy(_p(out), dst_type, _p(src), src_type, _p(sc), scale_type, _p(of), int(has_off),
+                          float(offset_scalar or 0.0), policy, m, n, group, k_dim, round_mode)
     return out
 
 

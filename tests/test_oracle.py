@@ -801,3 +801,193 @@ def test_antiquant_policy_fp4_e8m0():
     assert got[1, 2] == 0x0040 and got[2, 15] == 0xFF80  # 1 * 2^-127 (bf16 subnormal); -6 * 2^127 overflows to -inf
     h = O.antiquant_policy(packed, O.FP4_E2M1, e, O.E8M0, O.F16, O.PER_GROUP, m, n, g, k_dim=1)
     assert h[0, 15] == np.float16(-6.0).view(np.uint16) and h[2, 7] == 0x7BFF  # 6 * 2^127 saturates to 65504
+
+
+# --------------------------------------------------------------------------- AscendQuant policy form
+def _round_mode_np(y, mode):
+    """float64 round modes of docs/zh/api/SIMD-API/tensor_api/reg_vector_compute/type_conversion/rounding_mode.md:17-25"""
+    if mode == O.ROUND_FLOOR:
+        return np.floor(y)
+    if mode == O.ROUND_CEIL:
+        return np.ceil(y)
+    if mode == O.ROUND_TRUNC:
+        return np.trunc(y)
+    if mode == O.ROUND_ROUND:
+        return np.sign(y) * np.floor(np.abs(y) + 0.5)
+    return np.rint(y)
+
+
+def _sat_s8(y, mode):
+    with np.errstate(invalid="ignore"):
+        r = np.clip(_round_mode_np(np.nan_to_num(y, nan=0.0, posinf=1e9, neginf=-1e9), mode), -128, 127)
+    return r.astype(np.int8)
+
+
+def test_quant_policy_int8_round_mode_table():
+    """float -> integer round modes, the table of rounding_mode.md:40-47 (1.4, 1.5, 2.5, -1.4, -1.5, -2.5); 257
+    saturates to 127 and NaN gives 0 under SAT (type_conversion/cast.md:108)"""
+    x = np.array([[1.4, 1.5, 2.5, -1.4, -1.5, -2.5, 257.0, -300.0, np.nan, np.inf, -np.inf, 0.0]], np.float32)
+    one = np.ones(1, np.float32)
+    table = {O.ROUND_RINT: [1, 2, 2, -1, -2, -2], O.ROUND_ROUND: [1, 2, 3, -1, -2, -3],
+             O.ROUND_FLOOR: [1, 1, 2, -2, -2, -3], O.ROUND_CEIL: [2, 2, 3, -1, -1, -2],
+             O.ROUND_TRUNC: [1, 1, 2, -1, -1, -2], O.ROUND_NONE: [1, 2, 2, -1, -2, -2]}
+    for mode, exp in table.items():
+        got = O.quant_policy(x, O.F32, one, O.F32, O.INT8, O.PER_TOKEN, 1, x.shape[1], round_mode=mode)
+        assert got[0].tolist() == exp + [127, -128, 0, 127, -128, 0], mode
+
+
+@pytest.mark.parametrize("mode", [O.ROUND_RINT, O.ROUND_FLOOR, O.ROUND_CEIL, O.ROUND_ROUND, O.ROUND_TRUNC])
+def test_quant_policy_int8_scale_type_arithmetic(mode):
+    """int8 dst: x * s (+ o) with each op rounded in scaleT -- numpy float16 arithmetic for half, torch bfloat16 for
+    bf16, numpy float32 for an f32 scale met by a half source -- then the round mode and saturation
+    (ascend_quant_per_group_3510_impl.h:499-540, 1001-1046; TransRegForS8 ascend_quant_3510_impl.h:934-992)"""
+    rng = np.random.default_rng(950 + mode)
+    m, n, g = 64, 96, 32
+    x = rng.uniform(-160.0, 160.0, (m, n))
+    x[0, :8] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -127.5]  # exact ties with s = 1, o = 0
+    sc = rng.uniform(0.05, 2.0, (m, (n + g - 1) // g))
+    of = rng.uniform(-8.0, 8.0, sc.shape)
+    sc[0, 0], of[0, 0] = 1.0, 0.0
+    col = np.arange(n) // g
+    xh, sh, oh = x.astype(np.float16), sc.astype(np.float16), of.astype(np.float16)
+    got = O.quant_policy(xh.view(np.uint16), O.F16, sh.view(np.uint16), O.F16, O.INT8, O.PER_GROUP, m, n, g,
+                         offset=oh.view(np.uint16), k_dim=1, round_mode=mode)
+    y = (xh * sh[:, col]) + oh[:, col]
+    assert np.array_equal(got, _sat_s8(y.astype(np.float64), mode))
+    xb, sb, ob = _bf16_bits(x), _bf16_bits(sc), _bf16_bits(of)
+    got = O.quant_policy(xb, O.BF16, sb, O.BF16, O.INT8, O.PER_GROUP, m, n, g, offset=ob, k_dim=1, round_mode=mode)
+    t = lambda b: torch.from_numpy(_bf16_vals(b)).to(torch.bfloat16)
+    yb = (t(xb) * t(sb)[:, col] + t(ob)[:, col]).double().numpy()
+    assert np.array_equal(got, _sat_s8(yb, mode))
+    s32, o32 = sc.astype(np.float32), of.astype(np.float32)
+    got = O.quant_policy(xh.view(np.uint16), O.F16, s32, O.F32, O.INT8, O.PER_GROUP, m, n, g, offset=o32, k_dim=1,
+                         round_mode=mode)
+    y32 = xh.astype(np.float32) * s32[:, col] + o32[:, col]
+    assert np.array_equal(got, _sat_s8(y32.astype(np.float64), mode))
+
+
+def test_quant_policy_per_token_matches_fp32_per_token():
+    """PER_TOKEN with an f32 scale and offset is the per-token quant already restated (quant_per_token); the two
+    restatements agree element for element"""
+    rng = np.random.default_rng(960)
+    m, n = 32, 200
+    x = rng.uniform(-300.0, 300.0, (m, n)).astype(np.float16)
+    sc = rng.uniform(0.01, 1.5, m).astype(np.float32)
+    of = rng.uniform(-4.0, 4.0, m).astype(np.float32)
+    for mode in (O.ROUND_RINT, O.ROUND_FLOOR, O.ROUND_ROUND):
+        a = O.quant_policy(x.view(np.uint16), O.F16, sc, O.F32, O.INT8, O.PER_TOKEN, m, n, offset=of, round_mode=mode)
+        b = O.quant_per_token(x.view(np.uint16), O.F16, sc, of, round_mode=mode)
+        assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("fmt", [O.FP8_E4M3, O.FP8_E5M2])
+def test_quant_policy_fp8_in_fp32(fmt):
+    """fp8 dst: x * s + o in fp32 whatever scaleT, then rint with saturation (ascend_quant_per_group_3510_impl.h:
+    33-79, 393-431; TransRegForFp8 ascend_quant_3510_impl.h:888-896): torch's float8 casts (rne) after a clamp to
+    the largest finite value; NaN -> 0 (cast.md:109)"""
+    rng = np.random.default_rng(970 + fmt)
+    m, n = 48, 128
+    mx = 448.0 if fmt == O.FP8_E4M3 else 57344.0
+    x = (rng.standard_normal((m, n)) * np.exp2(rng.integers(-12, 14, (m, n)))).astype(np.float16)
+    x[0, :6] = [np.nan, np.inf, -np.inf, 65504.0, -65504.0, 0.0]
+    sh = rng.uniform(0.5, 2.0, m).astype(np.float16)
+    oh = rng.uniform(-1.0, 1.0, m).astype(np.float16)
+    got = O.quant_policy(x.view(np.uint16), O.F16, sh.view(np.uint16), O.F16, fmt, O.PER_TOKEN, m, n,
+                         offset=oh.view(np.uint16))
+    with np.errstate(invalid="ignore", over="ignore"):
+        v = x.astype(np.float32) * sh.astype(np.float32)[:, None] + oh.astype(np.float32)[:, None]
+    v = np.where(np.isnan(v), 0.0, np.clip(v, -mx, mx)).astype(np.float32)
+    dt = torch.float8_e4m3fn if fmt == O.FP8_E4M3 else torch.float8_e5m2
+    exp = torch.from_numpy(v).to(dt).view(torch.uint8).numpy()
+    assert np.array_equal(got, exp)
+    assert got[0, 0] == 0 and got[0, 1] == (0x7E if fmt == O.FP8_E4M3 else 0x7B)
+    # an f32 scale with a bf16 source: still one f32 product
+    xb = _bf16_bits(rng.uniform(-30.0, 30.0, (m, n)))
+    s32 = rng.uniform(0.5, 4.0, m).astype(np.float32)
+    got = O.quant_policy(xb, O.BF16, s32, O.F32, fmt, O.PER_TOKEN, m, n)
+    v = np.clip(_bf16_vals(xb) * s32[:, None], -mx, mx).astype(np.float32)
+    assert np.array_equal(got, torch.from_numpy(v).to(dt).view(torch.uint8).numpy())
+
+
+# E2M1 casts of a bf16 value, worked by hand from the mode definitions (rounding_mode.md:17-25) on the code table
+# {0, 0.5, 1, 1.5, 2, 3, 4, 6}: the seven tie points, both signs, inside-interval values and saturation
+_E2M1_X = [0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, -0.25, -2.5, 0.3, -0.3, 5.5, 7.0, -100.0, 6.0, -1.0]
+_E2M1_KAT = {
+    O.ROUND_RINT: [0x0, 0x2, 0x2, 0x4, 0x4, 0x6, 0x6, 0x8, 0xC, 0x1, 0x9, 0x7, 0x7, 0xF, 0x7, 0xA],
+    O.ROUND_ROUND: [0x1, 0x2, 0x3, 0x4, 0x5, 0x6, 0x7, 0x9, 0xD, 0x1, 0x9, 0x7, 0x7, 0xF, 0x7, 0xA],
+    O.ROUND_FLOOR: [0x0, 0x1, 0x2, 0x3, 0x4, 0x5, 0x6, 0x9, 0xD, 0x0, 0x9, 0x6, 0x7, 0xF, 0x7, 0xA],
+    O.ROUND_CEIL: [0x1, 0x2, 0x3, 0x4, 0x5, 0x6, 0x7, 0x8, 0xC, 0x1, 0x8, 0x7, 0x7, 0xF, 0x7, 0xA],
+    O.ROUND_TRUNC: [0x0, 0x1, 0x2, 0x3, 0x4, 0x5, 0x6, 0x8, 0xC, 0x0, 0x8, 0x6, 0x7, 0xF, 0x7, 0xA],
+}
+
+
+@pytest.mark.parametrize("mode", sorted(_E2M1_KAT))
+def test_quant_policy_e2m1_round_modes(mode):
+    """E2M1 dst (PER_GROUP): the bf16 -> E2M1 cast in each round mode with saturation (cast.md:96;
+    TransRegForFp4 ascend_quant_3510_impl.h:995-1036), against the hand-worked table; packed two a byte, even
+    element in the low nibble"""
+    x = np.array([_E2M1_X], np.float32)
+    n = x.shape[1]
+    assert [O.lib().oq_e2m1_encode(float(v), mode) for v in _E2M1_X] == _E2M1_KAT[mode]
+    one = _bf16_bits(np.ones((1, 1), np.float32))
+    got = O.quant_policy(_bf16_bits(x), O.BF16, one, O.BF16, O.FP4_E2M1, O.PER_GROUP, 1, n, 32, k_dim=1,
+                         round_mode=mode)
+    k = np.array(_E2M1_KAT[mode], np.uint8)
+    assert np.array_equal(got[0], k[0::2] | (k[1::2] << 4))
+
+
+def test_quant_policy_e2m1_rint_matches_mx_encoder():
+    """rint E2M1 agrees with the MX quantiser's nearest-even encoder (pinned by the MX golden) on a sweep of bf16
+    values"""
+    v = _bf16_vals(np.arange(0, 0x10000, 7, dtype=np.uint32).astype(np.uint16))
+    v = v[np.isfinite(v) & (np.abs(v) < 64)]
+    L = O.lib()
+    assert all(L.oq_e2m1_encode(float(a), O.ROUND_RINT) == L.oq_e2m1_encode_rne(float(a)) for a in v)
+
+
+def test_quant_policy_e2m1_through_bf16():
+    """a half or f32 product is first rounded to bf16 (rne, saturating; NaN -> 0), then cast to E2M1: 0.7495 rounds to
+    bf16 0.75, a tie that rint sends to 1.0 (code 2), where a direct cast would give 0.5 (code 1); an offset is
+    ignored for E2M1 (ascend_quant_per_group_3510_impl.h:1385)"""
+    xh = np.array([[0.74951171875, 2.49, -5.01, 70000.0 / 2, np.nan, 0.74951171875]], np.float16)
+    xh = np.concatenate([xh, np.zeros((1, 26), np.float16)], axis=1)
+    sh = np.ones((1, 1), np.float16)
+    got = O.quant_policy(xh.view(np.uint16), O.F16, sh.view(np.uint16), O.F16, O.FP4_E2M1, O.PER_GROUP, 1, 32, 32,
+                         offset=np.full((1, 1), 9.0, np.float16).view(np.uint16), k_dim=1)
+    # 2.49 -> bf16 2.484375 -> 2 (code 4); -5.01 -> bf16 -5.0 -> tie -> -4 (code 0xE); 35000 -> 6; NaN -> 0
+    assert got[0, :3].tolist() == [0x2 | (0x4 << 4), 0xE | (0x7 << 4), 0x0 | (0x2 << 4)]
+    x32 = np.zeros((1, 32), np.float32)
+    x32[0, :2] = [0.7499, 0.7499]
+    got = O.quant_policy(x32, O.F32, np.ones((1, 1), np.float32), O.F32, O.FP4_E2M1, O.PER_GROUP, 1, 32, 32,
+                         k_dim=1)
+    assert got[0, 0] == 0x22  # f32 0.7499 -> bf16 0.75 -> rint 1.0
+
+
+@pytest.mark.parametrize("k_dim", [0, 1])
+def test_quant_policy_group_axis(k_dim):
+    """PER_GROUP scale layout: kDim 1 groups along a row, scale [m][ceil(n/g)]; kDim 0 groups down a column,
+    scale [ceil(m/g)][n] (ascend_quant_per_group_3510_impl.h:347-380, 727-760, 1001-1046); with x = 1 and integer
+    scales the int8 output is the scale each element read, compared with numpy's repeat of the scale table"""
+    m, n, g = 80, 96, 32
+    shape = (m, (n + g - 1) // g) if k_dim == 1 else ((m + g - 1) // g, n)
+    sc = ((np.arange(shape[0] * shape[1]) % 251) - 125).astype(np.float32).reshape(shape)
+    got = O.quant_policy(np.ones((m, n), np.float32), O.F32, sc, O.F32, O.INT8, O.PER_GROUP, m, n, g, k_dim=k_dim)
+    exp = np.repeat(sc, g, axis=1)[:, :n] if k_dim == 1 else np.repeat(sc, g, axis=0)[:m]
+    assert np.array_equal(got, exp.astype(np.int8))
+
+
+def test_quant_policy_scalar_offset():
+    """the scalar-offset overloads take a scaleT value (ascend_quant_per_group_3510_impl.h:192-235, 297-333): a
+    scalar 0.1 with half scales acts as the half 0.0999755859375 everywhere, like a tensor filled with it"""
+    rng = np.random.default_rng(980)
+    m, n, g = 8, 64, 32
+    x = rng.uniform(-50.0, 50.0, (m, n)).astype(np.float16)
+    sh = rng.uniform(0.5, 2.0, (m, 2)).astype(np.float16)
+    full = np.full(sh.shape, np.float16(0.1), np.float16)
+    for dst in (O.INT8, O.FP8_E5M2):
+        a = O.quant_policy(x.view(np.uint16), O.F16, sh.view(np.uint16), O.F16, dst, O.PER_GROUP, m, n, g,
+                           offset_scalar=0.1, k_dim=1)
+        b = O.quant_policy(x.view(np.uint16), O.F16, sh.view(np.uint16), O.F16, dst, O.PER_GROUP, m, n, g,
+                           offset=full.view(np.uint16), k_dim=1)
+        c = O.quant_policy(x.view(np.uint16), O.F16, sh.view(np.uint16), O.F16, dst, O.PER_GROUP, m, n, g, k_dim=1)
+        assert np.array_equal(a, b) and not np.array_equal(a, c)

@@ -5,7 +5,8 @@ QUANT_PRE multiplier, half-away instead of half-even rounding, a swapped int4 ni
 reordered group-matmul epilogue, a transposed MX scale index, offset/scale applied in the wrong order, a
 double-rounded multiplier, a wrong E2M1 code, a ties-away f16 cast, an unrounded half add, a per-channel
 dequant indexed by row, a requant offset added before the clamp, a ties-away fp8 cast, an ignored requant
-sign flag and a FasterGelu with the wrong sign.  Each mutant is compiled on the CPU into a temporary library and the pinning tests of
+sign flag, a FasterGelu with the wrong sign, and policy-form quant mistakes (arithmetic type, bf16 step, group
+axis, offset rounding, directed E2M1 modes).  Each mutant is compiled on the CPU into a temporary library and the pinning tests of
 tests/test_oracle.py are run against it; every mutant must fail at least one of them.
 """
 from __future__ import annotations
@@ -41,6 +42,11 @@ MUTANTS = {
     18: "int4 requant output nibbles swapped",
     19: "per-group antiquant scales indexed along the wrong axis",
     20: "fp8 antiquant computed in the scale type instead of fp32",
+    21: "fp8 quant computed in the scale type instead of fp32",
+    22: "E2M1 quant cast without the bf16 rounding step",
+    23: "per-group quant scales indexed along the wrong axis",
+    24: "quant product not rounded to the scale type before the offset add",
+    25: "E2M1 floor / ceil applied to the magnitude regardless of sign",
 }
 
 
