@@ -438,7 +438,22 @@ hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int
 // length is not a multiple of 8, or unaligned pointers, take the per-element path of the same kernel.
 // ---------------------------------------------------------------------------------------------
 enum : int { QD_INT8 = 0, QD_E4M3 = 1, QD_E5M2 = 2, QD_E2M1 = 3 };
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 enum : int { QL_TOKEN = 0, QL_KCOL = 1, QL_KROW = 2 };
+
+// Unsigned division by a runtime constant d for dividends below 2^31: s = ceil(log2 d),
+// m = floor(2^32 (2^s - d) / d) + 1, q = (mulhi(n, m) + n) >> s (Granlund & Montgomery, "Division by invariant
+// integers using multiplication", PLDI 1994, section 4).
+struct FastDiv {
+    uint32_t m, s;
+};
+static FastDiv fast_div(uint32_t d)
+{
+    uint32_t s = 0;
+    while ((1ull << s) < d) ++s;
+    return FastDiv{(uint32_t)(((1ull << 32) * ((1ull << s) - d)) / d + 1), s};
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) { return (__umulhi(n, f.m) + n) >> f.s; }
 
 struct QuantPolicyArgs {
     void* dst;
@@ -446,9 +461,11 @@ struct QuantPolicyArgs {
     const void* scale;
     const void* offset;  // tensor indexed like scale, or null
     float off_scalar;    // used when has_off and offset is null (already a scaleT value)
-    int has_off;
-    int src_type, scale_type, round_mode, layout, fast;
-    int64_t m, n, g, sk, units;  // units: ceil(m * n / 8)
+    int has_off;         // 0 for E2M1, which takes no offset
+    int src_type, scale_type, round_mode, layout;
+    int64_t m, n, g, sk;
+    uint32_t units, upr;  // vector kernel: units of 8 elements, units per row (n / 8)
+    FastDiv upr_div, g_div;
 };
 
 // f32 -> fp8 with rint and saturation: NaN -> 0, overflow and inf -> +-max finite (TransRegForFp8,
@@ -460,25 +477,29 @@ __device__ __forceinline__ uint32_t f32_to_fp8_sat(float x, bool e5m2)
     return f32_to_fp8(__builtin_fminf(__builtin_fmaxf(x, -mx), mx), e5m2 ? 1 : 0);
 }
 
-// bf16 value -> E2M1 code in round mode `mode`, saturating at +-6 (Cast<fp4x2_e2m1_t, bfloat16_t>, cast.md:96).
-// The code table is three uniform segments -- [0, 2) in steps of 0.5 (codes 0-4), [2, 4) in steps of 1 (4-6),
-// [4, 6] in steps of 2 (6-7) -- so the code is the segment base plus the rounded, exactly scaled offset into it;
-// every base is even, so ties to even on the offset are ties to an even code.  A directed mode on a negative value
-// rounds the magnitude the other way.  NaN -> 0.
-__device__ __forceinline__ uint32_t bf16_to_e2m1(float v, int mode)
+// bf16 value -> E2M1 code in round mode MODE, saturating at +-6 (Cast<fp4x2_e2m1_t, bfloat16_t>, cast.md:96); NaN -> 0.
+// |v| >= 1: the E2M1 codes from 1.0 (code 2) up are consecutive fp32 patterns rounded to one mantissa bit, so the
+// code is (pattern + rounding bias) >> 22 less 252 (1.0 = 0x3F800000 -> 254).  The bias rounds the dropped 22 bits:
+// half-to-even, half-away, none (trunc), or all-ones (magnitude up: ceil of a positive, floor of a negative value).
+// |v| < 1: codes 0, 1, 2 are |round(2 v)| with the signed value rounded, so the directed modes see the sign.  A
+// negative value that rounds to zero keeps its sign bit.
+template <int MODE>
+__device__ __forceinline__ uint32_t e2m1_code(float v)
 {
-    if (v != v) return 0u;
-    const uint32_t s = (__float_as_uint(v) >> 28) & 8u;
-    const float a = __builtin_fabsf(v);
-    if (a >= 6.0f) return s | 7u;
-    int mm = mode;
-    if (s) mm = mode == RM_FLOOR ? RM_CEIL : (mode == RM_CEIL ? RM_FLOOR : mode);
-    float q;
-    uint32_t base;
-    if (a < 2.0f) q = a * 2.0f, base = 0u;
-    else if (a < 4.0f) q = a - 2.0f, base = 4u;
-    else q = (a - 4.0f) * 0.5f, base = 6u;
-    return s | (base + (uint32_t)round_mode_f(q, mm));
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t s = (u >> 28) & 8u;
+    const uint32_t a = u & 0x7fffffffu;
+    uint32_t bias;
+    if constexpr (MODE == RM_TRUNC) bias = 0u;
+    else if constexpr (MODE == RM_ROUND) bias = 0x200000u;
+    else if constexpr (MODE == RM_FLOOR) bias = s ? 0x3FFFFFu : 0u;
+    else if constexpr (MODE == RM_CEIL) bias = s ? 0u : 0x3FFFFFu;
+    else bias = 0x1FFFFFu + ((a >> 22) & 1u);
+    const uint32_t hi = ((a + bias) >> 22) - 252u;
+    const uint32_t lo = (uint32_t)__builtin_fminf(__builtin_fabsf(round_mode_f(2.0f * v, MODE)), 2.0f);
+    uint32_t c = a >= 0x3F800000u ? hi : lo;
+    c = c > 7u ? 7u : c;
+    return v != v ? 0u : (s | c);
 }
 
 // one scaleT rounding of an fp32 result (exact for products of two 16-bit values; a single correct rounding for
@@ -489,6 +510,34 @@ __device__ __forceinline__ float rnd_t(float x)
     if constexpr (T == DT_F16) return (float)(_Float16)x;
     else if constexpr (T == DT_BF16) return bf16_round(x);
     else return x;
+}
+
+// the output code of a scaleT result v (after the offset): int8 byte, fp8 byte or E2M1 nibble
+template <int DST, int T, int MODE>
+__device__ __forceinline__ uint32_t quant_code(float v)
+{
+    if constexpr (DST == QD_INT8) {
+        return (uint32_t)sat_s8_from_integral(round_mode_f(v, MODE)) & 0xffu;
+    } else if constexpr (DST == QD_E4M3 || DST == QD_E5M2) {
+        return f32_to_fp8_sat(v, DST == QD_E5M2);
+    } else {
+        // f16 / f32 results go through bf16 (rne, saturating, NaN -> 0): plain rne here gives the same E2M1 code,
+        // as NaN maps to 0 and every overflow to +-6 either way
+        if constexpr (T != DT_BF16) v = bf16_round(v);
+        return e2m1_code<MODE>(v);
+    }
+}
+
+template <int DST, int T>
+__device__ __forceinline__ uint32_t quant_code_rt(float v, int mode)
+{
+    switch (mode) {
+    case RM_FLOOR: return quant_code<DST, T, RM_FLOOR>(v);
+    case RM_CEIL: return quant_code<DST, T, RM_CEIL>(v);
+    case RM_ROUND: return quant_code<DST, T, RM_ROUND>(v);
+    case RM_TRUNC: return quant_code<DST, T, RM_TRUNC>(v);
+    default: return quant_code<DST, T, RM_RINT>(v);
+    }
 }
 
 __device__ __forceinline__ void load8_f32(const void* p, int t, int64_t i, float (&o)[8])
@@ -503,86 +552,295 @@ __device__ __forceinline__ void load8_f32(const void* p, int t, int64_t i, float
     }
     const u32x4 a = __builtin_nontemporal_load((const u32x4*)((const uint16_t*)p + i));
     const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+    const bool bf = t == DT_BF16;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const uint16_t lo = (uint16_t)(w[j] & 0xffffu), hi = (uint16_t)(w[j] >> 16);
-        o[2 * j] = t == DT_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
-        o[2 * j + 1] = t == DT_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+        o[2 * j] = bf ? __uint_as_float(w[j] << 16) : f16_to_f32((uint16_t)(w[j] & 0xffffu));
+        o[2 * j + 1] = bf ? __uint_as_float(w[j] & 0xffff0000u) : f16_to_f32((uint16_t)(w[j] >> 16));
     }
 }
 
-template <int DST, int T>
-__global__ __launch_bounds__(256) void quant_policy_kernel(QuantPolicyArgs a)
+// 8 elements of a 16- or 32-bit float type as raw 32-bit words (f16 / bf16: 4 words, f32: 8) and their values
+template <int TY>
+struct Raw8 {
+    uint32_t w[TY == DT_F32 ? 8 : 4];
+};
+template <int TY>
+__device__ __forceinline__ void load_raw8(const void* p, int64_t unit, Raw8<TY>& r)
 {
-    const int64_t total = a.m * a.n;
-    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < a.units; u += (int64_t)gridDim.x * 256) {
-        const int64_t e0 = u * 8;
-        float x[8], s[8], o[8];
-        if (a.fast) {  // n % 8 == 0: the 8 elements share a row; aligned 16-byte loads
-            const int64_t r = e0 / a.n, c = e0 - r * a.n;
-            load8_f32(a.src, a.src_type, e0, x);
-            if (a.layout == QL_KROW) {
-                const int64_t si = (r / a.g) * a.n + c;
-                load8_f32(a.scale, a.scale_type, si, s);
-                if (a.offset) load8_f32(a.offset, a.scale_type, si, o);
-            } else {
-                const int64_t si = a.layout == QL_TOKEN ? r : r * a.sk + c / a.g;
-                const float sv = load_scale_t(a.scale, a.scale_type, si);
-                const float ov = a.offset ? load_scale_t(a.offset, a.scale_type, si) : 0.0f;
+    const u32x4* q = (const u32x4*)p + (TY == DT_F32 ? 2 * unit : unit);
+    const u32x4 a = __builtin_nontemporal_load(q);
+    r.w[0] = a.x, r.w[1] = a.y, r.w[2] = a.z, r.w[3] = a.w;
+    if constexpr (TY == DT_F32) {
+        const u32x4 b = __builtin_nontemporal_load(q + 1);
+        r.w[4] = b.x, r.w[5] = b.y, r.w[6] = b.z, r.w[7] = b.w;
+    }
+}
+template <int TY>
+__device__ __forceinline__ float raw_to_f32(uint32_t w)  // one element in the low bits (16-bit types) or whole word
+{
+    if constexpr (TY == DT_F32) return __uint_as_float(w);
+    else if constexpr (TY == DT_BF16) return __uint_as_float(w << 16);
+    else return f16_to_f32((uint16_t)w);
+}
+template <int TY>
+__device__ __forceinline__ float raw8_at(const Raw8<TY>& r, int j)
+{
+    if constexpr (TY == DT_F32) return __uint_as_float(r.w[j]);
+    else return raw_to_f32<TY>((j & 1) ? (r.w[j >> 1] >> 16) : (r.w[j >> 1] & 0xffffu));
+}
+template <int TY>
+__device__ __forceinline__ uint32_t load_raw1(const void* p, int64_t i)
+{
+    if constexpr (TY == DT_F32) return ((const uint32_t*)p)[i];
+    else return ((const uint16_t*)p)[i];
+}
+
+// f32 -> fp8 with rint and saturation through the gfx950 conversion (OCP e4m3fn / e5m2, round to nearest even):
+// the input is clamped to the largest finite magnitude first and NaN replaced by 0, so only in-range values reach
+// the instruction
+template <bool E5M2>
+__device__ __forceinline__ uint32_t fp8_sat_hw(float x)
+{
+    const float mx = E5M2 ? 57344.0f : 448.0f;
+    x = x != x ? 0.0f : __builtin_fminf(__builtin_fmaxf(x, -mx), mx);
+    if constexpr (E5M2) return (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(x, 0.0f, 0, false) & 0xffu;
+    else return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x, 0.0f, 0, false) & 0xffu;
+}
+
+// Vector path (n % 8 == 0, 16-byte aligned source and row-group scales, fewer than 2^31 units): a unit is 8
+// consecutive elements of one row; each lane takes UNR units and first issues every load they need -- source,
+// scale and offset, unconditionally (indices clamped into the tensors, the scale table standing in for a missing
+// offset tensor) so that no load waits on another -- then converts them.
+//  * scales along the row (PER_GROUP kDim 1; PER_TOKEN is the case sk = 1, g = n): a workgroup takes UNR * 256
+//    consecutive units per pass, one scale per unit at r * sk + c / g (group sizes are multiples of 32, so a unit
+//    never straddles two groups);
+//  * groups down the columns (kDim 0, KROW): a lane takes the same 8 columns of UNR consecutive rows r0 .. r0 + UNR - 1
+//    (r0 a multiple of UNR, which divides every group size), so one load of 8 scales (and offsets) serves all UNR
+//    units; the lanes of a wave still cover consecutive units of each row.
+// Stores: 8 bytes (int8 / fp8) or 4 (E2M1) per unit.
+// SC: scale type; the arithmetic type T is SC for int8 / E2M1 and fp32 for fp8.  With T = f16 the product and the
+// offset add run as packed half operations (each correctly rounded, which is the scaleT arithmetic itself).
+constexpr int QP_UNR = 4;
+
+template <int DST, int SRC, int SC, int MODE, bool KROW>
+__device__ __forceinline__ void quant_unit(const QuantPolicyArgs& a, uint32_t u, const Raw8<SRC>& xr,
+                                           const Raw8<SC>& sr, Raw8<SC> orw, bool off_tensor, uint32_t osc)
+{
+    constexpr bool FP8 = DST == QD_E4M3 || DST == QD_E5M2;
+    constexpr int T = FP8 ? DT_F32 : SC;
+    constexpr bool HALF = T == DT_F16;  // then SRC == SC == f16
+    if (!off_tensor) {  // scalar offset (or none): broadcast it like a per-unit scale
+        if constexpr (KROW) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) s[j] = sv, o[j] = ov;
-            }
-            if (!a.offset) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) o[j] = a.off_scalar;
-            }
+            for (int q = 0; q < (SC == DT_F32 ? 8 : 4); ++q) orw.w[q] = SC == DT_F32 ? osc : (osc | (osc << 16));
         } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int64_t e = e0 + j < total ? e0 + j : total - 1;  // clamped; lanes past the end are not stored
-                const int64_t r = e / a.n, c = e - r * a.n;
-                const int64_t si = a.layout == QL_TOKEN ? r : (a.layout == QL_KCOL ? r * a.sk + c / a.g
-                                                                                    : (r / a.g) * a.n + c);
-                x[j] = load_scale_t(a.src, a.src_type, e);
-                s[j] = load_scale_t(a.scale, a.scale_type, si);
-                o[j] = a.offset ? load_scale_t(a.offset, a.scale_type, si) : a.off_scalar;
-            }
+            orw.w[0] = osc;
         }
-        uint32_t code[8];
+    }
+    float v[8];
+    if constexpr (HALF) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t sw = KROW ? sr.w[q] : (sr.w[0] | (sr.w[0] << 16));
+            h2 p = __builtin_bit_cast(h2, xr.w[q]) * __builtin_bit_cast(h2, sw);
+            if (a.has_off) {
+                const uint32_t ow = KROW ? orw.w[q] : (orw.w[0] | (orw.w[0] << 16));
+                p = p + __builtin_bit_cast(h2, ow);
+            }
+            v[2 * q] = (float)p.x;
+            v[2 * q + 1] = (float)p.y;
+        }
+    } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            float v = rnd_t<T>(x[j] * s[j]);
-            if (DST != QD_E2M1 && a.has_off) v = rnd_t<T>(v + o[j]);
-            if constexpr (DST == QD_INT8) {
-                code[j] = (uint32_t)sat_s8_from_integral(round_mode_f(v, a.round_mode)) & 0xffu;
-            } else if constexpr (DST == QD_E4M3 || DST == QD_E5M2) {
-                code[j] = f32_to_fp8_sat(v, DST == QD_E5M2);
-            } else {
-                if constexpr (T != DT_BF16) v = v != v ? 0.0f : bf16_to_f32(f32_to_bf16_sat(v));
-                code[j] = bf16_to_e2m1(v, a.round_mode);
-            }
+            const float sj = KROW ? raw8_at<SC>(sr, j) : raw_to_f32<SC>(sr.w[0]);
+            float t = rnd_t<T>(raw8_at<SRC>(xr, j) * sj);
+            if (a.has_off) t = rnd_t<T>(t + (KROW ? raw8_at<SC>(orw, j) : raw_to_f32<SC>(orw.w[0])));
+            v[j] = t;
         }
-        if constexpr (DST == QD_E2M1) {
-            const uint32_t w = code[0] | (code[1] << 4) | (code[2] << 8) | (code[3] << 12) | (code[4] << 16) |
-                               (code[5] << 20) | (code[6] << 24) | (code[7] << 28);
-            uint8_t* d = (uint8_t*)a.dst + e0 / 2;
-            if (a.fast) {
-                __builtin_nontemporal_store(w, (uint32_t*)d);
-            } else {
-                for (int j = 0; j < 4; ++j)
-                    if (e0 + 2 * j < total) d[j] = (uint8_t)(w >> (8 * j));
-            }
-        } else {
-            uint8_t* d = (uint8_t*)a.dst + e0;
-            if (a.fast) {
-                const u32x2 w = {code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24),
-                                 code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24)};
-                __builtin_nontemporal_store(w, (u32x2*)d);
-            } else {
-                for (int j = 0; j < 8; ++j)
-                    if (e0 + j < total) d[j] = (uint8_t)code[j];
-            }
+    }
+    if constexpr (DST == QD_E2M1 && MODE == RM_RINT) {
+        // rint E2M1 through the gfx950 conversions: fp32 -> bf16 (v_cvt_pk_bf16_f32, rne) and bf16 -> E2M1
+        // (v_cvt_scalef32_pk_fp4_bf16 with scale 1: nearest even, saturating at +-6), two elements each; both agree
+        // with the software rounding (bf16_round, e2m1_code<RM_RINT>) on every non-NaN input, and NaN is replaced
+        // by 0 first (its code under the saturating casts)
+        bf2 b[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float v0 = v[2 * q] != v[2 * q] ? 0.0f : v[2 * q];
+            const float v1 = v[2 * q + 1] != v[2 * q + 1] ? 0.0f : v[2 * q + 1];
+            if constexpr (T == DT_BF16)  // already bf16 values
+                b[q] = (bf2){__builtin_bit_cast(__bf16, (uint16_t)(__float_as_uint(v0) >> 16)),
+                             __builtin_bit_cast(__bf16, (uint16_t)(__float_as_uint(v1) >> 16))};
+            else
+                b[q] = (bf2){(__bf16)v0, (__bf16)v1};
         }
+        uint32_t w = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(0u, b[0], 1.0f, 0);  // elements 0, 1 -> byte 0
+        w = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(w, b[1], 1.0f, 1);
+        w = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(w, b[2], 1.0f, 2);
+        w = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(w, b[3], 1.0f, 3);
+        __builtin_nontemporal_store(w, (uint32_t*)a.dst + u);
+        return;
+    }
+    uint32_t code[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        if constexpr (FP8) code[j] = fp8_sat_hw<DST == QD_E5M2>(v[j]);
+        else code[j] = quant_code<DST, T, MODE>(v[j]);
+    }
+    if constexpr (DST == QD_E2M1) {
+        const uint32_t w = code[0] | (code[1] << 4) | (code[2] << 8) | (code[3] << 12) | (code[4] << 16) |
+                           (code[5] << 20) | (code[6] << 24) | (code[7] << 28);
+        __builtin_nontemporal_store(w, (uint32_t*)a.dst + u);
+    } else {
+        const u32x2 w = {code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24),
+                         code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24)};
+        __builtin_nontemporal_store(w, (u32x2*)a.dst + u);
+    }
+}
+
+template <int SC>
+__device__ __forceinline__ uint32_t offset_scalar_bits(float o)
+{
+    if constexpr (SC == DT_F32) return __float_as_uint(o);
+    else if constexpr (SC == DT_BF16) return __float_as_uint(o) >> 16;  // already a bf16 value
+    else return (uint32_t)h_bits((_Float16)o);                          // already a half value
+}
+
+template <int DST, int SRC, int SC, int MODE>
+__global__ __launch_bounds__(256) void quant_policy_vec_kernel(QuantPolicyArgs a)  // scales along the row
+{
+    const void* offp = a.offset ? a.offset : a.scale;
+    const bool off_tensor = a.offset != nullptr;
+    const uint32_t osc = offset_scalar_bits<SC>(a.off_scalar);
+    for (uint32_t b0 = blockIdx.x * (256u * QP_UNR); b0 < a.units; b0 += gridDim.x * (256u * QP_UNR)) {
+        Raw8<SRC> xr[QP_UNR];
+        Raw8<SC> sr[QP_UNR], orw[QP_UNR];  // one scale / offset each, in w[0]
+#pragma unroll
+        for (int k = 0; k < QP_UNR; ++k) {
+            uint32_t u = b0 + k * 256u + threadIdx.x;
+            u = u < a.units ? u : a.units - 1u;  // past the end: load a valid unit, store nothing
+            load_raw8<SRC>(a.src, u, xr[k]);
+            const uint32_t r = fdiv(u, a.upr_div), c = (u - r * a.upr) * 8u;
+            const int64_t si = (int64_t)r * a.sk + fdiv(c, a.g_div);
+            sr[k].w[0] = load_raw1<SC>(a.scale, si);
+            orw[k].w[0] = load_raw1<SC>(offp, si);
+        }
+#pragma unroll
+        for (int k = 0; k < QP_UNR; ++k) {
+            const uint32_t u = b0 + k * 256u + threadIdx.x;
+            if (u >= a.units) break;
+            quant_unit<DST, SRC, SC, MODE, false>(a, u, xr[k], sr[k], orw[k], off_tensor, osc);
+        }
+    }
+}
+
+template <int DST, int SRC, int SC, int MODE>
+__global__ __launch_bounds__(256) void quant_policy_vec_krow_kernel(QuantPolicyArgs a)  // groups down the columns
+{
+    const void* offp = a.offset ? a.offset : a.scale;
+    const bool off_tensor = a.offset != nullptr;
+    const uint32_t osc = offset_scalar_bits<SC>(a.off_scalar);
+    const uint32_t rows = (uint32_t)a.m;
+    for (uint32_t v = blockIdx.x * 256u + threadIdx.x; v < a.units; v += gridDim.x * 256u) {  // units: row blocks x upr
+        const uint32_t rb = fdiv(v, a.upr_div), wu = v - rb * a.upr, r0 = rb * QP_UNR;
+        const int64_t su = ((int64_t)fdiv(r0, a.g_div) * a.n) / 8 + wu;
+        Raw8<SRC> xr[QP_UNR];
+        Raw8<SC> sr, orw;
+        load_raw8<SC>(a.scale, su, sr);
+        load_raw8<SC>(offp, su, orw);
+#pragma unroll
+        for (int k = 0; k < QP_UNR; ++k) {
+            const uint32_t r = r0 + k < rows ? r0 + k : rows - 1u;
+            load_raw8<SRC>(a.src, (int64_t)r * a.upr + wu, xr[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < QP_UNR; ++k) {
+            if (r0 + k >= rows) break;
+            quant_unit<DST, SRC, SC, MODE, true>(a, (r0 + k) * a.upr + wu, xr[k], sr, orw, off_tensor, osc);
+        }
+    }
+}
+
+// Any shape or alignment: one thread per output byte (one element; two for E2M1), 64-bit indices.
+template <int DST, int T>
+__global__ __launch_bounds__(256) void quant_policy_generic_kernel(QuantPolicyArgs a)
+{
+    const int64_t total = a.m * a.n;
+    const int64_t per = DST == QD_E2M1 ? 2 : 1;
+    const int64_t bytes = total / per;
+    for (int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x; b < bytes; b += (int64_t)gridDim.x * 256) {
+        uint32_t w = 0;
+        for (int64_t h = 0; h < per; ++h) {
+            const int64_t e = b * per + h;
+            const int64_t r = e / a.n, c = e - r * a.n;
+            const int64_t si = a.layout == QL_TOKEN ? r : (a.layout == QL_KCOL ? r * a.sk + c / a.g
+                                                                                : (r / a.g) * a.n + c);
+            const float x = load_scale_t(a.src, a.src_type, e);
+            const float s = load_scale_t(a.scale, a.scale_type, si);
+            float v = rnd_t<T>(x * s);
+            if (a.has_off) v = rnd_t<T>(v + (a.offset ? load_scale_t(a.offset, a.scale_type, si) : a.off_scalar));
+            w |= quant_code_rt<DST, T>(v, a.round_mode) << (4 * h);
+        }
+        ((uint8_t*)a.dst)[b] = (uint8_t)w;
+    }
+}
+
+template <int DST, int SRC, int SC, int MODE>
+static void launch_qp_layout(const QuantPolicyArgs& a, hipStream_t st)
+{
+    if (a.layout == QL_KROW)
+        launch_k(quant_policy_vec_krow_kernel<DST, SRC, SC, MODE>, dim3(grid_for(a.units)), dim3(256), 0, st, a);
+    else
+        launch_k(quant_policy_vec_kernel<DST, SRC, SC, MODE>, dim3(grid_for((a.units + QP_UNR - 1) / QP_UNR)),
+                 dim3(256), 0, st, a);
+}
+
+template <int DST, int SRC, int SC>
+static void launch_qp_vec(const QuantPolicyArgs& a, hipStream_t st)
+{
+    if constexpr (DST == QD_E4M3 || DST == QD_E5M2) {  // every round mode is rint for fp8
+        launch_qp_layout<DST, SRC, SC, RM_RINT>(a, st);
+        return;
+    }
+    switch (a.round_mode) {
+    case RM_FLOOR: launch_qp_layout<DST, SRC, SC, RM_FLOOR>(a, st); break;
+    case RM_CEIL: launch_qp_layout<DST, SRC, SC, RM_CEIL>(a, st); break;
+    case RM_ROUND: launch_qp_layout<DST, SRC, SC, RM_ROUND>(a, st); break;
+    case RM_TRUNC: launch_qp_layout<DST, SRC, SC, RM_TRUNC>(a, st); break;
+    default: launch_qp_layout<DST, SRC, SC, RM_RINT>(a, st); break;
+    }
+}
+
+template <int DST, int SC>
+static void launch_qp_src(const QuantPolicyArgs& a, hipStream_t st)
+{
+    if (a.src_type == DT_F16) launch_qp_vec<DST, DT_F16, SC>(a, st);
+    else if (a.src_type == DT_BF16) launch_qp_vec<DST, DT_BF16, SC>(a, st);
+    else launch_qp_vec<DST, DT_F32, SC>(a, st);
+}
+
+// T: arithmetic type -- the scale type for int8 / E2M1, which pair it with a source of the same type or an f32
+// scale; fp32 for fp8, which takes any source and scale type
+template <int DST, int T>
+static void launch_qp(const QuantPolicyArgs& a, bool vec, hipStream_t st)
+{
+    if (!vec) {
+        const int64_t bytes = DST == QD_E2M1 ? a.m * a.n / 2 : a.m * a.n;
+        launch_k(quant_policy_generic_kernel<DST, T>, dim3(grid_for(bytes)), dim3(256), 0, st, a);
+        return;
+    }
+    if constexpr (DST == QD_E4M3 || DST == QD_E5M2) {
+        if (a.scale_type == DT_F16) launch_qp_src<DST, DT_F16>(a, st);
+        else if (a.scale_type == DT_BF16) launch_qp_src<DST, DT_BF16>(a, st);
+        else launch_qp_src<DST, DT_F32>(a, st);
+    } else if constexpr (T == DT_F16) {
+        launch_qp_vec<DST, DT_F16, DT_F16>(a, st);
+    } else if constexpr (T == DT_BF16) {
+        launch_qp_vec<DST, DT_BF16, DT_BF16>(a, st);
+    } else {
+        launch_qp_src<DST, DT_F32>(a, st);
     }
 }
 
@@ -590,11 +848,15 @@ hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src
                                int scale_type, const void* offset, int has_offset, float offset_scalar, int per_token,
                                int64_t m, int64_t n, int64_t g, int k_dim, int round_mode, hipStream_t st)
 {
+    const int dk = dst_type == DT_INT8 ? QD_INT8
+                   : dst_type == DT_FP8_E4M3 ? QD_E4M3
+                   : dst_type == DT_FP8_E5M2 ? QD_E5M2 : QD_E2M1;
     QuantPolicyArgs a;
     a.dst = dst;
     a.src = src;
     a.scale = scale;
-    a.offset = has_offset ? offset : nullptr;
+    a.has_off = has_offset && dk != QD_E2M1;
+    a.offset = a.has_off ? offset : nullptr;
     // the scalar offset is a scaleT value: round it (rne) to the scale type once, here
     float os = offset_scalar;
     if (scale_type == DT_F16) {
@@ -605,7 +867,6 @@ hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src
         os = __builtin_bit_cast(float, u);
     }
     a.off_scalar = os;
-    a.has_off = has_offset;
     a.src_type = src_type;
     a.scale_type = scale_type;
     a.round_mode = round_mode;
@@ -614,29 +875,32 @@ hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src
     a.n = n;
     a.g = g > 0 ? g : 1;
     a.sk = (n + a.g - 1) / a.g;
-    a.units = (m * n + 7) / 8;
-    const int dk = dst_type == DT_INT8 ? QD_INT8
-                   : dst_type == DT_FP8_E4M3 ? QD_E4M3
-                   : dst_type == DT_FP8_E5M2 ? QD_E5M2 : QD_E2M1;
-    const uintptr_t dal = dk == QD_E2M1 ? 4 : 8;
-    const bool al = (uintptr_t)src % 16 == 0 && (uintptr_t)dst % dal == 0 &&
+    // vector kernels: units of 8 elements; for groups down the columns, blocks of QP_UNR rows x (n / 8) units
+    const int64_t units = a.layout == QL_KROW ? (m + QP_UNR - 1) / QP_UNR * (n / 8) : m * n / 8;
+    const bool al = (uintptr_t)src % 16 == 0 && (uintptr_t)dst % (dk == QD_E2M1 ? 4 : 8) == 0 &&
                     (a.layout != QL_KROW || ((uintptr_t)scale % 16 == 0 && (uintptr_t)a.offset % 16 == 0));
-    a.fast = n % 8 == 0 && al;
-    const int t = (dk == QD_E4M3 || dk == QD_E5M2) ? DT_F32 : scale_type;  // arithmetic type
-    dim3 grid(grid_for(a.units)), block(256);
-#define QP_LAUNCH(D, T) launch_k(quant_policy_kernel<D, T>, grid, block, 0, st, a)
-    if (dk == QD_E4M3) QP_LAUNCH(QD_E4M3, DT_F32);
-    else if (dk == QD_E5M2) QP_LAUNCH(QD_E5M2, DT_F32);
-    else if (dk == QD_INT8) {
-        if (t == DT_F16) QP_LAUNCH(QD_INT8, DT_F16);
-        else if (t == DT_BF16) QP_LAUNCH(QD_INT8, DT_BF16);
-        else QP_LAUNCH(QD_INT8, DT_F32);
+    const bool vec = n % 8 == 0 && al && m * n / 8 < (1ll << 31) && a.g < (1ll << 31) && n < (1ll << 31);
+    a.units = vec ? (uint32_t)units : 0u;
+    a.upr = vec ? (uint32_t)(n / 8) : 1u;
+    a.upr_div = fast_div(a.upr);
+    if (vec && a.layout == QL_TOKEN) {  // the vector kernel reads PER_TOKEN as one group of n per row
+        a.sk = 1;
+        a.g_div = fast_div((uint32_t)n);
     } else {
-        if (t == DT_F16) QP_LAUNCH(QD_E2M1, DT_F16);
-        else if (t == DT_BF16) QP_LAUNCH(QD_E2M1, DT_BF16);
-        else QP_LAUNCH(QD_E2M1, DT_F32);
+        a.g_div = fast_div((uint32_t)(vec ? a.g : 1));
     }
-#undef QP_LAUNCH
+    const int t = (dk == QD_E4M3 || dk == QD_E5M2) ? DT_F32 : scale_type;  // arithmetic type
+    if (dk == QD_E4M3) launch_qp<QD_E4M3, DT_F32>(a, vec, st);
+    else if (dk == QD_E5M2) launch_qp<QD_E5M2, DT_F32>(a, vec, st);
+    else if (dk == QD_INT8) {
+        if (t == DT_F16) launch_qp<QD_INT8, DT_F16>(a, vec, st);
+        else if (t == DT_BF16) launch_qp<QD_INT8, DT_BF16>(a, vec, st);
+        else launch_qp<QD_INT8, DT_F32>(a, vec, st);
+    } else {
+        if (t == DT_F16) launch_qp<QD_E2M1, DT_F16>(a, vec, st);
+        else if (t == DT_BF16) launch_qp<QD_E2M1, DT_BF16>(a, vec, st);
+        else launch_qp<QD_E2M1, DT_F32>(a, vec, st);
+    }
     return hipGetLastError();
 }
 

@@ -381,7 +381,38 @@ def traffic_probe(torch, ascq):
     return {"traffic_probe": "copy 268435456 B, quant f16 8192x8192, dequant int8 8192x8192 -> f16"}
 
 
+def bench_quant_policy(torch, ascq, dst_type, policy, iters, k_dim=1, g=128):
+    """AscendQuant policy form over an f16 [8192, 8192] activation: PER_GROUP (group 128 along the rows) or
+    PER_TOKEN, f16 scales, to int8 / fp8 / E2M1"""
+    M = N = 8192
+    out_b = M * N // 2 if dst_type == ascq.FP4_E2M1 else M * N
+    ss = (M,) if policy == ascq.PER_TOKEN else ((M, N // g) if k_dim == 1 else (M // g, N))
+    nbytes = 2 * M * N + out_b + 2 * int(np.prod(ss))
+    R = rotation(nbytes)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    xs = [torch.randn((M, N), generator=gen, device="cuda").half() for _ in range(R)]
+    sc = torch.empty(ss, device="cuda").uniform_(0.5, 8.0, generator=gen).half()
+    shape = (M, N // 2) if dst_type == ascq.FP4_E2M1 else (M, N)
+    qs = [torch.empty(shape, dtype=torch.uint8, device="cuda") for _ in range(R)]
+
+    def fn(i):
+        ascq.ascend_quant_policy(xs[i % R], sc, policy, dst_type, g if policy == ascq.PER_GROUP else 0, k_dim=k_dim,
+                                 out=qs[i % R])
+
+    ms = _time_loop(torch, fn, iters)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    name = {ascq.INT8: "int8", ascq.FP8_E4M3: "fp8_e4m3", ascq.FP4_E2M1: "E2M1"}[dst_type]
+    pol = "PER_TOKEN" if policy == ascq.PER_TOKEN else f"PER_GROUP g={g} kDim={k_dim}"
+    return dict(workload=f"AscendQuant {pol} f16 [{M},{N}] -> {name} (f16 scales)", ms=ms, value=gbs, unit="GB/s",
+                frac_of_peak=gbs / HBM_PEAK_GBS)
+
+
 OTHER = {
+    "quant": [lambda t, a: bench_quant_policy(t, a, a.INT8, a.PER_GROUP, 50),
+              lambda t, a: bench_quant_policy(t, a, a.INT8, a.PER_GROUP, 50, k_dim=0),
+              lambda t, a: bench_quant_policy(t, a, a.FP8_E4M3, a.PER_TOKEN, 50),
+              lambda t, a: bench_quant_policy(t, a, a.FP4_E2M1, a.PER_GROUP, 50)],
     "w8a8": [lambda t, a: bench_w8a8(t, a, 128, 256, 512, 200), lambda t, a: bench_w8a8(t, a, 8192, 8192, 8192, 10)],
     "gemv": [lambda t, a, w=w, m=m: bench_gemv(t, a, getattr(a, w), m, 200)
              for w in ("INT4", "INT8") for m in (1, 16, 64)],
@@ -394,7 +425,7 @@ OTHER = {
 
 def run_others(torch, ascq, which):
     out = []
-    for key in (["w8a8", "gemv", "group", "mx", "fp8"] if which == "all" else [which]):
+    for key in (["quant", "w8a8", "gemv", "group", "mx", "fp8"] if which == "all" else [which]):
         for fn in OTHER[key]:
             try:
                 r = fn(torch, ascq)
@@ -412,7 +443,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="all",
-                    choices=["all", "headline", "w8a8", "gemv", "group", "mx", "fp8", "traffic"],
+                    choices=["all", "headline", "quant", "w8a8", "gemv", "group", "mx", "fp8", "traffic"],
                     help="run one workload family (the JSON contract line is printed for all / headline)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -428,7 +459,7 @@ def main() -> int:
     if args.only == "traffic":
         print(json.dumps(traffic_probe(torch, ascq)))
         return 0
-    if args.only in ("w8a8", "gemv", "group", "mx", "fp8"):
+    if args.only in ("quant", "w8a8", "gemv", "group", "mx", "fp8"):
         print(json.dumps({"other_configs": run_others(torch, ascq, args.only)}))
         return 0
     h = bench_headline(torch, ascq, args.steps, args.warmup)

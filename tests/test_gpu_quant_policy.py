@@ -61,7 +61,7 @@ _LAYOUTS = [(O.PER_TOKEN, 0, 1), (O.PER_GROUP, 32, 1), (O.PER_GROUP, 64, 0)]
 
 @pytest.mark.parametrize("pair", _PAIRS)
 @pytest.mark.parametrize("layout", _LAYOUTS)
-@pytest.mark.parametrize("shape", [(75, 160), (37, 100)])  # n % 8 == 0 (vector path) and a ragged row length
+@pytest.mark.parametrize("shape", [(75, 160), (37, 96), (37, 100)])  # vector path (m % 4 of 3 and 1), ragged rows
 def test_int8(ascq_gpu, pair, layout, shape):
     st, sct = pair
     policy, g, k_dim = layout
@@ -145,13 +145,16 @@ def test_per_token_matches_fp32_entry(ascq_gpu):
 
 
 def test_full_size_group_int8_and_e2m1(ascq_gpu):
-    """[8192, 8192] f16 source, group 128 along the rows (kDim 1): int8 and E2M1 outputs against the oracle"""
+    """[8192, 8192] f16 source, groups of 128 along the rows (kDim 1; int8 and E2M1) and down the columns (kDim 0;
+    int8), against the oracle"""
     m, n, g = 8192, 8192, 128
     rng = seeded(1600)
     x = rng.standard_normal((m, n), dtype=np.float32).astype(np.float16).view(np.uint16)
     sc = _bits(rng.uniform(0.5, 40.0, (m, n // g)), O.F16)
     for dst in (O.INT8, O.FP4_E2M1):
         _check(ascq_gpu, x, O.F16, sc, O.F16, dst, O.PER_GROUP, m, n, g, None, None, 1)
+    sc0 = _bits(rng.uniform(0.5, 40.0, (m // g, n)), O.F16)  # groups of 128 rows (kDim 0)
+    _check(ascq_gpu, x, O.F16, sc0, O.F16, O.INT8, O.PER_GROUP, m, n, g, None, None, 0)
 
 
 def test_argument_checks(ascq_gpu):
