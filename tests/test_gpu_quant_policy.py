@@ -172,3 +172,20 @@ def test_argument_checks(ascq_gpu):
     with pytest.raises(ascq_gpu.AscqError):  # E2M1 rows pack two a byte
         ascq_gpu.ascend_quant_policy(torch.zeros((4, 63), dtype=torch.float16, device="cuda"), s, O.PER_GROUP,
                                      O.FP4_E2M1, 32)
+
+
+def test_conversion_sweeps(ascq_gpu):
+    """the vector kernels convert with the gfx950 instructions (fp32 -> fp8 / bf16, bf16 -> E2M1): every bf16 pattern
+    to E2M1 (rint), and 2^22 fp32 patterns spread over the whole range to fp8 e4m3 / e5m2 and to E2M1 through bf16,
+    each against the oracle"""
+    bf = np.arange(0x10000, dtype=np.uint32).astype(np.uint16).reshape(256, 256)
+    one_b = _bits(np.ones((256, 256 // 32)), O.BF16)
+    _check(ascq_gpu, bf, O.BF16, one_b, O.BF16, O.FP4_E2M1, O.PER_GROUP, 256, 256, 32, None, None, 1)
+    rng = seeded(1700)
+    f = (np.arange(1 << 22, dtype=np.uint64) * 1021 + rng.integers(0, 1021, 1 << 22)).astype(np.uint32)
+    f = f.view(np.float32).reshape(2048, 2048)
+    one_f = np.ones(2048, np.float32)
+    for fmt in (O.FP8_E4M3, O.FP8_E5M2):
+        _check(ascq_gpu, f, O.F32, one_f, O.F32, fmt, O.PER_TOKEN, 2048, 2048)
+    one_g = np.ones((2048, 2048 // 32), np.float32)
+    _check(ascq_gpu, f, O.F32, one_g, O.F32, O.FP4_E2M1, O.PER_GROUP, 2048, 2048, 32, None, None, 1)
