@@ -38,11 +38,12 @@ __global__ __launch_bounds__(256) void quant_dyn_row_kernel(const u32x4* __restr
     u32x4 v[VEC];
     float amax = 0.0f;
     h2 hmax = {(_Float16)0.0f, (_Float16)0.0f};
+    // every lane loads VEC chunks unconditionally (a chunk past the row end repeats the row's last chunk: the
+    // absmax is unchanged and it is not stored), so all VEC loads are in flight before the first wait
 #pragma unroll
     for (int j = 0; j < VEC; ++j) {
-        uint32_t c = t + j * 256u;
-        if (c < chunks) v[j] = __builtin_nontemporal_load(xr + c);
-        else v[j] = (u32x4){0u, 0u, 0u, 0u};
+        const uint32_t c = t + j * 256u;
+        v[j] = __builtin_nontemporal_load(xr + (c < chunks ? c : chunks - 1u));
     }
 #pragma unroll
     for (int j = 0; j < VEC; ++j) {
@@ -342,7 +343,10 @@ hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, 
     const bool fast = policy == 2 && src_type == DT_INT8 && dst_type == DT_F16 && scale_type == DT_F32 &&
                       n % 8 == 0 && ((uintptr_t)src % 8 == 0) && ((uintptr_t)y % 16 == 0) && m > 0 && n > 0;
     if (fast) {
-        constexpr int U = 2;  // measured best at 8192 x 8192 (U = 1: 37.6 us, 2: 33.7 us, 4: 34.6 us)
+        // measured at 8192 x 8192: U = 1 37.6 us, 2 33.7 us, 4 34.6 us; 16-element units (one 16-byte load, two
+        // 16-byte stores per lane) 34.9 us at U = 1 and slower above, as each store instruction then covers every
+        // other 16 bytes of its span
+        constexpr int U = 2;
         const uint32_t upr = n / 8;
         const uint32_t segs = (upr + 256 * U - 1) / (256 * U);
         const uint64_t blocks = (uint64_t)m * segs;
