@@ -684,8 +684,11 @@ ascq_status ascq_ascend_quant_per_token(int8_t* dst, const void* src, int32_t sr
     if (para->has_offset && !offset) return fail(ASCQ_E_INVALID_ARG, "quant_per_token: has_offset needs an offset tensor");
     const uint32_t m = para->cal_count / para->n;
     if (m == 0) return ASCQ_OK;
-    return hip_status(ascq::launch_quant_per_token(dst, src, src_type, scale, para->has_offset ? offset : nullptr, m,
-                                                   para->n, para->round_mode, S(stream)),
+    // the PER_TOKEN policy form with an f32 scale computes exactly this (f32 product and offset, round mode,
+    // saturation), through the vectorised policy kernels
+    return hip_status(ascq::launch_quant_policy(dst, ASCQ_DT_INT8, src, src_type, scale, ASCQ_DT_F32, offset,
+                                                para->has_offset ? 1 : 0, 0.0f, 1, m, para->n, 0, 1, para->round_mode,
+                                                S(stream)),
                       "quant_per_token");
 }
 

@@ -31,8 +31,6 @@ inline void launch_k(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t 
 // quant.hip
 hipError_t launch_quant_dynamic_per_token(int8_t* q, float* scale_out, const void* x, int src_type, uint32_t m,
                                           uint32_t n, int round_mode, hipStream_t st);
-hipError_t launch_quant_per_token(int8_t* q, const void* x, int src_type, const float* scale, const float* offset,
-                                  uint32_t m, uint32_t n, int round_mode, hipStream_t st);
 hipError_t launch_quant_legacy(int8_t* q, const void* x, int src_type, const uint16_t* scale, const uint16_t* offset,
                                uint16_t scale_scalar, uint16_t offset_scalar, uint32_t cal_count,
                                uint32_t scale_count, hipStream_t st);

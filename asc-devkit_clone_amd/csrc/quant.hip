@@ -107,23 +107,6 @@ __global__ __launch_bounds__(256) void quant_dyn_generic_kernel(const void* __re
 }
 
 // ---------------------------------------------------------------------------------------------
-// Per-token quant with given fp32 scale / offset (policy API PER_TOKEN).
-// ---------------------------------------------------------------------------------------------
-template <int MODE, bool HAS_OFFSET>
-__global__ __launch_bounds__(256) void quant_per_token_kernel(const void* __restrict__ x, int8_t* __restrict__ q,
-                                                              const float* __restrict__ scale,
-                                                              const float* __restrict__ offset, int64_t total,
-                                                              uint32_t n, int src_type)
-{
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-        int64_t row = i / n;
-        float v = load_f32_of(x, i, src_type) * scale[row];
-        if constexpr (HAS_OFFSET) v = v + offset[row];
-        q[i] = (int8_t)quant_s8<MODE>(v);
-    }
-}
-
-// ---------------------------------------------------------------------------------------------
 // Legacy AscendQuant: half arithmetic.  t = half(x); t = t*s; t = t+o; q = sat_s8(rint(t)).
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void quant_legacy_f16_kernel(const void* __restrict__ x, int8_t* __restrict__ q,
@@ -305,28 +288,6 @@ hipError_t launch_quant_dynamic_per_token(int8_t* q, float* scale_out, const voi
     return hipGetLastError();
 }
 
-hipError_t launch_quant_per_token(int8_t* q, const void* x, int src_type, const float* scale, const float* offset,
-                                  uint32_t m, uint32_t n, int round_mode, hipStream_t st)
-{
-    int64_t total = (int64_t)m * n;
-    dim3 grid(grid_for(total)), block(256);
-#define ASCQ_PT(MD)                                                                                                 \
-    if (offset) launch_k((quant_per_token_kernel<MD, true>), grid, block, 0, st, x, q, scale, offset,     \
-                                   total, n, src_type);                                                             \
-    else launch_k((quant_per_token_kernel<MD, false>), grid, block, 0, st, x, q, scale, offset, total, n, \
-                            src_type);                                                                              \
-    break;
-    switch (round_mode) {
-    case RM_FLOOR: ASCQ_PT(RM_FLOOR)
-    case RM_CEIL: ASCQ_PT(RM_CEIL)
-    case RM_ROUND: ASCQ_PT(RM_ROUND)
-    case RM_TRUNC: ASCQ_PT(RM_TRUNC)
-    default: ASCQ_PT(RM_RINT)
-    }
-#undef ASCQ_PT
-    return hipGetLastError();
-}
-
 hipError_t launch_quant_legacy(int8_t* q, const void* x, int src_type, const uint16_t* scale, const uint16_t* offset,
                                uint16_t scale_scalar, uint16_t offset_scalar, uint32_t cal_count,
                                uint32_t scale_count, hipStream_t st)
@@ -384,55 +345,6 @@ __device__ __forceinline__ float load_scale_t(const void* p, int t, int64_t i)
     return ((const float*)p)[i];
 }
 
-__global__ __launch_bounds__(256) void antiquant_policy_kernel(void* __restrict__ dst, int dst_type,
-                                                               const void* __restrict__ src, int src_type,
-                                                               const void* __restrict__ scale,
-                                                               const void* __restrict__ offset, int scale_type,
-                                                               int per_token, int64_t m, int64_t n, int64_t g,
-                                                               int col_groups, int is_transpose)
-{
-    const int64_t total = m * n, sk = g > 0 ? (n + g - 1) / g : 1;
-    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
-        const int64_t r = idx / n, c = idx % n;
-        const int64_t sidx = per_token ? (is_transpose ? c : r) : (col_groups ? r * sk + c / g : (r / g) * n + c);
-        if (src_type == DT_FP4_E2M1) {  // E8M0 scale, bf16 product, no offset
-            const uint32_t b = ((const uint8_t*)src)[idx >> 1];
-            const float v = e2m1_to_f32((idx & 1) ? (b >> 4) : (b & 0xFu));
-            const uint32_t e = ((const uint8_t*)scale)[sidx];
-            const float sc = e == 255u ? __uint_as_float(0x7fffffffu) : (e == 0u ? __uint_as_float(0x00400000u)
-                                                                                 : __uint_as_float(e << 23));
-            const float p = bf16_round(v * sc);
-            if (dst_type == DT_F16) ((uint16_t*)dst)[idx] = f32_to_f16_sat(p);
-            else ((uint16_t*)dst)[idx] = (uint16_t)(__float_as_uint(p) >> 16);
-            continue;
-        }
-        const float s = load_scale_t(scale, scale_type, sidx);
-        const float o = offset ? load_scale_t(offset, scale_type, sidx) : 0.0f;
-        if (src_type == DT_FP8_E4M3 || src_type == DT_FP8_E5M2) {  // fp32 arithmetic
-            float v = fp8_bits_to_f32(((const uint8_t*)src)[idx], src_type == DT_FP8_E5M2);
-            if (offset) v = v + o;
-            v = v * s;
-            store_cast(dst, idx, v, dst_type);
-            continue;
-        }
-        float v = (float)((const int8_t*)src)[idx];  // arithmetic in the scale type
-        if (offset) v = round_scale_t(v + o, scale_type);
-        v = round_scale_t(v * s, scale_type);
-        if (scale_type == DT_F16) ((uint16_t*)dst)[idx] = f32_to_f16(v);
-        else if (scale_type == DT_BF16) ((uint16_t*)dst)[idx] = (uint16_t)(__float_as_uint(v) >> 16);
-        else store_cast(dst, idx, v, dst_type);
-    }
-}
-
-hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale,
-                                   const void* offset, int scale_type, int per_token, int64_t m, int64_t n,
-                                   int64_t g, int col_groups, int is_transpose, hipStream_t st)
-{
-    dim3 grid(grid_for(m * n)), block(256);
-    launch_k(antiquant_policy_kernel, grid, block, 0, st, dst, dst_type, src, src_type, scale, offset, scale_type,
-             per_token, m, n, g, col_groups, is_transpose);
-    return hipGetLastError();
-}
 
 // ---------------------------------------------------------------------------------------------
 // AscendQuant policy form (arch 3510, ascend_quant_per_group_3510_impl.h:33-1340, dispatch :1451-1504):
@@ -905,6 +817,297 @@ hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src
         else if (t == DT_BF16) launch_qp<QD_E2M1, DT_BF16>(a, vec, st);
         else launch_qp<QD_E2M1, DT_F32>(a, vec, st);
     }
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void antiquant_policy_kernel(void* __restrict__ dst, int dst_type,
+                                                               const void* __restrict__ src, int src_type,
+                                                               const void* __restrict__ scale,
+                                                               const void* __restrict__ offset, int scale_type,
+                                                               int per_token, int64_t m, int64_t n, int64_t g,
+                                                               int col_groups, int is_transpose)
+{
+    const int64_t total = m * n, sk = g > 0 ? (n + g - 1) / g : 1;
+    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+        const int64_t r = idx / n, c = idx % n;
+        const int64_t sidx = per_token ? (is_transpose ? c : r) : (col_groups ? r * sk + c / g : (r / g) * n + c);
+        if (src_type == DT_FP4_E2M1) {  // E8M0 scale, bf16 product, no offset
+            const uint32_t b = ((const uint8_t*)src)[idx >> 1];
+            const float v = e2m1_to_f32((idx & 1) ? (b >> 4) : (b & 0xFu));
+            const uint32_t e = ((const uint8_t*)scale)[sidx];
+            const float sc = e == 255u ? __uint_as_float(0x7fffffffu) : (e == 0u ? __uint_as_float(0x00400000u)
+                                                                                 : __uint_as_float(e << 23));
+            const float p = bf16_round(v * sc);
+            if (dst_type == DT_F16) ((uint16_t*)dst)[idx] = f32_to_f16_sat(p);
+            else ((uint16_t*)dst)[idx] = (uint16_t)(__float_as_uint(p) >> 16);
+            continue;
+        }
+        const float s = load_scale_t(scale, scale_type, sidx);
+        const float o = offset ? load_scale_t(offset, scale_type, sidx) : 0.0f;
+        if (src_type == DT_FP8_E4M3 || src_type == DT_FP8_E5M2) {  // fp32 arithmetic
+            float v = fp8_bits_to_f32(((const uint8_t*)src)[idx], src_type == DT_FP8_E5M2);
+            if (offset) v = v + o;
+            v = v * s;
+            store_cast(dst, idx, v, dst_type);
+            continue;
+        }
+        float v = (float)((const int8_t*)src)[idx];  // arithmetic in the scale type
+        if (offset) v = round_scale_t(v + o, scale_type);
+        v = round_scale_t(v * s, scale_type);
+        if (scale_type == DT_F16) ((uint16_t*)dst)[idx] = f32_to_f16(v);
+        else if (scale_type == DT_BF16) ((uint16_t*)dst)[idx] = (uint16_t)(__float_as_uint(v) >> 16);
+        else store_cast(dst, idx, v, dst_type);
+    }
+}
+
+// Vector path of the policy form (n % 8 == 0, aligned pointers, fewer than 2^31 units): a unit is 8 consecutive
+// elements of one row; each lane issues all loads of its units -- source (8 bytes; 4 for fp4), scale and offset,
+// unconditionally with clamped indices, the scale table standing in for a missing offset -- before converting any.
+// Scales: one per unit at r * sk + c / g (groups along the row; PER_TOKEN is sk = 1, g = n) or 8 contiguous at
+// (r / g) * n + c (groups down the columns; transposed PER_TOKEN is g = m).  Stores: 16 bytes (f16 / bf16) or 32
+// (f32) per unit.
+constexpr int AQ_UNR = 4;
+struct AntiQuantVecArgs {
+    void* dst;
+    const void* src;
+    const void* scale;
+    const void* offset;  // or null
+    int64_t n, sk;
+    uint32_t rows, units, upr;  // units: m * n / 8 (the row-blocked kernel recomputes its own)
+    FastDiv upr_div, g_div;
+};
+
+// SRC: DT_INT8, DT_FP8_E4M3, DT_FP8_E5M2 or DT_FP4_E2M1; SC: scale type (E8M0 for fp4); DST: output type.
+// One unit: source words xw (8 int8 / fp8 codes in two words, or 8 E2M1 nibbles in xw0), scale / offset bits
+// (EIGHT: 8 per unit packed like the table; else one).
+template <int SRC, int SC, int DST, bool EIGHT>
+__device__ __forceinline__ void aq_unit(const AntiQuantVecArgs& a, uint32_t u, uint32_t xw0, uint32_t xw1,
+                                        const uint32_t* sw, const uint32_t* ow, bool has_off)
+{
+    constexpr bool FP4 = SRC == DT_FP4_E2M1, FP8 = SRC == DT_FP8_E4M3 || SRC == DT_FP8_E5M2;
+    constexpr int SB = SC == DT_F32 ? 4 : (SC == DT_E8M0 ? 1 : 2);
+    float y[8];
+    if constexpr (FP4) {
+        // E2M1 codes through the gfx950 decode with scale 1 (exact), then the E8M0 scale in fp32 and one bf16 rounding
+        float e[8];
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        const f2 d0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(xw0, 1.0f, 0);
+        const f2 d1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(xw0, 1.0f, 1);
+        const f2 d2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(xw0, 1.0f, 2);
+        const f2 d3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(xw0, 1.0f, 3);
+        e[0] = d0.x, e[1] = d0.y, e[2] = d1.x, e[3] = d1.y, e[4] = d2.x, e[5] = d2.y, e[6] = d3.x, e[7] = d3.y;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t sb = EIGHT ? (sw[j >> 2] >> (8 * (j & 3))) & 0xffu : sw[0];
+            const float sc = sb == 255u ? __uint_as_float(0x7fffffffu)
+                                        : (sb == 0u ? __uint_as_float(0x00400000u) : __uint_as_float(sb << 23));
+            y[j] = bf16_round(e[j] * sc);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t sb, ob;
+            if constexpr (EIGHT && SB == 4) sb = sw[j], ob = ow[j];
+            else if constexpr (EIGHT) sb = (sw[j >> 1] >> (16 * (j & 1))) & 0xffffu, ob = (ow[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+            else sb = sw[0], ob = ow[0];
+            const float s = raw_to_f32<SC>(sb), o = raw_to_f32<SC>(ob);
+            const uint32_t code = ((j < 4 ? xw0 : xw1) >> (8 * (j & 3))) & 0xffu;
+            if constexpr (FP8) {  // fp32 arithmetic
+                float v = fp8_bits_to_f32(code, SRC == DT_FP8_E5M2);
+                if (has_off) v = v + o;
+                y[j] = v * s;
+            } else {  // int8: arithmetic in the scale type
+                float v = (float)(int8_t)code;
+                if (has_off) v = rnd_t<SC>(v + o);
+                y[j] = rnd_t<SC>(v * s);
+            }
+        }
+    }
+    if constexpr (DST == DT_F32) {
+        u32x4* d = (u32x4*)a.dst + 2 * (int64_t)u;
+        __builtin_nontemporal_store((u32x4){__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]),
+                                            __float_as_uint(y[3])}, d);
+        __builtin_nontemporal_store((u32x4){__float_as_uint(y[4]), __float_as_uint(y[5]), __float_as_uint(y[6]),
+                                            __float_as_uint(y[7])}, d + 1);
+        return;
+    }
+    uint32_t h[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t lo, hi;
+        if constexpr (DST == DT_BF16) {
+            if constexpr (FP4 || (!FP8 && SC == DT_BF16))  // already bf16 values
+                lo = __float_as_uint(y[2 * q]) >> 16, hi = __float_as_uint(y[2 * q + 1]) >> 16;
+            else
+                lo = f32_to_bf16_sat(y[2 * q]), hi = f32_to_bf16_sat(y[2 * q + 1]);
+        } else {
+            if constexpr (!FP4 && !FP8 && SC == DT_F16)  // half arithmetic: already half values (inf kept)
+                lo = f32_to_f16(y[2 * q]), hi = f32_to_f16(y[2 * q + 1]);
+            else
+                lo = f32_to_f16_sat(y[2 * q]), hi = f32_to_f16_sat(y[2 * q + 1]);
+        }
+        h[q] = lo | (hi << 16);
+    }
+    __builtin_nontemporal_store((u32x4){h[0], h[1], h[2], h[3]}, (u32x4*)a.dst + u);
+}
+
+template <int SRC>
+__device__ __forceinline__ void aq_load_src(const void* src, uint32_t u, uint32_t& w0, uint32_t& w1)
+{
+    if constexpr (SRC == DT_FP4_E2M1) {
+        w0 = __builtin_nontemporal_load((const uint32_t*)src + u), w1 = 0u;
+    } else {
+        const u32x2 x = __builtin_nontemporal_load((const u32x2*)src + u);
+        w0 = x.x, w1 = x.y;
+    }
+}
+
+// 8 scale (or offset) entries from element index si (a multiple of 8) into w, packed as in memory
+template <int SB>
+__device__ __forceinline__ void aq_load8(const void* p, int64_t si, uint32_t* w)
+{
+    if constexpr (SB == 4) {
+        const u32x4* q = (const u32x4*)((const float*)p + si);
+        const u32x4 a = q[0], b = q[1];
+        w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w, w[4] = b.x, w[5] = b.y, w[6] = b.z, w[7] = b.w;
+    } else if constexpr (SB == 2) {
+        const u32x4 a = *(const u32x4*)((const uint16_t*)p + si);
+        w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w;
+    } else {
+        const u32x2 a = *(const u32x2*)((const uint8_t*)p + si);
+        w[0] = a.x, w[1] = a.y;
+    }
+}
+
+// one scale per unit (groups along the row; PER_TOKEN by row): AQ_UNR * 256 consecutive units per workgroup pass
+template <int SRC, int SC, int DST>
+__global__ __launch_bounds__(256) void antiquant_policy_vec_kernel(AntiQuantVecArgs a)
+{
+    constexpr int SB = SC == DT_F32 ? 4 : (SC == DT_E8M0 ? 1 : 2);
+    const bool has_off = a.offset != nullptr;
+    const void* offp = has_off ? a.offset : a.scale;
+    for (uint32_t b0 = blockIdx.x * (256u * AQ_UNR); b0 < a.units; b0 += gridDim.x * (256u * AQ_UNR)) {
+        uint32_t x0[AQ_UNR], x1[AQ_UNR], sw[AQ_UNR], ow[AQ_UNR];
+#pragma unroll
+        for (int k = 0; k < AQ_UNR; ++k) {
+            uint32_t u = b0 + k * 256u + threadIdx.x;
+            u = u < a.units ? u : a.units - 1u;  // past the end: load a valid unit, store nothing
+            aq_load_src<SRC>(a.src, u, x0[k], x1[k]);
+            const uint32_t r = fdiv(u, a.upr_div), c = (u - r * a.upr) * 8u;
+            const int64_t si = (int64_t)r * a.sk + fdiv(c, a.g_div);
+            if constexpr (SB == 4) sw[k] = ((const uint32_t*)a.scale)[si], ow[k] = ((const uint32_t*)offp)[si];
+            else if constexpr (SB == 2) sw[k] = ((const uint16_t*)a.scale)[si], ow[k] = ((const uint16_t*)offp)[si];
+            else sw[k] = ((const uint8_t*)a.scale)[si], ow[k] = 0u;
+        }
+#pragma unroll
+        for (int k = 0; k < AQ_UNR; ++k) {
+            const uint32_t u = b0 + k * 256u + threadIdx.x;
+            if (u >= a.units) break;
+            aq_unit<SRC, SC, DST, false>(a, u, x0[k], x1[k], &sw[k], &ow[k], has_off);
+        }
+    }
+}
+
+// 8 scales per unit (groups down the columns; PER_TOKEN by column): a lane takes the same 8 columns of AQ_UNR
+// consecutive rows (AQ_UNR divides every group size), so one load of 8 scales and offsets serves all of them;
+// units: row blocks x (n / 8)
+template <int SRC, int SC, int DST>
+__global__ __launch_bounds__(256) void antiquant_policy_vec_krow_kernel(AntiQuantVecArgs a)
+{
+    constexpr int SB = SC == DT_F32 ? 4 : (SC == DT_E8M0 ? 1 : 2);
+    constexpr int SW = (8 * SB + 3) / 4;
+    const bool has_off = a.offset != nullptr;
+    const void* offp = has_off ? a.offset : a.scale;
+    const uint32_t rows = a.rows;
+    for (uint32_t v = blockIdx.x * 256u + threadIdx.x; v < a.units; v += gridDim.x * 256u) {
+        const uint32_t rb = fdiv(v, a.upr_div), wu = v - rb * a.upr, r0 = rb * AQ_UNR;
+        const int64_t si = (int64_t)fdiv(r0, a.g_div) * a.n + 8 * (int64_t)wu;
+        uint32_t sw[SW], ow[SW], x0[AQ_UNR], x1[AQ_UNR];
+        aq_load8<SB>(a.scale, si, sw);
+        if constexpr (SB != 1) aq_load8<SB>(offp, si, ow);
+#pragma unroll
+        for (int k = 0; k < AQ_UNR; ++k) {
+            const uint32_t r = r0 + k < rows ? r0 + k : rows - 1u;
+            aq_load_src<SRC>(a.src, r * a.upr + wu, x0[k], x1[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < AQ_UNR; ++k) {
+            if (r0 + k >= rows) break;
+            aq_unit<SRC, SC, DST, true>(a, (r0 + k) * a.upr + wu, x0[k], x1[k], sw, ow, has_off);
+        }
+    }
+}
+
+template <int SRC, int SC, int DST>
+static void launch_aq_vec(const AntiQuantVecArgs& a, bool eight, hipStream_t st)
+{
+    if (eight) {
+        AntiQuantVecArgs b = a;
+        b.units = (a.rows + AQ_UNR - 1) / AQ_UNR * a.upr;
+        launch_k(antiquant_policy_vec_krow_kernel<SRC, SC, DST>, dim3(grid_for(b.units)), dim3(256), 0, st, b);
+    } else {
+        launch_k(antiquant_policy_vec_kernel<SRC, SC, DST>, dim3(grid_for((a.units + AQ_UNR - 1) / AQ_UNR)),
+                 dim3(256), 0, st, a);
+    }
+}
+
+template <int SRC, int SC>
+static void launch_aq_dst(const AntiQuantVecArgs& a, int dst_type, bool eight, hipStream_t st)
+{
+    if (dst_type == DT_F16) launch_aq_vec<SRC, SC, DT_F16>(a, eight, st);
+    else if (dst_type == DT_BF16) launch_aq_vec<SRC, SC, DT_BF16>(a, eight, st);
+    else if constexpr (SRC != DT_FP4_E2M1) launch_aq_vec<SRC, SC, DT_F32>(a, eight, st);
+}
+
+template <int SRC>
+static void launch_aq_scale(const AntiQuantVecArgs& a, int dst_type, int scale_type, bool eight, hipStream_t st)
+{
+    if constexpr (SRC == DT_FP4_E2M1) {
+        launch_aq_dst<SRC, DT_E8M0>(a, dst_type, eight, st);
+    } else if constexpr (SRC == DT_INT8) {  // a 16-bit scale writes its own type
+        if (scale_type == DT_F16) launch_aq_vec<SRC, DT_F16, DT_F16>(a, eight, st);
+        else if (scale_type == DT_BF16) launch_aq_vec<SRC, DT_BF16, DT_BF16>(a, eight, st);
+        else launch_aq_dst<SRC, DT_F32>(a, dst_type, eight, st);
+    } else {
+        if (scale_type == DT_F16) launch_aq_dst<SRC, DT_F16>(a, dst_type, eight, st);
+        else if (scale_type == DT_BF16) launch_aq_dst<SRC, DT_BF16>(a, dst_type, eight, st);
+        else launch_aq_dst<SRC, DT_F32>(a, dst_type, eight, st);
+    }
+}
+
+hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale,
+                                   const void* offset, int scale_type, int per_token, int64_t m, int64_t n,
+                                   int64_t g, int col_groups, int is_transpose, hipStream_t st)
+{
+    // one scale per unit (groups along the row, PER_TOKEN by row) or 8 contiguous (groups down the columns,
+    // PER_TOKEN by column); for the vector path the per-token cases become groups of n columns / m rows
+    const bool eight = per_token ? is_transpose != 0 : !col_groups;
+    const int64_t gv = per_token ? (is_transpose ? m : n) : g;
+    const int sbytes = scale_type == DT_F32 ? 4 : (scale_type == DT_E8M0 ? 1 : 2);
+    const bool al = (uintptr_t)src % 8 == 0 && (uintptr_t)dst % 16 == 0 &&
+                    (!eight || ((uintptr_t)scale % (8 * sbytes) == 0 && (uintptr_t)offset % (8 * sbytes) == 0));
+    if (n % 8 == 0 && al && m * n / 8 < (1ll << 31) && gv > 0 && gv < (1ll << 31) && n < (1ll << 31)) {
+        AntiQuantVecArgs a;
+        a.dst = dst;
+        a.src = src;
+        a.scale = scale;
+        a.offset = offset;
+        a.n = n;
+        a.sk = per_token ? 1 : (n + g - 1) / g;
+        a.rows = (uint32_t)m;
+        a.units = (uint32_t)(m * n / 8);
+        a.upr = (uint32_t)(n / 8);
+        a.upr_div = fast_div(a.upr);
+        a.g_div = fast_div((uint32_t)gv);
+        if (src_type == DT_INT8) launch_aq_scale<DT_INT8>(a, dst_type, scale_type, eight, st);
+        else if (src_type == DT_FP8_E4M3) launch_aq_scale<DT_FP8_E4M3>(a, dst_type, scale_type, eight, st);
+        else if (src_type == DT_FP8_E5M2) launch_aq_scale<DT_FP8_E5M2>(a, dst_type, scale_type, eight, st);
+        else launch_aq_scale<DT_FP4_E2M1>(a, dst_type, scale_type, eight, st);
+        return hipGetLastError();
+    }
+    dim3 grid(grid_for(m * n)), block(256);
+    launch_k(antiquant_policy_kernel, grid, block, 0, st, dst, dst_type, src, src_type, scale, offset, scale_type,
+             per_token, m, n, g, col_groups, is_transpose);
     return hipGetLastError();
 }
 

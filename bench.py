@@ -408,8 +408,41 @@ def bench_quant_policy(torch, ascq, dst_type, policy, iters, k_dim=1, g=128):
                 frac_of_peak=gbs / HBM_PEAK_GBS)
 
 
+def bench_antiquant_policy(torch, ascq, src_type, iters):
+    """AscendAntiQuant policy form to an f16 / bf16 [8192, 8192] output: int8 with f16 scales and offsets in groups of
+    128 rows (kDim 0), or fp4 E2M1 with E8M0 scales in groups of 32 along the rows"""
+    M = N = 8192
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(6)
+    if src_type == ascq.FP4_E2M1:
+        g, sb, ss = 32, M * N // 2, (M, N // 32)
+        sc = torch.randint(110, 140, ss, generator=gen, device="cuda", dtype=torch.int32).to(torch.uint8)
+        of, st, kd, dt, name = None, ascq.E8M0, 1, torch.bfloat16, "fp4 E2M1 (E8M0 scales, g=32 kDim=1) -> bf16"
+        nbytes = sb + M * N // 32 + 2 * M * N
+    else:
+        g, sb, ss = 128, M * N, (M // 128, N)
+        sc = torch.empty(ss, device="cuda").uniform_(0.01, 1.0, generator=gen).half()
+        of = torch.empty(ss, device="cuda").uniform_(-4.0, 4.0, generator=gen).half()
+        st, kd, dt, name = ascq.F16, 0, torch.float16, "int8 (f16 scale + offset, g=128 kDim=0) -> f16"
+        nbytes = sb + 4 * (M // 128) * N + 2 * M * N
+    R = rotation(nbytes)
+    srcs = [torch.randint(0, 256, (sb,), generator=gen, device="cuda", dtype=torch.int32).to(torch.uint8)
+            for _ in range(R)]
+    ys = [torch.empty((M, N), dtype=dt, device="cuda") for _ in range(R)]
+
+    def fn(i):
+        ascq.ascend_antiquant_policy(srcs[i % R], src_type, sc, st, ascq.PER_GROUP, M, N, g, of, kd, False, dt,
+                                     out=ys[i % R])
+
+    ms = _time_loop(torch, fn, iters)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(workload=f"AscendAntiQuant PER_GROUP [{M},{N}] {name}", ms=ms, value=gbs, unit="GB/s",
+                frac_of_peak=gbs / HBM_PEAK_GBS)
+
+
 OTHER = {
-    "quant": [lambda t, a: bench_quant_policy(t, a, a.INT8, a.PER_GROUP, 50),
+    "quant": [lambda t, a: bench_antiquant_policy(t, a, a.INT8, 50),
+              lambda t, a: bench_antiquant_policy(t, a, a.FP4_E2M1, 50),lambda t, a: bench_quant_policy(t, a, a.INT8, a.PER_GROUP, 50),
               lambda t, a: bench_quant_policy(t, a, a.INT8, a.PER_GROUP, 50, k_dim=0),
               lambda t, a: bench_quant_policy(t, a, a.FP8_E4M3, a.PER_TOKEN, 50),
               lambda t, a: bench_quant_policy(t, a, a.FP4_E2M1, a.PER_GROUP, 50)],

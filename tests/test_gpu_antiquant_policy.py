@@ -112,3 +112,45 @@ def test_argument_checks(ascq_gpu):
     with pytest.raises(ascq_gpu.AscqError):  # fp4 takes no offset
         ascq_gpu.ascend_antiquant_policy(q, O.FP4_E2M1, q, O.E8M0, O.PER_GROUP, 4, 64, 32, offset=s,
                                          dst_dtype=torch.bfloat16)
+
+
+@pytest.mark.parametrize("src_type", [O.INT8, O.FP8_E5M2, O.FP4_E2M1])
+def test_ragged_rows_and_unaligned(ascq_gpu, src_type):
+    """n % 8 != 0, or a destination off a 16-byte boundary, takes the per-element kernel"""
+    m, n, g = 21, 98, 32
+    rng = seeded(91 + src_type)
+    if src_type == O.FP4_E2M1:
+        src = rng.integers(0, 256, (m, n // 2)).astype(np.uint8)
+        sc, sct, of, dt, k_dim = rng.integers(110, 140, (m, (n + g - 1) // g)).astype(np.uint8), O.E8M0, None, O.BF16, 1
+    else:
+        src = rng.integers(-128 if src_type == O.INT8 else 0, 128 if src_type == O.INT8 else 256, (m, n))
+        src = src.astype(np.int8 if src_type == O.INT8 else np.uint8)
+        sct, dt, k_dim = O.F16, O.F16, 0
+        sc, of = _scales(rng, ((m + g - 1) // g, n), sct)
+    got = _run(ascq_gpu, src, src_type, sc, sct, dt, O.PER_GROUP, m, n, g, of, k_dim)
+    exp = O.antiquant_policy(src, src_type, sc, sct, dt, O.PER_GROUP, m, n, g, of, k_dim)
+    assert _same(got, exp, dt)
+    if src_type == O.INT8:  # n % 8 == 0 but the output one element off alignment
+        n2 = 96
+        src2 = np.ascontiguousarray(src[:, :n2])
+        sc2, of2 = _scales(rng, ((m + g - 1) // g, n2), sct)
+        yd = torch.empty(m * n2 + 1, dtype=torch.float16, device="cuda")
+        y = yd[1:].view(m, n2)
+        ascq_gpu.ascend_antiquant_policy(_dev(src2), src_type, _dev(sc2), sct, O.PER_GROUP, m, n2, g, _dev(of2), k_dim,
+                                         False, torch.float16, out=y)
+        torch.cuda.synchronize()
+        exp2 = O.antiquant_policy(src2, src_type, sc2, sct, dt, O.PER_GROUP, m, n2, g, of2, k_dim)
+        assert _same(y.cpu().view(torch.int16).numpy().view(np.uint16), exp2, dt)
+
+
+@pytest.mark.parametrize("dst_type", [O.BF16, O.F16])
+def test_fp4_every_byte_every_position(ascq_gpu, dst_type):
+    """every byte value (two E2M1 codes) in each of the four byte positions of a 32-bit source word, under scales
+    2^0, 2^-127 (e = 0), 2^127 and NaN (e = 255)"""
+    m, n, g = 4, 2048, 32
+    b = np.arange(256, dtype=np.uint8)
+    packed = np.stack([np.roll(np.repeat(b, 4), p) for p in range(m)]).astype(np.uint8)  # [4, 1024] bytes
+    e = np.tile(np.array([127, 0, 254, 255], np.uint8), (m, n // g // 4))
+    got = _run(ascq_gpu, packed, O.FP4_E2M1, e, O.E8M0, dst_type, O.PER_GROUP, m, n, g, None, 1)
+    exp = O.antiquant_policy(packed, O.FP4_E2M1, e, O.E8M0, dst_type, O.PER_GROUP, m, n, g, None, 1)
+    assert _same(got, exp, dst_type)
