@@ -145,9 +145,9 @@ __global__ __launch_bounds__(256) void dequant_i8_token_f16_kernel(const u32x2* 
     const float s = scale[row];
     u32x2 v[U];
 #pragma unroll
-    for (int k = 0; k < U; ++k) {
+    for (int k = 0; k < U; ++k) {  // unconditional (past the row end: the row's last unit, not stored)
         const uint32_t u = u0 + k * 256u;
-        v[k] = u < units_per_row ? __builtin_nontemporal_load(q + base + u) : (u32x2){0u, 0u};
+        v[k] = __builtin_nontemporal_load(q + base + (u < units_per_row ? u : units_per_row - 1u));
     }
 #pragma unroll
     for (int k = 0; k < U; ++k) {
@@ -304,9 +304,9 @@ hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, 
     const bool fast = policy == 2 && src_type == DT_INT8 && dst_type == DT_F16 && scale_type == DT_F32 &&
                       n % 8 == 0 && ((uintptr_t)src % 8 == 0) && ((uintptr_t)y % 16 == 0) && m > 0 && n > 0;
     if (fast) {
-        // measured at 8192 x 8192: U = 1 37.6 us, 2 33.7 us, 4 34.6 us; 16-element units (one 16-byte load, two
-        // 16-byte stores per lane) 34.9 us at U = 1 and slower above, as each store instruction then covers every
-        // other 16 bytes of its span
+        // measured at 8192 x 8192: U = 1 34.9 us, 2 34.1 us, 4 36.1 us (unconditional loads); 16-element units (one
+        // 16-byte load, two 16-byte stores per lane) 34.9 us at U = 1 and slower above, as each store instruction
+        // then covers every other 16 bytes of its span
         constexpr int U = 2;
         const uint32_t upr = n / 8;
         const uint32_t segs = (upr + 256 * U - 1) / (256 * U);
