@@ -456,26 +456,6 @@ __device__ __forceinline__ uint32_t quant_code_rt(float v, int mode)
     }
 }
 
-__device__ __forceinline__ void load8_f32(const void* p, int t, int64_t i, float (&o)[8])
-{
-    if (t == DT_F32) {
-        const u32x4 a = __builtin_nontemporal_load((const u32x4*)((const float*)p + i));
-        const u32x4 b = __builtin_nontemporal_load((const u32x4*)((const float*)p + i) + 1);
-        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = __uint_as_float(w[j]);
-        return;
-    }
-    const u32x4 a = __builtin_nontemporal_load((const u32x4*)((const uint16_t*)p + i));
-    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-    const bool bf = t == DT_BF16;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        o[2 * j] = bf ? __uint_as_float(w[j] << 16) : f16_to_f32((uint16_t)(w[j] & 0xffffu));
-        o[2 * j + 1] = bf ? __uint_as_float(w[j] & 0xffff0000u) : f16_to_f32((uint16_t)(w[j] >> 16));
-    }
-}
-
 // 8 elements of a 16- or 32-bit float type as raw 32-bit words (f16 / bf16: 4 words, f32: 8) and their values
 template <int TY>
 struct Raw8 {
