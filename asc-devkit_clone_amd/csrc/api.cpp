@@ -696,7 +696,7 @@ ascq_status ascq_ascend_quant_policy(void* dst, int32_t dst_type, const void* sr
                                      const void* scale, const void* offset, float offset_scalar, int32_t scale_type,
                                      int32_t policy, const ascq_quant_param* para, void* stream)
 {
-    if (!dst || !src || !scale || !para) return fail(ASCQ_E_INVALID_ARG, "ascend_quant_policy: null argument");
+    if (!para) return fail(ASCQ_E_INVALID_ARG, "ascend_quant_policy: null argument");
     const auto fp_type = [](int32_t t) { return t == ASCQ_DT_F16 || t == ASCQ_DT_BF16 || t == ASCQ_DT_F32; };
     if (!fp_type(src_type)) return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: src must be f16, bf16 or f32");
     if (!fp_type(scale_type)) return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: scale must be f16, bf16 or f32");
@@ -721,7 +721,8 @@ ascq_status ascq_ascend_quant_policy(void* dst, int32_t dst_type, const void* sr
         return fail(ASCQ_E_INVALID_ARG, "ascend_quant_policy: calCount must be an integer multiple of n");
     if (fp4 && para->n % 2 != 0) return fail(ASCQ_E_INVALID_ARG, "ascend_quant_policy: fp4 rows pack two per byte (n even)");
     const int64_t rows = para->cal_count / para->n;
-    if (rows == 0) return ASCQ_OK;
+    if (rows == 0) return ASCQ_OK;  // calCount = 0: nothing to do (empty tensors may carry null pointers)
+    if (!dst || !src || !scale) return fail(ASCQ_E_INVALID_ARG, "ascend_quant_policy: null argument");
     return hip_status(ascq::launch_quant_policy(dst, dst_type, src, src_type, scale, scale_type, offset,
                                                 para->has_offset ? 1 : 0, offset_scalar,
                                                 policy == ASCQ_POLICY_PER_TOKEN ? 1 : 0, rows, para->n,
@@ -807,7 +808,6 @@ ascq_status ascq_ascend_antiquant_policy(void* dst, int32_t dst_type, const void
                                          int64_t m, int64_t n, int64_t group_size, int32_t k_dim, int32_t is_transpose,
                                          void* stream)
 {
-    if (!dst || !src || !scale) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_policy: null argument");
     if (m < 0 || n < 0) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_policy: negative shape");
     if (policy != ASCQ_POLICY_PER_TOKEN && policy != ASCQ_POLICY_PER_GROUP)
         return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: policy must be PER_TOKEN or PER_GROUP");
@@ -831,7 +831,8 @@ ascq_status ascq_ascend_antiquant_policy(void* dst, int32_t dst_type, const void
     } else {
         return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: src must be int8, fp8_e4m3, fp8_e5m2 or fp4_e2m1");
     }
-    if (m == 0 || n == 0) return ASCQ_OK;
+    if (m == 0 || n == 0) return ASCQ_OK;  // empty tensors may carry null pointers
+    if (!dst || !src || !scale) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_policy: null argument");
     const int col_groups = (k_dim == 1 && !is_transpose) || (k_dim == 0 && is_transpose);
     return hip_status(ascq::launch_antiquant_policy(dst, dst_type, src, src_type, scale, offset, scale_type,
                                                     policy == ASCQ_POLICY_PER_TOKEN ? 1 : 0, m, n, group_size, col_groups,

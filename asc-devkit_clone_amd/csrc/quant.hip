@@ -288,15 +288,6 @@ hipError_t launch_quant_dynamic_per_token(int8_t* q, float* scale_out, const voi
     return hipGetLastError();
 }
 
-hipError_t launch_quant_legacy(int8_t* q, const void* x, int src_type, const uint16_t* scale, const uint16_t* offset,
-                               uint16_t scale_scalar, uint16_t offset_scalar, uint32_t cal_count,
-                               uint32_t scale_count, hipStream_t st)
-{
-    dim3 grid(grid_for(cal_count)), block(256);
-    launch_k(quant_legacy_f16_kernel, grid, block, 0, st, x, q, scale, offset, scale_scalar, offset_scalar,
-                       (int64_t)cal_count, scale_count, src_type);
-    return hipGetLastError();
-}
 
 hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
                           float scale_scalar, int policy, uint32_t m, uint32_t n, uint32_t cal_count, hipStream_t st)
@@ -657,6 +648,124 @@ __global__ __launch_bounds__(256) void quant_policy_vec_krow_kernel(QuantPolicyA
             quant_unit<DST, SRC, SC, MODE, true>(a, (r0 + k) * a.upr + wu, xr[k], sr, orw, off_tensor, osc);
         }
     }
+}
+
+// Legacy AscendQuant, vector path (cal_count % 8 == 0 and below 2^31, 16-byte aligned source, scale / offset
+// vectors of a multiple of 8 entries, 16-byte aligned).  Element i uses channel i % scale_count, and scale_count
+// divides cal_count, so the data is R = cal_count / scale_count rows of scale_count channels; a unit is 8
+// consecutive channels of one row.  With channel vectors a lane takes the same 8 channels of QP_UNR consecutive
+// rows and loads their scales / offsets once; with scalars only, QP_UNR consecutive units per workgroup pass.  Each
+// lane issues all loads before converting.  The half product and the half offset add run as packed half operations,
+// each correctly rounded like the reference's Muls / Adds in half; an f32 source is first cast to half (rne).
+template <bool F32SRC>
+__device__ __forceinline__ u32x2 quant_legacy_unit(const uint32_t* xw, const uint32_t* sw, const uint32_t* ow)
+{
+    int32_t r[8];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        h2 xh;
+        if constexpr (F32SRC) xh = (h2){(_Float16)__uint_as_float(xw[2 * p]), (_Float16)__uint_as_float(xw[2 * p + 1])};
+        else xh = __builtin_bit_cast(h2, xw[p]);
+        h2 t = xh * __builtin_bit_cast(h2, sw[p]);
+        t = t + __builtin_bit_cast(h2, ow[p]);
+        r[2 * p] = quant_s8<RM_RINT>((float)t.x);
+        r[2 * p + 1] = quant_s8<RM_RINT>((float)t.y);
+    }
+    return (u32x2){pack4_s8(r[0], r[1], r[2], r[3]), pack4_s8(r[4], r[5], r[6], r[7])};
+}
+
+template <bool F32SRC, bool SV, bool OV>
+__global__ __launch_bounds__(256) void quant_legacy_vec_kernel(const void* __restrict__ x, u32x2* __restrict__ q,
+                                                               const uint16_t* __restrict__ scale,
+                                                               const uint16_t* __restrict__ offset,
+                                                               uint32_t ss, uint32_t os, uint32_t units, uint32_t rows,
+                                                               uint32_t upr, FastDiv upr_div)
+{
+    constexpr int SRC = F32SRC ? DT_F32 : DT_F16;
+    const uint32_t s2 = ss | (ss << 16), o2 = os | (os << 16);
+    if constexpr (SV || OV) {  // units: row blocks x upr
+        for (uint32_t v = blockIdx.x * 256u + threadIdx.x; v < units; v += gridDim.x * 256u) {
+            const uint32_t rb = fdiv(v, upr_div), w = v - rb * upr, r0 = rb * QP_UNR;
+            uint32_t sw[4] = {s2, s2, s2, s2}, ow[4] = {o2, o2, o2, o2};
+            if constexpr (SV) {
+                const u32x4 t = *(const u32x4*)(scale + 8 * w);
+                sw[0] = t.x, sw[1] = t.y, sw[2] = t.z, sw[3] = t.w;
+            }
+            if constexpr (OV) {
+                const u32x4 t = *(const u32x4*)(offset + 8 * w);
+                ow[0] = t.x, ow[1] = t.y, ow[2] = t.z, ow[3] = t.w;
+            }
+            Raw8<SRC> xr[QP_UNR];
+#pragma unroll
+            for (int k = 0; k < QP_UNR; ++k) {
+                const uint32_t r = r0 + k < rows ? r0 + k : rows - 1u;  // past the last row: reload it, store nothing
+                load_raw8<SRC>(x, r * upr + w, xr[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < QP_UNR; ++k) {
+                if (r0 + k >= rows) break;
+                __builtin_nontemporal_store(quant_legacy_unit<F32SRC>(xr[k].w, sw, ow), q + (r0 + k) * upr + w);
+            }
+        }
+    } else {  // units: m * n / 8
+        const uint32_t sw[4] = {s2, s2, s2, s2}, ow[4] = {o2, o2, o2, o2};
+        for (uint32_t b0 = blockIdx.x * (256u * QP_UNR); b0 < units; b0 += gridDim.x * (256u * QP_UNR)) {
+            Raw8<SRC> xr[QP_UNR];
+#pragma unroll
+            for (int k = 0; k < QP_UNR; ++k) {
+                const uint32_t u = b0 + k * 256u + threadIdx.x;
+                load_raw8<SRC>(x, u < units ? u : units - 1u, xr[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < QP_UNR; ++k) {
+                const uint32_t u = b0 + k * 256u + threadIdx.x;
+                if (u >= units) break;
+                __builtin_nontemporal_store(quant_legacy_unit<F32SRC>(xr[k].w, sw, ow), q + u);
+            }
+        }
+    }
+}
+
+template <bool F32SRC, bool SV>
+static void launch_legacy_vec(const void* x, int8_t* q, const uint16_t* scale, const uint16_t* offset, uint32_t ss,
+                              uint32_t os, uint32_t cal_count, uint32_t sc, hipStream_t st)
+{
+    const bool vecs = SV || offset;
+    const uint32_t upr = vecs ? sc / 8 : 1u, rows = vecs ? cal_count / sc : 0u;
+    const uint32_t units = vecs ? (rows + QP_UNR - 1) / QP_UNR * upr : cal_count / 8;
+    const dim3 grid(grid_for(vecs ? units : (units + QP_UNR - 1) / QP_UNR)), block(256);
+    const FastDiv d = fast_div(upr);
+    if (offset)
+        launch_k(quant_legacy_vec_kernel<F32SRC, SV, true>, grid, block, 0, st, x, (u32x2*)q, scale, offset, ss, os,
+                 units, rows, upr, d);
+    else
+        launch_k(quant_legacy_vec_kernel<F32SRC, SV, false>, grid, block, 0, st, x, (u32x2*)q, scale, offset, ss, os,
+                 units, rows, upr, d);
+}
+
+hipError_t launch_quant_legacy(int8_t* q, const void* x, int src_type, const uint16_t* scale, const uint16_t* offset,
+                               uint16_t scale_scalar, uint16_t offset_scalar, uint32_t cal_count,
+                               uint32_t scale_count, hipStream_t st)
+{
+    const bool vecs = scale || offset;
+    const bool vec = cal_count % 8 == 0 && cal_count < (1u << 31) && (uintptr_t)x % 16 == 0 &&
+                     (uintptr_t)q % 8 == 0 && (!vecs || (scale_count % 8 == 0 && scale_count > 0)) &&
+                     (uintptr_t)scale % 16 == 0 && (uintptr_t)offset % 16 == 0;
+    if (vec && cal_count > 0) {
+        const bool f32 = src_type == DT_F32;
+        if (f32) {
+            if (scale) launch_legacy_vec<true, true>(x, q, scale, offset, scale_scalar, offset_scalar, cal_count, scale_count, st);
+            else launch_legacy_vec<true, false>(x, q, scale, offset, scale_scalar, offset_scalar, cal_count, scale_count, st);
+        } else {
+            if (scale) launch_legacy_vec<false, true>(x, q, scale, offset, scale_scalar, offset_scalar, cal_count, scale_count, st);
+            else launch_legacy_vec<false, false>(x, q, scale, offset, scale_scalar, offset_scalar, cal_count, scale_count, st);
+        }
+        return hipGetLastError();
+    }
+    dim3 grid(grid_for(cal_count)), block(256);
+    launch_k(quant_legacy_f16_kernel, grid, block, 0, st, x, q, scale, offset, scale_scalar, offset_scalar,
+                       (int64_t)cal_count, scale_count, src_type);
+    return hipGetLastError();
 }
 
 // Any shape or alignment: one thread per output byte (one element; two for E2M1), 64-bit indices.

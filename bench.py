@@ -440,8 +440,30 @@ def bench_antiquant_policy(torch, ascq, src_type, iters):
                 frac_of_peak=gbs / HBM_PEAK_GBS)
 
 
+def bench_quant_legacy(torch, ascq, iters):
+    """legacy AscendQuant (half arithmetic) of an f16 [8192, 8192] tensor with per-channel f16 scale and offset
+    vectors of 8192 entries"""
+    M = N = 8192
+    nbytes = 2 * M * N + M * N + 4 * N
+    R = rotation(nbytes)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    xs = [torch.randn((M, N), generator=gen, device="cuda").half() for _ in range(R)]
+    qs = [torch.empty((M, N), dtype=torch.int8, device="cuda") for _ in range(R)]
+    sc = torch.empty(N, device="cuda").uniform_(0.5, 40.0, generator=gen).half()
+    of = torch.empty(N, device="cuda").uniform_(-1.0, 1.0, generator=gen).half()
+
+    def fn(i):
+        ascq.ascend_quant(xs[i % R], scale=sc, offset=of, out=qs[i % R])
+
+    ms = _time_loop(torch, fn, iters)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(workload=f"AscendQuant legacy per-channel (half arithmetic) f16 [{M},{N}] -> int8", ms=ms, value=gbs,
+                unit="GB/s", frac_of_peak=gbs / HBM_PEAK_GBS)
+
+
 OTHER = {
-    "quant": [lambda t, a: bench_antiquant_policy(t, a, a.INT8, 50),
+    "quant": [lambda t, a: bench_quant_legacy(t, a, 50),lambda t, a: bench_antiquant_policy(t, a, a.INT8, 50),
               lambda t, a: bench_antiquant_policy(t, a, a.FP4_E2M1, 50),lambda t, a: bench_quant_policy(t, a, a.INT8, a.PER_GROUP, 50),
               lambda t, a: bench_quant_policy(t, a, a.INT8, a.PER_GROUP, 50, k_dim=0),
               lambda t, a: bench_quant_policy(t, a, a.FP8_E4M3, a.PER_TOKEN, 50),

@@ -113,6 +113,31 @@ def test_legacy_quant_f16_arith(ascq_gpu, oracle, per_channel, src):
     np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
 
 
+@pytest.mark.parametrize("case", [(4096, 64, True, True), (4096, 64, True, False), (4096, 64, False, True),
+                                  (4092, 12, True, True), (4100, 4, True, True), (8, 8, True, True),
+                                  (16392, 8, False, False), (1 << 20, 4096, True, True)])
+@pytest.mark.parametrize("src", ["f16", "f32"])
+def test_legacy_quant_layouts(ascq_gpu, oracle, case, src):
+    """scale / offset vectors or scalars, channel counts that are and are not multiples of 8, ragged totals (the
+    vector and the per-element kernels), ties and saturation"""
+    n_total, sc, sv, ov = case
+    rng = seeded(37 + n_total % 97 + sc + 2 * sv + ov)
+    x32 = rng.uniform(-300, 300, n_total).astype(np.float32)
+    x32[:6] = [0.5, 1.5, 2.5, -0.5, 126.5, -127.5]
+    scale = rng.uniform(0.25, 4, sc).astype(np.float16)
+    offset = rng.uniform(-2, 2, sc).astype(np.float16)
+    scale[0], offset[0] = 1.0, 0.0
+    xs = x32.astype(np.float16) if src == "f16" else x32
+    q = ascq_gpu.ascend_quant(torch.from_numpy(xs).cuda(), scale=_dev(scale) if sv else None,
+                              offset=_dev(offset) if ov else None, scale_scalar=1.0, offset_scalar=0.0,
+                              scale_count=sc if (sv or ov) else 0)
+    q_ref = O.quant_legacy_f16(xs.view(np.uint16) if src == "f16" else xs, O.F16 if src == "f16" else O.F32,
+                               scale_vec=scale.view(np.uint16) if sv else None, scale_scalar=0x3C00,
+                               offset_vec=offset.view(np.uint16) if ov else None, offset_scalar=0,
+                               scale_count=sc if (sv or ov) else 0)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+
+
 @pytest.mark.parametrize("m,n", [(64, 8192), (5, 48), (3, 20), (2, 8), (4, 24), (3, 8200), (1, 16392), (9, 1000)])
 def test_dequant_per_token_int8(ascq_gpu, oracle, m, n):
     rng = seeded(41 + n)

@@ -189,3 +189,15 @@ def test_conversion_sweeps(ascq_gpu):
         _check(ascq_gpu, f, O.F32, one_f, O.F32, fmt, O.PER_TOKEN, 2048, 2048)
     one_g = np.ones((2048, 2048 // 32), np.float32)
     _check(ascq_gpu, f, O.F32, one_g, O.F32, O.FP4_E2M1, O.PER_GROUP, 2048, 2048, 32, None, None, 1)
+
+
+def test_empty_inputs(ascq_gpu):
+    """rows = 0 (cal_count 0) is a no-op for the quant and antiquant policy forms, as calCount = 0 is in the reference"""
+    x = torch.zeros((0, 64), dtype=torch.float16, device="cuda")
+    s = torch.ones((0, 2), dtype=torch.float16, device="cuda")
+    q = ascq_gpu.ascend_quant_policy(x, s, O.PER_GROUP, O.INT8, 32)
+    assert q.shape == (0, 64)
+    y = ascq_gpu.ascend_antiquant_policy(torch.zeros((0, 64), dtype=torch.int8, device="cuda"), O.INT8, s, O.F16,
+                                         O.PER_GROUP, 0, 64, 32, None, 1)
+    torch.cuda.synchronize()
+    assert y.shape == (0, 64)
