@@ -969,7 +969,7 @@ struct AntiQuantVecArgs {
 // SRC: DT_INT8, DT_FP8_E4M3, DT_FP8_E5M2 or DT_FP4_E2M1; SC: scale type (E8M0 for fp4); DST: output type.
 // One unit: source words xw (8 int8 / fp8 codes in two words, or 8 E2M1 nibbles in xw0), scale / offset bits
 // (EIGHT: 8 per unit packed like the table; else one).
-template <int SRC, int SC, int DST, bool EIGHT>
+template <int SRC, int SC, int DST, bool EIGHT, int AR>
 __device__ __forceinline__ void aq_unit(const AntiQuantVecArgs& a, uint32_t u, uint32_t xw0, uint32_t xw1,
                                         const uint32_t* sw, const uint32_t* ow, bool has_off)
 {
@@ -1005,10 +1005,10 @@ __device__ __forceinline__ void aq_unit(const AntiQuantVecArgs& a, uint32_t u, u
                 float v = fp8_bits_to_f32(code, SRC == DT_FP8_E5M2);
                 if (has_off) v = v + o;
                 y[j] = v * s;
-            } else {  // int8: arithmetic in the scale type
-                float v = (float)(int8_t)code;
-                if (has_off) v = rnd_t<SC>(v + o);
-                y[j] = rnd_t<SC>(v * s);
+            } else {  // int8 / int4: arithmetic in AR (the scale type, or fp32 for the legacy fp32 path)
+                float v = SRC == DT_INT4 ? (float)((int32_t)(xw0 << (28 - 4 * j)) >> 28) : (float)(int8_t)code;
+                if (has_off) v = rnd_t<AR>(v + o);
+                y[j] = rnd_t<AR>(v * s);
             }
         }
     }
@@ -1025,12 +1025,12 @@ __device__ __forceinline__ void aq_unit(const AntiQuantVecArgs& a, uint32_t u, u
     for (int q = 0; q < 4; ++q) {
         uint32_t lo, hi;
         if constexpr (DST == DT_BF16) {
-            if constexpr (FP4 || (!FP8 && SC == DT_BF16))  // already bf16 values
+            if constexpr (FP4 || (!FP8 && AR == DT_BF16))  // already bf16 values
                 lo = __float_as_uint(y[2 * q]) >> 16, hi = __float_as_uint(y[2 * q + 1]) >> 16;
             else
                 lo = f32_to_bf16_sat(y[2 * q]), hi = f32_to_bf16_sat(y[2 * q + 1]);
         } else {
-            if constexpr (!FP4 && !FP8 && SC == DT_F16)  // half arithmetic: already half values (inf kept)
+            if constexpr (!FP4 && !FP8 && AR == DT_F16)  // half arithmetic: already half values (inf kept)
                 lo = f32_to_f16(y[2 * q]), hi = f32_to_f16(y[2 * q + 1]);
             else
                 lo = f32_to_f16_sat(y[2 * q]), hi = f32_to_f16_sat(y[2 * q + 1]);
@@ -1043,7 +1043,7 @@ __device__ __forceinline__ void aq_unit(const AntiQuantVecArgs& a, uint32_t u, u
 template <int SRC>
 __device__ __forceinline__ void aq_load_src(const void* src, uint32_t u, uint32_t& w0, uint32_t& w1)
 {
-    if constexpr (SRC == DT_FP4_E2M1) {
+    if constexpr (SRC == DT_FP4_E2M1 || SRC == DT_INT4) {
         w0 = __builtin_nontemporal_load((const uint32_t*)src + u), w1 = 0u;
     } else {
         const u32x2 x = __builtin_nontemporal_load((const u32x2*)src + u);
@@ -1069,7 +1069,7 @@ __device__ __forceinline__ void aq_load8(const void* p, int64_t si, uint32_t* w)
 }
 
 // one scale per unit (groups along the row; PER_TOKEN by row): AQ_UNR * 256 consecutive units per workgroup pass
-template <int SRC, int SC, int DST>
+template <int SRC, int SC, int DST, int AR = SC>
 __global__ __launch_bounds__(256) void antiquant_policy_vec_kernel(AntiQuantVecArgs a)
 {
     constexpr int SB = SC == DT_F32 ? 4 : (SC == DT_E8M0 ? 1 : 2);
@@ -1092,7 +1092,7 @@ __global__ __launch_bounds__(256) void antiquant_policy_vec_kernel(AntiQuantVecA
         for (int k = 0; k < AQ_UNR; ++k) {
             const uint32_t u = b0 + k * 256u + threadIdx.x;
             if (u >= a.units) break;
-            aq_unit<SRC, SC, DST, false>(a, u, x0[k], x1[k], &sw[k], &ow[k], has_off);
+            aq_unit<SRC, SC, DST, false, AR>(a, u, x0[k], x1[k], &sw[k], &ow[k], has_off);
         }
     }
 }
@@ -1100,7 +1100,7 @@ __global__ __launch_bounds__(256) void antiquant_policy_vec_kernel(AntiQuantVecA
 // 8 scales per unit (groups down the columns; PER_TOKEN by column): a lane takes the same 8 columns of AQ_UNR
 // consecutive rows (AQ_UNR divides every group size), so one load of 8 scales and offsets serves all of them;
 // units: row blocks x (n / 8)
-template <int SRC, int SC, int DST>
+template <int SRC, int SC, int DST, int AR = SC>
 __global__ __launch_bounds__(256) void antiquant_policy_vec_krow_kernel(AntiQuantVecArgs a)
 {
     constexpr int SB = SC == DT_F32 ? 4 : (SC == DT_E8M0 ? 1 : 2);
@@ -1122,20 +1122,20 @@ __global__ __launch_bounds__(256) void antiquant_policy_vec_krow_kernel(AntiQuan
 #pragma unroll
         for (int k = 0; k < AQ_UNR; ++k) {
             if (r0 + k >= rows) break;
-            aq_unit<SRC, SC, DST, true>(a, (r0 + k) * a.upr + wu, x0[k], x1[k], sw, ow, has_off);
+            aq_unit<SRC, SC, DST, true, AR>(a, (r0 + k) * a.upr + wu, x0[k], x1[k], sw, ow, has_off);
         }
     }
 }
 
-template <int SRC, int SC, int DST>
+template <int SRC, int SC, int DST, int AR = SC>
 static void launch_aq_vec(const AntiQuantVecArgs& a, bool eight, hipStream_t st)
 {
     if (eight) {
         AntiQuantVecArgs b = a;
         b.units = (a.rows + AQ_UNR - 1) / AQ_UNR * a.upr;
-        launch_k(antiquant_policy_vec_krow_kernel<SRC, SC, DST>, dim3(grid_for(b.units)), dim3(256), 0, st, b);
+        launch_k(antiquant_policy_vec_krow_kernel<SRC, SC, DST, AR>, dim3(grid_for(b.units)), dim3(256), 0, st, b);
     } else {
-        launch_k(antiquant_policy_vec_kernel<SRC, SC, DST>, dim3(grid_for((a.units + AQ_UNR - 1) / AQ_UNR)),
+        launch_k(antiquant_policy_vec_kernel<SRC, SC, DST, AR>, dim3(grid_for((a.units + AQ_UNR - 1) / AQ_UNR)),
                  dim3(256), 0, st, a);
     }
 }
@@ -1200,10 +1200,46 @@ hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int
     return hipGetLastError();
 }
 
+// Legacy AscendAntiQuant through the vector kernels of the policy form: [K, N] with scales [K/g, N] is groups of g
+// rows down the columns, the transposed [N, K] with scales [N, K/g] groups of g along each row.  The half path is
+// the policy form's int8 arithmetic with half scales; the fp32 path keeps its f16 / bf16 tables but computes in
+// fp32 (AR) and casts once.  Needs rows of a multiple of 8 elements, g % 4 == 0 (groups down the columns: four
+// rows share a scale load) or g % 8 == 0 (along a row), and aligned pointers.
+template <int SRC>
+static void launch_antiquant_legacy_vec(const AntiQuantVecArgs& a, int dst_type, int arith, bool eight, hipStream_t st)
+{
+    if (dst_type == DT_BF16) launch_aq_vec<SRC, DT_BF16, DT_BF16, DT_F32>(a, eight, st);
+    else if (arith == 0) launch_aq_vec<SRC, DT_F16, DT_F16, DT_F16>(a, eight, st);
+    else launch_aq_vec<SRC, DT_F16, DT_F16, DT_F32>(a, eight, st);
+}
+
 hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset,
                             const void* scale, uint32_t K, uint32_t N, uint32_t g, int is_transpose, int arith,
                             hipStream_t st)
 {
+    {
+        const bool eight = !is_transpose;
+        const int64_t rows = is_transpose ? N : K, n = is_transpose ? K : N;
+        const bool al = (uintptr_t)src % 8 == 0 && (uintptr_t)dst % 16 == 0 &&
+                        (!eight || ((uintptr_t)scale % 16 == 0 && (uintptr_t)offset % 16 == 0));
+        if (n % 8 == 0 && g % (eight ? 4 : 8) == 0 && al && rows * n / 8 < (1ll << 31)) {
+            AntiQuantVecArgs a;
+            a.dst = dst;
+            a.src = src;
+            a.scale = scale;
+            a.offset = offset;
+            a.n = n;
+            a.sk = eight ? 1 : K / g;
+            a.rows = (uint32_t)rows;
+            a.units = (uint32_t)(rows * n / 8);
+            a.upr = (uint32_t)(n / 8);
+            a.upr_div = fast_div(a.upr);
+            a.g_div = fast_div(g);
+            if (src_type == DT_INT4) launch_antiquant_legacy_vec<DT_INT4>(a, dst_type, arith, eight, st);
+            else launch_antiquant_legacy_vec<DT_INT8>(a, dst_type, arith, eight, st);
+            return hipGetLastError();
+        }
+    }
     dim3 grid(grid_for((int64_t)K * N)), block(256);
     launch_k(antiquant_kernel, grid, block, 0, st, dst, dst_type, src, src_type, (const uint16_t*)offset,
                        (const uint16_t*)scale, K, N, g, is_transpose, arith);

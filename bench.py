@@ -462,8 +462,31 @@ def bench_quant_legacy(torch, ascq, iters):
                 unit="GB/s", frac_of_peak=gbs / HBM_PEAK_GBS)
 
 
+def bench_antiquant_legacy(torch, ascq, iters):
+    """legacy AscendAntiQuant of the antiquant matmul workload's weight: int4 [4096, 11008] with f16 scale and offset
+    per 128 rows, to f16 in half arithmetic"""
+    K, N, g = 4096, 11008, 128
+    nbytes = K * N // 2 + 2 * 2 * (K // g) * N + 2 * K * N
+    R = rotation(nbytes)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(8)
+    ws = [torch.randint(0, 256, (K * N // 2,), generator=gen, device="cuda", dtype=torch.int32).to(torch.uint8)
+          for _ in range(R)]
+    ys = [torch.empty((K, N), dtype=torch.float16, device="cuda") for _ in range(R)]
+    sc = torch.empty((K // g, N), device="cuda").uniform_(0.001, 0.1, generator=gen).half()
+    of = torch.empty((K // g, N), device="cuda").uniform_(-8.0, 8.0, generator=gen).half()
+
+    def fn(i):
+        ascq.ascend_antiquant(ws[i % R], ascq.INT4, sc, of, K, N, g, False, torch.float16, ascq.ARITH_F16, out=ys[i % R])
+
+    ms = _time_loop(torch, fn, iters)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(workload=f"AscendAntiQuant legacy int4 [{K},{N}] g={g} -> f16 (half arithmetic)", ms=ms, value=gbs,
+                unit="GB/s", frac_of_peak=gbs / HBM_PEAK_GBS)
+
+
 OTHER = {
-    "quant": [lambda t, a: bench_quant_legacy(t, a, 50),lambda t, a: bench_antiquant_policy(t, a, a.INT8, 50),
+    "quant": [lambda t, a: bench_antiquant_legacy(t, a, 100),lambda t, a: bench_quant_legacy(t, a, 50),lambda t, a: bench_antiquant_policy(t, a, a.INT8, 50),
               lambda t, a: bench_antiquant_policy(t, a, a.FP4_E2M1, 50),lambda t, a: bench_quant_policy(t, a, a.INT8, a.PER_GROUP, 50),
               lambda t, a: bench_quant_policy(t, a, a.INT8, a.PER_GROUP, 50, k_dim=0),
               lambda t, a: bench_quant_policy(t, a, a.FP8_E4M3, a.PER_TOKEN, 50),

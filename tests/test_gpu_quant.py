@@ -220,6 +220,51 @@ def test_antiquant(ascq_gpu, oracle, src_type, transpose, group, dst, arith, wit
     np.testing.assert_array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), y_ref)
 
 
+@pytest.mark.parametrize("src_type", ["int8", "int4"])
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("group", [0, 20])
+@pytest.mark.parametrize("dst,arith", [("f16", 0), ("bf16", 1)])
+def test_antiquant_ragged(ascq_gpu, oracle, src_type, transpose, group, dst, arith):
+    """K = 100, N = 90 and a group of 20: rows whose length is not a multiple of 8 or groups that split a unit take
+    the per-element kernel, the others the vector kernels"""
+    _antiquant_case(ascq_gpu, src_type, transpose, group, dst, arith, True, 100, 90, 73)
+
+
+def test_antiquant_config3_full_size(ascq_gpu, oracle):
+    """the weight of the antiquant matmul workload, int4 [4096, 11008] with f16 scale / offset per 128 rows, to f16
+    (half arithmetic) and to bf16, against the oracle"""
+    for dst, arith in (("f16", 0), ("bf16", 1)):
+        _antiquant_case(ascq_gpu, "int4", False, 128, dst, arith, True, 4096, 11008, 74)
+
+
+def _antiquant_case(ascq_gpu, src_type, transpose, group, dst, arith, with_offset, K, N, seed):
+    rng = seeded(seed)
+    G = K // group if group else 1
+    if src_type == "int8":
+        w = rng.integers(-128, 128, (N, K) if transpose else (K, N), dtype=np.int8)
+        code = O.INT8
+    else:
+        nib = rng.integers(0, 16, K * N, dtype=np.uint8)
+        w = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8)
+        code = O.INT4
+    sshape = (N, G) if transpose else (G, N)
+    scale32 = np.exp(rng.uniform(np.log(1e-3), np.log(1e-1), sshape)).astype(np.float32)
+    off32 = rng.uniform(-8, 8, sshape).astype(np.float32)
+    if dst == "f16":
+        scale_t, off_t = torch.from_numpy(scale32.astype(np.float16)), torch.from_numpy(off32.astype(np.float16))
+        dtt, dcode = torch.float16, O.F16
+    else:
+        scale_t, off_t = torch.from_numpy(scale32).to(torch.bfloat16), torch.from_numpy(off32).to(torch.bfloat16)
+        dtt, dcode = torch.bfloat16, O.BF16
+    off_dev = off_t.cuda() if with_offset else None
+    y = ascq_gpu.ascend_antiquant(_dev(w), ascq_gpu.INT8 if src_type == "int8" else ascq_gpu.INT4, scale_t.cuda(),
+                                  off_dev, K, N, group, transpose, dtt, arith)
+    y_ref = O.antiquant(w, code, scale_t.view(torch.int16).numpy().view(np.uint16),
+                        off_t.view(torch.int16).numpy().view(np.uint16) if with_offset else None,
+                        K, N, group, transpose, dcode, arith)
+    np.testing.assert_array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), y_ref)
+
+
 def test_config2_full_size_quant_dequant(ascq_gpu, oracle):
     """AscendQuant per-token dynamic quant f16 [8192, 8192] (0.1% outliers x50) -> int8 + fp32 scale, then
     AscendDequant back to f16: both outputs bit-exact vs the oracle at the full workload size."""
