@@ -289,30 +289,6 @@ hipError_t launch_quant_dynamic_per_token(int8_t* q, float* scale_out, const voi
 }
 
 
-hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
-                          float scale_scalar, int policy, uint32_t m, uint32_t n, uint32_t cal_count, hipStream_t st)
-{
-    const bool fast = policy == 2 && src_type == DT_INT8 && dst_type == DT_F16 && scale_type == DT_F32 &&
-                      n % 8 == 0 && ((uintptr_t)src % 8 == 0) && ((uintptr_t)y % 16 == 0) && m > 0 && n > 0;
-    if (fast) {
-        // measured at 8192 x 8192: U = 1 34.9 us, 2 34.1 us, 4 36.1 us (unconditional loads); 16-element units (one
-        // 16-byte load, two 16-byte stores per lane) 34.9 us at U = 1 and slower above, as each store instruction
-        // then covers every other 16 bytes of its span
-        constexpr int U = 2;
-        const uint32_t upr = n / 8;
-        const uint32_t segs = (upr + 256 * U - 1) / (256 * U);
-        const uint64_t blocks = (uint64_t)m * segs;
-        if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
-        launch_k(dequant_i8_token_f16_kernel<U>, dim3((unsigned)blocks), dim3(256), 0, st,
-                           (const u32x2*)src, (const float*)scale, (u32x4*)y, upr, segs);
-        return hipGetLastError();
-    }
-    uint32_t cols = policy == 1 ? cal_count : n;
-    dim3 grid(grid_for((int64_t)m * cols)), block(256);
-    launch_k(dequant_generic_kernel, grid, block, 0, st, y, dst_type, src, src_type, scale, scale_type,
-                       scale_scalar, policy, m, n, cols);
-    return hipGetLastError();
-}
 
 // AscendAntiQuant policy form (arch 3510, ascend_antiquant_3510_impl.h:1386-1412, 1458-2110, 2175-2221): one thread
 // per element of the [m, n] tensor.  Half and bf16 arithmetic is an fp32 operation rounded once to the 16-bit
@@ -765,6 +741,135 @@ hipError_t launch_quant_legacy(int8_t* q, const void* x, int src_type, const uin
     dim3 grid(grid_for(cal_count)), block(256);
     launch_k(quant_legacy_f16_kernel, grid, block, 0, st, x, q, scale, offset, scale_scalar, offset_scalar,
                        (int64_t)cal_count, scale_count, src_type);
+    return hipGetLastError();
+}
+
+// AscendDequant, vector path for an f32 scale (per channel, per token or per tensor), int32 / int8 source and
+// f16 / bf16 / f32 output: rows of `cols` computed elements (cal_count per channel, else n) at a row stride of n;
+// a unit is 8 consecutive columns of one row.  A lane takes the same 8 columns of QP_UNR consecutive rows: their 8
+// per-channel scales are loaded once, the source loads of all rows are issued before converting.  Needs cols and n
+// multiples of 8 and aligned pointers.  dst = cast(f32(src) * scale), cast rne + saturating (store_cast).
+template <int SRC, int DST, int POL>
+__global__ __launch_bounds__(256) void dequant_vec_kernel(void* __restrict__ y, const void* __restrict__ src,
+                                                          const float* __restrict__ scale, float scale_scalar,
+                                                          uint32_t units, uint32_t rows, uint32_t upr, uint32_t n,
+                                                          FastDiv upr_div)
+{
+    for (uint32_t v = blockIdx.x * 256u + threadIdx.x; v < units; v += gridDim.x * 256u) {
+        const uint32_t rb = fdiv(v, upr_div), w = v - rb * upr, r0 = rb * QP_UNR;
+        float sc[8];
+        if constexpr (POL == 1) {  // per channel
+            const u32x4 a = *(const u32x4*)(scale + 8 * w), b = *(const u32x4*)(scale + 8 * w + 4);
+            const uint32_t t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) sc[j] = __uint_as_float(t[j]);
+        }
+        uint32_t xw[QP_UNR][SRC == DT_INT32 ? 8 : 2];
+        float st[QP_UNR];
+#pragma unroll
+        for (int k = 0; k < QP_UNR; ++k) {
+            const uint32_t r = r0 + k < rows ? r0 + k : rows - 1u;  // past the last row: reload it, store nothing
+            const int64_t e = (int64_t)r * n + 8 * (int64_t)w;
+            if constexpr (SRC == DT_INT32) {
+                const u32x4 a = __builtin_nontemporal_load((const u32x4*)((const int32_t*)src + e));
+                const u32x4 b = __builtin_nontemporal_load((const u32x4*)((const int32_t*)src + e) + 1);
+                xw[k][0] = a.x, xw[k][1] = a.y, xw[k][2] = a.z, xw[k][3] = a.w;
+                xw[k][4] = b.x, xw[k][5] = b.y, xw[k][6] = b.z, xw[k][7] = b.w;
+            } else {
+                const u32x2 a = __builtin_nontemporal_load((const u32x2*)((const int8_t*)src + e));
+                xw[k][0] = a.x, xw[k][1] = a.y;
+            }
+            st[k] = POL == 2 ? scale[r] : scale_scalar;
+        }
+#pragma unroll
+        for (int k = 0; k < QP_UNR; ++k) {
+            if (r0 + k >= rows) break;
+            float o[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = SRC == DT_INT32 ? (float)(int32_t)xw[k][j]
+                                                : (float)(int8_t)((xw[k][j >> 2] >> (8 * (j & 3))) & 0xffu);
+                o[j] = x * (POL == 1 ? sc[j] : st[k]);
+            }
+            const int64_t e = (int64_t)(r0 + k) * n + 8 * (int64_t)w;
+            if constexpr (DST == DT_F32) {
+                u32x4* d = (u32x4*)((float*)y + e);
+                __builtin_nontemporal_store((u32x4){__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]),
+                                                    __float_as_uint(o[3])}, d);
+                __builtin_nontemporal_store((u32x4){__float_as_uint(o[4]), __float_as_uint(o[5]), __float_as_uint(o[6]),
+                                                    __float_as_uint(o[7])}, d + 1);
+            } else {
+                uint32_t h[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t lo = DST == DT_BF16 ? f32_to_bf16_sat(o[2 * q]) : f32_to_f16_sat(o[2 * q]);
+                    const uint32_t hi = DST == DT_BF16 ? f32_to_bf16_sat(o[2 * q + 1]) : f32_to_f16_sat(o[2 * q + 1]);
+                    h[q] = lo | (hi << 16);
+                }
+                __builtin_nontemporal_store((u32x4){h[0], h[1], h[2], h[3]}, (u32x4*)((uint16_t*)y + e));
+            }
+        }
+    }
+}
+
+template <int SRC, int DST>
+static void launch_dequant_vec(void* y, const void* src, const float* scale, float ss, int policy, uint32_t rows,
+                               uint32_t cols, uint32_t n, hipStream_t st)
+{
+    const uint32_t upr = cols / 8, units = (rows + QP_UNR - 1) / QP_UNR * upr;
+    const dim3 grid(grid_for(units)), block(256);
+    const FastDiv d = fast_div(upr);
+    if (policy == 1) launch_k(dequant_vec_kernel<SRC, DST, 1>, grid, block, 0, st, y, src, scale, ss, units, rows, upr, n, d);
+    else if (policy == 2) launch_k(dequant_vec_kernel<SRC, DST, 2>, grid, block, 0, st, y, src, scale, ss, units, rows, upr, n, d);
+    else launch_k(dequant_vec_kernel<SRC, DST, 0>, grid, block, 0, st, y, src, scale, ss, units, rows, upr, n, d);
+}
+
+// dispatch of the vector path; false when the shape or alignment needs the per-element kernel
+static bool dequant_vec(void* y, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                        float ss, int policy, uint32_t m, uint32_t n, uint32_t cols, hipStream_t st)
+{
+    const int eb = src_type == DT_INT32 ? 4 : 1;
+    if (policy != 0 && scale_type != DT_F32) return false;
+    if (cols % 8 != 0 || n % 8 != 0 || m == 0 || cols == 0 || (uint64_t)m * n >= (1ull << 31)) return false;
+    if ((uintptr_t)src % (8 * eb > 16 ? 16 : 8 * eb) != 0 || (uintptr_t)y % 16 != 0) return false;
+    if (policy == 1 && (uintptr_t)scale % 16 != 0) return false;
+    const float* sc = (const float*)scale;
+    if (src_type == DT_INT32) {
+        if (dst_type == DT_F16) launch_dequant_vec<DT_INT32, DT_F16>(y, src, sc, ss, policy, m, cols, n, st);
+        else if (dst_type == DT_BF16) launch_dequant_vec<DT_INT32, DT_BF16>(y, src, sc, ss, policy, m, cols, n, st);
+        else launch_dequant_vec<DT_INT32, DT_F32>(y, src, sc, ss, policy, m, cols, n, st);
+    } else {
+        if (dst_type == DT_F16) launch_dequant_vec<DT_INT8, DT_F16>(y, src, sc, ss, policy, m, cols, n, st);
+        else if (dst_type == DT_BF16) launch_dequant_vec<DT_INT8, DT_BF16>(y, src, sc, ss, policy, m, cols, n, st);
+        else launch_dequant_vec<DT_INT8, DT_F32>(y, src, sc, ss, policy, m, cols, n, st);
+    }
+    return true;
+}
+
+hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                          float scale_scalar, int policy, uint32_t m, uint32_t n, uint32_t cal_count, hipStream_t st)
+{
+    const bool fast = policy == 2 && src_type == DT_INT8 && dst_type == DT_F16 && scale_type == DT_F32 &&
+                      n % 8 == 0 && ((uintptr_t)src % 8 == 0) && ((uintptr_t)y % 16 == 0) && m > 0 && n > 0;
+    if (fast) {
+        // measured at 8192 x 8192: U = 1 34.9 us, 2 34.1 us, 4 36.1 us (unconditional loads); 16-element units (one
+        // 16-byte load, two 16-byte stores per lane) 34.9 us at U = 1 and slower above, as each store instruction
+        // then covers every other 16 bytes of its span
+        constexpr int U = 2;
+        const uint32_t upr = n / 8;
+        const uint32_t segs = (upr + 256 * U - 1) / (256 * U);
+        const uint64_t blocks = (uint64_t)m * segs;
+        if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+        launch_k(dequant_i8_token_f16_kernel<U>, dim3((unsigned)blocks), dim3(256), 0, st,
+                           (const u32x2*)src, (const float*)scale, (u32x4*)y, upr, segs);
+        return hipGetLastError();
+    }
+    uint32_t cols = policy == 1 ? cal_count : n;
+    if (dequant_vec(y, dst_type, src, src_type, scale, scale_type, scale_scalar, policy, m, n, cols, st))
+        return hipGetLastError();
+    dim3 grid(grid_for((int64_t)m * cols)), block(256);
+    launch_k(dequant_generic_kernel, grid, block, 0, st, y, dst_type, src, src_type, scale, scale_type,
+                       scale_scalar, policy, m, n, cols);
     return hipGetLastError();
 }
 

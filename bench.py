@@ -485,8 +485,28 @@ def bench_antiquant_legacy(torch, ascq, iters):
                 unit="GB/s", frac_of_peak=gbs / HBM_PEAK_GBS)
 
 
+def bench_dequant_channel(torch, ascq, iters):
+    """AscendDequant (legacy form) of an int32 [8192, 8192] accumulator with per-channel f32 scales to f16"""
+    M = N = 8192
+    nbytes = 4 * M * N + 2 * M * N + 4 * N
+    R = rotation(nbytes)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(9)
+    xs = [torch.randint(-(1 << 20), 1 << 20, (M, N), generator=gen, device="cuda", dtype=torch.int32) for _ in range(R)]
+    ys = [torch.empty((M, N), dtype=torch.float16, device="cuda") for _ in range(R)]
+    sc = torch.empty(N, device="cuda").uniform_(1e-4, 1e-2, generator=gen)
+
+    def fn(i):
+        ascq.ascend_dequant(xs[i % R], sc, ascq.PER_CHANNEL, torch.float16, out=ys[i % R])
+
+    ms = _time_loop(torch, fn, iters)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(workload=f"AscendDequant per-channel int32 [{M},{N}] -> f16 (f32 scales)", ms=ms, value=gbs,
+                unit="GB/s", frac_of_peak=gbs / HBM_PEAK_GBS)
+
+
 OTHER = {
-    "quant": [lambda t, a: bench_antiquant_legacy(t, a, 100),lambda t, a: bench_quant_legacy(t, a, 50),lambda t, a: bench_antiquant_policy(t, a, a.INT8, 50),
+    "quant": [lambda t, a: bench_dequant_channel(t, a, 50),lambda t, a: bench_antiquant_legacy(t, a, 100),lambda t, a: bench_quant_legacy(t, a, 50),lambda t, a: bench_antiquant_policy(t, a, a.INT8, 50),
               lambda t, a: bench_antiquant_policy(t, a, a.FP4_E2M1, 50),lambda t, a: bench_quant_policy(t, a, a.INT8, a.PER_GROUP, 50),
               lambda t, a: bench_quant_policy(t, a, a.INT8, a.PER_GROUP, 50, k_dim=0),
               lambda t, a: bench_quant_policy(t, a, a.FP8_E4M3, a.PER_TOKEN, 50),

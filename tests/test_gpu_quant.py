@@ -178,6 +178,42 @@ def test_dequant_per_channel_int32(ascq_gpu, oracle, dst, scale_kind):
     assert (got[:, cal:] == ref0[:, cal:]).all()
 
 
+@pytest.mark.parametrize("src_kind", ["int32", "int8"])
+@pytest.mark.parametrize("policy", ["channel", "token", "tensor"])
+@pytest.mark.parametrize("dst", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(37, 96, 88), (37, 96, 90), (2048, 8192, 8192)])
+def test_dequant_layouts(ascq_gpu, oracle, src_kind, policy, dst, shape):
+    """f32 scales per channel (calCount of a multiple of 8 or not), per token or per tensor; int32 / int8 sources;
+    saturation at the f16 range; rows not a multiple of 4 (the vector kernels' row blocks)"""
+    m, n, cal = shape
+    if policy != "channel":
+        cal = n
+    rng = seeded(81 + m + cal)
+    if src_kind == "int32":
+        src = rng.integers(-(1 << 24), 1 << 24, (m, n), dtype=np.int32)
+        code = O.INT32
+    else:
+        src = rng.integers(-128, 128, (m, n), dtype=np.int8)
+        code = O.INT8
+    pol = {"channel": ascq_gpu.PER_CHANNEL, "token": ascq_gpu.PER_TOKEN, "tensor": ascq_gpu.PER_TENSOR}[policy]
+    s32 = np.exp(rng.uniform(np.log(1e-4), np.log(8.0), n if policy == "channel" else m)).astype(np.float32)
+    init = torch.full((m, n), 5.0, dtype=dst)
+    out = init.cuda()
+    ascq_gpu.ascend_dequant(_dev(src), None if policy == "tensor" else _dev(s32), pol, dst, cal_count=cal,
+                            scale_scalar=0.0173, out=out)
+    dst_code = {torch.float16: O.F16, torch.bfloat16: O.BF16, torch.float32: O.F32}[dst]
+    if dst == torch.float32:
+        ref0, got = init.numpy().copy(), out.cpu().numpy()
+    else:
+        ref0 = init.view(torch.int16).numpy().view(np.uint16).copy()
+        got = out.cpu().view(torch.int16).numpy().view(np.uint16)
+    y_ref = O.dequant(src, code, None if policy == "tensor" else s32, 0 if policy == "tensor" else O.F32,
+                      {"channel": O.PER_CHANNEL, "token": O.PER_TOKEN, "tensor": O.PER_TENSOR}[policy], dst_code,
+                      cal_count=cal, scale_scalar=np.float32(0.0173), dst=ref0)
+    np.testing.assert_array_equal(got.view(np.uint32) if dst == torch.float32 else got,
+                                  y_ref.view(np.uint32) if dst == torch.float32 else y_ref)
+
+
 def test_dequant_per_tensor(ascq_gpu, oracle):
     rng = seeded(61)
     src = rng.integers(-(1 << 24), 1 << 24, (17, 40), dtype=np.int32)
