@@ -745,36 +745,41 @@ hipError_t launch_quant_legacy(int8_t* q, const void* x, int src_type, const uin
 }
 
 // AscendDequant, vector path for an f32 scale (per channel, per token or per tensor), int32 / int8 source and
-// f16 / bf16 / f32 output: rows of `cols` computed elements (cal_count per channel, else n) at a row stride of n;
-// a unit is 8 consecutive columns of one row.  A lane takes the same 8 columns of QP_UNR consecutive rows: their 8
-// per-channel scales are loaded once, the source loads of all rows are issued before converting.  Needs cols and n
-// multiples of 8 and aligned pointers.  dst = cast(f32(src) * scale), cast rne + saturating (store_cast).
+// f16 / bf16 / f32 output: rows of `cols` computed elements (cal_count per channel, else n) at a row stride of n.
+// A unit is UE consecutive columns of one row -- 4 int32 or 8 int8, one 16- or 8-byte load, so every load (and
+// store) instruction of a wave covers one contiguous span.  A lane takes the same UE columns of RB consecutive
+// rows: their per-channel scales are loaded once and all source loads are issued before converting.  Needs cols
+// and n multiples of UE and aligned pointers.  dst = cast(f32(src) * scale), cast rne + saturating (store_cast).
 template <int SRC, int DST, int POL>
 __global__ __launch_bounds__(256) void dequant_vec_kernel(void* __restrict__ y, const void* __restrict__ src,
                                                           const float* __restrict__ scale, float scale_scalar,
                                                           uint32_t units, uint32_t rows, uint32_t upr, uint32_t n,
                                                           FastDiv upr_div)
 {
+    constexpr int UE = SRC == DT_INT32 ? 4 : 8;   // elements per unit
+    constexpr int RB = SRC == DT_INT32 ? 8 : 4;   // rows per lane
     for (uint32_t v = blockIdx.x * 256u + threadIdx.x; v < units; v += gridDim.x * 256u) {
-        const uint32_t rb = fdiv(v, upr_div), w = v - rb * upr, r0 = rb * QP_UNR;
-        float sc[8];
+        const uint32_t rb = fdiv(v, upr_div), w = v - rb * upr, r0 = rb * RB;
+        float sc[UE];
         if constexpr (POL == 1) {  // per channel
-            const u32x4 a = *(const u32x4*)(scale + 8 * w), b = *(const u32x4*)(scale + 8 * w + 4);
-            const uint32_t t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) sc[j] = __uint_as_float(t[j]);
+            const u32x4 a = *(const u32x4*)(scale + UE * w);
+            sc[0] = __uint_as_float(a.x), sc[1] = __uint_as_float(a.y), sc[2] = __uint_as_float(a.z);
+            sc[3] = __uint_as_float(a.w);
+            if constexpr (UE == 8) {
+                const u32x4 b = *(const u32x4*)(scale + UE * w + 4);
+                sc[4] = __uint_as_float(b.x), sc[5] = __uint_as_float(b.y), sc[6] = __uint_as_float(b.z);
+                sc[7] = __uint_as_float(b.w);
+            }
         }
-        uint32_t xw[QP_UNR][SRC == DT_INT32 ? 8 : 2];
-        float st[QP_UNR];
+        uint32_t xw[RB][UE == 4 ? 4 : 2];
+        float st[RB];
 #pragma unroll
-        for (int k = 0; k < QP_UNR; ++k) {
+        for (int k = 0; k < RB; ++k) {
             const uint32_t r = r0 + k < rows ? r0 + k : rows - 1u;  // past the last row: reload it, store nothing
-            const int64_t e = (int64_t)r * n + 8 * (int64_t)w;
+            const int64_t e = (int64_t)r * n + UE * (int64_t)w;
             if constexpr (SRC == DT_INT32) {
                 const u32x4 a = __builtin_nontemporal_load((const u32x4*)((const int32_t*)src + e));
-                const u32x4 b = __builtin_nontemporal_load((const u32x4*)((const int32_t*)src + e) + 1);
                 xw[k][0] = a.x, xw[k][1] = a.y, xw[k][2] = a.z, xw[k][3] = a.w;
-                xw[k][4] = b.x, xw[k][5] = b.y, xw[k][6] = b.z, xw[k][7] = b.w;
             } else {
                 const u32x2 a = __builtin_nontemporal_load((const u32x2*)((const int8_t*)src + e));
                 xw[k][0] = a.x, xw[k][1] = a.y;
@@ -782,31 +787,32 @@ __global__ __launch_bounds__(256) void dequant_vec_kernel(void* __restrict__ y, 
             st[k] = POL == 2 ? scale[r] : scale_scalar;
         }
 #pragma unroll
-        for (int k = 0; k < QP_UNR; ++k) {
+        for (int k = 0; k < RB; ++k) {
             if (r0 + k >= rows) break;
-            float o[8];
+            float o[UE];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+            for (int j = 0; j < UE; ++j) {
                 const float x = SRC == DT_INT32 ? (float)(int32_t)xw[k][j]
                                                 : (float)(int8_t)((xw[k][j >> 2] >> (8 * (j & 3))) & 0xffu);
                 o[j] = x * (POL == 1 ? sc[j] : st[k]);
             }
-            const int64_t e = (int64_t)(r0 + k) * n + 8 * (int64_t)w;
+            const int64_t e = (int64_t)(r0 + k) * n + UE * (int64_t)w;
             if constexpr (DST == DT_F32) {
-                u32x4* d = (u32x4*)((float*)y + e);
-                __builtin_nontemporal_store((u32x4){__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]),
-                                                    __float_as_uint(o[3])}, d);
-                __builtin_nontemporal_store((u32x4){__float_as_uint(o[4]), __float_as_uint(o[5]), __float_as_uint(o[6]),
-                                                    __float_as_uint(o[7])}, d + 1);
-            } else {
-                uint32_t h[4];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int q = 0; q < UE / 4; ++q)
+                    __builtin_nontemporal_store((u32x4){__float_as_uint(o[4 * q]), __float_as_uint(o[4 * q + 1]),
+                                                        __float_as_uint(o[4 * q + 2]), __float_as_uint(o[4 * q + 3])},
+                                                (u32x4*)((float*)y + e) + q);
+            } else {
+                uint32_t h[UE / 2];
+#pragma unroll
+                for (int q = 0; q < UE / 2; ++q) {
                     const uint32_t lo = DST == DT_BF16 ? f32_to_bf16_sat(o[2 * q]) : f32_to_f16_sat(o[2 * q]);
                     const uint32_t hi = DST == DT_BF16 ? f32_to_bf16_sat(o[2 * q + 1]) : f32_to_f16_sat(o[2 * q + 1]);
                     h[q] = lo | (hi << 16);
                 }
-                __builtin_nontemporal_store((u32x4){h[0], h[1], h[2], h[3]}, (u32x4*)((uint16_t*)y + e));
+                if constexpr (UE == 4) __builtin_nontemporal_store((u32x2){h[0], h[1]}, (u32x2*)((uint16_t*)y + e));
+                else __builtin_nontemporal_store((u32x4){h[0], h[1], h[2], h[3]}, (u32x4*)((uint16_t*)y + e));
             }
         }
     }
@@ -816,7 +822,8 @@ template <int SRC, int DST>
 static void launch_dequant_vec(void* y, const void* src, const float* scale, float ss, int policy, uint32_t rows,
                                uint32_t cols, uint32_t n, hipStream_t st)
 {
-    const uint32_t upr = cols / 8, units = (rows + QP_UNR - 1) / QP_UNR * upr;
+    constexpr uint32_t UE = SRC == DT_INT32 ? 4 : 8, RB = SRC == DT_INT32 ? 8 : 4;
+    const uint32_t upr = cols / UE, units = (rows + RB - 1) / RB * upr;
     const dim3 grid(grid_for(units)), block(256);
     const FastDiv d = fast_div(upr);
     if (policy == 1) launch_k(dequant_vec_kernel<SRC, DST, 1>, grid, block, 0, st, y, src, scale, ss, units, rows, upr, n, d);
@@ -828,10 +835,11 @@ static void launch_dequant_vec(void* y, const void* src, const float* scale, flo
 static bool dequant_vec(void* y, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
                         float ss, int policy, uint32_t m, uint32_t n, uint32_t cols, hipStream_t st)
 {
-    const int eb = src_type == DT_INT32 ? 4 : 1;
+    const uint32_t ue = src_type == DT_INT32 ? 4 : 8;  // elements per unit
     if (policy != 0 && scale_type != DT_F32) return false;
-    if (cols % 8 != 0 || n % 8 != 0 || m == 0 || cols == 0 || (uint64_t)m * n >= (1ull << 31)) return false;
-    if ((uintptr_t)src % (8 * eb > 16 ? 16 : 8 * eb) != 0 || (uintptr_t)y % 16 != 0) return false;
+    if (cols % ue != 0 || n % ue != 0 || m == 0 || cols == 0 || (uint64_t)m * n >= (1ull << 31)) return false;
+    if ((uintptr_t)src % (src_type == DT_INT32 ? 16 : 8) != 0) return false;
+    if ((uintptr_t)y % (dst_type == DT_F32 ? 16 : 2 * ue) != 0) return false;
     if (policy == 1 && (uintptr_t)scale % 16 != 0) return false;
     const float* sc = (const float*)scale;
     if (src_type == DT_INT32) {
