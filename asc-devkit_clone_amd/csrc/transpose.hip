@@ -51,14 +51,22 @@ __global__ __launch_bounds__(256) void transpose_tile_kernel(uint8_t* __restrict
     const int64_t tiles_c = (cols + 127) / 128;
     const int64_t k0 = (int64_t)(blockIdx.x / tiles_c) * 128, c0 = (int64_t)(blockIdx.x % tiles_c) * 128;
     const int t = threadIdx.x;
+    // all four loads are issued before any is used (a chunk past the matrix edge reads the matrix's first chunk and
+    // is zeroed afterwards), so they are in flight together
+    u32x4 v[4];
+    bool in[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int id = t + i * 256, r = id / 8, ch = id % 8;  // row r, 16-byte chunk ch
         const int64_t k = k0 + r, c = c0 + ch * 16;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (k < rows && c < cols) v = *(const u32x4*)(src + k * cols + c);
+        in[i] = k < rows && c < cols;
+        v[i] = *(const u32x4*)(src + (in[i] ? k * cols + c : 0));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int id = t + i * 256, r = id / 8, ch = id % 8;
         const int dw = (ch * 4) ^ (((r >> 4) & 3) << 3);
-        *(u32x4*)&tile[r * 32 + dw] = v;
+        *(u32x4*)&tile[r * 32 + dw] = in[i] ? v[i] : (u32x4){0u, 0u, 0u, 0u};
     }
     __syncthreads();
     const int lane = t & 63, wave = t >> 6;
