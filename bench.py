@@ -545,7 +545,7 @@ def main() -> int:
                     help="run one workload family (the JSON contract line is printed for all / headline)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build targets one MI355X; run with --gpus 1 (no multi-GPU path exists)"}))
+        print(json.dumps({"error": "this library targets one MI355X; run with --gpus 1 (no multi-GPU path exists)"}))
         return 2
 
     import torch

@@ -37,7 +37,7 @@ extern "C" {
 typedef int32_t ascq_status;
 #define ASCQ_OK 0
 #define ASCQ_E_INVALID_ARG (-1) /* mirrors GetTiling's -1 (matmul_tiling.cpp:26-33) */
-#define ASCQ_E_UNSUPPORTED (-2) /* a dtype / layout / mode combination this build does not implement */
+#define ASCQ_E_UNSUPPORTED (-2) /* a dtype / layout / mode combination this library does not implement */
 #define ASCQ_E_HIP (-3)         /* a HIP runtime call failed (see ascq_last_error) */
 #define ASCQ_E_STATE (-4)       /* calls out of order, e.g. IterateAll before SetTensorA */
 

@@ -1,7 +1,7 @@
 /*
  * ascq_oracle.c -- CPU restatement of the asc-devkit quantized-inference arithmetic.
  *
- * TEST INFRASTRUCTURE ONLY (the checker, and bench.py's CPU baseline).  The
+ * TEST INFRASTRUCTURE ONLY (the tests' reference results and bench.py's CPU baseline).  The
  * product library never links or calls this file.  See ascq_oracle.h for the
  * numeric conventions; each function below cites the reference lines it follows.
  *

@@ -1,8 +1,8 @@
 /*
  * ascq_oracle.h -- CPU restatement of the asc-devkit quantized-inference arithmetic.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP product
- * path and the CPU baseline timed by bench.py.  Only tests/, the smoke check in
+ * TEST INFRASTRUCTURE ONLY.  This library is what the tests compare the HIP product
+ * path against, and the CPU baseline timed by bench.py.  Only tests/, the smoke check in
  * __graft_entry__.py and bench.py's cpu_baseline leg may load it.  The product
  * library (libascq.so) never links, loads or calls it, and has no CPU fallback.
  *
