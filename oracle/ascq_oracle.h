@@ -110,7 +110,9 @@ uint8_t oq_e2m1_encode(double x, int mode);
 /* f32 -> fp8, rint + saturation (overflow and inf -> +-max finite, NaN -> 0) */
 uint8_t oq_f32_to_fp8_sat(float x, int fmt);
 /* AscendQuant policy form (arch 3510): PER_TOKEN / PER_GROUP over [m, n] to int8 (scaleT arithmetic), fp8 (fp32
- * arithmetic) or E2M1 (scaleT product -> bf16 -> E2M1, PER_GROUP only); offset tensor, scalar or none */
+ * arithmetic) or E2M1 (scaleT product -> bf16 -> E2M1, PER_GROUP only); offset tensor, scalar or none.
+ * Parity unpinned for two E2M1 sub-cases only: the sign kept on a negative value that rounds to zero, and the
+ * code 0 for a NaN bf16 product (no reference data covers either). */
 void oq_quant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
                      const void* offset, int has_offset, float offset_scalar, int policy, int64_t m, int64_t n,
                      int64_t group, int k_dim, int round_mode);
