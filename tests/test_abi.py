@@ -74,6 +74,40 @@ def test_quant_argument_checks():
     _err(L.ascq_ascend_quant_dynamic_per_token(dummy, dummy, dummy, ascq.F16, 0, 16, 1, None), ascq.OK)
 
 
+def test_policy_form_argument_checks():
+    """AscendQuant / AscendAntiQuant policy forms reject what the reference's static_asserts and checks reject,
+    before any device work (ascend_quant_per_group_3510_impl.h:1465-1498; ascend_antiquant_3510_impl.h:2175-2221)"""
+    L = ascq.lib()
+    d = ctypes.c_void_p(0x1000)
+    P = ascq._QuantParam(4, 64, 256, 32, 0, 1, ascq.ROUND_RINT)
+    qp = lambda dst, src, sc, pol, p=P: L.ascq_ascend_quant_policy(d, dst, d, src, d, None, 0.0, sc, pol, ctypes.byref(p), None)
+    _err(qp(ascq.FP4_E2M1, ascq.F16, ascq.F16, ascq.PER_TOKEN), ascq.E_UNSUPPORTED)      # PER_TOKEN: int8 / fp8 only
+    _err(qp(ascq.INT4, ascq.F16, ascq.F16, ascq.PER_GROUP), ascq.E_UNSUPPORTED)          # no int4 / hifloat8 output
+    _err(qp(ascq.INT8, ascq.F32, ascq.F16, ascq.PER_GROUP), ascq.E_UNSUPPORTED)          # 16-bit scale, f32 source
+    _err(qp(ascq.INT8, ascq.F16, ascq.F16, ascq.PER_CHANNEL), ascq.E_UNSUPPORTED)        # policy
+    _err(qp(ascq.INT8, ascq.INT8, ascq.F16, ascq.PER_GROUP), ascq.E_UNSUPPORTED)         # source type
+    for bad in (ascq._QuantParam(4, 64, 256, 48, 0, 1, 1),   # group not a multiple of 32
+                ascq._QuantParam(4, 64, 256, 32, 0, 2, 1),   # kDim
+                ascq._QuantParam(4, 64, 250, 32, 0, 1, 1),   # calCount not a multiple of n
+                ascq._QuantParam(4, 64, 256, 32, 0, 1, 9)):  # round mode
+        _err(qp(ascq.INT8, ascq.F16, ascq.F16, ascq.PER_GROUP, bad), ascq.E_INVALID_ARG)
+    _err(qp(ascq.FP4_E2M1, ascq.F16, ascq.F16, ascq.PER_GROUP, ascq._QuantParam(4, 63, 252, 32, 0, 1, 1)),
+         ascq.E_INVALID_ARG)  # E2M1 rows pack two a byte
+    # calCount 0 is a no-op that succeeds without touching the device, even with null pointers
+    z = ascq._QuantParam(0, 64, 0, 32, 0, 1, 1)
+    _err(L.ascq_ascend_quant_policy(None, ascq.INT8, None, ascq.F16, None, None, 0.0, ascq.F16, ascq.PER_GROUP,
+                                    ctypes.byref(z), None), ascq.OK)
+    aq = lambda src, sc, dst, pol, g=32, off=None: L.ascq_ascend_antiquant_policy(d, dst, d, src, d, off, sc, pol, 4, 64,
+                                                                                  g, 1, 0, None)
+    _err(aq(ascq.FP4_E2M1, ascq.F16, ascq.BF16, ascq.PER_GROUP), ascq.E_UNSUPPORTED)    # fp4 needs E8M0 scales
+    _err(aq(ascq.FP4_E2M1, ascq.E8M0, ascq.BF16, ascq.PER_GROUP, off=d), ascq.E_UNSUPPORTED)  # and no offset
+    _err(aq(ascq.INT8, ascq.F16, ascq.BF16, ascq.PER_GROUP), ascq.E_UNSUPPORTED)        # half scale writes half
+    _err(aq(ascq.INT4, ascq.F16, ascq.F16, ascq.PER_GROUP), ascq.E_UNSUPPORTED)         # no int4 in the policy form
+    _err(aq(ascq.INT8, ascq.F16, ascq.F16, ascq.PER_GROUP, g=16), ascq.E_INVALID_ARG)   # group % 32
+    _err(L.ascq_ascend_antiquant_policy(None, ascq.F16, None, ascq.INT8, None, None, ascq.F16, ascq.PER_GROUP, 0, 64,
+                                        32, 1, 0, None), ascq.OK)                        # m = 0: no-op
+
+
 def test_dequant_antiquant_argument_checks():
     L = ascq.lib()
     d = ctypes.c_void_p(0x1000)
