@@ -112,13 +112,28 @@ hipError_t launch_fp4_transpose(uint8_t* dst, const uint8_t* src, int64_t K, int
 // E8M0 scales -> the stage-major layout the kernel reads: the SCB bytes of (group g, row r) are blocks
 // SCB g .. SCB g + SCB - 1 of row r, at byte (g * R + r) * SCB.  src_layout 0: [R, sK] row-major; 1: [sK/2, R, 2]
 // (pairs of blocks, rows inner).  One thread per (group, row).
+// Both operands' scales in one launch (the rearrangement of one operand is ~2 MB at 8192 x 8192 and costs little
+// beyond its launch): workgroups [0, blocks_a) rearrange A, the rest B.
+struct ScaleJob {
+    uint8_t* dst;
+    const uint8_t* src;
+    int64_t R;
+    int src_layout;
+};
+
 template <int SCB>
-__global__ __launch_bounds__(256) void mx_scale_stage_major_kernel(uint8_t* __restrict__ dst,
-                                                                   const uint8_t* __restrict__ src, int64_t R,
-                                                                   int64_t sK, int src_layout)
+__global__ __launch_bounds__(256) void mx_scale_stage_major_kernel(ScaleJob ja, ScaleJob jb, int64_t sK,
+                                                                   uint32_t blocks_a)
 {
+    const bool is_a = blockIdx.x < blocks_a;
+    const ScaleJob j = is_a ? ja : jb;
+    uint8_t* __restrict__ dst = j.dst;
+    const uint8_t* __restrict__ src = j.src;
+    const int64_t R = j.R;
+    const int src_layout = j.src_layout;
+    const int64_t bid = is_a ? blockIdx.x : blockIdx.x - blocks_a, nb = is_a ? blocks_a : gridDim.x - blocks_a;
     const int64_t groups = sK / SCB, total = groups * R;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    for (int64_t i = bid * 256 + threadIdx.x; i < total; i += nb * 256) {
         const int64_t g = i / R, r = i % R;
         if constexpr (SCB == 2) {  // one 16-bit pair of blocks (2g, 2g + 1); layout 1 stores exactly those pairs
             ((uint16_t*)dst)[i] = src_layout == 0 ? *(const uint16_t*)(src + r * sK + 2 * g)
@@ -143,14 +158,15 @@ __global__ __launch_bounds__(256) void mx_scale_stage_major_kernel(uint8_t* __re
 }
 
 template <int SCB>
-static hipError_t launch_scale_stage_major(uint8_t* dst, const uint8_t* src, int64_t R, int64_t sK, int src_layout,
-                                           hipStream_t st)
+static hipError_t launch_scale_stage_major(const ScaleJob& a, const ScaleJob& b, int64_t sK, hipStream_t st)
 {
-    int64_t blocks = (R * (sK / SCB) + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(mx_scale_stage_major_kernel<SCB>, dim3((unsigned)blocks), dim3(256), 0, st, dst, src, R, sK,
-                       src_layout);
+    const auto blocks_for = [&](int64_t R) {
+        int64_t n = (R * (sK / SCB) + 255) / 256;
+        return n > 32768 ? (int64_t)32768 : (n < 1 ? (int64_t)1 : n);
+    };
+    const int64_t ba = blocks_for(a.R), bb = blocks_for(b.R);
+    hipLaunchKernelGGL(mx_scale_stage_major_kernel<SCB>, dim3((unsigned)(ba + bb)), dim3(256), 0, st, a, b, sK,
+                       (uint32_t)ba);
     return hipGetLastError();
 }
 
@@ -168,9 +184,8 @@ static hipError_t launch_mx_tiled(const MxGemmArgs& a, hipStream_t st)
     const int64_t sK = (a.K + 63) / 64 * 2;
     uint8_t* sa_sm = a.ws_scales;
     uint8_t* sb_sm = a.ws_scales + (a.M * sK + 16 + 255) / 256 * 256;
-    hipError_t e = launch_scale_stage_major<SCB>(sa_sm, a.sA, a.M, sK, a.sa_layout == 1 ? 1 : 0, st);
-    if (e != hipSuccess) return e;
-    e = launch_scale_stage_major<SCB>(sb_sm, a.sB, a.N, sK, a.sb_layout == 0 ? 1 : 0, st);
+    hipError_t e = launch_scale_stage_major<SCB>(ScaleJob{sa_sm, a.sA, a.M, a.sa_layout == 1 ? 1 : 0},
+                                                 ScaleJob{sb_sm, a.sB, a.N, a.sb_layout == 0 ? 1 : 0}, sK, st);
     if (e != hipSuccess) return e;
     static bool attr = false;
     if (!attr) {
