@@ -164,13 +164,8 @@ static hipError_t launch_f8_tiled(const GemmF8Args& a, hipStream_t st)
 {
     using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_F8, RB, FMT>;
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    const hipError_t e = ensure_dynamic_lds<gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT>>((int)T::LDS_BYTES);
+    if (e != hipSuccess) return e;
     launch_k((gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
     return hipGetLastError();
 }

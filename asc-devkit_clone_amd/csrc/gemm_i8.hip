@@ -241,13 +241,8 @@ static hipError_t launch_tiled(const GemmI8Args& a, hipStream_t st)
 {
     using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB>;
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    const hipError_t e = ensure_dynamic_lds<gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>>((int)T::LDS_BYTES);
+    if (e != hipSuccess) return e;
     launch_k((gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
     return hipGetLastError();
 }
@@ -305,13 +300,8 @@ static hipError_t launch_group_tiled(const GroupGemmArgs& a, hipStream_t st)
 {
     using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB>;
     const int64_t slots = (((a.M + BM - 1) / BM + a.G) * ((a.N + BN - 1) / BN) + 7) / 8 * 8;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    const hipError_t e = ensure_dynamic_lds<group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>>((int)T::LDS_BYTES);
+    if (e != hipSuccess) return e;
     launch_k((group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>), dim3((unsigned)slots), dim3(T::NT), T::LDS_BYTES,
                        st, a);
     return hipGetLastError();

@@ -7,7 +7,26 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 namespace ascq {
+
+// Raises the dynamic-LDS limit of kernel K to `bytes` once per device (the attribute belongs to the function on
+// the current device), thread-safe; K is the kernel itself, so each instantiation keeps its own record.
+template <auto K>
+inline hipError_t ensure_dynamic_lds(int bytes)
+{
+    static std::mutex mu;
+    static uint64_t done = 0;  // bit d: set on device d (devices 64 and up are set on every call)
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    if (dev < 64 && ((done >> dev) & 1u)) return hipSuccess;
+    e = hipFuncSetAttribute((const void*)K, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess && dev < 64) done |= 1ull << dev;
+    return e;
+}
 
 // One-shot kernel timing hook (ascq_set_launch_events): the next launch_k on this thread records the two events
 // at its dispatch's start and end -- hipExtLaunchKernelGGL binds them to the dispatch itself, so no marker packet

@@ -187,13 +187,8 @@ static hipError_t launch_mx_tiled(const MxGemmArgs& a, hipStream_t st)
     hipError_t e = launch_scale_stage_major<SCB>(ScaleJob{sa_sm, a.sA, a.M, a.sa_layout == 1 ? 1 : 0},
                                                  ScaleJob{sb_sm, a.sB, a.N, a.sb_layout == 0 ? 1 : 0}, sK, st);
     if (e != hipSuccess) return e;
-    static bool attr = false;
-    if (!attr) {
-        e = hipFuncSetAttribute((const void*)mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT, ILV>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    e = ensure_dynamic_lds<mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT, ILV>>((int)T::LDS_BYTES);
+    if (e != hipSuccess) return e;
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
     launch_k((mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT, ILV>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a,
                        sa_sm, sb_sm);
