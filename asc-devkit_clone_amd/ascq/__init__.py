@@ -22,7 +22,7 @@ _PKG_DIR = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("ASCQ_LIB", _PKG_DIR / "libascq.so"))
 
 # ascq_dtype
-INT8, UINT8, INT4, INT32, F16, BF16, F32, U64, FP8_E4M3, FP8_E5M2, FP4_E2M1, E8M0, INT64 = range(1, 14)
+INT8, UINT8, INT4, INT32, F16, BF16, F32, U64, FP8_E4M3, FP8_E5M2, FP4_E2M1, E8M0, INT64, FP4_E1M2 = range(1, 15)
 # ascq_round_mode
 ROUND_NONE, ROUND_RINT, ROUND_FLOOR, ROUND_CEIL, ROUND_ROUND, ROUND_TRUNC = range(6)
 # ascq_policy
@@ -211,7 +211,7 @@ def ascend_quant_policy(x: torch.Tensor, scale: torch.Tensor, policy: int, dst_t
                         group_size: int = 0, offset=None, offset_scalar=None, k_dim: int = 1,
                         round_mode: int = ROUND_RINT, scale_type: int | None = None, out=None, stream=None):
     """AscendQuant policy form (PER_TOKEN / PER_GROUP) of x [m, n] (f16 / bf16 / f32) to int8, fp8 (e4m3 / e5m2;
-    returned as uint8 codes) or E2M1 (two codes a byte, [m, n/2] uint8).  scale / offset f16 / bf16 / f32; a
+    returned as uint8 codes) or fp4 E2M1 / E1M2 (two codes a byte, [m, n/2] uint8).  scale / offset f16 / bf16 / f32; a
     scalar offset_scalar applies when no offset tensor is given."""
     m, n = x.shape
     src_type = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}[x.dtype]
@@ -219,7 +219,7 @@ def ascend_quant_policy(x: torch.Tensor, scale: torch.Tensor, policy: int, dst_t
         scale_type = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}[scale.dtype]
     if out is not None:
         q = out
-    elif dst_type == FP4_E2M1:
+    elif dst_type in (FP4_E2M1, FP4_E1M2):
         q = torch.empty((m, n // 2), dtype=torch.uint8, device=x.device)
     else:
         q = torch.empty((m, n), dtype=torch.int8 if dst_type == INT8 else torch.uint8, device=x.device)
@@ -274,7 +274,7 @@ def ascend_antiquant_policy(src: torch.Tensor, src_type: int, scale: torch.Tenso
                             m: int, n: int, group_size: int = 0, offset=None, k_dim: int = 0,
                             is_transpose: bool = False, dst_dtype=torch.float16, out=None, stream=None):
     """AscendAntiQuant policy form (PER_TOKEN / PER_GROUP) over [m, n]: int8 / fp8 sources with f16 / bf16 / f32
-    scales, fp4 E2M1 sources with E8M0 group scales.  Returns [m, n] of dst_dtype."""
+    scales, fp4 E2M1 / E1M2 sources with E8M0 group scales.  Returns [m, n] of dst_dtype."""
     dst_type = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}[dst_dtype]
     y = out if out is not None else torch.empty((m, n), dtype=dst_dtype, device=src.device)
     check(lib().ascq_ascend_antiquant_policy(_ptr(y), dst_type, _ptr(src), src_type, _ptr(scale), _ptr(offset),

@@ -701,9 +701,10 @@ ascq_status ascq_ascend_quant_policy(void* dst, int32_t dst_type, const void* sr
     if (!fp_type(src_type)) return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: src must be f16, bf16 or f32");
     if (!fp_type(scale_type)) return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: scale must be f16, bf16 or f32");
     const bool fp8 = dst_type == ASCQ_DT_FP8_E4M3 || dst_type == ASCQ_DT_FP8_E5M2;
-    const bool fp4 = dst_type == ASCQ_DT_FP4_E2M1;
+    const bool fp4 = dst_type == ASCQ_DT_FP4_E2M1 || dst_type == ASCQ_DT_FP4_E1M2;
     if (!fp8 && !fp4 && dst_type != ASCQ_DT_INT8)
-        return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: dst must be int8, fp8_e4m3, fp8_e5m2 or fp4_e2m1");
+        return fail(ASCQ_E_UNSUPPORTED,
+                    "ascend_quant_policy: dst must be int8, fp8_e4m3, fp8_e5m2, fp4_e2m1 or fp4_e1m2");
     if (policy != ASCQ_POLICY_PER_TOKEN && policy != ASCQ_POLICY_PER_GROUP)
         return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: policy must be PER_TOKEN or PER_GROUP");
     if (policy == ASCQ_POLICY_PER_TOKEN && fp4)
@@ -816,7 +817,7 @@ ascq_status ascq_ascend_antiquant_policy(void* dst, int32_t dst_type, const void
         return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_policy: group_size must be a positive multiple of 32");
     const bool fp8 = src_type == ASCQ_DT_FP8_E4M3 || src_type == ASCQ_DT_FP8_E5M2;
     const bool out_ok = dst_type == ASCQ_DT_F16 || dst_type == ASCQ_DT_BF16 || dst_type == ASCQ_DT_F32;
-    if (src_type == ASCQ_DT_FP4_E2M1) {
+    if (src_type == ASCQ_DT_FP4_E2M1 || src_type == ASCQ_DT_FP4_E1M2) {
         if (policy != ASCQ_POLICY_PER_GROUP || scale_type != ASCQ_DT_E8M0 || offset)
             return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: fp4 takes PER_GROUP E8M0 scales and no offset");
         if (dst_type != ASCQ_DT_F16 && dst_type != ASCQ_DT_BF16)
@@ -829,7 +830,7 @@ ascq_status ascq_ascend_antiquant_policy(void* dst, int32_t dst_type, const void
         if (!fp8 && scale_type != ASCQ_DT_F32 && dst_type != scale_type)
             return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: int8 with a 16-bit scale writes the scale type");
     } else {
-        return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: src must be int8, fp8_e4m3, fp8_e5m2 or fp4_e2m1");
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: src must be int8, fp8_e4m3, fp8_e5m2, fp4_e2m1 or fp4_e1m2");
     }
     if (m == 0 || n == 0) return ASCQ_OK;  // empty tensors may carry null pointers
     if (!dst || !src || !scale) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_policy: null argument");

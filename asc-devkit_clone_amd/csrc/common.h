@@ -27,7 +27,7 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 // dtype / round-mode codes shared with include/ascq.h
 enum : int32_t {
     DT_INT8 = 1, DT_UINT8 = 2, DT_INT4 = 3, DT_INT32 = 4, DT_F16 = 5, DT_BF16 = 6, DT_F32 = 7, DT_U64 = 8,
-    DT_FP8_E4M3 = 9, DT_FP8_E5M2 = 10, DT_FP4_E2M1 = 11, DT_E8M0 = 12, DT_INT64 = 13
+    DT_FP8_E4M3 = 9, DT_FP8_E5M2 = 10, DT_FP4_E2M1 = 11, DT_E8M0 = 12, DT_INT64 = 13, DT_FP4_E1M2 = 14
 };
 enum : int32_t { RM_NONE = 0, RM_RINT = 1, RM_FLOOR = 2, RM_CEIL = 3, RM_ROUND = 4, RM_TRUNC = 5 };
 
@@ -135,6 +135,15 @@ __device__ __forceinline__ float e2m1_to_f32(uint32_t nib)
 {
     const uint32_t e = (nib >> 1) & 3u, m = nib & 1u;
     const float mag = e == 0u ? 0.5f * (float)m : (1.0f + 0.5f * (float)m) * (float)(1u << (e - 1u));
+    return (nib & 8u) ? -mag : mag;
+}
+
+// E1M2 nibble: sign | 1-bit exponent (bias 1) | 2-bit mantissa, magnitudes {0, .25, .5, .75, 1, 1.25, 1.5, 1.75}
+// -- the 3-bit magnitude code times 0.25 (docs/zh/api/SIMD-API/c_api/cube_compute/mmad_mx_interface_boundary_value_summary.md:11:
+// largest finite 1.75)
+__device__ __forceinline__ float e1m2_to_f32(uint32_t nib)
+{
+    const float mag = (float)(nib & 7u) * 0.25f;
     return (nib & 8u) ? -mag : mag;
 }
 

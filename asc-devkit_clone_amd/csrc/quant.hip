@@ -320,7 +320,8 @@ __device__ __forceinline__ float load_scale_t(const void* p, int t, int64_t i)
 // 8 contiguous scales (groups down the columns), and an 8- (int8 / fp8) or 4-byte (E2M1) store.  Rows whose
 // length is not a multiple of 8, or unaligned pointers, take the per-element path of the same kernel.
 // ---------------------------------------------------------------------------------------------
-enum : int { QD_INT8 = 0, QD_E4M3 = 1, QD_E5M2 = 2, QD_E2M1 = 3 };
+enum : int { QD_INT8 = 0, QD_E4M3 = 1, QD_E5M2 = 2, QD_E2M1 = 3, QD_E1M2 = 4 };
+constexpr bool qd_nibble(int d) { return d == QD_E2M1 || d == QD_E1M2; }  // two codes a byte
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 enum : int { QL_TOKEN = 0, QL_KCOL = 1, QL_KROW = 2 };
 
@@ -385,6 +386,18 @@ __device__ __forceinline__ uint32_t e2m1_code(float v)
     return v != v ? 0u : (s | c);
 }
 
+// bf16 value -> E1M2 code in round mode MODE, saturating at +-1.75 (Cast<fp4x2_e1m2_t, bfloat16_t>); NaN -> 0.
+// The E1M2 magnitudes are the multiples of 0.25 up to 1.75, so the code is round(4 v) on the signed value (the
+// directed modes see the sign), its magnitude clamped to 7; 4 v is exact (an overflow to inf clamps to 7 too).
+// A negative value that rounds to zero keeps its sign bit.
+template <int MODE>
+__device__ __forceinline__ uint32_t e1m2_code(float v)
+{
+    const uint32_t s = (__float_as_uint(v) >> 28) & 8u;
+    const uint32_t c = (uint32_t)__builtin_fminf(__builtin_fabsf(round_mode_f(4.0f * v, MODE)), 7.0f);
+    return v != v ? 0u : (s | c);
+}
+
 // one scaleT rounding of an fp32 result (exact for products of two 16-bit values; a single correct rounding for
 // sums, since fp32 holds more than 2p + 2 bits of half and bf16)
 template <int T>
@@ -407,7 +420,8 @@ __device__ __forceinline__ uint32_t quant_code(float v)
         // f16 / f32 results go through bf16 (rne, saturating, NaN -> 0): plain rne here gives the same E2M1 code,
         // as NaN maps to 0 and every overflow to +-6 either way
         if constexpr (T != DT_BF16) v = bf16_round(v);
-        return e2m1_code<MODE>(v);
+        if constexpr (DST == QD_E1M2) return e1m2_code<MODE>(v);  // bf16 rounding first: E1M2 steps are finer
+        else return e2m1_code<MODE>(v);
     }
 }
 
@@ -552,7 +566,7 @@ __device__ __forceinline__ void quant_unit(const QuantPolicyArgs& a, uint32_t u,
         if constexpr (FP8) code[j] = fp8_sat_hw<DST == QD_E5M2>(v[j]);
         else code[j] = quant_code<DST, T, MODE>(v[j]);
     }
-    if constexpr (DST == QD_E2M1) {
+    if constexpr (qd_nibble(DST)) {
         const uint32_t w = code[0] | (code[1] << 4) | (code[2] << 8) | (code[3] << 12) | (code[4] << 16) |
                            (code[5] << 20) | (code[6] << 24) | (code[7] << 28);
         __builtin_nontemporal_store(w, (uint32_t*)a.dst + u);
@@ -886,7 +900,7 @@ template <int DST, int T>
 __global__ __launch_bounds__(256) void quant_policy_generic_kernel(QuantPolicyArgs a)
 {
     const int64_t total = a.m * a.n;
-    const int64_t per = DST == QD_E2M1 ? 2 : 1;
+    const int64_t per = qd_nibble(DST) ? 2 : 1;
     const int64_t bytes = total / per;
     for (int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x; b < bytes; b += (int64_t)gridDim.x * 256) {
         uint32_t w = 0;
@@ -945,7 +959,7 @@ template <int DST, int T>
 static void launch_qp(const QuantPolicyArgs& a, bool vec, hipStream_t st)
 {
     if (!vec) {
-        const int64_t bytes = DST == QD_E2M1 ? a.m * a.n / 2 : a.m * a.n;
+        const int64_t bytes = qd_nibble(DST) ? a.m * a.n / 2 : a.m * a.n;
         launch_k(quant_policy_generic_kernel<DST, T>, dim3(grid_for(bytes)), dim3(256), 0, st, a);
         return;
     }
@@ -968,12 +982,13 @@ hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src
 {
     const int dk = dst_type == DT_INT8 ? QD_INT8
                    : dst_type == DT_FP8_E4M3 ? QD_E4M3
-                   : dst_type == DT_FP8_E5M2 ? QD_E5M2 : QD_E2M1;
+                   : dst_type == DT_FP8_E5M2 ? QD_E5M2
+                   : dst_type == DT_FP4_E1M2 ? QD_E1M2 : QD_E2M1;
     QuantPolicyArgs a;
     a.dst = dst;
     a.src = src;
     a.scale = scale;
-    a.has_off = has_offset && dk != QD_E2M1;
+    a.has_off = has_offset && !qd_nibble(dk);
     a.offset = a.has_off ? offset : nullptr;
     // the scalar offset is a scaleT value: round it (rne) to the scale type once, here
     float os = offset_scalar;
@@ -995,7 +1010,7 @@ hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src
     a.sk = (n + a.g - 1) / a.g;
     // vector kernels: units of 8 elements; for groups down the columns, blocks of QP_UNR rows x (n / 8) units
     const int64_t units = a.layout == QL_KROW ? (m + QP_UNR - 1) / QP_UNR * (n / 8) : m * n / 8;
-    const bool al = (uintptr_t)src % 16 == 0 && (uintptr_t)dst % (dk == QD_E2M1 ? 4 : 8) == 0 &&
+    const bool al = (uintptr_t)src % 16 == 0 && (uintptr_t)dst % (qd_nibble(dk) ? 4 : 8) == 0 &&
                     (a.layout != QL_KROW || ((uintptr_t)scale % 16 == 0 && (uintptr_t)a.offset % 16 == 0));
     const bool vec = n % 8 == 0 && al && m * n / 8 < (1ll << 31) && a.g < (1ll << 31) && n < (1ll << 31);
     a.units = vec ? (uint32_t)units : 0u;
@@ -1014,6 +1029,10 @@ hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src
         if (t == DT_F16) launch_qp<QD_INT8, DT_F16>(a, vec, st);
         else if (t == DT_BF16) launch_qp<QD_INT8, DT_BF16>(a, vec, st);
         else launch_qp<QD_INT8, DT_F32>(a, vec, st);
+    } else if (dk == QD_E1M2) {
+        if (t == DT_F16) launch_qp<QD_E1M2, DT_F16>(a, vec, st);
+        else if (t == DT_BF16) launch_qp<QD_E1M2, DT_BF16>(a, vec, st);
+        else launch_qp<QD_E1M2, DT_F32>(a, vec, st);
     } else {
         if (t == DT_F16) launch_qp<QD_E2M1, DT_F16>(a, vec, st);
         else if (t == DT_BF16) launch_qp<QD_E2M1, DT_BF16>(a, vec, st);
@@ -1033,9 +1052,10 @@ __global__ __launch_bounds__(256) void antiquant_policy_kernel(void* __restrict_
     for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
         const int64_t r = idx / n, c = idx % n;
         const int64_t sidx = per_token ? (is_transpose ? c : r) : (col_groups ? r * sk + c / g : (r / g) * n + c);
-        if (src_type == DT_FP4_E2M1) {  // E8M0 scale, bf16 product, no offset
+        if (src_type == DT_FP4_E2M1 || src_type == DT_FP4_E1M2) {  // E8M0 scale, bf16 product, no offset
             const uint32_t b = ((const uint8_t*)src)[idx >> 1];
-            const float v = e2m1_to_f32((idx & 1) ? (b >> 4) : (b & 0xFu));
+            const uint32_t nib = (idx & 1) ? (b >> 4) : (b & 0xFu);
+            const float v = src_type == DT_FP4_E1M2 ? e1m2_to_f32(nib) : e2m1_to_f32(nib);
             const uint32_t e = ((const uint8_t*)scale)[sidx];
             const float sc = e == 255u ? __uint_as_float(0x7fffffffu) : (e == 0u ? __uint_as_float(0x00400000u)
                                                                                  : __uint_as_float(e << 23));
@@ -1079,25 +1099,30 @@ struct AntiQuantVecArgs {
     FastDiv upr_div, g_div;
 };
 
-// SRC: DT_INT8, DT_FP8_E4M3, DT_FP8_E5M2 or DT_FP4_E2M1; SC: scale type (E8M0 for fp4); DST: output type.
+// SRC: DT_INT8, DT_FP8_E4M3, DT_FP8_E5M2, DT_FP4_E2M1 or DT_FP4_E1M2; SC: scale type (E8M0 for fp4); DST: output type.
 // One unit: source words xw (8 int8 / fp8 codes in two words, or 8 E2M1 nibbles in xw0), scale / offset bits
 // (EIGHT: 8 per unit packed like the table; else one).
 template <int SRC, int SC, int DST, bool EIGHT, int AR>
 __device__ __forceinline__ void aq_unit(const AntiQuantVecArgs& a, uint32_t u, uint32_t xw0, uint32_t xw1,
                                         const uint32_t* sw, const uint32_t* ow, bool has_off)
 {
-    constexpr bool FP4 = SRC == DT_FP4_E2M1, FP8 = SRC == DT_FP8_E4M3 || SRC == DT_FP8_E5M2;
+    constexpr bool FP4 = SRC == DT_FP4_E2M1 || SRC == DT_FP4_E1M2, FP8 = SRC == DT_FP8_E4M3 || SRC == DT_FP8_E5M2;
     constexpr int SB = SC == DT_F32 ? 4 : (SC == DT_E8M0 ? 1 : 2);
     float y[8];
     if constexpr (FP4) {
         // E2M1 codes through the gfx950 decode with scale 1 (exact), then the E8M0 scale in fp32 and one bf16 rounding
         float e[8];
         typedef float f2 __attribute__((ext_vector_type(2)));
+        if constexpr (SRC == DT_FP4_E1M2) {  // no E1M2 decode instruction: code * 0.25, exact
+#pragma unroll
+            for (int j = 0; j < 8; ++j) e[j] = e1m2_to_f32(xw0 >> (4 * j));
+        } else {
         const f2 d0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(xw0, 1.0f, 0);
         const f2 d1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(xw0, 1.0f, 1);
         const f2 d2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(xw0, 1.0f, 2);
         const f2 d3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(xw0, 1.0f, 3);
         e[0] = d0.x, e[1] = d0.y, e[2] = d1.x, e[3] = d1.y, e[4] = d2.x, e[5] = d2.y, e[6] = d3.x, e[7] = d3.y;
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint32_t sb = EIGHT ? (sw[j >> 2] >> (8 * (j & 3))) & 0xffu : sw[0];
@@ -1156,7 +1181,7 @@ __device__ __forceinline__ void aq_unit(const AntiQuantVecArgs& a, uint32_t u, u
 template <int SRC>
 __device__ __forceinline__ void aq_load_src(const void* src, uint32_t u, uint32_t& w0, uint32_t& w1)
 {
-    if constexpr (SRC == DT_FP4_E2M1 || SRC == DT_INT4) {
+    if constexpr (SRC == DT_FP4_E2M1 || SRC == DT_FP4_E1M2 || SRC == DT_INT4) {
         w0 = __builtin_nontemporal_load((const uint32_t*)src + u), w1 = 0u;
     } else {
         const u32x2 x = __builtin_nontemporal_load((const u32x2*)src + u);
@@ -1258,13 +1283,13 @@ static void launch_aq_dst(const AntiQuantVecArgs& a, int dst_type, bool eight, h
 {
     if (dst_type == DT_F16) launch_aq_vec<SRC, SC, DT_F16>(a, eight, st);
     else if (dst_type == DT_BF16) launch_aq_vec<SRC, SC, DT_BF16>(a, eight, st);
-    else if constexpr (SRC != DT_FP4_E2M1) launch_aq_vec<SRC, SC, DT_F32>(a, eight, st);
+    else if constexpr (SRC != DT_FP4_E2M1 && SRC != DT_FP4_E1M2) launch_aq_vec<SRC, SC, DT_F32>(a, eight, st);
 }
 
 template <int SRC>
 static void launch_aq_scale(const AntiQuantVecArgs& a, int dst_type, int scale_type, bool eight, hipStream_t st)
 {
-    if constexpr (SRC == DT_FP4_E2M1) {
+    if constexpr (SRC == DT_FP4_E2M1 || SRC == DT_FP4_E1M2) {
         launch_aq_dst<SRC, DT_E8M0>(a, dst_type, eight, st);
     } else if constexpr (SRC == DT_INT8) {  // a 16-bit scale writes its own type
         if (scale_type == DT_F16) launch_aq_vec<SRC, DT_F16, DT_F16>(a, eight, st);
@@ -1304,6 +1329,7 @@ hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int
         if (src_type == DT_INT8) launch_aq_scale<DT_INT8>(a, dst_type, scale_type, eight, st);
         else if (src_type == DT_FP8_E4M3) launch_aq_scale<DT_FP8_E4M3>(a, dst_type, scale_type, eight, st);
         else if (src_type == DT_FP8_E5M2) launch_aq_scale<DT_FP8_E5M2>(a, dst_type, scale_type, eight, st);
+        else if (src_type == DT_FP4_E1M2) launch_aq_scale<DT_FP4_E1M2>(a, dst_type, scale_type, eight, st);
         else launch_aq_scale<DT_FP4_E2M1>(a, dst_type, scale_type, eight, st);
         return hipGetLastError();
     }

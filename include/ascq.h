@@ -57,7 +57,9 @@ typedef enum {
     ASCQ_DT_FP8_E5M2 = 10, /* fp8_e5m2_t */
     ASCQ_DT_FP4_E2M1 = 11, /* fp4x2_e2m1_t, two per byte, even element in the low nibble */
     ASCQ_DT_E8M0 = 12,     /* fp8_e8m0_t shared exponent */
-    ASCQ_DT_INT64 = 13
+    ASCQ_DT_INT64 = 13,
+    ASCQ_DT_FP4_E1M2 = 14  /* fp4x2_e1m2_t: sign | 1-bit exponent (bias 1) | 2-bit mantissa, magnitudes k / 4,
+                              k = 0..7; two per byte, even element in the low nibble */
 } ascq_dtype;
 
 /* RoundMode (impl/basic_api/utils/kernel_utils_mode.h:103-118). NONE acts as RINT on lossy casts. */
@@ -247,12 +249,14 @@ ascq_status ascq_ascend_quant_dynamic_per_token(int8_t* dst, float* scale_out, c
  *         inf -> +-max finite, NaN -> 0); round_mode is not used (every mode is rint, :888-896);
  *   FP4_E2M1 (PER_GROUP only; offset ignored, :1385): y = x * scale in scale_type; an f16 / f32 y is rounded to
  *         bf16 (rne, saturating, NaN -> 0); then E2M1 in round_mode with saturation at +-6; two codes a byte, even
- *         element in the low nibble (n even).
- * src_type F16, BF16 or F32; scale_type F16, BF16 or F32.  For INT8 / FP4_E2M1 a 16-bit scale_type needs a source
+ *         element in the low nibble (n even);
+ *   FP4_E1M2: as FP4_E2M1, with E1M2 codes in round_mode saturating at +-1.75 (the same per-group kernels,
+ *         ascend_quant_per_group_3510_impl.h:1383-1440, serve both fp4 types).
+ * src_type F16, BF16 or F32; scale_type F16, BF16 or F32.  For INT8 / FP4 a 16-bit scale_type needs a source
  * of the same type (a 16-bit source meets an F32 scale as fp32); FP8 accepts every pair.
  * Offset (para->has_offset): the tensor `offset` (scale_type, indexed like scale) or, when it is NULL, the scalar
  * offset_scalar rounded (rne) to scale_type -- the overloads taking `const scaleT offset` (ascend_quant.h:737-777).
- * hifloat8 and fp4 e1m2 outputs are not accepted (no gfx950 encoding). */
+ * hifloat8 outputs are not accepted (no gfx950 encoding). */
 ascq_status ascq_ascend_quant_policy(void* dst, int32_t dst_type, const void* src, int32_t src_type,
                                      const void* scale, const void* offset, float offset_scalar, int32_t scale_type,
                                      int32_t policy, const ascq_quant_param* para, void* stream);
@@ -315,8 +319,9 @@ ascq_status ascq_ascend_antiquant(void* dst, int32_t dst_type, const void* src, 
  *   src FP8_E4M3 / FP8_E5M2: the same in fp32 whatever scale_type (F16 / BF16 / F32), cast to dst;
  *   src FP4_E2M1 ([m, n/2] bytes, even element in the low nibble; n even): PER_GROUP only, scale_type E8M0
  *             (2^(e-127); e = 0 -> 2^-127, e = 255 -> NaN), no offset; bf16(src) * bf16(scale) rounded to bf16,
- *             dst BF16 or F16 (saturating cast).
- * fp4 e1m2 and hifloat8 sources are not accepted (no published encoding / no gfx950 encoding).
+ *             dst BF16 or F16 (saturating cast);
+ *   src FP4_E1M2: as FP4_E2M1 with E1M2 codes (exact in bf16; :2144-2159 route both fp4 types alike).
+ * hifloat8 sources are not accepted (no gfx950 encoding).
  * (ConvertSrc / StoreF32Res: ascend_antiquant_3510_impl.h:1363-1403; fp4 kernels :1724-1828) */
 ascq_status ascq_ascend_antiquant_policy(void* dst, int32_t dst_type, const void* src, int32_t src_type,
                                          const void* scale, const void* offset, int32_t scale_type, int32_t policy,

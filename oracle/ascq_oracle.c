@@ -628,9 +628,10 @@ void oq_antiquant_policy(void* dst, int dst_type, const void* src, int src_type,
             if (policy == OQ_PER_TOKEN) sidx = is_transpose ? c : r;
             else if (col_groups ^ (OQ_MUTANT == 19)) sidx = r * sk + c / group;
             else sidx = (r / group) * n + c;
-            if (src_type == OQ_FP4_E2M1) {
+            if (src_type == OQ_FP4_E2M1 || src_type == OQ_FP4_E1M2) {
                 const uint8_t b = ((const uint8_t*)src)[idx >> 1];
-                const double v = oq_e2m1_decode((idx & 1) ? (uint8_t)(b >> 4) : (uint8_t)(b & 0xF));
+                const uint8_t nib = (idx & 1) ? (uint8_t)(b >> 4) : (uint8_t)(b & 0xF);
+                const double v = src_type == OQ_FP4_E1M2 ? oq_e1m2_decode(nib) : oq_e2m1_decode(nib);
                 const uint8_t e = ((const uint8_t*)scale)[sidx];
                 const double sc = e == 255 ? NAN : (e == 0 ? ldexp(1.0, -127) : ldexp(1.0, (int)e - 127));
                 const double p = round_to(v * sc, OQ_BF16);  /* exact product, one bf16 rounding */
@@ -690,6 +691,45 @@ uint8_t oq_e2m1_encode(double x, int mode)
     return (uint8_t)(s | c);
 }
 
+/* fp4x2_e1m2_t: sign | 1-bit exponent (bias 1) | 2-bit mantissa.  Exponent field 0 is subnormal (0.mm x 2^0),
+ * field 1 normal (1.mm x 2^0): magnitudes {0, .25, .5, .75, 1, 1.25, 1.5, 1.75}; the largest finite 1.75
+ * (docs/zh/api/SIMD-API/c_api/cube_compute/mmad_mx_interface_boundary_value_summary.md:11: +inf -> 1.75,
+ * -inf -> -1.75, NaN -> 0) and e1m2 -> bf16 lossless (docs/zh/api/SIMD-API/tensor_api/reg_vector_compute/
+ * type_conversion/precision_conversion.md:112-115). */
+float oq_e1m2_decode(uint8_t nib)
+{
+    const int e = (nib >> 2) & 1, mm = nib & 3;
+    const float mag = e ? 1.0f + 0.25f * (float)mm : 0.25f * (float)mm;
+    return (nib & 8) ? -mag : mag;
+}
+
+/* E1M2 code of x in round mode `mode` (bf16 -> fp4x2_e1m2_t, precision_conversion.md:345-354; every other mode
+ * rint, TransRegForFp4 ascend_quant_3510_impl.h:995-1036), bracketed on the decoded code table like
+ * oq_e2m1_encode: saturating at +-1.75, NaN -> 0, a negative value that rounds to zero keeps its sign. */
+uint8_t oq_e1m2_encode(double x, int mode)
+{
+    if (x != x) return 0;
+    const int neg = signbit(x) != 0;
+    const uint8_t s = neg ? 8u : 0u;
+    const double a = fabs(x);
+    if (a >= oq_e1m2_decode(7)) return (uint8_t)(s | 7u);
+    int lo = 0;
+    while (oq_e1m2_decode((uint8_t)(lo + 1)) <= a) ++lo;
+    const double ml = oq_e1m2_decode((uint8_t)lo), mh = oq_e1m2_decode((uint8_t)(lo + 1));
+    if (ml == a) return (uint8_t)(s | lo);
+    const int hi = lo + 1;
+    const double dl = a - ml, dh = mh - a;
+    int c;
+    switch (mode) {
+    case OQ_ROUND_TRUNC: c = lo; break;
+    case OQ_ROUND_FLOOR: c = neg ? hi : lo; break;
+    case OQ_ROUND_CEIL: c = neg ? lo : hi; break;
+    case OQ_ROUND_ROUND: c = dl < dh ? lo : hi; break;
+    default: c = dl < dh ? lo : (dh < dl ? hi : ((lo & 1 && OQ_MUTANT != 26) ? hi : lo)); break;
+    }
+    return (uint8_t)(s | c);
+}
+
 /* f32 -> fp8 with rint and saturation (TransRegForFp8, ascend_quant_3510_impl.h:888-896: every round mode but
  * rint maps to LayoutZMrgZRndRSatS, i.e. rint + SAT): finite overflow and +-inf clamp to the largest finite
  * magnitude, NaN -> 0 (cast.md:108-109). */
@@ -719,7 +759,7 @@ void oq_quant_policy(void* dst, int dst_type, const void* src, int src_type, con
                      int64_t group, int k_dim, int round_mode)
 {
     const int fp8 = dst_type == OQ_FP8_E4M3 || dst_type == OQ_FP8_E5M2;
-    const int fp4 = dst_type == OQ_FP4_E2M1;
+    const int fp4 = dst_type == OQ_FP4_E2M1 || dst_type == OQ_FP4_E1M2;
     const int t = (fp8 && OQ_MUTANT != 21) ? OQ_F32 : scale_type; /* arithmetic type */
     const int off = has_offset && !fp4;
     const int64_t sk = group > 0 ? (n + group - 1) / group : 1;
@@ -743,7 +783,7 @@ void oq_quant_policy(void* dst, int dst_type, const void* src, int src_type, con
             } else if (fp4) {
                 double b = v;
                 if (t != OQ_BF16 && OQ_MUTANT != 22) b = v != v ? 0.0 : oq_bf16_to_f32(oq_f64_to_bf16(v, 1));
-                codes[idx] = oq_e2m1_encode(b, round_mode);
+                codes[idx] = dst_type == OQ_FP4_E1M2 ? oq_e1m2_encode(b, round_mode) : oq_e2m1_encode(b, round_mode);
             } else {
                 ((int8_t*)dst)[idx] = oq_sat_s8(oq_round_to_int((float)v, round_mode));
             }

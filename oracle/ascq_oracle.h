@@ -30,7 +30,8 @@ extern "C" {
 /* dtype codes: identical to ascq_dtype in include/ascq.h */
 enum {
     OQ_INT8 = 1, OQ_UINT8 = 2, OQ_INT4 = 3, OQ_INT32 = 4, OQ_F16 = 5, OQ_BF16 = 6,
-    OQ_F32 = 7, OQ_U64 = 8, OQ_FP8_E4M3 = 9, OQ_FP8_E5M2 = 10, OQ_FP4_E2M1 = 11, OQ_E8M0 = 12, OQ_INT64 = 13
+    OQ_F32 = 7, OQ_U64 = 8, OQ_FP8_E4M3 = 9, OQ_FP8_E5M2 = 10, OQ_FP4_E2M1 = 11, OQ_E8M0 = 12, OQ_INT64 = 13,
+    OQ_FP4_E1M2 = 14
 };
 /* RoundMode: impl/basic_api/utils/kernel_utils_mode.h:103-118 (CAST_NONE acts as CAST_RINT on lossy casts,
  * docs/zh/api/SIMD-API/basic_api/memory_vector_compute/type_conversion/Cast.md:92) */
@@ -102,16 +103,20 @@ void oq_dequant(void* dst, int dst_type, const void* src, int src_type, const vo
 void oq_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset, const void* scale,
                   int64_t K, int64_t N, int64_t group_size, int is_transpose, int arith);
 /* AscendAntiQuant policy form (arch 3510): PER_TOKEN / PER_GROUP over [m, n]; int8 (scaleT arithmetic), fp8 (fp32
- * arithmetic) or fp4 E2M1 with E8M0 scales (bf16 product) sources */
+ * arithmetic) or fp4 E2M1 / E1M2 with E8M0 scales (bf16 product) sources */
 void oq_antiquant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale, const void* offset,
                          int scale_type, int policy, int64_t m, int64_t n, int64_t group, int k_dim, int is_transpose);
 /* E2M1 code of x in round mode `mode`, saturating at +-6, NaN -> 0 */
 uint8_t oq_e2m1_encode(double x, int mode);
+/* E1M2 (sign | 1-bit exponent, bias 1 | 2-bit mantissa): decode, and the code of x in round mode `mode`,
+ * saturating at +-1.75, NaN -> 0 */
+float oq_e1m2_decode(uint8_t nibble);
+uint8_t oq_e1m2_encode(double x, int mode);
 /* f32 -> fp8, rint + saturation (overflow and inf -> +-max finite, NaN -> 0) */
 uint8_t oq_f32_to_fp8_sat(float x, int fmt);
 /* AscendQuant policy form (arch 3510): PER_TOKEN / PER_GROUP over [m, n] to int8 (scaleT arithmetic), fp8 (fp32
- * arithmetic) or E2M1 (scaleT product -> bf16 -> E2M1, PER_GROUP only); offset tensor, scalar or none.
- * Parity unpinned for two E2M1 sub-cases only: the sign kept on a negative value that rounds to zero, and the
+ * arithmetic) or fp4 E2M1 / E1M2 (scaleT product -> bf16 -> fp4, PER_GROUP only); offset tensor, scalar or none.
+ * Parity unpinned for two fp4 sub-cases only: the sign kept on a negative value that rounds to zero, and the
  * code 0 for a NaN bf16 product (no reference data covers either). */
 void oq_quant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
                      const void* offset, int has_offset, float offset_scalar, int policy, int64_t m, int64_t n,

@@ -16,7 +16,7 @@ ROOT = Path(__file__).resolve().parent.parent
 ORACLE_DIR = ROOT / "oracle"
 ORACLE_SO = Path(os.environ.get("ASCQ_ORACLE_SO", ORACLE_DIR / "liboracle.so"))
 
-INT8, UINT8, INT4, INT32, F16, BF16, F32, U64, FP8_E4M3, FP8_E5M2, FP4_E2M1, E8M0, INT64 = range(1, 14)
+INT8, UINT8, INT4, INT32, F16, BF16, F32, U64, FP8_E4M3, FP8_E5M2, FP4_E2M1, E8M0, INT64, FP4_E1M2 = range(1, 15)
 ROUND_NONE, ROUND_RINT, ROUND_FLOOR, ROUND_CEIL, ROUND_ROUND, ROUND_TRUNC = range(6)
 PER_TENSOR, PER_CHANNEL, PER_TOKEN, PER_GROUP = range(4)
 ARITH_F16, ARITH_F32 = 0, 1
@@ -59,6 +59,8 @@ def lib() -> ctypes.CDLL:
                                            _I64, _I64, _I64, ctypes.c_int, ctypes.c_int]),
             "oq_mm_requant4": (None, [_P, _P, _I64, _I64, _P, ctypes.c_uint64]),
             "oq_e2m1_encode": (ctypes.c_uint8, [ctypes.c_double, ctypes.c_int]),
+            "oq_e1m2_encode": (ctypes.c_uint8, [ctypes.c_double, ctypes.c_int]),
+            "oq_e1m2_decode": (ctypes.c_float, [ctypes.c_uint8]),
             "oq_f32_to_fp8_sat": (ctypes.c_uint8, [ctypes.c_float, ctypes.c_int]),
             "oq_quant_policy": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int,
                                        ctypes.c_float, ctypes.c_int, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int]),
@@ -185,9 +187,9 @@ def antiquant_policy(src, src_type, scale, scale_type, dst_type, policy, m, n, g
 def quant_policy(src, src_type, scale, scale_type, dst_type, policy, m, n, group=0, offset=None,
                  offset_scalar=None, k_dim=1, round_mode=ROUND_RINT):
     """AscendQuant policy form over [m, n]: src (uint16 bits or float32) [m, n]; scale / offset arrays of
-    scale_type; offset_scalar a float (rounded to scale_type); returns int8 [m, n], fp8 bytes [m, n] or E2M1
+    scale_type; offset_scalar a float (rounded to scale_type); returns int8 [m, n], fp8 bytes [m, n] or fp4
     codes packed [m, n/2]"""
-    if dst_type == FP4_E2M1:
+    if dst_type in (FP4_E2M1, FP4_E1M2):
         out = np.empty((m, n // 2), np.uint8)
     else:
         out = np.empty((m, n), np.int8 if dst_type == INT8 else np.uint8)

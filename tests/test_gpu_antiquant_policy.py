@@ -91,14 +91,15 @@ def test_fp8_source(ascq_gpu, src_type, scale_type, dst_type):
 
 @pytest.mark.parametrize("dst_type", [O.BF16, O.F16])
 @pytest.mark.parametrize("k_dim", [0, 1])
-def test_fp4_source_e8m0(ascq_gpu, dst_type, k_dim):
+@pytest.mark.parametrize("fp4", [O.FP4_E2M1, O.FP4_E1M2])
+def test_fp4_source_e8m0(ascq_gpu, dst_type, k_dim, fp4):
     m, n, g = 96, 128, 32
-    rng = seeded(71 + dst_type + k_dim)
+    rng = seeded(71 + dst_type + k_dim + 3 * fp4)
     packed = rng.integers(0, 256, (m, n // 2)).astype(np.uint8)
     e = rng.integers(100, 155, _sshape(O.PER_GROUP, m, n, g, k_dim, False)).astype(np.uint8)
     e.flat[:4] = [0, 255, 254, 1]  # 2^-127, NaN, overflowing products, tiny products
-    got = _run(ascq_gpu, packed, O.FP4_E2M1, e, O.E8M0, dst_type, O.PER_GROUP, m, n, g, None, k_dim)
-    exp = O.antiquant_policy(packed, O.FP4_E2M1, e, O.E8M0, dst_type, O.PER_GROUP, m, n, g, None, k_dim)
+    got = _run(ascq_gpu, packed, fp4, e, O.E8M0, dst_type, O.PER_GROUP, m, n, g, None, k_dim)
+    exp = O.antiquant_policy(packed, fp4, e, O.E8M0, dst_type, O.PER_GROUP, m, n, g, None, k_dim)
     assert _same(got, exp, dst_type)
 
 
@@ -114,12 +115,12 @@ def test_argument_checks(ascq_gpu):
                                          dst_dtype=torch.bfloat16)
 
 
-@pytest.mark.parametrize("src_type", [O.INT8, O.FP8_E5M2, O.FP4_E2M1])
+@pytest.mark.parametrize("src_type", [O.INT8, O.FP8_E5M2, O.FP4_E2M1, O.FP4_E1M2])
 def test_ragged_rows_and_unaligned(ascq_gpu, src_type):
     """n % 8 != 0, or a destination off a 16-byte boundary, takes the per-element kernel"""
     m, n, g = 21, 98, 32
     rng = seeded(91 + src_type)
-    if src_type == O.FP4_E2M1:
+    if src_type in (O.FP4_E2M1, O.FP4_E1M2):
         src = rng.integers(0, 256, (m, n // 2)).astype(np.uint8)
         sc, sct, of, dt, k_dim = rng.integers(110, 140, (m, (n + g - 1) // g)).astype(np.uint8), O.E8M0, None, O.BF16, 1
     else:
@@ -144,13 +145,14 @@ def test_ragged_rows_and_unaligned(ascq_gpu, src_type):
 
 
 @pytest.mark.parametrize("dst_type", [O.BF16, O.F16])
-def test_fp4_every_byte_every_position(ascq_gpu, dst_type):
-    """every byte value (two E2M1 codes) in each of the four byte positions of a 32-bit source word, under scales
+@pytest.mark.parametrize("fp4", [O.FP4_E2M1, O.FP4_E1M2])
+def test_fp4_every_byte_every_position(ascq_gpu, dst_type, fp4):
+    """every byte value (two E2M1 or E1M2 codes) in each of the four byte positions of a 32-bit source word, under scales
     2^0, 2^-127 (e = 0), 2^127 and NaN (e = 255)"""
     m, n, g = 4, 2048, 32
     b = np.arange(256, dtype=np.uint8)
     packed = np.stack([np.roll(np.repeat(b, 4), p) for p in range(m)]).astype(np.uint8)  # [4, 1024] bytes
     e = np.tile(np.array([127, 0, 254, 255], np.uint8), (m, n // g // 4))
-    got = _run(ascq_gpu, packed, O.FP4_E2M1, e, O.E8M0, dst_type, O.PER_GROUP, m, n, g, None, 1)
-    exp = O.antiquant_policy(packed, O.FP4_E2M1, e, O.E8M0, dst_type, O.PER_GROUP, m, n, g, None, 1)
+    got = _run(ascq_gpu, packed, fp4, e, O.E8M0, dst_type, O.PER_GROUP, m, n, g, None, 1)
+    exp = O.antiquant_policy(packed, fp4, e, O.E8M0, dst_type, O.PER_GROUP, m, n, g, None, 1)
     assert _same(got, exp, dst_type)

@@ -95,12 +95,15 @@ def test_fp8(ascq_gpu, fmt, pair):
 
 @pytest.mark.parametrize("pair", _PAIRS)
 @pytest.mark.parametrize("k_dim", [0, 1])
-def test_e2m1(ascq_gpu, pair, k_dim):
+@pytest.mark.parametrize("fp4", [O.FP4_E2M1, O.FP4_E1M2])
+def test_e2m1(ascq_gpu, pair, k_dim, fp4):
+    """fp4 outputs (E2M1 and E1M2) in every round mode, with the tie points of both code tables"""
     st, sct = pair
     m, n, g = 96, 128, 32
-    rng = seeded(1300 + 10 * st + sct + k_dim)
-    v = rng.uniform(-8.0, 8.0, (m, n))
-    ties = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, 6.0, 7.0, -0.25, -0.75, -2.5, -5.0, 0.3, -0.3, 1e9])
+    rng = seeded(1300 + 10 * st + sct + k_dim + 7 * fp4)
+    v = rng.uniform(-8.0 if fp4 == O.FP4_E2M1 else -2.5, 8.0 if fp4 == O.FP4_E2M1 else 2.5, (m, n))
+    ties = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, 6.0, 7.0, -0.25, -0.75, -2.5, -5.0, 0.3, -0.3, 1e9,
+                     0.125, 0.375, 0.625, 0.875, 1.125, 1.375, 1.625, -0.125, -1.375, -1.625, 1.8, -1.9, 0.1, -0.1])
     v[0, :ties.size] = ties
     v[1, :3] = [np.nan, np.inf, -np.inf]
     x = _bits(v, st)
@@ -108,9 +111,9 @@ def test_e2m1(ascq_gpu, pair, k_dim):
     s = rng.uniform(0.5, 1.5, ss)
     s[0] = 1.0  # row 0 / row group 0: the ties reach the cast unchanged
     sc = _bits(s, sct)
-    of = _bits(np.full(ss, 3.0), sct)  # ignored for E2M1
+    of = _bits(np.full(ss, 3.0), sct)  # ignored for fp4
     for mode in _MODES:
-        _check(ascq_gpu, x, st, sc, sct, O.FP4_E2M1, O.PER_GROUP, m, n, g, of, None, k_dim, mode)
+        _check(ascq_gpu, x, st, sc, sct, fp4, O.PER_GROUP, m, n, g, of, None, k_dim, mode)
 
 
 def test_unaligned_pointers(ascq_gpu):
@@ -123,7 +126,7 @@ def test_unaligned_pointers(ascq_gpu):
     xd[1:] = _dev(x.reshape(-1), O.F16)
     sd = torch.empty(sc.size + 1, dtype=torch.float16, device="cuda")
     sd[1:] = _dev(sc.reshape(-1), O.F16)
-    for dst in (O.INT8, O.FP8_E4M3, O.FP4_E2M1):
+    for dst in (O.INT8, O.FP8_E4M3, O.FP4_E2M1, O.FP4_E1M2):
         q = ascq_gpu.ascend_quant_policy(xd[1:].view(m, n), sd[1:], O.PER_GROUP, dst, g, k_dim=0)
         torch.cuda.synchronize()
         exp = O.quant_policy(x, O.F16, sc, O.F16, dst, O.PER_GROUP, m, n, g, k_dim=0).view(np.uint8)
@@ -181,6 +184,8 @@ def test_conversion_sweeps(ascq_gpu):
     bf = np.arange(0x10000, dtype=np.uint32).astype(np.uint16).reshape(256, 256)
     one_b = _bits(np.ones((256, 256 // 32)), O.BF16)
     _check(ascq_gpu, bf, O.BF16, one_b, O.BF16, O.FP4_E2M1, O.PER_GROUP, 256, 256, 32, None, None, 1)
+    for mode in _MODES:  # E1M2 has no conversion instruction: the software encoder on every bf16 pattern
+        _check(ascq_gpu, bf, O.BF16, one_b, O.BF16, O.FP4_E1M2, O.PER_GROUP, 256, 256, 32, None, None, 1, mode)
     rng = seeded(1700)
     f = (np.arange(1 << 22, dtype=np.uint64) * 1021 + rng.integers(0, 1021, 1 << 22)).astype(np.uint32)
     f = f.view(np.float32).reshape(2048, 2048)
@@ -189,6 +194,7 @@ def test_conversion_sweeps(ascq_gpu):
         _check(ascq_gpu, f, O.F32, one_f, O.F32, fmt, O.PER_TOKEN, 2048, 2048)
     one_g = np.ones((2048, 2048 // 32), np.float32)
     _check(ascq_gpu, f, O.F32, one_g, O.F32, O.FP4_E2M1, O.PER_GROUP, 2048, 2048, 32, None, None, 1)
+    _check(ascq_gpu, f, O.F32, one_g, O.F32, O.FP4_E1M2, O.PER_GROUP, 2048, 2048, 32, None, None, 1)
 
 
 def test_empty_inputs(ascq_gpu):

@@ -963,6 +963,72 @@ def test_quant_policy_e2m1_through_bf16():
     assert got[0, 0] == 0x22  # f32 0.7499 -> bf16 0.75 -> rint 1.0
 
 
+def test_e1m2_decode_table():
+    """fp4x2_e1m2_t decode: sign | 1-bit exponent (bias 1) | 2-bit mantissa gives the magnitudes k / 4, k = 0..7; the
+    largest finite value is 1.75 (mmad_mx_interface_boundary_value_summary.md:11) and every code is exact in bf16
+    (precision_conversion.md:112-115)"""
+    L = O.lib()
+    got = [L.oq_e1m2_decode(c) for c in range(16)]
+    assert got[:8] == [k / 4 for k in range(8)]
+    assert got[8:] == [-k / 4 for k in range(8)] and math.copysign(1.0, got[8]) < 0
+    assert all(_bf16_vals(_bf16_bits(np.array([v], np.float32)))[0] == v for v in got)
+
+
+def test_e1m2_encode_published_cases():
+    """bf16 -> fp4x2_e1m2_t worked example (precision_conversion.md:345-354): 1.375 -> CAST_RINT 1.5, CAST_FLOOR
+    1.25, CAST_CEIL 1.5, CAST_ROUND 1.5, CAST_TRUNC 1.25; boundary table (mmad_mx_interface_boundary_value_summary.md:11):
+    +inf -> 1.75, -inf -> -1.75, NaN -> 0"""
+    L = O.lib()
+    want = {O.ROUND_RINT: 1.5, O.ROUND_FLOOR: 1.25, O.ROUND_CEIL: 1.5, O.ROUND_ROUND: 1.5, O.ROUND_TRUNC: 1.25}
+    for mode, v in want.items():
+        assert L.oq_e1m2_decode(L.oq_e1m2_encode(1.375, mode)) == v
+    for mode in want:
+        assert L.oq_e1m2_encode(math.inf, mode) == 0x7
+        assert L.oq_e1m2_encode(-math.inf, mode) == 0xF
+        assert L.oq_e1m2_encode(math.nan, mode) == 0x0
+
+
+def test_e1m2_encode_closed_form():
+    """the E1M2 grid is uniform (step 0.25), so each round mode is numpy's integer rounding of 4 x on the signed value
+    (rint ties to even, round ties away), magnitude clamped to 7, sign kept; checked on a sweep of bf16 values"""
+    v = _bf16_vals(np.arange(0, 0x10000, 3, dtype=np.uint32).astype(np.uint16))
+    v = v[np.isfinite(v)].astype(np.float64)
+    away = lambda t: np.sign(t) * np.floor(np.abs(t) + 0.5)
+    fns = {O.ROUND_RINT: np.rint, O.ROUND_FLOOR: np.floor, O.ROUND_CEIL: np.ceil, O.ROUND_ROUND: away,
+           O.ROUND_TRUNC: np.trunc}
+    L = O.lib()
+    for mode, f in fns.items():
+        with np.errstate(over="ignore", invalid="ignore"):
+            k = np.minimum(np.abs(f(4.0 * v)), 7).astype(np.uint8)
+        want = k | np.where(np.signbit(v), 8, 0).astype(np.uint8)
+        got = np.array([L.oq_e1m2_encode(float(a), mode) for a in v], np.uint8)
+        assert np.array_equal(got, want), mode
+
+
+def test_quant_policy_e1m2_through_bf16():
+    """E1M2 dst takes the same path as E2M1 (ascend_quant_per_group_3510_impl.h:1383-1440): an f32 product is rounded
+    to bf16 first, so 0.3749 becomes 0.375, a tie (4 x = 1.5) that rint sends to code 2, where a direct cast would
+    give code 1; saturation at 1.75 and NaN -> 0"""
+    x = np.zeros((1, 32), np.float32)
+    x[0, :6] = [0.3749, -0.3749, 3.0, -1e30, np.nan, 1.375]
+    got = O.quant_policy(x, O.F32, np.ones((1, 1), np.float32), O.F32, O.FP4_E1M2, O.PER_GROUP, 1, 32, 32, k_dim=1)
+    assert got[0, :3].tolist() == [0x2 | (0xA << 4), 0x7 | (0xF << 4), 0x0 | (0x6 << 4)]
+
+
+def test_antiquant_policy_e1m2():
+    """fp4 E1M2 source (PER_GROUP, E8M0 scales; ascend_antiquant_3510_impl.h:2144-2159 route both fp4 types alike):
+    every code times 2^(e - 127), exact in bf16, equals the decoded value scaled by a power of two"""
+    m, n, g = 4, 32, 32
+    codes = np.arange(m * n, dtype=np.uint8).reshape(m, n) % 16
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    e = np.array([[127], [120], [130], [0]], np.uint8)
+    got = O.antiquant_policy(packed, O.FP4_E1M2, e, O.E8M0, O.BF16, O.PER_GROUP, m, n, g, k_dim=1)
+    L = O.lib()
+    dec = np.array([[L.oq_e1m2_decode(int(c)) for c in row] for row in codes], np.float64)
+    want = dec * np.ldexp(1.0, e.astype(np.int64) - 127)
+    assert np.array_equal(_bf16_vals(got).astype(np.float64), want)
+
+
 @pytest.mark.parametrize("k_dim", [0, 1])
 def test_quant_policy_group_axis(k_dim):
     """PER_GROUP scale layout: kDim 1 groups along a row, scale [m][ceil(n/g)]; kDim 0 groups down a column,

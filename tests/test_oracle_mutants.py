@@ -47,6 +47,7 @@ MUTANTS = {
     23: "per-group quant scales indexed along the wrong axis",
     24: "quant product not rounded to the scale type before the offset add",
     25: "E2M1 floor / ceil applied to the magnitude regardless of sign",
+    26: "E1M2 rint ties resolved toward zero instead of to the even code",
 }
 
 
