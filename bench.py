@@ -381,11 +381,13 @@ def traffic_probe(torch, ascq):
     return {"traffic_probe": "copy 268435456 B, quant f16 8192x8192, dequant int8 8192x8192 -> f16"}
 
 
-def bench_quant_policy(torch, ascq, dst_type, policy, iters, k_dim=1, g=128):
+def bench_quant_policy(torch, ascq, dst_type, policy, iters, k_dim=1, g=128, round_mode=None):
     """AscendQuant policy form over an f16 [8192, 8192] activation: PER_GROUP (group 128 along the rows) or
-    PER_TOKEN, f16 scales, to int8 / fp8 / E2M1"""
+    PER_TOKEN, f16 scales, to int8 / fp8 / fp4 E2M1 / E1M2 (round_mode: rint unless given)"""
+    fp4 = dst_type in (ascq.FP4_E2M1, ascq.FP4_E1M2)
+    mode = ascq.ROUND_RINT if round_mode is None else round_mode
     M = N = 8192
-    out_b = M * N // 2 if dst_type == ascq.FP4_E2M1 else M * N
+    out_b = M * N // 2 if fp4 else M * N
     ss = (M,) if policy == ascq.PER_TOKEN else ((M, N // g) if k_dim == 1 else (M // g, N))
     nbytes = 2 * M * N + out_b + 2 * int(np.prod(ss))
     R = rotation(nbytes)
@@ -393,16 +395,19 @@ def bench_quant_policy(torch, ascq, dst_type, policy, iters, k_dim=1, g=128):
     gen.manual_seed(5)
     xs = [torch.randn((M, N), generator=gen, device="cuda").half() for _ in range(R)]
     sc = torch.empty(ss, device="cuda").uniform_(0.5, 8.0, generator=gen).half()
-    shape = (M, N // 2) if dst_type == ascq.FP4_E2M1 else (M, N)
+    shape = (M, N // 2) if fp4 else (M, N)
     qs = [torch.empty(shape, dtype=torch.uint8, device="cuda") for _ in range(R)]
 
     def fn(i):
         ascq.ascend_quant_policy(xs[i % R], sc, policy, dst_type, g if policy == ascq.PER_GROUP else 0, k_dim=k_dim,
-                                 out=qs[i % R])
+                                 round_mode=mode, out=qs[i % R])
 
     ms = _time_loop(torch, fn, iters)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    name = {ascq.INT8: "int8", ascq.FP8_E4M3: "fp8_e4m3", ascq.FP4_E2M1: "E2M1"}[dst_type]
+    name = {ascq.INT8: "int8", ascq.FP8_E4M3: "fp8_e4m3", ascq.FP4_E2M1: "E2M1", ascq.FP4_E1M2: "E1M2"}[dst_type]
+    if round_mode is not None:
+        name += {ascq.ROUND_RINT: " rint", ascq.ROUND_FLOOR: " floor", ascq.ROUND_CEIL: " ceil",
+                 ascq.ROUND_ROUND: " round", ascq.ROUND_TRUNC: " trunc"}[round_mode]
     pol = "PER_TOKEN" if policy == ascq.PER_TOKEN else f"PER_GROUP g={g} kDim={k_dim}"
     return dict(workload=f"AscendQuant {pol} f16 [{M},{N}] -> {name} (f16 scales)", ms=ms, value=gbs, unit="GB/s",
                 frac_of_peak=gbs / HBM_PEAK_GBS)
@@ -414,10 +419,11 @@ def bench_antiquant_policy(torch, ascq, src_type, iters):
     M = N = 8192
     gen = torch.Generator(device="cuda")
     gen.manual_seed(6)
-    if src_type == ascq.FP4_E2M1:
+    if src_type in (ascq.FP4_E2M1, ascq.FP4_E1M2):
         g, sb, ss = 32, M * N // 2, (M, N // 32)
         sc = torch.randint(110, 140, ss, generator=gen, device="cuda", dtype=torch.int32).to(torch.uint8)
-        of, st, kd, dt, name = None, ascq.E8M0, 1, torch.bfloat16, "fp4 E2M1 (E8M0 scales, g=32 kDim=1) -> bf16"
+        fname = "E2M1" if src_type == ascq.FP4_E2M1 else "E1M2"
+        of, st, kd, dt, name = None, ascq.E8M0, 1, torch.bfloat16, f"fp4 {fname} (E8M0 scales, g=32 kDim=1) -> bf16"
         nbytes = sb + M * N // 32 + 2 * M * N
     else:
         g, sb, ss = 128, M * N, (M // 128, N)
@@ -510,7 +516,10 @@ OTHER = {
               lambda t, a: bench_antiquant_policy(t, a, a.FP4_E2M1, 50),lambda t, a: bench_quant_policy(t, a, a.INT8, a.PER_GROUP, 50),
               lambda t, a: bench_quant_policy(t, a, a.INT8, a.PER_GROUP, 50, k_dim=0),
               lambda t, a: bench_quant_policy(t, a, a.FP8_E4M3, a.PER_TOKEN, 50),
-              lambda t, a: bench_quant_policy(t, a, a.FP4_E2M1, a.PER_GROUP, 50)],
+              lambda t, a: bench_quant_policy(t, a, a.FP4_E2M1, a.PER_GROUP, 50),
+              lambda t, a: bench_quant_policy(t, a, a.FP4_E2M1, a.PER_GROUP, 50, round_mode=a.ROUND_FLOOR),
+              lambda t, a: bench_quant_policy(t, a, a.FP4_E1M2, a.PER_GROUP, 50),
+              lambda t, a: bench_antiquant_policy(t, a, a.FP4_E1M2, 50)],
     "w8a8": [lambda t, a: bench_w8a8(t, a, 128, 256, 512, 200), lambda t, a: bench_w8a8(t, a, 8192, 8192, 8192, 10)],
     "gemv": [lambda t, a, w=w, m=m: bench_gemv(t, a, getattr(a, w), m, 200)
              for w in ("INT4", "INT8") for m in (1, 16, 64)],
