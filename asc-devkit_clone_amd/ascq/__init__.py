@@ -30,6 +30,8 @@ ACT_NONE, ACT_FASTER_GELU = 0, 1
 PER_TENSOR, PER_CHANNEL, PER_TOKEN, PER_GROUP = range(4)
 # ascq_arith
 ARITH_F16, ARITH_F32 = 0, 1
+# ascq_dequant_mode (DeQuantMode)
+DEQUANT_SINGLE_ROW, DEQUANT_MULTI_ROW = 0, 1
 # ascq_format
 FORMAT_ND, FORMAT_PACKED = 0, 1
 
@@ -58,6 +60,11 @@ class _QuantParam(ctypes.Structure):
 
 class _DequantParam(ctypes.Structure):
     _fields_ = [("m", ctypes.c_uint32), ("n", ctypes.c_uint32), ("cal_count", ctypes.c_uint32)]
+
+
+class _DequantPolicyParam(ctypes.Structure):
+    _fields_ = [("m", ctypes.c_uint32), ("n", ctypes.c_uint32), ("cal_count", ctypes.c_uint32),
+                ("group_size", ctypes.c_uint32), ("has_offset", ctypes.c_int32), ("kdim", ctypes.c_int32)]
 
 
 class _MatmulTypes(ctypes.Structure):
@@ -119,7 +126,12 @@ SIGNATURES = {
     "ascq_ascend_quant_dynamic_per_token": (_I32, [_P, _P, _P, _I32, _U32, _U32, _I32, _P]),
     "ascq_ascend_quant_policy": (_I32, [_P, _I32, _P, _I32, _P, _P, _F32, _I32, _I32, ctypes.POINTER(_QuantParam), _P]),
     "ascq_ascend_quant": (_I32, [_P, _P, _I32, _P, _P, _U16, _U16, _U32, _U32, _P]),
-    "ascq_ascend_dequant": (_I32, [_P, _I32, _P, _I32, _P, _I32, _F32, _I32, ctypes.POINTER(_DequantParam), _P]),
+    "ascq_ascend_dequant": (_I32, [_P, _I32, _P, _I32, _P, _I32, _F32, _I32, _I32, ctypes.POINTER(_DequantParam),
+                                   _P]),
+    "ascq_ascend_dequant_dst_shape": (_I32, [_I32, _I32, ctypes.POINTER(_DequantParam), ctypes.POINTER(_U32),
+                                             ctypes.POINTER(_U32)]),
+    "ascq_ascend_dequant_policy": (_I32, [_P, _I32, _P, _I32, _P, _P, _I32, _I32, ctypes.POINTER(_DequantPolicyParam),
+                                          _P]),
     "ascq_ascend_antiquant": (_I32, [_P, _I32, _P, _I32, _P, _P, _U32, _U32, _U32, _I32, _I32, _P]),
     "ascq_ascend_antiquant_policy": (_I32, [_P, _I32, _P, _I32, _P, _P, _I32, _I32, ctypes.c_int64, ctypes.c_int64,
                                             ctypes.c_int64, _I32, _I32, _P]),
@@ -243,18 +255,54 @@ def ascend_quant(x: torch.Tensor, scale=None, offset=None, scale_scalar: float =
     return q
 
 
-def ascend_dequant(src: torch.Tensor, scale, policy: int, dst_dtype=torch.float16, cal_count=None,
-                   scale_scalar: float = 1.0, scale_type: int | None = None, out=None, stream=None):
-    """AscendDequant: dst = cast(f32(src) * scale); policy PER_CHANNEL / PER_TOKEN / PER_TENSOR."""
-    m, n = src.shape
+def _dtype_code(t) -> int:
+    return {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}[t]
+
+
+def dequant_dst_shape(dst_dtype, m: int, n: int, cal_count: int, mode: int = DEQUANT_SINGLE_ROW):
+    """(rows, row stride) of the legacy AscendDequant's dst after the DEQUANT_WITH_SINGLE_ROW rule"""
+    rows, ldd = _U32(), _U32()
+    p = _DequantParam(m, n, cal_count)
+    check(lib().ascq_ascend_dequant_dst_shape(_dtype_code(dst_dtype), mode, ctypes.byref(p), ctypes.byref(rows),
+                                              ctypes.byref(ldd)), "ascend_dequant_dst_shape")
+    return rows.value, ldd.value
+
+
+def ascend_dequant(src: torch.Tensor, scale, dst_dtype=torch.float16, cal_count=None, scale_scalar: float = 1.0,
+                   scale_type: int | None = None, mode: int = DEQUANT_SINGLE_ROW, m: int | None = None,
+                   n: int | None = None, out=None, stream=None):
+    """Legacy AscendDequant<dstT, scaleT, mode>(dst, src, deqScale, {m, n, calCount}): `scale` a deqScale tensor
+    (f32 / bf16, or int64 holding uint64 words) or None for the scalar `scale_scalar` (scale_type F32 or BF16).
+    Returns dst as [rows, row stride] (rows of n padded to 32 bytes; unwritten elements keep `out`'s values)."""
+    if m is None:
+        m, n = src.shape
+    cal = n if cal_count is None else cal_count
     src_type = {torch.int32: INT32, torch.int8: INT8}[src.dtype]
-    dst_type = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}[dst_dtype]
-    if scale_type is None and scale is not None:
-        scale_type = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.int64: U64}[scale.dtype]
+    dst_type = _dtype_code(dst_dtype)
+    if scale_type is None:
+        scale_type = F32 if scale is None else {torch.float32: F32, torch.bfloat16: BF16, torch.int64: U64}[scale.dtype]
+    rows, ldd = dequant_dst_shape(dst_dtype, m, n, cal, mode)
+    y = out if out is not None else torch.empty((rows, ldd), dtype=dst_dtype, device=src.device)
+    p = _DequantParam(m, n, cal)
+    check(lib().ascq_ascend_dequant(_ptr(y), dst_type, _ptr(src), src_type, _ptr(scale), scale_type,
+                                    float(scale_scalar), PER_TENSOR if scale is None else PER_CHANNEL, mode,
+                                    ctypes.byref(p), _stream(stream)), "ascend_dequant")
+    return y
+
+
+def ascend_dequant_policy(src: torch.Tensor, scale: torch.Tensor, policy: int, dst_dtype=torch.float16,
+                          group_size: int = 0, kdim: int = 1, cal_count=None, offset=None, out=None, stream=None):
+    """AscendDequant<dstT, srcT, scaleT, {hasOffset, kDim}, policy>(dst, src, scale, offset, {m, n, calCount,
+    groupSize}): PER_TOKEN (scale[row]) or PER_GROUP (kdim 1: scale[row][col / g]; kdim 0: scale[row / g][col])
+    on src [rows, n] int32 / f32 (or int8); scale f32 / f16 / bf16."""
+    m, n = src.shape
+    src_type = {torch.int32: INT32, torch.float32: F32, torch.int8: INT8}[src.dtype]
+    scale_type = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[scale.dtype]
     y = out if out is not None else torch.empty((m, n), dtype=dst_dtype, device=src.device)
-    p = _DequantParam(m, n, n if cal_count is None else cal_count)
-    check(lib().ascq_ascend_dequant(_ptr(y), dst_type, _ptr(src), src_type, _ptr(scale), scale_type or 0,
-                                    float(scale_scalar), policy, ctypes.byref(p), _stream(stream)), "ascend_dequant")
+    p = _DequantPolicyParam(m, n, m * n if cal_count is None else cal_count, group_size, int(offset is not None), kdim)
+    check(lib().ascq_ascend_dequant_policy(_ptr(y), _dtype_code(dst_dtype), _ptr(src), src_type, _ptr(scale),
+                                           _ptr(offset), scale_type, policy, ctypes.byref(p), _stream(stream)),
+          "ascend_dequant_policy")
     return y
 
 

@@ -759,29 +759,109 @@ ascq_status ascq_ascend_quant(int8_t* dst, const void* src, int32_t src_type, co
                       "ascend_quant");
 }
 
+// quant.hip's scale addressing codes (DQ_*)
+enum { DQ_SCALAR = 0, DQ_COL = 1, DQ_ROW = 2, DQ_GROUP_COL = 3, DQ_GROUP_ROW = 4 };
+
+ascq_status ascq_ascend_dequant_dst_shape(int32_t dst_type, int32_t mode, const ascq_dequant_param* params,
+                                          uint32_t* rows, uint32_t* row_stride)
+{
+    if (!params || !rows || !row_stride) return fail(ASCQ_E_INVALID_ARG, "ascend_dequant_dst_shape: null argument");
+    if (dst_type != ASCQ_DT_F16 && dst_type != ASCQ_DT_BF16 && dst_type != ASCQ_DT_F32)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant_dst_shape: dst must be f16, bf16 or f32");
+    if (mode != ASCQ_DEQUANT_SINGLE_ROW && mode != ASCQ_DEQUANT_MULTI_ROW)
+        return fail(ASCQ_E_INVALID_ARG, "ascend_dequant_dst_shape: bad DeQuantMode %d", mode);
+    uint32_t m = params->m, n = params->n;
+    const uint32_t blk = dst_type == ASCQ_DT_F32 ? 8u : 16u, cal = params->cal_count;  // dst elements per 32 bytes
+    // UpdateDequantParams (ascend_dequant_common_impl.h:208-223)
+    if (mode == ASCQ_DEQUANT_SINGLE_ROW && m == 1 && cal > 0 && cal % blk == 0 && n % cal == 0) {
+        m = n / cal;
+        n = cal;
+    }
+    *rows = m;
+    *row_stride = (n + blk - 1) / blk * blk;  // dstInner
+    return ASCQ_OK;
+}
+
 ascq_status ascq_ascend_dequant(void* dst, int32_t dst_type, const void* src, int32_t src_type, const void* scale,
-                                int32_t scale_type, float scale_scalar, int32_t policy,
+                                int32_t scale_type, float scale_scalar, int32_t policy, int32_t mode,
                                 const ascq_dequant_param* params, void* stream)
 {
-    if (!dst || !src || !params) return fail(ASCQ_E_INVALID_ARG, "ascend_dequant: null argument");
+    if (!params) return fail(ASCQ_E_INVALID_ARG, "ascend_dequant: null params");
     if (dst_type != ASCQ_DT_F16 && dst_type != ASCQ_DT_BF16 && dst_type != ASCQ_DT_F32)
         return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant: dst must be f16, bf16 or f32");
     if (src_type != ASCQ_DT_INT32 && src_type != ASCQ_DT_INT8)
-        return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant: src must be int32 or int8");
-    if (policy != ASCQ_POLICY_PER_TENSOR && policy != ASCQ_POLICY_PER_CHANNEL && policy != ASCQ_POLICY_PER_TOKEN)
-        return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant: policy must be per-tensor, per-channel or per-token");
-    if (policy != ASCQ_POLICY_PER_TENSOR) {
-        if (!scale) return fail(ASCQ_E_INVALID_ARG, "ascend_dequant: null scale");
-        if (scale_type != ASCQ_DT_F32 && scale_type != ASCQ_DT_F16 && scale_type != ASCQ_DT_BF16 &&
-            scale_type != ASCQ_DT_U64)
-            return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant: scale must be f32, f16, bf16 or u64");
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant: src must be int32 (or int8)");
+    if (policy != ASCQ_POLICY_PER_TENSOR && policy != ASCQ_POLICY_PER_CHANNEL)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant: the legacy form takes a deqScale tensor (PER_CHANNEL) or a "
+                                        "scalar (PER_TENSOR); PER_TOKEN / PER_GROUP are ascq_ascend_dequant_policy");
+    if (mode != ASCQ_DEQUANT_SINGLE_ROW && mode != ASCQ_DEQUANT_MULTI_ROW)
+        return fail(ASCQ_E_INVALID_ARG, "ascend_dequant: bad DeQuantMode %d", mode);
+    // IsTemplateValid (ascend_dequant_common_impl.h:126-155)
+    const bool tensor = policy == ASCQ_POLICY_PER_CHANNEL;
+    const int32_t s = scale_type, d = dst_type;
+    const bool ok = tensor ? ((s == ASCQ_DT_U64 && d == ASCQ_DT_F16) || (s == ASCQ_DT_F32 && d == ASCQ_DT_F32) ||
+                              (s == ASCQ_DT_BF16 && d == ASCQ_DT_F32) || (s == ASCQ_DT_BF16 && d == ASCQ_DT_BF16) ||
+                              (s == ASCQ_DT_F32 && d == ASCQ_DT_BF16))
+                           : ((s == ASCQ_DT_BF16 || s == ASCQ_DT_F32) && (d == ASCQ_DT_BF16 || d == ASCQ_DT_F32));
+    if (!ok)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant: deqScale type %d with dst type %d is not a combination the "
+                                        "reference accepts", s, d);
+    // the reference's CPU-debug checks (dequant_check_common.h)
+    if (params->n % 8 != 0) return fail(ASCQ_E_INVALID_ARG, "ascend_dequant: params.n must be divisible by 8");
+    if (params->cal_count == 0 || params->cal_count > params->n)
+        return fail(ASCQ_E_INVALID_ARG, "ascend_dequant: params.calCount must be in (0, n]");
+    if (params->m == 0) return ASCQ_OK;
+    if (!dst || !src || (tensor && !scale)) return fail(ASCQ_E_INVALID_ARG, "ascend_dequant: null argument");
+    uint32_t rows = 0, ldd = 0;
+    ascq_status st = ascq_ascend_dequant_dst_shape(dst_type, mode, params, &rows, &ldd);
+    if (st != ASCQ_OK) return st;
+    const uint32_t n = rows == params->m ? params->n : params->cal_count;
+    if ((uint64_t)rows * ldd >= (1ull << 40)) return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant: tensor too large");
+    float ss = scale_scalar;
+    if (!tensor && scale_type == ASCQ_DT_BF16) {  // the scalar is a bfloat16_t value
+        uint32_t u;
+        std::memcpy(&u, &ss, 4);
+        if ((u & 0x7fffffffu) <= 0x7f800000u) u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+        std::memcpy(&ss, &u, 4);
     }
-    if (policy == ASCQ_POLICY_PER_CHANNEL && params->cal_count > params->n)
-        return fail(ASCQ_E_INVALID_ARG, "ascend_dequant: calCount must not exceed n");
-    if (params->m == 0 || params->n == 0) return ASCQ_OK;
-    return hip_status(ascq::launch_dequant(dst, dst_type, src, src_type, scale, scale_type, scale_scalar, policy,
-                                           params->m, params->n, params->cal_count, S(stream)),
+    return hip_status(ascq::launch_dequant(dst, dst_type, src, src_type, scale, scale_type, ss,
+                                           tensor ? DQ_COL : DQ_SCALAR, rows, params->cal_count, n, ldd, 0,
+                                           S(stream)),
                       "ascend_dequant");
+}
+
+ascq_status ascq_ascend_dequant_policy(void* dst, int32_t dst_type, const void* src, int32_t src_type,
+                                       const void* scale, const void* offset, int32_t scale_type, int32_t policy,
+                                       const ascq_dequant_policy_param* para, void* stream)
+{
+    (void)offset;  // never read by the reference's policy kernels (ascend_dequant_3510_impl.h:254-598)
+    if (!para) return fail(ASCQ_E_INVALID_ARG, "ascend_dequant_policy: null argument");
+    if (dst_type != ASCQ_DT_F16 && dst_type != ASCQ_DT_BF16 && dst_type != ASCQ_DT_F32)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant_policy: dst must be f16, bf16 or f32");
+    if (src_type != ASCQ_DT_INT32 && src_type != ASCQ_DT_F32 && src_type != ASCQ_DT_INT8)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant_policy: src must be int32 or f32 (or int8)");
+    if (scale_type != ASCQ_DT_F16 && scale_type != ASCQ_DT_BF16 && scale_type != ASCQ_DT_F32)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant_policy: scale must be f16, bf16 or f32");
+    if (policy != ASCQ_POLICY_PER_TOKEN && policy != ASCQ_POLICY_PER_GROUP)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant_policy: policy must be PER_TOKEN or PER_GROUP");
+    if (policy == ASCQ_POLICY_PER_GROUP) {
+        if (para->kdim != 0 && para->kdim != 1) return fail(ASCQ_E_INVALID_ARG, "ascend_dequant_policy: kdim must be 0 or 1");
+        if (para->group_size == 0 || para->group_size % 32 != 0)
+            return fail(ASCQ_E_INVALID_ARG, "ascend_dequant_policy: group_size must be a positive multiple of 32");
+    }
+    if (para->n == 0) return fail(ASCQ_E_INVALID_ARG, "ascend_dequant_policy: n must be positive");
+    const uint32_t rows = para->cal_count / para->n;
+    if (rows == 0) return ASCQ_OK;  // calCount < n: nothing to do (empty tensors may carry null pointers)
+    if (!dst || !src || !scale) return fail(ASCQ_E_INVALID_ARG, "ascend_dequant_policy: null argument");
+    int smode = DQ_ROW;
+    uint32_t group = 0;
+    if (policy == ASCQ_POLICY_PER_GROUP) {
+        smode = para->kdim == 1 ? DQ_GROUP_COL : DQ_GROUP_ROW;
+        group = para->group_size;
+    }
+    return hip_status(ascq::launch_dequant(dst, dst_type, src, src_type, scale, scale_type, 0.0f, smode, rows, para->n,
+                                           para->n, para->n, group, S(stream)),
+                      "ascend_dequant_policy");
 }
 
 ascq_status ascq_ascend_antiquant(void* dst, int32_t dst_type, const void* src, int32_t src_type, const void* offset,

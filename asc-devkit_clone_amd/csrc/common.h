@@ -185,6 +185,20 @@ __device__ __forceinline__ uint32_t pack4_s8(int32_t a, int32_t b, int32_t c, in
            ((uint32_t)(d & 0xff) << 24);
 }
 
+// int32 -> fp32 with ties away from zero (the AscendDequant kernels' Cast<float, int32_t, MrgZRndA>, CAST_ROUND):
+// exact below 2^24; above, the magnitude's 24-bit significand is rounded half up (add half of the dropped range,
+// truncate) and the result converts exactly
+__device__ __forceinline__ float i32_to_f32_rna(int32_t v)
+{
+    uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
+    const int s = 8 - (int)__builtin_clz(a | 1u);  // bits below the 24-bit significand (<= 0: none)
+    if (s > 0) a = ((a + (1u << (s - 1))) >> s) << s;
+    const float f = (float)a;
+    return v < 0 ? -f : f;
+}
+// |v| > 2^24: the only values whose nearest-even conversion (float)v can differ from i32_to_f32_rna
+__device__ __forceinline__ bool i32_beyond_f32_exact(int32_t v) { return (uint32_t)v + (1u << 24) > (2u << 24); }
+
 // store an fp32 value as dtype (F16 / BF16 / F32), rne + sat
 __device__ __forceinline__ void store_cast(void* p, int64_t i, float v, int dtype)
 {
@@ -205,6 +219,19 @@ __device__ __forceinline__ float load_f32_of(const void* p, int64_t i, int dtype
     default: return 0.0f;
     }
 }
+
+// Division by a runtime-constant divisor d (1 <= d < 2^31) for dividends below 2^31: n / d = (umulhi(n, m) + n) >> s
+// with s = ceil(log2 d) and m = floor(2^32 (2^s - d) / d) + 1 (the round-up multiplier method)
+struct FastDiv {
+    uint32_t m, s;
+};
+static inline FastDiv fast_div(uint32_t d)
+{
+    uint32_t s = 0;
+    while ((1ull << s) < d) ++s;
+    return FastDiv{(uint32_t)(((1ull << 32) * ((1ull << s) - d)) / d + 1), s};
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) { return (__umulhi(n, f.m) + n) >> f.s; }
 
 // wave64 reductions
 __device__ __forceinline__ float wave_max(float v)

@@ -53,8 +53,12 @@ hipError_t launch_quant_dynamic_per_token(int8_t* q, float* scale_out, const voi
 hipError_t launch_quant_legacy(int8_t* q, const void* x, int src_type, const uint16_t* scale, const uint16_t* offset,
                                uint16_t scale_scalar, uint16_t offset_scalar, uint32_t cal_count,
                                uint32_t scale_count, hipStream_t st);
+// AscendDequant, both forms: rows x cols computed elements at source row stride n and destination row stride ldd;
+// smode picks the scale addressing (quant.hip DQ_*: scalar, per column, per row, per group along the row with
+// `group` columns, per group down the columns with `group` rows)
 hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
-                          float scale_scalar, int policy, uint32_t m, uint32_t n, uint32_t cal_count, hipStream_t st);
+                          float scale_scalar, int smode, uint32_t rows, uint32_t cols, uint32_t n, uint32_t ldd,
+                          uint32_t group, hipStream_t st);
 hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale,
                                    const void* offset, int scale_type, int per_token, int64_t m, int64_t n,
                                    int64_t g, int col_groups, int is_transpose, hipStream_t st);

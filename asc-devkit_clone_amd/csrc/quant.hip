@@ -168,21 +168,56 @@ __global__ __launch_bounds__(256) void dequant_i8_token_f16_kernel(const u32x2* 
     }
 }
 
-// Generic: policy PER_CHANNEL (j < cal_count uses scale[j]), PER_TOKEN (scale[i]), PER_TENSOR (scalar).
-__global__ __launch_bounds__(256) void dequant_generic_kernel(void* __restrict__ y, int dst_type,
-                                                              const void* __restrict__ src, int src_type,
-                                                              const void* __restrict__ scale, int scale_type,
-                                                              float scale_scalar, int policy, uint32_t m, uint32_t n,
-                                                              uint32_t cols)
+// Scale addressing of the dequant kernels (DequantArgs::smode): one scalar; scale[c] (legacy deqScale tensor);
+// scale[r] (PER_TOKEN); scale[r][c / g] over [rows][sk] (PER_GROUP kDim 1); scale[r / g][c] over
+// [ceil(rows / g)][n] (PER_GROUP kDim 0).
+enum : int { DQ_SCALAR = 0, DQ_COL = 1, DQ_ROW = 2, DQ_GROUP_COL = 3, DQ_GROUP_ROW = 4 };
+
+struct DequantArgs {
+    void* y;
+    const void* src;
+    const void* scale;
+    float scale_scalar;
+    int scale_type;       // DT_F32 / DT_F16 / DT_BF16 / DT_U64 (low 32 bits as fp32)
+    uint32_t rows, cols;  // computed block: rows x cols (cols = calCount of the legacy form, else n)
+    uint32_t n, ldd;      // source and destination row strides (elements)
+    uint32_t group, sk;   // PER_GROUP group size; scales per row for DQ_GROUP_COL
+    uint32_t units, upr;  // vector kernel: work units and units per row band
+    FastDiv upr_div, g_div;
+};
+
+__device__ __forceinline__ float dq_src_f32(const void* p, int64_t i, int src_type)
 {
-    const int64_t total = (int64_t)m * cols;
+    if (src_type == DT_INT32) return i32_to_f32_rna(((const int32_t*)p)[i]);
+    if (src_type == DT_INT8) return (float)((const int8_t*)p)[i];
+    return ((const float*)p)[i];
+}
+
+__device__ __forceinline__ float dq_scale_at(const void* s, int64_t i, int type)
+{
+    switch (type) {
+    case DT_F16: return f16_to_f32(((const uint16_t*)s)[i]);
+    case DT_BF16: return bf16_to_f32(((const uint16_t*)s)[i]);
+    case DT_U64: return __uint_as_float(((const uint32_t*)s)[2 * i]);
+    default: return ((const float*)s)[i];
+    }
+}
+
+// Any shape or alignment: one thread per computed element, 64-bit indices.
+__global__ __launch_bounds__(256) void dequant_generic_kernel(DequantArgs a, int dst_type, int src_type, int smode)
+{
+    const int64_t total = (int64_t)a.rows * a.cols;
     for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
-        int64_t i = t / cols, j = t % cols;
-        float s = policy == 1 ? load_f32_of(scale, j, scale_type)
-                              : (policy == 2 ? load_f32_of(scale, i, scale_type) : scale_scalar);
-        int64_t idx = i * n + j;
-        float v = load_f32_of(src, idx, src_type) * s;
-        store_cast(y, idx, v, dst_type);
+        const int64_t i = t / a.cols, j = t % a.cols;
+        float s;
+        switch (smode) {
+        case DQ_COL: s = dq_scale_at(a.scale, j, a.scale_type); break;
+        case DQ_ROW: s = dq_scale_at(a.scale, i, a.scale_type); break;
+        case DQ_GROUP_COL: s = dq_scale_at(a.scale, i * a.sk + j / a.group, a.scale_type); break;
+        case DQ_GROUP_ROW: s = dq_scale_at(a.scale, (i / a.group) * a.n + j, a.scale_type); break;
+        default: s = a.scale_scalar; break;
+        }
+        store_cast(a.y, i * a.ldd + j, dq_src_f32(a.src, i * a.n + j, src_type) * s, dst_type);
     }
 }
 
@@ -328,16 +363,6 @@ enum : int { QL_TOKEN = 0, QL_KCOL = 1, QL_KROW = 2 };
 // Unsigned division by a runtime constant d for dividends below 2^31: s = ceil(log2 d),
 // m = floor(2^32 (2^s - d) / d) + 1, q = (mulhi(n, m) + n) >> s (Granlund & Montgomery, "Division by invariant
 // integers using multiplication", PLDI 1994, section 4).
-struct FastDiv {
-    uint32_t m, s;
-};
-static FastDiv fast_div(uint32_t d)
-{
-    uint32_t s = 0;
-    while ((1ull << s) < d) ++s;
-    return FastDiv{(uint32_t)(((1ull << 32) * ((1ull << s) - d)) / d + 1), s};
-}
-__device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) { return (__umulhi(n, f.m) + n) >> f.s; }
 
 struct QuantPolicyArgs {
     void* dst;
@@ -758,65 +783,112 @@ hipError_t launch_quant_legacy(int8_t* q, const void* x, int src_type, const uin
     return hipGetLastError();
 }
 
-// AscendDequant, vector path for an f32 scale (per channel, per token or per tensor), int32 / int8 source and
-// f16 / bf16 / f32 output: rows of `cols` computed elements (cal_count per channel, else n) at a row stride of n.
-// A unit is UE consecutive columns of one row -- 4 int32 or 8 int8, one 16- or 8-byte load, so every load (and
-// store) instruction of a wave covers one contiguous span.  A lane takes the same UE columns of RB consecutive
-// rows: their per-channel scales are loaded once and all source loads are issued before converting.  Needs cols
-// and n multiples of UE and aligned pointers.  dst = cast(f32(src) * scale), cast rne + saturating (store_cast).
-template <int SRC, int DST, int POL>
-__global__ __launch_bounds__(256) void dequant_vec_kernel(void* __restrict__ y, const void* __restrict__ src,
-                                                          const float* __restrict__ scale, float scale_scalar,
-                                                          uint32_t units, uint32_t rows, uint32_t upr, uint32_t n,
-                                                          FastDiv upr_div)
+// AscendDequant, vector path: rows of `cols` computed elements at a source row stride of n and a destination row
+// stride of ldd (the legacy form's 32-byte padded rows, or n).  A unit is UE consecutive columns of RB
+// consecutive rows: UE = 4 for 4-byte sources (int32 / fp32: one 16-byte load per row), 8 for int8 (one 8-byte
+// load), so every load and store instruction of a wave covers contiguous spans.  The UE scales of a unit are
+// loaded once for its RB rows (per column, or per column of a row group: the groups are multiples of 32 rows, so
+// RB rows never straddle one), and all RB source loads are issued before converting.  An int32 source converts
+// with ties away from zero: the plain conversion is exact up to 2^24, so the unit takes the slower exact path only
+// when one of its values lies beyond (one wave-uniform branch per unit).  dst = cast(f32(src) * scale), rne +
+// saturating (store_cast semantics).
+template <int UE>
+__device__ __forceinline__ void dq_scale_vec(const void* s, int64_t i0, int type, float (&o)[UE])
 {
-    constexpr int UE = SRC == DT_INT32 ? 4 : 8;   // elements per unit
-    constexpr int RB = SRC == DT_INT32 ? 8 : 4;   // rows per lane
-    for (uint32_t v = blockIdx.x * 256u + threadIdx.x; v < units; v += gridDim.x * 256u) {
-        const uint32_t rb = fdiv(v, upr_div), w = v - rb * upr, r0 = rb * RB;
-        float sc[UE];
-        if constexpr (POL == 1) {  // per channel
-            const u32x4 a = *(const u32x4*)(scale + UE * w);
-            sc[0] = __uint_as_float(a.x), sc[1] = __uint_as_float(a.y), sc[2] = __uint_as_float(a.z);
-            sc[3] = __uint_as_float(a.w);
-            if constexpr (UE == 8) {
-                const u32x4 b = *(const u32x4*)(scale + UE * w + 4);
-                sc[4] = __uint_as_float(b.x), sc[5] = __uint_as_float(b.y), sc[6] = __uint_as_float(b.z);
-                sc[7] = __uint_as_float(b.w);
-            }
+    // i0 is a multiple of UE and s is 16-byte aligned, so every load below is naturally aligned
+    if (type == DT_F32) {
+#pragma unroll
+        for (int q = 0; q < UE / 4; ++q) {
+            const u32x4 a = *((const u32x4*)((const float*)s + i0) + q);
+            o[4 * q] = __uint_as_float(a.x), o[4 * q + 1] = __uint_as_float(a.y);
+            o[4 * q + 2] = __uint_as_float(a.z), o[4 * q + 3] = __uint_as_float(a.w);
         }
+    } else if (type == DT_U64) {
+#pragma unroll
+        for (int q = 0; q < UE / 2; ++q) {
+            const u32x4 a = *((const u32x4*)((const uint64_t*)s + i0) + q);
+            o[2 * q] = __uint_as_float(a.x), o[2 * q + 1] = __uint_as_float(a.z);
+        }
+    } else {
+        uint32_t w[UE / 2];
+        if constexpr (UE == 4) {
+            const u32x2 a = *(const u32x2*)((const uint16_t*)s + i0);
+            w[0] = a.x, w[1] = a.y;
+        } else {
+            const u32x4 a = *(const u32x4*)((const uint16_t*)s + i0);
+            w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w;
+        }
+#pragma unroll
+        for (int q = 0; q < UE / 2; ++q) {
+            o[2 * q] = type == DT_BF16 ? bf16_to_f32((uint16_t)w[q]) : f16_to_f32((uint16_t)w[q]);
+            o[2 * q + 1] = type == DT_BF16 ? bf16_to_f32((uint16_t)(w[q] >> 16)) : f16_to_f32((uint16_t)(w[q] >> 16));
+        }
+    }
+}
+
+template <int SRC, int DST, int SM>
+__global__ __launch_bounds__(256) void dequant_vec_kernel(DequantArgs a)
+{
+    constexpr int UE = SRC == DT_INT8 ? 8 : 4;  // elements per unit row
+    constexpr int RB = SRC == DT_INT8 ? 4 : 8;  // rows per unit
+    for (uint32_t v = blockIdx.x * 256u + threadIdx.x; v < a.units; v += gridDim.x * 256u) {
+        const uint32_t rb = fdiv(v, a.upr_div), w = v - rb * a.upr, r0 = rb * RB, c0 = UE * w;
+        float sc[UE];
+        if constexpr (SM == DQ_COL) dq_scale_vec<UE>(a.scale, c0, a.scale_type, sc);
+        if constexpr (SM == DQ_GROUP_ROW) dq_scale_vec<UE>(a.scale, (int64_t)fdiv(r0, a.g_div) * a.n + c0, a.scale_type, sc);
         uint32_t xw[RB][UE == 4 ? 4 : 2];
         float st[RB];
 #pragma unroll
         for (int k = 0; k < RB; ++k) {
-            const uint32_t r = r0 + k < rows ? r0 + k : rows - 1u;  // past the last row: reload it, store nothing
-            const int64_t e = (int64_t)r * n + UE * (int64_t)w;
-            if constexpr (SRC == DT_INT32) {
-                const u32x4 a = __builtin_nontemporal_load((const u32x4*)((const int32_t*)src + e));
-                xw[k][0] = a.x, xw[k][1] = a.y, xw[k][2] = a.z, xw[k][3] = a.w;
+            const uint32_t r = r0 + k < a.rows ? r0 + k : a.rows - 1u;  // past the last row: reload it, store nothing
+            const int64_t e = (int64_t)r * a.n + c0;
+            if constexpr (SRC == DT_INT8) {
+                const u32x2 x = __builtin_nontemporal_load((const u32x2*)((const int8_t*)a.src + e));
+                xw[k][0] = x.x, xw[k][1] = x.y;
             } else {
-                const u32x2 a = __builtin_nontemporal_load((const u32x2*)((const int8_t*)src + e));
-                xw[k][0] = a.x, xw[k][1] = a.y;
+                const u32x4 x = __builtin_nontemporal_load((const u32x4*)((const uint32_t*)a.src + e));
+                xw[k][0] = x.x, xw[k][1] = x.y, xw[k][2] = x.z, xw[k][3] = x.w;
             }
-            st[k] = POL == 2 ? scale[r] : scale_scalar;
+            if constexpr (SM == DQ_ROW) st[k] = dq_scale_at(a.scale, r, a.scale_type);
+            else if constexpr (SM == DQ_GROUP_COL) st[k] = dq_scale_at(a.scale, (int64_t)r * a.sk + fdiv(c0, a.g_div), a.scale_type);
+            else st[k] = a.scale_scalar;
+        }
+        float x[RB][UE];
+        bool beyond = false;
+#pragma unroll
+        for (int k = 0; k < RB; ++k)
+#pragma unroll
+            for (int j = 0; j < UE; ++j) {
+                if constexpr (SRC == DT_INT32) {
+                    x[k][j] = (float)(int32_t)xw[k][j];
+                    beyond |= i32_beyond_f32_exact((int32_t)xw[k][j]);
+                } else if constexpr (SRC == DT_F32) {
+                    x[k][j] = __uint_as_float(xw[k][j]);
+                } else {
+                    x[k][j] = (float)(int8_t)((xw[k][j >> 2] >> (8 * (j & 3))) & 0xffu);
+                }
+            }
+        if constexpr (SRC == DT_INT32) {
+            if (beyond) {
+#pragma unroll
+                for (int k = 0; k < RB; ++k)
+#pragma unroll
+                    for (int j = 0; j < UE; ++j) x[k][j] = i32_to_f32_rna((int32_t)xw[k][j]);
+            }
         }
 #pragma unroll
         for (int k = 0; k < RB; ++k) {
-            if (r0 + k >= rows) break;
+            if (r0 + k >= a.rows) break;
             float o[UE];
 #pragma unroll
-            for (int j = 0; j < UE; ++j) {
-                const float x = SRC == DT_INT32 ? (float)(int32_t)xw[k][j]
-                                                : (float)(int8_t)((xw[k][j >> 2] >> (8 * (j & 3))) & 0xffu);
-                o[j] = x * (POL == 1 ? sc[j] : st[k]);
-            }
-            const int64_t e = (int64_t)(r0 + k) * n + UE * (int64_t)w;
+            for (int j = 0; j < UE; ++j) o[j] = x[k][j] * ((SM == DQ_COL || SM == DQ_GROUP_ROW) ? sc[j] : st[k]);
+            const int64_t e = (int64_t)(r0 + k) * a.ldd + c0;
             if constexpr (DST == DT_F32) {
 #pragma unroll
                 for (int q = 0; q < UE / 4; ++q)
                     __builtin_nontemporal_store((u32x4){__float_as_uint(o[4 * q]), __float_as_uint(o[4 * q + 1]),
                                                         __float_as_uint(o[4 * q + 2]), __float_as_uint(o[4 * q + 3])},
-                                                (u32x4*)((float*)y + e) + q);
+                                                (u32x4*)((float*)a.y + e) + q);
             } else {
                 uint32_t h[UE / 2];
 #pragma unroll
@@ -825,54 +897,46 @@ __global__ __launch_bounds__(256) void dequant_vec_kernel(void* __restrict__ y, 
                     const uint32_t hi = DST == DT_BF16 ? f32_to_bf16_sat(o[2 * q + 1]) : f32_to_f16_sat(o[2 * q + 1]);
                     h[q] = lo | (hi << 16);
                 }
-                if constexpr (UE == 4) __builtin_nontemporal_store((u32x2){h[0], h[1]}, (u32x2*)((uint16_t*)y + e));
-                else __builtin_nontemporal_store((u32x4){h[0], h[1], h[2], h[3]}, (u32x4*)((uint16_t*)y + e));
+                if constexpr (UE == 4) __builtin_nontemporal_store((u32x2){h[0], h[1]}, (u32x2*)((uint16_t*)a.y + e));
+                else __builtin_nontemporal_store((u32x4){h[0], h[1], h[2], h[3]}, (u32x4*)((uint16_t*)a.y + e));
             }
         }
     }
 }
 
 template <int SRC, int DST>
-static void launch_dequant_vec(void* y, const void* src, const float* scale, float ss, int policy, uint32_t rows,
-                               uint32_t cols, uint32_t n, hipStream_t st)
+static void launch_dequant_vec(DequantArgs a, int smode, hipStream_t st)
 {
-    constexpr uint32_t UE = SRC == DT_INT32 ? 4 : 8, RB = SRC == DT_INT32 ? 8 : 4;
-    const uint32_t upr = cols / UE, units = (rows + RB - 1) / RB * upr;
-    const dim3 grid(grid_for(units)), block(256);
-    const FastDiv d = fast_div(upr);
-    if (policy == 1) launch_k(dequant_vec_kernel<SRC, DST, 1>, grid, block, 0, st, y, src, scale, ss, units, rows, upr, n, d);
-    else if (policy == 2) launch_k(dequant_vec_kernel<SRC, DST, 2>, grid, block, 0, st, y, src, scale, ss, units, rows, upr, n, d);
-    else launch_k(dequant_vec_kernel<SRC, DST, 0>, grid, block, 0, st, y, src, scale, ss, units, rows, upr, n, d);
+    const dim3 grid(grid_for(a.units)), block(256);
+    switch (smode) {
+    case DQ_COL: launch_k(dequant_vec_kernel<SRC, DST, DQ_COL>, grid, block, 0, st, a); break;
+    case DQ_ROW: launch_k(dequant_vec_kernel<SRC, DST, DQ_ROW>, grid, block, 0, st, a); break;
+    case DQ_GROUP_COL: launch_k(dequant_vec_kernel<SRC, DST, DQ_GROUP_COL>, grid, block, 0, st, a); break;
+    case DQ_GROUP_ROW: launch_k(dequant_vec_kernel<SRC, DST, DQ_GROUP_ROW>, grid, block, 0, st, a); break;
+    default: launch_k(dequant_vec_kernel<SRC, DST, DQ_SCALAR>, grid, block, 0, st, a); break;
+    }
 }
 
-// dispatch of the vector path; false when the shape or alignment needs the per-element kernel
-static bool dequant_vec(void* y, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
-                        float ss, int policy, uint32_t m, uint32_t n, uint32_t cols, hipStream_t st)
+template <int SRC>
+static void launch_dequant_vec_dst(DequantArgs a, int dst_type, int smode, hipStream_t st)
 {
-    const uint32_t ue = src_type == DT_INT32 ? 4 : 8;  // elements per unit
-    if (policy != 0 && scale_type != DT_F32) return false;
-    if (cols % ue != 0 || n % ue != 0 || m == 0 || cols == 0 || (uint64_t)m * n >= (1ull << 31)) return false;
-    if ((uintptr_t)src % (src_type == DT_INT32 ? 16 : 8) != 0) return false;
-    if ((uintptr_t)y % (dst_type == DT_F32 ? 16 : 2 * ue) != 0) return false;
-    if (policy == 1 && (uintptr_t)scale % 16 != 0) return false;
-    const float* sc = (const float*)scale;
-    if (src_type == DT_INT32) {
-        if (dst_type == DT_F16) launch_dequant_vec<DT_INT32, DT_F16>(y, src, sc, ss, policy, m, cols, n, st);
-        else if (dst_type == DT_BF16) launch_dequant_vec<DT_INT32, DT_BF16>(y, src, sc, ss, policy, m, cols, n, st);
-        else launch_dequant_vec<DT_INT32, DT_F32>(y, src, sc, ss, policy, m, cols, n, st);
-    } else {
-        if (dst_type == DT_F16) launch_dequant_vec<DT_INT8, DT_F16>(y, src, sc, ss, policy, m, cols, n, st);
-        else if (dst_type == DT_BF16) launch_dequant_vec<DT_INT8, DT_BF16>(y, src, sc, ss, policy, m, cols, n, st);
-        else launch_dequant_vec<DT_INT8, DT_F32>(y, src, sc, ss, policy, m, cols, n, st);
-    }
-    return true;
+    if (dst_type == DT_F16) launch_dequant_vec<SRC, DT_F16>(a, smode, st);
+    else if (dst_type == DT_BF16) launch_dequant_vec<SRC, DT_BF16>(a, smode, st);
+    else launch_dequant_vec<SRC, DT_F32>(a, smode, st);
 }
 
 hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
-                          float scale_scalar, int policy, uint32_t m, uint32_t n, uint32_t cal_count, hipStream_t st)
+                          float scale_scalar, int smode, uint32_t rows, uint32_t cols, uint32_t n, uint32_t ldd,
+                          uint32_t group, hipStream_t st)
 {
-    const bool fast = policy == 2 && src_type == DT_INT8 && dst_type == DT_F16 && scale_type == DT_F32 &&
-                      n % 8 == 0 && ((uintptr_t)src % 8 == 0) && ((uintptr_t)y % 16 == 0) && m > 0 && n > 0;
+    (void)hipGetLastError();  // clear a stale error so the status below is this launch's
+    DequantArgs a{};
+    a.y = y, a.src = src, a.scale = scale, a.scale_scalar = scale_scalar, a.scale_type = scale_type;
+    a.rows = rows, a.cols = cols, a.n = n, a.ldd = ldd, a.group = group;
+    a.sk = group ? (n + group - 1) / group : 0;
+    a.g_div = fast_div(group ? group : 1u);
+    const bool fast = smode == DQ_ROW && src_type == DT_INT8 && dst_type == DT_F16 && scale_type == DT_F32 &&
+                      cols == n && ldd == n && n % 8 == 0 && ((uintptr_t)src % 8 == 0) && ((uintptr_t)y % 16 == 0);
     if (fast) {
         // measured at 8192 x 8192: U = 1 34.9 us, 2 34.1 us, 4 36.1 us (unconditional loads); 16-element units (one
         // 16-byte load, two 16-byte stores per lane) 34.9 us at U = 1 and slower above, as each store instruction
@@ -880,18 +944,32 @@ hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, 
         constexpr int U = 2;
         const uint32_t upr = n / 8;
         const uint32_t segs = (upr + 256 * U - 1) / (256 * U);
-        const uint64_t blocks = (uint64_t)m * segs;
+        const uint64_t blocks = (uint64_t)rows * segs;
         if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
-        launch_k(dequant_i8_token_f16_kernel<U>, dim3((unsigned)blocks), dim3(256), 0, st,
-                           (const u32x2*)src, (const float*)scale, (u32x4*)y, upr, segs);
+        launch_k(dequant_i8_token_f16_kernel<U>, dim3((unsigned)blocks), dim3(256), 0, st, (const u32x2*)src,
+                 (const float*)scale, (u32x4*)y, upr, segs);
         return hipGetLastError();
     }
-    uint32_t cols = policy == 1 ? cal_count : n;
-    if (dequant_vec(y, dst_type, src, src_type, scale, scale_type, scale_scalar, policy, m, n, cols, st))
+    const uint32_t ue = src_type == DT_INT8 ? 8 : 4, rb = src_type == DT_INT8 ? 4 : 8;
+    const int esz = dst_type == DT_F32 ? 4 : 2;
+    const int ssz = scale_type == DT_F32 ? 4 : (scale_type == DT_U64 ? 8 : 2);
+    const bool vec_scale = smode == DQ_COL || smode == DQ_GROUP_ROW;
+    const bool vec = cols % ue == 0 && n % ue == 0 && ldd % ue == 0 && cols > 0 && rows > 0 &&
+                     (uint64_t)rows * n < (1ull << 31) && (uint64_t)rows * ldd < (1ull << 31) &&
+                     (uintptr_t)src % (src_type == DT_INT8 ? 8 : 16) == 0 &&
+                     (uintptr_t)y % (ue * esz > 16 ? 16 : ue * esz) == 0 &&
+                     (!vec_scale || (uintptr_t)scale % 16 == 0) && (group == 0 || group % 32 == 0) && ssz > 0;
+    if (vec) {
+        a.upr = cols / ue;
+        a.units = (rows + rb - 1) / rb * a.upr;
+        a.upr_div = fast_div(a.upr);
+        if (src_type == DT_INT32) launch_dequant_vec_dst<DT_INT32>(a, dst_type, smode, st);
+        else if (src_type == DT_INT8) launch_dequant_vec_dst<DT_INT8>(a, dst_type, smode, st);
+        else launch_dequant_vec_dst<DT_F32>(a, dst_type, smode, st);
         return hipGetLastError();
-    dim3 grid(grid_for((int64_t)m * cols)), block(256);
-    launch_k(dequant_generic_kernel, grid, block, 0, st, y, dst_type, src, src_type, scale, scale_type,
-                       scale_scalar, policy, m, n, cols);
+    }
+    dim3 grid(grid_for((int64_t)rows * cols)), block(256);
+    launch_k(dequant_generic_kernel, grid, block, 0, st, a, dst_type, src_type, smode);
     return hipGetLastError();
 }
 

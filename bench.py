@@ -129,7 +129,7 @@ def bench_headline(torch, ascq, steps, warmup):
         ascq.quant_dynamic_per_token(xs[r], out=qs[r], scale_out=ss[r])
         if kev is not None and j in di:
             kev.arm(2 * j + 1)
-        ascq.ascend_dequant(qs[r], ss[r], ascq.PER_TOKEN, torch.float16, out=ys[r])
+        ascq.ascend_dequant_policy(qs[r], ss[r], ascq.PER_TOKEN, torch.float16, out=ys[r])
 
     for i in range(warmup):
         step(i)
@@ -167,7 +167,7 @@ def cpu_baseline_headline(budget_s=10.0):
     while reps < 2 or spent < budget_s:
         t0 = time.perf_counter()
         q, s = O.quant_dynamic_per_token(x, O.F16)
-        O.dequant(q, O.INT8, s, O.F32, O.PER_TOKEN, O.F16)
+        O.dequant_policy(q, O.INT8, s, O.F32, O.PER_TOKEN, O.F16)
         spent += time.perf_counter() - t0
         reps += 1
     per = spent / reps
@@ -376,7 +376,7 @@ def traffic_probe(torch, ascq):
     flush.fill_(2)
     q, s = ascq.quant_dynamic_per_token(x)
     flush.fill_(3)
-    ascq.ascend_dequant(q, s, ascq.PER_TOKEN, torch.float16)
+    ascq.ascend_dequant_policy(q, s, ascq.PER_TOKEN, torch.float16)
     torch.cuda.synchronize()
     return {"traffic_probe": "copy 268435456 B, quant f16 8192x8192, dequant int8 8192x8192 -> f16"}
 
@@ -492,22 +492,23 @@ def bench_antiquant_legacy(torch, ascq, iters):
 
 
 def bench_dequant_channel(torch, ascq, iters):
-    """AscendDequant (legacy form) of an int32 [8192, 8192] accumulator with per-channel f32 scales to f16"""
+    """AscendDequant (legacy form) of an int32 [8192, 8192] accumulator with a per-channel uint64 deqScale (fp32
+    in the low word) to f16 -- the legacy form's f16-output combination"""
     M = N = 8192
-    nbytes = 4 * M * N + 2 * M * N + 4 * N
+    nbytes = 4 * M * N + 2 * M * N + 8 * N
     R = rotation(nbytes)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(9)
     xs = [torch.randint(-(1 << 20), 1 << 20, (M, N), generator=gen, device="cuda", dtype=torch.int32) for _ in range(R)]
     ys = [torch.empty((M, N), dtype=torch.float16, device="cuda") for _ in range(R)]
-    sc = torch.empty(N, device="cuda").uniform_(1e-4, 1e-2, generator=gen)
+    sc = torch.empty(N, device="cuda").uniform_(1e-4, 1e-2, generator=gen).view(torch.int32).to(torch.int64)
 
     def fn(i):
-        ascq.ascend_dequant(xs[i % R], sc, ascq.PER_CHANNEL, torch.float16, out=ys[i % R])
+        ascq.ascend_dequant(xs[i % R], sc, torch.float16, out=ys[i % R])
 
     ms = _time_loop(torch, fn, iters)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return dict(workload=f"AscendDequant per-channel int32 [{M},{N}] -> f16 (f32 scales)", ms=ms, value=gbs,
+    return dict(workload=f"AscendDequant per-channel int32 [{M},{N}] -> f16 (uint64 deqScale)", ms=ms, value=gbs,
                 unit="GB/s", frac_of_peak=gbs / HBM_PEAK_GBS)
 
 

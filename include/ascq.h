@@ -271,24 +271,68 @@ ascq_status ascq_ascend_quant(int8_t* dst, const void* src, int32_t src_type, co
 /* ------------------------------------------------------------------------------------------
  * AscendDequant
  * ------------------------------------------------------------------------------------------ */
-/* DequantParams{m, n, calCount} (ascend_dequant_utils.h:26-30) */
+/* DequantParams{m, n, calCount} (include/adv_api/quantization/ascend_dequant_utils.h:26-30) */
 typedef struct {
     uint32_t m;
     uint32_t n;
     uint32_t cal_count;
 } ascq_dequant_param;
 
-/* AscendDequant<dstT, scaleT>(dst, src, deqScale, params) (ascend_dequant.h:59-122; impl
- * ascend_dequant_common_impl.h:196-364, ascend_dequant_3510_impl.h:37-75) and the PER_TOKEN policy form
- * (ascend_dequant.h:293-315; ascend_dequant_3510_impl.h:254-287).
- *   policy PER_CHANNEL: dst[i][j] = cast(f32(src[i][j]) * scale[j]) for j < cal_count (other columns untouched)
- *   policy PER_TOKEN:   dst[i][j] = cast(f32(src[i][j]) * scale[i])
- *   policy PER_TENSOR:  dst[i][j] = cast(f32(src[i][j]) * scale_scalar)
- * src_type INT32 (the reference's type) or INT8 (widened on load); dst_type F16, BF16 or F32;
- * scale_type F32, F16, BF16 or U64 (low 32 bits).  cast = round to nearest even, saturating. */
+/* DeQuantMode (impl/basic_api/utils/kernel_utils_mode.h:193-196): how the legacy form reads params {1, m*n, n} */
+typedef enum { ASCQ_DEQUANT_SINGLE_ROW = 0, ASCQ_DEQUANT_MULTI_ROW = 1 } ascq_dequant_mode;
+
+/* Legacy AscendDequant<dstT, scaleT, mode>(dst, src, deqScale, params) and its scalar-deqScale overload
+ * (include/adv_api/quantization/ascend_dequant.h:38-291), with arch 3510's kernels
+ * (DequantPerchannelVFImpl / DequantPertensorVFImpl, impl/adv_api/detail/quantization/dequant/
+ * ascend_dequant_3510_impl.h:37-210):
+ *   policy PER_CHANNEL: the deqScale tensor `scale` (scale_type); PER_TENSOR: the scalar scale_scalar of
+ *     scale_type (a BF16 scale_type rounds it to bf16, rne, first).
+ *   mode SINGLE_ROW (the reference's default): {1, n, calCount} whose calCount is a whole number of 32-byte dst
+ *     blocks and divides n is processed as {n / calCount, calCount, calCount} (UpdateDequantParams,
+ *     ascend_dequant_common_impl.h:208-223); MULTI_ROW takes params as given.
+ *   For each row i < m and column j < calCount: dst[i * ldd + j] = cast(f32(src[i * n + j]) * scale), with
+ *     ldd = n rounded up to a whole 32-byte block of dst elements (dstInner, ascend_dequant_3510_impl.h:44, 99):
+ *     dst holds m * ldd elements (ascq_ascend_dequant_dst_shape gives m and ldd after the SINGLE_ROW rule); columns
+ *     >= calCount and the padding are not written.  int32 -> fp32 rounds ties away from zero (MrgZRndA, :61);
+ *     cast = rne + saturating to f16 / bf16, or a plain f32 store.  A U64 deqScale contributes the low 32 bits
+ *     of each word as an fp32 (:62-64).
+ *   src_type INT32 (INT8 is accepted too: widened to int32, exact).
+ *   (scale_type, dst_type) as IsTemplateValid allows (ascend_dequant_common_impl.h:126-155): tensor (U64, F16),
+ *     (F32, F32), (BF16, F32), (BF16, BF16), (F32, BF16); scalar (BF16, BF16), (BF16, F32), (F32, F32), (F32, BF16).
+ *   Argument checks of the reference's CPU-debug build (api_check/kernel_check/quantization/dequant/
+ *     dequant_check_common.h): n % 8 == 0 and 0 < calCount <= n. */
 ascq_status ascq_ascend_dequant(void* dst, int32_t dst_type, const void* src, int32_t src_type, const void* scale,
-                                int32_t scale_type, float scale_scalar, int32_t policy,
+                                int32_t scale_type, float scale_scalar, int32_t policy, int32_t mode,
                                 const ascq_dequant_param* params, void* stream);
+/* Rows and dst row stride (elements) that ascq_ascend_dequant writes for these params: the SINGLE_ROW rule of
+ * UpdateDequantParams (ascend_dequant_common_impl.h:208-223) and dstInner (ascend_dequant_3510_impl.h:44, 99).
+ * Host only. */
+ascq_status ascq_ascend_dequant_dst_shape(int32_t dst_type, int32_t mode, const ascq_dequant_param* params,
+                                          uint32_t* rows, uint32_t* row_stride);
+
+/* AscendDeQuantParam{m, n, calCount, groupSize} + AscendDeQuantConfig{hasOffset, kDim}
+ * (include/adv_api/quantization/ascend_dequant_utils.h:32-44) */
+typedef struct {
+    uint32_t m;
+    uint32_t n;
+    uint32_t cal_count;
+    uint32_t group_size;
+    int32_t has_offset;
+    int32_t kdim;
+} ascq_dequant_policy_param;
+
+/* AscendDequant<dstT, srcT, scaleT, config, policy>(dst, src, scale, offset, para), the arch-3510 policy form
+ * (include/adv_api/quantization/ascend_dequant.h:293-315; impl ascend_dequant_3510_impl.h:254-598, dispatch
+ * :643-690).  src and dst [rows, n] row-major, rows = cal_count / n:
+ *   PER_TOKEN: dst[r][c] = cast(f32(src[r][c]) * scale[r]);
+ *   PER_GROUP, kdim 1: scale[r][c / group] ([rows][ceil(n / group)]); kdim 0: scale[r / group][c]
+ *     ([ceil(rows / group)][n]); group_size a positive multiple of 32.
+ * src_type INT32 (ties-away conversion) or F32 (INT8 accepted too, widened exactly); scale_type F16, BF16 or F32
+ * (widened exactly); dst_type F16 / BF16 (rne, saturating) or F32.  The reference's kernels never read the
+ * offset tensor, and neither does this one (offset and has_offset are accepted and unused). */
+ascq_status ascq_ascend_dequant_policy(void* dst, int32_t dst_type, const void* src, int32_t src_type,
+                                       const void* scale, const void* offset, int32_t scale_type, int32_t policy,
+                                       const ascq_dequant_policy_param* para, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * AscendAntiQuant

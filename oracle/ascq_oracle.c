@@ -509,29 +509,96 @@ void oq_quant_legacy_f16(int8_t* dst, const void* src, int src_type, const uint1
 /* AscendDequant                                                             */
 /* ------------------------------------------------------------------------ */
 
-/* dst = cast(f32(src) * f32(scale)), cast = rne + sat:
- *  - PER_CHANNEL (legacy DequantParams{m, n, calCount}): dst[i][j] for j < calCount uses scale[j]
- *    (include/adv_api/quantization/ascend_dequant.h:38-72, v220 impl ascend_dequant_common_impl.h:196-364,
- *    3510 DequantPerchannelVFImpl ascend_dequant_3510_impl.h:37-75); columns >= calCount are not written.
- *    A uint64 deqScale uses the low 32 bits as the fp32 scale ("only half of uint64_t is used", :62-64).
- *  - PER_TENSOR: scalar deqScale (AscendDequantScalarImpl, ascend_dequant.h:278-291).
- *  - PER_TOKEN (policy API, ascend_dequant.h:293-315): scale[i] broadcast along the row,
- *    DeQuantPerTokenForS32VF (ascend_dequant_3510_impl.h:254-287): int32 -> fp32, Mul, cast RINT/SAT.
- * int8 sources are widened to int32 first (exact).  int32 -> fp32 rounds to nearest: v220 uses RINT, 3510
- * uses round-half-away (MrgZRndA); both are exact below 2^24 and the restatement uses RINT. */
-void oq_dequant(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
-                float scale_scalar, int policy, int64_t m, int64_t n, int64_t cal_count)
+/* int32 -> fp32 with ties away from zero: the dequant kernels convert their int32 source with
+ * Reg::Cast<float, int32_t, MrgZRndA> (impl/adv_api/detail/quantization/dequant/ascend_dequant_3510_impl.h:61, 115,
+ * 184, 434, 504), and MrgZRndA carries RoundMode::CAST_ROUND (impl/basic_api/dav_3510/kernel_operator_vec_vconv_impl.h:
+ * 56-57), "away-zero" (impl/basic_api/utils/kernel_utils_mode.h:108).  Exact below 2^24; above, the 24-bit
+ * significand of |v| is rounded half up on the magnitude. */
+float oq_i32_to_f32_rna(int32_t v)
 {
+    if (OQ_MUTANT == 27) return (float)v; /* mutant: nearest-even */
+    uint64_t a = v < 0 ? (uint64_t)(-(int64_t)v) : (uint64_t)v;
+    if (a >= (1u << 24)) {
+        int bits = 0;
+        while ((a >> bits) > 1) ++bits; /* index of the leading one */
+        const int s = bits - 23;        /* bits below the 24-bit significand */
+        a = ((a + (1ull << (s - 1))) >> s) << s;
+    }
+    const float f = (float)a; /* exact: at most 24 significant bits */
+    return v < 0 ? -f : f;
+}
+
+static inline float dq_src_f32(const void* src, int src_type, int64_t i)
+{
+    if (src_type == OQ_INT32) return oq_i32_to_f32_rna(((const int32_t*)src)[i]);
+    if (src_type == OQ_INT8) return (float)((const int8_t*)src)[i]; /* int8 widened to int32: exact */
+    return ((const float*)src)[i];
+}
+
+/* UpdateDequantParams (impl/adv_api/detail/quantization/dequant/ascend_dequant_common_impl.h:208-223): under
+ * DEQUANT_WITH_SINGLE_ROW (the default mode, include/adv_api/quantization/ascend_dequant.h:59, 88, 150) a
+ * {1, n, calCount} whose calCount is a whole number of 32-byte dst blocks and divides n is processed as
+ * {n / calCount, calCount, calCount} -- e.g. int32 {1, 16, 8} becomes {2, 8, 8} for an f32 dst but stays
+ * {1, 16, 8} for a bf16 dst (8 bf16 elements are half a block).  The dst row stride is n rounded up to a whole
+ * 32-byte block of dst elements (dstInner, ascend_dequant_3510_impl.h:44, 99 and ascend_dequant_common_impl.h:
+ * 376-377); the source row stride stays n. */
+int64_t oq_dequant_legacy_shape(int dst_type, int mode, int64_t* m, int64_t* n, int64_t cal_count)
+{
+    const int64_t blk = dst_type == OQ_F32 ? 8 : 16; /* dst elements per 32-byte block */
+    if (mode == OQ_DEQUANT_SINGLE_ROW && *m == 1 && cal_count > 0 && cal_count % blk == 0 && *n % cal_count == 0 &&
+        OQ_MUTANT != 28) {
+        *m = *n / cal_count;
+        *n = cal_count;
+    }
+    return OQ_MUTANT == 29 ? *n : (*n + blk - 1) / blk * blk;
+}
+
+/* Legacy AscendDequant (include/adv_api/quantization/ascend_dequant.h:38-291, DequantParams{m, n, calCount}
+ * ascend_dequant_utils.h:26-30), restated after arch 3510 (DequantPerchannelVFImpl / DequantPertensorVFImpl,
+ * ascend_dequant_3510_impl.h:37-210): after the SINGLE_ROW rule above, for each of the m rows and each column
+ * j < calCount, dst[i * dstInner + j] = cast(f32(src[i * n + j]) * scale), where scale is deqScale[j] (a uint64
+ * deqScale contributes its low 32 bits as an fp32, "only half of uint64_t is used", :62-64; bf16 widens exactly)
+ * or, per_tensor, the scalar (Muls, :183-187); f32(int32) rounds ties away (oq_i32_to_f32_rna); cast is rne with
+ * saturation to f16 / bf16 (LayoutZMrgZRndRSatS, :70, 131) or a plain fp32 store.  Columns j >= calCount of dst
+ * and the padding columns are not written (the 2201 form, CalculateByInner of ascend_dequant_common_impl.h:
+ * 366-430, instead writes columns >= calCount unscaled). */
+void oq_dequant_legacy(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                       float scale_scalar, int per_tensor, int mode, int64_t m, int64_t n, int64_t cal_count)
+{
+    const int64_t ldd = oq_dequant_legacy_shape(dst_type, mode, &m, &n, cal_count);
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < m; ++i) {
-        int64_t cols = policy == OQ_PER_CHANNEL ? cal_count : n;
-        for (int64_t j = 0; j < cols; ++j) {
-            float s;
-            if (policy == OQ_PER_CHANNEL) s = load_as_f32(scale, scale_type, OQ_MUTANT == 12 ? i % cal_count : j);
-            else if (policy == OQ_PER_TOKEN) s = load_as_f32(scale, scale_type, i);
-            else s = scale_scalar;
-            float v = load_as_f32(src, src_type, i * n + j) * s;
-            store_from_f32(dst, dst_type, i * n + j, v);
+        for (int64_t j = 0; j < cal_count; ++j) {
+            const float s = per_tensor ? scale_scalar : load_as_f32(scale, scale_type, OQ_MUTANT == 12 ? i % cal_count : j);
+            store_from_f32(dst, dst_type, i * ldd + j, dq_src_f32(src, src_type, i * n + j) * s);
+        }
+    }
+}
+
+/* AscendDequant policy form, arch 3510 (include/adv_api/quantization/ascend_dequant.h:293-315;
+ * AscendDeQuantParam{m, n, calCount, groupSize}, AscendDeQuantConfig{hasOffset, kDim} ascend_dequant_utils.h:
+ * 32-44; dispatch ascend_dequant_3510_impl.h:643-690).  rows = calCount / n, src and dst [rows, n]:
+ *   PER_TOKEN (DeQuantPerTokenFor{S32,F32}VF, :254-343): dst[r][c] = cast(f32(src[r][c]) * f32(scale[r]));
+ *   PER_GROUP kDim 1 (DeQuantPerGroupForCol{S32,F32}VF, :367-504, GetPerGroupScale :345-366): scale[r][c / g]
+ *             with [rows][ceil(n / g)] scales;
+ *   PER_GROUP kDim 0 (DeQuantPerGroupForRowVF / RowTailBlock, :506-598): scale[r / g][c] with [ceil(rows / g)][n].
+ * int32 sources convert with ties away (MrgZRndA), fp32 sources are used as they are; 16-bit scales widen exactly;
+ * one fp32 multiply; StoreRes (:237-252) casts rne + saturating to f16 / bf16 or stores fp32.  The config's offset
+ * tensor is never read by these kernels. */
+void oq_dequant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                       int policy, int k_dim, int64_t n, int64_t cal_count, int64_t group)
+{
+    const int64_t rows = cal_count / n;
+    const int64_t sk = group > 0 ? (n + group - 1) / group : 0;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int64_t c = 0; c < n; ++c) {
+            int64_t sidx;
+            if (policy == OQ_PER_TOKEN) sidx = r;
+            else if ((k_dim == 1) ^ (OQ_MUTANT == 30)) sidx = r * sk + c / group;
+            else sidx = (r / group) * n + c;
+            const float v = dq_src_f32(src, src_type, r * n + c) * load_as_f32(scale, scale_type, sidx);
+            store_from_f32(dst, dst_type, r * n + c, v);
         }
     }
 }

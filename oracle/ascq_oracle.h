@@ -96,9 +96,21 @@ void oq_quant_dynamic_per_token(int8_t* dst, float* scale_out, const void* src, 
 void oq_quant_legacy_f16(int8_t* dst, const void* src, int src_type, const uint16_t* scale_vec,
                          uint16_t scale_scalar, const uint16_t* offset_vec, uint16_t offset_scalar,
                          int64_t cal_count, int64_t scale_count);
-/* AscendDequant: dst = cast(f32(src) * scale) (rne, sat) */
-void oq_dequant(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
-                float scale_scalar, int policy, int64_t m, int64_t n, int64_t cal_count);
+/* int32 -> fp32 rounding half away from zero (the dequant kernels' MrgZRndA cast); exact below 2^24 */
+float oq_i32_to_f32_rna(int32_t v);
+/* DeQuantMode (impl/basic_api/utils/kernel_utils_mode.h:193-196) */
+enum { OQ_DEQUANT_SINGLE_ROW = 0, OQ_DEQUANT_MULTI_ROW = 1 };
+/* Legacy AscendDequant, DequantParams{m, n, calCount} (ascend_dequant.h:38-291): the SINGLE_ROW reshape of
+ * {1, m*n, n}, dst rows padded to 32 bytes, columns >= calCount not written; per_tensor selects the scalar
+ * deqScale.  dst = cast(f32(src) * scale) (rne, sat). */
+void oq_dequant_legacy(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                       float scale_scalar, int per_tensor, int mode, int64_t m, int64_t n, int64_t cal_count);
+/* Row stride (elements) of the legacy form's dst after the SINGLE_ROW rule; also returns the effective m, n */
+int64_t oq_dequant_legacy_shape(int dst_type, int mode, int64_t* m, int64_t* n, int64_t cal_count);
+/* AscendDequant policy form (arch 3510): PER_TOKEN / PER_GROUP (kDim 0 / 1) over rows = calCount / n, int32 or
+ * fp32 sources, f16 / bf16 / f32 scales; dst [rows, n] */
+void oq_dequant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                       int policy, int k_dim, int64_t n, int64_t cal_count, int64_t group);
 /* AscendAntiQuant: dst = (src + offset) * scale, per-channel or per-group */
 void oq_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset, const void* scale,
                   int64_t K, int64_t N, int64_t group_size, int is_transpose, int arith);

@@ -72,8 +72,13 @@ def lib() -> ctypes.CDLL:
             "oq_quant_per_token": (None, [_P, _P, ctypes.c_int, _P, _P, _I64, _I64, ctypes.c_int]),
             "oq_quant_dynamic_per_token": (None, [_P, _P, _P, ctypes.c_int, _I64, _I64, ctypes.c_int]),
             "oq_quant_legacy_f16": (None, [_P, _P, ctypes.c_int, _P, ctypes.c_uint16, _P, ctypes.c_uint16, _I64, _I64]),
-            "oq_dequant": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int, ctypes.c_float, ctypes.c_int,
-                                  _I64, _I64, _I64]),
+            "oq_i32_to_f32_rna": (ctypes.c_float, [ctypes.c_int32]),
+            "oq_dequant_legacy": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int, ctypes.c_float,
+                                         ctypes.c_int, ctypes.c_int, _I64, _I64, _I64]),
+            "oq_dequant_legacy_shape": (_I64, [ctypes.c_int, ctypes.c_int, ctypes.POINTER(_I64),
+                                               ctypes.POINTER(_I64), _I64]),
+            "oq_dequant_policy": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_int, _I64, _I64, _I64]),
             "oq_antiquant": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, _P, _I64, _I64, _I64, ctypes.c_int,
                                     ctypes.c_int]),
             "oq_antiquant_matmul": (None, [_P, _P, _P, _P, _P, ctypes.c_int, _P, _P, _I64, _I64, _I64, _I64,
@@ -271,14 +276,43 @@ def quant_legacy_f16(x, src_type, scale_vec=None, scale_scalar=0x3C00, offset_ve
     return q
 
 
-def dequant(src, src_type, scale, scale_type, policy, dst_type=F16, cal_count=None, scale_scalar=1.0, dst=None):
+SINGLE_ROW, MULTI_ROW = 0, 1
+
+
+def dequant_legacy_shape(dst_type, m, n, cal_count, mode=SINGLE_ROW):
+    """(rows, cols, dst row stride) of the legacy form after the DEQUANT_WITH_SINGLE_ROW rule"""
+    mm, nn = _I64(m), _I64(n)
+    ldd = lib().oq_dequant_legacy_shape(dst_type, mode, ctypes.byref(mm), ctypes.byref(nn), cal_count)
+    return mm.value, nn.value, ldd
+
+
+def dequant_legacy(src, src_type, scale, scale_type, per_tensor=False, dst_type=F16, cal_count=None,
+                   scale_scalar=1.0, mode=SINGLE_ROW, dst=None, m=None, n=None):
+    """Legacy AscendDequant on DequantParams {m, n, calCount} (src holds m * n elements).  Returns dst as
+    [rows, dst row stride] (the reference's padded layout); unwritten elements keep dst's initial values."""
     src = np.ascontiguousarray(src)
-    m, n = src.shape
+    if m is None:
+        m, n = src.shape
+    cal = n if cal_count is None else cal_count
+    rows, _, ldd = dequant_legacy_shape(dst_type, m, n, cal, mode)
     if dst is None:
-        dst = np.zeros((m, n), np.float32 if dst_type == F32 else np.uint16)
+        dst = np.zeros((rows, ldd), np.float32 if dst_type == F32 else np.uint16)
     sc = None if scale is None else np.ascontiguousarray(scale)
-    lib().oq_dequant(_p(dst), dst_type, _p(src), src_type, _p(sc), scale_type, float(scale_scalar), policy, m, n,
-                     n if cal_count is None else cal_count)
+    lib().oq_dequant_legacy(_p(dst), dst_type, _p(src), src_type, _p(sc), scale_type, float(scale_scalar),
+                            int(per_tensor), mode, m, n, cal)
+    return dst
+
+
+def dequant_policy(src, src_type, scale, scale_type, policy, dst_type=F16, k_dim=1, group=0, cal_count=None,
+                   dst=None):
+    """AscendDequant policy form (PER_TOKEN / PER_GROUP) on src [rows, n]"""
+    src = np.ascontiguousarray(src)
+    rows, n = src.shape
+    cal = rows * n if cal_count is None else cal_count
+    if dst is None:
+        dst = np.zeros((rows, n), np.float32 if dst_type == F32 else np.uint16)
+    lib().oq_dequant_policy(_p(dst), dst_type, _p(src), src_type, _p(np.ascontiguousarray(scale)), scale_type, policy,
+                            k_dim, n, cal, group)
     return dst
 
 

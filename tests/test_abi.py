@@ -8,6 +8,7 @@ import subprocess
 from pathlib import Path
 
 import pytest
+import torch
 
 import ascq
 
@@ -111,14 +112,38 @@ def test_policy_form_argument_checks():
 def test_dequant_antiquant_argument_checks():
     L = ascq.lib()
     d = ctypes.c_void_p(0x1000)
+    dq = lambda dst, sc, pol, p, mode=0, scale=d: L.ascq_ascend_dequant(d, dst, d, ascq.INT32, scale, sc, 1.0, pol,
+                                                                        mode, ctypes.byref(p), None)
     p = ascq._DequantParam(4, 8, 9)  # calCount > n
-    _err(L.ascq_ascend_dequant(d, ascq.F16, d, ascq.INT32, d, ascq.F32, 1.0, ascq.PER_CHANNEL, ctypes.byref(p), None),
-         ascq.E_INVALID_ARG)
+    _err(dq(ascq.F32, ascq.F32, ascq.PER_CHANNEL, p), ascq.E_INVALID_ARG)
+    _err(dq(ascq.F32, ascq.F32, ascq.PER_CHANNEL, ascq._DequantParam(4, 12, 8)), ascq.E_INVALID_ARG)  # n % 8
+    _err(dq(ascq.F32, ascq.F32, ascq.PER_CHANNEL, ascq._DequantParam(4, 8, 0)), ascq.E_INVALID_ARG)   # calCount 0
     p = ascq._DequantParam(4, 8, 8)
-    _err(L.ascq_ascend_dequant(d, ascq.INT8, d, ascq.INT32, d, ascq.F32, 1.0, ascq.PER_CHANNEL, ctypes.byref(p), None),
-         ascq.E_UNSUPPORTED)
-    _err(L.ascq_ascend_dequant(d, ascq.F16, d, ascq.INT32, None, ascq.F32, 1.0, ascq.PER_TOKEN, ctypes.byref(p), None),
-         ascq.E_INVALID_ARG)
+    _err(dq(ascq.INT8, ascq.F32, ascq.PER_CHANNEL, p), ascq.E_UNSUPPORTED)
+    _err(dq(ascq.F32, ascq.F32, ascq.PER_CHANNEL, p, mode=2), ascq.E_INVALID_ARG)
+    _err(dq(ascq.F32, ascq.F32, ascq.PER_TOKEN, p), ascq.E_UNSUPPORTED)          # the policy form's entry point
+    _err(dq(ascq.F32, ascq.F32, ascq.PER_CHANNEL, p, scale=None), ascq.E_INVALID_ARG)
+    # IsTemplateValid: tensor (U64, F16) (F32, F32) (BF16, F32) (BF16, BF16) (F32, BF16); scalar without U64 / F16
+    for sc, dst, ok in [(ascq.U64, ascq.F16, True), (ascq.F32, ascq.F16, False), (ascq.F16, ascq.F16, False),
+                        (ascq.BF16, ascq.BF16, True), (ascq.U64, ascq.F32, False), (ascq.F32, ascq.BF16, True)]:
+        _err(dq(dst, sc, ascq.PER_CHANNEL, ascq._DequantParam(0, 8, 8)), ascq.OK if ok else ascq.E_UNSUPPORTED)
+    for sc, dst, ok in [(ascq.BF16, ascq.F32, True), (ascq.F32, ascq.F16, False), (ascq.U64, ascq.F16, False)]:
+        _err(dq(dst, sc, ascq.PER_TENSOR, ascq._DequantParam(0, 8, 8)), ascq.OK if ok else ascq.E_UNSUPPORTED)
+    rows, ldd = ascq.dequant_dst_shape(torch.float32, 1, 16, 8)
+    assert (rows, ldd) == (2, 8)
+    assert ascq.dequant_dst_shape(torch.bfloat16, 1, 16, 8) == (1, 16)
+    assert ascq.dequant_dst_shape(torch.float16, 3, 24, 24) == (3, 32)
+    assert ascq.dequant_dst_shape(torch.float32, 1, 16, 8, ascq.DEQUANT_MULTI_ROW) == (1, 16)
+    pp = lambda g=32, k=1: ascq._DequantPolicyParam(4, 64, 256, g, 0, k)
+    dqp = lambda src, sc, dst, pol, p: L.ascq_ascend_dequant_policy(d, dst, d, src, d, None, sc, pol, ctypes.byref(p),
+                                                                    None)
+    _err(dqp(ascq.INT32, ascq.F32, ascq.F16, ascq.PER_GROUP, pp(g=16)), ascq.E_INVALID_ARG)      # group % 32
+    _err(dqp(ascq.INT32, ascq.F32, ascq.F16, ascq.PER_GROUP, pp(k=2)), ascq.E_INVALID_ARG)       # kDim 0 / 1
+    _err(dqp(ascq.F16, ascq.F32, ascq.F16, ascq.PER_TOKEN, pp()), ascq.E_UNSUPPORTED)            # src int32 / f32
+    _err(dqp(ascq.INT32, ascq.U64, ascq.F16, ascq.PER_TOKEN, pp()), ascq.E_UNSUPPORTED)          # scale 16/32-bit fp
+    _err(dqp(ascq.INT32, ascq.F32, ascq.F16, ascq.PER_CHANNEL, pp()), ascq.E_UNSUPPORTED)
+    _err(L.ascq_ascend_dequant_policy(None, ascq.F16, None, ascq.INT32, None, None, ascq.F32, ascq.PER_TOKEN,
+                                      ctypes.byref(ascq._DequantPolicyParam(4, 64, 63, 0, 0, 1)), None), ascq.OK)
     _err(L.ascq_ascend_antiquant(d, ascq.F16, d, ascq.INT8, d, d, 100, 8, 32, 0, 0, None), ascq.E_INVALID_ARG)
     _err(L.ascq_ascend_antiquant(d, ascq.F32, d, ascq.INT8, d, d, 128, 8, 32, 0, 0, None), ascq.E_UNSUPPORTED)
 

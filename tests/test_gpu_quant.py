@@ -138,90 +138,6 @@ def test_legacy_quant_layouts(ascq_gpu, oracle, case, src):
     np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
 
 
-@pytest.mark.parametrize("m,n", [(64, 8192), (5, 48), (3, 20), (2, 8), (4, 24), (3, 8200), (1, 16392), (9, 1000)])
-def test_dequant_per_token_int8(ascq_gpu, oracle, m, n):
-    rng = seeded(41 + n)
-    q = rng.integers(-128, 128, (m, n), dtype=np.int8)
-    scale = (rng.uniform(0.0, 1.0, m) * 0.05).astype(np.float32)
-    scale[0] = 1000.0  # |q| * 1000 > 65504: saturates to the largest finite half
-    y = ascq_gpu.ascend_dequant(_dev(q), _dev(scale), ascq_gpu.PER_TOKEN, torch.float16)
-    y_ref = O.dequant(q, O.INT8, scale, O.F32, O.PER_TOKEN, O.F16)
-    np.testing.assert_array_equal(y.cpu().numpy().view(np.uint16), y_ref)
-
-
-@pytest.mark.parametrize("dst", [torch.float16, torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("scale_kind", ["f32", "f16", "u64"])
-def test_dequant_per_channel_int32(ascq_gpu, oracle, dst, scale_kind):
-    """Legacy DequantParams{m, n, calCount}: columns >= calCount must be left untouched."""
-    rng = seeded(51)
-    m, n, cal = 128, 32, 24
-    src = rng.integers(-(1 << 20), 1 << 20, (m, n), dtype=np.int32)
-    s32 = rng.uniform(-100, 100, n).astype(np.float32)
-    if scale_kind == "f32":
-        st, sn, code = torch.from_numpy(s32), s32, O.F32
-    elif scale_kind == "f16":
-        st, sn, code = torch.from_numpy(s32.astype(np.float16)), s32.astype(np.float16), O.F16
-    else:
-        words = s32.view(np.uint32).astype(np.uint64) | (np.uint64(0xABC) << np.uint64(40))
-        st, sn, code = torch.from_numpy(words.view(np.int64)), words, O.U64
-    init = torch.full((m, n), 7.0, dtype=dst)
-    out = init.cuda()
-    ascq_gpu.ascend_dequant(_dev(src), st.cuda(), ascq_gpu.PER_CHANNEL, dst, cal_count=cal, out=out)
-    dst_code = {torch.float16: O.F16, torch.bfloat16: O.BF16, torch.float32: O.F32}[dst]
-    if dst == torch.float32:
-        ref0, got = init.numpy().copy(), out.cpu().numpy()
-    else:
-        ref0, got = init.view(torch.int16).numpy().view(np.uint16).copy(), out.cpu().view(torch.int16).numpy().view(np.uint16)
-    y_ref = O.dequant(src, O.INT32, sn, code, O.PER_CHANNEL, dst_code, cal_count=cal, dst=ref0)
-    np.testing.assert_array_equal(got.view(np.uint32) if dst == torch.float32 else got,
-                                  y_ref.view(np.uint32) if dst == torch.float32 else y_ref)
-    assert (got[:, cal:] == ref0[:, cal:]).all()
-
-
-@pytest.mark.parametrize("src_kind", ["int32", "int8"])
-@pytest.mark.parametrize("policy", ["channel", "token", "tensor"])
-@pytest.mark.parametrize("dst", [torch.float16, torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("shape", [(37, 96, 88), (37, 96, 90), (2048, 8192, 8192)])
-def test_dequant_layouts(ascq_gpu, oracle, src_kind, policy, dst, shape):
-    """f32 scales per channel (calCount of a multiple of 8 or not), per token or per tensor; int32 / int8 sources;
-    saturation at the f16 range; rows not a multiple of 4 (the vector kernels' row blocks)"""
-    m, n, cal = shape
-    if policy != "channel":
-        cal = n
-    rng = seeded(81 + m + cal)
-    if src_kind == "int32":
-        src = rng.integers(-(1 << 24), 1 << 24, (m, n), dtype=np.int32)
-        code = O.INT32
-    else:
-        src = rng.integers(-128, 128, (m, n), dtype=np.int8)
-        code = O.INT8
-    pol = {"channel": ascq_gpu.PER_CHANNEL, "token": ascq_gpu.PER_TOKEN, "tensor": ascq_gpu.PER_TENSOR}[policy]
-    s32 = np.exp(rng.uniform(np.log(1e-4), np.log(8.0), n if policy == "channel" else m)).astype(np.float32)
-    init = torch.full((m, n), 5.0, dtype=dst)
-    out = init.cuda()
-    ascq_gpu.ascend_dequant(_dev(src), None if policy == "tensor" else _dev(s32), pol, dst, cal_count=cal,
-                            scale_scalar=0.0173, out=out)
-    dst_code = {torch.float16: O.F16, torch.bfloat16: O.BF16, torch.float32: O.F32}[dst]
-    if dst == torch.float32:
-        ref0, got = init.numpy().copy(), out.cpu().numpy()
-    else:
-        ref0 = init.view(torch.int16).numpy().view(np.uint16).copy()
-        got = out.cpu().view(torch.int16).numpy().view(np.uint16)
-    y_ref = O.dequant(src, code, None if policy == "tensor" else s32, 0 if policy == "tensor" else O.F32,
-                      {"channel": O.PER_CHANNEL, "token": O.PER_TOKEN, "tensor": O.PER_TENSOR}[policy], dst_code,
-                      cal_count=cal, scale_scalar=np.float32(0.0173), dst=ref0)
-    np.testing.assert_array_equal(got.view(np.uint32) if dst == torch.float32 else got,
-                                  y_ref.view(np.uint32) if dst == torch.float32 else y_ref)
-
-
-def test_dequant_per_tensor(ascq_gpu, oracle):
-    rng = seeded(61)
-    src = rng.integers(-(1 << 24), 1 << 24, (17, 40), dtype=np.int32)
-    y = ascq_gpu.ascend_dequant(_dev(src), None, ascq_gpu.PER_TENSOR, torch.bfloat16, scale_scalar=0.0123)
-    y_ref = O.dequant(src, O.INT32, None, 0, O.PER_TENSOR, O.BF16, scale_scalar=np.float32(0.0123))
-    np.testing.assert_array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), y_ref)
-
-
 @pytest.mark.parametrize("src_type", ["int8", "int4"])
 @pytest.mark.parametrize("transpose", [False, True])
 @pytest.mark.parametrize("group", [0, 32, 128])
@@ -309,14 +225,14 @@ def test_config2_full_size_quant_dequant(ascq_gpu, oracle):
     x = _f16_input(rng, m, n)
     xd = _dev(x)
     q, s = ascq_gpu.quant_dynamic_per_token(xd)
-    y = ascq_gpu.ascend_dequant(q, s, ascq_gpu.PER_TOKEN, torch.float16)
+    y = ascq_gpu.ascend_dequant_policy(q, s, ascq_gpu.PER_TOKEN, torch.float16)
     torch.cuda.synchronize()
     q_ref, s_ref = O.quant_dynamic_per_token(x.view(np.uint16), O.F16)
     qn = q.cpu().numpy()
     np.testing.assert_array_equal(qn, q_ref)
     np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
     assert np.abs(qn.astype(np.int32)).max() <= 127
-    y_ref = O.dequant(q_ref, O.INT8, s_ref, O.F32, O.PER_TOKEN, O.F16)
+    y_ref = O.dequant_policy(q_ref, O.INT8, s_ref, O.F32, O.PER_TOKEN, O.F16)
     np.testing.assert_array_equal(y.cpu().numpy().view(np.uint16), y_ref)
 
 

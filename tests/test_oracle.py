@@ -203,8 +203,157 @@ def test_quant_example_golden_exact():
 
 def test_dequant_example_golden_exact():
     f = np.load(GOLD / "dequant_example.npz")
-    y = O.dequant(f["inp"], O.INT32, f["scale"], O.F32, O.PER_CHANNEL, O.F32, cal_count=32)
+    y = O.dequant_legacy(f["inp"], O.INT32, f["scale"], O.F32, dst_type=O.F32, cal_count=32)
     assert (y.view(np.uint32) == f["golden"].view(np.uint32)).all()
+
+
+# --------------------------------------------------------------------------- AscendDequant layout contract
+def _rna_exact(v: int) -> int:
+    """nearest binary32 value to the integer v, ties away from zero (exact integer arithmetic)"""
+    a = abs(v)
+    if a < (1 << 24):
+        return v
+    s = a.bit_length() - 24
+    lo = (a >> s) << s
+    rem = a - lo
+    r = lo + (1 << s) if 2 * rem >= (1 << s) else lo
+    return -r if v < 0 else r
+
+
+def test_i32_to_f32_ties_away():
+    """MrgZRndA = CAST_ROUND (half away from zero): 2^24 + 1 -> 2^24 + 2 (nearest-even would give 2^24),
+    2^24 + 5 -> 2^24 + 6 (nearest-even: 2^24 + 4); non-ties round to nearest; INT_MIN / INT_MAX -> -+2^31"""
+    L = O.lib()
+    kat = {(1 << 24) + 1: (1 << 24) + 2, -((1 << 24) + 1): -((1 << 24) + 2), (1 << 24) + 5: (1 << 24) + 6,
+           (1 << 24) + 3: (1 << 24) + 4, (1 << 25) + 2: (1 << 25) + 4, (1 << 25) + 1: 1 << 25,
+           2 ** 31 - 1: 2 ** 31, -(2 ** 31): -(2 ** 31), (1 << 24) - 1: (1 << 24) - 1, 0: 0, 7: 7, -5: -5}
+    for v, want in kat.items():
+        assert int(L.oq_i32_to_f32_rna(v)) == want, v
+    vals = np.concatenate([rng0.integers(-(2 ** 31), 2 ** 31, 20000, dtype=np.int64),
+                           ((rng0.integers(1 << 24, 2 ** 31 - 512, 5000, dtype=np.int64) >> 3) << 3) | 4,
+                           ((rng0.integers(1 << 24, 1 << 25, 2000, dtype=np.int64) >> 1) << 1) | 1])
+    for v in vals.tolist():
+        assert int(L.oq_i32_to_f32_rna(int(v))) == _rna_exact(int(v)), v
+
+
+def _f16_sat(v32):
+    return np.clip(v32, -65504, 65504).astype(np.float16).view(np.uint16)
+
+
+def _bf16_sat(v32):
+    big = float(torch.finfo(torch.bfloat16).max)
+    t = torch.from_numpy(np.clip(v32, -big, big).astype(np.float32)).to(torch.bfloat16)
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+def _cast(v32, dst_type):
+    return {O.F16: _f16_sat, O.BF16: _bf16_sat, O.F32: lambda v: v.astype(np.float32)}[dst_type](v32)
+
+
+@pytest.mark.parametrize("dst_type", [O.F16, O.BF16, O.F32])
+def test_dequant_single_row_worked_examples(dst_type):
+    """UpdateDequantParams' own examples (ascend_dequant_common_impl.h:214-216): int32 {1, 16, 8} is processed as
+    {2, 8, 8} for an f32 dst (8 fp32 fill a 32-byte block) but stays {1, 16, 8} for a bf16 dst, so only 8 of the
+    16 elements are dequantised; MULTI_ROW never reshapes."""
+    src = np.arange(-7, 9, dtype=np.int32) * 3
+    scale = np.linspace(0.5, 4.0, 8).astype(np.float32)
+    sentinel = 0x7777 if dst_type != O.F32 else np.float32(-1.25)
+    for mode in (O.SINGLE_ROW, O.MULTI_ROW):
+        init = np.full((2, 16), sentinel, np.float32 if dst_type == O.F32 else np.uint16)
+        rows, cols, ldd = O.dequant_legacy_shape(dst_type, 1, 16, 8, mode)
+        out = O.dequant_legacy(src, O.INT32, scale, O.F32, dst_type=dst_type, cal_count=8, mode=mode, m=1, n=16,
+                               dst=init)
+        flat = out.reshape(-1)
+        exp = _cast(src[:8].astype(np.float32) * scale, dst_type)
+        assert (flat[:8] == exp).all()
+        reshaped = mode == O.SINGLE_ROW and dst_type == O.F32
+        assert (rows, cols, ldd) == ((2, 8, 8) if reshaped else (1, 16, 16))
+        if reshaped:
+            assert (flat[8:16] == _cast(src[8:].astype(np.float32) * scale, dst_type)).all()
+        else:
+            assert (flat[8:] == init.reshape(-1)[8:]).all()
+
+
+@pytest.mark.parametrize("n,cal", [(8, 8), (24, 24), (40, 40), (24, 16), (40, 8)])
+@pytest.mark.parametrize("dst_type", [O.F16, O.BF16, O.F32])
+@pytest.mark.parametrize("per_tensor", [False, True])
+def test_dequant_padded_dst_rows(n, cal, dst_type, per_tensor):
+    """dst rows start every ceil(n / block) * block elements (dstInner, ascend_dequant_3510_impl.h:44, 99), block =
+    32 bytes of dst; columns >= calCount and the padding stay unwritten; with m = 1 the SINGLE_ROW rule may first
+    reshape {1, n, cal} into {n / cal, cal, cal}"""
+    rng = np.random.default_rng(n * 131 + cal)
+    for m in (1, 3):
+        src = rng.integers(-(1 << 20), 1 << 20, (m, n), dtype=np.int32)
+        scale = rng.uniform(-3, 3, n).astype(np.float32)
+        ss = np.float32(0.0371)
+        blk = 8 if dst_type == O.F32 else 16
+        mm, nn = m, n
+        if m == 1 and cal % blk == 0 and n % cal == 0:
+            mm, nn = n // cal, cal
+        ldd = -(-nn // blk) * blk
+        init = np.full((mm, ldd), 0x5555 if dst_type != O.F32 else np.float32(3.5),
+                       np.float32 if dst_type == O.F32 else np.uint16)
+        out = O.dequant_legacy(src, O.INT32, scale, O.F32, per_tensor=per_tensor, dst_type=dst_type, cal_count=cal,
+                               scale_scalar=ss, dst=init.copy())
+        assert out.shape == (mm, ldd)
+        s2 = src.reshape(mm, nn)
+        sc = ss if per_tensor else scale[:cal]
+        exp = _cast(s2[:, :cal].astype(np.float32) * sc, dst_type)
+        assert (out[:, :cal] == exp).all()
+        assert (out[:, cal:] == init[:, cal:]).all()
+
+
+@pytest.mark.parametrize("src_type", [O.INT32, O.F32])
+@pytest.mark.parametrize("scale_type", [O.F32, O.F16, O.BF16])
+@pytest.mark.parametrize("k_dim", [0, 1])
+def test_dequant_policy_per_group_axes(src_type, scale_type, k_dim):
+    """PER_GROUP: kDim 1 scales [rows][ceil(n/g)] along each row, kDim 0 scales [ceil(rows/g)][n] down the columns
+    (ascend_dequant_3510_impl.h:367-598); checked against numpy's repeat of the scale table, with ragged row and
+    column counts (tail groups)"""
+    rng = np.random.default_rng(7 + k_dim + 3 * scale_type + 11 * src_type)
+    rows, n, g = 70, 200, 64
+    if src_type == O.INT32:
+        src = rng.integers(-(1 << 23), 1 << 23, (rows, n), dtype=np.int32)
+        s32 = src.astype(np.float32)
+    else:
+        src = (rng.standard_normal((rows, n)) * 1000).astype(np.float32)
+        s32 = src
+    shape = (rows, -(-n // g)) if k_dim == 1 else (-(-rows // g), n)
+    sf = rng.uniform(-2, 2, shape).astype(np.float32)
+    if scale_type == O.F16:
+        sf = sf.astype(np.float16)
+        sw, sv = sf, sf.astype(np.float32)
+    elif scale_type == O.BF16:
+        bt = torch.from_numpy(sf).to(torch.bfloat16)
+        sw, sv = bt.view(torch.int16).numpy().view(np.uint16), bt.float().numpy()
+    else:
+        sw, sv = sf, sf
+    full = np.repeat(sv, g, axis=1)[:, :n] if k_dim == 1 else np.repeat(sv, g, axis=0)[:rows]
+    for dst_type in (O.F16, O.BF16, O.F32):
+        out = O.dequant_policy(src, src_type, sw, scale_type, O.PER_GROUP, dst_type, k_dim=k_dim, group=g)
+        assert (out == _cast(s32 * full, dst_type)).all()
+
+
+def test_dequant_policy_per_token_and_cal_count():
+    """PER_TOKEN: scale[r] along row r; rows = calCount / n (a partial last row is not processed)"""
+    rng = np.random.default_rng(99)
+    src = rng.integers(-(1 << 22), 1 << 22, (9, 48), dtype=np.int32)
+    sc = rng.uniform(0.001, 0.1, 9).astype(np.float32)
+    init = np.full((9, 48), 0x4242, np.uint16)
+    out = O.dequant_policy(src, O.INT32, sc, O.F32, O.PER_TOKEN, O.F16, cal_count=8 * 48 + 5, dst=init.copy())
+    assert (out[:8] == _f16_sat(src[:8].astype(np.float32) * sc[:8, None])).all()
+    assert (out[8] == init[8]).all()
+
+
+def test_dequant_int32_sources_round_ties_away():
+    """large int32 accumulators convert with ties away before the multiply (scale 1 keeps the conversion visible)"""
+    src = np.array([[(1 << 24) + 1, (1 << 24) + 5, -((1 << 24) + 1), (1 << 25) + 2] * 2], np.int32)
+    want = np.array([_rna_exact(int(v)) for v in src[0]], np.float32)
+    one = np.ones(8, np.float32)
+    y = O.dequant_legacy(src, O.INT32, one, O.F32, dst_type=O.F32, cal_count=8)
+    assert (y[0] == want).all()
+    yp = O.dequant_policy(src, O.INT32, np.ones(1, np.float32), O.F32, O.PER_TOKEN, O.F32)
+    assert (yp[0] == want).all()
 
 
 @pytest.mark.parametrize("arch,arith", [("2201", O.ARITH_F16), ("3510", O.ARITH_F32)])

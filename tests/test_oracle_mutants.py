@@ -6,7 +6,8 @@ reordered group-matmul epilogue, a transposed MX scale index, offset/scale appli
 double-rounded multiplier, a wrong E2M1 code, a ties-away f16 cast, an unrounded half add, a per-channel
 dequant indexed by row, a requant offset added before the clamp, a ties-away fp8 cast, an ignored requant
 sign flag, a FasterGelu with the wrong sign, and policy-form quant mistakes (arithmetic type, bf16 step, group
-axis, offset rounding, directed E2M1 modes).  Each mutant is compiled on the CPU into a temporary library and the pinning tests of
+axis, offset rounding, directed E2M1 modes) and dequant layout mistakes (int32 rounding, the single-row
+reshape, padded dst rows, group axis).  Each mutant is compiled on the CPU into a temporary library and the pinning tests of
 tests/test_oracle.py are run against it; every mutant must fail at least one of them.
 """
 from __future__ import annotations
@@ -48,6 +49,10 @@ MUTANTS = {
     24: "quant product not rounded to the scale type before the offset add",
     25: "E2M1 floor / ceil applied to the magnitude regardless of sign",
     26: "E1M2 rint ties resolved toward zero instead of to the even code",
+    27: "dequant int32 -> fp32 rounded to nearest even instead of ties away",
+    28: "legacy dequant without the DEQUANT_WITH_SINGLE_ROW reshape",
+    29: "legacy dequant dst rows not padded to 32 bytes",
+    30: "per-group dequant scales indexed along the wrong axis",
 }
 
 
