@@ -120,6 +120,7 @@ SIGNATURES = {
     "ascq_matmul_workspace_size": (_I32, [_P, ctypes.POINTER(ctypes.c_size_t)]),
     "ascq_matmul_set_workspace": (_I32, [_P, _P, ctypes.c_size_t]),
     "ascq_matmul_iterate_all": (_I32, [_P, _P, _U8, _P]),
+    "ascq_matmul_iterate_all_noalloc": (_I32, [_P, _P, _U8, _P]),
     "ascq_matmul_end": (_I32, [_P]),
     "ascq_matmul_destroy": (_I32, [_P]),
     "ascq_ascend_quant_per_token": (_I32, [_P, _P, _I32, _P, _P, ctypes.POINTER(_QuantParam), _P]),
@@ -482,6 +483,10 @@ class Matmul:
 
     def IterateAll(self, c, en_atomic: int = 0, stream=None):
         check(lib().ascq_matmul_iterate_all(self._h, _ptr(c), en_atomic, _stream(stream)), "IterateAll")
+
+    def IterateAllNoAlloc(self, c, en_atomic: int = 0, stream=None):
+        """IterateAll with the workspace taken from the library's static per-device scratch (allocates nothing)"""
+        check(lib().ascq_matmul_iterate_all_noalloc(self._h, _ptr(c), en_atomic, _stream(stream)), "IterateAllNoAlloc")
 
     def End(self):
         check(lib().ascq_matmul_end(self._h), "End")

@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -38,6 +39,36 @@ inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 inline bool valid_round(int32_t r) { return r >= ASCQ_ROUND_NONE && r <= ASCQ_ROUND_TRUNC; }
 
+}  // namespace
+
+// Scratch of ascq_matmul_iterate_all_noalloc: one array per device (the code object's copy on each GPU), held
+// until the process ends.  Host code never uses the array's name as an address: it is looked up once per device
+// with hipGetSymbolAddress and only that per-device pointer is handed to kernels.
+static __device__ __align__(256) uint8_t scratch[ASCQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// the current device's scratch address (looked up on the first call on each device)
+ascq_status scratch_for_current_device(void** out)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(ASCQ_E_UNSUPPORTED, "device %d: at most %d devices", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e, "hipGetSymbolAddress(scratch)");
+        if (!ptr) return fail(ASCQ_E_HIP, "hipGetSymbolAddress(scratch) returned a null address");
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return ASCQ_OK;
+}
 }  // namespace
 
 struct ascq_matmul_s {
@@ -647,6 +678,34 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
     }
     default: return fail(ASCQ_E_UNSUPPORTED, "iterate_all: unsupported handle");
     }
+}
+
+ascq_status ascq_matmul_iterate_all_noalloc(ascq_matmul_t h, void* c, uint8_t en_atomic, void* stream)
+{
+    if (!h || !c) return fail(ASCQ_E_INVALID_ARG, "iterate_all_noalloc: null argument");
+    const size_t need = workspace_need(h);
+    if (need > ASCQ_NOALLOC_SCRATCH_BYTES)
+        return fail(ASCQ_E_UNSUPPORTED,
+                    "iterate_all_noalloc: this handle needs %zu bytes of workspace, above the %zu-byte static scratch "
+                    "(use ascq_matmul_iterate_all with a workspace)", need, (size_t)ASCQ_NOALLOC_SCRATCH_BYTES);
+    void* ptr = nullptr;
+    if (need > 0) {
+        ascq_status s = scratch_for_current_device(&ptr);
+        if (s != ASCQ_OK) return s;
+    }
+    // run IterateAll on the scratch in place of the handle's workspace (ensure_workspace then sees enough room and
+    // allocates nothing), and give the handle its own workspace back afterwards
+    void* const ws = h->ws;
+    const size_t ws_bytes = h->ws_bytes;
+    const bool ws_owned = h->ws_owned;
+    h->ws = ptr;
+    h->ws_bytes = need > 0 ? (size_t)ASCQ_NOALLOC_SCRATCH_BYTES : 0;
+    h->ws_owned = false;
+    const ascq_status s = ascq_matmul_iterate_all(h, c, en_atomic, stream);
+    h->ws = ws;
+    h->ws_bytes = ws_bytes;
+    h->ws_owned = ws_owned;
+    return s;
 }
 
 ascq_status ascq_matmul_end(ascq_matmul_t h)

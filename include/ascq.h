@@ -203,6 +203,15 @@ ascq_status ascq_matmul_workspace_size(ascq_matmul_t h, size_t* bytes);
 ascq_status ascq_matmul_set_workspace(ascq_matmul_t h, void* workspace, size_t bytes);
 /* IterateAll(GlobalTensor<C>, enAtomic) (matmul.h:262; matmul_impl.h:119-137).  en_atomic must be 0. */
 ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic, void* stream);
+/* IterateAll that allocates nothing -- no counterpart in the reference; for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).  Same arguments and
+ * results as ascq_matmul_iterate_all, but a handle that needs a workspace (ascq_matmul_workspace_size > 0) uses
+ * the library's static per-device scratch of ASCQ_NOALLOC_SCRATCH_BYTES instead of its own workspace or a
+ * hipMalloc; a handle needing more is rejected with ASCQ_E_UNSUPPORTED before anything is launched.  Every call
+ * on one device shares that device's scratch: calls that overlap on a device (other streams, other threads) race.
+ * Nothing of the scratch's previous contents is read. */
+#define ASCQ_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+ascq_status ascq_matmul_iterate_all_noalloc(ascq_matmul_t h, void* c, uint8_t en_atomic, void* stream);
 /* End (matmul.h:358): releases per-call bindings; the handle may be re-bound and reused */
 ascq_status ascq_matmul_end(ascq_matmul_t h);
 ascq_status ascq_matmul_destroy(ascq_matmul_t h);

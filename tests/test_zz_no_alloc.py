@@ -1,0 +1,102 @@
+"""ascq_matmul_iterate_all_noalloc (IterateAll with the workspace taken from the library's static per-device
+scratch, allocating nothing) against ascq_matmul_iterate_all, bit-exact, on two calls in a row -- the second with a
+smaller problem -- for each kind of handle that uses a workspace: int8 with a [K, N] B transposed into it, MX-FP4
+with its scales rearranged (and a [K, N] B transposed) into it, and int4 operands unpacked into it.  The handle
+keeps its own workspace across the allocation-free calls."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from conftest import seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _both(ascq, mm, shape, dtype):
+    """IterateAll into one buffer and IterateAllNoAlloc into another (both pre-filled with different garbage);
+    returns the two outputs"""
+    c1 = torch.full(shape, 3, dtype=dtype, device="cuda")
+    c2 = torch.full(shape, 5, dtype=dtype, device="cuda")
+    mm.IterateAll(c1)
+    mm.IterateAllNoAlloc(c2)
+    torch.cuda.synchronize()
+    return c1, c2
+
+
+def _same(c1, c2):
+    a, b = c1.cpu(), c2.cpu()
+    if a.dtype in (torch.float16, torch.bfloat16):
+        a, b = a.view(torch.int16), b.view(torch.int16)
+    elif a.dtype == torch.float32:
+        a, b = a.view(torch.int32), b.view(torch.int32)
+    assert torch.equal(a, b)
+
+
+def test_noalloc_int8_kn_b(ascq_gpu, oracle):
+    """int8 x int8 -> f16 (VDEQF16), B given [K, N] with M >= 512: B is transposed into the workspace"""
+    ascq = ascq_gpu
+    mm = ascq.Matmul(ascq.INT8, ascq.INT8, ascq.F16, ascq.INT32)
+    for i, (M, N, K) in enumerate([(1024, 768, 512), (512, 256, 384)]):
+        rng = seeded(300 + i)
+        A = rng.integers(-127, 128, (M, K), dtype=np.int8)
+        B = rng.integers(-127, 128, (K, N), dtype=np.int8)
+        bias = rng.integers(-(1 << 15), 1 << 15, N, dtype=np.int32)
+        sc = np.exp(rng.uniform(np.log(2.0 ** -12), np.log(2.0 ** -6), N)).astype(np.float32)
+        words = sc.view(np.uint32).astype(np.uint64)
+        mm.SetOrgShape(M, N, K)
+        assert mm.WorkspaceSize() > 0
+        mm.SetQuantVector(_dev(words.view(np.int64)))
+        mm.SetTensorA(_dev(A))
+        mm.SetTensorB(_dev(B), False)
+        mm.SetBias(_dev(bias))
+        c1, c2 = _both(ascq, mm, (M, N), torch.float16)
+        _same(c1, c2)
+        ref = O.mm_dequant(O.matmul_i8(A, B, bias), O.F16, qvec=words)
+        np.testing.assert_array_equal(c2.cpu().view(torch.int16).numpy().view(np.uint16), ref)
+        mm.End()
+
+
+def test_noalloc_mx_fp4(ascq_gpu, oracle):
+    """MX-FP4 -> bf16 with a [K, N] B: B transposed and both scale tensors rearranged in the workspace"""
+    from test_gpu_mx import mx_inputs, scale_pairs, to_kn
+
+    ascq = ascq_gpu
+    mm = ascq.Matmul(ascq.FP4_E2M1, ascq.FP4_E2M1, ascq.BF16, 0, ascq.E8M0)
+    for i, (M, N, K) in enumerate([(256, 384, 512), (128, 128, 256)]):
+        A, sA, Bt, sBt = mx_inputs(seeded(310 + i), M, N, K)
+        mm.SetOrgShape(M, N, K)
+        assert mm.WorkspaceSize() > 0
+        mm.SetTensorA(_dev(A))
+        mm.SetTensorB(_dev(to_kn(Bt, N, K)), False)
+        mm.SetTensorScaleA(_dev(sA), 0)
+        mm.SetTensorScaleB(_dev(scale_pairs(sBt)), 0)
+        c1, c2 = _both(ascq, mm, (M, N), torch.bfloat16)
+        _same(c1, c2)
+        mm.End()
+
+
+def test_noalloc_int4(ascq_gpu, oracle):
+    """int4 x int4 -> int32: both operands unpacked to int8 in the workspace (B given [K, N], nibble-transposed)"""
+    ascq = ascq_gpu
+    mm = ascq.Matmul(ascq.INT4, ascq.INT4, ascq.INT32, ascq.INT32)
+    for i, (M, N, K) in enumerate([(256, 512, 256), (64, 128, 128)]):
+        rng = seeded(320 + i)
+        a = rng.integers(-8, 8, (M, K), dtype=np.int8)
+        b = rng.integers(-8, 8, (K, N), dtype=np.int8)
+        pa = ((a[:, 0::2] & 0xF) | ((a[:, 1::2] & 0xF) << 4)).astype(np.uint8)
+        pb = ((b[:, 0::2] & 0xF) | ((b[:, 1::2] & 0xF) << 4)).astype(np.uint8)
+        mm.SetOrgShape(M, N, K)
+        assert mm.WorkspaceSize() > 0
+        mm.SetTensorA(_dev(pa))
+        mm.SetTensorB(_dev(pb), False)
+        c1, c2 = _both(ascq, mm, (M, N), torch.int32)
+        _same(c1, c2)
+        np.testing.assert_array_equal(c2.cpu().numpy(), O.matmul_i8(a, b))
+        mm.End()
