@@ -22,7 +22,7 @@ _PKG_DIR = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("ASCQ_LIB", _PKG_DIR / "libascq.so"))
 
 # ascq_dtype
-INT8, UINT8, INT4, INT32, F16, BF16, F32, U64, FP8_E4M3, FP8_E5M2, FP4_E2M1, E8M0, INT64, FP4_E1M2 = range(1, 15)
+INT8, UINT8, INT4, INT32, F16, BF16, F32, U64, FP8_E4M3, FP8_E5M2, FP4_E2M1, E8M0, INT64, FP4_E1M2, HIF8 = range(1, 16)
 # ascq_round_mode
 ROUND_NONE, ROUND_RINT, ROUND_FLOOR, ROUND_CEIL, ROUND_ROUND, ROUND_TRUNC = range(6)
 # ascq_policy
@@ -126,7 +126,8 @@ SIGNATURES = {
     "ascq_ascend_quant_per_token": (_I32, [_P, _P, _I32, _P, _P, ctypes.POINTER(_QuantParam), _P]),
     "ascq_ascend_quant_dynamic_per_token": (_I32, [_P, _P, _P, _I32, _U32, _U32, _I32, _P]),
     "ascq_ascend_quant_policy": (_I32, [_P, _I32, _P, _I32, _P, _P, _F32, _I32, _I32, ctypes.POINTER(_QuantParam), _P]),
-    "ascq_ascend_quant": (_I32, [_P, _P, _I32, _P, _P, _U16, _U16, _U32, _U32, _P]),
+    "ascq_ascend_quant": (_I32, [_P, _I32, _P, _I32, _P, _P, _F32, _F32, _U32, _U32, _P]),
+    "ascq_ascend_antiquant_scalar": (_I32, [_P, _I32, _P, _I32, _U16, _U16, _I32, _U64, _P]),
     "ascq_ascend_dequant": (_I32, [_P, _I32, _P, _I32, _P, _I32, _F32, _I32, _I32, ctypes.POINTER(_DequantParam),
                                    _P]),
     "ascq_ascend_dequant_dst_shape": (_I32, [_I32, _I32, ctypes.POINTER(_DequantParam), ctypes.POINTER(_U32),
@@ -244,15 +245,18 @@ def ascend_quant_policy(x: torch.Tensor, scale: torch.Tensor, policy: int, dst_t
     return q
 
 
-def ascend_quant(x: torch.Tensor, scale=None, offset=None, scale_scalar: float = 1.0, offset_scalar: float = 0.0,
-                 scale_count: int = 0, out=None, stream=None):
-    """Legacy AscendQuant (half arithmetic), per-tensor (scalars) or per-channel (half vectors)."""
-    src_type = {torch.float16: F16, torch.float32: F32}[x.dtype]
-    q = out if out is not None else torch.empty(x.shape, dtype=torch.int8, device=x.device)
-    if scale is not None or offset is not None:
-        scale_count = scale_count or (scale.numel() if scale is not None else offset.numel())
-    check(lib().ascq_ascend_quant(_ptr(q), _ptr(x), src_type, _ptr(scale), _ptr(offset), _half_bits(scale_scalar),
-                                  _half_bits(offset_scalar), x.numel(), scale_count, _stream(stream)), "ascend_quant")
+def ascend_quant(x: torch.Tensor, dst_type: int = INT8, scale=None, offset=None, scale_scalar: float = 1.0,
+                 offset_scalar: float = 0.0, scale_count: int = 0, out=None, stream=None):
+    """Legacy AscendQuant (arch-3510 form): per tensor (float scalars) or per channel (scale / offset tensors of the
+    source's type; offset None takes offset_scalar as a source-typed value).  dst INT8 / HIF8 (half arithmetic) or
+    FP8_E4M3 / FP8_E5M2 (fp32 arithmetic); returns int8 (INT8) or uint8 codes of x's shape."""
+    src_type = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}[x.dtype]
+    q = out if out is not None else torch.empty(x.shape, dtype=torch.int8 if dst_type == INT8 else torch.uint8,
+                                                device=x.device)
+    if scale is not None:
+        scale_count = scale_count or scale.numel()
+    check(lib().ascq_ascend_quant(_ptr(q), dst_type, _ptr(x), src_type, _ptr(scale), _ptr(offset), float(scale_scalar),
+                                  float(offset_scalar), x.numel(), scale_count, _stream(stream)), "ascend_quant")
     return q
 
 
@@ -316,6 +320,18 @@ def ascend_antiquant(src: torch.Tensor, src_type: int, scale: torch.Tensor, offs
     y = out if out is not None else torch.empty(shape, dtype=dst_dtype, device=src.device)
     check(lib().ascq_ascend_antiquant(_ptr(y), dst_type, _ptr(src), src_type, _ptr(offset), _ptr(scale), k, n,
                                       group_size, int(is_transpose), arith, _stream(stream)), "ascend_antiquant")
+    return y
+
+
+def ascend_antiquant_scalar(src: torch.Tensor, src_type: int, offset: float | None, scale: float, count: int,
+                            dst_dtype=torch.float16, out=None, stream=None):
+    """AscendAntiQuant per tensor: dst[i] = (src[i] + offset) * scale with offset / scale of dst_dtype (offset None:
+    scale only); count elements (int4 two per byte)."""
+    dst_type = {torch.float16: F16, torch.bfloat16: BF16}[dst_dtype]
+    bits = lambda v: int(torch.tensor([v], dtype=dst_dtype).view(torch.int16).item()) & 0xFFFF
+    y = out if out is not None else torch.empty(count, dtype=dst_dtype, device=src.device)
+    check(lib().ascq_ascend_antiquant_scalar(_ptr(y), dst_type, _ptr(src), src_type, bits(offset or 0.0), bits(scale),
+                                             int(offset is not None), count, _stream(stream)), "ascend_antiquant_scalar")
     return y
 
 

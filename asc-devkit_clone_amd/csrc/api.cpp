@@ -761,13 +761,13 @@ ascq_status ascq_ascend_quant_policy(void* dst, int32_t dst_type, const void* sr
     if (!fp_type(scale_type)) return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: scale must be f16, bf16 or f32");
     const bool fp8 = dst_type == ASCQ_DT_FP8_E4M3 || dst_type == ASCQ_DT_FP8_E5M2;
     const bool fp4 = dst_type == ASCQ_DT_FP4_E2M1 || dst_type == ASCQ_DT_FP4_E1M2;
-    if (!fp8 && !fp4 && dst_type != ASCQ_DT_INT8)
+    if (!fp8 && !fp4 && dst_type != ASCQ_DT_INT8 && dst_type != ASCQ_DT_HIF8)
         return fail(ASCQ_E_UNSUPPORTED,
-                    "ascend_quant_policy: dst must be int8, fp8_e4m3, fp8_e5m2, fp4_e2m1 or fp4_e1m2");
+                    "ascend_quant_policy: dst must be int8, hifloat8, fp8_e4m3, fp8_e5m2, fp4_e2m1 or fp4_e1m2");
     if (policy != ASCQ_POLICY_PER_TOKEN && policy != ASCQ_POLICY_PER_GROUP)
         return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: policy must be PER_TOKEN or PER_GROUP");
     if (policy == ASCQ_POLICY_PER_TOKEN && fp4)
-        return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: PER_TOKEN writes int8 or fp8");
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: PER_TOKEN writes int8, hifloat8 or fp8");
     if (policy == ASCQ_POLICY_PER_GROUP) {
         if (para->kdim != 0 && para->kdim != 1) return fail(ASCQ_E_INVALID_ARG, "ascend_quant_policy: kdim must be 0 or 1");
         if (para->group_size == 0 || para->group_size % 32 != 0)
@@ -802,19 +802,26 @@ ascq_status ascq_ascend_quant_dynamic_per_token(int8_t* dst, float* scale_out, c
                       "quant_dynamic_per_token");
 }
 
-ascq_status ascq_ascend_quant(int8_t* dst, const void* src, int32_t src_type, const uint16_t* scale,
-                              const uint16_t* offset, uint16_t scale_scalar, uint16_t offset_scalar, uint32_t cal_count,
+ascq_status ascq_ascend_quant(void* dst, int32_t dst_type, const void* src, int32_t src_type, const void* scale,
+                              const void* offset, float scale_scalar, float offset_scalar, uint32_t cal_count,
                               uint32_t scale_count, void* stream)
 {
-    if (!dst || !src) return fail(ASCQ_E_INVALID_ARG, "ascend_quant: null argument");
-    if (src_type != ASCQ_DT_F16 && src_type != ASCQ_DT_F32)
-        return fail(ASCQ_E_UNSUPPORTED, "ascend_quant: src must be f16 or f32");
-    if ((scale || offset) && scale_count == 0) return fail(ASCQ_E_INVALID_ARG, "ascend_quant: scale_count must be positive");
-    if (scale_count && cal_count % scale_count != 0)
-        return fail(ASCQ_E_INVALID_ARG, "ascend_quant: calCount must be an integer multiple of scaleCount");
+    if (src_type != ASCQ_DT_F16 && src_type != ASCQ_DT_BF16 && src_type != ASCQ_DT_F32)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_quant: src must be f16, bf16 or f32");
+    if (dst_type != ASCQ_DT_INT8 && dst_type != ASCQ_DT_HIF8 && dst_type != ASCQ_DT_FP8_E4M3 &&
+        dst_type != ASCQ_DT_FP8_E5M2)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_quant: dst must be int8, hifloat8, fp8_e4m3 or fp8_e5m2");
+    if (offset && !scale)
+        return fail(ASCQ_E_INVALID_ARG, "ascend_quant: an offset tensor needs a scale tensor (per-channel form)");
+    if (scale) {  // the per-channel checks of ascend_quant_3510_impl.h:551-557
+        if (scale_count == 0) return fail(ASCQ_E_INVALID_ARG, "ascend_quant: scaleCount must be positive");
+        if (cal_count % scale_count != 0 || cal_count % 32 != 0)
+            return fail(ASCQ_E_INVALID_ARG, "ascend_quant: calCount must be an integer multiple of 32 and scaleCount");
+    }
     if (cal_count == 0) return ASCQ_OK;
-    return hip_status(ascq::launch_quant_legacy(dst, src, src_type, scale, offset, scale_scalar, offset_scalar, cal_count,
-                                                (scale || offset) ? scale_count : 0u, S(stream)),
+    if (!dst || !src) return fail(ASCQ_E_INVALID_ARG, "ascend_quant: null argument");
+    return hip_status(ascq::launch_quant_legacy(dst, dst_type, src, src_type, scale, offset, scale_scalar,
+                                                offset_scalar, cal_count, scale ? scale_count : 0u, S(stream)),
                       "ascend_quant");
 }
 
@@ -930,8 +937,11 @@ ascq_status ascq_ascend_antiquant(void* dst, int32_t dst_type, const void* src, 
     if (!dst || !src || !scale) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant: null argument");
     if (dst_type != ASCQ_DT_F16 && dst_type != ASCQ_DT_BF16)
         return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant: dst must be f16 or bf16");
-    if (src_type != ASCQ_DT_INT8 && src_type != ASCQ_DT_INT4)
-        return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant: src must be int8 or int4");
+    const bool b8 = src_type == ASCQ_DT_HIF8 || src_type == ASCQ_DT_FP8_E4M3 || src_type == ASCQ_DT_FP8_E5M2;
+    if (src_type != ASCQ_DT_INT8 && src_type != ASCQ_DT_INT4 && !b8)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant: src must be int8, int4, hifloat8, fp8_e4m3 or fp8_e5m2");
+    if (b8 && group_size != 0)  // AntiQuantPerchannelImpl (ascend_antiquant_3510_impl.h:752-770): per channel only
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant: hifloat8 / fp8 sources are per channel (group_size 0)");
     if (arith != ASCQ_ARITH_F16 && arith != ASCQ_ARITH_F32) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant: bad arith");
     if (group_size && k % group_size != 0) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant: group_size must divide K");
     if (src_type == ASCQ_DT_INT4 && ((uint64_t)k * n) % 2 != 0)
@@ -941,6 +951,26 @@ ascq_status ascq_ascend_antiquant(void* dst, int32_t dst_type, const void* src, 
     return hip_status(ascq::launch_antiquant(dst, dst_type, src, src_type, offset, scale, k, n, g, is_transpose ? 1 : 0,
                                              dst_type == ASCQ_DT_BF16 ? 1 : arith, S(stream)),
                       "ascend_antiquant");
+}
+
+ascq_status ascq_ascend_antiquant_scalar(void* dst, int32_t dst_type, const void* src, int32_t src_type,
+                                         uint16_t offset, uint16_t scale, int32_t has_offset, uint64_t count,
+                                         void* stream)
+{
+    if (dst_type != ASCQ_DT_F16 && dst_type != ASCQ_DT_BF16)
+        return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_scalar: dst must be f16 or bf16");
+    if (src_type != ASCQ_DT_INT8 && src_type != ASCQ_DT_INT4 && src_type != ASCQ_DT_HIF8 &&
+        src_type != ASCQ_DT_FP8_E4M3 && src_type != ASCQ_DT_FP8_E5M2)
+        return fail(ASCQ_E_UNSUPPORTED,
+                    "ascend_antiquant_scalar: src must be int8, int4, hifloat8, fp8_e4m3 or fp8_e5m2");
+    if (src_type == ASCQ_DT_INT4 && count % 2 != 0)
+        return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_scalar: int4 needs an even element count");
+    if (count >= (1ull << 40)) return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_scalar: tensor too large");
+    if (count == 0) return ASCQ_OK;
+    if (!dst || !src) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_scalar: null argument");
+    return hip_status(ascq::launch_antiquant_scalar(dst, dst_type, src, src_type, offset, scale, has_offset ? 1 : 0,
+                                                    (int64_t)count, S(stream)),
+                      "ascend_antiquant_scalar");
 }
 
 ascq_status ascq_ascend_antiquant_policy(void* dst, int32_t dst_type, const void* src, int32_t src_type,
@@ -962,14 +992,16 @@ ascq_status ascq_ascend_antiquant_policy(void* dst, int32_t dst_type, const void
         if (dst_type != ASCQ_DT_F16 && dst_type != ASCQ_DT_BF16)
             return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: fp4 output must be f16 or bf16");
         if (n % 2 != 0) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_policy: fp4 rows pack two per byte (n even)");
-    } else if (src_type == ASCQ_DT_INT8 || fp8) {
+    } else if (src_type == ASCQ_DT_INT8 || src_type == ASCQ_DT_HIF8 || fp8) {
         if (scale_type != ASCQ_DT_F16 && scale_type != ASCQ_DT_BF16 && scale_type != ASCQ_DT_F32)
             return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: scale must be f16, bf16 or f32");
         if (!out_ok) return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: dst must be f16, bf16 or f32");
         if (!fp8 && scale_type != ASCQ_DT_F32 && dst_type != scale_type)
-            return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: int8 with a 16-bit scale writes the scale type");
+            return fail(ASCQ_E_UNSUPPORTED,
+                        "ascend_antiquant_policy: int8 / hifloat8 with a 16-bit scale writes the scale type");
     } else {
-        return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: src must be int8, fp8_e4m3, fp8_e5m2, fp4_e2m1 or fp4_e1m2");
+        return fail(ASCQ_E_UNSUPPORTED,
+                    "ascend_antiquant_policy: src must be int8, hifloat8, fp8_e4m3, fp8_e5m2, fp4_e2m1 or fp4_e1m2");
     }
     if (m == 0 || n == 0) return ASCQ_OK;  // empty tensors may carry null pointers
     if (!dst || !src || !scale) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_policy: null argument");

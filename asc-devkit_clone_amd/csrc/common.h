@@ -27,7 +27,7 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 // dtype / round-mode codes shared with include/ascq.h
 enum : int32_t {
     DT_INT8 = 1, DT_UINT8 = 2, DT_INT4 = 3, DT_INT32 = 4, DT_F16 = 5, DT_BF16 = 6, DT_F32 = 7, DT_U64 = 8,
-    DT_FP8_E4M3 = 9, DT_FP8_E5M2 = 10, DT_FP4_E2M1 = 11, DT_E8M0 = 12, DT_INT64 = 13, DT_FP4_E1M2 = 14
+    DT_FP8_E4M3 = 9, DT_FP8_E5M2 = 10, DT_FP4_E2M1 = 11, DT_E8M0 = 12, DT_INT64 = 13, DT_FP4_E1M2 = 14, DT_HIF8 = 15
 };
 enum : int32_t { RM_NONE = 0, RM_RINT = 1, RM_FLOOR = 2, RM_CEIL = 3, RM_ROUND = 4, RM_TRUNC = 5 };
 
@@ -55,6 +55,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16_sat(float x)
     return b;
 }
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+// fp32 -> bf16 value (kept in an fp32 register): rne, overflow to inf, NaN kept
+__device__ __forceinline__ float bf16_round(float x)  // rne to bf16, overflow to inf, NaN kept
+{
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return x;
+    return __uint_as_float(((u + 0x7fffu + ((u >> 16) & 1u)) >> 16) << 16);
+}
 
 // QUANT_PRE word -> M1 multiplier: bits [31:13] as fp32, low 13 bits cleared
 __device__ __forceinline__ float quant_pre_m1(uint64_t w) { return __uint_as_float((uint32_t)w & 0xFFFFE000u); }
@@ -136,6 +143,62 @@ __device__ __forceinline__ float e2m1_to_f32(uint32_t nib)
     const uint32_t e = (nib >> 1) & 3u, m = nib & 1u;
     const float mag = e == 0u ? 0.5f * (float)m : (1.0f + 0.5f * (float)m) * (float)(1u << (e - 1u));
     return (nib & 8u) ? -mag : mag;
+}
+
+// HiFloat8 (the layout of the reference's decoder, impl/utils/debug/npu_arch_9201/asc_type_conversion_utils.h:62-149):
+// bit 7 sign; a prefix-coded dot field from bit 6 selects the exponent width w -- 11: 4, 10: 3, 01: 2, 001: 1,
+// 0001: 0 -- and the mantissa gets the 7 - |dot| - w remaining bits; the exponent field holds the exponent's sign in
+// its top bit and its magnitude with that bit standing for an implicit 1; dot 0000 is the subnormal class 2^(M - 23)
+// (M = 0: zero, or NaN with the sign bit); 0x6F / 0xEF are +-inf.  Every code is exact in f16 and f32.
+__device__ __forceinline__ float hif8_to_f32(uint32_t c)
+{
+    const uint32_t s = (c & 0x80u) << 24, b = c & 0x7fu;
+    if (c == 0x80u) return __uint_as_float(0x7fc00000u);
+    if (b == 0x6Fu) return __uint_as_float(s | 0x7f800000u);
+    if ((b & 0x78u) == 0u) return b == 0u ? 0.0f : __uint_as_float(s | ((b + 104u) << 23));  // 2^(M - 23)
+    // exponent width w and mantissa width mw from the dot field
+    const uint32_t top = b >> 5;
+    const uint32_t w = top == 3u ? 4u : (top == 2u ? 3u : (top == 1u ? 2u : ((b >> 4) & 1u)));
+    const uint32_t mw = top >= 2u ? 4u - top : 3u;  // 11: 1, 10: 2, else 3
+    const uint32_t field = (b >> mw) & ((1u << w) - 1u);
+    const uint32_t mag = w ? ((field & ((1u << (w - 1u)) - 1u)) | (1u << (w - 1u))) : 0u;
+    const int32_t e = (w && (field >> (w - 1u))) ? -(int32_t)mag : (int32_t)mag;
+    const uint32_t m = b & ((1u << mw) - 1u);
+    return __uint_as_float(s | ((uint32_t)(e + 127) << 23) | (m << (23u - mw)));
+}
+
+// x -> HiFloat8 with ties away from zero and saturation (Cast<hifloat8_t, half | float> under CAST_ROUND with SatS,
+// docs/zh/api/SIMD-API/basic_api/reg_vector_compute/type_conversion/Cast.md:254-348): NaN -> 0; |x| < 2^-23 -> 0
+// (whatever the sign); [2^-23, 2^-22) -> the smallest subnormal; the subnormal class rounds between powers of two on
+// the first fraction bit; otherwise the mantissa keeps 3 / 2 / 1 bits for |E| <= 3 / <= 7 / <= 15 and rounds up on
+// the next bit, carrying into the exponent; every overflow (E > 15, or E = 15 with a mantissa bit, the inf code)
+// saturates to +-32768.  Returns the code in the low 8 bits.
+__device__ __forceinline__ uint32_t hif8_code_rna_sat(float x)
+{
+    const uint32_t u = __float_as_uint(x), a = u & 0x7fffffffu, s = (u >> 24) & 0x80u;
+    int32_t e = (int32_t)(a >> 23) - 127;
+    const uint32_t f = a & 0x7fffffu;
+    if (a > 0x7f800000u || e < -23) return 0u;  // NaN, zero, tiny
+    if (e == -23) return s | 1u;
+    uint32_t m = 0u;
+    if (e <= -16) {
+        e += (int32_t)(f >> 22);
+        if (e <= -16) return s | (uint32_t)(e + 23);
+    } else if (e <= 15) {
+        const uint32_t ae0 = (uint32_t)(e < 0 ? -e : e);
+        const uint32_t mw = ae0 <= 3u ? 3u : (ae0 <= 7u ? 2u : 1u);
+        m = (f >> (23u - mw)) + ((f >> (22u - mw)) & 1u);
+        if (m >> mw) m = 0u, ++e;
+    }
+    if (e > 15 || (e == 15 && m)) return s | 0x6Eu;
+    const uint32_t ae = (uint32_t)(e < 0 ? -e : e), ng = e < 0 ? 1u : 0u;
+    uint32_t c;
+    if (ae == 0u) c = 0x08u;
+    else if (ae == 1u) c = 0x10u | (ng << 3);
+    else if (ae <= 3u) c = 0x20u | (((ng << 1) | (ae & 1u)) << 3);
+    else if (ae <= 7u) c = 0x40u | (((ng << 2) | (ae & 3u)) << 2);
+    else c = 0x60u | (((ng << 3) | (ae & 7u)) << 1);
+    return s | c | m;
 }
 
 // E1M2 nibble: sign | 1-bit exponent (bias 1) | 2-bit mantissa, magnitudes {0, .25, .5, .75, 1, 1.25, 1.5, 1.75}

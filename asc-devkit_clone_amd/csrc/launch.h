@@ -50,8 +50,10 @@ inline void launch_k(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t 
 // quant.hip
 hipError_t launch_quant_dynamic_per_token(int8_t* q, float* scale_out, const void* x, int src_type, uint32_t m,
                                           uint32_t n, int round_mode, hipStream_t st);
-hipError_t launch_quant_legacy(int8_t* q, const void* x, int src_type, const uint16_t* scale, const uint16_t* offset,
-                               uint16_t scale_scalar, uint16_t offset_scalar, uint32_t cal_count,
+// legacy AscendQuant, arch-3510 form: dst int8 / hifloat8 / fp8; src f16 / bf16 / f32; srcT scale / offset tensors
+// of scale_count (scale null: the scalars; offset null with a scale tensor: the scalar offset as a srcT value)
+hipError_t launch_quant_legacy(void* q, int dst_type, const void* x, int src_type, const void* scale,
+                               const void* offset, float scale_scalar, float offset_scalar, uint32_t cal_count,
                                uint32_t scale_count, hipStream_t st);
 // AscendDequant, both forms: rows x cols computed elements at source row stride n and destination row stride ldd;
 // smode picks the scale addressing (quant.hip DQ_*: scalar, per column, per row, per group along the row with
@@ -65,6 +67,9 @@ hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int
 hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset,
                             const void* scale, uint32_t K, uint32_t N, uint32_t g, int is_transpose, int arith,
                             hipStream_t st);
+// AscendAntiQuant per tensor: dst[i] = (src[i] + offset) * scale with offset / scale the output type's bits
+hipError_t launch_antiquant_scalar(void* dst, int dst_type, const void* src, int src_type, uint16_t offset,
+                                   uint16_t scale, int has_offset, int64_t count, hipStream_t st);
 hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale,
                                int scale_type, const void* offset, int has_offset, float offset_scalar, int per_token,
                                int64_t m, int64_t n, int64_t g, int k_dim, int round_mode, hipStream_t st);

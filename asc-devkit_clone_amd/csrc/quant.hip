@@ -107,26 +107,6 @@ __global__ __launch_bounds__(256) void quant_dyn_generic_kernel(const void* __re
 }
 
 // ---------------------------------------------------------------------------------------------
-// Legacy AscendQuant: half arithmetic.  t = half(x); t = t*s; t = t+o; q = sat_s8(rint(t)).
-// ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void quant_legacy_f16_kernel(const void* __restrict__ x, int8_t* __restrict__ q,
-                                                               const uint16_t* __restrict__ scale,
-                                                               const uint16_t* __restrict__ offset,
-                                                               uint16_t scale_scalar, uint16_t offset_scalar,
-                                                               int64_t total, uint32_t scale_count, int src_type)
-{
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-        _Float16 xh = src_type == DT_F16 ? bits_h(((const uint16_t*)x)[i]) : (_Float16)(((const float*)x)[i]);
-        uint32_t c = scale_count ? (uint32_t)(i % scale_count) : 0u;
-        _Float16 s = bits_h(scale ? scale[c] : scale_scalar);
-        _Float16 o = bits_h(offset ? offset[c] : offset_scalar);
-        _Float16 t = xh * s;
-        t = t + o;
-        q[i] = (int8_t)quant_s8<RM_RINT>((float)t);
-    }
-}
-
-// ---------------------------------------------------------------------------------------------
 // Dequant
 // ---------------------------------------------------------------------------------------------
 // Fast path: int8 [m, n] x fp32 scale[row] -> f16, n % 8 == 0.  A block owns one row segment of 256 * U
@@ -232,6 +212,46 @@ __device__ __forceinline__ int32_t load_q(const void* src, int src_type, int64_t
     return nib >= 8 ? nib - 16 : nib;
 }
 
+// one source element's exact value: int8 / int4 (two per byte, even element low) / fp8 / hifloat8
+__device__ __forceinline__ float aq_src_value(const void* src, int src_type, int64_t idx)
+{
+    if (src_type == DT_INT8 || src_type == DT_INT4) return (float)load_q(src, src_type, idx);
+    const uint32_t c = ((const uint8_t*)src)[idx];
+    if (src_type == DT_HIF8) return hif8_to_f32(c);
+    return fp8_bits_to_f32(c, src_type == DT_FP8_E5M2);
+}
+
+// The arithmetic of one legacy AscendAntiQuant element (AR: DT_F16 half ops, DT_BF16 bf16 ops, DT_F32 fp32 ops with
+// one rne + saturating cast): (q + offset) * scale, written as dst_type
+__device__ __forceinline__ void aq_elem(void* dst, int dst_type, int64_t idx, float q, bool has_off, float of, float sc,
+                                        int ar)
+{
+    if (ar == DT_F16 && dst_type == DT_F16) {
+        _Float16 w = (_Float16)q;
+        if (has_off) w = w + (_Float16)of;
+        w = w * (_Float16)sc;
+        ((uint16_t*)dst)[idx] = h_bits(w);
+    } else if (ar == DT_BF16 && dst_type == DT_BF16) {
+        float w = q;  // exact in bf16 (hifloat8 codes)
+        if (has_off) w = bf16_round(w + of);
+        w = bf16_round(w * sc);
+        ((uint16_t*)dst)[idx] = (uint16_t)(__float_as_uint(w) >> 16);
+    } else {
+        float v = q;
+        if (has_off) v = v + of;
+        store_cast(dst, idx, v * sc, dst_type);
+    }
+}
+
+// the arithmetic the reference uses: fp8 in fp32; hifloat8 in half (f16), bf16 along rows, fp32 transposed or per
+// tensor; int8 / int4 the caller's choice (bf16 output always fp32)
+__host__ __device__ __forceinline__ int aq_arith(int src_type, int dst_type, int is_transpose, int per_tensor, int arith)
+{
+    if (src_type == DT_FP8_E4M3 || src_type == DT_FP8_E5M2) return DT_F32;
+    if (src_type == DT_HIF8) return dst_type == DT_F16 ? DT_F16 : ((is_transpose || per_tensor) ? DT_F32 : DT_BF16);
+    return (dst_type == DT_F16 && arith == 0) ? DT_F16 : DT_F32;
+}
+
 __global__ __launch_bounds__(256) void antiquant_kernel(void* __restrict__ dst, int dst_type,
                                                         const void* __restrict__ src, int src_type,
                                                         const uint16_t* __restrict__ offset,
@@ -240,26 +260,27 @@ __global__ __launch_bounds__(256) void antiquant_kernel(void* __restrict__ dst, 
 {
     const int64_t total = (int64_t)K * N;
     const uint32_t G = K / g;
+    const int ar = aq_arith(src_type, dst_type, is_transpose, 0, arith);
     for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
         // t enumerates dst in memory order
         int64_t k, n;
         if (is_transpose) { n = t / K; k = t % K; }
         else { k = t / N; n = t % N; }
-        int64_t sidx = is_transpose ? n * G + k / g : (k / g) * N + n;
-        int32_t qv = load_q(src, src_type, t);
-        if (dst_type == DT_F16 && arith == 0) {
-            _Float16 w = (_Float16)(float)qv;
-            if (offset) w = w + bits_h(offset[sidx]);
-            w = w * bits_h(scale[sidx]);
-            ((uint16_t*)dst)[t] = h_bits(w);
-        } else {
-            float sc = load_f32_of(scale, sidx, dst_type);
-            float v = (float)qv;
-            if (offset) v = v + load_f32_of(offset, sidx, dst_type);
-            v = v * sc;
-            store_cast(dst, t, v, dst_type);
-        }
+        const int64_t sidx = is_transpose ? n * G + k / g : (k / g) * N + n;
+        const float sc = load_f32_of(scale, sidx, dst_type);
+        const float of = offset ? load_f32_of(offset, sidx, dst_type) : 0.0f;
+        aq_elem(dst, dst_type, t, aq_src_value(src, src_type, t), offset != nullptr, of, sc, ar);
     }
+}
+
+// per tensor, any count or alignment
+__global__ __launch_bounds__(256) void antiquant_scalar_elem_kernel(void* __restrict__ dst, int dst_type,
+                                                                    const void* __restrict__ src, int src_type,
+                                                                    float of, float sc, int has_off, int64_t count)
+{
+    const int ar = aq_arith(src_type, dst_type, 0, 1, dst_type == DT_F16 ? 0 : 1);
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < count; t += (int64_t)gridDim.x * 256)
+        aq_elem(dst, dst_type, t, aq_src_value(src, src_type, t), has_off != 0, of, sc, ar);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -328,17 +349,35 @@ hipError_t launch_quant_dynamic_per_token(int8_t* q, float* scale_out, const voi
 // AscendAntiQuant policy form (arch 3510, ascend_antiquant_3510_impl.h:1386-1412, 1458-2110, 2175-2221): one thread
 // per element of the [m, n] tensor.  Half and bf16 arithmetic is an fp32 operation rounded once to the 16-bit
 // type, which equals the correctly rounded 16-bit operation (fp32 carries more than 2p + 2 bits of either).
-__device__ __forceinline__ float bf16_round(float x)  // rne to bf16, overflow to inf, NaN kept
+// One scaleT multiply / add of two scaleT values, correctly rounded with signed zeros kept: f16 runs as a half
+// operation (rounding the exact fp32 product to half gives the same value, but the compiler turns that rounding into
+// an fma with a +0 addend, v_fma_mixlo_f16 a, b, 0, which makes a -0 product +0); bf16 rounds the fp32 result on
+// its bits (exact products; sums are correctly rounded because fp32 has more than 2p + 2 bits of bf16).
+__device__ __forceinline__ float mul_rt(float a, float b, int t)
 {
-    const uint32_t u = __float_as_uint(x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return x;
-    return __uint_as_float(((u + 0x7fffu + ((u >> 16) & 1u)) >> 16) << 16);
+    if (t == DT_F16) return (float)((_Float16)a * (_Float16)b);
+    if (t == DT_BF16) return bf16_round(a * b);
+    return a * b;
 }
-__device__ __forceinline__ float round_scale_t(float x, int t)
+__device__ __forceinline__ float add_rt(float a, float b, int t)
 {
-    if (t == DT_F16) return (float)(_Float16)x;
-    if (t == DT_BF16) return bf16_round(x);
-    return x;
+    if (t == DT_F16) return (float)((_Float16)a + (_Float16)b);
+    if (t == DT_BF16) return bf16_round(a + b);
+    return a + b;
+}
+template <int T>
+__device__ __forceinline__ float mul_t(float a, float b)
+{
+    if constexpr (T == DT_F16) return (float)((_Float16)a * (_Float16)b);
+    else if constexpr (T == DT_BF16) return bf16_round(a * b);
+    else return a * b;
+}
+template <int T>
+__device__ __forceinline__ float add_t(float a, float b)
+{
+    if constexpr (T == DT_F16) return (float)((_Float16)a + (_Float16)b);
+    else if constexpr (T == DT_BF16) return bf16_round(a + b);
+    else return a + b;
 }
 __device__ __forceinline__ float load_scale_t(const void* p, int t, int64_t i)
 {
@@ -355,7 +394,7 @@ __device__ __forceinline__ float load_scale_t(const void* p, int t, int64_t i)
 // 8 contiguous scales (groups down the columns), and an 8- (int8 / fp8) or 4-byte (E2M1) store.  Rows whose
 // length is not a multiple of 8, or unaligned pointers, take the per-element path of the same kernel.
 // ---------------------------------------------------------------------------------------------
-enum : int { QD_INT8 = 0, QD_E4M3 = 1, QD_E5M2 = 2, QD_E2M1 = 3, QD_E1M2 = 4 };
+enum : int { QD_INT8 = 0, QD_E4M3 = 1, QD_E5M2 = 2, QD_E2M1 = 3, QD_E1M2 = 4, QD_HIF8 = 5 };
 constexpr bool qd_nibble(int d) { return d == QD_E2M1 || d == QD_E1M2; }  // two codes a byte
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 enum : int { QL_TOKEN = 0, QL_KCOL = 1, QL_KROW = 2 };
@@ -423,15 +462,6 @@ __device__ __forceinline__ uint32_t e1m2_code(float v)
     return v != v ? 0u : (s | c);
 }
 
-// one scaleT rounding of an fp32 result (exact for products of two 16-bit values; a single correct rounding for
-// sums, since fp32 holds more than 2p + 2 bits of half and bf16)
-template <int T>
-__device__ __forceinline__ float rnd_t(float x)
-{
-    if constexpr (T == DT_F16) return (float)(_Float16)x;
-    else if constexpr (T == DT_BF16) return bf16_round(x);
-    else return x;
-}
 
 // the output code of a scaleT result v (after the offset): int8 byte, fp8 byte or E2M1 nibble
 template <int DST, int T, int MODE>
@@ -439,6 +469,8 @@ __device__ __forceinline__ uint32_t quant_code(float v)
 {
     if constexpr (DST == QD_INT8) {
         return (uint32_t)sat_s8_from_integral(round_mode_f(v, MODE)) & 0xffu;
+    } else if constexpr (DST == QD_HIF8) {  // TransRegForHif8: every mode but HYBRID is CAST_ROUND (ties away)
+        return hif8_code_rna_sat(v);
     } else if constexpr (DST == QD_E4M3 || DST == QD_E5M2) {
         return f32_to_fp8_sat(v, DST == QD_E5M2);
     } else {
@@ -557,8 +589,8 @@ __device__ __forceinline__ void quant_unit(const QuantPolicyArgs& a, uint32_t u,
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const float sj = KROW ? raw8_at<SC>(sr, j) : raw_to_f32<SC>(sr.w[0]);
-            float t = rnd_t<T>(raw8_at<SRC>(xr, j) * sj);
-            if (a.has_off) t = rnd_t<T>(t + (KROW ? raw8_at<SC>(orw, j) : raw_to_f32<SC>(orw.w[0])));
+            float t = mul_t<T>(raw8_at<SRC>(xr, j), sj);
+            if (a.has_off) t = add_t<T>(t, KROW ? raw8_at<SC>(orw, j) : raw_to_f32<SC>(orw.w[0]));
             v[j] = t;
         }
     }
@@ -665,121 +697,190 @@ __global__ __launch_bounds__(256) void quant_policy_vec_krow_kernel(QuantPolicyA
     }
 }
 
-// Legacy AscendQuant, vector path (cal_count % 8 == 0 and below 2^31, 16-byte aligned source, scale / offset
-// vectors of a multiple of 8 entries, 16-byte aligned).  Element i uses channel i % scale_count, and scale_count
-// divides cal_count, so the data is R = cal_count / scale_count rows of scale_count channels; a unit is 8
-// consecutive channels of one row.  With channel vectors a lane takes the same 8 channels of QP_UNR consecutive
-// rows and loads their scales / offsets once; with scalars only, QP_UNR consecutive units per workgroup pass.  Each
-// lane issues all loads before converting.  The half product and the half offset add run as packed half operations,
-// each correctly rounded like the reference's Muls / Adds in half; an f32 source is first cast to half (rne).
-template <bool F32SRC>
-__device__ __forceinline__ u32x2 quant_legacy_unit(const uint32_t* xw, const uint32_t* sw, const uint32_t* ow)
+// Legacy AscendQuant, arch-3510 form (include/adv_api/quantization/ascend_quant.h:64-293, 360-460; impl
+// ascend_quant_3510_impl.h:35-620).  Element i uses channel i % scale_count of the srcT scale / offset tensors, or
+// the scalars.  int8 / hifloat8 outputs run in half arithmetic: the source and the srcT tensors become half with rne
+// and saturation, the scalars arrive as half already (the host's static_cast<half>), then t = x * s and t = t + o as
+// packed half operations (each correctly rounded), then rint with saturation (int8) or ties away with saturation
+// (hifloat8).  fp8 outputs run in fp32: y = x * s, y = y + o (exact conversions of srcT), rint with saturation.
+struct QuantLegacyArgs {
+    void* q;
+    const void* x;
+    const void* scale;   // srcT [scale_count], or null for the scalars
+    const void* offset;  // srcT [scale_count], or null for the scalar offset
+    uint32_t sh, oh;     // the scalars as half bits (half arithmetic)
+    float sf, of;        // the scalars in fp32 (fp8 outputs)
+    int out;             // QD_INT8 / QD_HIF8 / QD_E4M3 / QD_E5M2
+    int src_type;        // element kernel
+    uint32_t units, rows, upr, scale_count;
+    FastDiv upr_div;
+    int64_t total;
+};
+
+// elements 2q and 2q + 1 of a unit as packed half bits, rne + saturating
+template <int SRC>
+__device__ __forceinline__ uint32_t half2_sat(const Raw8<SRC>& r, int q)
 {
-    int32_t r[8];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        h2 xh;
-        if constexpr (F32SRC) xh = (h2){(_Float16)__uint_as_float(xw[2 * p]), (_Float16)__uint_as_float(xw[2 * p + 1])};
-        else xh = __builtin_bit_cast(h2, xw[p]);
-        h2 t = xh * __builtin_bit_cast(h2, sw[p]);
-        t = t + __builtin_bit_cast(h2, ow[p]);
-        r[2 * p] = quant_s8<RM_RINT>((float)t.x);
-        r[2 * p + 1] = quant_s8<RM_RINT>((float)t.y);
-    }
-    return (u32x2){pack4_s8(r[0], r[1], r[2], r[3]), pack4_s8(r[4], r[5], r[6], r[7])};
+    if constexpr (SRC == DT_F16) return r.w[q];
+    else return (uint32_t)f32_to_f16_sat(raw8_at<SRC>(r, 2 * q)) | ((uint32_t)f32_to_f16_sat(raw8_at<SRC>(r, 2 * q + 1)) << 16);
 }
 
-template <bool F32SRC, bool SV, bool OV>
-__global__ __launch_bounds__(256) void quant_legacy_vec_kernel(const void* __restrict__ x, u32x2* __restrict__ q,
-                                                               const uint16_t* __restrict__ scale,
-                                                               const uint16_t* __restrict__ offset,
-                                                               uint32_t ss, uint32_t os, uint32_t units, uint32_t rows,
-                                                               uint32_t upr, FastDiv upr_div)
+template <int SRC, bool F32A>
+__device__ __forceinline__ u32x2 quant_legacy_unit(const QuantLegacyArgs& a, const Raw8<SRC>& xr, const Raw8<SRC>* sr,
+                                                   const Raw8<SRC>* orr)
 {
-    constexpr int SRC = F32SRC ? DT_F32 : DT_F16;
-    const uint32_t s2 = ss | (ss << 16), o2 = os | (os << 16);
-    if constexpr (SV || OV) {  // units: row blocks x upr
-        for (uint32_t v = blockIdx.x * 256u + threadIdx.x; v < units; v += gridDim.x * 256u) {
-            const uint32_t rb = fdiv(v, upr_div), w = v - rb * upr, r0 = rb * QP_UNR;
-            uint32_t sw[4] = {s2, s2, s2, s2}, ow[4] = {o2, o2, o2, o2};
-            if constexpr (SV) {
-                const u32x4 t = *(const u32x4*)(scale + 8 * w);
-                sw[0] = t.x, sw[1] = t.y, sw[2] = t.z, sw[3] = t.w;
-            }
-            if constexpr (OV) {
-                const u32x4 t = *(const u32x4*)(offset + 8 * w);
-                ow[0] = t.x, ow[1] = t.y, ow[2] = t.z, ow[3] = t.w;
-            }
-            Raw8<SRC> xr[QP_UNR];
+    uint32_t code[8];
+    if constexpr (F32A) {
 #pragma unroll
-            for (int k = 0; k < QP_UNR; ++k) {
-                const uint32_t r = r0 + k < rows ? r0 + k : rows - 1u;  // past the last row: reload it, store nothing
-                load_raw8<SRC>(x, r * upr + w, xr[k]);
-            }
+        for (int j = 0; j < 8; ++j) {
+            float v = raw8_at<SRC>(xr, j) * (sr ? raw8_at<SRC>(*sr, j) : a.sf);
+            v = v + (orr ? raw8_at<SRC>(*orr, j) : a.of);
+            code[j] = a.out == QD_E5M2 ? fp8_sat_hw<true>(v) : fp8_sat_hw<false>(v);
+        }
+    } else {
+        const uint32_t s2 = a.sh | (a.sh << 16), o2 = a.oh | (a.oh << 16);
 #pragma unroll
-            for (int k = 0; k < QP_UNR; ++k) {
-                if (r0 + k >= rows) break;
-                __builtin_nontemporal_store(quant_legacy_unit<F32SRC>(xr[k].w, sw, ow), q + (r0 + k) * upr + w);
+        for (int q = 0; q < 4; ++q) {
+            h2 t = __builtin_bit_cast(h2, half2_sat<SRC>(xr, q)) * __builtin_bit_cast(h2, sr ? half2_sat<SRC>(*sr, q) : s2);
+            t = t + __builtin_bit_cast(h2, orr ? half2_sat<SRC>(*orr, q) : o2);
+            if (a.out == QD_HIF8) {
+                code[2 * q] = hif8_code_rna_sat((float)t.x);
+                code[2 * q + 1] = hif8_code_rna_sat((float)t.y);
+            } else {
+                code[2 * q] = (uint32_t)quant_s8<RM_RINT>((float)t.x) & 0xffu;
+                code[2 * q + 1] = (uint32_t)quant_s8<RM_RINT>((float)t.y) & 0xffu;
             }
         }
-    } else {  // units: m * n / 8
-        const uint32_t sw[4] = {s2, s2, s2, s2}, ow[4] = {o2, o2, o2, o2};
-        for (uint32_t b0 = blockIdx.x * (256u * QP_UNR); b0 < units; b0 += gridDim.x * (256u * QP_UNR)) {
+    }
+    return (u32x2){code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24),
+                   code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24)};
+}
+
+// Vector path (cal_count % 8 == 0 and below 2^31, 16-byte aligned source and tensors, scale_count % 8 == 0): a unit
+// is 8 consecutive elements.  With channel tensors the data is rows = cal_count / scale_count rows of scale_count
+// channels; a lane takes the same 8 channels of QP_UNR consecutive rows and loads their scales / offsets once.  With
+// scalars, QP_UNR consecutive units per workgroup pass.  Each lane issues all loads before converting.
+template <int SRC, bool F32A, bool SV>
+__global__ __launch_bounds__(256) void quant_legacy_vec_kernel(QuantLegacyArgs a)
+{
+    u32x2* q = (u32x2*)a.q;
+    if constexpr (SV) {  // units: row blocks x upr
+        const bool ov = a.offset != nullptr;
+        for (uint32_t v = blockIdx.x * 256u + threadIdx.x; v < a.units; v += gridDim.x * 256u) {
+            const uint32_t rb = fdiv(v, a.upr_div), w = v - rb * a.upr, r0 = rb * QP_UNR;
+            Raw8<SRC> sr, orr, xr[QP_UNR];
+            load_raw8<SRC>(a.scale, w, sr);
+            load_raw8<SRC>(ov ? a.offset : a.scale, w, orr);
+#pragma unroll
+            for (int k = 0; k < QP_UNR; ++k) {
+                const uint32_t r = r0 + k < a.rows ? r0 + k : a.rows - 1u;  // past the last row: reload it, no store
+                load_raw8<SRC>(a.x, r * a.upr + w, xr[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < QP_UNR; ++k) {
+                if (r0 + k >= a.rows) break;
+                __builtin_nontemporal_store(quant_legacy_unit<SRC, F32A>(a, xr[k], &sr, ov ? &orr : nullptr),
+                                            q + (r0 + k) * a.upr + w);
+            }
+        }
+    } else {  // units: cal_count / 8
+        for (uint32_t b0 = blockIdx.x * (256u * QP_UNR); b0 < a.units; b0 += gridDim.x * (256u * QP_UNR)) {
             Raw8<SRC> xr[QP_UNR];
 #pragma unroll
             for (int k = 0; k < QP_UNR; ++k) {
                 const uint32_t u = b0 + k * 256u + threadIdx.x;
-                load_raw8<SRC>(x, u < units ? u : units - 1u, xr[k]);
+                load_raw8<SRC>(a.x, u < a.units ? u : a.units - 1u, xr[k]);
             }
 #pragma unroll
             for (int k = 0; k < QP_UNR; ++k) {
                 const uint32_t u = b0 + k * 256u + threadIdx.x;
-                if (u >= units) break;
-                __builtin_nontemporal_store(quant_legacy_unit<F32SRC>(xr[k].w, sw, ow), q + u);
+                if (u >= a.units) break;
+                __builtin_nontemporal_store(quant_legacy_unit<SRC, F32A>(a, xr[k], nullptr, nullptr), q + u);
             }
         }
     }
 }
 
-template <bool F32SRC, bool SV>
-static void launch_legacy_vec(const void* x, int8_t* q, const uint16_t* scale, const uint16_t* offset, uint32_t ss,
-                              uint32_t os, uint32_t cal_count, uint32_t sc, hipStream_t st)
+// Any shape or alignment: one thread per element.
+__global__ __launch_bounds__(256) void quant_legacy_elem_kernel(QuantLegacyArgs a)
 {
-    const bool vecs = SV || offset;
-    const uint32_t upr = vecs ? sc / 8 : 1u, rows = vecs ? cal_count / sc : 0u;
-    const uint32_t units = vecs ? (rows + QP_UNR - 1) / QP_UNR * upr : cal_count / 8;
-    const dim3 grid(grid_for(vecs ? units : (units + QP_UNR - 1) / QP_UNR)), block(256);
-    const FastDiv d = fast_div(upr);
-    if (offset)
-        launch_k(quant_legacy_vec_kernel<F32SRC, SV, true>, grid, block, 0, st, x, (u32x2*)q, scale, offset, ss, os,
-                 units, rows, upr, d);
+    const bool f32a = a.out == QD_E4M3 || a.out == QD_E5M2;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.total; i += (int64_t)gridDim.x * 256) {
+        const int64_t c = a.scale_count ? i % a.scale_count : 0;
+        const float x = load_scale_t(a.x, a.src_type, i);
+        uint32_t code;
+        if (f32a) {
+            float v = x * (a.scale ? load_scale_t(a.scale, a.src_type, c) : a.sf);
+            v = v + (a.offset ? load_scale_t(a.offset, a.src_type, c) : a.of);
+            code = a.out == QD_E5M2 ? fp8_sat_hw<true>(v) : fp8_sat_hw<false>(v);
+        } else {
+            const _Float16 sh = bits_h(a.scale ? f32_to_f16_sat(load_scale_t(a.scale, a.src_type, c)) : (uint16_t)a.sh);
+            const _Float16 oh = bits_h(a.offset ? f32_to_f16_sat(load_scale_t(a.offset, a.src_type, c)) : (uint16_t)a.oh);
+            _Float16 t = bits_h(f32_to_f16_sat(x)) * sh;
+            t = t + oh;
+            code = a.out == QD_HIF8 ? hif8_code_rna_sat((float)t) : ((uint32_t)quant_s8<RM_RINT>((float)t) & 0xffu);
+        }
+        ((uint8_t*)a.q)[i] = (uint8_t)code;
+    }
+}
+
+template <int SRC, bool F32A>
+static void launch_legacy_vec(const QuantLegacyArgs& a, hipStream_t st)
+{
+    if (a.scale)
+        launch_k(quant_legacy_vec_kernel<SRC, F32A, true>, dim3(grid_for(a.units)), dim3(256), 0, st, a);
     else
-        launch_k(quant_legacy_vec_kernel<F32SRC, SV, false>, grid, block, 0, st, x, (u32x2*)q, scale, offset, ss, os,
-                 units, rows, upr, d);
+        launch_k(quant_legacy_vec_kernel<SRC, F32A, false>, dim3(grid_for((a.units + QP_UNR - 1) / QP_UNR)), dim3(256),
+                 0, st, a);
 }
 
-hipError_t launch_quant_legacy(int8_t* q, const void* x, int src_type, const uint16_t* scale, const uint16_t* offset,
-                               uint16_t scale_scalar, uint16_t offset_scalar, uint32_t cal_count,
+template <int SRC>
+static void launch_legacy_vec_arith(const QuantLegacyArgs& a, hipStream_t st)
+{
+    if (a.out == QD_E4M3 || a.out == QD_E5M2) launch_legacy_vec<SRC, true>(a, st);
+    else launch_legacy_vec<SRC, false>(a, st);
+}
+
+hipError_t launch_quant_legacy(void* q, int dst_type, const void* x, int src_type, const void* scale,
+                               const void* offset, float scale_scalar, float offset_scalar, uint32_t cal_count,
                                uint32_t scale_count, hipStream_t st)
 {
-    const bool vecs = scale || offset;
-    const bool vec = cal_count % 8 == 0 && cal_count < (1u << 31) && (uintptr_t)x % 16 == 0 &&
-                     (uintptr_t)q % 8 == 0 && (!vecs || (scale_count % 8 == 0 && scale_count > 0)) &&
-                     (uintptr_t)scale % 16 == 0 && (uintptr_t)offset % 16 == 0;
+    (void)hipGetLastError();
+    QuantLegacyArgs a{};
+    a.q = q;
+    a.x = x;
+    a.scale = scale;
+    a.offset = scale ? offset : nullptr;
+    a.out = dst_type == DT_HIF8 ? QD_HIF8 : (dst_type == DT_FP8_E4M3 ? QD_E4M3 : (dst_type == DT_FP8_E5M2 ? QD_E5M2 : QD_INT8));
+    a.src_type = src_type;
+    // a scale tensor's scalar offset is a srcT value (the `const T offset` overloads)
+    float os = offset_scalar;
+    if (scale && src_type == DT_F16) {
+        os = (float)(_Float16)os;
+    } else if (scale && src_type == DT_BF16) {
+        uint32_t u = __builtin_bit_cast(uint32_t, os);
+        if ((u & 0x7fffffffu) <= 0x7f800000u) u = ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16) << 16;
+        os = __builtin_bit_cast(float, u);
+    }
+    a.sf = scale_scalar;
+    a.of = os;
+    a.sh = __builtin_bit_cast(uint16_t, (_Float16)scale_scalar);  // static_cast<half>: rne, IEEE overflow
+    a.oh = __builtin_bit_cast(uint16_t, (_Float16)os);
+    a.scale_count = scale ? scale_count : 0u;
+    a.total = cal_count;
+    const bool vec = cal_count % 8 == 0 && cal_count < (1u << 31) && (uintptr_t)x % 16 == 0 && (uintptr_t)q % 8 == 0 &&
+                     (!scale || (scale_count % 8 == 0 && (uintptr_t)scale % 16 == 0 && (uintptr_t)a.offset % 16 == 0));
     if (vec && cal_count > 0) {
-        const bool f32 = src_type == DT_F32;
-        if (f32) {
-            if (scale) launch_legacy_vec<true, true>(x, q, scale, offset, scale_scalar, offset_scalar, cal_count, scale_count, st);
-            else launch_legacy_vec<true, false>(x, q, scale, offset, scale_scalar, offset_scalar, cal_count, scale_count, st);
-        } else {
-            if (scale) launch_legacy_vec<false, true>(x, q, scale, offset, scale_scalar, offset_scalar, cal_count, scale_count, st);
-            else launch_legacy_vec<false, false>(x, q, scale, offset, scale_scalar, offset_scalar, cal_count, scale_count, st);
-        }
+        a.upr = scale ? scale_count / 8 : 1u;
+        a.rows = scale ? cal_count / scale_count : 0u;
+        a.units = scale ? (a.rows + QP_UNR - 1) / QP_UNR * a.upr : cal_count / 8;
+        a.upr_div = fast_div(a.upr);
+        if (src_type == DT_F16) launch_legacy_vec_arith<DT_F16>(a, st);
+        else if (src_type == DT_BF16) launch_legacy_vec_arith<DT_BF16>(a, st);
+        else launch_legacy_vec_arith<DT_F32>(a, st);
         return hipGetLastError();
     }
-    dim3 grid(grid_for(cal_count)), block(256);
-    launch_k(quant_legacy_f16_kernel, grid, block, 0, st, x, q, scale, offset, scale_scalar, offset_scalar,
-                       (int64_t)cal_count, scale_count, src_type);
+    launch_k(quant_legacy_elem_kernel, dim3(grid_for(cal_count)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
@@ -989,8 +1090,8 @@ __global__ __launch_bounds__(256) void quant_policy_generic_kernel(QuantPolicyAr
                                                                                 : (r / a.g) * a.n + c);
             const float x = load_scale_t(a.src, a.src_type, e);
             const float s = load_scale_t(a.scale, a.scale_type, si);
-            float v = rnd_t<T>(x * s);
-            if (a.has_off) v = rnd_t<T>(v + (a.offset ? load_scale_t(a.offset, a.scale_type, si) : a.off_scalar));
+            float v = mul_t<T>(x, s);
+            if (a.has_off) v = add_t<T>(v, a.offset ? load_scale_t(a.offset, a.scale_type, si) : a.off_scalar);
             w |= quant_code_rt<DST, T>(v, a.round_mode) << (4 * h);
         }
         ((uint8_t*)a.dst)[b] = (uint8_t)w;
@@ -1010,7 +1111,7 @@ static void launch_qp_layout(const QuantPolicyArgs& a, hipStream_t st)
 template <int DST, int SRC, int SC>
 static void launch_qp_vec(const QuantPolicyArgs& a, hipStream_t st)
 {
-    if constexpr (DST == QD_E4M3 || DST == QD_E5M2) {  // every round mode is rint for fp8
+    if constexpr (DST == QD_E4M3 || DST == QD_E5M2 || DST == QD_HIF8) {  // one rounding whatever the mode
         launch_qp_layout<DST, SRC, SC, RM_RINT>(a, st);
         return;
     }
@@ -1059,6 +1160,7 @@ hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src
                                int64_t m, int64_t n, int64_t g, int k_dim, int round_mode, hipStream_t st)
 {
     const int dk = dst_type == DT_INT8 ? QD_INT8
+                   : dst_type == DT_HIF8 ? QD_HIF8
                    : dst_type == DT_FP8_E4M3 ? QD_E4M3
                    : dst_type == DT_FP8_E5M2 ? QD_E5M2
                    : dst_type == DT_FP4_E1M2 ? QD_E1M2 : QD_E2M1;
@@ -1107,6 +1209,10 @@ hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src
         if (t == DT_F16) launch_qp<QD_INT8, DT_F16>(a, vec, st);
         else if (t == DT_BF16) launch_qp<QD_INT8, DT_BF16>(a, vec, st);
         else launch_qp<QD_INT8, DT_F32>(a, vec, st);
+    } else if (dk == QD_HIF8) {  // the int8 path's scaleT arithmetic
+        if (t == DT_F16) launch_qp<QD_HIF8, DT_F16>(a, vec, st);
+        else if (t == DT_BF16) launch_qp<QD_HIF8, DT_BF16>(a, vec, st);
+        else launch_qp<QD_HIF8, DT_F32>(a, vec, st);
     } else if (dk == QD_E1M2) {
         if (t == DT_F16) launch_qp<QD_E1M2, DT_F16>(a, vec, st);
         else if (t == DT_BF16) launch_qp<QD_E1M2, DT_BF16>(a, vec, st);
@@ -1151,9 +1257,10 @@ __global__ __launch_bounds__(256) void antiquant_policy_kernel(void* __restrict_
             store_cast(dst, idx, v, dst_type);
             continue;
         }
-        float v = (float)((const int8_t*)src)[idx];  // arithmetic in the scale type
-        if (offset) v = round_scale_t(v + o, scale_type);
-        v = round_scale_t(v * s, scale_type);
+        const uint32_t code = ((const uint8_t*)src)[idx];
+        float v = src_type == DT_HIF8 ? hif8_to_f32(code) : (float)(int8_t)code;  // arithmetic in the scale type
+        if (offset) v = add_rt(v, o, scale_type);
+        v = mul_rt(v, s, scale_type);
         if (scale_type == DT_F16) ((uint16_t*)dst)[idx] = f32_to_f16(v);
         else if (scale_type == DT_BF16) ((uint16_t*)dst)[idx] = (uint16_t)(__float_as_uint(v) >> 16);
         else store_cast(dst, idx, v, dst_type);
@@ -1221,10 +1328,11 @@ __device__ __forceinline__ void aq_unit(const AntiQuantVecArgs& a, uint32_t u, u
                 float v = fp8_bits_to_f32(code, SRC == DT_FP8_E5M2);
                 if (has_off) v = v + o;
                 y[j] = v * s;
-            } else {  // int8 / int4: arithmetic in AR (the scale type, or fp32 for the legacy fp32 path)
-                float v = SRC == DT_INT4 ? (float)((int32_t)(xw0 << (28 - 4 * j)) >> 28) : (float)(int8_t)code;
-                if (has_off) v = rnd_t<AR>(v + o);
-                y[j] = rnd_t<AR>(v * s);
+            } else {  // int8 / int4 / hifloat8: arithmetic in AR (the scale type, or the legacy form's choice)
+                float v = SRC == DT_INT4 ? (float)((int32_t)(xw0 << (28 - 4 * j)) >> 28)
+                                         : (SRC == DT_HIF8 ? hif8_to_f32(code) : (float)(int8_t)code);
+                if (has_off) v = add_t<AR>(v, o);
+                y[j] = mul_t<AR>(v, s);
             }
         }
     }
@@ -1369,7 +1477,7 @@ static void launch_aq_scale(const AntiQuantVecArgs& a, int dst_type, int scale_t
 {
     if constexpr (SRC == DT_FP4_E2M1 || SRC == DT_FP4_E1M2) {
         launch_aq_dst<SRC, DT_E8M0>(a, dst_type, eight, st);
-    } else if constexpr (SRC == DT_INT8) {  // a 16-bit scale writes its own type
+    } else if constexpr (SRC == DT_INT8 || SRC == DT_HIF8) {  // a 16-bit scale writes its own type
         if (scale_type == DT_F16) launch_aq_vec<SRC, DT_F16, DT_F16>(a, eight, st);
         else if (scale_type == DT_BF16) launch_aq_vec<SRC, DT_BF16, DT_BF16>(a, eight, st);
         else launch_aq_dst<SRC, DT_F32>(a, dst_type, eight, st);
@@ -1405,6 +1513,7 @@ hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int
         a.upr_div = fast_div(a.upr);
         a.g_div = fast_div((uint32_t)gv);
         if (src_type == DT_INT8) launch_aq_scale<DT_INT8>(a, dst_type, scale_type, eight, st);
+        else if (src_type == DT_HIF8) launch_aq_scale<DT_HIF8>(a, dst_type, scale_type, eight, st);
         else if (src_type == DT_FP8_E4M3) launch_aq_scale<DT_FP8_E4M3>(a, dst_type, scale_type, eight, st);
         else if (src_type == DT_FP8_E5M2) launch_aq_scale<DT_FP8_E5M2>(a, dst_type, scale_type, eight, st);
         else if (src_type == DT_FP4_E1M2) launch_aq_scale<DT_FP4_E1M2>(a, dst_type, scale_type, eight, st);
@@ -1425,9 +1534,81 @@ hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int
 template <int SRC>
 static void launch_antiquant_legacy_vec(const AntiQuantVecArgs& a, int dst_type, int arith, bool eight, hipStream_t st)
 {
-    if (dst_type == DT_BF16) launch_aq_vec<SRC, DT_BF16, DT_BF16, DT_F32>(a, eight, st);
-    else if (arith == 0) launch_aq_vec<SRC, DT_F16, DT_F16, DT_F16>(a, eight, st);
-    else launch_aq_vec<SRC, DT_F16, DT_F16, DT_F32>(a, eight, st);
+    if constexpr (SRC == DT_FP8_E4M3 || SRC == DT_FP8_E5M2) {  // fp32 ops, one rne cast, whatever arith
+        if (dst_type == DT_BF16) launch_aq_vec<SRC, DT_BF16, DT_BF16, DT_F32>(a, eight, st);
+        else launch_aq_vec<SRC, DT_F16, DT_F16, DT_F32>(a, eight, st);
+    } else if constexpr (SRC == DT_HIF8) {  // half ops to f16; bf16 ops along rows ([K, N]), fp32 ops transposed
+        if (dst_type == DT_F16) launch_aq_vec<SRC, DT_F16, DT_F16, DT_F16>(a, eight, st);
+        else if (eight) launch_aq_vec<SRC, DT_BF16, DT_BF16, DT_BF16>(a, eight, st);
+        else launch_aq_vec<SRC, DT_BF16, DT_BF16, DT_F32>(a, eight, st);
+    } else {
+        if (dst_type == DT_BF16) launch_aq_vec<SRC, DT_BF16, DT_BF16, DT_F32>(a, eight, st);
+        else if (arith == 0) launch_aq_vec<SRC, DT_F16, DT_F16, DT_F16>(a, eight, st);
+        else launch_aq_vec<SRC, DT_F16, DT_F16, DT_F32>(a, eight, st);
+    }
+}
+
+// AscendAntiQuant per tensor (scalar offset / scale of the output type): a unit is 8 consecutive elements, AQ_UNR
+// units per lane, every load issued before converting; the scalars ride in the argument block.
+template <int SRC, int DST, int AR>
+__global__ __launch_bounds__(256) void antiquant_scalar_vec_kernel(AntiQuantVecArgs a, uint32_t sbits, uint32_t obits,
+                                                                   int has_off)
+{
+    for (uint32_t b0 = blockIdx.x * (256u * AQ_UNR); b0 < a.units; b0 += gridDim.x * (256u * AQ_UNR)) {
+        uint32_t x0[AQ_UNR], x1[AQ_UNR];
+#pragma unroll
+        for (int k = 0; k < AQ_UNR; ++k) {
+            const uint32_t u = b0 + k * 256u + threadIdx.x;
+            aq_load_src<SRC>(a.src, u < a.units ? u : a.units - 1u, x0[k], x1[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < AQ_UNR; ++k) {
+            const uint32_t u = b0 + k * 256u + threadIdx.x;
+            if (u >= a.units) break;
+            aq_unit<SRC, DST, DST, false, AR>(a, u, x0[k], x1[k], &sbits, &obits, has_off != 0);
+        }
+    }
+}
+
+template <int SRC, int DST>
+static void launch_aq_scalar(const AntiQuantVecArgs& a, int ar, uint32_t sb, uint32_t ob, int has_off, hipStream_t st)
+{
+    const dim3 grid(grid_for((a.units + AQ_UNR - 1) / AQ_UNR)), block(256);
+    if (ar == DT_F16) launch_k(antiquant_scalar_vec_kernel<SRC, DST, DT_F16>, grid, block, 0, st, a, sb, ob, has_off);
+    else launch_k(antiquant_scalar_vec_kernel<SRC, DST, DT_F32>, grid, block, 0, st, a, sb, ob, has_off);
+}
+
+template <int SRC>
+static void launch_aq_scalar_dst(const AntiQuantVecArgs& a, int dst_type, int ar, uint32_t sb, uint32_t ob,
+                                 int has_off, hipStream_t st)
+{
+    if (dst_type == DT_F16) launch_aq_scalar<SRC, DT_F16>(a, ar, sb, ob, has_off, st);
+    else launch_aq_scalar<SRC, DT_BF16>(a, ar, sb, ob, has_off, st);
+}
+
+hipError_t launch_antiquant_scalar(void* dst, int dst_type, const void* src, int src_type, uint16_t offset,
+                                   uint16_t scale, int has_offset, int64_t count, hipStream_t st)
+{
+    (void)hipGetLastError();
+    const int ar = aq_arith(src_type, dst_type, 0, 1, dst_type == DT_F16 ? 0 : 1);
+    const int64_t sbytes = src_type == DT_INT4 ? 4 : 8;  // source bytes per 8 elements
+    if (count % 8 == 0 && count / 8 < (1ll << 31) && (uintptr_t)src % sbytes == 0 && (uintptr_t)dst % 16 == 0) {
+        AntiQuantVecArgs a{};
+        a.dst = dst;
+        a.src = src;
+        a.units = (uint32_t)(count / 8);
+        if (src_type == DT_INT8) launch_aq_scalar_dst<DT_INT8>(a, dst_type, ar, scale, offset, has_offset, st);
+        else if (src_type == DT_INT4) launch_aq_scalar_dst<DT_INT4>(a, dst_type, ar, scale, offset, has_offset, st);
+        else if (src_type == DT_HIF8) launch_aq_scalar_dst<DT_HIF8>(a, dst_type, ar, scale, offset, has_offset, st);
+        else if (src_type == DT_FP8_E4M3) launch_aq_scalar_dst<DT_FP8_E4M3>(a, dst_type, ar, scale, offset, has_offset, st);
+        else launch_aq_scalar_dst<DT_FP8_E5M2>(a, dst_type, ar, scale, offset, has_offset, st);
+        return hipGetLastError();
+    }
+    const float sc = dst_type == DT_F16 ? (float)__builtin_bit_cast(_Float16, scale) : __builtin_bit_cast(float, (uint32_t)scale << 16);
+    const float of = dst_type == DT_F16 ? (float)__builtin_bit_cast(_Float16, offset) : __builtin_bit_cast(float, (uint32_t)offset << 16);
+    launch_k(antiquant_scalar_elem_kernel, dim3(grid_for(count)), dim3(256), 0, st, dst, dst_type, src, src_type, of, sc,
+             has_offset, count);
+    return hipGetLastError();
 }
 
 hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset,
@@ -1453,6 +1634,9 @@ hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_ty
             a.upr_div = fast_div(a.upr);
             a.g_div = fast_div(g);
             if (src_type == DT_INT4) launch_antiquant_legacy_vec<DT_INT4>(a, dst_type, arith, eight, st);
+            else if (src_type == DT_HIF8) launch_antiquant_legacy_vec<DT_HIF8>(a, dst_type, arith, eight, st);
+            else if (src_type == DT_FP8_E4M3) launch_antiquant_legacy_vec<DT_FP8_E4M3>(a, dst_type, arith, eight, st);
+            else if (src_type == DT_FP8_E5M2) launch_antiquant_legacy_vec<DT_FP8_E5M2>(a, dst_type, arith, eight, st);
             else launch_antiquant_legacy_vec<DT_INT8>(a, dst_type, arith, eight, st);
             return hipGetLastError();
         }

@@ -58,8 +58,11 @@ typedef enum {
     ASCQ_DT_FP4_E2M1 = 11, /* fp4x2_e2m1_t, two per byte, even element in the low nibble */
     ASCQ_DT_E8M0 = 12,     /* fp8_e8m0_t shared exponent */
     ASCQ_DT_INT64 = 13,
-    ASCQ_DT_FP4_E1M2 = 14  /* fp4x2_e1m2_t: sign | 1-bit exponent (bias 1) | 2-bit mantissa, magnitudes k / 4,
+    ASCQ_DT_FP4_E1M2 = 14, /* fp4x2_e1m2_t: sign | 1-bit exponent (bias 1) | 2-bit mantissa, magnitudes k / 4,
                               k = 0..7; two per byte, even element in the low nibble */
+    ASCQ_DT_HIF8 = 15      /* hifloat8_t: sign | dot field (11 / 10 / 01 / 001 / 0001 / 0000) | exponent | mantissa
+                              (layout of impl/utils/debug/npu_arch_9201/asc_type_conversion_utils.h:62-149); finite
+                              range 2^-22 .. 2^15, 0x80 NaN, 0x6F / 0xEF +-inf */
 } ascq_dtype;
 
 /* RoundMode (impl/basic_api/utils/kernel_utils_mode.h:103-118). NONE acts as RINT on lossy casts. */
@@ -256,6 +259,9 @@ ascq_status ascq_ascend_quant_dynamic_per_token(int8_t* dst, float* scale_out, c
  *   INT8: y = x * scale (+ offset), each op rounded in scale_type, then clamp(round_mode(y), -128, 127), NaN -> 0;
  *   FP8_E4M3 / FP8_E5M2: the same ops in fp32 whatever scale_type, then rint with saturation (overflow and
  *         inf -> +-max finite, NaN -> 0); round_mode is not used (every mode is rint, :888-896);
+ *   HIF8: the INT8 arithmetic (in scale_type), then ties away from zero with saturation at +-32768, NaN -> 0
+ *         (TransRegForHif8, ascend_quant_3510_impl.h:899-933: every round mode but CAST_HYBRID, which this library does
+ *         not take, is CAST_ROUND);
  *   FP4_E2M1 (PER_GROUP only; offset ignored, :1385): y = x * scale in scale_type; an f16 / f32 y is rounded to
  *         bf16 (rne, saturating, NaN -> 0); then E2M1 in round_mode with saturation at +-6; two codes a byte, even
  *         element in the low nibble (n even);
@@ -265,17 +271,26 @@ ascq_status ascq_ascend_quant_dynamic_per_token(int8_t* dst, float* scale_out, c
  * of the same type (a 16-bit source meets an F32 scale as fp32); FP8 accepts every pair.
  * Offset (para->has_offset): the tensor `offset` (scale_type, indexed like scale) or, when it is NULL, the scalar
  * offset_scalar rounded (rne) to scale_type -- the overloads taking `const scaleT offset` (ascend_quant.h:737-777).
- * hifloat8 outputs are not accepted (no gfx950 encoding). */
+ */
 ascq_status ascq_ascend_quant_policy(void* dst, int32_t dst_type, const void* src, int32_t src_type,
                                      const void* scale, const void* offset, float offset_scalar, int32_t scale_type,
                                      int32_t policy, const ascq_quant_param* para, void* stream);
-/* Legacy AscendQuant per-tensor / per-channel, half arithmetic (ascend_quant.h:64-293;
- * impl ascend_quant_pre_impl.h:101-164, 320-483).  src_type F16 or F32.
- * scale / offset: device half vectors of scale_count elements, or NULL to use the scalars
- * (half bit patterns).  Element i uses scale[i % scale_count]; scale_count must divide cal_count. */
-ascq_status ascq_ascend_quant(int8_t* dst, const void* src, int32_t src_type, const uint16_t* scale,
-                              const uint16_t* offset, uint16_t scale_scalar, uint16_t offset_scalar,
-                              uint32_t cal_count, uint32_t scale_count, void* stream);
+/* Legacy AscendQuant, the arch-3510 form (include/adv_api/quantization/ascend_quant.h:64-293, 360-460; impl
+ * impl/adv_api/detail/quantization/quant/ascend_quant_3510_impl.h:35-620):
+ *   scale == NULL: AscendQuant(dst, src, const float scale, const float offset, calCount) -- scale_scalar and
+ *     offset_scalar for every element (offset must be NULL too);
+ *   scale != NULL: the per-channel overloads, element i using channel i % scale_count of `scale` and `offset`
+ *     (srcT tensors of scale_count elements); offset == NULL is the `const T offset` overload, offset_scalar rounded
+ *     (rne) to srcT.  calCount must be a multiple of 32 and of scale_count (ascend_quant_3510_impl.h:551-557).
+ * src_type F16, BF16 or F32.  dst_type and arithmetic:
+ *   INT8 / HIF8: half arithmetic -- source and srcT tensors cast to half with rne and saturation, the float scalars
+ *     with rne (static_cast<half>); t = half(x * s); t = half(t + o); INT8: rint with saturation (NaN -> 0); HIF8:
+ *     ties away from zero with saturation (+-32768; NaN -> 0);
+ *   FP8_E4M3 / FP8_E5M2: fp32 arithmetic (exact conversions), rint with saturation, NaN -> 0.
+ * dst holds cal_count bytes. */
+ascq_status ascq_ascend_quant(void* dst, int32_t dst_type, const void* src, int32_t src_type, const void* scale,
+                              const void* offset, float scale_scalar, float offset_scalar, uint32_t cal_count,
+                              uint32_t scale_count, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * AscendDequant
@@ -350,12 +365,25 @@ ascq_status ascq_ascend_dequant_policy(void* dst, int32_t dst_type, const void* 
  * (include/adv_api/quantization/ascend_antiquant.h:47-225; AntiQuantShapeInfo ascend_antiquant_utils.h:26-31;
  * impl ascend_antiquant_impl.h:48-96, 285-411, ascend_antiquant_c220_impl.h:46-100).
  *   dst = (src + offset) * scale.  src_type INT8 or INT4; dst_type F16 or BF16 (offset/scale are dst_type).
+ *   src_type HIF8 / FP8_E4M3 / FP8_E5M2 (arch 3510, per channel only: group_size 0; AntiQuantPerchannelImpl
+ *   ascend_antiquant_3510_impl.h:752-770): fp8 in fp32 ops with one rne cast; hifloat8 in half ops to F16, in bf16 ops
+ *   to BF16 when not transposed (PerchannelNoTransposeForB8 :470-495) and in fp32 ops when transposed
+ *   (PerchannelTransposeForB8 :646-687); `arith` applies to INT8 / INT4 only.
  *   is_transpose 0: src [K, N], offset/scale [K/group, N];  1: src [N, K], offset/scale [N, K/group].
  *   group_size 0 = per-channel ([1, N] / [N, 1]).  offset NULL = scale only.  arith: ascq_arith
  *   (BF16 output always uses fp32 arithmetic). */
 ascq_status ascq_ascend_antiquant(void* dst, int32_t dst_type, const void* src, int32_t src_type,
                                   const void* offset, const void* scale, uint32_t k, uint32_t n,
                                   uint32_t group_size, int32_t is_transpose, int32_t arith, void* stream);
+/* AscendAntiQuant with scalar offset and scale of the output type, per tensor
+ * (include/adv_api/quantization/ascend_antiquant.h:136-210; arch 3510 AntiQuantPertensorImpl,
+ * impl/adv_api/detail/quantization/antiquant/ascend_antiquant_3510_impl.h:301-415):
+ *   dst[i] = (src[i] + offset) * scale for i < count (has_offset 0: the scale-only overload, :166-190);
+ * offset / scale are f16 or bf16 bit patterns of dst_type.  src INT8, INT4, HIF8: half ops for F16, fp32 ops and one
+ * rne cast for BF16 (PerTensorProcessForB8 :334-392); FP8_E4M3 / FP8_E5M2: fp32 ops (PerTensorProcessForFp8 :301-333). */
+ascq_status ascq_ascend_antiquant_scalar(void* dst, int32_t dst_type, const void* src, int32_t src_type,
+                                         uint16_t offset, uint16_t scale, int32_t has_offset, uint64_t count,
+                                         void* stream);
 
 /* AscendAntiQuant<dstT, srcT, scaleT, config{hasOffset, isTranspose, kDim}, policy>(dst, src, scale, offset,
  * {m, n, calCount = m * n, groupSize}), the arch-3510 policy form (include/adv_api/quantization/ascend_antiquant.h:
@@ -367,14 +395,13 @@ ascq_status ascq_ascend_antiquant(void* dst, int32_t dst_type, const void* src, 
  *              (k_dim == 0 && is_transpose); else along the rows, scale[r / group][c] ([ceil(m/group)][n]);
  *              group_size a positive multiple of 32.
  * Arithmetic:
- *   src INT8: (src + offset) * scale, each op rounded in scale_type (F16 / BF16 / F32); a 16-bit scale_type
+ *   src INT8 / HIF8: (src + offset) * scale, each op rounded in scale_type (F16 / BF16 / F32); a 16-bit scale_type
  *             writes dst of that type, F32 writes F32 or casts rne + saturating to F16 / BF16;
  *   src FP8_E4M3 / FP8_E5M2: the same in fp32 whatever scale_type (F16 / BF16 / F32), cast to dst;
  *   src FP4_E2M1 ([m, n/2] bytes, even element in the low nibble; n even): PER_GROUP only, scale_type E8M0
  *             (2^(e-127); e = 0 -> 2^-127, e = 255 -> NaN), no offset; bf16(src) * bf16(scale) rounded to bf16,
  *             dst BF16 or F16 (saturating cast);
  *   src FP4_E1M2: as FP4_E2M1 with E1M2 codes (exact in bf16; :2144-2159 route both fp4 types alike).
- * hifloat8 sources are not accepted (no gfx950 encoding).
  * (ConvertSrc / StoreF32Res: ascend_antiquant_3510_impl.h:1363-1403; fp4 kernels :1724-1828) */
 ascq_status ascq_ascend_antiquant_policy(void* dst, int32_t dst_type, const void* src, int32_t src_type,
                                          const void* scale, const void* offset, int32_t scale_type, int32_t policy,

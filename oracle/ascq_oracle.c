@@ -176,6 +176,83 @@ uint8_t oq_mx_shared_exp(float amax)
 }
 
 /* fp8: fmt OQ_FP8_E4M3 (e4m3fn: bias 7, no inf, 0x7f/0xff NaN) or OQ_FP8_E5M2 (bias 15, IEEE inf/NaN) */
+/* HiFloat8 (impl/utils/debug/npu_arch_9201/asc_type_conversion_utils.h:62-149): bit 7 is the sign; a prefix-coded
+ * dot field starting at bit 6 gives the exponent width w -- 11: 4, 10: 3, 01: 2, 001: 1, 0001: 0 -- and the
+ * mantissa takes the 7 - |dot| - w bits left; a w-bit exponent field stores the exponent's sign in its top bit and
+ * its magnitude with that bit replaced by an implicit 1 (so |E| lies in [2^(w-1), 2^w - 1]); value
+ * (-1)^S 2^E (1 + M / 2^mw).  Dot 0000 is the subnormal class 2^(M - 23), M = 1..7 (M = 0: zero, or NaN with the
+ * sign bit, 0x80); 0x6F / 0xEF (E = +15 with M = 1) are +-inf.  Largest finite 2^15 (0x6E), smallest 2^-22. */
+float oq_hif8_decode(uint8_t code)
+{
+    if (code == 0x00u) return 0.0f;
+    if (code == 0x80u) return NAN;
+    if (code == 0x6Fu) return INFINITY;
+    if (code == 0xEFu) return -INFINITY;
+    const int neg = code >> 7;
+    double v;
+    if ((code & 0x78u) == 0) {
+        v = ldexp(1.0, (int)(code & 7u) - 23);
+    } else {
+        int w, dw;
+        if (code & 0x40u) w = (code & 0x20u) ? 4 : 3, dw = 2;
+        else if (code & 0x20u) w = 2, dw = 2;
+        else if (code & 0x10u) w = 1, dw = 3;
+        else w = 0, dw = 4;
+        const int mw = 7 - dw - w;
+        const int mant = code & ((1 << mw) - 1);
+        int e = 0;
+        if (w > 0) {
+            const int field = (code >> mw) & ((1 << w) - 1);
+            const int mag = (field & ((1 << (w - 1)) - 1)) | (1 << (w - 1));
+            e = ((field >> (w - 1)) ^ (OQ_MUTANT == 34 && w == 1)) ? -mag : mag;
+        }
+        v = ldexp(1.0 + (double)mant / (double)(1 << mw), e);
+    }
+    return (float)(neg ? -v : v);
+}
+
+/* x -> HiFloat8 under CAST_ROUND, the rule of docs/zh/api/SIMD-API/basic_api/reg_vector_compute/type_conversion/
+ * Cast.md:254-301 (float source; a half source is the same value, :303-348): E = the unbiased exponent; E > 15 and
+ * inf overflow, NaN is 0x80, E < -23 gives 0 (0x00, whatever the sign), E = -23 gives the smallest subnormal
+ * 2^-22; E in [-22, -16] rounds to 2^E or 2^(E+1) on the first fraction bit; otherwise the mantissa keeps 3 bits
+ * for |E| <= 3, 2 for |E| in [4, 7], 1 for |E| in [8, 15] and rounds up on the next bit (ties away), carrying
+ * into E.  Saturation (the SatS casts; __half22hif82_rna_sat.md's table: nan -> 0, +-inf and +-65504 -> +-32768,
+ * +-0 -> 0) turns every overflow code into +-32768. */
+uint8_t oq_hif8_encode(float x, int sat)
+{
+    const uint32_t u = f2u(x), a = u & 0x7fffffffu;
+    const uint8_t s = (uint8_t)((u >> 24) & 0x80u);
+    if (a > 0x7f800000u) return sat ? 0x00u : 0x80u;
+    const uint8_t over = (uint8_t)(s | (sat ? 0x6Eu : 0x6Fu));
+    if (a == 0x7f800000u) return over;
+    int e = (int)(a >> 23) - 127;
+    const uint32_t f = a & 0x7fffffu;
+    if (e > 15) return over;
+    if (e < -23) return 0x00u;
+    if (e == -23) return (uint8_t)(s | 0x01u);
+    int m = 0;
+    if (e <= -16) {
+        if (f >> 22) ++e;  /* rounds up to the next power of two */
+        if (e <= -16) return (uint8_t)(s | (uint8_t)(e + 23));
+    } else {
+        const int ae = e < 0 ? -e : e;
+        const int mw = ae <= 3 ? 3 : (ae <= 7 ? 2 : 1);
+        m = (int)(f >> (23 - mw));
+        const int tie = (f & ((1u << (22 - mw)) - 1u)) == 0;
+        if (((f >> (22 - mw)) & 1u) && !(OQ_MUTANT == 33 && tie)) {
+            if (++m >> mw) m = 0, ++e;
+        }
+    }
+    if (e > 15 || (e == 15 && m != 0)) return over;  /* E = 15, M = 1 is the inf code */
+    const int ae = e < 0 ? -e : e, ng = e < 0;
+    if (OQ_MUTANT == 31 && ae >= 2) return (uint8_t)(s | 0x20u | ((ae & 3) << 3) | m);
+    if (ae == 0) return (uint8_t)(s | 0x08u | m);
+    if (ae == 1) return (uint8_t)(s | 0x10u | (ng << 3) | m);
+    if (ae <= 3) return (uint8_t)(s | 0x20u | (((ng << 1) | (ae & 1)) << 3) | m);
+    if (ae <= 7) return (uint8_t)(s | 0x40u | (((ng << 2) | (ae & 3)) << 2) | m);
+    return (uint8_t)(s | 0x60u | (((ng << 3) | (ae & 7)) << 1) | m);
+}
+
 float oq_fp8_decode(uint8_t v, int fmt)
 {
     int s = v >> 7;
@@ -286,6 +363,13 @@ void oq_requant4_f32(const float* v, uint8_t* out, int64_t M, int64_t N, const u
             }
             out[(m * N + n) / 2] = OQ_MUTANT == 18 ? (uint8_t)(q[1] | (q[0] << 4)) : (uint8_t)(q[0] | (q[1] << 4));
         }
+}
+
+static inline double round_to(double x, int t) /* one IEEE rounding into scaleT (half / bf16 / fp32), rne */
+{
+    if (t == OQ_F16) return oq_f16_to_f32(oq_f64_to_f16(x, 0));
+    if (t == OQ_BF16) return oq_bf16_to_f32(oq_f64_to_bf16(x, 0));
+    return (double)(float)x;
 }
 
 static inline float load_as_f32(const void* p, int type, int64_t i)
@@ -480,6 +564,46 @@ void oq_quant_dynamic_per_token(int8_t* dst, float* scale_out, const void* src, 
     }
 }
 
+/* Legacy AscendQuant, arch-3510 form (include/adv_api/quantization/ascend_quant.h:64-293, 360-460; impl
+ * impl/adv_api/detail/quantization/quant/ascend_quant_3510_impl.h:35-620).  Element i of cal_count uses channel
+ * c = i % scale_count of the srcT scale / offset tensors, or the float scalars when scale is NULL; a scale tensor with
+ * offset NULL is the `const T offset` overload (offset_scalar rounded to srcT).
+ *  - int8 / hifloat8 out (QuantPertensorForB8 :35-128, QuantPerchannelForB8 :292-483): source, scale and offset
+ *    tensors become half with rne and saturation (MrgZRndRSatS / LayoutZMrgZRndRSatS), the float scalars with a
+ *    plain rne conversion (static_cast<half>); t = half(x * s); t = half(t + o); int8: rint with saturation
+ *    (LayoutZMrgZRndRSatS), NaN -> 0; hifloat8: ties away with saturation (LayoutZMrgZRndASatS).
+ *  - fp8 e4m3 / e5m2 out (QuantPertensorForFp8 :144-170, QuantPerchannelForFp8 :207-260, :483-530): source, scale and
+ *    offset in fp32 (exact); y = f32(x * s); y = f32(y + o); rint with saturation (NaN -> 0). */
+void oq_quant_legacy(void* dst, int dst_type, const void* src, int src_type, const void* scale, const void* offset,
+                     float scale_scalar, float offset_scalar, int64_t cal_count, int64_t scale_count)
+{
+    const int fp8 = (dst_type == OQ_FP8_E4M3 || dst_type == OQ_FP8_E5M2) && OQ_MUTANT != 32;
+    /* the `const T offset` overload: a srcT value */
+    const float os = scale ? (float)round_to((double)offset_scalar, src_type) : offset_scalar;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < cal_count; ++i) {
+        const int64_t c = scale_count > 0 ? i % scale_count : 0;
+        const float x = load_as_f32(src, src_type, i);
+        const float s = scale ? load_as_f32(scale, src_type, c) : scale_scalar;
+        const float o = offset ? load_as_f32(offset, src_type, c) : os;
+        if (fp8) {
+            float v = (float)((double)x * (double)s); /* one fp32 rounding of the exact product */
+            v = (float)((double)v + (double)o);
+            ((uint8_t*)dst)[i] = oq_f32_to_fp8_sat(v, dst_type);
+            continue;
+        }
+        const uint16_t xh = src_type == OQ_F16 ? ((const uint16_t*)src)[i] : oq_f32_to_f16(x, 1);
+        const uint16_t sh = scale ? (src_type == OQ_F16 ? oq_f32_to_f16(s, 0) : oq_f32_to_f16(s, 1)) : oq_f32_to_f16(s, 0);
+        const uint16_t oh = offset ? (src_type == OQ_F16 ? oq_f32_to_f16(o, 0) : oq_f32_to_f16(o, 1)) : oq_f32_to_f16(o, 0);
+        uint16_t t = oq_f64_to_f16((double)oq_f16_to_f32(xh) * (double)oq_f16_to_f32(sh), 0);
+        t = oq_f64_to_f16((double)oq_f16_to_f32(t) + (double)oq_f16_to_f32(oh), 0);
+        const float tv = oq_f16_to_f32(t);
+        if (dst_type == OQ_HIF8) ((uint8_t*)dst)[i] = oq_hif8_encode(tv, 1);
+        else if (dst_type != OQ_INT8) ((uint8_t*)dst)[i] = oq_f32_to_fp8_sat(tv, dst_type); /* mutant 32 only */
+        else ((int8_t*)dst)[i] = oq_sat_s8(oq_round_to_int(tv, OQ_ROUND_RINT));
+    }
+}
+
 /* Legacy AscendQuant (per-tensor / per-channel) in fp16 arithmetic, arch 2201:
  * AscendQuantPerChannelIntrinsicsImpl (impl/adv_api/detail/quantization/quant/ascend_quant_pre_impl.h:101-164):
  * fp32 input is first Cast to half (CAST_NONE = rint), then Mul (half), Add/Adds offset (half), then
@@ -626,37 +750,87 @@ static inline int32_t load_q(const void* src, int src_type, int64_t idx)
  *  is_transpose == 0: src [K, N], offset/scale [K/group, N] (group == K: per-channel [1, N]);
  *  is_transpose == 1: src [N, K], offset/scale [N, K/group] (AntiQuantShapeInfo, ascend_antiquant_utils.h:26-31).
  * offset == NULL means no offset (the scale-only overloads). */
+static inline double aq_src_value(const void* src, int src_type, int64_t idx)
+{
+    if (src_type == OQ_FP8_E4M3 || src_type == OQ_FP8_E5M2) return oq_fp8_decode(((const uint8_t*)src)[idx], src_type);
+    if (src_type == OQ_HIF8) return oq_hif8_decode(((const uint8_t*)src)[idx]);
+    return (double)load_q(src, src_type, idx);
+}
+
+/* The arithmetic arch 3510 uses for a legacy AscendAntiQuant of an fp8 or hifloat8 source
+ * (AntiQuantPerchannelImpl / AntiQuantPertensorImpl, impl/adv_api/detail/quantization/antiquant/
+ * ascend_antiquant_3510_impl.h:334-470, 560-770): fp8 always in fp32 (PerTensorProcessForFp8 :307-333,
+ * PerchannelNoTransposeForFp8 :440-468, PerchannelTransposeForFp8 :688-735, PerchannelUnalignedForFp8 :515-558);
+ * hifloat8 to f16 in half ops (:334-355, :470-495, :630-645); hifloat8 to bf16 in bf16 ops along rows
+ * (PerchannelNoTransposeForB8 :470-495, PerchannelUnalignedForB8 :560-593) and in fp32 ops with one rint cast when
+ * transposed or per tensor (:646-687, :357-392).  Other sources keep the caller's choice. */
+static int aq_arith_for(int src_type, int dst_type, int is_transpose, int per_tensor, int arith)
+{
+    if (src_type == OQ_FP8_E4M3 || src_type == OQ_FP8_E5M2) return OQ_ARITH_F32;
+    if (src_type == OQ_HIF8) {
+        if (dst_type == OQ_F16) return OQ_ARITH_F16;
+        return (is_transpose || per_tensor) ? OQ_ARITH_F32 : OQ_ARITH_BF16;
+    }
+    return arith;
+}
+
+/* one element: (q + offset) * scale in the chosen arithmetic, written as dst_type */
+static inline void aq_element(void* dst, int dst_type, int64_t idx, double q, int has_off, float of, float sc,
+                              int arith)
+{
+    if (arith == OQ_ARITH_F16 && dst_type == OQ_F16) {
+        /* half(q) is exact; q + offset and the product are exact in double, rounded once each */
+        uint16_t w = oq_f64_to_f16(q, 0);
+        if (OQ_MUTANT == 7) {
+            w = oq_f64_to_f16(q * (double)sc, 0);
+            if (has_off) w = oq_f64_to_f16((double)oq_f16_to_f32(w) + (double)of, 0);
+        } else {
+            if (has_off) w = oq_f64_to_f16(q + (double)of, 0);
+            w = oq_f64_to_f16((double)oq_f16_to_f32(w) * (double)sc, 0);
+        }
+        ((uint16_t*)dst)[idx] = w;
+    } else if (arith == OQ_ARITH_BF16 && dst_type == OQ_BF16) {
+        uint16_t w = oq_f64_to_bf16(q, 0);
+        if (has_off) w = oq_f64_to_bf16((double)oq_bf16_to_f32(w) + (double)of, 0);
+        w = oq_f64_to_bf16((double)oq_bf16_to_f32(w) * (double)sc, 0);
+        ((uint16_t*)dst)[idx] = w;
+    } else {
+        float v = (float)q;
+        if (has_off) v = v + of;
+        v = v * sc;
+        store_from_f32(dst, dst_type, idx, v);
+    }
+}
+
 void oq_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset, const void* scale,
                   int64_t K, int64_t N, int64_t group_size, int is_transpose, int arith)
 {
     int64_t G = group_size > 0 ? K / group_size : 1;
     int64_t g = group_size > 0 ? group_size : K;
+    const int ar = aq_arith_for(src_type, dst_type, is_transpose, 0, arith);
 #pragma omp parallel for schedule(static)
     for (int64_t k = 0; k < K; ++k)
         for (int64_t n = 0; n < N; ++n) {
             int64_t idx = is_transpose ? n * K + k : k * N + n;
             int64_t sidx = is_transpose ? n * G + k / g : (k / g) * N + n;
-            int32_t q = load_q(src, src_type, idx);
             float sc = load_as_f32(scale, dst_type, sidx);
             float of = offset ? load_as_f32(offset, dst_type, sidx) : 0.0f;
-            if (arith == OQ_ARITH_F16 && dst_type == OQ_F16) {
-                /* half(q) is exact; q + offset and the product are exact in double, rounded once each */
-                uint16_t w = oq_f32_to_f16((float)q, 0);
-                if (OQ_MUTANT == 7) {
-                    w = oq_f64_to_f16((double)q * (double)sc, 0);
-                    if (offset) w = oq_f64_to_f16((double)oq_f16_to_f32(w) + (double)of, 0);
-                } else {
-                    if (offset) w = oq_f64_to_f16((double)q + (double)of, 0);
-                    w = oq_f64_to_f16((double)oq_f16_to_f32(w) * (double)sc, 0);
-                }
-                ((uint16_t*)dst)[idx] = w;
-            } else {
-                float v = (float)q;
-                if (offset) v = v + of;
-                v = v * sc;
-                store_from_f32(dst, dst_type, idx, v);
-            }
+            aq_element(dst, dst_type, idx, aq_src_value(src, src_type, idx), offset != NULL, of, sc, ar);
         }
+}
+
+/* AscendAntiQuant with scalar offset / scale of the output type (include/adv_api/quantization/ascend_antiquant.h:
+ * 136-210; arch 3510 AntiQuantPertensorImpl, ascend_antiquant_3510_impl.h:394-415): int8 and hifloat8 in half ops for
+ * f16 and fp32 ops for bf16 (PerTensorProcessForB8 :334-392), fp8 in fp32 ops (PerTensorProcessForFp8 :301-333). */
+void oq_antiquant_scalar(void* dst, int dst_type, const void* src, int src_type, uint16_t offset, uint16_t scale,
+                         int has_offset, int64_t count)
+{
+    const float sc = dst_type == OQ_F16 ? oq_f16_to_f32(scale) : oq_bf16_to_f32(scale);
+    const float of = dst_type == OQ_F16 ? oq_f16_to_f32(offset) : oq_bf16_to_f32(offset);
+    const int ar = aq_arith_for(src_type, dst_type, 0, 1, dst_type == OQ_F16 ? OQ_ARITH_F16 : OQ_ARITH_F32);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < count; ++i)
+        aq_element(dst, dst_type, i, aq_src_value(src, src_type, i), has_offset, of, sc, ar);
 }
 
 /* AscendAntiQuant<dstT, srcT, scaleT, config{hasOffset, isTranspose, kDim}, policy>(dst, src, scale, offset,
@@ -675,13 +849,6 @@ void oq_antiquant(void* dst, int dst_type, const void* src, int src_type, const 
  *    the scale as bf16 (e << 7; e = 0 gives 0x0040 = 2^-127, e = 255 gives NaN 0x7FFF), one bf16 rounding, then for
  *    half output a rne + saturating cast.
  * offset == NULL: no offset (config.hasOffset false). */
-static inline double round_to(double x, int t) /* one IEEE rounding into scaleT (half / bf16 / fp32), rne */
-{
-    if (t == OQ_F16) return oq_f16_to_f32(oq_f64_to_f16(x, 0));
-    if (t == OQ_BF16) return oq_bf16_to_f32(oq_f64_to_bf16(x, 0));
-    return (double)(float)x;
-}
-
 void oq_antiquant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale, const void* offset,
                          int scale_type, int policy, int64_t m, int64_t n, int64_t group, int k_dim, int is_transpose)
 {
@@ -716,7 +883,8 @@ void oq_antiquant_policy(void* dst, int dst_type, const void* src, int src_type,
                 store_from_f32(dst, dst_type, idx, (float)v);
                 continue;
             }
-            double v = (double)((const int8_t*)src)[idx];  /* exact in every scaleT */
+            double v = src_type == OQ_HIF8 ? (double)oq_hif8_decode(((const uint8_t*)src)[idx])
+                                           : (double)((const int8_t*)src)[idx]; /* exact in every scaleT */
             if (offset) v = round_to(v + o, scale_type);
             v = round_to(v * s, scale_type);
             if (scale_type == OQ_F16) ((uint16_t*)dst)[idx] = oq_f64_to_f16(v, 0);
@@ -847,6 +1015,8 @@ void oq_quant_policy(void* dst, int dst_type, const void* src, int src_type, con
             if (off) v = round_to(v + (offset ? (double)load_as_f32(offset, scale_type, sidx) : os), t);
             if (fp8) {
                 ((uint8_t*)dst)[idx] = oq_f32_to_fp8_sat((float)v, dst_type);
+            } else if (dst_type == OQ_HIF8) {
+                ((uint8_t*)dst)[idx] = oq_hif8_encode((float)v, 1);
             } else if (fp4) {
                 double b = v;
                 if (t != OQ_BF16 && OQ_MUTANT != 22) b = v != v ? 0.0 : oq_bf16_to_f32(oq_f64_to_bf16(v, 1));

@@ -31,7 +31,7 @@ extern "C" {
 enum {
     OQ_INT8 = 1, OQ_UINT8 = 2, OQ_INT4 = 3, OQ_INT32 = 4, OQ_F16 = 5, OQ_BF16 = 6,
     OQ_F32 = 7, OQ_U64 = 8, OQ_FP8_E4M3 = 9, OQ_FP8_E5M2 = 10, OQ_FP4_E2M1 = 11, OQ_E8M0 = 12, OQ_INT64 = 13,
-    OQ_FP4_E1M2 = 14
+    OQ_FP4_E1M2 = 14, OQ_HIF8 = 15
 };
 /* RoundMode: impl/basic_api/utils/kernel_utils_mode.h:103-118 (CAST_NONE acts as CAST_RINT on lossy casts,
  * docs/zh/api/SIMD-API/basic_api/memory_vector_compute/type_conversion/Cast.md:92) */
@@ -41,9 +41,13 @@ enum { OQ_ROUND_NONE = 0, OQ_ROUND_RINT = 1, OQ_ROUND_FLOOR = 2, OQ_ROUND_CEIL =
 enum { OQ_PER_TENSOR = 0, OQ_PER_CHANNEL = 1, OQ_PER_TOKEN = 2, OQ_PER_GROUP = 3 };
 /* antiquant arithmetic: fp16 ops (ascend_antiquant_impl.h:63-96, arch 2201) or fp32 ops
  * (ascend_antiquant_c220_impl.h:46-75 bf16 path; ascend_antiquant_3510_impl.h:320-330) */
-enum { OQ_ARITH_F16 = 0, OQ_ARITH_F32 = 1 };
+enum { OQ_ARITH_F16 = 0, OQ_ARITH_F32 = 1, OQ_ARITH_BF16 = 2 };
 
 /* ---------------- scalar codecs ---------------- */
+/* HiFloat8: value of a code (NaN for 0x80, +-inf for 0x6F / 0xEF) and the code of x with ties away from zero
+ * (CAST_ROUND); sat != 0 maps NaN to 0 and every overflow to +-32768 (0x6E / 0xEE) */
+float oq_hif8_decode(uint8_t code);
+uint8_t oq_hif8_encode(float x, int sat);
 uint16_t oq_f32_to_f16(float x, int sat);
 float oq_f16_to_f32(uint16_t h);
 uint16_t oq_f32_to_bf16(float x, int sat);
@@ -92,6 +96,11 @@ void oq_quant_per_token(int8_t* dst, const void* src, int src_type, const float*
 /* dynamic per-token: absmax per row, multiplier 127/absmax, scale_out = absmax/127 */
 void oq_quant_dynamic_per_token(int8_t* dst, float* scale_out, const void* src, int src_type,
                                 int64_t m, int64_t n, int round_mode);
+/* legacy AscendQuant, arch-3510 form: src f16 / bf16 / f32; dst int8 / hifloat8 (half arithmetic) or fp8
+ * (fp32 arithmetic); scale / offset srcT tensors of scale_count, or (scale NULL) the float scalars; a scale tensor
+ * with offset NULL takes offset_scalar rounded to srcT */
+void oq_quant_legacy(void* dst, int dst_type, const void* src, int src_type, const void* scale, const void* offset,
+                     float scale_scalar, float offset_scalar, int64_t cal_count, int64_t scale_count);
 /* legacy AscendQuant per-tensor / per-channel in fp16 arithmetic */
 void oq_quant_legacy_f16(int8_t* dst, const void* src, int src_type, const uint16_t* scale_vec,
                          uint16_t scale_scalar, const uint16_t* offset_vec, uint16_t offset_scalar,
@@ -111,6 +120,9 @@ int64_t oq_dequant_legacy_shape(int dst_type, int mode, int64_t* m, int64_t* n, 
  * fp32 sources, f16 / bf16 / f32 scales; dst [rows, n] */
 void oq_dequant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
                        int policy, int k_dim, int64_t n, int64_t cal_count, int64_t group);
+/* AscendAntiQuant per tensor: dst[i] = (src[i] + offset) * scale with dst-typed scalars (has_offset 0: scale only) */
+void oq_antiquant_scalar(void* dst, int dst_type, const void* src, int src_type, uint16_t offset, uint16_t scale,
+                         int has_offset, int64_t count);
 /* AscendAntiQuant: dst = (src + offset) * scale, per-channel or per-group */
 void oq_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset, const void* scale,
                   int64_t K, int64_t N, int64_t group_size, int is_transpose, int arith);

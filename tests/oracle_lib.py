@@ -16,10 +16,10 @@ ROOT = Path(__file__).resolve().parent.parent
 ORACLE_DIR = ROOT / "oracle"
 ORACLE_SO = Path(os.environ.get("ASCQ_ORACLE_SO", ORACLE_DIR / "liboracle.so"))
 
-INT8, UINT8, INT4, INT32, F16, BF16, F32, U64, FP8_E4M3, FP8_E5M2, FP4_E2M1, E8M0, INT64, FP4_E1M2 = range(1, 15)
+INT8, UINT8, INT4, INT32, F16, BF16, F32, U64, FP8_E4M3, FP8_E5M2, FP4_E2M1, E8M0, INT64, FP4_E1M2, HIF8 = range(1, 16)
 ROUND_NONE, ROUND_RINT, ROUND_FLOOR, ROUND_CEIL, ROUND_ROUND, ROUND_TRUNC = range(6)
 PER_TENSOR, PER_CHANNEL, PER_TOKEN, PER_GROUP = range(4)
-ARITH_F16, ARITH_F32 = 0, 1
+ARITH_F16, ARITH_F32, ARITH_BF16 = 0, 1, 2
 
 _lib = None
 _P = ctypes.c_void_p
@@ -73,6 +73,12 @@ def lib() -> ctypes.CDLL:
             "oq_quant_dynamic_per_token": (None, [_P, _P, _P, ctypes.c_int, _I64, _I64, ctypes.c_int]),
             "oq_quant_legacy_f16": (None, [_P, _P, ctypes.c_int, _P, ctypes.c_uint16, _P, ctypes.c_uint16, _I64, _I64]),
             "oq_i32_to_f32_rna": (ctypes.c_float, [ctypes.c_int32]),
+            "oq_hif8_decode": (ctypes.c_float, [ctypes.c_uint8]),
+            "oq_hif8_encode": (ctypes.c_uint8, [ctypes.c_float, ctypes.c_int]),
+            "oq_quant_legacy": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, _P, ctypes.c_float, ctypes.c_float, _I64,
+                                       _I64]),
+            "oq_antiquant_scalar": (None, [_P, ctypes.c_int, _P, ctypes.c_int, ctypes.c_uint16, ctypes.c_uint16,
+                                           ctypes.c_int, _I64]),
             "oq_dequant_legacy": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int, ctypes.c_float,
                                          ctypes.c_int, ctypes.c_int, _I64, _I64, _I64]),
             "oq_dequant_legacy_shape": (_I64, [ctypes.c_int, ctypes.c_int, ctypes.POINTER(_I64),
@@ -274,6 +280,40 @@ def quant_legacy_f16(x, src_type, scale_vec=None, scale_scalar=0x3C00, offset_ve
     lib().oq_quant_legacy_f16(_p(q), _p(x), src_type, _p(sv), scale_scalar, _p(ov), offset_scalar, x.size,
                               scale_count)
     return q
+
+
+def hif8_table():
+    """float32 values of the 256 HiFloat8 codes"""
+    L = lib()
+    return np.array([L.oq_hif8_decode(c) for c in range(256)], np.float32)
+
+
+def hif8_encode(x, sat=True):
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    L = lib()
+    return np.array([L.oq_hif8_encode(float(v), int(sat)) for v in x], np.uint8)
+
+
+def quant_legacy(x, src_type, dst_type, scale=None, offset=None, scale_scalar=1.0, offset_scalar=0.0, scale_count=0):
+    """Legacy AscendQuant (arch-3510 form): x raw array (f16 / bf16 as uint16 bits, or float32); scale / offset
+    srcT arrays or None"""
+    x = np.ascontiguousarray(x)
+    q = np.empty(x.shape, np.uint8)
+    sc = None if scale is None else np.ascontiguousarray(scale)
+    of = None if offset is None else np.ascontiguousarray(offset)
+    lib().oq_quant_legacy(_p(q), dst_type, _p(x), src_type, _p(sc), _p(of), float(scale_scalar), float(offset_scalar),
+                          x.size, scale_count)
+    return q.view(np.int8) if dst_type == INT8 else q
+
+
+def antiquant_scalar(src, src_type, offset_bits, scale_bits, dst_type=F16, has_offset=True):
+    """per-tensor AscendAntiQuant of every element of src (int4: two per byte)"""
+    src = np.ascontiguousarray(src)
+    count = src.size * (2 if src_type == INT4 else 1)
+    dst = np.empty(count, np.uint16)
+    lib().oq_antiquant_scalar(_p(dst), dst_type, _p(src), src_type, int(offset_bits), int(scale_bits),
+                              int(has_offset), count)
+    return dst
 
 
 SINGLE_ROW, MULTI_ROW = 0, 1

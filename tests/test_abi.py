@@ -70,7 +70,17 @@ def test_quant_argument_checks():
     _err(L.ascq_ascend_quant_per_token(None, dummy, ascq.F16, dummy, None, ctypes.byref(P), None),
          ascq.E_INVALID_ARG)
     _err(L.ascq_ascend_quant_dynamic_per_token(dummy, dummy, dummy, ascq.INT32, 4, 4, 1, None), ascq.E_UNSUPPORTED)
-    _err(L.ascq_ascend_quant(dummy, dummy, ascq.F16, dummy, None, 0, 0, 100, 3, None), ascq.E_INVALID_ARG)
+    aq = lambda dst, src, sc, of, cal, cnt: L.ascq_ascend_quant(dummy, dst, dummy, src, sc, of, 1.0, 0.0, cal, cnt, None)
+    _err(aq(ascq.INT8, ascq.F16, dummy, None, 96, 5), ascq.E_INVALID_ARG)        # calCount % scaleCount
+    _err(aq(ascq.INT8, ascq.F16, dummy, None, 100, 4), ascq.E_INVALID_ARG)       # calCount % 32 (per channel)
+    _err(aq(ascq.INT8, ascq.F16, None, dummy, 96, 4), ascq.E_INVALID_ARG)        # offset tensor without scales
+    _err(aq(ascq.FP4_E2M1, ascq.F16, None, None, 96, 0), ascq.E_UNSUPPORTED)     # int8 / hif8 / fp8 outputs only
+    _err(aq(ascq.INT8, ascq.INT8, None, None, 96, 0), ascq.E_UNSUPPORTED)        # float sources only
+    _err(aq(ascq.HIF8, ascq.BF16, None, None, 0, 0), ascq.OK)                    # calCount 0: nothing to do
+    _err(L.ascq_ascend_antiquant_scalar(dummy, ascq.F32, dummy, ascq.INT8, 0, 0, 1, 8, None), ascq.E_UNSUPPORTED)
+    _err(L.ascq_ascend_antiquant_scalar(dummy, ascq.F16, dummy, ascq.INT4, 0, 0, 1, 7, None), ascq.E_INVALID_ARG)
+    _err(L.ascq_ascend_antiquant(dummy, ascq.F16, dummy, ascq.HIF8, dummy, dummy, 64, 32, 32, 0, 0, None),
+         ascq.E_UNSUPPORTED)                                                      # hif8 / fp8: per channel only
     # zero-sized work is a no-op that succeeds without touching the device
     _err(L.ascq_ascend_quant_dynamic_per_token(dummy, dummy, dummy, ascq.F16, 0, 16, 1, None), ascq.OK)
 
@@ -291,3 +301,17 @@ def test_noalloc_iterate_all_rejects_oversized_workspace():
     assert b"static scratch" in L.ascq_last_error()
     _err(L.ascq_matmul_iterate_all_noalloc(h, None, 0, None), ascq.E_INVALID_ARG)
     _err(L.ascq_matmul_destroy(h), ascq.OK)
+
+
+def test_no_fma_with_zero_addend_in_half_arithmetic(tmp_path):
+    """The half-arithmetic paths of quant.hip must not round an fp32 product to half through v_fma_mix*_f16 a, b, 0:
+    an fma with a +0 addend turns a -0 product into +0, which the reference's half multiply keeps (e.g.
+    (3 + -3) * -1.3 = -0).  Compiles the kernels to gfx950 assembly (CPU only) and looks for that instruction form."""
+    out = tmp_path / "quant.s"
+    cmd = ["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-Xclang",
+           "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S", "-x", "hip",
+           str(ROOT / "asc-devkit_clone_amd" / "csrc" / "quant.hip"), "-o", str(out)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    bad = [ln for ln in out.read_text().splitlines() if re.search(r"v_fma_mix(lo|hi)?_f16 .*, 0( |$)", ln)]
+    assert not bad, bad[:5]

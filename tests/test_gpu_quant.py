@@ -90,51 +90,31 @@ def test_per_token_given_scale(ascq_gpu, oracle, src, has_offset):
     np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
 
 
-@pytest.mark.parametrize("per_channel", [False, True])
-@pytest.mark.parametrize("src", ["f16", "f32"])
-def test_legacy_quant_f16_arith(ascq_gpu, oracle, per_channel, src):
-    rng = seeded(31)
-    n_total, sc = 4096, 64
-    x32 = rng.uniform(-8, 8, n_total).astype(np.float32)
-    if per_channel:
-        scale = rng.uniform(0.5, 8, sc).astype(np.float16)
-        offset = rng.uniform(-2, 2, sc).astype(np.float16)
-        q = ascq_gpu.ascend_quant(torch.from_numpy(x32.astype(np.float16) if src == "f16" else x32).cuda(),
-                                  scale=_dev(scale), offset=_dev(offset))
-        q_ref = O.quant_legacy_f16(x32.astype(np.float16).view(np.uint16) if src == "f16" else x32,
-                                   O.F16 if src == "f16" else O.F32, scale_vec=scale.view(np.uint16),
-                                   offset_vec=offset.view(np.uint16), scale_count=sc)
-    else:
-        q = ascq_gpu.ascend_quant(torch.from_numpy(x32.astype(np.float16) if src == "f16" else x32).cuda(),
-                                  scale_scalar=2.0, offset_scalar=0.9)
-        q_ref = O.quant_legacy_f16(x32.astype(np.float16).view(np.uint16) if src == "f16" else x32,
-                                   O.F16 if src == "f16" else O.F32, scale_scalar=0x4000,
-                                   offset_scalar=int(np.float16(0.9).view(np.uint16)))
-    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
-
-
-@pytest.mark.parametrize("case", [(4096, 64, True, True), (4096, 64, True, False), (4096, 64, False, True),
-                                  (4092, 12, True, True), (4100, 4, True, True), (8, 8, True, True),
-                                  (16392, 8, False, False), (1 << 20, 4096, True, True)])
+@pytest.mark.parametrize("case", [(4096, 64, True, True), (4096, 64, True, False), (4096, 0, False, False),
+                                  (4128, 12, True, True), (4160, 20, True, False), (32, 8, True, True),
+                                  (16392, 0, False, False), (4092, 0, False, False), (1 << 20, 4096, True, True)])
 @pytest.mark.parametrize("src", ["f16", "f32"])
 def test_legacy_quant_layouts(ascq_gpu, oracle, case, src):
-    """scale / offset vectors or scalars, channel counts that are and are not multiples of 8, ragged totals (the
-    vector and the per-element kernels), ties and saturation"""
+    """legacy AscendQuant to int8: scale / offset tensors, a tensor scale with a scalar offset, or scalars; channel
+    counts that are and are not multiples of 8 and ragged per-tensor totals (the vector and the element kernels);
+    ties and saturation"""
     n_total, sc, sv, ov = case
     rng = seeded(37 + n_total % 97 + sc + 2 * sv + ov)
     x32 = rng.uniform(-300, 300, n_total).astype(np.float32)
     x32[:6] = [0.5, 1.5, 2.5, -0.5, 126.5, -127.5]
-    scale = rng.uniform(0.25, 4, sc).astype(np.float16)
-    offset = rng.uniform(-2, 2, sc).astype(np.float16)
+    scale = rng.uniform(0.25, 4, max(sc, 1)).astype(np.float32)
+    offset = rng.uniform(-2, 2, max(sc, 1)).astype(np.float32)
     scale[0], offset[0] = 1.0, 0.0
     xs = x32.astype(np.float16) if src == "f16" else x32
-    q = ascq_gpu.ascend_quant(torch.from_numpy(xs).cuda(), scale=_dev(scale) if sv else None,
-                              offset=_dev(offset) if ov else None, scale_scalar=1.0, offset_scalar=0.0,
-                              scale_count=sc if (sv or ov) else 0)
-    q_ref = O.quant_legacy_f16(xs.view(np.uint16) if src == "f16" else xs, O.F16 if src == "f16" else O.F32,
-                               scale_vec=scale.view(np.uint16) if sv else None, scale_scalar=0x3C00,
-                               offset_vec=offset.view(np.uint16) if ov else None, offset_scalar=0,
-                               scale_count=sc if (sv or ov) else 0)
+    st = scale.astype(np.float16) if src == "f16" else scale
+    ot = offset.astype(np.float16) if src == "f16" else offset
+    q = ascq_gpu.ascend_quant(torch.from_numpy(xs).cuda(), ascq_gpu.INT8, scale=_dev(st) if sv else None,
+                              offset=_dev(ot) if ov else None, scale_scalar=1.0 if sv else 0.75,
+                              offset_scalar=0.25, scale_count=sc)
+    code = O.F16 if src == "f16" else O.F32
+    raw = lambda a: a.view(np.uint16) if src == "f16" else a
+    q_ref = O.quant_legacy(raw(xs), code, O.INT8, raw(st) if sv else None, raw(ot) if ov else None,
+                           scale_scalar=1.0 if sv else 0.75, offset_scalar=0.25, scale_count=sc)
     np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
 
 

@@ -1206,3 +1206,245 @@ def test_quant_policy_scalar_offset():
                            offset=full.view(np.uint16), k_dim=1)
         c = O.quant_policy(x.view(np.uint16), O.F16, sh.view(np.uint16), O.F16, dst, O.PER_GROUP, m, n, g, k_dim=1)
         assert np.array_equal(a, b) and not np.array_equal(a, c)
+
+
+# --------------------------------------------------------------------------- HiFloat8
+def _hif8_nearest(x, table):
+    """brute-force HiFloat8 code of each x: the nearest finite table value, ties to the larger magnitude, |x| >= 2^15
+    saturating to +-32768, NaN -> 0, results of magnitude 0 coded 0x00 (exact rationals: every value involved is a
+    float32)"""
+    fin = [c for c in range(256) if np.isfinite(table[c]) and c != 0x80]
+    vals = [(Fraction(float(table[c])), c) for c in fin]
+    out = []
+    for v in np.asarray(x, np.float32).reshape(-1):
+        if np.isnan(v):
+            out.append(0)
+            continue
+        if np.isinf(v) or abs(float(v)) >= 32768.0:
+            out.append(0x6E if v > 0 else 0xEE)
+            continue
+        fv = Fraction(float(v))
+        best = None
+        for tv, c in vals:
+            if (tv < 0) != (fv < 0) and tv != 0:
+                continue
+            d = abs(tv - fv)
+            key = (d, -abs(tv))  # ties go to the larger magnitude (away from zero)
+            if best is None or key < best[0]:
+                best = (key, c, tv)
+        out.append(0x00 if best[2] == 0 else best[1])
+    return np.array(out, np.uint8)
+
+
+def test_hif8_decode_published_points():
+    """0x00 zero, 0x80 NaN, 0x6F / 0xEF +-inf, 0x6E the saturation value 32768 (__half22hif82_rna_sat.md table),
+    0x01 the smallest subnormal 2^-22 that Ev = -23 rounds to (Cast.md:263-266), the documented example D = 01,
+    E = 3, M = 2^-1 + 2^-2 -> 14 (fp8_data_type_intro.md:36), and the 1-bit exponent field's sign"""
+    t = O.hif8_table()
+    assert t[0x00] == 0 and np.isnan(t[0x80]) and t[0x6F] == np.inf and t[0xEF] == -np.inf
+    assert t[0x6E] == 32768.0 and t[0xEE] == -32768.0
+    assert t[0x01] == 2.0 ** -22 and t[0x81] == -(2.0 ** -22)
+    assert t[0b0_01_01_110] == 14.0
+    assert t[0b0_001_0_000] == 2.0 and t[0b0_001_1_000] == 0.5 and t[0b0_0001_000] == 1.0
+    fin = t[np.isfinite(t)]
+    assert np.abs(fin).max() == 32768.0 and np.abs(fin[fin != 0]).min() == 2.0 ** -22
+    assert (fin.astype(np.float16).astype(np.float32) == fin).all()  # every code is an f16 value
+    pos = np.unique(fin[fin > 0])
+    assert len(pos) == 126  # 0x01..0x7F without the inf code 0x6F, each a distinct value
+    assert (t[0x81:0x100][np.isfinite(t[0x81:0x100])] == -t[0x01:0x80][np.isfinite(t[0x01:0x80])]).all()
+
+
+def test_hif8_encode_inverts_decode():
+    """the encoder (Cast.md's rules) and the decoder (the layout of asc_type_conversion_utils.h) are independent
+    restatements: encoding every finite code's value gives the code back"""
+    t = O.hif8_table()
+    for c in range(256):
+        if c in (0x80, 0x6F, 0xEF) or (c == 0x00):
+            continue
+        assert O.lib().oq_hif8_encode(float(t[c]), 0) == c, hex(c)
+
+
+def test_hif8_encode_saturation_table():
+    """__half22hif82_rna_sat.md: +-0 -> 0, nan -> 0, +-inf -> +-32768, +-65504 -> +-32768, 2^-24 -> 0; without
+    saturation nan is 0x80 and overflow +-inf"""
+    L = O.lib()
+    kat = {0.0: 0x00, -0.0: 0x00, float("nan"): 0x00, float("inf"): 0x6E, float("-inf"): 0xEE, 65504.0: 0x6E,
+           -65504.0: 0xEE, 2.0 ** -24: 0x00, 40960.0: 0x6E, 32768.0: 0x6E}
+    for x, c in kat.items():
+        assert L.oq_hif8_encode(x, 1) == c, x
+    assert L.oq_hif8_encode(float("nan"), 0) == 0x80
+    assert L.oq_hif8_encode(65504.0, 0) == 0x6F and L.oq_hif8_encode(-1e30, 0) == 0xEF
+    assert L.oq_hif8_encode(36000.0, 0) == 0x6E  # below 1.25 * 2^15: still 32768
+
+
+def test_hif8_encode_matches_nearest_ties_away_on_every_f16():
+    """every f16 bit pattern (the half -> hifloat8 cast of the legacy quant) against the brute-force nearest code"""
+    t = O.hif8_table()
+    x = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+    got = O.hif8_encode(x, sat=True)
+    sel = rng0.choice(65536, 6000, replace=False)
+    np.testing.assert_array_equal(got[sel], _hif8_nearest(x[sel], t))
+    # exact ties between neighbouring codes round away from zero
+    pos = np.unique(t[np.isfinite(t) & (t > 0)]).astype(np.float64)
+    mids = ((pos[:-1] + pos[1:]) / 2).astype(np.float32)
+    assert (mids.astype(np.float64) == (pos[:-1] + pos[1:]) / 2).all()
+    np.testing.assert_array_equal(O.hif8_encode(mids), _hif8_nearest(mids, t))
+    np.testing.assert_array_equal(O.hif8_encode(-mids), _hif8_nearest(-mids, t))
+
+
+def test_hif8_encode_random_f32():
+    t = O.hif8_table()
+    x = (rng0.standard_normal(4000) * np.exp2(rng0.uniform(-26, 17, 4000))).astype(np.float32)
+    np.testing.assert_array_equal(O.hif8_encode(x), _hif8_nearest(x, t))
+
+
+# --------------------------------------------------------------------------- legacy AscendQuant, arch-3510 form
+def _h(v):
+    return np.asarray(v, np.float64).astype(np.float16)  # one correctly rounded conversion
+
+
+def _half_ops(x32, s32, o32, sat_x=True, sat_so=True):
+    """t = half(x*s); t = half(t + o) with x, s, o first rounded to half (saturating where the reference saturates)"""
+    def to_h(v, sat):
+        v = np.asarray(v, np.float64)
+        return (np.clip(v, -65504, 65504) if sat else v).astype(np.float16)
+    xh, sh, oh = to_h(x32, sat_x), to_h(s32, sat_so), to_h(o32, sat_so)
+    t = _h(xh.astype(np.float64) * sh.astype(np.float64))
+    return _h(t.astype(np.float64) + oh.astype(np.float64))
+
+
+def _bf16(v):
+    t = torch.from_numpy(np.ascontiguousarray(v, np.float32)).to(torch.bfloat16)
+    return t.view(torch.int16).numpy().view(np.uint16), t.float().numpy()
+
+
+def test_quant_legacy_int8_f16_matches_the_half_form():
+    """an f16 source with f16 scale / offset tensors is the 2201 half-arithmetic form (oq_quant_legacy_f16), and
+    the quant example golden (scale 2.0, offset 0.9) is reproduced from float scalars"""
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(4096) * 40).astype(np.float16)
+    sc = rng.uniform(-3, 3, 64).astype(np.float16)
+    of = rng.uniform(-20, 20, 64).astype(np.float16)
+    a = O.quant_legacy(x.view(np.uint16), O.F16, O.INT8, sc.view(np.uint16), of.view(np.uint16), scale_count=64)
+    b = O.quant_legacy_f16(x.view(np.uint16), O.F16, scale_vec=sc.view(np.uint16), offset_vec=of.view(np.uint16),
+                           scale_count=64)
+    np.testing.assert_array_equal(a, b)
+    f = np.load(GOLD / "quant_example.npz")
+    q = O.quant_legacy(f["src"].view(np.uint16), O.F16, O.INT8, scale_scalar=2.0, offset_scalar=0.9)
+    assert (q == f["golden"]).all()
+
+
+@pytest.mark.parametrize("src_type", [O.F16, O.BF16, O.F32])
+@pytest.mark.parametrize("dst_type", [O.INT8, O.HIF8, O.FP8_E4M3, O.FP8_E5M2])
+@pytest.mark.parametrize("kind", ["tensor", "scalar_offset", "per_tensor"])
+def test_quant_legacy_3510_forms(src_type, dst_type, kind):
+    """int8 / hifloat8: half arithmetic after saturating casts of the srcT tensors (plain rne for the float scalars),
+    rint / ties-away with saturation; fp8: fp32 arithmetic, rint with saturation, NaN -> 0 -- checked with numpy /
+    torch arithmetic, torch's fp8 casts and the brute-force HiFloat8 coder; sources beyond the f16 range included"""
+    rng = np.random.default_rng(10 * src_type + dst_type + len(kind))
+    n, sc_n = 2048, 32
+    x = (rng.standard_normal(n) * np.exp2(rng.uniform(-6, 10, n))).astype(np.float32)
+    x[:4] = [1e6, -7e4, 70000.0, np.nan]
+    s = rng.uniform(-2, 2, sc_n).astype(np.float32) * np.float32(0.01 if dst_type == O.INT8 else 1.0)
+    o = rng.uniform(-30, 30, sc_n).astype(np.float32)
+    if src_type == O.F16:
+        xs, s_, o_ = x.astype(np.float16), s.astype(np.float16), o.astype(np.float16)
+        xw, sw, ow = xs.view(np.uint16), s_.view(np.uint16), o_.view(np.uint16)
+        xv, sv, ov = xs.astype(np.float32), s_.astype(np.float32), o_.astype(np.float32)
+    elif src_type == O.BF16:
+        (xw, xv), (sw, sv), (ow, ov) = _bf16(x), _bf16(s), _bf16(o)
+    else:
+        xw, sw, ow, xv, sv, ov = x, s, o, x, s, o
+    ss, osc = np.float32(0.0137), np.float32(2.71875)
+    if kind == "tensor":
+        q = O.quant_legacy(xw, src_type, dst_type, sw, ow, scale_count=sc_n)
+        S, OFF, sat_so = np.tile(sv, n // sc_n), np.tile(ov, n // sc_n), True
+    elif kind == "scalar_offset":
+        q = O.quant_legacy(xw, src_type, dst_type, sw, None, offset_scalar=float(osc), scale_count=sc_n)
+        o_src = {O.F16: np.float32(np.float16(osc)), O.BF16: _bf16(np.array([osc]))[1][0], O.F32: osc}[src_type]
+        S, OFF, sat_so = np.tile(sv, n // sc_n), np.full(n, o_src, np.float32), True
+    else:
+        q = O.quant_legacy(xw, src_type, dst_type, scale_scalar=float(ss), offset_scalar=float(osc))
+        S, OFF, sat_so = np.full(n, ss, np.float32), np.full(n, osc, np.float32), False
+    if dst_type in (O.FP8_E4M3, O.FP8_E5M2):
+        v = (xv * S).astype(np.float32) + OFF  # numpy float32 ops: one rounding each
+        mx = 448.0 if dst_type == O.FP8_E4M3 else 57344.0
+        fdt = torch.float8_e4m3fn if dst_type == O.FP8_E4M3 else torch.float8_e5m2
+        c = torch.from_numpy(np.clip(np.nan_to_num(v, nan=0.0), -mx, mx).astype(np.float32)).to(fdt)
+        np.testing.assert_array_equal(q, c.view(torch.uint8).numpy())
+        return
+    sat_x = src_type != O.F16
+    t = _half_ops(xv, S, OFF, sat_x=sat_x, sat_so=sat_so)
+    tv = t.astype(np.float32)
+    if dst_type == O.INT8:
+        exp = np.clip(np.rint(np.nan_to_num(tv, nan=0.0, posinf=127, neginf=-128)), -128, 127).astype(np.int8)
+        np.testing.assert_array_equal(q, exp)
+    else:
+        sel = rng.choice(n, 300, replace=False)
+        np.testing.assert_array_equal(q[sel], _hif8_nearest(tv[sel], O.hif8_table()))
+
+
+def test_quant_policy_hif8():
+    """PER_TOKEN / PER_GROUP to hifloat8: the int8 path's scaleT arithmetic, then ties away with saturation"""
+    rng = np.random.default_rng(17)
+    m, n = 16, 256
+    x = (rng.standard_normal((m, n)) * 50).astype(np.float32)
+    sc = np.exp2(rng.uniform(-3, 8, m)).astype(np.float32)
+    of = rng.uniform(-4, 4, m).astype(np.float32)
+    q = O.quant_policy(x, O.F32, sc, O.F32, O.HIF8, O.PER_TOKEN, m, n, offset=of)
+    v = (x * sc[:, None]).astype(np.float32) + of[:, None]
+    sel = rng.choice(m * n, 400, replace=False)
+    np.testing.assert_array_equal(q.reshape(-1)[sel], _hif8_nearest(v.reshape(-1)[sel], O.hif8_table()))
+    xh = x.astype(np.float16)
+    sh = sc.astype(np.float16)
+    q = O.quant_policy(xh.view(np.uint16), O.F16, sh.view(np.uint16), O.F16, O.HIF8, O.PER_TOKEN, m, n)
+    v = _h(xh.astype(np.float64) * sh.astype(np.float64)[:, None]).astype(np.float32)
+    np.testing.assert_array_equal(q.reshape(-1)[sel], _hif8_nearest(v.reshape(-1)[sel], O.hif8_table()))
+
+
+def test_antiquant_hif8_and_fp8_sources():
+    """legacy AscendAntiQuant of hifloat8 / fp8: fp8 in fp32 ops; hifloat8 to f16 in half ops; hifloat8 to bf16 in
+    bf16 ops along rows and in fp32 ops when transposed; the policy form treats hifloat8 like int8 (scaleT ops)"""
+    rng = np.random.default_rng(23)
+    K, N = 64, 48
+    t = O.hif8_table()
+    codes = rng.integers(0, 256, (K, N), dtype=np.uint8)
+    codes[np.isin(codes, [0x80, 0x6F, 0xEF])] = 0x21
+    q = t[codes].astype(np.float64)
+    s32 = rng.uniform(-0.5, 0.5, N).astype(np.float32)
+    o32 = rng.uniform(-3, 3, N).astype(np.float32)
+    # f16 dst: half ops
+    sh, oh = s32.astype(np.float16), o32.astype(np.float16)
+    y = O.antiquant(codes, O.HIF8, sh.view(np.uint16), oh.view(np.uint16), K, N, 0, False, O.F16, O.ARITH_F32)
+    e = _h(_h(q + oh.astype(np.float64)).astype(np.float64) * sh.astype(np.float64))
+    np.testing.assert_array_equal(y, e.view(np.uint16))
+    # bf16 dst along rows: bf16 ops (torch bf16 add / mul, each correctly rounded)
+    sbw, sbv = _bf16(s32)
+    obw, obv = _bf16(o32)
+    y = O.antiquant(codes, O.HIF8, sbw, obw, K, N, 0, False, O.BF16, O.ARITH_F32)
+    qt = torch.from_numpy(q.astype(np.float32)).to(torch.bfloat16)
+    e = (qt + torch.from_numpy(obv).to(torch.bfloat16)) * torch.from_numpy(sbv).to(torch.bfloat16)
+    np.testing.assert_array_equal(y, e.view(torch.int16).numpy().view(np.uint16))
+    # bf16 dst transposed ([N, K] source): fp32 ops, one rint cast
+    ct = np.ascontiguousarray(codes.T)
+    y = O.antiquant(ct, O.HIF8, sbw, obw, K, N, 0, True, O.BF16, O.ARITH_F16)
+    e32 = ((t[ct] + obv[:, None]).astype(np.float32) * sbv[:, None]).astype(np.float32)
+    np.testing.assert_array_equal(y, _bf16(e32)[0])
+    # fp8 source, f16 dst: fp32 ops then one rne cast, whatever arith the caller passes
+    f8 = rng.integers(0, 256, (K, N), dtype=np.uint8)
+    f8[(f8 & 0x7F) == 0x7F] = 0x11
+    fv = torch.from_numpy(f8).view(torch.float8_e4m3fn).float().numpy()
+    y = O.antiquant(f8, O.FP8_E4M3, sh.view(np.uint16), oh.view(np.uint16), K, N, 0, False, O.F16, O.ARITH_F16)
+    e32 = ((fv + oh.astype(np.float32)).astype(np.float32) * sh.astype(np.float32)).astype(np.float32)
+    np.testing.assert_array_equal(y, np.clip(e32, -65504, 65504).astype(np.float16).view(np.uint16))
+    # per tensor: hifloat8 -> f16 half ops, -> bf16 fp32 ops; scale only
+    ys = O.antiquant_scalar(codes, O.HIF8, int(oh[0].view(np.uint16)), int(sh[0].view(np.uint16)), O.F16)
+    np.testing.assert_array_equal(ys, _h(_h(q + float(oh[0])).astype(np.float64) * float(sh[0])).view(np.uint16)
+                                  .reshape(-1))
+    ys = O.antiquant_scalar(codes, O.HIF8, int(obw[0]), int(sbw[0]), O.BF16, has_offset=False)
+    np.testing.assert_array_equal(ys, _bf16((t[codes] * np.float32(sbv[0])).astype(np.float32))[0].reshape(-1))
+    # policy form: hifloat8 like int8 in f16 scaleT ops
+    yp = O.antiquant_policy(codes, O.HIF8, sh.view(np.uint16), O.F16, O.F16, O.PER_TOKEN, K, N, is_transpose=True,
+                            offset=oh.view(np.uint16))
+    np.testing.assert_array_equal(yp, _h(_h(q + oh.astype(np.float64)).astype(np.float64) * sh.astype(np.float64))
+                                  .view(np.uint16))

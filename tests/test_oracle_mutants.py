@@ -7,7 +7,7 @@ double-rounded multiplier, a wrong E2M1 code, a ties-away f16 cast, an unrounded
 dequant indexed by row, a requant offset added before the clamp, a ties-away fp8 cast, an ignored requant
 sign flag, a FasterGelu with the wrong sign, and policy-form quant mistakes (arithmetic type, bf16 step, group
 axis, offset rounding, directed E2M1 modes) and dequant layout mistakes (int32 rounding, the single-row
-reshape, padded dst rows, group axis).  Each mutant is compiled on the CPU into a temporary library and the pinning tests of
+reshape, padded dst rows, group axis) and HiFloat8 / arch-3510 legacy quant mistakes.  Each mutant is compiled on the CPU into a temporary library and the pinning tests of
 tests/test_oracle.py are run against it; every mutant must fail at least one of them.
 """
 from __future__ import annotations
@@ -53,6 +53,10 @@ MUTANTS = {
     28: "legacy dequant without the DEQUANT_WITH_SINGLE_ROW reshape",
     29: "legacy dequant dst rows not padded to 32 bytes",
     30: "per-group dequant scales indexed along the wrong axis",
+    31: "HiFloat8 encoder writes the 2-bit exponent field for every |E| >= 2",
+    32: "legacy quant to fp8 computed in half arithmetic instead of fp32",
+    33: "HiFloat8 ties rounded toward zero instead of away",
+    34: "HiFloat8 decoder reads the 1-bit exponent field's sign inverted",
 }
 
 
