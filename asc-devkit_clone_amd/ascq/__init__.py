@@ -28,6 +28,8 @@ ROUND_NONE, ROUND_RINT, ROUND_FLOOR, ROUND_CEIL, ROUND_ROUND, ROUND_TRUNC = rang
 # ascq_policy
 ACT_NONE, ACT_FASTER_GELU = 0, 1
 PER_TENSOR, PER_CHANNEL, PER_TOKEN, PER_GROUP = range(4)
+# IterateAll enAtomic (matmul_config_utils.h:53-55)
+ATOMIC_NONE, ATOMIC_ADD, ATOMIC_MAX, ATOMIC_MIN = range(4)
 # ascq_arith
 ARITH_F16, ARITH_F32 = 0, 1
 # ascq_dequant_mode (DeQuantMode)

@@ -103,8 +103,10 @@ namespace {
 enum Kind { K_NONE, K_INT8, K_ANTIQUANT, K_MX, K_F8, K_INT4 };
 
 bool is_f8(int32_t t) { return t == ASCQ_DT_FP8_E4M3 || t == ASCQ_DT_FP8_E5M2; }
+bool is_fp4(int32_t t) { return t == ASCQ_DT_FP4_E2M1 || t == ASCQ_DT_FP4_E1M2; }
 // f8f6f4 format code of an fp8 / fp4 element type (the MFMA's cbsz / blgp field)
 int f8f6f4_code(int32_t t) { return t == ASCQ_DT_FP8_E5M2 ? 1 : (t == ASCQ_DT_FP4_E2M1 ? 4 : 0); }
+constexpr int kF8F6F4Fp6E2M3 = 2;  // the code of fp6 E2M3 (the operand format of the E1M2 path)
 
 Kind kind_of(const ascq_matmul_types& t)
 {
@@ -112,13 +114,18 @@ Kind kind_of(const ascq_matmul_types& t)
     if (t.a_type == ASCQ_DT_INT4 && t.b_type == ASCQ_DT_INT4) return K_INT4;
     if (t.a_type == ASCQ_DT_F16 && (t.b_type == ASCQ_DT_INT8 || t.b_type == ASCQ_DT_INT4)) return K_ANTIQUANT;
     if (t.scale_type == ASCQ_DT_E8M0 &&
-        ((t.a_type == ASCQ_DT_FP4_E2M1 && t.b_type == ASCQ_DT_FP4_E2M1) || (is_f8(t.a_type) && is_f8(t.b_type))))
+        ((is_fp4(t.a_type) && is_fp4(t.b_type)) || (is_f8(t.a_type) && is_f8(t.b_type))))
         return K_MX;
     if (t.scale_type == 0 && is_f8(t.a_type) && is_f8(t.b_type)) return K_F8;
     return K_NONE;
 }
 
-bool mx_is_fp4(const ascq_matmul_s* h) { return h->ty.a_type == ASCQ_DT_FP4_E2M1; }
+bool mx_is_fp4(const ascq_matmul_s* h) { return is_fp4(h->ty.a_type); }
+// an E1M2 operand: both operands are rewritten to fp6 E2M3 planes (exact) for the f8f6f4 MFMA
+bool mx_is_fp6(const ascq_matmul_s* h)
+{
+    return mx_is_fp4(h) && (h->ty.a_type == ASCQ_DT_FP4_E1M2 || h->ty.b_type == ASCQ_DT_FP4_E1M2);
+}
 
 // DEQF16 / QS322BF16_PRE for int8 with f16 / bf16 C; QF322{F16,BF16,F32}_PRE for fp8 (quant_processor_utils.h:31-55)
 bool has_quant_epilogue(const ascq_matmul_types& t)
@@ -164,9 +171,13 @@ size_t workspace_need(const ascq_matmul_s* h)
     }
     case K_MX: {
         // [K, N] B transposed to [N, K]; both scale tensors rearranged stage-major; 256-byte aligned parts
+        // fp6 (an E1M2 operand): the P and Q planes of A and of B as well
         const size_t kb = mx_is_fp4(h) ? (size_t)(h->K / 2) : (size_t)h->K;
         size_t need = h->trans_b ? 0 : align256((size_t)h->N * kb);
         need += ascq::mx_scale_workspace_bytes(h->M, h->N, h->K);
+        if (mx_is_fp6(h))
+            need += align256((size_t)h->M * kb) + align256(ascq::fp6_q_plane_bytes(h->M, h->K)) +
+                    align256((size_t)h->N * kb) + align256(ascq::fp6_q_plane_bytes(h->N, h->K));
         return need;
     }
     default: return 0;
@@ -299,7 +310,8 @@ ascq_status ascq_matmul_create(const ascq_matmul_types* types, ascq_matmul_t* ou
     } else {
         if (types->c_type != ASCQ_DT_BF16 && types->c_type != ASCQ_DT_F32)
             return fail(ASCQ_E_UNSUPPORTED, "matmul_create: MX matmul supports C = bf16 or f32");
-        if (types->bias_type != 0) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: MX matmul bias is not supported");
+        if (types->bias_type != 0 && types->bias_type != ASCQ_DT_F32)
+            return fail(ASCQ_E_UNSUPPORTED, "matmul_create: MX matmul bias must be f32");
         if (types->b_format != ASCQ_FORMAT_ND) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: MX B must be ND");
     }
     auto* h = new (std::nothrow) ascq_matmul_s();
@@ -469,7 +481,17 @@ ascq_status ascq_matmul_set_workspace(ascq_matmul_t h, void* workspace, size_t b
 ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic, void* stream)
 {
     if (!h || !c) return fail(ASCQ_E_INVALID_ARG, "iterate_all: null argument");
-    if (en_atomic != 0) return fail(ASCQ_E_UNSUPPORTED, "iterate_all: enAtomic != 0 is not supported");
+    if (en_atomic > 3) return fail(ASCQ_E_INVALID_ARG, "iterate_all: enAtomic must be 0 (store), 1 (add), 2 (max) or 3 (min)");
+    // The copy-out combines into C only for the C types SetAtomic takes (scheduler_base.h:484-494: float, half,
+    // int16_t, int32_t, int8_t, bfloat16_t); for the others (uint8, int4, fp8) the reference stores, and so does this.
+    // int8 C is refused: the saturation of the int8 accumulation is not published.
+    const int32_t ct = h->ty.c_type;
+    int atomic = en_atomic;
+    if (ct != ASCQ_DT_INT32 && ct != ASCQ_DT_F32 && ct != ASCQ_DT_F16 && ct != ASCQ_DT_BF16) {
+        if (ct == ASCQ_DT_INT8 && atomic != 0)
+            return fail(ASCQ_E_UNSUPPORTED, "iterate_all: enAtomic with an int8 C is not supported");
+        atomic = ascq::C_STORE;
+    }
     if (!h->a || !h->b) return fail(ASCQ_E_STATE, "iterate_all: SetTensorA and SetTensorB must precede IterateAll");
     if (h->M <= 0) return fail(ASCQ_E_STATE, "iterate_all: SetOrgShape must precede IterateAll");
     const int64_t m = h->sm > 0 ? h->sm : h->M, n = h->sn > 0 ? h->sn : h->N, k = h->sk > 0 ? h->sk : h->K;
@@ -510,6 +532,7 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         g.ldb = o.ldb;
         g.trans_a = o.trans_a;
         g.trans_b = o.trans_b;
+        g.atomic = atomic;
         return hip_status(ascq::launch_gemm_i8(g, st), "gemm_i8");
     }
     case K_INT4: {
@@ -553,6 +576,7 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         g.qscalar = h->qscalar;
         g.trans_a = 0;
         g.trans_b = 1;
+        g.atomic = atomic;
         switch (h->ty.c_type) {
         case ASCQ_DT_INT32: g.epi = ascq::EPI_I32; break;
         case ASCQ_DT_F16: g.epi = ascq::EPI_DEQ_F16; break;
@@ -590,6 +614,7 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         g.c_type = h->ty.c_type;  // ascq_dtype codes equal the device DT_* codes
         g.fmt_a = f8f6f4_code(h->ty.a_type);
         g.fmt_b = f8f6f4_code(h->ty.b_type);
+        g.atomic = atomic;
         return hip_status(ascq::launch_gemm_f8(g, st), "gemm_f8");
     }
     case K_ANTIQUANT: {
@@ -629,7 +654,7 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
             grp = 0;
         }
         return hip_status(ascq::launch_antiquant_matmul((uint16_t*)c, (const uint16_t*)h->a, wp, h->ty.b_type, sc, of,
-                                                        grp, h->M, h->N, h->K, st),
+                                                        grp, h->M, h->N, h->K, atomic, st),
                           "antiquant_matmul");
     }
     case K_MX: {
@@ -648,6 +673,7 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
             return fail(ASCQ_E_INVALID_ARG, "iterate_all: MX operands must be 16-byte (scales 4-byte) aligned");
         ascq_status s = ensure_workspace(h);
         if (s != ASCQ_OK) return s;
+        const uint8_t* at = (const uint8_t*)h->a;
         const uint8_t* bt = (const uint8_t*)h->b;
         const uint8_t* sa = h->scale_a;
         const uint8_t* sb = h->scale_b;
@@ -659,9 +685,29 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
             bt = ws;
             ws += align256((size_t)h->N * (size_t)(fp4 ? h->K / 2 : h->K));
         }
+        const bool fp6 = mx_is_fp6(h);
+        const uint8_t* aq = nullptr;
+        const uint8_t* bq = nullptr;
+        if (fp6) {  // both operands -> fp6 E2M3 P / Q planes
+            uint8_t* pa = ws;
+            uint8_t* qa = pa + align256((size_t)h->M * (size_t)(h->K / 2));
+            uint8_t* pb = qa + align256(ascq::fp6_q_plane_bytes(h->M, h->K));
+            uint8_t* qb = pb + align256((size_t)h->N * (size_t)(h->K / 2));
+            ws = qb + align256(ascq::fp6_q_plane_bytes(h->N, h->K));
+            hipError_t e = ascq::launch_fp4_to_fp6_planes(pa, qa, at, h->M, h->K, h->ty.a_type == ASCQ_DT_FP4_E1M2, st);
+            if (e == hipSuccess)
+                e = ascq::launch_fp4_to_fp6_planes(pb, qb, bt, h->N, h->K, h->ty.b_type == ASCQ_DT_FP4_E1M2, st);
+            if (e != hipSuccess) return hip_status(e, "fp4 -> fp6 planes");
+            at = pa;
+            bt = pb;
+            aq = qa;
+            bq = qb;
+        }
         ascq::MxGemmArgs g{};
-        g.A = (const uint8_t*)h->a;
+        g.A = at;
         g.B = bt;
+        g.Aq = aq;
+        g.Bq = bq;
         g.sA = sa;
         g.sB = sb;
         g.sa_layout = h->trans_sa ? 1 : 0;  // scaleA [M, sK], or [sK/2, M, 2] with isTransposeScaleA
@@ -672,8 +718,10 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         g.K = h->K;
         g.C = c;
         g.c_type = h->ty.c_type;  // ascq_dtype codes equal the device DT_* codes
-        g.fmt_a = f8f6f4_code(h->ty.a_type);
-        g.fmt_b = f8f6f4_code(h->ty.b_type);
+        g.fmt_a = fp6 ? kF8F6F4Fp6E2M3 : f8f6f4_code(h->ty.a_type);
+        g.fmt_b = fp6 ? kF8F6F4Fp6E2M3 : f8f6f4_code(h->ty.b_type);
+        g.bias = (const float*)h->bias;
+        g.atomic = atomic;
         return hip_status(ascq::launch_mx_gemm(g, st), "mx_gemm");
     }
     default: return fail(ASCQ_E_UNSUPPORTED, "iterate_all: unsupported handle");
@@ -1051,7 +1099,8 @@ ascq_status ascq_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w_
         return fail(ASCQ_E_INVALID_ARG, "antiquant_matmul: x and the packed weight must be 16-byte aligned");
     if (k * n >= (1ll << 31) || 64 * k * 2 >= (1ll << 31))
         return fail(ASCQ_E_UNSUPPORTED, "antiquant_matmul: the weight must stay below 2^31 elements");
-    return hip_status(ascq::launch_antiquant_matmul(y, x, w_packed, w_type, scale, offset, group_size, m, n, k, S(stream)),
+    return hip_status(ascq::launch_antiquant_matmul(y, x, w_packed, w_type, scale, offset, group_size, m, n, k,
+                                                    ascq::C_STORE, S(stream)),
                       "antiquant_matmul");
 }
 

@@ -10,6 +10,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include "launch.h"
 
 namespace ascq {
 
@@ -302,6 +303,58 @@ __device__ __forceinline__ float wave_max(float v)
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
     return v;
+}
+
+// The combined bits of one C element.  int32: wrapping add, signed max / min.  f32: IEEE add (rne).  f16 / bf16:
+// the fp32 sum of the two values rounded once to the C type (rne, overflow to inf); an fp32 intermediate
+// (24 bits >= 2p + 1 for p = 11 and 8) makes the double rounding innocuous, so this is the correctly rounded
+// f16 / bf16 sum.  max / min: the new value replaces the old one only when it compares greater / smaller (a NaN
+// never replaces and is never replaced; +0 and -0 compare equal, so the old zero stays).
+template <int DT>
+__device__ __forceinline__ uint32_t c_combine(uint32_t old, uint32_t v, int op)
+{
+    if constexpr (DT == DT_INT32) {
+        const int32_t a = (int32_t)old, b = (int32_t)v;
+        if (op == C_ADD) return old + v;
+        return (op == C_MAX ? b > a : b < a) ? v : old;
+    } else {
+        const float a = DT == DT_F32 ? __uint_as_float(old) : (DT == DT_F16 ? f16_to_f32((uint16_t)old) : bf16_to_f32((uint16_t)old));
+        const float b = DT == DT_F32 ? __uint_as_float(v) : (DT == DT_F16 ? f16_to_f32((uint16_t)v) : bf16_to_f32((uint16_t)v));
+        if (op == C_ADD) {
+            const float s = a + b;
+            if constexpr (DT == DT_F32) return __float_as_uint(s);
+            else if constexpr (DT == DT_F16) return f32_to_f16(s);
+            else return __float_as_uint(bf16_round(s)) >> 16;
+        }
+        return (op == C_MAX ? b > a : b < a) ? v : old;
+    }
+}
+
+// C[p] = combine(C[p], v) as one atomic operation: the native int32 atomics, else a compare-and-swap loop on the
+// aligned 32-bit word that holds the element (it ends once no other writer changed the word in between).
+template <int DT>
+__device__ __forceinline__ void c_atomic(uint8_t* p, uint32_t v, int op)
+{
+    if constexpr (DT == DT_INT32) {
+        if (op == C_ADD) atomicAdd((int*)p, (int)v);
+        else if (op == C_MAX) atomicMax((int*)p, (int)v);
+        else atomicMin((int*)p, (int)v);
+    } else {
+        constexpr bool W16 = DT != DT_F32;
+        unsigned* w = (unsigned*)((uintptr_t)p & ~(uintptr_t)3);
+        const uint32_t sh = W16 ? (uint32_t)((uintptr_t)p & 2) * 8u : 0u;
+        const uint32_t mask = W16 ? 0xFFFFu << sh : 0xFFFFFFFFu;
+        unsigned old = *(volatile unsigned*)w;
+        for (;;) {
+            const uint32_t cur = W16 ? (old & mask) >> sh : old;
+            const uint32_t nv = c_combine<DT>(cur, v, op);
+            if (nv == cur) break;
+            const unsigned nw = W16 ? (old & ~mask) | (nv << sh) : nv;
+            const unsigned prev = atomicCAS(w, old, nw);
+            if (prev == old) break;
+            old = prev;
+        }
+    }
 }
 
 }  // namespace ascq

@@ -71,11 +71,15 @@ __device__ __forceinline__ uint32_t bload2(rsrc_t r, uint32_t off) { return __bu
 struct TileOut {
     rsrc_t r;
     uint32_t pitch;  // bytes per row
+    uint8_t* base;   // the same range as a plain pointer (the enAtomic read-modify-write path)
+    uint32_t bytes;
 };
 __device__ __forceinline__ TileOut tile_out(void* C, int64_t m0, int64_t n0, int64_t ldc, int rows, int cols, int esize)
 {
     TileOut t;
-    t.r = make_rsrc((uint8_t*)C + (m0 * ldc + n0) * esize, (uint32_t)(((int64_t)(rows - 1) * ldc + cols) * esize));
+    t.base = (uint8_t*)C + (m0 * ldc + n0) * esize;
+    t.bytes = (uint32_t)(((int64_t)(rows - 1) * ldc + cols) * esize);
+    t.r = make_rsrc(t.base, t.bytes);
     t.pitch = (uint32_t)(ldc * esize);
     return t;
 }
@@ -84,7 +88,9 @@ __device__ __forceinline__ TileOut tile_out(void* C, int64_t m0, int64_t n0, int
 __device__ __forceinline__ TileOut tile_out_int4(void* C, int64_t m0, int64_t n0, int64_t ldc, int rows, int cols)
 {
     TileOut t;
-    t.r = make_rsrc((uint8_t*)C + (m0 * ldc + n0) / 2, (uint32_t)((int64_t)(rows - 1) * (ldc / 2) + (cols + 1) / 2));
+    t.base = (uint8_t*)C + (m0 * ldc + n0) / 2;
+    t.bytes = (uint32_t)((int64_t)(rows - 1) * (ldc / 2) + (cols + 1) / 2);
+    t.r = make_rsrc(t.base, t.bytes);
     t.pitch = (uint32_t)(ldc / 2);
     return t;
 }
@@ -161,11 +167,11 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
 }
 
 // operand kinds: int8; MX block-scaled E2M1; fp8 (per-tensor / per-channel dequant in the epilogue); MX
-// block-scaled fp8
-enum { OP_I8 = 0, OP_MXFP4 = 1, OP_F8 = 2, OP_MXF8 = 3 };
+// block-scaled fp8; MX block-scaled fp6 E2M3 in split planes (the E1M2 / mixed fp4 path)
+enum { OP_I8 = 0, OP_MXFP4 = 1, OP_F8 = 2, OP_MXF8 = 3, OP_MXFP6 = 4 };
 
 // f8f6f4 format codes (the MFMA's cbsz / blgp fields)
-enum { F8F6F4_E4M3 = 0, F8F6F4_E5M2 = 1, F8F6F4_E2M1 = 4 };
+enum { F8F6F4_E4M3 = 0, F8F6F4_E5M2 = 1, F8F6F4_E2M3 = 2, F8F6F4_E2M1 = 4 };
 
 struct CoreArgs {
     rsrc_t a, b;          // A: rows of lda bytes; B: rows of ldb bytes ([n][k] when K-contiguous, else [k][n])
@@ -179,15 +185,20 @@ struct CoreArgs {
     uint32_t sa0_row, sb0_row;  // first row / column index of the tile
     uint32_t sa_rows, sb_rows;  // M / N: the stage stride in rows
     uint32_t sk;                // scale blocks per row (sK, a multiple of SCB)
+    // fp6 Q planes (OP_MXFP6), read through the a / b resources (each plane follows its P plane in one buffer):
+    // byte offset of the tile's first 32-row group in stage 0, and the stage stride (1 KiB x groups)
+    uint32_t qa_off, qa_stride, qb_off, qb_stride;
 };
 
 // FMT (fp8 ops): f8f6f4 format code of A in bits 0-2 and of B in bits 3-5
 template <int BM, int BN, int WM, int WN, int STAGES, bool B_KCONTIG, int OP, int ROWB_ = 64, int FMT = 0, bool ILV = true>
 struct GemmCore {
-    static constexpr bool IS_MX = OP == OP_MXFP4 || OP == OP_MXF8;
+    static constexpr bool IS_MX = OP == OP_MXFP4 || OP == OP_MXF8 || OP == OP_MXFP6;
     static constexpr bool IS_F8 = OP == OP_F8 || OP == OP_MXF8;
-    static constexpr int CBSZ = OP == OP_MXFP4 ? F8F6F4_E2M1 : (FMT & 7);
-    static constexpr int BLGP = OP == OP_MXFP4 ? F8F6F4_E2M1 : ((FMT >> 3) & 7);
+    static constexpr bool IS_FP6 = OP == OP_MXFP6;
+    static constexpr int CBSZ = OP == OP_MXFP4 ? F8F6F4_E2M1 : (IS_FP6 ? F8F6F4_E2M3 : (FMT & 7));
+    static constexpr int BLGP = OP == OP_MXFP4 ? F8F6F4_E2M1 : (IS_FP6 ? F8F6F4_E2M3 : ((FMT >> 3) & 7));
+    static constexpr int TBM = BM, TBN = BN, TWN = WN;  // the tile shape, for code outside the template
     static constexpr int NW = WM * WN;
     static constexpr int NT = NW * 64;
     static constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -209,16 +220,26 @@ struct GemmCore {
     // one stage are 1 KiB contiguous, one wave-wide 16-byte copy.  SA_REG / SB_REG: the A / B scale regions
     // of a stage.  Every wave issues SC_COPIES copies; those past the real ones read out of range into a
     // dummy area, so the per-wave copy count (and with it the vmcnt threshold) is the same for all waves.
+    // fp6 (split planes): the P plane (dwords 0-3 of each block's six) is the operand the copies above stage, ROWB
+    // bytes per row like fp4; the Q plane (dwords 4-5) arrives as 1 KiB blocks per (stage, 32-row group) holding
+    // the 8-byte pieces of the group's 32 rows block by block ([4 blocks][32 rows][8 bytes] for ROWB = 64), one
+    // copy each, staged after the P regions: QA_INSTR + QB_INSTR copies, spread over the waves with the scales.
+    // An MFMA read of k-step s then takes 8 consecutive bytes per lane across 32 rows (no bank conflicts).
+    static constexpr int QROW = IS_FP6 ? ROWB / 2 : 0;  // Q bytes per row per stage
+    static constexpr int QA_INSTR = IS_FP6 ? BM / 32 : 0, QB_INSTR = IS_FP6 ? BN / 32 : 0;
+    static constexpr int Q_REG = (QA_INSTR + QB_INSTR) * 1024;
     static constexpr int SA_INSTR = IS_MX ? (BM + SC_ROWS - 1) / SC_ROWS : 0;
     static constexpr int SB_INSTR = IS_MX ? (BN + SC_ROWS - 1) / SC_ROWS : 0;
     static constexpr int SA_REG = SA_INSTR * 1024, SB_REG = SB_INSTR * 1024;
-    static constexpr int SC_COPIES = (SA_INSTR + SB_INSTR + NW - 1) / NW;
+    static constexpr int AUX_INSTR = SA_INSTR + SB_INSTR + QA_INSTR + QB_INSTR;
+    static constexpr int SC_COPIES = (AUX_INSTR + NW - 1) / NW;
     static constexpr int SC_BYTES = SA_REG + SB_REG;
-    static constexpr int DUMMY_BYTES = IS_MX && SC_COPIES * NW > SA_INSTR + SB_INSTR ? 1024 : 0;
+    static constexpr int DUMMY_BYTES = IS_MX && SC_COPIES * NW > AUX_INSTR ? 1024 : 0;
     static constexpr int COPIES = A_COPIES + B_COPIES + SC_COPIES;
     static constexpr int B_BLK = B_KCONTIG ? 0 : (ROWB / 8) * (BN / 4) / NT;  // 8x4-byte blocks per lane
     static constexpr int B_LOADS = 8 * B_BLK;         // dword loads per lane per stage for a [K, N] B
-    static constexpr int STAGE = (BM + BN) * ROWB + SC_BYTES;
+    static constexpr int STAGE = (BM + BN) * ROWB + Q_REG + SC_BYTES;
+    static constexpr int SC_OFF = (BM + BN) * ROWB + Q_REG;  // the scale regions within a stage
     static constexpr size_t LDS_BYTES = (size_t)STAGES * STAGE + DUMMY_BYTES;
     // vmem operations of this wave issued after stage kt's copies, at the top of iteration kt
     static constexpr int IN_FLIGHT = (STAGES - 2) * (COPIES + B_LOADS);
@@ -232,6 +253,7 @@ struct GemmCore {
     static_assert(!IS_MX || B_KCONTIG, "MX B must be K-contiguous");
     static_assert(!IS_MX || (BM % 64 == 0 && BN % 64 == 0), "scale row groups");
     static_assert(!IS_MX || SCB % 4 == 0 || SCB == 2, "MX stage scale bytes per row");
+    static_assert(!IS_FP6 || (ROWB == 64 && BM % 32 == 0 && BN % 32 == 0), "fp6 Q blocks: 4 MX blocks per stage");
     static_assert(KPS >= 1, "a stage holds at least one k-step");
     static_assert((STAGES >= 3 || (B_KCONTIG && STAGES == 2)) && IN_FLIGHT < 64, "stages");
     static_assert(ROWB == 64 || ROWB == 128, "stage row");
@@ -264,6 +286,13 @@ struct GemmCore {
             const v4i y = *(const v4i*)(base + row * ROWB + swz(row, c + 2) * 16);
             return (v8i){x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
         }
+    }
+
+    // fp6: the Q piece (8 bytes) of k-step s, lane half kh, for tile row `row` (a multiple of 32 plus r32) from a Q
+    // region ([32-row group][4 blocks][32 rows][8 bytes])
+    __device__ __forceinline__ static u32x2 read_q(const uint8_t* qbase, int row, int s, int kh)
+    {
+        return *(const u32x2*)(qbase + (row >> 5) * 1024 + ((2 * s + kh) * 32 + (row & 31)) * 8);
     }
 
     __device__ __forceinline__ static void run(const CoreArgs& p, uint8_t* smem, acc_t (&acc)[FM][FN])
@@ -333,10 +362,22 @@ struct GemmCore {
                 const uint32_t off = (row < p.cols && k < p.kbytes) ? p.b0 + (uint32_t)row * p.ldb + (uint32_t)k : OOB;
                 copy16_to_lds(p.b, sB + row0 * ROWB, off);
             } else if constexpr (IS_MX) {
-                uint8_t* sS = sA + (BM + BN) * ROWB;
+                uint8_t* sS = sA + SC_OFF;
                 const bool kval = (uint32_t)(kt * SCB) < p.sk;
                 const int g = wave * SC_COPIES + (u - A_COPIES - B_COPIES);  // wave-uniform
-                if (g < SA_INSTR) {
+                if (g >= SA_INSTR + SB_INSTR && g < AUX_INSTR) {  // fp6 Q blocks of A, then of B
+                    const int q = g - SA_INSTR - SB_INSTR;
+                    uint8_t* sQ = sA + (BM + BN) * ROWB;
+                    // (groups past the operand's last belong to rows past M / N, whose outputs are dropped: they read
+                    // the next stage's first groups, or zeros past the buffer)
+                    if (q < QA_INSTR)
+                        copy16_to_lds(p.a, sQ + q * 1024,
+                                      kval ? (uint32_t)kt * p.qa_stride + p.qa_off + (uint32_t)(q * 1024 + lane * 16) : OOB);
+                    else
+                        copy16_to_lds(p.b, sQ + q * 1024,
+                                      kval ? (uint32_t)kt * p.qb_stride + p.qb_off + (uint32_t)((q - QA_INSTR) * 1024 + lane * 16)
+                                           : OOB);
+                } else if (g < SA_INSTR) {
                     const uint32_t off =
                         kval ? ((uint32_t)kt * p.sa_rows + p.sa0_row + g * SC_ROWS) * SCB + lane * 16 : OOB;
                     copy16_to_lds(p.sa, sS + g * 1024, off);
@@ -344,7 +385,7 @@ struct GemmCore {
                     const uint32_t off =
                         kval ? ((uint32_t)kt * p.sb_rows + p.sb0_row + (g - SA_INSTR) * SC_ROWS) * SCB + lane * 16 : OOB;
                     copy16_to_lds(p.sb, sS + SA_REG + (g - SA_INSTR) * 1024, off);
-                } else {
+                } else if (g >= AUX_INSTR) {
                     copy16_to_lds(p.sa, smem + STAGES * STAGE, OOB);
                 }
             }
@@ -397,7 +438,7 @@ struct GemmCore {
                 if (h > 0) __builtin_amdgcn_sched_barrier(0);
                 uint32_t swa[IS_MX ? FM : 1], swb[IS_MX ? FN : 1];
                 if constexpr (IS_MX) {
-                    const uint8_t* sS = sA + (BM + BN) * ROWB;
+                    const uint8_t* sS = sA + SC_OFF;
 #pragma unroll
                     for (int i = 0; i < FM; ++i) swa[i] = scale_word(sS, wm * WTM + i * 32 + r32, h) >> (8 * kh);
 #pragma unroll
@@ -415,10 +456,22 @@ struct GemmCore {
                     // (fp8)
                     v8i fa[FM];
 #pragma unroll
-                    for (int i = 0; i < FM; ++i) fa[i] = read_frag(sA, wm * WTM + i * 32 + r32, s, kh);
+                    for (int i = 0; i < FM; ++i) {
+                        fa[i] = read_frag(sA, wm * WTM + i * 32 + r32, s, kh);
+                        if constexpr (IS_FP6) {
+                            const u32x2 q = read_q(sA + (BM + BN) * ROWB, wm * WTM + i * 32 + r32, s, kh);
+                            fa[i][4] = (int)q[0];
+                            fa[i][5] = (int)q[1];
+                        }
+                    }
 #pragma unroll
                     for (int j = 0; j < FN; ++j) {
-                        const v8i fb = read_frag(sB, wn * WTN + j * 32 + r32, s, kh);
+                        v8i fb = read_frag(sB, wn * WTN + j * 32 + r32, s, kh);
+                        if constexpr (IS_FP6) {
+                            const u32x2 q = read_q(sA + (BM + BN) * ROWB + QA_INSTR * 1024, wn * WTN + j * 32 + r32, s, kh);
+                            fb[4] = (int)q[0];
+                            fb[5] = (int)q[1];
+                        }
 #pragma unroll
                         for (int i = 0; i < FM; ++i) {
                             if constexpr (OP == OP_I8) {
@@ -456,5 +509,51 @@ struct GemmCore {
         wait_vmcnt<0>();
     }
 };
+
+// the 32 bits of one accumulator element (a value copy: __builtin_bit_cast of a vector-element lvalue reads the
+// vector's first element under this compiler)
+__device__ __forceinline__ uint32_t acc_bits(float x) { return __float_as_uint(x); }
+__device__ __forceinline__ uint32_t acc_bits(int x) { return (uint32_t)x; }
+
+// enAtomic epilogue of a GemmCore tile (T): the raw accumulators are parked in LDS -- free once every wave has
+// left the main loop -- and a rolled loop then takes one element per thread per step, applies the output
+// conversion conv(tile column, accumulator bits) -> C bits, and combines it into C (c_atomic).  Rolling the loop
+// keeps the conversion, the compare-and-swap code and their registers out of the unrolled store path.  A tile
+// that does not fit the LDS at once goes in NCH chunks of whole wave rows: in chunk ch the waves whose rows lie
+// in it write all their fragments.
+template <class T, int DT, class F>
+__device__ __forceinline__ void atomic_epilogue(uint8_t* smem, const typename T::acc_t (&acc)[T::FM][T::FN],
+                                                const TileOut& out, int rows, int cols, int op, F conv)
+{
+    constexpr int ES = (DT == DT_INT32 || DT == DT_F32) ? 4 : 2;  // bytes per C element
+    constexpr int NCH = (size_t)T::TBM * T::TBN * 4 <= T::LDS_BYTES ? 1 : (size_t)T::TBM * T::TBN * 2 <= T::LDS_BYTES ? 2 : 4;
+    constexpr int CHR = T::TBM / NCH;  // rows per chunk
+    static_assert((size_t)CHR * T::TBN * 4 <= T::LDS_BYTES && CHR % T::WTM == 0 && (T::TBN & (T::TBN - 1)) == 0,
+                  "atomic epilogue chunks");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / T::TWN, wn = wave % T::TWN;
+    const int my_chunk = wm * T::WTM / CHR;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+        __syncthreads();  // the main loop's last LDS reads (or the previous chunk's) are done
+        if (my_chunk == ch) {
+#pragma unroll
+            for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+                for (int j = 0; j < T::FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        *(uint32_t*)(smem + ((T::frag_row(wm, i, r, lane) - ch * CHR) * T::TBN + T::frag_col(wn, j, lane)) * 4) =
+                            acc_bits(acc[i][j][r]);
+        }
+        __syncthreads();
+#pragma unroll 1
+        for (int e = threadIdx.x; e < CHR * T::TBN; e += T::NT) {
+            const int rr = ch * CHR + e / T::TBN, cc = e % T::TBN;
+            if (rr >= rows || cc >= cols) continue;
+            c_atomic<DT>(out.base + (uint32_t)rr * out.pitch + (uint32_t)(cc * ES), conv(cc, *(const uint32_t*)(smem + e * 4)), op);
+        }
+    }
+}
 
 }  // namespace ascq

@@ -30,10 +30,15 @@ namespace ascq {
 // fp8 bits -> fp32 (common.h), the format picked by its f8f6f4 code
 __device__ __forceinline__ float fp8_to_f32(uint8_t v, int fmt) { return fp8_bits_to_f32(v, fmt != F8F6F4_E4M3); }
 
-// w: the column's QUANT_PRE word (offset and sign flag of QF322B8)
-__device__ __forceinline__ void store_f8_out(void* C, int c_type, int64_t o, float v, uint64_t w)
+// w: the column's QUANT_PRE word (offset and sign flag of QF322B8); atomic: IterateAll's enAtomic (f32 / f16 /
+// bf16 C only, checked by the host layer)
+__device__ __forceinline__ void store_f8_out(void* C, int c_type, int64_t o, float v, uint64_t w, int atomic)
 {
-    if (c_type == DT_F32) ((float*)C)[o] = v;
+    if (atomic != C_STORE) {
+        if (c_type == DT_F32) c_atomic<DT_F32>((uint8_t*)C + 4 * o, __float_as_uint(v), atomic);
+        else if (c_type == DT_F16) c_atomic<DT_F16>((uint8_t*)C + 2 * o, f32_to_f16_sat(v), atomic);
+        else c_atomic<DT_BF16>((uint8_t*)C + 2 * o, f32_to_bf16_sat(v), atomic);
+    } else if (c_type == DT_F32) ((float*)C)[o] = v;
     else if (c_type == DT_F16) ((uint16_t*)C)[o] = f32_to_f16_sat(v);
     else if (c_type == DT_BF16) ((uint16_t*)C)[o] = f32_to_bf16_sat(v);
     else if (c_type == DT_INT8 || c_type == DT_UINT8) ((uint8_t*)C)[o] = requant8(v, w);
@@ -111,6 +116,25 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
                 }
         }
     };
+    if (p.atomic != C_STORE) {  // enAtomic: f32 / f16 / bf16 C (the host layer refuses the others)
+        // (acc + bias) x M1 of the column -- the store path's arithmetic
+        auto v = [&](int cl, uint32_t a) {
+            float x = __uint_as_float(a);
+            if (p.bias) x = x + p.bias[n0 + cl];
+            if (p.use_quant) x = x * (p.qvec ? quant_pre_m1(p.qvec[n0 + cl]) : mscalar);
+            return x;
+        };
+        if (p.c_type == DT_F32)
+            atomic_epilogue<T, DT_F32>(smem_f8, acc, out, c.rows, c.cols, p.atomic,
+                                       [&](int cl, uint32_t a) { return __float_as_uint(v(cl, a)); });
+        else if (p.c_type == DT_F16)
+            atomic_epilogue<T, DT_F16>(smem_f8, acc, out, c.rows, c.cols, p.atomic,
+                                       [&](int cl, uint32_t a) { return (uint32_t)f32_to_f16_sat(v(cl, a)); });
+        else
+            atomic_epilogue<T, DT_BF16>(smem_f8, acc, out, c.rows, c.cols, p.atomic,
+                                        [&](int cl, uint32_t a) { return (uint32_t)f32_to_bf16_sat(v(cl, a)); });
+        return;
+    }
     auto put32 = [&](uint32_t x, uint32_t o) { __builtin_amdgcn_raw_buffer_store_b32(x, out.r, o, 0, 0); };
     auto put16 = [&](uint16_t x, uint32_t o) { __builtin_amdgcn_raw_buffer_store_b16(x, out.r, o, 0, 0); };
     auto put8 = [&](uint8_t x, uint32_t o) { __builtin_amdgcn_raw_buffer_store_b8(x, out.r, o, 0, 0); };
@@ -155,7 +179,7 @@ __global__ __launch_bounds__(256) void gemm_f8_generic_kernel(GemmF8Args p)
     for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
         const int64_t m = e / p.N, n = e % p.N;
         const uint64_t w = p.qvec ? p.qvec[n] : p.qscalar;
-        store_f8_out(p.C, p.c_type, m * p.ldc + n, value(m, n, w), w);
+        store_f8_out(p.C, p.c_type, m * p.ldc + n, value(m, n, w), w, p.atomic);
     }
 }
 

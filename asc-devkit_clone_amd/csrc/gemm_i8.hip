@@ -85,6 +85,23 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
                 }
         }
     };
+    if (p.atomic != C_STORE) {  // enAtomic: int32 / f16 / bf16 C (the host layer refuses the others)
+        // acc + bias (int32, wrapping), then x M1 of the column for f16 / bf16 -- the store path's arithmetic
+        auto v = [&](int cl, uint32_t a) { return (int32_t)(a + (uint32_t)(p.bias ? p.bias[n0 + cl] : 0)); };
+        auto m1 = [&](int cl) { return p.qvec ? quant_pre_m1(p.qvec[n0 + cl]) : mscalar; };
+        if (p.epi == EPI_I32)
+            atomic_epilogue<T, DT_INT32>(smem, acc, out, c.rows, c.cols, p.atomic,
+                                         [&](int cl, uint32_t a) { return (uint32_t)v(cl, a); });
+        else if (p.epi == EPI_DEQ_F16)
+            atomic_epilogue<T, DT_F16>(smem, acc, out, c.rows, c.cols, p.atomic, [&](int cl, uint32_t a) {
+                return (uint32_t)f32_to_f16_sat((float)v(cl, a) * m1(cl));
+            });
+        else
+            atomic_epilogue<T, DT_BF16>(smem, acc, out, c.rows, c.cols, p.atomic, [&](int cl, uint32_t a) {
+                return (uint32_t)f32_to_bf16_sat((float)v(cl, a) * m1(cl));
+            });
+        return;
+    }
     if (p.epi == EPI_I32)
         store([](int32_t v, float, uint64_t) { return (uint32_t)v; },
               [&](uint32_t x, uint32_t o) { __builtin_amdgcn_raw_buffer_store_b32(x, out.r, o, 0, 0); });
@@ -229,7 +246,11 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(GemmI8Args p)
         const uint64_t w = p.qvec ? p.qvec[n] : p.qscalar;
         const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
         const int64_t o = m * p.ldc + n;
-        if (p.epi == EPI_I32) ((int32_t*)p.C)[o] = v;
+        if (p.atomic != C_STORE) {  // int32 / f16 / bf16 C only (checked by the host layer)
+            if (p.epi == EPI_I32) c_atomic<DT_INT32>((uint8_t*)p.C + 4 * o, (uint32_t)v, p.atomic);
+            else if (p.epi == EPI_DEQ_F16) c_atomic<DT_F16>((uint8_t*)p.C + 2 * o, f32_to_f16_sat((float)v * m1), p.atomic);
+            else c_atomic<DT_BF16>((uint8_t*)p.C + 2 * o, f32_to_bf16_sat((float)v * m1), p.atomic);
+        } else if (p.epi == EPI_I32) ((int32_t*)p.C)[o] = v;
         else if (p.epi == EPI_DEQ_F16) ((uint16_t*)p.C)[o] = f32_to_f16_sat((float)v * m1);
         else if (p.epi == EPI_DEQ_BF16) ((uint16_t*)p.C)[o] = f32_to_bf16_sat((float)v * m1);
         else ((uint8_t*)p.C)[o] = requant8((float)v * m1, w);

@@ -29,6 +29,13 @@
 
 namespace ascq {
 
+// one f16 output element: a store, or IterateAll's enAtomic combine
+__device__ __forceinline__ void y_put(uint16_t* p, uint16_t v, int atomic)
+{
+    if (atomic == C_STORE) *p = v;
+    else c_atomic<DT_F16>((uint8_t*)p, v, atomic);
+}
+
 constexpr int KT = 128;  // k per packed tile
 
 size_t weight_pack_bytes(int w_type, int64_t K, int64_t N)
@@ -173,7 +180,8 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
                                                                      const uint8_t* __restrict__ wp,
                                                                      const uint16_t* __restrict__ scale,
                                                                      const uint16_t* __restrict__ offset,
-                                                                     int64_t M, int64_t N, int64_t K, int64_t g)
+                                                                     int64_t M, int64_t N, int64_t K, int64_t g,
+                                                                     int atomic)
 {
     constexpr int TILE_BYTES = INT4 ? 1024 : 2048;
     constexpr int LANE_BYTES = INT4 ? 16 : 32;
@@ -380,7 +388,7 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int64_t m = 16 * a + 4 * kq + i;
-                if (m < M) y[m * N + n] = f32_to_f16_sat(acc[a][b][i]);
+                if (m < M) y_put(y + m * N + n, f32_to_f16_sat(acc[a][b][i]), atomic);
             }
         }
 }
@@ -417,7 +425,8 @@ __global__ __launch_bounds__(NS * KSW * 64) void aq_dma_kernel(uint16_t* __restr
                                                                const uint8_t* __restrict__ wp,
                                                                const uint16_t* __restrict__ scale,
                                                                const uint16_t* __restrict__ offset, int64_t M,
-                                                               int64_t N, int64_t K, int64_t g, int64_t ldx)
+                                                               int64_t N, int64_t K, int64_t g, int64_t ldx,
+                                                               int atomic)
 {
     using P = AqDma<MT, NS, KSW, ST, INT4, HAS_OFF>;
     constexpr int TILE_BYTES = INT4 ? 1024 : 2048;
@@ -554,49 +563,49 @@ __global__ __launch_bounds__(NS * KSW * 64) void aq_dma_kernel(uint16_t* __restr
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int64_t m = 16 * a + 4 * kq + i;
-            if (m < M) y[m * N + n] = f32_to_f16_sat(acc[a][i]);
+            if (m < M) y_put(y + m * N + n, f32_to_f16_sat(acc[a][i]), atomic);
         }
 }
 
 template <int MT, int NBW, int KSPLIT, int TPW, bool INT4, bool HAS_OFF, bool XLDS>
 static void launch_aq2(uint16_t* y, const uint16_t* x, const void* wp, const uint16_t* scale, const uint16_t* offset,
-                       int64_t g, int64_t M, int64_t N, int64_t K, hipStream_t st)
+                       int64_t g, int64_t M, int64_t N, int64_t K, int atomic, hipStream_t st)
 {
     const unsigned blocks = (unsigned)((N / 16 + NBW - 1) / NBW);
     const size_t lds = XLDS ? (size_t)(M * K * 2 + 16) : 0;
     if (g % KT == 0)
         launch_k((antiquant_gemm_kernel<MT, NBW, KSPLIT, TPW, INT4, HAS_OFF, true, XLDS>), dim3(blocks),
-                           dim3(KSPLIT * 64), lds, st, y, x, (const uint8_t*)wp, scale, offset, M, N, K, g);
+                           dim3(KSPLIT * 64), lds, st, y, x, (const uint8_t*)wp, scale, offset, M, N, K, g, atomic);
     else
         launch_k((antiquant_gemm_kernel<MT, NBW, KSPLIT, TPW, INT4, HAS_OFF, false, XLDS>), dim3(blocks),
-                           dim3(KSPLIT * 64), lds, st, y, x, (const uint8_t*)wp, scale, offset, M, N, K, g);
+                           dim3(KSPLIT * 64), lds, st, y, x, (const uint8_t*)wp, scale, offset, M, N, K, g, atomic);
 }
 
 template <int MT, int NBW, int KSPLIT, int TPW, bool XLDS = false>
 static void launch_aq(uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
-                      const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, hipStream_t st)
+                      const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, int atomic, hipStream_t st)
 {
     if (int4) {
-        if (offset) launch_aq2<MT, NBW, KSPLIT, TPW, true, true, XLDS>(y, x, wp, scale, offset, g, M, N, K, st);
-        else launch_aq2<MT, NBW, KSPLIT, TPW, true, false, XLDS>(y, x, wp, scale, offset, g, M, N, K, st);
+        if (offset) launch_aq2<MT, NBW, KSPLIT, TPW, true, true, XLDS>(y, x, wp, scale, offset, g, M, N, K, atomic, st);
+        else launch_aq2<MT, NBW, KSPLIT, TPW, true, false, XLDS>(y, x, wp, scale, offset, g, M, N, K, atomic, st);
     } else {
-        if (offset) launch_aq2<MT, NBW, KSPLIT, TPW, false, true, XLDS>(y, x, wp, scale, offset, g, M, N, K, st);
-        else launch_aq2<MT, NBW, KSPLIT, TPW, false, false, XLDS>(y, x, wp, scale, offset, g, M, N, K, st);
+        if (offset) launch_aq2<MT, NBW, KSPLIT, TPW, false, true, XLDS>(y, x, wp, scale, offset, g, M, N, K, atomic, st);
+        else launch_aq2<MT, NBW, KSPLIT, TPW, false, false, XLDS>(y, x, wp, scale, offset, g, M, N, K, atomic, st);
     }
 }
 
 template <int MT, int NS, int KSW, int ST, bool ROT>
 static void launch_dma(uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
-                       const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, hipStream_t st)
+                       const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, int atomic, hipStream_t st)
 {
     const dim3 grid((unsigned)((N / 16 + NS - 1) / NS)), block(NS * KSW * 64);
     const uint8_t* w = (const uint8_t*)wp;
     if (int4) {
-        if (offset) launch_k((aq_dma_kernel<MT, NS, KSW, ST, true, true, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K);
-        else launch_k((aq_dma_kernel<MT, NS, KSW, ST, true, false, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K);
+        if (offset) launch_k((aq_dma_kernel<MT, NS, KSW, ST, true, true, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K, atomic);
+        else launch_k((aq_dma_kernel<MT, NS, KSW, ST, true, false, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K, atomic);
     } else {
-        if (offset) launch_k((aq_dma_kernel<MT, NS, KSW, ST, false, true, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K);
-        else launch_k((aq_dma_kernel<MT, NS, KSW, ST, false, false, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K);
+        if (offset) launch_k((aq_dma_kernel<MT, NS, KSW, ST, false, true, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K, atomic);
+        else launch_k((aq_dma_kernel<MT, NS, KSW, ST, false, false, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K, atomic);
     }
 }
 
@@ -604,7 +613,7 @@ static void launch_dma(uint16_t* y, const uint16_t* x, const void* wp, bool int4
 // x and the scales must each stay below 2^31 bytes (buffer offsets; checked by the caller).
 hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* wp, int w_type, const uint16_t* scale,
                                    const uint16_t* offset, int64_t group, int64_t M, int64_t N, int64_t K,
-                                   hipStream_t st)
+                                   int atomic, hipStream_t st)
 {
     const int64_t g = group > 0 ? group : K;
     const bool int4 = w_type == DT_INT4;
@@ -617,21 +626,21 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
         // Larger batches: x through the LDS ring of aq_dma_kernel (shapes measured fastest at K = 4096,
         // N = 11008; the 64-row form rotates each workgroup's k order, which measured ~8 % faster there).
         if (mc <= 4 && mc * K * 2 + 16 <= 48 * 1024) {
-            if (int4) launch_aq<1, 1, 4, 8, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
-            else launch_aq<1, 1, 8, 4, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+            if (int4) launch_aq<1, 1, 4, 8, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+            else launch_aq<1, 1, 8, 4, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
         }
         else if (mc > 4 && g % KT == 0) {
             if (mc <= 16) {
-                if (int4) launch_dma<1, 2, 4, 4, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
-                else launch_dma<1, 2, 4, 3, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+                if (int4) launch_dma<1, 2, 4, 4, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+                else launch_dma<1, 2, 4, 3, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
             } else if (mc <= 32) {
-                launch_dma<2, 4, 4, 4, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+                launch_dma<2, 4, 4, 4, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
             } else {
-                launch_dma<4, 4, 2, 3, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+                launch_dma<4, 4, 2, 3, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
             }
-        } else if (mc <= 16) launch_aq<1, 1, 8, 4>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
-        else if (mc <= 32) launch_aq<2, 2, 8, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
-        else launch_aq<4, 2, 8, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, st);
+        } else if (mc <= 16) launch_aq<1, 1, 8, 4>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+        else if (mc <= 32) launch_aq<2, 2, 8, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+        else launch_aq<4, 2, 8, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

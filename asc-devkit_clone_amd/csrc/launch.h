@@ -11,6 +11,11 @@
 
 namespace ascq {
 
+// IterateAll's enAtomic (impl/adv_api/detail/matmul/utils/matmul_config_utils.h:53-55, applied to the copy-out by
+// scheduler/base/scheduler_base.h:484-494): 0 stores C; 1 / 2 / 3 combine C = add / max / min (C, v) in C's type,
+// one atomic read-modify-write per element (c_atomic), so concurrent IterateAll calls into the same C compose.
+enum : int { C_STORE = 0, C_ADD = 1, C_MAX = 2, C_MIN = 3 };
+
 // Raises the dynamic-LDS limit of kernel K to `bytes` once per device (the attribute belongs to the function on
 // the current device), thread-safe; K is the kernel itself, so each instantiation keeps its own record.
 template <auto K>
@@ -86,6 +91,7 @@ struct GemmI8Args {
     uint64_t qscalar;
     int epi;              // EPI_*
     int trans_a, trans_b;
+    int atomic;           // C_STORE, or C_ADD / C_MAX / C_MIN (int32 / f16 / bf16 C): IterateAll's enAtomic
 };
 hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st);
 
@@ -102,6 +108,7 @@ struct GemmF8Args {
     int c_type;           // DT_F16 / DT_BF16 / DT_F32; DT_INT8 / DT_UINT8 (QF322B8); DT_FP8_E4M3 / _E5M2 (QF322FP8)
     int fmt_a, fmt_b;     // f8f6f4 codes: 0 e4m3fn, 1 e5m2
     int trans_a, trans_b;
+    int atomic;           // C_STORE, or C_ADD / C_MAX / C_MIN (f32 / f16 / bf16 C): IterateAll's enAtomic
 };
 hipError_t launch_gemm_f8(const GemmF8Args& a, hipStream_t st);
 
@@ -127,7 +134,7 @@ hipError_t launch_weight_pack(void* packed, const void* w, int w_type, int64_t K
                               hipStream_t st);
 hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* wp, int w_type, const uint16_t* scale,
                                    const uint16_t* offset, int64_t group, int64_t M, int64_t N, int64_t K,
-                                   hipStream_t st);
+                                   int atomic, hipStream_t st);
 
 // mx_gemm.hip
 struct MxGemmArgs {
@@ -141,8 +148,19 @@ struct MxGemmArgs {
     void* C;                // [M, N]
     int c_type;             // DT_BF16 / DT_F32
     int fmt_a, fmt_b;       // f8f6f4 codes of the elements: 4 E2M1 (both), or fp8 0 e4m3fn / 1 e5m2 (any mix)
+    const float* bias;      // [N] f32, added to the fp32 sums before the output cast, or null
+    int atomic;             // C_STORE, or C_ADD / C_MAX / C_MIN: IterateAll's enAtomic
+    // fp6 E2M3 (fmt 2, both operands): A / B are the P planes and Aq / Bq the Q planes written by
+    // launch_fp4_to_fp6_planes
+    const uint8_t* Aq;
+    const uint8_t* Bq;
 };
 hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st);
+// fp4 (E2M1 or E1M2) [R, K/2] -> fp6 E2M3 split planes: P [R, K/2] (dwords 0-3 of each MX block's six) and Q
+// (fp6_q_plane_bytes(R, K): dwords 4-5, 1 KiB per (128 K, 32-row group)); K a multiple of 128
+size_t fp6_q_plane_bytes(int64_t R, int64_t K);
+hipError_t launch_fp4_to_fp6_planes(uint8_t* P, uint8_t* Q, const uint8_t* src, int64_t R, int64_t K, bool e1m2,
+                                    hipStream_t st);
 // transpose.hip: int8 [rows, cols] -> [cols, rows]; fp4 [K, N] -> [N, K] tiled fast path (returns false when
 // the shape / alignment does not allow it)
 hipError_t launch_transpose_i8(uint8_t* dst, const uint8_t* src, int64_t rows, int64_t cols, hipStream_t st);

@@ -17,6 +17,15 @@
 // (the reference's non-transposed layout, two fp4 per byte along N) is first transposed to [N, K] in a
 // workspace by fp4_transpose_kernel.
 //
+// E1M2 elements (fp4x2_e1m2_t, the reference's high-performance MX sample) have no gfx950 format, but every E1M2
+// value k/4 (k = 0..7) is exact in fp6 E2M3, a native format of the same instruction at the fp4 rate, and so is
+// every E2M1 value.  When either operand is E1M2 both are rewritten to fp6 by fp4_to_fp6_planes_kernel and
+// multiplied by the OP_MXFP6 form of the core (cbsz = blgp = 2): per lane 32 fp6 of row (lane % 32), MX block
+// (lane / 32), packed 6 bits each (element i at bits 6i .. 6i + 5 of six registers: the layout measured for the
+// fp6 operand matches fp4's lane / block assignment).  The six registers are split into two planes so the P
+// plane (registers 0-3) is staged exactly like fp4 and the Q plane (registers 4-5) rides in 1 KiB blocks like
+// the scales; 3 stages of 256 x 256 (51200 bytes each) fit the 160 KiB of LDS.
+//
 // MX-FP8 uses the same instruction with fp8 format codes: per lane 32 fp8 of one row (32 bytes, two register
 // quads; MX block b of a k-step is quad b of all 64 lanes, see gemm_core.h);
 // 64 fp8 of K per 64-byte stage row (one k-step, a 16-bit pair of scales per row), four stages of 256 x 256
@@ -35,15 +44,26 @@ __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, con
     using T = GemmCore<BM, BN, WM, WN, ST, true, OP, RB, FMT, ILV>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_mx[];
     const int64_t M = p.M, N = p.N, K = p.K;
-    const int64_t KB = OP == OP_MXFP4 ? K / 2 : K;  // bytes per row
+    const int64_t KB = OP == OP_MXF8 ? K : K / 2;  // bytes per row (fp6: of the P plane)
     const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
     int tm, tn;
     tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     const int64_t sK = (K + 63) / 64 * 2;
     CoreArgs c{};
-    c.a = make_rsrc(p.A, (uint32_t)(M * KB));
-    c.b = make_rsrc(p.B, (uint32_t)(N * KB));
+    if constexpr (OP == OP_MXFP6) {  // P and Q planes in one buffer per operand (launch_mx_gemm checks the layout)
+        const uint32_t qa0 = (uint32_t)(p.Aq - p.A), qb0 = (uint32_t)(p.Bq - p.B);
+        const uint32_t ga = (uint32_t)((M + 31) / 32), gb = (uint32_t)((N + 31) / 32);
+        c.a = make_rsrc(p.A, qa0 + (uint32_t)(K / 128) * ga * 1024u);
+        c.b = make_rsrc(p.B, qb0 + (uint32_t)(K / 128) * gb * 1024u);
+        c.qa_stride = ga * 1024u;
+        c.qb_stride = gb * 1024u;
+        c.qa_off = qa0 + (uint32_t)(m0 / 32) * 1024u;
+        c.qb_off = qb0 + (uint32_t)(n0 / 32) * 1024u;
+    } else {
+        c.a = make_rsrc(p.A, (uint32_t)(M * KB));
+        c.b = make_rsrc(p.B, (uint32_t)(N * KB));
+    }
     c.lda = c.ldb = (uint32_t)KB;
     c.rows = (int32_t)(M - m0 < BM ? M - m0 : BM);
     c.cols = (int32_t)(N - n0 < BN ? N - n0 : BN);
@@ -71,12 +91,27 @@ __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, con
         for (int j = 0; j < T::FN; ++j) {
             const int cl = T::frag_col(wn, j, lane);
             const uint32_t cbase = cl < c.cols ? (uint32_t)(cl * esize) : OOB;
+            const float bias = (p.bias && cl < c.cols) ? p.bias[n0 + cl] : 0.0f;
 #pragma unroll
             for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) put(acc[i][j][r], cbase + (uint32_t)T::frag_row(wm, i, r, lane) * out.pitch);
+                for (int r = 0; r < 16; ++r) {
+                    float v = acc[i][j][r];
+                    if (p.bias) v = v + bias;
+                    put(v, cbase + (uint32_t)T::frag_row(wm, i, r, lane) * out.pitch);
+                }
         }
     };
+    if (p.atomic != C_STORE) {  // enAtomic: acc + bias, then the output cast -- the store path's arithmetic
+        auto v = [&](int cl, uint32_t a) { return p.bias ? __uint_as_float(a) + p.bias[n0 + cl] : __uint_as_float(a); };
+        if (p.c_type == DT_F32)
+            atomic_epilogue<T, DT_F32>(smem_mx, acc, out, c.rows, c.cols, p.atomic,
+                                       [&](int cl, uint32_t a) { return __float_as_uint(v(cl, a)); });
+        else
+            atomic_epilogue<T, DT_BF16>(smem_mx, acc, out, c.rows, c.cols, p.atomic,
+                                        [&](int cl, uint32_t a) { return (uint32_t)f32_to_bf16_sat(v(cl, a)); });
+        return;
+    }
     if (p.c_type == DT_F32)
         store([&](float v, uint32_t o) { __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), out.r, o, 0, 0); });
     else
@@ -106,6 +141,57 @@ hipError_t launch_fp4_transpose(uint8_t* dst, const uint8_t* src, int64_t K, int
     int64_t blocks = (N * K / 2 + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     hipLaunchKernelGGL(fp4_transpose_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, src, K, N);
+    return hipGetLastError();
+}
+
+// fp4 -> fp6 E2M3 split planes.  A nibble s|abc is E1M2 (sign, 1-bit exponent, 2-bit mantissa, value abc / 4) or
+// E2M1 (sign, 2-bit exponent, 1-bit mantissa, bias 1); its E2M3 code (sign, 2-bit exponent, 3-bit mantissa,
+// bias 1) is s|0abc|0 for E1M2 (abc / 4 = a.bc, or 0.bc when a = 0) and s|abc|00 for E2M1 -- both exact, signed
+// zero included.  Each MX block's 32 codes pack into six dwords (element i at bits 6i .. 6i + 5); dwords 0-3 go to
+// P (block b of row r at byte r K/2 + 16 b) and dwords 4-5 to Q ([stage t = b / 4][32-row group][b % 4][row % 32]
+// x 8 bytes).  Workgroup (x: pair of stages, y: 32-row group) of 256 = 2 stages x 4 blocks x 32 rows, so each row's
+// 128 bytes are one cache line in and out and each Q block is written as 1 KiB contiguous.  Rows past R write zero
+// Q pieces (read by the GEMM's last group only for rows it drops).
+__global__ __launch_bounds__(256) void fp4_to_fp6_planes_kernel(uint8_t* __restrict__ P, uint8_t* __restrict__ Q,
+                                                                const uint8_t* __restrict__ src, int64_t R, int64_t K,
+                                                                int e1m2)
+{
+    const int r32 = threadIdx.x & 31, b4 = (threadIdx.x >> 5) & 3;
+    const int64_t t = 2 * (int64_t)blockIdx.x + (threadIdx.x >> 7);
+    const int64_t groups = gridDim.y, g = blockIdx.y;
+    if (t >= K / 128) return;
+    const int64_t r = g * 32 + r32, b = t * 4 + b4;
+    uint32_t in[4] = {0u, 0u, 0u, 0u};
+    if (r < R) {
+        const u32x4 v = *(const u32x4*)(src + r * (K / 2) + b * 16);
+        in[0] = v[0];
+        in[1] = v[1];
+        in[2] = v[2];
+        in[3] = v[3];
+    }
+    const uint32_t msh = e1m2 ? 1u : 2u;
+    uint32_t out[6] = {0u, 0u, 0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const uint32_t n = (in[i / 8] >> (4 * (i % 8))) & 0xFu;
+        const uint32_t c = ((n & 8u) << 2) | ((n & 7u) << msh);
+        const int bit = 6 * i;
+        out[bit / 32] |= c << (bit % 32);
+        if (bit % 32 > 26) out[bit / 32 + 1] |= c >> (32 - bit % 32);
+    }
+    if (r < R) *(u32x4*)(P + r * (K / 2) + b * 16) = (u32x4){out[0], out[1], out[2], out[3]};
+    *(u32x2*)(Q + (((t * groups + g) * 4 + b4) * 32 + r32) * 8) = (u32x2){out[4], out[5]};
+}
+
+size_t fp6_q_plane_bytes(int64_t R, int64_t K) { return (size_t)((K / 128) * ((R + 31) / 32) * 1024); }
+
+hipError_t launch_fp4_to_fp6_planes(uint8_t* P, uint8_t* Q, const uint8_t* src, int64_t R, int64_t K, bool e1m2,
+                                    hipStream_t st)
+{
+    const int64_t groups = (R + 31) / 32, pairs = (K / 128 + 1) / 2;
+    if (K % 128 != 0 || groups > 65535 || pairs < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(fp4_to_fp6_planes_kernel, dim3((unsigned)pairs, (unsigned)groups), dim3(256), 0, st, P, Q, src,
+                       R, K, e1m2 ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -208,9 +294,19 @@ static hipError_t launch_mx_f8(const MxGemmArgs& a, hipStream_t st)
 hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st)
 {
     const bool fp4 = a.fmt_a == F8F6F4_E2M1 && a.fmt_b == F8F6F4_E2M1;
+    const bool fp6 = a.fmt_a == F8F6F4_E2M3 && a.fmt_b == F8F6F4_E2M3;
     // (the epilogue addresses a 256-row output tile with 32-bit offsets: N < 2^21)
-    if (a.K % (fp4 ? 128 : 64) != 0 || !a.ws_scales || a.N >= (1ll << 21)) return hipErrorInvalidValue;
+    if (a.K % (fp4 || fp6 ? 128 : 64) != 0 || !a.ws_scales || a.N >= (1ll << 21)) return hipErrorInvalidValue;
     const bool big = a.M >= 1024 && a.N >= 1024;
+    if (fp6) {
+        // each Q plane follows its P plane in one buffer below 2 GiB (one buffer resource covers both)
+        const auto fits = [&](const uint8_t* p, const uint8_t* q, int64_t R) {
+            return q && q - p >= R * (a.K / 2) && (q - p) + (int64_t)fp6_q_plane_bytes(R, a.K) < (1ll << 31);
+        };
+        if (!fits(a.A, a.Aq, a.M) || !fits(a.B, a.Bq, a.N)) return hipErrorInvalidValue;
+        if (big) return launch_mx_tiled<256, 128, 4, 2, 4, 64, OP_MXFP6, 0>(a, st);
+        return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP6, 0>(a, st);
+    }
     if (fp4) {
         if (big) return launch_mx_tiled<256, 256, 4, 2, 4, 64, OP_MXFP4, 0>(a, st);
         return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP4, 0>(a, st);

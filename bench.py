@@ -280,14 +280,34 @@ def bench_group(torch, ascq, iters, w_trans=False):
                 group_counts=[int(c) for c in counts])
 
 
+def _mx_fp4_normal(torch, R, K, g):
+    """N(0, 1) [R, K] MX-quantised on the GPU with torch ops (data generation only): per 32-element block the
+    shared exponent e = floor(log2(absmax)) - 2 (E2M1's largest binade), codes = E2M1 nearest of x / 2^e (ties
+    to the even code), clamped to 6.  Returns packed [R, K/2] codes (even k low nibble) and scales [R, K/32]."""
+    x = torch.randn((R, K // 32, 32), generator=g, device="cuda")
+    amax = x.abs().amax(-1, keepdim=True).clamp_min(2.0 ** -126)
+    e = torch.floor(torch.log2(amax)) - 2
+    v = (x / torch.exp2(e)).abs().clamp_max(6.0)
+    mags = torch.tensor([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], device="cuda")
+    mids = (mags[1:] + mags[:-1]) / 2
+    idx = torch.bucketize(v, mids)  # v on midpoint j gets the lower code j ...
+    tie = (idx < 7) & (v == mids[idx.clamp_max(6)])
+    idx = torch.where(tie & (idx % 2 == 1), idx + 1, idx)  # ... or j + 1 when that is the even one
+    code = (idx | torch.where(x < 0, 8, 0)).to(torch.uint8).reshape(R, K)
+    packed = (code[:, 0::2] | (code[:, 1::2] << 4)).contiguous()
+    scales = (e.reshape(R, K // 32) + 127).to(torch.uint8).contiguous()
+    return packed, scales
+
+
 def bench_mx(torch, ascq, iters, trans_b=True):
     M = N = K = 8192
     g = torch.Generator(device="cuda")
     g.manual_seed(5)
-    A = torch.randint(0, 256, (M, K // 2), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8)
-    B = torch.randint(0, 256, (N, K // 2), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8)
-    sA = torch.randint(124, 129, (M, K // 32), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8)
-    sB = torch.randint(124, 129, (N, K // 32), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8)
+    A, sA = _mx_fp4_normal(torch, M, K, g)
+    B, sB = _mx_fp4_normal(torch, N, K, g)
+    if not trans_b:  # [N, K/2] packed along K -> [K, N/2] packed along N
+        nib = torch.stack([B & 0xF, B >> 4], -1).reshape(N, K).t().contiguous()
+        B = (nib[:, 0::2] | (nib[:, 1::2] << 4)).contiguous()
     C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     mm = ascq.Matmul(ascq.FP4_E2M1, ascq.FP4_E2M1, ascq.BF16, 0, ascq.E8M0)
     mm.SetOrgShape(M, N, K)
@@ -301,9 +321,88 @@ def bench_mx(torch, ascq, iters, trans_b=True):
 
     ms = _time_loop(torch, fn, iters, warmup=2)
     tf = 2 * M * N * K / (ms * 1e-3) / 1e12
-    return dict(workload=f"MX-FP4 E2M1/E8M0 GEMM {M}x{N}x{K}, fp32 acc, bf16 out, B given "
+    return dict(workload=f"MX-FP4 E2M1/E8M0 GEMM {M}x{N}x{K}, N(0,1) MX-quantised, fp32 acc, bf16 out, B given "
                          + ("[N,K] (isTransposeB)" if trans_b else "[K,N] (transposed on the fly)"),
                 ms=ms, value=tf, unit="TFLOPS", frac_of_peak=tf / MXFP4_PEAK_TFLOPS)
+
+
+# the reference's published figures for its own two high-performance samples (Ascend 950PR, msprof)
+REF_MX_E1M2_US = 693.283      # matmul_mxfp4_high_performance/README_en.md:177 (Case 2)
+REF_GROUP_GELU_US = 204.129   # quant_group_matmul_high_performance/README_en.md:368 (scenario 2)
+
+
+def bench_mx_e1m2_sample(torch, ascq, iters):
+    """The reference's high-performance MX sample (matmul_mxfp4_high_performance): A [8192, 8192] and B given
+    [K, N] = [8192, 8192], fp4x2_e1m2_t from randint(-1, 2), E8M0 scales randint(127, 130) (B's [sK/2, N, 2]),
+    fp32 accumulation, bf16 out.  One IterateAll: B transpose, fp4 -> fp6 planes of both operands, scale
+    rearrangement and the fp6 MFMA GEMM."""
+    M = N = K = 8192
+    g = torch.Generator(device="cuda")
+    g.manual_seed(8)
+    lut = torch.tensor([0xC, 0x0, 0x4], dtype=torch.uint8, device="cuda")  # e1m2 codes of -1, 0, 1
+    a = lut[torch.randint(0, 3, (M, K), generator=g, device="cuda")]
+    b = lut[torch.randint(0, 3, (K, N), generator=g, device="cuda")]
+    A = (a[:, 0::2] | (a[:, 1::2] << 4)).contiguous()
+    B = (b[:, 0::2] | (b[:, 1::2] << 4)).contiguous()
+    del a, b
+    sK = K // 32
+    sA = torch.randint(127, 130, (M, sK), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8)
+    sB = torch.randint(127, 130, (sK // 2, N, 2), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8)
+    C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    mm = ascq.Matmul(ascq.FP4_E1M2, ascq.FP4_E1M2, ascq.BF16, 0, ascq.E8M0)
+    mm.SetOrgShape(M, N, K)
+    mm.SetTensorA(A)
+    mm.SetTensorB(B, False)
+    mm.SetTensorScaleA(sA, False)
+    mm.SetTensorScaleB(sB, False)
+
+    def fn(i):
+        mm.IterateAll(C)
+
+    ms = _time_loop(torch, fn, iters, warmup=2)
+    tf = 2 * M * N * K / (ms * 1e-3) / 1e12
+    return dict(workload=f"reference MX sample: fp4x2_e1m2 MX GEMM {M}x{N}x{K} (randint(-1,2) elements, scales "
+                         "127-129), B given [K,N], bf16 out; the whole IterateAll (B transpose, fp6 planes, scales, "
+                         "GEMM)", ms=ms, value=tf, unit="TFLOPS", frac_of_peak=tf / MXFP4_PEAK_TFLOPS,
+                reference_us=REF_MX_E1M2_US, speedup_vs_reference=REF_MX_E1M2_US / (ms * 1e3))
+
+
+def bench_group_sample(torch, ascq, iters):
+    """The reference's QuantGroupMatmul sample (quant_group_matmul_high_performance, scenario 2): M = 8192 tokens
+    in 8 equal groups, K = 1024, N = 8192, int8 x and NZ int8 weights [8, 1024, 8192], f32 per-token and
+    per-channel scales, FasterGelu, f16 out.  The NZ weights are re-laid [G, N, K] once outside the timed loop
+    (weights are static; the reference's NZ layout is itself prepared offline)."""
+    G, M, K, N = 8, 8192, 1024, 8192
+    g = torch.Generator(device="cuda")
+    g.manual_seed(9)
+    x = torch.randint(-127, 128, (M, K), generator=g, device="cuda", dtype=torch.int8)
+    w = torch.randint(-127, 128, (G, K, N), generator=g, device="cuda", dtype=torch.int8)
+    w_nz = w.reshape(G, K // 16, 16, N // 32, 32).permute(0, 3, 1, 2, 4).contiguous()  # gen_data.py:62
+    del w
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    wt = ascq.nz_to_nd(w_nz.view(torch.uint8).reshape(-1), ascq.INT8, G, K, N, transpose_out=True).view(torch.int8)
+    torch.cuda.synchronize()
+    relayout_ms = (time.perf_counter() - t0) * 1e3
+    pts = torch.rand(M, generator=g, device="cuda") * 0.01
+    scale = torch.rand((G, N), generator=g, device="cuda") * 0.01
+    counts = torch.full((G,), M // G, dtype=torch.int64, device="cuda")
+    y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+
+    def fn(i):
+        ascq.quant_group_matmul(x, pts, wt, scale, counts, 1, out=y, w_trans=True, out_dtype=torch.float16,
+                                activation=ascq.ACT_FASTER_GELU)
+
+    ms = _time_loop(torch, fn, iters)
+    ops = 2 * M * K * N
+    tops = ops / (ms * 1e-3) / 1e12
+    nbytes = M * K + 4 * M + G * K * N + 4 * G * N + 2 * M * N + 8 * G
+    attainable = min(INT8_PEAK_TOPS, ops / nbytes * HBM_PEAK_GBS / 1e3)
+    return dict(workload=f"reference QuantGroupMatmul sample: M={M} in {G} equal groups, K={K}, N={N}, NZ int8 "
+                         "weights (re-laid [G,N,K] once), per-token x per-channel f32 scales, FasterGelu, f16 out",
+                ms=ms, value=tops, unit="TOPS", frac_of_peak=tops / INT8_PEAK_TOPS,
+                frac_of_attainable=tops / attainable, nz_relayout_ms_once=relayout_ms,
+                reference_us=REF_GROUP_GELU_US, speedup_vs_reference=REF_GROUP_GELU_US / (ms * 1e3))
 
 
 def _fp8_bytes(torch, shape, g, dt):
@@ -524,8 +623,10 @@ OTHER = {
     "w8a8": [lambda t, a: bench_w8a8(t, a, 128, 256, 512, 200), lambda t, a: bench_w8a8(t, a, 8192, 8192, 8192, 10)],
     "gemv": [lambda t, a, w=w, m=m: bench_gemv(t, a, getattr(a, w), m, 200)
              for w in ("INT4", "INT8") for m in (1, 16, 64)],
-    "group": [lambda t, a: bench_group(t, a, 20, True), lambda t, a: bench_group(t, a, 20, False)],
-    "mx": [lambda t, a: bench_mx(t, a, 10, True), lambda t, a: bench_mx(t, a, 5, False)],
+    "group": [lambda t, a: bench_group(t, a, 20, True), lambda t, a: bench_group(t, a, 20, False),
+              lambda t, a: bench_group_sample(t, a, 20)],
+    "mx": [lambda t, a: bench_mx(t, a, 10, True), lambda t, a: bench_mx(t, a, 5, False),
+           lambda t, a: bench_mx_e1m2_sample(t, a, 10)],
     "fp8": [lambda t, a: bench_fp8(t, a, 10, True), lambda t, a: bench_fp8(t, a, 5, False),
             lambda t, a: bench_mxfp8(t, a, 10)],
 }

@@ -136,8 +136,12 @@ uint64_t ascq_pack_quant_pre(float m1, int32_t offset9, int32_t sign_flag);
  *  fp8, fp8, int4 + SetQuantScalar/Vector -> QF322S4_PRE (as REQ4 on the fp32 accumulator)
  *  fp8, fp8, int8|uint8 + SetQuantScalar/Vector -> QF322B8_PRE (as REQ8 on the fp32 accumulator)
  *  fp8, fp8, fp8_e4m3|fp8_e5m2 + SetQuantScalar/Vector -> QF322FP8_PRE (rne; e4m3 saturates at +-448, NaN -> 0)
- *  fp4_e2m1, fp4_e2m1, bf16|f32 with E8M0 scales (SetTensorScaleA/B) -> MX block-scaled (K % 128 == 0)
- *  fp8_e4m3|fp8_e5m2 (any mix), bf16|f32 with E8M0 scales -> MX-FP8 (matmul_mx.asc:90-244; K % 64 == 0)
+ *  fp4_e2m1|fp4_e1m2 (any mix), bf16|f32, f32 bias, with E8M0 scales (SetTensorScaleA/B) -> MX block-scaled
+ *                               (K % 128 == 0; fp4x2_e1m2_t operands, the high-performance MX sample
+ *                               matmul_mxfp4_high_performance/matmul_mx.h:117-133, run as exact fp6 E2M3 after a
+ *                               conversion pass into the workspace)
+ *  fp8_e4m3|fp8_e5m2 (any mix), bf16|f32, f32 bias, with E8M0 scales -> MX-FP8 (matmul_mx.asc:90-244, bias
+ *                               :99-116,199-201; K % 64 == 0)
  * int8 / fp8 A given [K, M] (isTransA) and a large [K, N] B are transposed into the workspace first.
  * ------------------------------------------------------------------------------------------ */
 typedef struct ascq_matmul_s* ascq_matmul_t;
@@ -204,7 +208,17 @@ ascq_status ascq_matmul_set_tensor_scale_b(ascq_matmul_t h, const uint8_t* scale
  * ascq_matmul_workspace_size() bytes.  Without it IterateAll allocates on first use. */
 ascq_status ascq_matmul_workspace_size(ascq_matmul_t h, size_t* bytes);
 ascq_status ascq_matmul_set_workspace(ascq_matmul_t h, void* workspace, size_t bytes);
-/* IterateAll(GlobalTensor<C>, enAtomic) (matmul.h:262; matmul_impl.h:119-137).  en_atomic must be 0. */
+/* IterateAll(GlobalTensor<C>, enAtomic) (matmul.h:255-265; matmul_impl.h:119-137).  en_atomic (ATOMIC_ADD / MAX /
+ * MIN = 1 / 2 / 3, matmul_config_utils.h:53-55; scheduler_base.h:484-494) combines the result into C instead of
+ * storing it: C = add / max / min(C, result) per element in C's type, as one atomic read-modify-write, so
+ * concurrent calls into one C compose.  int32 C: wrapping add, signed max / min; f32 / f16 / bf16 C: the exact sum
+ * rounded once (rne, overflow to inf), max / min by comparison (a NaN neither replaces nor is replaced).  For a
+ * uint8 / int4 / fp8 C the reference's SetAtomic does nothing and the result is stored; int8 C with en_atomic != 0
+ * is refused (ASCQ_E_UNSUPPORTED); en_atomic > 3 is ASCQ_E_INVALID_ARG. */
+#define ASCQ_ATOMIC_NONE 0
+#define ASCQ_ATOMIC_ADD 1
+#define ASCQ_ATOMIC_MAX 2
+#define ASCQ_ATOMIC_MIN 3
 ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic, void* stream);
 /* IterateAll that allocates nothing -- no counterpart in the reference; for callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).  Same arguments and

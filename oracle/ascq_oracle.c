@@ -1123,9 +1123,10 @@ void oq_group_matmul(void* y, int out_type, const int8_t* x, const float* pts, c
 
 static inline float mx_elem(const uint8_t* p, int64_t idx, int fmt)
 {
-    if (fmt == OQ_FP4_E2M1) {
+    if (fmt == OQ_FP4_E2M1 || fmt == OQ_FP4_E1M2) {
         uint8_t b = p[idx >> 1];
-        return oq_e2m1_decode((idx & 1) ? (uint8_t)(b >> 4) : (uint8_t)(b & 0xf));
+        const uint8_t nib = (idx & 1) ? (uint8_t)(b >> 4) : (uint8_t)(b & 0xf);
+        return (fmt == OQ_FP4_E1M2 && OQ_MUTANT != 35) ? oq_e1m2_decode(nib) : oq_e2m1_decode(nib);
     }
     return oq_fp8_decode(p[idx], fmt);
 }
@@ -1138,14 +1139,17 @@ static inline float mx_elem(const uint8_t* p, int64_t idx, int fmt)
  * A [M,K]; B [K,N] (transB: [N,K]).  sK = ceil(K/64)*2 (gen_data.py:40).
  * scale_a_layout 0: scaleA [M, sK]; 1: [sK/2, M, 2].  scale_b_layout 0: scaleB [sK/2, N, 2] (the sample's
  * layout, gen_data.py:63 and README_en.md:64-66); 1: [N, sK].
- * elem_fmt: element type of A (OQ_FP4_E2M1, OQ_FP8_E4M3, OQ_FP8_E5M2; fp8 elements are one per byte, the
- * MX-FP8 sample matmul_mx/matmul_mx.asc:90-244); B uses elem_fmt >> 8 when that is nonzero, else elem_fmt.
+ * elem_fmt: element type of A (OQ_FP4_E2M1, OQ_FP4_E1M2 -- the high-performance sample's fp4x2_e1m2_t,
+ * matmul_mxfp4_high_performance/matmul_mx.h:117-133 --, OQ_FP8_E4M3, OQ_FP8_E5M2; fp8 elements are one per byte,
+ * the MX-FP8 sample matmul_mx/matmul_mx.asc:90-244); B uses elem_fmt >> 8 when that is nonzero, else elem_fmt.
  * rows != NULL restricts the computation to the listed rows (C rows not listed are untouched).
- * C_blockmax (may be NULL): per output, the sum over 16-element K groups of the group's largest |a b|. */
+ * C_blockmax (may be NULL): per output, the sum over 16-element K groups of the group's largest |a b|.
+ * bias (may be NULL): f32 [N] added to the exact sum (the MX sample's SetBias, matmul_mx.asc:99-116,199-201);
+ * its magnitude is counted into C_absdot. */
 void oq_mx_matmul(uint16_t* C, double* C_exact, double* C_absdot, const uint8_t* A, const uint8_t* B,
                   const uint8_t* scaleA, const uint8_t* scaleB, int64_t M, int64_t N, int64_t K, int transB,
                   int scale_a_layout, int scale_b_layout, int elem_fmt, const int64_t* rows, int64_t n_rows,
-                  double* C_blockmax)
+                  double* C_blockmax, const float* bias)
 {
     int64_t sK = (K + 63) / 64 * 2;
     int64_t nr = rows ? n_rows : M;
@@ -1176,12 +1180,70 @@ void oq_mx_matmul(uint16_t* C, double* C_exact, double* C_absdot, const uint8_t*
                     bmx = 0.0;
                 }
             }
+            if (bias && OQ_MUTANT != 36) {
+                s += (double)bias[n];
+                sa_ += fabs((double)bias[n]);
+            }
             if (C_exact) C_exact[m * N + n] = s;
             if (C_absdot) C_absdot[m * N + n] = sa_;
             if (C_blockmax) C_blockmax[m * N + n] = sbm;
             if (C) C[m * N + n] = oq_f64_to_bf16(s, 1);
         }
         free(arow);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* IterateAll enAtomic                                                       */
+/* ------------------------------------------------------------------------ */
+
+/* C = op(C, v) element-wise in C's type (IterateAll(gm, enAtomic): ATOMIC_ADD / MAX / MIN = 1 / 2 / 3,
+ * impl/adv_api/detail/matmul/utils/matmul_config_utils.h:53-55; the copy-out sets SetAtomicAdd/Max/Min<DstT>,
+ * scheduler/base/scheduler_base.h:484-494, and "adds the copied data to what GM holds" --
+ * docs/zh/api/SIMD-API/basic_api/atomic_operations/SetAtomicAdd.md).  c_type: OQ_INT32 (add wraps, signed
+ * max / min), OQ_F32, OQ_F16, OQ_BF16 (add: the exact sum rounded once to C's type, rne, overflow to inf).
+ * max / min keep C unless v compares greater / smaller, so a NaN never replaces and is never replaced and a
+ * zero of the other sign does not replace a zero.  Parity unpinned: the saturation of the hardware's half /
+ * bf16 accumulation and its NaN handling are not published; this restates the IEEE behaviour. */
+static double combine_val(uint32_t bits, int t)
+{
+    if (t == OQ_F32) { float f; memcpy(&f, &bits, 4); return f; }
+    if (t == OQ_F16) return oq_f16_to_f32((uint16_t)bits);
+    return oq_bf16_to_f32((uint16_t)bits);
+}
+
+void oq_c_combine(void* c, const void* v, int c_type, int op, int64_t count)
+{
+    const int es = (c_type == OQ_INT32 || c_type == OQ_F32) ? 4 : 2;
+    for (int64_t i = 0; i < count; ++i) {
+        uint32_t a = 0, b = 0;
+        memcpy(&a, (const uint8_t*)c + i * es, es);
+        memcpy(&b, (const uint8_t*)v + i * es, es);
+        uint32_t r = a;
+        if (c_type == OQ_INT32) {
+            if (op == 1) r = a + b;
+            else if (op == 2) r = (int32_t)b > (int32_t)a ? b : a;
+            else r = (int32_t)b < (int32_t)a ? b : a;
+        } else {
+            const double x = combine_val(a, c_type), y = combine_val(b, c_type);
+            if (op == 1) {
+                const double s = x + y; /* exact: two f32 / f16 / bf16 values sum exactly in fp64 unless their
+                                           exponents differ by more than 29, where the rounding cannot change */
+                if (c_type == OQ_F32) {
+                    const float f = (float)s;
+                    memcpy(&r, &f, 4);
+                } else if (c_type == OQ_F16) {
+                    r = oq_f64_to_f16(s, 0);
+                } else {
+                    r = oq_f64_to_bf16(s, 0);
+                }
+            } else if (op == 2) {
+                r = (OQ_MUTANT == 37 ? y < x : y > x) ? b : a;
+            } else {
+                r = (OQ_MUTANT == 37 ? y > x : y < x) ? b : a;
+            }
+        }
+        memcpy((uint8_t*)c + i * es, &r, es);
     }
 }
 

@@ -162,7 +162,9 @@ void oq_group_matmul(void* y, int out_type, const int8_t* x, const float* pts, c
 void oq_mx_matmul(uint16_t* C, double* C_exact, double* C_absdot, const uint8_t* A, const uint8_t* B,
                   const uint8_t* scaleA, const uint8_t* scaleB, int64_t M, int64_t N, int64_t K, int transB,
                   int scale_a_layout, int scale_b_layout, int elem_fmt, const int64_t* rows, int64_t n_rows,
-                  double* C_blockmax);
+                  double* C_blockmax, const float* bias);
+/* IterateAll enAtomic: C = op(C, v) in C's type (op 1 add, 2 max, 3 min; c_type OQ_INT32 / F32 / F16 / BF16) */
+void oq_c_combine(void* c, const void* v, int c_type, int op, int64_t count);
 /* MX quantisation of fp32 data along K: one e8m0 per 32 elements, E2M1 elements (used to make inputs) */
 void oq_mx_quantize_fp4(uint8_t* packed, uint8_t* scales, const float* x, int64_t R, int64_t K);
 

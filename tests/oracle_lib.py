@@ -95,7 +95,8 @@ def lib() -> ctypes.CDLL:
             "oq_nz_to_nd": (None, [_P, _P, ctypes.c_int, _I64, _I64, _I64, ctypes.c_int]),
             "oq_nd_to_nz": (None, [_P, _P, ctypes.c_int, _I64, _I64, _I64]),
             "oq_mx_matmul": (None, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int,
-                                    ctypes.c_int, ctypes.c_int, _P, _I64, _P]),
+                                    ctypes.c_int, ctypes.c_int, _P, _I64, _P, _P]),
+            "oq_c_combine": (None, [_P, _P, ctypes.c_int, ctypes.c_int, _I64]),
             "oq_mx_quantize_fp4": (None, [_P, _P, _P, _I64, _I64]),
         }
         for name, (res, args) in sig.items():
@@ -393,9 +394,9 @@ def group_matmul(x, pts, w, scale, group_list, list_type, G, M, K, N, out_type=B
 
 
 def mx_matmul(A, B, sA, sB, M, N, K, trans_b=False, sa_layout=0, sb_layout=0, elem_fmt=FP4_E2M1, rows=None,
-              fmt_b=None, blockmax=False):
-    """returns (bf16 C, exact fp64 C, sum |a b|) and, with blockmax=True, the sum over 16-element K groups of
-    the group's largest |a b| as a fourth array"""
+              fmt_b=None, blockmax=False, bias=None):
+    """returns (bf16 C, exact fp64 C, sum |a b| (+ |bias|)) and, with blockmax=True, the sum over 16-element K
+    groups of the group's largest |a b| as a fourth array; bias: f32 [N] added to the sums"""
     A = np.ascontiguousarray(A, np.uint8)
     B = np.ascontiguousarray(B, np.uint8)
     sA = np.ascontiguousarray(sA, np.uint8)
@@ -405,9 +406,21 @@ def mx_matmul(A, B, sA, sB, M, N, K, trans_b=False, sa_layout=0, sb_layout=0, el
     Ca = np.zeros((M, N), np.float64)
     Cb = np.zeros((M, N), np.float64) if blockmax else None
     r = None if rows is None else np.ascontiguousarray(rows, np.int64)
+    bb = None if bias is None else np.ascontiguousarray(bias, np.float32)
     lib().oq_mx_matmul(_p(C), _p(Ce), _p(Ca), _p(A), _p(B), _p(sA), _p(sB), M, N, K, int(trans_b), sa_layout,
-                       sb_layout, elem_fmt | ((fmt_b or 0) << 8), _p(r), 0 if r is None else r.size, _p(Cb))
+                       sb_layout, elem_fmt | ((fmt_b or 0) << 8), _p(r), 0 if r is None else r.size, _p(Cb), _p(bb))
     return (C, Ce, Ca, Cb) if blockmax else (C, Ce, Ca)
+
+
+def c_combine(c, v, c_type, op):
+    """IterateAll enAtomic on the host: returns op(c, v) element-wise in C's type (op 1 add, 2 max, 3 min);
+    c / v: int32, float32, or uint16 bit patterns for F16 / BF16"""
+    dt = {INT32: np.int32, F32: np.float32, F16: np.uint16, BF16: np.uint16}[c_type]
+    out = np.ascontiguousarray(c, dt).copy()
+    vv = np.ascontiguousarray(v, dt)
+    assert out.shape == vv.shape
+    lib().oq_c_combine(_p(out), _p(vv), c_type, op, out.size)
+    return out
 
 
 def mx_quantize_fp4(x):

@@ -188,7 +188,7 @@ def test_matmul_handle_state_machine():
     _err(L.ascq_matmul_iterate_all(h, d, 0, None), ascq.E_STATE)          # no org shape
     _err(L.ascq_matmul_set_org_shape(h, 128, 256, 512), ascq.OK)
     _err(L.ascq_matmul_iterate_all(h, d, 0, None), ascq.E_STATE)          # f16 out without quant params
-    _err(L.ascq_matmul_iterate_all(h, d, 1, None), ascq.E_UNSUPPORTED)    # enAtomic
+    _err(L.ascq_matmul_iterate_all(h, d, 4, None), ascq.E_INVALID_ARG)    # enAtomic > ATOMIC_MIN
     _err(L.ascq_matmul_set_antiquant_scalar(h, 0, 0), ascq.E_UNSUPPORTED)
     _err(L.ascq_matmul_set_tensor_scale_a(h, d, 0), ascq.E_UNSUPPORTED)
     _err(L.ascq_matmul_set_single_shape(h, 256, 256, 512), ascq.OK)
@@ -205,6 +205,36 @@ def test_matmul_handle_state_machine():
     _err(L.ascq_matmul_set_tensor_scale_a(h, d, 0), ascq.OK)
     _err(L.ascq_matmul_set_tensor_scale_b(h, d, 1), ascq.OK)
     _err(L.ascq_matmul_iterate_all(h, d, 0, None), ascq.E_UNSUPPORTED)    # K % 128
+    _err(L.ascq_matmul_destroy(h), ascq.OK)
+
+
+def test_mx_e1m2_and_bias_handle():
+    """fp4x2_e1m2_t MX operands (either side, with E2M1 on the other) are accepted and need the fp6 planes of both
+    operands in the workspace; the MX bias must be f32; an int8 C refuses enAtomic before any launch"""
+    L = ascq.lib()
+    h = ctypes.c_void_p()
+    d = ctypes.c_void_p(0x1000)
+    for fa, fb in ((ascq.FP4_E1M2, ascq.FP4_E1M2), (ascq.FP4_E1M2, ascq.FP4_E2M1), (ascq.FP4_E2M1, ascq.FP4_E1M2)):
+        t = ascq._MatmulTypes(fa, fb, ascq.BF16, ascq.F32, ascq.E8M0, 0)
+        _err(L.ascq_matmul_create(ctypes.byref(t), ctypes.byref(h)), ascq.OK)
+        _err(L.ascq_matmul_set_org_shape(h, 256, 256, 256), ascq.OK)
+        _err(L.ascq_matmul_set_tensor_b(h, d, 1), ascq.OK)
+        ws = ctypes.c_size_t()
+        _err(L.ascq_matmul_workspace_size(h, ctypes.byref(ws)), ascq.OK)
+        scales = 2 * ((256 * 8 + 16 + 255) // 256 * 256)
+        p_plane, q_plane = 256 * 128, (256 // 128) * (256 // 32) * 1024
+        assert ws.value == scales + 2 * (p_plane + q_plane)
+        _err(L.ascq_matmul_destroy(h), ascq.OK)
+    for bt in (ascq.INT32, ascq.F16):
+        t = ascq._MatmulTypes(ascq.FP4_E2M1, ascq.FP4_E1M2, ascq.F32, bt, ascq.E8M0, 0)
+        _err(L.ascq_matmul_create(ctypes.byref(t), ctypes.byref(h)), ascq.E_UNSUPPORTED)
+    t = ascq._MatmulTypes(ascq.INT8, ascq.INT8, ascq.INT8, 0, 0, 0)
+    _err(L.ascq_matmul_create(ctypes.byref(t), ctypes.byref(h)), ascq.OK)
+    _err(L.ascq_matmul_set_org_shape(h, 64, 64, 64), ascq.OK)
+    _err(L.ascq_matmul_set_tensor_a(h, d, 0), ascq.OK)
+    _err(L.ascq_matmul_set_tensor_b(h, d, 0), ascq.OK)
+    _err(L.ascq_matmul_set_quant_scalar(h, 0x3F800000), ascq.OK)
+    _err(L.ascq_matmul_iterate_all(h, d, ascq.ATOMIC_ADD, None), ascq.E_UNSUPPORTED)
     _err(L.ascq_matmul_destroy(h), ascq.OK)
 
 

@@ -50,13 +50,17 @@ def scale_pairs(s_rows):
     return np.ascontiguousarray(s_rows.T.reshape(sK // 2, 2, R).transpose(0, 2, 1))
 
 
-def run_mx(ascq, A, sA, B, sB, M, N, K, trans_b, sa_t, sb_t, c_type):
-    mm = ascq.Matmul(ascq.FP4_E2M1, ascq.FP4_E2M1, c_type, 0, ascq.E8M0)
+def run_mx(ascq, A, sA, B, sB, M, N, K, trans_b, sa_t, sb_t, c_type, fa=None, fb=None, bias=None):
+    fa = ascq.FP4_E2M1 if fa is None else fa
+    fb = ascq.FP4_E2M1 if fb is None else fb
+    mm = ascq.Matmul(fa, fb, c_type, ascq.F32 if bias is not None else 0, ascq.E8M0)
     mm.SetOrgShape(M, N, K)
     mm.SetTensorA(_dev(A))
     mm.SetTensorB(_dev(B), trans_b)
     mm.SetTensorScaleA(_dev(sA), sa_t)
     mm.SetTensorScaleB(_dev(sB), sb_t)
+    if bias is not None:
+        mm.SetBias(_dev(bias))
     c = torch.empty((M, N), dtype=torch.bfloat16 if c_type == ascq.BF16 else torch.float32, device="cuda")
     mm.IterateAll(c)
     mm.End()
@@ -112,17 +116,106 @@ def test_mx_f32_out(ascq_gpu, oracle):
     assert (np.abs(got - Ce) <= d + 1e-30).all()
 
 
+def tile_rows(rng, M):
+    """two rows in every 256-row output tile (the first and last rows of the matrix among them), so a tile-order
+    mistake confined to any tile is seen; the fp64 golden of every row would take minutes on the CPU"""
+    r = [np.array([t, min(t + 255, M - 1)]) if t == 0 else t + rng.integers(0, min(256, M - t), 2)
+         for t in range(0, M, 256)]
+    return np.unique(np.concatenate(r + [np.array([M - 1])])).astype(np.int64)
+
+
 @pytest.mark.parametrize("trans_b", [True, False])
 def test_config5_full_size_sampled(ascq_gpu, oracle, trans_b):
     """A, B E2M1 [8192, 8192] from N(0,1), MX-quantised per 32-element K block, fp32 accumulate, bf16 out;
-    rows sampled across the whole output (the fp64 golden of every row would take minutes on the CPU)."""
+    two rows of every 256-row tile compared against the fp64 golden."""
     M = N = K = 8192
     rng = seeded(5)
     A, sA, Bt, sBt = mx_inputs(rng, M, N, K)
     B_dev = Bt if trans_b else to_kn(Bt, N, K)
     sB_dev = sBt if trans_b else scale_pairs(sBt)
     c = run_mx(ascq_gpu, A, sA, B_dev, sB_dev, M, N, K, trans_b, 0, 1 if trans_b else 0, ascq_gpu.BF16)
-    rows = np.unique(np.concatenate([[0, 1, 255, 256, 4095, 8191], rng.integers(0, M, 10)])).astype(np.int64)
+    rows = tile_rows(rng, M)
     C, Ce, Ca = O.mx_matmul(A, Bt, sA, sBt, M, N, K, trans_b=True, sa_layout=0, sb_layout=1, rows=rows)
     got = bf16_to_f64(c.view(torch.int16).numpy().view(np.uint16)[rows])
     check(got, Ce[rows], Ca[rows], K, C[rows])
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# fp4x2_e1m2_t operands (the fp6 E2M3 kernel) and the f32 bias
+# ---------------------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("fmts", [("e1m2", "e1m2"), ("e1m2", "e2m1"), ("e2m1", "e1m2")])
+@pytest.mark.parametrize("trans_b", [True, False])
+@pytest.mark.parametrize("shape", [(256, 256, 512), (130, 70, 384), (1030, 1026, 256), (2051, 1026, 128),
+                                   (1024, 2048, 1024)])
+def test_mx_e1m2(ascq_gpu, oracle, fmts, trans_b, shape):
+    """every fp4 code of either format, block exponents spread over +-20, both B layouts; the 256 x 128 fp6 tiles
+    (M, N >= 1024, ragged edges included) and the 64 x 64 ones"""
+    M, N, K = shape
+    rng = seeded(M + 3 * N + K + len(fmts[0]) + 5 * len(fmts[1]) + trans_b)
+    code = {"e2m1": (ascq_gpu.FP4_E2M1, O.FP4_E2M1), "e1m2": (ascq_gpu.FP4_E1M2, O.FP4_E1M2)}
+    A = rng.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    Bt = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sA = rng.integers(107, 148, (M, K // 32), dtype=np.uint8)
+    sBt = rng.integers(107, 148, (N, K // 32), dtype=np.uint8)
+    B_dev = Bt if trans_b else to_kn(Bt, N, K)
+    sB_dev = sBt if trans_b else scale_pairs(sBt)
+    c = run_mx(ascq_gpu, A, sA, B_dev, sB_dev, M, N, K, trans_b, 0, 1 if trans_b else 0, ascq_gpu.BF16,
+               fa=code[fmts[0]][0], fb=code[fmts[1]][0])
+    rows = tile_rows(rng, M) if M > 512 else None
+    C, Ce, Ca = O.mx_matmul(A, Bt, sA, sBt, M, N, K, trans_b=True, sa_layout=0, sb_layout=1,
+                            elem_fmt=code[fmts[0]][1], fmt_b=code[fmts[1]][1], rows=rows)
+    got = bf16_to_f64(c.view(torch.int16).numpy().view(np.uint16))
+    if rows is not None:
+        got, C, Ce, Ca = got[rows], C[rows], Ce[rows], Ca[rows]
+    check(got, Ce, Ca, K, C, rel=2.0 ** -8)
+
+
+@pytest.mark.parametrize("c_type", ["bf16", "f32"])
+@pytest.mark.parametrize("fa", ["e2m1", "e1m2"])
+@pytest.mark.parametrize("shape", [(128, 192, 256), (1024, 1024, 512)])
+def test_mx_bias(ascq_gpu, oracle, c_type, fa, shape):
+    """SetBias with an f32 bias on the MX matmul (matmul_mx/matmul_mx.asc:99-116,199-201), bf16 and f32 C"""
+    M, N, K = shape
+    rng = seeded(M + N + K + len(fa) + len(c_type))
+    A, sA, Bt, sBt = mx_inputs(rng, M, N, K)
+    bias = (rng.standard_normal(N) * 4).astype(np.float32)
+    code = {"e2m1": (ascq_gpu.FP4_E2M1, O.FP4_E2M1), "e1m2": (ascq_gpu.FP4_E1M2, O.FP4_E1M2)}[fa]
+    ct = ascq_gpu.BF16 if c_type == "bf16" else ascq_gpu.F32
+    c = run_mx(ascq_gpu, A, sA, Bt, sBt, M, N, K, True, 0, 1, ct, fa=code[0], bias=bias)
+    C, Ce, Ca = O.mx_matmul(A, Bt, sA, sBt, M, N, K, trans_b=True, sa_layout=0, sb_layout=1, elem_fmt=code[1],
+                            fmt_b=O.FP4_E2M1, bias=bias)
+    if c_type == "bf16":
+        check(bf16_to_f64(c.view(torch.int16).numpy().view(np.uint16)), Ce, Ca, K, C)
+    else:
+        d = (K + 1) * 2.0 ** -24 * Ca
+        assert (np.abs(c.numpy().astype(np.float64) - Ce) <= d + 1e-30).all()
+
+
+def test_e1m2_sample_full_size(ascq_gpu, oracle):
+    """The reference's high-performance MX sample (matmul_mxfp4_high_performance/scripts/gen_data.py:38-66):
+    A [8192, 8192] and B [8192, 8192] (given [K, N]) e1m2 from randint(-1, 2), scales randint(127, 130) with B's
+    as [sK/2, N, 2], bf16 out.  Every product is a power of two up to 16 and every sum an integer below 2^24, so
+    the fp32 accumulation is exact and the output must equal the bf16 golden bit for bit, on two rows of every
+    256-row tile."""
+    M = N = K = 8192
+    rng = seeded(2026)
+    a = rng.integers(-1, 2, (M, K)).astype(np.int8)
+    b = rng.integers(-1, 2, (K, N)).astype(np.int8)
+    lut = np.array([0xC, 0x0, 0x4], np.uint8)  # e1m2 codes of -1, 0, 1
+    ca, cb = lut[a + 1], lut[b + 1]
+    A = (ca[:, 0::2] | (ca[:, 1::2] << 4)).astype(np.uint8)
+    B = (cb[:, 0::2] | (cb[:, 1::2] << 4)).astype(np.uint8)
+    del ca, cb
+    sK = K // 32
+    sA = rng.integers(127, 130, (M, sK), dtype=np.uint8)
+    sB = rng.integers(127, 130, (sK, N), dtype=np.uint8)
+    sB_pairs = np.ascontiguousarray(sB.reshape(sK // 2, 2, N).transpose(0, 2, 1))
+    c = run_mx(ascq_gpu, A, sA, B, sB_pairs, M, N, K, False, 0, 0, ascq_gpu.BF16, fa=ascq_gpu.FP4_E1M2,
+               fb=ascq_gpu.FP4_E1M2)
+    rows = tile_rows(rng, M)
+    ea = (a[rows].astype(np.float64) * 2.0 ** (np.repeat(sA[rows].astype(np.float64), 32, 1) - 127))
+    eb = b.astype(np.float64) * 2.0 ** (np.repeat(sB.astype(np.float64), 32, 0) - 127)
+    exact = ea @ eb
+    got = c.view(torch.int16).numpy().view(np.uint16)[rows]
+    want = (exact.astype(np.float32).view(np.uint32) + 0x7FFF + ((exact.astype(np.float32).view(np.uint32) >> 16) & 1)) >> 16
+    np.testing.assert_array_equal(got, want.astype(np.uint16))

@@ -1448,3 +1448,135 @@ def test_antiquant_hif8_and_fp8_sources():
                             offset=oh.view(np.uint16))
     np.testing.assert_array_equal(yp, _h(_h(q + oh.astype(np.float64)).astype(np.float64) * sh.astype(np.float64))
                                   .view(np.uint16))
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# MX matmul with fp4x2_e1m2_t elements and an f32 bias
+# ---------------------------------------------------------------------------------------------------------------
+E1M2 = [k / 4 for k in range(8)]  # sign | 1-bit exponent (bias 1) | 2-bit mantissa: magnitudes k / 4
+
+
+def _fp4_table(fmt):
+    mags = E1M2 if fmt == O.FP4_E1M2 else E2M1
+    return np.array([mags[c & 7] * (-1 if c & 8 else 1) for c in range(16)])
+
+
+@pytest.mark.parametrize("fa,fb", [(O.FP4_E1M2, O.FP4_E1M2), (O.FP4_E1M2, O.FP4_E2M1), (O.FP4_E2M1, O.FP4_E1M2)])
+def test_mx_matmul_e1m2_vs_numpy_decode(fa, fb):
+    """the reference golden of the E1M2 sample (matmul_mxfp4_high_performance/scripts/gen_data.py:47-61): each
+    element times 2^(scale - 127) of its 32-element K block, fp64 matmul; here against an independent numpy
+    decode of the format tables, every code and a spread of block scales"""
+    M, N, K = 8, 12, 256
+    A = rng0.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    Bt = rng0.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sA = rng0.integers(110, 140, (M, K // 32), dtype=np.uint8)
+    sB = rng0.integers(110, 140, (N, K // 32), dtype=np.uint8)
+
+    def dec(p, s, fmt):
+        v = _fp4_table(fmt)[np.stack([p & 0xF, p >> 4], -1).reshape(p.shape[0], -1)]
+        return v * 2.0 ** (np.repeat(s.astype(np.float64), 32, axis=1) - 127)
+
+    exact = dec(A, sA, fa) @ dec(Bt, sB, fb).T
+    _, Ce, _ = O.mx_matmul(A, Bt, sA, sB, M, N, K, trans_b=True, sa_layout=0, sb_layout=1, elem_fmt=fa, fmt_b=fb)
+    assert np.allclose(Ce, exact, rtol=1e-13, atol=1e-13)
+
+
+def test_mx_matmul_e1m2_sample_data():
+    """the sample's own data classes: elements randint(-1, 2) cast to e1m2 (codes for -1, 0, 1), scales
+    randint(127, 130), B given [K, N] with scales [sK/2, N, 2]; the exact sums are integers times powers of two,
+    so the bf16 golden of each is its rne cast"""
+    M, N, K = 16, 24, 256
+    a = rng0.integers(-1, 2, (M, K))
+    b = rng0.integers(-1, 2, (K, N))
+    code = {-1: 0xC, 0: 0x0, 1: 0x4}  # e1m2: 1.0 = exponent 1, mantissa 0
+    ca = np.vectorize(code.get)(a).astype(np.uint8)
+    cb = np.vectorize(code.get)(b).astype(np.uint8)
+    A = (ca[:, 0::2] | (ca[:, 1::2] << 4)).astype(np.uint8)
+    B = (cb[:, 0::2] | (cb[:, 1::2] << 4)).astype(np.uint8)  # [K, N/2], two per byte along N
+    sK = K // 32
+    sA = rng0.integers(127, 130, (M, sK), dtype=np.uint8)
+    sB = rng0.integers(127, 130, (sK, N), dtype=np.uint8)
+    sB_pairs = np.ascontiguousarray(sB.reshape(sK // 2, 2, N).transpose(0, 2, 1))
+    exact = (a * 2.0 ** (np.repeat(sA.astype(np.float64), 32, 1) - 127)) @ (
+        b * 2.0 ** (np.repeat(sB.astype(np.float64), 32, 0) - 127))
+    C, Ce, _ = O.mx_matmul(A, B, sA, sB_pairs, M, N, K, trans_b=False, sa_layout=0, sb_layout=0,
+                           elem_fmt=O.FP4_E1M2)
+    assert np.array_equal(Ce, exact)
+    assert np.array_equal(C, _bf16_bits(exact.astype(np.float32)))
+
+
+def test_mx_matmul_bias():
+    """SetBias on the MX matmul (matmul_mx/matmul_mx.asc:99-116,199-201): an f32 [N] bias joins the sum before the
+    output cast, and its magnitude the absolute sum"""
+    M, N, K = 4, 8, 128
+    A = rng0.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    Bt = rng0.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sA = np.full((M, K // 32), 127, np.uint8)
+    sB = np.full((N, K // 32), 127, np.uint8)
+    bias = rng0.standard_normal(N).astype(np.float32)
+    _, Ce0, Ca0 = O.mx_matmul(A, Bt, sA, sB, M, N, K, trans_b=True, sa_layout=0, sb_layout=1)
+    C, Ce, Ca = O.mx_matmul(A, Bt, sA, sB, M, N, K, trans_b=True, sa_layout=0, sb_layout=1, bias=bias)
+    assert np.array_equal(Ce, Ce0 + bias.astype(np.float64))
+    assert np.array_equal(Ca, Ca0 + np.abs(bias.astype(np.float64)))
+    assert np.array_equal(C, _bf16_bits(Ce.astype(np.float32))) or np.abs(
+        _bf16_vals(C) - Ce).max() <= np.abs(Ce).max() * 2.0 ** -8
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# IterateAll enAtomic: C = add / max / min (C, result) in C's type
+# ---------------------------------------------------------------------------------------------------------------
+def test_combine_int32():
+    """int32 C: wrapping add (two's complement, as the int32 accumulators wrap), signed max / min"""
+    c = rng0.integers(-2**31, 2**31, 4096).astype(np.int32)
+    v = rng0.integers(-2**31, 2**31, 4096).astype(np.int32)
+    add = ((c.astype(np.int64) + v) & 0xFFFFFFFF).astype(np.uint32).view(np.int32)
+    assert np.array_equal(O.c_combine(c, v, O.INT32, 1), add)
+    assert np.array_equal(O.c_combine(c, v, O.INT32, 2), np.maximum(c, v))
+    assert np.array_equal(O.c_combine(c, v, O.INT32, 3), np.minimum(c, v))
+
+
+def test_combine_float_add_known_answers():
+    """single rounding to nearest even in C's type, overflow to inf (the IEEE sum)"""
+    f32 = O.c_combine(np.array([1.0, 1.0, 3e38], np.float32), np.array([2.0 ** -24, 3 * 2.0 ** -24, 3e38], np.float32),
+                      O.F32, 1)
+    assert f32[0] == 1.0 and f32[1] == np.float32(1.0 + 2.0 ** -22) and np.isinf(f32[2])
+    h = lambda xs: np.array(xs, np.float16).view(np.uint16)
+    # 2048 + 1 = 2049: a tie between 2048 and 2050, even -> 2048; 2048 + 3 -> 2052; 65504 + 16 = 65520: a tie
+    # between 65504 (odd) and 65536 -> inf; 1 + 2^-11 (a tie) -> 1; subnormal sum exact
+    got = O.c_combine(h([2048, 2048, 65504, 1.0, 2.0 ** -24]), h([1, 3, 16, 2.0 ** -11, 2.0 ** -23]), O.F16, 1)
+    assert np.array_equal(got.view(np.float16), np.array([2048, 2052, np.inf, 1.0, 3 * 2.0 ** -24], np.float16))
+    # bf16: 1 + 2^-8 is a tie -> 1; 1 + 3 * 2^-8 -> 1 + 2^-6 (tie to even); 1.5 * 2^127 + 2^127 -> inf
+    b = lambda xs: _bf16_bits(np.array(xs, np.float32))
+    got = O.c_combine(b([1.0, 1.0, 1.5 * 2.0 ** 127]), b([2.0 ** -8, 3 * 2.0 ** -8, 2.0 ** 127]), O.BF16, 1)
+    assert np.array_equal(_bf16_vals(got), np.array([1.0, 1.0 + 2.0 ** -6, np.inf]))
+
+
+def test_combine_half_add_matches_torch():
+    """random f16 / bf16 pairs over the whole finite range against torch's CPU add (fp32 sum, rne cast): the
+    fp32 intermediate of p' = 24 >= 2p + 1 bits makes that the correctly rounded sum"""
+    import torch
+    for ct, tdt in ((O.F16, torch.float16), (O.BF16, torch.bfloat16)):
+        bits = rng0.integers(0, 65536, (2, 20000)).astype(np.uint16)
+        t = torch.from_numpy(bits.view(np.int16)).view(tdt)
+        ok = torch.isfinite(t).all(0)
+        a, v = t[0][ok], t[1][ok]
+        want = (a + v).view(torch.int16).numpy().view(np.uint16)
+        got = O.c_combine(a.view(torch.int16).numpy().view(np.uint16), v.view(torch.int16).numpy().view(np.uint16),
+                          ct, 1)
+        nan = torch.isnan(a + v).numpy()
+        assert np.array_equal(got[~nan], want[~nan])
+
+
+def test_combine_max_min_special_values():
+    """max / min replace C only when the new value compares greater / smaller: a NaN never replaces and is never
+    replaced, -0 does not replace +0 (nor the reverse)"""
+    c = np.array([1.0, np.nan, 0.0, -0.0, -3.0, 2.0], np.float32)
+    v = np.array([2.0, 5.0, -0.0, 0.0, np.nan, -7.0], np.float32)
+    mx = O.c_combine(c, v, O.F32, 2)
+    mn = O.c_combine(c, v, O.F32, 3)
+    assert np.array_equal(mx.view(np.uint32), np.array([2.0, np.nan, 0.0, -0.0, -3.0, 2.0], np.float32).view(np.uint32))
+    assert np.array_equal(mn.view(np.uint32), np.array([1.0, np.nan, 0.0, -0.0, -3.0, -7.0], np.float32).view(np.uint32))
+    h16 = np.array([1.0, -2.0, 3.0], np.float16).view(np.uint16)
+    w16 = np.array([0.5, -1.0, 3.0], np.float16).view(np.uint16)
+    assert np.array_equal(O.c_combine(h16, w16, O.F16, 2).view(np.float16), np.array([1.0, -1.0, 3.0], np.float16))
+    assert np.array_equal(O.c_combine(h16, w16, O.F16, 3).view(np.float16), np.array([0.5, -2.0, 3.0], np.float16))

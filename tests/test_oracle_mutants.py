@@ -7,7 +7,7 @@ double-rounded multiplier, a wrong E2M1 code, a ties-away f16 cast, an unrounded
 dequant indexed by row, a requant offset added before the clamp, a ties-away fp8 cast, an ignored requant
 sign flag, a FasterGelu with the wrong sign, and policy-form quant mistakes (arithmetic type, bf16 step, group
 axis, offset rounding, directed E2M1 modes) and dequant layout mistakes (int32 rounding, the single-row
-reshape, padded dst rows, group axis) and HiFloat8 / arch-3510 legacy quant mistakes.  Each mutant is compiled on the CPU into a temporary library and the pinning tests of
+reshape, padded dst rows, group axis) and HiFloat8 / arch-3510 legacy quant mistakes, MX E1M2 / bias and enAtomic mistakes.  Each mutant is compiled on the CPU into a temporary library and the pinning tests of
 tests/test_oracle.py are run against it; every mutant must fail at least one of them.
 """
 from __future__ import annotations
@@ -57,6 +57,9 @@ MUTANTS = {
     32: "legacy quant to fp8 computed in half arithmetic instead of fp32",
     33: "HiFloat8 ties rounded toward zero instead of away",
     34: "HiFloat8 decoder reads the 1-bit exponent field's sign inverted",
+    35: "MX E1M2 elements decoded as E2M1",
+    36: "MX bias dropped",
+    37: "enAtomic max / min swapped",
 }
 
 
