@@ -48,12 +48,13 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)bits_h(h
 // fp32 -> bf16, rne, saturating (overflow and inf -> +-max finite, NaN quieted)
 __device__ __forceinline__ uint16_t f32_to_bf16_sat(float x)
 {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-    uint32_t r = u + 0x7fffu + ((u >> 16) & 1u);
-    uint16_t b = (uint16_t)(r >> 16);
-    if ((b & 0x7fffu) == 0x7f80u) b = (uint16_t)((b & 0x8000u) | 0x7f7fu);
-    return b;
+    // the hardware rne conversion (v_cvt_pk_bf16_f32: equal to the bit-level rne on all 2^32 inputs but NaN,
+    // checked exhaustively on gfx950), then selects instead of branches: an overflow to inf saturates to +-max
+    // finite (0x7F7F), a NaN keeps its sign and top payload bits, quieted
+    const uint32_t u = __float_as_uint(x);
+    uint32_t b = __builtin_bit_cast(uint16_t, (__bf16)x);
+    b = (b & 0x7fffu) == 0x7f80u ? ((b & 0x8000u) | 0x7f7fu) : b;
+    return (u & 0x7fffffffu) > 0x7f800000u ? (uint16_t)((u >> 16) | 0x40u) : (uint16_t)b;
 }
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 // fp32 -> bf16 value (kept in an fp32 register): rne, overflow to inf, NaN kept
@@ -67,9 +68,19 @@ __device__ __forceinline__ float bf16_round(float x)  // rne to bf16, overflow t
 // QUANT_PRE word -> M1 multiplier: bits [31:13] as fp32, low 13 bits cleared
 __device__ __forceinline__ float quant_pre_m1(uint64_t w) { return __uint_as_float((uint32_t)w & 0xFFFFE000u); }
 
-// FasterGelu, x / (1 + exp(-1.702 x)) in fp32 (impl/adv_api/detail/activation/gelu/gelu_3510_impl.h:113-122):
-// for x -> -inf the exp overflows to inf and the result is -0, as there
-__device__ __forceinline__ float faster_gelu(float x) { return x / (1.0f + expf(-1.702f * x)); }
+// FasterGelu, x / (1 + exp(-1.702 x)) in fp32 (impl/adv_api/detail/activation/gelu/gelu_3510_impl.h:113-122).
+// While -1.702 x < 64 (1 + exp < 2^93, a normal reciprocal) with the hardware exp2 (v_exp_f32 of -1.702 x
+// log2(e)) and reciprocal (v_rcp_f32): both accurate to about an fp32 ulp, so the result is within ~|2.5 x| fp32
+// ulps of the correctly rounded expression -- far below one f16 / bf16 output ulp -- at a quarter of the cost
+// of expf and an IEEE division.  Beyond (x < -37.6, results below ~1e-26 that bf16 still represents, down to
+// its subnormals) and for NaN: expf and the IEEE division; for x -> -inf the exp overflows to inf and the
+// result is -0, as there.
+__device__ __forceinline__ float faster_gelu(float x)
+{
+    const float t = -1.702f * x;
+    if (t < 64.0f) return x * __builtin_amdgcn_rcpf(1.0f + __expf(t));
+    return x / (1.0f + expf(t));
+}
 
 // (V)REQ8 / (V)QF322B8_PRE after the multiply by M1 (examples/02_simd_c_api/03_c_api/03_matrix_compute/
 // asc_copy_l0c2gm/scripts/gen_data_s322s8.py:56-80): NaN -> 0, clamp to [-256, 255], round half to even, add

@@ -510,6 +510,60 @@ struct GemmCore {
     }
 };
 
+// Coalesced epilogue store of a GemmCore tile (T): the output bits val(i, j, r) of every accumulator element
+// (ES = 2 or 4 bytes per C element) are written to LDS -- free once every wave has left the main loop -- and
+// leave as whole 16-byte row pieces (buffer_store_dwordx4) instead of one 2- or 4-byte store per element: the
+// element stores of a 128 x 256 f16 tile measured slower than its K = 1024 main loop.  LDS rows hold TBN * ES
+// bytes, 16-byte pieces XOR-swizzled by (row % 8), so the two rows of one ds_write (lanes 0-31, 32-63) and the
+// 16 lanes of one ds_read fall in distinct banks.  A tile larger than the LDS goes in chunks of whole wave rows
+// (the waves whose rows lie in chunk ch write it).  The caller guarantees 16-byte aligned output rows and
+// cols % (16 / ES) == 0 (no piece straddles the last column); rows past `rows` and pieces past `cols` are not
+// stored (with a row pitch of N elements the latter would land in the next row).
+template <class T, int ES, class F>
+__device__ __forceinline__ void store_tile_lds(uint8_t* smem, const TileOut& out, int rows, int cols, F val)
+{
+    constexpr int RBY = T::TBN * ES;  // LDS bytes per tile row
+    constexpr int PR = RBY / 16;      // 16-byte pieces per row
+    constexpr int NCH = (size_t)T::TBM * RBY <= T::LDS_BYTES ? 1 : (size_t)T::TBM * RBY <= 2 * T::LDS_BYTES ? 2 : 4;
+    constexpr int CHR = T::TBM / NCH;  // rows per chunk
+    constexpr int ITER = CHR * PR / T::NT;
+    static_assert((ES == 2 || ES == 4) && PR >= 8 && (size_t)CHR * RBY <= T::LDS_BYTES && CHR % T::WTM == 0 &&
+                      (CHR * PR) % T::NT == 0, "coalesced epilogue shape");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / T::TWN, wn = wave % T::TWN;
+    const int my_chunk = wm * T::WTM / CHR;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+        __syncthreads();  // the main loop's last LDS reads (or the previous chunk's) are done
+        if (my_chunk == ch) {
+#pragma unroll
+            for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+                for (int j = 0; j < T::FN; ++j) {
+                    const int cb = T::frag_col(wn, j, lane) * ES;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = T::frag_row(wm, i, r, lane) - ch * CHR;
+                        uint8_t* d = smem + row * RBY + (((cb >> 4) ^ (row & 7)) << 4) + (cb & 15);
+                        const uint32_t v = val(i, j, r);
+                        if constexpr (ES == 4) *(uint32_t*)d = v;
+                        else *(uint16_t*)d = (uint16_t)v;
+                    }
+                }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < ITER; ++it) {
+            const int k = it * T::NT + threadIdx.x;
+            const int row = k / PR, pc = k % PR;
+            const u32x4 v = *(const u32x4*)(smem + row * RBY + ((pc ^ (row & 7)) << 4));
+            const int grow = ch * CHR + row;
+            const bool ok = grow < rows && pc * (16 / ES) < cols;
+            __builtin_amdgcn_raw_buffer_store_b128(v, out.r, ok ? (uint32_t)grow * out.pitch + (uint32_t)(pc * 16) : OOB, 0, 0);
+        }
+    }
+}
+
 // the 32 bits of one accumulator element (a value copy: __builtin_bit_cast of a vector-element lvalue reads the
 // vector's first element under this compiler)
 __device__ __forceinline__ uint32_t acc_bits(float x) { return __float_as_uint(x); }

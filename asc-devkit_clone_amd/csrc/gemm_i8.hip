@@ -16,6 +16,14 @@
 
 namespace ascq {
 
+// a value every lane of the wave holds alike, moved to scalar registers
+__device__ __forceinline__ int64_t uniform64(int64_t v)
+{
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
 {
@@ -120,96 +128,165 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
 // W[g].  The real tiles are ordered group-major, then n-tile, then m-tile within the group, and the order is cut
 // into 8 contiguous ranges, one per XCD (workgroup ids go round-robin over the XCDs): an XCD then works on one
 // or two experts' column ranges, so its L2 holds the weight columns it streams instead of every XCD fetching
-// every expert's weights.  Ids past the real tile count exit at once (the grid is sized for ceil(M/BM) + G
-// m-tiles); m-tiles never straddle a group.
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64>
-__global__ __launch_bounds__(WM * WN * 64) void group_gemm_i8_kernel(GroupGemmArgs p)
+// every expert's weights.  m-tiles never straddle a group.  The grid is sized for ceil(M / BM) + G m-tiles per
+// n-tile; ids past the real tile count exit at once.
+constexpr int GROUP_MAX = 1024;  // groups the tiled kernel takes (the host refuses more)
+
+// exclusive prefix sum over the workgroup of one value per thread (NT threads); *total gets the full sum
+template <int NT>
+__device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* wtot, int64_t* total)
+{
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int64_t x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int64_t y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) wtot[w] = x;
+    __syncthreads();
+    int64_t base = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i) {
+        if (i < w) base += wtot[i];
+        tot += wtot[i];
+    }
+    __syncthreads();  // wtot may be reused
+    *total = tot;
+    return base + x - v;
+}
+
+// WPE: waves per SIMD the register allocation must allow (2 for two 4-wave workgroups per CU)
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1>
+__global__ __launch_bounds__(WM * WN * 64, WPE) void group_gemm_i8_kernel(GroupGemmArgs p)
 {
     using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ int64_t g_start[65], g_tile[65], g_list[65];
+    __shared__ int64_t wtot[T::NT / 64];
+    __shared__ int64_t tile_info[4];  // group, first row, end row, first m-tile of this workgroup's tile
+    // the tile's per-token (BM) and per-channel (BN) scales, copied global -> LDS by one wave-wide copy each
+    // (1 KiB: lanes past the scales read zeros)
+    static_assert(BM <= 256 && BN <= 256, "one 1 KiB copy per scale vector");
+    __shared__ __attribute__((aligned(16))) float s_pt[256], s_sc[256];
     const int G = (int)p.G;
-    // the group list is read by G + 1 lanes at once (a serial walk would put G dependent loads in front of
-    // every workgroup), then prefix-summed from LDS
-    const int nl = p.list_type == 0 ? G + 1 : G;
-    if ((int)threadIdx.x < nl) g_list[threadIdx.x] = p.group_list[threadIdx.x];
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int64_t s = p.list_type == 0 ? g_list[0] : 0, tiles = 0;
-        for (int g = 0; g < G; ++g) {
-            int64_t cnt = p.list_type == 0 ? g_list[g + 1] - g_list[g] : g_list[g];
-            if (cnt < 0) cnt = 0;
-            g_start[g] = s;
-            g_tile[g] = tiles;
-            s += cnt;
-            tiles += (cnt + BM - 1) / BM;
-        }
-        g_start[G] = s;
-        g_tile[G] = tiles;
+    const int64_t M = p.M;
+    // Group g's rows are [start_g, end_g) clamped to [0, M) (rows outside [0, M) exist in no group) and its
+    // m-tiles follow those of groups 0 .. g-1.  Thread t owns groups [t * per, (t + 1) * per): two block-wide
+    // prefix sums (rows, then m-tiles) give every thread its groups' starts, and the thread owning this
+    // workgroup's tile publishes it -- no G-sized table, so the LDS stays with the stage ring.
+    const int per = (G + T::NT - 1) / T::NT, ga = (int)threadIdx.x * per;
+    auto count = [&](int g) {
+        const int64_t c = p.list_type == 0 ? p.group_list[g + 1] - p.group_list[g] : p.group_list[g];
+        return c < 0 ? (int64_t)0 : c;
+    };
+    auto clampM = [&](int64_t v) { return v < 0 ? (int64_t)0 : (v > M ? M : v); };
+    const int64_t base = p.list_type == 0 ? p.group_list[0] : 0;
+    int64_t rows_total, tiles_total, mine = 0;
+    for (int k = 0; k < per; ++k)
+        if (ga + k < G) mine += count(ga + k);
+    const int64_t s0 = base + block_exclusive_scan<T::NT>(mine, wtot, &rows_total);
+    mine = 0;
+    {
+        int64_t st = s0;
+        for (int k = 0; k < per; ++k)
+            if (ga + k < G) {
+                const int64_t c = count(ga + k);
+                mine += (clampM(st + c) - clampM(st) + BM - 1) / BM;
+                st += c;
+            }
     }
-    __syncthreads();
     const int64_t tiles_n = (p.N + BN - 1) / BN;
-    const int64_t total = g_tile[G] * tiles_n;   // real (m-tile, n-tile) pairs
+    const int64_t t0 = block_exclusive_scan<T::NT>(mine, wtot, &tiles_total);
+    const int64_t total = tiles_total * tiles_n;  // real (m-tile, n-tile) pairs
     const int64_t per_xcd = (total + 7) / 8;
-    const int64_t lin = (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-    if ((int64_t)(blockIdx.x / 8) >= per_xcd || lin >= total) return;
-    int g = 0;
-    while (g + 1 < G && g_tile[g + 1] * tiles_n <= lin) ++g;
-    const int64_t mt_g = g_tile[g + 1] - g_tile[g];  // m-tiles of group g (>= 1 here)
-    const int64_t rem = lin - g_tile[g] * tiles_n;
-    const int tn = (int)(rem / mt_g);
-    const int64_t m0 = g_start[g] + (rem % mt_g) * BM;
-    int64_t m_end = g_start[g + 1];
-    if (m_end > p.M) m_end = p.M;
-    if (m0 < 0 || m0 >= m_end) return;  // offsets come from device memory: never form a row outside [0, M)
-    const int64_t n0 = (int64_t)tn * BN;
-    CoreArgs c{};
-    c.a = make_rsrc(p.X, (uint32_t)(p.M * p.K));
-    c.b = make_rsrc(p.W + (int64_t)g * p.K * p.N, (uint32_t)(p.K * p.N));
-    c.lda = (uint32_t)p.K;
-    c.ldb = (uint32_t)(TB ? p.K : p.N);
-    c.rows = (int32_t)(m_end - m0 < BM ? m_end - m0 : BM);
-    c.cols = (int32_t)(p.N - n0 < BN ? p.N - n0 : BN);
-    c.a0 = (uint32_t)(m0 * p.K);
-    c.b0 = (uint32_t)(TB ? n0 * p.K : n0);
-    c.kbytes = p.K;
-    typename T::acc_t acc[T::FM][T::FN];
-    T::run(c, smem, acc);
-
-    // epilogue (quant_group_matmul_custom.asc:424-452): AscendDequant acc*scale[g,n] in fp32, Mul by the
-    // per-token scale in fp32, optional FasterGelu in fp32, one rounding cast to the output type.
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
-    // stores through a buffer resource over the output tile: rows past the group's end are out of its range
-    const TileOut out = tile_out(p.Y, m0, n0, p.N, c.rows, c.cols, 2);
-    const rsrc_t rp = make_rsrc(p.pts + m0, (uint32_t)(c.rows * 4));
-    float pt[T::FM][16];  // per-token scales of this lane's rows (rows past the group read 0 and are not stored)
-#pragma unroll
-    for (int i = 0; i < T::FM; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-            pt[i][r] = __uint_as_float(bload4(rp, (uint32_t)T::frag_row(wm, i, r, lane) * 4));
-    auto store = [&](auto cvt) {
-#pragma unroll
-        for (int j = 0; j < T::FN; ++j) {
-            const int cl = T::frag_col(wn, j, lane);
-            const bool cok = cl < c.cols;
-            const float sc = cok ? p.scale[(int64_t)g * p.N + n0 + cl] : 0.0f;
-            const uint32_t cbase = cok ? (uint32_t)(cl * 2) : OOB;
-#pragma unroll
-            for (int i = 0; i < T::FM; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float v = (float)acc[i][j][r] * sc;
-                    v = v * pt[i][r];
-                    if (p.act) v = faster_gelu(v);
-                    __builtin_amdgcn_raw_buffer_store_b16(cvt(v), out.r, cbase + (uint32_t)T::frag_row(wm, i, r, lane) * out.pitch,
-                                                          0, 0);
+    {
+        const int64_t lin = (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+        if ((int64_t)(blockIdx.x / 8) >= per_xcd || lin >= total) return;
+        int64_t st = s0, tf = t0;
+        for (int k = 0; k < per; ++k)
+            if (ga + k < G) {
+                const int64_t c = count(ga + k), a0 = clampM(st), a1 = clampM(st + c);
+                const int64_t nt = (a1 - a0 + BM - 1) / BM;
+                if (nt > 0 && tf * tiles_n <= lin && lin < (tf + nt) * tiles_n) {
+                    tile_info[0] = ga + k;
+                    tile_info[1] = a0;
+                    tile_info[2] = a1;
+                    tile_info[3] = tf;
                 }
+                st += c;
+                tf += nt;
+            }
+        __syncthreads();
+        // every lane reads the same values; readfirstlane keeps them (and the buffer resources built from them)
+        // in scalar registers -- a resource in VGPRs costs a waterfall loop around every access
+        const int g = __builtin_amdgcn_readfirstlane((int)tile_info[0]);
+        const int64_t g_first = uniform64(tile_info[1]), m_end = uniform64(tile_info[2]);
+        const int64_t g_tile0 = uniform64(tile_info[3]);
+        const int64_t mt_g = (m_end - g_first + BM - 1) / BM;  // m-tiles of group g (>= 1 here)
+        const int64_t rem = lin - g_tile0 * tiles_n;
+        const int tn = __builtin_amdgcn_readfirstlane((int)(rem / mt_g));
+        const int64_t m0 = uniform64(g_first + (rem % mt_g) * BM);
+        const int64_t n0 = (int64_t)tn * BN;
+        CoreArgs c{};
+        c.a = make_rsrc(p.X, (uint32_t)(p.M * p.K));
+        c.b = make_rsrc(p.W + (int64_t)g * p.K * p.N, (uint32_t)(p.K * p.N));
+        c.lda = (uint32_t)p.K;
+        c.ldb = (uint32_t)(TB ? p.K : p.N);
+        c.rows = (int32_t)(m_end - m0 < BM ? m_end - m0 : BM);
+        c.cols = (int32_t)(p.N - n0 < BN ? p.N - n0 : BN);
+        c.a0 = (uint32_t)(m0 * p.K);
+        c.b0 = (uint32_t)(TB ? n0 * p.K : n0);
+        c.kbytes = p.K;
+
+        // the epilogue's scales go global -> LDS now (waves 0 and 1, one copy each, no registers held), so their
+        // latency hides under the main loop: the copies are older than the main loop's, whose first wait covers
+        // them, and its first barrier publishes them.  Rows past the group and columns past N read 0.
+        if (wave == 0)
+            copy16_to_lds(make_rsrc(p.pts + m0, (uint32_t)(c.rows * 4)), (uint8_t*)s_pt, (uint32_t)lane * 16);
+        else if (wave == 1)
+            copy16_to_lds(make_rsrc(p.scale + (int64_t)g * p.N + n0, (uint32_t)(c.cols * 4)), (uint8_t*)s_sc,
+                          (uint32_t)lane * 16);
+        typename T::acc_t acc[T::FM][T::FN];
+        T::run(c, smem, acc);
+
+        // epilogue (quant_group_matmul_custom.asc:424-452): AscendDequant acc*scale[g,n] in fp32, Mul by the
+        // per-token scale in fp32, optional FasterGelu in fp32, one rounding cast to the output type.  Stores go
+        // through a buffer resource over the output tile: rows past the group's end are out of its range.
+        const TileOut out = tile_out(p.Y, m0, n0, p.N, c.rows, c.cols, 2);
+        auto value = [&](int i, int j, int r) {
+            float v = (float)acc[i][j][r] * s_sc[T::frag_col(wn, j, lane)];
+            v = v * s_pt[T::frag_row(wm, i, r, lane)];
+            return p.act ? faster_gelu(v) : v;
+        };
+        // whole 16-byte row pieces through LDS when the rows allow it (N a multiple of 8, Y 16-byte aligned),
+        // else one 2-byte store per element
+        if (p.N % 8 == 0 && ((uintptr_t)p.Y & 15) == 0) {
+            if (p.out_type == DT_F16)
+                store_tile_lds<T, 2>(smem, out, c.rows, c.cols,
+                                     [&](int i, int j, int r) { return (uint32_t)f32_to_f16_sat(value(i, j, r)); });
+            else
+                store_tile_lds<T, 2>(smem, out, c.rows, c.cols,
+                                     [&](int i, int j, int r) { return (uint32_t)f32_to_bf16_sat(value(i, j, r)); });
+            return;
         }
-    };
-    if (p.out_type == DT_F16) store([](float v) { return f32_to_f16_sat(v); });
-    else store([](float v) { return f32_to_bf16_sat(v); });
+        auto store = [&](auto cvt) {
+#pragma unroll
+            for (int j = 0; j < T::FN; ++j) {
+                const int cl = T::frag_col(wn, j, lane);
+                const uint32_t cbase = cl < c.cols ? (uint32_t)(cl * 2) : OOB;
+#pragma unroll
+                for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        __builtin_amdgcn_raw_buffer_store_b16(cvt(value(i, j, r)), out.r,
+                                                              cbase + (uint32_t)T::frag_row(wm, i, r, lane) * out.pitch, 0, 0);
+            }
+        };
+        if (p.out_type == DT_F16) store([](float v) { return f32_to_f16_sat(v); });
+        else store([](float v) { return f32_to_bf16_sat(v); });
+    }
 }
 
 // Any shape / layout / alignment: one thread per output element, int32 accumulate, same epilogue.
@@ -316,29 +393,32 @@ __global__ __launch_bounds__(256) void group_gemm_generic_kernel(GroupGemmArgs p
     }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1>
 static hipError_t launch_group_tiled(const GroupGemmArgs& a, hipStream_t st)
 {
     using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB>;
-    const int64_t slots = (((a.M + BM - 1) / BM + a.G) * ((a.N + BN - 1) / BN) + 7) / 8 * 8;
-    const hipError_t e = ensure_dynamic_lds<group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>>((int)T::LDS_BYTES);
+    const int64_t upper = ((a.M + BM - 1) / BM + a.G) * ((a.N + BN - 1) / BN);  // tiles, at most
+    const hipError_t e = ensure_dynamic_lds<group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, WPE>>((int)T::LDS_BYTES);
     if (e != hipSuccess) return e;
-    launch_k((group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>), dim3((unsigned)slots), dim3(T::NT), T::LDS_BYTES,
-                       st, a);
+    launch_k((group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, WPE>), dim3((unsigned)((upper + 7) / 8 * 8)), dim3(T::NT),
+             T::LDS_BYTES, st, a);
     return hipGetLastError();
 }
 
 hipError_t launch_group_gemm(const GroupGemmArgs& a, hipStream_t st)
 {
     const bool ok = a.K % 16 == 0 && ((uintptr_t)a.X % 16 == 0) &&
-                    (a.w_trans ? ((uintptr_t)a.W % 16 == 0) : (a.N % 4 == 0 && (uintptr_t)a.W % 4 == 0)) && a.G <= 64 &&
-                    a.M * a.K < (1ll << 31) && a.K * a.N < (1ll << 31);
+                    (a.w_trans ? ((uintptr_t)a.W % 16 == 0) : (a.N % 4 == 0 && (uintptr_t)a.W % 4 == 0)) &&
+                    a.G <= GROUP_MAX && a.M * a.K < (1ll << 31) && a.K * a.N < (1ll << 31) && a.N < (1ll << 21);
     if (ok) {
-        // 128 x 256 tiles on 8 waves: the MoE shape (4096 tokens, 16 experts, N = 1408) needs ~250 tiles, one
-        // per CU; 128-byte stages give each wave 16 MFMAs per barrier, three stages keep two in flight
+        // 128 x 256 tiles.  Short K (the reference sample's K = 1024): 4 waves with 64 x 128 wave tiles and
+        // 64-byte stages, two workgroups per CU, so one's epilogue and its store / load latencies overlap the
+        // other's MFMAs (measured 110-120 us against 145-150 us for one 8-wave workgroup per CU).  Long K (the
+        // MoE shape, 4096 tokens, 16 experts, K = 4096, N = 1408: ~250 tiles, one per CU): 8 waves, 128-byte
+        // stages (16 MFMAs per wave per barrier), three stages keep two in flight.
+        if (a.w_trans && a.K <= 2048) return launch_group_tiled<128, 256, 2, 2, 3, true, 64, 2>(a, st);
         if (a.w_trans && a.K % 128 == 0) return launch_group_tiled<128, 256, 2, 4, 3, true, 128>(a, st);
         if (a.w_trans) return launch_group_tiled<128, 256, 2, 4, 6, true>(a, st);
-        if (a.w_trans) return launch_group_tiled<128, 128, 2, 2, 4, true>(a, st);
         return launch_group_tiled<128, 128, 2, 2, 4, false>(a, st);
     }
     int64_t blocks = (a.M * a.N + 255) / 256;

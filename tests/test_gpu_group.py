@@ -116,3 +116,30 @@ def test_group_matmul_gelu_sample_golden(ascq_gpu, oracle):
     out = y.cpu().numpy().astype(np.float64)
     bad = ~np.isclose(out, f["golden"].astype(np.float64), rtol=1e-3, atol=1e-3)
     assert bad.mean() <= 1e-4
+
+
+@pytest.mark.parametrize("G,list_type,w_trans,K", [(128, 0, True, 512), (128, 1, False, 512), (256, 1, True, 1024),
+                                                   (1024, 0, True, 256)])
+def test_many_experts_zipf(ascq_gpu, oracle, G, list_type, w_trans, K):
+    """128 to 1024 experts with Zipf(1.1)-ragged groups (most of them empty or a handful of rows): the MFMA kernel
+    takes up to 1024 groups (the table is a block-wide prefix sum, no per-group LDS), bit-exact vs the oracle.
+    The sample's group list forms: prefix offsets (list_type 0) and counts (1); a leading offset > 0 and trailing
+    rows outside every group stay untouched."""
+    rng = seeded(G + K + list_type)
+    T, N = 4096, 256
+    counts = zipf_counts(rng, T, G)
+    lead = 5
+    M = lead + T + 7
+    x = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    pts = np.exp(rng.uniform(np.log(1e-3), np.log(1e-1), M)).astype(np.float32)
+    w = rng.integers(-127, 128, (G, N, K) if w_trans else (G, K, N), dtype=np.int8)
+    scale = np.exp(rng.uniform(np.log(1e-4), np.log(1e-2), (G, N))).astype(np.float32)
+    if list_type == 0:
+        gl = np.concatenate([[lead], lead + np.cumsum(counts)]).astype(np.int64)
+    else:
+        gl = counts.astype(np.int64)
+    y = torch.full((M, N), 3.0, dtype=torch.bfloat16, device="cuda")
+    ascq_gpu.quant_group_matmul(_dev(x), _dev(pts), _dev(w), _dev(scale), _dev(gl), list_type, w_trans, out=y)
+    y0 = torch.full((M, N), 3.0, dtype=torch.bfloat16).view(torch.int16).numpy().view(np.uint16).copy()
+    ref = O.group_matmul(x, pts, w, scale, gl, list_type, G, M, K, N, O.BF16, w_trans, y=y0)
+    np.testing.assert_array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), ref)
