@@ -153,28 +153,128 @@ def bench_headline(torch, ascq, steps, warmup):
                 bytes_dequant=bytes_dequant, q_samples=len(qi), d_samples=len(di))
 
 
-def cpu_baseline_headline(budget_s=10.0):
-    """The oracle (C restatement, OpenMP) timed on the host: dynamic per-token quant + dequant over the
-    full 8192 x 8192 workload, repeated until ~budget_s seconds have been spent (min 2 reps)."""
+def _cpu_info():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    nproc = os.cpu_count() or 1
+    threads = int(os.environ.get("OMP_NUM_THREADS", nproc))
+    return model, nproc, threads
+
+
+def _median_s(fn, runs=5, warmup=1):
+    """median wall time of `runs` calls after `warmup` untimed ones"""
+    for _ in range(warmup):
+        fn()
+    t = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        t.append(time.perf_counter() - t0)
+    return float(np.median(t)), t
+
+
+def _cpu_record(value, unit, sample, secs, runs):
+    model, nproc, threads = _cpu_info()
+    return dict(value=value, unit=unit, cores=threads, kind="port", sample=sample, cpu_model=model, nproc=nproc,
+                omp_threads=threads, median_s=round(secs, 5), runs=[round(x, 5) for x in runs],
+                method="median of 5 timed runs after 1 untimed warm-up; oracle/ascq_oracle.c at -O3 "
+                       "-march=x86-64-v3 with OpenMP")
+
+
+def _oracle():
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_lib as O
+    return O
 
+
+def cpu_baseline_headline():
+    """The oracle (C restatement, OpenMP) on the host: dynamic per-token quant + dequant over the full
+    8192 x 8192 workload."""
+    O = _oracle()
     M = N = 8192
     rng = np.random.default_rng(7)
     x = rng.standard_normal((M, N), dtype=np.float32).astype(np.float16).view(np.uint16)
-    O.quant_dynamic_per_token(x[:64], O.F16)  # load + warm
-    reps, spent = 0, 0.0
-    while reps < 2 or spent < budget_s:
-        t0 = time.perf_counter()
+
+    def run():
         q, s = O.quant_dynamic_per_token(x, O.F16)
         O.dequant_policy(q, O.INT8, s, O.F32, O.PER_TOKEN, O.F16)
-        spent += time.perf_counter() - t0
-        reps += 1
-    per = spent / reps
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return dict(value=(6 * M * N + 8 * M) / per / 1e9, unit="GB/s", cores=threads, kind="port",
-                sample=f"full 8192x8192 f16 workload, {reps} reps of quant+dequant ({spent:.1f} s), "
-                       f"oracle/ascq_oracle.c at -O3 -march=x86-64-v3 with {threads} OpenMP threads")
+
+    secs, runs = _median_s(run)
+    return _cpu_record((6 * M * N + 8 * M) / secs / 1e9, "GB/s", "full 8192x8192 f16 workload (quant + dequant)",
+                       secs, runs)
+
+
+def cpu_baseline_w8a8(M, N, K):
+    """int32 GEMM + bias + per-channel DEQF16 on the host; the 8192^3 shape on a 64-row sample"""
+    O = _oracle()
+    rng = np.random.default_rng(1)
+    rows = M if M <= 1024 else 64
+    A = rng.integers(-127, 128, (rows, K), dtype=np.int8)
+    B = rng.integers(-127, 128, (K, N), dtype=np.int8)
+    bias = rng.integers(-(1 << 15), 1 << 15, N, dtype=np.int32)
+    words = np.full(N, np.float32(2.0 ** -9).view(np.uint32), np.uint64)
+    secs, runs = _median_s(lambda: O.mm_dequant(O.matmul_i8(A, B, bias), O.F16, qvec=words))
+    return _cpu_record(2 * rows * N * K / secs / 1e12, "TOPS", f"{rows} of {M} rows x N={N} x K={K}", secs, runs)
+
+
+def cpu_baseline_gemv(bits, M):
+    """dequant-on-the-fly dot products (oracle antiquant_matmul) at K = 4096, N = 11008, group 128"""
+    O = _oracle()
+    K, N, g = 4096, 11008, 128
+    rng = np.random.default_rng(3)
+    rows = min(M, 4)
+    x = rng.standard_normal((rows, K)).astype(np.float16).view(np.uint16)
+    if bits == 4:
+        w = rng.integers(0, 256, (K, N // 2), dtype=np.uint8)
+    else:
+        w = rng.integers(-128, 128, (K, N), dtype=np.int8)
+    sc = np.full((K // g, N), np.float16(0.01).view(np.uint16), np.uint16)
+    of = np.full((K // g, N), np.float16(1.0).view(np.uint16), np.uint16)
+    secs, runs = _median_s(lambda: O.antiquant_matmul(x, w, O.INT4 if bits == 4 else O.INT8, sc, of, g, rows, N, K))
+    nbytes = K * N * bits // 8 + 2 * (K // g) * N * 2 + 2 * rows * K + 2 * rows * N
+    return _cpu_record(nbytes / secs / 1e9, "GB/s", f"M={rows} (of {M}) x K={K} x N={N}; bytes as the GPU line "
+                       "counts them for that M", secs, runs)
+
+
+def cpu_baseline_group():
+    """the MoE group matmul on a 512-token, 2-expert sample of the 4096-token, 16-expert workload (same K, N)"""
+    O = _oracle()
+    G, T, K, N = 2, 512, 4096, 1408
+    rng = np.random.default_rng(4)
+    x = rng.integers(-127, 128, (T, K), dtype=np.int8)
+    w = rng.integers(-127, 128, (G, K, N), dtype=np.int8)
+    pts = np.full(T, 0.01, np.float32)
+    scale = np.full((G, N), 0.01, np.float32)
+    gl = np.array([0, 300, T], np.int64)
+    secs, runs = _median_s(lambda: O.group_matmul(x, pts, w, scale, gl, 0, G, T, K, N))
+    return _cpu_record(2 * T * K * N / secs / 1e12, "TOPS", f"T={T} tokens in {G} groups, K={K}, N={N}", secs, runs)
+
+
+def cpu_baseline_mx():
+    """the MX-FP4 8192^3 GEMM (fp64 dequant-then-matmul, the reference golden) on 4 output rows"""
+    O = _oracle()
+    M = N = K = 8192
+    rng = np.random.default_rng(5)
+    rows = np.arange(4, dtype=np.int64)
+    A = rng.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    Bt = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sA = np.full((M, K // 32), 127, np.uint8)
+    sB = np.full((N, K // 32), 127, np.uint8)
+    secs, runs = _median_s(lambda: O.mx_matmul(A, Bt, sA, sB, M, N, K, trans_b=True, sa_layout=0, sb_layout=1,
+                                                rows=rows), runs=5, warmup=1)
+    return _cpu_record(2 * len(rows) * N * K / secs / 1e12, "TFLOPS", f"{len(rows)} of {M} rows x N={N} x K={K}",
+                       secs, runs)
+
+
+def _roof(bound, achieved, peak, unit):
+    return dict(bound=bound, achieved=round(achieved, 3), peak=peak, unit=unit, frac=round(achieved / peak, 4))
 
 
 # ----------------------------------------------------------------------------------------------
@@ -632,16 +732,51 @@ OTHER = {
 }
 
 
-def run_others(torch, ascq, which):
-    out = []
+def _with_roofline(r):
+    """the roofline object of a GPU record: MFMA-bound GEMMs against their dense peak, HBM-bound ops against
+    8 TB/s; the group matmul against its attainable min(peak, AI x HBM)"""
+    if "value" not in r or "unit" not in r:
+        return r
+    if "frac_of_attainable" in r:
+        peak = r["value"] / r["frac_of_attainable"]
+        r["roofline"] = _roof("hbm" if peak < INT8_PEAK_TOPS - 1e-6 else "mfma", r["value"], round(peak, 2), r["unit"])
+    elif "frac_of_peak" in r:
+        r["roofline"] = _roof("hbm" if r["unit"] == "GB/s" else "mfma", r["value"], round(r["value"] / r["frac_of_peak"], 2),
+                              r["unit"])
+    return r
+
+
+# CPU baselines of the BASELINE configs' families: (family, index in OTHER[family]) -> oracle timing
+CPU_FOR = {
+    ("w8a8", 0): lambda: cpu_baseline_w8a8(128, 256, 512),
+    ("w8a8", 1): lambda: cpu_baseline_w8a8(8192, 8192, 8192),
+    ("gemv", 0): lambda: cpu_baseline_gemv(4, 1), ("gemv", 1): lambda: cpu_baseline_gemv(4, 16),
+    ("gemv", 2): lambda: cpu_baseline_gemv(4, 64), ("gemv", 3): lambda: cpu_baseline_gemv(8, 1),
+    ("gemv", 4): lambda: cpu_baseline_gemv(8, 16), ("gemv", 5): lambda: cpu_baseline_gemv(8, 64),
+    ("group", 0): cpu_baseline_group, ("group", 1): cpu_baseline_group,
+    ("mx", 0): cpu_baseline_mx, ("mx", 1): cpu_baseline_mx,
+}
+
+
+def run_others(torch, ascq, which, with_cpu=False):
+    out, cpu_cache = [], {}
     for key in (["quant", "w8a8", "gemv", "group", "mx", "fp8"] if which == "all" else [which]):
-        for fn in OTHER[key]:
+        for idx, fn in enumerate(OTHER[key]):
             try:
-                r = fn(torch, ascq)
-                out.append({k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()})
+                r = _with_roofline(fn(torch, ascq))
+                rec = {k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()}
             except Exception as e:  # report, do not hide
-                out.append({"error": repr(e)})
+                rec = {"error": repr(e)}
             torch.cuda.empty_cache()
+            cf = CPU_FOR.get((key, idx)) if with_cpu else None
+            if cf is not None:
+                try:
+                    if cf not in cpu_cache:
+                        cpu_cache[cf] = cf()
+                    rec["cpu_baseline"] = cpu_cache[cf]
+                except Exception as e:
+                    rec["cpu_baseline"] = {"error": repr(e)}
+            out.append(rec)
     return out
 
 
@@ -669,7 +804,7 @@ def main() -> int:
         print(json.dumps(traffic_probe(torch, ascq)))
         return 0
     if args.only in ("quant", "w8a8", "gemv", "group", "mx", "fp8"):
-        print(json.dumps({"other_configs": run_others(torch, ascq, args.only)}))
+        print(json.dumps({"other_configs": run_others(torch, ascq, args.only, with_cpu=not args.no_cpu)}))
         return 0
     h = bench_headline(torch, ascq, args.steps, args.warmup)
     step_ms = h["total_ms"] / args.steps
@@ -704,7 +839,7 @@ def main() -> int:
                            "avg_launch_ms": round(h["d_ms"], 5)},
     }
     if args.only == "all":
-        rec["other_configs"] = run_others(torch, ascq, "all")
+        rec["other_configs"] = run_others(torch, ascq, "all", with_cpu=not args.no_cpu)
     if not args.no_cpu:
         rec["cpu_baseline"] = cpu_baseline_headline()
     print(json.dumps(rec))
