@@ -5,6 +5,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <new>
@@ -18,6 +19,28 @@ namespace {
 thread_local std::string g_err;
 thread_local ascq::LaunchEvents g_launch_events;
 
+// Host log, gated by the environment variable ASCQ_LOG (read once): unset or 0 = silent; 1 = the message of every
+// failed call on stderr; 2 = also one line per accepted call of the main entry points (name, types, shape).
+int log_level()
+{
+    static const int level = [] {
+        const char* e = std::getenv("ASCQ_LOG");
+        return e ? std::atoi(e) : 0;
+    }();
+    return level;
+}
+
+void trace(const char* fmt, ...)
+{
+    if (log_level() < 2) return;
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    std::fprintf(stderr, "ascq: %s\n", buf);
+}
+
 ascq_status fail(ascq_status code, const char* fmt, ...)
 {
     char buf[512];
@@ -26,6 +49,7 @@ ascq_status fail(ascq_status code, const char* fmt, ...)
     vsnprintf(buf, sizeof(buf), fmt, ap);
     va_end(ap);
     g_err = buf;
+    if (log_level() >= 1) std::fprintf(stderr, "ascq: error %d: %s\n", (int)code, buf);
     return code;
 }
 
@@ -497,6 +521,9 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
     const int64_t m = h->sm > 0 ? h->sm : h->M, n = h->sn > 0 ? h->sn : h->N, k = h->sk > 0 ? h->sk : h->K;
     if (m > h->M || n > h->N || k > h->K) return fail(ASCQ_E_INVALID_ARG, "iterate_all: single shape exceeds org shape");
     hipStream_t st = S(stream);
+    trace("iterate_all: A %d B %d C %d kind %d, M %lld N %lld K %lld, transA %d transB %d, enAtomic %d", h->ty.a_type,
+          h->ty.b_type, h->ty.c_type, (int)kind_of(h->ty), (long long)m, (long long)n, (long long)k, h->trans_a,
+          h->trans_b, atomic);
     switch (kind_of(h->ty)) {
     case K_INT8: {
         if (h->ty.c_type != ASCQ_DT_INT32 && !h->quant_set)
@@ -1099,6 +1126,8 @@ ascq_status ascq_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w_
         return fail(ASCQ_E_INVALID_ARG, "antiquant_matmul: x and the packed weight must be 16-byte aligned");
     if (k * n >= (1ll << 31) || 64 * k * 2 >= (1ll << 31))
         return fail(ASCQ_E_UNSUPPORTED, "antiquant_matmul: the weight must stay below 2^31 elements");
+    trace("antiquant_matmul: W %d, M %lld N %lld K %lld, group %lld, offset %d", w_type, (long long)m, (long long)n,
+          (long long)k, (long long)group_size, offset ? 1 : 0);
     return hip_status(ascq::launch_antiquant_matmul(y, x, w_packed, w_type, scale, offset, group_size, m, n, k,
                                                     ascq::C_STORE, S(stream)),
                       "antiquant_matmul");
@@ -1136,6 +1165,8 @@ ascq_status ascq_quant_group_matmul(void* y, int32_t out_type, const int8_t* x, 
     g.K = k;
     g.N = n;
     g.act = activation;
+    trace("quant_group_matmul: out %d, G %lld M %lld K %lld N %lld, w_trans %d, list_type %d, act %d", out_type,
+          (long long)num_groups, (long long)m, (long long)k, (long long)n, g.w_trans, list_type, activation);
     return hip_status(ascq::launch_group_gemm(g, S(stream)), "quant_group_matmul");
 }
 

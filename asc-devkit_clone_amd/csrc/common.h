@@ -214,7 +214,7 @@ __device__ __forceinline__ uint32_t hif8_code_rna_sat(float x)
 }
 
 // E1M2 nibble: sign | 1-bit exponent (bias 1) | 2-bit mantissa, magnitudes {0, .25, .5, .75, 1, 1.25, 1.5, 1.75}
-// -- the 3-bit magnitude code times 0.25 (docs/zh/api/SIMD-API/c_api/cube_compute/mmad_mx_interface_boundary_value_summary.md:11:
+// -- the 3-bit magnitude code times 0.25 (docs/zh/api/appendix/mmad_mx_interface_boundary_value_summary.md:11:
 // largest finite 1.75)
 __device__ __forceinline__ float e1m2_to_f32(uint32_t nib)
 {

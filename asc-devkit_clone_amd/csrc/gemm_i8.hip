@@ -353,10 +353,14 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
     // the tiled epilogue addresses a 256-row output tile with 32-bit offsets
     if (a_ok && b_ok && a.K % 16 == 0 && a.ldc < (1ll << 21)) {
         const bool big = a.M >= 1024 && a.N >= 1024;
+        // small problems (the W8A8 sample, 128 x 256 x 512: 4 tiles of 64 x 128) take 32 x 32 single-wave tiles so
+        // that at least 32 workgroups share the work
+        const bool tiny = ((a.M + 63) / 64) * ((a.N + 127) / 128) < 32;
         if (a.trans_b)
             return big ? (a.K % 128 == 0 ? launch_tiled<256, 256, 4, 2, 2, true, 128>(a, st)
                                          : launch_tiled<256, 256, 4, 2, 4, true>(a, st))
-                       : launch_tiled<64, 64, 2, 2, 4, true>(a, st);
+                       : (tiny ? launch_tiled<32, 32, 1, 1, 4, true>(a, st) : launch_tiled<64, 64, 2, 2, 4, true>(a, st));
+        if (tiny) return launch_tiled<32, 32, 1, 1, 4, false>(a, st);
         return big ? launch_tiled<256, 256, 4, 2, 4, false>(a, st) : launch_tiled<64, 128, 2, 2, 4, false>(a, st);
     }
     int64_t blocks = (a.M * a.N + 255) / 256;

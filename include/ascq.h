@@ -199,7 +199,7 @@ ascq_status ascq_matmul_set_quant_vector(ascq_matmul_t h, const uint64_t* quant_
 ascq_status ascq_matmul_set_antiquant_scalar(ascq_matmul_t h, uint16_t offset_f16, uint16_t scale_f16);
 ascq_status ascq_matmul_set_antiquant_vector(ascq_matmul_t h, const void* offset, const void* scale,
                                              int64_t group_size);
-/* SetTensorScaleA / SetTensorScaleB (mx_matmul_impl.h:136-188; examples/.../matmul_mx/matmul_mx.asc:194-203).
+/* SetTensorScaleA / SetTensorScaleB (mx_matmul_impl.h:136-188; examples/01_simd_cpp_api/04_advanced_api/00_matmul/matmul_mx/matmul_mx.asc:194-203).
  * scaleA: [M, sK] (transpose: [sK/2, M, 2]); scaleB: [sK/2, N, 2] (transpose: [N, sK]); sK = ceil(K/64)*2. */
 ascq_status ascq_matmul_set_tensor_scale_a(ascq_matmul_t h, const uint8_t* scale_a, int32_t is_transpose_scale_a);
 ascq_status ascq_matmul_set_tensor_scale_b(ascq_matmul_t h, const uint8_t* scale_b, int32_t is_transpose_scale_b);

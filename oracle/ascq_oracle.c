@@ -928,9 +928,9 @@ uint8_t oq_e2m1_encode(double x, int mode)
 
 /* fp4x2_e1m2_t: sign | 1-bit exponent (bias 1) | 2-bit mantissa.  Exponent field 0 is subnormal (0.mm x 2^0),
  * field 1 normal (1.mm x 2^0): magnitudes {0, .25, .5, .75, 1, 1.25, 1.5, 1.75}; the largest finite 1.75
- * (docs/zh/api/SIMD-API/c_api/cube_compute/mmad_mx_interface_boundary_value_summary.md:11: +inf -> 1.75,
- * -inf -> -1.75, NaN -> 0) and e1m2 -> bf16 lossless (docs/zh/api/SIMD-API/tensor_api/reg_vector_compute/
- * type_conversion/precision_conversion.md:112-115). */
+ * (docs/zh/api/appendix/mmad_mx_interface_boundary_value_summary.md:11: +inf -> 1.75,
+ * -inf -> -1.75, NaN -> 0) and e1m2 -> bf16 lossless (docs/zh/api/SIMD-API/basic_api/
+ * data_structures/precision_conversion.md:112-115). */
 float oq_e1m2_decode(uint8_t nib)
 {
     const int e = (nib >> 2) & 1, mm = nib & 3;

@@ -3,6 +3,7 @@ invalid arguments on the host (negative status, nothing launched) -- no GPU need
 from __future__ import annotations
 
 import ctypes
+import os
 import re
 import subprocess
 from pathlib import Path
@@ -345,3 +346,18 @@ def test_no_fma_with_zero_addend_in_half_arithmetic(tmp_path):
     assert r.returncode == 0, r.stderr[-2000:]
     bad = [ln for ln in out.read_text().splitlines() if re.search(r"v_fma_mix(lo|hi)?_f16 .*, 0( |$)", ln)]
     assert not bad, bad[:5]
+
+
+def test_env_gated_host_log():
+    """ASCQ_LOG=1 prints the message of a failed call on stderr; unset, the library is silent"""
+    import subprocess
+    import sys
+
+    code = ("import sys; sys.path.insert(0, %r); import ascq; "
+            "print(ascq.lib().ascq_quant_group_matmul(None, 0, None, None, None, 0, None, None, 0, 0, 0, 0, 0, 0, None))"
+            % str(ROOT / "asc-devkit_clone_amd"))
+    for env_val, expect in (("1", True), ("0", False)):
+        env = dict(os.environ, ASCQ_LOG=env_val)
+        r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, r.stderr
+        assert ("ascq: error" in r.stderr and "null argument" in r.stderr) == expect, r.stderr
