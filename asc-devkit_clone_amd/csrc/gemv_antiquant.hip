@@ -24,6 +24,9 @@
 //
 // Roofline: at decode shapes the kernel streams the packed weight once (K*N/2 or K*N bytes) plus the
 // scales/offsets; it is HBM-bound at M = 1 and 16 and near the fp16 MFMA ridge at M = 64.
+#include <algorithm>
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
@@ -397,12 +400,13 @@ __global__ __launch_bounds__(KSPLIT * 64) void antiquant_gemm_kernel(uint16_t* _
 // of each round is copied global -> LDS by buffer loads with an LDS destination (no registers) into a ring of ST
 // stages, ST - 1 rounds ahead, and shared by all waves of the workgroup; wave (s, kw) owns 16-column strip s of the
 // workgroup's NS strips and k tile (round * KSW + kw), whose weight tile (with its scale / offset) is loaded into a
-// register ring ST - 1 rounds ahead as well.  Every wave issues the same number of memory operations per round, so
-// one s_waitcnt vmcnt with a constant threshold plus one barrier per round make a stage visible and free the
-// stage read in the previous round.  Each 16-byte chunk c of row r is stored at chunk c ^ (r % 16) of its LDS
+// register ring DW - 1 rounds ahead (DW a multiple of ST: the weights may run further ahead than the activations, so
+// that enough bytes are in flight).  Every wave issues the same number of memory operations per round, so one
+// s_waitcnt vmcnt with a constant threshold plus one barrier per round make a stage visible and free the stage read
+// in the previous round.  Each 16-byte chunk c of row r is stored at chunk c ^ (r % 16) of its LDS
 // row (the swizzle is applied to the global address of the copy), so the 16 rows of an MFMA fragment read hit 16
 // distinct bank groups.  The KSW partial 16x16 tiles of a strip are summed through LDS in a fixed order.
-template <int MT, int NS, int KSW, int ST, bool INT4, bool HAS_OFF>
+template <int MT, int NS, int KSW, int ST, bool INT4, bool HAS_OFF, int DW = ST>
 struct AqDma {
     static constexpr int NW = NS * KSW, NT = NW * 64;
     static constexpr int ROWS = 16 * MT;
@@ -412,15 +416,17 @@ struct AqDma {
     static constexpr int CPW = 4 * MT / NS;              // 1 KiB copies per wave per round
     static constexpr int WV = INT4 ? 1 : 2;              // 16-byte weight loads per lane per tile
     static constexpr int WL = WV + (HAS_OFF ? 2 : 1);    // vmem operations per wave per round besides the copies
-    static constexpr int IN_FLIGHT = (ST - 2) * (CPW + WL);
+    // at the top of round r, the copies of round r (issued in round r - ST + 1) must have landed; with DW > ST the
+    // weights of round r were issued before them, with DW == ST right after them in the same round
+    static constexpr int IN_FLIGHT = (DW > ST ? WL : 0) + (ST - 2) * (CPW + WL);
     static constexpr int RED = (KSW - 1) * NS * MT * 64 * 16;
     static constexpr int LDS = ST * SLOT > RED ? ST * SLOT : RED;
     static_assert((4 * MT) % NS == 0 && CPW >= 1, "copies split evenly over the waves");
     static_assert(CH >= 16 && (CH & (CH - 1)) == 0, "swizzle needs 16+ chunks per row, a power of two");
-    static_assert(ST >= 3 && IN_FLIGHT < 64 && LDS <= 160 * 1024, "stages");
+    static_assert(ST >= 3 && IN_FLIGHT < 64 && LDS <= 160 * 1024 && DW % ST == 0, "stages");
 };
 
-template <int MT, int NS, int KSW, int ST, bool INT4, bool HAS_OFF, bool ROT = false>
+template <int MT, int NS, int KSW, int ST, bool INT4, bool HAS_OFF, bool ROT = false, int DW = ST>
 __global__ __launch_bounds__(NS * KSW * 64) void aq_dma_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
                                                                const uint8_t* __restrict__ wp,
                                                                const uint16_t* __restrict__ scale,
@@ -428,7 +434,7 @@ __global__ __launch_bounds__(NS * KSW * 64) void aq_dma_kernel(uint16_t* __restr
                                                                int64_t N, int64_t K, int64_t g, int64_t ldx,
                                                                int atomic)
 {
-    using P = AqDma<MT, NS, KSW, ST, INT4, HAS_OFF>;
+    using P = AqDma<MT, NS, KSW, ST, INT4, HAS_OFF, DW>;
     constexpr int TILE_BYTES = INT4 ? 1024 : 2048;
     constexpr int LANE_BYTES = INT4 ? 16 : 32;
     __shared__ __attribute__((aligned(16))) uint8_t smem[P::LDS];
@@ -510,18 +516,20 @@ __global__ __launch_bounds__(NS * KSW * 64) void aq_dma_kernel(uint16_t* __restr
         }
     };
 
-    WTile wt[ST];
-    // prologue: rounds 0 .. ST - 2 in flight
+    WTile wt[DW];
+    // prologue: the DW - 1 rounds before round 0 as the loop would have issued them (activations of rounds
+    // 0 .. ST - 2, weights of rounds 0 .. DW - 2)
 #pragma unroll
-    for (int r = 0; r < ST - 1; ++r) {
-        issue_x(r, r);
-        load_w(r, wt[r]);
+    for (int q = 0; q < DW - 1; ++q) {
+        if (q >= DW - ST) issue_x(q - DW + ST, q - DW + ST);
+        load_w(q, wt[q]);
     }
     // round r: its stage has landed (this wave's copies: vmcnt; everyone's: the barrier, which also frees the
-    // stage read in round r - 1), then round r + ST - 1 is issued into that freed stage, then round r computes
-    for (int64_t r0 = 0; r0 < rounds; r0 += ST) {
+    // stage read in round r - 1), then round r + ST - 1 is issued into that freed stage and the weights of round
+    // r + DW - 1 into the weight slot freed by round r - 1, then round r computes
+    for (int64_t r0 = 0; r0 < rounds; r0 += DW) {
 #pragma unroll
-        for (int u = 0; u < ST; ++u) {
+        for (int u = 0; u < DW; ++u) {
             const int64_t r = r0 + u;
             if (r < rounds) {
                 __builtin_amdgcn_sched_barrier(0);
@@ -534,9 +542,9 @@ __global__ __launch_bounds__(NS * KSW * 64) void aq_dma_kernel(uint16_t* __restr
                 // the next round's operations are always issued (out-of-range ones read zeros), so every wave
                 // keeps the same number in flight and the vmcnt threshold stays exact
                 issue_x(r + ST - 1, (u + ST - 1) % ST);
-                load_w(r + ST - 1, wt[(u + ST - 1) % ST]);
+                load_w(r + DW - 1, wt[(u + DW - 1) % DW]);
                 __builtin_amdgcn_sched_barrier(0);
-                compute(u, wt[u]);
+                compute(u % ST, wt[u]);
             }
         }
     }
@@ -594,19 +602,564 @@ static void launch_aq(uint16_t* y, const uint16_t* x, const void* wp, bool int4,
     }
 }
 
-template <int MT, int NS, int KSW, int ST, bool ROT>
+// Column-block form for small batches (M <= 16, group size 128 << s).  The grid is C column blocks; block c covers
+// the 16-column strips [c sq + min(c, sr), ...) -- sq or sq + 1 of them, so any C balances.  The workgroup first
+// copies x[0:M, 0:K] into LDS once (16-byte chunk c of row r at chunk c ^ (r % 16) of its LDS row, so the 16 rows of
+// an MFMA fragment read hit 16 distinct bank groups; fragment rows m >= M read a zeroed row), as buffer loads with an
+// LDS destination and the uniform part of every address in the scalar offset.  Wave (sg, kw) of the SG x KW waves
+// owns strips sg NBW .. sg NBW + NBW - 1 of the block and the T = KB / KW k tiles kw, kw + KW, ... (T a multiple of
+// D); it copies the
+// scale / offset rows of its tiles over its strips into its own LDS area, and its weight tiles stream through a
+// register ring: D tiles are in flight, and tile i + D is issued as soon as tile i has been multiplied (tiles past
+// the end read zeros, so the count in flight stays constant and one s_waitcnt threshold serves every step).  Each
+// activation fragment is read from LDS once for the wave's NBW strips; every LDS address is a per-lane base plus a
+// uniform offset.  The KW partial 16 x 16 tiles of a strip are summed through LDS in kw order by the wave kw = 0,
+// which writes y.
+template <int NBW, int SG, int KW, int D>
+struct AqXs {
+    static constexpr int NW = SG * KW, NT = NW * 64;
+    static constexpr int SMAX = SG * NBW;                 // strips per block at most
+    static constexpr int WPT = NBW * 8;                   // 4-byte words of scale row per tile and wave
+    static constexpr int TPC = 64 / WPT;                  // tiles per 256-byte scale copy
+    static constexpr int RED = (KW - 1) * SG * NBW * 1024;  // k-wave partial tiles
+    static_assert(TPC >= 1, "scale row of a tile within one copy");
+};
+
+// kernel arguments of aq_xs_kernel / aq_ring_kernel, all index arithmetic in 32 bits (the host checks every byte
+// size < 2^31)
+struct AqXsArgs {
+    uint16_t* y;
+    const uint16_t* x;
+    const uint8_t* wp;
+    const uint16_t* scale;
+    const uint16_t* offset;
+    uint32_t M, N, K, KB;
+    uint32_t sq, sr;  // block c has sq + (c < sr) strips, starting at strip c sq + min(c, sr)
+    uint32_t gshift;  // group size = 128 << gshift
+    uint32_t x_bytes, w_bytes, s_bytes;
+    int atomic;
+};
+
+template <int NBW, int SG, int KW, int D, bool INT4, bool HAS_OFF>
+__global__ __launch_bounds__(SG * KW * 64) void aq_xs_kernel(AqXsArgs A)
+{
+    using P = AqXs<NBW, SG, KW, D>;
+    constexpr int NW = P::NW, NT = P::NT, WPT = P::WPT, TPC = P::TPC;
+    constexpr int TILE_BYTES = INT4 ? 1024 : 2048;
+    constexpr int LANE_BYTES = INT4 ? 16 : 32;
+    constexpr int WV = INT4 ? 1 : 2;
+    constexpr int TOPS = NBW * WV;  // vector memory operations per ring tile
+    static_assert(D * TOPS < 64, "vmcnt range");
+    extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int sg = wave / KW, kw = wave % KW;
+    const uint32_t col_in = lane & 15, kq = lane >> 4;
+    const uint32_t cb = blockIdx.x;
+    const uint32_t M = A.M, N = A.N, KB = A.KB;
+    const uint32_t T = KB / KW;  // k tiles per wave (KB % KW == 0)
+    const uint32_t s0 = cb * A.sq + (cb < A.sr ? cb : A.sr), s1 = s0 + A.sq + (cb < A.sr ? 1u : 0u);
+    const uint32_t sb = s0 + (uint32_t)(sg * NBW);  // first strip of this wave
+    const uint32_t RL = KB * 256;                   // LDS activation row bytes
+    const uint32_t ncp = (T + TPC - 1) / TPC, wsb = ncp * 256;
+    // LDS: M activation rows | zero row | scale rows of each wave [ncp][256 B] | offset rows of each wave
+    const uint32_t zrow_at = M * RL, sc_at = zrow_at + RL, of_at = sc_at + NW * wsb;
+    const aq_rsrc_t rw = aq_rsrc(A.wp, A.w_bytes);
+    const aq_rsrc_t rx = aq_rsrc(A.x, A.x_bytes);
+    const aq_rsrc_t rs = aq_rsrc(A.scale, A.s_bytes);
+    const aq_rsrc_t ro = aq_rsrc(HAS_OFF ? A.offset : A.scale, A.s_bytes);
+    const uint32_t magic = half_magic_vgpr();
+
+    // activation rows: 1 KiB block pb of row r (4 k tiles) lands at r RL + 1024 pb; lane l fills physical chunk
+    // 64 pb + l, which holds logical chunk 64 pb + (l ^ r % 16)
+    {
+        const uint32_t bpr = KB / 4;
+        for (uint32_t b = (uint32_t)wave; b < M * bpr; b += NW) {
+            const uint32_t r = b / bpr, pb = b - r * bpr;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(xs + r * RL + pb * 1024), 16, (lane ^ (r & 15u)) * 16,
+                                                     (int)(r * A.K * 2 + pb * 1024), 0, 0);
+        }
+    }
+    for (uint32_t c = threadIdx.x; c < RL / 16; c += NT) *(u32x4*)(xs + zrow_at + c * 16) = (u32x4){0u, 0u, 0u, 0u};
+    // this wave's scale / offset rows, NBW * 16 halves per tile: copy c holds tiles c TPC .. c TPC + TPC - 1, lane l
+    // word l % WPT of tile c TPC + l / WPT (lanes past TPC WPT and columns past the block read zeros)
+    for (uint32_t c = 0; c < ncp; ++c) {
+        const uint32_t i = c * TPC + (uint32_t)lane / WPT, wd = (uint32_t)lane % WPT;
+        const uint32_t kt = (uint32_t)kw + i * KW;
+        const bool ok = (uint32_t)lane < TPC * WPT && i < T && 2 * wd < (s1 > sb ? (s1 - sb) * 16 : 0u);
+        const uint32_t voff = ok ? ((kt >> A.gshift) * N * 2 + wd * 4) : AQ_OOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(xs + sc_at + wave * wsb + c * 256), 4, voff, (int)(sb * 32), 0, 0);
+        if constexpr (HAS_OFF)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ro, (lds_ptr)(xs + of_at + wave * wsb + c * 256), 4, voff, (int)(sb * 32), 0, 0);
+    }
+
+    // per-lane LDS bases: fragment j of tile i at xa_at[j] + i KW 256, with
+    // (4 j + kq) ^ col_in = ((4 j) ^ (col_in & 12)) | (kq ^ (col_in & 3)); the scale of (i, strip b) at
+    // s_at + (i / TPC) 256 + (i % TPC) WPT 4 + 32 b
+    const uint32_t xo0 = ((col_in & 12u) | (kq ^ (col_in & 3u))) * 16;
+    uint32_t xa_at[4];
+    {
+        const uint32_t rb = (col_in < M ? col_in * RL : zrow_at) + (uint32_t)kw * 256;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xa_at[j] = rb + (xo0 ^ (64u * j));
+    }
+    const uint32_t s_at = (uint32_t)wave * wsb + col_in * 2;
+    const int nvalid = (int)s1 - (int)sb < NBW ? (int)s1 - (int)sb : NBW;  // strips of this wave in the block
+
+    v4f acc[NBW];
+#pragma unroll
+    for (int b = 0; b < NBW; ++b) acc[b] = (v4f){0.f, 0.f, 0.f, 0.f};
+    // the pipeline for NV = nvalid strips (a compile-time count, so the loop body has no per-strip branch and the
+    // memory-operation counts behind every s_waitcnt are exact)
+    auto pipeline = [&](auto nv_tag) {
+        constexpr int NV = decltype(nv_tag)::value;
+        constexpr int TOPS = NV * WV;  // vector memory operations per ring tile
+        static_assert(D * TOPS < 64, "vmcnt range");
+        // ring tile i: weight tile kw + i KW of the NV strips; tiles past T read zeros
+        u32x4 wv[D][NV > 0 ? NV : 1][WV];
+        auto load_t = [&](uint32_t i, int slot) {
+            const uint32_t kt = (uint32_t)kw + i * KW;
+#pragma unroll
+            for (int b = 0; b < NV; ++b) {
+                const uint32_t off = i < T ? lane * LANE_BYTES : AQ_OOB;
+                const int soff = i < T ? (int)(((sb + b) * KB + kt) * TILE_BYTES) : 0;
+#pragma unroll
+                for (int v = 0; v < WV; ++v)
+                    wv[slot][b][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, off + 16 * v, soff, 0);
+            }
+        };
+#pragma unroll
+        for (int i = 0; i < D; ++i) load_t((uint32_t)i, i);
+        // this wave's copies are older than its ring loads: they have landed once at most D TOPS remain
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt_aq<D * TOPS>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the zero row is written
+        __builtin_amdgcn_sched_barrier(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (NV > 0) {
+            for (uint32_t i0 = 0; i0 < T; i0 += D) {
+#pragma unroll
+                for (int u = 0; u < D; ++u) {
+                    const uint32_t i = i0 + u;
+                    // tile i has landed once only the D - 1 tiles issued after it are in flight
+                    __builtin_amdgcn_sched_barrier(0);
+                    wait_vmcnt_aq<(D - 1) * TOPS>();
+                    __builtin_amdgcn_sched_barrier(0);
+                    const uint32_t so = s_at + (i / TPC) * 256 + (i % TPC) * WPT * 4;
+                    const uint32_t xi = i * KW * 256;
+                    h2 s2[NV], o2[NV];
+#pragma unroll
+                    for (int b = 0; b < NV; ++b) {
+                        const _Float16 sv = *(const _Float16*)(xs + sc_at + so + 32 * b);
+                        const _Float16 ov = HAS_OFF ? *(const _Float16*)(xs + of_at + so + 32 * b) : (_Float16)0.0f;
+                        s2[b] = (h2){sv, sv};
+                        o2[b] = (h2){ov, ov};
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const h8 xa = *(const h8*)(xs + xa_at[j] + xi);
+#pragma unroll
+                        for (int b = 0; b < NV; ++b) {
+                            uint32_t w0, w1 = 0;
+                            if constexpr (INT4) {
+                                w0 = wv[u][b][0][j];
+                            } else {
+                                w0 = wv[u][b][j >> 1][(j & 1) * 2];
+                                w1 = wv[u][b][j >> 1][(j & 1) * 2 + 1];
+                            }
+                            const h8 bf = dequant8<INT4, HAS_OFF>(w0, w1, o2[b], s2[b], magic);
+                            acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, bf, acc[b], 0, 0, 0);
+                        }
+                    }
+                    // the slot of tile i is free again: tile i + D goes into it (past T: zeros, same count)
+                    __builtin_amdgcn_sched_barrier(0);
+                    load_t(i + D, u);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+        wait_vmcnt_aq<0>();
+    };
+    // a wave holds NBW strips of its block, fewer in the block's last strip group
+    static_assert(NBW >= 1 && NBW <= 4, "strips per wave");
+    if (nvalid >= NBW) pipeline(std::integral_constant<int, NBW>{});
+    else if (NBW > 1 && nvalid == 1) pipeline(std::integral_constant<int, 1>{});
+    else if (NBW > 2 && nvalid == 2) pipeline(std::integral_constant<int, (NBW > 2 ? 2 : 1)>{});
+    else if (NBW > 3 && nvalid == 3) pipeline(std::integral_constant<int, (NBW > 3 ? 3 : 1)>{});
+    else pipeline(std::integral_constant<int, 0>{});
+
+    // KW partial tiles -> wave kw = 0 of each strip group, summed in kw order (the shared rows are dead)
+    __syncthreads();
+    if constexpr (KW > 1) {
+        v4f* red = (v4f*)xs;  // [KW - 1][SG][NBW][64]
+        if (kw > 0) {
+#pragma unroll
+            for (int b = 0; b < NBW; ++b) red[(((kw - 1) * SG + sg) * NBW + b) * 64 + lane] = acc[b];
+        }
+        __syncthreads();
+        if (kw != 0) return;
+#pragma unroll
+        for (int w = 0; w < KW - 1; ++w)
+#pragma unroll
+            for (int b = 0; b < NBW; ++b) acc[b] += red[((w * SG + sg) * NBW + b) * 64 + lane];
+    }
+    // D layout: lane holds rows 4 kq + i, column col_in of each 16 x 16 tile
+#pragma unroll
+    for (int b = 0; b < NBW; ++b) {
+        if (b >= nvalid) break;
+        uint16_t* yc = A.y + (sb + b) * 16 + col_in;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t m = 4 * kq + i;
+            if (m < M) y_put(yc + (uint64_t)m * N, f32_to_f16_sat(acc[b][i]), A.atomic);
+        }
+    }
+}
+
+// LDS bytes of aq_xs_kernel (0 when the shape does not fit)
+template <int NBW, int SG, int KW, int D>
+inline int64_t aq_xs_lds(int64_t M, int64_t K, bool has_off)
+{
+    using P = AqXs<NBW, SG, KW, D>;
+    const int64_t KB = K / KT, T = KB / KW, ncp = (T + P::TPC - 1) / P::TPC;
+    const int64_t lds = std::max<int64_t>((M + 1) * KB * 256 + (int64_t)P::NW * ncp * 256 * (has_off ? 2 : 1), P::RED);
+    return lds <= 160 * 1024 ? lds : 0;
+}
+
+// checks of the column-block and ring kernels common to both; fills the 32-bit argument block
+inline bool aq_cols_args(AqXsArgs& A, uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
+                         const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, int C, int smax, int atomic)
+{
+    const int64_t NBT = N / 16, KB = K / KT;
+    const uint64_t w_bytes = (uint64_t)K * N / (int4 ? 2 : 1), s_bytes = (uint64_t)((K + g - 1) / g) * N * 2;
+    const uint64_t x_bytes = (uint64_t)M * K * 2, lim = 0x7FFFFFFFull;
+    if (C < 1 || C > NBT || (NBT + C - 1) / C > smax || g % KT != 0 || ((g / KT) & (g / KT - 1)) != 0 || M < 1 ||
+        w_bytes >= lim || s_bytes >= lim || x_bytes >= lim || N >= (int64_t)lim)
+        return false;
+    A.y = y;
+    A.x = x;
+    A.wp = (const uint8_t*)wp;
+    A.scale = scale;
+    A.offset = offset;
+    A.M = (uint32_t)M;
+    A.N = (uint32_t)N;
+    A.K = (uint32_t)K;
+    A.KB = (uint32_t)KB;
+    A.sq = (uint32_t)(NBT / C);
+    A.sr = (uint32_t)(NBT % C);
+    A.gshift = (uint32_t)__builtin_ctzll((unsigned long long)(g / KT));
+    A.x_bytes = (uint32_t)x_bytes;
+    A.w_bytes = (uint32_t)w_bytes;
+    A.s_bytes = (uint32_t)s_bytes;
+    A.atomic = atomic;
+    return true;
+}
+
+template <int NBW, int SG, int KW, int D>
+static hipError_t launch_aq_xs(uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
+                               const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, int C, int atomic,
+                               hipStream_t st)
+{
+    using P = AqXs<NBW, SG, KW, D>;
+    AqXsArgs A;
+    const int64_t lds = aq_xs_lds<NBW, SG, KW, D>(M, K, offset != nullptr);
+    if (M > 16 || (K / KT) % 4 != 0 || (K / KT) % (KW * D) != 0 || lds == 0 ||
+        !aq_cols_args(A, y, x, wp, int4, scale, offset, g, M, N, K, C, P::SMAX, atomic))
+        return hipErrorInvalidValue;
+#define AQ_XS_LAUNCH(I4, OF)                                                 \
+    do {                                                                     \
+        constexpr auto kern = aq_xs_kernel<NBW, SG, KW, D, I4, OF>;           \
+        hipError_t e = ensure_dynamic_lds<kern>((int)lds);                   \
+        if (e != hipSuccess) return e;                                       \
+        launch_k(kern, dim3((unsigned)C), dim3(P::NT), (uint32_t)lds, st, A); \
+    } while (0)
+    if (int4) {
+        if (offset) AQ_XS_LAUNCH(true, true);
+        else AQ_XS_LAUNCH(true, false);
+    } else {
+        if (offset) AQ_XS_LAUNCH(false, true);
+        else AQ_XS_LAUNCH(false, false);
+    }
+#undef AQ_XS_LAUNCH
+    return hipGetLastError();
+}
+
+// Batch form (16 < M <= 16 MT, group size 128 << s): the column blocks of aq_xs_kernel, with the activations
+// streamed.  Block c covers the strips [c sq + min(c, sr), ...); wave (sg, kw) of the SG x KW waves owns strips
+// sg NBW .. sg NBW + NBW - 1 of the block and, in round r, k tile r KW + kw.  The activation tile x[0:16 MT,
+// 128 KW r .. 128 KW (r + 1)) of each round is copied into an LDS ring of ST stages (buffer loads with an LDS
+// destination, 16-byte chunk c of row r at chunk c ^ (r % 16); rows m >= M read zeros), ST - 1 rounds ahead, and
+// shared by all waves; every wave reads each activation fragment once for its NBW strips, which is what keeps the
+// LDS read traffic of a 64-row batch within bounds.  Weight tiles stream through a register ring DW - 1 rounds
+// ahead (DW a multiple of ST); the scale / offset rows of a wave's tiles are copied into LDS once, at the start.
+// Every wave issues the same number of memory operations per round, so one s_waitcnt vmcnt with a constant threshold
+// plus one barrier per round make a stage visible and free the stage read in the previous round.  The KW partial
+// tiles of a strip are summed through LDS in kw order by the wave kw = 0, which writes y.
+template <int MT, int NBW, int SG, int KW, int ST, int DW, bool INT4, bool HAS_OFF>
+struct AqRing {
+    static constexpr int NW = SG * KW, NT = NW * 64;
+    static constexpr int ROWS = 16 * MT;
+    static constexpr int ROWB = KW * KT * 2;   // LDS bytes per staged row (one round)
+    static constexpr int CH = ROWB / 16;        // 16-byte chunks per row
+    static constexpr int SLOT = ROWS * ROWB;    // one stage
+    static constexpr int CPW = 4 * MT * KW / NW;  // 1 KiB copies per wave per round
+    static constexpr int WV = INT4 ? 1 : 2;
+    static constexpr int WL = NBW * WV;          // weight loads per wave per round
+    static constexpr int IN_FLIGHT = (DW > ST ? WL : 0) + (ST - 2) * (CPW + WL);
+    static constexpr int WPT = NBW * 8;          // 4-byte words of scale row per tile and wave
+    static constexpr int TPC = 64 / WPT;         // tiles per 256-byte scale copy
+    static constexpr int RED = (KW - 1) * SG * MT * NBW * 1024;
+    static_assert((4 * MT * KW) % NW == 0 && CPW >= 1, "copies split evenly over the waves");
+    static_assert(CH >= 16 && (CH & (CH - 1)) == 0, "swizzle needs 16+ chunks per row, a power of two");
+    static_assert(ST >= 2 && DW % ST == 0 && DW > ST - 1 && IN_FLIGHT < 64 && TPC >= 1, "stages");
+};
+
+template <int MT, int NBW, int SG, int KW, int ST, int DW, bool INT4, bool HAS_OFF>
+__global__ __launch_bounds__(SG * KW * 64) void aq_ring_kernel(AqXsArgs A)
+{
+    using P = AqRing<MT, NBW, SG, KW, ST, DW, INT4, HAS_OFF>;
+    constexpr int NW = P::NW, TPC = P::TPC, WPT = P::WPT;
+    constexpr int TILE_BYTES = INT4 ? 1024 : 2048;
+    constexpr int LANE_BYTES = INT4 ? 16 : 32;
+    constexpr int WV = P::WV;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int sg = wave / KW, kw = wave % KW;
+    const uint32_t col_in = lane & 15, kq = lane >> 4;
+    const uint32_t cb = blockIdx.x;
+    const uint32_t M = A.M, N = A.N, KB = A.KB;
+    const uint32_t s0 = cb * A.sq + (cb < A.sr ? cb : A.sr), s1 = s0 + A.sq + (cb < A.sr ? 1u : 0u);
+    const uint32_t sb = s0 + (uint32_t)(sg * NBW);  // first strip of this wave
+    const uint32_t rounds = KB / KW;                // KB % KW == 0
+    const uint32_t ncp = (rounds + TPC - 1) / TPC;  // scale copies per wave
+    // LDS: ST activation stages | scale rows of each wave [ncp][256 B] | offset rows of each wave
+    const uint32_t sc_at = ST * P::SLOT, wsb = ncp * 256;
+    const uint32_t of_at = sc_at + NW * wsb;
+    const aq_rsrc_t rw = aq_rsrc(A.wp, A.w_bytes);
+    const aq_rsrc_t rx = aq_rsrc(A.x, A.x_bytes);
+    const aq_rsrc_t rs = aq_rsrc(A.scale, A.s_bytes);
+    const aq_rsrc_t ro = aq_rsrc(HAS_OFF ? A.offset : A.scale, A.s_bytes);
+    const uint32_t magic = half_magic_vgpr();
+
+    // this wave's scale / offset rows, NBW * 16 halves per round: copy c holds rounds c TPC .. c TPC + TPC - 1
+    for (uint32_t c = 0; c < ncp; ++c) {
+        const uint32_t i = c * TPC + (uint32_t)lane / WPT, wd = (uint32_t)lane % WPT;
+        const uint32_t kt = i * KW + (uint32_t)kw;
+        const bool ok = (uint32_t)lane < TPC * WPT && i < rounds && 2 * wd < (s1 > sb ? (s1 - sb) * 16 : 0u);
+        const uint32_t voff = ok ? ((kt >> A.gshift) * N * 2 + wd * 4) : AQ_OOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(smem + sc_at + wave * wsb + c * 256), 4, voff, (int)(sb * 32), 0, 0);
+        if constexpr (HAS_OFF)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ro, (lds_ptr)(smem + of_at + wave * wsb + c * 256), 4, voff, (int)(sb * 32), 0, 0);
+    }
+
+    // activation copies of round r into stage `slot`: copy j of this wave covers chunks 64 (wave CPW + j) .. + 63
+    auto issue_x = [&](uint32_t r, int slot) {
+#pragma unroll
+        for (int j = 0; j < P::CPW; ++j) {
+            const uint32_t gcopy = (uint32_t)(wave * P::CPW + j);
+            const uint32_t q = gcopy * 64 + lane;
+            const uint32_t row = q / P::CH, p = q % P::CH;
+            const uint32_t c = p ^ (row & 15u);  // logical chunk held at physical chunk p
+            const uint32_t off = row < M && r < rounds ? (row * A.K + r * KW * KT + c * 8) * 2 : AQ_OOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(smem + slot * P::SLOT + gcopy * 1024), 16, off, 0, 0, 0);
+        }
+    };
+    struct WTile {
+        u32x4 w[NBW][WV];
+    };
+    auto load_w = [&](uint32_t r, WTile& t) {
+        const uint32_t kt = r * KW + (uint32_t)kw;
+#pragma unroll
+        for (int b = 0; b < NBW; ++b) {
+            const uint32_t s = sb + b;
+            const uint32_t off = r < rounds && s < s1 ? (s * KB + kt) * TILE_BYTES + lane * LANE_BYTES : AQ_OOB;
+#pragma unroll
+            for (int v = 0; v < WV; ++v) t.w[b][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, off + 16 * v, 0, 0);
+        }
+    };
+    // per-lane LDS bases: fragment (a, j) of this wave's tile in a stage at xa_at[a][j], with
+    // (4 j + kq) ^ col_in = ((4 j) ^ (col_in & 12)) | (kq ^ (col_in & 3)) within the wave's 256-byte k tile
+    const uint32_t xo0 = ((col_in & 12u) | (kq ^ (col_in & 3u))) * 16;
+    uint32_t xa_at[MT][4];
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xa_at[a][j] = (16 * a + col_in) * P::ROWB + (uint32_t)kw * 256 + (xo0 ^ (64u * j));
+    const uint32_t s_at = (uint32_t)wave * wsb + col_in * 2;
+    const int nvalid = (int)s1 - (int)sb < NBW ? (int)s1 - (int)sb : NBW;  // strips of this wave in the block
+
+    v4f acc[MT][NBW];
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int b = 0; b < NBW; ++b) acc[a][b] = (v4f){0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](uint32_t r, int slot, const WTile& t) {
+        const uint8_t* xb = smem + slot * P::SLOT;
+        h2 s2[NBW], o2[NBW];
+#pragma unroll
+        for (int b = 0; b < NBW; ++b) {
+            const uint32_t so = s_at + (r / TPC) * 256 + (r % TPC) * WPT * 4 + 32 * b;
+            const _Float16 sv = *(const _Float16*)(smem + sc_at + so);
+            const _Float16 ov = HAS_OFF ? *(const _Float16*)(smem + of_at + so) : (_Float16)0.0f;
+            s2[b] = (h2){sv, sv};
+            o2[b] = (h2){ov, ov};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            h8 xa[MT];
+#pragma unroll
+            for (int a = 0; a < MT; ++a) xa[a] = *(const h8*)(xb + xa_at[a][j]);
+#pragma unroll
+            for (int b = 0; b < NBW; ++b) {
+                if (b >= nvalid) break;
+                uint32_t w0, w1 = 0;
+                if constexpr (INT4) {
+                    w0 = t.w[b][0][j];
+                } else {
+                    w0 = t.w[b][j >> 1][(j & 1) * 2];
+                    w1 = t.w[b][j >> 1][(j & 1) * 2 + 1];
+                }
+                const h8 bf = dequant8<INT4, HAS_OFF>(w0, w1, o2[b], s2[b], magic);
+#pragma unroll
+                for (int a = 0; a < MT; ++a)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[a], bf, acc[a][b], 0, 0, 0);
+            }
+        }
+    };
+
+    WTile wt[DW];
+    // prologue: the DW - 1 rounds before round 0 as the loop would have issued them (activations of rounds
+    // 0 .. ST - 2, weights of rounds 0 .. DW - 2)
+#pragma unroll
+    for (int q = 0; q < DW - 1; ++q) {
+        if (q >= DW - ST) issue_x((uint32_t)(q - DW + ST), q - DW + ST);
+        load_w((uint32_t)q, wt[q]);
+    }
+    // round r: its stage has landed (this wave's copies: vmcnt; everyone's: the barrier, which also frees the stage
+    // read in round r - 1), then round r + ST - 1 is issued into that freed stage and the weights of round r + DW - 1
+    // into the slot freed by round r - 1; out-of-range rounds read zeros, so the counts stay exact
+    for (uint32_t r0 = 0; r0 < rounds; r0 += DW) {
+#pragma unroll
+        for (int u = 0; u < DW; ++u) {
+            const uint32_t r = r0 + u;
+            if (r < rounds) {
+                __builtin_amdgcn_sched_barrier(0);
+                wait_vmcnt_aq<P::IN_FLIGHT>();
+                __builtin_amdgcn_sched_barrier(0);
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                __builtin_amdgcn_s_barrier();
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                __builtin_amdgcn_sched_barrier(0);
+                issue_x(r + ST - 1, (u + ST - 1) % ST);
+                load_w(r + DW - 1, wt[(u + DW - 1) % DW]);
+                __builtin_amdgcn_sched_barrier(0);
+                compute(r, u % ST, wt[u]);
+            }
+        }
+    }
+    wait_vmcnt_aq<0>();  // no copy may still target LDS when it is reused below or the wave ends
+    __syncthreads();
+
+    if constexpr (KW > 1) {
+        v4f* red = (v4f*)smem;  // [KW - 1][SG][MT][NBW][64]
+        if (kw > 0) {
+#pragma unroll
+            for (int a = 0; a < MT; ++a)
+#pragma unroll
+                for (int b = 0; b < NBW; ++b) red[((((kw - 1) * SG + sg) * MT + a) * NBW + b) * 64 + lane] = acc[a][b];
+        }
+        __syncthreads();
+        if (kw != 0) return;
+#pragma unroll
+        for (int w = 0; w < KW - 1; ++w)
+#pragma unroll
+            for (int a = 0; a < MT; ++a)
+#pragma unroll
+                for (int b = 0; b < NBW; ++b) acc[a][b] += red[(((w * SG + sg) * MT + a) * NBW + b) * 64 + lane];
+    }
+    // D layout: lane holds rows 4 kq + i, column col_in of each 16 x 16 tile
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int b = 0; b < NBW; ++b) {
+            if (b >= nvalid) break;
+            uint16_t* yc = A.y + (sb + b) * 16 + col_in;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t m = 16 * a + 4 * kq + i;
+                if (m < M) y_put(yc + (uint64_t)m * N, f32_to_f16_sat(acc[a][b][i]), A.atomic);
+            }
+        }
+}
+
+// LDS bytes of aq_ring_kernel (0 when the shape does not fit)
+template <int MT, int NBW, int SG, int KW, int ST, int DW>
+inline int64_t aq_ring_lds(int64_t K, bool has_off)
+{
+    using P = AqRing<MT, NBW, SG, KW, ST, DW, true, true>;
+    const int64_t rounds = K / KT / KW, ncp = (rounds + P::TPC - 1) / P::TPC;
+    const int64_t lds = std::max<int64_t>((int64_t)ST * P::SLOT + (int64_t)P::NW * ncp * 256 * (has_off ? 2 : 1), P::RED);
+    return lds <= 160 * 1024 ? lds : 0;
+}
+
+template <int MT, int NBW, int SG, int KW, int ST, int DW>
+static hipError_t launch_aq_ring(uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
+                                 const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, int C, int atomic,
+                                 hipStream_t st)
+{
+    using P4 = AqRing<MT, NBW, SG, KW, ST, DW, true, true>;
+    AqXsArgs A;
+    const int64_t lds = aq_ring_lds<MT, NBW, SG, KW, ST, DW>(K, offset != nullptr);
+    if (M > 16 * MT || (K / KT) % KW != 0 || lds == 0 ||
+        !aq_cols_args(A, y, x, wp, int4, scale, offset, g, M, N, K, C, SG * NBW, atomic))
+        return hipErrorInvalidValue;
+#define AQ_RING_LAUNCH(I4, OF)                                                     \
+    do {                                                                           \
+        constexpr auto kern = aq_ring_kernel<MT, NBW, SG, KW, ST, DW, I4, OF>;      \
+        hipError_t e = ensure_dynamic_lds<kern>((int)lds);                         \
+        if (e != hipSuccess) return e;                                             \
+        launch_k(kern, dim3((unsigned)C), dim3(P4::NT), (uint32_t)lds, st, A);      \
+    } while (0)
+    if (int4) {
+        if (offset) AQ_RING_LAUNCH(true, true);
+        else AQ_RING_LAUNCH(true, false);
+    } else {
+        if (offset) AQ_RING_LAUNCH(false, true);
+        else AQ_RING_LAUNCH(false, false);
+    }
+#undef AQ_RING_LAUNCH
+    return hipGetLastError();
+}
+
+template <int MT, int NS, int KSW, int ST, bool ROT, int DW = ST>
 static void launch_dma(uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
                        const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, int atomic, hipStream_t st)
 {
     const dim3 grid((unsigned)((N / 16 + NS - 1) / NS)), block(NS * KSW * 64);
     const uint8_t* w = (const uint8_t*)wp;
     if (int4) {
-        if (offset) launch_k((aq_dma_kernel<MT, NS, KSW, ST, true, true, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K, atomic);
-        else launch_k((aq_dma_kernel<MT, NS, KSW, ST, true, false, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K, atomic);
+        if (offset) launch_k((aq_dma_kernel<MT, NS, KSW, ST, true, true, ROT, DW>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K, atomic);
+        else launch_k((aq_dma_kernel<MT, NS, KSW, ST, true, false, ROT, DW>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K, atomic);
     } else {
-        if (offset) launch_k((aq_dma_kernel<MT, NS, KSW, ST, false, true, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K, atomic);
-        else launch_k((aq_dma_kernel<MT, NS, KSW, ST, false, false, ROT>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K, atomic);
+        if (offset) launch_k((aq_dma_kernel<MT, NS, KSW, ST, false, true, ROT, DW>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K, atomic);
+        else launch_k((aq_dma_kernel<MT, NS, KSW, ST, false, false, ROT, DW>), grid, block, 0, st, y, x, w, scale, offset, M, N, K, g, K, atomic);
     }
+}
+
+// column blocks for a grid of about `target` workgroups whose blocks hold at most smax strips
+inline int aq_blocks(int64_t NBT, int smax, int target)
+{
+    int64_t C = NBT < target ? NBT : target;
+    if ((NBT + C - 1) / C > smax) C = (NBT + smax - 1) / smax;
+    return (int)C;
 }
 
 // M is processed in chunks of 64 rows (4 m tiles); decode shapes are a single launch.  The packed weight,
@@ -617,31 +1170,43 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
 {
     const int64_t g = group > 0 ? group : K;
     const bool int4 = w_type == DT_INT4;
+    const int64_t NBT = N / 16, KB = K / KT;
+    const bool cols_ok = g % KT == 0 && ((g / KT) & (g / KT - 1)) == 0;  // column-block kernels: group 128 << s
     for (int64_t m0 = 0; m0 < M; m0 += 64) {
         const int64_t mc = (M - m0) < 64 ? (M - m0) : 64;
         const uint16_t* xc = x + m0 * K;
         uint16_t* yc = y + m0 * N;
-        // decode batches (M <= 4): x staged in LDS; int4 with 4 waves x 8 k tiles, int8 (twice the bytes per
-        // element) with 8 waves x 4 tiles, both measured fastest at K = 4096.
-        // Larger batches: x through the LDS ring of aq_dma_kernel (shapes measured fastest at K = 4096,
-        // N = 11008; the 64-row form rotates each workgroup's k order, which measured ~8 % faster there).
-        if (mc <= 4 && mc * K * 2 + 16 <= 48 * 1024) {
-            if (int4) launch_aq<1, 1, 4, 8, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
-            else launch_aq<1, 1, 8, 4, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+        // Column-block kernels (about 256 workgroups of 2 - 4 strips; shapes measured at K = 4096, N = 11008):
+        // M <= 16 with x[0:M, 0:K] resident in LDS, larger batches with x streamed through an LDS ring.  Shapes
+        // they do not take go to the earlier forms: x staged in LDS for decode batches, else the one-strip ring of
+        // aq_dma_kernel (group a multiple of 128) or activations straight from memory.
+        hipError_t e = hipErrorInvalidValue;
+        if (cols_ok && mc <= 16 && KB % 8 == 0 && aq_xs_lds<2, 2, 4, 2>(mc, K, offset != nullptr))
+            e = launch_aq_xs<2, 2, 4, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 4, 256), atomic, st);
+        else if (cols_ok && mc <= 16 && KB % 4 == 0 && aq_xs_lds<2, 2, 4, 1>(mc, K, offset != nullptr))
+            e = launch_aq_xs<2, 2, 4, 1>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 4, 256), atomic, st);
+        else if (cols_ok && mc > 16 && mc <= 32 && KB % 8 == 0 && aq_ring_lds<2, 3, 1, 8, 2, 2>(K, offset != nullptr))
+            e = launch_aq_ring<2, 3, 1, 8, 2, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 3, 256), atomic, st);
+        else if (cols_ok && mc > 32 && KB % 4 == 0 && aq_ring_lds<4, 2, 2, 4, 2, 4>(K, offset != nullptr))
+            e = launch_aq_ring<4, 2, 2, 4, 2, 4>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 4, 172), atomic, st);
+        else {
+            if (mc <= 4 && mc * K * 2 + 16 <= 48 * 1024) {
+                if (int4) launch_aq<1, 1, 4, 8, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+                else launch_aq<1, 1, 8, 4, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+            } else if (mc > 4 && g % KT == 0) {
+                if (mc <= 16) {
+                    if (int4) launch_dma<1, 2, 4, 4, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+                    else launch_dma<1, 2, 4, 3, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+                } else if (mc <= 32) {
+                    launch_dma<2, 4, 4, 4, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+                } else {
+                    launch_dma<4, 4, 2, 3, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+                }
+            } else if (mc <= 16) launch_aq<1, 1, 8, 4>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+            else if (mc <= 32) launch_aq<2, 2, 8, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+            else launch_aq<4, 2, 8, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+            e = hipGetLastError();
         }
-        else if (mc > 4 && g % KT == 0) {
-            if (mc <= 16) {
-                if (int4) launch_dma<1, 2, 4, 4, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
-                else launch_dma<1, 2, 4, 3, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
-            } else if (mc <= 32) {
-                launch_dma<2, 4, 4, 4, false>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
-            } else {
-                launch_dma<4, 4, 2, 3, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
-            }
-        } else if (mc <= 16) launch_aq<1, 1, 8, 4>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
-        else if (mc <= 32) launch_aq<2, 2, 8, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
-        else launch_aq<4, 2, 8, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
-        hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -115,6 +115,35 @@ def test_batch_ring_partial_rounds(ascq_gpu, oracle, w_type, M, K):
 
 
 @pytest.mark.parametrize("w_type", ["int4", "int8"])
+@pytest.mark.parametrize("with_offset", [True, False])
+@pytest.mark.parametrize("M,K,N,group", [
+    (1, 512, 112, 128),      # one k tile per wave: ring slots past the end
+    (7, 1536, 1008, 256),    # 3 tiles per wave, group of two tiles
+    (16, 4096, 4112, 128),   # 257 strips over 256 blocks: one block of two strips
+    (12, 2048, 272, 2048),   # one group over all of K
+    (9, 8192, 112, 128),     # x too large for LDS residency: earlier ring form
+    (17, 1024, 4112, 128),   # 32-row ring, a single round
+    (32, 3072, 1008, 512),
+    (33, 512, 112, 128),     # 64-row ring, a single round
+    (64, 2048, 4112, 256),
+    (50, 4096, 1008, 128),
+])
+def test_column_block_kernels(ascq_gpu, oracle, w_type, with_offset, M, K, N, group):
+    """Column blocks of 1 - 4 strips (sizes within one strip of each other), x resident in LDS (M <= 16) or streamed
+    through an LDS ring (16 < M <= 64), group sizes 128 << s, with and without offset."""
+    rng = seeded(M * 7 + K + N + group)
+    code = O.INT8 if w_type == "int8" else O.INT4
+    at = ascq_gpu.INT8 if w_type == "int8" else ascq_gpu.INT4
+    w, scale, offset = make_weights(rng, K, N, code, group, with_offset)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    wp = ascq_gpu.weight_pack(_dev(w), at, K, N)
+    y = ascq_gpu.antiquant_matmul(_dev(x), wp, at, _dev(scale), None if offset is None else _dev(offset), group, N)
+    _, y_exact, y_abs = O.antiquant_matmul(x.view(np.uint16), w, code, scale.view(np.uint16),
+                                           None if offset is None else offset.view(np.uint16), group, M, N, K)
+    check_close(y.cpu().numpy(), y_exact, y_abs, K)
+
+
+@pytest.mark.parametrize("w_type", ["int4", "int8"])
 @pytest.mark.parametrize("b_format", ["nd", "packed"])
 def test_matmul_handle_antiquant(ascq_gpu, oracle, w_type, b_format):
     """Matmul<half, int8|int4, half> with SetAntiQuantVector (per group) and SetAntiQuantScalar."""
