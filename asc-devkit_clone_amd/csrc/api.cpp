@@ -59,6 +59,17 @@ ascq_status hip_status(hipError_t e, const char* what)
     return fail(ASCQ_E_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+// Per-call state of an entry point that launches kernels: a HIP error left on this thread by an unrelated earlier
+// call is cleared first, so the status the entry point returns is that of its own launches, and launch events armed
+// by ascq_set_launch_events are disarmed on every return -- including argument-check failures that launch nothing,
+// which would otherwise leave them armed for whatever kernel the thread launches next.
+struct CallScope {
+    CallScope() { (void)hipGetLastError(); }
+    ~CallScope() { g_launch_events = ascq::LaunchEvents{}; }
+    CallScope(const CallScope&) = delete;
+    CallScope& operator=(const CallScope&) = delete;
+};
+
 inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 inline bool valid_round(int32_t r) { return r >= ASCQ_ROUND_NONE && r <= ASCQ_ROUND_TRUNC; }
@@ -504,6 +515,7 @@ ascq_status ascq_matmul_set_workspace(ascq_matmul_t h, void* workspace, size_t b
 
 ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic, void* stream)
 {
+    CallScope scope;
     if (!h || !c) return fail(ASCQ_E_INVALID_ARG, "iterate_all: null argument");
     if (en_atomic > 3) return fail(ASCQ_E_INVALID_ARG, "iterate_all: enAtomic must be 0 (store), 1 (add), 2 (max) or 3 (min)");
     // The copy-out combines into C only for the C types SetAtomic takes (scheduler_base.h:484-494: float, half,
@@ -757,6 +769,7 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
 
 ascq_status ascq_matmul_iterate_all_noalloc(ascq_matmul_t h, void* c, uint8_t en_atomic, void* stream)
 {
+    CallScope scope;
     if (!h || !c) return fail(ASCQ_E_INVALID_ARG, "iterate_all_noalloc: null argument");
     const size_t need = workspace_need(h);
     if (need > ASCQ_NOALLOC_SCRATCH_BYTES)
@@ -808,6 +821,7 @@ ascq_status ascq_matmul_destroy(ascq_matmul_t h)
 ascq_status ascq_ascend_quant_per_token(int8_t* dst, const void* src, int32_t src_type, const float* scale,
                                         const float* offset, const ascq_quant_param* para, void* stream)
 {
+    CallScope scope;
     if (!dst || !src || !scale || !para) return fail(ASCQ_E_INVALID_ARG, "quant_per_token: null argument");
     if (src_type != ASCQ_DT_F16 && src_type != ASCQ_DT_BF16 && src_type != ASCQ_DT_F32)
         return fail(ASCQ_E_UNSUPPORTED, "quant_per_token: src must be f16, bf16 or f32");
@@ -830,6 +844,7 @@ ascq_status ascq_ascend_quant_policy(void* dst, int32_t dst_type, const void* sr
                                      const void* scale, const void* offset, float offset_scalar, int32_t scale_type,
                                      int32_t policy, const ascq_quant_param* para, void* stream)
 {
+    CallScope scope;
     if (!para) return fail(ASCQ_E_INVALID_ARG, "ascend_quant_policy: null argument");
     const auto fp_type = [](int32_t t) { return t == ASCQ_DT_F16 || t == ASCQ_DT_BF16 || t == ASCQ_DT_F32; };
     if (!fp_type(src_type)) return fail(ASCQ_E_UNSUPPORTED, "ascend_quant_policy: src must be f16, bf16 or f32");
@@ -868,6 +883,7 @@ ascq_status ascq_ascend_quant_policy(void* dst, int32_t dst_type, const void* sr
 ascq_status ascq_ascend_quant_dynamic_per_token(int8_t* dst, float* scale_out, const void* src, int32_t src_type,
                                                 uint32_t m, uint32_t n, int32_t round_mode, void* stream)
 {
+    CallScope scope;
     if (!dst || !scale_out || !src) return fail(ASCQ_E_INVALID_ARG, "quant_dynamic_per_token: null argument");
     if (src_type != ASCQ_DT_F16 && src_type != ASCQ_DT_BF16 && src_type != ASCQ_DT_F32)
         return fail(ASCQ_E_UNSUPPORTED, "quant_dynamic_per_token: src must be f16, bf16 or f32");
@@ -881,6 +897,7 @@ ascq_status ascq_ascend_quant(void* dst, int32_t dst_type, const void* src, int3
                               const void* offset, float scale_scalar, float offset_scalar, uint32_t cal_count,
                               uint32_t scale_count, void* stream)
 {
+    CallScope scope;
     if (src_type != ASCQ_DT_F16 && src_type != ASCQ_DT_BF16 && src_type != ASCQ_DT_F32)
         return fail(ASCQ_E_UNSUPPORTED, "ascend_quant: src must be f16, bf16 or f32");
     if (dst_type != ASCQ_DT_INT8 && dst_type != ASCQ_DT_HIF8 && dst_type != ASCQ_DT_FP8_E4M3 &&
@@ -927,6 +944,7 @@ ascq_status ascq_ascend_dequant(void* dst, int32_t dst_type, const void* src, in
                                 int32_t scale_type, float scale_scalar, int32_t policy, int32_t mode,
                                 const ascq_dequant_param* params, void* stream)
 {
+    CallScope scope;
     if (!params) return fail(ASCQ_E_INVALID_ARG, "ascend_dequant: null params");
     if (dst_type != ASCQ_DT_F16 && dst_type != ASCQ_DT_BF16 && dst_type != ASCQ_DT_F32)
         return fail(ASCQ_E_UNSUPPORTED, "ascend_dequant: dst must be f16, bf16 or f32");
@@ -975,6 +993,7 @@ ascq_status ascq_ascend_dequant_policy(void* dst, int32_t dst_type, const void* 
                                        const void* scale, const void* offset, int32_t scale_type, int32_t policy,
                                        const ascq_dequant_policy_param* para, void* stream)
 {
+    CallScope scope;
     (void)offset;  // never read by the reference's policy kernels (ascend_dequant_3510_impl.h:254-598)
     if (!para) return fail(ASCQ_E_INVALID_ARG, "ascend_dequant_policy: null argument");
     if (dst_type != ASCQ_DT_F16 && dst_type != ASCQ_DT_BF16 && dst_type != ASCQ_DT_F32)
@@ -1009,6 +1028,7 @@ ascq_status ascq_ascend_antiquant(void* dst, int32_t dst_type, const void* src, 
                                   const void* scale, uint32_t k, uint32_t n, uint32_t group_size, int32_t is_transpose,
                                   int32_t arith, void* stream)
 {
+    CallScope scope;
     if (!dst || !src || !scale) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant: null argument");
     if (dst_type != ASCQ_DT_F16 && dst_type != ASCQ_DT_BF16)
         return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant: dst must be f16 or bf16");
@@ -1032,6 +1052,7 @@ ascq_status ascq_ascend_antiquant_scalar(void* dst, int32_t dst_type, const void
                                          uint16_t offset, uint16_t scale, int32_t has_offset, uint64_t count,
                                          void* stream)
 {
+    CallScope scope;
     if (dst_type != ASCQ_DT_F16 && dst_type != ASCQ_DT_BF16)
         return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_scalar: dst must be f16 or bf16");
     if (src_type != ASCQ_DT_INT8 && src_type != ASCQ_DT_INT4 && src_type != ASCQ_DT_HIF8 &&
@@ -1053,6 +1074,7 @@ ascq_status ascq_ascend_antiquant_policy(void* dst, int32_t dst_type, const void
                                          int64_t m, int64_t n, int64_t group_size, int32_t k_dim, int32_t is_transpose,
                                          void* stream)
 {
+    CallScope scope;
     if (m < 0 || n < 0) return fail(ASCQ_E_INVALID_ARG, "ascend_antiquant_policy: negative shape");
     if (policy != ASCQ_POLICY_PER_TOKEN && policy != ASCQ_POLICY_PER_GROUP)
         return fail(ASCQ_E_UNSUPPORTED, "ascend_antiquant_policy: policy must be PER_TOKEN or PER_GROUP");
@@ -1103,6 +1125,7 @@ ascq_status ascq_weight_pack_size(int32_t w_type, int64_t k, int64_t n, size_t* 
 ascq_status ascq_weight_pack(void* packed, const void* w, int32_t w_type, int64_t k, int64_t n, int32_t is_transpose,
                              void* stream)
 {
+    CallScope scope;
     size_t bytes = 0;
     ascq_status s = ascq_weight_pack_size(w_type, k, n, &bytes);
     if (s != ASCQ_OK) return s;
@@ -1115,6 +1138,7 @@ ascq_status ascq_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w_
                                   const uint16_t* scale, const uint16_t* offset, int64_t group_size, int64_t m,
                                   int64_t n, int64_t k, void* stream)
 {
+    CallScope scope;
     if (!y || !x || !w_packed || !scale) return fail(ASCQ_E_INVALID_ARG, "antiquant_matmul: null argument");
     if (w_type != ASCQ_DT_INT8 && w_type != ASCQ_DT_INT4) return fail(ASCQ_E_UNSUPPORTED, "antiquant_matmul: int8 or int4");
     if (m <= 0 || n <= 0 || k <= 0) return fail(ASCQ_E_INVALID_ARG, "antiquant_matmul: shape must be positive");
@@ -1141,6 +1165,7 @@ ascq_status ascq_quant_group_matmul(void* y, int32_t out_type, const int8_t* x, 
                                     int32_t list_type, int64_t num_groups, int64_t m, int64_t k, int64_t n,
                                     int32_t activation, void* stream)
 {
+    CallScope scope;
     if (!y || !x || !per_token_scale || !w || !scale || !group_list)
         return fail(ASCQ_E_INVALID_ARG, "quant_group_matmul: null argument");
     if (out_type != ASCQ_DT_BF16 && out_type != ASCQ_DT_F16)
@@ -1211,6 +1236,7 @@ size_t ascq_nz_size(int32_t dtype, int64_t batch, int64_t rows, int64_t cols)
 ascq_status ascq_nz_to_nd(void* dst, const void* src, int32_t dtype, int64_t batch, int64_t rows, int64_t cols,
                           int32_t transpose_out, void* stream)
 {
+    CallScope scope;
     ascq_status s = check_nz_args("nz_to_nd", dst, src, dtype, batch, rows, cols);
     if (s != ASCQ_OK) return s;
     if (transpose_out && elem_bytes(dtype) != 1)
@@ -1223,6 +1249,7 @@ ascq_status ascq_nz_to_nd(void* dst, const void* src, int32_t dtype, int64_t bat
 ascq_status ascq_nd_to_nz(void* dst, const void* src, int32_t dtype, int64_t batch, int64_t rows, int64_t cols,
                           void* stream)
 {
+    CallScope scope;
     ascq_status s = check_nz_args("nd_to_nz", dst, src, dtype, batch, rows, cols);
     if (s != ASCQ_OK) return s;
     return hip_status(ascq::launch_nd_to_nz(dst, src, elem_bytes(dtype), batch, rows, cols, S(stream)), "nd_to_nz");

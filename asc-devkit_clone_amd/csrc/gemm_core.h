@@ -179,14 +179,17 @@ struct CoreArgs {
     int32_t rows, cols;   // valid rows of A / columns of B in this tile (from the tile origin)
     uint32_t a0, b0;      // byte offsets of the tile origin in the A / B buffers
     int64_t kbytes;       // K extent in bytes (int8, fp8: K; fp4: K/2); a multiple of 16
-    // MX scales, stage-major: the SCB bytes of (stage s, row r) = blocks SCB s .. SCB s + SCB - 1 of row r, at
-    // byte (s * rows + r) * SCB
-    rsrc_t sa, sb;
+    // MX auxiliary data, all read through the one resource `aux` (so a copy's source differs between waves only in
+    // its offset, and the copy code needs no branches): the stage-major scales -- the SCB bytes of (stage s, row r)
+    // = blocks SCB s .. SCB s + SCB - 1 of row r, at byte sa_base + (s * rows + r) * SCB for A, sb_base + ... for
+    // B -- and, for fp6, the Q planes
+    rsrc_t aux;
+    uint32_t sa_base, sb_base;  // byte offsets of the A / B stage-major scales in aux
     uint32_t sa0_row, sb0_row;  // first row / column index of the tile
     uint32_t sa_rows, sb_rows;  // M / N: the stage stride in rows
     uint32_t sk;                // scale blocks per row (sK, a multiple of SCB)
-    // fp6 Q planes (OP_MXFP6), read through the a / b resources (each plane follows its P plane in one buffer):
-    // byte offset of the tile's first 32-row group in stage 0, and the stage stride (1 KiB x groups)
+    // fp6 Q planes (OP_MXFP6) in aux: byte offset of the tile's first 32-row group in stage 0, and the stage stride
+    // (1 KiB x groups)
     uint32_t qa_off, qa_stride, qb_off, qb_stride;
 };
 
@@ -218,8 +221,9 @@ struct GemmCore {
     static constexpr int SC_ROWS = 1024 / SCB;        // rows whose stage scales fill one 1 KiB copy
     // MX scales, stage-major in memory ([sK/SCB][rows][SCB]): the scale bytes of SC_ROWS consecutive rows for
     // one stage are 1 KiB contiguous, one wave-wide 16-byte copy.  SA_REG / SB_REG: the A / B scale regions
-    // of a stage.  Every wave issues SC_COPIES copies; those past the real ones read out of range into a
-    // dummy area, so the per-wave copy count (and with it the vmcnt threshold) is the same for all waves.
+    // of a stage.  Every wave issues SC_COPIES copies, so the per-wave copy count (and with it the vmcnt
+    // threshold) is the same for all waves; copies past the real ones repeat a real one (the same bytes to the
+    // same LDS address, harmless), so no wave needs a dummy destination.
     // fp6 (split planes): the P plane (dwords 0-3 of each block's six) is the operand the copies above stage, ROWB
     // bytes per row like fp4; the Q plane (dwords 4-5) arrives as 1 KiB blocks per (stage, 32-row group) holding
     // the 8-byte pieces of the group's 32 rows block by block ([4 blocks][32 rows][8 bytes] for ROWB = 64), one
@@ -234,13 +238,12 @@ struct GemmCore {
     static constexpr int AUX_INSTR = SA_INSTR + SB_INSTR + QA_INSTR + QB_INSTR;
     static constexpr int SC_COPIES = (AUX_INSTR + NW - 1) / NW;
     static constexpr int SC_BYTES = SA_REG + SB_REG;
-    static constexpr int DUMMY_BYTES = IS_MX && SC_COPIES * NW > AUX_INSTR ? 1024 : 0;
     static constexpr int COPIES = A_COPIES + B_COPIES + SC_COPIES;
     static constexpr int B_BLK = B_KCONTIG ? 0 : (ROWB / 8) * (BN / 4) / NT;  // 8x4-byte blocks per lane
     static constexpr int B_LOADS = 8 * B_BLK;         // dword loads per lane per stage for a [K, N] B
     static constexpr int STAGE = (BM + BN) * ROWB + Q_REG + SC_BYTES;
     static constexpr int SC_OFF = (BM + BN) * ROWB + Q_REG;  // the scale regions within a stage
-    static constexpr size_t LDS_BYTES = (size_t)STAGES * STAGE + DUMMY_BYTES;
+    static constexpr size_t LDS_BYTES = (size_t)STAGES * STAGE;
     // vmem operations of this wave issued after stage kt's copies, at the top of iteration kt
     static constexpr int IN_FLIGHT = (STAGES - 2) * (COPIES + B_LOADS);
     // copies issued before each k-step of a stage (ILV false: all before the first)
@@ -343,6 +346,39 @@ struct GemmCore {
             }
         };
 
+        // MX auxiliary copies of this wave (A scales, B scales, then the fp6 Q blocks of A and of B): their source
+        // (offset in p.aux at stage 0, stride per stage) and LDS offset within a stage depend on the wave only, so
+        // they are worked out here, once.  The main loop then issues them with no branches: a branch there splits
+        // the loop body into blocks, and the compiler sinks each stage's MFMAs (pure operations to it) past the
+        // next stage's barrier, which leaves every SIMD without MFMA work between the two barriers.
+        struct AuxCopy {
+            uint32_t base, stride, dst;
+        };
+        AuxCopy aux[IS_MX ? SC_COPIES : 1];
+        if constexpr (IS_MX) {
+#pragma unroll
+            for (int v = 0; v < SC_COPIES; ++v) {
+                const int g = (wave * SC_COPIES + v) % AUX_INSTR;  // wave-uniform; past the real copies: a repeat
+                const int q = g - SA_INSTR - SB_INSTR;
+                if (g < SA_INSTR)
+                    aux[v] = {p.sa_base + (p.sa0_row + (uint32_t)(g * SC_ROWS)) * SCB, p.sa_rows * SCB,
+                              (uint32_t)(SC_OFF + g * 1024)};
+                else if (q < 0)
+                    aux[v] = {p.sb_base + (p.sb0_row + (uint32_t)((g - SA_INSTR) * SC_ROWS)) * SCB, p.sb_rows * SCB,
+                              (uint32_t)(SC_OFF + SA_REG + (g - SA_INSTR) * 1024)};
+                // (Q groups past the operand's last belong to rows past M / N, whose outputs are dropped: they read
+                // the next stage's first groups, or other data past the plane)
+                else if (q < QA_INSTR)
+                    aux[v] = {p.qa_off + (uint32_t)(q * 1024), p.qa_stride, (uint32_t)((BM + BN) * ROWB + q * 1024)};
+                else
+                    aux[v] = {p.qb_off + (uint32_t)((q - QA_INSTR) * 1024), p.qb_stride,
+                              (uint32_t)((BM + BN) * ROWB + q * 1024)};
+                aux[v].base = __builtin_amdgcn_readfirstlane(aux[v].base);
+                aux[v].stride = __builtin_amdgcn_readfirstlane(aux[v].stride);
+                aux[v].dst = __builtin_amdgcn_readfirstlane(aux[v].dst);
+            }
+        }
+
         // copy u (0 <= u < COPIES) of stage kt into slot: A rows, then B rows, then MX scale blocks
         auto issue_copy = [&](int64_t kt, int slot, int u) {
             uint8_t* sA = smem + slot * STAGE;
@@ -362,32 +398,9 @@ struct GemmCore {
                 const uint32_t off = (row < p.cols && k < p.kbytes) ? p.b0 + (uint32_t)row * p.ldb + (uint32_t)k : OOB;
                 copy16_to_lds(p.b, sB + row0 * ROWB, off);
             } else if constexpr (IS_MX) {
-                uint8_t* sS = sA + SC_OFF;
+                const AuxCopy& x = aux[u - A_COPIES - B_COPIES];
                 const bool kval = (uint32_t)(kt * SCB) < p.sk;
-                const int g = wave * SC_COPIES + (u - A_COPIES - B_COPIES);  // wave-uniform
-                if (g >= SA_INSTR + SB_INSTR && g < AUX_INSTR) {  // fp6 Q blocks of A, then of B
-                    const int q = g - SA_INSTR - SB_INSTR;
-                    uint8_t* sQ = sA + (BM + BN) * ROWB;
-                    // (groups past the operand's last belong to rows past M / N, whose outputs are dropped: they read
-                    // the next stage's first groups, or zeros past the buffer)
-                    if (q < QA_INSTR)
-                        copy16_to_lds(p.a, sQ + q * 1024,
-                                      kval ? (uint32_t)kt * p.qa_stride + p.qa_off + (uint32_t)(q * 1024 + lane * 16) : OOB);
-                    else
-                        copy16_to_lds(p.b, sQ + q * 1024,
-                                      kval ? (uint32_t)kt * p.qb_stride + p.qb_off + (uint32_t)((q - QA_INSTR) * 1024 + lane * 16)
-                                           : OOB);
-                } else if (g < SA_INSTR) {
-                    const uint32_t off =
-                        kval ? ((uint32_t)kt * p.sa_rows + p.sa0_row + g * SC_ROWS) * SCB + lane * 16 : OOB;
-                    copy16_to_lds(p.sa, sS + g * 1024, off);
-                } else if (g < SA_INSTR + SB_INSTR) {
-                    const uint32_t off =
-                        kval ? ((uint32_t)kt * p.sb_rows + p.sb0_row + (g - SA_INSTR) * SC_ROWS) * SCB + lane * 16 : OOB;
-                    copy16_to_lds(p.sb, sS + SA_REG + (g - SA_INSTR) * 1024, off);
-                } else if (g >= AUX_INSTR) {
-                    copy16_to_lds(p.sa, smem + STAGES * STAGE, OOB);
-                }
+                copy16_to_lds(p.aux, sA + x.dst, kval ? x.base + (uint32_t)kt * x.stride + (uint32_t)(lane * 16) : OOB);
             }
         };
         auto issue_copies = [&](int64_t kt, int slot) {

@@ -11,8 +11,8 @@
 // FP4 (cbsz = blgp = 4): per lane 32 E2M1 values (16 bytes, one MX block) of row (lane % 32) at k block
 // (lane / 32), and one E8M0 scale byte for that (row, block) -- the hardware applies 2^(e-127) per 32-element
 // block, which is exactly the MX product.  Two fp4 per byte, even k in the low nibble: the reference packing
-// (gen_data.py:25-34) is also the MFMA's nibble order.  Block tile 256 x 256, 128 fp4 of K per stage, four
-// stages, 8 waves (4 x 2), wave tile 64 x 128.  The E8M0 scales, rearranged
+// (gen_data.py:25-34) is also the MFMA's nibble order.  Block tile 256 x 256, 256 fp4 of K per stage (128-byte
+// rows, four k-steps per barrier), two stages, 8 waves (4 x 2), wave tile 64 x 128.  The E8M0 scales, rearranged
 // stage-major by mx_scale_stage_major_kernel, ride in the same LDS stage.  B stored [K, N]
 // (the reference's non-transposed layout, two fp4 per byte along N) is first transposed to [N, K] in a
 // workspace by fp4_transpose_kernel.
@@ -24,18 +24,20 @@
 // (lane / 32), packed 6 bits each (element i at bits 6i .. 6i + 5 of six registers: the layout measured for the
 // fp6 operand matches fp4's lane / block assignment).  The six registers are split into two planes so the P
 // plane (registers 0-3) is staged exactly like fp4 and the Q plane (registers 4-5) rides in 1 KiB blocks like
-// the scales; 3 stages of 256 x 256 (51200 bytes each) fit the 160 KiB of LDS.
+// the scales; four stages of 256 x 128 fit the 160 KiB of LDS.
 //
 // MX-FP8 uses the same instruction with fp8 format codes: per lane 32 fp8 of one row (32 bytes, two register
 // quads; MX block b of a k-step is quad b of all 64 lanes, see gemm_core.h);
-// 64 fp8 of K per 64-byte stage row (one k-step, a 16-bit pair of scales per row), four stages of 256 x 256
-// (128-byte stages spill the copy offsets at 256 VGPRs).  A [K, N] fp8 B is transposed to [N, K] by the byte
-// transpose first.
+// 128 fp8 of K per 128-byte stage row (two k-steps, a 32-bit word of scales per row), two stages of 256 x 256.
+// A [K, N] fp8 B is transposed to [N, K] by the byte transpose first.
 #include "common.h"
 #include "gemm_core.h"
 #include "launch.h"
 
 namespace ascq {
+
+// scale blocks per row in the stage-major copies: sK rounded up to whole groups of the largest stage (8 blocks)
+__host__ __device__ inline int64_t sk_stage_major(int64_t K) { return ((K + 63) / 64 * 2 + 7) / 8 * 8; }
 
 template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true>
 __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, const uint8_t* __restrict__ sa_sm,
@@ -51,28 +53,28 @@ __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, con
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     const int64_t sK = (K + 63) / 64 * 2;
     CoreArgs c{};
-    if constexpr (OP == OP_MXFP6) {  // P and Q planes in one buffer per operand (launch_mx_gemm checks the layout)
-        const uint32_t qa0 = (uint32_t)(p.Aq - p.A), qb0 = (uint32_t)(p.Bq - p.B);
-        const uint32_t ga = (uint32_t)((M + 31) / 32), gb = (uint32_t)((N + 31) / 32);
-        c.a = make_rsrc(p.A, qa0 + (uint32_t)(K / 128) * ga * 1024u);
-        c.b = make_rsrc(p.B, qb0 + (uint32_t)(K / 128) * gb * 1024u);
-        c.qa_stride = ga * 1024u;
-        c.qb_stride = gb * 1024u;
-        c.qa_off = qa0 + (uint32_t)(m0 / 32) * 1024u;
-        c.qb_off = qb0 + (uint32_t)(n0 / 32) * 1024u;
-    } else {
-        c.a = make_rsrc(p.A, (uint32_t)(M * KB));
-        c.b = make_rsrc(p.B, (uint32_t)(N * KB));
-    }
+    c.a = make_rsrc(p.A, (uint32_t)(M * KB));
+    c.b = make_rsrc(p.B, (uint32_t)(N * KB));
     c.lda = c.ldb = (uint32_t)KB;
     c.rows = (int32_t)(M - m0 < BM ? M - m0 : BM);
     c.cols = (int32_t)(N - n0 < BN ? N - n0 : BN);
     c.a0 = (uint32_t)(m0 * KB);
     c.b0 = (uint32_t)(n0 * KB);
     c.kbytes = KB;
-    // the stage-major scale buffers carry 16 bytes of slack: a 16-byte copy at the end never straddles the range
-    c.sa = make_rsrc(sa_sm, (uint32_t)(M * sK + 16));
-    c.sb = make_rsrc(sb_sm, (uint32_t)(N * sK + 16));
+    // One resource over every auxiliary region (launch_mx_gemm checks the layout): the stage-major scales (which
+    // carry 16 bytes of slack, so a 16-byte copy at the end never straddles the range) and, for fp6, the Q planes
+    // before them: [Aq][P plane of B][Bq][scales of A][scales of B].
+    const uint8_t* aux = OP == OP_MXFP6 ? p.Aq : sa_sm;
+    c.aux = make_rsrc(aux, (uint32_t)(sb_sm - aux) + (uint32_t)(N * sk_stage_major(K) + 16));
+    c.sa_base = (uint32_t)(sa_sm - aux);
+    c.sb_base = (uint32_t)(sb_sm - aux);
+    if constexpr (OP == OP_MXFP6) {
+        const uint32_t ga = (uint32_t)((M + 31) / 32), gb = (uint32_t)((N + 31) / 32);
+        c.qa_stride = ga * 1024u;
+        c.qb_stride = gb * 1024u;
+        c.qa_off = (uint32_t)(m0 / 32) * 1024u;
+        c.qb_off = (uint32_t)(p.Bq - p.Aq) + (uint32_t)(n0 / 32) * 1024u;
+    }
     c.sa0_row = (uint32_t)m0;
     c.sb0_row = (uint32_t)n0;
     c.sa_rows = (uint32_t)M;
@@ -196,8 +198,10 @@ hipError_t launch_fp4_to_fp6_planes(uint8_t* P, uint8_t* Q, const uint8_t* src, 
 }
 
 // E8M0 scales -> the stage-major layout the kernel reads: the SCB bytes of (group g, row r) are blocks
-// SCB g .. SCB g + SCB - 1 of row r, at byte (g * R + r) * SCB.  src_layout 0: [R, sK] row-major; 1: [sK/2, R, 2]
-// (pairs of blocks, rows inner).  One thread per (group, row).
+// SCB g .. SCB g + SCB - 1 of row r, at byte (g * R + r) * SCB, for ceil(sK / SCB) groups; blocks past sK (the
+// K tail of a stage, whose elements the GEMM reads as zeros) get the scale 127 = 2^0, so no NaN code (0xFF)
+// meets them.  src_layout 0: [R, sK] row-major; 1: [sK/2, R, 2] (pairs of blocks, rows inner).  sK is even.
+// One thread per (group, row).
 // Both operands' scales in one launch (the rearrangement of one operand is ~2 MB at 8192 x 8192 and costs little
 // beyond its launch): workgroups [0, blocks_a) rearrange A, the rest B.
 struct ScaleJob {
@@ -218,28 +222,24 @@ __global__ __launch_bounds__(256) void mx_scale_stage_major_kernel(ScaleJob ja, 
     const int64_t R = j.R;
     const int src_layout = j.src_layout;
     const int64_t bid = is_a ? blockIdx.x : blockIdx.x - blocks_a, nb = is_a ? blocks_a : gridDim.x - blocks_a;
-    const int64_t groups = sK / SCB, total = groups * R;
+    const int64_t groups = (sK + SCB - 1) / SCB, total = groups * R;
+    const uint16_t* s16 = (const uint16_t*)src;
+    // the 16-bit pair of blocks (b, b + 1), b even; past sK the neutral scale
+    auto pair = [&](int64_t b, int64_t r) -> uint32_t {
+        if (b >= sK) return 0x7F7Fu;
+        return src_layout == 0 ? *(const uint16_t*)(src + r * sK + b) : s16[(b / 2) * R + r];
+    };
     for (int64_t i = bid * 256 + threadIdx.x; i < total; i += nb * 256) {
         const int64_t g = i / R, r = i % R;
-        if constexpr (SCB == 2) {  // one 16-bit pair of blocks (2g, 2g + 1); layout 1 stores exactly those pairs
-            ((uint16_t*)dst)[i] = src_layout == 0 ? *(const uint16_t*)(src + r * sK + 2 * g)
-                                                  : ((const uint16_t*)src)[g * R + r];
-            continue;
-        }
-        uint32_t w[SCB / 4 > 0 ? SCB / 4 : 1];
-        if (src_layout == 0) {
-#pragma unroll
-            for (int q = 0; q < SCB / 4; ++q) w[q] = *(const uint32_t*)(src + r * sK + SCB * g + 4 * q);
+        if constexpr (SCB == 2) {
+            ((uint16_t*)dst)[i] = (uint16_t)pair(2 * g, r);
         } else {
-            const uint16_t* s16 = (const uint16_t*)src;
 #pragma unroll
             for (int q = 0; q < SCB / 4; ++q) {
-                const int64_t p0 = (SCB * g + 4 * q) / 2;  // pair index of block SCB g + 4 q
-                w[q] = (uint32_t)s16[p0 * R + r] | ((uint32_t)s16[(p0 + 1) * R + r] << 16);
+                const int64_t b = SCB * g + 4 * q;
+                ((uint32_t*)dst)[i * (SCB / 4) + q] = pair(b, r) | (pair(b + 2, r) << 16);
             }
         }
-#pragma unroll
-        for (int q = 0; q < SCB / 4; ++q) ((uint32_t*)dst)[i * (SCB / 4) + q] = w[q];
     }
 }
 
@@ -247,7 +247,7 @@ template <int SCB>
 static hipError_t launch_scale_stage_major(const ScaleJob& a, const ScaleJob& b, int64_t sK, hipStream_t st)
 {
     const auto blocks_for = [&](int64_t R) {
-        int64_t n = (R * (sK / SCB) + 255) / 256;
+        int64_t n = (R * ((sK + SCB - 1) / SCB) + 255) / 256;
         return n > 32768 ? (int64_t)32768 : (n < 1 ? (int64_t)1 : n);
     };
     const int64_t ba = blocks_for(a.R), bb = blocks_for(b.R);
@@ -258,8 +258,8 @@ static hipError_t launch_scale_stage_major(const ScaleJob& a, const ScaleJob& b,
 
 size_t mx_scale_workspace_bytes(int64_t M, int64_t N, int64_t K)
 {
-    const int64_t sK = (K + 63) / 64 * 2;
-    return (size_t)((M * sK + 16 + 255) / 256 * 256 + (N * sK + 16 + 255) / 256 * 256);
+    const int64_t sKp = sk_stage_major(K);
+    return (size_t)((M * sKp + 16 + 255) / 256 * 256 + (N * sKp + 16 + 255) / 256 * 256);
 }
 
 template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true>
@@ -269,7 +269,7 @@ static hipError_t launch_mx_tiled(const MxGemmArgs& a, hipStream_t st)
     constexpr int SCB = T::SCB;
     const int64_t sK = (a.K + 63) / 64 * 2;
     uint8_t* sa_sm = a.ws_scales;
-    uint8_t* sb_sm = a.ws_scales + (a.M * sK + 16 + 255) / 256 * 256;
+    uint8_t* sb_sm = a.ws_scales + (a.M * sk_stage_major(a.K) + 16 + 255) / 256 * 256;
     hipError_t e = launch_scale_stage_major<SCB>(ScaleJob{sa_sm, a.sA, a.M, a.sa_layout == 1 ? 1 : 0},
                                                  ScaleJob{sb_sm, a.sB, a.N, a.sb_layout == 0 ? 1 : 0}, sK, st);
     if (e != hipSuccess) return e;
@@ -285,7 +285,7 @@ template <int FMT>
 static hipError_t launch_mx_f8(const MxGemmArgs& a, hipStream_t st)
 {
     const bool big = a.M >= 1024 && a.N >= 1024;
-    if (big) return launch_mx_tiled<256, 256, 4, 2, 4, 64, OP_MXF8, FMT>(a, st);
+    if (big) return launch_mx_tiled<256, 256, 4, 2, 2, 128, OP_MXF8, FMT>(a, st);
     return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXF8, FMT>(a, st);
 }
 
@@ -298,17 +298,22 @@ hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st)
     // (the epilogue addresses a 256-row output tile with 32-bit offsets: N < 2^21)
     if (a.K % (fp4 || fp6 ? 128 : 64) != 0 || !a.ws_scales || a.N >= (1ll << 21)) return hipErrorInvalidValue;
     const bool big = a.M >= 1024 && a.N >= 1024;
+    {
+        // the auxiliary regions the kernel reads through one resource: (fp6) Aq < Bq < the scale workspace, all
+        // within 2 GiB of the first
+        const uint8_t* base = fp6 ? a.Aq : a.ws_scales;
+        if (fp6 && (!a.Aq || !a.Bq || a.Bq - a.Aq < (int64_t)fp6_q_plane_bytes(a.M, a.K) ||
+                    a.ws_scales - a.Bq < (int64_t)fp6_q_plane_bytes(a.N, a.K)))
+            return hipErrorInvalidValue;
+        if ((a.ws_scales - base) + (int64_t)mx_scale_workspace_bytes(a.M, a.N, a.K) >= (1ll << 31))
+            return hipErrorInvalidValue;
+    }
     if (fp6) {
-        // each Q plane follows its P plane in one buffer below 2 GiB (one buffer resource covers both)
-        const auto fits = [&](const uint8_t* p, const uint8_t* q, int64_t R) {
-            return q && q - p >= R * (a.K / 2) && (q - p) + (int64_t)fp6_q_plane_bytes(R, a.K) < (1ll << 31);
-        };
-        if (!fits(a.A, a.Aq, a.M) || !fits(a.B, a.Bq, a.N)) return hipErrorInvalidValue;
         if (big) return launch_mx_tiled<256, 128, 4, 2, 4, 64, OP_MXFP6, 0>(a, st);
         return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP6, 0>(a, st);
     }
     if (fp4) {
-        if (big) return launch_mx_tiled<256, 256, 4, 2, 4, 64, OP_MXFP4, 0>(a, st);
+        if (big) return launch_mx_tiled<256, 256, 4, 2, 2, 128, OP_MXFP4, 0>(a, st);
         return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP4, 0>(a, st);
     }
     switch (a.fmt_a | (a.fmt_b << 3)) {

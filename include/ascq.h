@@ -98,7 +98,10 @@ int32_t ascq_device_count(void);
 /* Kernel timing hook, no counterpart in the reference (for benchmarks and profilers that need a kernel's own
  * duration without marker packets between kernels): start / stop are hipEvent_t handles (both or neither); the
  * next entry point called on this thread records them at the start and end of its main kernel's dispatch
- * (hipExtLaunchKernelGGL), then the hook clears itself. */
+ * (hipExtLaunchKernelGGL), then the hook clears itself.  Every entry point that launches kernels disarms the hook
+ * when it returns, also when it fails its argument checks and launches nothing.  Where one call runs its main
+ * kernel more than once (ascq_antiquant_matmul and a weight-only IterateAll with M > 64 go in 64-row chunks), the
+ * events time the first launch only. */
 ascq_status ascq_set_launch_events(void* start, void* stop);
 
 /* Pack an fp32 multiplier, a 9-bit offset and the sign flag into a QUANT_PRE word
