@@ -24,7 +24,7 @@
 // (lane / 32), packed 6 bits each (element i at bits 6i .. 6i + 5 of six registers: the layout measured for the
 // fp6 operand matches fp4's lane / block assignment).  The six registers are split into two planes so the P
 // plane (registers 0-3) is staged exactly like fp4 and the Q plane (registers 4-5) rides in 1 KiB blocks like
-// the scales; four stages of 256 x 128 fit the 160 KiB of LDS.
+// the scales; three stages of 256 x 256 (50 KiB each) fit the 160 KiB of LDS.
 //
 // MX-FP8 uses the same instruction with fp8 format codes: per lane 32 fp8 of one row (32 bytes, two register
 // quads; MX block b of a k-step is quad b of all 64 lanes, see gemm_core.h);
@@ -309,7 +309,7 @@ hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st)
             return hipErrorInvalidValue;
     }
     if (fp6) {
-        if (big) return launch_mx_tiled<256, 128, 4, 2, 4, 64, OP_MXFP6, 0>(a, st);
+        if (big) return launch_mx_tiled<256, 256, 4, 2, 3, 64, OP_MXFP6, 0>(a, st);
         return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP6, 0>(a, st);
     }
     if (fp4) {
