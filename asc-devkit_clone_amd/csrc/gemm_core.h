@@ -194,11 +194,17 @@ struct CoreArgs {
 };
 
 // FMT (fp8 ops): f8f6f4 format code of A in bits 0-2 and of B in bits 3-5
-template <int BM, int BN, int WM, int WN, int STAGES, bool B_KCONTIG, int OP, int ROWB_ = 64, int FMT = 0, bool ILV = true>
+// CT (int8 only): the MFMA takes the B fragment as its first operand and the A fragment as its second, so each
+// 32 x 32 accumulator holds the transposed block: lane l, register r = 4 q + e holds row (l % 32) and column
+// 8 q + 4 (l / 32) + e -- four consecutive columns of one row per register quad, which an epilogue stores as one
+// vector (no LDS round trip); ct_row / ct_col give the coordinates.
+template <int BM, int BN, int WM, int WN, int STAGES, bool B_KCONTIG, int OP, int ROWB_ = 64, int FMT = 0, bool ILV = true,
+          bool CT = false>
 struct GemmCore {
     static constexpr bool IS_MX = OP == OP_MXFP4 || OP == OP_MXF8 || OP == OP_MXFP6;
     static constexpr bool IS_F8 = OP == OP_F8 || OP == OP_MXF8;
     static constexpr bool IS_FP6 = OP == OP_MXFP6;
+    static_assert(!CT || OP == OP_I8, "transposed accumulators: int8 only");
     static constexpr int CBSZ = OP == OP_MXFP4 ? F8F6F4_E2M1 : (IS_FP6 ? F8F6F4_E2M3 : (FMT & 7));
     static constexpr int BLGP = OP == OP_MXFP4 ? F8F6F4_E2M1 : (IS_FP6 ? F8F6F4_E2M3 : ((FMT >> 3) & 7));
     static constexpr int TBM = BM, TBN = BN, TWN = WN;  // the tile shape, for code outside the template
@@ -267,6 +273,12 @@ struct GemmCore {
         return wm * WTM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
     }
     __device__ __forceinline__ static int frag_col(int wn, int j, int lane) { return wn * WTN + j * 32 + (lane & 31); }
+    // CT layout: the row of fragment (i, *) and the first of the four columns of register quad q of fragment (*, j)
+    __device__ __forceinline__ static int ct_row(int wm, int i, int lane) { return wm * WTM + i * 32 + (lane & 31); }
+    __device__ __forceinline__ static int ct_col(int wn, int j, int q, int lane)
+    {
+        return wn * WTN + j * 32 + 8 * q + 4 * (lane >> 5);
+    }
     __device__ __forceinline__ static int swz(int row, int c) { return c ^ ((row / RPW) % CH); }
 
     // MX scale bytes of pair h for one tile row: four blocks (a 32-bit word), or two when a stage holds a single
@@ -490,7 +502,8 @@ struct GemmCore {
                             if constexpr (OP == OP_I8) {
                                 const v4i a4 = (v4i){fa[i][0], fa[i][1], fa[i][2], fa[i][3]};
                                 const v4i b4 = (v4i){fb[0], fb[1], fb[2], fb[3]};
-                                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, b4, acc[i][j], 0, 0, 0);
+                                if constexpr (CT) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b4, a4, acc[i][j], 0, 0, 0);
+                                else acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, b4, acc[i][j], 0, 0, 0);
                             } else if constexpr (OP == OP_F8) {
                                 acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb, acc[i][j], CBSZ,
                                                                                              BLGP, 0, 0, 0, 0);
@@ -522,60 +535,6 @@ struct GemmCore {
         wait_vmcnt<0>();
     }
 };
-
-// Coalesced epilogue store of a GemmCore tile (T): the output bits val(i, j, r) of every accumulator element
-// (ES = 2 or 4 bytes per C element) are written to LDS -- free once every wave has left the main loop -- and
-// leave as whole 16-byte row pieces (buffer_store_dwordx4) instead of one 2- or 4-byte store per element: the
-// element stores of a 128 x 256 f16 tile measured slower than its K = 1024 main loop.  LDS rows hold TBN * ES
-// bytes, 16-byte pieces XOR-swizzled by (row % 8), so the two rows of one ds_write (lanes 0-31, 32-63) and the
-// 16 lanes of one ds_read fall in distinct banks.  A tile larger than the LDS goes in chunks of whole wave rows
-// (the waves whose rows lie in chunk ch write it).  The caller guarantees 16-byte aligned output rows and
-// cols % (16 / ES) == 0 (no piece straddles the last column); rows past `rows` and pieces past `cols` are not
-// stored (with a row pitch of N elements the latter would land in the next row).
-template <class T, int ES, class F>
-__device__ __forceinline__ void store_tile_lds(uint8_t* smem, const TileOut& out, int rows, int cols, F val)
-{
-    constexpr int RBY = T::TBN * ES;  // LDS bytes per tile row
-    constexpr int PR = RBY / 16;      // 16-byte pieces per row
-    constexpr int NCH = (size_t)T::TBM * RBY <= T::LDS_BYTES ? 1 : (size_t)T::TBM * RBY <= 2 * T::LDS_BYTES ? 2 : 4;
-    constexpr int CHR = T::TBM / NCH;  // rows per chunk
-    constexpr int ITER = CHR * PR / T::NT;
-    static_assert((ES == 2 || ES == 4) && PR >= 8 && (size_t)CHR * RBY <= T::LDS_BYTES && CHR % T::WTM == 0 &&
-                      (CHR * PR) % T::NT == 0, "coalesced epilogue shape");
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave / T::TWN, wn = wave % T::TWN;
-    const int my_chunk = wm * T::WTM / CHR;
-#pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-        __syncthreads();  // the main loop's last LDS reads (or the previous chunk's) are done
-        if (my_chunk == ch) {
-#pragma unroll
-            for (int i = 0; i < T::FM; ++i)
-#pragma unroll
-                for (int j = 0; j < T::FN; ++j) {
-                    const int cb = T::frag_col(wn, j, lane) * ES;
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int row = T::frag_row(wm, i, r, lane) - ch * CHR;
-                        uint8_t* d = smem + row * RBY + (((cb >> 4) ^ (row & 7)) << 4) + (cb & 15);
-                        const uint32_t v = val(i, j, r);
-                        if constexpr (ES == 4) *(uint32_t*)d = v;
-                        else *(uint16_t*)d = (uint16_t)v;
-                    }
-                }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int it = 0; it < ITER; ++it) {
-            const int k = it * T::NT + threadIdx.x;
-            const int row = k / PR, pc = k % PR;
-            const u32x4 v = *(const u32x4*)(smem + row * RBY + ((pc ^ (row & 7)) << 4));
-            const int grow = ch * CHR + row;
-            const bool ok = grow < rows && pc * (16 / ES) < cols;
-            __builtin_amdgcn_raw_buffer_store_b128(v, out.r, ok ? (uint32_t)grow * out.pitch + (uint32_t)(pc * 16) : OOB, 0, 0);
-        }
-    }
-}
 
 // the 32 bits of one accumulator element (a value copy: __builtin_bit_cast of a vector-element lvalue reads the
 // vector's first element under this compiler)

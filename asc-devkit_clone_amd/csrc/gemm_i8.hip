@@ -160,7 +160,8 @@ __device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* wtot
 template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1>
 __global__ __launch_bounds__(WM * WN * 64, WPE) void group_gemm_i8_kernel(GroupGemmArgs p)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB>;
+    // transposed accumulators: four consecutive output columns per register quad, stored as one 8-byte vector
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB, 0, true, true>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int64_t wtot[T::NT / 64];
     __shared__ int64_t tile_info[4];  // group, first row, end row, first m-tile of this workgroup's tile
@@ -255,37 +256,46 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void group_gemm_i8_kernel(GroupG
         // per-token scale in fp32, optional FasterGelu in fp32, one rounding cast to the output type.  Stores go
         // through a buffer resource over the output tile: rows past the group's end are out of its range.
         const TileOut out = tile_out(p.Y, m0, n0, p.N, c.rows, c.cols, 2);
-        auto value = [&](int i, int j, int r) {
-            float v = (float)acc[i][j][r] * s_sc[T::frag_col(wn, j, lane)];
-            v = v * s_pt[T::frag_row(wm, i, r, lane)];
-            return p.act ? faster_gelu(v) : v;
-        };
-        // whole 16-byte row pieces through LDS when the rows allow it (N a multiple of 8, Y 16-byte aligned),
-        // else one 2-byte store per element
-        if (p.N % 8 == 0 && ((uintptr_t)p.Y & 15) == 0) {
-            if (p.out_type == DT_F16)
-                store_tile_lds<T, 2>(smem, out, c.rows, c.cols,
-                                     [&](int i, int j, int r) { return (uint32_t)f32_to_f16_sat(value(i, j, r)); });
-            else
-                store_tile_lds<T, 2>(smem, out, c.rows, c.cols,
-                                     [&](int i, int j, int r) { return (uint32_t)f32_to_bf16_sat(value(i, j, r)); });
-            return;
-        }
+        // Lane l holds, for each fragment row (i) and register quad q of each column fragment (j), the four columns
+        // ct_col .. ct_col + 3 of row ct_row: with N a multiple of 4 and Y 8-byte aligned they leave as one 8-byte
+        // store (a quad is wholly inside or wholly past the tile's columns, whose count is then a multiple of 4),
+        // else as four 2-byte stores.
+        const bool vec = p.N % 4 == 0 && ((uintptr_t)p.Y & 7) == 0;
         auto store = [&](auto cvt) {
 #pragma unroll
-            for (int j = 0; j < T::FN; ++j) {
-                const int cl = T::frag_col(wn, j, lane);
-                const uint32_t cbase = cl < c.cols ? (uint32_t)(cl * 2) : OOB;
+            for (int i = 0; i < T::FM; ++i) {
+                const int row = T::ct_row(wm, i, lane);
+                const float pt = s_pt[row];
+                const uint32_t roff = (uint32_t)row * out.pitch;
 #pragma unroll
-                for (int i = 0; i < T::FM; ++i)
+                for (int j = 0; j < T::FN; ++j)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        __builtin_amdgcn_raw_buffer_store_b16(cvt(value(i, j, r)), out.r,
-                                                              cbase + (uint32_t)T::frag_row(wm, i, r, lane) * out.pitch, 0, 0);
+                    for (int q = 0; q < 4; ++q) {
+                        const int cl = T::ct_col(wn, j, q, lane);
+                        const v4f sc = *(const v4f*)(s_sc + cl);
+                        uint32_t h[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            float v = (float)acc[i][j][4 * q + e] * sc[e];
+                            v = v * pt;
+                            h[e] = cvt(p.act ? faster_gelu(v) : v);
+                        }
+                        if (vec) {
+                            const uint32_t off = cl < c.cols ? roff + (uint32_t)(cl * 2) : OOB;
+                            __builtin_amdgcn_raw_buffer_store_b64((u32x2){h[0] | (h[1] << 16), h[2] | (h[3] << 16)},
+                                                                  out.r, off, 0, 0);
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)h[e], out.r,
+                                                                      cl + e < c.cols ? roff + (uint32_t)((cl + e) * 2) : OOB,
+                                                                      0, 0);
+                        }
+                    }
             }
         };
-        if (p.out_type == DT_F16) store([](float v) { return f32_to_f16_sat(v); });
-        else store([](float v) { return f32_to_bf16_sat(v); });
+        if (p.out_type == DT_F16) store([](float v) { return (uint32_t)f32_to_f16_sat(v); });
+        else store([](float v) { return (uint32_t)f32_to_bf16_sat(v); });
     }
 }
 

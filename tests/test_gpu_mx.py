@@ -148,7 +148,7 @@ def test_config5_full_size_sampled(ascq_gpu, oracle, trans_b):
 @pytest.mark.parametrize("shape", [(256, 256, 512), (130, 70, 384), (1030, 1026, 256), (2051, 1026, 128),
                                    (1024, 2048, 1024)])
 def test_mx_e1m2(ascq_gpu, oracle, fmts, trans_b, shape):
-    """every fp4 code of either format, block exponents spread over +-20, both B layouts; the 256 x 128 fp6 tiles
+    """every fp4 code of either format, block exponents spread over +-20, both B layouts; the 256 x 256 fp6 tiles
     (M, N >= 1024, ragged edges included) and the 64 x 64 ones"""
     M, N, K = shape
     rng = seeded(M + 3 * N + K + len(fmts[0]) + 5 * len(fmts[1]) + trans_b)
