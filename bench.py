@@ -7,10 +7,11 @@ the figure is HBM, not MALL, bandwidth.
 
 Also measured and reported under "other_configs": the W8A8 int8 Matmul + per-channel DEQF16 (128x512x256 and the
 8192^3 throughput shape), the W4A16 / W8A16 decode GEMV (M in {1, 16, 64}), the MoE group matmul (both weight
-layouts), the MX-FP4 8192^3 GEMM and the fp8 / MX-FP8 8192^3 GEMMs.
+layouts), the MX-FP4 8192^3 GEMM and the fp8 / MX-FP8 8192^3 GEMMs, and -- for scale, not this library -- the
+vendor BLAS (hipBLASLt through torch) on the int8 and fp8 8192^3 shapes.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                  [--only all|headline|w8a8|gemv|group|mx|fp8|traffic]
+                  [--only all|headline|quant|w8a8|gemv|group|mx|fp8|vendor|traffic]
 """
 from __future__ import annotations
 
@@ -535,6 +536,35 @@ def bench_fp8(torch, ascq, iters, trans_b=True):
                 ms=ms, value=tf, unit="TFLOPS", frac_of_peak=tf / FP8_PEAK_TFLOPS)
 
 
+def bench_vendor(torch, kind, iters):
+    """The vendor BLAS on the same box and shape, for scale (not this library): hipBLASLt through torch._int_mm (int8,
+    int32 out) and torch._scaled_mm (fp8 e4m3, per-tensor scales, bf16 out), M = N = K = 8192, B given [N, K]."""
+    M = N = K = 8192
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    if kind == "int8":
+        A = torch.randint(-127, 128, (M, K), generator=g, device="cuda", dtype=torch.int8)
+        B = torch.randint(-127, 128, (N, K), generator=g, device="cuda", dtype=torch.int8)
+
+        def fn(i):
+            torch._int_mm(A, B.t())
+
+        name, peak, unit = "hipBLASLt int8 GEMM (torch._int_mm)", INT8_PEAK_TOPS, "TOPS"
+    else:
+        A = torch.randn((M, K), generator=g, device="cuda").to(torch.float8_e4m3fn)
+        B = torch.randn((N, K), generator=g, device="cuda").to(torch.float8_e4m3fn)
+        one = torch.ones((), device="cuda")
+
+        def fn(i):
+            torch._scaled_mm(A, B.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+
+        name, peak, unit = "hipBLASLt fp8 e4m3 GEMM (torch._scaled_mm), bf16 out", FP8_PEAK_TFLOPS, "TFLOPS"
+    ms = _time_loop(torch, fn, iters, warmup=2)
+    v = 2 * M * N * K / (ms * 1e-3) / 1e12
+    return dict(workload=f"vendor reference: {name} {M}x{N}x{K}, B given [N,K]", ms=ms, value=v, unit=unit,
+                frac_of_peak=v / peak)
+
+
 def bench_mxfp8(torch, ascq, iters):
     """MX-FP8 (e4m3 elements, E8M0 per 32 K) GEMM 8192^3 -> bf16"""
     M = N = K = 8192
@@ -725,6 +755,7 @@ OTHER = {
              for w in ("INT4", "INT8") for m in (1, 16, 64)],
     "group": [lambda t, a: bench_group(t, a, 20, True), lambda t, a: bench_group(t, a, 20, False),
               lambda t, a: bench_group_sample(t, a, 20)],
+    "vendor": [lambda t, a: bench_vendor(t, "int8", 10), lambda t, a: bench_vendor(t, "fp8", 10)],
     "mx": [lambda t, a: bench_mx(t, a, 10, True), lambda t, a: bench_mx(t, a, 5, False),
            lambda t, a: bench_mx_e1m2_sample(t, a, 10)],
     "fp8": [lambda t, a: bench_fp8(t, a, 10, True), lambda t, a: bench_fp8(t, a, 5, False),
@@ -760,7 +791,7 @@ CPU_FOR = {
 
 def run_others(torch, ascq, which, with_cpu=False):
     out, cpu_cache = [], {}
-    for key in (["quant", "w8a8", "gemv", "group", "mx", "fp8"] if which == "all" else [which]):
+    for key in (["quant", "w8a8", "gemv", "group", "mx", "fp8", "vendor"] if which == "all" else [which]):
         for idx, fn in enumerate(OTHER[key]):
             try:
                 r = _with_roofline(fn(torch, ascq))
@@ -787,7 +818,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="all",
-                    choices=["all", "headline", "quant", "w8a8", "gemv", "group", "mx", "fp8", "traffic"],
+                    choices=["all", "headline", "quant", "w8a8", "gemv", "group", "mx", "fp8", "vendor", "traffic"],
                     help="run one workload family (the JSON contract line is printed for all / headline)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -803,7 +834,7 @@ def main() -> int:
     if args.only == "traffic":
         print(json.dumps(traffic_probe(torch, ascq)))
         return 0
-    if args.only in ("quant", "w8a8", "gemv", "group", "mx", "fp8"):
+    if args.only in ("quant", "w8a8", "gemv", "group", "mx", "fp8", "vendor"):
         print(json.dumps({"other_configs": run_others(torch, ascq, args.only, with_cpu=not args.no_cpu)}))
         return 0
     h = bench_headline(torch, ascq, args.steps, args.warmup)
