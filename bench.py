@@ -59,43 +59,6 @@ def parse_traffic() -> dict:
     return out
 
 
-class KernelEvents:
-    """HIP event pairs bound to single kernel dispatches: ascq_set_launch_events arms the library so that the next
-    entry point's main kernel is launched with hipExtLaunchKernelGGL(start, stop) on its stream; the events then
-    time that dispatch alone, with no marker packets between kernels.  The events come from the HIP runtime that
-    torch (and through it libascq) already loaded."""
-
-    def __init__(self, torch, ascq, n):
-        import ctypes
-
-        p = Path(torch.__file__).resolve().parent / "lib" / "libamdhip64.so"
-        self.hip = ctypes.CDLL(str(p) if p.exists() else "libamdhip64.so.7")
-        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
-        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
-        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
-        self.ascq = ascq
-        self.ctypes = ctypes
-        self.ev = []
-        for _ in range(n):
-            a, b = ctypes.c_void_p(), ctypes.c_void_p()
-            assert self.hip.hipEventCreate(ctypes.byref(a)) == 0 and self.hip.hipEventCreate(ctypes.byref(b)) == 0
-            self.ev.append((a, b))
-
-    def arm(self, i):
-        a, b = self.ev[i]
-        self.ascq.check(self.ascq.lib().ascq_set_launch_events(a, b), "set_launch_events")
-
-    def ms(self, i):
-        out = self.ctypes.c_float()
-        assert self.hip.hipEventElapsedTime(self.ctypes.byref(out), *self.ev[i]) == 0
-        return out.value
-
-    def close(self):
-        for a, b in self.ev:
-            self.hip.hipEventDestroy(a)
-            self.hip.hipEventDestroy(b)
-
-
 def bench_headline(torch, ascq, steps, warmup):
     M = N = 8192
     bytes_quant = 2 * M * N + M * N + 4 * M
@@ -115,43 +78,42 @@ def bench_headline(torch, ascq, steps, warmup):
         ys.append(torch.empty((M, N), dtype=torch.float16, device="cuda"))
     stream = torch.cuda.current_stream()
 
-    # The kernels are timed by event pairs bound to their dispatches (KernelEvents) on a sample of the timed steps:
-    # the quant kernel on steps 0, 4, 8, ..., the dequant kernel on steps 2, 6, 10, ...  A timed dispatch costs
-    # ~4 us of extra GPU time (measured: 70.7 us per step untimed, 78.9 us with both kernels timed every step), so
-    # sampling keeps the whole-job figure close to the untimed one.
-    qi = [i for i in range(steps) if i % 4 == 0]
-    di = [i for i in range(steps) if i % 4 == 2] or [min(1, steps - 1)]
-
-    def step(i, kev=None):
+    def quant(i):
         r = i % R
-        j = i - warmup
-        if kev is not None and j in qi:
-            kev.arm(2 * j)
         ascq.quant_dynamic_per_token(xs[r], out=qs[r], scale_out=ss[r])
-        if kev is not None and j in di:
-            kev.arm(2 * j + 1)
+
+    def dequant(i):
+        r = i % R
         ascq.ascend_dequant_policy(qs[r], ss[r], ascq.PER_TOKEN, torch.float16, out=ys[r])
 
     for i in range(warmup):
-        step(i)
+        quant(i)
+        dequant(i)
     torch.cuda.synchronize()
-    kev = KernelEvents(torch, ascq, 2 * steps)
-    torch.cuda.synchronize()
+
+    def timed(fn, n):
+        """events on the launch stream around n back-to-back calls (queued ahead, so the GPU runs them without
+        host gaps); returns the elapsed ms"""
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(n):
+            fn(i)
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end)
+
+    # whole job: `steps` steps of quant then dequant, nothing else in the timed region
     t0 = time.perf_counter()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(steps):
-        step(warmup + i, kev)
-    end.record(stream)
-    torch.cuda.synchronize()
+    total_ms = timed(lambda i: (quant(warmup + i), dequant(warmup + i)), steps)
     wall = time.perf_counter() - t0
-    total_ms = start.elapsed_time(end)
-    q_ms = float(np.mean([kev.ms(2 * i) for i in qi]))
-    d_ms = float(np.mean([kev.ms(2 * i + 1) for i in di]))
-    kev.close()
+    # each kernel on its own: n launches in a row (rotating buffers, so every launch reads from HBM); the average
+    # includes the small gap between consecutive dispatches
+    n_k = max(steps // 2, 10)
+    q_ms = timed(quant, n_k) / n_k
+    d_ms = timed(dequant, n_k) / n_k
     return dict(M=M, N=N, R=R, total_ms=total_ms, wall_s=wall, q_ms=q_ms, d_ms=d_ms, bytes_quant=bytes_quant,
-                bytes_dequant=bytes_dequant, q_samples=len(qi), d_samples=len(di))
+                bytes_dequant=bytes_dequant, q_samples=n_k, d_samples=n_k)
 
 
 def _cpu_info():
@@ -869,7 +831,7 @@ def main() -> int:
                      "kernel": "quant_dyn_row_kernel (AscendQuant per-token dynamic)",
                      "algorithmic_bytes_per_launch": h["bytes_quant"], "avg_launch_ms": round(h["q_ms"], 5),
                      "timed_launches": h["q_samples"],
-                     "timing": "HIP events bound to each dispatch (hipExtLaunchKernelGGL) on the launch stream"},
+                     "timing": "HIP events on the launch stream around back-to-back launches of this kernel alone"},
         "dequant_kernel": {"achieved": round(h["bytes_dequant"] / (h["d_ms"] * 1e-3) / 1e9, 2), "unit": "GB/s",
                            "avg_launch_ms": round(h["d_ms"], 5)},
     }
