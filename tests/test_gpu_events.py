@@ -18,6 +18,7 @@ def _hip():
     hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
     hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
     hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+    hip.hipGetLastError.argtypes = []
     return hip
 
 
@@ -60,6 +61,9 @@ def test_failed_call_disarms_events(ascq_gpu):
     ascq_gpu.quant_dynamic_per_token(x)
     torch.cuda.synchronize()
     rc, _ = _elapsed(hip, a, b)
+    # the query of unrecorded events leaves its error as the thread's last HIP error: clear it, or the next HIP
+    # call of another test (torch's included) reports it as its own
+    hip.hipGetLastError()
     assert rc != 0, "events armed before a failed call still timed the next call"
     hip.hipEventDestroy(a)
     hip.hipEventDestroy(b)
