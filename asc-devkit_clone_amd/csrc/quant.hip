@@ -397,6 +397,7 @@ __device__ __forceinline__ float load_scale_t(const void* p, int t, int64_t i)
 enum : int { QD_INT8 = 0, QD_E4M3 = 1, QD_E5M2 = 2, QD_E2M1 = 3, QD_E1M2 = 4, QD_HIF8 = 5 };
 constexpr bool qd_nibble(int d) { return d == QD_E2M1 || d == QD_E1M2; }  // two codes a byte
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+typedef float f2x __attribute__((ext_vector_type(2)));
 enum : int { QL_TOKEN = 0, QL_KCOL = 1, QL_KROW = 2 };
 
 // Unsigned division by a runtime constant d for dividends below 2^31: s = ceil(log2 d),
@@ -475,8 +476,10 @@ __device__ __forceinline__ uint32_t quant_code(float v)
         return f32_to_fp8_sat(v, DST == QD_E5M2);
     } else {
         // f16 / f32 results go through bf16 (rne, saturating, NaN -> 0): plain rne here gives the same E2M1 code,
-        // as NaN maps to 0 and every overflow to +-6 either way
-        if constexpr (T != DT_BF16) v = bf16_round(v);
+        // as NaN maps to 0 and every overflow to +-6 either way.  The rounding is the gfx950 conversion
+        // (v_cvt_pk_bf16_f32), equal to the bit-level rne (bf16_round) on every non-NaN fp32 input; a NaN stays a
+        // NaN either way and the code functions map it to 0.
+        if constexpr (T != DT_BF16) v = (float)(__bf16)v;
         if constexpr (DST == QD_E1M2) return e1m2_code<MODE>(v);  // bf16 rounding first: E1M2 steps are finer
         else return e2m1_code<MODE>(v);
     }
@@ -618,10 +621,22 @@ __device__ __forceinline__ void quant_unit(const QuantPolicyArgs& a, uint32_t u,
         return;
     }
     uint32_t code[8];
+    if constexpr (qd_nibble(DST) && T != DT_BF16) {
+        // the bf16 step of the fp4 codes two elements per conversion (v_cvt_pk_bf16_f32, rne), then the codes of
+        // the bf16 values
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        if constexpr (FP8) code[j] = fp8_sat_hw<DST == QD_E5M2>(v[j]);
-        else code[j] = quant_code<DST, T, MODE>(v[j]);
+        for (int q = 0; q < 4; ++q) {
+            const bf2 b = __builtin_convertvector((f2x){v[2 * q], v[2 * q + 1]}, bf2);
+            const uint32_t w = __builtin_bit_cast(uint32_t, b);
+            code[2 * q] = quant_code<DST, DT_BF16, MODE>(__uint_as_float(w << 16));
+            code[2 * q + 1] = quant_code<DST, DT_BF16, MODE>(__uint_as_float(w & 0xffff0000u));
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if constexpr (FP8) code[j] = fp8_sat_hw<DST == QD_E5M2>(v[j]);
+            else code[j] = quant_code<DST, T, MODE>(v[j]);
+        }
     }
     if constexpr (qd_nibble(DST)) {
         const uint32_t w = code[0] | (code[1] << 4) | (code[2] << 8) | (code[3] << 12) | (code[4] << 16) |
