@@ -143,3 +143,29 @@ def test_many_experts_zipf(ascq_gpu, oracle, G, list_type, w_trans, K):
     y0 = torch.full((M, N), 3.0, dtype=torch.bfloat16).view(torch.int16).numpy().view(np.uint16).copy()
     ref = O.group_matmul(x, pts, w, scale, gl, list_type, G, M, K, N, O.BF16, w_trans, y=y0)
     np.testing.assert_array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), ref)
+
+
+@pytest.mark.parametrize("N,shift", [(150, 0), (162, 0), (160, 1)])
+@pytest.mark.parametrize("w_trans", [False, True])
+def test_group_matmul_store_fallback(ascq_gpu, oracle, N, shift, w_trans):
+    """Output rows that are not whole 8-byte quads (N % 4 != 0) or a Y that is not 8-byte aligned (a view one
+    element into its buffer) take the element-wise stores of the tiled kernel (w_trans) or the generic kernel; both
+    bit-exact vs the oracle, and nothing outside Y is written."""
+    rng = seeded(700 + N + shift + w_trans)
+    G, K = 4, 256
+    counts = np.array([97, 0, 140, 33], np.int64)
+    M = int(counts.sum()) + 3
+    x = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-127, 128, (G, N, K) if w_trans else (G, K, N), dtype=np.int8)
+    pts = np.exp(rng.uniform(np.log(1e-3), np.log(1e-1), M)).astype(np.float32)
+    scale = np.exp(rng.uniform(np.log(1e-4), np.log(1e-2), (G, N))).astype(np.float32)
+    gl = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    buf = torch.full((M * N + 2 * shift,), 3.0, dtype=torch.float16, device="cuda")
+    y = buf[shift:shift + M * N].view(M, N)
+    ascq_gpu.quant_group_matmul(_dev(x), _dev(pts), _dev(w), _dev(scale), _dev(gl), 0, w_trans, torch.float16, out=y)
+    y0 = torch.full((M, N), 3.0, dtype=torch.float16).view(torch.int16).numpy().view(np.uint16).copy()
+    ref = O.group_matmul(x, pts, w, scale, gl, 0, G, M, K, N, O.F16, w_trans, y=y0)
+    got = buf.cpu().view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(got[shift:shift + M * N].reshape(M, N), ref)
+    three = np.float16(3.0).view(np.uint16)
+    assert (got[:shift] == three).all() and (got[shift + M * N:] == three).all()
