@@ -560,6 +560,27 @@ __device__ __forceinline__ uint32_t fp8_sat_hw(float x)
 // offset add run as packed half operations (each correctly rounded, which is the scaleT arithmetic itself).
 constexpr int QP_UNR = 4;
 
+// two f32 -> E2M1 nearest-even codes into byte Q of w (saturating at +-6) / the two values of byte Q of w (gfx950;
+// the byte select is an immediate)
+template <int Q>
+__device__ __forceinline__ uint32_t fp4_pk_f32(uint32_t w, float a, float b)
+{
+    return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a, b, 1.0f, Q);
+}
+template <int Q>
+__device__ __forceinline__ f2x f32_pk_fp4(uint32_t w)
+{
+    return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, Q);
+}
+// the eight E2M1 nearest-even codes of f[0..7], element j at bits 4j .. 4j + 3, each value scaled by s first
+__device__ __forceinline__ uint32_t fp4_codes8(const float (&f)[8], float s)
+{
+    uint32_t w = fp4_pk_f32<0>(0u, f[0] * s, f[1] * s);
+    w = fp4_pk_f32<1>(w, f[2] * s, f[3] * s);
+    w = fp4_pk_f32<2>(w, f[4] * s, f[5] * s);
+    return fp4_pk_f32<3>(w, f[6] * s, f[7] * s);
+}
+
 template <int DST, int SRC, int SC, int MODE, bool KROW>
 __device__ __forceinline__ void quant_unit(const QuantPolicyArgs& a, uint32_t u, const Raw8<SRC>& xr,
                                            const Raw8<SC>& sr, Raw8<SC> orw, bool off_tensor, uint32_t osc)
@@ -617,6 +638,64 @@ __device__ __forceinline__ void quant_unit(const QuantPolicyArgs& a, uint32_t u,
         w = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(w, b[1], 1.0f, 1);
         w = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(w, b[2], 1.0f, 2);
         w = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(w, b[3], 1.0f, 3);
+        __builtin_nontemporal_store(w, (uint32_t*)a.dst + u);
+        return;
+    }
+    if constexpr (DST == QD_E2M1 && MODE != RM_RINT) {
+        // The directed modes from the gfx950 conversions.  f = the bf16 value of each result (NaN -> 0, its code),
+        // w = the nearest-even codes of f (v_cvt_scalef32_pk_fp4_f32, saturating at +-6).
+        //  * FLOOR / CEIL / TRUNC: d = the value of each code (v_cvt_scalef32_pk_f32_fp4); where d lies on the wrong
+        //    side of f the code moves one step, magnitude +1 or -1 in its low three bits.  Those steps never pass 0 or
+        //    7 (a +1 is skipped at 7, where the mode saturates; a -1 only happens above 0), so the eight nibbles of the
+        //    word step together by one add and one subtract.
+        //  * ROUND (half away): the nearest-even codes of f * (1 + 2^-10).  The nudge moves an exact tie (a midpoint of
+        //    the E2M1 grid is a bf16 value) away from zero and moves no other bf16 value across a midpoint: those
+        //    lie at least one bf16 step, 2^-8 of the midpoint, away from it.
+        float f[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float f0 = v[2 * q], f1 = v[2 * q + 1];
+            if constexpr (T != DT_BF16) {
+                const uint32_t bw = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2x){f0, f1}, bf2));
+                f0 = __uint_as_float(bw << 16);
+                f1 = __uint_as_float(bw & 0xffff0000u);
+            }
+            f[2 * q] = f0 != f0 ? 0.0f : f0;
+            f[2 * q + 1] = f1 != f1 ? 0.0f : f1;
+        }
+        uint32_t w;
+        if constexpr (MODE == RM_ROUND) {
+            w = fp4_codes8(f, 1.0f + 0x1p-10f);
+        } else {
+            w = fp4_codes8(f, 1.0f);
+            const f2x dq[4] = {f32_pk_fp4<0>(w), f32_pk_fp4<1>(w), f32_pk_fp4<2>(w), f32_pk_fp4<3>(w)};
+            uint32_t inc = 0u, dec = 0u;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f2x d = dq[q];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int j = 2 * q + e;
+                    const float dj = e ? d.y : d.x, fj = f[j];
+                    const bool neg = (__float_as_uint(fj) >> 31) != 0u, top = ((w >> (4 * j)) & 7u) == 7u;
+                    const uint32_t bit = 1u << (4 * j);
+                    if constexpr (MODE == RM_FLOOR) {
+                        if (dj > fj) {
+                            if (!neg) dec |= bit;
+                            else if (!top) inc |= bit;
+                        }
+                    } else if constexpr (MODE == RM_CEIL) {
+                        if (dj < fj) {
+                            if (neg) dec |= bit;
+                            else if (!top) inc |= bit;
+                        }
+                    } else {  // RM_TRUNC
+                        if (__builtin_fabsf(dj) > __builtin_fabsf(fj)) dec |= bit;
+                    }
+                }
+            }
+            w = w + inc - dec;
+        }
         __builtin_nontemporal_store(w, (uint32_t*)a.dst + u);
         return;
     }

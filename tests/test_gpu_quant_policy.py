@@ -178,14 +178,20 @@ def test_argument_checks(ascq_gpu):
 
 
 def test_conversion_sweeps(ascq_gpu):
-    """the vector kernels convert with the gfx950 instructions (fp32 -> fp8 / bf16, bf16 -> E2M1): every bf16 pattern
-    to E2M1 (rint), and 2^22 fp32 patterns spread over the whole range to fp8 e4m3 / e5m2 and to E2M1 through bf16,
-    each against the oracle"""
+    """the vector kernels convert with the gfx950 instructions (fp32 -> fp8 / bf16, bf16 / fp32 -> E2M1, E2M1 -> fp32):
+    every bf16 pattern and every f16 pattern to E2M1 and E1M2 in all five modes, and 2^22 fp32 patterns spread over
+    the whole range to fp8 e4m3 / e5m2 and, through bf16, to E2M1 / E1M2 in all five modes, each against the oracle"""
     bf = np.arange(0x10000, dtype=np.uint32).astype(np.uint16).reshape(256, 256)
     one_b = _bits(np.ones((256, 256 // 32)), O.BF16)
-    _check(ascq_gpu, bf, O.BF16, one_b, O.BF16, O.FP4_E2M1, O.PER_GROUP, 256, 256, 32, None, None, 1)
-    for mode in _MODES:  # E1M2 has no conversion instruction: the software encoder on every bf16 pattern
-        _check(ascq_gpu, bf, O.BF16, one_b, O.BF16, O.FP4_E1M2, O.PER_GROUP, 256, 256, 32, None, None, 1, mode)
+    one_h = _bits(np.ones((256, 256 // 32)), O.F16)
+    for mode in _MODES:
+        # E2M1: rint is the bf16 -> E2M1 instruction; the directed modes start from the fp32 -> E2M1 nearest-even
+        # instruction and step one code where its value lies on the wrong side (round: a 2^-10 nudge).  E1M2 has no
+        # conversion instruction: the software encoder.  Every bf16 pattern, and every f16 pattern through the f16
+        # product and the bf16 step (scale 1, exact).
+        for fp4 in (O.FP4_E2M1, O.FP4_E1M2):
+            _check(ascq_gpu, bf, O.BF16, one_b, O.BF16, fp4, O.PER_GROUP, 256, 256, 32, None, None, 1, mode)
+            _check(ascq_gpu, bf, O.F16, one_h, O.F16, fp4, O.PER_GROUP, 256, 256, 32, None, None, 1, mode)
     rng = seeded(1700)
     f = (np.arange(1 << 22, dtype=np.uint64) * 1021 + rng.integers(0, 1021, 1 << 22)).astype(np.uint32)
     f = f.view(np.float32).reshape(2048, 2048)
@@ -193,8 +199,9 @@ def test_conversion_sweeps(ascq_gpu):
     for fmt in (O.FP8_E4M3, O.FP8_E5M2):
         _check(ascq_gpu, f, O.F32, one_f, O.F32, fmt, O.PER_TOKEN, 2048, 2048)
     one_g = np.ones((2048, 2048 // 32), np.float32)
-    _check(ascq_gpu, f, O.F32, one_g, O.F32, O.FP4_E2M1, O.PER_GROUP, 2048, 2048, 32, None, None, 1)
-    _check(ascq_gpu, f, O.F32, one_g, O.F32, O.FP4_E1M2, O.PER_GROUP, 2048, 2048, 32, None, None, 1)
+    for mode in _MODES:
+        _check(ascq_gpu, f, O.F32, one_g, O.F32, O.FP4_E2M1, O.PER_GROUP, 2048, 2048, 32, None, None, 1, mode)
+        _check(ascq_gpu, f, O.F32, one_g, O.F32, O.FP4_E1M2, O.PER_GROUP, 2048, 2048, 32, None, None, 1, mode)
 
 
 def test_empty_inputs(ascq_gpu):
