@@ -831,15 +831,24 @@ inline int64_t aq_xs_lds(int64_t M, int64_t K, bool has_off)
     return lds <= 160 * 1024 ? lds : 0;
 }
 
+// the weight, x and scale buffers of the column-block kernels, each below 2^31 - 2^16 bytes: their 32-bit buffer
+// offsets, with bit 31 set for an out-of-range load and a step or immediate of under 2^16 added, never wrap
+inline bool aq_cols_fit(int64_t M, int64_t N, int64_t K, int64_t g, bool int4)
+{
+    const uint64_t w_bytes = (uint64_t)K * N / (int4 ? 2 : 1), s_bytes = (uint64_t)((K + g - 1) / g) * N * 2;
+    const uint64_t x_bytes = (uint64_t)M * K * 2, lim = 0x7FFF0000ull;
+    return M >= 1 && w_bytes < lim && s_bytes < lim && x_bytes < lim && (uint64_t)N < lim;
+}
+
 // checks of the column-block and ring kernels common to both; fills the 32-bit argument block
 inline bool aq_cols_args(AqXsArgs& A, uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
                          const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, int C, int smax, int atomic)
 {
     const int64_t NBT = N / 16, KB = K / KT;
     const uint64_t w_bytes = (uint64_t)K * N / (int4 ? 2 : 1), s_bytes = (uint64_t)((K + g - 1) / g) * N * 2;
-    const uint64_t x_bytes = (uint64_t)M * K * 2, lim = 0x7FFFFFFFull;
-    if (C < 1 || C > NBT || (NBT + C - 1) / C > smax || g % KT != 0 || ((g / KT) & (g / KT - 1)) != 0 || M < 1 ||
-        w_bytes >= lim || s_bytes >= lim || x_bytes >= lim || N >= (int64_t)lim)
+    const uint64_t x_bytes = (uint64_t)M * K * 2;
+    if (C < 1 || C > NBT || (NBT + C - 1) / C > smax || g % KT != 0 || ((g / KT) & (g / KT - 1)) != 0 ||
+        !aq_cols_fit(M, N, K, g, int4))
         return false;
     A.y = y;
     A.x = x;
@@ -1139,6 +1148,220 @@ static hipError_t launch_aq_ring(uint16_t* y, const uint16_t* x, const void* wp,
     return hipGetLastError();
 }
 
+// K-split column-block form for batches M <= 16 MT (group size 128 << s).  The grid is C <= 256 column blocks, one per
+// CU; block c covers the strips [c sq + min(c, sr), ...), sq or sq + 1 <= NS of them.  Its KW waves split the k
+// tiles -- wave kw takes tiles [kw KB / KW, (kw + 1) KB / KW) -- so every CU reads only its own strips of the weight
+// and each wave its own k range of x.  Nothing in the main loop is shared, so it has no LDS and no barrier: a wave
+// streams its weight tiles, its activation fragments and its tiles' scale / offset values straight into a
+// register ring of D tiles (tiles past the end read zeros and multiply zeros, so every step issues the same loads
+// and the compiler's counted waits keep D - 1 tiles in flight), dequantises each weight fragment once and multiplies
+// it against all MT row tiles.  The NS strips of a short block (sq < NS) read zeros and are not stored.  At the end
+// the waves park their partial tiles in LDS row-major and every thread sums a pair of outputs over the KW waves in kw
+// order (deterministic), rounds once to half and stores it.
+template <int MT, int NS, int KW>
+struct AqKw {
+    static constexpr int NT = KW * 64;
+    static constexpr int ROW = NS * 16;                 // floats per partial row
+    static constexpr int LDS = KW * MT * 16 * ROW * 4;  // partial tiles of all waves
+    static_assert(LDS <= 160 * 1024, "partials fit in LDS");
+};
+
+template <int MT, int NS, int KW, int D, bool INT4, bool HAS_OFF>
+__global__ __launch_bounds__(KW * 64) void aq_kw_kernel(AqXsArgs A)
+{
+    using P = AqKw<MT, NS, KW>;
+    constexpr int TILE_BYTES = INT4 ? 1024 : 2048;
+    constexpr int LANE_BYTES = INT4 ? 16 : 32;
+    constexpr int WV = INT4 ? 1 : 2;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+    const int lane = threadIdx.x & 63;
+    const uint32_t kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t col_in = lane & 15, kq = lane >> 4;
+    const uint32_t cb = blockIdx.x;
+    const uint32_t M = A.M, N = A.N, K = A.K, KB = A.KB;
+    const uint32_t s0 = cb * A.sq + (cb < A.sr ? cb : A.sr), ns = A.sq + (cb < A.sr ? 1u : 0u);
+    const uint32_t t0 = kw * KB / KW, T = (kw + 1) * KB / KW - t0;  // this wave's k tiles
+    const aq_rsrc_t rw = aq_rsrc(A.wp, A.w_bytes);
+    const aq_rsrc_t rx = aq_rsrc(A.x, A.x_bytes);
+    const aq_rsrc_t rs = aq_rsrc(A.scale, A.s_bytes);
+    const aq_rsrc_t ro = aq_rsrc(HAS_OFF ? A.offset : A.scale, A.s_bytes);
+    const uint32_t magic = half_magic_vgpr();
+
+    struct Tile {
+        u32x4 w[NS][WV];
+        u32x4 x[MT][4];
+        uint32_t sc[NS], of[NS];  // 16-bit values, held in 32 bits (16-bit fields of a ring slot went to scratch)
+    };
+    // Lane (kq, col_in) reads the B fragment of column col_in of each strip, the A fragments of rows 16 a + col_in
+    // (k 32 j + 8 kq .. + 7 of the tile) and the scale / offset of its column.  The per-lane base offsets of tile 0
+    // are fixed here, out of range for the strips past the block and the rows past M; in the loop tile t only adds
+    // its uniform step and, past this wave's tiles, sets bit 31 (an out-of-range offset: the loads return zeros).
+    // Every condition stays out of the loop, so the compiler has no branch to duplicate loads into.  The host keeps
+    // every buffer below 2^31 - 2^16 bytes, so no offset plus its step or immediate wraps past 2^32.
+    uint32_t wb[NS], sbo[NS], xb[MT];
+#pragma unroll
+    for (int b = 0; b < NS; ++b) {
+        wb[b] = (uint32_t)b < ns ? ((s0 + b) * KB + t0) * TILE_BYTES + lane * LANE_BYTES : AQ_OOB;
+        sbo[b] = (uint32_t)b < ns ? ((s0 + b) * 16 + col_in) * 2 : AQ_OOB;
+    }
+#pragma unroll
+    for (int a = 0; a < MT; ++a) {
+        const uint32_t row = 16 * a + col_in;
+        xb[a] = row < M ? (row * K + t0 * KT + 8 * kq) * 2 : AQ_OOB;
+    }
+    const uint32_t n2 = N * 2;
+    auto issue = [&](uint32_t t, Tile& r) {
+        const uint32_t past = (T - 1 - t) & 0x80000000u;  // t >= T (both below 2^31)
+        const uint32_t sg = ((t0 + t) >> A.gshift) * n2;
+#pragma unroll
+        for (int b = 0; b < NS; ++b) {
+            const uint32_t off = (wb[b] + t * TILE_BYTES) | past;
+#pragma unroll
+            for (int v = 0; v < WV; ++v) r.w[b][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, off + 16 * v, 0, 0);
+        }
+#pragma unroll
+        for (int a = 0; a < MT; ++a) {
+            const uint32_t off = (xb[a] + t * (KT * 2)) | past;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) r.x[a][j] = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 64 * j, 0, 0);
+        }
+#pragma unroll
+        for (int b = 0; b < NS; ++b) {
+            const uint32_t off = (sbo[b] + sg) | past;
+            r.sc[b] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+            if constexpr (HAS_OFF) r.of[b] = __builtin_amdgcn_raw_buffer_load_b16(ro, off, 0, 0);
+        }
+    };
+
+    v4f acc[MT][NS];
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int b = 0; b < NS; ++b) acc[a][b] = (v4f){0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const Tile& r) {
+        h2 s2[NS], o2[NS];
+#pragma unroll
+        for (int b = 0; b < NS; ++b) {
+            const _Float16 sv = __builtin_bit_cast(_Float16, (uint16_t)r.sc[b]);
+            const _Float16 ov = HAS_OFF ? __builtin_bit_cast(_Float16, (uint16_t)r.of[b]) : (_Float16)0.0f;
+            s2[b] = (h2){sv, sv};
+            o2[b] = (h2){ov, ov};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int b = 0; b < NS; ++b) {
+                uint32_t w0, w1 = 0;
+                if constexpr (INT4) {
+                    w0 = r.w[b][0][j];
+                } else {
+                    w0 = r.w[b][j >> 1][(j & 1) * 2];
+                    w1 = r.w[b][j >> 1][(j & 1) * 2 + 1];
+                }
+                const h8 bf = dequant8<INT4, HAS_OFF>(w0, w1, o2[b], s2[b], magic);
+#pragma unroll
+                for (int a = 0; a < MT; ++a)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, r.x[a][j]), bf, acc[a][b],
+                                                                       0, 0, 0);
+            }
+    };
+
+    Tile ring[D];
+#pragma unroll
+    for (int q = 0; q < D - 1; ++q) {
+        issue((uint32_t)q, ring[q]);
+        __builtin_amdgcn_sched_barrier(0);  // tiles in order, so each wait below leaves the later ones in flight
+    }
+    // step t issues tile t + D - 1 into the slot step t - 1 consumed, then multiplies tile t; the steps are rounded up
+    // to a multiple of D (tiles past T read and multiply zeros).  The scheduling barrier keeps each step's loads
+    // ahead of its arithmetic (left alone, the scheduler sinks them below it and the ring runs a tile short).
+    for (uint32_t r0 = 0; r0 < T; r0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            issue(r0 + u + D - 1, ring[(u + D - 1) % D]);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(ring[u]);
+        }
+    }
+
+    // partial tiles row-major in LDS: wave kw's value of output (row, col) at red[(kw * 16 MT + row) * ROW + col]
+    float* red = (float*)smem;
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int b = 0; b < NS; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                red[(kw * 16 * MT + 16 * a + 4 * kq + i) * P::ROW + 16 * b + col_in] = acc[a][b][i];
+    __syncthreads();
+    constexpr int PAIRS = MT * 16 * NS * 8;
+    for (int p = threadIdx.x; p < PAIRS; p += P::NT) {
+        const uint32_t row = (uint32_t)p / (NS * 8), c = 2 * ((uint32_t)p % (NS * 8));
+        if (row >= M || c / 16 >= ns) continue;
+        f2x s = *(const f2x*)(red + row * P::ROW + c);
+#pragma unroll
+        for (int w = 1; w < KW; ++w) s += *(const f2x*)(red + (w * 16 * MT + row) * P::ROW + c);
+        uint16_t* yp = A.y + (uint64_t)row * N + s0 * 16 + c;
+        y_put(yp, f32_to_f16_sat(s.x), A.atomic);
+        y_put(yp + 1, f32_to_f16_sat(s.y), A.atomic);
+    }
+}
+
+template <int MT, int NS, int KW, int D>
+static hipError_t launch_aq_kw(uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
+                               const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, int C, int atomic,
+                               hipStream_t st)
+{
+    using P = AqKw<MT, NS, KW>;
+    AqXsArgs A;
+    if (M > 16 * MT || !aq_cols_args(A, y, x, wp, int4, scale, offset, g, M, N, K, C, NS, atomic))
+        return hipErrorInvalidValue;
+#define AQ_KW_LAUNCH(I4, OF)                                                    \
+    do {                                                                        \
+        constexpr auto kern = aq_kw_kernel<MT, NS, KW, D, I4, OF>;               \
+        hipError_t e = ensure_dynamic_lds<kern>(P::LDS);                        \
+        if (e != hipSuccess) return e;                                          \
+        launch_k(kern, dim3((unsigned)C), dim3(P::NT), (uint32_t)P::LDS, st, A); \
+    } while (0)
+    if (int4) {
+        if (offset) AQ_KW_LAUNCH(true, true);
+        else AQ_KW_LAUNCH(true, false);
+    } else {
+        if (offset) AQ_KW_LAUNCH(false, true);
+        else AQ_KW_LAUNCH(false, false);
+    }
+#undef AQ_KW_LAUNCH
+    return hipGetLastError();
+}
+
+// aq_kw_kernel for M <= 32 over C = min(strips, 256) blocks: strips per block NS = ceil(strips / C) <= 4, row tiles
+// MT = 1 or 2.  Four waves (one per SIMD) with two tiles in flight each: against 8 or 16 waves and rings of 1 - 4
+// tiles this measured fastest at K = 4096, N = 11008 for every M in {1, 8, 16, 24, 32}, int4 and int8 (graph
+// replays; e.g. int4 7.9 / 8.7 / 12.2 us at M = 1 / 16 / 32, where 8 waves with 4 tiles in flight took 9.4 / 10.7 /
+// 16.2 us).  Above 32 rows every CU reading all of x costs more than the LDS ring of aq_ring_kernel, which
+// shares each activation copy between two strip groups; those batches stay there.
+static hipError_t launch_aq_kw_any(uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
+                                   const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, int atomic,
+                                   hipStream_t st)
+{
+    const int64_t NBT = N / 16;
+    const int C = (int)(NBT < 256 ? NBT : 256);
+    const int64_t ns = (NBT + C - 1) / C;
+#define AQ_KW_NS(MT)                                                                                  \
+    switch (ns) {                                                                                      \
+    case 1: return launch_aq_kw<MT, 1, 4, 2>(y, x, wp, int4, scale, offset, g, M, N, K, C, atomic, st); \
+    case 2: return launch_aq_kw<MT, 2, 4, 2>(y, x, wp, int4, scale, offset, g, M, N, K, C, atomic, st); \
+    case 3: return launch_aq_kw<MT, 3, 4, 2>(y, x, wp, int4, scale, offset, g, M, N, K, C, atomic, st); \
+    case 4: return launch_aq_kw<MT, 4, 4, 2>(y, x, wp, int4, scale, offset, g, M, N, K, C, atomic, st); \
+    default: return hipErrorInvalidValue;                                                            \
+    }
+    if (M <= 16) { AQ_KW_NS(1) }
+    if (M <= 32) { AQ_KW_NS(2) }
+#undef AQ_KW_NS
+    return hipErrorInvalidValue;
+}
+
 template <int MT, int NS, int KSW, int ST, bool ROT, int DW = ST>
 static void launch_dma(uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
                        const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, int atomic, hipStream_t st)
@@ -1176,12 +1399,15 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
         const int64_t mc = (M - m0) < 64 ? (M - m0) : 64;
         const uint16_t* xc = x + m0 * K;
         uint16_t* yc = y + m0 * N;
-        // Column-block kernels (about 256 workgroups of 2 - 4 strips; shapes measured at K = 4096, N = 11008):
-        // M <= 16 with x[0:M, 0:K] resident in LDS, larger batches with x streamed through an LDS ring.  Shapes
-        // they do not take go to the earlier forms: x staged in LDS for decode batches, else the one-strip ring of
-        // aq_dma_kernel (group a multiple of 128) or activations straight from memory.
+        // Column-block kernels (about 256 workgroups of 1 - 4 strips; shapes measured at K = 4096, N = 11008):
+        // M <= 32 with the K-split waves of aq_kw_kernel, larger batches with x streamed through an LDS ring.
+        // Shapes they do not take (more than 1024 strips, buffers near 2^31 bytes) go to the earlier forms: x
+        // resident in LDS for M <= 16, the LDS ring above, else the one-strip ring of aq_dma_kernel (group a
+        // multiple of 128) or activations straight from memory.
         hipError_t e = hipErrorInvalidValue;
-        if (cols_ok && mc <= 16 && KB % 8 == 0 && aq_xs_lds<2, 2, 4, 2>(mc, K, offset != nullptr))
+        if (cols_ok && mc <= 32 && NBT <= 1024 && aq_cols_fit(mc, N, K, g, int4))
+            e = launch_aq_kw_any(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
+        else if (cols_ok && mc <= 16 && KB % 8 == 0 && aq_xs_lds<2, 2, 4, 2>(mc, K, offset != nullptr))
             e = launch_aq_xs<2, 2, 4, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 4, 256), atomic, st);
         else if (cols_ok && mc <= 16 && KB % 4 == 0 && aq_xs_lds<2, 2, 4, 1>(mc, K, offset != nullptr))
             e = launch_aq_xs<2, 2, 4, 1>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 4, 256), atomic, st);

@@ -397,7 +397,6 @@ __device__ __forceinline__ float load_scale_t(const void* p, int t, int64_t i)
 enum : int { QD_INT8 = 0, QD_E4M3 = 1, QD_E5M2 = 2, QD_E2M1 = 3, QD_E1M2 = 4, QD_HIF8 = 5 };
 constexpr bool qd_nibble(int d) { return d == QD_E2M1 || d == QD_E1M2; }  // two codes a byte
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-typedef float f2x __attribute__((ext_vector_type(2)));
 enum : int { QL_TOKEN = 0, QL_KCOL = 1, QL_KROW = 2 };
 
 // Unsigned division by a runtime constant d for dividends below 2^31: s = ceil(log2 d),

@@ -99,8 +99,8 @@ def test_groups_and_layouts(ascq_gpu, oracle, w_type, group, with_offset, transp
 @pytest.mark.parametrize("M", [6, 16, 24, 48, 64])
 @pytest.mark.parametrize("K", [640, 384])
 def test_batch_ring_partial_rounds(ascq_gpu, oracle, w_type, M, K):
-    """Batches 4 < M <= 64 stage x through an LDS ring of k rounds (128 x 2 or 128 x 4 k per round) and give each
-    workgroup 2 or 4 column strips: K = 640 / 384 end in a partial round, N = 48 in a partial workgroup."""
+    """K = 640 / 384 (5 / 3 k tiles): the waves of a K-split block (M <= 32) get uneven tile counts, one of them none
+    at K = 384; batches above 32 rows end their LDS ring in a partial round.  N = 48: three one-strip blocks."""
     rng = seeded(900 + M + K)
     N, g = 48, 128
     code = O.INT8 if w_type == "int8" else O.INT4
@@ -127,10 +127,15 @@ def test_batch_ring_partial_rounds(ascq_gpu, oracle, w_type, M, K):
     (33, 512, 112, 128),     # 64-row ring, a single round
     (64, 2048, 4112, 256),
     (50, 4096, 1008, 128),
+    (3, 1024, 16384, 128),   # 1024 strips: four per block
+    (20, 768, 13072, 256),   # 817 strips: three or four per block, 32 rows
+    (5, 512, 16400, 128),    # 1025 strips: past the K-split blocks, x resident in LDS
+    (20, 512, 16400, 128),   # 1025 strips, 32-row LDS ring
 ])
 def test_column_block_kernels(ascq_gpu, oracle, w_type, with_offset, M, K, N, group):
-    """Column blocks of 1 - 4 strips (sizes within one strip of each other), x resident in LDS (M <= 16) or streamed
-    through an LDS ring (16 < M <= 64), group sizes 128 << s, with and without offset."""
+    """Column blocks of 1 - 4 strips (sizes within one strip of each other): K-split waves with x read into registers
+    (M <= 32, up to 1024 strips), x resident in LDS (M <= 16) or streamed through an LDS ring (M > 16) beyond that;
+    group sizes 128 << s, with and without offset."""
     rng = seeded(M * 7 + K + N + group)
     code = O.INT8 if w_type == "int8" else O.INT4
     at = ascq_gpu.INT8 if w_type == "int8" else ascq_gpu.INT4
