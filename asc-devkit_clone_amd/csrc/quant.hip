@@ -1406,8 +1406,25 @@ __device__ __forceinline__ void aq_unit(const AntiQuantVecArgs& a, uint32_t u, u
             const uint32_t sb = EIGHT ? (sw[j >> 2] >> (8 * (j & 3))) & 0xffu : sw[0];
             const float sc = sb == 255u ? __uint_as_float(0x7fffffffu)
                                         : (sb == 0u ? __uint_as_float(0x00400000u) : __uint_as_float(sb << 23));
-            y[j] = bf16_round(e[j] * sc);
+            y[j] = e[j] * sc;  // exact (a power of two times a 3-bit value) up to overflow to inf
         }
+        if constexpr (DST == DT_BF16) {
+            // the bf16 rounding two elements per gfx950 conversion (v_cvt_pk_bf16_f32, rne, equal to bf16_round on
+            // every non-NaN input); a NaN product (E8M0 scale 0xFF) keeps its payload's top half, as bf16_round does
+            uint32_t h[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float p0 = y[2 * q], p1 = y[2 * q + 1];
+                const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2x){p0, p1}, bf2));
+                const uint32_t lo = p0 != p0 ? __float_as_uint(p0) >> 16 : w & 0xffffu;
+                const uint32_t hi = p1 != p1 ? __float_as_uint(p1) & 0xffff0000u : w & 0xffff0000u;
+                h[q] = lo | hi;
+            }
+            __builtin_nontemporal_store((u32x4){h[0], h[1], h[2], h[3]}, (u32x4*)a.dst + u);
+            return;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = bf16_round(y[j]);
     } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
