@@ -162,6 +162,38 @@ def test_antiquant_ragged(ascq_gpu, oracle, src_type, transpose, group, dst, ari
     _antiquant_case(ascq_gpu, src_type, transpose, group, dst, arith, True, 100, 90, 73)
 
 
+@pytest.mark.parametrize("src_type", ["int8", "int4"])
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("with_offset", [True, False])
+def test_antiquant_half_extremes(ascq_gpu, oracle, src_type, transpose, with_offset):
+    """Half arithmetic to f16 with scales and offsets at the edges of binary16: +-inf, NaN, 65504, subnormals, and
+    products that overflow; every non-NaN output equals the oracle bit for bit, NaN where the oracle has NaN."""
+    rng = seeded(75)
+    K, N, group = 256, 96, 32
+    G = K // group
+    if src_type == "int8":
+        w = rng.integers(-128, 128, (N, K) if transpose else (K, N), dtype=np.int8)
+        code = O.INT8
+    else:
+        nib = rng.integers(0, 16, K * N, dtype=np.uint8)
+        w = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8)
+        code = O.INT4
+    sshape = (N, G) if transpose else (G, N)
+    special = np.array([np.inf, -np.inf, np.nan, 65504.0, -65504.0, 6e-8, -6e-8, 1e-5, 0.0, -0.0, 300.0, 2.0],
+                       np.float16)
+    scale = rng.choice(special, sshape).astype(np.float16)
+    off = rng.choice(np.concatenate([special, np.float16([-7.5, 0.125, 1000.0])]), sshape).astype(np.float16)
+    off_dev = torch.from_numpy(off).cuda() if with_offset else None
+    y = ascq_gpu.ascend_antiquant(_dev(w), ascq_gpu.INT8 if src_type == "int8" else ascq_gpu.INT4,
+                                  torch.from_numpy(scale).cuda(), off_dev, K, N, group, transpose, torch.float16, 0)
+    y_ref = O.antiquant(w, code, scale.view(np.uint16), off.view(np.uint16) if with_offset else None, K, N, group,
+                        transpose, O.F16, 0)
+    got = y.cpu().view(torch.int16).numpy().view(np.uint16)
+    nan_g, nan_r = np.isnan(got.view(np.float16)), np.isnan(y_ref.view(np.float16))
+    np.testing.assert_array_equal(nan_g, nan_r)
+    np.testing.assert_array_equal(got[~nan_r], y_ref[~nan_r])
+
+
 def test_antiquant_config3_full_size(ascq_gpu, oracle):
     """the weight of the antiquant matmul workload, int4 [4096, 11008] with f16 scale / offset per 128 rows, to f16
     (half arithmetic) and to bf16, against the oracle"""
