@@ -752,7 +752,9 @@ __global__ __launch_bounds__(256) void quant_policy_vec_kernel(QuantPolicyArgs a
             const uint32_t r = fdiv(u, a.upr_div), c = (u - r * a.upr) * 8u;
             const int64_t si = (int64_t)r * a.sk + fdiv(c, a.g_div);
             sr[k].w[0] = load_raw1<SC>(a.scale, si);
-            orw[k].w[0] = load_raw1<SC>(offp, si);
+            // without an offset tensor quant_unit takes the scalar offset: no load (the fp4 outputs, which write a
+            // quarter of what they read, ran 11-12 % faster for it)
+            orw[k].w[0] = off_tensor ? load_raw1<SC>(offp, si) : 0u;
         }
 #pragma unroll
         for (int k = 0; k < QP_UNR; ++k) {
@@ -774,9 +776,9 @@ __global__ __launch_bounds__(256) void quant_policy_vec_krow_kernel(QuantPolicyA
         const uint32_t rb = fdiv(v, a.upr_div), wu = v - rb * a.upr, r0 = rb * QP_UNR;
         const int64_t su = ((int64_t)fdiv(r0, a.g_div) * a.n) / 8 + wu;
         Raw8<SRC> xr[QP_UNR];
-        Raw8<SC> sr, orw;
+        Raw8<SC> sr, orw = {};
         load_raw8<SC>(a.scale, su, sr);
-        load_raw8<SC>(offp, su, orw);
+        if (off_tensor) load_raw8<SC>(offp, su, orw);
 #pragma unroll
         for (int k = 0; k < QP_UNR; ++k) {
             const uint32_t r = r0 + k < rows ? r0 + k : rows - 1u;
