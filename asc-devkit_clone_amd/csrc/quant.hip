@@ -1520,8 +1520,9 @@ __global__ __launch_bounds__(256) void antiquant_policy_vec_kernel(AntiQuantVecA
             aq_load_src<SRC>(a.src, u, x0[k], x1[k]);
             const uint32_t r = fdiv(u, a.upr_div), c = (u - r * a.upr) * 8u;
             const int64_t si = (int64_t)r * a.sk + fdiv(c, a.g_div);
-            if constexpr (SB == 4) sw[k] = ((const uint32_t*)a.scale)[si], ow[k] = ((const uint32_t*)offp)[si];
-            else if constexpr (SB == 2) sw[k] = ((const uint16_t*)a.scale)[si], ow[k] = ((const uint16_t*)offp)[si];
+            // no offset tensor: aq_unit reads no offset, so none is loaded
+            if constexpr (SB == 4) sw[k] = ((const uint32_t*)a.scale)[si], ow[k] = has_off ? ((const uint32_t*)offp)[si] : 0u;
+            else if constexpr (SB == 2) sw[k] = ((const uint16_t*)a.scale)[si], ow[k] = has_off ? ((const uint16_t*)offp)[si] : 0u;
             else sw[k] = ((const uint8_t*)a.scale)[si], ow[k] = 0u;
         }
 #pragma unroll
@@ -1547,9 +1548,9 @@ __global__ __launch_bounds__(256) void antiquant_policy_vec_krow_kernel(AntiQuan
     for (uint32_t v = blockIdx.x * 256u + threadIdx.x; v < a.units; v += gridDim.x * 256u) {
         const uint32_t rb = fdiv(v, a.upr_div), wu = v - rb * a.upr, r0 = rb * AQ_UNR;
         const int64_t si = (int64_t)fdiv(r0, a.g_div) * a.n + 8 * (int64_t)wu;
-        uint32_t sw[SW], ow[SW], x0[AQ_UNR], x1[AQ_UNR];
+        uint32_t sw[SW], ow[SW] = {}, x0[AQ_UNR], x1[AQ_UNR];
         aq_load8<SB>(a.scale, si, sw);
-        if constexpr (SB != 1) aq_load8<SB>(offp, si, ow);
+        if (SB != 1 && has_off) aq_load8<SB>(offp, si, ow);
 #pragma unroll
         for (int k = 0; k < AQ_UNR; ++k) {
             const uint32_t r = r0 + k < rows ? r0 + k : rows - 1u;
