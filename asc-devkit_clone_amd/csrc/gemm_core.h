@@ -199,7 +199,7 @@ struct CoreArgs {
 // 8 q + 4 (l / 32) + e -- four consecutive columns of one row per register quad, which an epilogue stores as one
 // vector (no LDS round trip); ct_row / ct_col give the coordinates.
 template <int BM, int BN, int WM, int WN, int STAGES, bool B_KCONTIG, int OP, int ROWB_ = 64, int FMT = 0, bool ILV = true,
-          bool CT = false>
+          bool CT = false, bool B_TR = false>
 struct GemmCore {
     static constexpr bool IS_MX = OP == OP_MXFP4 || OP == OP_MXF8 || OP == OP_MXFP6;
     static constexpr bool IS_F8 = OP == OP_F8 || OP == OP_MXF8;
@@ -217,7 +217,11 @@ struct GemmCore {
     static constexpr int RPW = 256 / ROWB;            // rows per 256-byte bank window
     static constexpr int ROWS_PER_COPY = 64 / CH;     // rows one wave-wide 1 KiB copy covers
     static constexpr int A_COPIES = BM / ROWS_PER_COPY / NW;              // per wave per stage
-    static constexpr int B_COPIES = B_KCONTIG ? BN / ROWS_PER_COPY / NW : 0;
+    // B_TR (int8, B given [K, N]): B's K rows are copied like A's (16-byte DMA chunks, BN bytes a row, 1 KiB a copy)
+    // into a [ROWB][BN] region and each fragment is read with two ds_read_b64_tr_b8 (below)
+    static constexpr int B_COPIES = B_KCONTIG ? BN / ROWS_PER_COPY / NW : (B_TR ? ROWB * BN / 1024 / NW : 0);
+    static constexpr int CHB = BN / 16;                  // B_TR: 16-byte chunks per K row
+    static constexpr int RWB = CHB >= 16 ? 1 : 16 / CHB;  // B_TR: K rows per 256-byte bank window
     static constexpr int KSB = IS_F8 ? 64 : 32;       // K bytes per row per k-step
     static constexpr int LCH = KSB / 32;              // 16-byte chunks per lane per k-step
     static constexpr int KPS = ROWB / KSB;            // k-steps per stage
@@ -245,7 +249,7 @@ struct GemmCore {
     static constexpr int SC_COPIES = (AUX_INSTR + NW - 1) / NW;
     static constexpr int SC_BYTES = SA_REG + SB_REG;
     static constexpr int COPIES = A_COPIES + B_COPIES + SC_COPIES;
-    static constexpr int B_BLK = B_KCONTIG ? 0 : (ROWB / 8) * (BN / 4) / NT;  // 8x4-byte blocks per lane
+    static constexpr int B_BLK = (B_KCONTIG || B_TR) ? 0 : (ROWB / 8) * (BN / 4) / NT;  // 8x4-byte blocks per lane
     static constexpr int B_LOADS = 8 * B_BLK;         // dword loads per lane per stage for a [K, N] B
     static constexpr int STAGE = (BM + BN) * ROWB + Q_REG + SC_BYTES;
     static constexpr int SC_OFF = (BM + BN) * ROWB + Q_REG;  // the scale regions within a stage
@@ -258,13 +262,15 @@ struct GemmCore {
     static_assert(FM >= 1 && FN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
     static_assert(BM % (ROWS_PER_COPY * NW) == 0 && A_COPIES >= 1, "A copies must split evenly over the waves");
     static_assert(!B_KCONTIG || (BN % (ROWS_PER_COPY * NW) == 0 && B_COPIES >= 1), "B copies");
-    static_assert(B_KCONTIG || (((ROWB / 8) * (BN / 4)) % NT == 0 && B_BLK >= 1), "B blocks");
+    static_assert(B_KCONTIG || B_TR || (((ROWB / 8) * (BN / 4)) % NT == 0 && B_BLK >= 1), "B blocks");
+    static_assert(!B_TR || (!B_KCONTIG && OP == OP_I8 && 1024 % BN == 0 && BN >= 32 &&
+                            (ROWB * BN) % (1024 * NW) == 0 && B_COPIES >= 1), "B_TR copies");
     static_assert(!IS_MX || B_KCONTIG, "MX B must be K-contiguous");
     static_assert(!IS_MX || (BM % 64 == 0 && BN % 64 == 0), "scale row groups");
     static_assert(!IS_MX || SCB % 4 == 0 || SCB == 2, "MX stage scale bytes per row");
     static_assert(!IS_FP6 || (ROWB == 64 && BM % 32 == 0 && BN % 32 == 0), "fp6 Q blocks: 4 MX blocks per stage");
     static_assert(KPS >= 1, "a stage holds at least one k-step");
-    static_assert((STAGES >= 3 || (B_KCONTIG && STAGES == 2)) && IN_FLIGHT < 64, "stages");
+    static_assert((STAGES >= 3 || ((B_KCONTIG || B_TR) && STAGES == 2)) && IN_FLIGHT < 64, "stages");
     static_assert(ROWB == 64 || ROWB == 128, "stage row");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 
@@ -280,6 +286,63 @@ struct GemmCore {
         return wn * WTN + j * 32 + 8 * q + 4 * (lane >> 5);
     }
     __device__ __forceinline__ static int swz(int row, int c) { return c ^ ((row / RPW) % CH); }
+    // B_TR: the physical 16-byte chunk of logical chunk c of K row kr.  A transposed read of k-step s takes 16 K rows
+    // (two runs of 8) x 32 bytes; the XOR spreads each run's 8 rows x 2 chunks over 16 distinct 16-byte bank groups
+    // (the second run repeats them: two passes, the minimum for 512 bytes)
+    __device__ __forceinline__ static int swzb(int kr, int c) { return c ^ (((kr / RWB) & (CHB / 2 - 1)) << 1); }
+
+    // B_TR: the int8 B fragment of k-step s, column block starting at n0 (a multiple of 32), from a [ROWB][BN] region.
+    // ds_read_b64_tr_b8 gives lane j of each 16-lane group byte (j % 8) of the 8-byte pieces addressed by lanes
+    // 2r + j / 8, r = 0..7: here lanes 2r, 2r + 1 address the two halves of 16 columns of K row k0 + r, so lane j
+    // receives K rows k0 .. k0 + 7 of column j -- the group (kh, nh) = (lane / 32, lane / 16 % 2) takes rows
+    // 32 s + 16 kh + 8 q + (0..7) and columns n0 + 16 nh + (0..15); two reads (q = 0, 1) give the lane's 16
+    // consecutive K bytes, in the order of the A fragment's 16 bytes.
+    // The reads are inline assembly: through the builtin the compiler cannot tell them apart from the stage copies'
+    // LDS destinations and drains every copy in flight (s_waitcnt vmcnt(0)) before each one, which measured twice
+    // the kernel time.  The stage protocol (each wave's counted wait, then the barrier) already orders them after
+    // the copies of their stage, and volatile keeps them below that barrier.  All FN fragments of a k-step are read
+    // in one block that ends with s_waitcnt lgkmcnt(0), so its outputs hold the data when the block completes (the
+    // compiler does not track the loads; a separate wait would let it schedule the MFMAs above it).
+    __device__ __forceinline__ static uint32_t tr_addr(const uint8_t* base, int n0, int s, int q, int lane)
+    {
+        const int i = lane & 15, g = lane >> 4;
+        const int c = (n0 >> 4) + (g & 1);
+        const int kr = 32 * s + 16 * (g >> 1) + 8 * q + (i >> 1);
+        const uint8_t* a = base + kr * BN + swzb(kr, c) * 16 + (i & 1) * 8;
+        return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)a;
+    }
+    __device__ __forceinline__ static void read_frags_tr(const uint8_t* base, int n0w, int s, int lane, v4i (&f)[FN])
+    {
+        typedef int v2i_t __attribute__((ext_vector_type(2)));
+        static_assert(FN == 1 || FN == 2 || FN == 4, "B_TR fragments per wave");
+        v2i_t r[2 * FN];
+        uint32_t ad[2 * FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) ad[2 * j + q] = tr_addr(base, n0w + 32 * j, s, q, lane);
+        if constexpr (FN == 1) {
+            asm volatile("ds_read_b64_tr_b8 %0, %2\n\tds_read_b64_tr_b8 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                         : "=&v"(r[0]), "=&v"(r[1])
+                         : "v"(ad[0]), "v"(ad[1]));
+        } else if constexpr (FN == 2) {
+            asm volatile("ds_read_b64_tr_b8 %0, %4\n\tds_read_b64_tr_b8 %1, %5\n\t"
+                         "ds_read_b64_tr_b8 %2, %6\n\tds_read_b64_tr_b8 %3, %7\n\ts_waitcnt lgkmcnt(0)"
+                         : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+                         : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]));
+        } else {
+            asm volatile("ds_read_b64_tr_b8 %0, %8\n\tds_read_b64_tr_b8 %1, %9\n\t"
+                         "ds_read_b64_tr_b8 %2, %10\n\tds_read_b64_tr_b8 %3, %11\n\t"
+                         "ds_read_b64_tr_b8 %4, %12\n\tds_read_b64_tr_b8 %5, %13\n\t"
+                         "ds_read_b64_tr_b8 %6, %14\n\tds_read_b64_tr_b8 %7, %15\n\ts_waitcnt lgkmcnt(0)"
+                         : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]),
+                           "=&v"(r[7])
+                         : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "v"(ad[4]), "v"(ad[5]), "v"(ad[6]),
+                           "v"(ad[7]));
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) f[j] = (v4i){r[2 * j].x, r[2 * j].y, r[2 * j + 1].x, r[2 * j + 1].y};
+    }
 
     // MX scale bytes of pair h for one tile row: four blocks (a 32-bit word), or two when a stage holds a single
     // fp8 k-step (SCB = 2)
@@ -320,7 +383,7 @@ struct GemmCore {
 
         // [K, N] B: the 8x4-byte blocks of stage kt into rbt
         auto load_b_regs = [&](breg_t& rbt, int64_t kt) {
-            if constexpr (!B_KCONTIG) {
+            if constexpr (!B_KCONTIG && !B_TR) {
                 const int64_t kb0 = kt * ROWB;
 #pragma unroll
                 for (int i = 0; i < B_BLK; ++i) {
@@ -337,7 +400,7 @@ struct GemmCore {
         };
         // transpose the blocks held in rb and write them K-contiguous into the B part of a slot
         auto store_b_regs = [&](breg_t& rb, int slot) {
-            if constexpr (!B_KCONTIG) {
+            if constexpr (!B_KCONTIG && !B_TR) {
                 uint8_t* sB = smem + slot * STAGE + BM * ROWB;
 #pragma unroll
                 for (int i = 0; i < B_BLK; ++i) {
@@ -404,11 +467,23 @@ struct GemmCore {
                 const uint32_t off = (row < p.rows && k < p.kbytes) ? p.a0 + (uint32_t)row * p.lda + (uint32_t)k : OOB;
                 copy16_to_lds(p.a, sA + row0 * ROWB, off);
             } else if (u < A_COPIES + B_COPIES) {
-                const int row0 = (wave * B_COPIES + (u - A_COPIES)) * ROWS_PER_COPY;
-                const int row = row0 + rin;
-                const int64_t k = kb0 + swz(row, phys) * 16;
-                const uint32_t off = (row < p.cols && k < p.kbytes) ? p.b0 + (uint32_t)row * p.ldb + (uint32_t)k : OOB;
-                copy16_to_lds(p.b, sB + row0 * ROWB, off);
+                if constexpr (B_TR) {
+                    // K rows kr of the stage, BN bytes each; lane's LDS chunk pb of row kr holds logical chunk
+                    // swzb(kr, pb) (the XOR is its own inverse); chunks past the tile's columns read zeros
+                    const int cc = wave * B_COPIES + (u - A_COPIES);
+                    const int kr = cc * (1024 / BN) + lane / CHB, pb = lane % CHB;
+                    const int c = swzb(kr, pb);
+                    const int64_t k = kb0 + kr;
+                    const uint32_t off =
+                        (c * 16 < p.cols && k < p.kbytes) ? p.b0 + (uint32_t)k * p.ldb + (uint32_t)(c * 16) : OOB;
+                    copy16_to_lds(p.b, sB + cc * 1024, off);
+                } else {
+                    const int row0 = (wave * B_COPIES + (u - A_COPIES)) * ROWS_PER_COPY;
+                    const int row = row0 + rin;
+                    const int64_t k = kb0 + swz(row, phys) * 16;
+                    const uint32_t off = (row < p.cols && k < p.kbytes) ? p.b0 + (uint32_t)row * p.ldb + (uint32_t)k : OOB;
+                    copy16_to_lds(p.b, sB + row0 * ROWB, off);
+                }
             } else if constexpr (IS_MX) {
                 const AuxCopy& x = aux[u - A_COPIES - B_COPIES];
                 const bool kval = (uint32_t)(kt * SCB) < p.sk;
@@ -489,9 +564,16 @@ struct GemmCore {
                             fa[i][5] = (int)q[1];
                         }
                     }
+                    v4i ftr[FN];
+                    if constexpr (B_TR) read_frags_tr(sB, wn * WTN, s, lane, ftr);
 #pragma unroll
                     for (int j = 0; j < FN; ++j) {
-                        v8i fb = read_frag(sB, wn * WTN + j * 32 + r32, s, kh);
+                        v8i fb;
+                        if constexpr (B_TR) {
+                            fb = (v8i){ftr[j][0], ftr[j][1], ftr[j][2], ftr[j][3], 0, 0, 0, 0};
+                        } else {
+                            fb = read_frag(sB, wn * WTN + j * 32 + r32, s, kh);
+                        }
                         if constexpr (IS_FP6) {
                             const u32x2 q = read_q(sA + (BM + BN) * ROWB + QA_INSTR * 1024, wn * WTN + j * 32 + r32, s, kh);
                             fb[4] = (int)q[0];
@@ -519,7 +601,7 @@ struct GemmCore {
                     }
                 }
             }
-            if constexpr (!B_KCONTIG) {
+            if constexpr (!B_KCONTIG && !B_TR) {
                 // rb_old's slot was freed two iterations ago and is next read after at least one more barrier
                 __builtin_amdgcn_sched_barrier(0);
                 store_b_regs(rb_old, pslot);

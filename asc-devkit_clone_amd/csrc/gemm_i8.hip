@@ -157,11 +157,12 @@ __device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* wtot
 }
 
 // WPE: waves per SIMD the register allocation must allow (2 for two 4-wave workgroups per CU)
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1, bool BTR = false>
 __global__ __launch_bounds__(WM * WN * 64, WPE) void group_gemm_i8_kernel(GroupGemmArgs p)
 {
-    // transposed accumulators: four consecutive output columns per register quad, stored as one 8-byte vector
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB, 0, true, true>;
+    // transposed accumulators: four consecutive output columns per register quad, stored as one 8-byte vector;
+    // BTR: W given [G, K, N] staged by K rows and read with LDS transpose reads
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB, 0, true, true, BTR>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int64_t wtot[T::NT / 64];
     __shared__ int64_t tile_info[4];  // group, first row, end row, first m-tile of this workgroup's tile
@@ -407,15 +408,15 @@ __global__ __launch_bounds__(256) void group_gemm_generic_kernel(GroupGemmArgs p
     }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1, bool BTR = false>
 static hipError_t launch_group_tiled(const GroupGemmArgs& a, hipStream_t st)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB>;
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB, 0, true, true, BTR>;
     const int64_t upper = ((a.M + BM - 1) / BM + a.G) * ((a.N + BN - 1) / BN);  // tiles, at most
-    const hipError_t e = ensure_dynamic_lds<group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, WPE>>((int)T::LDS_BYTES);
+    const hipError_t e = ensure_dynamic_lds<group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, WPE, BTR>>((int)T::LDS_BYTES);
     if (e != hipSuccess) return e;
-    launch_k((group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, WPE>), dim3((unsigned)((upper + 7) / 8 * 8)), dim3(T::NT),
-             T::LDS_BYTES, st, a);
+    launch_k((group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, WPE, BTR>), dim3((unsigned)((upper + 7) / 8 * 8)),
+             dim3(T::NT), T::LDS_BYTES, st, a);
     return hipGetLastError();
 }
 
@@ -433,6 +434,12 @@ hipError_t launch_group_gemm(const GroupGemmArgs& a, hipStream_t st)
         if (a.w_trans && a.K <= 2048) return launch_group_tiled<128, 256, 2, 2, 3, true, 64, 2>(a, st);
         if (a.w_trans && a.K % 128 == 0) return launch_group_tiled<128, 256, 2, 4, 3, true, 128>(a, st);
         if (a.w_trans) return launch_group_tiled<128, 256, 2, 4, 6, true>(a, st);
+        // W [G, K, N] with 16-byte K rows: the same tiles, K rows copied like A's and read by LDS transpose reads
+        if (a.N % 16 == 0 && (uintptr_t)a.W % 16 == 0) {
+            if (a.K <= 2048) return launch_group_tiled<128, 256, 2, 2, 3, false, 64, 2, true>(a, st);
+            if (a.K % 128 == 0) return launch_group_tiled<128, 256, 2, 4, 3, false, 128, 1, true>(a, st);
+            return launch_group_tiled<128, 256, 2, 4, 6, false, 64, 1, true>(a, st);
+        }
         return launch_group_tiled<128, 128, 2, 2, 4, false>(a, st);
     }
     int64_t blocks = (a.M * a.N + 255) / 256;
