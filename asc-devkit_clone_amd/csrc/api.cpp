@@ -171,11 +171,14 @@ bool has_quant_epilogue(const ascq_matmul_types& t)
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-// int8 / fp8 B given [K, N]: for large problems the whole org B is transposed to [N, K] in the workspace
-// first, so the GEMM copies both operands straight into LDS (the transpose costs 2 K N bytes of traffic; the
-// in-loop byte transpose of the [K, N] path roughly halves the GEMM's rate).
+// int8 / fp8 B given [K, N]: for large problems the whole org B is transposed to [N, K] in the workspace first,
+// so the GEMM copies both operands straight into LDS (the transpose costs 2 K N bytes of traffic; the in-loop byte
+// transpose of the [K, N] path roughly halves the GEMM's rate).  Below the 256 x 256 tile sizes (M or N < 1024) an
+// int8 B [K, N] with N % 16 == 0 is not transposed: its GEMM copies the K rows into LDS and reads them with LDS
+// transpose reads.
 bool bytes_transposes_b(const ascq_matmul_s* h)
 {
+    if (kind_of(h->ty) == K_INT8 && h->N % 16 == 0 && (h->M < 1024 || h->N < 1024)) return false;
     return !h->trans_b && h->M >= 512 && h->N % 16 == 0 && h->K % 16 == 0;
 }
 

@@ -24,10 +24,10 @@ __device__ __forceinline__ int64_t uniform64(int64_t v)
     return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, bool BTR = false>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB>;
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB, 0, true, false, BTR>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tiles_m = (int)((p.M + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
     int tm, tn;
@@ -345,14 +345,14 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(GemmI8Args p)
     }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, bool BTR = false>
 static hipError_t launch_tiled(const GemmI8Args& a, hipStream_t st)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB>;
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB, 0, true, false, BTR>;
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
-    const hipError_t e = ensure_dynamic_lds<gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>>((int)T::LDS_BYTES);
+    const hipError_t e = ensure_dynamic_lds<gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, BTR>>((int)T::LDS_BYTES);
     if (e != hipSuccess) return e;
-    launch_k((gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
+    launch_k((gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, BTR>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
     return hipGetLastError();
 }
 
@@ -371,6 +371,12 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
             return big ? (a.K % 128 == 0 ? launch_tiled<256, 256, 4, 2, 2, true, 128>(a, st)
                                          : launch_tiled<256, 256, 4, 2, 4, true>(a, st))
                        : (tiny ? launch_tiled<32, 32, 1, 1, 4, true>(a, st) : launch_tiled<64, 64, 2, 2, 4, true>(a, st));
+        // B [K, N] with 16-byte K rows (small and medium problems; the host transposes a large one first): the K
+        // rows are copied like A's and read by LDS transpose reads.  For 256 x 256 tiles that measured slower than
+        // the transpose plus the K-contiguous kernel (632.7 against 602 us at 8192^3: the 128-byte-stage form spills)
+        if (!big && a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0)
+            return tiny ? launch_tiled<32, 32, 1, 1, 4, false, 64, true>(a, st)
+                        : launch_tiled<64, 128, 2, 2, 4, false, 64, true>(a, st);
         if (tiny) return launch_tiled<32, 32, 1, 1, 4, false>(a, st);
         return big ? launch_tiled<256, 256, 4, 2, 4, false>(a, st) : launch_tiled<64, 128, 2, 2, 4, false>(a, st);
     }
@@ -435,8 +441,8 @@ hipError_t launch_group_gemm(const GroupGemmArgs& a, hipStream_t st)
         if (a.w_trans && a.K % 128 == 0) return launch_group_tiled<128, 256, 2, 4, 3, true, 128>(a, st);
         if (a.w_trans) return launch_group_tiled<128, 256, 2, 4, 6, true>(a, st);
         // W [G, K, N] with 16-byte K rows: the same tiles, K rows copied like A's and read by LDS transpose reads
+        // (the 4-wave, two-workgroups-per-CU form of the short-K case spills here: 8 waves for every K)
         if (a.N % 16 == 0 && (uintptr_t)a.W % 16 == 0) {
-            if (a.K <= 2048) return launch_group_tiled<128, 256, 2, 2, 3, false, 64, 2, true>(a, st);
             if (a.K % 128 == 0) return launch_group_tiled<128, 256, 2, 4, 3, false, 128, 1, true>(a, st);
             return launch_group_tiled<128, 256, 2, 4, 6, false, 64, 1, true>(a, st);
         }

@@ -40,10 +40,11 @@ def _same(c1, c2):
 
 
 def test_noalloc_int8_kn_b(ascq_gpu, oracle):
-    """int8 x int8 -> f16 (VDEQF16), B given [K, N] with M >= 512: B is transposed into the workspace"""
+    """int8 x int8 -> f16 (VDEQF16), B given [K, N] with M, N >= 1024 (the 256 x 256 tile sizes): B is transposed
+    into the workspace (smaller [K, N] problems read it in place with LDS transpose reads)"""
     ascq = ascq_gpu
     mm = ascq.Matmul(ascq.INT8, ascq.INT8, ascq.F16, ascq.INT32)
-    for i, (M, N, K) in enumerate([(1024, 768, 512), (512, 256, 384)]):
+    for i, (M, N, K) in enumerate([(1024, 1024, 512), (1024, 1024, 256)]):
         rng = seeded(300 + i)
         A = rng.integers(-127, 128, (M, K), dtype=np.int8)
         B = rng.integers(-127, 128, (K, N), dtype=np.int8)
