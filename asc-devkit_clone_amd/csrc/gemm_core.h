@@ -263,7 +263,7 @@ struct GemmCore {
     static_assert(BM % (ROWS_PER_COPY * NW) == 0 && A_COPIES >= 1, "A copies must split evenly over the waves");
     static_assert(!B_KCONTIG || (BN % (ROWS_PER_COPY * NW) == 0 && B_COPIES >= 1), "B copies");
     static_assert(B_KCONTIG || B_TR || (((ROWB / 8) * (BN / 4)) % NT == 0 && B_BLK >= 1), "B blocks");
-    static_assert(!B_TR || (!B_KCONTIG && OP == OP_I8 && 1024 % BN == 0 && BN >= 32 &&
+    static_assert(!B_TR || (!B_KCONTIG && OP == OP_I8 && 1024 % BN == 0 && BN >= 32 && BN <= 256 &&
                             (ROWB * BN) % (1024 * NW) == 0 && B_COPIES >= 1), "B_TR copies");
     static_assert(!IS_MX || B_KCONTIG, "MX B must be K-contiguous");
     static_assert(!IS_MX || (BM % 64 == 0 && BN % 64 == 0), "scale row groups");
@@ -303,15 +303,17 @@ struct GemmCore {
     // the copies of their stage, and volatile keeps them below that barrier.  All FN fragments of a k-step are read
     // in one block that ends with s_waitcnt lgkmcnt(0), so its outputs hold the data when the block completes (the
     // compiler does not track the loads; a separate wait would let it schedule the MFMAs above it).
-    __device__ __forceinline__ static uint32_t tr_addr(const uint8_t* base, int n0, int s, int q, int lane)
+    // lane offset in the B region of its first transposed read (k-step 0, q = 0) of the fragment at columns n0 .. n0
+    // + 31: the read of k-step s, piece q is 32 s + 8 q rows further down, and swzb is the same for those rows (the
+    // step is a multiple of its period for BN <= 256), so this offset is worked out once per fragment column
+    __device__ __forceinline__ static uint32_t tr_lane_off(int n0, int lane)
     {
         const int i = lane & 15, g = lane >> 4;
         const int c = (n0 >> 4) + (g & 1);
-        const int kr = 32 * s + 16 * (g >> 1) + 8 * q + (i >> 1);
-        const uint8_t* a = base + kr * BN + swzb(kr, c) * 16 + (i & 1) * 8;
-        return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)a;
+        const int kr = 16 * (g >> 1) + (i >> 1);
+        return (uint32_t)(kr * BN + swzb(kr, c) * 16 + (i & 1) * 8);
     }
-    __device__ __forceinline__ static void read_frags_tr(const uint8_t* base, int n0w, int s, int lane, v4i (&f)[FN])
+    __device__ __forceinline__ static void read_frags_tr(uint32_t region, const uint32_t (&off)[FN], int s, v4i (&f)[FN])
     {
         typedef int v2i_t __attribute__((ext_vector_type(2)));
         static_assert(FN == 1 || FN == 2 || FN == 4, "B_TR fragments per wave");
@@ -320,7 +322,7 @@ struct GemmCore {
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int q = 0; q < 2; ++q) ad[2 * j + q] = tr_addr(base, n0w + 32 * j, s, q, lane);
+            for (int q = 0; q < 2; ++q) ad[2 * j + q] = region + off[j] + (uint32_t)((32 * s + 8 * q) * BN);
         if constexpr (FN == 1) {
             asm volatile("ds_read_b64_tr_b8 %0, %2\n\tds_read_b64_tr_b8 %1, %3\n\ts_waitcnt lgkmcnt(0)"
                          : "=&v"(r[0]), "=&v"(r[1])
@@ -502,6 +504,9 @@ struct GemmCore {
 
         const int r32 = lane & 31, kh = lane >> 5;
         const int64_t nk = (p.kbytes + ROWB - 1) / ROWB;
+        uint32_t troff[FN];  // B_TR: this lane's read offsets, one per fragment column
+#pragma unroll
+        for (int j = 0; j < FN; ++j) troff[j] = B_TR ? tr_lane_off(wn * WTN + j * 32, lane) : 0u;
 
         // prologue: stages 0 .. STAGES - 2 in flight; a [K, N] B is written for stages 0 .. STAGES - 3 and
         // held in rb1 for stage STAGES - 2 (written at the end of iteration 0)
@@ -565,7 +570,8 @@ struct GemmCore {
                         }
                     }
                     v4i ftr[FN];
-                    if constexpr (B_TR) read_frags_tr(sB, wn * WTN, s, lane, ftr);
+                    if constexpr (B_TR)
+                        read_frags_tr((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)sB, troff, s, ftr);
 #pragma unroll
                     for (int j = 0; j < FN; ++j) {
                         v8i fb;
