@@ -156,3 +156,33 @@ def test_fp4_every_byte_every_position(ascq_gpu, dst_type, fp4):
     got = _run(ascq_gpu, packed, fp4, e, O.E8M0, dst_type, O.PER_GROUP, m, n, g, None, 1)
     exp = O.antiquant_policy(packed, fp4, e, O.E8M0, dst_type, O.PER_GROUP, m, n, g, None, 1)
     assert _same(got, exp, dst_type)
+
+
+@pytest.mark.parametrize("case", ["int8_g32_off", "int8_token_tr", "fp8_g64_f32", "fp4_g32", "int8_g96_f32"])
+def test_large_row_blocks_with_tails(ascq_gpu, case):
+    """Groups down the columns on [~2060, 16384] tensors (over 2^20 lanes of the row-blocked kernel): row counts
+    that leave a partial last block of rows, a group size that is a multiple of the block, and PER_TOKEN by column
+    as one group over every row."""
+    n = 16384
+    rng = seeded(131 + len(case))
+    if case == "int8_g32_off":
+        m, src_type, sct, dt, policy, g, tr = 2057, O.INT8, O.F16, O.F16, O.PER_GROUP, 32, False
+    elif case == "int8_token_tr":
+        m, src_type, sct, dt, policy, g, tr = 2050, O.INT8, O.BF16, O.BF16, O.PER_TOKEN, 0, True
+    elif case == "fp8_g64_f32":
+        m, src_type, sct, dt, policy, g, tr = 2113, O.FP8_E4M3, O.F32, O.F16, O.PER_GROUP, 64, False
+    elif case == "fp4_g32":
+        m, src_type, sct, dt, policy, g, tr = 2074, O.FP4_E2M1, O.E8M0, O.BF16, O.PER_GROUP, 32, False
+    else:
+        m, src_type, sct, dt, policy, g, tr = 2063, O.INT8, O.F32, O.BF16, O.PER_GROUP, 96, False
+    shape = _sshape(policy, m, n, g, 0, tr)
+    if src_type == O.FP4_E2M1:
+        src = rng.integers(0, 256, (m, n // 2)).astype(np.uint8)
+        sc, of = rng.integers(100, 155, shape).astype(np.uint8), None
+    else:
+        src = rng.integers(-128 if src_type == O.INT8 else 0, 128 if src_type == O.INT8 else 256, (m, n))
+        src = src.astype(np.int8 if src_type == O.INT8 else np.uint8)
+        sc, of = _scales(rng, shape, sct)
+    got = _run(ascq_gpu, src, src_type, sc, sct, dt, policy, m, n, g, of, 0, tr)
+    exp = O.antiquant_policy(src, src_type, sc, sct, dt, policy, m, n, g, of, 0, tr)
+    assert _same(got, exp, dt), int((got != exp).sum())
