@@ -789,7 +789,7 @@ def _with_roofline(r):
     return r
 
 
-# CPU baselines of the BASELINE configs' families: (family, index in OTHER[family]) -> oracle timing
+# CPU baselines of the benchmark workload families: (family, index in OTHER[family]) -> oracle timing
 CPU_FOR = {
     ("w8a8", 0): lambda: cpu_baseline_w8a8(128, 256, 512),
     ("w8a8", 1): lambda: cpu_baseline_w8a8(8192, 8192, 8192),
