@@ -135,7 +135,7 @@ struct ascq_matmul_s {
 
 namespace {
 
-enum Kind { K_NONE, K_INT8, K_ANTIQUANT, K_MX, K_F8, K_INT4 };
+enum Kind { K_NONE, K_INT8, K_ANTIQUANT, K_MX, K_F8, K_INT4, K_HIF8 };
 
 bool is_f8(int32_t t) { return t == ASCQ_DT_FP8_E4M3 || t == ASCQ_DT_FP8_E5M2; }
 bool is_fp4(int32_t t) { return t == ASCQ_DT_FP4_E2M1 || t == ASCQ_DT_FP4_E1M2; }
@@ -152,6 +152,8 @@ Kind kind_of(const ascq_matmul_types& t)
         ((is_fp4(t.a_type) && is_fp4(t.b_type)) || (is_f8(t.a_type) && is_f8(t.b_type))))
         return K_MX;
     if (t.scale_type == 0 && is_f8(t.a_type) && is_f8(t.b_type)) return K_F8;
+    // hifloat8 A and B (the same type for both, matmul_fp8/README_en.md; quant_processor_utils.h:36-41)
+    if (t.scale_type == 0 && t.a_type == ASCQ_DT_HIF8 && t.b_type == ASCQ_DT_HIF8) return K_HIF8;
     return K_NONE;
 }
 
@@ -166,8 +168,12 @@ bool mx_is_fp6(const ascq_matmul_s* h)
 bool has_quant_epilogue(const ascq_matmul_types& t)
 {
     const Kind k = kind_of(t);
-    return ((k == K_INT8 || k == K_INT4) && t.c_type != ASCQ_DT_INT32) || k == K_F8;
+    return ((k == K_INT8 || k == K_INT4) && t.c_type != ASCQ_DT_INT32) || k == K_F8 || k == K_HIF8;
 }
+
+// hifloat8 Matmul: both operands are decoded to bf16 rows of hif8_k_pad(K) values (K rounded up to a whole 16-byte
+// chunk, the padding zero) in the workspace, A as [M, Kp] and B as [N, Kp]
+int64_t hif8_k_pad(int64_t K) { return (K + 7) / 8 * 8; }
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
@@ -198,6 +204,8 @@ size_t workspace_need(const ascq_matmul_s* h)
     switch (kind_of(h->ty)) {
     case K_INT8:
     case K_F8: return bytes_workspace(h);
+    case K_HIF8:
+        return align256((size_t)h->M * (size_t)hif8_k_pad(h->K) * 2) + align256((size_t)h->N * (size_t)hif8_k_pad(h->K) * 2);
     case K_INT4:  // A and B unpacked to int8 [M, K] / [N, K]; a [K, N] B is nibble-transposed to [N, K/2] first
         return align256((size_t)h->M * (size_t)h->K) + align256((size_t)h->N * (size_t)h->K) +
                (h->trans_b ? 0 : align256((size_t)h->N * (size_t)h->K / 2));
@@ -336,15 +344,17 @@ ascq_status ascq_matmul_create(const ascq_matmul_types* types, ascq_matmul_t* ou
     } else if (k == K_ANTIQUANT) {
         if (types->c_type != ASCQ_DT_F16) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: weight-only matmul supports C = f16");
         if (types->bias_type != 0) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: weight-only matmul has no bias path");
-    } else if (k == K_F8) {
+    } else if (k == K_F8 || k == K_HIF8) {
+        const char* what = k == K_F8 ? "fp8" : "hifloat8";
         if (types->c_type != ASCQ_DT_F16 && types->c_type != ASCQ_DT_BF16 && types->c_type != ASCQ_DT_F32 &&
             types->c_type != ASCQ_DT_INT8 && types->c_type != ASCQ_DT_UINT8 && types->c_type != ASCQ_DT_INT4 &&
-            !is_f8(types->c_type))
+            !is_f8(types->c_type) && types->c_type != ASCQ_DT_HIF8)
             return fail(ASCQ_E_UNSUPPORTED,
-                        "matmul_create: fp8 matmul supports C = f16, bf16, f32, int8, uint8, int4, fp8_e4m3 or fp8_e5m2");
+                        "matmul_create: %s matmul supports C = f16, bf16, f32, int8, uint8, int4, fp8_e4m3, fp8_e5m2 or "
+                        "hifloat8", what);
         if (types->bias_type != 0 && types->bias_type != ASCQ_DT_F32)
-            return fail(ASCQ_E_UNSUPPORTED, "matmul_create: fp8 matmul bias must be f32");
-        if (types->b_format != ASCQ_FORMAT_ND) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: fp8 B must be ND");
+            return fail(ASCQ_E_UNSUPPORTED, "matmul_create: %s matmul bias must be f32", what);
+        if (types->b_format != ASCQ_FORMAT_ND) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: %s B must be ND", what);
     } else {
         if (types->c_type != ASCQ_DT_BF16 && types->c_type != ASCQ_DT_F32)
             return fail(ASCQ_E_UNSUPPORTED, "matmul_create: MX matmul supports C = bf16 or f32");
@@ -628,10 +638,52 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         }
         return hip_status(ascq::launch_gemm_i8(g, st), "gemm_i8 (int4 operands)");
     }
+    case K_HIF8: {
+        // hifloat8 A / B (matmul_fp8.asc:229): both decoded exactly to bf16 K-contiguous rows in the workspace (every
+        // HiF8 value is a bf16 value), then the bf16-MFMA form of the fp8 GEMM with the same fp32 accumulators and
+        // QF322*_PRE epilogues
+        const int32_t ct = h->ty.c_type;
+        if ((ct == ASCQ_DT_INT8 || ct == ASCQ_DT_UINT8 || ct == ASCQ_DT_INT4 || is_f8(ct) || ct == ASCQ_DT_HIF8) &&
+            !h->quant_set)
+            return fail(ASCQ_E_STATE,
+                        "iterate_all: int8/uint8/int4/fp8/hifloat8 output needs SetQuantScalar or SetQuantVector");
+        if (ct == ASCQ_DT_INT4 && (h->N % 2 != 0 || n % 2 != 0))
+            return fail(ASCQ_E_INVALID_ARG, "iterate_all: int4 C packs two codes per byte: N must be even");
+        const int64_t kp = hif8_k_pad(h->K);
+        ascq_status s = ensure_workspace(h);
+        if (s != ASCQ_OK) return s;
+        uint16_t* a16 = (uint16_t*)h->ws;
+        uint16_t* b16 = (uint16_t*)((uint8_t*)h->ws + align256((size_t)h->M * (size_t)kp * 2));
+        hipError_t e = ascq::launch_hif8_to_bf16(a16, kp, (const uint8_t*)h->a, h->M, h->K, h->trans_a, st);
+        if (e == hipSuccess) e = ascq::launch_hif8_to_bf16(b16, kp, (const uint8_t*)h->b, h->N, h->K, !h->trans_b, st);
+        if (e != hipSuccess) return hip_status(e, "hifloat8 -> bf16");
+        ascq::GemmF8Args g{};
+        g.A = (const uint8_t*)a16;
+        g.B = (const uint8_t*)b16;
+        g.lda = kp;
+        g.ldb = kp;
+        g.trans_a = 0;
+        g.trans_b = 1;
+        g.bias = (const float*)h->bias;
+        g.C = c;
+        g.M = m;
+        g.N = n;
+        g.K = k == h->K ? kp : k;  // the zero padding adds nothing
+        g.ldc = h->N;
+        g.qvec = h->qvec;
+        g.qscalar = h->qscalar;
+        g.use_quant = h->quant_set ? 1 : 0;
+        g.c_type = ct;
+        g.fmt_a = g.fmt_b = ascq::FMT_BF16;
+        g.atomic = atomic;
+        return hip_status(ascq::launch_gemm_f8(g, st), "gemm_f8 (hifloat8 operands)");
+    }
     case K_F8: {
         const int32_t ct = h->ty.c_type;
-        if ((ct == ASCQ_DT_INT8 || ct == ASCQ_DT_UINT8 || ct == ASCQ_DT_INT4 || is_f8(ct)) && !h->quant_set)
-            return fail(ASCQ_E_STATE, "iterate_all: int8/uint8/int4/fp8 output needs SetQuantScalar or SetQuantVector");
+        if ((ct == ASCQ_DT_INT8 || ct == ASCQ_DT_UINT8 || ct == ASCQ_DT_INT4 || is_f8(ct) || ct == ASCQ_DT_HIF8) &&
+            !h->quant_set)
+            return fail(ASCQ_E_STATE,
+                        "iterate_all: int8/uint8/int4/fp8/hifloat8 output needs SetQuantScalar or SetQuantVector");
         if (ct == ASCQ_DT_INT4 && (h->N % 2 != 0 || n % 2 != 0))
             return fail(ASCQ_E_INVALID_ARG, "iterate_all: int4 C packs two codes per byte: N must be even");
         ascq::GemmF8Args g{};
@@ -784,19 +836,13 @@ ascq_status ascq_matmul_iterate_all_noalloc(ascq_matmul_t h, void* c, uint8_t en
         ascq_status s = scratch_for_current_device(&ptr);
         if (s != ASCQ_OK) return s;
     }
-    // run IterateAll on the scratch in place of the handle's workspace (ensure_workspace then sees enough room and
-    // allocates nothing), and give the handle its own workspace back afterwards
-    void* const ws = h->ws;
-    const size_t ws_bytes = h->ws_bytes;
-    const bool ws_owned = h->ws_owned;
-    h->ws = ptr;
-    h->ws_bytes = need > 0 ? (size_t)ASCQ_NOALLOC_SCRATCH_BYTES : 0;
-    h->ws_owned = false;
-    const ascq_status s = ascq_matmul_iterate_all(h, c, en_atomic, stream);
-    h->ws = ws;
-    h->ws_bytes = ws_bytes;
-    h->ws_owned = ws_owned;
-    return s;
+    // run IterateAll on a copy of the handle whose workspace is the scratch (ensure_workspace then sees enough room
+    // and allocates nothing); the caller's handle is only read, so it never holds the scratch as its workspace
+    ascq_matmul_s tmp = *h;
+    tmp.ws = ptr;
+    tmp.ws_bytes = need > 0 ? (size_t)ASCQ_NOALLOC_SCRATCH_BYTES : 0;
+    tmp.ws_owned = false;
+    return ascq_matmul_iterate_all(&tmp, c, en_atomic, stream);
 }
 
 ascq_status ascq_matmul_end(ascq_matmul_t h)

@@ -167,8 +167,10 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
 }
 
 // operand kinds: int8; MX block-scaled E2M1; fp8 (per-tensor / per-channel dequant in the epilogue); MX
-// block-scaled fp8; MX block-scaled fp6 E2M3 in split planes (the E1M2 / mixed fp4 path)
-enum { OP_I8 = 0, OP_MXFP4 = 1, OP_F8 = 2, OP_MXF8 = 3, OP_MXFP6 = 4 };
+// block-scaled fp8; MX block-scaled fp6 E2M3 in split planes (the E1M2 / mixed fp4 path); bf16 (the hifloat8
+// Matmul, whose operands are decoded exactly to bf16 first: v_mfma_f32_32x32x16_bf16, 16 K = 32 bytes per row per
+// k-step, a lane holding 8 bf16 of row l % 32 at K 8 (l / 32) .. + 7 -- the int8 fragment's bytes)
+enum { OP_I8 = 0, OP_MXFP4 = 1, OP_F8 = 2, OP_MXF8 = 3, OP_MXFP6 = 4, OP_BF16 = 5 };
 
 // f8f6f4 format codes (the MFMA's cbsz / blgp fields)
 enum { F8F6F4_E4M3 = 0, F8F6F4_E5M2 = 1, F8F6F4_E2M3 = 2, F8F6F4_E2M1 = 4 };
@@ -266,6 +268,7 @@ struct GemmCore {
     static_assert(!B_TR || (!B_KCONTIG && OP == OP_I8 && 1024 % BN == 0 && BN >= 32 && BN <= 256 &&
                             (ROWB * BN) % (1024 * NW) == 0 && B_COPIES >= 1), "B_TR copies");
     static_assert(!IS_MX || B_KCONTIG, "MX B must be K-contiguous");
+    static_assert(OP != OP_BF16 || B_KCONTIG, "bf16 B must be K-contiguous");
     static_assert(!IS_MX || (BM % 64 == 0 && BN % 64 == 0), "scale row groups");
     static_assert(!IS_MX || SCB % 4 == 0 || SCB == 2, "MX stage scale bytes per row");
     static_assert(!IS_FP6 || (ROWB == 64 && BM % 32 == 0 && BN % 32 == 0), "fp6 Q blocks: 4 MX blocks per stage");
@@ -592,6 +595,13 @@ struct GemmCore {
                                 const v4i b4 = (v4i){fb[0], fb[1], fb[2], fb[3]};
                                 if constexpr (CT) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b4, a4, acc[i][j], 0, 0, 0);
                                 else acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, b4, acc[i][j], 0, 0, 0);
+                            } else if constexpr (OP == OP_BF16) {
+                                typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
+                                const v4i a4 = (v4i){fa[i][0], fa[i][1], fa[i][2], fa[i][3]};
+                                const v4i b4 = (v4i){fb[0], fb[1], fb[2], fb[3]};
+                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf_t, a4),
+                                                                                    __builtin_bit_cast(v8bf_t, b4),
+                                                                                    acc[i][j], 0, 0, 0);
                             } else if constexpr (OP == OP_F8) {
                                 acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb, acc[i][j], CBSZ,
                                                                                              BLGP, 0, 0, 0, 0);

@@ -19,8 +19,15 @@
 // results differ from an fp32-accumulated sum by up to ~2^-13 of the group maxima.  gfx950's fp8 formats are
 // the OCP ones: e4m3 with no infinities and S.1111.111 as NaN (fp8_e4m3fn_t) and IEEE-like e5m2 (fp8_e5m2_t).
 // Tiles, stages and the [K, N] B register transpose are those of the int8 GEMM (fp8 operands are bytes like
-// int8).  hifloat8 (the reference's third format) has no gfx950 hardware encoding and is not accepted by the
-// host API.
+// int8).
+// hifloat8 operands (the sample's default scenario, MatmulFp8Kernel<hifloat8_t, hifloat8_t, float, float>,
+// matmul_fp8.asc:229; A and B both hifloat8, README_en.md) have no gfx950 MFMA format, but every HiF8 value (a
+// significand of at most 4 bits, 2^-22 .. 2^15, +-inf, NaN) is a bf16 value -- a normal one, where f16 would need
+// subnormals below 2^-14 -- so the host layer decodes both operands to bf16 K-contiguous rows in the workspace and
+// this kernel runs them through v_mfma_f32_32x32x16_bf16 (fmt code FMT_BF16, GemmCore OP_BF16) with the same fp32
+// accumulators and epilogue.  C may be hifloat8 for either operand kind
+// ((V)QF322HIF8_PRE, quant_processor_fixpipe.h:106-107: ties away from zero, saturating at +-32768, NaN -> 0 -- the
+// saturation-mode row of matrix_compute_move_out_interface_boundary_value_summary.md:68-70).
 #include "common.h"
 #include "gemm_core.h"
 #include "launch.h"
@@ -29,6 +36,11 @@ namespace ascq {
 
 // fp8 bits -> fp32 (common.h), the format picked by its f8f6f4 code
 __device__ __forceinline__ float fp8_to_f32(uint8_t v, int fmt) { return fp8_bits_to_f32(v, fmt != F8F6F4_E4M3); }
+// element idx of an operand: fp8 bytes, or bf16 for FMT_BF16
+__device__ __forceinline__ float op_elem(const uint8_t* p, int64_t idx, int fmt)
+{
+    return fmt == FMT_BF16 ? bf16_to_f32(((const uint16_t*)p)[idx]) : fp8_to_f32(p[idx], fmt);
+}
 
 // w: the column's QUANT_PRE word (offset and sign flag of QF322B8); atomic: IterateAll's enAtomic (f32 / f16 /
 // bf16 C only, checked by the host layer)
@@ -42,28 +54,36 @@ __device__ __forceinline__ void store_f8_out(void* C, int c_type, int64_t o, flo
     else if (c_type == DT_F16) ((uint16_t*)C)[o] = f32_to_f16_sat(v);
     else if (c_type == DT_BF16) ((uint16_t*)C)[o] = f32_to_bf16_sat(v);
     else if (c_type == DT_INT8 || c_type == DT_UINT8) ((uint8_t*)C)[o] = requant8(v, w);
+    else if (c_type == DT_HIF8) ((uint8_t*)C)[o] = (uint8_t)hif8_code_rna_sat(v);
     else ((uint8_t*)C)[o] = f32_to_fp8(v, c_type == DT_FP8_E5M2 ? 1 : 0);
 }
+
+// FMT: f8f6f4 codes of A (bits 0-2) and B (bits 3-5), or FMT_BF16 in both for bf16 operands
+template <int FMT>
+constexpr int op_of_fmt = (FMT == (FMT_BF16 | (FMT_BF16 << 3))) ? OP_BF16 : OP_F8;
 
 template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_F8, RB, FMT>;
+    constexpr int OP = op_of_fmt<FMT>;
+    constexpr int ES = OP == OP_BF16 ? 2 : 1;  // bytes per operand element
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP, RB, FMT>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_f8[];
     const int tiles_m = (int)((p.M + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
     int tm, tn;
     tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     CoreArgs c{};
-    c.a = make_rsrc(p.A, (uint32_t)(p.lda * (p.M - 1) + p.K));
-    c.b = TB ? make_rsrc(p.B, (uint32_t)(p.ldb * (p.N - 1) + p.K)) : make_rsrc(p.B, (uint32_t)(p.ldb * (p.K - 1) + p.N));
-    c.lda = (uint32_t)p.lda;
-    c.ldb = (uint32_t)p.ldb;
+    c.a = make_rsrc(p.A, (uint32_t)((p.lda * (p.M - 1) + p.K) * ES));
+    c.b = TB ? make_rsrc(p.B, (uint32_t)((p.ldb * (p.N - 1) + p.K) * ES))
+             : make_rsrc(p.B, (uint32_t)(p.ldb * (p.K - 1) + p.N));
+    c.lda = (uint32_t)(p.lda * ES);
+    c.ldb = (uint32_t)(TB ? p.ldb * ES : p.ldb);
     c.rows = (int32_t)(p.M - m0 < BM ? p.M - m0 : BM);
     c.cols = (int32_t)(p.N - n0 < BN ? p.N - n0 : BN);
-    c.a0 = (uint32_t)(m0 * p.lda);
-    c.b0 = (uint32_t)(TB ? n0 * p.ldb : n0);
-    c.kbytes = p.K;
+    c.a0 = (uint32_t)(m0 * p.lda * ES);
+    c.b0 = (uint32_t)(TB ? n0 * p.ldb * ES : n0);
+    c.kbytes = p.K * ES;
     typename T::acc_t acc[T::FM][T::FN];
     T::run(c, smem_f8, acc);
 
@@ -143,6 +163,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
     else if (p.c_type == DT_BF16) store([](float v, uint64_t) { return f32_to_bf16_sat(v); }, put16);
     else if (p.c_type == DT_INT8 || p.c_type == DT_UINT8) store([](float v, uint64_t w) { return requant8(v, w); }, put8);
     else if (p.c_type == DT_FP8_E5M2) store([](float v, uint64_t) { return f32_to_fp8(v, 1); }, put8);
+    else if (p.c_type == DT_HIF8) store([](float v, uint64_t) { return (uint8_t)hif8_code_rna_sat(v); }, put8);
     else store([](float v, uint64_t) { return f32_to_fp8(v, 0); }, put8);
 }
 
@@ -154,9 +175,9 @@ __global__ __launch_bounds__(256) void gemm_f8_generic_kernel(GemmF8Args p)
     auto value = [&](int64_t m, int64_t n, uint64_t w) {
         float acc = 0.0f;
         for (int64_t k = 0; k < p.K; ++k) {
-            const float a = fp8_to_f32(p.trans_a ? p.A[k * p.lda + m] : p.A[m * p.lda + k], p.fmt_a);
-            const float b = fp8_to_f32(p.trans_b ? p.B[n * p.ldb + k] : p.B[k * p.ldb + n], p.fmt_b);
-            acc = acc + a * b;  // the product of two fp8 values is exact in fp32
+            const float a = op_elem(p.A, p.trans_a ? k * p.lda + m : m * p.lda + k, p.fmt_a);
+            const float b = op_elem(p.B, p.trans_b ? n * p.ldb + k : k * p.ldb + n, p.fmt_b);
+            acc = acc + a * b;  // the product of two fp8 (or two decoded hifloat8) values is exact in fp32
         }
         if (p.bias) acc = acc + p.bias[n];
         if (p.use_quant) acc = acc * (p.qvec ? quant_pre_m1(w) : mscalar);
@@ -186,7 +207,7 @@ __global__ __launch_bounds__(256) void gemm_f8_generic_kernel(GemmF8Args p)
 template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT>
 static hipError_t launch_f8_tiled(const GemmF8Args& a, hipStream_t st)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_F8, RB, FMT>;
+    using T = GemmCore<BM, BN, WM, WN, ST, TB, op_of_fmt<FMT>, RB, FMT>;
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
     const hipError_t e = ensure_dynamic_lds<gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT>>((int)T::LDS_BYTES);
     if (e != hipSuccess) return e;
@@ -197,25 +218,33 @@ static hipError_t launch_f8_tiled(const GemmF8Args& a, hipStream_t st)
 template <int FMT>
 static hipError_t launch_f8_fmt(const GemmF8Args& a, hipStream_t st)
 {
+    constexpr int ES = op_of_fmt<FMT> == OP_BF16 ? 2 : 1;
     const bool big = a.M >= 1024 && a.N >= 1024;
     if (a.trans_b) {
-        if (big) return a.K % 128 == 0 ? launch_f8_tiled<256, 256, 4, 2, 2, true, 128, FMT>(a, st)
-                                       : launch_f8_tiled<256, 256, 4, 2, 4, true, 64, FMT>(a, st);
+        if (big) return (a.K * ES) % 128 == 0 ? launch_f8_tiled<256, 256, 4, 2, 2, true, 128, FMT>(a, st)
+                                              : launch_f8_tiled<256, 256, 4, 2, 4, true, 64, FMT>(a, st);
         return launch_f8_tiled<64, 64, 2, 2, 4, true, 64, FMT>(a, st);
     }
-    // a large [K, N] B is transposed by the host layer first; this in-loop transpose serves the rest
-    return launch_f8_tiled<64, 128, 2, 2, 4, false, 64, FMT>(a, st);
+    // a large [K, N] B is transposed by the host layer first; this in-loop transpose serves the rest (fp8 only: the
+    // bf16 operands of a hifloat8 Matmul are always K-contiguous)
+    if constexpr (ES == 1) return launch_f8_tiled<64, 128, 2, 2, 4, false, 64, FMT>(a, st);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemm_f8(const GemmF8Args& a, hipStream_t st)
 {
-    if ((a.fmt_a != F8F6F4_E4M3 && a.fmt_a != F8F6F4_E5M2) || (a.fmt_b != F8F6F4_E4M3 && a.fmt_b != F8F6F4_E5M2))
+    const bool bf = a.fmt_a == FMT_BF16 && a.fmt_b == FMT_BF16;
+    if (!bf &&
+        ((a.fmt_a != F8F6F4_E4M3 && a.fmt_a != F8F6F4_E5M2) || (a.fmt_b != F8F6F4_E4M3 && a.fmt_b != F8F6F4_E5M2)))
         return hipErrorInvalidValue;
-    const bool a_ok = !a.trans_a && a.lda % 16 == 0 && ((uintptr_t)a.A % 16 == 0) && a.lda * a.M < (1ll << 31);
-    const bool b_ok = a.trans_b ? (a.ldb % 16 == 0 && ((uintptr_t)a.B % 16 == 0) && a.ldb * a.N < (1ll << 31))
+    if (bf && (a.trans_a || !a.trans_b)) return hipErrorInvalidValue;
+    const int64_t es = bf ? 2 : 1;
+    const bool a_ok = !a.trans_a && (a.lda * es) % 16 == 0 && ((uintptr_t)a.A % 16 == 0) && a.lda * es * a.M < (1ll << 31);
+    const bool b_ok = a.trans_b ? ((a.ldb * es) % 16 == 0 && ((uintptr_t)a.B % 16 == 0) && a.ldb * es * a.N < (1ll << 31))
                                 : (a.ldb % 4 == 0 && a.N % 4 == 0 && ((uintptr_t)a.B % 4 == 0) && a.ldb * a.K < (1ll << 31));
     // the tiled epilogue addresses a 256-row output tile with 32-bit offsets
-    if (a_ok && b_ok && a.K % 16 == 0 && a.ldc < (1ll << 21)) {
+    if (a_ok && b_ok && (a.K * es) % 16 == 0 && a.ldc < (1ll << 21)) {
+        if (bf) return launch_f8_fmt<FMT_BF16 | (FMT_BF16 << 3)>(a, st);
         switch (a.fmt_a | (a.fmt_b << 3)) {
         case F8F6F4_E4M3 | (F8F6F4_E4M3 << 3): return launch_f8_fmt<F8F6F4_E4M3 | (F8F6F4_E4M3 << 3)>(a, st);
         case F8F6F4_E5M2 | (F8F6F4_E5M2 << 3): return launch_f8_fmt<F8F6F4_E5M2 | (F8F6F4_E5M2 << 3)>(a, st);

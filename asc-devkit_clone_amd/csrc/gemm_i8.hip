@@ -253,7 +253,8 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void group_gemm_i8_kernel(GroupG
         typename T::acc_t acc[T::FM][T::FN];
         T::run(c, smem, acc);
 
-        // epilogue (quant_group_matmul_custom.asc:424-452): AscendDequant acc*scale[g,n] in fp32, Mul by the
+        // epilogue (quant_group_matmul_custom.asc:424-452): AscendDequant acc*scale[g,n] in fp32 (its int32 -> fp32
+        // conversion rounds ties away from zero above 2^24, as every AscendDequant here does), Mul by the
         // per-token scale in fp32, optional FasterGelu in fp32, one rounding cast to the output type.  Stores go
         // through a buffer resource over the output tile: rows past the group's end are out of its range.
         const TileOut out = tile_out(p.Y, m0, n0, p.N, c.rows, c.cols, 2);
@@ -277,7 +278,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void group_gemm_i8_kernel(GroupG
                         uint32_t h[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            float v = (float)acc[i][j][4 * q + e] * sc[e];
+                            float v = i32_to_f32_rna(acc[i][j][4 * q + e]) * sc[e];
                             v = v * pt;
                             h[e] = cvt(p.act ? faster_gelu(v) : v);
                         }
@@ -406,7 +407,7 @@ __global__ __launch_bounds__(256) void group_gemm_generic_kernel(GroupGemmArgs p
         uint32_t acc = 0;
         for (int64_t k = 0; k < p.K; ++k)
             acc += (uint32_t)((int32_t)p.X[m * p.K + k] * (int32_t)(p.w_trans ? Wg[n * p.K + k] : Wg[k * p.N + n]));
-        float v = (float)(int32_t)acc * p.scale[(int64_t)g * p.N + n];
+        float v = i32_to_f32_rna((int32_t)acc) * p.scale[(int64_t)g * p.N + n];
         v = v * p.pts[m];
         if (p.act) v = faster_gelu(v);
         if (p.out_type == DT_F16) ((uint16_t*)p.Y)[m * p.N + n] = f32_to_f16_sat(v);

@@ -96,6 +96,7 @@ struct GemmI8Args {
 hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st);
 
 // gemm_f8.hip
+constexpr int FMT_BF16 = 7;  // operand format code outside the f8f6f4 codes: bf16 elements (OP_BF16)
 struct GemmF8Args {
     const uint8_t* A;     // fp8 [M, K] row-major (lda), or [K, M] when trans_a
     const uint8_t* B;     // fp8 [K, N] row-major (ldb), or [N, K] when trans_b
@@ -105,8 +106,11 @@ struct GemmF8Args {
     const uint64_t* qvec; // per-channel QUANT_PRE words [N] or null
     uint64_t qscalar;
     int use_quant;        // 1: multiply by M1 (SetQuantScalar / SetQuantVector was called)
-    int c_type;           // DT_F16 / DT_BF16 / DT_F32; DT_INT8 / DT_UINT8 (QF322B8); DT_FP8_E4M3 / _E5M2 (QF322FP8)
-    int fmt_a, fmt_b;     // f8f6f4 codes: 0 e4m3fn, 1 e5m2
+    int c_type;           // DT_F16 / DT_BF16 / DT_F32; DT_INT8 / DT_UINT8 (QF322B8); DT_FP8_E4M3 / _E5M2 (QF322FP8);
+                          // DT_HIF8 (QF322HIF8); DT_INT4 (QF322S4)
+    int fmt_a, fmt_b;     // f8f6f4 codes: 0 e4m3fn, 1 e5m2; FMT_BF16 in both: A / B are bf16 (a hifloat8 Matmul's
+                          // operands decoded by the host layer; A [M, K] and B [N, K], K-contiguous, lda / ldb in
+                          // elements)
     int trans_a, trans_b;
     int atomic;           // C_STORE, or C_ADD / C_MAX / C_MIN (f32 / f16 / bf16 C): IterateAll's enAtomic
 };
@@ -172,6 +176,10 @@ hipError_t launch_nz_to_nd(void* dst, const void* src, int esize, int64_t batch,
                            int transpose_out, hipStream_t st);
 hipError_t launch_nd_to_nz(void* dst, const void* src, int esize, int64_t batch, int64_t rows, int64_t cols,
                            hipStream_t st);
+// hifloat8 -> bf16 (exact): dst [R, ldd] bf16 (ldd % 8 == 0, columns C .. ldd - 1 zero, dst 16-byte aligned) from
+// src [R, C], or from src [C, R] with transpose
+hipError_t launch_hif8_to_bf16(uint16_t* dst, int64_t ldd, const uint8_t* src, int64_t R, int64_t C, int transpose,
+                              hipStream_t st);
 // int4 (two per byte, even element in the low nibble) -> int8, elementwise over `bytes` input bytes
 hipError_t launch_unpack_int4(int8_t* dst, const uint8_t* src, int64_t bytes, hipStream_t st);
 // transpose a [K, N] packed fp4 matrix (two per byte along N) into [N, K] (two per byte along K)

@@ -1,5 +1,5 @@
 // transpose.hip -- byte and nibble transposes that turn a row-major [K, N] B operand into the K-contiguous
-// [N, K] layout the GEMM main loop copies straight into LDS.
+// [N, K] layout the GEMM main loop copies straight into LDS (and the hifloat8 -> bf16 operand decode).
 //
 // One 256-thread workgroup per 128 (k) x 128 (byte column) tile:
 //  * load: 16-byte chunks, eight lanes per 128-byte row segment, into LDS [k][128 bytes]; the dword column
@@ -177,6 +177,76 @@ __global__ __launch_bounds__(256) void unpack_int4_kernel(int8_t* __restrict__ d
         dst[2 * i] = (int8_t)(s & 0xFFu);
         dst[2 * i + 1] = (int8_t)((s >> 8) & 0xFFu);
     }
+}
+
+// hifloat8 -> bf16 operand rows for the hifloat8 Matmul: dst [R, ldd] bf16 (ldd a multiple of 8, columns C .. ldd - 1
+// written as zero) from src [R, C] (TRANS false) or [C, R] (TRANS true: the [K, M] A of isTransA or the [K, N] B).
+// Every HiF8 code is a bf16 value (the finite ones have at most 4 significant bits within 2^-22 .. 2^15, all bf16
+// normals; 0x80 is NaN, 0x6F / 0xEF are +-inf): the upper half of hif8_to_f32's bits, looked up in a 256-entry table
+// built per workgroup.  TRANS false: a thread writes 8 values (one 16-byte store) of one row; TRANS true: a workgroup
+// stages a 64 (c) x 64 (r) byte tile in LDS (loads coalesced along r) and writes 64 rows x 64 values (stores
+// coalesced along c).
+template <bool TRANS>
+__global__ __launch_bounds__(256) void hif8_to_bf16_kernel(uint16_t* __restrict__ dst, int64_t ldd,
+                                                          const uint8_t* __restrict__ src, int64_t R, int64_t C)
+{
+    __shared__ uint16_t lut[256];
+    __shared__ uint8_t tile[64][68];
+    const int t = threadIdx.x;
+    lut[t] = (uint16_t)(__float_as_uint(hif8_to_f32((uint32_t)t)) >> 16);
+    __syncthreads();
+    if constexpr (!TRANS) {
+        const int64_t chunks = ldd / 8, total = R * chunks;
+        for (int64_t e = (int64_t)blockIdx.x * 256 + t; e < total; e += (int64_t)gridDim.x * 256) {
+            const int64_t r = e / chunks, c0 = (e % chunks) * 8;
+            uint32_t h[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) h[j] = c0 + j < C ? lut[src[r * C + c0 + j]] : 0u;
+            *(u32x4*)(dst + r * ldd + c0) = (u32x4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                                                    h[6] | (h[7] << 16)};
+        }
+    } else {
+        const int64_t tiles_c = (ldd + 63) / 64;
+        const int64_t r0 = (int64_t)(blockIdx.x / tiles_c) * 64, c0 = (int64_t)(blockIdx.x % tiles_c) * 64;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int e = t + 256 * i, cc = e >> 6, rr = e & 63;
+            const int64_t c = c0 + cc, r = r0 + rr;
+            tile[cc][rr] = (c < C && r < R) ? src[c * R + r] : (uint8_t)0;
+        }
+        __syncthreads();
+        const int rr = t >> 2, q = t & 3;
+        const int64_t r = r0 + rr;
+        if (r < R) {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int cb = 16 * q + 8 * hh;
+                if (c0 + cb >= ldd) break;
+                uint32_t h[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) h[j] = lut[tile[cb + j][rr]];
+                *(u32x4*)(dst + r * ldd + c0 + cb) = (u32x4){h[0] | (h[1] << 16), h[2] | (h[3] << 16),
+                                                             h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+            }
+        }
+    }
+}
+
+hipError_t launch_hif8_to_bf16(uint16_t* dst, int64_t ldd, const uint8_t* src, int64_t R, int64_t C, int transpose,
+                              hipStream_t st)
+{
+    if (R <= 0 || C <= 0) return hipSuccess;
+    if (ldd % 8 != 0 || ldd < C || (uintptr_t)dst % 16 != 0) return hipErrorInvalidValue;
+    if (transpose) {
+        const int64_t tiles = ((R + 63) / 64) * ((ldd + 63) / 64);
+        if (tiles > 0x7FFFFFFF) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(hif8_to_bf16_kernel<true>, dim3((unsigned)tiles), dim3(256), 0, st, dst, ldd, src, R, C);
+    } else {
+        int64_t blocks = (R * (ldd / 8) + 255) / 256;
+        if (blocks > 65536) blocks = 65536;
+        hipLaunchKernelGGL(hif8_to_bf16_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, dst, ldd, src, R, C);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_unpack_int4(int8_t* dst, const uint8_t* src, int64_t bytes, hipStream_t st)

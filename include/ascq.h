@@ -139,6 +139,14 @@ uint64_t ascq_pack_quant_pre(float m1, int32_t offset9, int32_t sign_flag);
  *  fp8, fp8, int4 + SetQuantScalar/Vector -> QF322S4_PRE (as REQ4 on the fp32 accumulator)
  *  fp8, fp8, int8|uint8 + SetQuantScalar/Vector -> QF322B8_PRE (as REQ8 on the fp32 accumulator)
  *  fp8, fp8, fp8_e4m3|fp8_e5m2 + SetQuantScalar/Vector -> QF322FP8_PRE (rne; e4m3 saturates at +-448, NaN -> 0)
+ *  fp8, fp8, hifloat8 + SetQuantScalar/Vector -> QF322HIF8_PRE (ties away from zero, saturating at +-32768,
+ *                               NaN -> 0: the saturation-mode row of
+ *                               matrix_compute_move_out_interface_boundary_value_summary.md:68-70)
+ *  hifloat8, hifloat8 (both; matmul_fp8/README_en.md), any C of the fp8 rows above or hifloat8, f32 bias
+ *                               (matmul_fp8.asc:229, the sample's default MatmulFp8Kernel<hifloat8_t, hifloat8_t,
+ *                               float, float>; mode table quant_processor_utils.h:36-41): both operands are decoded
+ *                               exactly to bf16 in the workspace (every HiF8 value is a bf16 value) and multiplied
+ *                               with fp32 accumulation, then the fp8 rows' epilogues
  *  fp4_e2m1|fp4_e1m2 (any mix), bf16|f32, f32 bias, with E8M0 scales (SetTensorScaleA/B) -> MX block-scaled
  *                               (K % 128 == 0; fp4x2_e1m2_t operands, the high-performance MX sample
  *                               matmul_mxfp4_high_performance/matmul_mx.h:117-133, run as exact fp6 E2M3 after a
@@ -206,7 +214,7 @@ ascq_status ascq_matmul_set_antiquant_vector(ascq_matmul_t h, const void* offset
  * scaleA: [M, sK] (transpose: [sK/2, M, 2]); scaleB: [sK/2, N, 2] (transpose: [N, sK]); sK = ceil(K/64)*2. */
 ascq_status ascq_matmul_set_tensor_scale_a(ascq_matmul_t h, const uint8_t* scale_a, int32_t is_transpose_scale_a);
 ascq_status ascq_matmul_set_tensor_scale_b(ascq_matmul_t h, const uint8_t* scale_b, int32_t is_transpose_scale_b);
-/* Optional device workspace for handles that need one (int8 / fp8 with isTransA or a large [K,N] B; MX;
+/* Optional device workspace for handles that need one (int8 / fp8 with isTransA or a large [K,N] B; MX; hifloat8;
  * W4/W8 with ND B):
  * ascq_matmul_workspace_size() bytes.  Without it IterateAll allocates on first use. */
 ascq_status ascq_matmul_workspace_size(ascq_matmul_t h, size_t* bytes);

@@ -455,6 +455,14 @@ void oq_mm_requant(const int32_t* acc, uint8_t* out, int64_t M, int64_t N, const
         }
 }
 
+/* an operand element of the fp8 / hifloat8 Matmul: fp8 e4m3fn / e5m2, or hifloat8 (the sample's default scenario,
+ * matmul_fp8.asc:229) */
+static inline double mm8_decode(uint8_t v, int fmt)
+{
+    if (fmt == OQ_HIF8) return OQ_MUTANT == 39 ? (double)oq_fp8_decode(v, OQ_FP8_E4M3) : (double)oq_hif8_decode(v);
+    return (double)oq_fp8_decode(v, fmt);
+}
+
 /* fp8 operands: L0C is fp32 (matmul_utils.h:134-175); a float bias seeds L0C before the k loop (MmadCompute
  * with isBias, mmad_compute.h:40-90; the fp8 sample adds a float [1, N] bias, matmul_fp8/scripts/gen_data.py
  * tf_matmul + bias); the epilogue is (V)QF322{F16,BF16,F32}_PRE (quant_processor_fixpipe.h:101-115):
@@ -465,7 +473,11 @@ void oq_mm_requant(const int32_t* acc, uint8_t* out, int64_t M, int64_t N, const
  * K groups of the group's largest |a b| (blockmax_out; either output may be NULL).
  * use_q: 1 when SetQuantScalar / SetQuantVector was called.
  * out_type OQ_INT8 / OQ_UINT8: (V)QF322B8_PRE, oq_requant8((acc + bias) * M1, word); OQ_FP8_E4M3 / _E5M2:
- * (V)QF322FP8_PRE (quant_processor_fixpipe.h:101-103, 219-221), oq_f32_to_fp8((acc + bias) * M1). */
+ * (V)QF322FP8_PRE (quant_processor_fixpipe.h:101-103, 219-221), oq_f32_to_fp8((acc + bias) * M1); OQ_HIF8:
+ * (V)QF322HIF8_PRE (quant_processor_fixpipe.h:106-107, 223-224), ties away with the saturation-mode rules
+ * (matrix_compute_move_out_interface_boundary_value_summary.md:68-70, 88-90: +-inf and every |v| >= 32768 ->
+ * +-32768, NaN -> 0), oq_hif8_encode((acc + bias) * M1, sat).
+ * a_fmt / b_fmt OQ_HIF8 (both, the hifloat8 Matmul): elements decoded by oq_hif8_decode. */
 void oq_matmul_fp8(const uint8_t* A, const uint8_t* B, int a_fmt, int b_fmt, const float* bias, void* out,
                    int out_type, int64_t M, int64_t N, int64_t K, int transA, int transB, int use_q,
                    const uint64_t* qvec, uint64_t qscalar, double* exact_out, double* absdot_out,
@@ -477,12 +489,12 @@ void oq_matmul_fp8(const uint8_t* A, const uint8_t* B, int a_fmt, int b_fmt, con
     if (!bd) return;
 #pragma omp parallel for schedule(static)
     for (int64_t n = 0; n < N; ++n)
-        for (int64_t k = 0; k < K; ++k) bd[n * K + k] = oq_fp8_decode(transB ? B[n * K + k] : B[k * N + n], b_fmt);
+        for (int64_t k = 0; k < K; ++k) bd[n * K + k] = mm8_decode(transB ? B[n * K + k] : B[k * N + n], b_fmt);
 #pragma omp parallel for schedule(static)
     for (int64_t m = 0; m < M; ++m) {
         double* arow = (double*)malloc((size_t)K * sizeof(double));
         if (!arow) continue;
-        for (int64_t k = 0; k < K; ++k) arow[k] = oq_fp8_decode(transA ? A[k * M + m] : A[m * K + k], a_fmt);
+        for (int64_t k = 0; k < K; ++k) arow[k] = mm8_decode(transA ? A[k * M + m] : A[m * K + k], a_fmt);
         for (int64_t n = 0; n < N; ++n) {
             const double* bn = bd + n * K;
             double s = 0.0, sa = 0.0, sb = 0.0, bmx = 0.0;
@@ -506,6 +518,8 @@ void oq_matmul_fp8(const uint8_t* A, const uint8_t* B, int a_fmt, int b_fmt, con
                 ((uint8_t*)out)[m * N + n] = oq_requant8(v, qvec ? qvec[n] : qscalar);
             else if (out_type == OQ_FP8_E4M3 || out_type == OQ_FP8_E5M2)
                 ((uint8_t*)out)[m * N + n] = oq_f32_to_fp8(v, out_type);
+            else if (out_type == OQ_HIF8) /* QF322HIF8_PRE, saturation mode */
+                ((uint8_t*)out)[m * N + n] = oq_hif8_encode(v, 1);
             else
                 store_from_f32(out, out_type, m * N + n, v);
         }
@@ -1085,7 +1099,8 @@ float oq_faster_gelu(float x)
 
 /* examples/01_simd_cpp_api/05_best_practices/03_fusion_compute/quant_group_matmul_high_performance/
  * quant_group_matmul_custom.asc: group rows [s_g, s_g+cnt_g) (Process :255-288), int32 accumulate on the
- * cube (MMCompute :296-334), then AscendDequant(acc x scale[g,n]) to fp32 (:433), Mul by perTokenScale[m]
+ * cube (MMCompute :296-334), then AscendDequant(acc x scale[g,n]) to fp32 (:433; its int32 -> fp32 conversion
+ * rounds ties away from zero, as the dequant kernels do: oq_i32_to_f32_rna), Mul by perTokenScale[m]
  * (:439), act != 0: the sample's FasterGelu (:445, oq_faster_gelu in fp32 ops), and the final Cast (:450;
  * CAST_NONE = rint).
  * list_type 0: group_list holds G+1 int64 prefix offsets (offsets[0] = first row); 1: G int64 counts
@@ -1108,7 +1123,9 @@ void oq_group_matmul(void* y, int out_type, const int8_t* x, const float* pts, c
                 int64_t acc = 0;
                 for (int64_t k = 0; k < K; ++k)
                     acc += (int64_t)x[m * K + k] * (int64_t)(w_trans ? wg[n * K + k] : wg[k * N + n]);
-                float v = (float)(int32_t)(uint32_t)(uint64_t)acc * (OQ_MUTANT == 5 ? pts[m] : scale[g * N + n]);
+                const int32_t a32 = (int32_t)(uint32_t)(uint64_t)acc;
+                const float f = OQ_MUTANT == 38 ? (float)a32 : oq_i32_to_f32_rna(a32);
+                float v = f * (OQ_MUTANT == 5 ? pts[m] : scale[g * N + n]);
                 v = v * (OQ_MUTANT == 5 ? scale[g * N + n] : pts[m]);
                 if (act) v = oq_faster_gelu(v);
                 store_from_f32(y, out_type, m * N + n, v);

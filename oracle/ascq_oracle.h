@@ -84,7 +84,7 @@ void oq_mm_requant4(const int32_t* acc, uint8_t* out, int64_t M, int64_t N, cons
 void oq_requant4_f32(const float* v, uint8_t* out, int64_t M, int64_t N, const uint64_t* qvec, uint64_t qscalar);
 /* (V)REQ8: int32 -> int8 / uint8 with the word's M1, offset and sign flag */
 void oq_mm_requant(const int32_t* acc, uint8_t* out, int64_t M, int64_t N, const uint64_t* qvec, uint64_t qscalar);
-/* fp8 x fp8 -> fp32 accumulate (exact products, double sum) -> (V)QF322{F16,BF16,F32}_PRE */
+/* fp8 x fp8 (or hifloat8 x hifloat8) -> fp32 accumulate (exact products, double sum) -> the QF322*_PRE epilogues */
 void oq_matmul_fp8(const uint8_t* A, const uint8_t* B, int a_fmt, int b_fmt, const float* bias, void* out,
                    int out_type, int64_t M, int64_t N, int64_t K, int transA, int transB, int use_q,
                    const uint64_t* qvec, uint64_t qscalar, double* exact_out, double* absdot_out,

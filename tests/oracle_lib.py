@@ -135,15 +135,15 @@ def matmul_i8(A, B, bias=None, trans_a=False, trans_b=False):
 
 def matmul_fp8(A, B, a_fmt, b_fmt, bias=None, out_type=F32, trans_a=False, trans_b=False, use_q=False, qvec=None,
                qscalar=0):
-    """fp8 Matmul (bytes in, fp8 codes FP8_E4M3 / FP8_E5M2): returns (out, exact fp64 sum + bias, sum |a b|,
-    sum over 16-element K groups of the group's largest |a b|)."""
+    """fp8 / hifloat8 Matmul (bytes in, codes FP8_E4M3 / FP8_E5M2, or HIF8 for both): returns (out, exact fp64
+    sum + bias, sum |a b|, sum over 16-element K groups of the group's largest |a b|)."""
     A = np.ascontiguousarray(A, np.uint8)
     B = np.ascontiguousarray(B, np.uint8)
     M = A.shape[1] if trans_a else A.shape[0]
     K = A.shape[0] if trans_a else A.shape[1]
     N = B.shape[0] if trans_b else B.shape[1]
-    odt = {F32: np.float32, INT8: np.int8, UINT8: np.uint8, FP8_E4M3: np.uint8, FP8_E5M2: np.uint8}.get(out_type,
-                                                                                                    np.uint16)
+    odt = {F32: np.float32, INT8: np.int8, UINT8: np.uint8, FP8_E4M3: np.uint8, FP8_E5M2: np.uint8,
+           HIF8: np.uint8}.get(out_type, np.uint16)
     out = np.empty((M, N), odt)
     exact = np.empty((M, N), np.float64)
     absd = np.empty((M, N), np.float64)

@@ -267,6 +267,39 @@ def test_int4_operand_handle():
     _err(L.ascq_matmul_create(ctypes.byref(t), ctypes.byref(h)), ascq.E_UNSUPPORTED)
 
 
+def test_hif8_operand_handle():
+    """hifloat8 A and B (matmul_fp8.asc:229; both the same type, matmul_fp8/README_en.md): accepted with every C of
+    the fp8 Matmul plus hifloat8 C; the workspace holds both operands decoded to bf16 rows of K rounded up to 8;
+    hifloat8 mixed with fp8 is refused; a hifloat8 C needs a quant word before IterateAll"""
+    L = ascq.lib()
+    h = ctypes.c_void_p()
+    d = ctypes.c_void_p(0x1000)
+    for ct in (ascq.F32, ascq.F16, ascq.BF16, ascq.INT8, ascq.UINT8, ascq.INT4, ascq.FP8_E4M3, ascq.FP8_E5M2,
+               ascq.HIF8):
+        t = ascq._MatmulTypes(ascq.HIF8, ascq.HIF8, ct, ascq.F32, 0, 0)
+        _err(L.ascq_matmul_create(ctypes.byref(t), ctypes.byref(h)), ascq.OK)
+        _err(L.ascq_matmul_destroy(h), ascq.OK)
+    for fa, fb in ((ascq.HIF8, ascq.FP8_E4M3), (ascq.FP8_E5M2, ascq.HIF8)):
+        t = ascq._MatmulTypes(fa, fb, ascq.F32, 0, 0, 0)
+        _err(L.ascq_matmul_create(ctypes.byref(t), ctypes.byref(h)), ascq.E_UNSUPPORTED)
+    t = ascq._MatmulTypes(ascq.HIF8, ascq.HIF8, ascq.F32, ascq.INT32, 0, 0)
+    _err(L.ascq_matmul_create(ctypes.byref(t), ctypes.byref(h)), ascq.E_UNSUPPORTED)  # bias must be f32
+    t = ascq._MatmulTypes(ascq.FP8_E4M3, ascq.FP8_E4M3, ascq.HIF8, 0, 0, 0)
+    _err(L.ascq_matmul_create(ctypes.byref(t), ctypes.byref(h)), ascq.OK)               # QF322HIF8_PRE on fp8
+    _err(L.ascq_matmul_destroy(h), ascq.OK)
+    t = ascq._MatmulTypes(ascq.HIF8, ascq.HIF8, ascq.HIF8, 0, 0, 0)
+    _err(L.ascq_matmul_create(ctypes.byref(t), ctypes.byref(h)), ascq.OK)
+    _err(L.ascq_matmul_set_org_shape(h, 428, 479, 158), ascq.OK)
+    _err(L.ascq_matmul_set_tensor_a(h, d, 0), ascq.OK)
+    _err(L.ascq_matmul_set_tensor_b(h, d, 0), ascq.OK)
+    ws = ctypes.c_size_t()
+    _err(L.ascq_matmul_workspace_size(h, ctypes.byref(ws)), ascq.OK)
+    rup = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    assert ws.value == rup(428 * 160 * 2) + rup(479 * 160 * 2)
+    _err(L.ascq_matmul_iterate_all(h, d, 0, None), ascq.E_STATE)  # hifloat8 C without a quant word
+    _err(L.ascq_matmul_destroy(h), ascq.OK)
+
+
 def test_no_device_reports_zero_or_more():
     assert ascq.lib().ascq_device_count() >= 0
 

@@ -5,6 +5,7 @@ import numpy as np
 import pytest
 import torch
 
+import group_cases as GC
 import oracle_lib as O
 from conftest import seeded
 
@@ -52,7 +53,7 @@ def test_config4_moe_full_size(ascq_gpu, oracle, w_trans):
     """16 experts, 4096 tokens routed by a seeded multinomial (Zipf s=1.1), K=4096, N=1408, int64 prefix-sum
     offsets, bf16 out; the expert weights given [G, K, N] or K-contiguous [G, N, K].  Reference: exact int
     accumulators from fp64 BLAS (|acc| < 2^53), then the epilogue f32(f32(acc)*scale[g,n])*pts[m] in numpy float32
-    and torch's rne bfloat16 cast."""
+    (f32(acc) ties away from zero) and torch's rne bfloat16 cast."""
     rng = seeded(4)
     G, T, K, N = 16, 4096, 4096, 1408
     counts = zipf_counts(rng, T, G)
@@ -69,9 +70,29 @@ def test_config4_moe_full_size(ascq_gpu, oracle, w_trans):
         s, e = offsets[g], offsets[g + 1]
         if e == s:
             continue
-        acc = (xf[s:e] @ w[g].astype(np.float64)).astype(np.float32)  # exact int -> f32 rne
+        acc = GC.i32_to_f32_rna((xf[s:e] @ w[g].astype(np.float64)).astype(np.int64))  # ties away above 2^24
         v = (acc * scale[g][None, :]).astype(np.float32) * pts[s:e, None]
         np.testing.assert_array_equal(got[s:e], bf16_bits_of_f32(v.astype(np.float32)), err_msg=f"group {g}")
+
+
+@pytest.mark.parametrize("w_trans", [False, True])
+@pytest.mark.parametrize("list_type", [0, 1])
+def test_group_ties_above_2_24(ascq_gpu, oracle, w_trans, list_type):
+    """Accumulators on fp32 ties in [2^24, 2^26) with scales chosen so that the int32 -> fp32 rounding rule shows in
+    the bf16 output: the group epilogue rounds ties away from zero, as AscendDequant does
+    (ascend_dequant_3510_impl.h:61); bit-exact against the oracle and the numpy restatement, and more than 50 outputs
+    differ from what a nearest-even conversion gives."""
+    x, w, pts, sc, counts = GC.tie_case(11)
+    M, K = x.shape
+    G, _, N = w.shape
+    gl = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64) if list_type == 0 else counts
+    w_dev = _dev(np.ascontiguousarray(w.transpose(0, 2, 1))) if w_trans else _dev(w)
+    y = ascq_gpu.quant_group_matmul(_dev(x), _dev(pts), w_dev, _dev(sc), _dev(gl), list_type, w_trans)
+    got = y.cpu().view(torch.int16).numpy().view(np.uint16)
+    ref = O.group_matmul(x, pts, w, sc, gl, list_type, G, M, K, N, O.BF16)
+    np.testing.assert_array_equal(got, ref)
+    np.testing.assert_array_equal(got, GC.group_reference(x, w, pts, sc, counts))
+    assert GC.rne_differs(x, w, pts, sc, counts) > 50
 
 
 def _f16_ulp(v):

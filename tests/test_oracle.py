@@ -539,6 +539,20 @@ def test_group_matmul_f32_epilogue_order():
         assert not np.array_equal(other, exp)  # the two orders differ on these inputs
 
 
+def test_group_matmul_ties_above_2_24_round_away():
+    """Accumulators on fp32 ties in [2^24, 2^26): the group epilogue's AscendDequant converts int32 -> fp32 with ties
+    away from zero (ascend_dequant_3510_impl.h:61), checked against the numpy restatement of group_cases.py; the
+    nearest-even conversion changes more than 50 of these bf16 outputs."""
+    import group_cases as GC
+
+    x, w, pts, sc, counts = GC.tie_case(7)
+    M, K = x.shape
+    G, _, N = w.shape
+    y = O.group_matmul(x, pts, w, sc, counts, 1, G, M, K, N, O.BF16)
+    assert np.array_equal(y, GC.group_reference(x, w, pts, sc, counts))
+    assert GC.rne_differs(x, w, pts, sc, counts) > 50
+
+
 def test_mx_matmul_vs_numpy_decode():
     M, N, K = 8, 12, 128
     A = rng0.integers(0, 256, (M, K // 2), dtype=np.uint8)
@@ -1296,6 +1310,81 @@ def test_hif8_encode_random_f32():
     t = O.hif8_table()
     x = (rng0.standard_normal(4000) * np.exp2(rng0.uniform(-26, 17, 4000))).astype(np.float32)
     np.testing.assert_array_equal(O.hif8_encode(x), _hif8_nearest(x, t))
+
+
+def hif8_codes(rng, shape, lo=None, hi=None):
+    """random finite HiFloat8 codes (no NaN 0x80, no +-inf 0x6F / 0xEF); with lo / hi, the codes of the integers
+    lo .. hi (the sample's data class: uniform(0, 5) cast to integers, then encoded)"""
+    if lo is not None:
+        ints = rng.integers(lo, hi + 1, shape).astype(np.float32)
+        return O.hif8_encode(ints.reshape(-1)).reshape(shape)
+    c = rng.integers(0, 256, shape, dtype=np.int64).astype(np.uint8)
+    bad = (c == 0x80) | ((c & 0x7F) == 0x6F)
+    return np.where(bad, np.uint8(0x08), c).astype(np.uint8)
+
+
+def test_hif8_matmul_vs_numpy_decode():
+    """hifloat8 x hifloat8 Matmul (matmul_fp8.asc:229): the oracle's exact sums against a numpy fp64 matmul of the
+    HiFloat8 table's values (the table pinned above), with f32 bias, both transposes, and f32 / f16 / bf16 outputs
+    as the casts of (sum + bias) * M1"""
+    t = O.hif8_table().astype(np.float64)
+    M, N, K = 24, 40, 96
+    A = hif8_codes(rng0, (M, K))
+    B = hif8_codes(rng0, (K, N))
+    bias = rng0.standard_normal(N).astype(np.float32)
+    exact_np = t[A] @ t[B] + bias.astype(np.float64)[None, :]
+    for ta, tb in [(False, False), (True, True)]:
+        Ain = np.ascontiguousarray(A.T) if ta else A
+        Bin = np.ascontiguousarray(B.T) if tb else B
+        out, exact, absd, bmax = O.matmul_fp8(Ain, Bin, O.HIF8, O.HIF8, bias=bias, out_type=O.F32, trans_a=ta,
+                                              trans_b=tb)
+        assert np.allclose(exact, exact_np, rtol=1e-12, atol=0)
+        assert np.allclose(absd, np.abs(t[A]) @ np.abs(t[B]), rtol=1e-12, atol=0)
+        assert np.array_equal(out, exact.astype(np.float32))
+    m1 = np.float32(2.0 ** -9)
+    word = int(m1.view(np.uint32))
+    for ot, cast in [(O.F16, np.float16), (O.BF16, None)]:
+        out, exact, _, _ = O.matmul_fp8(A, B, O.HIF8, O.HIF8, bias=bias, out_type=ot, use_q=True, qscalar=word)
+        v = (exact.astype(np.float32) * m1).astype(np.float32)
+        if cast is not None:
+            exp = np.clip(v, -65504, 65504).astype(np.float16).view(np.uint16)
+        else:
+            exp = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(out, exp)
+
+
+def test_hif8_matmul_sample_golden():
+    """the sample's own data class and check (matmul_fp8/scripts/gen_data.py gen_golden_data_hif8: A [428, 158] and
+    B [158, 479] from uniform(0, 5) cast to uint8, encoded to hifloat8, f32 bias uniform(-1, 1), golden = fp32
+    matmul + bias; verify_result.py: rtol = atol = 1e-3, error ratio <= 1e-3): the sums are integers below 2^24, so
+    the oracle matches the fp32 golden exactly"""
+    rng = np.random.default_rng(229)
+    M, N, K = 428, 479, 158
+    a_int = rng.uniform(0, 5, (M, K)).astype(np.uint8)
+    b_int = rng.uniform(0, 5, (K, N)).astype(np.uint8)
+    bias = rng.uniform(-1, 1, N).astype(np.float32)
+    A = O.hif8_encode(a_int.astype(np.float32).reshape(-1)).reshape(M, K)
+    B = O.hif8_encode(b_int.astype(np.float32).reshape(-1)).reshape(K, N)
+    golden = ((a_int.astype(np.float32) @ b_int.astype(np.float32)) + bias[None, :]).astype(np.float32)
+    out, _, _, _ = O.matmul_fp8(A, B, O.HIF8, O.HIF8, bias=bias, out_type=O.F32)
+    assert ref_verify(out, golden)
+    assert np.array_equal(out, golden)
+
+
+def test_hif8_matmul_hif8_output():
+    """(V)QF322HIF8_PRE: (sum + bias) * M1 encoded with ties away and saturation (the encoder pinned above); the
+    per-channel words reach the right columns, and sums past 32768 saturate"""
+    M, N, K = 16, 24, 64
+    A = hif8_codes(rng0, (M, K), -4, 4)
+    B = hif8_codes(rng0, (K, N), -4, 4)
+    t = O.hif8_table().astype(np.float64)
+    m1 = np.exp2(rng0.integers(-4, 9, N)).astype(np.float32) * np.float32(1.375)
+    words = m1.view(np.uint32).astype(np.uint64)
+    out, exact, _, _ = O.matmul_fp8(A, B, O.HIF8, O.HIF8, out_type=O.HIF8, use_q=True, qvec=words)
+    assert np.array_equal(exact, t[A] @ t[B])
+    v = (exact.astype(np.float32) * m1[None, :]).astype(np.float32)
+    assert np.array_equal(out, O.hif8_encode(v.reshape(-1)).reshape(M, N))
+    assert (np.abs(v) >= 32768).any() and ((out & 0x7F) == 0x6E).any()
 
 
 # --------------------------------------------------------------------------- legacy AscendQuant, arch-3510 form

@@ -60,6 +60,8 @@ MUTANTS = {
     35: "MX E1M2 elements decoded as E2M1",
     36: "MX bias dropped",
     37: "enAtomic max / min swapped",
+    38: "group epilogue int32 -> fp32 rounded to nearest even instead of ties away",
+    39: "hifloat8 Matmul operands decoded as fp8 e4m3",
 }
 
 
