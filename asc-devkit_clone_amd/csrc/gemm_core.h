@@ -639,45 +639,54 @@ struct GemmCore {
 __device__ __forceinline__ uint32_t acc_bits(float x) { return __float_as_uint(x); }
 __device__ __forceinline__ uint32_t acc_bits(int x) { return (uint32_t)x; }
 
-// enAtomic epilogue of a GemmCore tile (T): the raw accumulators are parked in LDS -- free once every wave has
-// left the main loop -- and a rolled loop then takes one element per thread per step, applies the output
-// conversion conv(tile column, accumulator bits) -> C bits, and combines it into C (c_atomic).  Rolling the loop
-// keeps the conversion, the compare-and-swap code and their registers out of the unrolled store path.  A tile
-// that does not fit the LDS at once goes in NCH chunks of whole wave rows: in chunk ch the waves whose rows lie
-// in it write all their fragments.
-template <class T, int DT, class F>
-__device__ __forceinline__ void atomic_epilogue(uint8_t* smem, const typename T::acc_t (&acc)[T::FM][T::FN],
-                                                const TileOut& out, int rows, int cols, int op, F conv)
+// Rolled epilogue of a GemmCore tile (T): the raw accumulators are parked in LDS -- free once every wave has left
+// the main loop -- and a rolled loop then takes one element per thread per step and hands put(tile row, tile
+// column, accumulator bits) the element.  Rolling the loop keeps the per-element code (a compare-and-swap, a software
+// encoder) and its registers out of an unrolled store path.  A tile that does not fit the LDS at once goes in NCH
+// chunks of rows: in chunk ch every wave writes the 32-row fragments that lie in it.
+template <class T, class F>
+__device__ __forceinline__ void rolled_epilogue(uint8_t* smem, const typename T::acc_t (&acc)[T::FM][T::FN], int rows,
+                                                int cols, F put)
 {
-    constexpr int ES = (DT == DT_INT32 || DT == DT_F32) ? 4 : 2;  // bytes per C element
     constexpr int NCH = (size_t)T::TBM * T::TBN * 4 <= T::LDS_BYTES ? 1 : (size_t)T::TBM * T::TBN * 2 <= T::LDS_BYTES ? 2 : 4;
     constexpr int CHR = T::TBM / NCH;  // rows per chunk
-    static_assert((size_t)CHR * T::TBN * 4 <= T::LDS_BYTES && CHR % T::WTM == 0 && (T::TBN & (T::TBN - 1)) == 0,
-                  "atomic epilogue chunks");
+    static_assert((size_t)CHR * T::TBN * 4 <= T::LDS_BYTES && CHR % 32 == 0 && (T::TBN & (T::TBN - 1)) == 0,
+                  "rolled epilogue chunks");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / T::TWN, wn = wave % T::TWN;
-    const int my_chunk = wm * T::WTM / CHR;
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) {
         __syncthreads();  // the main loop's last LDS reads (or the previous chunk's) are done
-        if (my_chunk == ch) {
 #pragma unroll
-            for (int i = 0; i < T::FM; ++i)
+        for (int i = 0; i < T::FM; ++i) {
+            if ((wm * T::WTM + i * 32) / CHR != ch) continue;  // 32-row fragment i lies in chunk ch or not at all
 #pragma unroll
-                for (int j = 0; j < T::FN; ++j)
+            for (int j = 0; j < T::FN; ++j)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        *(uint32_t*)(smem + ((T::frag_row(wm, i, r, lane) - ch * CHR) * T::TBN + T::frag_col(wn, j, lane)) * 4) =
-                            acc_bits(acc[i][j][r]);
+                for (int r = 0; r < 16; ++r)
+                    *(uint32_t*)(smem + ((T::frag_row(wm, i, r, lane) - ch * CHR) * T::TBN + T::frag_col(wn, j, lane)) * 4) =
+                        acc_bits(acc[i][j][r]);
         }
         __syncthreads();
 #pragma unroll 1
         for (int e = threadIdx.x; e < CHR * T::TBN; e += T::NT) {
             const int rr = ch * CHR + e / T::TBN, cc = e % T::TBN;
             if (rr >= rows || cc >= cols) continue;
-            c_atomic<DT>(out.base + (uint32_t)rr * out.pitch + (uint32_t)(cc * ES), conv(cc, *(const uint32_t*)(smem + e * 4)), op);
+            put(rr, cc, *(const uint32_t*)(smem + e * 4));
         }
     }
+}
+
+// enAtomic epilogue of a GemmCore tile (T): the rolled epilogue with the output conversion conv(tile column,
+// accumulator bits) -> C bits combined into C by c_atomic.
+template <class T, int DT, class F>
+__device__ __forceinline__ void atomic_epilogue(uint8_t* smem, const typename T::acc_t (&acc)[T::FM][T::FN],
+                                                const TileOut& out, int rows, int cols, int op, F conv)
+{
+    constexpr int ES = (DT == DT_INT32 || DT == DT_F32) ? 4 : 2;  // bytes per C element
+    rolled_epilogue<T>(smem, acc, rows, cols, [&](int rr, int cc, uint32_t a) {
+        c_atomic<DT>(out.base + (uint32_t)rr * out.pitch + (uint32_t)(cc * ES), conv(cc, a), op);
+    });
 }
 
 }  // namespace ascq

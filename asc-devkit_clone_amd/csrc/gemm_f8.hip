@@ -42,6 +42,14 @@ __device__ __forceinline__ float op_elem(const uint8_t* p, int64_t idx, int fmt)
     return fmt == FMT_BF16 ? bf16_to_f32(((const uint16_t*)p)[idx]) : fp8_to_f32(p[idx], fmt);
 }
 
+// a 1-byte C element: (V)QF322B8_PRE for int8 / uint8, (V)QF322FP8_PRE, (V)QF322HIF8_PRE
+__device__ __forceinline__ uint8_t byte_out(float v, uint64_t w, int c_type)
+{
+    if (c_type == DT_INT8 || c_type == DT_UINT8) return requant8(v, w);
+    if (c_type == DT_HIF8) return (uint8_t)hif8_code_rna_sat(v);
+    return f32_to_fp8(v, c_type == DT_FP8_E5M2 ? 1 : 0);
+}
+
 // w: the column's QUANT_PRE word (offset and sign flag of QF322B8); atomic: IterateAll's enAtomic (f32 / f16 /
 // bf16 C only, checked by the host layer)
 __device__ __forceinline__ void store_f8_out(void* C, int c_type, int64_t o, float v, uint64_t w, int atomic)
@@ -53,9 +61,7 @@ __device__ __forceinline__ void store_f8_out(void* C, int c_type, int64_t o, flo
     } else if (c_type == DT_F32) ((float*)C)[o] = v;
     else if (c_type == DT_F16) ((uint16_t*)C)[o] = f32_to_f16_sat(v);
     else if (c_type == DT_BF16) ((uint16_t*)C)[o] = f32_to_bf16_sat(v);
-    else if (c_type == DT_INT8 || c_type == DT_UINT8) ((uint8_t*)C)[o] = requant8(v, w);
-    else if (c_type == DT_HIF8) ((uint8_t*)C)[o] = (uint8_t)hif8_code_rna_sat(v);
-    else ((uint8_t*)C)[o] = f32_to_fp8(v, c_type == DT_FP8_E5M2 ? 1 : 0);
+    else ((uint8_t*)C)[o] = byte_out(v, w, c_type);
 }
 
 // FMT: f8f6f4 codes of A (bits 0-2) and B (bits 3-5), or FMT_BF16 in both for bf16 operands
@@ -161,10 +167,20 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
     if (p.c_type == DT_F32) store([](float v, uint64_t) { return __float_as_uint(v); }, put32);
     else if (p.c_type == DT_F16) store([](float v, uint64_t) { return f32_to_f16_sat(v); }, put16);
     else if (p.c_type == DT_BF16) store([](float v, uint64_t) { return f32_to_bf16_sat(v); }, put16);
-    else if (p.c_type == DT_INT8 || p.c_type == DT_UINT8) store([](float v, uint64_t w) { return requant8(v, w); }, put8);
-    else if (p.c_type == DT_FP8_E5M2) store([](float v, uint64_t) { return f32_to_fp8(v, 1); }, put8);
-    else if (p.c_type == DT_HIF8) store([](float v, uint64_t) { return (uint8_t)hif8_code_rna_sat(v); }, put8);
-    else store([](float v, uint64_t) { return f32_to_fp8(v, 0); }, put8);
+    else {
+        // the 1-byte C types -- int8 / uint8 (QF322B8), fp8 (QF322FP8), hifloat8 (QF322HIF8) -- in the rolled
+        // epilogue: one more unrolled store loop (the hifloat8 encoder alone is ~30 instructions per element) grew
+        // the kernel until the compiler kept the accumulators in scratch memory in the main loop
+        rolled_epilogue<T>(smem_f8, acc, c.rows, c.cols, [&](int rr, int cc, uint32_t a) {
+            float v = __uint_as_float(a);
+            const int64_t col = n0 + cc;
+            if (p.bias) v = v + p.bias[col];
+            const uint64_t w = p.qvec ? p.qvec[col] : p.qscalar;
+            if (p.use_quant) v = v * (p.qvec ? quant_pre_m1(w) : mscalar);
+            __builtin_amdgcn_raw_buffer_store_b8(byte_out(v, w, p.c_type), out.r, (uint32_t)rr * out.pitch + (uint32_t)cc,
+                                                 0, 0);
+        });
+    }
 }
 
 // Any shape / layout / alignment: one thread per output element, fp32 accumulation in k order.

@@ -6,6 +6,7 @@ import ctypes
 import os
 import re
 import subprocess
+import tempfile
 from pathlib import Path
 
 import pytest
@@ -379,6 +380,45 @@ def test_no_fma_with_zero_addend_in_half_arithmetic(tmp_path):
     assert r.returncode == 0, r.stderr[-2000:]
     bad = [ln for ln in out.read_text().splitlines() if re.search(r"v_fma_mix(lo|hi)?_f16 .*, 0( |$)", ln)]
     assert not bad, bad[:5]
+
+
+def _kernel_private_segments():
+    """{kernel name: private (scratch) bytes per lane} of every kernel in the built libascq.so: the .hip_fatbin section
+    holds one offload bundle per translation unit; each bundle's gfx950 code object carries the kernel metadata"""
+    llvm = Path("/opt/rocm/llvm/bin")
+    so = ROOT / "asc-devkit_clone_amd" / "libascq.so"
+    out = {}
+    with tempfile.TemporaryDirectory() as d:
+        fb = Path(d) / "fatbin"
+        subprocess.run([str(llvm / "llvm-objcopy"), f"--dump-section=.hip_fatbin={fb}", str(so), str(Path(d) / "x")],
+                       check=True, capture_output=True)
+        data = fb.read_bytes()
+        starts = [m.start() for m in re.finditer(re.escape(b"__CLANG_OFFLOAD_BUNDLE__"), data)]
+        for n, (a, b) in enumerate(zip(starts, starts[1:] + [len(data)])):
+            piece, co = Path(d) / f"b{n}", Path(d) / f"c{n}.o"
+            piece.write_bytes(data[a:b])
+            subprocess.run([str(llvm / "clang-offload-bundler"), "--unbundle", "--type=o", f"--input={piece}",
+                            "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--output={co}"], check=True,
+                           capture_output=True)
+            notes = subprocess.run([str(llvm / "llvm-readelf"), "--notes", str(co)], check=True, capture_output=True,
+                                   text=True).stdout
+            names = re.findall(r"\.name:\s+(\S+)", notes)
+            sizes = re.findall(r"\.private_segment_fixed_size:\s+(\d+)", notes)
+            assert len(names) == len(sizes)
+            out.update(zip(names, map(int, sizes)))
+    return out
+
+
+def test_matmul_kernels_use_no_scratch():
+    """The GEMM, group-matmul, MX and antiquant-GEMV kernels keep their accumulators and operands in registers: a
+    kernel that needs private (scratch) memory has had its accumulator array or argument block demoted to memory by
+    the compiler, which costs several times the kernel's time (an fp8 GEMM with an extra unrolled epilogue ran 13x
+    slower that way).  Reads the kernel metadata of the built library's code objects (CPU only)."""
+    seg = _kernel_private_segments()
+    hot = {k: v for k, v in seg.items() if re.search(r"gemm|aq_|antiquant_gemm", k)}
+    assert len(hot) > 50
+    bad = {k: v for k, v in hot.items() if v}
+    assert not bad, bad
 
 
 def test_env_gated_host_log():
