@@ -378,9 +378,12 @@ struct GemmCore {
         return *(const u32x2*)(qbase + (row >> 5) * 1024 + ((2 * s + kh) * 32 + (row & 31)) * 8);
     }
 
-    __device__ __forceinline__ static void run(const CoreArgs& p, uint8_t* smem, acc_t (&acc)[FM][FN])
+    // t: the thread's index within the NT threads that run this tile (threadIdx.x, or its lane when each wave of a
+    // workgroup runs a one-wave GemmCore on its own k range)
+    __device__ __forceinline__ static void run(const CoreArgs& p, uint8_t* smem, acc_t (&acc)[FM][FN],
+                                               int t = (int)threadIdx.x)
     {
-        const int t = threadIdx.x, lane = t & 63;
+        const int lane = t & 63;
         const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: copy bases stay scalar
         const int wm = wave / WN, wn = wave % WN;
         typedef uint32_t breg_t[B_BLK > 0 ? B_BLK : 1][8];

@@ -24,15 +24,22 @@ __device__ __forceinline__ int64_t uniform64(int64_t v)
     return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, bool BTR = false>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
+// KW > 1 (one-wave tiles, WM = WN = 1; store epilogues only): the workgroup's KW waves each run the tile's main loop on
+// their own K / KW range (K a multiple of KW * RB, so every wave runs the same stages and meets the same barriers) in
+// their own LDS ring, then sum their int32 accumulators through LDS (exact in any order) and wave 0 runs the epilogue.
+// For small problems (the W8A8 sample, 32 tiles) this cuts the serial K loop of each tile KW-fold.
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, bool BTR = false, int KW = 1>
+__global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_i8_kernel(GemmI8Args p)
 {
     using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB, 0, true, false, BTR>;
+    static_assert(KW == 1 || (WM == 1 && WN == 1), "k-split waves run one-wave tiles");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tiles_m = (int)((p.M + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
     int tm, tn;
     tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int kw = KW > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
+    const int64_t kc = p.K / KW, k0 = kw * kc;  // this wave's K range (KW > 1: K % (KW RB) == 0)
     CoreArgs c{};
     c.a = make_rsrc(p.A, (uint32_t)(p.lda * (p.M - 1) + p.K));
     c.b = TB ? make_rsrc(p.B, (uint32_t)(p.ldb * (p.N - 1) + p.K)) : make_rsrc(p.B, (uint32_t)(p.ldb * (p.K - 1) + p.N));
@@ -40,11 +47,21 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
     c.ldb = (uint32_t)p.ldb;
     c.rows = (int32_t)(p.M - m0 < BM ? p.M - m0 : BM);
     c.cols = (int32_t)(p.N - n0 < BN ? p.N - n0 : BN);
-    c.a0 = (uint32_t)(m0 * p.lda);
-    c.b0 = (uint32_t)(TB ? n0 * p.ldb : n0);
-    c.kbytes = p.K;
+    c.a0 = (uint32_t)(m0 * p.lda + k0);
+    c.b0 = (uint32_t)(TB ? n0 * p.ldb + k0 : n0 + k0 * p.ldb);
+    c.kbytes = kc;
     typename T::acc_t acc[T::FM][T::FN];
-    T::run(c, smem, acc);
+    T::run(c, smem + (KW > 1 ? kw * T::LDS_BYTES : 0), acc, KW > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x);
+    if constexpr (KW > 1) {
+        __syncthreads();  // every wave's main loop is done with its LDS ring
+        v16i* red = (v16i*)smem;  // [KW - 1][64 lanes] accumulator fragments
+        const int lane = threadIdx.x & 63;
+        if (kw > 0) red[(kw - 1) * 64 + lane] = acc[0][0];
+        __syncthreads();
+        if (kw != 0) return;
+#pragma unroll
+        for (int w = 0; w < KW - 1; ++w) acc[0][0] += red[w * 64 + lane];
+    }
 
     // epilogue: per 32x32 accumulator tile, lane holds column lane%32 and 16 rows (GemmCore::frag_row); stores go
     // through a buffer resource over the output tile (rows past M dropped by its range, 32-bit offsets)
@@ -93,7 +110,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(GemmI8Args p)
                 }
         }
     };
-    if (p.atomic != C_STORE) {  // enAtomic: int32 / f16 / bf16 C (the host layer refuses the others)
+    if (KW == 1 && p.atomic != C_STORE) {  // enAtomic: int32 / f16 / bf16 C (the host layer refuses the others)
         // acc + bias (int32, wrapping), then x M1 of the column for f16 / bf16 -- the store path's arithmetic
         auto v = [&](int cl, uint32_t a) { return (int32_t)(a + (uint32_t)(p.bias ? p.bias[n0 + cl] : 0)); };
         auto m1 = [&](int cl) { return p.qvec ? quant_pre_m1(p.qvec[n0 + cl]) : mscalar; };
@@ -346,14 +363,15 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(GemmI8Args p)
     }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, bool BTR = false>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, bool BTR = false, int KW = 1>
 static hipError_t launch_tiled(const GemmI8Args& a, hipStream_t st)
 {
     using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB, 0, true, false, BTR>;
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
-    const hipError_t e = ensure_dynamic_lds<gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, BTR>>((int)T::LDS_BYTES);
+    constexpr size_t lds = T::LDS_BYTES * KW;
+    const hipError_t e = ensure_dynamic_lds<gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, BTR, KW>>((int)lds);
     if (e != hipSuccess) return e;
-    launch_k((gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, BTR>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
+    launch_k((gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, BTR, KW>), dim3(tiles), dim3(T::NT * KW), (uint32_t)lds, st, a);
     return hipGetLastError();
 }
 
@@ -368,6 +386,12 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
         // small problems (the W8A8 sample, 128 x 256 x 512: 4 tiles of 64 x 128) take 32 x 32 single-wave tiles so
         // that at least 32 workgroups share the work
         const bool tiny = ((a.M + 63) / 64) * ((a.N + 127) / 128) < 32;
+        // ... and, when K holds four 64-byte stages per wave and C is stored (not combined by enAtomic), each tile's K
+        // split over four waves of one workgroup, so a tile's loads are all in flight at once
+        const bool ksplit = tiny && a.K % 256 == 0 && a.atomic == C_STORE;
+        if (ksplit && a.trans_b) return launch_tiled<32, 32, 1, 1, 4, true, 64, false, 4>(a, st);
+        if (ksplit && a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0)
+            return launch_tiled<32, 32, 1, 1, 4, false, 64, true, 4>(a, st);
         if (a.trans_b)
             return big ? (a.K % 128 == 0 ? launch_tiled<256, 256, 4, 2, 2, true, 128>(a, st)
                                          : launch_tiled<256, 256, 4, 2, 4, true>(a, st))
