@@ -20,8 +20,8 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libascq.so"
-SOURCES = ["api.cpp", "quant.hip", "gemm_i8.hip", "gemm_f8.hip", "gemv_antiquant.hip", "mx_gemm.hip", "transpose.hip",
-           "layout.hip"]
+SOURCES = ["api.cpp", "quant.hip", "gemm_i8.hip", "gemm_f8.hip", "gemv_antiquant.hip", "aq_gemm.hip", "mx_gemm.hip",
+           "transpose.hip", "layout.hip"]
 ARCH = os.environ.get("ASCQ_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

@@ -27,6 +27,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "aq_frag.h"
 #include "common.h"
 #include "launch.h"
 
@@ -94,61 +95,6 @@ hipError_t launch_weight_pack(void* packed, const void* w, int w_type, int64_t K
     hipLaunchKernelGGL(weight_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (uint8_t*)packed,
                        (const uint8_t*)w, w_type, K, N, is_transpose);
     return hipGetLastError();
-}
-
-// 0x64006400 (two binary16 1024.0) held in a VGPR: with both masks as literals the compiler cannot fuse the
-// and / or of the int4 unpacking into one v_and_or_b32 (a VOP3 instruction takes no literal operand here)
-__device__ __forceinline__ uint32_t half_magic_vgpr()
-{
-    uint32_t m;
-    asm("v_mov_b32 %0, 0x64006400" : "=v"(m));
-    return m;
-}
-
-// dequantise one 8-element B fragment: codes -> half(half(q + off) * scale)
-template <bool INT4, bool HAS_OFF>
-__device__ __forceinline__ h8 dequant8(uint32_t w0, uint32_t w1, h2 off, h2 sc, uint32_t magic)
-{
-    uint32_t d[4];
-    h2 qv[4];
-    if constexpr (INT4) {
-        // w0 holds all 8 nibbles of the step.  Pairs 0 / 2 (bits 0-3 / 8-11 of each half) OR under the exponent of
-        // 1024 as 1024 + c; pairs 1 / 3 (bits 4-7 / 12-15) are masked in place, giving 1024 + 16 c, and
-        // 1024 + 16 c -> c - 8 is one exact fma (x / 16 - 72), so no shift by 4 or 12 is needed
-        const uint32_t w8 = w0 >> 8;
-        d[0] = (w0 & 0x000F000Fu) | magic;
-        d[1] = (w0 & 0x00F000F0u) | magic;
-        d[2] = (w8 & 0x000F000Fu) | magic;
-        d[3] = (w8 & 0x00F000F0u) | magic;
-        const h2 bias = (h2){(_Float16)1032.0f, (_Float16)1032.0f};
-        const h2 sixteenth = (h2){(_Float16)0.0625f, (_Float16)0.0625f}, b16 = (h2){(_Float16)-72.0f, (_Float16)-72.0f};
-        qv[0] = __builtin_bit_cast(h2, d[0]) - bias;                                       // exact
-        qv[1] = __builtin_elementwise_fma(__builtin_bit_cast(h2, d[1]), sixteenth, b16);  // exact
-        qv[2] = __builtin_bit_cast(h2, d[2]) - bias;
-        qv[3] = __builtin_elementwise_fma(__builtin_bit_cast(h2, d[3]), sixteenth, b16);
-    } else {
-        // bytes b0..b3 of w0 and w1 -> halves 0x64bb (selector 5 = byte 1 of magic = 0x64)
-        d[0] = __builtin_amdgcn_perm(magic, w0, 0x05010500u);
-        d[1] = __builtin_amdgcn_perm(magic, w0, 0x05030502u);
-        d[2] = __builtin_amdgcn_perm(magic, w1, 0x05010500u);
-        d[3] = __builtin_amdgcn_perm(magic, w1, 0x05030502u);
-        const h2 bias = (h2){(_Float16)1152.0f, (_Float16)1152.0f};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qv[i] = __builtin_bit_cast(h2, d[i]) - bias;  // exact
-    }
-    h2 r[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        h2 q = qv[i];
-        if constexpr (HAS_OFF) q = q + off;  // one rounding
-        r[i] = q * sc;                       // one rounding
-    }
-    h8 out;
-    out.s01 = r[0];
-    out.s23 = r[1];
-    out.s45 = r[2];
-    out.s67 = r[3];
-    return out;
 }
 
 // s_waitcnt vmcnt(N) with the other counters left alone (vmcnt[3:0] | expcnt << 4 | lgkmcnt << 8 | vmcnt[5:4] << 14)
@@ -1395,6 +1341,13 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
     const bool int4 = w_type == DT_INT4;
     const int64_t NBT = N / 16, KB = K / KT;
     const bool cols_ok = g % KT == 0 && ((g / KT) & (g / KT - 1)) == 0;  // column-block kernels: group 128 << s
+    // above 64 rows: the LDS-staged GEMM of aq_gemm.hip (each weight tile dequantised once per 256 rows) where it takes
+    // the shape, else 64-row passes of the kernels below
+    if (M > 64 && cols_ok) {
+        const hipError_t e = launch_aq_gemm(y, x, wp, w_type, scale, offset, group, M, N, K, atomic, st);
+        if (e != hipErrorInvalidValue) return e;
+        (void)hipGetLastError();
+    }
     for (int64_t m0 = 0; m0 < M; m0 += 64) {
         const int64_t mc = (M - m0) < 64 ? (M - m0) : 64;
         const uint16_t* xc = x + m0 * K;

@@ -140,6 +140,13 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
                                    const uint16_t* offset, int64_t group, int64_t M, int64_t N, int64_t K,
                                    int atomic, hipStream_t st);
 
+// aq_gemm.hip: the weight-only antiquant matmul for M > 64 (an LDS-staged f16 GEMM whose weight tiles are dequantised
+// once per 256 rows); hipErrorInvalidValue for shapes it does not take (K % 128, N % 16, group not 128 << s, buffers
+// of 2^31 bytes)
+hipError_t launch_aq_gemm(uint16_t* y, const uint16_t* x, const void* wp, int w_type, const uint16_t* scale,
+                          const uint16_t* offset, int64_t group, int64_t M, int64_t N, int64_t K, int atomic,
+                          hipStream_t st);
+
 // mx_gemm.hip
 struct MxGemmArgs {
     const uint8_t* A;       // [M, K/2] packed E2M1, or [M, K] fp8

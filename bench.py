@@ -64,7 +64,9 @@ def bench_headline(torch, ascq, steps, warmup):
     bytes_quant = 2 * M * N + M * N + 4 * M
     bytes_dequant = M * N + 4 * M + 2 * M * N
     per_set = 2 * M * N + M * N + 4 * M + 2 * M * N
-    R = rotation(per_set)
+    # four sets at least: the kernel-alone loops below touch x and q (quant) or q and y (dequant) of a set, 201 MB,
+    # so four sets keep them above 3 x the 256 MB Infinity Cache
+    R = rotation(per_set, 4)
     g = torch.Generator(device="cuda")
     g.manual_seed(20261201)
     xs, qs, ss, ys = [], [], [], []
@@ -243,18 +245,50 @@ def _roof(bound, achieved, peak, unit):
 # ----------------------------------------------------------------------------------------------
 # other configs (GPU only)
 # ----------------------------------------------------------------------------------------------
-def _time_loop(torch, fn, iters, warmup=3):
+def bench_prefill(torch, ascq, w_type, M, iters):
+    """weight-only antiquant matmul at a prefill batch: x f16 [M, 4096] against the config-3 weight (int4 / int8
+    [4096, 11008], g = 128 f16 scale + offset), fp32 accumulation, f16 out -- the LDS-staged f16 GEMM of aq_gemm.hip"""
+    K, N, grp = 4096, 11008, 128
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    wb = K * N // (2 if w_type == ascq.INT4 else 1)
+    R = rotation(wb + 2 * 2 * (K // grp) * N + 2 * M * K + 2 * M * N)
+    wps, scs, ofs, xs, ys = [], [], [], [], []
+    for _ in range(R):
+        wps.append(torch.randint(0, 256, (wb,), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8))
+        scs.append(torch.exp(torch.empty((K // grp, N), device="cuda").uniform_(np.log(1e-3), np.log(1e-1),
+                                                                                 generator=g)).half())
+        ofs.append(torch.empty((K // grp, N), device="cuda").uniform_(-8, 8, generator=g).half())
+        xs.append(torch.randn((M, K), generator=g, device="cuda").half())
+        ys.append(torch.empty((M, N), dtype=torch.float16, device="cuda"))
+
+    def fn(i):
+        r = i % R
+        ascq.antiquant_matmul(xs[r], wps[r], w_type, scs[r], ofs[r], grp, N, out=ys[r])
+
+    ms = _time_loop(torch, fn, iters)
+    bits = 4 if w_type == ascq.INT4 else 8
+    tf = 2 * M * N * K / (ms * 1e-3) / 1e12
+    return dict(workload=f"W{bits}A16 antiquant matmul (prefill), M={M} K={K} N={N} g={grp}", ms=ms, value=tf,
+                unit="TFLOPS", frac_of_peak=tf / F16_PEAK_TFLOPS)
+
+
+def _time_loop(torch, fn, iters, warmup=3, reps=3):
+    """ms per call: the median over `reps` timed loops of `iters` back-to-back calls (events around each loop)"""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
-    s = torch.cuda.Event(enable_timing=True)
-    e = torch.cuda.Event(enable_timing=True)
-    s.record()
-    for i in range(iters):
-        fn(i)
-    e.record()
-    torch.cuda.synchronize()
-    return s.elapsed_time(e) / iters
+    res = []
+    for _ in range(reps):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for i in range(iters):
+            fn(i)
+        e.record()
+        torch.cuda.synchronize()
+        res.append(s.elapsed_time(e) / iters)
+    return sorted(res)[len(res) // 2]
 
 
 USE_GRAPH = True  # --no-graph: eager timing only (counter passes of rocprofv3)
@@ -334,17 +368,20 @@ def bench_gemv(torch, ascq, w_type, M, iters):
     g = torch.Generator(device="cuda")
     g.manual_seed(3)
     wb = K * N // (2 if w_type == ascq.INT4 else 1)
-    R = rotation(wb)
-    wps = []
+    R = rotation(wb + 2 * 2 * (K // grp) * N)
+    # weights, scales and offsets all rotate, so every call reads each of them from HBM
+    wps, scs, ofs = [], [], []
     for _ in range(R):
         wps.append(torch.randint(0, 256, (wb,), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8))
-    scale = torch.exp(torch.empty((K // grp, N), device="cuda").uniform_(np.log(1e-3), np.log(1e-1), generator=g)).half()
-    offset = torch.empty((K // grp, N), device="cuda").uniform_(-8, 8, generator=g).half()
+        scs.append(torch.exp(torch.empty((K // grp, N), device="cuda").uniform_(np.log(1e-3), np.log(1e-1),
+                                                                                 generator=g)).half())
+        ofs.append(torch.empty((K // grp, N), device="cuda").uniform_(-8, 8, generator=g).half())
     x = torch.randn((M, K), generator=g, device="cuda").half()
     y = torch.empty((M, N), dtype=torch.float16, device="cuda")
 
     def fn(i):
-        ascq.antiquant_matmul(x, wps[i % R], w_type, scale, offset, grp, N, out=y)
+        r = i % R
+        ascq.antiquant_matmul(x, wps[r], w_type, scs[r], ofs[r], grp, N, out=y)
 
     ms, eager = _time_graph(torch, fn, iters, y)
     bits = 4 if w_type == ascq.INT4 else 8
@@ -764,7 +801,8 @@ OTHER = {
               lambda t, a: bench_antiquant_policy(t, a, a.FP4_E1M2, 50)],
     "w8a8": [lambda t, a: bench_w8a8(t, a, 128, 256, 512, 200), lambda t, a: bench_w8a8(t, a, 8192, 8192, 8192, 10)],
     "gemv": [lambda t, a, w=w, m=m: bench_gemv(t, a, getattr(a, w), m, 200)
-             for w in ("INT4", "INT8") for m in (1, 16, 64)],
+             for w in ("INT4", "INT8") for m in (1, 16, 64)]
+            + [lambda t, a, w=w: bench_prefill(t, a, getattr(a, w), 512, 20) for w in ("INT4", "INT8")],
     "group": [lambda t, a: bench_group(t, a, 20, True), lambda t, a: bench_group(t, a, 20, False),
               lambda t, a: bench_group_sample(t, a, 20)],
     "vendor": [lambda t, a: bench_vendor(t, "int8", 10), lambda t, a: bench_vendor(t, "fp8", 10)],

@@ -145,9 +145,9 @@ def test_atomic_mx(ascq_gpu, oracle, c_type, fmts, shape):
     mm.End()
 
 
-@pytest.mark.parametrize("M", [1, 16, 64, 70])
+@pytest.mark.parametrize("M", [1, 16, 64, 70, 300])
 def test_atomic_weight_only(ascq_gpu, oracle, M):
-    """W4A16 through the Matmul handle: decode (M <= 4), the LDS-ring batch forms and a second 64-row chunk"""
+    """W4A16 through the Matmul handle: decode (M <= 4), the LDS-ring batch forms and the prefill GEMM (M > 64)"""
     from test_gpu_gemv import make_weights
 
     rng = seeded(500 + M)

@@ -149,6 +149,47 @@ def test_column_block_kernels(ascq_gpu, oracle, w_type, with_offset, M, K, N, gr
 
 
 @pytest.mark.parametrize("w_type", ["int4", "int8"])
+@pytest.mark.parametrize("with_offset", [True, False])
+@pytest.mark.parametrize("M,K,N,group", [
+    (65, 512, 112, 128),      # one row past the decode kernels; a single column block narrower than the tile
+    (200, 1024, 4112, 256),   # partial row block; 257 strips: the last column block holds one strip
+    (128, 2048, 272, 2048),   # one group over all of K
+    (1000, 768, 1008, 128),   # eight row blocks, the last one partial
+])
+def test_prefill_gemm(ascq_gpu, oracle, w_type, with_offset, M, K, N, group):
+    """M > 64: the LDS-staged GEMM whose weight tiles are dequantised once per 256 rows (aq_gemm.hip); the weights
+    bit-exact as AscendAntiQuant, fp32 accumulation within the bound of check_close"""
+    rng = seeded(M + K + N + group + with_offset)
+    code = O.INT8 if w_type == "int8" else O.INT4
+    at = ascq_gpu.INT8 if w_type == "int8" else ascq_gpu.INT4
+    w, scale, offset = make_weights(rng, K, N, code, group, with_offset)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    wp = ascq_gpu.weight_pack(_dev(w), at, K, N)
+    y = ascq_gpu.antiquant_matmul(_dev(x), wp, at, _dev(scale), None if offset is None else _dev(offset), group, N)
+    _, y_exact, y_abs = O.antiquant_matmul(x.view(np.uint16), w, code, scale.view(np.uint16),
+                                           None if offset is None else offset.view(np.uint16), group, M, N, K)
+    check_close(y.cpu().numpy(), y_exact, y_abs, K)
+
+
+@pytest.mark.parametrize("w_type", ["int4", "int8"])
+def test_prefill_gemm_config3_weight(ascq_gpu, oracle, w_type):
+    """M = 512 prefill rows against the config-3 weight (K = 4096, N = 11008, g = 128, f16 scale and offset): every
+    output of 64 sampled rows (16 in each 128 rows, the first and last rows among them)"""
+    rng = seeded(512)
+    M, K, N, g = 512, 4096, 11008, 128
+    code = O.INT8 if w_type == "int8" else O.INT4
+    at = ascq_gpu.INT8 if w_type == "int8" else ascq_gpu.INT4
+    w, scale, offset = make_weights(rng, K, N, code, g)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    wp = ascq_gpu.weight_pack(_dev(w), at, K, N)
+    y = ascq_gpu.antiquant_matmul(_dev(x), wp, at, _dev(scale), _dev(offset), g, N).cpu().numpy()
+    rows = np.unique(np.concatenate([[0, M - 1]] + [b + rng.choice(128, 16, replace=False) for b in range(0, M, 128)]))
+    _, y_exact, y_abs = O.antiquant_matmul(np.ascontiguousarray(x[rows]).view(np.uint16), w, code,
+                                           scale.view(np.uint16), offset.view(np.uint16), g, len(rows), N, K)
+    check_close(y[rows], y_exact, y_abs, K)
+
+
+@pytest.mark.parametrize("w_type", ["int4", "int8"])
 @pytest.mark.parametrize("b_format", ["nd", "packed"])
 def test_matmul_handle_antiquant(ascq_gpu, oracle, w_type, b_format):
     """Matmul<half, int8|int4, half> with SetAntiQuantVector (per group) and SetAntiQuantScalar."""
