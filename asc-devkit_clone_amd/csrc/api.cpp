@@ -20,7 +20,8 @@ thread_local std::string g_err;
 thread_local ascq::LaunchEvents g_launch_events;
 
 // Host log, gated by the environment variable ASCQ_LOG (read once): unset or 0 = silent; 1 = the message of every
-// failed call on stderr; 2 = also one line per accepted call of the main entry points (name, types, shape).
+// failed call and every launch that takes a generic (fallback) kernel, on stderr; 2 = also one line per accepted call
+// of the main entry points (name, types, shape).
 int log_level()
 {
     static const int level = [] {
@@ -75,6 +76,13 @@ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_
 inline bool valid_round(int32_t r) { return r >= ASCQ_ROUND_NONE && r <= ASCQ_ROUND_TRUNC; }
 
 }  // namespace
+
+namespace ascq {
+void log_fallback(const char* kernel, const char* reason)
+{
+    if (log_level() >= 1) std::fprintf(stderr, "ascq: fallback: %s (%s)\n", kernel, reason);
+}
+}  // namespace ascq
 
 // Scratch of ascq_matmul_iterate_all_noalloc: one array per device (the code object's copy on each GPU), held
 // until the process ends.  Host code never uses the array's name as an address: it is looked up once per device

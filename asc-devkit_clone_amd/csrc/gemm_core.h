@@ -637,6 +637,190 @@ struct GemmCore {
     }
 };
 
+// A raw buffer resource over the `bytes` bytes at p whose base is p aligned down to 16 bytes; delta = p % 16 is to be
+// added to every offset into it.  Multi-dword buffer loads are range-checked per dword, so the range is rounded up to
+// whole dwords: the dword that holds the operand's last byte then reads that byte (it lies in the byte's page).
+__device__ __forceinline__ rsrc_t make_rsrc_a16(const void* p, uint32_t bytes, uint32_t& delta)
+{
+    delta = (uint32_t)((uintptr_t)p & 15u);
+    return make_rsrc((const uint8_t*)p - delta, (bytes + delta + 3u) & ~3u);
+}
+
+// GemmCoreUA: GemmCore's int8 / fp8 tiles, two-stage LDS layout (ROWB = 64), fragment reads and MFMAs for operands of
+// any alignment and any K: K not a multiple of 16, leading dimensions and base pointers of any byte alignment.  The
+// operands go global -> registers -> LDS.  A lane takes one 16-byte chunk per copy unit -- 16 K bytes of an A row or
+// of a K-contiguous B row, or (int8) 16 columns of one K row of a [K, N] B (staged as GemmCore's B_TR region and read
+// by its transposed reads) -- as the two 16-byte-aligned blocks that cover it, picks the chunk's five dwords and
+// realigns them with v_alignbyte_b32, zeroes its bytes at k >= K, and writes it with one 16-byte LDS store to the
+// chunk the swizzle assigns.  Zeroing both operands' bytes past K keeps other rows' (or other groups') bytes out of
+// every product, also for a chunk that straddles the end of a row (fp8: a zero byte is +0, so no NaN or infinity
+// from past K reaches a sum).
+// Every load is 16-byte aligned in memory (the resources' bases are aligned down to 16 bytes, make_rsrc_a16, and the
+// offsets carry the difference): a block that holds a byte of the operand lies in that byte's page, and a block that
+// starts past the operand is out of the resource's range and reads zeros (the second block is skipped outright
+// when the chunk's valid bytes end in the first).
+// Pipeline: two register sets hold the chunks of the two stages after the one being multiplied.  Iteration kt: one
+// barrier (stage kt is in its slot, the other slot's readers are done), the MFMAs of stage kt, then stage kt + 1
+// from its register set into the other slot and the loads of stage kt + 3 into that set -- two stages of MFMAs
+// cover each load.
+template <int BM, int BN, int WM, int WN, bool B_KCONTIG, bool CT, int OP = OP_I8, int FMT = 0>
+struct GemmCoreUA : GemmCore<BM, BN, WM, WN, 2, B_KCONTIG, OP, 64, FMT, true, CT, !B_KCONTIG> {
+    using Base = GemmCore<BM, BN, WM, WN, 2, B_KCONTIG, OP, 64, FMT, true, CT, !B_KCONTIG>;
+    using acc_t = typename Base::acc_t;
+    static_assert(OP == OP_I8 || (OP == OP_F8 && B_KCONTIG), "int8, or fp8 with a K-contiguous B");
+    static constexpr int ROWB = 64, CH = 4;
+    static constexpr int NT = Base::NT, FM = Base::FM, FN = Base::FN, WTM = Base::WTM, WTN = Base::WTN;
+    static constexpr int CHB = BN / 16;                // [K, N] B: chunks per K row
+    static constexpr int AC = BM * CH / NT;            // A chunks per thread per stage
+    static constexpr int BC = BN * CH / NT;            // B chunks per thread per stage (BN rows or 64 K rows)
+    static constexpr int U = AC + BC;
+    static_assert(AC >= 1 && BC >= 1 && AC * NT == BM * CH && BC * NT == BN * CH, "chunks per thread");
+
+    struct Regs {
+        u32x4 lo[U], hi[U];
+    };
+
+    // chunk u of this thread in stage kt: byte offset in its resource (past the resource's delta), the number of its
+    // 16 bytes that hold operand data (0: rows past the tile, chunks past K or past the tile's columns) and its
+    // offset within an LDS stage
+    __device__ __forceinline__ static void chunk(const CoreArgs& p, int t, int64_t kt, int u, uint32_t& off, int& valid,
+                                                 uint32_t& lds)
+    {
+        const int64_t kb0 = kt * ROWB;
+        auto kvalid = [&](int64_t k) {
+            const int64_t v = p.kbytes - k;
+            return v <= 0 ? 0 : (v >= 16 ? 16 : (int)v);
+        };
+        if (u < AC) {
+            const int id = t + u * NT, row = id / CH, c = id % CH;
+            const int64_t k = kb0 + c * 16;
+            valid = row < p.rows ? kvalid(k) : 0;
+            off = p.a0 + (uint32_t)row * p.lda + (uint32_t)k;
+            lds = (uint32_t)(row * ROWB + Base::swz(row, c) * 16);
+        } else if constexpr (B_KCONTIG) {
+            const int id = t + (u - AC) * NT, row = id / CH, c = id % CH;
+            const int64_t k = kb0 + c * 16;
+            valid = row < p.cols ? kvalid(k) : 0;
+            off = p.b0 + (uint32_t)row * p.ldb + (uint32_t)k;
+            lds = (uint32_t)(BM * ROWB + row * ROWB + Base::swz(row, c) * 16);
+        } else {
+            const int id = t + (u - AC) * NT, kr = id / CHB, c = id % CHB;
+            const int64_t k = kb0 + kr;
+            // columns past the tile's within a chunk are other data: their products land in unstored outputs
+            valid = (k < p.kbytes && c * 16 < p.cols) ? 16 : 0;
+            off = p.b0 + (uint32_t)k * p.ldb + (uint32_t)(c * 16);
+            lds = (uint32_t)(BM * ROWB + kr * BN + Base::swzb(kr, c) * 16);
+        }
+    }
+
+    __device__ __forceinline__ static void run(const CoreArgs& p, uint8_t* smem, acc_t (&acc)[FM][FN],
+                                               int t = (int)threadIdx.x)
+    {
+        const int lane = t & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+        const int wm = wave / WN, wn = wave % WN;
+        const int r32 = lane & 31, kh = lane >> 5;
+        const int64_t nk = (p.kbytes + ROWB - 1) / ROWB;
+
+        auto load = [&](Regs& R, int64_t kt) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                uint32_t off, lds;
+                int valid;
+                chunk(p, t, kt, u, off, valid, lds);
+                const rsrc_t r = u < AC ? p.a : p.b;
+                const uint32_t o = off & ~15u, s = off & 15u;
+                R.lo[u] = bload16(r, valid > 0 ? o : OOB);
+                R.hi[u] = bload16(r, (int)s + valid > 16 ? o + 16 : OOB);
+            }
+        };
+        auto store = [&](const Regs& R, int64_t kt, int slot) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                uint32_t off, lds;
+                int valid;
+                chunk(p, t, kt, u, off, valid, lds);
+                const uint32_t s = off & 15u, q = s >> 2, sh = s & 3u;
+                const uint32_t w[8] = {R.lo[u][0], R.lo[u][1], R.lo[u][2], R.lo[u][3],
+                                       R.hi[u][0], R.hi[u][1], R.hi[u][2], R.hi[u][3]};
+                uint32_t d[5];
+#pragma unroll
+                for (int i = 0; i < 5; ++i)
+                    d[i] = q == 0 ? w[i] : (q == 1 ? w[i + 1] : (q == 2 ? w[i + 2] : w[i + 3]));
+                u32x4 out;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int nv = valid - 4 * j;  // valid bytes of dword j
+                    const uint32_t m = nv >= 4 ? ~0u : (nv <= 0 ? 0u : (1u << (8 * nv)) - 1u);
+                    out[j] = __builtin_amdgcn_alignbyte(d[j + 1], d[j], sh) & m;
+                }
+                *(u32x4*)(smem + slot * Base::STAGE + lds) = out;
+            }
+        };
+
+        uint32_t troff[FN];  // [K, N] B: this lane's transposed-read offsets, one per fragment column
+#pragma unroll
+        for (int j = 0; j < FN; ++j) troff[j] = B_KCONTIG ? 0u : Base::tr_lane_off(wn * WTN + j * 32, lane);
+        auto compute = [&](int slot) {
+            const uint8_t* sA = smem + slot * Base::STAGE;
+            const uint8_t* sB = sA + BM * ROWB;
+#pragma unroll
+            for (int s = 0; s < Base::KPS; ++s) {
+                v8i fa[FM];
+#pragma unroll
+                for (int i = 0; i < FM; ++i) fa[i] = Base::read_frag(sA, wm * WTM + i * 32 + r32, s, kh);
+                v4i ftr[FN];
+                if constexpr (!B_KCONTIG)
+                    Base::read_frags_tr((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)sB, troff,
+                                        s, ftr);
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    v8i fb;
+                    if constexpr (B_KCONTIG) fb = Base::read_frag(sB, wn * WTN + j * 32 + r32, s, kh);
+                    else fb = (v8i){ftr[j][0], ftr[j][1], ftr[j][2], ftr[j][3], 0, 0, 0, 0};
+#pragma unroll
+                    for (int i = 0; i < FM; ++i) {
+                        if constexpr (OP == OP_I8) {
+                            const v4i a4 = (v4i){fa[i][0], fa[i][1], fa[i][2], fa[i][3]};
+                            const v4i b4 = (v4i){fb[0], fb[1], fb[2], fb[3]};
+                            if constexpr (CT) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b4, a4, acc[i][j], 0, 0, 0);
+                            else acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, b4, acc[i][j], 0, 0, 0);
+                        } else {
+                            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb, acc[i][j], Base::CBSZ,
+                                                                                         Base::BLGP, 0, 0, 0, 0);
+                        }
+                    }
+                }
+            }
+        };
+
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = (acc_t){};
+        Regs R0, R1;
+        load(R0, 0);
+        if (nk > 1) load(R1, 1);
+        store(R0, 0, 0);
+        if (nk > 2) load(R0, 2);
+        // Rn holds stage kt + 1 (same parity as kt + 3)
+        auto iteration = [&](int64_t kt, Regs& Rn) {
+            __syncthreads();
+            compute((int)(kt & 1));
+            if (kt + 1 < nk) {
+                store(Rn, kt + 1, (int)((kt + 1) & 1));
+                if (kt + 3 < nk) load(Rn, kt + 3);
+            }
+        };
+        int64_t kt = 0;
+        for (; kt + 1 < nk; kt += 2) {
+            iteration(kt, R1);
+            iteration(kt + 1, R0);
+        }
+        if (kt < nk) iteration(kt, R1);
+    }
+};
+
 // the 32 bits of one accumulator element (a value copy: __builtin_bit_cast of a vector-element lvalue reads the
 // vector's first element under this compiler)
 __device__ __forceinline__ uint32_t acc_bits(float x) { return __float_as_uint(x); }

@@ -68,27 +68,36 @@ __device__ __forceinline__ void store_f8_out(void* C, int c_type, int64_t o, flo
 template <int FMT>
 constexpr int op_of_fmt = (FMT == (FMT_BF16 | (FMT_BF16 << 3))) ? OP_BF16 : OP_F8;
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT, bool UA = false>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
 {
     constexpr int OP = op_of_fmt<FMT>;
     constexpr int ES = OP == OP_BF16 ? 2 : 1;  // bytes per operand element
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP, RB, FMT>;
+    // UA (fp8, B K-contiguous): operands of any alignment and any K (GemmCoreUA)
+    using T = typename std::conditional<UA, GemmCoreUA<BM, BN, WM, WN, TB, false, OP, FMT>,
+                                        GemmCore<BM, BN, WM, WN, ST, TB, OP, RB, FMT>>::type;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_f8[];
     const int tiles_m = (int)((p.M + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
     int tm, tn;
     tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     CoreArgs c{};
-    c.a = make_rsrc(p.A, (uint32_t)((p.lda * (p.M - 1) + p.K) * ES));
-    c.b = TB ? make_rsrc(p.B, (uint32_t)((p.ldb * (p.N - 1) + p.K) * ES))
-             : make_rsrc(p.B, (uint32_t)(p.ldb * (p.K - 1) + p.N));
+    const uint32_t a_bytes = (uint32_t)((p.lda * (p.M - 1) + p.K) * ES);
+    const uint32_t b_bytes = (uint32_t)(TB ? (p.ldb * (p.N - 1) + p.K) * ES : p.ldb * (p.K - 1) + p.N);
+    uint32_t da = 0, db = 0;  // UA: the operands' offsets from their resources' 16-byte-aligned bases
+    if constexpr (UA) {
+        c.a = make_rsrc_a16(p.A, a_bytes, da);
+        c.b = make_rsrc_a16(p.B, b_bytes, db);
+    } else {
+        c.a = make_rsrc(p.A, a_bytes);
+        c.b = make_rsrc(p.B, b_bytes);
+    }
     c.lda = (uint32_t)(p.lda * ES);
     c.ldb = (uint32_t)(TB ? p.ldb * ES : p.ldb);
     c.rows = (int32_t)(p.M - m0 < BM ? p.M - m0 : BM);
     c.cols = (int32_t)(p.N - n0 < BN ? p.N - n0 : BN);
-    c.a0 = (uint32_t)(m0 * p.lda * ES);
-    c.b0 = (uint32_t)(TB ? n0 * p.ldb * ES : n0);
+    c.a0 = (uint32_t)(m0 * p.lda * ES) + da;
+    c.b0 = (uint32_t)(TB ? n0 * p.ldb * ES : n0) + db;
     c.kbytes = p.K * ES;
     typename T::acc_t acc[T::FM][T::FN];
     T::run(c, smem_f8, acc);
@@ -220,21 +229,30 @@ __global__ __launch_bounds__(256) void gemm_f8_generic_kernel(GemmF8Args p)
     }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT, bool UA = false>
 static hipError_t launch_f8_tiled(const GemmF8Args& a, hipStream_t st)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, op_of_fmt<FMT>, RB, FMT>;
+    using T = typename std::conditional<UA, GemmCoreUA<BM, BN, WM, WN, TB, false, op_of_fmt<FMT>, FMT>,
+                                        GemmCore<BM, BN, WM, WN, ST, TB, op_of_fmt<FMT>, RB, FMT>>::type;
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
-    const hipError_t e = ensure_dynamic_lds<gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT>>((int)T::LDS_BYTES);
+    const hipError_t e = ensure_dynamic_lds<gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT, UA>>((int)T::LDS_BYTES);
     if (e != hipSuccess) return e;
-    launch_k((gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
+    launch_k((gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT, UA>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
     return hipGetLastError();
 }
 
 template <int FMT>
-static hipError_t launch_f8_fmt(const GemmF8Args& a, hipStream_t st)
+static hipError_t launch_f8_fmt(const GemmF8Args& a, bool ua, hipStream_t st)
 {
     constexpr int ES = op_of_fmt<FMT> == OP_BF16 ? 2 : 1;
+    // fp8 operands of any alignment / any K with a K-contiguous B: GemmCoreUA tiles, 64 x 64 while 128 x 128 would
+    // leave fewer than 256 workgroups
+    if constexpr (ES == 1) {
+        if (ua)
+            return ((a.M + 127) / 128) * ((a.N + 127) / 128) < 256 ? launch_f8_tiled<64, 64, 2, 2, 2, true, 64, FMT, true>(a, st)
+                                                                  : launch_f8_tiled<128, 128, 2, 2, 2, true, 64, FMT, true>(a, st);
+    }
+    if (ua) return hipErrorInvalidValue;
     const bool big = a.M >= 1024 && a.N >= 1024;
     if (a.trans_b) {
         if (big) return (a.K * ES) % 128 == 0 ? launch_f8_tiled<256, 256, 4, 2, 2, true, 128, FMT>(a, st)
@@ -259,15 +277,26 @@ hipError_t launch_gemm_f8(const GemmF8Args& a, hipStream_t st)
     const bool b_ok = a.trans_b ? ((a.ldb * es) % 16 == 0 && ((uintptr_t)a.B % 16 == 0) && a.ldb * es * a.N < (1ll << 31))
                                 : (a.ldb % 4 == 0 && a.N % 4 == 0 && ((uintptr_t)a.B % 4 == 0) && a.ldb * a.K < (1ll << 31));
     // the tiled epilogue addresses a 256-row output tile with 32-bit offsets
-    if (a_ok && b_ok && (a.K * es) % 16 == 0 && a.ldc < (1ll << 21)) {
-        if (bf) return launch_f8_fmt<FMT_BF16 | (FMT_BF16 << 3)>(a, st);
+    const bool tiled = a_ok && b_ok && (a.K * es) % 16 == 0 && a.ldc < (1ll << 21);
+    // otherwise fp8 with A [M, K] and B [N, K] (any alignment, any K) takes the any-alignment tiles
+    const char* why = tiled ? nullptr
+                      : bf ? "bf16 operands: K not a multiple of 8"
+                      : a.trans_a ? "A given [K, M]"
+                      : !a.trans_b ? "B given [K, N] with K not a multiple of 16 or operands not aligned"
+                      : (a.lda * (a.M - 1) + a.K >= (1ll << 31) - 16 || a.ldb * (a.N - 1) + a.K >= (1ll << 31) - 16)
+                          ? "an operand spans 2^31 bytes"
+                      : a.ldc >= (1ll << 21) ? "ldc >= 2^21"
+                                             : nullptr;
+    if (!why) {
+        if (bf) return launch_f8_fmt<FMT_BF16 | (FMT_BF16 << 3)>(a, false, st);
         switch (a.fmt_a | (a.fmt_b << 3)) {
-        case F8F6F4_E4M3 | (F8F6F4_E4M3 << 3): return launch_f8_fmt<F8F6F4_E4M3 | (F8F6F4_E4M3 << 3)>(a, st);
-        case F8F6F4_E5M2 | (F8F6F4_E5M2 << 3): return launch_f8_fmt<F8F6F4_E5M2 | (F8F6F4_E5M2 << 3)>(a, st);
-        case F8F6F4_E4M3 | (F8F6F4_E5M2 << 3): return launch_f8_fmt<F8F6F4_E4M3 | (F8F6F4_E5M2 << 3)>(a, st);
-        default: return launch_f8_fmt<F8F6F4_E5M2 | (F8F6F4_E4M3 << 3)>(a, st);
+        case F8F6F4_E4M3 | (F8F6F4_E4M3 << 3): return launch_f8_fmt<F8F6F4_E4M3 | (F8F6F4_E4M3 << 3)>(a, !tiled, st);
+        case F8F6F4_E5M2 | (F8F6F4_E5M2 << 3): return launch_f8_fmt<F8F6F4_E5M2 | (F8F6F4_E5M2 << 3)>(a, !tiled, st);
+        case F8F6F4_E4M3 | (F8F6F4_E5M2 << 3): return launch_f8_fmt<F8F6F4_E4M3 | (F8F6F4_E5M2 << 3)>(a, !tiled, st);
+        default: return launch_f8_fmt<F8F6F4_E5M2 | (F8F6F4_E4M3 << 3)>(a, !tiled, st);
         }
     }
+    log_fallback("gemm_f8_generic_kernel", why);
     int64_t blocks = (a.M * a.N + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (blocks < 1) blocks = 1;

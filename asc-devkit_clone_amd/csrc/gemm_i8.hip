@@ -24,14 +24,21 @@ __device__ __forceinline__ int64_t uniform64(int64_t v)
     return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
+// The int8 main loop of a tile: GemmCore (16-byte-aligned K-contiguous rows, K % 16 == 0), or GemmCoreUA (UA: any
+// alignment, any K; two stages of 64 bytes, a [K, N] B staged by K rows)
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, bool CT, bool BTR, bool UA>
+using I8Core = typename std::conditional<UA, GemmCoreUA<BM, BN, WM, WN, TB, CT>,
+                                         GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB, 0, true, CT, BTR>>::type;
+
 // KW > 1 (one-wave tiles, WM = WN = 1; store epilogues only): the workgroup's KW waves each run the tile's main loop on
 // their own K / KW range (K a multiple of KW * RB, so every wave runs the same stages and meets the same barriers) in
 // their own LDS ring, then sum their int32 accumulators through LDS (exact in any order) and wave 0 runs the epilogue.
 // For small problems (the W8A8 sample, 32 tiles) this cuts the serial K loop of each tile KW-fold.
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, bool BTR = false, int KW = 1>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, bool BTR = false, int KW = 1, bool UA = false>
 __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_i8_kernel(GemmI8Args p)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB, 0, true, false, BTR>;
+    using T = I8Core<BM, BN, WM, WN, ST, TB, RB, false, BTR, UA>;
+    static_assert(!UA || KW == 1, "any-alignment tiles run whole K");
     static_assert(KW == 1 || (WM == 1 && WN == 1), "k-split waves run one-wave tiles");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tiles_m = (int)((p.M + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
@@ -41,14 +48,22 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_i8_kernel(GemmI8Args p
     const int kw = KW > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
     const int64_t kc = p.K / KW, k0 = kw * kc;  // this wave's K range (KW > 1: K % (KW RB) == 0)
     CoreArgs c{};
-    c.a = make_rsrc(p.A, (uint32_t)(p.lda * (p.M - 1) + p.K));
-    c.b = TB ? make_rsrc(p.B, (uint32_t)(p.ldb * (p.N - 1) + p.K)) : make_rsrc(p.B, (uint32_t)(p.ldb * (p.K - 1) + p.N));
+    const uint32_t a_bytes = (uint32_t)(p.lda * (p.M - 1) + p.K);
+    const uint32_t b_bytes = (uint32_t)(TB ? p.ldb * (p.N - 1) + p.K : p.ldb * (p.K - 1) + p.N);
+    uint32_t da = 0, db = 0;  // UA: the operands' offsets from their resources' 16-byte-aligned bases
+    if constexpr (UA) {
+        c.a = make_rsrc_a16(p.A, a_bytes, da);
+        c.b = make_rsrc_a16(p.B, b_bytes, db);
+    } else {
+        c.a = make_rsrc(p.A, a_bytes);
+        c.b = make_rsrc(p.B, b_bytes);
+    }
     c.lda = (uint32_t)p.lda;
     c.ldb = (uint32_t)p.ldb;
     c.rows = (int32_t)(p.M - m0 < BM ? p.M - m0 : BM);
     c.cols = (int32_t)(p.N - n0 < BN ? p.N - n0 : BN);
-    c.a0 = (uint32_t)(m0 * p.lda + k0);
-    c.b0 = (uint32_t)(TB ? n0 * p.ldb + k0 : n0 + k0 * p.ldb);
+    c.a0 = (uint32_t)(m0 * p.lda + k0) + da;
+    c.b0 = (uint32_t)(TB ? n0 * p.ldb + k0 : n0 + k0 * p.ldb) + db;
     c.kbytes = kc;
     typename T::acc_t acc[T::FM][T::FN];
     T::run(c, smem + (KW > 1 ? kw * T::LDS_BYTES : 0), acc, KW > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x);
@@ -174,12 +189,13 @@ __device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* wtot
 }
 
 // WPE: waves per SIMD the register allocation must allow (2 for two 4-wave workgroups per CU)
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1, bool BTR = false>
+// UA: X and W of any alignment and any K (GemmCoreUA)
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1, bool BTR = false, bool UA = false>
 __global__ __launch_bounds__(WM * WN * 64, WPE) void group_gemm_i8_kernel(GroupGemmArgs p)
 {
     // transposed accumulators: four consecutive output columns per register quad, stored as one 8-byte vector;
     // BTR: W given [G, K, N] staged by K rows and read with LDS transpose reads
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB, 0, true, true, BTR>;
+    using T = I8Core<BM, BN, WM, WN, ST, TB, RB, true, BTR, UA>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int64_t wtot[T::NT / 64];
     __shared__ int64_t tile_info[4];  // group, first row, end row, first m-tile of this workgroup's tile
@@ -249,14 +265,20 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void group_gemm_i8_kernel(GroupG
         const int64_t m0 = uniform64(g_first + (rem % mt_g) * BM);
         const int64_t n0 = (int64_t)tn * BN;
         CoreArgs c{};
-        c.a = make_rsrc(p.X, (uint32_t)(p.M * p.K));
-        c.b = make_rsrc(p.W + (int64_t)g * p.K * p.N, (uint32_t)(p.K * p.N));
+        uint32_t da = 0, db = 0;  // UA: the operands' offsets from their resources' 16-byte-aligned bases
+        if constexpr (UA) {
+            c.a = make_rsrc_a16(p.X, (uint32_t)(p.M * p.K), da);
+            c.b = make_rsrc_a16(p.W + (int64_t)g * p.K * p.N, (uint32_t)(p.K * p.N), db);
+        } else {
+            c.a = make_rsrc(p.X, (uint32_t)(p.M * p.K));
+            c.b = make_rsrc(p.W + (int64_t)g * p.K * p.N, (uint32_t)(p.K * p.N));
+        }
         c.lda = (uint32_t)p.K;
         c.ldb = (uint32_t)(TB ? p.K : p.N);
         c.rows = (int32_t)(m_end - m0 < BM ? m_end - m0 : BM);
         c.cols = (int32_t)(p.N - n0 < BN ? p.N - n0 : BN);
-        c.a0 = (uint32_t)(m0 * p.K);
-        c.b0 = (uint32_t)(TB ? n0 * p.K : n0);
+        c.a0 = (uint32_t)(m0 * p.K) + da;
+        c.b0 = (uint32_t)(TB ? n0 * p.K : n0) + db;
         c.kbytes = p.K;
 
         // the epilogue's scales go global -> LDS now (waves 0 and 1, one copy each, no registers held), so their
@@ -363,15 +385,16 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(GemmI8Args p)
     }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, bool BTR = false, int KW = 1>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, bool BTR = false, int KW = 1, bool UA = false>
 static hipError_t launch_tiled(const GemmI8Args& a, hipStream_t st)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB, 0, true, false, BTR>;
+    using T = I8Core<BM, BN, WM, WN, ST, TB, RB, false, BTR, UA>;
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
     constexpr size_t lds = T::LDS_BYTES * KW;
-    const hipError_t e = ensure_dynamic_lds<gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, BTR, KW>>((int)lds);
+    const hipError_t e = ensure_dynamic_lds<gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, BTR, KW, UA>>((int)lds);
     if (e != hipSuccess) return e;
-    launch_k((gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, BTR, KW>), dim3(tiles), dim3(T::NT * KW), (uint32_t)lds, st, a);
+    launch_k((gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, BTR, KW, UA>), dim3(tiles), dim3(T::NT * KW), (uint32_t)lds, st,
+             a);
     return hipGetLastError();
 }
 
@@ -405,6 +428,22 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
         if (tiny) return launch_tiled<32, 32, 1, 1, 4, false>(a, st);
         return big ? launch_tiled<256, 256, 4, 2, 4, false>(a, st) : launch_tiled<64, 128, 2, 2, 4, false>(a, st);
     }
+    // K not a multiple of 16, or operands / leading dimensions not 16-byte (A, K-contiguous B) or 4-byte ([K, N] B)
+    // aligned: the any-alignment tiles (GemmCoreUA), 64 x 64 while that leaves fewer than 256 workgroups of 128 x 128
+    const int64_t a_span = a.lda * (a.M - 1) + a.K, b_span = a.trans_b ? a.ldb * (a.N - 1) + a.K : a.ldb * (a.K - 1) + a.N;
+    const char* why = a.trans_a                            ? "A given [K, M]"
+                      : (a_span >= (1ll << 31) - 16 || b_span >= (1ll << 31) - 16) ? "an operand spans 2^31 bytes"
+                      : a.ldc >= (1ll << 21)               ? "ldc >= 2^21"
+                                                           : nullptr;
+    if (!why) {
+        const bool small = ((a.M + 127) / 128) * ((a.N + 127) / 128) < 256;
+        if (a.trans_b)
+            return small ? launch_tiled<64, 64, 2, 2, 2, true, 64, false, 1, true>(a, st)
+                         : launch_tiled<128, 128, 2, 2, 2, true, 64, false, 1, true>(a, st);
+        return small ? launch_tiled<64, 64, 2, 2, 2, false, 64, true, 1, true>(a, st)
+                     : launch_tiled<128, 128, 2, 2, 2, false, 64, true, 1, true>(a, st);
+    }
+    log_fallback("gemm_i8_generic_kernel", why);
     int64_t blocks = (a.M * a.N + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (blocks < 1) blocks = 1;
@@ -439,24 +478,40 @@ __global__ __launch_bounds__(256) void group_gemm_generic_kernel(GroupGemmArgs p
     }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1, bool BTR = false>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1, bool BTR = false, bool UA = false>
 static hipError_t launch_group_tiled(const GroupGemmArgs& a, hipStream_t st)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, TB, OP_I8, RB, 0, true, true, BTR>;
+    using T = I8Core<BM, BN, WM, WN, ST, TB, RB, true, BTR, UA>;
     const int64_t upper = ((a.M + BM - 1) / BM + a.G) * ((a.N + BN - 1) / BN);  // tiles, at most
-    const hipError_t e = ensure_dynamic_lds<group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, WPE, BTR>>((int)T::LDS_BYTES);
+    const hipError_t e =
+        ensure_dynamic_lds<group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, WPE, BTR, UA>>((int)T::LDS_BYTES);
     if (e != hipSuccess) return e;
-    launch_k((group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, WPE, BTR>), dim3((unsigned)((upper + 7) / 8 * 8)),
+    launch_k((group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, WPE, BTR, UA>), dim3((unsigned)((upper + 7) / 8 * 8)),
              dim3(T::NT), T::LDS_BYTES, st, a);
     return hipGetLastError();
 }
 
 hipError_t launch_group_gemm(const GroupGemmArgs& a, hipStream_t st)
 {
-    const bool ok = a.K % 16 == 0 && ((uintptr_t)a.X % 16 == 0) &&
-                    (a.w_trans ? ((uintptr_t)a.W % 16 == 0) : (a.N % 4 == 0 && (uintptr_t)a.W % 4 == 0)) &&
-                    a.G <= GROUP_MAX && a.M * a.K < (1ll << 31) && a.K * a.N < (1ll << 31) && a.N < (1ll << 21);
-    if (ok) {
+    const char* why = a.G > GROUP_MAX                                          ? "more than 1024 groups"
+                      : (a.M * a.K >= (1ll << 31) - 16 || a.K * a.N >= (1ll << 31) - 16) ? "an operand spans 2^31 bytes"
+                      : a.N >= (1ll << 21)                                     ? "N >= 2^21"
+                                                                               : nullptr;
+    if (why) {
+        log_fallback("group_gemm_generic_kernel", why);
+        int64_t blocks = (a.M * a.N + 255) / 256;
+        if (blocks > 65536) blocks = 65536;
+        if (blocks < 1) blocks = 1;
+        launch_k(group_gemm_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+        return hipGetLastError();
+    }
+    const bool aligned = a.K % 16 == 0 && ((uintptr_t)a.X % 16 == 0) &&
+                         (a.w_trans ? ((uintptr_t)a.W % 16 == 0) : (a.N % 4 == 0 && (uintptr_t)a.W % 4 == 0));
+    // K not a multiple of 16 or X / W not aligned: 128 x 128 tiles of GemmCoreUA, two workgroups per CU
+    if (!aligned)
+        return a.w_trans ? launch_group_tiled<128, 128, 2, 2, 2, true, 64, 2, false, true>(a, st)
+                         : launch_group_tiled<128, 128, 2, 2, 2, false, 64, 2, true, true>(a, st);
+    {
         // 128 x 256 tiles.  Short K (the reference sample's K = 1024): 4 waves with 64 x 128 wave tiles and
         // 64-byte stages, two workgroups per CU, so one's epilogue and its store / load latencies overlap the
         // other's MFMAs (measured 110-120 us against 145-150 us for one 8-wave workgroup per CU).  Long K (the
@@ -473,11 +528,6 @@ hipError_t launch_group_gemm(const GroupGemmArgs& a, hipStream_t st)
         }
         return launch_group_tiled<128, 128, 2, 2, 4, false>(a, st);
     }
-    int64_t blocks = (a.M * a.N + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    if (blocks < 1) blocks = 1;
-    launch_k(group_gemm_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
-    return hipGetLastError();
 }
 
 }  // namespace ascq

@@ -16,6 +16,11 @@ namespace ascq {
 // one atomic read-modify-write per element (c_atomic), so concurrent IterateAll calls into the same C compose.
 enum : int { C_STORE = 0, C_ADD = 1, C_MAX = 2, C_MIN = 3 };
 
+// A launcher took a generic kernel (one thread per output element, or an element-wise kernel without vector loads)
+// instead of a tiled / vectorised one: with the environment variable ASCQ_LOG set to 1 or more, one line on stderr
+// names the kernel and the reason (api.cpp).
+void log_fallback(const char* kernel, const char* reason);
+
 // Raises the dynamic-LDS limit of kernel K to `bytes` once per device (the attribute belongs to the function on
 // the current device), thread-safe; K is the kernel itself, so each instantiation keeps its own record.
 template <auto K>

@@ -331,6 +331,8 @@ hipError_t launch_quant_dynamic_per_token(int8_t* q, float* scale_out, const voi
         default: return launch_dyn_row<RM_RINT>(x, q, scale_out, m, chunks, bf, st);
         }
     }
+    log_fallback("quant_dyn_generic_kernel", !half_src ? "f32 source" : !aligned ? "x not 16-byte or q not 8-byte aligned"
+                                               : n % 8 != 0 ? "n not a multiple of 8" : "n > 16384");
     dim3 grid(m), block(256);
     switch (round_mode) {
 #define ASCQ_G(MD) launch_k((quant_dyn_generic_kernel<MD>), grid, block, 0, st, x, q, scale_out, n, src_type); break;
@@ -975,6 +977,7 @@ hipError_t launch_quant_legacy(void* q, int dst_type, const void* x, int src_typ
         else launch_legacy_vec_arith<DT_F32>(a, st);
         return hipGetLastError();
     }
+    if (cal_count > 0) log_fallback("quant_legacy_elem_kernel", "count, scale count or pointers not aligned to 8 elements");
     launch_k(quant_legacy_elem_kernel, dim3(grid_for(cal_count)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
@@ -1164,6 +1167,7 @@ hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, 
         else launch_dequant_vec_dst<DT_F32>(a, dst_type, smode, st);
         return hipGetLastError();
     }
+    log_fallback("dequant_generic_kernel", "columns, row pitch or pointers not aligned to the vector unit");
     dim3 grid(grid_for((int64_t)rows * cols)), block(256);
     launch_k(dequant_generic_kernel, grid, block, 0, st, a, dst_type, src_type, smode);
     return hipGetLastError();
@@ -1233,6 +1237,7 @@ template <int DST, int T>
 static void launch_qp(const QuantPolicyArgs& a, bool vec, hipStream_t st)
 {
     if (!vec) {
+        log_fallback("quant_policy_generic_kernel", "n, group or pointers not aligned to the vector unit");
         const int64_t bytes = qd_nibble(DST) ? a.m * a.n / 2 : a.m * a.n;
         launch_k(quant_policy_generic_kernel<DST, T>, dim3(grid_for(bytes)), dim3(256), 0, st, a);
         return;
@@ -1633,6 +1638,7 @@ hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int
         else launch_aq_scale<DT_FP4_E2M1>(a, dst_type, scale_type, eight, st);
         return hipGetLastError();
     }
+    log_fallback("antiquant_policy_kernel", "n, group or pointers not aligned to the vector unit");
     dim3 grid(grid_for(m * n)), block(256);
     launch_k(antiquant_policy_kernel, grid, block, 0, st, dst, dst_type, src, src_type, scale, offset, scale_type,
              per_token, m, n, g, col_groups, is_transpose);
@@ -1719,6 +1725,7 @@ hipError_t launch_antiquant_scalar(void* dst, int dst_type, const void* src, int
     }
     const float sc = dst_type == DT_F16 ? (float)__builtin_bit_cast(_Float16, scale) : __builtin_bit_cast(float, (uint32_t)scale << 16);
     const float of = dst_type == DT_F16 ? (float)__builtin_bit_cast(_Float16, offset) : __builtin_bit_cast(float, (uint32_t)offset << 16);
+    log_fallback("antiquant_scalar_elem_kernel", "count not a multiple of 8 or pointers not aligned");
     launch_k(antiquant_scalar_elem_kernel, dim3(grid_for(count)), dim3(256), 0, st, dst, dst_type, src, src_type, of, sc,
              has_offset, count);
     return hipGetLastError();
@@ -1754,6 +1761,7 @@ hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_ty
             return hipGetLastError();
         }
     }
+    log_fallback("antiquant_kernel", "n, group or pointers not aligned to the vector unit");
     dim3 grid(grid_for((int64_t)K * N)), block(256);
     launch_k(antiquant_kernel, grid, block, 0, st, dst, dst_type, src, src_type, (const uint16_t*)offset,
                        (const uint16_t*)scale, K, N, g, is_transpose, arith);

@@ -125,6 +125,7 @@ hipError_t launch_transpose_i8(uint8_t* dst, const uint8_t* src, int64_t rows, i
         hipLaunchKernelGGL(transpose_tile_kernel<false>, dim3((unsigned)tiles), dim3(256), 0, st, dst, src, rows, cols);
         return hipGetLastError();
     }
+    log_fallback("transpose_i8_plain_kernel", "rows, columns or pointers not aligned to the 128 x 128 tiles");
     int64_t blocks = (rows * cols + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     hipLaunchKernelGGL(transpose_i8_plain_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, src, rows, cols);
