@@ -69,6 +69,13 @@ class _DequantPolicyParam(ctypes.Structure):
                 ("group_size", ctypes.c_uint32), ("has_offset", ctypes.c_int32), ("kdim", ctypes.c_int32)]
 
 
+class _QuantizeParam(ctypes.Structure):
+    """ascq_quantize_param: QuantizeConfig{policy, hasOffset, roundMode, kDim} + QuantizeParams{m, n, groupSize}"""
+    _fields_ = [("policy", ctypes.c_int32), ("has_offset", ctypes.c_int32), ("round_mode", ctypes.c_int32),
+                ("kdim", ctypes.c_int32), ("m", ctypes.c_uint32), ("n", ctypes.c_uint32),
+                ("group_size", ctypes.c_uint32)]
+
+
 class _MatmulTypes(ctypes.Structure):
     _fields_ = [
         ("a_type", ctypes.c_int32),
@@ -137,6 +144,9 @@ SIGNATURES = {
     "ascq_ascend_dequant_policy": (_I32, [_P, _I32, _P, _I32, _P, _P, _I32, _I32, ctypes.POINTER(_DequantPolicyParam),
                                           _P]),
     "ascq_ascend_antiquant": (_I32, [_P, _I32, _P, _I32, _P, _P, _U32, _U32, _U32, _I32, _I32, _P]),
+    "ascq_quantize": (_I32, [_P, _I32, _P, _I32, _P, _P, _F32, _F32, _I32, ctypes.POINTER(_QuantizeParam), _P]),
+    "ascq_dequantize": (_I32, [_P, _I32, _P, _I32, _P, _F32, _I32, ctypes.POINTER(_QuantizeParam), _P]),
+    "ascq_antiquantize": (_I32, [_P, _I32, _P, _I32, _P, _P, _F32, _F32, _I32, ctypes.POINTER(_QuantizeParam), _P]),
     "ascq_ascend_antiquant_policy": (_I32, [_P, _I32, _P, _I32, _P, _P, _I32, _I32, ctypes.c_int64, ctypes.c_int64,
                                             ctypes.c_int64, _I32, _I32, _P]),
     "ascq_weight_pack_size": (_I32, [_I32, _I64, _I64, ctypes.POINTER(ctypes.c_size_t)]),
@@ -347,6 +357,70 @@ def ascend_antiquant_policy(src: torch.Tensor, src_type: int, scale: torch.Tenso
     check(lib().ascq_ascend_antiquant_policy(_ptr(y), dst_type, _ptr(src), src_type, _ptr(scale), _ptr(offset),
                                              scale_type, policy, m, n, group_size, k_dim, int(is_transpose),
                                              _stream(stream)), "ascend_antiquant_policy")
+    return y
+
+
+# ------------------------------------------------------------------------------------------
+# Quantize / Dequantize / AntiQuantize (quantize.h / dequantize.h / antiquantize.h)
+# ------------------------------------------------------------------------------------------
+_FLOAT_CODE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
+
+
+def quantize(x: torch.Tensor, policy: int, dst_type: int = INT8, scale=None, offset=None, scale_scalar: float = 1.0,
+             offset_scalar=None, scale_type: int | None = None, group_size: int = 0, kdim: int = 1,
+             round_mode: int = ROUND_RINT, out=None, stream=None):
+    """Quantize<{policy, hasOffset, roundMode, kDim}>(dst, x, scale, offset, {m, n, groupSize}) of x [m, n] in fp32
+    arithmetic.  PER_TENSOR: scale_scalar / offset_scalar (values of scale_type); the other policies: `scale` (and
+    `offset`, or offset_scalar) tensors.  Returns int8 (INT8) or uint8 codes [m, n] ([m, n / 2] for fp4)."""
+    m, n = x.shape
+    if scale_type is None:
+        scale_type = _FLOAT_CODE[scale.dtype] if scale is not None else F32
+    if out is not None:
+        q = out
+    elif dst_type in (FP4_E2M1, FP4_E1M2):
+        q = torch.empty((m, n // 2), dtype=torch.uint8, device=x.device)
+    else:
+        q = torch.empty((m, n), dtype=torch.int8 if dst_type == INT8 else torch.uint8, device=x.device)
+    has_off = offset is not None or offset_scalar is not None
+    p = _QuantizeParam(policy, int(has_off), round_mode, kdim, m, n, group_size)
+    check(lib().ascq_quantize(_ptr(q), dst_type, _ptr(x), _FLOAT_CODE[x.dtype], _ptr(scale), _ptr(offset),
+                              float(scale_scalar), float(offset_scalar or 0.0), scale_type, ctypes.byref(p),
+                              _stream(stream)), "quantize")
+    return q
+
+
+def dequantize(src: torch.Tensor, policy: int, dst_dtype=torch.float32, scale=None, scale_scalar: float = 1.0,
+               scale_type: int | None = None, group_size: int = 0, kdim: int = 1, out=None, stream=None):
+    """Dequantize<{policy, false, kDim}>(dst, src, scale, {m, n, groupSize}): dst = cast(f32(src) * scale) over src
+    [m, n] int32 (PER_TOKEN / PER_GROUP: int32 or f32).  PER_TENSOR: scale_scalar; PER_CHANNEL: scale [n] (f32, bf16,
+    or int64 holding uint64 words)."""
+    m, n = src.shape
+    src_type = {torch.int32: INT32, torch.float32: F32}[src.dtype]
+    if scale_type is None:
+        scale_type = F32 if scale is None else {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16,
+                                                torch.int64: U64}[scale.dtype]
+    y = out if out is not None else torch.empty((m, n), dtype=dst_dtype, device=src.device)
+    p = _QuantizeParam(policy, 0, ROUND_RINT, kdim, m, n, group_size)
+    check(lib().ascq_dequantize(_ptr(y), _FLOAT_CODE[dst_dtype], _ptr(src), src_type, _ptr(scale), float(scale_scalar),
+                                scale_type, ctypes.byref(p), _stream(stream)), "dequantize")
+    return y
+
+
+def antiquantize(src: torch.Tensor, src_type: int, policy: int, m: int, n: int, dst_dtype=torch.float16, scale=None,
+                 offset=None, scale_scalar: float = 1.0, offset_scalar=None, scale_type: int | None = None,
+                 group_size: int = 0, kdim: int = 1, out=None, stream=None):
+    """AntiQuantize<{policy, hasOffset, kDim}>(dst, src, scale, offset, {m, n, groupSize}): dst = (src + offset) *
+    scale in fp32, one cast, over [m, n] (int8 / hifloat8 / fp8 codes; fp4 [m, n / 2] bytes with E8M0 scales).
+    PER_TENSOR: scale_scalar / offset_scalar (values of dst_dtype); the other policies: `scale` / `offset` tensors."""
+    if scale_type is None:
+        scale_type = _FLOAT_CODE[dst_dtype] if scale is None else {torch.float32: F32, torch.float16: F16,
+                                                                   torch.bfloat16: BF16, torch.uint8: E8M0}[scale.dtype]
+    y = out if out is not None else torch.empty((m, n), dtype=dst_dtype, device=src.device)
+    has_off = offset is not None or offset_scalar is not None
+    p = _QuantizeParam(policy, int(has_off), ROUND_RINT, kdim, m, n, group_size)
+    check(lib().ascq_antiquantize(_ptr(y), _FLOAT_CODE[dst_dtype], _ptr(src), src_type, _ptr(scale), _ptr(offset),
+                                  float(scale_scalar), float(offset_scalar or 0.0), scale_type, ctypes.byref(p),
+                                  _stream(stream)), "antiquantize")
     return y
 
 

@@ -1167,6 +1167,174 @@ ascq_status ascq_ascend_antiquant_policy(void* dst, int32_t dst_type, const void
 }
 
 // ------------------------------------------------------------------------------------------------
+// Quantize / Dequantize / AntiQuantize (quantize.h, dequantize.h, antiquantize.h): the AscendQuant / AscendDequant /
+// AscendAntiQuant kernels with fp32 arithmetic (Quantize, AntiQuantize) and the newer interface's type rules
+// ------------------------------------------------------------------------------------------------
+namespace {
+
+bool valid_policy(int32_t p) { return p >= ASCQ_POLICY_PER_TENSOR && p <= ASCQ_POLICY_PER_GROUP; }
+
+// bits of v rounded (rne) to the 16-bit float type t (F16 / BF16)
+uint16_t half_bits_of(float v, int32_t t)
+{
+    if (t == ASCQ_DT_F16) {
+        const _Float16 h = (_Float16)v;
+        uint16_t b;
+        std::memcpy(&b, &h, 2);
+        return b;
+    }
+    uint32_t u;
+    std::memcpy(&u, &v, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // NaN stays NaN
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// one group covering every row: scale[r / g][c] is then scale[c] (PER_CHANNEL through the per-group kernels, whose
+// row blocks need a group size that is a multiple of 32)
+int64_t whole_column_group(uint32_t m) { return ((int64_t)(m > 0 ? m : 1) + 31) / 32 * 32; }
+
+}  // namespace
+
+ascq_status ascq_quantize(void* dst, int32_t dst_type, const void* src, int32_t src_type, const void* scale,
+                          const void* offset, float scale_scalar, float offset_scalar, int32_t scale_type,
+                          const ascq_quantize_param* p, void* stream)
+{
+    CallScope scope;
+    if (!p) return fail(ASCQ_E_INVALID_ARG, "quantize: null params");
+    if (!valid_policy(p->policy)) return fail(ASCQ_E_INVALID_ARG, "quantize: bad policy %d", p->policy);
+    const auto fp_type = [](int32_t t) { return t == ASCQ_DT_F16 || t == ASCQ_DT_BF16 || t == ASCQ_DT_F32; };
+    if (!fp_type(src_type)) return fail(ASCQ_E_UNSUPPORTED, "quantize: src must be f16, bf16 or f32");
+    // CheckApiDtypeValid (quantize_impl.h:33-61): (src, scale) = (f16, f16), (bf16, bf16), (f32, f32), (f16, f32),
+    // (bf16, f32)
+    if (!fp_type(scale_type) || (scale_type != ASCQ_DT_F32 && scale_type != src_type))
+        return fail(ASCQ_E_UNSUPPORTED, "quantize: the scale is f32 or of the source's type");
+    const bool fp4 = dst_type == ASCQ_DT_FP4_E2M1 || dst_type == ASCQ_DT_FP4_E1M2;
+    if (dst_type != ASCQ_DT_INT8 && dst_type != ASCQ_DT_HIF8 && dst_type != ASCQ_DT_FP8_E4M3 &&
+        dst_type != ASCQ_DT_FP8_E5M2 && !fp4)
+        return fail(ASCQ_E_UNSUPPORTED, "quantize: dst must be int8, hifloat8, fp8_e4m3, fp8_e5m2, fp4_e2m1 or fp4_e1m2");
+    if (fp4 && p->policy != ASCQ_POLICY_PER_GROUP)
+        return fail(ASCQ_E_UNSUPPORTED, "quantize: fp4 outputs are PER_GROUP only (quantize_impl.h:1021-1053)");
+    if (p->policy == ASCQ_POLICY_PER_GROUP) {
+        if (p->kdim != 0 && p->kdim != 1) return fail(ASCQ_E_INVALID_ARG, "quantize: kdim must be 0 or 1");
+        if (p->group_size == 0 || p->group_size % 32 != 0)
+            return fail(ASCQ_E_INVALID_ARG, "quantize: group_size must be a positive multiple of 32");
+    }
+    if (p->policy == ASCQ_POLICY_PER_TENSOR && (scale || offset))
+        return fail(ASCQ_E_INVALID_ARG, "quantize: PER_TENSOR takes scalar scale and offset (pass NULL tensors)");
+    if (!valid_round(p->round_mode)) return fail(ASCQ_E_INVALID_ARG, "quantize: bad round mode");
+    if (p->n % 32 != 0) return fail(ASCQ_E_INVALID_ARG, "quantize: params.n must be a multiple of 32");
+    if (p->m == 0 || p->n == 0) return ASCQ_OK;
+    if (!dst || !src || (p->policy != ASCQ_POLICY_PER_TENSOR && !scale))
+        return fail(ASCQ_E_INVALID_ARG, "quantize: null argument");
+    const bool scalar_layout = p->policy == ASCQ_POLICY_PER_TENSOR || p->policy == ASCQ_POLICY_PER_TOKEN;
+    const bool channel = p->policy == ASCQ_POLICY_PER_CHANNEL;
+    trace("quantize: policy %d, dst %d src %d scale %d, m %u n %u group %u kdim %d offset %d", p->policy, dst_type,
+          src_type, scale_type, p->m, p->n, p->group_size, p->kdim, p->has_offset);
+    return hip_status(ascq::launch_quant_policy(dst, dst_type, src, src_type, scale, scale_type, offset,
+                                                p->has_offset ? 1 : 0, offset_scalar, scalar_layout ? 1 : 0, p->m,
+                                                p->n, channel ? whole_column_group(p->m) : (int64_t)p->group_size,
+                                                channel ? 0 : p->kdim, p->round_mode, S(stream), scale_scalar, 1),
+                      "quantize");
+}
+
+ascq_status ascq_dequantize(void* dst, int32_t dst_type, const void* src, int32_t src_type, const void* scale,
+                            float scale_scalar, int32_t scale_type, const ascq_quantize_param* p, void* stream)
+{
+    CallScope scope;
+    if (!p) return fail(ASCQ_E_INVALID_ARG, "dequantize: null params");
+    if (!valid_policy(p->policy)) return fail(ASCQ_E_INVALID_ARG, "dequantize: bad policy %d", p->policy);
+    if (p->has_offset) return fail(ASCQ_E_UNSUPPORTED, "dequantize: offset is not supported (dequantize_impl.h:102)");
+    const int32_t s = scale_type, d = dst_type;
+    const bool legacy = p->policy == ASCQ_POLICY_PER_TENSOR || p->policy == ASCQ_POLICY_PER_CHANNEL;
+    // IsDataTypeValid (dequantize_impl.h:67-92)
+    bool ok;
+    if (p->policy == ASCQ_POLICY_PER_CHANNEL)
+        ok = (s == ASCQ_DT_U64 && d == ASCQ_DT_F16) || (s == ASCQ_DT_F32 && d == ASCQ_DT_F32) ||
+             (s == ASCQ_DT_BF16 && d == ASCQ_DT_F32) || (s == ASCQ_DT_BF16 && d == ASCQ_DT_BF16) ||
+             (s == ASCQ_DT_F32 && d == ASCQ_DT_BF16);
+    else if (p->policy == ASCQ_POLICY_PER_TENSOR)
+        ok = (s == ASCQ_DT_BF16 || s == ASCQ_DT_F32) && (d == ASCQ_DT_BF16 || d == ASCQ_DT_F32);
+    else
+        ok = (s == ASCQ_DT_F16 && d == ASCQ_DT_F16) || (s == ASCQ_DT_BF16 && d == ASCQ_DT_BF16) ||
+             (s == ASCQ_DT_F32 && (d == ASCQ_DT_F32 || d == ASCQ_DT_F16 || d == ASCQ_DT_BF16));
+    if (!ok) return fail(ASCQ_E_UNSUPPORTED, "dequantize: scale type %d with dst type %d is not accepted", s, d);
+    if (src_type != ASCQ_DT_INT32 && (legacy || src_type != ASCQ_DT_F32))
+        return fail(ASCQ_E_UNSUPPORTED, "dequantize: src must be int32 (PER_TOKEN / PER_GROUP: int32 or f32)");
+    const uint32_t dsz = d == ASCQ_DT_F32 ? 4 : 2;
+    if ((p->n * 4u) % 32 != 0 || (p->n * dsz) % 32 != 0)
+        return fail(ASCQ_E_INVALID_ARG, "dequantize: rows of src and dst must be whole 32-byte blocks");
+    if (p->m == 0 || p->n == 0) return ASCQ_OK;
+    if (p->policy == ASCQ_POLICY_PER_GROUP) {
+        if (p->kdim != 0 && p->kdim != 1) return fail(ASCQ_E_INVALID_ARG, "dequantize: kdim must be 0 or 1");
+        if (p->group_size == 0 || p->group_size % 32 != 0)
+            return fail(ASCQ_E_INVALID_ARG, "dequantize: group_size must be a positive multiple of 32");
+    }
+    if ((uint64_t)p->m * p->n >= (1ull << 32)) return fail(ASCQ_E_UNSUPPORTED, "dequantize: tensor too large");
+    if (legacy) {
+        const ascq_dequant_param dp{p->m, p->n, p->n};
+        return ascq_ascend_dequant(dst, dst_type, src, src_type, scale, scale_type, scale_scalar, p->policy,
+                                   ASCQ_DEQUANT_MULTI_ROW, &dp, stream);
+    }
+    const ascq_dequant_policy_param pp{p->m, p->n, p->m * p->n, p->group_size, 0, p->kdim};
+    return ascq_ascend_dequant_policy(dst, dst_type, src, src_type, scale, nullptr, scale_type, p->policy, &pp, stream);
+}
+
+ascq_status ascq_antiquantize(void* dst, int32_t dst_type, const void* src, int32_t src_type, const void* scale,
+                              const void* offset, float scale_scalar, float offset_scalar, int32_t scale_type,
+                              const ascq_quantize_param* p, void* stream)
+{
+    CallScope scope;
+    if (!p) return fail(ASCQ_E_INVALID_ARG, "antiquantize: null params");
+    if (!valid_policy(p->policy)) return fail(ASCQ_E_INVALID_ARG, "antiquantize: bad policy %d", p->policy);
+    const bool b8 = src_type == ASCQ_DT_INT8 || src_type == ASCQ_DT_HIF8 || src_type == ASCQ_DT_FP8_E4M3 ||
+                    src_type == ASCQ_DT_FP8_E5M2;
+    const bool fp4 = src_type == ASCQ_DT_FP4_E2M1 || src_type == ASCQ_DT_FP4_E1M2;
+    const int32_t s = scale_type, d = dst_type;
+    if (p->policy == ASCQ_POLICY_PER_TENSOR || p->policy == ASCQ_POLICY_PER_CHANNEL) {
+        if (!b8) return fail(ASCQ_E_UNSUPPORTED, "antiquantize: src must be int8, hifloat8, fp8_e4m3 or fp8_e5m2");
+        if (!((s == ASCQ_DT_F16 && d == ASCQ_DT_F16) || (s == ASCQ_DT_BF16 && d == ASCQ_DT_BF16)))
+            return fail(ASCQ_E_UNSUPPORTED, "antiquantize: PER_TENSOR / PER_CHANNEL take f16 or bf16 scales of the dst type");
+    } else if (fp4) {
+        if (p->policy != ASCQ_POLICY_PER_GROUP || s != ASCQ_DT_E8M0 || (d != ASCQ_DT_F16 && d != ASCQ_DT_BF16))
+            return fail(ASCQ_E_UNSUPPORTED, "antiquantize: fp4 takes PER_GROUP E8M0 scales and f16 / bf16 dst");
+        if (p->has_offset) return fail(ASCQ_E_UNSUPPORTED, "antiquantize: fp4 takes no offset (antiquantize_impl.h:191)");
+        if (p->n % 64 != 0) return fail(ASCQ_E_INVALID_ARG, "antiquantize: fp4 rows must be a multiple of 64");
+    } else {
+        if (!b8) return fail(ASCQ_E_UNSUPPORTED, "antiquantize: src must be int8, hifloat8, fp8 or fp4");
+        const bool ok = (s == ASCQ_DT_F16 && d == ASCQ_DT_F16) || (s == ASCQ_DT_BF16 && d == ASCQ_DT_BF16) ||
+                        (s == ASCQ_DT_F32 && (d == ASCQ_DT_F32 || d == ASCQ_DT_F16 || d == ASCQ_DT_BF16));
+        if (!ok) return fail(ASCQ_E_UNSUPPORTED, "antiquantize: scale type %d with dst type %d is not accepted", s, d);
+    }
+    if (p->policy == ASCQ_POLICY_PER_GROUP) {
+        if (p->kdim != 0 && p->kdim != 1) return fail(ASCQ_E_INVALID_ARG, "antiquantize: kdim must be 0 or 1");
+        if (p->group_size == 0 || p->group_size % 32 != 0)
+            return fail(ASCQ_E_INVALID_ARG, "antiquantize: group_size must be a positive multiple of 32");
+    }
+    if (b8 && p->n % 32 != 0) return fail(ASCQ_E_INVALID_ARG, "antiquantize: rows must be whole 32-byte blocks");
+    if (p->policy == ASCQ_POLICY_PER_TENSOR && (scale || offset))
+        return fail(ASCQ_E_INVALID_ARG, "antiquantize: PER_TENSOR takes scalar scale and offset (pass NULL tensors)");
+    if (p->policy != ASCQ_POLICY_PER_TENSOR && p->has_offset && !offset)
+        return fail(ASCQ_E_INVALID_ARG, "antiquantize: has_offset needs an offset tensor");
+    if (p->m == 0 || p->n == 0) return ASCQ_OK;
+    if (!dst || !src || (p->policy != ASCQ_POLICY_PER_TENSOR && !scale))
+        return fail(ASCQ_E_INVALID_ARG, "antiquantize: null argument");
+    trace("antiquantize: policy %d, dst %d src %d scale %d, m %u n %u group %u kdim %d offset %d", p->policy, d,
+          src_type, s, p->m, p->n, p->group_size, p->kdim, p->has_offset);
+    if (p->policy == ASCQ_POLICY_PER_TENSOR)
+        return hip_status(ascq::launch_antiquant_scalar(dst, d, src, src_type, half_bits_of(offset_scalar, s),
+                                                        half_bits_of(scale_scalar, s), p->has_offset ? 1 : 0,
+                                                        (int64_t)p->m * p->n, S(stream), 1),
+                          "antiquantize");
+    const bool channel = p->policy == ASCQ_POLICY_PER_CHANNEL;
+    const int col_groups = p->policy == ASCQ_POLICY_PER_GROUP && p->kdim == 1;
+    return hip_status(ascq::launch_antiquant_policy(dst, d, src, src_type, scale, p->has_offset ? offset : nullptr, s,
+                                                    p->policy == ASCQ_POLICY_PER_TOKEN ? 1 : 0, p->m, p->n,
+                                                    channel ? whole_column_group(p->m) : (int64_t)p->group_size,
+                                                    col_groups, 0, S(stream), 1),
+                      "antiquantize");
+}
+
+// ------------------------------------------------------------------------------------------------
 // weight-only antiquant matmul
 // ------------------------------------------------------------------------------------------------
 ascq_status ascq_weight_pack_size(int32_t w_type, int64_t k, int64_t n, size_t* bytes)

@@ -71,18 +71,23 @@ hipError_t launch_quant_legacy(void* q, int dst_type, const void* x, int src_typ
 hipError_t launch_dequant(void* y, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
                           float scale_scalar, int smode, uint32_t rows, uint32_t cols, uint32_t n, uint32_t ldd,
                           uint32_t group, hipStream_t st);
+// f32_arith: int8 / hifloat8 sources in fp32 whatever the scale type (the AntiQuantize form)
 hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale,
                                    const void* offset, int scale_type, int per_token, int64_t m, int64_t n,
-                                   int64_t g, int col_groups, int is_transpose, hipStream_t st);
+                                   int64_t g, int col_groups, int is_transpose, hipStream_t st, int f32_arith = 0);
 hipError_t launch_antiquant(void* dst, int dst_type, const void* src, int src_type, const void* offset,
                             const void* scale, uint32_t K, uint32_t N, uint32_t g, int is_transpose, int arith,
                             hipStream_t st);
 // AscendAntiQuant per tensor: dst[i] = (src[i] + offset) * scale with offset / scale the output type's bits
+// f32_arith: fp32 arithmetic and one cast whatever the types (the AntiQuantize form)
 hipError_t launch_antiquant_scalar(void* dst, int dst_type, const void* src, int src_type, uint16_t offset,
-                                   uint16_t scale, int has_offset, int64_t count, hipStream_t st);
+                                   uint16_t scale, int has_offset, int64_t count, hipStream_t st, int f32_arith = 0);
+// AscendQuant policy form; scale == null takes scale_scalar for every element (per_token layout, the Quantize
+// form's PER_TENSOR); f32_arith: fp32 arithmetic whatever the scale type (the Quantize form)
 hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale,
                                int scale_type, const void* offset, int has_offset, float offset_scalar, int per_token,
-                               int64_t m, int64_t n, int64_t g, int k_dim, int round_mode, hipStream_t st);
+                               int64_t m, int64_t n, int64_t g, int k_dim, int round_mode, hipStream_t st,
+                               float scale_scalar = 0.0f, int f32_arith = 0);
 
 // gemm_i8.hip
 enum : int { EPI_I32 = 0, EPI_DEQ_F16 = 1, EPI_DEQ_BF16 = 2, EPI_REQ8 = 3, EPI_REQ4 = 4 };

@@ -276,9 +276,9 @@ __global__ __launch_bounds__(256) void antiquant_kernel(void* __restrict__ dst, 
 // per tensor, any count or alignment
 __global__ __launch_bounds__(256) void antiquant_scalar_elem_kernel(void* __restrict__ dst, int dst_type,
                                                                     const void* __restrict__ src, int src_type,
-                                                                    float of, float sc, int has_off, int64_t count)
+                                                                    float of, float sc, int has_off, int64_t count,
+                                                                    int ar)
 {
-    const int ar = aq_arith(src_type, dst_type, 0, 1, dst_type == DT_F16 ? 0 : 1);
     for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < count; t += (int64_t)gridDim.x * 256)
         aq_elem(dst, dst_type, t, aq_src_value(src, src_type, t), has_off != 0, of, sc, ar);
 }
@@ -411,6 +411,7 @@ struct QuantPolicyArgs {
     const void* scale;
     const void* offset;  // tensor indexed like scale, or null
     float off_scalar;    // used when has_off and offset is null (already a scaleT value)
+    float sc_scalar;     // used when scale is null (PER_TENSOR; already a scaleT value)
     int has_off;         // 0 for E2M1, which takes no offset
     int src_type, scale_type, round_mode, layout;
     int64_t m, n, g, sk;
@@ -582,12 +583,14 @@ __device__ __forceinline__ uint32_t fp4_codes8(const float (&f)[8], float s)
     return fp4_pk_f32<3>(w, f[6] * s, f[7] * s);
 }
 
-template <int DST, int SRC, int SC, int MODE, bool KROW>
+// FA: fp32 arithmetic whatever the scale type (the Quantize form: scale and offset widened exactly, one fp32 multiply
+// and one fp32 add); otherwise fp32 for fp8 outputs and the scale type's arithmetic for the others (AscendQuant)
+template <int DST, int SRC, int SC, int MODE, bool KROW, bool FA = false>
 __device__ __forceinline__ void quant_unit(const QuantPolicyArgs& a, uint32_t u, const Raw8<SRC>& xr,
                                            const Raw8<SC>& sr, Raw8<SC> orw, bool off_tensor, uint32_t osc)
 {
     constexpr bool FP8 = DST == QD_E4M3 || DST == QD_E5M2;
-    constexpr int T = FP8 ? DT_F32 : SC;
+    constexpr int T = (FP8 || FA) ? DT_F32 : SC;
     constexpr bool HALF = T == DT_F16;  // then SRC == SC == f16
     if (!off_tensor) {  // scalar offset (or none): broadcast it like a per-unit scale
         if constexpr (KROW) {
@@ -737,12 +740,15 @@ __device__ __forceinline__ uint32_t offset_scalar_bits(float o)
     else return (uint32_t)h_bits((_Float16)o);                          // already a half value
 }
 
-template <int DST, int SRC, int SC, int MODE>
+// scale == null: the scalar sc_scalar for every element (PER_TENSOR)
+template <int DST, int SRC, int SC, int MODE, bool FA = false>
 __global__ __launch_bounds__(256) void quant_policy_vec_kernel(QuantPolicyArgs a)  // scales along the row
 {
-    const void* offp = a.offset ? a.offset : a.scale;
+    const bool sc_tensor = a.scale != nullptr;
+    const void* scp = sc_tensor ? a.scale : a.src;  // (never read without a scale tensor)
+    const void* offp = a.offset ? a.offset : scp;
     const bool off_tensor = a.offset != nullptr;
-    const uint32_t osc = offset_scalar_bits<SC>(a.off_scalar);
+    const uint32_t osc = offset_scalar_bits<SC>(a.off_scalar), ssc = offset_scalar_bits<SC>(a.sc_scalar);
     for (uint32_t b0 = blockIdx.x * (256u * QP_UNR); b0 < a.units; b0 += gridDim.x * (256u * QP_UNR)) {
         Raw8<SRC> xr[QP_UNR];
         Raw8<SC> sr[QP_UNR], orw[QP_UNR];  // one scale / offset each, in w[0]
@@ -753,7 +759,7 @@ __global__ __launch_bounds__(256) void quant_policy_vec_kernel(QuantPolicyArgs a
             load_raw8<SRC>(a.src, u, xr[k]);
             const uint32_t r = fdiv(u, a.upr_div), c = (u - r * a.upr) * 8u;
             const int64_t si = (int64_t)r * a.sk + fdiv(c, a.g_div);
-            sr[k].w[0] = load_raw1<SC>(a.scale, si);
+            sr[k].w[0] = sc_tensor ? load_raw1<SC>(scp, si) : ssc;
             // without an offset tensor quant_unit takes the scalar offset: no load (the fp4 outputs, which write a
             // quarter of what they read, ran 11-12 % faster for it)
             orw[k].w[0] = off_tensor ? load_raw1<SC>(offp, si) : 0u;
@@ -762,12 +768,12 @@ __global__ __launch_bounds__(256) void quant_policy_vec_kernel(QuantPolicyArgs a
         for (int k = 0; k < QP_UNR; ++k) {
             const uint32_t u = b0 + k * 256u + threadIdx.x;
             if (u >= a.units) break;
-            quant_unit<DST, SRC, SC, MODE, false>(a, u, xr[k], sr[k], orw[k], off_tensor, osc);
+            quant_unit<DST, SRC, SC, MODE, false, FA>(a, u, xr[k], sr[k], orw[k], off_tensor, osc);
         }
     }
 }
 
-template <int DST, int SRC, int SC, int MODE>
+template <int DST, int SRC, int SC, int MODE, bool FA = false>
 __global__ __launch_bounds__(256) void quant_policy_vec_krow_kernel(QuantPolicyArgs a)  // groups down the columns
 {
     const void* offp = a.offset ? a.offset : a.scale;
@@ -789,7 +795,7 @@ __global__ __launch_bounds__(256) void quant_policy_vec_krow_kernel(QuantPolicyA
 #pragma unroll
         for (int k = 0; k < QP_UNR; ++k) {
             if (r0 + k >= rows) break;
-            quant_unit<DST, SRC, SC, MODE, true>(a, (r0 + k) * a.upr + wu, xr[k], sr, orw, off_tensor, osc);
+            quant_unit<DST, SRC, SC, MODE, true, FA>(a, (r0 + k) * a.upr + wu, xr[k], sr, orw, off_tensor, osc);
         }
     }
 }
@@ -1188,7 +1194,7 @@ __global__ __launch_bounds__(256) void quant_policy_generic_kernel(QuantPolicyAr
             const int64_t si = a.layout == QL_TOKEN ? r : (a.layout == QL_KCOL ? r * a.sk + c / a.g
                                                                                 : (r / a.g) * a.n + c);
             const float x = load_scale_t(a.src, a.src_type, e);
-            const float s = load_scale_t(a.scale, a.scale_type, si);
+            const float s = a.scale ? load_scale_t(a.scale, a.scale_type, si) : a.sc_scalar;
             float v = mul_t<T>(x, s);
             if (a.has_off) v = add_t<T>(v, a.offset ? load_scale_t(a.offset, a.scale_type, si) : a.off_scalar);
             w |= quant_code_rt<DST, T>(v, a.round_mode) << (4 * h);
@@ -1197,29 +1203,29 @@ __global__ __launch_bounds__(256) void quant_policy_generic_kernel(QuantPolicyAr
     }
 }
 
-template <int DST, int SRC, int SC, int MODE>
+template <int DST, int SRC, int SC, int MODE, bool FA>
 static void launch_qp_layout(const QuantPolicyArgs& a, hipStream_t st)
 {
     if (a.layout == QL_KROW)
-        launch_k(quant_policy_vec_krow_kernel<DST, SRC, SC, MODE>, dim3(grid_for(a.units)), dim3(256), 0, st, a);
+        launch_k(quant_policy_vec_krow_kernel<DST, SRC, SC, MODE, FA>, dim3(grid_for(a.units)), dim3(256), 0, st, a);
     else
-        launch_k(quant_policy_vec_kernel<DST, SRC, SC, MODE>, dim3(grid_for((a.units + QP_UNR - 1) / QP_UNR)),
+        launch_k(quant_policy_vec_kernel<DST, SRC, SC, MODE, FA>, dim3(grid_for((a.units + QP_UNR - 1) / QP_UNR)),
                  dim3(256), 0, st, a);
 }
 
-template <int DST, int SRC, int SC>
+template <int DST, int SRC, int SC, bool FA = false>
 static void launch_qp_vec(const QuantPolicyArgs& a, hipStream_t st)
 {
     if constexpr (DST == QD_E4M3 || DST == QD_E5M2 || DST == QD_HIF8) {  // one rounding whatever the mode
-        launch_qp_layout<DST, SRC, SC, RM_RINT>(a, st);
+        launch_qp_layout<DST, SRC, SC, RM_RINT, FA>(a, st);
         return;
     }
     switch (a.round_mode) {
-    case RM_FLOOR: launch_qp_layout<DST, SRC, SC, RM_FLOOR>(a, st); break;
-    case RM_CEIL: launch_qp_layout<DST, SRC, SC, RM_CEIL>(a, st); break;
-    case RM_ROUND: launch_qp_layout<DST, SRC, SC, RM_ROUND>(a, st); break;
-    case RM_TRUNC: launch_qp_layout<DST, SRC, SC, RM_TRUNC>(a, st); break;
-    default: launch_qp_layout<DST, SRC, SC, RM_RINT>(a, st); break;
+    case RM_FLOOR: launch_qp_layout<DST, SRC, SC, RM_FLOOR, FA>(a, st); break;
+    case RM_CEIL: launch_qp_layout<DST, SRC, SC, RM_CEIL, FA>(a, st); break;
+    case RM_ROUND: launch_qp_layout<DST, SRC, SC, RM_ROUND, FA>(a, st); break;
+    case RM_TRUNC: launch_qp_layout<DST, SRC, SC, RM_TRUNC, FA>(a, st); break;
+    default: launch_qp_layout<DST, SRC, SC, RM_RINT, FA>(a, st); break;
     }
 }
 
@@ -1232,7 +1238,8 @@ static void launch_qp_src(const QuantPolicyArgs& a, hipStream_t st)
 }
 
 // T: arithmetic type -- the scale type for int8 / E2M1, which pair it with a source of the same type or an f32
-// scale; fp32 for fp8, which takes any source and scale type
+// scale; fp32 for fp8, which takes any source and scale type, and for the Quantize form (a 16-bit scale then meets a
+// source of its own type and is widened)
 template <int DST, int T>
 static void launch_qp(const QuantPolicyArgs& a, bool vec, hipStream_t st)
 {
@@ -1250,6 +1257,10 @@ static void launch_qp(const QuantPolicyArgs& a, bool vec, hipStream_t st)
         launch_qp_vec<DST, DT_F16, DT_F16>(a, st);
     } else if constexpr (T == DT_BF16) {
         launch_qp_vec<DST, DT_BF16, DT_BF16>(a, st);
+    } else if (a.scale_type == DT_F16) {
+        launch_qp_vec<DST, DT_F16, DT_F16, true>(a, st);
+    } else if (a.scale_type == DT_BF16) {
+        launch_qp_vec<DST, DT_BF16, DT_BF16, true>(a, st);
     } else {
         launch_qp_src<DST, DT_F32>(a, st);
     }
@@ -1257,7 +1268,8 @@ static void launch_qp(const QuantPolicyArgs& a, bool vec, hipStream_t st)
 
 hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale,
                                int scale_type, const void* offset, int has_offset, float offset_scalar, int per_token,
-                               int64_t m, int64_t n, int64_t g, int k_dim, int round_mode, hipStream_t st)
+                               int64_t m, int64_t n, int64_t g, int k_dim, int round_mode, hipStream_t st,
+                               float scale_scalar, int f32_arith)
 {
     const int dk = dst_type == DT_INT8 ? QD_INT8
                    : dst_type == DT_HIF8 ? QD_HIF8
@@ -1270,16 +1282,18 @@ hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src
     a.scale = scale;
     a.has_off = has_offset && !qd_nibble(dk);
     a.offset = a.has_off ? offset : nullptr;
-    // the scalar offset is a scaleT value: round it (rne) to the scale type once, here
-    float os = offset_scalar;
-    if (scale_type == DT_F16) {
-        os = (float)(_Float16)os;
-    } else if (scale_type == DT_BF16) {
-        uint32_t u = __builtin_bit_cast(uint32_t, os);
-        if ((u & 0x7fffffffu) <= 0x7f800000u) u = ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16) << 16;
-        os = __builtin_bit_cast(float, u);
-    }
-    a.off_scalar = os;
+    // the scalar offset (and a scalar scale) are scaleT values: round them (rne) to the scale type once, here
+    auto to_scale_type = [&](float v) {
+        if (scale_type == DT_F16) return (float)(_Float16)v;
+        if (scale_type == DT_BF16) {
+            uint32_t u = __builtin_bit_cast(uint32_t, v);
+            if ((u & 0x7fffffffu) <= 0x7f800000u) u = ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16) << 16;
+            return __builtin_bit_cast(float, u);
+        }
+        return v;
+    };
+    a.off_scalar = to_scale_type(offset_scalar);
+    a.sc_scalar = to_scale_type(scale_scalar);
     a.src_type = src_type;
     a.scale_type = scale_type;
     a.round_mode = round_mode;
@@ -1291,7 +1305,8 @@ hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src
     // vector kernels: units of 8 elements; for groups down the columns, blocks of QP_UNR rows x (n / 8) units
     const int64_t units = a.layout == QL_KROW ? (m + QP_UNR - 1) / QP_UNR * (n / 8) : m * n / 8;
     const bool al = (uintptr_t)src % 16 == 0 && (uintptr_t)dst % (qd_nibble(dk) ? 4 : 8) == 0 &&
-                    (a.layout != QL_KROW || ((uintptr_t)scale % 16 == 0 && (uintptr_t)a.offset % 16 == 0));
+                    (a.layout != QL_KROW || ((uintptr_t)scale % 16 == 0 && (uintptr_t)a.offset % 16 == 0)) &&
+                    (scale != nullptr || a.layout == QL_TOKEN);
     const bool vec = n % 8 == 0 && al && m * n / 8 < (1ll << 31) && a.g < (1ll << 31) && n < (1ll << 31);
     a.units = vec ? (uint32_t)units : 0u;
     a.upr = vec ? (uint32_t)(n / 8) : 1u;
@@ -1302,7 +1317,7 @@ hipError_t launch_quant_policy(void* dst, int dst_type, const void* src, int src
     } else {
         a.g_div = fast_div((uint32_t)(vec ? a.g : 1));
     }
-    const int t = (dk == QD_E4M3 || dk == QD_E5M2) ? DT_F32 : scale_type;  // arithmetic type
+    const int t = (dk == QD_E4M3 || dk == QD_E5M2 || f32_arith) ? DT_F32 : scale_type;  // arithmetic type
     if (dk == QD_E4M3) launch_qp<QD_E4M3, DT_F32>(a, vec, st);
     else if (dk == QD_E5M2) launch_qp<QD_E5M2, DT_F32>(a, vec, st);
     else if (dk == QD_INT8) {
@@ -1330,7 +1345,7 @@ __global__ __launch_bounds__(256) void antiquant_policy_kernel(void* __restrict_
                                                                const void* __restrict__ scale,
                                                                const void* __restrict__ offset, int scale_type,
                                                                int per_token, int64_t m, int64_t n, int64_t g,
-                                                               int col_groups, int is_transpose)
+                                                               int col_groups, int is_transpose, int f32_arith)
 {
     const int64_t total = m * n, sk = g > 0 ? (n + g - 1) / g : 1;
     for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
@@ -1358,11 +1373,13 @@ __global__ __launch_bounds__(256) void antiquant_policy_kernel(void* __restrict_
             continue;
         }
         const uint32_t code = ((const uint8_t*)src)[idx];
-        float v = src_type == DT_HIF8 ? hif8_to_f32(code) : (float)(int8_t)code;  // arithmetic in the scale type
-        if (offset) v = add_rt(v, o, scale_type);
-        v = mul_rt(v, s, scale_type);
-        if (scale_type == DT_F16) ((uint16_t*)dst)[idx] = f32_to_f16(v);
-        else if (scale_type == DT_BF16) ((uint16_t*)dst)[idx] = (uint16_t)(__float_as_uint(v) >> 16);
+        // arithmetic in the scale type (AscendAntiQuant), or in fp32 whatever the scale type (AntiQuantize)
+        const int ar = f32_arith ? DT_F32 : scale_type;
+        float v = src_type == DT_HIF8 ? hif8_to_f32(code) : (float)(int8_t)code;
+        if (offset) v = add_rt(v, o, ar);
+        v = mul_rt(v, s, ar);
+        if (ar == DT_F16) ((uint16_t*)dst)[idx] = f32_to_f16(v);
+        else if (ar == DT_BF16) ((uint16_t*)dst)[idx] = (uint16_t)(__float_as_uint(v) >> 16);
         else store_cast(dst, idx, v, dst_type);
     }
 }
@@ -1590,13 +1607,17 @@ static void launch_aq_dst(const AntiQuantVecArgs& a, int dst_type, bool eight, h
     else if constexpr (SRC != DT_FP4_E2M1 && SRC != DT_FP4_E1M2) launch_aq_vec<SRC, SC, DT_F32>(a, eight, st);
 }
 
+// fa: fp32 arithmetic for int8 / hifloat8 sources whatever the scale type (AntiQuantize), else the scale type's
 template <int SRC>
-static void launch_aq_scale(const AntiQuantVecArgs& a, int dst_type, int scale_type, bool eight, hipStream_t st)
+static void launch_aq_scale(const AntiQuantVecArgs& a, int dst_type, int scale_type, bool eight, hipStream_t st,
+                            bool fa)
 {
     if constexpr (SRC == DT_FP4_E2M1 || SRC == DT_FP4_E1M2) {
         launch_aq_dst<SRC, DT_E8M0>(a, dst_type, eight, st);
     } else if constexpr (SRC == DT_INT8 || SRC == DT_HIF8) {  // a 16-bit scale writes its own type
-        if (scale_type == DT_F16) launch_aq_vec<SRC, DT_F16, DT_F16>(a, eight, st);
+        if (scale_type == DT_F16 && fa) launch_aq_vec<SRC, DT_F16, DT_F16, DT_F32>(a, eight, st);
+        else if (scale_type == DT_BF16 && fa) launch_aq_vec<SRC, DT_BF16, DT_BF16, DT_F32>(a, eight, st);
+        else if (scale_type == DT_F16) launch_aq_vec<SRC, DT_F16, DT_F16>(a, eight, st);
         else if (scale_type == DT_BF16) launch_aq_vec<SRC, DT_BF16, DT_BF16>(a, eight, st);
         else launch_aq_dst<SRC, DT_F32>(a, dst_type, eight, st);
     } else {
@@ -1608,7 +1629,7 @@ static void launch_aq_scale(const AntiQuantVecArgs& a, int dst_type, int scale_t
 
 hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale,
                                    const void* offset, int scale_type, int per_token, int64_t m, int64_t n,
-                                   int64_t g, int col_groups, int is_transpose, hipStream_t st)
+                                   int64_t g, int col_groups, int is_transpose, hipStream_t st, int f32_arith)
 {
     // one scale per unit (groups along the row, PER_TOKEN by row) or 8 contiguous (groups down the columns,
     // PER_TOKEN by column); for the vector path the per-token cases become groups of n columns / m rows
@@ -1630,18 +1651,19 @@ hipError_t launch_antiquant_policy(void* dst, int dst_type, const void* src, int
         a.upr = (uint32_t)(n / 8);
         a.upr_div = fast_div(a.upr);
         a.g_div = fast_div((uint32_t)gv);
-        if (src_type == DT_INT8) launch_aq_scale<DT_INT8>(a, dst_type, scale_type, eight, st);
-        else if (src_type == DT_HIF8) launch_aq_scale<DT_HIF8>(a, dst_type, scale_type, eight, st);
-        else if (src_type == DT_FP8_E4M3) launch_aq_scale<DT_FP8_E4M3>(a, dst_type, scale_type, eight, st);
-        else if (src_type == DT_FP8_E5M2) launch_aq_scale<DT_FP8_E5M2>(a, dst_type, scale_type, eight, st);
-        else if (src_type == DT_FP4_E1M2) launch_aq_scale<DT_FP4_E1M2>(a, dst_type, scale_type, eight, st);
-        else launch_aq_scale<DT_FP4_E2M1>(a, dst_type, scale_type, eight, st);
+        const bool fa = f32_arith != 0;
+        if (src_type == DT_INT8) launch_aq_scale<DT_INT8>(a, dst_type, scale_type, eight, st, fa);
+        else if (src_type == DT_HIF8) launch_aq_scale<DT_HIF8>(a, dst_type, scale_type, eight, st, fa);
+        else if (src_type == DT_FP8_E4M3) launch_aq_scale<DT_FP8_E4M3>(a, dst_type, scale_type, eight, st, fa);
+        else if (src_type == DT_FP8_E5M2) launch_aq_scale<DT_FP8_E5M2>(a, dst_type, scale_type, eight, st, fa);
+        else if (src_type == DT_FP4_E1M2) launch_aq_scale<DT_FP4_E1M2>(a, dst_type, scale_type, eight, st, fa);
+        else launch_aq_scale<DT_FP4_E2M1>(a, dst_type, scale_type, eight, st, fa);
         return hipGetLastError();
     }
     log_fallback("antiquant_policy_kernel", "n, group or pointers not aligned to the vector unit");
     dim3 grid(grid_for(m * n)), block(256);
     launch_k(antiquant_policy_kernel, grid, block, 0, st, dst, dst_type, src, src_type, scale, offset, scale_type,
-             per_token, m, n, g, col_groups, is_transpose);
+             per_token, m, n, g, col_groups, is_transpose, f32_arith);
     return hipGetLastError();
 }
 
@@ -1706,10 +1728,11 @@ static void launch_aq_scalar_dst(const AntiQuantVecArgs& a, int dst_type, int ar
 }
 
 hipError_t launch_antiquant_scalar(void* dst, int dst_type, const void* src, int src_type, uint16_t offset,
-                                   uint16_t scale, int has_offset, int64_t count, hipStream_t st)
+                                   uint16_t scale, int has_offset, int64_t count, hipStream_t st, int f32_arith)
 {
     (void)hipGetLastError();
-    const int ar = aq_arith(src_type, dst_type, 0, 1, dst_type == DT_F16 ? 0 : 1);
+    // AscendAntiQuant's arithmetic, or fp32 with one cast whatever the types (AntiQuantize)
+    const int ar = f32_arith ? DT_F32 : aq_arith(src_type, dst_type, 0, 1, dst_type == DT_F16 ? 0 : 1);
     const int64_t sbytes = src_type == DT_INT4 ? 4 : 8;  // source bytes per 8 elements
     if (count % 8 == 0 && count / 8 < (1ll << 31) && (uintptr_t)src % sbytes == 0 && (uintptr_t)dst % 16 == 0) {
         AntiQuantVecArgs a{};
@@ -1727,7 +1750,7 @@ hipError_t launch_antiquant_scalar(void* dst, int dst_type, const void* src, int
     const float of = dst_type == DT_F16 ? (float)__builtin_bit_cast(_Float16, offset) : __builtin_bit_cast(float, (uint32_t)offset << 16);
     log_fallback("antiquant_scalar_elem_kernel", "count not a multiple of 8 or pointers not aligned");
     launch_k(antiquant_scalar_elem_kernel, dim3(grid_for(count)), dim3(256), 0, st, dst, dst_type, src, src_type, of, sc,
-             has_offset, count);
+             has_offset, count, ar);
     return hipGetLastError();
 }
 

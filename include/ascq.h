@@ -434,6 +434,79 @@ ascq_status ascq_ascend_antiquant_policy(void* dst, int32_t dst_type, const void
                                          void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * Quantize / Dequantize / AntiQuantize: the newer interface of include/adv_api/quantization/quantize.h:55-94,
+ * dequantize.h:59-95 and antiquantize.h:61-98, on the kernels of the AscendQuant / AscendDequant / AscendAntiQuant
+ * entry points above.  Tensors are [m, n] row-major; n is the element count of a row.
+ * ------------------------------------------------------------------------------------------ */
+/* QuantizeConfig{policy, hasOffset, roundMode, kDim} + QuantizeParams{m, n, groupSize}
+ * (include/adv_api/quantization/quantize_utils.h:32-46); DequantizeConfig / AntiQuantizeConfig and their params carry
+ * the same fields without roundMode (impl/adv_api/detail/quantization/dequantize/dequantize_common.h:27-44,
+ * antiquantize/antiquantize_common.h:27-44) -- round_mode is read by ascq_quantize only. */
+typedef struct {
+    int32_t policy;     /* ascq_policy */
+    int32_t has_offset;
+    int32_t round_mode; /* ascq_round_mode */
+    int32_t kdim;
+    uint32_t m;
+    uint32_t n;
+    uint32_t group_size;
+} ascq_quantize_param;
+
+/* Quantize<config>(dst, src, scale, offset, params) (quantize.h:55-63; impl impl/adv_api/detail/quantization/
+ * quantize/quantize_impl.h:1006-1066).  Every policy computes in fp32: y = f32(x) * f32(s), then + f32(o) when
+ * has_offset (one fp32 rounding each; QuantizePerGroupForKColCommonVF :361-364, the other policies alike), and casts
+ * y to dst_type:
+ *   INT8: clamp(round_mode(y), -128, 127), NaN -> 0 (TransRegForS8 :128-190; modes other than rint / round / floor /
+ *         ceil / trunc are rint);
+ *   FP8_E4M3 / FP8_E5M2: rint with saturation, NaN -> 0 (TransRegForFp8 :80-90);
+ *   HIF8: ties away from zero, saturating at +-32768, NaN -> 0 (TransRegForHif8 :92-126);
+ *   FP4_E2M1 / FP4_E1M2 (PER_GROUP only, no offset, n even): y rounded to bf16 (rne, saturating, NaN -> 0), then
+ *         the fp4 code in round_mode (TransRegForFp4 :192-230); two codes a byte, even element in the low nibble.
+ * Scale (and offset) of element (r, c), by policy (:701-966, 446-700):
+ *   PER_TENSOR: the scalars scale_scalar / offset_scalar (scale and offset must be NULL);
+ *   PER_CHANNEL: scale[c] ([n]);  PER_TOKEN: scale[r] ([m]);
+ *   PER_GROUP: kdim 1: scale[r][c / group] ([m][ceil(n / group)]); kdim 0: scale[r / group][c]
+ *              ([ceil(m / group)][n]); group_size a positive multiple of 32.
+ *   offset: a tensor indexed like scale, or (offset NULL, has_offset) the scalar offset_scalar.  Scalars are values
+ *   of scale_type (rounded rne to it).
+ * (src_type, scale_type) as CheckApiDtypeValid allows (:33-61): (F16, F16), (BF16, BF16), (F32, F32), (F16, F32),
+ * (BF16, F32).  params.n must be a multiple of 32 (quantize_impl.h:1020).  dst holds m * n bytes (fp4: m * n / 2). */
+ascq_status ascq_quantize(void* dst, int32_t dst_type, const void* src, int32_t src_type, const void* scale,
+                          const void* offset, float scale_scalar, float offset_scalar, int32_t scale_type,
+                          const ascq_quantize_param* params, void* stream);
+
+/* Dequantize<config>(dst, src, scale, offset, params) (dequantize.h:59-67; impl impl/adv_api/detail/quantization/
+ * dequantize/dequantize_impl.h:254-290), a dispatch onto AscendDequant (type pairs IsDataTypeValid :67-92):
+ *   PER_TENSOR: src INT32, the scalar scale_scalar (scale_type BF16 or F32; dst BF16 or F32) -- the legacy per-tensor
+ *     kernel with params {m, n, n} in DEQUANT_WITH_MULTI_ROW (:94-116);
+ *   PER_CHANNEL: src INT32, scale [n]: (U64, F16), (F32, F32), (BF16, F32), (BF16, BF16), (F32, BF16) -- the legacy
+ *     per-channel kernel, {m, n, n}, MULTI_ROW (:118-138);
+ *   PER_TOKEN / PER_GROUP: src INT32 or F32, scale [m] / as AscendDequant's policy form by kdim: (F16, F16),
+ *     (BF16, BF16), (F32, F32), (F32, F16), (F32, BF16) (:140-195).
+ * dst = cast(f32(src) * scale), int32 -> fp32 ties away from zero.  has_offset must be 0 (:102, 125, 148, 172: "do
+ * not support offset currently").  n * sizeof(src) and n * sizeof(dst) must be multiples of 32 bytes. */
+ascq_status ascq_dequantize(void* dst, int32_t dst_type, const void* src, int32_t src_type, const void* scale,
+                            float scale_scalar, int32_t scale_type, const ascq_quantize_param* params, void* stream);
+
+/* AntiQuantize<config>(dst, src, scale, offset, params) (antiquantize.h:61-69; impl impl/adv_api/detail/
+ * quantization/antiquantize/antiquantize_impl.h:284-302, antiquantize_3510_impl.h:38-396).  Every int8 / hifloat8 /
+ * fp8 policy computes in fp32: y = (f32(src) + f32(o)) * f32(s) (+ o only when has_offset), one cast to dst_type
+ * (rne, saturating; a plain store for F32):
+ *   PER_TENSOR: src INT8 / HIF8 / FP8_E4M3 / FP8_E5M2, scalars scale_scalar / offset_scalar of dst_type = scale_type
+ *     (F16 or BF16; rounded rne to it) (:76-102, 3510 :266-326);
+ *   PER_CHANNEL: the same sources, scale / offset [n] of dst_type = scale_type (F16 or BF16) (:104-129, 3510
+ *     :328-396);
+ *   PER_TOKEN: scale / offset [m] (:131-159);  PER_GROUP: kdim 1 [m][ceil(n / group)], kdim 0 [ceil(m / group)][n],
+ *     group_size a positive multiple of 32 (:161-226);  (scale_type, dst_type) for both: (F16, F16), (BF16, BF16),
+ *     (F32, F32), (F32, F16), (F32, BF16) (IsDataTypeValid :46-74);
+ *   PER_GROUP fp4: src FP4_E2M1 / FP4_E1M2 ([m, n / 2] bytes, n % 64 == 0), E8M0 scales, no offset, dst F16 or BF16:
+ *     bf16(src) * bf16(scale) rounded to bf16 (ascq_ascend_antiquant_policy's fp4 rule).
+ * n * sizeof(src) must be a multiple of 32 bytes (antiquantize_impl.h:99-100, 126-127, 153-154, 194). */
+ascq_status ascq_antiquantize(void* dst, int32_t dst_type, const void* src, int32_t src_type, const void* scale,
+                              const void* offset, float scale_scalar, float offset_scalar, int32_t scale_type,
+                              const ascq_quantize_param* params, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * Weight-only antiquant matmul (W8A16 / W4A16)
  * The reference composes AscendAntiQuant (per group) with a half Matmul (fp32 L0C, half out);
  * here one fused kernel dequantises B in registers and feeds fp16 MFMA.

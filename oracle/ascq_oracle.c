@@ -1046,6 +1046,122 @@ void oq_quant_policy(void* dst, int dst_type, const void* src, int src_type, con
     }
 }
 
+/* ------------------------------------------------------------------------ */
+/* Quantize / Dequantize / AntiQuantize (the newer interface, arch 3510)     */
+/* ------------------------------------------------------------------------ */
+
+/* scale / offset index of element (r, c) for the four policies of the newer interface; -1 = the scalar */
+static inline int64_t policy_index(int policy, int64_t r, int64_t c, int64_t n, int64_t group, int k_dim)
+{
+    const int64_t sk = group > 0 ? (n + group - 1) / group : 1;
+    switch (policy) {
+    case OQ_PER_TENSOR: return -1;
+    case OQ_PER_CHANNEL: return OQ_MUTANT == 40 ? r : c;
+    case OQ_PER_TOKEN: return r;
+    default: return k_dim == 1 ? r * sk + c / group : (r / group) * n + c;
+    }
+}
+
+/* Quantize<config>(dst, src, scale, offset, {m, n, groupSize}) (include/adv_api/quantization/quantize.h:55-94; impl
+ * impl/adv_api/detail/quantization/quantize/quantize_impl.h:1006-1066).  Every policy and output type computes in
+ * fp32: the source, the scale and the offset are widened exactly (GetPerGroupScaleToFloat :262-278,
+ * DuplicateScalarToFloatVector :280-294), y = x * s and then y + o are each one fp32 rounding (:361-364, 758-761,
+ * 855-858, 935-938), and CastFp32DstToExpect (:296-312) casts y:
+ *   int8: to int16 in round_mode with saturation, to half, to int8 with saturation (TransRegForS8 :128-190), i.e.
+ *         clamp(round_mode(y), -128, 127), NaN -> 0 (round modes other than rint / round / floor / ceil / trunc are
+ *         rint);
+ *   fp8: rint with saturation (TransRegForFp8 :80-90);  hifloat8: ties away from zero (TransRegForHif8 :92-126);
+ *   fp4 (PER_GROUP only, no offset: QuantizePerGroupForKColFp4VF :391-432): y to bf16 rne with saturation (NaN -> 0),
+ *         then the fp4 code in round_mode (TransRegForFp4 :192-230), two codes a byte, even element low.
+ * Scale index: PER_TENSOR the scalar scale_scalar, PER_CHANNEL c, PER_TOKEN r, PER_GROUP kDim 1 r * ceil(n / g) +
+ * c / g, kDim 0 (r / g) * n + c; the offset alike, or the scalar offset_scalar when there is no offset tensor.
+ * Scalars are scaleT values (rounded rne to scale_type). */
+void oq_quantize(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                 const void* offset, int has_offset, float scale_scalar, float offset_scalar, int policy, int64_t m,
+                 int64_t n, int64_t group, int k_dim, int round_mode)
+{
+    const int fp8 = dst_type == OQ_FP8_E4M3 || dst_type == OQ_FP8_E5M2;
+    const int fp4 = dst_type == OQ_FP4_E2M1 || dst_type == OQ_FP4_E1M2;
+    const int off = has_offset && !fp4;
+    const double ss = round_to((double)scale_scalar, scale_type);
+    const double os = round_to((double)offset_scalar, scale_type);
+    const int t = OQ_MUTANT == 41 ? scale_type : OQ_F32; /* arithmetic type (mutant: AscendQuant's scaleT) */
+    uint8_t* codes = fp4 ? (uint8_t*)malloc((size_t)(m * n) + 1) : NULL;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < m; ++r)
+        for (int64_t c = 0; c < n; ++c) {
+            const int64_t idx = r * n + c, si = policy_index(policy, r, c, n, group, k_dim);
+            const double x = load_as_f32(src, src_type, idx);
+            const double s = si < 0 ? ss : load_as_f32(scale, scale_type, si);
+            double v = round_to(x * s, t); /* x * s exact in double: two 24-bit significands */
+            if (off) v = round_to(v + ((offset && si >= 0) ? (double)load_as_f32(offset, scale_type, si) : os), t);
+            if (fp8) {
+                ((uint8_t*)dst)[idx] = oq_f32_to_fp8_sat((float)v, dst_type);
+            } else if (dst_type == OQ_HIF8) {
+                ((uint8_t*)dst)[idx] = oq_hif8_encode((float)v, 1);
+            } else if (fp4) {
+                const double b = v != v ? 0.0 : oq_bf16_to_f32(oq_f64_to_bf16(v, 1));
+                codes[idx] = dst_type == OQ_FP4_E1M2 ? oq_e1m2_encode(b, round_mode) : oq_e2m1_encode(b, round_mode);
+            } else {
+                ((int8_t*)dst)[idx] = oq_sat_s8(oq_round_to_int((float)v, round_mode));
+            }
+        }
+    if (fp4) {
+        for (int64_t i = 0; i < m * n; i += 2)
+            ((uint8_t*)dst)[i >> 1] = (uint8_t)(codes[i] | ((i + 1 < m * n ? codes[i + 1] : 0u) << 4));
+        free(codes);
+    }
+}
+
+/* Dequantize<config>(dst, src, scale, offset, {m, n, groupSize}) (include/adv_api/quantization/dequantize.h:59-95;
+ * impl impl/adv_api/detail/quantization/dequantize/dequantize_impl.h:254-290): PER_TENSOR / PER_CHANNEL are the legacy
+ * AscendDequant with params {m, n, n} in DEQUANT_WITH_MULTI_ROW (:94-138), PER_TOKEN / PER_GROUP the policy form with
+ * {m, n, m * n, groupSize} and the config's kDim (:140-195); no offset (:102). */
+void oq_dequantize(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                   float scale_scalar, int policy, int64_t m, int64_t n, int64_t group, int k_dim)
+{
+    if (policy == OQ_PER_TENSOR || policy == OQ_PER_CHANNEL) /* the scalar is a scaleT value */
+        oq_dequant_legacy(dst, dst_type, src, src_type, scale, scale_type, (float)round_to(scale_scalar, scale_type),
+                          policy == OQ_PER_TENSOR, OQ_DEQUANT_MULTI_ROW, m, n, n);
+    else
+        oq_dequant_policy(dst, dst_type, src, src_type, scale, scale_type, policy, k_dim, n, m * n, group);
+}
+
+/* AntiQuantize<config>(dst, src, scale, offset, {m, n, groupSize}) (include/adv_api/quantization/antiquantize.h:
+ * 61-98; impl impl/adv_api/detail/quantization/antiquantize/antiquantize_impl.h:284-322, antiquantize_3510_impl.h:
+ * 38-396).  int8 / hifloat8 / fp8 sources, every policy: fp32 throughout -- the source widened exactly (int8 and
+ * hifloat8 through half, CastAntiQuantizeSrcToFp32 :38-48), + offset then * scale, each one fp32 rounding, and one
+ * cast to dstT (rne with saturation; a plain store for fp32: StoreF32Res, PerTensorProcessCommon :266-300,
+ * PerChannelNoTransposeCommon :328-367, the per-token and per-group kernels :52-262).  Scale index: PER_TENSOR the
+ * scalar (a dstT value), PER_CHANNEL c, PER_TOKEN r, PER_GROUP by kDim (ForCol r * ceil(n / g) + c / g when kDim
+ * is 1, ForRow (r / g) * n + c when 0); the offset alike (PER_TENSOR: offset_scalar).  fp4 sources (PER_GROUP, E8M0
+ * scales, no offset) are the AscendAntiQuant policy form's fp4 rule (AntiQuantPerGroupForColFp4 / RowFp4,
+ * antiquantize_impl.h:201-225). */
+void oq_antiquantize(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                     const void* offset, int has_offset, float scale_scalar, float offset_scalar, int policy,
+                     int64_t m, int64_t n, int64_t group, int k_dim)
+{
+    if (src_type == OQ_FP4_E2M1 || src_type == OQ_FP4_E1M2) {
+        oq_antiquant_policy(dst, dst_type, src, src_type, scale, NULL, OQ_E8M0, OQ_PER_GROUP, m, n, group, k_dim, 0);
+        return;
+    }
+    const double ss = round_to((double)scale_scalar, scale_type);
+    const double os = round_to((double)offset_scalar, scale_type);
+    const int t = OQ_MUTANT == 42 ? scale_type : OQ_F32; /* arithmetic type (mutant: AscendAntiQuant's scaleT) */
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < m; ++r)
+        for (int64_t c = 0; c < n; ++c) {
+            const int64_t idx = r * n + c, si = policy_index(policy, r, c, n, group, k_dim);
+            const uint8_t code = ((const uint8_t*)src)[idx];
+            double v = src_type == OQ_HIF8 ? (double)oq_hif8_decode(code)
+                       : src_type == OQ_INT8 ? (double)(int8_t)code : (double)oq_fp8_decode(code, src_type);
+            const double s = si < 0 ? ss : load_as_f32(scale, scale_type, si);
+            if (has_offset) v = round_to(v + (si < 0 ? os : (double)load_as_f32(offset, scale_type, si)), t);
+            v = round_to(v * s, t);
+            store_from_f32(dst, dst_type, idx, (float)v);
+        }
+}
+
 /* Weight-only antiquant matmul (W8A16 / W4A16): the reference composes AscendAntiQuant (fp16 ops, above) with
  * a half x half Matmul whose L0C type is fp32 (GetMmDstType<half> = float, matmul_utils.h:171-174) and whose
  * fixpipe casts fp32 -> half with rint.  Products of two halves are exact; the restatement sums them in

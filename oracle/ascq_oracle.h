@@ -145,6 +145,20 @@ uint8_t oq_f32_to_fp8_sat(float x, int fmt);
 void oq_quant_policy(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
                      const void* offset, int has_offset, float offset_scalar, int policy, int64_t m, int64_t n,
                      int64_t group, int k_dim, int round_mode);
+/* Quantize (the newer interface): PER_TENSOR (scalar scale / offset), PER_CHANNEL, PER_TOKEN, PER_GROUP over [m, n]
+ * in fp32 arithmetic to int8 / fp8 / hifloat8 / fp4 (fp4 PER_GROUP only, packed [m, n/2]) */
+void oq_quantize(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                 const void* offset, int has_offset, float scale_scalar, float offset_scalar, int policy, int64_t m,
+                 int64_t n, int64_t group, int k_dim, int round_mode);
+/* Dequantize (the newer interface): PER_TENSOR / PER_CHANNEL through the legacy AscendDequant (MULTI_ROW, {m, n, n}),
+ * PER_TOKEN / PER_GROUP through the policy form; dst [m, n] */
+void oq_dequantize(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                   float scale_scalar, int policy, int64_t m, int64_t n, int64_t group, int k_dim);
+/* AntiQuantize (the newer interface): int8 / hifloat8 / fp8 sources in fp32 arithmetic for every policy (PER_TENSOR
+ * scalars of the dst type); fp4 sources as the AscendAntiQuant policy form */
+void oq_antiquantize(void* dst, int dst_type, const void* src, int src_type, const void* scale, int scale_type,
+                     const void* offset, int has_offset, float scale_scalar, float offset_scalar, int policy,
+                     int64_t m, int64_t n, int64_t group, int k_dim);
 /* weight-only antiquant matmul = AscendAntiQuant (fp16 ops) + fp16 matmul with fp32 accumulation.
  * Exact sum (double) -> f16; also returns the exact sum and sum |x*w| (for the accumulation bound) */
 void oq_antiquant_matmul(uint16_t* y, double* y_exact, double* y_absdot, const uint16_t* x, const void* w,

@@ -64,6 +64,16 @@ def quant_example():
     save("quant_example", f"{EX}/03_quantization/quant/scripts/gen_data.py:19-30", src=src, golden=golden)
 
 
+def quant_example_3510():
+    """03_quantization/quant/scripts/gen_data.py, the arch-3510 branch (float32 source), which quant.asc computes with
+    Quantize PER_TENSOR, scale 2.0, offset 0.9, CAST_RINT: golden = np.round(src * 2.0 + 0.9) as int8, float32
+    arithmetic."""
+    np.random.seed(1234)
+    src = np.random.uniform(low=-4, high=4, size=[1024]).astype(np.float32)
+    golden = np.round(src * 2.0 + 0.9).astype(np.int8)
+    save("quant_example_3510", f"{EX}/03_quantization/quant/scripts/gen_data.py:20-30", src=src, golden=golden)
+
+
 def dequant_example():
     """03_quantization/dequant/scripts/gen_data.py: int32 [128,32] in [-10,10), scale U(-100,100) [32],
     golden[j][i] = inp[j][i] * scale[i] as float32."""
@@ -220,7 +230,8 @@ def qf322b8_seed9():
          quant_word=np.array([word], np.uint64), golden=golden)
 
 
-ALL = ("deqf16_seed9", "matmul_quant_vector", "quant_example", "dequant_example", "antiquant_seed10",
+ALL = ("deqf16_seed9", "matmul_quant_vector", "quant_example", "quant_example_3510", "dequant_example",
+       "antiquant_seed10",
        "group_matmul_example", "mx_example", "req8_seed9", "qf322b8_seed9", "group_matmul_gelu_example")
 
 

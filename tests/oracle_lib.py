@@ -65,6 +65,13 @@ def lib() -> ctypes.CDLL:
             "oq_quant_policy": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int,
                                        ctypes.c_float, ctypes.c_int, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int]),
             "oq_requant4_f32": (None, [_P, _P, _I64, _I64, _P, ctypes.c_uint64]),
+            "oq_quantize": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int,
+                                   ctypes.c_float, ctypes.c_float, ctypes.c_int, _I64, _I64, _I64, ctypes.c_int,
+                                   ctypes.c_int]),
+            "oq_dequantize": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int, ctypes.c_float,
+                                     ctypes.c_int, _I64, _I64, _I64, ctypes.c_int]),
+            "oq_antiquantize": (None, [_P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int,
+                                       ctypes.c_float, ctypes.c_float, ctypes.c_int, _I64, _I64, _I64, ctypes.c_int]),
             "oq_matmul_i8": (None, [_P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int]),
             "oq_mm_dequant": (None, [_P, _P, ctypes.c_int, _I64, _I64, _P, ctypes.c_uint64]),
             "oq_matmul_fp8": (None, [_P, _P, ctypes.c_int, ctypes.c_int, _P, _P, ctypes.c_int, _I64, _I64, _I64,
@@ -212,6 +219,47 @@ def quant_policy(src, src_type, scale, scale_type, dst_type, policy, m, n, group
     lib().oq_quant_policy(_p(out), dst_type, _p(src), src_type, _p(sc), scale_type, _p(of), int(has_off),
                           float(offset_scalar or 0.0), policy, m, n, group, k_dim, round_mode)
     return out
+
+
+def quantize(src, src_type, dst_type, policy, m, n, scale=None, scale_type=F32, offset=None, scale_scalar=1.0,
+             offset_scalar=None, group=0, k_dim=1, round_mode=ROUND_RINT):
+    """Quantize (the newer interface) over [m, n]: src (uint16 bits or float32); scale / offset arrays of scale_type
+    (PER_TENSOR: the scalars); returns int8 [m, n], byte codes [m, n] or fp4 codes packed [m, n/2]"""
+    if dst_type in (FP4_E2M1, FP4_E1M2):
+        out = np.empty((m, n // 2), np.uint8)
+    else:
+        out = np.empty((m, n), np.int8 if dst_type == INT8 else np.uint8)
+    sc = None if scale is None else np.ascontiguousarray(scale)
+    of = None if offset is None else np.ascontiguousarray(offset)
+    has_off = offset is not None or offset_scalar is not None
+    lib().oq_quantize(_p(out), dst_type, _p(np.ascontiguousarray(src)), src_type, _p(sc), scale_type, _p(of),
+                      int(has_off), float(scale_scalar), float(offset_scalar or 0.0), policy, m, n, group, k_dim,
+                      round_mode)
+    return out
+
+
+def dequantize(src, src_type, dst_type, policy, scale=None, scale_type=F32, scale_scalar=1.0, group=0, k_dim=1):
+    """Dequantize (the newer interface) of src [m, n]; returns [m, n] (uint16 bits or float32)"""
+    src = np.ascontiguousarray(src)
+    m, n = src.shape
+    dst = np.zeros((m, n), np.float32 if dst_type == F32 else np.uint16)
+    sc = None if scale is None else np.ascontiguousarray(scale)
+    lib().oq_dequantize(_p(dst), dst_type, _p(src), src_type, _p(sc), scale_type, float(scale_scalar), policy, m, n,
+                        group, k_dim)
+    return dst
+
+
+def antiquantize(src, src_type, dst_type, policy, m, n, scale=None, scale_type=F16, offset=None, scale_scalar=1.0,
+                 offset_scalar=None, group=0, k_dim=1):
+    """AntiQuantize (the newer interface) over [m, n] (fp4: [m, n/2] bytes); returns [m, n] (uint16 bits or
+    float32)"""
+    dst = np.empty((m, n), np.float32 if dst_type == F32 else np.uint16)
+    sc = None if scale is None else np.ascontiguousarray(scale)
+    of = None if offset is None else np.ascontiguousarray(offset)
+    has_off = offset is not None or offset_scalar is not None
+    lib().oq_antiquantize(_p(dst), dst_type, _p(np.ascontiguousarray(src)), src_type, _p(sc), scale_type, _p(of),
+                          int(has_off), float(scale_scalar), float(offset_scalar or 0.0), policy, m, n, group, k_dim)
+    return dst
 
 
 def mm_requant4(acc, qvec=None, qscalar=0):

@@ -160,6 +160,51 @@ def test_dequant_antiquant_argument_checks():
     _err(L.ascq_ascend_antiquant(d, ascq.F32, d, ascq.INT8, d, d, 128, 8, 32, 0, 0, None), ascq.E_UNSUPPORTED)
 
 
+def test_quantize_interface_argument_checks():
+    """Quantize / Dequantize / AntiQuantize reject what the reference's static_asserts and asserts reject, before any
+    device work (quantize_impl.h:33-61, 1006-1066; dequantize_impl.h:67-195; antiquantize_impl.h:46-226)"""
+    L = ascq.lib()
+    d = ctypes.c_void_p(0x1000)
+    P = lambda pol, off=0, k=1, m=4, n=64, g=32, rm=ascq.ROUND_RINT: ascq._QuantizeParam(pol, off, rm, k, m, n, g)
+    q = lambda dst, src, sc, p, scale=d, off=None: L.ascq_quantize(d, dst, d, src, scale, off, 1.0, 0.0, sc,
+                                                                  ctypes.byref(p), None)
+    _err(q(ascq.INT8, ascq.F32, ascq.F16, P(ascq.PER_TOKEN)), ascq.E_UNSUPPORTED)            # (f32, f16) pair
+    _err(q(ascq.INT8, ascq.F16, ascq.BF16, P(ascq.PER_TOKEN)), ascq.E_UNSUPPORTED)           # (f16, bf16) pair
+    _err(q(ascq.FP4_E2M1, ascq.F16, ascq.F16, P(ascq.PER_TOKEN)), ascq.E_UNSUPPORTED)        # fp4: PER_GROUP only
+    _err(q(ascq.INT4, ascq.F16, ascq.F16, P(ascq.PER_GROUP)), ascq.E_UNSUPPORTED)            # no int4 output
+    _err(q(ascq.INT8, ascq.F16, ascq.F16, P(ascq.PER_TOKEN, n=48)), ascq.E_INVALID_ARG)      # n % 32
+    _err(q(ascq.INT8, ascq.F16, ascq.F16, P(ascq.PER_GROUP, g=48)), ascq.E_INVALID_ARG)      # group % 32
+    _err(q(ascq.INT8, ascq.F16, ascq.F16, P(ascq.PER_GROUP, k=2)), ascq.E_INVALID_ARG)       # kDim
+    _err(q(ascq.INT8, ascq.F16, ascq.F16, P(ascq.PER_TENSOR)), ascq.E_INVALID_ARG)           # PER_TENSOR: scalars
+    _err(q(ascq.INT8, ascq.F16, ascq.F16, P(ascq.PER_TOKEN, rm=9)), ascq.E_INVALID_ARG)      # round mode
+    _err(q(ascq.INT8, ascq.F16, ascq.F16, P(7)), ascq.E_INVALID_ARG)                         # policy
+    _err(L.ascq_quantize(None, ascq.INT8, None, ascq.F16, None, None, 1.0, 0.0, ascq.F16,
+                         ctypes.byref(P(ascq.PER_TOKEN, m=0)), None), ascq.OK)                # m = 0: no-op
+    dq = lambda dst, src, sc, p: L.ascq_dequantize(d, dst, d, src, d, 1.0, sc, ctypes.byref(p), None)
+    _err(dq(ascq.F32, ascq.INT32, ascq.F32, P(ascq.PER_CHANNEL, off=1)), ascq.E_UNSUPPORTED)  # no offset
+    _err(dq(ascq.F16, ascq.INT32, ascq.F32, P(ascq.PER_CHANNEL)), ascq.E_UNSUPPORTED)         # (f32, f16) channel
+    _err(dq(ascq.F16, ascq.INT32, ascq.F16, P(ascq.PER_TENSOR)), ascq.E_UNSUPPORTED)          # half scalar
+    _err(dq(ascq.F32, ascq.F32, ascq.F32, P(ascq.PER_CHANNEL)), ascq.E_UNSUPPORTED)           # channel: int32 src
+    _err(dq(ascq.F16, ascq.INT32, ascq.F16, P(ascq.PER_TOKEN, n=8)), ascq.E_INVALID_ARG)      # 16-byte f16 rows
+    _err(dq(ascq.F16, ascq.INT32, ascq.BF16, P(ascq.PER_TOKEN)), ascq.E_UNSUPPORTED)          # (bf16, f16) pair
+    _err(L.ascq_dequantize(None, ascq.F32, None, ascq.INT32, None, 1.0, ascq.F32,
+                           ctypes.byref(P(ascq.PER_CHANNEL, m=0)), None), ascq.OK)
+    aq = lambda dst, src, sc, p, scale=d, off=None: L.ascq_antiquantize(d, dst, d, src, scale, off, 1.0, 0.0, sc,
+                                                                        ctypes.byref(p), None)
+    _err(aq(ascq.F32, ascq.INT8, ascq.F32, P(ascq.PER_CHANNEL)), ascq.E_UNSUPPORTED)  # channel: f16 / bf16 scales
+    _err(aq(ascq.F16, ascq.INT8, ascq.BF16, P(ascq.PER_CHANNEL)), ascq.E_UNSUPPORTED)  # of the dst type
+    _err(aq(ascq.F16, ascq.INT4, ascq.F16, P(ascq.PER_TOKEN)), ascq.E_UNSUPPORTED)     # no int4
+    _err(aq(ascq.BF16, ascq.INT8, ascq.F16, P(ascq.PER_GROUP)), ascq.E_UNSUPPORTED)    # (f16, bf16) pair
+    _err(aq(ascq.BF16, ascq.FP4_E2M1, ascq.E8M0, P(ascq.PER_GROUP, off=1), off=d), ascq.E_UNSUPPORTED)  # fp4 offset
+    _err(aq(ascq.BF16, ascq.FP4_E2M1, ascq.E8M0, P(ascq.PER_TOKEN)), ascq.E_UNSUPPORTED)  # fp4: PER_GROUP
+    _err(aq(ascq.BF16, ascq.FP4_E2M1, ascq.E8M0, P(ascq.PER_GROUP, n=32)), ascq.E_INVALID_ARG)  # fp4 n % 64
+    _err(aq(ascq.F16, ascq.INT8, ascq.F16, P(ascq.PER_TOKEN, off=1)), ascq.E_INVALID_ARG)  # has_offset, no tensor
+    _err(aq(ascq.F16, ascq.INT8, ascq.F16, P(ascq.PER_TENSOR)), ascq.E_INVALID_ARG)        # PER_TENSOR: scalars
+    _err(aq(ascq.F16, ascq.INT8, ascq.F16, P(ascq.PER_TOKEN, n=40)), ascq.E_INVALID_ARG)   # 32-byte rows
+    _err(L.ascq_antiquantize(None, ascq.F16, None, ascq.INT8, None, None, 1.0, 0.0, ascq.F16,
+                             ctypes.byref(P(ascq.PER_TENSOR, m=0)), None), ascq.OK)
+
+
 def test_gemv_group_argument_checks():
     L = ascq.lib()
     d = ctypes.c_void_p(0x1000)

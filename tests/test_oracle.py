@@ -1669,3 +1669,171 @@ def test_combine_max_min_special_values():
     w16 = np.array([0.5, -1.0, 3.0], np.float16).view(np.uint16)
     assert np.array_equal(O.c_combine(h16, w16, O.F16, 2).view(np.float16), np.array([1.0, -1.0, 3.0], np.float16))
     assert np.array_equal(O.c_combine(h16, w16, O.F16, 3).view(np.float16), np.array([0.5, -2.0, 3.0], np.float16))
+
+
+# --------------------------------------------------------------------------- Quantize / Dequantize / AntiQuantize
+def test_quantize_per_tensor_example_golden_exact():
+    """the reference's quant example on arch 3510 (quant.asc: Quantize PER_TENSOR, scale 2.0, offset 0.9, CAST_RINT,
+    float32 source) against its own golden np.round(src * 2.0 + 0.9)"""
+    f = np.load(GOLD / "quant_example_3510.npz")
+    src = f["src"].reshape(1, -1)
+    got = O.quantize(src, O.F32, O.INT8, O.PER_TENSOR, 1, src.shape[1], scale_scalar=2.0, offset_scalar=0.9)
+    assert np.array_equal(got[0], f["golden"])
+
+
+def test_dequantize_per_channel_example_golden_exact():
+    """the reference's dequant example on arch 3510 (dequant.asc: Dequantize PER_CHANNEL, int32 [128, 32], f32 scale
+    [32]) against its golden inp * scale in float32"""
+    f = np.load(GOLD / "dequant_example.npz")
+    y = O.dequantize(f["inp"], O.INT32, O.F32, O.PER_CHANNEL, scale=f["scale"], scale_type=O.F32)
+    assert (y.view(np.uint32) == f["golden"].view(np.uint32)).all()
+
+
+def test_antiquantize_per_channel_example_golden_exact():
+    """the reference's antiquant example on arch 3510 (antiquant.asc: AntiQuantize PER_CHANNEL with an offset, int8
+    [8, 128], f16 offset / scale [1, 128]) against its golden: fp32 (src + offset) * scale, one cast to f16"""
+    f = np.load(GOLD / "antiquant_seed10.npz")
+    y = O.antiquantize(f["src"], O.INT8, O.F16, O.PER_CHANNEL, 8, 128, scale=f["scale"].view(np.uint16).reshape(-1),
+                       scale_type=O.F16, offset=f["offset"].view(np.uint16).reshape(-1))
+    assert np.array_equal(y, f["golden_3510"].view(np.uint16))
+    assert not np.array_equal(y, f["golden_2201"].view(np.uint16))  # the half-arithmetic golden differs
+
+
+def _policy_tables(rng, policy, m, n, g, lo, hi):
+    """(scale argument, broadcast [m, n] view) for a policy: PER_TENSOR a scalar, PER_CHANNEL [n], PER_TOKEN [m],
+    PER_GROUP kDim 0 [ceil(m / g)][n]"""
+    if policy == O.PER_TENSOR:
+        v = np.float32(rng.uniform(lo, hi))
+        return v, np.full((m, n), v, np.float32)
+    if policy == O.PER_CHANNEL:
+        v = rng.uniform(lo, hi, n).astype(np.float32)
+        return v, np.broadcast_to(v[None, :], (m, n))
+    if policy == O.PER_TOKEN:
+        v = rng.uniform(lo, hi, m).astype(np.float32)
+        return v, np.broadcast_to(v[:, None], (m, n))
+    v = rng.uniform(lo, hi, ((m + g - 1) // g, n)).astype(np.float32)
+    return v, v[np.arange(m) // g]
+
+
+@pytest.mark.parametrize("policy", [O.PER_TENSOR, O.PER_CHANNEL, O.PER_TOKEN, O.PER_GROUP])
+@pytest.mark.parametrize("mode", [O.ROUND_RINT, O.ROUND_FLOOR, O.ROUND_ROUND])
+def test_quantize_int8_vs_numpy(policy, mode):
+    """int8 Quantize for every policy: numpy float32 x * s, then + o, the round mode and saturation; the scale and
+    offset indexed per policy (PER_GROUP with kDim 0: one row of scales per group of rows)"""
+    rng = np.random.default_rng(1300 + 10 * policy + mode)
+    m, n, g = 70, 96, 32
+    x = rng.uniform(-200.0, 200.0, (m, n)).astype(np.float32)
+    s, S = _policy_tables(rng, policy, m, n, g, 0.05, 1.5)
+    o, Of = _policy_tables(rng, policy, m, n, g, -6.0, 6.0)
+    tensor = policy != O.PER_TENSOR
+    got = O.quantize(x, O.F32, O.INT8, policy, m, n, scale=s if tensor else None, scale_type=O.F32,
+                     offset=o if tensor else None, scale_scalar=float(s) if not tensor else 1.0,
+                     offset_scalar=float(o) if not tensor else None, group=g, k_dim=0, round_mode=mode)
+    y = (x * S) + Of
+    assert np.array_equal(got, _sat_s8(y.astype(np.float64), mode))
+
+
+@pytest.mark.parametrize("dst", [O.INT8, O.HIF8, O.FP8_E4M3, O.FP4_E2M1])
+@pytest.mark.parametrize("st", [O.F16, O.BF16])
+def test_quantize_16bit_scale_widened_to_fp32(dst, st):
+    """Quantize with a half / bf16 source, scale and offset computes in fp32 (the scale and offset widened exactly,
+    quantize_impl.h:262-294): it equals the AscendQuant policy form given the same scale and offset as f32 values (the
+    form that computes in fp32), and for int8 differs from that form's own 16-bit arithmetic on this data"""
+    rng = np.random.default_rng(1400 + dst + 7 * st)
+    m, n, g = 64, 128, 32
+    col = (n + g - 1) // g
+    x = rng.uniform(-150.0, 150.0, (m, n))
+    sc = rng.uniform(0.05, 1.9, (m, col))
+    of = rng.uniform(-4.0, 4.0, (m, col))
+    if dst == O.FP4_E2M1:
+        x, sc = x / 40.0, sc
+    bits = (lambda a: a.astype(np.float16).view(np.uint16)) if st == O.F16 else _bf16_bits
+    vals = (lambda b: b.view(np.float16).astype(np.float32)) if st == O.F16 else _bf16_vals
+    xb, sb, ob = bits(x), bits(sc), bits(of)
+    got = O.quantize(xb, st, dst, O.PER_GROUP, m, n, scale=sb, scale_type=st, offset=ob, group=g, k_dim=1)
+    ref = O.quant_policy(xb, st, vals(sb).astype(np.float32), O.F32, dst, O.PER_GROUP, m, n, g,
+                         offset=vals(ob).astype(np.float32), k_dim=1)
+    assert np.array_equal(got, ref)
+    if dst == O.INT8:
+        own = O.quant_policy(xb, st, sb, st, dst, O.PER_GROUP, m, n, g, offset=ob, k_dim=1)
+        assert not np.array_equal(got, own)
+
+
+def test_quantize_per_channel_is_one_group_of_rows():
+    """PER_CHANNEL (scale[c]) is PER_GROUP with kDim 0 and a single group spanning every row; PER_TENSOR is PER_TOKEN
+    with every row's scale equal -- both to hifloat8 and fp8 outputs as well"""
+    rng = np.random.default_rng(1500)
+    m, n = 40, 64
+    x = rng.uniform(-3000.0, 3000.0, (m, n)).astype(np.float32)
+    s = rng.uniform(0.01, 3.0, n).astype(np.float32)
+    o = rng.uniform(-9.0, 9.0, n).astype(np.float32)
+    for dst in (O.INT8, O.HIF8, O.FP8_E5M2):
+        a = O.quantize(x, O.F32, dst, O.PER_CHANNEL, m, n, scale=s, offset=o)
+        b = O.quant_policy(x, O.F32, s[None, :], O.F32, dst, O.PER_GROUP, m, n, 64, offset=o[None, :], k_dim=0)
+        assert np.array_equal(a, b)
+        t = O.quantize(x, O.F32, dst, O.PER_TENSOR, m, n, scale_scalar=0.75, offset_scalar=-1.25)
+        u = O.quant_policy(x, O.F32, np.full(m, 0.75, np.float32), O.F32, dst, O.PER_TOKEN, m, n,
+                           offset_scalar=-1.25)
+        assert np.array_equal(t, u)
+
+
+@pytest.mark.parametrize("policy", [O.PER_TENSOR, O.PER_CHANNEL, O.PER_TOKEN, O.PER_GROUP])
+def test_dequantize_vs_numpy(policy):
+    """Dequantize: f32(src) * scale, one cast: PER_TENSOR a bf16 scalar to bf16, PER_CHANNEL a bf16 tensor to f32,
+    PER_TOKEN / PER_GROUP (kDim 1) f32 scales to f16 (int32 values below 2^24: the conversion is exact)"""
+    rng = np.random.default_rng(1600 + policy)
+    m, n, g = 48, 64, 32
+    src = rng.integers(-(1 << 20), 1 << 20, (m, n)).astype(np.int32)
+    if policy == O.PER_TENSOR:
+        sv = _bf16_vals(_bf16_bits(np.array([0.0123], np.float32)))[0]
+        y = O.dequantize(src, O.INT32, O.BF16, policy, scale_scalar=0.0123, scale_type=O.BF16)
+        exp = _bf16_sat(src.astype(np.float32) * np.float32(sv))
+    elif policy == O.PER_CHANNEL:
+        sb = _bf16_bits(rng.uniform(-0.01, 0.01, n).astype(np.float32))
+        y = O.dequantize(src, O.INT32, O.F32, policy, scale=sb, scale_type=O.BF16)
+        exp = src.astype(np.float32) * _bf16_vals(sb)[None, :]
+    else:
+        shape = (m,) if policy == O.PER_TOKEN else (m, n // g)
+        s = rng.uniform(-1e-3, 1e-3, shape).astype(np.float32)
+        y = O.dequantize(src, O.INT32, O.F16, policy, scale=s, scale_type=O.F32, group=g, k_dim=1)
+        S = s[:, None] if policy == O.PER_TOKEN else s[:, np.arange(n) // g]
+        exp = _f16_sat(src.astype(np.float32) * S)
+    assert np.array_equal(y.view(np.uint32) if y.dtype == np.float32 else y,
+                          exp.view(np.uint32) if exp.dtype == np.float32 else exp)
+
+
+@pytest.mark.parametrize("policy", [O.PER_TENSOR, O.PER_CHANNEL, O.PER_TOKEN, O.PER_GROUP])
+@pytest.mark.parametrize("src_type", [O.INT8, O.FP8_E4M3])
+def test_antiquantize_vs_numpy(policy, src_type):
+    """AntiQuantize: fp32 (src + o) * s and one cast for every policy, also with half scales (PER_TENSOR /
+    PER_CHANNEL take scales of the dst type; PER_TOKEN / PER_GROUP here f16 scales to f16 and f32 scales to bf16)"""
+    rng = np.random.default_rng(1700 + 10 * policy + src_type)
+    m, n, g = 40, 96, 32
+    if src_type == O.INT8:
+        q = rng.integers(-128, 128, (m, n)).astype(np.int8)
+        xv = q.astype(np.float32)
+    else:
+        q = fp8_bytes(rng, (m, n), O.FP8_E4M3)
+        xv = torch.from_numpy(q).view(torch.float8_e4m3fn).float().numpy()
+    for st, dt in ((O.F16, O.F16), (O.F32, O.BF16)):
+        if st == O.F32 and policy in (O.PER_TENSOR, O.PER_CHANNEL):
+            st, dt = O.BF16, O.BF16
+        s, S = _policy_tables(rng, policy, m, n, g, 0.01, 2.0)
+        o, Of = _policy_tables(rng, policy, m, n, g, -30.0, 30.0)
+        if st == O.F16:
+            s, S, o, Of = [np.asarray(a).astype(np.float16) for a in (s, S, o, Of)]
+            sa, oa = (np.asarray(s).view(np.uint16), np.asarray(o).view(np.uint16))
+        elif st == O.BF16:
+            sa, oa = _bf16_bits(np.atleast_1d(s)), _bf16_bits(np.atleast_1d(o))
+            S = _bf16_vals(_bf16_bits(np.ascontiguousarray(S, np.float32)))
+            Of = _bf16_vals(_bf16_bits(np.ascontiguousarray(Of, np.float32)))
+        else:
+            sa, oa = s, o
+        tensor = policy != O.PER_TENSOR
+        y = O.antiquantize(q, src_type, dt, policy, m, n, scale=sa if tensor else None, scale_type=st,
+                           offset=oa if tensor else None,
+                           scale_scalar=1.0 if tensor else float(np.asarray(S).reshape(-1)[0]),
+                           offset_scalar=None if tensor else float(np.asarray(Of).reshape(-1)[0]), group=g, k_dim=0)
+        v = (xv + np.asarray(Of, np.float32)) * np.asarray(S, np.float32)
+        exp = _f16_sat(v) if dt == O.F16 else _bf16_sat(v)
+        assert np.array_equal(y, exp), (policy, st)

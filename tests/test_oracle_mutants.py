@@ -7,7 +7,8 @@ double-rounded multiplier, a wrong E2M1 code, a ties-away f16 cast, an unrounded
 dequant indexed by row, a requant offset added before the clamp, a ties-away fp8 cast, an ignored requant
 sign flag, a FasterGelu with the wrong sign, and policy-form quant mistakes (arithmetic type, bf16 step, group
 axis, offset rounding, directed E2M1 modes) and dequant layout mistakes (int32 rounding, the single-row
-reshape, padded dst rows, group axis) and HiFloat8 / arch-3510 legacy quant mistakes, MX E1M2 / bias and enAtomic mistakes.  Each mutant is compiled on the CPU into a temporary library and the pinning tests of
+reshape, padded dst rows, group axis) and HiFloat8 / arch-3510 legacy quant mistakes, MX E1M2 / bias and enAtomic
+mistakes, and the newer Quantize / AntiQuantize interface's channel index and fp32 arithmetic.  Each mutant is compiled on the CPU into a temporary library and the pinning tests of
 tests/test_oracle.py are run against it; every mutant must fail at least one of them.
 """
 from __future__ import annotations
@@ -62,6 +63,9 @@ MUTANTS = {
     37: "enAtomic max / min swapped",
     38: "group epilogue int32 -> fp32 rounded to nearest even instead of ties away",
     39: "hifloat8 Matmul operands decoded as fp8 e4m3",
+    40: "Quantize / AntiQuantize PER_CHANNEL scales indexed by row",
+    41: "Quantize computed in the scale type instead of fp32",
+    42: "AntiQuantize computed in the scale type instead of fp32",
 }
 
 
