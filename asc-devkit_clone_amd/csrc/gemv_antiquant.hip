@@ -844,11 +844,13 @@ static hipError_t launch_aq_xs(uint16_t* y, const uint16_t* x, const void* wp, b
     return hipGetLastError();
 }
 
-// Batch form (16 < M <= 16 MT, group size 128 << s): the column blocks of aq_xs_kernel, with the activations
-// streamed.  Block c covers the strips [c sq + min(c, sr), ...); wave (sg, kw) of the SG x KW waves owns strips
-// sg NBW .. sg NBW + NBW - 1 of the block and, in round r, k tile r KW + kw.  The activation tile x[0:16 MT,
-// 128 KW r .. 128 KW (r + 1)) of each round is copied into an LDS ring of ST stages (buffer loads with an LDS
-// destination, 16-byte chunk c of row r at chunk c ^ (r % 16); rows m >= M read zeros), ST - 1 rounds ahead, and
+// Batch form (M > 16, group size 128 << s): the column blocks of aq_xs_kernel, with the activations streamed; the
+// grid's y dimension walks row blocks of 16 MT rows (one for a decode batch).  Block c covers the strips
+// [c sq + min(c, sr), ...); wave (sg, kw) of the SG x KW waves owns strips
+// sg NBW .. sg NBW + NBW - 1 of the block and, in round r, k tile r KW + kw.  The activation tile x[r0:r0 + 16 MT,
+// 128 KW r .. 128 KW (r + 1)) of each round (r0 the row block's first row) is copied into an LDS ring of ST stages
+// (buffer loads with an LDS destination, 16-byte chunk c of row r at chunk c ^ (r % 16); rows m >= M read zeros),
+// ST - 1 rounds ahead, and
 // shared by all waves; every wave reads each activation fragment once for its NBW strips, which is what keeps the
 // LDS read traffic of a 64-row batch within bounds.  Weight tiles stream through a register ring DW - 1 rounds
 // ahead (DW a multiple of ST); the scale / offset rows of a wave's tiles are copied into LDS once, at the start.
@@ -891,6 +893,7 @@ __global__ __launch_bounds__(SG * KW * 64) void aq_ring_kernel(AqXsArgs A)
     const uint32_t col_in = lane & 15, kq = lane >> 4;
     const uint32_t cb = blockIdx.x;
     const uint32_t M = A.M, N = A.N, KB = A.KB;
+    const uint32_t row0 = blockIdx.y * (uint32_t)P::ROWS;  // this block's first row (row blocks of 16 MT rows)
     const uint32_t s0 = cb * A.sq + (cb < A.sr ? cb : A.sr), s1 = s0 + A.sq + (cb < A.sr ? 1u : 0u);
     const uint32_t sb = s0 + (uint32_t)(sg * NBW);  // first strip of this wave
     const uint32_t rounds = KB / KW;                // KB % KW == 0
@@ -923,7 +926,7 @@ __global__ __launch_bounds__(SG * KW * 64) void aq_ring_kernel(AqXsArgs A)
             const uint32_t q = gcopy * 64 + lane;
             const uint32_t row = q / P::CH, p = q % P::CH;
             const uint32_t c = p ^ (row & 15u);  // logical chunk held at physical chunk p
-            const uint32_t off = row < M && r < rounds ? (row * A.K + r * KW * KT + c * 8) * 2 : AQ_OOB;
+            const uint32_t off = row0 + row < M && r < rounds ? ((row0 + row) * A.K + r * KW * KT + c * 8) * 2 : AQ_OOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(smem + slot * P::SLOT + gcopy * 1024), 16, off, 0, 0, 0);
         }
     };
@@ -1049,7 +1052,7 @@ __global__ __launch_bounds__(SG * KW * 64) void aq_ring_kernel(AqXsArgs A)
             uint16_t* yc = A.y + (sb + b) * 16 + col_in;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t m = 16 * a + 4 * kq + i;
+                const uint32_t m = row0 + 16 * a + 4 * kq + i;
                 if (m < M) y_put(yc + (uint64_t)m * N, f32_to_f16_sat(acc[a][b][i]), A.atomic);
             }
         }
@@ -1073,15 +1076,15 @@ static hipError_t launch_aq_ring(uint16_t* y, const uint16_t* x, const void* wp,
     using P4 = AqRing<MT, NBW, SG, KW, ST, DW, true, true>;
     AqXsArgs A;
     const int64_t lds = aq_ring_lds<MT, NBW, SG, KW, ST, DW>(K, offset != nullptr);
-    if (M > 16 * MT || (K / KT) % KW != 0 || lds == 0 ||
-        !aq_cols_args(A, y, x, wp, int4, scale, offset, g, M, N, K, C, SG * NBW, atomic))
+    if ((K / KT) % KW != 0 || lds == 0 || !aq_cols_args(A, y, x, wp, int4, scale, offset, g, M, N, K, C, SG * NBW, atomic))
         return hipErrorInvalidValue;
+    const unsigned RB = (unsigned)((M + 16 * MT - 1) / (16 * MT));  // row blocks (grid.y)
 #define AQ_RING_LAUNCH(I4, OF)                                                     \
     do {                                                                           \
         constexpr auto kern = aq_ring_kernel<MT, NBW, SG, KW, ST, DW, I4, OF>;      \
         hipError_t e = ensure_dynamic_lds<kern>((int)lds);                         \
         if (e != hipSuccess) return e;                                             \
-        launch_k(kern, dim3((unsigned)C), dim3(P4::NT), (uint32_t)lds, st, A);      \
+        launch_k(kern, dim3((unsigned)C, RB), dim3(P4::NT), (uint32_t)lds, st, A);  \
     } while (0)
     if (int4) {
         if (offset) AQ_RING_LAUNCH(true, true);
@@ -1341,10 +1344,26 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
     const bool int4 = w_type == DT_INT4;
     const int64_t NBT = N / 16, KB = K / KT;
     const bool cols_ok = g % KT == 0 && ((g / KT) & (g / KT - 1)) == 0;  // column-block kernels: group 128 << s
-    // above 64 rows: the LDS-staged GEMM of aq_gemm.hip (each weight tile dequantised once per 256 rows) where it takes
-    // the shape, else 64-row passes of the kernels below
+    // Above 64 rows: aq_ring_kernel over row blocks (grid.y) -- x shared through the LDS ring by the strip groups of a
+    // block, each weight fragment dequantised once per block of rows and multiplied against all of them.  64-row
+    // blocks of 6 strips (2 strip groups x 4 k-split waves) while they make about one block per CU, else 128-row blocks
+    // of 12 strips (4 strip groups x 2 k-split waves).  Measured at K = 4096, N = 11008 (int4 / int8, M = 128 / 512 /
+    // 2048): 27 / 63 / 239 us against 71 / 78 / 250 us for the LDS-staged MFMA GEMM of aq_gemm.hip, which takes the
+    // shapes the ring does not (K not a multiple of 256 or 512, LDS too small for the scale rows), then 64-row passes
+    // of the kernels below.
     if (M > 64 && cols_ok) {
-        const hipError_t e = launch_aq_gemm(y, x, wp, w_type, scale, offset, group, M, N, K, atomic, st);
+        const int64_t rb64 = (M + 63) / 64, rb128 = (M + 127) / 128;
+        const int c64 = aq_blocks(NBT, 6, (int)((256 + rb64 - 1) / rb64));
+        hipError_t e = hipErrorInvalidValue;
+        if (c64 * rb64 <= 320 && KB % 4 == 0 && aq_ring_lds<4, 3, 2, 4, 2, 2>(K, offset != nullptr))
+            e = launch_aq_ring<4, 3, 2, 4, 2, 2>(y, x, wp, int4, scale, offset, g, M, N, K, c64, atomic, st);
+        else if (KB % 2 == 0 && aq_ring_lds<8, 3, 4, 2, 2, 2>(K, offset != nullptr))
+            e = launch_aq_ring<8, 3, 4, 2, 2, 2>(y, x, wp, int4, scale, offset, g, M, N, K,
+                                                 aq_blocks(NBT, 12, (int)((256 + rb128 - 1) / rb128)), atomic, st);
+        if (e == hipErrorInvalidValue) {
+            (void)hipGetLastError();
+            e = launch_aq_gemm(y, x, wp, w_type, scale, offset, group, M, N, K, atomic, st);
+        }
         if (e != hipErrorInvalidValue) return e;
         (void)hipGetLastError();
     }

@@ -155,10 +155,12 @@ def test_column_block_kernels(ascq_gpu, oracle, w_type, with_offset, M, K, N, gr
     (200, 1024, 4112, 256),   # partial row block; 257 strips: the last column block holds one strip
     (128, 2048, 272, 2048),   # one group over all of K
     (1000, 768, 1008, 128),   # eight row blocks, the last one partial
+    (300, 640, 272, 128),     # K = 5 tiles of 128: the LDS-staged MFMA GEMM (the ring kernels split K in 2 or 4)
 ])
 def test_prefill_gemm(ascq_gpu, oracle, w_type, with_offset, M, K, N, group):
-    """M > 64: the LDS-staged GEMM whose weight tiles are dequantised once per 256 rows (aq_gemm.hip); the weights
-    bit-exact as AscendAntiQuant, fp32 accumulation within the bound of check_close"""
+    """M > 64: the ring kernel over row blocks (64-row blocks while they make about one block per CU, else 128-row
+    blocks) or, for K not a multiple of 256, the LDS-staged MFMA GEMM of aq_gemm.hip; the weights bit-exact as
+    AscendAntiQuant, fp32 accumulation within the bound of check_close"""
     rng = seeded(M + K + N + group + with_offset)
     code = O.INT8 if w_type == "int8" else O.INT4
     at = ascq_gpu.INT8 if w_type == "int8" else ascq_gpu.INT4
