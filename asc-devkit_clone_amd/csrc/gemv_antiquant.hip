@@ -1385,8 +1385,10 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
             e = launch_aq_xs<2, 2, 4, 1>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 4, 256), atomic, st);
         else if (cols_ok && mc > 16 && mc <= 32 && KB % 8 == 0 && aq_ring_lds<2, 3, 1, 8, 2, 2>(K, offset != nullptr))
             e = launch_aq_ring<2, 3, 1, 8, 2, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 3, 256), atomic, st);
-        else if (cols_ok && mc > 32 && KB % 4 == 0 && aq_ring_lds<4, 2, 2, 4, 2, 4>(K, offset != nullptr))
-            e = launch_aq_ring<4, 2, 2, 4, 2, 4>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 4, 172), atomic, st);
+        // (32 < M <= 64: 2 strip groups x 4 k-split waves, weights 1 round ahead, about 256 blocks of <= 4 strips;
+        // measured against 172 blocks with 3 rounds ahead and seven other splits: W4 M = 64 17.7 against 18.5-28 us)
+        else if (cols_ok && mc > 32 && KB % 4 == 0 && aq_ring_lds<4, 2, 2, 4, 2, 2>(K, offset != nullptr))
+            e = launch_aq_ring<4, 2, 2, 4, 2, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 4, 256), atomic, st);
         else {
             if (mc <= 4 && mc * K * 2 + 16 <= 48 * 1024) {
                 if (int4) launch_aq<1, 1, 4, 8, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);

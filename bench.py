@@ -247,7 +247,7 @@ def _roof(bound, achieved, peak, unit):
 # ----------------------------------------------------------------------------------------------
 def bench_prefill(torch, ascq, w_type, M, iters):
     """weight-only antiquant matmul at a prefill batch: x f16 [M, 4096] against the config-3 weight (int4 / int8
-    [4096, 11008], g = 128 f16 scale + offset), fp32 accumulation, f16 out -- the LDS-staged f16 GEMM of aq_gemm.hip"""
+    [4096, 11008], g = 128 f16 scale + offset), fp32 accumulation, f16 out -- the LDS-ring kernel over 128-row blocks"""
     K, N, grp = 4096, 11008, 128
     g = torch.Generator(device="cuda")
     g.manual_seed(5)
