@@ -65,6 +65,20 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_i8_kernel(GemmI8Args p
     c.a0 = (uint32_t)(m0 * p.lda + k0) + da;
     c.b0 = (uint32_t)(TB ? n0 * p.ldb + k0 : n0 + k0 * p.ldb) + db;
     c.kbytes = kc;
+    // KW > 1 (small problems, where the kernel is one chain of latencies): the epilogue's bias and QUANT_PRE words are
+    // loaded before the main loop, so their latency hides under it instead of following it.  They are older than the
+    // main loop's copies, whose counted waits therefore still cover exactly those copies (loads return in order).
+    int32_t pre_bias[T::FN];
+    uint64_t pre_w[T::FN];
+    if constexpr (KW > 1) {
+#pragma unroll
+        for (int j = 0; j < T::FN; ++j) {
+            const int cl = T::frag_col(0, j, (int)threadIdx.x & 63);
+            const bool cok = cl < c.cols;
+            pre_bias[j] = (p.bias && cok) ? p.bias[n0 + cl] : 0;
+            pre_w[j] = (p.qvec && cok) ? p.qvec[n0 + cl] : p.qscalar;
+        }
+    }
     typename T::acc_t acc[T::FM][T::FN];
     T::run(c, smem + (KW > 1 ? kw * T::LDS_BYTES : 0), acc, KW > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x);
     if constexpr (KW > 1) {
@@ -112,8 +126,8 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_i8_kernel(GemmI8Args p
             const int cl = T::frag_col(wn, j, lane);
             const bool cok = cl < c.cols;
             const int64_t col = n0 + cl;
-            const int32_t bias = (p.bias && cok) ? p.bias[col] : 0;
-            const uint64_t w = (p.qvec && cok) ? p.qvec[col] : p.qscalar;
+            const int32_t bias = KW > 1 ? pre_bias[j] : (p.bias && cok) ? p.bias[col] : 0;
+            const uint64_t w = KW > 1 ? pre_w[j] : (p.qvec && cok) ? p.qvec[col] : p.qscalar;
             const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
             const uint32_t cbase = cok ? (uint32_t)(cl * esize) : OOB;
 #pragma unroll
