@@ -35,7 +35,7 @@ ARITH_F16, ARITH_F32 = 0, 1
 # ascq_dequant_mode (DeQuantMode)
 DEQUANT_SINGLE_ROW, DEQUANT_MULTI_ROW = 0, 1
 # ascq_format
-FORMAT_ND, FORMAT_PACKED = 0, 1
+FORMAT_ND, FORMAT_PACKED, FORMAT_NZ = 0, 1, 2
 
 OK, E_INVALID_ARG, E_UNSUPPORTED, E_HIP, E_STATE = 0, -1, -2, -3, -4
 

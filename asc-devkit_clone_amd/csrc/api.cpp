@@ -192,6 +192,7 @@ size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 // transpose reads.
 bool bytes_transposes_b(const ascq_matmul_s* h)
 {
+    if (h->ty.b_format == ASCQ_FORMAT_NZ) return false;  // converted from NZ instead (bytes_nz_b)
     if (kind_of(h->ty) == K_INT8 && h->N % 16 == 0 && (h->M < 1024 || h->N < 1024)) return false;
     return !h->trans_b && h->M >= 512 && h->N % 16 == 0 && h->K % 16 == 0;
 }
@@ -200,9 +201,12 @@ bool bytes_transposes_b(const ascq_matmul_s* h)
 // GEMM reads K-contiguous A rows only)
 bool bytes_transposes_a(const ascq_matmul_s* h) { return h->trans_a != 0; }
 
+// int8 / fp8 B in the NZ fractal layout: converted to a K-contiguous [N, K] copy in the workspace at every IterateAll
+bool bytes_nz_b(const ascq_matmul_s* h) { return h->ty.b_format == ASCQ_FORMAT_NZ; }
+
 size_t bytes_workspace(const ascq_matmul_s* h)
 {
-    size_t need = bytes_transposes_b(h) ? align256((size_t)h->N * (size_t)h->K) : 0;
+    size_t need = bytes_transposes_b(h) || bytes_nz_b(h) ? align256((size_t)h->N * (size_t)h->K) : 0;
     if (bytes_transposes_a(h)) need += align256((size_t)h->M * (size_t)h->K);
     return need;
 }
@@ -270,11 +274,20 @@ ascq_status prepare_byte_operands(ascq_matmul_s* h, hipStream_t st, ByteOperands
     o.ldb = h->trans_b ? h->K : h->N;
     o.trans_a = h->trans_a;
     o.trans_b = h->trans_b;
-    const bool tb = bytes_transposes_b(h), ta = bytes_transposes_a(h);
-    if (!tb && !ta) return ASCQ_OK;
+    const bool tb = bytes_transposes_b(h), ta = bytes_transposes_a(h), nz = bytes_nz_b(h);
+    if (!tb && !ta && !nz) return ASCQ_OK;
     ascq_status s = ensure_workspace(h);
     if (s != ASCQ_OK) return s;
     uint8_t* ws = (uint8_t*)h->ws;
+    if (nz) {  // NZ B [K, N] (transposed on the way out) or [N, K] -> ND [N, K]
+        hipError_t e = h->trans_b ? ascq::launch_nz_to_nd(ws, h->b, 1, 1, h->N, h->K, 0, st)
+                                  : ascq::launch_nz_to_nd(ws, h->b, 1, 1, h->K, h->N, 1, st);
+        if (e != hipSuccess) return hip_status(e, "NZ B to ND");
+        o.B = ws;
+        o.ldb = h->K;
+        o.trans_b = 1;
+        ws += align256((size_t)h->N * (size_t)h->K);
+    }
     if (tb) {  // B [K, N] -> [N, K]
         hipError_t e = ascq::launch_transpose_i8(ws, (const uint8_t*)h->b, h->K, h->N, st);
         if (e != hipSuccess) return hip_status(e, "transpose B");
@@ -348,9 +361,12 @@ ascq_status ascq_matmul_create(const ascq_matmul_types* types, ascq_matmul_t* ou
                         "matmul_create: int8 matmul supports C = f16, bf16, int32, int8, uint8 or int4");
         if (types->bias_type != 0 && types->bias_type != ASCQ_DT_INT32)
             return fail(ASCQ_E_UNSUPPORTED, "matmul_create: int8 matmul bias must be int32");
-        if (types->b_format != ASCQ_FORMAT_ND) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: int8 B must be ND");
+        if (types->b_format != ASCQ_FORMAT_ND && !(k == K_INT8 && types->b_format == ASCQ_FORMAT_NZ))
+            return fail(ASCQ_E_UNSUPPORTED, "matmul_create: int8 B must be ND or NZ, int4 B ND");
     } else if (k == K_ANTIQUANT) {
         if (types->c_type != ASCQ_DT_F16) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: weight-only matmul supports C = f16");
+        if (types->b_format != ASCQ_FORMAT_ND && types->b_format != ASCQ_FORMAT_PACKED)
+            return fail(ASCQ_E_UNSUPPORTED, "matmul_create: weight-only B must be ND or PACKED");
         if (types->bias_type != 0) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: weight-only matmul has no bias path");
     } else if (k == K_F8 || k == K_HIF8) {
         const char* what = k == K_F8 ? "fp8" : "hifloat8";
@@ -362,7 +378,8 @@ ascq_status ascq_matmul_create(const ascq_matmul_types* types, ascq_matmul_t* ou
                         "hifloat8", what);
         if (types->bias_type != 0 && types->bias_type != ASCQ_DT_F32)
             return fail(ASCQ_E_UNSUPPORTED, "matmul_create: %s matmul bias must be f32", what);
-        if (types->b_format != ASCQ_FORMAT_ND) return fail(ASCQ_E_UNSUPPORTED, "matmul_create: %s B must be ND", what);
+        if (types->b_format != ASCQ_FORMAT_ND && !(k == K_F8 && types->b_format == ASCQ_FORMAT_NZ))
+            return fail(ASCQ_E_UNSUPPORTED, "matmul_create: %s B must be ND%s", what, k == K_F8 ? " or NZ" : "");
     } else {
         if (types->c_type != ASCQ_DT_BF16 && types->c_type != ASCQ_DT_F32)
             return fail(ASCQ_E_UNSUPPORTED, "matmul_create: MX matmul supports C = bf16 or f32");

@@ -159,8 +159,10 @@ typedef struct ascq_matmul_s* ascq_matmul_t;
 
 /* CubeFormat of B (MatmulType<TPosition, CubeFormat, T>, impl/adv_api/detail/matmul/utils/matmul_type_def.h:40;
  * CubeFormat include/adv_api/matmul/matmul_config.h:23-35):
- * ND is the reference's row-major layout; PACKED is the output of ascq_weight_pack (weight-only only). */
-typedef enum { ASCQ_FORMAT_ND = 0, ASCQ_FORMAT_PACKED = 1 } ascq_format;
+ * ND is the reference's row-major layout; PACKED is the output of ascq_weight_pack (weight-only only); NZ is the
+ * reference's fractal layout (the one ascq_nz_to_nd reads: B [K, N], or [N, K] with isTransposeB, as [K, N] / [N, K]
+ * NZ matrices) for int8 and fp8 B, turned into a K-contiguous [N, K] copy in the workspace at every IterateAll. */
+typedef enum { ASCQ_FORMAT_ND = 0, ASCQ_FORMAT_PACKED = 1, ASCQ_FORMAT_NZ = 2 } ascq_format;
 
 typedef struct {
     int32_t a_type;     /* ascq_dtype of A */

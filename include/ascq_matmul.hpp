@@ -131,9 +131,12 @@ public:
         const int32_t Kb = okb_ > 0 ? okb_ : Ka;
         if (!a_.set || !b_.set || !c_.set || M <= 0 || N <= 0 || Ka <= 0 || Ka != Kb) return -1;
         if (m_ > M || n_ > N || k_ > Ka) return -1;
-        if (a_.fmt != CubeFormat::ND || b_.fmt != CubeFormat::ND || c_.fmt != CubeFormat::ND) return -1;
+        // A and C row-major; B row-major or NZ (int8 / fp8 B: Matmul(..., ASCQ_FORMAT_NZ) takes it as it is)
+        if (a_.fmt != CubeFormat::ND || c_.fmt != CubeFormat::ND) return -1;
+        if (b_.fmt != CubeFormat::ND && b_.fmt != CubeFormat::NZ) return -1;
         // the type combination must have a kernel: the library decides (a transient handle)
-        ascq_matmul_types ty{a_.type, b_.type, c_.type, bias_.set && isBias_ ? bias_.type : 0, 0, ASCQ_FORMAT_ND};
+        ascq_matmul_types ty{a_.type, b_.type, c_.type, bias_.set && isBias_ ? bias_.type : 0, 0,
+                             b_.fmt == CubeFormat::NZ ? ASCQ_FORMAT_NZ : ASCQ_FORMAT_ND};
         ascq_matmul_t h = nullptr;
         if (ascq_matmul_create(&ty, &h) != ASCQ_OK) return -1;
         ascq_matmul_destroy(h);

@@ -49,7 +49,8 @@ int main()
     size_t ws = 1;
     EXPECT(ascq_matmul_workspace_size(mm.handle(), &ws) == ASCQ_OK);
 
-    // GetTiling's -1 cases: a type combination without a kernel, missing types, Ka != Kb, NZ operands
+    // GetTiling's -1 cases: a type combination without a kernel, missing types, Ka != Kb, an NZ A, an NZ B of a
+    // type without an NZ path (int4)
     ascq::MultiCoreMatmulTiling bad;
     bad.SetAType(TPosition::GM, CubeFormat::ND, ASCQ_DT_F32);
     bad.SetBType(TPosition::GM, CubeFormat::ND, ASCQ_DT_F32);
@@ -65,12 +66,30 @@ int main()
     kk.SetCType(TPosition::GM, CubeFormat::ND, ASCQ_DT_INT32);
     kk.SetOrgShape(16, 16, 32, 48);
     EXPECT(kk.GetTiling(t) == -1);
+    ascq::MultiCoreMatmulTiling nza;
+    nza.SetAType(TPosition::GM, CubeFormat::NZ, ASCQ_DT_INT8);
+    nza.SetBType(TPosition::GM, CubeFormat::ND, ASCQ_DT_INT8);
+    nza.SetCType(TPosition::GM, CubeFormat::ND, ASCQ_DT_INT32);
+    nza.SetShape(16, 16, 16);
+    EXPECT(nza.GetTiling(t) == -1);
+    ascq::MultiCoreMatmulTiling nz4;
+    nz4.SetAType(TPosition::GM, CubeFormat::ND, ASCQ_DT_INT4);
+    nz4.SetBType(TPosition::GM, CubeFormat::NZ, ASCQ_DT_INT4);
+    nz4.SetCType(TPosition::GM, CubeFormat::ND, ASCQ_DT_INT32);
+    nz4.SetShape(16, 16, 16);
+    EXPECT(nz4.GetTiling(t) == -1);
+
+    // an NZ int8 B (the group-matmul sample's MatmulType<GM, NZ, int8_t>, quant_group_matmul_custom.asc:110): a
+    // tiling, and a handle created with ASCQ_FORMAT_NZ that counts the ND copy of B in its workspace
     ascq::MultiCoreMatmulTiling nz;
     nz.SetAType(TPosition::GM, CubeFormat::ND, ASCQ_DT_INT8);
     nz.SetBType(TPosition::GM, CubeFormat::NZ, ASCQ_DT_INT8);
     nz.SetCType(TPosition::GM, CubeFormat::ND, ASCQ_DT_INT32);
-    nz.SetShape(16, 16, 16);
-    EXPECT(nz.GetTiling(t) == -1);
+    nz.SetShape(64, 96, 128);
+    EXPECT(nz.GetTiling(t) == 0);
+    ascq::Matmul mnz(ASCQ_DT_INT8, ASCQ_DT_INT8, ASCQ_DT_INT32, 0, 0, ASCQ_FORMAT_NZ);
+    mnz.Init(&t);
+    EXPECT(ascq_matmul_workspace_size(mnz.handle(), &ws) == ASCQ_OK && ws >= (size_t)96 * 128);
 
     // Init rejects Ka != Kb
     ascq_cube_tiling t2 = {};

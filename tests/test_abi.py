@@ -285,6 +285,33 @@ def test_mx_e1m2_and_bias_handle():
     _err(L.ascq_matmul_destroy(h), ascq.OK)
 
 
+def test_nz_b_format_handle():
+    """B declared CubeFormat::NZ (ASCQ_FORMAT_NZ): accepted for int8 and fp8 B, whose workspace then holds the ND
+    [N, K] copy of B (whatever the transpose flag, and in place of the [K, N] transpose); refused for int4, MX,
+    hifloat8 and weight-only B, and an unknown format is refused everywhere"""
+    L = ascq.lib()
+    h = ctypes.c_void_p()
+    d = ctypes.c_void_p(0x1000)
+    ws = ctypes.c_size_t()
+    for at, bt, ct in ((ascq.INT8, ascq.INT8, ascq.INT32), (ascq.FP8_E4M3, ascq.FP8_E5M2, ascq.F32)):
+        t = ascq._MatmulTypes(at, bt, ct, 0, 0, ascq.FORMAT_NZ)
+        _err(L.ascq_matmul_create(ctypes.byref(t), ctypes.byref(h)), ascq.OK)
+        _err(L.ascq_matmul_set_org_shape(h, 2048, 1280, 512), ascq.OK)
+        for tb in (0, 1):
+            _err(L.ascq_matmul_set_tensor_b(h, d, tb), ascq.OK)
+            _err(L.ascq_matmul_workspace_size(h, ctypes.byref(ws)), ascq.OK)
+            assert ws.value == 1280 * 512
+        _err(L.ascq_matmul_destroy(h), ascq.OK)
+    refused = [ascq._MatmulTypes(ascq.INT4, ascq.INT4, ascq.INT32, 0, 0, ascq.FORMAT_NZ),
+               ascq._MatmulTypes(ascq.FP4_E2M1, ascq.FP4_E2M1, ascq.BF16, 0, ascq.E8M0, ascq.FORMAT_NZ),
+               ascq._MatmulTypes(ascq.HIF8, ascq.HIF8, ascq.F32, 0, 0, ascq.FORMAT_NZ),
+               ascq._MatmulTypes(ascq.F16, ascq.INT8, ascq.F16, 0, 0, ascq.FORMAT_NZ),
+               ascq._MatmulTypes(ascq.INT8, ascq.INT8, ascq.INT32, 0, 0, 7),
+               ascq._MatmulTypes(ascq.F16, ascq.INT4, ascq.F16, 0, 0, 7)]
+    for t in refused:
+        _err(L.ascq_matmul_create(ctypes.byref(t), ctypes.byref(h)), ascq.E_UNSUPPORTED)
+
+
 def test_int4_operand_handle():
     """int4b_t A / B (matmul_int4): accepted with int32 / f16 C; the workspace holds both operands unpacked to
     int8, plus the nibble-transposed B when B is given [K, N]; a transposed A and odd K / N are rejected before

@@ -67,3 +67,69 @@ def test_group_matmul_from_nz_weights(ascq_gpu, oracle):
                                      torch.bfloat16)
     ref0 = O.group_matmul(x, pts, w, scale, counts, 1, G, M, K, N, O.BF16)
     assert np.array_equal(y0.cpu().view(torch.int16).numpy().view(np.uint16), ref0)
+
+
+def _nz_of(b):
+    """the NZ form of one [rows, cols] 1-byte matrix (the oracle's restatement of the fractal layout)"""
+    rows, cols = b.shape
+    return O.nd_to_nz(b.view(np.uint8)[None], 1, 1, rows, cols)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 96, 128), (100, 72, 96), (1024, 1280, 512)])
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_matmul_nz_b_int8(ascq_gpu, oracle, M, N, K, trans_b):
+    """an int8 Matmul whose B is declared NZ (MatmulType<GM, NZ, int8_t>, the group-matmul sample's B,
+    quant_group_matmul_custom.asc:110): IterateAll on the NZ bytes equals the oracle on the ND B bit for bit, int32 C
+    and DEQF16 f16 C with bias, B given [K, N] or (isTransposeB) [N, K], shapes padded inside the fractals and one
+    on the 256 x 256 tiles"""
+    rng = seeded(M + 3 * N + 7 * K + int(trans_b))
+    A = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-127, 128, (K, N), dtype=np.int8)
+    nz = _nz_of(np.ascontiguousarray(B.T) if trans_b else B)
+    mm = ascq_gpu.Matmul(ascq_gpu.INT8, ascq_gpu.INT8, ascq_gpu.INT32, 0, 0, ascq_gpu.FORMAT_NZ)
+    mm.SetOrgShape(M, N, K)
+    mm.SetTensorA(_dev(A))
+    mm.SetTensorB(_dev(nz), trans_b)
+    c = torch.full((M, N), 7, dtype=torch.int32, device="cuda")
+    mm.IterateAll(c)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(c.cpu().numpy(), O.matmul_i8(A, B))
+    mm.End()
+    bias = rng.integers(-(1 << 15), 1 << 15, N, dtype=np.int32)
+    sc = np.exp(rng.uniform(np.log(2.0 ** -12), np.log(2.0 ** -6), N)).astype(np.float32)
+    words = sc.view(np.uint32).astype(np.uint64)
+    mq = ascq_gpu.Matmul(ascq_gpu.INT8, ascq_gpu.INT8, ascq_gpu.F16, ascq_gpu.INT32, 0, ascq_gpu.FORMAT_NZ)
+    mq.SetOrgShape(M, N, K)
+    mq.SetQuantVector(_dev(words.view(np.int64)))
+    mq.SetTensorA(_dev(A))
+    mq.SetTensorB(_dev(nz), trans_b)
+    mq.SetBias(_dev(bias))
+    y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    mq.IterateAll(y)
+    torch.cuda.synchronize()
+    ref = O.mm_dequant(O.matmul_i8(A, B, bias), O.F16, qvec=words)
+    np.testing.assert_array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), ref)
+    mq.End()
+
+
+@pytest.mark.parametrize("M,N,K", [(96, 160, 192), (1024, 1024, 256)])
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_matmul_nz_b_fp8(ascq_gpu, M, N, K, trans_b):
+    """an fp8 Matmul with B declared NZ equals the same Matmul with the ND B, bit for bit (f32 C: the same kernel
+    on the same K-contiguous B)"""
+    rng = seeded(5 * M + N + K + int(trans_b))
+    A = torch.randn((M, K), generator=torch.Generator().manual_seed(M + K)).to(torch.float8_e4m3fn).view(torch.uint8)
+    B = torch.randn((K, N), generator=torch.Generator().manual_seed(N + K)).to(torch.float8_e4m3fn).view(torch.uint8)
+    Bn = np.ascontiguousarray(B.numpy().T) if trans_b else B.numpy()
+    outs = []
+    for fmt, b in ((ascq_gpu.FORMAT_ND, Bn), (ascq_gpu.FORMAT_NZ, _nz_of(Bn))):
+        mm = ascq_gpu.Matmul(ascq_gpu.FP8_E4M3, ascq_gpu.FP8_E4M3, ascq_gpu.F32, 0, 0, fmt)
+        mm.SetOrgShape(M, N, K)
+        mm.SetTensorA(A.cuda())
+        mm.SetTensorB(_dev(b), trans_b)
+        c = torch.full((M, N), float(rng.integers(1, 9)), dtype=torch.float32, device="cuda")
+        mm.IterateAll(c)
+        torch.cuda.synchronize()
+        outs.append(c.cpu().view(torch.int32).numpy())
+        mm.End()
+    np.testing.assert_array_equal(outs[1], outs[0])
