@@ -1284,7 +1284,15 @@ static hipError_t launch_aq_kw(uint16_t* y, const uint16_t* x, const void* wp, b
     return hipGetLastError();
 }
 
-// aq_kw_kernel for M <= 32 over C = min(strips, 256) blocks: strips per block NS = ceil(strips / C) <= 4, row tiles
+// column blocks for a grid of about `target` workgroups whose blocks hold at most smax strips
+inline int aq_blocks(int64_t NBT, int smax, int target)
+{
+    int64_t C = NBT < target ? NBT : target;
+    if ((NBT + C - 1) / C > smax) C = (NBT + smax - 1) / smax;
+    return (int)C;
+}
+
+// aq_kw_kernel for M <= 32 over C = aq_blocks(strips, 4, 256) blocks: strips per block NS = ceil(strips / C) <= 4, row tiles
 // MT = 1 or 2.  Four waves (one per SIMD) with two tiles in flight each: against 8 or 16 waves and rings of 1 - 4
 // tiles this measured fastest at K = 4096, N = 11008 for every M in {1, 8, 16, 24, 32}, int4 and int8 (graph
 // replays; e.g. int4 7.9 / 8.7 / 12.2 us at M = 1 / 16 / 32, where 8 waves with 4 tiles in flight took 9.4 / 10.7 /
@@ -1295,7 +1303,8 @@ static hipError_t launch_aq_kw_any(uint16_t* y, const uint16_t* x, const void* w
                                    hipStream_t st)
 {
     const int64_t NBT = N / 16;
-    const int C = (int)(NBT < 256 ? NBT : 256);
+    // about 256 blocks; above 1024 strips, blocks of 4 strips (more than one block per CU)
+    const int C = aq_blocks(NBT, 4, 256);
     const int64_t ns = (NBT + C - 1) / C;
 #define AQ_KW_NS(MT)                                                                                  \
     switch (ns) {                                                                                      \
@@ -1326,13 +1335,6 @@ static void launch_dma(uint16_t* y, const uint16_t* x, const void* wp, bool int4
     }
 }
 
-// column blocks for a grid of about `target` workgroups whose blocks hold at most smax strips
-inline int aq_blocks(int64_t NBT, int smax, int target)
-{
-    int64_t C = NBT < target ? NBT : target;
-    if ((NBT + C - 1) / C > smax) C = (NBT + smax - 1) / smax;
-    return (int)C;
-}
 
 // M is processed in chunks of 64 rows (4 m tiles); decode shapes are a single launch.  The packed weight,
 // x and the scales must each stay below 2^31 bytes (buffer offsets; checked by the caller).
@@ -1377,7 +1379,10 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
         // resident in LDS for M <= 16, the LDS ring above, else the one-strip ring of aq_dma_kernel (group a
         // multiple of 128) or activations straight from memory.
         hipError_t e = hipErrorInvalidValue;
-        if (cols_ok && mc <= 32 && NBT <= 1024 && aq_cols_fit(mc, N, K, g, int4))
+        // (past 1024 strips the K-split form runs several blocks per CU: measured at K = 4096, int4, N = 32000 /
+        // 128256, M = 16 it takes 18.7 / 61.2 us against 21.4 / 77.7 us for the LDS-resident form below, while a
+        // single row stays with that form, 52.2 against 53.8 us at N = 128256)
+        if (cols_ok && mc <= 32 && (NBT <= 1024 || mc > 1) && aq_cols_fit(mc, N, K, g, int4))
             e = launch_aq_kw_any(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
         else if (cols_ok && mc <= 16 && KB % 8 == 0 && aq_xs_lds<2, 2, 4, 2>(mc, K, offset != nullptr))
             e = launch_aq_xs<2, 2, 4, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 4, 256), atomic, st);

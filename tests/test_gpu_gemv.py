@@ -129,13 +129,15 @@ def test_batch_ring_partial_rounds(ascq_gpu, oracle, w_type, M, K):
     (50, 4096, 1008, 128),
     (3, 1024, 16384, 128),   # 1024 strips: four per block
     (20, 768, 13072, 256),   # 817 strips: three or four per block, 32 rows
-    (5, 512, 16400, 128),    # 1025 strips: past the K-split blocks, x resident in LDS
-    (20, 512, 16400, 128),   # 1025 strips, 32-row LDS ring
+    (5, 512, 16400, 128),    # 1025 strips: 257 K-split blocks of up to four strips (more than one block per CU)
+    (20, 512, 16400, 128),   # 1025 strips, 32 rows
+    (1, 4096, 32000, 128),   # a vocabulary-sized N, one row: x resident in LDS
+    (16, 1024, 32000, 256),  # a vocabulary-sized N: 500 K-split blocks of four strips
 ])
 def test_column_block_kernels(ascq_gpu, oracle, w_type, with_offset, M, K, N, group):
     """Column blocks of 1 - 4 strips (sizes within one strip of each other): K-split waves with x read into registers
-    (M <= 32, up to 1024 strips), x resident in LDS (M <= 16) or streamed through an LDS ring (M > 16) beyond that;
-    group sizes 128 << s, with and without offset."""
+    (M <= 32; about 256 blocks, more above 1024 strips but for a single row), x resident in LDS (one row above 1024
+    strips) or x streamed through an LDS ring (M > 32); group sizes 128 << s, with and without offset."""
     rng = seeded(M * 7 + K + N + group)
     code = O.INT8 if w_type == "int8" else O.INT4
     at = ascq_gpu.INT8 if w_type == "int8" else ascq_gpu.INT4
