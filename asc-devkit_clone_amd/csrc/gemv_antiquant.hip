@@ -581,7 +581,7 @@ struct AqXsArgs {
     const uint16_t* offset;
     uint32_t M, N, K, KB;
     uint32_t sq, sr;  // block c has sq + (c < sr) strips, starting at strip c sq + min(c, sr)
-    uint32_t gshift;  // group size = 128 << gshift
+    uint32_t gshift;  // group size = 128 << gshift (aq_kw_kernel also takes 32 and 64: gshift 0, its SPG says which)
     uint32_t x_bytes, w_bytes, s_bytes;
     int atomic;
 };
@@ -788,14 +788,14 @@ inline bool aq_cols_fit(int64_t M, int64_t N, int64_t K, int64_t g, bool int4)
 
 // checks of the column-block and ring kernels common to both; fills the 32-bit argument block
 inline bool aq_cols_args(AqXsArgs& A, uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
-                         const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, int C, int smax, int atomic)
+                         const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, int C, int smax, int atomic,
+                         bool small_groups = false)
 {
     const int64_t NBT = N / 16, KB = K / KT;
     const uint64_t w_bytes = (uint64_t)K * N / (int4 ? 2 : 1), s_bytes = (uint64_t)((K + g - 1) / g) * N * 2;
     const uint64_t x_bytes = (uint64_t)M * K * 2;
-    if (C < 1 || C > NBT || (NBT + C - 1) / C > smax || g % KT != 0 || ((g / KT) & (g / KT - 1)) != 0 ||
-        !aq_cols_fit(M, N, K, g, int4))
-        return false;
+    const bool g_ok = (g % KT == 0 && ((g / KT) & (g / KT - 1)) == 0) || (small_groups && (g == 32 || g == 64));
+    if (C < 1 || C > NBT || (NBT + C - 1) / C > smax || !g_ok || !aq_cols_fit(M, N, K, g, int4)) return false;
     A.y = y;
     A.x = x;
     A.wp = (const uint8_t*)wp;
@@ -807,7 +807,7 @@ inline bool aq_cols_args(AqXsArgs& A, uint16_t* y, const uint16_t* x, const void
     A.KB = (uint32_t)KB;
     A.sq = (uint32_t)(NBT / C);
     A.sr = (uint32_t)(NBT % C);
-    A.gshift = (uint32_t)__builtin_ctzll((unsigned long long)(g / KT));
+    A.gshift = g >= KT ? (uint32_t)__builtin_ctzll((unsigned long long)(g / KT)) : 0u;
     A.x_bytes = (uint32_t)x_bytes;
     A.w_bytes = (uint32_t)w_bytes;
     A.s_bytes = (uint32_t)s_bytes;
@@ -1115,7 +1115,9 @@ struct AqKw {
     static_assert(LDS <= 160 * 1024, "partials fit in LDS");
 };
 
-template <int MT, int NS, int KW, int D, bool INT4, bool HAS_OFF>
+// SPG: scale / offset groups per k tile of 128 -- 1 for groups of 128 << s, 2 for 64, 4 for 32 (a lane's eight k
+// values of MFMA step j lie in group 4 kb / SPG ... of its tile: step j takes group j * SPG / 4 of the tile's SPG)
+template <int MT, int NS, int KW, int D, bool INT4, bool HAS_OFF, int SPG = 1>
 __global__ __launch_bounds__(KW * 64) void aq_kw_kernel(AqXsArgs A)
 {
     using P = AqKw<MT, NS, KW>;
@@ -1140,7 +1142,7 @@ __global__ __launch_bounds__(KW * 64) void aq_kw_kernel(AqXsArgs A)
     struct Tile {
         u32x4 w[NS][WV];
         u32x4 x[MT][4];
-        uint32_t sc[NS], of[NS];  // 16-bit values, held in 32 bits (16-bit fields of a ring slot went to scratch)
+        uint32_t sc[NS][SPG], of[NS][SPG];  // 16-bit values, held in 32 bits (16-bit fields of a ring slot went to scratch)
     };
     // Lane (kq, col_in) reads the B fragment of column col_in of each strip, the A fragments of rows 16 a + col_in
     // (k 32 j + 8 kq .. + 7 of the tile) and the scale / offset of its column.  The per-lane base offsets of tile 0
@@ -1162,7 +1164,7 @@ __global__ __launch_bounds__(KW * 64) void aq_kw_kernel(AqXsArgs A)
     const uint32_t n2 = N * 2;
     auto issue = [&](uint32_t t, Tile& r) {
         const uint32_t past = (T - 1 - t) & 0x80000000u;  // t >= T (both below 2^31)
-        const uint32_t sg = ((t0 + t) >> A.gshift) * n2;
+        const uint32_t sg = (SPG == 1 ? (t0 + t) >> A.gshift : (t0 + t) * SPG) * n2;
 #pragma unroll
         for (int b = 0; b < NS; ++b) {
             const uint32_t off = (wb[b] + t * TILE_BYTES) | past;
@@ -1176,11 +1178,13 @@ __global__ __launch_bounds__(KW * 64) void aq_kw_kernel(AqXsArgs A)
             for (int j = 0; j < 4; ++j) r.x[a][j] = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 64 * j, 0, 0);
         }
 #pragma unroll
-        for (int b = 0; b < NS; ++b) {
-            const uint32_t off = (sbo[b] + sg) | past;
-            r.sc[b] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
-            if constexpr (HAS_OFF) r.of[b] = __builtin_amdgcn_raw_buffer_load_b16(ro, off, 0, 0);
-        }
+        for (int b = 0; b < NS; ++b)
+#pragma unroll
+            for (int q = 0; q < SPG; ++q) {
+                const uint32_t off = (sbo[b] + sg + q * n2) | past;
+                r.sc[b][q] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+                if constexpr (HAS_OFF) r.of[b][q] = __builtin_amdgcn_raw_buffer_load_b16(ro, off, 0, 0);
+            }
     };
 
     v4f acc[MT][NS];
@@ -1189,18 +1193,21 @@ __global__ __launch_bounds__(KW * 64) void aq_kw_kernel(AqXsArgs A)
 #pragma unroll
         for (int b = 0; b < NS; ++b) acc[a][b] = (v4f){0.f, 0.f, 0.f, 0.f};
     auto compute = [&](const Tile& r) {
-        h2 s2[NS], o2[NS];
+        h2 s2[NS][SPG], o2[NS][SPG];
 #pragma unroll
-        for (int b = 0; b < NS; ++b) {
-            const _Float16 sv = __builtin_bit_cast(_Float16, (uint16_t)r.sc[b]);
-            const _Float16 ov = HAS_OFF ? __builtin_bit_cast(_Float16, (uint16_t)r.of[b]) : (_Float16)0.0f;
-            s2[b] = (h2){sv, sv};
-            o2[b] = (h2){ov, ov};
-        }
+        for (int b = 0; b < NS; ++b)
+#pragma unroll
+            for (int q = 0; q < SPG; ++q) {
+                const _Float16 sv = __builtin_bit_cast(_Float16, (uint16_t)r.sc[b][q]);
+                const _Float16 ov = HAS_OFF ? __builtin_bit_cast(_Float16, (uint16_t)r.of[b][q]) : (_Float16)0.0f;
+                s2[b][q] = (h2){sv, sv};
+                o2[b][q] = (h2){ov, ov};
+            }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int b = 0; b < NS; ++b) {
+                constexpr int JPG = 4 / SPG;  // MFMA steps per group
                 uint32_t w0, w1 = 0;
                 if constexpr (INT4) {
                     w0 = r.w[b][0][j];
@@ -1208,7 +1215,7 @@ __global__ __launch_bounds__(KW * 64) void aq_kw_kernel(AqXsArgs A)
                     w0 = r.w[b][j >> 1][(j & 1) * 2];
                     w1 = r.w[b][j >> 1][(j & 1) * 2 + 1];
                 }
-                const h8 bf = dequant8<INT4, HAS_OFF>(w0, w1, o2[b], s2[b], magic);
+                const h8 bf = dequant8<INT4, HAS_OFF>(w0, w1, o2[b][j / JPG], s2[b][j / JPG], magic);
 #pragma unroll
                 for (int a = 0; a < MT; ++a)
                     acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, r.x[a][j]), bf, acc[a][b],
@@ -1257,18 +1264,19 @@ __global__ __launch_bounds__(KW * 64) void aq_kw_kernel(AqXsArgs A)
     }
 }
 
-template <int MT, int NS, int KW, int D>
+template <int MT, int NS, int KW, int D, int SPG>
 static hipError_t launch_aq_kw(uint16_t* y, const uint16_t* x, const void* wp, bool int4, const uint16_t* scale,
                                const uint16_t* offset, int64_t g, int64_t M, int64_t N, int64_t K, int C, int atomic,
                                hipStream_t st)
 {
     using P = AqKw<MT, NS, KW>;
     AqXsArgs A;
-    if (M > 16 * MT || !aq_cols_args(A, y, x, wp, int4, scale, offset, g, M, N, K, C, NS, atomic))
+    if (M > 16 * MT || (SPG == 1 ? g < KT : g != KT / SPG) ||
+        !aq_cols_args(A, y, x, wp, int4, scale, offset, g, M, N, K, C, NS, atomic, SPG > 1))
         return hipErrorInvalidValue;
 #define AQ_KW_LAUNCH(I4, OF)                                                    \
     do {                                                                        \
-        constexpr auto kern = aq_kw_kernel<MT, NS, KW, D, I4, OF>;               \
+        constexpr auto kern = aq_kw_kernel<MT, NS, KW, D, I4, OF, SPG>;          \
         hipError_t e = ensure_dynamic_lds<kern>(P::LDS);                        \
         if (e != hipSuccess) return e;                                          \
         launch_k(kern, dim3((unsigned)C), dim3(P::NT), (uint32_t)P::LDS, st, A); \
@@ -1306,18 +1314,26 @@ static hipError_t launch_aq_kw_any(uint16_t* y, const uint16_t* x, const void* w
     // about 256 blocks; above 1024 strips, blocks of 4 strips (more than one block per CU)
     const int C = aq_blocks(NBT, 4, 256);
     const int64_t ns = (NBT + C - 1) / C;
-#define AQ_KW_NS(MT)                                                                                  \
-    switch (ns) {                                                                                      \
-    case 1: return launch_aq_kw<MT, 1, 4, 2>(y, x, wp, int4, scale, offset, g, M, N, K, C, atomic, st); \
-    case 2: return launch_aq_kw<MT, 2, 4, 2>(y, x, wp, int4, scale, offset, g, M, N, K, C, atomic, st); \
-    case 3: return launch_aq_kw<MT, 3, 4, 2>(y, x, wp, int4, scale, offset, g, M, N, K, C, atomic, st); \
-    case 4: return launch_aq_kw<MT, 4, 4, 2>(y, x, wp, int4, scale, offset, g, M, N, K, C, atomic, st); \
-    default: return hipErrorInvalidValue;                                                            \
+#define AQ_KW_NS(MT, SPG)                                                                                  \
+    switch (ns) {                                                                                           \
+    case 1: return launch_aq_kw<MT, 1, 4, 2, SPG>(y, x, wp, int4, scale, offset, g, M, N, K, C, atomic, st); \
+    case 2: return launch_aq_kw<MT, 2, 4, 2, SPG>(y, x, wp, int4, scale, offset, g, M, N, K, C, atomic, st); \
+    case 3: return launch_aq_kw<MT, 3, 4, 2, SPG>(y, x, wp, int4, scale, offset, g, M, N, K, C, atomic, st); \
+    case 4: return launch_aq_kw<MT, 4, 4, 2, SPG>(y, x, wp, int4, scale, offset, g, M, N, K, C, atomic, st); \
+    default: return hipErrorInvalidValue;                                                                 \
     }
-    if (M <= 16) { AQ_KW_NS(1) }
-    if (M <= 32) { AQ_KW_NS(2) }
+#define AQ_KW_MT(SPG)                 \
+    do {                              \
+        if (M <= 16) { AQ_KW_NS(1, SPG) } \
+        if (M <= 32) { AQ_KW_NS(2, SPG) } \
+        return hipErrorInvalidValue;  \
+    } while (0)
+    // groups of 32 / 64 take 4 / 2 scale and offset rows per k tile of 128
+    if (g == 32) AQ_KW_MT(4);
+    if (g == 64) AQ_KW_MT(2);
+    AQ_KW_MT(1);
+#undef AQ_KW_MT
 #undef AQ_KW_NS
-    return hipErrorInvalidValue;
 }
 
 template <int MT, int NS, int KSW, int ST, bool ROT, int DW = ST>
@@ -1382,7 +1398,8 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
         // (past 1024 strips the K-split form runs several blocks per CU: measured at K = 4096, int4, N = 32000 /
         // 128256, M = 16 it takes 18.7 / 61.2 us against 21.4 / 77.7 us for the LDS-resident form below, while a
         // single row stays with that form, 52.2 against 53.8 us at N = 128256)
-        if (cols_ok && mc <= 32 && (NBT <= 1024 || mc > 1) && aq_cols_fit(mc, N, K, g, int4))
+        if ((cols_ok || g == 32 || g == 64) && mc <= 32 && (NBT <= 1024 || mc > 1 || !cols_ok) &&
+            aq_cols_fit(mc, N, K, g, int4))
             e = launch_aq_kw_any(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
         else if (cols_ok && mc <= 16 && KB % 8 == 0 && aq_xs_lds<2, 2, 4, 2>(mc, K, offset != nullptr))
             e = launch_aq_xs<2, 2, 4, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 4, 256), atomic, st);
