@@ -1322,13 +1322,15 @@ static hipError_t launch_aq_kw_any(uint16_t* y, const uint16_t* x, const void* w
     case 4: return launch_aq_kw<MT, 4, 4, 2, SPG>(y, x, wp, int4, scale, offset, g, M, N, K, C, atomic, st); \
     default: return hipErrorInvalidValue;                                                                 \
     }
-#define AQ_KW_MT(SPG)                 \
-    do {                              \
-        if (M <= 16) { AQ_KW_NS(1, SPG) } \
-        if (M <= 32) { AQ_KW_NS(2, SPG) } \
-        return hipErrorInvalidValue;  \
+#define AQ_KW_MT(SPG)                                  \
+    do {                                               \
+        if (M <= 16) { AQ_KW_NS(1, SPG) }                  \
+        if (M <= 32) { AQ_KW_NS(2, SPG) }                  \
+        if (SPG > 1 && M <= 64) { AQ_KW_NS(4, SPG) }       \
+        return hipErrorInvalidValue;                   \
     } while (0)
-    // groups of 32 / 64 take 4 / 2 scale and offset rows per k tile of 128
+    // groups of 32 / 64 take 4 / 2 scale and offset rows per k tile of 128, and batches up to 64 rows (the LDS ring
+    // of the larger batches holds every scale row of K in LDS, which groups this small do not fit)
     if (g == 32) AQ_KW_MT(4);
     if (g == 64) AQ_KW_MT(2);
     AQ_KW_MT(1);
@@ -1398,7 +1400,7 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
         // (past 1024 strips the K-split form runs several blocks per CU: measured at K = 4096, int4, N = 32000 /
         // 128256, M = 16 it takes 18.7 / 61.2 us against 21.4 / 77.7 us for the LDS-resident form below, while a
         // single row stays with that form, 52.2 against 53.8 us at N = 128256)
-        if ((cols_ok || g == 32 || g == 64) && mc <= 32 && (NBT <= 1024 || mc > 1 || !cols_ok) &&
+        if ((cols_ok || g == 32 || g == 64) && (mc <= 32 || !cols_ok) && (NBT <= 1024 || mc > 1 || !cols_ok) &&
             aq_cols_fit(mc, N, K, g, int4))
             e = launch_aq_kw_any(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
         else if (cols_ok && mc <= 16 && KB % 8 == 0 && aq_xs_lds<2, 2, 4, 2>(mc, K, offset != nullptr))

@@ -137,12 +137,14 @@ def test_batch_ring_partial_rounds(ascq_gpu, oracle, w_type, M, K):
     (16, 2048, 4112, 64),    # groups of 64: two per k tile
     (29, 1536, 2000, 32),
     (2, 512, 16400, 64),     # groups of 64 past 1024 strips, one row
+    (40, 2048, 1008, 32),    # groups of 32 / 64 above 32 rows: the K-split blocks with four row tiles
+    (64, 1024, 4112, 64),
 ])
 def test_column_block_kernels(ascq_gpu, oracle, w_type, with_offset, M, K, N, group):
     """Column blocks of 1 - 4 strips (sizes within one strip of each other): K-split waves with x read into registers
     (M <= 32; about 256 blocks, more above 1024 strips but for a single row), x resident in LDS (one row above 1024
-    strips) or x streamed through an LDS ring (M > 32); group sizes 128 << s, and 32 / 64 (the K-split blocks), with
-    and without offset."""
+    strips) or x streamed through an LDS ring (M > 32); group sizes 128 << s, and 32 / 64 (the K-split blocks up to
+    64 rows), with and without offset."""
     rng = seeded(M * 7 + K + N + group)
     code = O.INT8 if w_type == "int8" else O.INT4
     at = ascq_gpu.INT8 if w_type == "int8" else ascq_gpu.INT4
