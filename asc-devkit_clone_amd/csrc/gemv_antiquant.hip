@@ -581,7 +581,8 @@ struct AqXsArgs {
     const uint16_t* offset;
     uint32_t M, N, K, KB;
     uint32_t sq, sr;  // block c has sq + (c < sr) strips, starting at strip c sq + min(c, sr)
-    uint32_t gshift;  // group size = 128 << gshift (aq_kw_kernel also takes 32 and 64: gshift 0, its SPG says which)
+    uint32_t gshift;  // group size = 128 << gshift; 31: one group over all of K (aq_kw_kernel also takes 32 and 64:
+                      // gshift 0, its SPG says which)
     uint32_t x_bytes, w_bytes, s_bytes;
     int atomic;
 };
@@ -794,7 +795,9 @@ inline bool aq_cols_args(AqXsArgs& A, uint16_t* y, const uint16_t* x, const void
     const int64_t NBT = N / 16, KB = K / KT;
     const uint64_t w_bytes = (uint64_t)K * N / (int4 ? 2 : 1), s_bytes = (uint64_t)((K + g - 1) / g) * N * 2;
     const uint64_t x_bytes = (uint64_t)M * K * 2;
-    const bool g_ok = (g % KT == 0 && ((g / KT) & (g / KT - 1)) == 0) || (small_groups && (g == 32 || g == 64));
+    // groups of 128 << s, one group over all of K (per channel), or (the K-split kernel) 32 / 64
+    const bool g_ok = (g % KT == 0 && ((g / KT) & (g / KT - 1)) == 0) || (g >= K && K % KT == 0) ||
+                      (small_groups && (g == 32 || g == 64));
     if (C < 1 || C > NBT || (NBT + C - 1) / C > smax || !g_ok || !aq_cols_fit(M, N, K, g, int4)) return false;
     A.y = y;
     A.x = x;
@@ -807,7 +810,7 @@ inline bool aq_cols_args(AqXsArgs& A, uint16_t* y, const uint16_t* x, const void
     A.KB = (uint32_t)KB;
     A.sq = (uint32_t)(NBT / C);
     A.sr = (uint32_t)(NBT % C);
-    A.gshift = g >= KT ? (uint32_t)__builtin_ctzll((unsigned long long)(g / KT)) : 0u;
+    A.gshift = g >= K ? 31u : g >= KT ? (uint32_t)__builtin_ctzll((unsigned long long)(g / KT)) : 0u;
     A.x_bytes = (uint32_t)x_bytes;
     A.w_bytes = (uint32_t)w_bytes;
     A.s_bytes = (uint32_t)s_bytes;
@@ -896,7 +899,9 @@ __global__ __launch_bounds__(SG * KW * 64) void aq_ring_kernel(AqXsArgs A)
     const uint32_t row0 = blockIdx.y * (uint32_t)P::ROWS;  // this block's first row (row blocks of 16 MT rows)
     const uint32_t s0 = cb * A.sq + (cb < A.sr ? cb : A.sr), s1 = s0 + A.sq + (cb < A.sr ? 1u : 0u);
     const uint32_t sb = s0 + (uint32_t)(sg * NBW);  // first strip of this wave
-    const uint32_t rounds = KB / KW;                // KB % KW == 0
+    // rounds of KW k tiles; when KW does not divide KB the last round is partial: its tiles past KB read zeros
+    // (weights, activations and scale / offset alike, so they add exact zeros)
+    const uint32_t rounds = (KB + KW - 1) / KW;
     const uint32_t ncp = (rounds + TPC - 1) / TPC;  // scale copies per wave
     // LDS: ST activation stages | scale rows of each wave [ncp][256 B] | offset rows of each wave
     const uint32_t sc_at = ST * P::SLOT, wsb = ncp * 256;
@@ -911,7 +916,7 @@ __global__ __launch_bounds__(SG * KW * 64) void aq_ring_kernel(AqXsArgs A)
     for (uint32_t c = 0; c < ncp; ++c) {
         const uint32_t i = c * TPC + (uint32_t)lane / WPT, wd = (uint32_t)lane % WPT;
         const uint32_t kt = i * KW + (uint32_t)kw;
-        const bool ok = (uint32_t)lane < TPC * WPT && i < rounds && 2 * wd < (s1 > sb ? (s1 - sb) * 16 : 0u);
+        const bool ok = (uint32_t)lane < TPC * WPT && i < rounds && kt < KB && 2 * wd < (s1 > sb ? (s1 - sb) * 16 : 0u);
         const uint32_t voff = ok ? ((kt >> A.gshift) * N * 2 + wd * 4) : AQ_OOB;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(smem + sc_at + wave * wsb + c * 256), 4, voff, (int)(sb * 32), 0, 0);
         if constexpr (HAS_OFF)
@@ -926,7 +931,8 @@ __global__ __launch_bounds__(SG * KW * 64) void aq_ring_kernel(AqXsArgs A)
             const uint32_t q = gcopy * 64 + lane;
             const uint32_t row = q / P::CH, p = q % P::CH;
             const uint32_t c = p ^ (row & 15u);  // logical chunk held at physical chunk p
-            const uint32_t off = row0 + row < M && r < rounds ? ((row0 + row) * A.K + r * KW * KT + c * 8) * 2 : AQ_OOB;
+            const uint32_t k = r * KW * KT + c * 8;
+            const uint32_t off = row0 + row < M && r < rounds && k < A.K ? ((row0 + row) * A.K + k) * 2 : AQ_OOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(smem + slot * P::SLOT + gcopy * 1024), 16, off, 0, 0, 0);
         }
     };
@@ -938,7 +944,7 @@ __global__ __launch_bounds__(SG * KW * 64) void aq_ring_kernel(AqXsArgs A)
 #pragma unroll
         for (int b = 0; b < NBW; ++b) {
             const uint32_t s = sb + b;
-            const uint32_t off = r < rounds && s < s1 ? (s * KB + kt) * TILE_BYTES + lane * LANE_BYTES : AQ_OOB;
+            const uint32_t off = r < rounds && kt < KB && s < s1 ? (s * KB + kt) * TILE_BYTES + lane * LANE_BYTES : AQ_OOB;
 #pragma unroll
             for (int v = 0; v < WV; ++v) t.w[b][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, off + 16 * v, 0, 0);
         }
@@ -1063,7 +1069,7 @@ template <int MT, int NBW, int SG, int KW, int ST, int DW>
 inline int64_t aq_ring_lds(int64_t K, bool has_off)
 {
     using P = AqRing<MT, NBW, SG, KW, ST, DW, true, true>;
-    const int64_t rounds = K / KT / KW, ncp = (rounds + P::TPC - 1) / P::TPC;
+    const int64_t rounds = (K / KT + KW - 1) / KW, ncp = (rounds + P::TPC - 1) / P::TPC;
     const int64_t lds = std::max<int64_t>((int64_t)ST * P::SLOT + (int64_t)P::NW * ncp * 256 * (has_off ? 2 : 1), P::RED);
     return lds <= 160 * 1024 ? lds : 0;
 }
@@ -1076,7 +1082,7 @@ static hipError_t launch_aq_ring(uint16_t* y, const uint16_t* x, const void* wp,
     using P4 = AqRing<MT, NBW, SG, KW, ST, DW, true, true>;
     AqXsArgs A;
     const int64_t lds = aq_ring_lds<MT, NBW, SG, KW, ST, DW>(K, offset != nullptr);
-    if ((K / KT) % KW != 0 || lds == 0 || !aq_cols_args(A, y, x, wp, int4, scale, offset, g, M, N, K, C, SG * NBW, atomic))
+    if (K % KT != 0 || lds == 0 || !aq_cols_args(A, y, x, wp, int4, scale, offset, g, M, N, K, C, SG * NBW, atomic))
         return hipErrorInvalidValue;
     const unsigned RB = (unsigned)((M + 16 * MT - 1) / (16 * MT));  // row blocks (grid.y)
 #define AQ_RING_LAUNCH(I4, OF)                                                     \
@@ -1363,23 +1369,28 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
     const int64_t g = group > 0 ? group : K;
     const bool int4 = w_type == DT_INT4;
     const int64_t NBT = N / 16, KB = K / KT;
-    const bool cols_ok = g % KT == 0 && ((g / KT) & (g / KT - 1)) == 0;  // column-block kernels: group 128 << s
+    // column-block kernels: groups of 128 << s, or one group over all of K (per channel)
+    const bool cols_ok = K % KT == 0 && ((g % KT == 0 && ((g / KT) & (g / KT - 1)) == 0) || g >= K);
     // Above 64 rows: aq_ring_kernel over row blocks (grid.y) -- x shared through the LDS ring by the strip groups of a
     // block, each weight fragment dequantised once per block of rows and multiplied against all of them.  64-row
     // blocks of 6 strips (2 strip groups x 4 k-split waves) while they make about one block per CU, else 128-row blocks
     // of 12 strips (4 strip groups x 2 k-split waves).  Measured at K = 4096, N = 11008 (int4 / int8, M = 128 / 512 /
     // 2048): 27 / 63 / 239 us against 71 / 78 / 250 us for the LDS-staged MFMA GEMM of aq_gemm.hip, which takes the
-    // shapes the ring does not (K not a multiple of 256 or 512, LDS too small for the scale rows), then 64-row passes
-    // of the kernels below.
+    // shapes the ring does not (LDS too small for the scale rows), then 64-row passes of the kernels below.  When KW does
+    // not divide the k tiles (K = 11008: 86 tiles) the ring's last round is partial.
     if (M > 64 && cols_ok) {
         const int64_t rb64 = (M + 63) / 64, rb128 = (M + 127) / 128;
         const int c64 = aq_blocks(NBT, 6, (int)((256 + rb64 - 1) / rb64));
         hipError_t e = hipErrorInvalidValue;
-        if (c64 * rb64 <= 320 && KB % 4 == 0 && aq_ring_lds<4, 3, 2, 4, 2, 2>(K, offset != nullptr))
+        if (c64 * rb64 <= 320 && aq_ring_lds<4, 3, 2, 4, 2, 2>(K, offset != nullptr))
             e = launch_aq_ring<4, 3, 2, 4, 2, 2>(y, x, wp, int4, scale, offset, g, M, N, K, c64, atomic, st);
-        else if (KB % 2 == 0 && aq_ring_lds<8, 3, 4, 2, 2, 2>(K, offset != nullptr))
+        else if (aq_ring_lds<8, 3, 4, 2, 2, 2>(K, offset != nullptr))
             e = launch_aq_ring<8, 3, 4, 2, 2, 2>(y, x, wp, int4, scale, offset, g, M, N, K,
                                                  aq_blocks(NBT, 12, (int)((256 + rb128 - 1) / rb128)), atomic, st);
+        // long K with a scale row per k tile (K = 11008, g = 128: 86 rows) leaves both forms above without LDS for
+        // the scale rows; 64-row blocks of two k-split waves halve the activation stages
+        else if (aq_ring_lds<4, 3, 2, 2, 2, 2>(K, offset != nullptr))
+            e = launch_aq_ring<4, 3, 2, 2, 2, 2>(y, x, wp, int4, scale, offset, g, M, N, K, c64, atomic, st);
         if (e == hipErrorInvalidValue) {
             (void)hipGetLastError();
             e = launch_aq_gemm(y, x, wp, w_type, scale, offset, group, M, N, K, atomic, st);
@@ -1407,11 +1418,11 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
             e = launch_aq_xs<2, 2, 4, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 4, 256), atomic, st);
         else if (cols_ok && mc <= 16 && KB % 4 == 0 && aq_xs_lds<2, 2, 4, 1>(mc, K, offset != nullptr))
             e = launch_aq_xs<2, 2, 4, 1>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 4, 256), atomic, st);
-        else if (cols_ok && mc > 16 && mc <= 32 && KB % 8 == 0 && aq_ring_lds<2, 3, 1, 8, 2, 2>(K, offset != nullptr))
+        else if (cols_ok && mc > 16 && mc <= 32 && aq_ring_lds<2, 3, 1, 8, 2, 2>(K, offset != nullptr))
             e = launch_aq_ring<2, 3, 1, 8, 2, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 3, 256), atomic, st);
         // (32 < M <= 64: 2 strip groups x 4 k-split waves, weights 1 round ahead, about 256 blocks of <= 4 strips;
         // measured against 172 blocks with 3 rounds ahead and seven other splits: W4 M = 64 17.7 against 18.5-28 us)
-        else if (cols_ok && mc > 32 && KB % 4 == 0 && aq_ring_lds<4, 2, 2, 4, 2, 2>(K, offset != nullptr))
+        else if (cols_ok && mc > 32 && aq_ring_lds<4, 2, 2, 4, 2, 2>(K, offset != nullptr))
             e = launch_aq_ring<4, 2, 2, 4, 2, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 4, 256), atomic, st);
         else {
             if (mc <= 4 && mc * K * 2 + 16 <= 48 * 1024) {

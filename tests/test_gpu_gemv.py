@@ -158,6 +158,31 @@ def test_column_block_kernels(ascq_gpu, oracle, w_type, with_offset, M, K, N, gr
 
 
 @pytest.mark.parametrize("w_type", ["int4", "int8"])
+@pytest.mark.parametrize("M,K,N,group", [
+    (1, 1408, 272, 0),       # per channel (one group over K), 11 k tiles: K-split waves with uneven tile counts
+    (16, 1408, 272, 0),
+    (40, 1408, 272, 0),      # LDS ring of four k-split waves: a partial last round (11 = 2 x 4 + 3)
+    (100, 1408, 272, 0),     # row blocks of the ring, partial last round
+    (40, 11008, 4096, 128),  # a down projection: 86 k tiles (4 does not divide them), 256 strips
+    (200, 11008, 4096, 0),
+    (256, 11008, 4096, 128), # 86 scale rows: 64-row blocks of two k-split waves (the wider forms lack LDS for them)
+])
+def test_partial_rounds_and_per_channel(ascq_gpu, oracle, w_type, M, K, N, group):
+    """per-channel scales (group 0: one group over all of K) on the column-block kernels, and k-tile counts that the
+    ring's k-split waves do not divide (its last round partial: the tiles past K read zeros)"""
+    rng = seeded(M + K + N + group)
+    code = O.INT8 if w_type == "int8" else O.INT4
+    at = ascq_gpu.INT8 if w_type == "int8" else ascq_gpu.INT4
+    w, scale, offset = make_weights(rng, K, N, code, group)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    wp = ascq_gpu.weight_pack(_dev(w), at, K, N)
+    y = ascq_gpu.antiquant_matmul(_dev(x), wp, at, _dev(scale), _dev(offset), group, N)
+    _, y_exact, y_abs = O.antiquant_matmul(x.view(np.uint16), w, code, scale.view(np.uint16), offset.view(np.uint16),
+                                           group, M, N, K)
+    check_close(y.cpu().numpy(), y_exact, y_abs, K)
+
+
+@pytest.mark.parametrize("w_type", ["int4", "int8"])
 @pytest.mark.parametrize("with_offset", [True, False])
 @pytest.mark.parametrize("M,K,N,group", [
     (65, 512, 112, 128),      # one row past the decode kernels; a single column block narrower than the tile
