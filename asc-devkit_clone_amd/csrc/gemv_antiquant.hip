@@ -1332,11 +1332,11 @@ static hipError_t launch_aq_kw_any(uint16_t* y, const uint16_t* x, const void* w
     do {                                               \
         if (M <= 16) { AQ_KW_NS(1, SPG) }                  \
         if (M <= 32) { AQ_KW_NS(2, SPG) }                  \
-        if (SPG > 1 && M <= 64) { AQ_KW_NS(4, SPG) }       \
+        if (M <= 64) { AQ_KW_NS(4, SPG) }                  \
         return hipErrorInvalidValue;                   \
     } while (0)
-    // groups of 32 / 64 take 4 / 2 scale and offset rows per k tile of 128, and batches up to 64 rows (the LDS ring
-    // of the larger batches holds every scale row of K in LDS, which groups this small do not fit)
+    // groups of 32 / 64 take 4 / 2 scale and offset rows per k tile of 128; batches up to 64 rows where the LDS ring
+    // (which holds every scale row of K in LDS) does not fit: groups this small, or a long K
     if (g == 32) AQ_KW_MT(4);
     if (g == 64) AQ_KW_MT(2);
     AQ_KW_MT(1);
@@ -1424,6 +1424,11 @@ hipError_t launch_antiquant_matmul(uint16_t* y, const uint16_t* x, const void* w
         // measured against 172 blocks with 3 rounds ahead and seven other splits: W4 M = 64 17.7 against 18.5-28 us)
         else if (cols_ok && mc > 32 && aq_ring_lds<4, 2, 2, 4, 2, 2>(K, offset != nullptr))
             e = launch_aq_ring<4, 2, 2, 4, 2, 2>(yc, xc, wp, int4, scale, offset, g, mc, N, K, aq_blocks(NBT, 4, 256), atomic, st);
+        // (a long K with a scale row per k tile leaves the ring no LDS for them: the K-split blocks with four row
+        // tiles, measured at K = 28672, N = 8192, int4: M = 40 / 64 in 83 / 108 us against 122 / 122 us for a ring of
+        // two k-split waves)
+        else if (cols_ok && mc > 32 && aq_cols_fit(mc, N, K, g, int4))
+            e = launch_aq_kw_any(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);
         else {
             if (mc <= 4 && mc * K * 2 + 16 <= 48 * 1024) {
                 if (int4) launch_aq<1, 1, 4, 8, true>(yc, xc, wp, int4, scale, offset, g, mc, N, K, atomic, st);

@@ -166,6 +166,7 @@ def test_column_block_kernels(ascq_gpu, oracle, w_type, with_offset, M, K, N, gr
     (40, 11008, 4096, 128),  # a down projection: 86 k tiles (4 does not divide them), 256 strips
     (200, 11008, 4096, 0),
     (256, 11008, 4096, 128), # 86 scale rows: 64-row blocks of two k-split waves (the wider forms lack LDS for them)
+    (48, 28672, 1024, 128),  # 224 scale rows at 48 rows: no LDS for the ring, the K-split blocks with four row tiles
 ])
 def test_partial_rounds_and_per_channel(ascq_gpu, oracle, w_type, M, K, N, group):
     """per-channel scales (group 0: one group over all of K) on the column-block kernels, and k-tile counts that the
