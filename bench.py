@@ -11,7 +11,10 @@ layouts), the MX-FP4 8192^3 GEMM and the fp8 / MX-FP8 8192^3 GEMMs, and -- for s
 vendor BLAS (hipBLASLt through torch) on the int8 and fp8 8192^3 shapes.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                  [--only all|headline|quant|w8a8|gemv|group|mx|fp8|vendor|traffic]
+                  [--only all|headline|quant|w8a8|gemv|group|mx|fp8|vendor|traffic|shapes]
+
+`--only shapes` (not part of the default run) times the weight-only matmul over model shapes (attention and MLP
+projections of 7B / 13B / 70B-class models) at M = 1 / 16 / 64 / 512.
 """
 from __future__ import annotations
 
@@ -391,6 +394,38 @@ def bench_gemv(torch, ascq, w_type, M, iters):
                 frac_of_peak=gbs / HBM_PEAK_GBS, tflops=2 * M * N * K / (ms * 1e-3) / 1e12,
                 timing="HIP graph of the calls (weights rotating), replayed" if USE_GRAPH else "eager calls",
                 eager_ms=eager)
+
+
+def bench_wo_shape(torch, ascq, K, N, M, iters, grp=128, w_type=None):
+    """weight-only matmul (int4, g = 128 f16 scale + offset) at one model shape: the same call as the decode GEMV and
+    prefill lines, weights rotating past the Infinity Cache, timed as a HIP graph of the calls replayed"""
+    w_type = ascq.INT4 if w_type is None else w_type
+    g = torch.Generator(device="cuda")
+    g.manual_seed(9)
+    G = K // grp
+    wb = K * N // (2 if w_type == ascq.INT4 else 1)
+    R = rotation(wb + 4 * G * N)
+    wps = [torch.randint(0, 256, (wb,), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8)
+           for _ in range(R)]
+    sc = torch.exp(torch.empty((G, N), device="cuda").uniform_(np.log(1e-3), np.log(1e-1), generator=g)).half()
+    of = torch.empty((G, N), device="cuda").uniform_(-8, 8, generator=g).half()
+    x = torch.randn((M, K), generator=g, device="cuda").half()
+    y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+
+    def fn(i):
+        ascq.antiquant_matmul(x, wps[i % R], w_type, sc, of, grp, N, out=y)
+
+    ms, eager = _time_graph(torch, fn, iters, y)
+    tf = 2 * M * N * K / (ms * 1e-3) / 1e12
+    gbs = (K * N // 2 + 4 * G * N + 2 * M * K + 2 * M * N) / (ms * 1e-3) / 1e9
+    return dict(workload=f"W4A16 weight-only matmul K={K} N={N} M={M} g={grp}", ms=ms, value=tf, unit="TFLOPS",
+                frac_of_peak=tf / F16_PEAK_TFLOPS, gbs=round(gbs, 1), eager_ms=eager)
+
+
+# model shapes of the weight-only matmul (attention and MLP projections of 7B / 13B / 70B-class models), opt-in:
+# `--only shapes`
+WO_SHAPES = [(4096, 4096), (4096, 11008), (11008, 4096), (5120, 13824), (13824, 5120), (8192, 8192), (8192, 28672),
+             (28672, 8192)]
 
 
 def bench_group(torch, ascq, iters, w_trans=False):
@@ -810,6 +845,8 @@ OTHER = {
            lambda t, a: bench_mx_e1m2_sample(t, a, 10)],
     "fp8": [lambda t, a: bench_fp8(t, a, 10, True), lambda t, a: bench_fp8(t, a, 5, False),
             lambda t, a: bench_mxfp8(t, a, 10)],
+    "shapes": [lambda t, a, k=k, n=n, m=m: bench_wo_shape(t, a, k, n, m, 50 if m < 512 else 10)
+               for k, n in WO_SHAPES for m in (1, 16, 64, 512)],
 }
 
 
@@ -870,7 +907,8 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true",
                     help="time the launch-bound lines (decode GEMV, the W8A8 sample) eagerly, without a HIP graph")
     ap.add_argument("--only", default="all",
-                    choices=["all", "headline", "quant", "w8a8", "gemv", "group", "mx", "fp8", "vendor", "traffic"],
+                    choices=["all", "headline", "quant", "w8a8", "gemv", "group", "mx", "fp8", "vendor", "traffic",
+                             "shapes"],
                     help="run one workload family (the JSON contract line is printed for all / headline)")
     args = ap.parse_args()
     global USE_GRAPH
@@ -888,7 +926,7 @@ def main() -> int:
     if args.only == "traffic":
         print(json.dumps(traffic_probe(torch, ascq)))
         return 0
-    if args.only in ("quant", "w8a8", "gemv", "group", "mx", "fp8", "vendor"):
+    if args.only in ("quant", "w8a8", "gemv", "group", "mx", "fp8", "vendor", "shapes"):
         print(json.dumps({"other_configs": run_others(torch, ascq, args.only, with_cpu=not args.no_cpu)}))
         return 0
     h = bench_headline(torch, ascq, args.steps, args.warmup)
