@@ -424,8 +424,14 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
         // that at least 32 workgroups share the work
         const bool tiny = ((a.M + 63) / 64) * ((a.N + 127) / 128) < 32;
         // ... and, when K holds four 64-byte stages per wave and C is stored (not combined by enAtomic), each tile's K
-        // split over four waves of one workgroup, so a tile's loads are all in flight at once
-        const bool ksplit = tiny && a.K % 256 == 0 && a.atomic == C_STORE;
+        // split over four waves of one workgroup, so a tile's loads are all in flight at once.  Decode-sized batches
+        // (B streamed once) take the same tiles up to 32 rows, and up to 64 while 64 x 64 tiles would leave fewer than
+        // 160 workgroups (measured, DEQF16: K = 11008, N = 4096, M = 1 / 16 / 64 in 15.6 / 21.0 / 25.5 us against
+        // 35.4 / 35.5 / 44.5 us on 64 x 64 tiles; at K = 4096, N = 11008, M = 64 the 172 tiles of 64 x 64 keep it, 18.8
+        // against 21.4 us)
+        const int64_t t64 = ((a.M + 63) / 64) * ((a.N + 63) / 64);
+        const bool skinny = a.M <= 32 || (a.M <= 64 && t64 < 160);
+        const bool ksplit = (tiny || skinny) && a.K % 256 == 0 && a.atomic == C_STORE;
         if (ksplit && a.trans_b) return launch_tiled<32, 32, 1, 1, 4, true, 64, false, 4>(a, st);
         if (ksplit && a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0)
             return launch_tiled<32, 32, 1, 1, 4, false, 64, true, 4>(a, st);
