@@ -68,14 +68,19 @@ __device__ __forceinline__ void store_f8_out(void* C, int c_type, int64_t o, flo
 template <int FMT>
 constexpr int op_of_fmt = (FMT == (FMT_BF16 | (FMT_BF16 << 3))) ? OP_BF16 : OP_F8;
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT, bool UA = false>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
+// KW > 1 (one-wave tiles, B K-contiguous, f32 / f16 / bf16 C stored, not combined by enAtomic): the workgroup's KW
+// waves each run the tile's main loop on their own K / KW range in their own LDS ring, then wave 0 adds the other
+// waves' fp32 accumulators in wave order (one fixed order, so the result does not vary between calls) and runs the
+// epilogue.  For decode-sized batches this puts a tile's whole K in flight at once instead of one serial ring.
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT, bool UA = false, int KW = 1>
+__global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_f8_kernel(GemmF8Args p)
 {
     constexpr int OP = op_of_fmt<FMT>;
     constexpr int ES = OP == OP_BF16 ? 2 : 1;  // bytes per operand element
     // UA (fp8, B K-contiguous): operands of any alignment and any K (GemmCoreUA)
     using T = typename std::conditional<UA, GemmCoreUA<BM, BN, WM, WN, TB, false, OP, FMT>,
                                         GemmCore<BM, BN, WM, WN, ST, TB, OP, RB, FMT>>::type;
+    static_assert(KW == 1 || (WM == 1 && WN == 1 && TB && !UA), "k-split waves run one-wave tiles of a K-contiguous B");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_f8[];
     const int tiles_m = (int)((p.M + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
     int tm, tn;
@@ -96,11 +101,36 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
     c.ldb = (uint32_t)(TB ? p.ldb * ES : p.ldb);
     c.rows = (int32_t)(p.M - m0 < BM ? p.M - m0 : BM);
     c.cols = (int32_t)(p.N - n0 < BN ? p.N - n0 : BN);
-    c.a0 = (uint32_t)(m0 * p.lda * ES) + da;
-    c.b0 = (uint32_t)(TB ? n0 * p.ldb * ES : n0) + db;
-    c.kbytes = p.K * ES;
+    const int kw = KW > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
+    const int64_t kc = p.K / KW, k0 = kw * kc;  // this wave's K range (KW > 1: K ES % (KW RB) == 0)
+    c.a0 = (uint32_t)((m0 * p.lda + k0) * ES) + da;
+    c.b0 = (uint32_t)(TB ? (n0 * p.ldb + k0) * ES : n0) + db;
+    c.kbytes = kc * ES;
+    // KW > 1: the epilogue's bias and QUANT_PRE words are loaded before the main loop (their latency hides under it;
+    // they are older than the main loop's copies, so its counted waits still cover exactly those copies)
+    float pre_bias[T::FN];
+    uint64_t pre_w[T::FN];
+    if constexpr (KW > 1) {
+#pragma unroll
+        for (int j = 0; j < T::FN; ++j) {
+            const int cl = T::frag_col(0, j, (int)threadIdx.x & 63);
+            const bool cok = cl < c.cols;
+            pre_bias[j] = (p.bias && cok) ? p.bias[n0 + cl] : 0.0f;
+            pre_w[j] = (p.qvec && cok) ? p.qvec[n0 + cl] : p.qscalar;
+        }
+    }
     typename T::acc_t acc[T::FM][T::FN];
-    T::run(c, smem_f8, acc);
+    T::run(c, smem_f8 + (KW > 1 ? kw * T::LDS_BYTES : 0), acc, KW > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x);
+    if constexpr (KW > 1) {
+        __syncthreads();  // every wave's main loop is done with its LDS ring
+        typename T::acc_t* red = (typename T::acc_t*)smem_f8;  // [KW - 1][64 lanes] accumulator fragments
+        const int ln = threadIdx.x & 63;
+        if (kw > 0) red[(kw - 1) * 64 + ln] = acc[0][0];
+        __syncthreads();
+        if (kw != 0) return;
+#pragma unroll
+        for (int w = 0; w < KW - 1; ++w) acc[0][0] += red[w * 64 + ln];
+    }
 
     // epilogue through a buffer resource over the output tile (rows past M dropped by its range)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -136,8 +166,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
             const int cl = T::frag_col(wn, j, lane);
             const bool cok = cl < c.cols;
             const int64_t col = n0 + cl;
-            const float bias = (p.bias && cok) ? p.bias[col] : 0.0f;
-            const uint64_t w = (p.qvec && cok) ? p.qvec[col] : p.qscalar;
+            const float bias = KW > 1 ? pre_bias[j] : (p.bias && cok) ? p.bias[col] : 0.0f;
+            const uint64_t w = KW > 1 ? pre_w[j] : (p.qvec && cok) ? p.qvec[col] : p.qscalar;
             const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
             const uint32_t cbase = cok ? (uint32_t)(cl * esize) : OOB;
 #pragma unroll
@@ -151,7 +181,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f8_kernel(GemmF8Args p)
                 }
         }
     };
-    if (p.atomic != C_STORE) {  // enAtomic: f32 / f16 / bf16 C (the host layer refuses the others)
+    if (KW == 1 && p.atomic != C_STORE) {  // enAtomic: f32 / f16 / bf16 C (the host layer refuses the others)
         // (acc + bias) x M1 of the column -- the store path's arithmetic
         auto v = [&](int cl, uint32_t a) {
             float x = __uint_as_float(a);
@@ -229,15 +259,17 @@ __global__ __launch_bounds__(256) void gemm_f8_generic_kernel(GemmF8Args p)
     }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT, bool UA = false>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT, bool UA = false, int KW = 1>
 static hipError_t launch_f8_tiled(const GemmF8Args& a, hipStream_t st)
 {
     using T = typename std::conditional<UA, GemmCoreUA<BM, BN, WM, WN, TB, false, op_of_fmt<FMT>, FMT>,
                                         GemmCore<BM, BN, WM, WN, ST, TB, op_of_fmt<FMT>, RB, FMT>>::type;
+    constexpr int LDS = (int)T::LDS_BYTES * KW;
+    static_assert(KW == 1 || (size_t)(KW - 1) * 64 * sizeof(typename T::acc_t) <= (size_t)LDS, "k-split reduction");
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
-    const hipError_t e = ensure_dynamic_lds<gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT, UA>>((int)T::LDS_BYTES);
+    const hipError_t e = ensure_dynamic_lds<gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT, UA, KW>>(LDS);
     if (e != hipSuccess) return e;
-    launch_k((gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT, UA>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a);
+    launch_k((gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT, UA, KW>), dim3(tiles), dim3(T::NT * KW), LDS, st, a);
     return hipGetLastError();
 }
 
@@ -254,6 +286,16 @@ static hipError_t launch_f8_fmt(const GemmF8Args& a, bool ua, hipStream_t st)
     }
     if (ua) return hipErrorInvalidValue;
     const bool big = a.M >= 1024 && a.N >= 1024;
+    // decode-sized batches (B streamed once) with a K-contiguous B and f32 / f16 / bf16 C stored: 32 x 32 tiles,
+    // each tile's K split over four waves of one workgroup, up to 32 rows, and up to 64 while 64 x 64 tiles would
+    // leave fewer than 160 workgroups (the int8 Matmul's rule)
+    const int64_t t64 = ((a.M + 63) / 64) * ((a.N + 63) / 64);
+    const bool skinny = a.M <= 32 || (a.M <= 64 && t64 < 160);
+    const bool c_wide = a.c_type == DT_F32 || a.c_type == DT_F16 || a.c_type == DT_BF16;
+    if constexpr (ES == 1) {
+        if (a.trans_b && skinny && c_wide && a.atomic == C_STORE && a.K % 256 == 0)
+            return launch_f8_tiled<32, 32, 1, 1, 4, true, 64, FMT, false, 4>(a, st);
+    }
     if (a.trans_b) {
         if (big) return (a.K * ES) % 128 == 0 ? launch_f8_tiled<256, 256, 4, 2, 2, true, 128, FMT>(a, st)
                                               : launch_f8_tiled<256, 256, 4, 2, 4, true, 64, FMT>(a, st);
