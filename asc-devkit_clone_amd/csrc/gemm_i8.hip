@@ -204,14 +204,20 @@ __device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* wtot
 
 // WPE: waves per SIMD the register allocation must allow (2 for two 4-wave workgroups per CU)
 // UA: X and W of any alignment and any K (GemmCoreUA)
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1, bool BTR = false, bool UA = false>
-__global__ __launch_bounds__(WM * WN * 64, WPE) void group_gemm_i8_kernel(GroupGemmArgs p)
+// KW > 1 (one-wave tiles, few rows per group: decode-sized MoE batches): the workgroup's KW waves each run the tile's
+// main loop on their own K / KW range in their own LDS ring, then sum their int32 accumulators through LDS (exact in
+// any order) and wave 0 runs the epilogue
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1, bool BTR = false, bool UA = false,
+          int KW = 1>
+__global__ __launch_bounds__(WM * WN * 64 * KW, WPE) void group_gemm_i8_kernel(GroupGemmArgs p)
 {
     // transposed accumulators: four consecutive output columns per register quad, stored as one 8-byte vector;
     // BTR: W given [G, K, N] staged by K rows and read with LDS transpose reads
     using T = I8Core<BM, BN, WM, WN, ST, TB, RB, true, BTR, UA>;
+    static_assert(KW == 1 || (WM == 1 && WN == 1 && !UA), "k-split waves run one-wave tiles");
+    constexpr int NTT = T::NT * KW;  // threads of the workgroup
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ int64_t wtot[T::NT / 64];
+    __shared__ int64_t wtot[NTT / 64];
     __shared__ int64_t tile_info[4];  // group, first row, end row, first m-tile of this workgroup's tile
     // the tile's per-token (BM) and per-channel (BN) scales, copied global -> LDS by one wave-wide copy each
     // (1 KiB: lanes past the scales read zeros)
@@ -223,7 +229,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void group_gemm_i8_kernel(GroupG
     // m-tiles follow those of groups 0 .. g-1.  Thread t owns groups [t * per, (t + 1) * per): two block-wide
     // prefix sums (rows, then m-tiles) give every thread its groups' starts, and the thread owning this
     // workgroup's tile publishes it -- no G-sized table, so the LDS stays with the stage ring.
-    const int per = (G + T::NT - 1) / T::NT, ga = (int)threadIdx.x * per;
+    const int per = (G + NTT - 1) / NTT, ga = (int)threadIdx.x * per;
     auto count = [&](int g) {
         const int64_t c = p.list_type == 0 ? p.group_list[g + 1] - p.group_list[g] : p.group_list[g];
         return c < 0 ? (int64_t)0 : c;
@@ -233,7 +239,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void group_gemm_i8_kernel(GroupG
     int64_t rows_total, tiles_total, mine = 0;
     for (int k = 0; k < per; ++k)
         if (ga + k < G) mine += count(ga + k);
-    const int64_t s0 = base + block_exclusive_scan<T::NT>(mine, wtot, &rows_total);
+    const int64_t s0 = base + block_exclusive_scan<NTT>(mine, wtot, &rows_total);
     mine = 0;
     {
         int64_t st = s0;
@@ -245,11 +251,12 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void group_gemm_i8_kernel(GroupG
             }
     }
     const int64_t tiles_n = (p.N + BN - 1) / BN;
-    const int64_t t0 = block_exclusive_scan<T::NT>(mine, wtot, &tiles_total);
+    const int64_t t0 = block_exclusive_scan<NTT>(mine, wtot, &tiles_total);
     const int64_t total = tiles_total * tiles_n;  // real (m-tile, n-tile) pairs
     const int64_t per_xcd = (total + 7) / 8;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave / WN, wn = wave % WN;
+    const int wm = KW > 1 ? 0 : wave / WN, wn = KW > 1 ? 0 : wave % WN;
+    const int kw = KW > 1 ? __builtin_amdgcn_readfirstlane(wave) : 0;
     {
         const int64_t lin = (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
         if ((int64_t)(blockIdx.x / 8) >= per_xcd || lin >= total) return;
@@ -291,9 +298,10 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void group_gemm_i8_kernel(GroupG
         c.ldb = (uint32_t)(TB ? p.K : p.N);
         c.rows = (int32_t)(m_end - m0 < BM ? m_end - m0 : BM);
         c.cols = (int32_t)(p.N - n0 < BN ? p.N - n0 : BN);
-        c.a0 = (uint32_t)(m0 * p.K) + da;
-        c.b0 = (uint32_t)(TB ? n0 * p.K : n0) + db;
-        c.kbytes = p.K;
+        const int64_t kc = p.K / KW, k0 = kw * kc;  // this wave's K range (KW > 1: K % (KW RB) == 0)
+        c.a0 = (uint32_t)(m0 * p.K + k0) + da;
+        c.b0 = (uint32_t)(TB ? n0 * p.K + k0 : n0 + k0 * p.N) + db;
+        c.kbytes = kc;
 
         // the epilogue's scales go global -> LDS now (waves 0 and 1, one copy each, no registers held), so their
         // latency hides under the main loop: the copies are older than the main loop's, whose first wait covers
@@ -304,7 +312,16 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void group_gemm_i8_kernel(GroupG
             copy16_to_lds(make_rsrc(p.scale + (int64_t)g * p.N + n0, (uint32_t)(c.cols * 4)), (uint8_t*)s_sc,
                           (uint32_t)lane * 16);
         typename T::acc_t acc[T::FM][T::FN];
-        T::run(c, smem, acc);
+        T::run(c, smem + (KW > 1 ? kw * T::LDS_BYTES : 0), acc, KW > 1 ? lane : (int)threadIdx.x);
+        if constexpr (KW > 1) {
+            __syncthreads();  // every wave's main loop is done with its LDS ring
+            typename T::acc_t* red = (typename T::acc_t*)smem;  // [KW - 1][64 lanes] accumulator fragments
+            if (kw > 0) red[(kw - 1) * 64 + lane] = acc[0][0];
+            __syncthreads();
+            if (kw != 0) return;
+#pragma unroll
+            for (int w = 0; w < KW - 1; ++w) acc[0][0] += red[w * 64 + lane];
+        }
 
         // epilogue (quant_group_matmul_custom.asc:424-452): AscendDequant acc*scale[g,n] in fp32 (its int32 -> fp32
         // conversion rounds ties away from zero above 2^24, as every AscendDequant here does), Mul by the
@@ -498,16 +515,18 @@ __global__ __launch_bounds__(256) void group_gemm_generic_kernel(GroupGemmArgs p
     }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1, bool BTR = false, bool UA = false>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, int WPE = 1, bool BTR = false, bool UA = false,
+          int KW = 1>
 static hipError_t launch_group_tiled(const GroupGemmArgs& a, hipStream_t st)
 {
     using T = I8Core<BM, BN, WM, WN, ST, TB, RB, true, BTR, UA>;
+    constexpr int LDS = (int)T::LDS_BYTES * KW;
+    static_assert(KW == 1 || (size_t)(KW - 1) * 64 * sizeof(typename T::acc_t) <= (size_t)LDS, "k-split reduction");
     const int64_t upper = ((a.M + BM - 1) / BM + a.G) * ((a.N + BN - 1) / BN);  // tiles, at most
-    const hipError_t e =
-        ensure_dynamic_lds<group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, WPE, BTR, UA>>((int)T::LDS_BYTES);
+    const hipError_t e = ensure_dynamic_lds<group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, WPE, BTR, UA, KW>>(LDS);
     if (e != hipSuccess) return e;
-    launch_k((group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, WPE, BTR, UA>), dim3((unsigned)((upper + 7) / 8 * 8)),
-             dim3(T::NT), T::LDS_BYTES, st, a);
+    launch_k((group_gemm_i8_kernel<BM, BN, WM, WN, ST, TB, RB, WPE, BTR, UA, KW>), dim3((unsigned)((upper + 7) / 8 * 8)),
+             dim3(T::NT * KW), LDS, st, a);
     return hipGetLastError();
 }
 
@@ -531,6 +550,14 @@ hipError_t launch_group_gemm(const GroupGemmArgs& a, hipStream_t st)
     if (!aligned)
         return a.w_trans ? launch_group_tiled<128, 128, 2, 2, 2, true, 64, 2, false, true>(a, st)
                          : launch_group_tiled<128, 128, 2, 2, 2, false, 64, 2, true, true>(a, st);
+    // decode-sized MoE batches (at most 16 rows per group on average, so most groups fill one 32-row tile and every
+    // expert's weights are streamed about once): 32 x 32 tiles, each tile's K split over four waves of one
+    // workgroup, so many more workgroups stream the weights than the 128 x 256 tiles give
+    if (a.M <= 16 * a.G && a.K % 256 == 0) {
+        if (a.w_trans) return launch_group_tiled<32, 32, 1, 1, 4, true, 64, 1, false, false, 4>(a, st);
+        if (a.N % 16 == 0 && (uintptr_t)a.W % 16 == 0)
+            return launch_group_tiled<32, 32, 1, 1, 4, false, 64, 1, true, false, 4>(a, st);
+    }
     {
         // 128 x 256 tiles.  Short K (the reference sample's K = 1024): 4 waves with 64 x 128 wave tiles and
         // 64-byte stages, two workgroups per CU, so one's epilogue and its store / load latencies overlap the

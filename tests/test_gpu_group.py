@@ -95,6 +95,47 @@ def test_group_ties_above_2_24(ascq_gpu, oracle, w_trans, list_type):
     assert GC.rne_differs(x, w, pts, sc, counts) > 50
 
 
+@pytest.mark.parametrize("T,K,N", [(1, 512, 160), (16, 1024, 256), (64, 768, 96), (200, 4096, 1408)])
+@pytest.mark.parametrize("w_trans", [False, True])
+@pytest.mark.parametrize("list_type", [0, 1])
+def test_group_decode_ksplit(ascq_gpu, oracle, T, K, N, w_trans, list_type):
+    """decode-sized MoE batches (at most 16 rows per expert on average, K % 256 == 0): 32 x 32 tiles with each
+    tile's K split over four waves (int32 partials, exact); 16 Zipf-ragged experts, a leading offset and trailing
+    rows outside every group, bit-exact vs the oracle"""
+    G = 16
+    rng = seeded(T + K + N + 2 * w_trans + list_type)
+    counts = zipf_counts(rng, T, G)
+    lead = 3
+    M = lead + T + 5
+    x = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    pts = np.exp(rng.uniform(np.log(1e-3), np.log(1e-1), M)).astype(np.float32)
+    w = rng.integers(-127, 128, (G, N, K) if w_trans else (G, K, N), dtype=np.int8)
+    scale = np.exp(rng.uniform(np.log(1e-4), np.log(1e-2), (G, N))).astype(np.float32)
+    # offsets start at row `lead`; counts start at row 0 (the rows past the last group stay untouched either way)
+    gl = (np.concatenate([[lead], lead + np.cumsum(counts)]) if list_type == 0 else counts).astype(np.int64)
+    y = torch.full((M, N), 3.0, dtype=torch.bfloat16, device="cuda")
+    ascq_gpu.quant_group_matmul(_dev(x), _dev(pts), _dev(w), _dev(scale), _dev(gl), list_type, w_trans, out=y)
+    y0 = torch.full((M, N), 3.0, dtype=torch.bfloat16).view(torch.int16).numpy().view(np.uint16).copy()
+    ref = O.group_matmul(x, pts, w, scale, gl, list_type, G, M, K, N, O.BF16, w_trans, y=y0)
+    np.testing.assert_array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), ref)
+
+
+@pytest.mark.parametrize("w_trans", [False, True])
+def test_group_decode_ties_above_2_24(ascq_gpu, oracle, w_trans):
+    """the fp32-tie accumulators of test_group_ties_above_2_24 over eight 8-row experts (the K-split 32 x 32 tiles):
+    the four waves' int32 partials add exactly, and the group epilogue rounds ties away from zero"""
+    x, w, pts, sc, counts = GC.tie_case(13, M=64, N=64, K=4096, groups=(8,) * 8)
+    M, K = x.shape
+    G, _, N = w.shape
+    gl = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    w_dev = _dev(np.ascontiguousarray(w.transpose(0, 2, 1))) if w_trans else _dev(w)
+    y = ascq_gpu.quant_group_matmul(_dev(x), _dev(pts), w_dev, _dev(sc), _dev(gl), 0, w_trans)
+    got = y.cpu().view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(got, O.group_matmul(x, pts, w, sc, gl, 0, G, M, K, N, O.BF16))
+    np.testing.assert_array_equal(got, GC.group_reference(x, w, pts, sc, counts))
+    assert GC.rne_differs(x, w, pts, sc, counts) > 20
+
+
 def _f16_ulp(v):
     a = np.maximum(np.abs(v), 2.0 ** -14)
     return 2.0 ** (np.floor(np.log2(a)) - 10)
