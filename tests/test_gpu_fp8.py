@@ -256,6 +256,18 @@ def test_mx_fp8_small(ascq_gpu, fa, fb, trans_b, sa_t, sb_t):
     check_out(got, Ce, mx_bound(Ca, Cb, K), O.BF16, "mx small")
 
 
+@pytest.mark.parametrize("trans_b", [True, False])
+@pytest.mark.parametrize("M,N,K", [(1, 200, 512), (40, 136, 384), (64, 96, 1024)])
+def test_mx_fp8_decode(ascq_gpu, trans_b, M, N, K):
+    """decode-sized batches (M <= 64, a single row among them), both B layouts"""
+    fa, fb = O.FP8_E4M3, O.FP8_E5M2
+    A, B, sA, sB = mx_fp8_inputs(seeded(29 + M), M, N, K, fa, fb, trans_b)
+    got = run_mx_fp8(ascq_gpu, A, B, sA, pairs(sB), fa, fb, M, N, K, trans_b, 0, 0, O.BF16)
+    _, Ce, Ca, Cb = O.mx_matmul(A, B, sA, pairs(sB), M, N, K, trans_b=trans_b, sa_layout=0, sb_layout=0, elem_fmt=fa,
+                                fmt_b=fb, blockmax=True)
+    check_out(got, Ce, mx_bound(Ca, Cb, K), O.BF16, "mx decode")
+
+
 @pytest.mark.parametrize("fa,fb", [(O.FP8_E4M3, O.FP8_E4M3), (O.FP8_E4M3, O.FP8_E5M2)])
 @pytest.mark.parametrize("M,N,K", [(1024, 1024, 512), (1100, 1300, 448)])
 def test_mx_fp8_big(ascq_gpu, fa, fb, M, N, K):

@@ -105,6 +105,33 @@ def test_mx_small(ascq_gpu, oracle, trans_b, sa_t, sb_t, shape):
     check(got, Ce, Ca, K, C, rel=2.0 ** -8)
 
 
+@pytest.mark.parametrize("trans_b", [True, False])
+@pytest.mark.parametrize("sa_t,sb_t", [(0, 0), (1, 1)])
+@pytest.mark.parametrize("shape", [(1, 200, 512), (16, 96, 768), (40, 64, 2048), (64, 130, 1024)])
+def test_mx_decode(ascq_gpu, oracle, trans_b, sa_t, sb_t, shape):
+    """decode-sized batches (M <= 64, a single row and ragged N among them) with scale exponents spread over +-20;
+    a second call returns the same bits; bias and f32 C once"""
+    M, N, K = shape
+    rng = seeded(3 * M + N + K)
+    A, sA, Bt, sBt = mx_inputs(rng, M, N, K)
+    sA = (sA.astype(np.int32) + rng.integers(-20, 21, sA.shape)).clip(1, 254).astype(np.uint8)
+    sBt = (sBt.astype(np.int32) + rng.integers(-20, 21, sBt.shape)).clip(1, 254).astype(np.uint8)
+    sA_dev = scale_pairs(sA) if sa_t else sA
+    sB_dev = sBt if sb_t else scale_pairs(sBt)
+    B_dev = Bt if trans_b else to_kn(Bt, N, K)
+    c = run_mx(ascq_gpu, A, sA_dev, B_dev, sB_dev, M, N, K, trans_b, sa_t, sb_t, ascq_gpu.BF16)
+    C, Ce, Ca = O.mx_matmul(A, Bt, sA, sBt, M, N, K, trans_b=True, sa_layout=0, sb_layout=1)
+    got = bf16_to_f64(c.view(torch.int16).numpy().view(np.uint16))
+    check(got, Ce, Ca, K, C, rel=2.0 ** -8)
+    again = run_mx(ascq_gpu, A, sA_dev, B_dev, sB_dev, M, N, K, trans_b, sa_t, sb_t, ascq_gpu.BF16)
+    assert torch.equal(c.view(torch.int16), again.view(torch.int16))
+    if trans_b and sa_t == 0:
+        bias = rng.standard_normal(N).astype(np.float32)
+        c32 = run_mx(ascq_gpu, A, sA_dev, B_dev, sB_dev, M, N, K, trans_b, sa_t, sb_t, ascq_gpu.F32, bias=bias)
+        d = K * 2.0 ** -24 * (Ca + np.abs(bias)[None, :]) + 2.0 ** -24 * np.abs(Ce + bias[None, :])
+        assert (np.abs(c32.numpy().astype(np.float64) - (Ce + bias[None, :])) <= d + 1e-30).all()
+
+
 def test_mx_f32_out(ascq_gpu, oracle):
     M, N, K = 128, 128, 256
     rng = seeded(77)
