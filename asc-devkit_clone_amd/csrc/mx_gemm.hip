@@ -39,11 +39,13 @@ namespace ascq {
 // scale blocks per row in the stage-major copies: sK rounded up to whole groups of the largest stage (8 blocks)
 __host__ __device__ inline int64_t sk_stage_major(int64_t K) { return ((K + 63) / 64 * 2 + 7) / 8 * 8; }
 
-template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true>
+// DIRECT: the scales are read as given, both row-major ([M, sK] and [N, sK]), by the core's per-row copies (sa_sm /
+// sb_sm unused); otherwise from the stage-major copies at sa_sm / sb_sm
+template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true, bool DIRECT = false>
 __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, const uint8_t* __restrict__ sa_sm,
                                                                 const uint8_t* __restrict__ sb_sm)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, true, OP, RB, FMT, ILV>;
+    using T = GemmCore<BM, BN, WM, WN, ST, true, OP, RB, FMT, ILV, false, false, DIRECT>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_mx[];
     const int64_t M = p.M, N = p.N, K = p.K;
     const int64_t KB = OP == OP_MXF8 ? K : K / 2;  // bytes per row (fp6: of the P plane)
@@ -64,10 +66,15 @@ __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, con
     // One resource over every auxiliary region (launch_mx_gemm checks the layout): the stage-major scales (which
     // carry 16 bytes of slack, so a 16-byte copy at the end never straddles the range) and, for fp6, the Q planes
     // before them: [Aq][P plane of B][Bq][scales of A][scales of B].
-    const uint8_t* aux = OP == OP_MXFP6 ? p.Aq : sa_sm;
-    c.aux = make_rsrc(aux, (uint32_t)(sb_sm - aux) + (uint32_t)(N * sk_stage_major(K) + 16));
-    c.sa_base = (uint32_t)(sa_sm - aux);
-    c.sb_base = (uint32_t)(sb_sm - aux);
+    if constexpr (DIRECT) {
+        c.aux = make_rsrc(p.sA, (uint32_t)(M * sK));
+        c.aux_b = make_rsrc(p.sB, (uint32_t)(N * sK));
+    } else {
+        const uint8_t* aux = OP == OP_MXFP6 ? p.Aq : sa_sm;
+        c.aux = make_rsrc(aux, (uint32_t)(sb_sm - aux) + (uint32_t)(N * sk_stage_major(K) + 16));
+        c.sa_base = (uint32_t)(sa_sm - aux);
+        c.sb_base = (uint32_t)(sb_sm - aux);
+    }
     if constexpr (OP == OP_MXFP6) {
         const uint32_t ga = (uint32_t)((M + 31) / 32), gb = (uint32_t)((N + 31) / 32);
         c.qa_stride = ga * 1024u;
@@ -262,22 +269,25 @@ size_t mx_scale_workspace_bytes(int64_t M, int64_t N, int64_t K)
     return (size_t)((M * sKp + 16 + 255) / 256 * 256 + (N * sKp + 16 + 255) / 256 * 256);
 }
 
-template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true>
+template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true, bool DIRECT = false>
 static hipError_t launch_mx_tiled(const MxGemmArgs& a, hipStream_t st)
 {
-    using T = GemmCore<BM, BN, WM, WN, ST, true, OP, RB, FMT, ILV>;
+    using T = GemmCore<BM, BN, WM, WN, ST, true, OP, RB, FMT, ILV, false, false, DIRECT>;
     constexpr int SCB = T::SCB;
     const int64_t sK = (a.K + 63) / 64 * 2;
     uint8_t* sa_sm = a.ws_scales;
     uint8_t* sb_sm = a.ws_scales + (a.M * sk_stage_major(a.K) + 16 + 255) / 256 * 256;
-    hipError_t e = launch_scale_stage_major<SCB>(ScaleJob{sa_sm, a.sA, a.M, a.sa_layout == 1 ? 1 : 0},
-                                                 ScaleJob{sb_sm, a.sB, a.N, a.sb_layout == 0 ? 1 : 0}, sK, st);
-    if (e != hipSuccess) return e;
-    e = ensure_dynamic_lds<mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT, ILV>>((int)T::LDS_BYTES);
+    hipError_t e = hipSuccess;
+    if (!DIRECT) {
+        e = launch_scale_stage_major<SCB>(ScaleJob{sa_sm, a.sA, a.M, a.sa_layout == 1 ? 1 : 0},
+                                          ScaleJob{sb_sm, a.sB, a.N, a.sb_layout == 0 ? 1 : 0}, sK, st);
+        if (e != hipSuccess) return e;
+    }
+    e = ensure_dynamic_lds<mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT, ILV, DIRECT>>((int)T::LDS_BYTES);
     if (e != hipSuccess) return e;
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
-    launch_k((mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT, ILV>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st, a,
-                       sa_sm, sb_sm);
+    launch_k((mx_gemm_kernel<BM, BN, WM, WN, ST, RB, OP, FMT, ILV, DIRECT>), dim3(tiles), dim3(T::NT), T::LDS_BYTES, st,
+             a, sa_sm, sb_sm);
     return hipGetLastError();
 }
 
@@ -314,6 +324,12 @@ hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st)
     }
     if (fp4) {
         if (big) return launch_mx_tiled<256, 256, 4, 2, 2, 128, OP_MXFP4, 0>(a, st);
+        // decode-sized batches (M <= 64) with both scale tensors row-major ([M, sK], [N, sK]; 4-byte aligned): the
+        // 64 x 64 tiles read the scales as given, so no rearrangement launch precedes the GEMM (measured, K = 4096,
+        // N = 11008: M = 1 / 16 / 64 in 11.9 / 12.7 / 16.3 us against 17.5 / 17.6 / 19.5 us; at M = 256 the per-row
+        // reads, 64 cache lines a copy, cost more than the launch: 45.4 against 38.0 us at K = N = 8192)
+        if (a.M <= 64 && a.sa_layout == 0 && a.sb_layout == 1 && (uintptr_t)a.sA % 4 == 0 && (uintptr_t)a.sB % 4 == 0)
+            return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP4, 0, true, true>(a, st);
         return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP4, 0>(a, st);
     }
     switch (a.fmt_a | (a.fmt_b << 3)) {

@@ -106,11 +106,12 @@ def test_mx_small(ascq_gpu, oracle, trans_b, sa_t, sb_t, shape):
 
 
 @pytest.mark.parametrize("trans_b", [True, False])
-@pytest.mark.parametrize("sa_t,sb_t", [(0, 0), (1, 1)])
+@pytest.mark.parametrize("sa_t,sb_t", [(0, 0), (1, 1), (0, 1), (1, 0)])
 @pytest.mark.parametrize("shape", [(1, 200, 512), (16, 96, 768), (40, 64, 2048), (64, 130, 1024)])
 def test_mx_decode(ascq_gpu, oracle, trans_b, sa_t, sb_t, shape):
-    """decode-sized batches (M <= 64, a single row and ragged N among them) with scale exponents spread over +-20;
-    a second call returns the same bits; bias and f32 C once"""
+    """decode-sized batches (M <= 64, a single row and ragged N among them) with scale exponents spread over +-20,
+    every scale layout pair (both row-major -- [M, sK] and [N, sK] -- is read as given, the others through the
+    stage-major copies); a second call returns the same bits; bias and f32 C once"""
     M, N, K = shape
     rng = seeded(3 * M + N + K)
     A, sA, Bt, sBt = mx_inputs(rng, M, N, K)
