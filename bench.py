@@ -11,10 +11,12 @@ layouts), the MX-FP4 8192^3 GEMM and the fp8 / MX-FP8 8192^3 GEMMs, and -- for s
 vendor BLAS (hipBLASLt through torch) on the int8 and fp8 8192^3 shapes.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                  [--only all|headline|quant|w8a8|gemv|group|mx|fp8|vendor|traffic|shapes]
+                  [--only all|headline|quant|w8a8|gemv|group|mx|fp8|vendor|traffic|shapes|decode]
 
 `--only shapes` (not part of the default run) times the weight-only matmul over model shapes (attention and MLP
-projections of 7B / 13B / 70B-class models) at M = 1 / 16 / 64 / 512.
+projections of 7B / 13B / 70B-class models) at M = 1 / 16 / 64 / 512; `--only decode` (not part of the default run
+either) times the int8, fp8 and MX-FP4 Matmuls at decode-sized batches (M = 1 / 16 / 64, B streamed once) and the MoE
+group matmul at 16 / 64 / 256 tokens.
 """
 from __future__ import annotations
 
@@ -420,6 +422,90 @@ def bench_wo_shape(torch, ascq, K, N, M, iters, grp=128, w_type=None):
     gbs = (K * N // 2 + 4 * G * N + 2 * M * K + 2 * M * N) / (ms * 1e-3) / 1e9
     return dict(workload=f"W4A16 weight-only matmul K={K} N={N} M={M} g={grp}", ms=ms, value=tf, unit="TFLOPS",
                 frac_of_peak=tf / F16_PEAK_TFLOPS, gbs=round(gbs, 1), eager_ms=eager)
+
+
+def bench_decode_matmul(torch, ascq, kind, K, N, M, iters=50):
+    """a quantized Matmul at a decode-sized batch (B [N, K] streamed once per call: the weight stream is the roofline),
+    weights rotating past the Infinity Cache, timed as a HIP graph of the calls replayed.  kind: "int8" (W8A8,
+    per-channel DEQF16 -> f16), "fp8" (e4m3, per-channel QF322BF16 -> bf16), "mxfp4" (E2M1 / E8M0 -> bf16; the
+    call includes the scale rearrangement launch)"""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2)
+    if kind == "int8":
+        wb = K * N
+        R = rotation(wb)
+        A = torch.randint(-127, 128, (M, K), generator=g, device="cuda", dtype=torch.int8)
+        Bs = [(torch.randint(-127, 128, (N, K), generator=g, device="cuda", dtype=torch.int8), None) for _ in range(R)]
+        C = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        mm = ascq.Matmul(ascq.INT8, ascq.INT8, ascq.F16)
+        mm.SetQuantVector(torch.full((N,), 0x3A800000, dtype=torch.int64, device="cuda"))
+        what = "W8A8 int8 Matmul, per-channel DEQF16 -> f16"
+    elif kind == "fp8":
+        wb = K * N
+        R = rotation(wb)
+        A = _fp8_bytes(torch, (M, K), g, torch.float8_e4m3fn)
+        Bs = [(_fp8_bytes(torch, (N, K), g, torch.float8_e4m3fn), None) for _ in range(R)]
+        C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        mm = ascq.Matmul(ascq.FP8_E4M3, ascq.FP8_E4M3, ascq.BF16)
+        mm.SetQuantVector(torch.full((N,), 0x3C000000, dtype=torch.int64, device="cuda"))
+        what = "fp8 e4m3 Matmul, per-channel QF322BF16 -> bf16"
+    else:
+        wb = K * N // 2 + K * N // 32
+        R = rotation(wb)
+        A, sA = _mx_fp4_normal(torch, M, K, g)
+        Bs = [_mx_fp4_normal(torch, N, K, g) for _ in range(R)]
+        C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        mm = ascq.Matmul(ascq.FP4_E2M1, ascq.FP4_E2M1, ascq.BF16, 0, ascq.E8M0)
+        what = "MX-FP4 Matmul (E2M1, E8M0 per 32) -> bf16"
+    mm.SetOrgShape(M, N, K)
+    mm.SetTensorA(A)
+    if kind == "mxfp4":
+        mm.SetTensorScaleA(sA, False)
+
+    def fn(i):
+        B, sB = Bs[i % R]
+        mm.SetTensorB(B, True)
+        if sB is not None:
+            mm.SetTensorScaleB(sB, True)
+        mm.IterateAll(C)
+
+    ms, eager = _time_graph(torch, fn, iters, C)
+    gbs = wb / (ms * 1e-3) / 1e9
+    return dict(workload=f"{what}, decode batch M={M}, K={K}, N={N}, B given [N,K]", ms=ms, value=round(gbs, 1),
+                unit="GB/s", frac_of_peak=gbs / HBM_PEAK_GBS, tops=round(2 * M * N * K / (ms * 1e-3) / 1e12, 1),
+                timing="HIP graph of the calls (weights rotating), replayed" if USE_GRAPH else "eager calls",
+                eager_ms=eager)
+
+
+def bench_group_decode(torch, ascq, T, iters=30, G=16, K=4096, N=1408):
+    """the MoE group matmul at a decode-sized batch: T tokens routed Zipf(1.1) over G experts, W [G, N, K] rotating;
+    rate = the used experts' weight bytes per call"""
+    rng = np.random.default_rng(4)
+    p = 1.0 / (np.arange(1, G + 1) ** 1.1)
+    counts = rng.multinomial(T, p / p.sum())
+    offsets = torch.from_numpy(np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)).cuda()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    R = rotation(G * K * N)
+    x = torch.randint(-127, 128, (T, K), generator=g, device="cuda", dtype=torch.int8)
+    ws = [torch.randint(-127, 128, (G, N, K), generator=g, device="cuda", dtype=torch.int8) for _ in range(R)]
+    pts = torch.rand(T, generator=g, device="cuda") * 0.01
+    scale = torch.rand((G, N), generator=g, device="cuda") * 0.01
+    y = torch.empty((T, N), dtype=torch.bfloat16, device="cuda")
+
+    def fn(i):
+        ascq.quant_group_matmul(x, pts, ws[i % R], scale, offsets, 0, out=y, w_trans=True)
+
+    ms, eager = _time_graph(torch, fn, iters, y)
+    used = int((counts > 0).sum())
+    gbs = used * K * N / (ms * 1e-3) / 1e9
+    return dict(workload=f"MoE quant group matmul, decode batch: {T} tokens over {G} experts Zipf(1.1) ({used} used), "
+                         f"K={K} N={N}, W [G,N,K], bf16 out", ms=ms, value=round(gbs, 1), unit="GB/s",
+                frac_of_peak=gbs / HBM_PEAK_GBS, timing="HIP graph of the calls (weights rotating), replayed"
+                if USE_GRAPH else "eager calls", eager_ms=eager)
+
+
+DECODE_SHAPES = [(4096, 11008), (11008, 4096), (8192, 8192)]
 
 
 # model shapes of the weight-only matmul (attention and MLP projections of 7B / 13B / 70B-class models), opt-in:
@@ -847,6 +933,9 @@ OTHER = {
             lambda t, a: bench_mxfp8(t, a, 10)],
     "shapes": [lambda t, a, k=k, n=n, m=m: bench_wo_shape(t, a, k, n, m, 50 if m < 512 else 10)
                for k, n in WO_SHAPES for m in (1, 16, 64, 512)],
+    "decode": [lambda t, a, kd=kd, k=k, n=n, m=m: bench_decode_matmul(t, a, kd, k, n, m)
+               for kd in ("int8", "fp8", "mxfp4") for k, n in DECODE_SHAPES for m in (1, 16, 64)]
+              + [lambda t, a, tk=tk: bench_group_decode(t, a, tk) for tk in (16, 64, 256)],
 }
 
 
@@ -908,7 +997,7 @@ def main() -> int:
                     help="time the launch-bound lines (decode GEMV, the W8A8 sample) eagerly, without a HIP graph")
     ap.add_argument("--only", default="all",
                     choices=["all", "headline", "quant", "w8a8", "gemv", "group", "mx", "fp8", "vendor", "traffic",
-                             "shapes"],
+                             "shapes", "decode"],
                     help="run one workload family (the JSON contract line is printed for all / headline)")
     args = ap.parse_args()
     global USE_GRAPH
@@ -926,7 +1015,7 @@ def main() -> int:
     if args.only == "traffic":
         print(json.dumps(traffic_probe(torch, ascq)))
         return 0
-    if args.only in ("quant", "w8a8", "gemv", "group", "mx", "fp8", "vendor", "shapes"):
+    if args.only in ("quant", "w8a8", "gemv", "group", "mx", "fp8", "vendor", "shapes", "decode"):
         print(json.dumps({"other_configs": run_others(torch, ascq, args.only, with_cpu=not args.no_cpu)}))
         return 0
     h = bench_headline(torch, ascq, args.steps, args.warmup)
