@@ -186,7 +186,8 @@ struct CoreArgs {
     // = blocks SCB s .. SCB s + SCB - 1 of row r, at byte sa_base + (s * rows + r) * SCB for A, sb_base + ... for
     // B -- and, for fp6, the Q planes
     rsrc_t aux;
-    // SC_DIRECT cores: aux is the A scales and aux_b the B scales as given, row-major [rows, sk] (sk bytes a row)
+    // SC_DIRECT cores: aux is the A scales as given, row-major [rows, sk] (sk bytes a row), and aux_b the B scales as
+    // given: row-major too (SC_DIRECT 1) or in block pairs [sk / 2, sb_rows, 2] (SC_DIRECT 2)
     rsrc_t aux_b;
     uint32_t sa_base, sb_base;  // byte offsets of the A / B stage-major scales in aux
     uint32_t sa0_row, sb0_row;  // first row / column index of the tile
@@ -202,12 +203,15 @@ struct CoreArgs {
 // 32 x 32 accumulator holds the transposed block: lane l, register r = 4 q + e holds row (l % 32) and column
 // 8 q + 4 (l / 32) + e -- four consecutive columns of one row per register quad, which an epilogue stores as one
 // vector (no LDS round trip); ct_row / ct_col give the coordinates.
-// SC_DIRECT (MX, 4 scale bytes per row per stage): the E8M0 scales are read where the caller left them, row-major
-// [rows, sK], instead of from a stage-major copy: each stage, one copy per 64 tile rows moves the stage's 4 bytes of
-// 64 consecutive rows (one 4-byte LDS-DMA load per lane, lane = row) into the same [row][4] region the stage-major
-// copies fill, so the fragment-side reads are unchanged.
+// SC_DIRECT (MX, 4 scale bytes per row per stage): the E8M0 scales are read where the caller left them instead of
+// from a stage-major copy.  A row-major scale tensor [rows, sK] (A always; B when SC_DIRECT == 1): each stage, one
+// copy per 64 tile rows moves the stage's 4 bytes of 64 consecutive rows (one 4-byte LDS-DMA load per lane, lane =
+// row) into the same [row][4] region the stage-major copies fill.  B in block pairs [sK / 2, N, 2] (SC_DIRECT == 2):
+// a stage's two pairs of a row lie in two planes, each 2 bytes a row and contiguous over rows, so one copy moves 128
+// rows of one plane (4 bytes = two rows per lane) into a [plane][row] u16 region, and the scale word of a row is its
+// two plane entries.
 template <int BM, int BN, int WM, int WN, int STAGES, bool B_KCONTIG, int OP, int ROWB_ = 64, int FMT = 0, bool ILV = true,
-          bool CT = false, bool B_TR = false, bool SC_DIRECT = false>
+          bool CT = false, bool B_TR = false, int SC_DIRECT = 0>
 struct GemmCore {
     static constexpr bool IS_MX = OP == OP_MXFP4 || OP == OP_MXF8 || OP == OP_MXFP6;
     static constexpr bool IS_F8 = OP == OP_F8 || OP == OP_MXF8;
@@ -254,7 +258,9 @@ struct GemmCore {
     static constexpr int SB_INSTR = IS_MX ? (BN + SC_ROWS - 1) / SC_ROWS : 0;
     static constexpr int SA_REG = SA_INSTR * 1024, SB_REG = SB_INSTR * 1024;
     // SC_DIRECT: copies of 64 rows' scale bytes (64 SCB <= 1 KiB, so the regions above hold them)
-    static constexpr int DA_INSTR = SC_DIRECT ? BM / 64 : 0, DB_INSTR = SC_DIRECT ? BN / 64 : 0;
+    static constexpr int PLANE_B = (BN + 127) / 128 * 256;  // SC_DIRECT 2: bytes of one pair plane of the B region
+    static constexpr int DA_INSTR = SC_DIRECT ? BM / 64 : 0;
+    static constexpr int DB_INSTR = SC_DIRECT == 1 ? BN / 64 : SC_DIRECT == 2 ? 2 * ((BN + 127) / 128) : 0;
     static constexpr int AUX_INSTR = SC_DIRECT ? DA_INSTR + DB_INSTR : SA_INSTR + SB_INSTR + QA_INSTR + QB_INSTR;
     static constexpr int SC_COPIES = (AUX_INSTR + NW - 1) / NW;
     static constexpr int SC_BYTES = SA_REG + SB_REG;
@@ -281,6 +287,7 @@ struct GemmCore {
     static_assert(!IS_MX || SCB % 4 == 0 || SCB == 2, "MX stage scale bytes per row");
     // (an LDS-DMA load places lane l's data at 4 l, so only 4-byte rows pack densely)
     static_assert(!SC_DIRECT || (IS_MX && !IS_FP6 && SCB == 4), "direct scales: one 4-byte load a row");
+    static_assert(SC_DIRECT != 2 || 2 * PLANE_B <= SB_INSTR * 1024, "pair planes fit the B scale region");
     static_assert(!IS_FP6 || (ROWB == 64 && BM % 32 == 0 && BN % 32 == 0), "fp6 Q blocks: 4 MX blocks per stage");
     static_assert(KPS >= 1, "a stage holds at least one k-step");
     static_assert((STAGES >= 3 || ((B_KCONTIG || B_TR) && STAGES == 2)) && IN_FLIGHT < 64, "stages");
@@ -448,19 +455,31 @@ struct GemmCore {
             uint32_t base, stride, dst;
         };
         AuxCopy aux[IS_MX ? SC_COPIES : 1];
-        uint32_t aux_is_b[SC_DIRECT ? SC_COPIES : 1];
+        uint32_t aux_is_b[SC_DIRECT ? SC_COPIES : 1], aux_lmul[SC_DIRECT ? SC_COPIES : 1];
         if constexpr (SC_DIRECT) {
-            // copy g: 64 rows of A (g < DA_INSTR) or of B; lane l takes row 64 g' + l, SCB bytes at row * sk + SCB kt
+            // copy g: 64 rows of A (g < DA_INSTR), lane l taking row 64 g + l (SCB bytes at row * sk + SCB kt); then B:
+            // 64 rows the same way (SC_DIRECT 1), or plane j = g' % 2 of 128-row group g' / 2 (SC_DIRECT 2), lane l
+            // taking rows 128 (g' / 2) + 2 l, + 1 at ((2 kt + j) N + row) * 2
 #pragma unroll
             for (int v = 0; v < SC_COPIES; ++v) {
                 const int g = (wave * SC_COPIES + v) % AUX_INSTR;  // wave-uniform; past the real copies: a repeat
                 const bool isb = g >= DA_INSTR;
                 const int gg = isb ? g - DA_INSTR : g;
-                aux[v] = {((isb ? p.sb0_row : p.sa0_row) + (uint32_t)(gg * 64)) * p.sk, (uint32_t)SCB,
-                          (uint32_t)(SC_OFF + (isb ? SA_REG : 0) + gg * 64 * SCB)};
+                if (isb && SC_DIRECT == 2) {
+                    const int j = gg % 2, q = gg / 2;
+                    aux[v] = {((uint32_t)j * p.sb_rows + p.sb0_row + (uint32_t)(q * 128)) * 2u, p.sb_rows * 4u,
+                              (uint32_t)(SC_OFF + SA_REG + j * PLANE_B + q * 256)};
+                    aux_lmul[v] = 4u;
+                } else {
+                    aux[v] = {((isb ? p.sb0_row : p.sa0_row) + (uint32_t)(gg * 64)) * p.sk, (uint32_t)SCB,
+                              (uint32_t)(SC_OFF + (isb ? SA_REG : 0) + gg * 64 * SCB)};
+                    aux_lmul[v] = p.sk;
+                }
                 aux[v].base = __builtin_amdgcn_readfirstlane(aux[v].base);
+                aux[v].stride = __builtin_amdgcn_readfirstlane(aux[v].stride);
                 aux[v].dst = __builtin_amdgcn_readfirstlane(aux[v].dst);
                 aux_is_b[v] = __builtin_amdgcn_readfirstlane((uint32_t)isb);
+                aux_lmul[v] = __builtin_amdgcn_readfirstlane(aux_lmul[v]);
             }
         } else if constexpr (IS_MX) {
 #pragma unroll
@@ -520,7 +539,7 @@ struct GemmCore {
                 const int v = u - A_COPIES - B_COPIES;
                 const AuxCopy& x = aux[v];
                 const bool kval = (uint32_t)(kt * SCB) < p.sk;
-                const uint32_t off = kval ? x.base + (uint32_t)kt * (uint32_t)SCB + (uint32_t)lane * p.sk : OOB;
+                const uint32_t off = kval ? x.base + (uint32_t)kt * x.stride + (uint32_t)lane * aux_lmul[v] : OOB;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(aux_is_b[v] ? p.aux_b : p.aux, (lds_ptr_t)(sA + x.dst), SCB, off,
                                                          0, 0, 0);
             } else if constexpr (IS_MX) {
@@ -584,7 +603,14 @@ struct GemmCore {
 #pragma unroll
                     for (int i = 0; i < FM; ++i) swa[i] = scale_word(sS, wm * WTM + i * 32 + r32, h) >> (8 * kh);
 #pragma unroll
-                    for (int j = 0; j < FN; ++j) swb[j] = scale_word(sS + SA_REG, wn * WTN + j * 32 + r32, h) >> (8 * kh);
+                    for (int j = 0; j < FN; ++j) {
+                        const int row = wn * WTN + j * 32 + r32;
+                        if constexpr (SC_DIRECT == 2)  // the row's entries of the two pair planes
+                            swb[j] = ((uint32_t)((const uint16_t*)(sS + SA_REG))[row] |
+                                      ((uint32_t)((const uint16_t*)(sS + SA_REG + PLANE_B))[row] << 16)) >> (8 * kh);
+                        else
+                            swb[j] = scale_word(sS + SA_REG, row, h) >> (8 * kh);
+                    }
                 }
 #pragma unroll
                 for (int s = SPH * h; s < SPH * h + SPH; ++s) {

@@ -39,9 +39,10 @@ namespace ascq {
 // scale blocks per row in the stage-major copies: sK rounded up to whole groups of the largest stage (8 blocks)
 __host__ __device__ inline int64_t sk_stage_major(int64_t K) { return ((K + 63) / 64 * 2 + 7) / 8 * 8; }
 
-// DIRECT: the scales are read as given, both row-major ([M, sK] and [N, sK]), by the core's per-row copies (sa_sm /
-// sb_sm unused); otherwise from the stage-major copies at sa_sm / sb_sm
-template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true, bool DIRECT = false>
+// DIRECT (the core's SC_DIRECT): the scales are read as given -- A row-major [M, sK], B row-major [N, sK] (1) or in
+// block pairs [sK / 2, N, 2] (2) -- by the core's copies (sa_sm / sb_sm unused); 0: from the stage-major copies at
+// sa_sm / sb_sm
+template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true, int DIRECT = 0>
 __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, const uint8_t* __restrict__ sa_sm,
                                                                 const uint8_t* __restrict__ sb_sm)
 {
@@ -269,7 +270,7 @@ size_t mx_scale_workspace_bytes(int64_t M, int64_t N, int64_t K)
     return (size_t)((M * sKp + 16 + 255) / 256 * 256 + (N * sKp + 16 + 255) / 256 * 256);
 }
 
-template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true, bool DIRECT = false>
+template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true, int DIRECT = 0>
 static hipError_t launch_mx_tiled(const MxGemmArgs& a, hipStream_t st)
 {
     using T = GemmCore<BM, BN, WM, WN, ST, true, OP, RB, FMT, ILV, false, false, DIRECT>;
@@ -324,12 +325,15 @@ hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st)
     }
     if (fp4) {
         if (big) return launch_mx_tiled<256, 256, 4, 2, 2, 128, OP_MXFP4, 0>(a, st);
-        // decode-sized batches (M <= 64) with both scale tensors row-major ([M, sK], [N, sK]; 4-byte aligned): the
-        // 64 x 64 tiles read the scales as given, so no rearrangement launch precedes the GEMM (measured, K = 4096,
-        // N = 11008: M = 1 / 16 / 64 in 11.9 / 12.7 / 16.3 us against 17.5 / 17.6 / 19.5 us; at M = 256 the per-row
-        // reads, 64 cache lines a copy, cost more than the launch: 45.4 against 38.0 us at K = N = 8192)
-        if (a.M <= 64 && a.sa_layout == 0 && a.sb_layout == 1 && (uintptr_t)a.sA % 4 == 0 && (uintptr_t)a.sB % 4 == 0)
-            return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP4, 0, true, true>(a, st);
+        // decode-sized batches (M <= 64) with A's scales row-major [M, sK] and B's row-major [N, sK] or in block
+        // pairs [sK / 2, N, 2] (N even; 4-byte aligned): the 64 x 64 tiles read the scales as given, so no
+        // rearrangement launch precedes the GEMM (measured, K = 4096, N = 11008, row-major B scales: M = 1 / 16 / 64
+        // in 11.9 / 12.7 / 16.3 us against 17.5 / 17.6 / 19.5 us; at M = 256 the per-row reads, 64 cache lines a
+        // copy, cost more than the launch: 45.4 against 38.0 us at K = N = 8192)
+        if (a.M <= 64 && a.sa_layout == 0 && (uintptr_t)a.sA % 4 == 0 && (uintptr_t)a.sB % 4 == 0) {
+            if (a.sb_layout == 1) return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP4, 0, true, 1>(a, st);
+            if (a.N % 2 == 0) return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP4, 0, true, 2>(a, st);
+        }
         return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP4, 0>(a, st);
     }
     switch (a.fmt_a | (a.fmt_b << 3)) {
