@@ -279,7 +279,7 @@ struct GemmCore {
     static_assert(BM % (ROWS_PER_COPY * NW) == 0 && A_COPIES >= 1, "A copies must split evenly over the waves");
     static_assert(!B_KCONTIG || (BN % (ROWS_PER_COPY * NW) == 0 && B_COPIES >= 1), "B copies");
     static_assert(B_KCONTIG || B_TR || (((ROWB / 8) * (BN / 4)) % NT == 0 && B_BLK >= 1), "B blocks");
-    static_assert(!B_TR || (!B_KCONTIG && OP == OP_I8 && 1024 % BN == 0 && BN >= 32 && BN <= 256 &&
+    static_assert(!B_TR || (!B_KCONTIG && (OP == OP_I8 || OP == OP_F8) && 1024 % BN == 0 && BN >= 32 && BN <= 256 &&
                             (ROWB * BN) % (1024 * NW) == 0 && B_COPIES >= 1), "B_TR copies");
     static_assert(!IS_MX || B_KCONTIG, "MX B must be K-contiguous");
     static_assert(OP != OP_BF16 || B_KCONTIG, "bf16 B must be K-contiguous");
@@ -632,13 +632,24 @@ struct GemmCore {
                             fa[i][5] = (int)q[1];
                         }
                     }
-                    v4i ftr[FN];
-                    if constexpr (B_TR)
-                        read_frags_tr((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)sB, troff, s, ftr);
+                    // B_TR fp8: the 32 bytes of k-step s (lane half kh: K rows 64 s + 16 kh .. and 64 s + 32 + 16 kh ..,
+                    // register quads 0 and 1) are the int8-sized transposed reads of steps 2 s and 2 s + 1
+                    v4i ftr[FN], ftr2[OP == OP_F8 ? FN : 1];
+                    if constexpr (B_TR) {
+                        const uint32_t region = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)sB;
+                        if constexpr (OP == OP_F8) {
+                            read_frags_tr(region, troff, 2 * s, ftr);
+                            read_frags_tr(region, troff, 2 * s + 1, ftr2);
+                        } else {
+                            read_frags_tr(region, troff, s, ftr);
+                        }
+                    }
 #pragma unroll
                     for (int j = 0; j < FN; ++j) {
                         v8i fb;
-                        if constexpr (B_TR) {
+                        if constexpr (B_TR && OP == OP_F8) {
+                            fb = (v8i){ftr[j][0], ftr[j][1], ftr[j][2], ftr[j][3], ftr2[j][0], ftr2[j][1], ftr2[j][2], ftr2[j][3]};
+                        } else if constexpr (B_TR) {
                             fb = (v8i){ftr[j][0], ftr[j][1], ftr[j][2], ftr[j][3], 0, 0, 0, 0};
                         } else {
                             fb = read_frag(sB, wn * WTN + j * 32 + r32, s, kh);

@@ -72,15 +72,17 @@ constexpr int op_of_fmt = (FMT == (FMT_BF16 | (FMT_BF16 << 3))) ? OP_BF16 : OP_F
 // waves each run the tile's main loop on their own K / KW range in their own LDS ring, then wave 0 adds the other
 // waves' fp32 accumulators in wave order (one fixed order, so the result does not vary between calls) and runs the
 // epilogue.  For decode-sized batches this puts a tile's whole K in flight at once instead of one serial ring.
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT, bool UA = false, int KW = 1>
+// BTR (B given [K, N], 16-byte K rows): B's K rows are staged like A's and read by LDS transpose reads
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT, bool UA = false, int KW = 1, bool BTR = false>
 __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_f8_kernel(GemmF8Args p)
 {
     constexpr int OP = op_of_fmt<FMT>;
     constexpr int ES = OP == OP_BF16 ? 2 : 1;  // bytes per operand element
     // UA (fp8, B K-contiguous): operands of any alignment and any K (GemmCoreUA)
     using T = typename std::conditional<UA, GemmCoreUA<BM, BN, WM, WN, TB, false, OP, FMT>,
-                                        GemmCore<BM, BN, WM, WN, ST, TB, OP, RB, FMT>>::type;
-    static_assert(KW == 1 || (WM == 1 && WN == 1 && TB && !UA), "k-split waves run one-wave tiles of a K-contiguous B");
+                                        GemmCore<BM, BN, WM, WN, ST, TB, OP, RB, FMT, true, false, BTR>>::type;
+    static_assert(KW == 1 || (WM == 1 && WN == 1 && (TB || BTR) && !UA),
+                  "k-split waves run one-wave tiles of a K-contiguous or LDS-transposed B");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_f8[];
     const int tiles_m = (int)((p.M + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
     int tm, tn;
@@ -104,7 +106,7 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_f8_kernel(GemmF8Args p
     const int kw = KW > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
     const int64_t kc = p.K / KW, k0 = kw * kc;  // this wave's K range (KW > 1: K ES % (KW RB) == 0)
     c.a0 = (uint32_t)((m0 * p.lda + k0) * ES) + da;
-    c.b0 = (uint32_t)(TB ? (n0 * p.ldb + k0) * ES : n0) + db;
+    c.b0 = (uint32_t)(TB ? (n0 * p.ldb + k0) * ES : n0 + k0 * p.ldb) + db;
     c.kbytes = kc * ES;
     // KW > 1: the epilogue's bias and QUANT_PRE words are loaded before the main loop (their latency hides under it;
     // they are older than the main loop's copies, so its counted waits still cover exactly those copies)
@@ -259,17 +261,17 @@ __global__ __launch_bounds__(256) void gemm_f8_generic_kernel(GemmF8Args p)
     }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT, bool UA = false, int KW = 1>
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT, bool UA = false, int KW = 1, bool BTR = false>
 static hipError_t launch_f8_tiled(const GemmF8Args& a, hipStream_t st)
 {
     using T = typename std::conditional<UA, GemmCoreUA<BM, BN, WM, WN, TB, false, op_of_fmt<FMT>, FMT>,
-                                        GemmCore<BM, BN, WM, WN, ST, TB, op_of_fmt<FMT>, RB, FMT>>::type;
+                                        GemmCore<BM, BN, WM, WN, ST, TB, op_of_fmt<FMT>, RB, FMT, true, false, BTR>>::type;
     constexpr int LDS = (int)T::LDS_BYTES * KW;
     static_assert(KW == 1 || (size_t)(KW - 1) * 64 * sizeof(typename T::acc_t) <= (size_t)LDS, "k-split reduction");
     const int tiles = (int)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
-    const hipError_t e = ensure_dynamic_lds<gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT, UA, KW>>(LDS);
+    const hipError_t e = ensure_dynamic_lds<gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT, UA, KW, BTR>>(LDS);
     if (e != hipSuccess) return e;
-    launch_k((gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT, UA, KW>), dim3(tiles), dim3(T::NT * KW), LDS, st, a);
+    launch_k((gemm_f8_kernel<BM, BN, WM, WN, ST, TB, RB, FMT, UA, KW, BTR>), dim3(tiles), dim3(T::NT * KW), LDS, st, a);
     return hipGetLastError();
 }
 
@@ -295,6 +297,10 @@ static hipError_t launch_f8_fmt(const GemmF8Args& a, bool ua, hipStream_t st)
     if constexpr (ES == 1) {
         if (a.trans_b && skinny && c_wide && a.atomic == C_STORE && a.K % 256 == 0)
             return launch_f8_tiled<32, 32, 1, 1, 4, true, 64, FMT, false, 4>(a, st);
+        // ... and with B given [K, N] (16-byte K rows): B's K rows staged like A's, read by LDS transpose reads
+        if (!a.trans_b && skinny && c_wide && a.atomic == C_STORE && a.K % 256 == 0 && a.ldb % 16 == 0 &&
+            (uintptr_t)a.B % 16 == 0)
+            return launch_f8_tiled<32, 32, 1, 1, 4, false, 64, FMT, false, 4, true>(a, st);
     }
     if (a.trans_b) {
         if (big) return (a.K * ES) % 128 == 0 ? launch_f8_tiled<256, 256, 4, 2, 2, true, 128, FMT>(a, st)

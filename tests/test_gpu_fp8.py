@@ -148,17 +148,21 @@ def test_fp8_tiled_small(ascq_gpu, fa, fb, out_type, quant):
 
 
 @pytest.mark.parametrize("out_type", [O.F16, O.BF16, O.F32])
-@pytest.mark.parametrize("M,N,K", [(1, 200, 512), (16, 136, 1024), (29, 96, 256), (40, 300, 768), (64, 1100, 2048)])
-def test_fp8_decode_ksplit(ascq_gpu, out_type, M, N, K):
-    """decode-sized batches with B [N, K] and K % 256 == 0: 32 x 32 tiles whose K is split over four waves (fp32
-    partials added in one fixed order), ragged N, bias and per-channel scales; a second call returns the same bits"""
+@pytest.mark.parametrize("trans_b", [True, False])
+@pytest.mark.parametrize("M,N,K", [(1, 200, 512), (1, 208, 512), (16, 136, 1024), (29, 96, 256), (40, 304, 768),
+                                   (64, 1100, 2048), (64, 1104, 2048)])
+def test_fp8_decode_ksplit(ascq_gpu, out_type, trans_b, M, N, K):
+    """decode-sized batches with K % 256 == 0: 32 x 32 tiles whose K is split over four waves (fp32 partials added
+    in one fixed order), B given [N, K], or [K, N] with N % 16 == 0 (its K rows staged like A's and read by LDS
+    transpose reads; other N take the general tiles), ragged N, bias and per-channel scales; a second call returns
+    the same bits"""
     fa, fb = O.FP8_E4M3, O.FP8_E5M2
     hi = 0x40 if out_type == O.F16 else 128
-    A, B, b, qs, qv = fp8_case(31 + M, M, N, K, fa, fb, out_type, trans_b=True, quant="vector", hi=hi)
-    got = run_fp8(ascq_gpu, A, B, fa, fb, M, N, K, out_type, trans_b=True, bias=b, qvec=qv)
-    v, d = expected(A, B, fa, fb, b, qs, qv, False, True, K)
+    A, B, b, qs, qv = fp8_case(31 + M, M, N, K, fa, fb, out_type, trans_b=trans_b, quant="vector", hi=hi)
+    got = run_fp8(ascq_gpu, A, B, fa, fb, M, N, K, out_type, trans_b=trans_b, bias=b, qvec=qv)
+    v, d = expected(A, B, fa, fb, b, qs, qv, False, trans_b, K)
     check_out(got, v, d, out_type, f"M={M}")
-    again = run_fp8(ascq_gpu, A, B, fa, fb, M, N, K, out_type, trans_b=True, bias=b, qvec=qv)
+    again = run_fp8(ascq_gpu, A, B, fa, fb, M, N, K, out_type, trans_b=trans_b, bias=b, qvec=qv)
     assert np.array_equal(np.nan_to_num(got, nan=7.0), np.nan_to_num(again, nan=7.0))
 
 
