@@ -204,11 +204,19 @@ bool bytes_transposes_a(const ascq_matmul_s* h) { return h->trans_a != 0; }
 // int8 / fp8 B in the NZ fractal layout: converted to a K-contiguous [N, K] copy in the workspace at every IterateAll
 bool bytes_nz_b(const ascq_matmul_s* h) { return h->ty.b_format == ASCQ_FORMAT_NZ; }
 
-size_t bytes_workspace(const ascq_matmul_s* h)
+// the operand copies of an int8 / fp8 Matmul (transposed or NZ-converted B, transposed A)
+size_t bytes_operands(const ascq_matmul_s* h)
 {
     size_t need = bytes_transposes_b(h) || bytes_nz_b(h) ? align256((size_t)h->N * (size_t)h->K) : 0;
     if (bytes_transposes_a(h)) need += align256((size_t)h->M * (size_t)h->K);
     return need;
+}
+
+// ... then, for decode-sized batches, the accumulators of the K split across workgroups
+size_t bytes_workspace(const ascq_matmul_s* h)
+{
+    const int tb = h->trans_b || bytes_transposes_b(h) || bytes_nz_b(h);  // B as the GEMM sees it
+    return bytes_operands(h) + align256(ascq::decode_split_ws_bytes(h->M, h->N, h->K, tb));
 }
 
 size_t workspace_need(const ascq_matmul_s* h)
@@ -254,6 +262,29 @@ ascq_status ensure_workspace(ascq_matmul_s* h)
     if (e != hipSuccess) return hip_status(e, "hipMalloc(workspace)");
     h->ws_bytes = need;
     h->ws_owned = true;
+    return ASCQ_OK;
+}
+
+// the K-split partials' region of the workspace for this call (null when the call cannot use it: no split form for
+// these sizes, enAtomic, or a caller's workspace too small for it -- then the call runs without the split)
+ascq_status split_region(ascq_matmul_s* h, int64_t m, int64_t n, int64_t k, uint8_t en_atomic, uint8_t** ws,
+                         size_t* bytes)
+{
+    *ws = nullptr;
+    *bytes = 0;
+    const int tb = h->trans_b || bytes_transposes_b(h) || bytes_nz_b(h);  // B as the GEMM sees it
+    const size_t need = ascq::decode_split_ws_bytes(m, n, k, tb);
+    if (need == 0 || en_atomic != 0) return ASCQ_OK;
+    const size_t off = bytes_operands(h);
+    if (h->ws && !h->ws_owned) {  // the caller's workspace: used when it has room, never replaced
+        if (h->ws_bytes < off + need) return ASCQ_OK;
+    } else {
+        ascq_status s = ensure_workspace(h);
+        if (s != ASCQ_OK) return s;
+        if (h->ws_bytes < off + need) return ASCQ_OK;
+    }
+    *ws = (uint8_t*)h->ws + off;
+    *bytes = h->ws_bytes - off;
     return ASCQ_OK;
 }
 
@@ -610,6 +641,8 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         g.trans_a = o.trans_a;
         g.trans_b = o.trans_b;
         g.atomic = atomic;
+        s = split_region(h, m, n, k, atomic, &g.ws, &g.ws_bytes);
+        if (s != ASCQ_OK) return s;
         return hip_status(ascq::launch_gemm_i8(g, st), "gemm_i8");
     }
     case K_INT4: {
@@ -734,6 +767,8 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         g.fmt_a = f8f6f4_code(h->ty.a_type);
         g.fmt_b = f8f6f4_code(h->ty.b_type);
         g.atomic = atomic;
+        s = split_region(h, m, n, k, atomic, &g.ws, &g.ws_bytes);
+        if (s != ASCQ_OK) return s;
         return hip_status(ascq::launch_gemm_f8(g, st), "gemm_f8");
     }
     case K_ANTIQUANT: {

@@ -34,19 +34,35 @@ using I8Core = typename std::conditional<UA, GemmCoreUA<BM, BN, WM, WN, TB, CT>,
 // their own K / KW range (K a multiple of KW * RB, so every wave runs the same stages and meets the same barriers) in
 // their own LDS ring, then sum their int32 accumulators through LDS (exact in any order) and wave 0 runs the epilogue.
 // For small problems (the W8A8 sample, 32 tiles) this cuts the serial K loop of each tile KW-fold.
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, bool BTR = false, int KW = 1, bool UA = false>
+// PH (K split across workgroups, decode-sized batches): 1 -- workgroup b runs split b / tiles of tile b % tiles, its
+// K range a whole number of KW RB units (the units shared out as evenly as p.splits allows), and stores the tile's
+// accumulators in p.ws ([split][tile][fragment][lane]); 2 -- one wave per tile adds the splits' accumulators in split
+// order (int32: exact) and runs the epilogue.
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, bool BTR = false, int KW = 1, bool UA = false,
+          int PH = 0>
 __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_i8_kernel(GemmI8Args p)
 {
     using T = I8Core<BM, BN, WM, WN, ST, TB, RB, false, BTR, UA>;
     static_assert(!UA || KW == 1, "any-alignment tiles run whole K");
     static_assert(KW == 1 || (WM == 1 && WN == 1), "k-split waves run one-wave tiles");
+    static_assert(PH == 0 || (WM == 1 && WN == 1 && !UA && (PH == 2 || KW > 1)), "K split across workgroups");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tiles_m = (int)((p.M + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
+    const int ntiles = tiles_m * tiles_n;
+    const int tile = PH == 1 ? (int)blockIdx.x % ntiles : (int)blockIdx.x;
+    const int split = PH == 1 ? (int)blockIdx.x / ntiles : 0;
     int tm, tn;
-    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    tile_coords(tile, tiles_m, tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     const int kw = KW > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
-    const int64_t kc = p.K / KW, k0 = kw * kc;  // this wave's K range (KW > 1: K % (KW RB) == 0)
+    int64_t kg0 = 0, kg = p.K;  // this workgroup's K range
+    if constexpr (PH == 1) {
+        const int64_t units = p.K / (KW * RB);
+        const int64_t u0 = units * split / p.splits, u1 = units * (split + 1) / p.splits;
+        kg0 = u0 * KW * RB;
+        kg = (u1 - u0) * KW * RB;
+    }
+    const int64_t kc = kg / KW, k0 = kg0 + kw * kc;  // this wave's K range (KW > 1: a multiple of RB)
     CoreArgs c{};
     const uint32_t a_bytes = (uint32_t)(p.lda * (p.M - 1) + p.K);
     const uint32_t b_bytes = (uint32_t)(TB ? p.ldb * (p.N - 1) + p.K : p.ldb * (p.K - 1) + p.N);
@@ -68,9 +84,10 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_i8_kernel(GemmI8Args p
     // KW > 1 (small problems, where the kernel is one chain of latencies): the epilogue's bias and QUANT_PRE words are
     // loaded before the main loop, so their latency hides under it instead of following it.  They are older than the
     // main loop's copies, whose counted waits therefore still cover exactly those copies (loads return in order).
+    constexpr bool PRE = KW > 1 && PH == 0;  // the epilogue's words loaded before the main loop
     int32_t pre_bias[T::FN];
     uint64_t pre_w[T::FN];
-    if constexpr (KW > 1) {
+    if constexpr (PRE) {
 #pragma unroll
         for (int j = 0; j < T::FN; ++j) {
             const int cl = T::frag_col(0, j, (int)threadIdx.x & 63);
@@ -80,16 +97,39 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_i8_kernel(GemmI8Args p
         }
     }
     typename T::acc_t acc[T::FM][T::FN];
-    T::run(c, smem + (KW > 1 ? kw * T::LDS_BYTES : 0), acc, KW > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x);
+    constexpr int F = T::FM * T::FN;  // accumulator fragments of the tile
+    v16i* part = (v16i*)p.ws;         // PH 1 / 2: [split][tile][F][64 lanes]
+    if constexpr (PH == 2) {
+        const int ln = threadIdx.x & 63;
+#pragma unroll
+        for (int f = 0; f < F; ++f) acc[f / T::FN][f % T::FN] = part[((int64_t)tile * F + f) * 64 + ln];
+        for (int sp = 1; sp < p.splits; ++sp)
+#pragma unroll
+            for (int f = 0; f < F; ++f)
+                acc[f / T::FN][f % T::FN] += part[(((int64_t)sp * ntiles + tile) * F + f) * 64 + ln];
+    } else {
+        T::run(c, smem + (KW > 1 ? kw * T::LDS_BYTES : 0), acc, KW > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x);
+    }
     if constexpr (KW > 1) {
         __syncthreads();  // every wave's main loop is done with its LDS ring
-        v16i* red = (v16i*)smem;  // [KW - 1][64 lanes] accumulator fragments
+        v16i* red = (v16i*)smem;  // [KW - 1][F][64 lanes] accumulator fragments
         const int lane = threadIdx.x & 63;
-        if (kw > 0) red[(kw - 1) * 64 + lane] = acc[0][0];
+        if (kw > 0) {
+#pragma unroll
+            for (int f = 0; f < F; ++f) red[((kw - 1) * F + f) * 64 + lane] = acc[f / T::FN][f % T::FN];
+        }
         __syncthreads();
         if (kw != 0) return;
 #pragma unroll
-        for (int w = 0; w < KW - 1; ++w) acc[0][0] += red[w * 64 + lane];
+        for (int w = 0; w < KW - 1; ++w)
+#pragma unroll
+            for (int f = 0; f < F; ++f) acc[f / T::FN][f % T::FN] += red[(w * F + f) * 64 + lane];
+    }
+    if constexpr (PH == 1) {
+        const int ln = threadIdx.x & 63;
+#pragma unroll
+        for (int f = 0; f < F; ++f) part[(((int64_t)split * ntiles + tile) * F + f) * 64 + ln] = acc[f / T::FN][f % T::FN];
+        return;
     }
 
     // epilogue: per 32x32 accumulator tile, lane holds column lane%32 and 16 rows (GemmCore::frag_row); stores go
@@ -126,8 +166,8 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_i8_kernel(GemmI8Args p
             const int cl = T::frag_col(wn, j, lane);
             const bool cok = cl < c.cols;
             const int64_t col = n0 + cl;
-            const int32_t bias = KW > 1 ? pre_bias[j] : (p.bias && cok) ? p.bias[col] : 0;
-            const uint64_t w = KW > 1 ? pre_w[j] : (p.qvec && cok) ? p.qvec[col] : p.qscalar;
+            const int32_t bias = PRE ? pre_bias[j] : (p.bias && cok) ? p.bias[col] : 0;
+            const uint64_t w = PRE ? pre_w[j] : (p.qvec && cok) ? p.qvec[col] : p.qscalar;
             const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
             const uint32_t cbase = cok ? (uint32_t)(cl * esize) : OOB;
 #pragma unroll
@@ -429,6 +469,45 @@ static hipError_t launch_tiled(const GemmI8Args& a, hipStream_t st)
     return hipGetLastError();
 }
 
+// the K split across workgroups of decode-sized batches: 32 x 128 one-wave tiles, four K-split waves per
+// workgroup, splits chosen so that tiles x splits is about 256 (one workgroup per CU); K % 256 == 0
+constexpr int DS_BM = 32, DS_BN = 128, DS_KW = 4, DS_RB = 64;
+int decode_splits(int64_t M, int64_t N, int64_t K, int trans_b)
+{
+    // B given [K, N] with long K or wide N only: elsewhere the 32 x 32 K-split tiles measured faster (K = 11008 /
+    // 14336, N = 4096, M = 1: 36.6 / 45.8 -> 23.3 / 26.0 us; K = N = 8192: 32.1 -> 26.8 us; K = 4096, N = 14336:
+    // 29.9 -> 23.1 us; slower at K = 4096, N = 8192 / 11008 and with B given [N, K])
+    if (trans_b || !(K >= 8192 || N >= 12288)) return 1;
+    if (M > DS_BM || M < 1 || N < 1 || K % (DS_KW * DS_RB) != 0) return 1;
+    const int64_t tiles = (N + DS_BN - 1) / DS_BN;
+    int64_t s = (256 + tiles / 2) / tiles;
+    const int64_t units = K / (DS_KW * DS_RB);
+    if (s > units) s = units;
+    return s < 2 ? 1 : (int)s;
+}
+size_t decode_split_ws_bytes(int64_t M, int64_t N, int64_t K, int trans_b)
+{
+    const int s = decode_splits(M, N, K, trans_b);
+    return s < 2 ? 0 : (size_t)s * (size_t)((N + DS_BN - 1) / DS_BN) * (DS_BN / 32) * 64 * 64;
+}
+
+template <bool TB, bool BTR>
+static hipError_t launch_i8_split(GemmI8Args a, hipStream_t st)
+{
+    using T = I8Core<DS_BM, DS_BN, 1, 1, 3, TB, DS_RB, false, BTR, false>;
+    const int tiles = (int)((a.N + DS_BN - 1) / DS_BN);
+    constexpr size_t lds = T::LDS_BYTES * DS_KW;
+    static_assert((size_t)(DS_KW - 1) * T::FM * T::FN * 64 * sizeof(typename T::acc_t) <= lds, "k-split reduction");
+    hipError_t e = ensure_dynamic_lds<gemm_i8_kernel<DS_BM, DS_BN, 1, 1, 3, TB, DS_RB, BTR, DS_KW, false, 1>>((int)lds);
+    if (e != hipSuccess) return e;
+    launch_k((gemm_i8_kernel<DS_BM, DS_BN, 1, 1, 3, TB, DS_RB, BTR, DS_KW, false, 1>), dim3(tiles * a.splits),
+             dim3(64 * DS_KW), (uint32_t)lds, st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    launch_k((gemm_i8_kernel<DS_BM, DS_BN, 1, 1, 3, TB, DS_RB, BTR, 1, false, 2>), dim3(tiles), dim3(64), 0u, st, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
 {
     const bool a_ok = !a.trans_a && a.lda % 16 == 0 && ((uintptr_t)a.A % 16 == 0) && a.lda * a.M < (1ll << 31);
@@ -449,6 +528,16 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
         const int64_t t64 = ((a.M + 63) / 64) * ((a.N + 63) / 64);
         const bool skinny = a.M <= 32 || (a.M <= 64 && t64 < 160);
         const bool ksplit = (tiny || skinny) && a.K % 256 == 0 && a.atomic == C_STORE;
+        // decode-sized batches (up to 32 rows) with B given [K, N] and a workspace for the partials: 32 x 128 tiles
+        // (whole 128-byte K-row runs instead of 32-byte ones) with the K split across workgroups as well, where
+        // decode_splits finds that faster than the 32 x 32 tiles below
+        const int splits = decode_splits(a.M, a.N, a.K, a.trans_b);
+        if (!tiny && splits > 1 && a.atomic == C_STORE && a.epi != EPI_REQ4 && a.ws &&
+            a.ws_bytes >= decode_split_ws_bytes(a.M, a.N, a.K, a.trans_b) && a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0) {
+            GemmI8Args b = a;
+            b.splits = splits;
+            return launch_i8_split<false, true>(b, st);
+        }
         if (ksplit && a.trans_b) return launch_tiled<32, 32, 1, 1, 4, true, 64, false, 4>(a, st);
         if (ksplit && a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0)
             return launch_tiled<32, 32, 1, 1, 4, false, 64, true, 4>(a, st);

@@ -102,8 +102,18 @@ struct GemmI8Args {
     int epi;              // EPI_*
     int trans_a, trans_b;
     int atomic;           // C_STORE, or C_ADD / C_MAX / C_MIN (int32 / f16 / bf16 C): IterateAll's enAtomic
+    uint8_t* ws;          // decode-sized batches: room for the K-split partials (decode_split_ws_bytes), or null
+    size_t ws_bytes;
+    int splits;           // (set by the launcher) workgroups per tile of the K-split form
 };
 hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st);
+// Decode-sized batches (M <= 32, K % 256 == 0) with B given [K, N] (trans_b 0) and long K or wide N run 32 x 128
+// tiles whose K is split over several workgroups (four waves each) so that about 256 workgroups stream B; their
+// accumulators meet in the workspace and a second launch adds them in split order and runs the epilogue.
+// decode_splits gives the workgroups per tile (1: the form is not used) and decode_split_ws_bytes the workspace the
+// partials need.
+int decode_splits(int64_t M, int64_t N, int64_t K, int trans_b);
+size_t decode_split_ws_bytes(int64_t M, int64_t N, int64_t K, int trans_b);
 
 // gemm_f8.hip
 constexpr int FMT_BF16 = 7;  // operand format code outside the f8f6f4 codes: bf16 elements (OP_BF16)
@@ -123,6 +133,9 @@ struct GemmF8Args {
                           // elements)
     int trans_a, trans_b;
     int atomic;           // C_STORE, or C_ADD / C_MAX / C_MIN (f32 / f16 / bf16 C): IterateAll's enAtomic
+    uint8_t* ws;          // decode-sized batches: room for the K-split partials (decode_split_ws_bytes), or null
+    size_t ws_bytes;
+    int splits;           // (set by the launcher) workgroups per tile of the K-split form
 };
 hipError_t launch_gemm_f8(const GemmF8Args& a, hipStream_t st);
 

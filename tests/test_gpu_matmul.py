@@ -89,6 +89,30 @@ def test_int8_matmul_variants(ascq_gpu, oracle, c_type, vector, trans_b, shape):
     np.testing.assert_array_equal(_bits(c), ref)
 
 
+@pytest.mark.parametrize("trans_b", [False, True])
+@pytest.mark.parametrize("shape", [(1, 4096, 8192), (16, 12400, 768), (32, 4096, 11008), (29, 4000, 9216), (5, 12300, 512),
+                                   (16, 5000, 768)])
+def test_int8_decode_split(ascq_gpu, oracle, trans_b, shape):
+    """decode-sized batches (M <= 32, K % 256 == 0).  B given [K, N] with long K or wide N: 32 x 128 tiles whose K is
+    split over several workgroups of four waves, the int32 partials meeting in the workspace and added (exactly) by a
+    second launch before the epilogue -- K split as evenly as its 256-byte units allow (K = 11008: 43 units; K = 512:
+    two splits); the other shapes and B given [N, K] take the 32 x 32 K-split tiles.  Ragged N; every epilogue: int32,
+    DEQF16 with per-channel words, bf16 with a scalar word, bit-exact vs the oracle"""
+    rng = seeded(sum(shape) + trans_b)
+    M, N, K = shape
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, (N, K) if trans_b else (K, N), dtype=np.int8)
+    bias = rng.integers(-(1 << 20), 1 << 20, N, dtype=np.int32)
+    acc_ref = O.matmul_i8(A, B, bias, trans_b=trans_b)
+    np.testing.assert_array_equal(_run(ascq_gpu, A, B, bias, ascq_gpu.INT32, trans_b=trans_b).numpy(), acc_ref)
+    words = _quant_words(rng, N, 2.0 ** -20, 2.0 ** -4)
+    c = _run(ascq_gpu, A, B, bias, ascq_gpu.F16, words=words, trans_b=trans_b)
+    np.testing.assert_array_equal(_bits(c), O.mm_dequant(acc_ref, O.F16, qvec=words))
+    word = int(np.float32(0.00123).view(np.uint32))
+    c = _run(ascq_gpu, A, B, bias, ascq_gpu.BF16, scalar=word, trans_b=trans_b)
+    np.testing.assert_array_equal(_bits(c), O.mm_dequant(acc_ref, O.BF16, qscalar=word))
+
+
 def test_int8_matmul_int32_big(ascq_gpu, oracle):
     rng = seeded(9)
     M, N, K = 2048, 1536, 2048
