@@ -73,7 +73,12 @@ constexpr int op_of_fmt = (FMT == (FMT_BF16 | (FMT_BF16 << 3))) ? OP_BF16 : OP_F
 // waves' fp32 accumulators in wave order (one fixed order, so the result does not vary between calls) and runs the
 // epilogue.  For decode-sized batches this puts a tile's whole K in flight at once instead of one serial ring.
 // BTR (B given [K, N], 16-byte K rows): B's K rows are staged like A's and read by LDS transpose reads
-template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT, bool UA = false, int KW = 1, bool BTR = false>
+// PH (K split across workgroups, decode-sized batches): 1 -- workgroup b runs split b / tiles of tile b % tiles, its K
+// range a whole number of KW RB units (shared out as evenly as p.splits allows), and stores the tile's fp32
+// accumulators in p.ws ([split][tile][fragment][lane]); 2 -- one wave per tile adds the splits' accumulators in split
+// order (one fixed order, so the result does not vary between calls) and runs the epilogue.
+template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT, bool UA = false, int KW = 1, bool BTR = false,
+          int PH = 0>
 __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_f8_kernel(GemmF8Args p)
 {
     constexpr int OP = op_of_fmt<FMT>;
@@ -83,10 +88,14 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_f8_kernel(GemmF8Args p
                                         GemmCore<BM, BN, WM, WN, ST, TB, OP, RB, FMT, true, false, BTR>>::type;
     static_assert(KW == 1 || (WM == 1 && WN == 1 && (TB || BTR) && !UA),
                   "k-split waves run one-wave tiles of a K-contiguous or LDS-transposed B");
+    static_assert(PH == 0 || (WM == 1 && WN == 1 && !UA && ES == 1 && (PH == 2 || KW > 1)), "K split across workgroups");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_f8[];
     const int tiles_m = (int)((p.M + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
+    const int ntiles = tiles_m * tiles_n;
+    const int tile = PH == 1 ? (int)blockIdx.x % ntiles : (int)blockIdx.x;
+    const int split = PH == 1 ? (int)blockIdx.x / ntiles : 0;
     int tm, tn;
-    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    tile_coords(tile, tiles_m, tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     CoreArgs c{};
     const uint32_t a_bytes = (uint32_t)((p.lda * (p.M - 1) + p.K) * ES);
@@ -104,15 +113,23 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_f8_kernel(GemmF8Args p
     c.rows = (int32_t)(p.M - m0 < BM ? p.M - m0 : BM);
     c.cols = (int32_t)(p.N - n0 < BN ? p.N - n0 : BN);
     const int kw = KW > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
-    const int64_t kc = p.K / KW, k0 = kw * kc;  // this wave's K range (KW > 1: K ES % (KW RB) == 0)
+    int64_t kg0 = 0, kg = p.K;  // this workgroup's K range
+    if constexpr (PH == 1) {
+        const int64_t units = p.K / (KW * RB);
+        const int64_t u0 = units * split / p.splits, u1 = units * (split + 1) / p.splits;
+        kg0 = u0 * KW * RB;
+        kg = (u1 - u0) * KW * RB;
+    }
+    const int64_t kc = kg / KW, k0 = kg0 + kw * kc;  // this wave's K range (KW > 1: K ES % (KW RB) == 0)
     c.a0 = (uint32_t)((m0 * p.lda + k0) * ES) + da;
     c.b0 = (uint32_t)(TB ? (n0 * p.ldb + k0) * ES : n0 + k0 * p.ldb) + db;
     c.kbytes = kc * ES;
     // KW > 1: the epilogue's bias and QUANT_PRE words are loaded before the main loop (their latency hides under it;
     // they are older than the main loop's copies, so its counted waits still cover exactly those copies)
+    constexpr bool PRE = KW > 1 && PH == 0;
     float pre_bias[T::FN];
     uint64_t pre_w[T::FN];
-    if constexpr (KW > 1) {
+    if constexpr (PRE) {
 #pragma unroll
         for (int j = 0; j < T::FN; ++j) {
             const int cl = T::frag_col(0, j, (int)threadIdx.x & 63);
@@ -121,17 +138,41 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_f8_kernel(GemmF8Args p
             pre_w[j] = (p.qvec && cok) ? p.qvec[n0 + cl] : p.qscalar;
         }
     }
-    typename T::acc_t acc[T::FM][T::FN];
-    T::run(c, smem_f8 + (KW > 1 ? kw * T::LDS_BYTES : 0), acc, KW > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x);
+    typedef typename T::acc_t acc_t;
+    acc_t acc[T::FM][T::FN];
+    constexpr int F = T::FM * T::FN;  // accumulator fragments of the tile
+    acc_t* part = (acc_t*)p.ws;       // PH 1 / 2: [split][tile][F][64 lanes]
+    if constexpr (PH == 2) {
+        const int ln = threadIdx.x & 63;
+#pragma unroll
+        for (int f = 0; f < F; ++f) acc[f / T::FN][f % T::FN] = part[((int64_t)tile * F + f) * 64 + ln];
+        for (int sp = 1; sp < p.splits; ++sp)
+#pragma unroll
+            for (int f = 0; f < F; ++f)
+                acc[f / T::FN][f % T::FN] += part[(((int64_t)sp * ntiles + tile) * F + f) * 64 + ln];
+    } else {
+        T::run(c, smem_f8 + (KW > 1 ? kw * T::LDS_BYTES : 0), acc, KW > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x);
+    }
     if constexpr (KW > 1) {
         __syncthreads();  // every wave's main loop is done with its LDS ring
-        typename T::acc_t* red = (typename T::acc_t*)smem_f8;  // [KW - 1][64 lanes] accumulator fragments
+        acc_t* red = (acc_t*)smem_f8;  // [KW - 1][F][64 lanes] accumulator fragments
         const int ln = threadIdx.x & 63;
-        if (kw > 0) red[(kw - 1) * 64 + ln] = acc[0][0];
+        if (kw > 0) {
+#pragma unroll
+            for (int f = 0; f < F; ++f) red[((kw - 1) * F + f) * 64 + ln] = acc[f / T::FN][f % T::FN];
+        }
         __syncthreads();
         if (kw != 0) return;
 #pragma unroll
-        for (int w = 0; w < KW - 1; ++w) acc[0][0] += red[w * 64 + ln];
+        for (int w = 0; w < KW - 1; ++w)
+#pragma unroll
+            for (int f = 0; f < F; ++f) acc[f / T::FN][f % T::FN] += red[(w * F + f) * 64 + ln];
+    }
+    if constexpr (PH == 1) {
+        const int ln = threadIdx.x & 63;
+#pragma unroll
+        for (int f = 0; f < F; ++f) part[(((int64_t)split * ntiles + tile) * F + f) * 64 + ln] = acc[f / T::FN][f % T::FN];
+        return;
     }
 
     // epilogue through a buffer resource over the output tile (rows past M dropped by its range)
@@ -168,8 +209,8 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_f8_kernel(GemmF8Args p
             const int cl = T::frag_col(wn, j, lane);
             const bool cok = cl < c.cols;
             const int64_t col = n0 + cl;
-            const float bias = KW > 1 ? pre_bias[j] : (p.bias && cok) ? p.bias[col] : 0.0f;
-            const uint64_t w = KW > 1 ? pre_w[j] : (p.qvec && cok) ? p.qvec[col] : p.qscalar;
+            const float bias = PRE ? pre_bias[j] : (p.bias && cok) ? p.bias[col] : 0.0f;
+            const uint64_t w = PRE ? pre_w[j] : (p.qvec && cok) ? p.qvec[col] : p.qscalar;
             const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
             const uint32_t cbase = cok ? (uint32_t)(cl * esize) : OOB;
 #pragma unroll
@@ -275,6 +316,26 @@ static hipError_t launch_f8_tiled(const GemmF8Args& a, hipStream_t st)
     return hipGetLastError();
 }
 
+// the K split across workgroups of decode-sized batches with B given [K, N] (decode_splits): 32 x 128 one-wave tiles,
+// four K-split waves per workgroup; fp32 partials in a.ws, added in split order by the second launch
+template <int FMT>
+static hipError_t launch_f8_split(GemmF8Args a, hipStream_t st)
+{
+    constexpr int BM = 32, BN = 128, KWS = 4, RB = 64;
+    using T = GemmCore<BM, BN, 1, 1, 3, false, op_of_fmt<FMT>, RB, FMT, true, false, true>;
+    const int tiles = (int)((a.N + BN - 1) / BN);
+    constexpr size_t lds = T::LDS_BYTES * KWS;
+    static_assert((size_t)(KWS - 1) * T::FM * T::FN * 64 * sizeof(typename T::acc_t) <= lds, "k-split reduction");
+    hipError_t e = ensure_dynamic_lds<gemm_f8_kernel<BM, BN, 1, 1, 3, false, RB, FMT, false, KWS, true, 1>>((int)lds);
+    if (e != hipSuccess) return e;
+    launch_k((gemm_f8_kernel<BM, BN, 1, 1, 3, false, RB, FMT, false, KWS, true, 1>), dim3(tiles * a.splits),
+             dim3(64 * KWS), (uint32_t)lds, st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    launch_k((gemm_f8_kernel<BM, BN, 1, 1, 3, false, RB, FMT, false, 1, true, 2>), dim3(tiles), dim3(64), 0u, st, a);
+    return hipGetLastError();
+}
+
 template <int FMT>
 static hipError_t launch_f8_fmt(const GemmF8Args& a, bool ua, hipStream_t st)
 {
@@ -297,9 +358,19 @@ static hipError_t launch_f8_fmt(const GemmF8Args& a, bool ua, hipStream_t st)
     if constexpr (ES == 1) {
         if (a.trans_b && skinny && c_wide && a.atomic == C_STORE && a.K % 256 == 0)
             return launch_f8_tiled<32, 32, 1, 1, 4, true, 64, FMT, false, 4>(a, st);
-        // ... and with B given [K, N] (16-byte K rows): B's K rows staged like A's, read by LDS transpose reads
-        if (!a.trans_b && skinny && c_wide && a.atomic == C_STORE && a.K % 256 == 0 && a.ldb % 16 == 0 &&
-            (uintptr_t)a.B % 16 == 0)
+        // ... and with B given [K, N] (16-byte K rows): B's K rows staged like A's, read by LDS transpose reads;
+        // for long K or wide N with a workspace for the partials, 32 x 128 tiles with the K split across workgroups
+        // too (decode_splits: the int8 Matmul's rule)
+        const int splits = decode_splits(a.M, a.N, a.K, a.trans_b);
+        const bool b_tr = !a.trans_b && a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0;
+        if (b_tr && splits > 1 && c_wide && a.atomic == C_STORE && a.ws &&
+            a.ws_bytes >= decode_split_ws_bytes(a.M, a.N, a.K, a.trans_b) &&
+            ((a.M + 63) / 64) * ((a.N + 127) / 128) >= 32) {
+            GemmF8Args b = a;
+            b.splits = splits;
+            return launch_f8_split<FMT>(b, st);
+        }
+        if (b_tr && skinny && c_wide && a.atomic == C_STORE && a.K % 256 == 0)
             return launch_f8_tiled<32, 32, 1, 1, 4, false, 64, FMT, false, 4, true>(a, st);
     }
     if (a.trans_b) {

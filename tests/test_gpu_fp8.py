@@ -150,12 +150,13 @@ def test_fp8_tiled_small(ascq_gpu, fa, fb, out_type, quant):
 @pytest.mark.parametrize("out_type", [O.F16, O.BF16, O.F32])
 @pytest.mark.parametrize("trans_b", [True, False])
 @pytest.mark.parametrize("M,N,K", [(1, 200, 512), (1, 208, 512), (16, 136, 1024), (29, 96, 256), (40, 304, 768),
-                                   (64, 1100, 2048), (64, 1104, 2048)])
+                                   (64, 1100, 2048), (64, 1104, 2048), (1, 4096, 8192), (16, 12400, 768)])
 def test_fp8_decode_ksplit(ascq_gpu, out_type, trans_b, M, N, K):
     """decode-sized batches with K % 256 == 0: 32 x 32 tiles whose K is split over four waves (fp32 partials added
     in one fixed order), B given [N, K], or [K, N] with N % 16 == 0 (its K rows staged like A's and read by LDS
-    transpose reads; other N take the general tiles), ragged N, bias and per-channel scales; a second call returns
-    the same bits"""
+    transpose reads; other N take the general tiles); with B given [K, N] and long K or wide N (the last two shapes)
+    32 x 128 tiles whose K is split across workgroups too, the fp32 partials added in split order by a second
+    launch.  Ragged N, bias and per-channel scales; a second call returns the same bits"""
     fa, fb = O.FP8_E4M3, O.FP8_E5M2
     hi = 0x40 if out_type == O.F16 else 128
     A, B, b, qs, qv = fp8_case(31 + M, M, N, K, fa, fb, out_type, trans_b=trans_b, quant="vector", hi=hi)
