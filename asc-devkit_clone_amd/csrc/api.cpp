@@ -241,6 +241,7 @@ size_t workspace_need(const ascq_matmul_s* h)
         const size_t kb = mx_is_fp4(h) ? (size_t)(h->K / 2) : (size_t)h->K;
         size_t need = h->trans_b ? 0 : align256((size_t)h->N * kb);
         need += ascq::mx_scale_workspace_bytes(h->M, h->N, h->K);
+        if (mx_is_fp4(h) && !mx_is_fp6(h)) need += align256(ascq::mx_decode_split_ws_bytes(h->M, h->N, h->K));
         if (mx_is_fp6(h))
             need += align256((size_t)h->M * kb) + align256(ascq::fp6_q_plane_bytes(h->M, h->K)) +
                     align256((size_t)h->N * kb) + align256(ascq::fp6_q_plane_bytes(h->N, h->K));
@@ -825,8 +826,14 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         if (fp4 && !h->trans_b && h->N % 2 != 0) return fail(ASCQ_E_INVALID_ARG, "iterate_all: [K, N] fp4 B needs even N");
         if (!aligned(h->a, 16) || !aligned(h->b, 16) || !aligned(h->scale_a, 4) || !aligned(h->scale_b, 4))
             return fail(ASCQ_E_INVALID_ARG, "iterate_all: MX operands must be 16-byte (scales 4-byte) aligned");
-        ascq_status s = ensure_workspace(h);
-        if (s != ASCQ_OK) return s;
+        // a caller's workspace sized without the decode partials runs the call without the K split across workgroups
+        const size_t part = fp4 && !mx_is_fp6(h) ? align256(ascq::mx_decode_split_ws_bytes(h->M, h->N, h->K)) : 0;
+        const size_t need = workspace_need(h);
+        const bool no_part = h->ws && !h->ws_owned && h->ws_bytes < need && h->ws_bytes + part >= need;
+        if (!no_part) {
+            ascq_status s = ensure_workspace(h);
+            if (s != ASCQ_OK) return s;
+        }
         const uint8_t* at = (const uint8_t*)h->a;
         const uint8_t* bt = (const uint8_t*)h->b;
         const uint8_t* sa = h->scale_a;
@@ -867,6 +874,10 @@ ascq_status ascq_matmul_iterate_all(ascq_matmul_t h, void* c, uint8_t en_atomic,
         g.sa_layout = h->trans_sa ? 1 : 0;  // scaleA [M, sK], or [sK/2, M, 2] with isTransposeScaleA
         g.sb_layout = h->trans_sb ? 1 : 0;  // scaleB [sK/2, N, 2], or [N, sK] with isTransposeScaleB
         g.ws_scales = ws;  // after the B transpose (if any); the GEMM rearranges both scale tensors here
+        if (part && !no_part) {  // then the decode partials
+            g.ws_part = ws + align256(ascq::mx_scale_workspace_bytes(h->M, h->N, h->K));
+            g.ws_part_bytes = part;
+        }
         g.M = h->M;
         g.N = h->N;
         g.K = h->K;

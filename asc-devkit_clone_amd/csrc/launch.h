@@ -188,8 +188,16 @@ struct MxGemmArgs {
     // launch_fp4_to_fp6_planes
     const uint8_t* Aq;
     const uint8_t* Bq;
+    uint8_t* ws_part;       // decode-sized MX-FP4 batches: room for the K-split partials (mx_decode_split_ws_bytes)
+    size_t ws_part_bytes;
+    int splits;             // (set by the launcher) workgroups per tile of the K-split form
 };
 hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st);
+// MX-FP4 at decode-sized batches (M <= 64) with the scales read in place: with few 64 x 64 tiles (N / 64 well under
+// 256) K is split across workgroups as well, the partials meeting in the workspace; the workgroups per tile (1: not
+// used) and the workspace the partials need
+int mx_decode_splits(int64_t M, int64_t N, int64_t K);
+size_t mx_decode_split_ws_bytes(int64_t M, int64_t N, int64_t K);
 // fp4 (E2M1 or E1M2) [R, K/2] -> fp6 E2M3 split planes: P [R, K/2] (dwords 0-3 of each MX block's six) and Q
 // (fp6_q_plane_bytes(R, K): dwords 4-5, 1 KiB per (128 K, 32-row group)); K a multiple of 128
 size_t fp6_q_plane_bytes(int64_t R, int64_t K);

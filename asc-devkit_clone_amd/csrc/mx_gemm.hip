@@ -42,17 +42,25 @@ __host__ __device__ inline int64_t sk_stage_major(int64_t K) { return ((K + 63) 
 // DIRECT (the core's SC_DIRECT): the scales are read as given -- A row-major [M, sK], B row-major [N, sK] (1) or in
 // block pairs [sK / 2, N, 2] (2) -- by the core's copies (sa_sm / sb_sm unused); 0: from the stage-major copies at
 // sa_sm / sb_sm
-template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true, int DIRECT = 0>
+// PH (K split across workgroups; decode tiles with direct scales): 1 -- workgroup b runs split b / tiles of tile
+// b % tiles over a whole number of stages (shared out as evenly as p.splits allows; the scale resources start at the
+// split's first stage) and stores its waves' fp32 accumulators in p.ws_part ([split][tile][wave][fragment][lane]);
+// 2 -- the same waves add the splits' accumulators in split order and run the epilogue.
+template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true, int DIRECT = 0, int PH = 0>
 __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, const uint8_t* __restrict__ sa_sm,
                                                                 const uint8_t* __restrict__ sb_sm)
 {
     using T = GemmCore<BM, BN, WM, WN, ST, true, OP, RB, FMT, ILV, false, false, DIRECT>;
+    static_assert(PH == 0 || (DIRECT && OP != OP_MXFP6), "K split across workgroups: tiles with direct scales");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_mx[];
     const int64_t M = p.M, N = p.N, K = p.K;
     const int64_t KB = OP == OP_MXF8 ? K : K / 2;  // bytes per row (fp6: of the P plane)
     const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
+    const int ntiles = tiles_m * tiles_n;
+    const int tile = PH == 1 ? (int)blockIdx.x % ntiles : (int)blockIdx.x;
+    const int split = PH == 1 ? (int)blockIdx.x / ntiles : 0;
     int tm, tn;
-    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    tile_coords(tile, tiles_m, tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     const int64_t sK = (K + 63) / 64 * 2;
     CoreArgs c{};
@@ -61,15 +69,23 @@ __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, con
     c.lda = c.ldb = (uint32_t)KB;
     c.rows = (int32_t)(M - m0 < BM ? M - m0 : BM);
     c.cols = (int32_t)(N - n0 < BN ? N - n0 : BN);
-    c.a0 = (uint32_t)(m0 * KB);
-    c.b0 = (uint32_t)(n0 * KB);
+    int64_t u0 = 0;  // PH 1: this workgroup's first stage; its K bytes (otherwise the whole row, a last stage partial)
     c.kbytes = KB;
+    if constexpr (PH == 1) {
+        const int64_t units = KB / RB;
+        u0 = units * split / p.splits;
+        c.kbytes = (units * (split + 1) / p.splits - u0) * RB;
+    }
+    c.a0 = (uint32_t)(m0 * KB + u0 * RB);
+    c.b0 = (uint32_t)(n0 * KB + u0 * RB);
     // One resource over every auxiliary region (launch_mx_gemm checks the layout): the stage-major scales (which
     // carry 16 bytes of slack, so a 16-byte copy at the end never straddles the range) and, for fp6, the Q planes
     // before them: [Aq][P plane of B][Bq][scales of A][scales of B].
     if constexpr (DIRECT) {
-        c.aux = make_rsrc(p.sA, (uint32_t)(M * sK));
-        c.aux_b = make_rsrc(p.sB, (uint32_t)(N * sK));
+        // from stage u0 on: row-major rows advance SCB bytes a stage, pair planes SCB N bytes
+        const int64_t sa_off = u0 * T::SCB, sb_off = u0 * T::SCB * (DIRECT == 2 ? N : 1);
+        c.aux = make_rsrc(p.sA + sa_off, (uint32_t)(M * sK - sa_off));
+        c.aux_b = make_rsrc(p.sB + sb_off, (uint32_t)(N * sK - sb_off));
     } else {
         const uint8_t* aux = OP == OP_MXFP6 ? p.Aq : sa_sm;
         c.aux = make_rsrc(aux, (uint32_t)(sb_sm - aux) + (uint32_t)(N * sk_stage_major(K) + 16));
@@ -88,8 +104,27 @@ __global__ __launch_bounds__(WM * WN * 64) void mx_gemm_kernel(MxGemmArgs p, con
     c.sa_rows = (uint32_t)M;
     c.sb_rows = (uint32_t)N;
     c.sk = (uint32_t)sK;
-    typename T::acc_t acc[T::FM][T::FN];
-    T::run(c, smem_mx, acc);
+    typedef typename T::acc_t acc_t;
+    acc_t acc[T::FM][T::FN];
+    constexpr int F = T::FM * T::FN;  // accumulator fragments of a wave
+    acc_t* part = (acc_t*)p.ws_part;  // PH 1 / 2: [split][tile][wave][F][64 lanes]
+    const int pw = (int)threadIdx.x >> 6, pl = (int)threadIdx.x & 63;
+    if constexpr (PH == 2) {
+#pragma unroll
+        for (int f = 0; f < F; ++f) acc[f / T::FN][f % T::FN] = part[(((int64_t)tile * T::NW + pw) * F + f) * 64 + pl];
+        for (int sp = 1; sp < p.splits; ++sp)
+#pragma unroll
+            for (int f = 0; f < F; ++f)
+                acc[f / T::FN][f % T::FN] += part[((((int64_t)sp * ntiles + tile) * T::NW + pw) * F + f) * 64 + pl];
+    } else {
+        T::run(c, smem_mx, acc);
+    }
+    if constexpr (PH == 1) {
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+            part[((((int64_t)split * ntiles + tile) * T::NW + pw) * F + f) * 64 + pl] = acc[f / T::FN][f % T::FN];
+        return;
+    }
 
     // epilogue through a buffer resource over the output tile (rows past M dropped by its range)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -270,6 +305,38 @@ size_t mx_scale_workspace_bytes(int64_t M, int64_t N, int64_t K)
     return (size_t)((M * sKp + 16 + 255) / 256 * 256 + (N * sKp + 16 + 255) / 256 * 256);
 }
 
+// the decode tiles' K split across workgroups (64 x 64 tiles of four waves, 128 fp4 of K per stage): splits so that
+// tiles x splits is about 256, for few tiles only
+int mx_decode_splits(int64_t M, int64_t N, int64_t K)
+{
+    if (M > 64 || M < 1 || N < 1 || K % 128 != 0) return 1;
+    const int64_t tiles = (N + 63) / 64, units = K / 128;
+    int64_t s = (256 + tiles / 2) / tiles;
+    if (s > units) s = units;
+    return s < 2 ? 1 : (int)s;
+}
+size_t mx_decode_split_ws_bytes(int64_t M, int64_t N, int64_t K)
+{
+    const int s = mx_decode_splits(M, N, K);
+    return s < 2 ? 0 : (size_t)s * (size_t)((N + 63) / 64) * 4 * 64 * 64;
+}
+
+template <int DIRECT>
+static hipError_t launch_mx_split(MxGemmArgs a, hipStream_t st)
+{
+    using T = GemmCore<64, 64, 2, 2, 4, true, OP_MXFP4, 64, 0, true, false, false, DIRECT>;
+    const int tiles = (int)((a.N + 63) / 64);
+    hipError_t e = ensure_dynamic_lds<mx_gemm_kernel<64, 64, 2, 2, 4, 64, OP_MXFP4, 0, true, DIRECT, 1>>((int)T::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    launch_k((mx_gemm_kernel<64, 64, 2, 2, 4, 64, OP_MXFP4, 0, true, DIRECT, 1>), dim3(tiles * a.splits), dim3(T::NT),
+             T::LDS_BYTES, st, a, (const uint8_t*)nullptr, (const uint8_t*)nullptr);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    launch_k((mx_gemm_kernel<64, 64, 2, 2, 4, 64, OP_MXFP4, 0, true, DIRECT, 2>), dim3(tiles), dim3(T::NT), 0u, st, a,
+             (const uint8_t*)nullptr, (const uint8_t*)nullptr);
+    return hipGetLastError();
+}
+
 template <int BM, int BN, int WM, int WN, int ST, int RB, int OP, int FMT, bool ILV = true, int DIRECT = 0>
 static hipError_t launch_mx_tiled(const MxGemmArgs& a, hipStream_t st)
 {
@@ -331,8 +398,17 @@ hipError_t launch_mx_gemm(const MxGemmArgs& a, hipStream_t st)
         // in 11.9 / 12.7 / 16.3 us against 17.5 / 17.6 / 19.5 us; at M = 256 the per-row reads, 64 cache lines a
         // copy, cost more than the launch: 45.4 against 38.0 us at K = N = 8192)
         if (a.M <= 64 && a.sa_layout == 0 && (uintptr_t)a.sA % 4 == 0 && (uintptr_t)a.sB % 4 == 0) {
-            if (a.sb_layout == 1) return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP4, 0, true, 1>(a, st);
-            if (a.N % 2 == 0) return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP4, 0, true, 2>(a, st);
+            // ... with few tiles (N / 64 well under 256) and a workspace for the partials, K split across workgroups
+            // too, the fp32 partials added in split order by a second launch
+            const int splits = mx_decode_splits(a.M, a.N, a.K);
+            const bool split = splits > 1 && a.atomic == C_STORE && a.ws_part &&
+                               a.ws_part_bytes >= mx_decode_split_ws_bytes(a.M, a.N, a.K);
+            MxGemmArgs b = a;
+            b.splits = splits;
+            if (a.sb_layout == 1)
+                return split ? launch_mx_split<1>(b, st) : launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP4, 0, true, 1>(a, st);
+            if (a.N % 2 == 0)
+                return split ? launch_mx_split<2>(b, st) : launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP4, 0, true, 2>(a, st);
         }
         return launch_mx_tiled<64, 64, 2, 2, 4, 64, OP_MXFP4, 0>(a, st);
     }
