@@ -316,23 +316,25 @@ static hipError_t launch_f8_tiled(const GemmF8Args& a, hipStream_t st)
     return hipGetLastError();
 }
 
-// the K split across workgroups of decode-sized batches with B given [K, N] (decode_splits): 32 x 128 one-wave tiles,
-// four K-split waves per workgroup; fp32 partials in a.ws, added in split order by the second launch
-template <int FMT>
+// the K split across workgroups of decode-sized batches (decode_splits): 32-row one-wave tiles (B [K, N]: 32 x 128,
+// K rows read by LDS transpose reads; B [N, K]: 32 x 32), four K-split waves per workgroup; fp32 partials in a.ws,
+// added in split order by the second launch
+template <int FMT, bool TB, int BN, int ST>
 static hipError_t launch_f8_split(GemmF8Args a, hipStream_t st)
 {
-    constexpr int BM = 32, BN = 128, KWS = 4, RB = 64;
-    using T = GemmCore<BM, BN, 1, 1, 3, false, op_of_fmt<FMT>, RB, FMT, true, false, true>;
+    constexpr int BM = 32, KWS = 4, RB = 64;
+    constexpr bool BTR = !TB;
+    using T = GemmCore<BM, BN, 1, 1, ST, TB, op_of_fmt<FMT>, RB, FMT, true, false, BTR>;
     const int tiles = (int)((a.N + BN - 1) / BN);
     constexpr size_t lds = T::LDS_BYTES * KWS;
     static_assert((size_t)(KWS - 1) * T::FM * T::FN * 64 * sizeof(typename T::acc_t) <= lds, "k-split reduction");
-    hipError_t e = ensure_dynamic_lds<gemm_f8_kernel<BM, BN, 1, 1, 3, false, RB, FMT, false, KWS, true, 1>>((int)lds);
+    hipError_t e = ensure_dynamic_lds<gemm_f8_kernel<BM, BN, 1, 1, ST, TB, RB, FMT, false, KWS, BTR, 1>>((int)lds);
     if (e != hipSuccess) return e;
-    launch_k((gemm_f8_kernel<BM, BN, 1, 1, 3, false, RB, FMT, false, KWS, true, 1>), dim3(tiles * a.splits),
+    launch_k((gemm_f8_kernel<BM, BN, 1, 1, ST, TB, RB, FMT, false, KWS, BTR, 1>), dim3(tiles * a.splits),
              dim3(64 * KWS), (uint32_t)lds, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_k((gemm_f8_kernel<BM, BN, 1, 1, 3, false, RB, FMT, false, 1, true, 2>), dim3(tiles), dim3(64), 0u, st, a);
+    launch_k((gemm_f8_kernel<BM, BN, 1, 1, ST, TB, RB, FMT, false, 1, BTR, 2>), dim3(tiles), dim3(64), 0u, st, a);
     return hipGetLastError();
 }
 
@@ -356,20 +358,20 @@ static hipError_t launch_f8_fmt(const GemmF8Args& a, bool ua, hipStream_t st)
     const bool skinny = a.M <= 32 || (a.M <= 64 && t64 < 160);
     const bool c_wide = a.c_type == DT_F32 || a.c_type == DT_F16 || a.c_type == DT_BF16;
     if constexpr (ES == 1) {
-        if (a.trans_b && skinny && c_wide && a.atomic == C_STORE && a.K % 256 == 0)
-            return launch_f8_tiled<32, 32, 1, 1, 4, true, 64, FMT, false, 4>(a, st);
-        // ... and with B given [K, N] (16-byte K rows): B's K rows staged like A's, read by LDS transpose reads;
-        // for long K or wide N with a workspace for the partials, 32 x 128 tiles with the K split across workgroups
-        // too (decode_splits: the int8 Matmul's rule)
+        // with a workspace for the partials, the K split across workgroups as well where decode_splits (the int8
+        // Matmul's rule) finds it faster: B [N, K] on the 32 x 32 tiles, B [K, N] (16-byte K rows) on 32 x 128 tiles
         const int splits = decode_splits(a.M, a.N, a.K, a.trans_b);
         const bool b_tr = !a.trans_b && a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0;
-        if (b_tr && splits > 1 && c_wide && a.atomic == C_STORE && a.ws &&
+        if ((a.trans_b || b_tr) && splits > 1 && c_wide && a.atomic == C_STORE && a.ws &&
             a.ws_bytes >= decode_split_ws_bytes(a.M, a.N, a.K, a.trans_b) &&
             ((a.M + 63) / 64) * ((a.N + 127) / 128) >= 32) {
             GemmF8Args b = a;
             b.splits = splits;
-            return launch_f8_split<FMT>(b, st);
+            return a.trans_b ? launch_f8_split<FMT, true, 32, 4>(b, st) : launch_f8_split<FMT, false, 128, 3>(b, st);
         }
+        if (a.trans_b && skinny && c_wide && a.atomic == C_STORE && a.K % 256 == 0)
+            return launch_f8_tiled<32, 32, 1, 1, 4, true, 64, FMT, false, 4>(a, st);
+        // ... and with B given [K, N] (16-byte K rows): B's K rows staged like A's, read by LDS transpose reads
         if (b_tr && skinny && c_wide && a.atomic == C_STORE && a.K % 256 == 0)
             return launch_f8_tiled<32, 32, 1, 1, 4, false, 64, FMT, false, 4, true>(a, st);
     }

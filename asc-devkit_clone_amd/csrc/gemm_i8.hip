@@ -469,17 +469,20 @@ static hipError_t launch_tiled(const GemmI8Args& a, hipStream_t st)
     return hipGetLastError();
 }
 
-// the K split across workgroups of decode-sized batches: 32 x 128 one-wave tiles, four K-split waves per
-// workgroup, splits chosen so that tiles x splits is about 256 (one workgroup per CU); K % 256 == 0
-constexpr int DS_BM = 32, DS_BN = 128, DS_KW = 4, DS_RB = 64;
+// the K split across workgroups of decode-sized batches: 32-row one-wave tiles, four K-split waves per workgroup,
+// splits chosen so that tiles x splits is about 256 (one workgroup per CU); K % 256 == 0.  B given [K, N]: 32 x 128
+// tiles (whole 128-byte K-row runs), for long K or wide N only -- elsewhere the 32 x 32 K-split tiles measured faster
+// (K = 11008 / 14336, N = 4096, M = 1: 36.6 / 45.8 -> 23.3 / 26.0 us; K = N = 8192: 32.1 -> 26.8 us; K = 4096,
+// N = 14336: 29.9 -> 23.1 us; slower at K = 4096, N = 8192 / 11008).  B given [N, K]: the 32 x 32 tiles themselves,
+// split when they are few (N / 32 well under 256) and K is long (K = 11008 / 14336, N = 4096, M = 16: 21.7 / 23.8 ->
+// 17.1 / 19.6 us; slower at K = 4096: 9.1 against 8.4 us)
+constexpr int DS_BM = 32, DS_KW = 4, DS_RB = 64;
+int decode_split_bn(int trans_b) { return trans_b ? 32 : 128; }
 int decode_splits(int64_t M, int64_t N, int64_t K, int trans_b)
 {
-    // B given [K, N] with long K or wide N only: elsewhere the 32 x 32 K-split tiles measured faster (K = 11008 /
-    // 14336, N = 4096, M = 1: 36.6 / 45.8 -> 23.3 / 26.0 us; K = N = 8192: 32.1 -> 26.8 us; K = 4096, N = 14336:
-    // 29.9 -> 23.1 us; slower at K = 4096, N = 8192 / 11008 and with B given [N, K])
-    if (trans_b || !(K >= 8192 || N >= 12288)) return 1;
     if (M > DS_BM || M < 1 || N < 1 || K % (DS_KW * DS_RB) != 0) return 1;
-    const int64_t tiles = (N + DS_BN - 1) / DS_BN;
+    if (!(K >= 8192 || (!trans_b && N >= 12288))) return 1;
+    const int64_t tiles = (N + decode_split_bn(trans_b) - 1) / decode_split_bn(trans_b);
     int64_t s = (256 + tiles / 2) / tiles;
     const int64_t units = K / (DS_KW * DS_RB);
     if (s > units) s = units;
@@ -487,24 +490,24 @@ int decode_splits(int64_t M, int64_t N, int64_t K, int trans_b)
 }
 size_t decode_split_ws_bytes(int64_t M, int64_t N, int64_t K, int trans_b)
 {
-    const int s = decode_splits(M, N, K, trans_b);
-    return s < 2 ? 0 : (size_t)s * (size_t)((N + DS_BN - 1) / DS_BN) * (DS_BN / 32) * 64 * 64;
+    const int s = decode_splits(M, N, K, trans_b), bn = decode_split_bn(trans_b);
+    return s < 2 ? 0 : (size_t)s * (size_t)((N + bn - 1) / bn) * (bn / 32) * 64 * 64;
 }
 
-template <bool TB, bool BTR>
+template <bool TB, bool BTR, int BN, int ST>
 static hipError_t launch_i8_split(GemmI8Args a, hipStream_t st)
 {
-    using T = I8Core<DS_BM, DS_BN, 1, 1, 3, TB, DS_RB, false, BTR, false>;
-    const int tiles = (int)((a.N + DS_BN - 1) / DS_BN);
+    using T = I8Core<DS_BM, BN, 1, 1, ST, TB, DS_RB, false, BTR, false>;
+    const int tiles = (int)((a.N + BN - 1) / BN);
     constexpr size_t lds = T::LDS_BYTES * DS_KW;
     static_assert((size_t)(DS_KW - 1) * T::FM * T::FN * 64 * sizeof(typename T::acc_t) <= lds, "k-split reduction");
-    hipError_t e = ensure_dynamic_lds<gemm_i8_kernel<DS_BM, DS_BN, 1, 1, 3, TB, DS_RB, BTR, DS_KW, false, 1>>((int)lds);
+    hipError_t e = ensure_dynamic_lds<gemm_i8_kernel<DS_BM, BN, 1, 1, ST, TB, DS_RB, BTR, DS_KW, false, 1>>((int)lds);
     if (e != hipSuccess) return e;
-    launch_k((gemm_i8_kernel<DS_BM, DS_BN, 1, 1, 3, TB, DS_RB, BTR, DS_KW, false, 1>), dim3(tiles * a.splits),
+    launch_k((gemm_i8_kernel<DS_BM, BN, 1, 1, ST, TB, DS_RB, BTR, DS_KW, false, 1>), dim3(tiles * a.splits),
              dim3(64 * DS_KW), (uint32_t)lds, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_k((gemm_i8_kernel<DS_BM, DS_BN, 1, 1, 3, TB, DS_RB, BTR, 1, false, 2>), dim3(tiles), dim3(64), 0u, st, a);
+    launch_k((gemm_i8_kernel<DS_BM, BN, 1, 1, ST, TB, DS_RB, BTR, 1, false, 2>), dim3(tiles), dim3(64), 0u, st, a);
     return hipGetLastError();
 }
 
@@ -528,15 +531,15 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
         const int64_t t64 = ((a.M + 63) / 64) * ((a.N + 63) / 64);
         const bool skinny = a.M <= 32 || (a.M <= 64 && t64 < 160);
         const bool ksplit = (tiny || skinny) && a.K % 256 == 0 && a.atomic == C_STORE;
-        // decode-sized batches (up to 32 rows) with B given [K, N] and a workspace for the partials: 32 x 128 tiles
-        // (whole 128-byte K-row runs instead of 32-byte ones) with the K split across workgroups as well, where
-        // decode_splits finds that faster than the 32 x 32 tiles below
+        // decode-sized batches (up to 32 rows) with a workspace for the partials: the K split across workgroups as
+        // well, where decode_splits finds it faster (B [K, N]: 32 x 128 tiles; B [N, K]: the 32 x 32 tiles below)
         const int splits = decode_splits(a.M, a.N, a.K, a.trans_b);
         if (!tiny && splits > 1 && a.atomic == C_STORE && a.epi != EPI_REQ4 && a.ws &&
-            a.ws_bytes >= decode_split_ws_bytes(a.M, a.N, a.K, a.trans_b) && a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0) {
+            a.ws_bytes >= decode_split_ws_bytes(a.M, a.N, a.K, a.trans_b)) {
             GemmI8Args b = a;
             b.splits = splits;
-            return launch_i8_split<false, true>(b, st);
+            if (a.trans_b) return launch_i8_split<true, false, 32, 4>(b, st);
+            if (a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0) return launch_i8_split<false, true, 128, 3>(b, st);
         }
         if (ksplit && a.trans_b) return launch_tiled<32, 32, 1, 1, 4, true, 64, false, 4>(a, st);
         if (ksplit && a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0)
