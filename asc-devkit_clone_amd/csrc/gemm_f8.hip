@@ -372,8 +372,11 @@ static hipError_t launch_f8_fmt(const GemmF8Args& a, bool ua, hipStream_t st)
         if (a.trans_b && skinny && c_wide && a.atomic == C_STORE && a.K % 256 == 0)
             return launch_f8_tiled<32, 32, 1, 1, 4, true, 64, FMT, false, 4>(a, st);
         // ... and with B given [K, N] (16-byte K rows): B's K rows staged like A's, read by LDS transpose reads
+        // (32 x 64 tiles from N = 10240 on, as the int8 Matmul: K = 4096, N = 11008, M = 1 / 16: 22.8 / 24.6 ->
+        // 21.4 / 21.6 us)
         if (b_tr && skinny && c_wide && a.atomic == C_STORE && a.K % 256 == 0)
-            return launch_f8_tiled<32, 32, 1, 1, 4, false, 64, FMT, false, 4, true>(a, st);
+            return a.N >= 10240 ? launch_f8_tiled<32, 64, 1, 1, 4, false, 64, FMT, false, 4, true>(a, st)
+                                : launch_f8_tiled<32, 32, 1, 1, 4, false, 64, FMT, false, 4, true>(a, st);
     }
     if (a.trans_b) {
         if (big) return (a.K * ES) % 128 == 0 ? launch_f8_tiled<256, 256, 4, 2, 2, true, 128, FMT>(a, st)

@@ -542,8 +542,12 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
             if (a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0) return launch_i8_split<false, true, 128, 3>(b, st);
         }
         if (ksplit && a.trans_b) return launch_tiled<32, 32, 1, 1, 4, true, 64, false, 4>(a, st);
+        // (B [K, N]: 32 x 64 tiles -- 64-byte K-row runs -- while they still give about 160 workgroups or more:
+        // K = 4096, N = 11008, M = 1 / 16: 22.1 / 23.8 -> 18.1 / 19.7 us; at N = 4096 / 8192 the 32 x 32 tiles are
+        // faster, 16.9 / 18.0 against 18.8 / 20.2 us)
         if (ksplit && a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0)
-            return launch_tiled<32, 32, 1, 1, 4, false, 64, true, 4>(a, st);
+            return a.N >= 10240 ? launch_tiled<32, 64, 1, 1, 4, false, 64, true, 4>(a, st)
+                                : launch_tiled<32, 32, 1, 1, 4, false, 64, true, 4>(a, st);
         if (a.trans_b)
             return big ? (a.K % 128 == 0 ? launch_tiled<256, 256, 4, 2, 2, true, 128>(a, st)
                                          : launch_tiled<256, 256, 4, 2, 4, true>(a, st))

@@ -1,6 +1,7 @@
 """GPU parity sweep over the decode-batch forms of the quantized Matmuls (M <= 64, B streamed once): shapes chosen on
 both sides of each dispatch rule -- K split over the waves of a workgroup, K split across workgroups as well (B [N, K]
 with few 32 x 32 tiles and long K; B [K, N] on 32 x 128 tiles with long K or wide N; MX-FP4 with few 64 x 64 tiles),
+B [K, N] on 32 x 64 tiles from N = 10240 on,
 B [K, N] rows that are not 16-byte multiples, row-major and block-pair MX scales -- against the oracle: int8 bit-exact
 (int32 and DEQF16 C), fp8 and MX-FP4 within the bounds their own test files state (fp32 accumulation, the fp8 MFMA's
 16-element group alignment)."""
@@ -21,7 +22,8 @@ pytestmark = pytest.mark.gpu
 # (M, N, K, B given [N, K])
 _I8 = [(1, 4096, 8192, False), (7, 4104, 8448, False), (16, 12416, 512, False), (32, 4000, 8192, True),
        (3, 5120, 9216, True), (20, 4096, 10240, True), (12, 8192, 8192, True), (1, 2048, 8192, False),
-       (29, 4608, 11264, False), (64, 4096, 8192, True), (33, 4096, 8192, False)]
+       (29, 4608, 11264, False), (64, 4096, 8192, True), (33, 4096, 8192, False), (1, 11008, 4096, False),
+       (16, 10256, 2048, False), (40, 10240, 1024, False)]
 
 
 @pytest.mark.parametrize("M,N,K,trans_b", _I8)
@@ -38,7 +40,7 @@ def test_int8_decode_forms(ascq_gpu, oracle, M, N, K, trans_b):
 
 
 @pytest.mark.parametrize("M,N,K,trans_b", [(1, 4096, 8192, False), (16, 12416, 512, False), (32, 4000, 8192, True),
-                                           (5, 5120, 9216, True), (9, 4104, 8192, False)])
+                                           (5, 5120, 9216, True), (9, 4104, 8192, False), (8, 11008, 4096, False)])
 def test_fp8_decode_forms(ascq_gpu, M, N, K, trans_b):
     fa, fb = O.FP8_E4M3, O.FP8_E4M3
     A, B, b, qs, qv = fp8_case(5 * M + N + K, M, N, K, fa, fb, O.BF16, trans_b=trans_b, quant="vector")
