@@ -95,7 +95,7 @@ def test_group_ties_above_2_24(ascq_gpu, oracle, w_trans, list_type):
     assert GC.rne_differs(x, w, pts, sc, counts) > 50
 
 
-@pytest.mark.parametrize("T,K,N", [(1, 512, 160), (16, 1024, 256), (64, 768, 96), (200, 4096, 1408)])
+@pytest.mark.parametrize("T,K,N", [(1, 512, 160), (16, 1024, 256), (64, 768, 96), (200, 4096, 1408), (150, 1024, 208)])
 @pytest.mark.parametrize("w_trans", [False, True])
 @pytest.mark.parametrize("list_type", [0, 1])
 def test_group_decode_ksplit(ascq_gpu, oracle, T, K, N, w_trans, list_type):
