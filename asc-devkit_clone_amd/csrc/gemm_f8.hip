@@ -316,13 +316,13 @@ static hipError_t launch_f8_tiled(const GemmF8Args& a, hipStream_t st)
     return hipGetLastError();
 }
 
-// the K split across workgroups of decode-sized batches (decode_splits): 32-row one-wave tiles (B [K, N]: 32 x 128,
-// K rows read by LDS transpose reads; B [N, K]: 32 x 32), four K-split waves per workgroup; fp32 partials in a.ws,
-// added in split order by the second launch
-template <int FMT, bool TB, int BN, int ST>
+// the K split across workgroups of decode-sized batches (decode_splits): one-wave tiles of 32 or 64 rows (one row
+// tile; B [K, N]: x 128, K rows read by LDS transpose reads; B [N, K]: x 32), four K-split waves per workgroup; fp32
+// partials in a.ws, added in split order by the second launch
+template <int FMT, bool TB, int BM, int BN, int ST>
 static hipError_t launch_f8_split(GemmF8Args a, hipStream_t st)
 {
-    constexpr int BM = 32, KWS = 4, RB = 64;
+    constexpr int KWS = 4, RB = 64;
     constexpr bool BTR = !TB;
     using T = GemmCore<BM, BN, 1, 1, ST, TB, op_of_fmt<FMT>, RB, FMT, true, false, BTR>;
     const int tiles = (int)((a.N + BN - 1) / BN);
@@ -367,7 +367,10 @@ static hipError_t launch_f8_fmt(const GemmF8Args& a, bool ua, hipStream_t st)
             ((a.M + 63) / 64) * ((a.N + 127) / 128) >= 32) {
             GemmF8Args b = a;
             b.splits = splits;
-            return a.trans_b ? launch_f8_split<FMT, true, 32, 4>(b, st) : launch_f8_split<FMT, false, 128, 3>(b, st);
+            if (a.M <= 32)
+                return a.trans_b ? launch_f8_split<FMT, true, 32, 32, 4>(b, st)
+                                 : launch_f8_split<FMT, false, 32, 128, 3>(b, st);
+            return a.trans_b ? launch_f8_split<FMT, true, 64, 32, 4>(b, st) : launch_f8_split<FMT, false, 64, 128, 3>(b, st);
         }
         if (a.trans_b && skinny && c_wide && a.atomic == C_STORE && a.K % 256 == 0)
             return launch_f8_tiled<32, 32, 1, 1, 4, true, 64, FMT, false, 4>(a, st);

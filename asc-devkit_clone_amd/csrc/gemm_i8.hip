@@ -482,11 +482,12 @@ static hipError_t launch_tiled(const GemmI8Args& a, hipStream_t st)
 // N = 14336: 29.9 -> 23.1 us; slower at K = 4096, N = 8192 / 11008).  B given [N, K]: the 32 x 32 tiles themselves,
 // split when they are few (N / 32 well under 256) and K is long (K = 11008 / 14336, N = 4096, M = 16: 21.7 / 23.8 ->
 // 17.1 / 19.6 us; slower at K = 4096: 9.1 against 8.4 us)
-constexpr int DS_BM = 32, DS_KW = 4, DS_RB = 64;
+constexpr int DS_KW = 4, DS_RB = 64;
 int decode_split_bn(int trans_b) { return trans_b ? 32 : 128; }
+int decode_split_bm(int64_t M) { return M <= 32 ? 32 : 64; }  // one row tile for M <= 64
 int decode_splits(int64_t M, int64_t N, int64_t K, int trans_b)
 {
-    if (M > DS_BM || M < 1 || N < 1 || K % (DS_KW * DS_RB) != 0) return 1;
+    if (M > 64 || M < 1 || N < 1 || K % (DS_KW * DS_RB) != 0) return 1;
     if (!(K >= 8192 || (!trans_b && N >= 12288))) return 1;
     const int64_t tiles = (N + decode_split_bn(trans_b) - 1) / decode_split_bn(trans_b);
     int64_t s = (256 + tiles / 2) / tiles;
@@ -496,24 +497,24 @@ int decode_splits(int64_t M, int64_t N, int64_t K, int trans_b)
 }
 size_t decode_split_ws_bytes(int64_t M, int64_t N, int64_t K, int trans_b)
 {
-    const int s = decode_splits(M, N, K, trans_b), bn = decode_split_bn(trans_b);
-    return s < 2 ? 0 : (size_t)s * (size_t)((N + bn - 1) / bn) * (bn / 32) * 64 * 64;
+    const int s = decode_splits(M, N, K, trans_b), bn = decode_split_bn(trans_b), bm = decode_split_bm(M);
+    return s < 2 ? 0 : (size_t)s * (size_t)((N + bn - 1) / bn) * (bm / 32) * (bn / 32) * 64 * 64;
 }
 
-template <bool TB, bool BTR, int BN, int ST>
+template <bool TB, bool BTR, int BM, int BN, int ST>
 static hipError_t launch_i8_split(GemmI8Args a, hipStream_t st)
 {
-    using T = I8Core<DS_BM, BN, 1, 1, ST, TB, DS_RB, false, BTR, false>;
+    using T = I8Core<BM, BN, 1, 1, ST, TB, DS_RB, false, BTR, false>;
     const int tiles = (int)((a.N + BN - 1) / BN);
     constexpr size_t lds = T::LDS_BYTES * DS_KW;
     static_assert((size_t)(DS_KW - 1) * T::FM * T::FN * 64 * sizeof(typename T::acc_t) <= lds, "k-split reduction");
-    hipError_t e = ensure_dynamic_lds<gemm_i8_kernel<DS_BM, BN, 1, 1, ST, TB, DS_RB, BTR, DS_KW, false, 1>>((int)lds);
+    hipError_t e = ensure_dynamic_lds<gemm_i8_kernel<BM, BN, 1, 1, ST, TB, DS_RB, BTR, DS_KW, false, 1>>((int)lds);
     if (e != hipSuccess) return e;
-    launch_k((gemm_i8_kernel<DS_BM, BN, 1, 1, ST, TB, DS_RB, BTR, DS_KW, false, 1>), dim3(tiles * a.splits),
+    launch_k((gemm_i8_kernel<BM, BN, 1, 1, ST, TB, DS_RB, BTR, DS_KW, false, 1>), dim3(tiles * a.splits),
              dim3(64 * DS_KW), (uint32_t)lds, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_k((gemm_i8_kernel<DS_BM, BN, 1, 1, ST, TB, DS_RB, BTR, 1, false, 2>), dim3(tiles), dim3(64), 0u, st, a);
+    launch_k((gemm_i8_kernel<BM, BN, 1, 1, ST, TB, DS_RB, BTR, 1, false, 2>), dim3(tiles), dim3(64), 0u, st, a);
     return hipGetLastError();
 }
 
@@ -537,15 +538,19 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
         const int64_t t64 = ((a.M + 63) / 64) * ((a.N + 63) / 64);
         const bool skinny = a.M <= 32 || (a.M <= 64 && t64 < 160);
         const bool ksplit = (tiny || skinny) && a.K % 256 == 0 && a.atomic == C_STORE;
-        // decode-sized batches (up to 32 rows) with a workspace for the partials: the K split across workgroups as
-        // well, where decode_splits finds it faster (B [K, N]: 32 x 128 tiles; B [N, K]: the 32 x 32 tiles below)
+        // decode-sized batches (up to 64 rows, one row tile of 32 or 64) with a workspace for the partials: the K split
+        // across workgroups as well, where decode_splits finds it faster (B [K, N]: x 128 tiles; B [N, K]: x 32)
         const int splits = decode_splits(a.M, a.N, a.K, a.trans_b);
         if (!tiny && splits > 1 && a.atomic == C_STORE && a.epi != EPI_REQ4 && a.ws &&
             a.ws_bytes >= decode_split_ws_bytes(a.M, a.N, a.K, a.trans_b)) {
             GemmI8Args b = a;
             b.splits = splits;
-            if (a.trans_b) return launch_i8_split<true, false, 32, 4>(b, st);
-            if (a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0) return launch_i8_split<false, true, 128, 3>(b, st);
+            const bool m32 = a.M <= 32;
+            if (a.trans_b)
+                return m32 ? launch_i8_split<true, false, 32, 32, 4>(b, st) : launch_i8_split<true, false, 64, 32, 4>(b, st);
+            if (a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0)
+                return m32 ? launch_i8_split<false, true, 32, 128, 3>(b, st)
+                           : launch_i8_split<false, true, 64, 128, 3>(b, st);
         }
         if (ksplit && a.trans_b) return launch_tiled<32, 32, 1, 1, 4, true, 64, false, 4>(a, st);
         // (B [K, N]: 32 x 64 tiles -- 64-byte K-row runs -- while they still give about 160 workgroups or more:

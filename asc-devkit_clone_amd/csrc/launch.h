@@ -107,10 +107,10 @@ struct GemmI8Args {
     int splits;           // (set by the launcher) workgroups per tile of the K-split form
 };
 hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st);
-// Decode-sized batches (M <= 32, K % 256 == 0) -- B given [K, N] (trans_b 0) with long K or wide N on 32 x 128 tiles,
-// B given [N, K] with few 32 x 32 tiles -- split each tile's K over several workgroups (four waves each) so that about
-// 256 workgroups stream B; their accumulators meet in the workspace and a second launch adds them in split order and
-// runs the epilogue.
+// Decode-sized batches (M <= 64: one row tile of 32 or 64 rows; K % 256 == 0) -- B given [K, N] (trans_b 0) with long
+// K or wide N on x 128 tiles, B given [N, K] with long K and few x 32 tiles -- split each tile's K over several
+// workgroups (four waves each) so that about 256 workgroups stream B; their accumulators meet in the workspace and a
+// second launch adds them in split order and runs the epilogue.
 // decode_splits gives the workgroups per tile (1: the form is not used) and decode_split_ws_bytes the workspace the
 // partials need.
 int decode_splits(int64_t M, int64_t N, int64_t K, int trans_b);

@@ -23,7 +23,7 @@ pytestmark = pytest.mark.gpu
 _I8 = [(1, 4096, 8192, False), (7, 4104, 8448, False), (16, 12416, 512, False), (32, 4000, 8192, True),
        (3, 5120, 9216, True), (20, 4096, 10240, True), (12, 8192, 8192, True), (1, 2048, 8192, False),
        (29, 4608, 11264, False), (64, 4096, 8192, True), (33, 4096, 8192, False), (1, 11008, 4096, False),
-       (16, 10256, 2048, False), (40, 10240, 1024, False)]
+       (16, 10256, 2048, False), (40, 10240, 1024, False), (50, 4096, 11008, True), (64, 12416, 768, False)]
 
 
 @pytest.mark.parametrize("M,N,K,trans_b", _I8)
@@ -40,7 +40,8 @@ def test_int8_decode_forms(ascq_gpu, oracle, M, N, K, trans_b):
 
 
 @pytest.mark.parametrize("M,N,K,trans_b", [(1, 4096, 8192, False), (16, 12416, 512, False), (32, 4000, 8192, True),
-                                           (5, 5120, 9216, True), (9, 4104, 8192, False), (8, 11008, 4096, False)])
+                                           (5, 5120, 9216, True), (9, 4104, 8192, False), (8, 11008, 4096, False),
+                                           (48, 4096, 8192, True), (64, 4096, 8192, False)])
 def test_fp8_decode_forms(ascq_gpu, M, N, K, trans_b):
     fa, fb = O.FP8_E4M3, O.FP8_E4M3
     A, B, b, qs, qv = fp8_case(5 * M + N + K, M, N, K, fa, fb, O.BF16, trans_b=trans_b, quant="vector")
