@@ -15,8 +15,8 @@ vendor BLAS (hipBLASLt through torch) on the int8 and fp8 8192^3 shapes.
 
 `--only shapes` (not part of the default run) times the weight-only matmul over model shapes (attention and MLP
 projections of 7B / 13B / 70B-class models) at M = 1 / 16 / 64 / 512; `--only decode` (not part of the default run
-either) times the int8, fp8 and MX-FP4 Matmuls at decode-sized batches (M = 1 / 16 / 64, B streamed once) and the MoE
-group matmul at 16 / 64 / 256 tokens.
+either) times the int8, fp8 and MX-FP4 Matmuls at decode-sized batches (M = 1 / 16 / 64, B [N, K] streamed once; int8
+and fp8 also with B given [K, N] at M = 1 / 64) and the MoE group matmul at 16 / 64 / 256 tokens.
 """
 from __future__ import annotations
 
@@ -424,7 +424,7 @@ def bench_wo_shape(torch, ascq, K, N, M, iters, grp=128, w_type=None):
                 frac_of_peak=tf / F16_PEAK_TFLOPS, gbs=round(gbs, 1), eager_ms=eager)
 
 
-def bench_decode_matmul(torch, ascq, kind, K, N, M, iters=50):
+def bench_decode_matmul(torch, ascq, kind, K, N, M, iters=50, trans_b=True):
     """a quantized Matmul at a decode-sized batch (B [N, K] streamed once per call: the weight stream is the roofline),
     weights rotating past the Infinity Cache, timed as a HIP graph of the calls replayed.  kind: "int8" (W8A8,
     per-channel DEQF16 -> f16), "fp8" (e4m3, per-channel QF322BF16 -> bf16), "mxfp4" (E2M1 / E8M0 -> bf16; the
@@ -435,7 +435,8 @@ def bench_decode_matmul(torch, ascq, kind, K, N, M, iters=50):
         wb = K * N
         R = rotation(wb)
         A = torch.randint(-127, 128, (M, K), generator=g, device="cuda", dtype=torch.int8)
-        Bs = [(torch.randint(-127, 128, (N, K), generator=g, device="cuda", dtype=torch.int8), None) for _ in range(R)]
+        Bs = [(torch.randint(-127, 128, (N, K) if trans_b else (K, N), generator=g, device="cuda", dtype=torch.int8), None)
+              for _ in range(R)]
         C = torch.empty((M, N), dtype=torch.float16, device="cuda")
         mm = ascq.Matmul(ascq.INT8, ascq.INT8, ascq.F16)
         mm.SetQuantVector(torch.full((N,), 0x3A800000, dtype=torch.int64, device="cuda"))
@@ -444,7 +445,7 @@ def bench_decode_matmul(torch, ascq, kind, K, N, M, iters=50):
         wb = K * N
         R = rotation(wb)
         A = _fp8_bytes(torch, (M, K), g, torch.float8_e4m3fn)
-        Bs = [(_fp8_bytes(torch, (N, K), g, torch.float8_e4m3fn), None) for _ in range(R)]
+        Bs = [(_fp8_bytes(torch, (N, K) if trans_b else (K, N), g, torch.float8_e4m3fn), None) for _ in range(R)]
         C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
         mm = ascq.Matmul(ascq.FP8_E4M3, ascq.FP8_E4M3, ascq.BF16)
         mm.SetQuantVector(torch.full((N,), 0x3C000000, dtype=torch.int64, device="cuda"))
@@ -464,14 +465,15 @@ def bench_decode_matmul(torch, ascq, kind, K, N, M, iters=50):
 
     def fn(i):
         B, sB = Bs[i % R]
-        mm.SetTensorB(B, True)
+        mm.SetTensorB(B, trans_b)
         if sB is not None:
             mm.SetTensorScaleB(sB, True)
         mm.IterateAll(C)
 
     ms, eager = _time_graph(torch, fn, iters, C)
     gbs = wb / (ms * 1e-3) / 1e9
-    return dict(workload=f"{what}, decode batch M={M}, K={K}, N={N}, B given [N,K]", ms=ms, value=round(gbs, 1),
+    return dict(workload=f"{what}, decode batch M={M}, K={K}, N={N}, B given " + ("[N,K]" if trans_b else "[K,N]"),
+                ms=ms, value=round(gbs, 1),
                 unit="GB/s", frac_of_peak=gbs / HBM_PEAK_GBS, tops=round(2 * M * N * K / (ms * 1e-3) / 1e12, 1),
                 timing="HIP graph of the calls (weights rotating), replayed" if USE_GRAPH else "eager calls",
                 eager_ms=eager)
@@ -935,6 +937,8 @@ OTHER = {
                for k, n in WO_SHAPES for m in (1, 16, 64, 512)],
     "decode": [lambda t, a, kd=kd, k=k, n=n, m=m: bench_decode_matmul(t, a, kd, k, n, m)
                for kd in ("int8", "fp8", "mxfp4") for k, n in DECODE_SHAPES for m in (1, 16, 64)]
+              + [lambda t, a, kd=kd, k=k, n=n, m=m: bench_decode_matmul(t, a, kd, k, n, m, trans_b=False)
+                 for kd in ("int8", "fp8") for k, n in DECODE_SHAPES for m in (1, 64)]
               + [lambda t, a, tk=tk: bench_group_decode(t, a, tk) for tk in (16, 64, 256)],
 }
 
