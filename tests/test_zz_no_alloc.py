@@ -1,6 +1,7 @@
 """ascq_matmul_iterate_all_noalloc (IterateAll with the workspace taken from the library's static per-device
 scratch, allocating nothing) against ascq_matmul_iterate_all, bit-exact, on two calls in a row -- the second with a
-smaller problem -- for each kind of handle that uses a workspace: int8 with a [K, N] B transposed into it, MX-FP4
+smaller problem -- for each kind of handle that uses a workspace: int8 with a [K, N] B transposed into it, int8 at
+decode-sized batches keeping K-split partials in it, MX-FP4
 with its scales rearranged (and a [K, N] B transposed) into it, and int4 operands unpacked into it.  The handle
 keeps its own workspace across the allocation-free calls.  A fresh handle that only calls the allocation-free entry
 leaves the device's free memory unchanged and owns no workspace afterwards, and the call replays correctly from a
@@ -48,6 +49,31 @@ def test_noalloc_int8_kn_b(ascq_gpu, oracle):
     mm = ascq.Matmul(ascq.INT8, ascq.INT8, ascq.F16, ascq.INT32)
     for i, (M, N, K) in enumerate([(1024, 1024, 512), (1024, 1024, 256)]):
         rng = seeded(300 + i)
+        A = rng.integers(-127, 128, (M, K), dtype=np.int8)
+        B = rng.integers(-127, 128, (K, N), dtype=np.int8)
+        bias = rng.integers(-(1 << 15), 1 << 15, N, dtype=np.int32)
+        sc = np.exp(rng.uniform(np.log(2.0 ** -12), np.log(2.0 ** -6), N)).astype(np.float32)
+        words = sc.view(np.uint32).astype(np.uint64)
+        mm.SetOrgShape(M, N, K)
+        assert mm.WorkspaceSize() > 0
+        mm.SetQuantVector(_dev(words.view(np.int64)))
+        mm.SetTensorA(_dev(A))
+        mm.SetTensorB(_dev(B), False)
+        mm.SetBias(_dev(bias))
+        c1, c2 = _both(ascq, mm, (M, N), torch.float16)
+        _same(c1, c2)
+        ref = O.mm_dequant(O.matmul_i8(A, B, bias), O.F16, qvec=words)
+        np.testing.assert_array_equal(c2.cpu().view(torch.int16).numpy().view(np.uint16), ref)
+        mm.End()
+
+
+def test_noalloc_int8_decode_split(ascq_gpu, oracle):
+    """int8 x int8 -> f16 at decode-sized batches with B given [K, N] and long K: the K split across workgroups keeps
+    its partials in the workspace (the static scratch for the allocation-free call); then a smaller problem"""
+    ascq = ascq_gpu
+    mm = ascq.Matmul(ascq.INT8, ascq.INT8, ascq.F16, ascq.INT32)
+    for i, (M, N, K) in enumerate([(8, 4096, 8192), (1, 2048, 8192)]):
+        rng = seeded(320 + i)
         A = rng.integers(-127, 128, (M, K), dtype=np.int8)
         B = rng.integers(-127, 128, (K, N), dtype=np.int8)
         bias = rng.integers(-(1 << 15), 1 << 15, N, dtype=np.int32)
