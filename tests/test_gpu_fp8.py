@@ -167,6 +167,18 @@ def test_fp8_decode_ksplit(ascq_gpu, out_type, trans_b, M, N, K):
     assert np.array_equal(np.nan_to_num(got, nan=7.0), np.nan_to_num(again, nan=7.0))
 
 
+@pytest.mark.parametrize("M,N,K", [(100, 1104, 512), (300, 272, 1040), (64, 11008, 4096), (65, 160, 208)])
+def test_fp8_kn_b_transposed_reads(ascq_gpu, M, N, K):
+    """B given [K, N] with 16-byte K rows below the sizes where the host transposes it: the 64 x 128 tiles stage B's
+    K rows like A's and read them with LDS transpose reads (an fp8 k-step = two int8-sized transposed reads); K not
+    a multiple of 64 among them (the last stage's rows past K read zeros)"""
+    fa, fb = O.FP8_E5M2, O.FP8_E4M3
+    A, B, b, qs, qv = fp8_case(41 + M, M, N, K, fa, fb, O.BF16, trans_b=False, quant="vector")
+    got = run_fp8(ascq_gpu, A, B, fa, fb, M, N, K, O.BF16, trans_b=False, bias=b, qvec=qv)
+    v, d = expected(A, B, fa, fb, b, qs, qv, False, False, K)
+    check_out(got, v, d, O.BF16, f"M={M}")
+
+
 @pytest.mark.parametrize("fa,fb", [(O.FP8_E4M3, O.FP8_E4M3), (O.FP8_E5M2, O.FP8_E4M3)])
 @pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (1100, 1040, 1040), (2048, 1280, 512)])
 def test_fp8_tiled_big(ascq_gpu, fa, fb, M, N, K):
