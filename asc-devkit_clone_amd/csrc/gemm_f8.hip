@@ -75,11 +75,12 @@ constexpr int op_of_fmt = (FMT == (FMT_BF16 | (FMT_BF16 << 3))) ? OP_BF16 : OP_F
 // BTR (B given [K, N], 16-byte K rows): B's K rows are staged like A's and read by LDS transpose reads
 // PH (K split across workgroups, decode-sized batches): 1 -- workgroup b runs split b / tiles of tile b % tiles, its K
 // range a whole number of KW RB units (shared out as evenly as p.splits allows), and stores the tile's fp32
-// accumulators in p.ws ([split][tile][fragment][lane]); 2 -- one wave per tile adds the splits' accumulators in split
-// order (one fixed order, so the result does not vary between calls) and runs the epilogue.
+// accumulators in p.ws ([split][tile][fragment][lane]); 2 -- one wave per 32 x 32 fragment of a tile adds the
+// splits' accumulators of its fragment in split order (one fixed order, so the result does not vary between calls)
+// and stores it through the epilogue.
 template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB, int FMT, bool UA = false, int KW = 1, bool BTR = false,
           int PH = 0>
-__global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_f8_kernel(GemmF8Args p)
+__global__ __launch_bounds__(PH == 2 ? (BM / 32) * (BN / 32) * 64 : WM * WN * 64 * KW) void gemm_f8_kernel(GemmF8Args p)
 {
     constexpr int OP = op_of_fmt<FMT>;
     constexpr int ES = OP == OP_BF16 ? 2 : 1;  // bytes per operand element
@@ -142,14 +143,17 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_f8_kernel(GemmF8Args p
     acc_t acc[T::FM][T::FN];
     constexpr int F = T::FM * T::FN;  // accumulator fragments of the tile
     acc_t* part = (acc_t*)p.ws;       // PH 1 / 2: [split][tile][F][64 lanes]
+    const int fw = PH == 2 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;  // PH 2: this wave's fragment
     if constexpr (PH == 2) {
         const int ln = threadIdx.x & 63;
 #pragma unroll
-        for (int f = 0; f < F; ++f) acc[f / T::FN][f % T::FN] = part[((int64_t)tile * F + f) * 64 + ln];
-        for (int sp = 1; sp < p.splits; ++sp)
-#pragma unroll
-            for (int f = 0; f < F; ++f)
+        for (int f = 0; f < F; ++f) {
+            acc[f / T::FN][f % T::FN] = acc_t{};
+            if (f != fw) continue;
+            acc[f / T::FN][f % T::FN] = part[((int64_t)tile * F + f) * 64 + ln];
+            for (int sp = 1; sp < p.splits; ++sp)
                 acc[f / T::FN][f % T::FN] += part[(((int64_t)sp * ntiles + tile) * F + f) * 64 + ln];
+        }
     } else {
         T::run(c, smem_f8 + (KW > 1 ? kw * T::LDS_BYTES : 0), acc, KW > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x);
     }
@@ -176,7 +180,7 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_f8_kernel(GemmF8Args p
     }
 
     // epilogue through a buffer resource over the output tile (rows past M dropped by its range)
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = PH == 2 ? 0 : threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const float mscalar = quant_pre_m1(p.qscalar);
     if (p.c_type == DT_INT4) {  // (V)QF322S4_PRE: int4 codes, two per byte
@@ -214,7 +218,8 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_f8_kernel(GemmF8Args p
             const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
             const uint32_t cbase = cok ? (uint32_t)(cl * esize) : OOB;
 #pragma unroll
-            for (int i = 0; i < T::FM; ++i)
+            for (int i = 0; i < T::FM; ++i) {
+                if (PH == 2 && i * T::FN + j != fw) continue;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     float v = acc[i][j][r];
@@ -222,6 +227,7 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_f8_kernel(GemmF8Args p
                     if (p.use_quant) v = v * m1;
                     put(conv(v, w), cbase + (uint32_t)T::frag_row(wm, i, r, lane) * out.pitch);
                 }
+            }
         }
     };
     if (KW == 1 && p.atomic != C_STORE) {  // enAtomic: f32 / f16 / bf16 C (the host layer refuses the others)
@@ -334,7 +340,8 @@ static hipError_t launch_f8_split(GemmF8Args a, hipStream_t st)
              dim3(64 * KWS), (uint32_t)lds, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_k((gemm_f8_kernel<BM, BN, 1, 1, ST, TB, RB, FMT, false, 1, BTR, 2>), dim3(tiles), dim3(64), 0u, st, a);
+    launch_k((gemm_f8_kernel<BM, BN, 1, 1, ST, TB, RB, FMT, false, 1, BTR, 2>), dim3(tiles), dim3(T::FM * T::FN * 64), 0u,
+             st, a);
     return hipGetLastError();
 }
 

@@ -36,11 +36,11 @@ using I8Core = typename std::conditional<UA, GemmCoreUA<BM, BN, WM, WN, TB, CT>,
 // For small problems (the W8A8 sample, 32 tiles) this cuts the serial K loop of each tile KW-fold.
 // PH (K split across workgroups, decode-sized batches): 1 -- workgroup b runs split b / tiles of tile b % tiles, its
 // K range a whole number of KW RB units (the units shared out as evenly as p.splits allows), and stores the tile's
-// accumulators in p.ws ([split][tile][fragment][lane]); 2 -- one wave per tile adds the splits' accumulators in split
-// order (int32: exact) and runs the epilogue.
+// accumulators in p.ws ([split][tile][fragment][lane]); 2 -- one wave per 32 x 32 fragment of a tile adds the
+// splits' accumulators of its fragment in split order (int32: exact) and stores it through the epilogue.
 template <int BM, int BN, int WM, int WN, int ST, bool TB, int RB = 64, bool BTR = false, int KW = 1, bool UA = false,
           int PH = 0>
-__global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_i8_kernel(GemmI8Args p)
+__global__ __launch_bounds__(PH == 2 ? (BM / 32) * (BN / 32) * 64 : WM * WN * 64 * KW) void gemm_i8_kernel(GemmI8Args p)
 {
     using T = I8Core<BM, BN, WM, WN, ST, TB, RB, false, BTR, UA>;
     static_assert(!UA || KW == 1, "any-alignment tiles run whole K");
@@ -99,14 +99,17 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_i8_kernel(GemmI8Args p
     typename T::acc_t acc[T::FM][T::FN];
     constexpr int F = T::FM * T::FN;  // accumulator fragments of the tile
     v16i* part = (v16i*)p.ws;         // PH 1 / 2: [split][tile][F][64 lanes]
+    const int fw = PH == 2 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;  // PH 2: this wave's fragment
     if constexpr (PH == 2) {
         const int ln = threadIdx.x & 63;
 #pragma unroll
-        for (int f = 0; f < F; ++f) acc[f / T::FN][f % T::FN] = part[((int64_t)tile * F + f) * 64 + ln];
-        for (int sp = 1; sp < p.splits; ++sp)
-#pragma unroll
-            for (int f = 0; f < F; ++f)
+        for (int f = 0; f < F; ++f) {
+            acc[f / T::FN][f % T::FN] = typename T::acc_t{};
+            if (f != fw) continue;
+            acc[f / T::FN][f % T::FN] = part[((int64_t)tile * F + f) * 64 + ln];
+            for (int sp = 1; sp < p.splits; ++sp)
                 acc[f / T::FN][f % T::FN] += part[(((int64_t)sp * ntiles + tile) * F + f) * 64 + ln];
+        }
     } else {
         T::run(c, smem + (KW > 1 ? kw * T::LDS_BYTES : 0), acc, KW > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x);
     }
@@ -134,7 +137,7 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_i8_kernel(GemmI8Args p
 
     // epilogue: per 32x32 accumulator tile, lane holds column lane%32 and 16 rows (GemmCore::frag_row); stores go
     // through a buffer resource over the output tile (rows past M dropped by its range, 32-bit offsets)
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = PH == 2 ? 0 : threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const float mscalar = quant_pre_m1(p.qscalar);
     if (p.epi == EPI_REQ4) {  // (V)REQ4: int4 codes, two per byte
@@ -171,12 +174,14 @@ __global__ __launch_bounds__(WM * WN * 64 * KW) void gemm_i8_kernel(GemmI8Args p
             const float m1 = p.qvec ? quant_pre_m1(w) : mscalar;
             const uint32_t cbase = cok ? (uint32_t)(cl * esize) : OOB;
 #pragma unroll
-            for (int i = 0; i < T::FM; ++i)
+            for (int i = 0; i < T::FM; ++i) {
+                if (PH == 2 && i * T::FN + j != fw) continue;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int32_t v = (int32_t)((uint32_t)acc[i][j][r] + (uint32_t)bias);
                     put(conv(v, m1, w), cbase + (uint32_t)T::frag_row(wm, i, r, lane) * out.pitch);
                 }
+            }
         }
     };
     if (KW == 1 && p.atomic != C_STORE) {  // enAtomic: int32 / f16 / bf16 C (the host layer refuses the others)
@@ -514,7 +519,8 @@ static hipError_t launch_i8_split(GemmI8Args a, hipStream_t st)
              dim3(64 * DS_KW), (uint32_t)lds, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_k((gemm_i8_kernel<BM, BN, 1, 1, ST, TB, DS_RB, BTR, 1, false, 2>), dim3(tiles), dim3(64), 0u, st, a);
+    launch_k((gemm_i8_kernel<BM, BN, 1, 1, ST, TB, DS_RB, BTR, 1, false, 2>), dim3(tiles), dim3(T::FM * T::FN * 64), 0u,
+             st, a);
     return hipGetLastError();
 }
 
