@@ -361,11 +361,12 @@ static hipError_t launch_f8_fmt(const GemmF8Args& a, bool ua, hipStream_t st)
     const bool big = a.M >= 1024 && a.N >= 1024;
     // decode-sized batches (B streamed once) with a K-contiguous B and f32 / f16 / bf16 C stored: 32 x 32 tiles,
     // each tile's K split over four waves of one workgroup, up to 32 rows, and up to 64 while 64 x 64 tiles would
-    // leave fewer than 160 workgroups (the int8 Matmul's rule; 33-64 rows take 64 x 32 tiles from N = 8192 on:
-    // K = N = 8192, M = 64: 29.1 -> 24.6 us)
+    // leave fewer than 160 workgroups (the int8 Matmul's rule; 33-64 rows take 64 x 32 tiles where those make one
+    // nearly full round of 225-256 workgroups: K = N = 8192, M = 64: 29.1 -> 24.6 us)
     const int64_t t64 = ((a.M + 63) / 64) * ((a.N + 63) / 64);
     const bool skinny = a.M <= 32 || (a.M <= 64 && t64 < 160);
     const bool c_wide = a.c_type == DT_F32 || a.c_type == DT_F16 || a.c_type == DT_BF16;
+    const bool m64x32 = a.M > 32 && a.N > 7168 && a.N <= 8192;
     if constexpr (ES == 1) {
         // with a workspace for the partials, the K split across workgroups as well where decode_splits (the int8
         // Matmul's rule) finds it faster: B [N, K] on the 32 x 32 tiles, B [K, N] (16-byte K rows) on 32 x 128 tiles
@@ -382,13 +383,14 @@ static hipError_t launch_f8_fmt(const GemmF8Args& a, bool ua, hipStream_t st)
             return a.trans_b ? launch_f8_split<FMT, true, 64, 32, 4>(b, st) : launch_f8_split<FMT, false, 64, 128, 3>(b, st);
         }
         if (a.trans_b && skinny && c_wide && a.atomic == C_STORE && a.K % 256 == 0)
-            return a.M > 32 && a.N >= 8192 ? launch_f8_tiled<64, 32, 1, 1, 4, true, 64, FMT, false, 4>(a, st)
-                                           : launch_f8_tiled<32, 32, 1, 1, 4, true, 64, FMT, false, 4>(a, st);
+            return m64x32 ? launch_f8_tiled<64, 32, 1, 1, 4, true, 64, FMT, false, 4>(a, st)
+                          : launch_f8_tiled<32, 32, 1, 1, 4, true, 64, FMT, false, 4>(a, st);
         // ... and with B given [K, N] (16-byte K rows): B's K rows staged like A's, read by LDS transpose reads
         // (32 x 64 tiles from N = 10240 on, as the int8 Matmul: K = 4096, N = 11008, M = 1 / 16: 22.8 / 24.6 ->
         // 21.4 / 21.6 us)
         if (b_tr && skinny && c_wide && a.atomic == C_STORE && a.K % 256 == 0)
             return a.N >= 10240 ? launch_f8_tiled<32, 64, 1, 1, 4, false, 64, FMT, false, 4, true>(a, st)
+                   : m64x32   ? launch_f8_tiled<64, 32, 1, 1, 4, false, 64, FMT, false, 4, true>(a, st)
                                 : launch_f8_tiled<32, 32, 1, 1, 4, false, 64, FMT, false, 4, true>(a, st);
     }
     if (a.trans_b) {

@@ -558,17 +558,20 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t st)
                 return m32 ? launch_i8_split<false, true, 32, 128, 3>(b, st)
                            : launch_i8_split<false, true, 64, 128, 3>(b, st);
         }
-        // (33-64 rows: one 64-row tile per 32 columns, B read by one workgroup, while that still leaves 256 workgroups
-        // or more -- K = N = 8192, M = 64: 28.7 -> 23.2 us; K = 4096, N = 8192: 16.5 -> 14.7 us; at N = 4096 / 2048
-        // the two 32-row tiles are faster, 9.7 / 6.9 against 11.7 / 9.1 us)
+        // (33-64 rows: one 64-row tile per 32 columns, B read by one workgroup, where those tiles make one nearly full
+        // round of 225-256 workgroups -- K = N = 8192, M = 64: 28.7 -> 23.2 us; K = 4096, N = 8192: 16.5 -> 14.7 us;
+        // at N = 4096 / 2048 the two 32-row tiles are faster, 9.7 / 6.9 against 11.7 / 9.1 us, and at N = 9216
+        // (288 such tiles, B [K, N]) 33.9 against 36.1 us)
+        const bool m64x32 = a.M > 32 && a.N > 7168 && a.N <= 8192;
         if (ksplit && a.trans_b)
-            return a.M > 32 && a.N >= 8192 ? launch_tiled<64, 32, 1, 1, 4, true, 64, false, 4>(a, st)
-                                           : launch_tiled<32, 32, 1, 1, 4, true, 64, false, 4>(a, st);
+            return m64x32 ? launch_tiled<64, 32, 1, 1, 4, true, 64, false, 4>(a, st)
+                          : launch_tiled<32, 32, 1, 1, 4, true, 64, false, 4>(a, st);
         // (B [K, N]: 32 x 64 tiles -- 64-byte K-row runs -- while they still give about 160 workgroups or more:
         // K = 4096, N = 11008, M = 1 / 16: 22.1 / 23.8 -> 18.1 / 19.7 us; at N = 4096 / 8192 the 32 x 32 tiles are
         // faster, 16.9 / 18.0 against 18.8 / 20.2 us)
         if (ksplit && a.ldb % 16 == 0 && (uintptr_t)a.B % 16 == 0)
             return a.N >= 10240 ? launch_tiled<32, 64, 1, 1, 4, false, 64, true, 4>(a, st)
+                   : m64x32   ? launch_tiled<64, 32, 1, 1, 4, false, 64, true, 4>(a, st)
                                 : launch_tiled<32, 32, 1, 1, 4, false, 64, true, 4>(a, st);
         if (a.trans_b)
             return big ? (a.K % 128 == 0 ? launch_tiled<256, 256, 4, 2, 2, true, 128>(a, st)

@@ -1,7 +1,7 @@
 """GPU parity sweep over the decode-batch forms of the quantized Matmuls (M <= 64, B streamed once): shapes chosen on
 both sides of each dispatch rule -- K split over the waves of a workgroup, K split across workgroups as well (B [N, K]
 with few 32 x 32 tiles and long K; B [K, N] on 32 x 128 tiles with long K or wide N; MX-FP4 with few 64 x 64 tiles),
-B [K, N] on 32 x 64 tiles from N = 10240 on, B [N, K] on 64 x 32 tiles for 33-64 rows from N = 8192 on,
+B [K, N] on 32 x 64 tiles from N = 10240 on, 64 x 32 tiles for 33-64 rows at N = 7169-8192,
 B [K, N] rows that are not 16-byte multiples, row-major and block-pair MX scales -- against the oracle: int8 bit-exact
 (int32 and DEQF16 C), fp8 and MX-FP4 within the bounds their own test files state (fp32 accumulation, the fp8 MFMA's
 16-element group alignment)."""
@@ -24,7 +24,7 @@ _I8 = [(1, 4096, 8192, False), (7, 4104, 8448, False), (16, 12416, 512, False), 
        (3, 5120, 9216, True), (20, 4096, 10240, True), (12, 8192, 8192, True), (1, 2048, 8192, False),
        (29, 4608, 11264, False), (64, 4096, 8192, True), (33, 4096, 8192, False), (1, 11008, 4096, False),
        (16, 10256, 2048, False), (40, 10240, 1024, False), (50, 4096, 11008, True), (64, 12416, 768, False),
-       (40, 8200, 1024, True), (64, 8192, 2048, True)]
+       (40, 8008, 1024, True), (64, 8192, 2048, True), (48, 8000, 1024, False), (64, 9216, 2048, False)]
 
 
 @pytest.mark.parametrize("M,N,K,trans_b", _I8)
@@ -42,7 +42,8 @@ def test_int8_decode_forms(ascq_gpu, oracle, M, N, K, trans_b):
 
 @pytest.mark.parametrize("M,N,K,trans_b", [(1, 4096, 8192, False), (16, 12416, 512, False), (32, 4000, 8192, True),
                                            (5, 5120, 9216, True), (9, 4104, 8192, False), (8, 11008, 4096, False),
-                                           (48, 4096, 8192, True), (64, 4096, 8192, False), (40, 8200, 1024, True)])
+                                           (48, 4096, 8192, True), (64, 4096, 8192, False), (40, 8008, 1024, True),
+                                           (48, 8000, 1024, False)])
 def test_fp8_decode_forms(ascq_gpu, M, N, K, trans_b):
     fa, fb = O.FP8_E4M3, O.FP8_E4M3
     A, B, b, qs, qv = fp8_case(5 * M + N + K, M, N, K, fa, fb, O.BF16, trans_b=trans_b, quant="vector")
